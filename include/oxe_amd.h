@@ -1,0 +1,86 @@
+/* oxe_amd.h - C ABI of the MI355X (gfx950) MTP depth-1 decode step.
+ *
+ * Drop-in boundary for the hot path of n0rpan/snapdragon-engine's `oxe` engine. The reference's
+ * Rust host (crates/model, crates/sched, crates/oxe-cli) calls its CPU kernels through the
+ * extern "C" block of crates/kernels-sys/src/lib.rs:36-333; this header is the device counterpart
+ * a Rust (or any C-ABI) host links instead. Plain C: device pointers, sizes, a stream handle
+ * (hipStream_t passed as void*), int status codes. No allocation inside kernel-level calls.
+ *
+ * Status codes: 0 ok, -1 bad shape/argument (nothing written, like the reference's
+ * oxe_repack_q8_0_4x8 returning -1), -2 HIP launch/runtime error, -3 out of device memory.
+ *
+ * Every declaration names the reference interface it replaces (file:line in the reference tree).
+ */
+#ifndef OXE_AMD_H
+#define OXE_AMD_H
+#include <stdint.h>
+#include "oxe_model.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define OXE_API
+
+typedef struct oxe_engine oxe_engine;
+
+/* ---- kernel level (device pointers, async on `stream`) -------------------------------------- */
+
+/* Q8_0 activation quantizer: nrows rows of k floats -> int8 codes [nrows][k] + fp16 scales
+ * [nrows][k/32]. Replaces quantize_row_q8_0 (crates/kernels-sys/src/lib.rs:62; NEON body
+ * vendor/ggml-subset/generated/quants_subset.c:6-42). */
+OXE_API int oxe_hip_quantize_row_q8_0(const float *x, int64_t k, int64_t nrows, int8_t *q, uint16_t *d, void *stream);
+
+/* Q8_0 lane GEMV: y[l][r] = W[r] . x[l] for nl = 1 or 2 lanes in one weight pass; weights as int8
+ * codes [nr][k] + fp16 scales [nr][k/32] (this build's layout; see oxe_hip_repack_q8_0), lanes as
+ * produced by oxe_hip_quantize_row_q8_0; k in {512, 2048, 4096}. isum (optional, may be NULL):
+ * the exact int32 block dots [nl][nr][k/32]. Replaces oxe_vl_gemv (lib.rs:113, type 80) and
+ * ggml_gemv_q8_0_4x8_q8_0 (lib.rs:75). */
+OXE_API int oxe_hip_gemv_q8_0(int64_t k, int64_t nr, int nl, const int8_t *wq, const uint16_t *wd, const int8_t *xq,
+                              const uint16_t *xd, float *y, int32_t *isum, void *stream);
+
+/* ---- engine level (crates/model/src/engine.rs Engine; one engine per stream) -------------- */
+
+/* Last error message of a failed call on this host thread (no exceptions cross the C ABI). */
+OXE_API const char *oxe_last_error(void);
+
+/* Create an engine for `desc` (the kernels are specialised for the 35B-A3B per-layer shape; layer
+ * count and vocabulary are free) with a context of n_ctx positions (rounded up to 256), all state in
+ * device memory. Replaces Engine::with_options (crates/model/src/engine.rs:869-1000) with
+ * verify_lanes 2 and an MTP head. */
+OXE_API int oxe_engine_create(const oxe_model_desc *desc, uint64_t seed, int n_ctx, oxe_engine **out);
+OXE_API void oxe_engine_destroy(oxe_engine *e);
+/* Fill every weight with the synthetic model of include/oxe_model.h (the benchmark's model). */
+OXE_API int oxe_engine_synth_weights(oxe_engine *e);
+
+/* Run n (1..2) tokens at positions pos..pos+n-1 as one batch-invariant run; argmax per lane.
+ * Replaces Engine::verify (engine.rs:2002-2025). The position moves only on commit. */
+OXE_API int oxe_engine_verify(oxe_engine *e, const uint32_t *toks, int n, uint32_t *argmax_out);
+/* Keep the first m tokens of the last verify (engine.rs:2030-2039): position pos0+m, recurrent
+ * state of lane m-1, V^T of rejected positions zeroed. */
+OXE_API int oxe_engine_commit(oxe_engine *e, int m);
+/* verify + commit(1) (engine.rs:1991-1997). */
+OXE_API int oxe_engine_step(oxe_engine *e, uint32_t tok, uint32_t *argmax_out);
+/* MTP head over toks at pos0.. with input hidden states hs [n][n_embd] (host memory); argmax of the
+ * last lane when head_last (engine.rs:2044-2071). */
+OXE_API int oxe_engine_mtp_run(oxe_engine *e, const uint32_t *toks, int n, int pos0, const float *hs, int head_last,
+                               uint32_t *argmax_out);
+/* MTP KV seeding of the pairs (toks[i], hs[i]) at pos0.. (engine.rs:2077-2091). */
+OXE_API int oxe_engine_mtp_seed(oxe_engine *e, const uint32_t *toks, int n, int pos0, const float *hs);
+OXE_API int oxe_engine_pos(const oxe_engine *e);
+OXE_API int oxe_engine_n_ctx(const oxe_engine *e);
+/* h_nextn of lane `lane` of the last run (Engine::hidden, engine.rs:1941-1945), host copy. */
+OXE_API int oxe_engine_hidden(oxe_engine *e, int lane, float *out);
+/* Logits of lane `lane` of the last verify (Engine::logits_lane, engine.rs:1934-1937), host copy. */
+OXE_API int oxe_engine_logits(oxe_engine *e, int lane, float *out);
+/* Diagnostic counters (64: top-k ties met, where the reference would sort). */
+OXE_API int oxe_engine_counter(oxe_engine *e, int which, uint32_t *out);
+/* State copy for parity checks / hand-off (see engine.hip for the regions). */
+OXE_API int oxe_engine_state_copy(oxe_engine *e, int which, int dir, int64_t offset, void *host, int64_t nbytes);
+OXE_API int oxe_engine_set_pos(oxe_engine *e, int pos);
+OXE_API int64_t oxe_engine_device_bytes(const oxe_engine *e);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* OXE_AMD_H */

@@ -1,0 +1,683 @@
+// TEST INFRASTRUCTURE ONLY (see oxo.h). The reference's qwen35moe decode engine restated on the CPU:
+// lanes, recurrent slots, KV cache, the per-layer phases, the LM head and the MTP head
+// (crates/model/src/engine.rs, crates/model/src/mtp.rs), on the synthetic model of
+// include/oxe_model.h. Phase bodies follow the reference's per-lane arithmetic exactly; the
+// per-thread row splits of the reference become OpenMP row loops (rows are independent, so the
+// split never changes a value: the reference's own thread-count-invariance property,
+// crates/model/src/tests.rs:288).
+#include "oxo.h"
+#include "oxo_model.h"
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <memory>
+#include <mutex>
+#include <vector>
+
+namespace {
+
+struct Q8 {
+    int64_t rows = 0, k = 0;
+    std::vector<int8_t> q;
+    std::vector<uint16_t> d;
+};
+
+// Generate rows [r0, r0+n) of expert e of a Q8_0 tensor [experts][rows][k] into m.
+void gen_q8(uint64_t seed, int layer, int kind, int64_t rows, int64_t k, int64_t e, Q8 &m) {
+    m.rows = rows;
+    m.k = k;
+    m.q.resize(rows * k);
+    m.d.resize(rows * k / 32);
+    const uint64_t key = oxe_tensor_key(seed, layer, kind);
+    const uint64_t skey = oxe_tensor_key(seed, layer, kind + OXE_T_SCALE_OFFSET);
+    const oxe_synth_param p = oxe_synth_param_of(kind);
+    const uint64_t base = (uint64_t)e * rows * k;
+#pragma omp parallel for schedule(static)
+    for (int64_t r = 0; r < rows; r++) {
+        for (int64_t i = 0; i < k; i++) m.q[r * k + i] = oxe_synth_code(key, base + r * k + i);
+        for (int64_t b = 0; b < k / 32; b++)
+            m.d[r * (k / 32) + b] = oxe_synth_scale(skey, (base + r * k) / 32 + b, p);
+    }
+}
+
+std::vector<float> gen_f32(uint64_t seed, int layer, int kind, int64_t n) {
+    std::vector<float> v(n);
+    const uint64_t key = oxe_tensor_key(seed, layer, kind);
+    for (int64_t i = 0; i < n; i++) v[i] = oxe_synth_f32(key, (uint64_t)i, kind);
+    return v;
+}
+
+struct Layer {
+    bool att = false;
+    std::vector<float> attn_norm, post_norm;
+    // delta-net
+    Q8 qkv, z, beta, alpha, out;
+    std::vector<float> conv, a, dt, ssm_norm;
+    // attention
+    Q8 wq, wk, wv;
+    std::vector<float> q_norm, k_norm;
+    // MoE
+    std::vector<float> router, shexp_gate;
+    Q8 gate_sh, up_sh, down_sh;
+    std::vector<std::unique_ptr<Q8[]>> experts;  // [expert] -> {gate, up, down}, lazily generated
+    // MTP block
+    Q8 eh_proj;
+    std::vector<float> enorm, hnorm, head_norm;
+    int index = 0;  // recurrent or attention index
+};
+
+inline int64_t padded_n_kv(int64_t pos, int64_t n_ctx) {
+    return std::min(n_ctx, std::max<int64_t>(256, (pos + 1 + 255) / 256 * 256));
+}
+
+}  // namespace
+
+struct oxo_engine {
+    oxe_model_desc d{};
+    uint64_t seed = 0;
+    int64_t n_ctx = 0;
+    int n_slots = 2, max_lanes = 8;
+    std::vector<Layer> layers;  // n_layer (+1 MTP)
+    std::vector<float> out_norm;
+    Q8 output;
+    std::mutex gen_mu;
+
+    int n_rec = 0, n_att = 0;  // n_att includes the MTP layer
+    int64_t conv_len = 0, ssm_len = 0, v_stride = 0;
+    std::vector<float> conv_state, ssm_state;   // [slot][rec layer][...]
+    std::vector<uint16_t> kcache, vcache;       // [att][kvh][n_ctx][hd], [att][kvh*hd][v_stride]
+    std::vector<float> rope_tab;                // [n_ctx][n_rot]
+    int64_t pos = 0;
+    int cur_slot = 0;
+    int64_t pend_pos0 = 0;
+    int pend_cur = 0, pend_n = 0, pend_done = 0;
+    int tie_count = 0;
+
+    // per-lane buffers
+    std::vector<std::vector<float>> xin, x1, x2, o, hout, hin, logits;
+    std::vector<uint32_t> argmax;
+    bool keep_logits = true;
+
+    const Q8 &expert(int l, int e, int which) {
+        Layer &L = layers[l];
+        std::lock_guard<std::mutex> g(gen_mu);
+        if (!L.experts[e]) {
+            std::unique_ptr<Q8[]> m(new Q8[3]);
+            const int64_t E = d.n_embd, F = d.ff_exp;
+            gen_q8(seed, l, OXE_T_GATE_EXPS, F, E, e, m[0]);
+            gen_q8(seed, l, OXE_T_UP_EXPS, F, E, e, m[1]);
+            gen_q8(seed, l, OXE_T_DOWN_EXPS, E, F, e, m[2]);
+            L.experts[e] = std::move(m);
+        }
+        return L.experts[e][which];
+    }
+
+    std::vector<float> embed(uint32_t tok) {
+        const int64_t E = d.n_embd;
+        std::vector<int8_t> q(E);
+        std::vector<uint16_t> dd(E / 32);
+        const uint64_t key = oxe_tensor_key(seed, OXE_GLOBAL_LAYER, OXE_T_TOK_EMBD);
+        const uint64_t skey = oxe_tensor_key(seed, OXE_GLOBAL_LAYER, OXE_T_TOK_EMBD + OXE_T_SCALE_OFFSET);
+        const oxe_synth_param p = oxe_synth_param_of(OXE_T_TOK_EMBD);
+        for (int64_t i = 0; i < E; i++) q[i] = oxe_synth_code(key, (uint64_t)tok * E + i);
+        for (int64_t b = 0; b < E / 32; b++) dd[b] = oxe_synth_scale(skey, (uint64_t)tok * E / 32 + b, p);
+        std::vector<float> y(E);
+        oxo_dequantize_row_q8_0(q.data(), dd.data(), E, y.data());
+        return y;
+    }
+
+    // y[nl][rows] = W . quantize(x[l]) for each lane
+    static void mv(const Q8 &w, const std::vector<const float *> &xs, std::vector<float *> ys) {
+        const int nl = (int)xs.size();
+        std::vector<int8_t> xq(nl * w.k);
+        std::vector<uint16_t> xd(nl * w.k / 32);
+        for (int l = 0; l < nl; l++) oxo_quantize_row_q8_0(xs[l], w.k, xq.data() + l * w.k, xd.data() + l * w.k / 32);
+        std::vector<float> y(nl * w.rows);
+        oxo_gemv_q8_0(w.k, w.rows, nl, w.q.data(), w.d.data(), xq.data(), xd.data(), y.data(), nullptr);
+        for (int l = 0; l < nl; l++) std::memcpy(ys[l], y.data() + l * w.rows, w.rows * sizeof(float));
+    }
+
+    void init(const oxe_model_desc &desc, uint64_t s, int64_t nctx) {
+        d = desc;
+        seed = s;
+        n_ctx = (nctx + 255) / 256 * 256;
+        const int64_t E = d.n_embd;
+        const int nl_total = d.n_layer + (d.has_mtp ? 1 : 0);
+        layers.resize(nl_total);
+        const int64_t ds = d.ssm_d_state, nk = d.ssm_n_kheads, nv = d.ssm_n_vheads;
+        const int64_t nch = d.ssm_d_inner + 2 * nk * ds, hv = d.ssm_d_inner / nv, hd = d.head_dim;
+        for (int il = 0; il < nl_total; il++) {
+            Layer &L = layers[il];
+            const bool mtp = il == d.n_layer;
+            L.att = mtp || ((il + 1) % d.full_attention_interval == 0);
+            L.index = L.att ? n_att++ : n_rec++;
+            L.attn_norm = gen_f32(seed, il, OXE_T_ATTN_NORM, E);
+            L.post_norm = gen_f32(seed, il, OXE_T_POST_NORM, E);
+            if (!L.att) {
+                gen_q8(seed, il, OXE_T_DN_QKV, nch, E, 0, L.qkv);
+                gen_q8(seed, il, OXE_T_DN_Z, d.ssm_d_inner, E, 0, L.z);
+                gen_q8(seed, il, OXE_T_DN_BETA, nv, E, 0, L.beta);
+                gen_q8(seed, il, OXE_T_DN_ALPHA, nv, E, 0, L.alpha);
+                gen_q8(seed, il, OXE_T_DN_OUT, E, d.ssm_d_inner, 0, L.out);
+                L.conv = gen_f32(seed, il, OXE_T_DN_CONV, nch * d.ssm_conv_kernel);
+                L.a = gen_f32(seed, il, OXE_T_DN_A, nv);
+                L.dt = gen_f32(seed, il, OXE_T_DN_DT, nv);
+                L.ssm_norm = gen_f32(seed, il, OXE_T_DN_NORM, hv);
+            } else {
+                gen_q8(seed, il, OXE_T_ATT_Q, d.n_head * 2 * hd, E, 0, L.wq);
+                gen_q8(seed, il, OXE_T_ATT_K, d.n_head_kv * hd, E, 0, L.wk);
+                gen_q8(seed, il, OXE_T_ATT_V, d.n_head_kv * hd, E, 0, L.wv);
+                gen_q8(seed, il, OXE_T_ATT_OUT, E, d.n_head * hd, 0, L.out);
+                L.q_norm = gen_f32(seed, il, OXE_T_ATT_QNORM, hd);
+                L.k_norm = gen_f32(seed, il, OXE_T_ATT_KNORM, hd);
+            }
+            L.router = gen_f32(seed, il, OXE_T_ROUTER, (int64_t)d.n_expert * E);
+            L.shexp_gate = gen_f32(seed, il, OXE_T_SHEXP_GATE, E);
+            gen_q8(seed, il, OXE_T_GATE_SHEXP, d.ff_shexp, E, 0, L.gate_sh);
+            gen_q8(seed, il, OXE_T_UP_SHEXP, d.ff_shexp, E, 0, L.up_sh);
+            gen_q8(seed, il, OXE_T_DOWN_SHEXP, E, d.ff_shexp, 0, L.down_sh);
+            L.experts.resize(d.n_expert);
+            if (mtp) {
+                gen_q8(seed, il, OXE_T_EH_PROJ, E, 2 * E, 0, L.eh_proj);
+                L.enorm = gen_f32(seed, il, OXE_T_ENORM, E);
+                L.hnorm = gen_f32(seed, il, OXE_T_HNORM, E);
+                L.head_norm = gen_f32(seed, il, OXE_T_HEAD_NORM, E);
+            }
+        }
+        out_norm = gen_f32(seed, OXE_GLOBAL_LAYER, OXE_T_OUT_NORM, E);
+        gen_q8(seed, OXE_GLOBAL_LAYER, OXE_T_OUTPUT, d.n_vocab, E, 0, output);
+        conv_len = (d.ssm_conv_kernel - 1) * nch;
+        ssm_len = nv * hv * hv;
+        conv_state.assign((size_t)n_slots * n_rec * conv_len, 0.0f);
+        ssm_state.assign((size_t)n_slots * n_rec * ssm_len, 0.0f);
+        v_stride = n_ctx;
+        kcache.assign((size_t)n_att * d.n_head_kv * n_ctx * hd, 0);
+        vcache.assign((size_t)n_att * d.n_head_kv * hd * v_stride, 0);
+        rope_tab.resize((size_t)n_ctx * d.n_rot);
+        for (int64_t p = 0; p < n_ctx; p++)
+            oxo_mrope_cache_init(p, d.rope_sections, 1, d.n_rot, d.n_rot, d.rope_freq_base, 1.0f, 0.0f, 1.0f,
+                                 32.0f, 1.0f, d.n_ctx_train, 0, rope_tab.data() + p * d.n_rot);
+        auto lanes = [&](int64_t n) { return std::vector<std::vector<float>>(max_lanes, std::vector<float>(n, 0.0f)); };
+        xin = lanes(E); x1 = lanes(E); x2 = lanes(E); hout = lanes(E); hin = lanes(E);
+        o = lanes(std::max<int64_t>(d.ssm_d_inner, d.n_head * hd));
+        logits = lanes(d.n_vocab);
+        argmax.assign(max_lanes, 0);
+    }
+
+    void reset() {
+        std::fill(conv_state.begin(), conv_state.end(), 0.0f);
+        std::fill(ssm_state.begin(), ssm_state.end(), 0.0f);
+        std::fill(vcache.begin(), vcache.end(), 0);
+        pos = 0;
+        cur_slot = 0;
+        pend_n = 0;
+    }
+
+    // ---- phases (engine.rs); every phase loops over the run's lanes in order
+
+    // rec_mix (engine.rs:2394-2570) for all lanes, then mixer_out (2573-2609)
+    void recurrent(int l, int nl) {
+        Layer &L = layers[l];
+        const int64_t E = d.n_embd, ds = d.ssm_d_state, nk = d.ssm_n_kheads, nv = d.ssm_n_vheads;
+        const int64_t hv = d.ssm_d_inner / nv, nch = d.ssm_d_inner + 2 * nk * ds, kc = d.ssm_conv_kernel;
+        const float eps = d.rms_eps;
+        std::vector<std::vector<float>> xn(nl, std::vector<float>(E)), qkv(nl, std::vector<float>(nch)),
+            z(nl, std::vector<float>(d.ssm_d_inner)), beta(nl, std::vector<float>(nv)), alpha(nl, std::vector<float>(nv));
+        std::vector<const float *> xs;
+        for (int ln = 0; ln < nl; ln++) {
+            oxo_rms_norm_mul_f32(xin[ln].data(), L.attn_norm.data(), xn[ln].data(), E, eps);
+            xs.push_back(xn[ln].data());
+        }
+        auto outs = [&](std::vector<std::vector<float>> &v) {
+            std::vector<float *> r;
+            for (int ln = 0; ln < nl; ln++) r.push_back(v[ln].data());
+            return r;
+        };
+        mv(L.qkv, xs, outs(qkv));
+        mv(L.z, xs, outs(z));
+        mv(L.beta, xs, outs(beta));
+        mv(L.alpha, xs, outs(alpha));
+        const int ri = L.index;
+        std::vector<float> conv(nch), tmp(nch), gdn(hv), tmpn(hv), zs(hv);
+        for (int ln = 0; ln < nl; ln++) {
+            const int dst = (cur_slot + ln) % n_slots;
+            const int src = ln == 0 ? dst : (cur_slot + ln - 1) % n_slots;
+            float *cs = conv_state.data() + ((size_t)dst * n_rec + ri) * conv_len;
+            if (src != dst) std::memcpy(cs, conv_state.data() + ((size_t)src * n_rec + ri) * conv_len, conv_len * 4);
+            oxo_ssm_conv_step_f32(cs, qkv[ln].data(), L.conv.data(), (int)nch, (int)kc, conv.data());
+            oxo_silu_f32((int)nch, tmp.data(), conv.data());
+            conv = tmp;
+            for (int64_t g = 0; g < nk; g++) {
+                oxo_gdn_l2_norm_f32(conv.data() + g * ds, ds, eps);
+                oxo_gdn_l2_norm_f32(conv.data() + nk * ds + g * ds, ds, eps);
+            }
+            std::vector<float> gate(nv), beta_s(nv);
+            for (int64_t vh = 0; vh < nv; vh++) {
+                const float ab = alpha[ln][vh] + L.dt[vh];
+                float sp;
+                oxo_softplus_f32(1, &sp, &ab);
+                gate[vh] = sp * L.a[vh];
+                oxo_sigmoid_f32(1, &beta_s[vh], &beta[ln][vh]);
+            }
+            for (int64_t vh = 0; vh < nv; vh++) {
+                const int64_t kh = vh % nk;
+                float *s = ssm_state.data() + ((size_t)dst * n_rec + ri) * ssm_len + vh * hv * hv;
+                const float *s_in = ssm_state.data() + ((size_t)src * n_rec + ri) * ssm_len + vh * hv * hv;
+                oxo_gated_delta_net_step_f32_from(s, s_in, conv.data() + kh * ds, conv.data() + nk * ds + kh * ds,
+                                                  conv.data() + 2 * nk * ds + vh * hv, gate[vh], beta_s[vh], hv, gdn.data());
+                oxo_rms_norm_mul_f32(gdn.data(), L.ssm_norm.data(), tmpn.data(), hv, eps);
+                oxo_silu_f32((int)hv, zs.data(), z[ln].data() + vh * hv);
+                for (int64_t j = 0; j < hv; j++) o[ln][vh * hv + j] = tmpn[j] * zs[j];
+            }
+        }
+        mixer_out(l, nl, d.ssm_d_inner);
+    }
+
+    void mixer_out(int l, int nl, int64_t width) {
+        Layer &L = layers[l];
+        const int64_t E = d.n_embd;
+        std::vector<const float *> xs;
+        std::vector<std::vector<float>> t(nl, std::vector<float>(E));
+        std::vector<float *> ys;
+        for (int ln = 0; ln < nl; ln++) { xs.push_back(o[ln].data()); ys.push_back(t[ln].data()); }
+        (void)width;
+        mv(L.out, xs, ys);
+        for (int ln = 0; ln < nl; ln++)
+            for (int64_t i = 0; i < E; i++) x1[ln][i] = t[ln][i] + xin[ln][i];
+    }
+
+    // attn_qkv + attn_kv + write_k (engine.rs:2614-2739): projections for all lanes; K and V of
+    // every lane written at pos0 + lane before any lane attends
+    void attn_kv(int l, int nl, int64_t pos0, const std::vector<std::vector<float>> &xn) {
+        Layer &L = layers[l];
+        const int64_t hd = d.head_dim, nkv = d.n_head_kv;
+        const int ai = L.index;
+        std::vector<const float *> xs;
+        std::vector<std::vector<float>> kraw(nl, std::vector<float>(nkv * hd)), vv(nl, std::vector<float>(nkv * hd));
+        std::vector<float *> ko, vo;
+        for (int ln = 0; ln < nl; ln++) { xs.push_back(xn[ln].data()); ko.push_back(kraw[ln].data()); vo.push_back(vv[ln].data()); }
+        mv(L.wk, xs, ko);
+        mv(L.wv, xs, vo);
+        std::vector<float> kn(hd);
+        for (int ln = 0; ln < nl; ln++) {
+            const int64_t p = pos0 + ln;
+            for (int64_t r = 0; r < nkv * hd; r++)
+                vcache[((size_t)ai * nkv * hd + r) * v_stride + p] = oxo_f32_to_f16(vv[ln][r]);
+            for (int64_t kvh = 0; kvh < nkv; kvh++) {
+                oxo_rms_norm_mul_f32(kraw[ln].data() + kvh * hd, L.k_norm.data(), kn.data(), hd, d.rms_eps);
+                oxo_rope_neox_inplace(kn.data(), d.n_rot, rope_tab.data() + p * d.n_rot);
+                uint16_t *kr = kcache.data() + (((size_t)ai * nkv + kvh) * n_ctx + p) * hd;
+                for (int64_t i = 0; i < hd; i++) kr[i] = oxo_f32_to_f16(kn[i]);
+            }
+        }
+    }
+
+    void attention(int l, int nl, int64_t pos0) {
+        Layer &L = layers[l];
+        const int64_t E = d.n_embd, hd = d.head_dim, nkv = d.n_head_kv, nh = d.n_head, group = nh / nkv;
+        const int ai = L.index;
+        std::vector<std::vector<float>> xn(nl, std::vector<float>(E)), qg(nl, std::vector<float>(nh * 2 * hd));
+        std::vector<const float *> xs;
+        std::vector<float *> qo;
+        for (int ln = 0; ln < nl; ln++) {
+            oxo_rms_norm_mul_f32(xin[ln].data(), L.attn_norm.data(), xn[ln].data(), E, d.rms_eps);
+            xs.push_back(xn[ln].data());
+            qo.push_back(qg[ln].data());
+        }
+        mv(L.wq, xs, qo);
+        attn_kv(l, nl, pos0, xn);
+        const float scale = 1.0f / sqrtf((float)hd);
+        for (int ln = 0; ln < nl; ln++) {
+            const int64_t p = pos0 + ln;
+            const int n_kv = (int)padded_n_kv(p, n_ctx);
+#pragma omp parallel for schedule(static)
+            for (int64_t h = 0; h < nh; h++) {
+                std::vector<float> q(hd), aout(hd), gs(hd);
+                oxo_rms_norm_mul_f32(qg[ln].data() + h * 2 * hd, L.q_norm.data(), q.data(), hd, d.rms_eps);
+                oxo_rope_neox_inplace(q.data(), d.n_rot, rope_tab.data() + p * d.n_rot);
+                const int64_t kvh = h / group;
+                const uint16_t *kb = kcache.data() + ((size_t)ai * nkv + kvh) * n_ctx * hd;
+                const uint16_t *vb = vcache.data() + ((size_t)ai * nkv * hd + kvh * hd) * v_stride;
+                oxo_attn_head_f16(q.data(), kb, hd, kb + p * hd, vb, v_stride, n_kv, (int)p, (int)hd, scale, aout.data());
+                oxo_sigmoid_f32(hd, gs.data(), qg[ln].data() + h * 2 * hd + hd);
+                for (int64_t j = 0; j < hd; j++) o[ln][h * hd + j] = aout[j] * gs[j];
+            }
+        }
+        mixer_out(l, nl, nh * hd);
+    }
+
+    // moe_router + route + moe_gate_up + moe_down (engine.rs:3372-3624)
+    void moe(int l, int nl) {
+        Layer &L = layers[l];
+        const int64_t E = d.n_embd, F = d.ff_exp, K = d.n_expert_used, NE = d.n_expert;
+        for (int ln = 0; ln < nl; ln++) {
+            std::vector<float> xn(E);
+            oxo_rms_norm_mul_f32(x1[ln].data(), L.post_norm.data(), xn.data(), E, d.rms_eps);
+            std::vector<float> lg(NE);
+#pragma omp parallel for schedule(static)
+            for (int64_t e = 0; e < NE; e++) lg[e] = oxo_vec_dot_f32((int)E, L.router.data() + e * E, xn.data());
+            const float sgd = oxo_vec_dot_f32((int)E, L.shexp_gate.data(), xn.data());
+            float sg;
+            oxo_sigmoid_f32(1, &sg, &sgd);
+            std::vector<float> gsh(d.ff_shexp), ush(d.ff_shexp), hsh(d.ff_shexp);
+            mv(L.gate_sh, {xn.data()}, {gsh.data()});
+            mv(L.up_sh, {xn.data()}, {ush.data()});
+            oxo_swiglu_f32(d.ff_shexp, hsh.data(), gsh.data(), ush.data());
+            // route (engine.rs:3414-3429)
+            std::vector<float> probs(NE), wp(NE);
+            oxo_soft_max_f32((int)NE, probs.data(), lg.data(), 1.0f, nullptr, wp.data());
+            std::vector<int32_t> ids(K), scr(NE);
+            int tie = 0;
+            oxo_argsort_top_k_f32(probs.data(), (int)NE, (int)K, ids.data(), scr.data(), &tie);
+            tie_count += tie;
+            std::vector<float> w(K);
+            for (int64_t j = 0; j < K; j++) w[j] = probs[ids[j]];
+            float s = oxo_vec_sum_f32((int)K, w.data());
+            s = std::max(std::min(s, INFINITY), 6.103515625e-5f);
+            for (int64_t j = 0; j < K; j++) w[j] = w[j] / s;
+            // experts
+            std::vector<std::vector<float>> dn(K, std::vector<float>(E));
+            for (int64_t j = 0; j < K; j++) {
+                const Q8 &wg = expert(l, ids[j], 0), &wu = expert(l, ids[j], 1), &wdn = expert(l, ids[j], 2);
+                std::vector<float> g(F), u(F), h(F);
+                mv(wg, {xn.data()}, {g.data()});
+                mv(wu, {xn.data()}, {u.data()});
+                oxo_swiglu_f32((int)F, h.data(), g.data(), u.data());
+                mv(wdn, {h.data()}, {dn[j].data()});
+            }
+            std::vector<float> dsh(E);
+            mv(L.down_sh, {hsh.data()}, {dsh.data()});
+            for (int64_t i = 0; i < E; i++) {
+                float m = dn[0][i] * w[0];
+                for (int64_t j = 1; j < K; j++) {
+                    const float p = dn[j][i] * w[j];
+                    m = m + p;
+                }
+                const float sh = dsh[i] * sg;
+                const float f = m + sh;
+                x2[ln][i] = f + x1[ln][i];
+            }
+        }
+    }
+
+    // head (engine.rs:3630-3715) + gather_argmax (1969-1987)
+    void head(int nl, uint32_t mask, const std::vector<float> &norm) {
+        const int64_t E = d.n_embd, V = d.n_vocab;
+        for (int ln = 0; ln < nl; ln++) {
+            oxo_rms_norm_mul_f32(x2[ln].data(), norm.data(), hout[ln].data(), E, d.rms_eps);
+            if (!(mask & (1u << ln))) continue;
+            std::vector<float> lg(V);
+            mv(output, {hout[ln].data()}, {lg.data()});
+            float best = -INFINITY;
+            uint32_t bi = UINT32_MAX;
+            for (int64_t r = 0; r < V; r++)
+                if (lg[r] > best) { best = lg[r]; bi = (uint32_t)r; }
+            argmax[ln] = bi == UINT32_MAX ? 0 : bi;
+            if (keep_logits) logits[ln] = lg;
+        }
+    }
+
+    void run_layer(int l, int nl, int64_t pos0, const uint32_t *toks) {
+        if (l == 0)
+            for (int ln = 0; ln < nl; ln++) xin[ln] = embed(toks[ln]);
+        else
+            for (int ln = 0; ln < nl; ln++) xin[ln] = x2[ln];
+        if (layers[l].att) attention(l, nl, pos0);
+        else recurrent(l, nl);
+        moe(l, nl);
+    }
+
+    int verify(const uint32_t *toks, int n, uint32_t *out) {
+        if (n < 1 || n > n_slots || pos + n > n_ctx) return -1;
+        pend_pos0 = pos;
+        pend_cur = cur_slot;
+        pend_n = n;
+        pend_done = 0;
+        for (int l = 0; l < d.n_layer; l++) run_layer(l, n, pos, toks);
+        head(n, (1u << n) - 1, out_norm);
+        for (int ln = 0; ln < n; ln++) out[ln] = argmax[ln];
+        return 0;
+    }
+
+    void zero_v(int64_t a, int64_t b) {
+        if (b <= a) return;
+        const int64_t rows = (int64_t)(n_att - (d.has_mtp ? 1 : 0)) * d.n_head_kv * d.head_dim;
+        for (int64_t r = 0; r < rows; r++)
+            for (int64_t p = a; p < b; p++) vcache[(size_t)r * v_stride + p] = 0;
+    }
+
+    int commit(int m) {
+        if (pend_n == 0) return -1;
+        const int hi = pend_done == 0 ? pend_n : pend_done;
+        if (m < 1 || m > hi) return -1;
+        zero_v(pend_pos0 + m, pend_pos0 + hi);
+        pos = pend_pos0 + m;
+        cur_slot = (pend_cur + m - 1) % n_slots;
+        pend_done = m;
+        return 0;
+    }
+
+    // mtp_entry (engine.rs:2362-2390): x2 = eh_proj . [enorm(embd(tok)); hnorm(h)]
+    void mtp_entry(int nl, const uint32_t *toks) {
+        Layer &L = layers[d.n_layer];
+        const int64_t E = d.n_embd;
+        std::vector<std::vector<float>> cat(nl, std::vector<float>(2 * E));
+        std::vector<const float *> xs;
+        std::vector<float *> ys;
+        for (int ln = 0; ln < nl; ln++) {
+            std::vector<float> e = embed(toks[ln]);
+            oxo_rms_norm_mul_f32(e.data(), L.enorm.data(), cat[ln].data(), E, d.rms_eps);
+            oxo_rms_norm_mul_f32(hin[ln].data(), L.hnorm.data(), cat[ln].data() + E, E, d.rms_eps);
+            xs.push_back(cat[ln].data());
+            ys.push_back(x2[ln].data());
+        }
+        mv(L.eh_proj, xs, ys);
+    }
+
+    uint32_t mtp_run(const uint32_t *toks, int n, int64_t pos0, const float *hs, int head_last) {
+        const int l = d.n_layer;
+        for (int ln = 0; ln < n; ln++) std::memcpy(hin[ln].data(), hs + ln * d.n_embd, d.n_embd * 4);
+        mtp_entry(n, toks);
+        for (int ln = 0; ln < n; ln++) xin[ln] = x2[ln];
+        attention(l, n, pos0);
+        moe(l, n);
+        head(n, head_last ? 1u << (n - 1) : 0u, layers[l].head_norm);
+        return head_last ? argmax[n - 1] : UINT32_MAX;
+    }
+
+    // mtp_seed (engine.rs:2077-2091, 2121-2136): entry + attn_norm + K/V rows only
+    void mtp_seed(const uint32_t *toks, int n, int64_t pos0, const float *hs) {
+        const int l = d.n_layer;
+        for (int ln = 0; ln < n; ln++) std::memcpy(hin[ln].data(), hs + ln * d.n_embd, d.n_embd * 4);
+        mtp_entry(n, toks);
+        std::vector<std::vector<float>> xn(n, std::vector<float>(d.n_embd));
+        for (int ln = 0; ln < n; ln++)
+            oxo_rms_norm_mul_f32(x2[ln].data(), layers[l].attn_norm.data(), xn[ln].data(), d.n_embd, d.rms_eps);
+        attn_kv(l, n, pos0, xn);
+    }
+};
+
+// ---- MtpDriver (crates/model/src/mtp.rs:314-608), depth 1..
+struct oxo_driver {
+    oxo_engine *eng = nullptr;
+    int depth = 1;
+    int64_t q = 0;
+    std::vector<uint32_t> cu_tok;
+    std::vector<float> cu_h;
+    std::vector<float> hl;
+    int64_t steps = 0, drafted = 0, accepted = 0, tokens_out = 0;
+
+    int mtp_lanes() const { return eng->max_lanes; }
+
+    void note(int64_t p0, const uint32_t *toks, int n) {
+        const int64_t E = eng->d.n_embd;
+        for (int i = 0; i < n; i++) {
+            const int64_t p = p0 + i;
+            if (p >= q) {
+                cu_tok.push_back(toks[i]);
+                if (i == 0) cu_h.insert(cu_h.end(), hl.begin(), hl.end());
+                else cu_h.insert(cu_h.end(), eng->hout[i - 1].begin(), eng->hout[i - 1].end());
+            }
+        }
+        hl = eng->hout[n - 1];
+        (void)E;
+    }
+
+    void flush(size_t keep) {
+        const int64_t E = eng->d.n_embd;
+        while (cu_tok.size() > keep) {
+            const int n = (int)std::min<size_t>(mtp_lanes(), cu_tok.size());
+            eng->mtp_seed(cu_tok.data(), n, q, cu_h.data());
+            cu_tok.erase(cu_tok.begin(), cu_tok.begin() + n);
+            cu_h.erase(cu_h.begin(), cu_h.begin() + n * E);
+            q += n;
+        }
+    }
+
+    uint32_t prefill(const uint32_t *toks, int n) {
+        uint32_t next = UINT32_MAX;
+        for (int c0 = 0; c0 < n; c0 += eng->n_slots) {
+            const int c = std::min(eng->n_slots, n - c0);
+            const int64_t p0 = eng->pos;
+            uint32_t g[8];
+            eng->verify(toks + c0, c, g);
+            eng->commit(c);
+            next = g[c - 1];
+            note(p0, toks + c0, c);
+            flush(mtp_lanes() - 1);
+        }
+        return next;
+    }
+
+    // MtpDriver::step (mtp.rs:522-592); `override_d1` >= 0 replaces the draft (test hook, mtp.rs:554-558)
+    int step(uint32_t x, uint32_t *out, int64_t override_d1) {
+        const int64_t p = eng->pos;
+        const int64_t k = std::min<int64_t>(depth, std::max<int64_t>(0, eng->n_ctx - (p + 1)));
+        flush(mtp_lanes() - 1);
+        if (k == 0) {
+            uint32_t g[8];
+            eng->verify(&x, 1, g);
+            eng->commit(1);
+            note(p, &x, 1);
+            out[0] = g[0];
+            return 1;
+        }
+        flush(0);
+        uint32_t drafts[8];
+        drafts[0] = eng->mtp_run(&x, 1, p, hl.data(), 1);
+        q = p + 1;
+        std::vector<float> h = eng->hout[0];
+        for (int64_t i = 1; i < k; i++) {
+            drafts[i] = eng->mtp_run(&drafts[i - 1], 1, p + i, h.data(), 1);
+            h = eng->hout[0];
+        }
+        if (override_d1 >= 0) drafts[0] = (uint32_t)override_d1;
+        uint32_t vt[8];
+        vt[0] = x;
+        for (int64_t i = 0; i < k; i++) vt[1 + i] = drafts[i];
+        uint32_t g[8];
+        eng->verify(vt, (int)k + 1, g);
+        int a = 0;
+        while (a < k && drafts[a] == g[a]) a++;
+        eng->commit(a + 1);
+        note(p, vt, a + 1);
+        steps++;
+        drafted += k;
+        accepted += a;
+        tokens_out += a + 1;
+        for (int i = 0; i <= a; i++) out[i] = g[i];
+        return a + 1;
+    }
+};
+
+extern "C" {
+
+oxo_engine *oxo_engine_new(const oxe_model_desc *d, uint64_t seed, int64_t n_ctx) {
+    oxo_engine *e = new oxo_engine();
+    e->init(*d, seed, n_ctx);
+    return e;
+}
+void oxo_engine_free(oxo_engine *e) { delete e; }
+void oxo_engine_reset(oxo_engine *e) { e->reset(); }
+int oxo_verify(oxo_engine *e, const uint32_t *toks, int n, uint32_t *out) { return e->verify(toks, n, out); }
+int oxo_commit(oxo_engine *e, int m) { return e->commit(m); }
+uint32_t oxo_step(oxo_engine *e, uint32_t tok) {
+    uint32_t g[8];
+    if (e->verify(&tok, 1, g) != 0) return UINT32_MAX;
+    e->commit(1);
+    return g[0];
+}
+uint32_t oxo_mtp_run(oxo_engine *e, const uint32_t *toks, int n, int64_t pos0, const float *hs, int head_last) {
+    return e->mtp_run(toks, n, pos0, hs, head_last);
+}
+void oxo_mtp_seed(oxo_engine *e, const uint32_t *toks, int n, int64_t pos0, const float *hs) { e->mtp_seed(toks, n, pos0, hs); }
+int64_t oxo_pos(const oxo_engine *e) { return e->pos; }
+int oxo_cur_slot(const oxo_engine *e) { return e->cur_slot; }
+int oxo_tie_count(const oxo_engine *e) { return e->tie_count; }
+const float *oxo_hidden(const oxo_engine *e, int lane) { return e->hout[lane].data(); }
+const float *oxo_logits(const oxo_engine *e, int lane) { return e->logits[lane].data(); }
+int64_t oxo_n_ctx(const oxo_engine *e) { return e->n_ctx; }
+void oxo_set_keep_logits(oxo_engine *e, int on) { e->keep_logits = on != 0; }
+
+// raw state views for parity checks: K cache [att][kvh][n_ctx][hd] f16, V^T [att][kvh*hd][n_ctx] f16,
+// conv [slot][rec][(kc-1)*channels], S [slot][rec][nv][hv][hv]
+const uint16_t *oxo_kcache(const oxo_engine *e) { return e->kcache.data(); }
+const uint16_t *oxo_vcache(const oxo_engine *e) { return e->vcache.data(); }
+float *oxo_conv_state(oxo_engine *e) { return e->conv_state.data(); }
+float *oxo_ssm_state(oxo_engine *e) { return e->ssm_state.data(); }
+uint16_t *oxo_kcache_mut(oxo_engine *e) { return e->kcache.data(); }
+uint16_t *oxo_vcache_mut(oxo_engine *e) { return e->vcache.data(); }
+void oxo_set_pos(oxo_engine *e, int64_t pos) { e->pos = pos; }
+
+// one mixer + MoE layer for parity of configs 2/3: x[nl][E] is the layer input, x2 out
+void oxo_mixer(oxo_engine *e, int l, int nl, int64_t pos0, const float *x, float *out) {
+    for (int ln = 0; ln < nl; ln++) std::memcpy(e->xin[ln].data(), x + ln * e->d.n_embd, e->d.n_embd * 4);
+    if (e->layers[l].att) e->attention(l, nl, pos0);
+    else e->recurrent(l, nl);
+    for (int ln = 0; ln < nl; ln++) std::memcpy(out + ln * e->d.n_embd, e->x1[ln].data(), e->d.n_embd * 4);
+}
+void oxo_moe(oxo_engine *e, int l, int nl, const float *x1, float *x2) {
+    for (int ln = 0; ln < nl; ln++) std::memcpy(e->x1[ln].data(), x1 + ln * e->d.n_embd, e->d.n_embd * 4);
+    e->moe(l, nl);
+    for (int ln = 0; ln < nl; ln++) std::memcpy(x2 + ln * e->d.n_embd, e->x2[ln].data(), e->d.n_embd * 4);
+}
+
+oxo_driver *oxo_driver_new(oxo_engine *e, int depth) {
+    oxo_driver *d = new oxo_driver();
+    d->eng = e;
+    d->depth = depth;
+    d->q = e->pos;
+    d->hl.assign(e->d.n_embd, 0.0f);
+    return d;
+}
+void oxo_driver_free(oxo_driver *d) { delete d; }
+uint32_t oxo_driver_prefill(oxo_driver *d, const uint32_t *toks, int n) { return d->prefill(toks, n); }
+int oxo_driver_step(oxo_driver *d, uint32_t x, uint32_t *out, int64_t override_d1) { return d->step(x, out, override_d1); }
+void oxo_driver_stats(const oxo_driver *d, int64_t *st) {
+    st[0] = d->steps; st[1] = d->drafted; st[2] = d->accepted; st[3] = d->tokens_out;
+}
+
+}  // extern "C"
+
+extern "C" {
+// Synthetic tensors of include/oxe_model.h on the host (inputs for parity tests).
+void oxo_synth_q8(uint64_t seed, int layer, int kind, int64_t expert, int64_t rows, int64_t k, int8_t *q, uint16_t *d) {
+    Q8 m;
+    gen_q8(seed, layer, kind, rows, k, expert, m);
+    std::memcpy(q, m.q.data(), m.q.size());
+    std::memcpy(d, m.d.data(), m.d.size() * 2);
+}
+void oxo_synth_f32(uint64_t seed, int layer, int kind, int64_t n, float *out) {
+    std::vector<float> v = gen_f32(seed, layer, kind, n);
+    std::memcpy(out, v.data(), n * 4);
+}
+// mu + sigma * z with the Irwin-Hall z of the generator, under the key of (seed, uid)
+void oxo_synth_normal(uint64_t seed, uint64_t uid, int64_t n, float mu, float sigma, float *out) {
+    const uint64_t key = oxe_rng(seed, uid);
+    for (int64_t i = 0; i < n; i++) {
+        const float t = sigma * oxe_synth_z(key, (uint64_t)i);
+        out[i] = mu + t;
+    }
+}
+}

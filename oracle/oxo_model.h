@@ -1,0 +1,48 @@
+// TEST INFRASTRUCTURE ONLY (see oxo.h). C API of the oracle engine and MTP driver (model.cpp).
+#pragma once
+#include <stdint.h>
+#include "../include/oxe_model.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+typedef struct oxo_engine oxo_engine;
+typedef struct oxo_driver oxo_driver;
+
+oxo_engine *oxo_engine_new(const oxe_model_desc *d, uint64_t seed, int64_t n_ctx);
+void oxo_engine_free(oxo_engine *e);
+void oxo_engine_reset(oxo_engine *e);
+int oxo_verify(oxo_engine *e, const uint32_t *toks, int n, uint32_t *out);      // engine.rs:2002-2025
+int oxo_commit(oxo_engine *e, int m);                                          // engine.rs:2030-2039
+uint32_t oxo_step(oxo_engine *e, uint32_t tok);                                // engine.rs:1991-1997
+uint32_t oxo_mtp_run(oxo_engine *e, const uint32_t *toks, int n, int64_t pos0, const float *hs, int head_last); // engine.rs:2044-2071
+void oxo_mtp_seed(oxo_engine *e, const uint32_t *toks, int n, int64_t pos0, const float *hs); // engine.rs:2077-2091
+int64_t oxo_pos(const oxo_engine *e);
+int oxo_cur_slot(const oxo_engine *e);
+int oxo_tie_count(const oxo_engine *e);
+const float *oxo_hidden(const oxo_engine *e, int lane);
+const float *oxo_logits(const oxo_engine *e, int lane);
+int64_t oxo_n_ctx(const oxo_engine *e);
+void oxo_set_keep_logits(oxo_engine *e, int on);
+const uint16_t *oxo_kcache(const oxo_engine *e);
+const uint16_t *oxo_vcache(const oxo_engine *e);
+float *oxo_conv_state(oxo_engine *e);
+float *oxo_ssm_state(oxo_engine *e);
+uint16_t *oxo_kcache_mut(oxo_engine *e);
+uint16_t *oxo_vcache_mut(oxo_engine *e);
+void oxo_set_pos(oxo_engine *e, int64_t pos);
+void oxo_mixer(oxo_engine *e, int l, int nl, int64_t pos0, const float *x, float *x1);
+void oxo_moe(oxo_engine *e, int l, int nl, const float *x1, float *x2);
+
+void oxo_synth_q8(uint64_t seed, int layer, int kind, int64_t expert, int64_t rows, int64_t k, int8_t *q, uint16_t *d);
+void oxo_synth_f32(uint64_t seed, int layer, int kind, int64_t n, float *out);
+void oxo_synth_normal(uint64_t seed, uint64_t uid, int64_t n, float mu, float sigma, float *out);
+
+oxo_driver *oxo_driver_new(oxo_engine *e, int depth);                          // mtp.rs:348-362
+void oxo_driver_free(oxo_driver *d);
+uint32_t oxo_driver_prefill(oxo_driver *d, const uint32_t *toks, int n);      // mtp.rs:450-463
+int oxo_driver_step(oxo_driver *d, uint32_t x, uint32_t *out, int64_t override_d1); // mtp.rs:522-592
+void oxo_driver_stats(const oxo_driver *d, int64_t *st);
+#ifdef __cplusplus
+}
+#endif

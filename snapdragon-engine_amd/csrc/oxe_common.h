@@ -1,0 +1,158 @@
+// Device-side building blocks shared by the gfx950 kernels: binary16 conversions, the integer
+// dot, wave shuffles, and the exact-reduction helpers that let a parallel GPU reduction return the
+// same bits as the reference's sequential double-precision sums.
+//
+// Every kernel source is compiled with -ffp-contract=off (no implicit fusion) and correctly rounded
+// f32 division/sqrt, so each float operation below is one IEEE operation, as in the reference.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/oxe_model.h"
+#include "oxe_libm.h"
+
+#define OXE_DEV __device__ __forceinline__
+
+namespace oxe {
+
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+
+OXE_DEV float h2f(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
+// v_cvt_f16_f32 under the default round-to-nearest-even mode (= __fp16 conversion on aarch64)
+OXE_DEV uint16_t f2h(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
+OXE_DEV _Float16 hbits(uint16_t h) { return __builtin_bit_cast(_Float16, h); }
+OXE_DEV uint16_t bitsh(_Float16 h) { return __builtin_bit_cast(uint16_t, h); }
+
+// 4 x int8 dot with int32 accumulate (v_dot4_i32_i8): exact integer arithmetic
+OXE_DEV int32_t dot4(uint32_t a, uint32_t b, int32_t c) {
+    return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
+}
+OXE_DEV int32_t dot16(uint4 a, uint4 b, int32_t c) {
+    c = dot4(a.x, b.x, c);
+    c = dot4(a.y, b.y, c);
+    c = dot4(a.z, b.z, c);
+    return dot4(a.w, b.w, c);
+}
+
+OXE_DEV float shfl_xor_f(float v, int m) { return __shfl_xor(v, m, 64); }
+OXE_DEV double shfl_xor_d(double v, int m) { return __shfl_xor(v, m, 64); }
+OXE_DEV int shfl_xor_i(int v, int m) { return __shfl_xor(v, m, 64); }
+
+// ggml_v_expf NEON (vendor/ggml-subset/generated/upstream/src/ggml-cpu/vec.h:1154-1175), one lane
+OXE_DEV float v_expf(float x) {
+    const float r = 0x1.8p23f;
+    const float z = __builtin_fmaf(x, 0x1.715476p+0f, r);
+    const float n = z - r;
+    const float b = __builtin_fmaf(-n, 0x1.7f7d1cp-20f, __builtin_fmaf(-n, 0x1.62e4p-1f, x));
+    const uint32_t e = __builtin_bit_cast(uint32_t, z) << 23;
+    const float k = __builtin_bit_cast(float, e + 0x3f800000u);
+    const bool c = __builtin_fabsf(n) > 126.0f;
+    const float u = b * b;
+    const float j = __builtin_fmaf(__builtin_fmaf(__builtin_fmaf(0x1.0e4020p-7f, b, 0x1.573e2ep-5f), u,
+                                                  __builtin_fmaf(0x1.555e66p-3f, b, 0x1.fffdb6p-2f)),
+                                   u, 0x1.ffffecp-1f * b);
+    if (!c) return __builtin_fmaf(j, k, k);
+    const uint32_t d = (n <= 0.0f) ? 0x82000000u : 0u;
+    const float s1 = __builtin_bit_cast(float, d + 0x7f000000u);
+    const float s2 = __builtin_bit_cast(float, e - d);
+    if (__builtin_fabsf(n) > 192.0f) return s1 * s1;
+    return __builtin_fmaf(s2, j, s2) * s1;
+}
+// ggml_v_silu (vec.h:1178-1185)
+OXE_DEV float v_silu(float x) { return x / (1.0f + v_expf(0.0f - x)); }
+// op_sigmoid with the C library's expf (crates/kernels-sys/csrc/oxe_ops.cpp:80-84)
+OXE_DEV float sigmoid_c(float x) { return 1.f / (1.f + oxe_libm::expf_c(-x)); }
+// op_softplus (oxe_ops.cpp:85-89)
+OXE_DEV float softplus_c(float x) { return (x > 20.0f) ? x : oxe_libm::log1pf_c(oxe_libm::expf_c(x)); }
+
+// quantize_row_q8_0, NEON branch (vendor/ggml-subset/generated/quants_subset.c:6-42), one thread
+// per 32-value block: amax (exact), d = amax/127, id = d ? 1/d : 0 from the f32 d, fp16(d) by RNE,
+// codes = round-to-nearest-even(x * id) (vcvtnq_s32_f32).
+OXE_DEV void quant_block_q8_0(const float *x, int8_t *q, uint16_t *d) {
+    float v[32];
+#pragma unroll
+    for (int j = 0; j < 32; j += 4) {
+        const float4 f = *(const float4 *)(x + j);
+        v[j] = f.x; v[j + 1] = f.y; v[j + 2] = f.z; v[j + 3] = f.w;
+    }
+    float amax = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 32; j++) amax = fmaxf(amax, __builtin_fabsf(v[j]));
+    const float dd = amax / 127.0f;
+    const float id = dd != 0.0f ? 1.0f / dd : 0.0f;
+    *d = f2h(dd);
+    uint32_t packed[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        uint32_t u = 0;
+#pragma unroll
+        for (int b = 0; b < 4; b++) {
+            const int32_t qi = (int32_t)__builtin_rintf(v[4 * j + b] * id);
+            u |= ((uint32_t)(qi & 0xff)) << (8 * b);
+        }
+        packed[j] = u;
+    }
+    *(uint4 *)q = make_uint4(packed[0], packed[1], packed[2], packed[3]);
+    *(uint4 *)(q + 16) = make_uint4(packed[4], packed[5], packed[6], packed[7]);
+}
+
+// ---- block reductions (blockDim.x threads, all participating)
+
+template <int NT>
+OXE_DEV double block_sum_d(double v, double *red) {
+    for (int m = 32; m >= 1; m >>= 1) v += shfl_xor_d(v, m);
+    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    if (lane == 0) red[w] = v;
+    __syncthreads();
+    double s = 0.0;
+    if (threadIdx.x == 0) {
+        for (int i = 0; i < NT / 64; i++) s += red[i];
+        red[NT / 64] = s;
+    }
+    __syncthreads();
+    s = red[NT / 64];
+    __syncthreads();
+    return s;
+}
+
+template <int NT>
+OXE_DEV float block_max_f(float v, float *red) {
+    for (int m = 32; m >= 1; m >>= 1) {
+        const float o = shfl_xor_f(v, m);
+        v = (v > o) ? v : o;
+    }
+    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    if (lane == 0) red[w] = v;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float s = red[0];
+        for (int i = 1; i < NT / 64; i++) s = (s > red[i]) ? s : red[i];
+        red[NT / 64] = s;
+    }
+    __syncthreads();
+    const float s = red[NT / 64];
+    __syncthreads();
+    return s;
+}
+
+// Exact-match helper for the reference's sequential double sums.
+// The reference forms S = (((0 + t0) + t1) + ...) over m terms in double and only uses a float
+// derived from S by a monotone map g (g(S) = (float)(S / n) or (float)(1.0 / S)). Both S and a
+// parallel tree sum P lie within (m - 1) * 2^-53 * sum|t_i| of the exact sum, so with
+// B = (m + 64) * 2^-52 * sum|t_i|, g(P - B) == g(P + B) proves g(S) == g(P); otherwise the caller
+// replays the sequential sum (rare: the interval must straddle a float rounding edge).
+OXE_DEV double bracket_width(double abs_sum, int m) { return abs_sum * (double)(m + 64) * 0x1p-52; }
+OXE_DEV bool bracket_ok_mean(double p, double abs_sum, int m, double n, float *out) {
+    const double b = bracket_width(abs_sum, m);
+    const float lo = (float)((p - b) / n), hi = (float)((p + b) / n);
+    *out = (float)(p / n);
+    return lo == hi;
+}
+OXE_DEV bool bracket_ok_recip(double p, double abs_sum, int m, float *out) {
+    const double b = bracket_width(abs_sum, m);
+    const float lo = (float)(1.0 / (p + b)), hi = (float)(1.0 / (p - b));
+    *out = (float)(1.0 / p);
+    return lo == hi;
+}
+
+}  // namespace oxe

@@ -1,0 +1,104 @@
+// Device-resident state of the MI355X decode engine: weight arena, recurrent slots, KV cache,
+// per-lane activations and the run control block every kernel reads.
+//
+// Reference state (crates/model/src/engine.rs:393-560, 918-953): conv/ssm state [slot][layer],
+// K cache [layer][kv head][pos][head_dim] f16, V^T cache [layer][kv head*head_dim + dim][pos] f16,
+// lanes of up to MAX_LANES tokens. Here all of it lives in HBM; the host never reads it on the hot
+// path. Lanes per kernel launch: at most OXE_NL (2, the verify width of depth-1 MTP).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/oxe_model.h"
+
+namespace oxe {
+
+constexpr int OXE_NL = 2;           // lanes per launch (verify width; MTP seeding batches by 2)
+constexpr int OXE_MAX_EXP_USED = 8; // top-k of the router
+constexpr int OXE_MAX_UNION = 16;   // union of two lanes' top-8
+
+// Q8_0 matrix in this build's layout: int8 codes [rows][k] + fp16 scales [rows][k/32]
+struct Q8W {
+    int8_t *q = nullptr;
+    uint16_t *d = nullptr;
+    int64_t rows = 0, k = 0;
+};
+
+constexpr int OXE_NSLOTS = OXE_NL + 1;  // recurrent slots: lane i reads slot cur+i, writes cur+i+1 (never in place)
+
+// Run control (device memory). Written by the host through a tiny kernel for host-driven calls and
+// by the commit kernel for the device-driven MTP step; read by every kernel of a run.
+struct RunCtl {
+    int32_t nl;          // lanes of this run (1..OXE_NL)
+    int32_t pos0;        // position of lane 0
+    int32_t cur;         // recurrent slot holding the state before lane 0 (lane i writes slot (cur + i + 1) % OXE_NSLOTS)
+    int32_t head_mask;   // lanes whose LM-head argmax is wanted
+    uint32_t tok[OXE_NL];
+    int32_t hin_sel[OXE_NL]; // MTP entry: which hidden buffer feeds lane i (index into hid[])
+    int32_t active;      // 0: every kernel of this run returns at once (conditional MTP seeding)
+    int32_t pad;
+};
+
+// Device-driven MTP depth-1 state (crates/model/src/mtp.rs:314-340 MtpDriver, depth 1)
+struct MtpState {
+    int32_t pos;         // committed position P (tokens in the target)
+    int32_t cur;         // current recurrent slot
+    uint32_t x;          // next token (not yet in the target)
+    int32_t pending;     // 1: pair (pend_tok, hidden buffer HID_PEND) waits for MTP seeding at pos-1
+    uint32_t pend_tok;
+    int32_t n_out;       // tokens emitted so far (ring position in out_tok)
+    int32_t steps, accepted;
+    uint32_t d1;         // draft of the current step
+    int32_t err;         // sticky error bits (1: context full)
+};
+
+// hidden-state buffers ([OXE_NL + 2][n_embd] floats): 0..NL-1 h_nextn per lane of the last run,
+// HID_HL the target h of position pos-1 (MtpDriver.hl), HID_PEND the pending catch-up pair's h.
+constexpr int HID_HL = OXE_NL;
+constexpr int HID_PEND = OXE_NL + 1;
+constexpr int HID_N = OXE_NL + 2;
+
+struct LayerW {
+    int att = 0;    // 1: full attention (+ MTP block), 0: gated delta-net
+    int index = 0;  // recurrent or attention index
+    float *attn_norm = nullptr, *post_norm = nullptr;
+    Q8W proj;       // DN: [qkv | z | beta | alpha]; ATT: [q(+gate) | k | v]
+    Q8W out;        // ssm_out / attn_output [n_embd][4096]
+    float *conv = nullptr, *ssm_a = nullptr, *dt_bias = nullptr, *ssm_norm = nullptr;  // DN
+    float *q_norm = nullptr, *k_norm = nullptr;                                          // ATT
+    float *router = nullptr, *shexp_gate = nullptr;  // [n_expert][n_embd], [n_embd]
+    Q8W shexp_gu;   // shared gate/up, rows interleaved per 16-row tile: 8 gate rows then 8 up rows
+    Q8W shexp_down; // [n_embd][ff_shexp]
+    Q8W exp_gu;     // [n_expert][2*ff_exp][n_embd], per expert interleaved like shexp_gu
+    Q8W exp_down;   // [n_expert][n_embd][ff_exp]
+    Q8W eh_proj;    // MTP block only: [n_embd][2*n_embd]
+    float *enorm = nullptr, *hnorm = nullptr, *head_norm = nullptr;
+};
+
+// Per-lane activation buffers, all [OXE_NL][...]
+struct ActBufs {
+    float *x;          // layer input
+    float *x1;         // after the mixer residual
+    float *x2;         // after the MoE (next layer input)
+    int8_t *xq;        // quantized normalized activations [NL][2*n_embd] (+ scales xd)
+    uint16_t *xd;
+    float *xn;         // normalized f32 (router input) [NL][n_embd]
+    float *proj;       // projection outputs [NL][proj_max]
+    float *gdn;        // delta-net outputs before the gated norm [NL][d_inner]
+    int8_t *oq;        // quantized mixer output [NL][4096] (+ od)
+    uint16_t *od;
+    float *scores;     // attention scores [NL][n_head][n_ctx]
+    float *router_lg;  // [NL][n_expert]
+    float *sh_gate;    // [NL]
+    float *hsh;        // shared expert swiglu [NL][ff_shexp]
+    float *hexp;       // routed expert swiglu [NL][k_used][ff_exp]
+    int32_t *route_ids;   // [NL][k_used]
+    float *route_w;       // [NL][k_used]
+    int32_t *uni;         // [OXE_MAX_UNION + 1]: count, then expert ids in first-use order
+    float *hid;           // [HID_N][n_embd]
+    float *logits;        // [NL][n_vocab] (optional)
+    unsigned long long *amax_key;  // [NL] packed argmax keys
+    uint32_t *counters;   // per-kernel completion counters (zeroed at allocation; self-resetting)
+};
+
+}  // namespace oxe

@@ -1,0 +1,49 @@
+// Argument blocks and launchers of the per-layer decode kernels (k_layer.hip, k_attn.hip,
+// k_moe.hip). Each launcher enqueues one kernel on `st`; kernels read the run's lanes, positions
+// and slots from the device-side RunCtl, so a whole step can be captured once in a HIP graph.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "oxe_engine.h"
+
+namespace oxe {
+
+// ids of the self-resetting completion counters in ActBufs::counters
+enum CounterId { CNT_DN = 0, CNT_ERR_TIE = 64, CNT_ERR_SUM = 65, CNT_N = 128 };
+
+struct ModelRt {
+    // runtime shape
+    int n_layer, n_vocab, n_ctx, n_att;
+    float eps;
+    // global tensors
+    Q8W tok_embd, output;
+    float *out_norm;
+    // state
+    float *conv_state;     // [NSLOTS][n_rec][NCH][KC-1]
+    float *ssm_state;      // [NSLOTS][n_rec][NVH][HV][HV]
+    uint16_t *kcache;      // [n_att][NKV][n_ctx][HD]
+    uint16_t *vcache;      // [n_att][NKV*HD][n_ctx]
+    float *rope;           // [n_ctx][NROT] (cos, sin pairs)
+    int n_rec;
+};
+
+void launch_set_run(RunCtl *ctl, const RunCtl &v, hipStream_t st);
+
+// layer input of the verify: layer 0 embeds the lanes' tokens (tok_embd != null)
+void launch_proj(const RunCtl *ctl, const ModelRt &m, const LayerW &w, const float *x, bool embed, float *x_store,
+                 const ActBufs &b, hipStream_t st, int64_t row_begin = 0);
+void launch_zero_v(const ModelRt &m, int n_att_main, int p0, int p1, hipStream_t st);
+void launch_dn(const RunCtl *ctl, const ModelRt &m, const LayerW &w, const ActBufs &b, hipStream_t st);
+void launch_out(const RunCtl *ctl, const LayerW &w, const float *x, const ActBufs &b, hipStream_t st);
+void launch_kwrite(const RunCtl *ctl, const ModelRt &m, const LayerW &w, const ActBufs &b, hipStream_t st);
+void launch_scores(const RunCtl *ctl, const ModelRt &m, const LayerW &w, const ActBufs &b, hipStream_t st);
+void launch_pv(const RunCtl *ctl, const ModelRt &m, const LayerW &w, const ActBufs &b, hipStream_t st);
+void launch_router(const RunCtl *ctl, const ModelRt &m, const LayerW &w, const ActBufs &b, hipStream_t st);
+void launch_experts(const RunCtl *ctl, const LayerW &w, const ActBufs &b, hipStream_t st);
+void launch_down(const RunCtl *ctl, const LayerW &w, const ActBufs &b, hipStream_t st);
+void launch_head(const RunCtl *ctl, const ModelRt &m, const float *norm_w, const ActBufs &b, bool store_logits,
+                 hipStream_t st);
+void launch_entry(const RunCtl *ctl, const ModelRt &m, const LayerW &w, const ActBufs &b, hipStream_t st);
+
+}  // namespace oxe

@@ -1,0 +1,219 @@
+"""Python binding of liboxe_amd.so (the MI355X C ABI declared in include/oxe_amd.h).
+
+PyTorch is used only for device memory and the current HIP stream; every computation runs in the
+library's own gfx950 kernels. Loading fails loudly when the library is missing: there is no CPU
+fallback anywhere on the product path.
+"""
+import ctypes as C
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "liboxe_amd.so")
+
+_lib = None
+
+
+class NotBuilt(RuntimeError):
+    pass
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        # torch ships its own libamdhip64.so.7 (same soname as the system ROCm one this library
+        # links): load torch first so one HIP runtime serves both in this process.
+        import torch  # noqa: F401
+        if not os.path.exists(LIB_PATH):
+            raise NotBuilt(f"{LIB_PATH} is missing: run `python snapdragon-engine_amd/build.py` (or __graft_entry__.build())")
+        L = C.CDLL(LIB_PATH)
+        vp, i64, i32 = C.c_void_p, C.c_int64, C.c_int
+        sig = {
+            "oxe_hip_quantize_row_q8_0": (i32, [vp, i64, i64, vp, vp, vp]),
+            "oxe_hip_gemv_q8_0": (i32, [i64, i64, i32, vp, vp, vp, vp, vp, vp, vp]),
+        }
+        for name, (res, args) in sig.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def exported_symbols():
+    """Names the header declares and the library must export."""
+    hdr = os.path.join(HERE, "..", "include", "oxe_amd.h")
+    names = []
+    with open(hdr) as f:
+        for line in f:
+            line = line.strip()
+            if line.startswith("OXE_API"):
+                name = line.split("(")[0].split()[-1].lstrip("*")
+                names.append(name)
+    return names
+
+
+def _p(t):
+    return C.c_void_p(t.data_ptr()) if t is not None else None
+
+
+def _stream():
+    import torch
+    return C.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def check(rc, what):
+    if rc != 0:
+        raise RuntimeError(f"{what} failed with status {rc}")
+
+
+# ---- kernel-level entry points (torch tensors on cuda)
+
+def quantize_q8_0(x):
+    """x: float32 [..., k] on the GPU -> (codes int8 [..., k], scales uint16 [..., k/32])."""
+    import torch
+    x = x.contiguous()
+    k = x.shape[-1]
+    nrows = x.numel() // k
+    q = torch.empty(x.shape, dtype=torch.int8, device=x.device)
+    d = torch.empty(x.shape[:-1] + (k // 32,), dtype=torch.int16, device=x.device)
+    check(lib().oxe_hip_quantize_row_q8_0(_p(x), k, nrows, _p(q), _p(d), _stream()), "quantize_q8_0")
+    return q, d
+
+
+def gemv_q8_0(wq, wd, xq, xd, y=None, isum=None):
+    """y[l, r] = Q8_0 GEMV of lanes l (1 or 2) over rows r; optional int32 block sums [nl, nr, k/32]."""
+    import torch
+    nr, k = wq.shape
+    nl = xq.shape[0]
+    if y is None:
+        y = torch.empty((nl, nr), dtype=torch.float32, device=wq.device)
+    check(lib().oxe_hip_gemv_q8_0(k, nr, nl, _p(wq), _p(wd), _p(xq), _p(xd), _p(y), _p(isum), _stream()), "gemv_q8_0")
+    return y
+
+
+# ---- engine level --------------------------------------------------------------------------
+
+def _engine_sigs(L):
+    vp, i64, i32, u32p, f32p = C.c_void_p, C.c_int64, C.c_int, C.POINTER(C.c_uint32), C.POINTER(C.c_float)
+    sig = {
+        "oxe_last_error": (C.c_char_p, []),
+        "oxe_engine_create": (i32, [vp, C.c_uint64, i32, C.POINTER(C.c_void_p)]),
+        "oxe_engine_destroy": (None, [vp]),
+        "oxe_engine_synth_weights": (i32, [vp]),
+        "oxe_engine_verify": (i32, [vp, u32p, i32, u32p]),
+        "oxe_engine_commit": (i32, [vp, i32]),
+        "oxe_engine_step": (i32, [vp, C.c_uint32, u32p]),
+        "oxe_engine_mtp_run": (i32, [vp, u32p, i32, i32, f32p, i32, u32p]),
+        "oxe_engine_mtp_seed": (i32, [vp, u32p, i32, i32, f32p]),
+        "oxe_engine_pos": (i32, [vp]),
+        "oxe_engine_n_ctx": (i32, [vp]),
+        "oxe_engine_hidden": (i32, [vp, i32, f32p]),
+        "oxe_engine_logits": (i32, [vp, i32, f32p]),
+        "oxe_engine_counter": (i32, [vp, i32, u32p]),
+        "oxe_engine_state_copy": (i32, [vp, i32, i32, i64, vp, i64]),
+        "oxe_engine_set_pos": (i32, [vp, i32]),
+        "oxe_engine_device_bytes": (i64, [vp]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(L, name)
+        fn.restype = res
+        fn.argtypes = args
+
+
+def _np_ptr(a, ct):
+    return a.ctypes.data_as(C.POINTER(ct))
+
+
+class Engine:
+    """MI355X engine through the C ABI (Engine::{verify, commit, step, mtp_run, mtp_seed})."""
+
+    def __init__(self, desc, seed=0, n_ctx=1024, synth=True):
+        import numpy as np  # noqa: F401
+        L = lib()
+        if not hasattr(L, "_engine_sigs"):
+            _engine_sigs(L)
+            L._engine_sigs = True
+        self.desc = desc
+        h = C.c_void_p()
+        rc = L.oxe_engine_create(C.byref(desc), seed, n_ctx, C.byref(h))
+        if rc != 0:
+            raise RuntimeError(f"oxe_engine_create: {rc} {L.oxe_last_error()}")
+        self.h = h
+        self.n_ctx = L.oxe_engine_n_ctx(h)
+        if synth:
+            check(L.oxe_engine_synth_weights(h), "synth_weights")
+
+    def close(self):
+        if getattr(self, "h", None):
+            lib().oxe_engine_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()
+
+    def verify(self, toks):
+        import numpy as np
+        t = np.ascontiguousarray(toks, np.uint32)
+        out = np.zeros(8, np.uint32)
+        check(lib().oxe_engine_verify(self.h, _np_ptr(t, C.c_uint32), len(t), _np_ptr(out, C.c_uint32)), "verify")
+        return out[: len(t)].copy()
+
+    def commit(self, m):
+        check(lib().oxe_engine_commit(self.h, m), "commit")
+
+    def step(self, tok):
+        import numpy as np
+        out = np.zeros(1, np.uint32)
+        check(lib().oxe_engine_step(self.h, tok, _np_ptr(out, C.c_uint32)), "step")
+        return int(out[0])
+
+    def mtp_run(self, toks, pos0, hs, head_last=True):
+        import numpy as np
+        t = np.ascontiguousarray(toks, np.uint32)
+        h = np.ascontiguousarray(hs, np.float32)
+        out = np.zeros(1, np.uint32)
+        check(lib().oxe_engine_mtp_run(self.h, _np_ptr(t, C.c_uint32), len(t), pos0, _np_ptr(h, C.c_float),
+                                       int(head_last), _np_ptr(out, C.c_uint32)), "mtp_run")
+        return int(out[0])
+
+    def mtp_seed(self, toks, pos0, hs):
+        import numpy as np
+        t = np.ascontiguousarray(toks, np.uint32)
+        h = np.ascontiguousarray(hs, np.float32)
+        check(lib().oxe_engine_mtp_seed(self.h, _np_ptr(t, C.c_uint32), len(t), pos0, _np_ptr(h, C.c_float)), "mtp_seed")
+
+    @property
+    def pos(self):
+        return int(lib().oxe_engine_pos(self.h))
+
+    def hidden(self, lane):
+        import numpy as np
+        out = np.empty(self.desc.n_embd, np.float32)
+        check(lib().oxe_engine_hidden(self.h, lane, _np_ptr(out, C.c_float)), "hidden")
+        return out
+
+    def logits(self, lane):
+        import numpy as np
+        out = np.empty(self.desc.n_vocab, np.float32)
+        check(lib().oxe_engine_logits(self.h, lane, _np_ptr(out, C.c_float)), "logits")
+        return out
+
+    def counter(self, which):
+        import numpy as np
+        out = np.zeros(1, np.uint32)
+        check(lib().oxe_engine_counter(self.h, which, _np_ptr(out, C.c_uint32)), "counter")
+        return int(out[0])
+
+    def state(self, which, nbytes, offset=0, dtype=None):
+        import numpy as np
+        buf = np.empty(nbytes, np.uint8)
+        check(lib().oxe_engine_state_copy(self.h, which, 0, offset, buf.ctypes.data_as(C.c_void_p), nbytes), "state_copy")
+        return buf.view(dtype) if dtype is not None else buf
+
+    def set_state(self, which, arr, offset=0):
+        import numpy as np
+        a = np.ascontiguousarray(arr)
+        check(lib().oxe_engine_state_copy(self.h, which, 1, offset, a.ctypes.data_as(C.c_void_p), a.nbytes), "state_copy")
+
+    def set_pos(self, pos):
+        check(lib().oxe_engine_set_pos(self.h, pos), "set_pos")

@@ -1,0 +1,74 @@
+"""Engine parity on the GPU: the MI355X engine (C ABI) against the CPU oracle engine on the same
+synthetic model, same tokens. Bar: bit-exact logits, hidden states, argmaxes and KV cache rows
+(the reference's verify-lane batch invariance makes its own noise zero on an all-Q8_0 model)."""
+import numpy as np
+import pytest
+
+import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+N_CTX = 512
+
+
+@pytest.fixture(scope="module")
+def small():
+    import oxe_amd as A
+    d = O.desc_small()
+    return d, A.Engine(d, seed=3, n_ctx=N_CTX), O.Engine(d, seed=3, n_ctx=N_CTX)
+
+
+def bits(a):
+    return np.ascontiguousarray(a, np.float32).view(np.uint32)
+
+
+def test_verify_two_lanes_bitexact(small):
+    d, g, o = small
+    toks = [1234, 77]
+    ag = g.verify(toks)
+    ao = o.verify(toks)
+    for ln in range(2):
+        lg, lo = g.logits(ln), o.logits(ln)
+        hg, ho = g.hidden(ln), o.hidden(ln)
+        assert np.array_equal(bits(hg), bits(ho)), f"hidden lane {ln}: max diff {np.abs(hg - ho).max()}"
+        assert np.array_equal(bits(lg), bits(lo)), f"logits lane {ln}: max diff {np.abs(lg - lo).max()}"
+    assert list(ag) == list(ao)
+    g.commit(2)
+    o.commit(2)
+
+
+def test_steps_and_rollback_bitexact(small):
+    d, g, o = small
+    # a rejected second lane, then more single steps
+    for toks, m in [([5, 4000], 1), ([17], 1), ([300, 301], 2), ([9, 10], 1)]:
+        ag, ao = g.verify(toks), o.verify(toks)
+        assert list(ag) == list(ao)
+        for ln in range(len(toks)):
+            assert np.array_equal(bits(g.logits(ln)), bits(o.logits(ln))), (toks, ln)
+        g.commit(m)
+        o.commit(m)
+        assert g.pos == o.pos
+
+
+def test_mtp_run_and_seed_bitexact(small):
+    d, g, o = small
+    p = g.pos
+    h = o.hidden(0)
+    dg = g.mtp_run([42], p, h[None, :])
+    do = o.mtp_run([42], p, h[None, :])
+    assert dg == do
+    assert np.array_equal(bits(g.hidden(0)), bits(o.hidden(0)))
+    g.mtp_seed([43, 44], p + 1, np.stack([h, h * 0.5]))
+    o.mtp_seed([43, 44], p + 1, np.stack([h, h * 0.5]))
+    n_ctx = g.n_ctx
+    # MTP layer K rows at p+1, p+2 (att index n_att-1 = 1 for the 4-layer model: 1 main + MTP)
+    hd, nkv = 256, 2
+    layer_bytes = nkv * n_ctx * hd * 2
+    kg = g.state(0, layer_bytes, offset=layer_bytes, dtype=np.uint16).reshape(nkv, n_ctx, hd)
+    ko = np.ctypeslib.as_array(O.lib().oxo_kcache(o.h), (2 * nkv * n_ctx * hd,)).reshape(2, nkv, n_ctx, hd)[1]
+    assert np.array_equal(kg[:, : p + 3], ko[:, : p + 3])
+
+
+def test_no_topk_ties(small):
+    d, g, o = small
+    assert g.counter(64) == 0
