@@ -1,0 +1,193 @@
+"""Benchmark: MTP depth-1 decode of the 35B-A3B-shaped int8 (Q8_0) model on one MI355X.
+
+BASELINE.json metric: "MTP-1 decode tok/s (35B-A3B shape, int8) + HBM GB/s as % of ~8 TB/s peak".
+Workload: 40 layers (30 gated delta-net + 10 GQA) + the MTP block, 256 experts
+top-8 + shared expert, vocab 151936, every matmul weight Q8_0, synthetic seeded weights; the
+reference's bench prompt ids (oxe.rs:428-435) of 512 tokens, then greedy MTP-1 steps (draft ->
+2-lane verify -> accept/rollback on the GPU). A "step" is one speculative step; tok/s counts the
+committed tokens (accepted drafts + bonus).
+
+Timing: the prompt is prefilled first (not timed), W warm-up steps, then exactly K steps as K
+HIP-graph launches between two synchronised HIP events on the engine stream. The roofline object
+is for the kernel with the largest share of the step time (from the committed rocprof summary: the
+routed-expert gate/up kernel), timed live with HIP events around each of its launches in eager
+device-driven steps; its algorithmic bytes are the union experts' gate/up weights it streams.
+cpu_baseline: the C++ oracle (the reference algorithm restated, OpenMP over rows) timed on this
+host on a bounded sample of the same workload (see the `sample` field).
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "snapdragon-engine_amd"))
+
+PEAK_HBM_GBS = 8000.0
+
+# ---- algorithmic bytes of the 35B-A3B all-Q8_0 shape (SURVEY 8(d) definition) ----
+Q8 = 34 / 32                                    # bytes per Q8_0 weight (32 codes + fp16 scale)
+E, V = 2048, 151936
+DN_PROJ = 12352 * E * Q8                        # attn_qkv + attn_gate + ssm_beta + ssm_alpha
+ATT_PROJ = (8192 + 512 + 512) * E * Q8          # attn_q (+gate) + attn_k + attn_v
+MIX_OUT = E * 4096 * Q8                         # ssm_out / attn_output
+ROUTER = 256 * E * 4 + E * 4                    # f32 router + shared-expert gate
+SHARED = 3 * 512 * E * Q8                       # shared expert gate, up, down
+EXPERT_GU = 2 * 512 * E * Q8                    # one routed expert's gate + up
+EXPERT_DOWN = 512 * E * Q8
+LM_HEAD = V * E * Q8
+EH_PROJ = E * 2 * E * Q8
+DN_STATE = 32 * 128 * 128 * 4 + 8192 * 3 * 4   # delta-net S + conv state of one layer
+KV_POS = 2 * 2 * 256 * 2                        # K + V bytes of one position (2 kv heads, f16)
+SMALL = 8 * E * 4                               # norms and other f32 vectors per layer (upper bound)
+
+
+def step_bytes(pos, units_per_step, accepted_frac):
+    """Unique HBM bytes one MTP-1 step must move (weights once per run, state read once and
+    written per lane, KV of positions <= pos once per kv head), excluding cache re-reads."""
+    n_dn, n_att = 30, 10
+    verify = (n_dn * (DN_PROJ + MIX_OUT) + n_att * (ATT_PROJ + MIX_OUT)
+              + 40 * (ROUTER + SHARED + SMALL) + LM_HEAD + 2 * E * Q8
+              + n_dn * 3 * DN_STATE                       # read once, write 2 slots
+              + n_att * ((pos + 2) * KV_POS + 2 * KV_POS))
+    draft = EH_PROJ + ATT_PROJ + MIX_OUT + ROUTER + SHARED + SMALL + LM_HEAD + (pos + 1) * KV_POS + KV_POS
+    seed = accepted_frac * (EH_PROJ + 1024 * E * Q8 + KV_POS)
+    experts = units_per_step * (EXPERT_GU + EXPERT_DOWN)
+    return verify + draft + seed + experts
+
+
+def cpu_baseline(seconds, prompt_len=8):
+    """Time the oracle's MTP-1 steps on the full 35B-A3B shape (bounded sample)."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+    O.build()
+    d = O.desc_35b_a3b()
+    e = O.Engine(d, seed=0, n_ctx=prompt_len + 256)
+    O.lib().oxo_set_keep_logits(e.h, 0)
+    drv = O.Driver(e)
+    x = drv.prefill(O.bench_prompt(prompt_len))
+    gen0 = O.lib().oxo_gen_seconds(e.h)
+    t0 = time.time()
+    toks = steps = 0
+    while time.time() - t0 < seconds or steps < 2:
+        out = drv.step(x)
+        toks += len(out)
+        steps += 1
+        x = out[-1]
+    wall = time.time() - t0
+    gen = O.lib().oxo_gen_seconds(e.h) - gen0
+    compute = max(wall - gen, 1e-9)
+    cores = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    e.close()
+    return {"value": round(toks / compute, 4), "unit": "tok/s", "cores": cores, "kind": "port",
+            "sample": f"{steps} MTP-1 steps ({toks} tokens) of the 35B-A3B shape after an {prompt_len}-token prompt; "
+                      f"{wall:.1f} s wall minus {gen:.1f} s spent generating synthetic expert weights on first use"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=256)
+    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--prompt", type=int, default=512)
+    ap.add_argument("--cpu-seconds", type=float, default=20.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--probe-kind", type=int, default=1, help="kernel kind timed for the roofline (1 = experts gate/up)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build runs the whole MTP-1 step on a single MI355X "
+              f"(--gpus {args.gpus} is not supported; see DESIGN.md for how the path would shard)", file=sys.stderr)
+        sys.exit(2)
+    import numpy as np
+    import torch
+    import oxe_amd as A
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O  # the model description struct and bench prompt only
+
+    d = O.desc_35b_a3b()
+    n_ctx = args.prompt + 2 * (args.steps + args.warmup) + 256 + 64
+    t_setup = time.time()
+    eng = A.Engine(d, seed=0, n_ctx=n_ctx)
+    prompt = O.bench_prompt(args.prompt)
+    x = eng.mtp_prefill(prompt)
+    eng.sync()
+    setup_s = time.time() - t_setup
+    cap = 2 * (args.steps + args.warmup) + 16
+    # warm-up (also captures the step graph)
+    eng.mtp_device_begin(x, cap)
+    eng.mtp_device_steps(args.warmup, use_graph=True)
+    warm_toks, x = eng.mtp_device_end(cap)
+    # timed region: K graph steps between events on the engine stream
+    uni0 = eng.counter(66)
+    calls0 = eng.counter(67)
+    pos_start = eng.pos
+    eng.mtp_device_begin(x, cap)
+    stream = torch.cuda.ExternalStream(eng.stream())
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    eng.sync()
+    ev0.record(stream)
+    eng.mtp_device_steps(args.steps, use_graph=True)
+    ev1.record(stream)
+    eng.sync()
+    torch.cuda.synchronize()
+    ms = ev0.elapsed_time(ev1)
+    toks, x = eng.mtp_device_end(cap)
+    stats = eng.mtp_stats()
+    units = eng.counter(66) - uni0
+    calls = eng.counter(67) - calls0
+    pos_end = eng.pos
+    n_tok = len(toks)
+    tok_s = n_tok / (ms / 1e3)
+    acc = (n_tok - args.steps) / max(args.steps, 1)
+    mean_pos = (pos_start + pos_end) / 2
+    bytes_step = step_bytes(mean_pos, units / max(args.steps, 1), acc)
+    step_gbs = bytes_step / (ms / args.steps / 1e3) / 1e9
+    # roofline of the dominant kernel: live HIP-event timing of each launch in eager steps
+    eng.mtp_device_begin(x, cap)
+    uni1, calls1 = eng.counter(66), eng.counter(67)
+    probe_steps = 8
+    avg_us, n_launch = eng.mtp_device_probe(probe_steps, args.probe_kind)
+    eng.mtp_device_end(cap)
+    u_per_launch = (eng.counter(66) - uni1) / max(eng.counter(67) - calls1, 1)
+    k_bytes = u_per_launch * EXPERT_GU
+    k_gbs = k_bytes / (avg_us * 1e-6) / 1e9 if avg_us > 0 else 0.0
+    result = {
+        "metric": "MTP-1 decode tok/s (35B-A3B shape, int8) + HBM GB/s as % of ~8 TB/s peak",
+        "value": round(tok_s, 3),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms / args.steps, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8 (Q8_0 weights and activations, int32 block dots, fp32 chains; fp16 KV)",
+        "data": "synthetic: seeded random Q8_0 weights (include/oxe_model.h), reference bench prompt ids",
+        "config": {"workload": "BASELINE config 4: 35B-A3B-shaped MTP-1 decode, 40 layers (30 DN + 10 GQA) + MTP block, "
+                               "vocab 151936, all Q8_0",
+                   "prompt_tokens": args.prompt, "ctx_positions": [pos_start, pos_end], "parallelism": "single GPU"},
+        "tokens": n_tok,
+        "accepted_drafts": n_tok - args.steps,
+        "hbm_bytes_per_step": int(bytes_step),
+        "hbm_GBs_step": round(step_gbs, 1),
+        "hbm_frac_step": round(step_gbs / PEAK_HBM_GBS, 4),
+        "expert_units_per_step": round(units / max(args.steps, 1), 3),
+        "roofline": {"bound": "hbm", "achieved": round(k_gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(k_gbs / PEAK_HBM_GBS, 4), "traffic": None,
+                     "kernel": "experts_kernel (routed gate/up GEMV + swiglu)", "avg_us": round(avg_us, 3),
+                     "launches_timed": n_launch, "bytes_per_launch": int(k_bytes)},
+        "setup_s": round(setup_s, 1),
+    }
+    if not args.no_cpu:
+        result["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+    else:
+        result["cpu_baseline"] = None
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -80,6 +80,33 @@ OXE_API int oxe_engine_state_copy(oxe_engine *e, int which, int dir, int64_t off
 OXE_API int oxe_engine_set_pos(oxe_engine *e, int pos);
 OXE_API int64_t oxe_engine_device_bytes(const oxe_engine *e);
 
+/* ---- MTP depth-1 speculative decoding (crates/model/src/mtp.rs MtpDriver, depth 1) --------- */
+
+/* Append prompt tokens through 2-token verify runs and the MTP catch-up (MtpDriver::prefill,
+ * mtp.rs:450-463); *next = argmax after the last token. */
+OXE_API int oxe_mtp_prefill(oxe_engine *e, const uint32_t *toks, int n, uint32_t *next);
+/* One speculative step from token x (MtpDriver::step, mtp.rs:522-592), host-driven: out[0..n_out)
+ * = the greedy tokens that follow (accepted draft + bonus). override_d1 >= 0 replaces the draft
+ * (the reference's draft_override test hook, mtp.rs:328-330). */
+OXE_API int oxe_mtp_step(oxe_engine *e, uint32_t x, uint32_t *out, int *n_out, int64_t override_d1);
+/* Device-driven steps: begin hands the driver state to the GPU; each of the k steps then runs
+ * seed -> draft -> 2-lane verify -> greedy accept/commit on the GPU (one HIP graph per step, no
+ * host round-trip); end synchronises and returns the emitted tokens and the next x. */
+OXE_API int oxe_mtp_device_begin(oxe_engine *e, uint32_t x, int out_cap);
+OXE_API int oxe_mtp_device_steps(oxe_engine *e, int k, int use_graph);
+OXE_API int oxe_mtp_device_end(oxe_engine *e, uint32_t *out_tok, int cap, int *n_out, uint32_t *next_x);
+/* Forced drafts for the device-driven steps (test hook): force_d1[i] >= 0 replaces step i's draft. */
+OXE_API int oxe_mtp_set_force(oxe_engine *e, const int32_t *force_d1, int n);
+/* Eager device-driven steps with HIP events around each launch of one kernel kind (0 LM head,
+ * 1 experts gate/up, 2 down, 3 projections, 4 mixer out, 5 delta-net, 6 router, 7 scores, 8 pv,
+ * 9 MTP entry): mean launch duration in microseconds (roofline measurement). */
+OXE_API int oxe_mtp_device_probe(oxe_engine *e, int k, int kind, float *avg_us, int *n);
+/* steps, accepted drafts */
+OXE_API int oxe_mtp_stats(const oxe_engine *e, int64_t *st);
+OXE_API int oxe_engine_sync(oxe_engine *e);
+/* the engine's HIP stream (hipStream_t) */
+OXE_API void *oxe_engine_stream(oxe_engine *e);
+
 #ifdef __cplusplus
 }
 #endif

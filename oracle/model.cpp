@@ -9,6 +9,7 @@
 #include "oxo_model.h"
 
 #include <algorithm>
+#include <chrono>
 #include <cmath>
 #include <cstring>
 #include <memory>
@@ -99,16 +100,19 @@ struct oxo_engine {
     std::vector<uint32_t> argmax;
     bool keep_logits = true;
 
+    double gen_seconds = 0.0;
     const Q8 &expert(int l, int e, int which) {
         Layer &L = layers[l];
         std::lock_guard<std::mutex> g(gen_mu);
         if (!L.experts[e]) {
+            const auto t0 = std::chrono::steady_clock::now();
             std::unique_ptr<Q8[]> m(new Q8[3]);
             const int64_t E = d.n_embd, F = d.ff_exp;
             gen_q8(seed, l, OXE_T_GATE_EXPS, F, E, e, m[0]);
             gen_q8(seed, l, OXE_T_UP_EXPS, F, E, e, m[1]);
             gen_q8(seed, l, OXE_T_DOWN_EXPS, E, F, e, m[2]);
             L.experts[e] = std::move(m);
+            gen_seconds += std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
         }
         return L.experts[e][which];
     }
@@ -619,6 +623,7 @@ const float *oxo_hidden(const oxo_engine *e, int lane) { return e->hout[lane].da
 const float *oxo_logits(const oxo_engine *e, int lane) { return e->logits[lane].data(); }
 int64_t oxo_n_ctx(const oxo_engine *e) { return e->n_ctx; }
 void oxo_set_keep_logits(oxo_engine *e, int on) { e->keep_logits = on != 0; }
+double oxo_gen_seconds(const oxo_engine *e) { return e->gen_seconds; }
 
 // raw state views for parity checks: K cache [att][kvh][n_ctx][hd] f16, V^T [att][kvh*hd][n_ctx] f16,
 // conv [slot][rec][(kc-1)*channels], S [slot][rec][nv][hv][hv]

@@ -3,357 +3,7 @@
 // and the C ABI of include/oxe_amd.h. Every run is a fixed sequence of kernels on one stream; the
 // run's lanes, positions and slots live in the device RunCtl, so the sequence needs no host value
 // at launch time and can be captured once into a HIP graph.
-#include <hip/hip_runtime.h>
-
-#include <algorithm>
-#include <cmath>
-#include <cstdio>
-#include <cstring>
-#include <mutex>
-#include <stdexcept>
-#include <string>
-#include <vector>
-
-#include "../../include/oxe_amd.h"
-#include "oxe_engine.h"
-#include "oxe_kernels.h"
-#include "oxe_model_kernels.h"
-#include "oxe_shape.h"
-
-namespace oxe {
-
-using namespace shp;
-
-static thread_local std::string g_last_error;
-static void set_err(const std::string &s) { g_last_error = s; }
-
-struct Engine {
-    oxe_model_desc d{};
-    uint64_t seed = 0;
-    hipStream_t st = nullptr;
-    ModelRt m{};
-    std::vector<LayerW> L;  // n_layer (+1 MTP block)
-    ActBufs b{};
-    RunCtl *ctl = nullptr;  // device
-    std::vector<void *> allocs;
-    size_t bytes = 0;
-    // host mirror of the engine position (host-driven API)
-    int pos = 0, cur = 0;
-    int pend_pos0 = 0, pend_cur = 0, pend_n = 0, pend_done = 0;
-    int n_att_main = 0;
-    bool keep_logits = true;
-
-    template <class T>
-    T *alloc(size_t n) {
-        void *p = nullptr;
-        if (hipMalloc(&p, n * sizeof(T) + 64) != hipSuccess) throw std::runtime_error("hipMalloc failed");
-        allocs.push_back(p);
-        bytes += n * sizeof(T);
-        return (T *)p;
-    }
-    Q8W q8(int64_t rows, int64_t k) {
-        Q8W w;
-        w.q = alloc<int8_t>(rows * k);
-        w.d = alloc<uint16_t>(rows * k / 32);
-        w.rows = rows;
-        w.k = k;
-        return w;
-    }
-    ~Engine() {
-        if (st) (void)hipStreamSynchronize(st);
-        for (void *p : allocs) (void)hipFree(p);
-        if (st) (void)hipStreamDestroy(st);
-    }
-
-    static bool shape_ok(const oxe_model_desc &d) {
-        return d.n_embd == E && d.n_head == NH && d.n_head_kv == NKV && d.head_dim == HD && d.n_expert == NEXP &&
-               d.n_expert_used == KUSED && d.ff_exp == FF && d.ff_shexp == FFSH && d.ssm_conv_kernel == KC &&
-               d.ssm_d_state == DS && d.ssm_n_kheads == NKH && d.ssm_n_vheads == NVH && d.ssm_d_inner == DIN &&
-               d.n_rot == NROT && d.n_layer >= 1 && d.n_layer <= 62 && d.n_vocab >= 16 && d.n_vocab % 16 == 0 &&
-               d.full_attention_interval >= 1 && d.has_mtp == 1;
-    }
-
-    void create(const oxe_model_desc &desc, uint64_t sd, int n_ctx) {
-        d = desc;
-        seed = sd;
-        if (hipStreamCreate(&st) != hipSuccess) throw std::runtime_error("hipStreamCreate failed");
-        m.n_layer = d.n_layer;
-        m.n_vocab = d.n_vocab;
-        m.n_ctx = (n_ctx + 255) / 256 * 256;
-        m.eps = d.rms_eps;
-        const int nl_total = d.n_layer + 1;
-        L.resize(nl_total);
-        int n_rec = 0, n_att = 0;
-        for (int il = 0; il < nl_total; il++) {
-            LayerW &w = L[il];
-            w.att = il == d.n_layer || ((il + 1) % d.full_attention_interval == 0);
-            w.index = w.att ? n_att++ : n_rec++;
-        }
-        m.n_rec = n_rec;
-        m.n_att = n_att;
-        n_att_main = n_att - 1;
-        // weights
-        for (int il = 0; il < nl_total; il++) {
-            LayerW &w = L[il];
-            w.attn_norm = alloc<float>(E);
-            w.post_norm = alloc<float>(E);
-            if (!w.att) {
-                w.proj = q8(DN_ROWS, E);
-                w.out = q8(E, DIN);
-                w.conv = alloc<float>((size_t)NCH * KC);
-                w.ssm_a = alloc<float>(NVH);
-                w.dt_bias = alloc<float>(NVH);
-                w.ssm_norm = alloc<float>(HV);
-            } else {
-                w.proj = q8(AT_ROWS, E);
-                w.out = q8(E, NH * HD);
-                w.q_norm = alloc<float>(HD);
-                w.k_norm = alloc<float>(HD);
-            }
-            w.router = alloc<float>((size_t)NEXP * E);
-            w.shexp_gate = alloc<float>(E);
-            w.shexp_gu = q8(2 * FFSH, E);
-            w.shexp_down = q8(E, FFSH);
-            w.exp_gu = q8((int64_t)NEXP * 2 * FF, E);
-            w.exp_down = q8((int64_t)NEXP * E, FF);
-            if (il == d.n_layer) {
-                w.eh_proj = q8(E, 2 * E);
-                w.enorm = alloc<float>(E);
-                w.hnorm = alloc<float>(E);
-                w.head_norm = alloc<float>(E);
-            }
-        }
-        m.tok_embd = q8(d.n_vocab, E);
-        m.output = q8(d.n_vocab, E);
-        m.out_norm = alloc<float>(E);
-        // state
-        m.conv_state = alloc<float>((size_t)OXE_NSLOTS * n_rec * NCH * (KC - 1));
-        m.ssm_state = alloc<float>((size_t)OXE_NSLOTS * n_rec * NVH * HV * HV);
-        m.kcache = alloc<uint16_t>((size_t)n_att * NKV * m.n_ctx * HD);
-        m.vcache = alloc<uint16_t>((size_t)n_att * NKV * HD * m.n_ctx);
-        m.rope = alloc<float>((size_t)m.n_ctx * NROT);
-        // activations
-        b.x = alloc<float>(OXE_NL * E);
-        b.x1 = alloc<float>(OXE_NL * E);
-        b.x2 = alloc<float>(OXE_NL * E);
-        b.xq = alloc<int8_t>(OXE_NL * 2 * E);
-        b.xd = alloc<uint16_t>(OXE_NL * 2 * E / 32);
-        b.xn = alloc<float>(OXE_NL * E);
-        b.proj = alloc<float>((size_t)OXE_NL * DN_ROWS);
-        b.gdn = alloc<float>(OXE_NL * DIN);
-        b.oq = alloc<int8_t>(OXE_NL * MIX_W);
-        b.od = alloc<uint16_t>(OXE_NL * MIX_W / 32);
-        b.scores = alloc<float>((size_t)OXE_NL * NH * m.n_ctx);
-        b.router_lg = alloc<float>(OXE_NL * NEXP);
-        b.sh_gate = alloc<float>(OXE_NL);
-        b.hsh = alloc<float>(OXE_NL * FFSH);
-        b.hexp = alloc<float>(OXE_NL * KUSED * FF);
-        b.route_ids = alloc<int32_t>(OXE_NL * KUSED);
-        b.route_w = alloc<float>(OXE_NL * KUSED);
-        b.uni = alloc<int32_t>(OXE_MAX_UNION + 1);
-        b.hid = alloc<float>((size_t)HID_N * E);
-        b.logits = alloc<float>((size_t)OXE_NL * d.n_vocab);
-        b.amax_key = alloc<unsigned long long>(OXE_NL);
-        b.counters = alloc<uint32_t>(CNT_N);
-        ctl = alloc<RunCtl>(1);
-        // zero what must start at zero (before any graph capture)
-        (void)hipMemsetAsync(m.conv_state, 0, (size_t)OXE_NSLOTS * n_rec * NCH * (KC - 1) * 4, st);
-        (void)hipMemsetAsync(m.ssm_state, 0, (size_t)OXE_NSLOTS * n_rec * NVH * HV * HV * 4, st);
-        (void)hipMemsetAsync(m.kcache, 0, (size_t)n_att * NKV * m.n_ctx * HD * 2, st);
-        (void)hipMemsetAsync(m.vcache, 0, (size_t)n_att * NKV * HD * m.n_ctx * 2, st);
-        (void)hipMemsetAsync(b.counters, 0, CNT_N * 4, st);
-        (void)hipMemsetAsync(b.hid, 0, (size_t)HID_N * E * 4, st);
-        (void)hipMemsetAsync(b.amax_key, 0, OXE_NL * 8, st);
-        // RoPE cache per position with the host C library (oxe_mrope_cache_init, oxe_ops.cpp:386-439)
-        std::vector<float> rope((size_t)m.n_ctx * NROT);
-        for (int p = 0; p < m.n_ctx; p++) mrope_cache(p, rope.data() + (size_t)p * NROT);
-        (void)hipMemcpyAsync(m.rope, rope.data(), rope.size() * 4, hipMemcpyHostToDevice, st);
-        (void)hipStreamSynchronize(st);
-        // the attention pv kernel keeps the group's probabilities in LDS: allow up to 160 KB
-        if (hipGetLastError() != hipSuccess) throw std::runtime_error("HIP error during engine creation");
-    }
-
-    // ggml_mrope_cache_init for a text position (IMRoPE sections, ext_factor 0, freq_scale 1)
-    void mrope_cache(int64_t p, float *cache) const {
-        const int n_dims = NROT;
-        const float theta_scale = powf(d.rope_freq_base, -2.0f / n_dims);
-        const int *sec = d.rope_sections;
-        const int sect_dims = sec[0] + sec[1] + sec[2] + sec[3];
-        float theta_t = (float)p, theta_h = (float)p, theta_w = (float)p, theta_e = 0.0f;
-        for (int i0 = 0; i0 < n_dims; i0 += 2) {
-            const int sector = (i0 / 2) % sect_dims;
-            float theta;
-            if (sector % 3 == 1 && sector < 3 * sec[1]) theta = theta_h;
-            else if (sector % 3 == 2 && sector < 3 * sec[2]) theta = theta_w;
-            else if (sector % 3 == 0 && sector < 3 * sec[0]) theta = theta_t;
-            else theta = theta_e;
-            const float th = 1.0f * theta;
-            cache[i0] = cosf(th) * 1.0f;
-            cache[i0 + 1] = sinf(th) * 1.0f;
-            theta_t *= theta_scale;
-            theta_w *= theta_scale;
-            theta_h *= theta_scale;
-            theta_e *= theta_scale;
-        }
-    }
-
-    int synth_weights() {
-        int rc = 0;
-        auto chk = [&](int r) { if (r) rc = r; };
-        const int nl_total = d.n_layer + 1;
-        for (int il = 0; il < nl_total; il++) {
-            LayerW &w = L[il];
-            chk(synth_f32(seed, il, OXE_T_ATTN_NORM, E, w.attn_norm, st));
-            chk(synth_f32(seed, il, OXE_T_POST_NORM, E, w.post_norm, st));
-            if (!w.att) {
-                chk(synth_q8(seed, il, OXE_T_DN_QKV, -1, NCH, E, NCH, 0, w.proj.q, w.proj.d, st));
-                chk(synth_q8(seed, il, OXE_T_DN_Z, -1, DIN, E, DIN, 0, w.proj.q + (int64_t)DN_Z * E, w.proj.d + (int64_t)DN_Z * E / 32, st));
-                chk(synth_q8(seed, il, OXE_T_DN_BETA, -1, NVH, E, NVH, 0, w.proj.q + (int64_t)DN_BETA * E, w.proj.d + (int64_t)DN_BETA * E / 32, st));
-                chk(synth_q8(seed, il, OXE_T_DN_ALPHA, -1, NVH, E, NVH, 0, w.proj.q + (int64_t)DN_ALPHA * E, w.proj.d + (int64_t)DN_ALPHA * E / 32, st));
-                chk(synth_q8(seed, il, OXE_T_DN_OUT, -1, E, DIN, E, 0, w.out.q, w.out.d, st));
-                chk(synth_f32(seed, il, OXE_T_DN_CONV, (int64_t)NCH * KC, w.conv, st));
-                chk(synth_f32(seed, il, OXE_T_DN_A, NVH, w.ssm_a, st));
-                chk(synth_f32(seed, il, OXE_T_DN_DT, NVH, w.dt_bias, st));
-                chk(synth_f32(seed, il, OXE_T_DN_NORM, HV, w.ssm_norm, st));
-            } else {
-                chk(synth_q8(seed, il, OXE_T_ATT_Q, -1, NH * 2 * HD, E, NH * 2 * HD, 0, w.proj.q, w.proj.d, st));
-                chk(synth_q8(seed, il, OXE_T_ATT_K, -1, NKV * HD, E, NKV * HD, 0, w.proj.q + (int64_t)AT_K * E, w.proj.d + (int64_t)AT_K * E / 32, st));
-                chk(synth_q8(seed, il, OXE_T_ATT_V, -1, NKV * HD, E, NKV * HD, 0, w.proj.q + (int64_t)AT_V * E, w.proj.d + (int64_t)AT_V * E / 32, st));
-                chk(synth_q8(seed, il, OXE_T_ATT_OUT, -1, E, NH * HD, E, 0, w.out.q, w.out.d, st));
-                chk(synth_f32(seed, il, OXE_T_ATT_QNORM, HD, w.q_norm, st));
-                chk(synth_f32(seed, il, OXE_T_ATT_KNORM, HD, w.k_norm, st));
-            }
-            chk(synth_f32(seed, il, OXE_T_ROUTER, (int64_t)NEXP * E, w.router, st));
-            chk(synth_f32(seed, il, OXE_T_SHEXP_GATE, E, w.shexp_gate, st));
-            chk(synth_q8(seed, il, OXE_T_GATE_SHEXP, OXE_T_UP_SHEXP, 2 * FFSH, E, FFSH, 0, w.shexp_gu.q, w.shexp_gu.d, st));
-            chk(synth_q8(seed, il, OXE_T_DOWN_SHEXP, -1, E, FFSH, E, 0, w.shexp_down.q, w.shexp_down.d, st));
-            for (int e = 0; e < NEXP; e++) {
-                chk(synth_q8(seed, il, OXE_T_GATE_EXPS, OXE_T_UP_EXPS, 2 * FF, E, FF, e, w.exp_gu.q + (int64_t)e * 2 * FF * E,
-                             w.exp_gu.d + (int64_t)e * 2 * FF * E / 32, st));
-                chk(synth_q8(seed, il, OXE_T_DOWN_EXPS, -1, E, FF, E, e, w.exp_down.q + (int64_t)e * E * FF,
-                             w.exp_down.d + (int64_t)e * E * FF / 32, st));
-            }
-            if (il == d.n_layer) {
-                chk(synth_q8(seed, il, OXE_T_EH_PROJ, -1, E, 2 * E, E, 0, w.eh_proj.q, w.eh_proj.d, st));
-                chk(synth_f32(seed, il, OXE_T_ENORM, E, w.enorm, st));
-                chk(synth_f32(seed, il, OXE_T_HNORM, E, w.hnorm, st));
-                chk(synth_f32(seed, il, OXE_T_HEAD_NORM, E, w.head_norm, st));
-            }
-        }
-        chk(synth_q8(seed, OXE_GLOBAL_LAYER, OXE_T_TOK_EMBD, -1, d.n_vocab, E, d.n_vocab, 0, m.tok_embd.q, m.tok_embd.d, st));
-        chk(synth_q8(seed, OXE_GLOBAL_LAYER, OXE_T_OUTPUT, -1, d.n_vocab, E, d.n_vocab, 0, m.output.q, m.output.d, st));
-        chk(synth_f32(seed, OXE_GLOBAL_LAYER, OXE_T_OUT_NORM, E, m.out_norm, st));
-        if (hipStreamSynchronize(st) != hipSuccess) return -2;
-        return rc;
-    }
-
-    // ---- run sequences (device-side lanes/positions from RunCtl) ----
-    void enqueue_layer(int l, bool first) {
-        const LayerW &w = L[l];
-        const float *x = first ? b.x : b.x2;
-        launch_proj(ctl, m, w, first ? nullptr : b.x2, first, first ? b.x : nullptr, b, st);
-        if (!w.att) {
-            launch_dn(ctl, m, w, b, st);
-        } else {
-            launch_kwrite(ctl, m, w, b, st);
-            launch_scores(ctl, m, w, b, st);
-            launch_pv(ctl, m, w, b, st);
-        }
-        launch_out(ctl, w, x, b, st);
-        launch_router(ctl, m, w, b, st);
-        launch_experts(ctl, w, b, st);
-        launch_down(ctl, w, b, st);
-    }
-    void enqueue_verify() {
-        for (int l = 0; l < d.n_layer; l++) enqueue_layer(l, l == 0);
-        launch_head(ctl, m, m.out_norm, b, keep_logits, st);
-    }
-    void enqueue_mtp_run() {
-        const LayerW &w = L[d.n_layer];
-        launch_entry(ctl, m, w, b, st);
-        // the MTP layer: input x2 (the entry output), as any layer > 0
-        launch_proj(ctl, m, w, b.x2, false, nullptr, b, st);
-        launch_kwrite(ctl, m, w, b, st);
-        launch_scores(ctl, m, w, b, st);
-        launch_pv(ctl, m, w, b, st);
-        launch_out(ctl, w, b.x2, b, st);
-        launch_router(ctl, m, w, b, st);
-        launch_experts(ctl, w, b, st);
-        launch_down(ctl, w, b, st);
-        launch_head(ctl, m, w.head_norm, b, false, st);
-    }
-    void enqueue_mtp_seed() {
-        const LayerW &w = L[d.n_layer];
-        launch_entry(ctl, m, w, b, st);
-        launch_proj(ctl, m, w, b.x2, false, nullptr, b, st, AT_K);  // K and V rows only
-        launch_kwrite(ctl, m, w, b, st);
-    }
-
-    // ---- host-driven API (mirrors Engine::{verify, commit, mtp_run, mtp_seed}) ----
-    int read_argmax(uint32_t *out, int n) {
-        unsigned long long keys[OXE_NL];
-        if (hipMemcpyAsync(keys, b.amax_key, sizeof(keys), hipMemcpyDeviceToHost, st) != hipSuccess) return -2;
-        if (hipStreamSynchronize(st) != hipSuccess) return -2;
-        for (int i = 0; i < n; i++) out[i] = keys[i] == 0 ? 0u : 0xffffffffu - (uint32_t)(keys[i] & 0xffffffffu);
-        return 0;
-    }
-    RunCtl run(int nl, int pos0, const uint32_t *toks, int head_mask) const {
-        RunCtl r{};
-        r.nl = nl;
-        r.pos0 = pos0;
-        r.cur = cur;
-        r.head_mask = head_mask;
-        for (int i = 0; i < nl; i++) r.tok[i] = toks[i];
-        r.hin_sel[0] = HID_HL;
-        r.hin_sel[1] = HID_PEND;
-        r.active = 1;
-        return r;
-    }
-    int verify(const uint32_t *toks, int n, uint32_t *out) {
-        if (n < 1 || n > OXE_NL || pos + n > m.n_ctx) return -1;
-        for (int i = 0; i < n; i++) if (toks[i] >= (uint32_t)d.n_vocab) return -1;
-        launch_set_run(ctl, run(n, pos, toks, (1 << n) - 1), st);
-        enqueue_verify();
-        pend_pos0 = pos;
-        pend_cur = cur;
-        pend_n = n;
-        pend_done = 0;
-        return read_argmax(out, n);
-    }
-    int commit(int mm) {
-        if (pend_n == 0) return -1;
-        const int hi = pend_done == 0 ? pend_n : pend_done;
-        if (mm < 1 || mm > hi) return -1;
-        launch_zero_v(m, n_att_main, pend_pos0 + mm, pend_pos0 + hi, st);
-        pos = pend_pos0 + mm;
-        cur = (pend_cur + mm) % OXE_NSLOTS;
-        pend_done = mm;
-        return hipStreamSynchronize(st) == hipSuccess ? 0 : -2;
-    }
-    int set_hidden(const float *hs, int n) {
-        // lane i of an MTP run reads hid[HID_HL + i]
-        return hipMemcpyAsync(b.hid + (size_t)HID_HL * E, hs, (size_t)n * E * 4, hipMemcpyHostToDevice, st) == hipSuccess ? 0 : -2;
-    }
-    int mtp_run(const uint32_t *toks, int n, int pos0, const float *hs, int head_last, uint32_t *out) {
-        if (n < 1 || n > OXE_NL || pos0 + n > m.n_ctx) return -1;
-        if (set_hidden(hs, n)) return -2;
-        launch_set_run(ctl, run(n, pos0, toks, head_last ? 1 << (n - 1) : 0), st);
-        enqueue_mtp_run();
-        uint32_t a[OXE_NL];
-        if (read_argmax(a, n)) return -2;
-        *out = head_last ? a[n - 1] : 0xffffffffu;
-        return 0;
-    }
-    int mtp_seed(const uint32_t *toks, int n, int pos0, const float *hs) {
-        if (n < 1 || n > OXE_NL || pos0 + n > m.n_ctx) return -1;
-        if (set_hidden(hs, n)) return -2;
-        launch_set_run(ctl, run(n, pos0, toks, 0), st);
-        enqueue_mtp_seed();
-        return hipStreamSynchronize(st) == hipSuccess ? 0 : -2;
-    }
-};
-
-}  // namespace oxe
+#include "oxe_engine_host.h"
 
 // ------------------------------------------------------------------------------------------------
 // C ABI

@@ -244,7 +244,7 @@ void launch_pv(const RunCtl *ctl, const ModelRt &m, const LayerW &w, const ActBu
     const size_t lds = (size_t)GQA * ((m.n_ctx + 1) & ~1) * 2 + (size_t)m.n_ctx * 4;
     static size_t configured = 0;
     if (lds > configured) {
-        hipFuncSetAttribute((const void *)pv_kernel<OXE_NL>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        (void)hipFuncSetAttribute((const void *)pv_kernel<OXE_NL>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         configured = lds;
     }
     hipLaunchKernelGGL(pv_kernel<OXE_NL>, dim3(NKV * OXE_NL * (HD / PV_D)), dim3(256), lds, st, ctl, a);

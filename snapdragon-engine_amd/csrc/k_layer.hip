@@ -121,11 +121,12 @@ void launch_proj(const RunCtl *ctl, const ModelRt &m, const LayerW &w, const flo
 }
 
 // ------------------------------------------------------------------------------------------------
-// delta-net recurrence. Workgroup = (value head vh, 16-row chunk of its 128x128 state), 256
-// threads = 16 rows x 16 lanes; lane c of a row owns state elements i = c + 16 s (s = 0..7), which
-// is exactly chain c of ggml_vec_dot_f32's 16 accumulation chains (element i -> accumulator
+// delta-net recurrence. Workgroup = one value head vh (1024 threads: 64 row groups x 16 lanes, two
+// state rows per row group). Lane c of a row owns state elements i = c + 16 s (s = 0..7), which is
+// exactly chain c of ggml_vec_dot_f32's 16 accumulation chains (element i -> accumulator
 // (i mod 16) / 4, lane i mod 4), so each row dot is 8 FMAs per lane and the NEON reduction tree
-// (a0+a2, a1+a3, a0+a1, then (l0+l1)+(l2+l3)) is the shuffle sequence xor 8, 4, 1, 2.
+// (a0+a2, a1+a3, a0+a1, then (l0+l1)+(l2+l3)) is the shuffle sequence xor 8, 4, 1, 2. The head's
+// 128 outputs stay in LDS for the gated RMS norm and the Q8_0 quantization of the mixer output.
 struct DnArgs {
     const float *proj;      // [NL][DN_ROWS]
     const float *conv_w;    // [NCH][KC]
@@ -135,14 +136,11 @@ struct DnArgs {
     int64_t ssm_slot;
     const float *ssm_a, *dt_bias, *ssm_norm;
     float eps;
-    float *gdn;             // [NL][DIN]
     int8_t *oq;             // [NL][DIN]
     uint16_t *od;           // [NL][DIN/32]
-    uint32_t *counters;     // [NVH]
 };
 
-constexpr int DN_ROWS_PER_WG = 16;
-constexpr int DN_CHUNKS = HV / DN_ROWS_PER_WG;  // 8
+constexpr int DN_THREADS = 1024;
 
 OXE_DEV float dot16_tree(float acc) {
     acc = acc + shfl_xor_f(acc, 8);
@@ -165,50 +163,55 @@ OXE_DEV float conv4(float s0, float s1, float s2, float xn, const float *c) {
 }
 
 template <int NL>
-__global__ __launch_bounds__(256) void dn_kernel(const RunCtl *__restrict__ ctl, DnArgs a) {
-    __shared__ float s_q[NL][DS], s_k[NL][DS], s_v[NL][DN_ROWS_PER_WG];
+__global__ __launch_bounds__(DN_THREADS) void dn_kernel(const RunCtl *__restrict__ ctl, DnArgs a) {
+    __shared__ float s_q[NL][DS], s_k[NL][DS], s_v[NL][HV], s_o[NL][HV];
     __shared__ float s_g[NL], s_b[NL];
-    __shared__ int s_last;
     if (!ctl->active) return;
     const int nl = ctl->nl, t = threadIdx.x;
-    const int vh = blockIdx.x / DN_CHUNKS, chunk = blockIdx.x % DN_CHUNKS, kh = vh % NKH;
-    const int j0 = chunk * DN_ROWS_PER_WG;
+    const int vh = blockIdx.x, kh = vh % NKH;
     const int cur = ctl->cur;
-    // 1. conv + silu for the channels this workgroup reads: q (128) and k (128) of key head kh,
-    //    v of its 16 rows. Lane l reads slot (cur + l) (lane 0's state, or the previous lane's
-    //    result recomputed here) and writes slot (cur + l + 1); the q/k channel states are written
-    //    by one designated workgroup (value head kh, chunk 0), the v channel states by their owner.
-    for (int i = t; i < 2 * DS + DN_ROWS_PER_WG; i += 256) {
+    // prefetch this thread's two state rows (slot cur) while the conv runs
+    const int rg = t >> 4, c = t & 15;
+    float r[2][8];
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+        const float *src = a.ssm + (int64_t)cur * a.ssm_slot + ((int64_t)vh * HV + rg + 64 * h) * HV;
+#pragma unroll
+        for (int s = 0; s < 8; s++) r[h][s] = src[c + 16 * s];
+    }
+    // 1. conv + silu of the channels this head reads: q and k of key head kh, v of head vh. Lane l
+    //    continues from lane l-1's window and writes slot (cur + l + 1); the q/k channel states are
+    //    written by the workgroup of value head kh (the other value head sharing them only reads).
+    if (t < 3 * DS) {
         int ch;
         bool writer;
-        if (i < DS) { ch = kh * DS + i; writer = vh < NKH && chunk == 0; }
-        else if (i < 2 * DS) { ch = NKH * DS + kh * DS + (i - DS); writer = vh < NKH && chunk == 0; }
-        else { ch = 2 * NKH * DS + vh * HV + j0 + (i - 2 * DS); writer = true; }
-        const float *c = a.conv_w + (int64_t)ch * KC;
+        if (t < DS) { ch = kh * DS + t; writer = vh < NKH; }
+        else if (t < 2 * DS) { ch = NKH * DS + kh * DS + (t - DS); writer = vh < NKH; }
+        else { ch = 2 * NKH * DS + vh * HV + (t - 2 * DS); writer = true; }
+        const float *cw = a.conv_w + (int64_t)ch * KC;
         const float *st = a.conv_state + (int64_t)cur * a.conv_slot + (int64_t)ch * (KC - 1);
         float s0 = st[0], s1 = st[1], s2 = st[2];
         for (int l = 0; l < nl; l++) {
             const float xn = a.proj[(int64_t)l * DN_ROWS + ch];
-            const float y = v_silu(conv4(s0, s1, s2, xn, c));
+            const float y = v_silu(conv4(s0, s1, s2, xn, cw));
             s0 = s1; s1 = s2; s2 = xn;
             if (writer) {
                 float *dst = a.conv_state + (int64_t)((cur + l + 1) % OXE_NSLOTS) * a.conv_slot + (int64_t)ch * (KC - 1);
                 dst[0] = s0; dst[1] = s1; dst[2] = s2;
             }
-            if (i < DS) s_q[l][i] = y;
-            else if (i < 2 * DS) s_k[l][i - DS] = y;
-            else s_v[l][i - 2 * DS] = y;
+            if (t < DS) s_q[l][t] = y;
+            else if (t < 2 * DS) s_k[l][t - DS] = y;
+            else s_v[l][t - 2 * DS] = y;
         }
     }
     __syncthreads();
     // 2. l2 norms of q and k per lane (oxe_gdn_l2_norm_f32: rms_norm with eps/n, then * 1/sqrt(n)),
-    //    one wave per (lane, q|k) vector; gates on wave 0 lane 0
+    //    one wave per (lane, q|k) vector; the gates (engine.rs:2509-2524) on wave 4
     {
         const int w = t >> 6, lane = t & 63;
-        for (int job = w; job < 2 * NL; job += 4) {
-            const int l = job >> 1;
-            if (l >= nl) continue;
-            float *x = (job & 1) ? s_k[l] : s_q[l];
+        if (w < 2 * NL && (w >> 1) < nl) {
+            const int l = w >> 1;
+            float *x = (w & 1) ? s_k[l] : s_q[l];
             const float a0 = x[lane], a1 = x[lane + 64];
             const float nf = (float)DS;
             const float mean = wave_mean_sq_128(a0, a1, x);
@@ -217,71 +220,55 @@ __global__ __launch_bounds__(256) void dn_kernel(const RunCtl *__restrict__ ctl,
             x[lane] = (a0 * scale) * s2;
             x[lane + 64] = (a1 * scale) * s2;
         }
-        if (t < NL && t < nl) {
-            // g = softplus(alpha + dt_bias) * ssm_a ; beta = sigmoid(beta)  (engine.rs:2509-2524)
-            const float ab = a.proj[(int64_t)t * DN_ROWS + DN_ALPHA + vh] + a.dt_bias[vh];
-            s_g[t] = oxe_libm::expf_c(softplus_c(ab) * a.ssm_a[vh]);   // e^g of the step
-            s_b[t] = sigmoid_c(a.proj[(int64_t)t * DN_ROWS + DN_BETA + vh]);
+        if (w == 2 * NL && lane < nl) {
+            const float ab = a.proj[(int64_t)lane * DN_ROWS + DN_ALPHA + vh] + a.dt_bias[vh];
+            s_g[lane] = oxe_libm::expf_c(softplus_c(ab) * a.ssm_a[vh]);   // e^g of the step
+            s_b[lane] = sigmoid_c(a.proj[(int64_t)lane * DN_ROWS + DN_BETA + vh]);
         }
     }
     __syncthreads();
-    // 3. delta rule (oxe_gated_delta_net_step_f32_x4_from, oxe_ops.cpp:268-345) on rows j0..j0+15
-    const int jr = t >> 4, c = t & 15, j = j0 + jr;
-    float r[8];
-    {
-        const float *src = a.ssm + (int64_t)cur * a.ssm_slot + ((int64_t)vh * HV + j) * HV;
-#pragma unroll
-        for (int s = 0; s < 8; s++) r[s] = src[c + 16 * s];
-    }
+    // 3. delta rule (oxe_gated_delta_net_step_f32_x4_from, oxe_ops.cpp:268-345) on rows rg, rg + 64
     const float scale = 1.0f / sqrtf((float)HV);
     for (int l = 0; l < nl; l++) {
         const float eg = s_g[l], beta = s_b[l];
-        float acc = 0.0f;
 #pragma unroll
-        for (int s = 0; s < 8; s++) {
-            r[s] = r[s] * eg;
-            acc = __builtin_fmaf(r[s], s_k[l][c + 16 * s], acc);
+        for (int h = 0; h < 2; h++) {
+            const int j = rg + 64 * h;
+            float acc = 0.0f;
+#pragma unroll
+            for (int s = 0; s < 8; s++) {
+                r[h][s] = r[h][s] * eg;
+                acc = __builtin_fmaf(r[h][s], s_k[l][c + 16 * s], acc);
+            }
+            const float s1 = dot16_tree(acc);
+            const float delta = (s_v[l][j] - s1) * beta;
+            acc = 0.0f;
+#pragma unroll
+            for (int s = 0; s < 8; s++) {
+                r[h][s] = __builtin_fmaf(s_k[l][c + 16 * s], delta, r[h][s]);
+                acc = __builtin_fmaf(r[h][s], s_q[l][c + 16 * s], acc);
+            }
+            const float s2 = dot16_tree(acc);
+            float *dst = a.ssm + (int64_t)((cur + l + 1) % OXE_NSLOTS) * a.ssm_slot + ((int64_t)vh * HV + j) * HV;
+#pragma unroll
+            for (int s = 0; s < 8; s++) dst[c + 16 * s] = r[h][s];
+            if (c == 0) s_o[l][j] = s2 * scale;
         }
-        const float s1 = dot16_tree(acc);
-        const float delta = (s_v[l][jr] - s1) * beta;
-        acc = 0.0f;
-#pragma unroll
-        for (int s = 0; s < 8; s++) {
-            r[s] = __builtin_fmaf(s_k[l][c + 16 * s], delta, r[s]);
-            acc = __builtin_fmaf(r[s], s_q[l][c + 16 * s], acc);
-        }
-        const float s2 = dot16_tree(acc);
-        float *dst = a.ssm + (int64_t)((cur + l + 1) % OXE_NSLOTS) * a.ssm_slot + ((int64_t)vh * HV + j) * HV;
-#pragma unroll
-        for (int s = 0; s < 8; s++) dst[c + 16 * s] = r[s];
-        if (c == 0) a.gdn[(int64_t)l * DIN + vh * HV + j] = s2 * scale;
-    }
-    // 4. the last workgroup of value head vh: gated RMS norm with z and the Q8_0 quantization of
-    //    the head's 128 outputs (engine.rs:2560-2566: o = rms_norm(out) * ssm_norm * silu(z))
-    __threadfence();
-    __syncthreads();
-    if (t == 0) {
-        const uint32_t prev = __hip_atomic_fetch_add(&a.counters[vh], 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-        s_last = prev == DN_CHUNKS - 1;
-        if (s_last) __hip_atomic_store(&a.counters[vh], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     __syncthreads();
-    if (!s_last) return;
-    __threadfence();
+    // 4. gated RMS norm with z (engine.rs:2560-2566: o = rms_norm(out) * ssm_norm * silu(z)) and the
+    //    Q8_0 quantization of the head's 128 outputs, one wave per lane
     {
         const int w = t >> 6, lane = t & 63;
         if (w < nl) {
             const int l = w;
-            const float *g = a.gdn + (int64_t)l * DIN + vh * HV;
-            const float x0 = __hip_atomic_load(&g[lane], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            const float x1 = __hip_atomic_load(&g[lane + 64], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            const float mean = wave_mean_sq_128(x0, x1, g);
+            const float x0 = s_o[l][lane], x1 = s_o[l][lane + 64];
+            const float mean = wave_mean_sq_128(x0, x1, s_o[l]);
             const float sc = 1.0f / sqrtf(mean + a.eps);
             const float *z = a.proj + (int64_t)l * DN_ROWS + DN_Z + vh * HV;
             const float o0 = ((x0 * sc) * a.ssm_norm[lane]) * v_silu(z[lane]);
             const float o1 = ((x1 * sc) * a.ssm_norm[lane + 64]) * v_silu(z[lane + 64]);
-            // Q8_0 blocks of 32: lanes 0..31 hold block 0 (o0) and block 2 (o1), lanes 32..63
-            // blocks 1 and 3; amax over 32 lanes
+            // Q8_0 blocks of 32: lanes 0..31 hold blocks 0 (o0) and 2 (o1), lanes 32..63 blocks 1 and 3
             float m0 = __builtin_fabsf(o0), m1 = __builtin_fabsf(o1);
             for (int mm = 16; mm >= 1; mm >>= 1) {
                 m0 = fmaxf(m0, shfl_xor_f(m0, mm));
@@ -311,11 +298,9 @@ void launch_dn(const RunCtl *ctl, const ModelRt &m, const LayerW &w, const ActBu
     a.dt_bias = w.dt_bias;
     a.ssm_norm = w.ssm_norm;
     a.eps = m.eps;
-    a.gdn = b.gdn;
     a.oq = b.oq;
     a.od = b.od;
-    a.counters = b.counters + CNT_DN;
-    hipLaunchKernelGGL(dn_kernel<OXE_NL>, dim3(NVH * DN_CHUNKS), dim3(256), 0, st, ctl, a);
+    hipLaunchKernelGGL(dn_kernel<OXE_NL>, dim3(NVH), dim3(DN_THREADS), 0, st, ctl, a);
 }
 
 // ------------------------------------------------------------------------------------------------

@@ -14,10 +14,111 @@ namespace oxe {
 
 using namespace shp;
 
+// Routing of one lane by one wave (engine.rs:3414-3429), lane tl holding experts 4tl..4tl+3:
+//   probs = oxe_soft_max_f32(logits, scale 1, no mask)   (oxe_ops.cpp:101-115): x*1, max, v_expf in
+//           groups of 4 with the group sum (v0+v1)+(v2+v3) added in double, scale by f32(1/sum)
+//   ids   = oxe_argsort_top_k_f32(probs, 8)              (oxe_ops.cpp:121-165)
+//   w_j   = probs[ids_j] / clamp(ggml_vec_sum_f32(w), 6.103515625e-5, inf)
+// The top 9 are taken by 9 wave arg-max rounds (largest value, then lowest index). When the 9 are
+// not strictly decreasing or the 9th value repeats (where the reference runs std::sort), the
+// lane's tie flag is set; the order used is then descending value, ascending index.
+OXE_DEV float wave_max_f(float v) {
+    for (int m = 32; m >= 1; m >>= 1) {
+        const float o = shfl_xor_f(v, m);
+        v = (v > o) ? v : o;
+    }
+    return v;
+}
+OXE_DEV int wave_min_i(int v) {
+    for (int m = 32; m >= 1; m >>= 1) {
+        const int o = shfl_xor_i(v, m);
+        v = v < o ? v : o;
+    }
+    return v;
+}
+OXE_DEV int wave_sum_i(int v) {
+    for (int m = 32; m >= 1; m >>= 1) v += shfl_xor_i(v, m);
+    return v;
+}
+
+struct RouteOut {
+    int32_t ids[OXE_NL][KUSED];
+    float w[OXE_NL][KUSED];
+    float gs[OXE_NL][NEXP / 4];
+    int32_t tie;
+};
+
+OXE_DEV void route_wave(const float *lg, int l, RouteOut &ro) {
+    const int tl = threadIdx.x & 63;
+    float p[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) p[k] = lg[4 * tl + k] * 1.0f;
+    float mx = p[0];
+#pragma unroll
+    for (int k = 1; k < 4; k++) mx = (mx > p[k]) ? mx : p[k];
+    mx = wave_max_f(mx);
+#pragma unroll
+    for (int k = 0; k < 4; k++) p[k] = v_expf(p[k] - mx);
+    const float g = (p[0] + p[1]) + (p[2] + p[3]);
+    ro.gs[l][tl] = g;
+    double P = (double)g;
+    for (int m = 32; m >= 1; m >>= 1) P += shfl_xor_d(P, m);
+    float f;
+    if (!bracket_ok_recip(P, P, NEXP / 4, &f)) {
+        double s = 0.0;
+        for (int i = 0; i < NEXP / 4; i++) s += (double)ro.gs[l][i];
+        f = (float)(1.0 / s);
+    }
+    bool nan = false;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        p[k] = p[k] * f;
+        nan |= p[k] != p[k];
+    }
+    // top 9 by wave arg-max rounds
+    bool taken[4] = {false, false, false, false};
+    float vals[KUSED + 1];
+    int ids[KUSED + 1];
+    for (int r = 0; r <= KUSED; r++) {
+        float bv = -__builtin_inff();
+        int bi = 0x7fffffff;
+#pragma unroll
+        for (int k = 0; k < 4; k++)
+            if (!taken[k] && (p[k] > bv || bi == 0x7fffffff)) { bv = p[k]; bi = 4 * tl + k; }
+        const float m = wave_max_f(bv);
+        const int i = wave_min_i(bv == m ? bi : 0x7fffffff);
+        if ((i >> 2) == tl) taken[i & 3] = true;
+        vals[r] = m;
+        ids[r] = i;
+    }
+    bool tie = false;
+    for (int r = 1; r <= KUSED; r++) tie |= !(vals[r - 1] > vals[r]);
+    int eq = 0;
+#pragma unroll
+    for (int k = 0; k < 4; k++) eq += p[k] == vals[KUSED];
+    eq = wave_sum_i(eq);
+    tie |= eq != 1;
+    tie |= wave_sum_i(nan ? 1 : 0) != 0;
+    if (tl == 0) {
+        double s = 0.0;
+        for (int j = 0; j < KUSED; j++) s += (double)vals[j];
+        float sf = (float)s;
+        sf = sf < __builtin_inff() ? sf : __builtin_inff();
+        sf = sf > 6.103515625e-5f ? sf : 6.103515625e-5f;
+        for (int j = 0; j < KUSED; j++) {
+            ro.ids[l][j] = ids[j];
+            ro.w[l][j] = vals[j] / sf;
+        }
+        if (tie) ro.tie = 1;
+    }
+}
+
 // ------------------------------------------------------------------------------------------------
-constexpr int RT_ROW_WG = NEXP / 16;       // 16 router workgroups of 16 rows
-constexpr int RT_SH_WG = 1;                // shared-gate dot
-constexpr int RT_GU_TILES = 2 * FFSH / 16; // 64 shared gate/up tiles
+constexpr int RT_ROWS = 8;                  // router rows per workgroup (staged in LDS)
+constexpr int RT_ROW_WG = NEXP / RT_ROWS;   // 32 router workgroups
+constexpr int RT_SH_WG = 1;                 // shared-gate dot
+constexpr int RT_GU_TILES = 2 * FFSH / 16;  // 64 shared gate/up tiles
+constexpr int RT_LDW = E + 16;              // padded LDS row of a staged router row
 
 struct RouterArgs {
     const float *x1;
@@ -41,9 +142,22 @@ __global__ __launch_bounds__(256) void router_kernel(const RunCtl *__restrict__ 
     __shared__ int8_t s_xq[NL][E];
     __shared__ uint16_t s_xd[NL][E / 32];
     __shared__ NormScratch ns;
-    __shared__ GemvSmem<E, R, NL> sm;
+    extern __shared__ float s_w[];  // [RT_ROWS][RT_LDW] staged f32 rows (router / shared-gate workgroups)
     if (!ctl->active) return;
-    const int nl = ctl->nl, t = threadIdx.x;
+    const int nl = ctl->nl, t = threadIdx.x, b = blockIdx.x;
+    const bool dot_wg = b < RT_ROW_WG + RT_SH_WG;
+    const bool sh = b == RT_ROW_WG;
+    // f32 rows first: their loads are in flight during the norm prologue
+    float4 wv[RT_ROWS * E / 4 / 256];
+    if (dot_wg) {
+#pragma unroll
+        for (int i = 0; i < RT_ROWS * E / 4 / 256; i++) {
+            const int idx = t + 256 * i, rr = idx / (E / 4);
+            if (sh && rr > 0) { wv[i] = make_float4(0, 0, 0, 0); continue; }
+            const float *row = sh ? a.shexp_gate : a.router + (int64_t)(b * RT_ROWS + rr) * E;
+            wv[i] = *(const float4 *)(row + 4 * (idx % (E / 4)));
+        }
+    }
 #pragma unroll
     for (int l = 0; l < NL; l++) {
         float v[EPT];
@@ -56,28 +170,34 @@ __global__ __launch_bounds__(256) void router_kernel(const RunCtl *__restrict__ 
         }
         store8(s_xn[l], v);
         quant8(v, &s_xq[l][EPT * t], &s_xd[l][(EPT * t) / 32]);
-        if (blockIdx.x == 0) {
+        if (b == 0) {
             store8(a.xn + (int64_t)l * E, v);
             *(uint2 *)(a.xq + (int64_t)l * 2 * E + EPT * t) = *(const uint2 *)&s_xq[l][EPT * t];
         }
     }
+    if (dot_wg) {
+#pragma unroll
+        for (int i = 0; i < RT_ROWS * E / 4 / 256; i++) {
+            const int idx = t + 256 * i, rr = idx / (E / 4);
+            *(float4 *)&s_w[rr * RT_LDW + 4 * (idx % (E / 4))] = wv[i];
+        }
+    }
     __syncthreads();
-    if (blockIdx.x == 0 && t < NL * (E / 32)) a.xd[(t / (E / 32)) * (2 * E / 32) + t % (E / 32)] = s_xd[t / (E / 32)][t % (E / 32)];
-    const int b = blockIdx.x;
-    if (b < RT_ROW_WG + RT_SH_WG) {
-        // f32 dots in ggml_vec_dot_f32 order: lane c of a 16-lane group runs chain c (elements
-        // c + 16 s); xor 8, 4, 1, 2 is the NEON reduction tree
+    if (b == 0 && t < NL * (E / 32)) a.xd[(t / (E / 32)) * (2 * E / 32) + t % (E / 32)] = s_xd[t / (E / 32)][t % (E / 32)];
+    if (dot_wg) {
+        // f32 dots in ggml_vec_dot_f32 order (vec.cpp:104-125): lane c of a 16-lane group runs chain
+        // c (elements c + 16 s); xor 8, 4, 1, 2 is the NEON reduction tree
         const int c = t & 15, rr = t >> 4;
-        const bool sh = b == RT_ROW_WG;
-        if (sh && rr > 0) return;
-        const float *w = sh ? a.shexp_gate : a.router + (int64_t)(b * 16 + rr) * E;
+        if (rr >= RT_ROWS || (sh && rr > 0)) return;
+        const float *w = &s_w[rr * RT_LDW];
         float acc[NL];
 #pragma unroll
         for (int l = 0; l < NL; l++) acc[l] = 0.0f;
+#pragma unroll 8
         for (int s = 0; s < E / 16; s++) {
-            const float wv = w[c + 16 * s];
+            const float x = w[c + 16 * s];
 #pragma unroll
-            for (int l = 0; l < NL; l++) acc[l] = __builtin_fmaf(wv, s_xn[l][c + 16 * s], acc[l]);
+            for (int l = 0; l < NL; l++) acc[l] = __builtin_fmaf(x, s_xn[l][c + 16 * s], acc[l]);
         }
 #pragma unroll
         for (int l = 0; l < NL; l++) {
@@ -88,12 +208,13 @@ __global__ __launch_bounds__(256) void router_kernel(const RunCtl *__restrict__ 
             v = v + shfl_xor_f(v, 2);
             if (c == 0 && l < nl) {
                 if (sh) a.sh_gate[l] = sigmoid_c(v);
-                else a.router_lg[l * NEXP + b * 16 + rr] = v;
+                else a.router_lg[l * NEXP + b * RT_ROWS + rr] = v;
             }
         }
         return;
     }
     // shared expert gate/up tile: rows 16*tile .. (8 gate rows then 8 up rows) -> 8 h values
+    __shared__ GemvSmem<E, R, NL> sm;
     const int tile = b - RT_ROW_WG - RT_SH_WG;
     const int8_t *xq[NL];
     const uint16_t *xd[NL];
@@ -120,107 +241,66 @@ void launch_router(const RunCtl *ctl, const ModelRt &m, const LayerW &w, const A
     a.xq = b.xq;
     a.xd = b.xd;
     a.xn = b.xn;
-    hipLaunchKernelGGL(router_kernel<OXE_NL>, dim3(RT_ROW_WG + RT_SH_WG + RT_GU_TILES), dim3(256), 0, st, ctl, a);
+    const size_t lds = (size_t)RT_ROWS * RT_LDW * 4;
+    static bool configured = false;
+    if (!configured) {
+        (void)hipFuncSetAttribute((const void *)router_kernel<OXE_NL>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        configured = true;
+    }
+    hipLaunchKernelGGL(router_kernel<OXE_NL>, dim3(RT_ROW_WG + RT_SH_WG + RT_GU_TILES), dim3(256), lds, st, ctl, a);
 }
 
-// ------------------------------------------------------------------------------------------------
-// Routing of one lane (engine.rs:3414-3429) by 256 threads (thread t = expert t):
-//   probs = oxe_soft_max_f32(logits, scale 1, no mask); ids = oxe_argsort_top_k_f32(probs, 8)
-//   w_j = probs[ids_j]; s = clamp(ggml_vec_sum_f32(w), 6.103515625e-5, inf); w_j /= s
-// Ties among the 9 largest probabilities (where the reference falls back to std::sort) are
-// counted in *tie_cnt; the order used is then descending value, ascending index.
-struct RouteSmem {
-    float p[NEXP];
-    float gs[NEXP / 4];
-    double red[8];
-    float mx[8];
-    int32_t ids[OXE_NL][KUSED];
-    float w[OXE_NL][KUSED];
-    int32_t uni[OXE_MAX_UNION];
-    int32_t n_uni;
-    int32_t tie;
+// routing of every lane (one wave each) and the union of the lanes' experts in first-use order,
+// lane-major (engine.rs:3414-3475)
+struct RouteArgs {
+    const float *router_lg;
+    int32_t *route_ids;       // [NL][KUSED]
+    float *route_w;           // [NL][KUSED]
+    int32_t *uni;             // [1 + OXE_MAX_UNION]
+    uint32_t *tie_cnt;
 };
 
 template <int NL>
-OXE_DEV void route_all(const RunCtl *ctl, const float *router_lg, RouteSmem &rs, uint32_t *tie_cnt, bool count_ties) {
-    const int nl = ctl->nl, t = threadIdx.x;
-    if (t == 0) rs.tie = 0;
-    if (t < OXE_NL * KUSED) { rs.ids[t / KUSED][t % KUSED] = 0; rs.w[t / KUSED][t % KUSED] = 0.0f; }
+__global__ __launch_bounds__(64 * NL) void route_kernel(const RunCtl *__restrict__ ctl, RouteArgs a) {
+    __shared__ RouteOut ro;
+    if (!ctl->active) return;
+    const int nl = ctl->nl, t = threadIdx.x, w = t >> 6;
+    if (t == 0) ro.tie = 0;
     __syncthreads();
-    for (int l = 0; l < nl; l++) {
-        const float wp = router_lg[l * NEXP + t] * 1.0f;
-        const float mx = block_max_f<256>(wp, rs.mx);
-        const float e = v_expf(wp - mx);
-        float g = e + shfl_xor_f(e, 1);
-        g = g + shfl_xor_f(g, 2);
-        if ((t & 3) == 0) rs.gs[t >> 2] = g;
-        const double P = block_sum_d<256>((t & 3) == 0 ? (double)g : 0.0, rs.red);
-        float f;
-        if (!bracket_ok_recip(P, P, NEXP / 4, &f)) {
-            if (t == 0) {
-                double s = 0.0;
-                for (int i = 0; i < NEXP / 4; i++) s += (double)rs.gs[i];
-                rs.red[0] = s;
-            }
-            __syncthreads();
-            f = (float)(1.0 / rs.red[0]);
-            __syncthreads();
-        }
-        const float pt = e * f;
-        rs.p[t] = pt;
-        __syncthreads();
-        int rank = 0;
-        bool eq = false;
-        for (int u = 0; u < NEXP; u++) {
-            const float pu = rs.p[u];
-            rank += (pu > pt) || (pu == pt && u < t);
-            eq |= (pu == pt) && (u != t);
-        }
-        if (rank <= KUSED && (eq || pt != pt)) rs.tie = 1;
-        if (rank < KUSED) { rs.ids[l][rank] = t; rs.w[l][rank] = pt; }
-        __syncthreads();
-        if (t == 0) {
-            double s = 0.0;
-            for (int j = 0; j < KUSED; j++) s += (double)rs.w[l][j];
-            float sf = (float)s;
-            sf = sf < __builtin_inff() ? sf : __builtin_inff();
-            sf = sf > 6.103515625e-5f ? sf : 6.103515625e-5f;
-            for (int j = 0; j < KUSED; j++) rs.w[l][j] = rs.w[l][j] / sf;
-        }
-        __syncthreads();
-    }
+    if (w < nl) route_wave(a.router_lg + w * NEXP, w, ro);
+    __syncthreads();
     if (t == 0) {
-        // union of the lanes' experts in first-use order, lane-major (engine.rs:3458-3475)
-        int n = 0;
+        int uni[OXE_MAX_UNION], n = 0;
         for (int l = 0; l < nl; l++)
             for (int j = 0; j < KUSED; j++) {
-                const int e = rs.ids[l][j];
+                const int e = ro.ids[l][j];
                 bool seen = false;
-                for (int u = 0; u < n; u++) seen |= rs.uni[u] == e;
-                if (!seen) rs.uni[n++] = e;
+                for (int u = 0; u < n; u++) seen |= uni[u] == e;
+                if (!seen) uni[n++] = e;
             }
-        rs.n_uni = n;
-        if (count_ties && rs.tie) atomicAdd(tie_cnt, 1u);
+        a.uni[0] = n;
+        for (int u = 0; u < OXE_MAX_UNION; u++) a.uni[1 + u] = u < n ? uni[u] : -1;
+        if (ro.tie) atomicAdd(a.tie_cnt, 1u);
     }
-    __syncthreads();
+    if (t < NL * KUSED && t / KUSED < nl) {
+        a.route_ids[t] = ro.ids[t / KUSED][t % KUSED];
+        a.route_w[t] = ro.w[t / KUSED][t % KUSED];
+    }
 }
 
-OXE_DEV int slot_of(const RouteSmem &rs, int l, int e) {
-    for (int j = 0; j < KUSED; j++)
-        if (rs.ids[l][j] == e) return j;
-    return -1;
+void launch_route(const RunCtl *ctl, const ActBufs &b, hipStream_t st) {
+    RouteArgs a{b.router_lg, b.route_ids, b.route_w, b.uni, b.counters + CNT_ERR_TIE};
+    hipLaunchKernelGGL(route_kernel<OXE_NL>, dim3(1), dim3(64 * OXE_NL), 0, st, ctl, a);
 }
 
 struct ExpertArgs {
-    const float *router_lg;
     const int8_t *xq;         // [NL][2E]
     const uint16_t *xd;       // [NL][2E/32]
     Q8W exp_gu;               // [NEXP][2FF][E]
     float *hexp;              // [NL][KUSED][FF]
-    int32_t *route_ids;
-    float *route_w;
-    int32_t *uni;
-    uint32_t *tie_cnt;
+    const int32_t *route_ids;
+    const int32_t *uni;
+    uint32_t *stats;          // [0] sum of union sizes, [1] launches
 };
 
 constexpr int EX_TILES = 2 * FF / 16;  // 64 tiles of 16 rows (8 gate + 8 up) per expert
@@ -228,22 +308,18 @@ constexpr int EX_TILES = 2 * FF / 16;  // 64 tiles of 16 rows (8 gate + 8 up) pe
 template <int NL>
 __global__ __launch_bounds__(256) void experts_kernel(const RunCtl *__restrict__ ctl, ExpertArgs a) {
     constexpr int R = GemvR<E>::R;
-    __shared__ RouteSmem rs;
     __shared__ GemvSmem<E, R, NL> sm;
     if (!ctl->active) return;
-    route_all<NL>(ctl, a.router_lg, rs, a.tie_cnt, blockIdx.x == 0);
     const int nl = ctl->nl, t = threadIdx.x;
-    if (blockIdx.x == 0) {
-        if (t < NL * KUSED) {
-            const int l = t / KUSED, j = t % KUSED;
-            if (l < nl) { a.route_ids[t] = rs.ids[l][j]; a.route_w[t] = rs.w[l][j]; }
-        }
-        if (t < OXE_MAX_UNION) a.uni[1 + t] = t < rs.n_uni ? rs.uni[t] : -1;
-        if (t == 0) a.uni[0] = rs.n_uni;
-    }
     const int u = blockIdx.x / EX_TILES, tile = blockIdx.x % EX_TILES;
-    if (u >= rs.n_uni) return;
-    const int e = rs.uni[u];
+    const int nu = a.uni[0];
+    if (blockIdx.x == 0 && t == 0) {
+        atomicAdd(a.stats, (uint32_t)nu);   // expert units streamed (algorithmic bytes)
+        atomicAdd(a.stats + 1, 1u);
+    }
+    if (u >= nu) return;
+    int e = a.uni[1 + u];
+    e = e < 0 ? 0 : (e >= NEXP ? NEXP - 1 : e);
     const int8_t *xq[NL];
     const uint16_t *xd[NL];
 #pragma unroll
@@ -254,7 +330,9 @@ __global__ __launch_bounds__(256) void experts_kernel(const RunCtl *__restrict__
     if (t < NL * 8) {
         const int l = t / 8, r = t % 8;
         if (l < nl) {
-            const int j = slot_of(rs, l, e);
+            int j = -1;
+            for (int jj = 0; jj < KUSED; jj++)
+                if (a.route_ids[l * KUSED + jj] == e) j = jj;
             if (j >= 0) a.hexp[((int64_t)l * KUSED + j) * FF + tile * 8 + r] = v_silu(sm.out[l][r]) * sm.out[l][8 + r];
         }
     }
@@ -262,15 +340,13 @@ __global__ __launch_bounds__(256) void experts_kernel(const RunCtl *__restrict__
 
 void launch_experts(const RunCtl *ctl, const LayerW &w, const ActBufs &b, hipStream_t st) {
     ExpertArgs a{};
-    a.router_lg = b.router_lg;
     a.xq = b.xq;
     a.xd = b.xd;
     a.exp_gu = w.exp_gu;
     a.hexp = b.hexp;
     a.route_ids = b.route_ids;
-    a.route_w = b.route_w;
     a.uni = b.uni;
-    a.tie_cnt = b.counters + CNT_ERR_TIE;
+    a.stats = b.counters + CNT_UNI_SUM;
     hipLaunchKernelGGL(experts_kernel<OXE_NL>, dim3(OXE_MAX_UNION * EX_TILES), dim3(256), 0, st, ctl, a);
 }
 

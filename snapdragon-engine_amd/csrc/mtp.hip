@@ -1,0 +1,332 @@
+// MTP depth-1 speculative decoding (crates/model/src/mtp.rs:314-608, MtpDriver with depth 1):
+//  * a host-driven driver with the reference's semantics (catch-up pairs, draft, 2-lane verify,
+//    greedy accept, commit, rewind) over the engine's host-driven calls, and
+//  * the device-driven step: the same state machine held in device memory (MtpState), one step
+//    = seed (if a pair is pending) -> draft -> verify -> accept/commit, all decided on the GPU and
+//    captured once as a HIP graph; K steps are K graph launches with no host round-trip.
+#include <hip/hip_runtime.h>
+
+#include <cstring>
+#include <vector>
+
+#include "../../include/oxe_amd.h"
+#include "oxe_engine.h"
+#include "oxe_engine_host.h"
+#include "oxe_model_kernels.h"
+#include "oxe_shape.h"
+
+namespace oxe {
+
+using namespace shp;
+
+OXE_HOST_DEV_INLINE uint32_t decode_key(unsigned long long k) { return k == 0 ? 0u : 0xffffffffu - (uint32_t)(k & 0xffffffffu); }
+
+// ---- device-driven step kernels ----------------------------------------------------------------
+
+__global__ void mtp_prep_seed_kernel(MtpState *ms, RunCtl *ctl) {
+    RunCtl r{};
+    r.nl = 1;
+    r.pos0 = ms->pos - 1;
+    r.cur = ms->cur;
+    r.tok[0] = ms->pend_tok;
+    r.hin_sel[0] = HID_PEND;
+    r.head_mask = 0;
+    r.active = ms->pending != 0 && ms->err == 0;
+    *ctl = r;
+}
+
+__global__ void mtp_prep_draft_kernel(MtpState *ms, RunCtl *ctl, int n_ctx) {
+    if (ms->pos + 2 > n_ctx) ms->err |= 1;  // no room for the 2-lane verify: stop (reference: k = 0)
+    RunCtl r{};
+    r.nl = 1;
+    r.pos0 = ms->pos;
+    r.cur = ms->cur;
+    r.tok[0] = ms->x;
+    r.hin_sel[0] = HID_HL;
+    r.head_mask = 1;
+    r.active = ms->err == 0;
+    *ctl = r;
+}
+
+__global__ void mtp_prep_verify_kernel(MtpState *ms, RunCtl *ctl, const unsigned long long *keys, const int32_t *force_d1,
+                                       int force_n) {
+    uint32_t d1 = decode_key(keys[0]);
+    if (force_d1 && ms->steps < force_n && force_d1[ms->steps] >= 0) d1 = (uint32_t)force_d1[ms->steps];  // test hook (mtp.rs:554-558)
+    ms->d1 = d1;
+    RunCtl r{};
+    r.nl = 2;
+    r.pos0 = ms->pos;
+    r.cur = ms->cur;
+    r.tok[0] = ms->x;
+    r.tok[1] = d1;
+    r.head_mask = 3;
+    r.hin_sel[0] = HID_HL;
+    r.hin_sel[1] = HID_PEND;
+    r.active = ms->err == 0;
+    *ctl = r;
+}
+
+// accept / commit / note (mtp.rs:564-591, engine.rs:2030-2039): a = (d1 == argmax lane 0)
+__global__ void mtp_commit_kernel(MtpState *ms, const unsigned long long *keys, float *hid, uint16_t *vcache,
+                                  int64_t vrows, int n_ctx, uint32_t *out_tok, int out_cap) {
+    __shared__ int s_a, s_ok, s_pos0;
+    const int t = threadIdx.x;
+    if (t == 0) {
+        s_ok = ms->err == 0;
+        const uint32_t g0 = decode_key(keys[0]);
+        s_a = s_ok && ms->d1 == g0;
+        s_pos0 = ms->pos;
+    }
+    __syncthreads();
+    if (!s_ok) return;
+    const int a = s_a, pos0 = s_pos0;
+    // hl = h_nextn after the last committed token; the accepted draft's pair (d1, h after x)
+    // waits for MTP seeding
+    for (int i = t; i < E; i += blockDim.x) {
+        const float h0 = hid[i], h1 = hid[E + i];
+        hid[(int64_t)HID_HL * E + i] = a ? h1 : h0;
+        if (a) hid[(int64_t)HID_PEND * E + i] = h0;
+    }
+    if (!a)  // the rejected lane's V^T column of the main attention layers back to +0 (zero_v)
+        for (int64_t r = t; r < vrows; r += blockDim.x) vcache[r * n_ctx + pos0 + 1] = 0;
+    if (t == 0) {
+        const uint32_t g0 = decode_key(keys[0]), g1 = decode_key(keys[1]);
+        int n = ms->n_out;
+        if (n < out_cap) out_tok[n++] = g0;
+        if (a && n < out_cap) out_tok[n++] = g1;
+        ms->n_out = n;
+        ms->x = a ? g1 : g0;
+        ms->pending = a;
+        ms->pend_tok = ms->d1;
+        ms->pos = pos0 + a + 1;
+        ms->cur = (ms->cur + a + 1) % OXE_NSLOTS;
+        ms->steps += 1;
+        ms->accepted += a;
+    }
+}
+
+// ---- host side ---------------------------------------------------------------------------------
+
+void MtpDriverHost::note(Engine &e, int p0, const uint32_t *toks, int n) {
+    std::vector<float> h((size_t)n * E);
+    for (int i = 0; i < n; i++) e.hidden_host(i, h.data() + (size_t)i * E);
+    for (int i = 0; i < n; i++) {
+        const int p = p0 + i;
+        if (p >= q) {
+            cu_tok.push_back(toks[i]);
+            if (i == 0) cu_h.insert(cu_h.end(), hl.begin(), hl.end());
+            else cu_h.insert(cu_h.end(), h.begin() + (size_t)(i - 1) * E, h.begin() + (size_t)i * E);
+        }
+    }
+    hl.assign(h.begin() + (size_t)(n - 1) * E, h.begin() + (size_t)n * E);
+}
+
+int MtpDriverHost::flush(Engine &e, size_t keep) {
+    while (cu_tok.size() > keep) {
+        const int n = (int)std::min<size_t>(OXE_NL, cu_tok.size());
+        const int rc = e.mtp_seed(cu_tok.data(), n, q, cu_h.data());
+        if (rc) return rc;
+        cu_tok.erase(cu_tok.begin(), cu_tok.begin() + n);
+        cu_h.erase(cu_h.begin(), cu_h.begin() + (size_t)n * E);
+        q += n;
+    }
+    return 0;
+}
+
+int MtpDriverHost::prefill(Engine &e, const uint32_t *toks, int n, uint32_t *next) {
+    uint32_t nx = 0xffffffffu;
+    for (int c0 = 0; c0 < n; c0 += OXE_NL) {
+        const int c = std::min(OXE_NL, n - c0);
+        const int p0 = e.pos;
+        uint32_t g[OXE_NL];
+        int rc = e.verify(toks + c0, c, g);
+        if (!rc) rc = e.commit(c);
+        if (rc) return rc;
+        nx = g[c - 1];
+        note(e, p0, toks + c0, c);
+        if ((rc = flush(e, 7))) return rc;  // the reference keeps up to mtp_lanes - 1 = 7 pairs pending
+    }
+    if (next) *next = nx;
+    return 0;
+}
+
+int MtpDriverHost::step(Engine &e, uint32_t x, uint32_t *out, int *n_out, int64_t override_d1) {
+    const int p = e.pos;
+    const int k = std::min(1, std::max(0, e.m.n_ctx - (p + 1)));
+    int rc = flush(e, 7);
+    if (rc) return rc;
+    if (k == 0) {
+        uint32_t g;
+        if ((rc = e.verify(&x, 1, &g)) || (rc = e.commit(1))) return rc;
+        note(e, p, &x, 1);
+        out[0] = g;
+        *n_out = 1;
+        return 0;
+    }
+    if ((rc = flush(e, 0))) return rc;
+    uint32_t d1;
+    if ((rc = e.mtp_run(&x, 1, p, hl.data(), 1, &d1))) return rc;
+    q = p + 1;
+    if (override_d1 >= 0) d1 = (uint32_t)override_d1;
+    const uint32_t vt[2] = {x, d1};
+    uint32_t g[2];
+    if ((rc = e.verify(vt, 2, g))) return rc;
+    const int a = d1 == g[0] ? 1 : 0;
+    if ((rc = e.commit(a + 1))) return rc;
+    note(e, p, vt, a + 1);
+    steps++;
+    accepted += a;
+    for (int i = 0; i <= a; i++) out[i] = g[i];
+    *n_out = a + 1;
+    return 0;
+}
+
+// device-driven: hand the host driver state to the device, run K graph steps, read it back
+int MtpDriverHost::dev_begin(Engine &e, uint32_t x) {
+    int rc = flush(e, 0);  // at most the pair the next step seeds stays pending: none here
+    if (rc) return rc;
+    MtpState s{};
+    s.pos = e.pos;
+    s.cur = e.cur;
+    s.x = x;
+    s.pending = 0;
+    s.n_out = 0;
+    if (hipMemcpyAsync(e.mtp_state, &s, sizeof(s), hipMemcpyHostToDevice, e.st) != hipSuccess) return -2;
+    if (hipMemcpyAsync(e.b.hid + (size_t)HID_HL * E, hl.data(), (size_t)E * 4, hipMemcpyHostToDevice, e.st) != hipSuccess) return -2;
+    return hipStreamSynchronize(e.st) == hipSuccess ? 0 : -2;
+}
+
+int MtpDriverHost::dev_end(Engine &e, uint32_t *out_tok, int cap, int *n_out, uint32_t *next_x) {
+    MtpState s{};
+    if (hipMemcpyAsync(&s, e.mtp_state, sizeof(s), hipMemcpyDeviceToHost, e.st) != hipSuccess) return -2;
+    if (hipStreamSynchronize(e.st) != hipSuccess) return -2;
+    const int n = std::min(s.n_out, cap);
+    if (n > 0 && hipMemcpy(out_tok, e.out_tok, (size_t)n * 4, hipMemcpyDeviceToHost) != hipSuccess) return -2;
+    *n_out = n;
+    *next_x = s.x;
+    hl.resize(E);
+    if (hipMemcpy(hl.data(), e.b.hid + (size_t)HID_HL * E, (size_t)E * 4, hipMemcpyDeviceToHost) != hipSuccess) return -2;
+    cu_tok.clear();
+    cu_h.clear();
+    if (s.pending) {
+        cu_tok.push_back(s.pend_tok);
+        cu_h.resize(E);
+        if (hipMemcpy(cu_h.data(), e.b.hid + (size_t)HID_PEND * E, (size_t)E * 4, hipMemcpyDeviceToHost) != hipSuccess) return -2;
+    }
+    q = s.pos - (s.pending ? 1 : 0);
+    e.pos = s.pos;
+    e.cur = s.cur;
+    e.pend_n = 0;
+    steps += s.steps;
+    accepted += s.accepted;
+    return s.err ? -4 : 0;
+}
+
+void Engine::enqueue_mtp_device_step() {
+    hipLaunchKernelGGL(mtp_prep_seed_kernel, dim3(1), dim3(1), 0, st, mtp_state, ctl);
+    enqueue_mtp_seed();
+    hipLaunchKernelGGL(mtp_prep_draft_kernel, dim3(1), dim3(1), 0, st, mtp_state, ctl, m.n_ctx);
+    enqueue_mtp_run();
+    hipLaunchKernelGGL(mtp_prep_verify_kernel, dim3(1), dim3(1), 0, st, mtp_state, ctl, (const unsigned long long *)b.amax_key,
+                       (const int32_t *)force_d1, force_n);
+    enqueue_verify();
+    hipLaunchKernelGGL(mtp_commit_kernel, dim3(1), dim3(256), 0, st, mtp_state, (const unsigned long long *)b.amax_key, b.hid,
+                       m.vcache, (int64_t)n_att_main * NKV * HD, m.n_ctx, out_tok, out_cap);
+}
+
+int Engine::mtp_steps_async(int k, bool use_graph) {
+    if (!use_graph) {
+        for (int i = 0; i < k; i++) enqueue_mtp_device_step();
+        return hipGetLastError() == hipSuccess ? 0 : -2;
+    }
+    if (!graph_exec) {
+        if (hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal) != hipSuccess) return -2;
+        enqueue_mtp_device_step();
+        hipGraph_t g;
+        if (hipStreamEndCapture(st, &g) != hipSuccess) return -2;
+        if (hipGraphInstantiate(&graph_exec, g, nullptr, nullptr, 0) != hipSuccess) return -2;
+        (void)hipGraphDestroy(g);
+    }
+    for (int i = 0; i < k; i++)
+        if (hipGraphLaunch(graph_exec, st) != hipSuccess) return -2;
+    return 0;
+}
+
+}  // namespace oxe
+
+using oxe::Engine;
+
+extern "C" {
+
+// Eagerly enqueue k device-driven MTP steps with HIP events around every launch of kernel `kind`
+// (engine stream); *avg_us = mean launch duration, *n = launches timed. For the bench's roofline.
+int oxe_mtp_device_probe(oxe_engine *e, int k, int kind, float *avg_us, int *n) {
+    Engine *g = (Engine *)e;
+    g->probe_kind = kind;
+    g->probe_used = 0;
+    const int rc = g->mtp_steps_async(k, false);
+    g->probe_kind = -1;
+    if (rc) return rc;
+    if (hipStreamSynchronize(g->st) != hipSuccess) return -2;
+    double tot = 0.0;
+    int cnt = 0;
+    for (size_t i = 0; i + 1 < g->probe_used; i += 2) {
+        float ms = 0.0f;
+        if (hipEventElapsedTime(&ms, g->probe_ev[i], g->probe_ev[i + 1]) != hipSuccess) return -2;
+        tot += ms;
+        cnt++;
+    }
+    *avg_us = cnt ? (float)(tot * 1000.0 / cnt) : 0.0f;
+    *n = cnt;
+    return 0;
+}
+
+int oxe_mtp_prefill(oxe_engine *e, const uint32_t *toks, int n, uint32_t *next) {
+    Engine *g = (Engine *)e;
+    if (n < 1 || !toks) return -1;
+    return g->drv.prefill(*g, toks, n, next);
+}
+
+int oxe_mtp_step(oxe_engine *e, uint32_t x, uint32_t *out, int *n_out, int64_t override_d1) {
+    Engine *g = (Engine *)e;
+    return g->drv.step(*g, x, out, n_out, override_d1);
+}
+
+int oxe_mtp_set_force(oxe_engine *e, const int32_t *force_d1, int n) {
+    Engine *g = (Engine *)e;
+    return g->set_force(force_d1, n);
+}
+
+int oxe_mtp_device_begin(oxe_engine *e, uint32_t x, int out_cap) {
+    Engine *g = (Engine *)e;
+    if (out_cap < 1) return -1;
+    if (g->ensure_out(out_cap)) return -3;
+    return g->drv.dev_begin(*g, x);
+}
+
+int oxe_mtp_device_steps(oxe_engine *e, int k, int use_graph) {
+    Engine *g = (Engine *)e;
+    if (k < 0) return -1;
+    return g->mtp_steps_async(k, use_graph != 0);
+}
+
+int oxe_mtp_device_end(oxe_engine *e, uint32_t *out_tok, int cap, int *n_out, uint32_t *next_x) {
+    Engine *g = (Engine *)e;
+    return g->drv.dev_end(*g, out_tok, cap, n_out, next_x);
+}
+
+int oxe_mtp_stats(const oxe_engine *e, int64_t *st) {
+    const Engine *g = (const Engine *)e;
+    st[0] = g->drv.steps;
+    st[1] = g->drv.accepted;
+    return 0;
+}
+
+int oxe_engine_sync(oxe_engine *e) {
+    Engine *g = (Engine *)e;
+    return hipStreamSynchronize(g->st) == hipSuccess ? 0 : -2;
+}
+
+void *oxe_engine_stream(oxe_engine *e) { return (void *)((Engine *)e)->st; }
+
+}  // extern "C"

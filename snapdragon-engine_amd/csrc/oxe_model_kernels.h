@@ -10,7 +10,7 @@
 namespace oxe {
 
 // ids of the self-resetting completion counters in ActBufs::counters
-enum CounterId { CNT_DN = 0, CNT_ERR_TIE = 64, CNT_ERR_SUM = 65, CNT_N = 128 };
+enum CounterId { CNT_DN = 0, CNT_ERR_TIE = 64, CNT_ROUTE = 65, CNT_UNI_SUM = 66, CNT_EXP_CALLS = 67, CNT_N = 128 };
 
 struct ModelRt {
     // runtime shape
@@ -40,6 +40,7 @@ void launch_kwrite(const RunCtl *ctl, const ModelRt &m, const LayerW &w, const A
 void launch_scores(const RunCtl *ctl, const ModelRt &m, const LayerW &w, const ActBufs &b, hipStream_t st);
 void launch_pv(const RunCtl *ctl, const ModelRt &m, const LayerW &w, const ActBufs &b, hipStream_t st);
 void launch_router(const RunCtl *ctl, const ModelRt &m, const LayerW &w, const ActBufs &b, hipStream_t st);
+void launch_route(const RunCtl *ctl, const ActBufs &b, hipStream_t st);
 void launch_experts(const RunCtl *ctl, const LayerW &w, const ActBufs &b, hipStream_t st);
 void launch_down(const RunCtl *ctl, const LayerW &w, const ActBufs &b, hipStream_t st);
 void launch_head(const RunCtl *ctl, const ModelRt &m, const float *norm_w, const ActBufs &b, bool store_logits,

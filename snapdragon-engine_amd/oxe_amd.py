@@ -113,6 +113,16 @@ def _engine_sigs(L):
         "oxe_engine_state_copy": (i32, [vp, i32, i32, i64, vp, i64]),
         "oxe_engine_set_pos": (i32, [vp, i32]),
         "oxe_engine_device_bytes": (i64, [vp]),
+        "oxe_mtp_prefill": (i32, [vp, u32p, i32, u32p]),
+        "oxe_mtp_step": (i32, [vp, C.c_uint32, u32p, C.POINTER(C.c_int), i64]),
+        "oxe_mtp_device_begin": (i32, [vp, C.c_uint32, i32]),
+        "oxe_mtp_device_steps": (i32, [vp, i32, i32]),
+        "oxe_mtp_device_end": (i32, [vp, u32p, i32, C.POINTER(C.c_int), u32p]),
+        "oxe_mtp_set_force": (i32, [vp, C.POINTER(C.c_int32), i32]),
+        "oxe_mtp_stats": (i32, [vp, C.POINTER(C.c_int64)]),
+        "oxe_engine_sync": (i32, [vp]),
+        "oxe_mtp_device_probe": (i32, [vp, i32, i32, C.POINTER(C.c_float), C.POINTER(C.c_int)]),
+        "oxe_engine_stream": (vp, [vp]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -217,3 +227,56 @@ class Engine:
 
     def set_pos(self, pos):
         check(lib().oxe_engine_set_pos(self.h, pos), "set_pos")
+
+    # ---- MTP depth-1 driver (mtp.rs MtpDriver) ----
+    def mtp_prefill(self, toks):
+        import numpy as np
+        t = np.ascontiguousarray(toks, np.uint32)
+        nx = np.zeros(1, np.uint32)
+        check(lib().oxe_mtp_prefill(self.h, _np_ptr(t, C.c_uint32), len(t), _np_ptr(nx, C.c_uint32)), "mtp_prefill")
+        return int(nx[0])
+
+    def mtp_step(self, x, override_d1=-1):
+        import numpy as np
+        out = np.zeros(8, np.uint32)
+        n = C.c_int(0)
+        check(lib().oxe_mtp_step(self.h, x, _np_ptr(out, C.c_uint32), C.byref(n), override_d1), "mtp_step")
+        return [int(v) for v in out[: n.value]]
+
+    def mtp_set_force(self, force):
+        import numpy as np
+        f = np.ascontiguousarray(force, np.int32)
+        check(lib().oxe_mtp_set_force(self.h, f.ctypes.data_as(C.POINTER(C.c_int32)), len(f)), "mtp_set_force")
+
+    def mtp_device_begin(self, x, out_cap):
+        check(lib().oxe_mtp_device_begin(self.h, x, out_cap), "mtp_device_begin")
+
+    def mtp_device_steps(self, k, use_graph=True):
+        check(lib().oxe_mtp_device_steps(self.h, k, int(use_graph)), "mtp_device_steps")
+
+    def mtp_device_end(self, cap):
+        import numpy as np
+        out = np.zeros(cap, np.uint32)
+        n = C.c_int(0)
+        nx = np.zeros(1, np.uint32)
+        check(lib().oxe_mtp_device_end(self.h, _np_ptr(out, C.c_uint32), cap, C.byref(n), _np_ptr(nx, C.c_uint32)),
+              "mtp_device_end")
+        return [int(v) for v in out[: n.value]], int(nx[0])
+
+    def mtp_stats(self):
+        import numpy as np
+        s = np.zeros(2, np.int64)
+        lib().oxe_mtp_stats(self.h, s.ctypes.data_as(C.POINTER(C.c_int64)))
+        return dict(steps=int(s[0]), accepted=int(s[1]))
+
+    def mtp_device_probe(self, k, kind):
+        avg = C.c_float(0)
+        n = C.c_int(0)
+        check(lib().oxe_mtp_device_probe(self.h, k, kind, C.byref(avg), C.byref(n)), "mtp_device_probe")
+        return float(avg.value), int(n.value)
+
+    def sync(self):
+        check(lib().oxe_engine_sync(self.h), "sync")
+
+    def stream(self):
+        return lib().oxe_engine_stream(self.h)
