@@ -39,6 +39,12 @@ OXE_API int oxe_hip_quantize_row_q8_0(const float *x, int64_t k, int64_t nrows, 
 OXE_API int oxe_hip_gemv_q8_0(int64_t k, int64_t nr, int nl, const int8_t *wq, const uint16_t *wd, const int8_t *xq,
                               const uint16_t *xd, float *y, int32_t *isum, void *stream);
 
+/* Parity hook (no counterpart in the reference): y[i] = f(x) for the float x with bits
+ * start + i*stride, i < n, on the device; f: 0 expf and 1 log1pf (the C library functions the
+ * reference calls, oxe_ops.cpp:80-89), 2 ggml_v_expf (vec.h:1154-1175), 3 the sigmoid and
+ * 4 the softplus of oxe_ops.cpp:80-89, 5 ggml_v_silu (vec.h:1178-1185). */
+OXE_API int oxe_hip_eval_unary(int fn, uint32_t start, int64_t n, int64_t stride, float *y, void *stream);
+
 /* ---- engine level (crates/model/src/engine.rs Engine; one engine per stream) -------------- */
 
 /* Last error message of a failed call on this host thread (no exceptions cross the C ABI). */

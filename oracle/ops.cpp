@@ -478,4 +478,23 @@ void oxo_attn_head_f16(const float *q, const uint16_t *k, int64_t k_stride, cons
     delete[] kq; delete[] mask; delete[] wp; delete[] p16;
 }
 
+// Test helper: the host-side counterparts of oxe_hip_eval_unary (0 the C library's expf, 1 its
+// log1pf, 2 oxo_v_expf, 3 sigmoid, 4 softplus, 5 oxo_v_silu) over float bit patterns start + i*stride.
+void oxo_eval_unary(int fn, uint32_t start, int64_t n, int64_t stride, float *y) {
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < n; i++) {
+        const float x = u2f((uint32_t)(start + (uint64_t)i * (uint64_t)stride));
+        float r;
+        switch (fn) {
+            case 0: r = expf(x); break;
+            case 1: r = log1pf(x); break;
+            case 2: r = oxo_v_expf(x); break;
+            case 3: oxo_sigmoid_f32(1, &r, &x); break;
+            case 4: oxo_softplus_f32(1, &r, &x); break;
+            default: r = oxo_v_silu(x); break;
+        }
+        y[i] = r;
+    }
+}
+
 }  // extern "C"

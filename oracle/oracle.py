@@ -93,6 +93,7 @@ def lib():
             "oxo_rope_neox_inplace": (None, [f32p, C.c_int, f32p]),
             "oxo_attn_head_f16": (None, [f32p, u16p, C.c_int64, u16p, u16p, C.c_int64, C.c_int, C.c_int, C.c_int,
                                          C.c_float, f32p]),
+            "oxo_eval_unary": (None, [C.c_int, C.c_uint32, C.c_int64, C.c_int64, f32p]),
             "oxo_engine_new": (C.c_void_p, [P(ModelDesc), C.c_uint64, C.c_int64]),
             "oxo_engine_free": (None, [C.c_void_p]),
             "oxo_engine_reset": (None, [C.c_void_p]),

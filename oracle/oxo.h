@@ -67,6 +67,9 @@ void  oxo_attn_head_f16(const float *q, const uint16_t *k, int64_t k_stride, con
                         const uint16_t *vt, int64_t v_stride, int n_kv, int pos_last, int head_dim,
                         float scale, float *out);                                             // :465-493
 
+// test helper: host counterparts of the device's oxe_hip_eval_unary over float bit patterns
+void  oxo_eval_unary(int fn, uint32_t start, int64_t n, int64_t stride, float *y);
+
 #ifdef __cplusplus
 }
 #endif

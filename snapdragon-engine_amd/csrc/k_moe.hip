@@ -76,22 +76,24 @@ OXE_DEV void route_wave(const float *lg, int l, RouteOut &ro) {
         nan |= p[k] != p[k];
     }
     // top 9 by wave arg-max rounds
-    bool taken[4] = {false, false, false, false};
+    unsigned taken = 0;  // bit k: expert 4tl+k already picked
     float vals[KUSED + 1];
     int ids[KUSED + 1];
+#pragma unroll
     for (int r = 0; r <= KUSED; r++) {
         float bv = -__builtin_inff();
         int bi = 0x7fffffff;
 #pragma unroll
         for (int k = 0; k < 4; k++)
-            if (!taken[k] && (p[k] > bv || bi == 0x7fffffff)) { bv = p[k]; bi = 4 * tl + k; }
+            if (!((taken >> k) & 1) && (p[k] > bv || bi == 0x7fffffff)) { bv = p[k]; bi = 4 * tl + k; }
         const float m = wave_max_f(bv);
         const int i = wave_min_i(bv == m ? bi : 0x7fffffff);
-        if ((i >> 2) == tl) taken[i & 3] = true;
+        if ((i >> 2) == tl) taken |= 1u << (i & 3);
         vals[r] = m;
         ids[r] = i;
     }
     bool tie = false;
+#pragma unroll
     for (int r = 1; r <= KUSED; r++) tie |= !(vals[r - 1] > vals[r]);
     int eq = 0;
 #pragma unroll
@@ -101,10 +103,12 @@ OXE_DEV void route_wave(const float *lg, int l, RouteOut &ro) {
     tie |= wave_sum_i(nan ? 1 : 0) != 0;
     if (tl == 0) {
         double s = 0.0;
+#pragma unroll
         for (int j = 0; j < KUSED; j++) s += (double)vals[j];
         float sf = (float)s;
         sf = sf < __builtin_inff() ? sf : __builtin_inff();
         sf = sf > 6.103515625e-5f ? sf : 6.103515625e-5f;
+#pragma unroll
         for (int j = 0; j < KUSED; j++) {
             ro.ids[l][j] = ids[j];
             ro.w[l][j] = vals[j] / sf;
@@ -269,18 +273,24 @@ __global__ __launch_bounds__(64 * NL) void route_kernel(const RunCtl *__restrict
     __syncthreads();
     if (w < nl) route_wave(a.router_lg + w * NEXP, w, ro);
     __syncthreads();
-    if (t == 0) {
-        int uni[OXE_MAX_UNION], n = 0;
-        for (int l = 0; l < nl; l++)
-            for (int j = 0; j < KUSED; j++) {
-                const int e = ro.ids[l][j];
-                bool seen = false;
-                for (int u = 0; u < n; u++) seen |= uni[u] == e;
-                if (!seen) uni[n++] = e;
-            }
-        a.uni[0] = n;
-        for (int u = 0; u < OXE_MAX_UNION; u++) a.uni[1 + u] = u < n ? uni[u] : -1;
-        if (ro.tie) atomicAdd(a.tie_cnt, 1u);
+    if (t < 64) {
+        // union in first-use order, lane-major: entry t = (lane t/8, rank t%8) is new when no earlier
+        // entry holds the same expert; its slot is the number of new entries before it
+        const int e = t < nl * KUSED ? ro.ids[t / KUSED][t % KUSED] : -1;
+        bool isnew = e >= 0;
+#pragma unroll
+        for (int u = 0; u < NL * KUSED; u++) {
+            const int o = __shfl(e, u);
+            isnew &= !(u < t && o == e);
+        }
+        const unsigned long long mask = __ballot(isnew);
+        const int n = __popcll(mask);
+        if (isnew) a.uni[1 + __popcll(mask & ((1ull << t) - 1))] = e;
+        if (t >= n && t < OXE_MAX_UNION) a.uni[1 + t] = -1;
+        if (t == 0) {
+            a.uni[0] = n;
+            if (ro.tie) atomicAdd(a.tie_cnt, 1u);
+        }
     }
     if (t < NL * KUSED && t / KUSED < nl) {
         a.route_ids[t] = ro.ids[t / KUSED][t % KUSED];

@@ -283,12 +283,13 @@ int oxe_mtp_device_probe(oxe_engine *e, int k, int kind, float *avg_us, int *n) 
 
 int oxe_mtp_prefill(oxe_engine *e, const uint32_t *toks, int n, uint32_t *next) {
     Engine *g = (Engine *)e;
-    if (n < 1 || !toks) return -1;
+    if (n < 1 || !g->toks_ok(toks, n) || g->pos + n > g->m.n_ctx) return -1;
     return g->drv.prefill(*g, toks, n, next);
 }
 
 int oxe_mtp_step(oxe_engine *e, uint32_t x, uint32_t *out, int *n_out, int64_t override_d1) {
     Engine *g = (Engine *)e;
+    if (!g->toks_ok(&x, 1) || override_d1 >= g->d.n_vocab || !out || !n_out) return -1;
     return g->drv.step(*g, x, out, n_out, override_d1);
 }
 
@@ -299,7 +300,7 @@ int oxe_mtp_set_force(oxe_engine *e, const int32_t *force_d1, int n) {
 
 int oxe_mtp_device_begin(oxe_engine *e, uint32_t x, int out_cap) {
     Engine *g = (Engine *)e;
-    if (out_cap < 1) return -1;
+    if (out_cap < 1 || !g->toks_ok(&x, 1)) return -1;
     if (g->ensure_out(out_cap)) return -3;
     return g->drv.dev_begin(*g, x);
 }

@@ -98,6 +98,8 @@ struct Engine {
         return 0;
     }
     int set_force(const int32_t *f, int n) {
+        for (int i = 0; i < n; i++)
+            if (f[i] >= d.n_vocab) return -1;
         if (n <= 0) {
             force_n = 0;
             force_d1 = nullptr;
@@ -394,9 +396,15 @@ struct Engine {
         r.active = 1;
         return r;
     }
+    // token ids index the embedding rows: every id from the host is checked before any launch
+    bool toks_ok(const uint32_t *toks, int n) const {
+        if (!toks) return false;
+        for (int i = 0; i < n; i++)
+            if (toks[i] >= (uint32_t)d.n_vocab) return false;
+        return true;
+    }
     int verify(const uint32_t *toks, int n, uint32_t *out) {
-        if (n < 1 || n > OXE_NL || pos + n > m.n_ctx) return -1;
-        for (int i = 0; i < n; i++) if (toks[i] >= (uint32_t)d.n_vocab) return -1;
+        if (n < 1 || n > OXE_NL || pos + n > m.n_ctx || !toks_ok(toks, n)) return -1;
         launch_set_run(ctl, run(n, pos, toks, (1 << n) - 1), st);
         enqueue_verify();
         pend_pos0 = pos;
@@ -420,7 +428,7 @@ struct Engine {
         return hipMemcpyAsync(b.hid + (size_t)HID_HL * E, hs, (size_t)n * E * 4, hipMemcpyHostToDevice, st) == hipSuccess ? 0 : -2;
     }
     int mtp_run(const uint32_t *toks, int n, int pos0, const float *hs, int head_last, uint32_t *out) {
-        if (n < 1 || n > OXE_NL || pos0 + n > m.n_ctx) return -1;
+        if (n < 1 || n > OXE_NL || pos0 < 0 || pos0 + n > m.n_ctx || !toks_ok(toks, n) || !hs) return -1;
         if (set_hidden(hs, n)) return -2;
         launch_set_run(ctl, run(n, pos0, toks, head_last ? 1 << (n - 1) : 0), st);
         enqueue_mtp_run();
@@ -430,7 +438,7 @@ struct Engine {
         return 0;
     }
     int mtp_seed(const uint32_t *toks, int n, int pos0, const float *hs) {
-        if (n < 1 || n > OXE_NL || pos0 + n > m.n_ctx) return -1;
+        if (n < 1 || n > OXE_NL || pos0 < 0 || pos0 + n > m.n_ctx || !toks_ok(toks, n) || !hs) return -1;
         if (set_hidden(hs, n)) return -2;
         launch_set_run(ctl, run(n, pos0, toks, 0), st);
         enqueue_mtp_seed();

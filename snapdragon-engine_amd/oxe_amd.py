@@ -30,6 +30,7 @@ def lib():
         sig = {
             "oxe_hip_quantize_row_q8_0": (i32, [vp, i64, i64, vp, vp, vp]),
             "oxe_hip_gemv_q8_0": (i32, [i64, i64, i32, vp, vp, vp, vp, vp, vp, vp]),
+            "oxe_hip_eval_unary": (i32, [i32, C.c_uint32, i64, i64, vp, vp]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -88,6 +89,12 @@ def gemv_q8_0(wq, wd, xq, xd, y=None, isum=None):
     if y is None:
         y = torch.empty((nl, nr), dtype=torch.float32, device=wq.device)
     check(lib().oxe_hip_gemv_q8_0(k, nr, nl, _p(wq), _p(wd), _p(xq), _p(xd), _p(y), _p(isum), _stream()), "gemv_q8_0")
+    return y
+
+
+def eval_unary(fn, start, n, stride, y):
+    """y[i] = device scalar function fn at the float with bits start + i*stride (parity hook)."""
+    check(lib().oxe_hip_eval_unary(fn, start, n, stride, _p(y), _stream()), "eval_unary")
     return y
 
 

@@ -1,0 +1,88 @@
+"""The oracle engine against the invariants the reference's own tests hold (no GPU).
+
+  verify(n) == n single steps, bit for bit (crates/model/src/tests.rs:868-926)
+  a rejected lane leaves no trace: verify([a, b]), commit(1) == step(a) (same file, random tails)
+  MTP depth-1 greedy == plain greedy, with forced drafts hitting accept and reject
+  (crates/model/src/tests.rs:1033-1117, draft_override hook mtp.rs:328-330)
+on the 4-layer model with the 35B-A3B per-layer shapes (3 delta-net + 1 attention layer + MTP).
+"""
+import numpy as np
+import pytest
+
+import oracle as O
+
+SEED = 11
+
+
+def bits(a):
+    return np.ascontiguousarray(a, np.float32).view(np.uint32)
+
+
+@pytest.fixture(scope="module")
+def desc():
+    return O.desc_small()
+
+
+def test_verify_equals_steps(desc):
+    a = O.Engine(desc, seed=SEED, n_ctx=256)
+    b = O.Engine(desc, seed=SEED, n_ctx=256)
+    for toks in ([17, 3001], [5, 6], [4095, 0]):
+        g = a.verify(toks)
+        la = [a.logits(i) for i in range(2)]
+        ha = [a.hidden(i) for i in range(2)]
+        a.commit(2)
+        for i, t in enumerate(toks):
+            assert b.step(t) == g[i]
+            assert np.array_equal(bits(b.logits(0)), bits(la[i]))
+            assert np.array_equal(bits(b.hidden(0)), bits(ha[i]))
+    assert a.pos == b.pos == 6
+
+
+def test_rejected_lane_leaves_no_trace(desc):
+    a = O.Engine(desc, seed=SEED, n_ctx=256)
+    b = O.Engine(desc, seed=SEED, n_ctx=256)
+    for x, rej, nxt in ((100, 2000, 7), (8, 9, 10), (77, 1234, 4000)):
+        a.verify([x, rej])
+        a.commit(1)
+        ga = a.step(nxt)
+        b.step(x)
+        gb = b.step(nxt)
+        assert ga == gb
+        assert np.array_equal(bits(a.logits(0)), bits(b.logits(0)))
+        assert np.array_equal(bits(a.hidden(0)), bits(b.hidden(0)))
+
+
+def plain_greedy(desc, prompt, n):
+    e = O.Engine(desc, seed=SEED, n_ctx=256)
+    x = None
+    for t in prompt:
+        x = e.step(int(t))
+    out = []
+    for _ in range(n):
+        out.append(x)
+        x = e.step(x)
+    return out, x
+
+
+def test_mtp_greedy_equals_plain_with_forced_drafts(desc):
+    prompt = (O.bench_prompt(5) % desc.n_vocab).tolist()
+    n = 14
+    ref, _ = plain_greedy(desc, prompt, n + 2)
+    e = O.Engine(desc, seed=SEED, n_ctx=256)
+    drv = O.Driver(e)
+    x = drv.prefill(prompt)
+    assert x == ref[0]
+    got = [x]
+    pattern = [1, 0, 1, 1, 0, 0, 1, 0, 1]   # 1: force the correct draft (accept), 0: a wrong one
+    i = 0
+    while len(got) < n:
+        k = len(got)
+        d1 = ref[k] if pattern[i % len(pattern)] else (ref[k] + 1) % desc.n_vocab
+        out = drv.step(x, override_d1=d1)
+        assert len(out) == (2 if pattern[i % len(pattern)] else 1)
+        got += out
+        x = out[-1]
+        i += 1
+    assert got[:n] == ref[:n]
+    st = drv.stats()
+    assert st["accepted"] == sum(pattern[j % len(pattern)] for j in range(i))
