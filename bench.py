@@ -85,6 +85,27 @@ def cpu_baseline(seconds, prompt_len=8):
                       f"{wall:.1f} s wall minus {gen:.1f} s spent generating synthetic expert weights on first use"}
 
 
+def calibrate_copy(torch, mib=1024, reps=4):
+    """A plain copy of `mib` MiB, `reps` times: under rocprofv3 --pmc its FETCH_SIZE / WRITE_SIZE
+    per dispatch calibrate the byte counters (bytes moved are known exactly)."""
+    src = torch.ones(mib << 18, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(reps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"calibrate_copy_bytes": mib << 20, "reps": reps}), flush=True)
+
+
+def load_traffic(kernel):
+    """Measured HBM traffic of `kernel` (profiles/<kernel>_traffic.json: rocprofv3 --pmc FETCH_SIZE
+    and WRITE_SIZE per dispatch, calibrated against a plain copy), or None."""
+    path = os.path.join(ROOT, "profiles", f"{kernel}_traffic.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        return json.load(f)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -94,13 +115,17 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--probe-kind", type=int, default=1, help="kernel kind timed for the roofline (1 = experts gate/up)")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="only run a plain device copy of known size (the PMC byte-counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build runs the whole MTP-1 step on a single MI355X "
               f"(--gpus {args.gpus} is not supported; see DESIGN.md for how the path would shard)", file=sys.stderr)
         sys.exit(2)
-    import numpy as np
     import torch
+    if args.calibrate_copy:
+        calibrate_copy(torch)
+        return
     import oxe_amd as A
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as O  # the model description struct and bench prompt only
@@ -149,11 +174,16 @@ def main():
     eng.mtp_device_begin(x, cap)
     uni1, calls1 = eng.counter(66), eng.counter(67)
     probe_steps = 8
-    avg_us, n_launch = eng.mtp_device_probe(probe_steps, args.probe_kind)
+    avg_us, n_launch = eng.mtp_device_probe(probe_steps, args.probe_kind, use_graph=True)
     eng.mtp_device_end(cap)
     u_per_launch = (eng.counter(66) - uni1) / max(eng.counter(67) - calls1, 1)
     k_bytes = u_per_launch * EXPERT_GU
     k_gbs = k_bytes / (avg_us * 1e-6) / 1e9 if avg_us > 0 else 0.0
+    tr = load_traffic("experts_kernel")
+    traffic = None
+    if tr is not None:
+        # measured bytes per expert unit (a 16-row gate/up tile pair set of one union expert)
+        traffic = int(tr["hbm_bytes_per_unit"] * u_per_launch)
     result = {
         "metric": "MTP-1 decode tok/s (35B-A3B shape, int8) + HBM GB/s as % of ~8 TB/s peak",
         "value": round(tok_s, 3),
@@ -177,7 +207,7 @@ def main():
         "hbm_frac_step": round(step_gbs / PEAK_HBM_GBS, 4),
         "expert_units_per_step": round(units / max(args.steps, 1), 3),
         "roofline": {"bound": "hbm", "achieved": round(k_gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                     "frac": round(k_gbs / PEAK_HBM_GBS, 4), "traffic": None,
+                     "frac": round(k_gbs / PEAK_HBM_GBS, 4), "traffic": traffic,
                      "kernel": "experts_kernel (routed gate/up GEMV + swiglu)", "avg_us": round(avg_us, 3),
                      "launches_timed": n_launch, "bytes_per_launch": int(k_bytes)},
         "setup_s": round(setup_s, 1),

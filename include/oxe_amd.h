@@ -95,6 +95,13 @@ OXE_API int oxe_mtp_prefill(oxe_engine *e, const uint32_t *toks, int n, uint32_t
  * = the greedy tokens that follow (accepted draft + bonus). override_d1 >= 0 replaces the draft
  * (the reference's draft_override test hook, mtp.rs:328-330). */
 OXE_API int oxe_mtp_step(oxe_engine *e, uint32_t x, uint32_t *out, int *n_out, int64_t override_d1);
+/* One plain target step from x that keeps the MTP catch-up in sync (MtpDriver::step_plain,
+ * mtp.rs:504-515); *out = argmax after x. */
+OXE_API int oxe_mtp_step_plain(oxe_engine *e, uint32_t x, uint32_t *out);
+/* Keep only the first m (1..committed) tokens of the last host-driven step (MtpDriver::rewind,
+ * mtp.rs:596-608; the server's spec_rewind, crates/server/src/engine.rs:100-104). -1 without a
+ * step to rewind. */
+OXE_API int oxe_mtp_rewind(oxe_engine *e, int m);
 /* Device-driven steps: begin hands the driver state to the GPU; each of the k steps then runs
  * seed -> draft -> 2-lane verify -> greedy accept/commit on the GPU (one HIP graph per step, no
  * host round-trip); end synchronises and returns the emitted tokens and the next x. */
@@ -103,10 +110,11 @@ OXE_API int oxe_mtp_device_steps(oxe_engine *e, int k, int use_graph);
 OXE_API int oxe_mtp_device_end(oxe_engine *e, uint32_t *out_tok, int cap, int *n_out, uint32_t *next_x);
 /* Forced drafts for the device-driven steps (test hook): force_d1[i] >= 0 replaces step i's draft. */
 OXE_API int oxe_mtp_set_force(oxe_engine *e, const int32_t *force_d1, int n);
-/* Eager device-driven steps with HIP events around each launch of one kernel kind (0 LM head,
+/* k device-driven steps with HIP events around each launch of one kernel kind (0 LM head,
  * 1 experts gate/up, 2 down, 3 projections, 4 mixer out, 5 delta-net, 6 router, 7 scores, 8 pv,
- * 9 MTP entry): mean launch duration in microseconds (roofline measurement). */
-OXE_API int oxe_mtp_device_probe(oxe_engine *e, int k, int kind, float *avg_us, int *n);
+ * 9 MTP entry): mean kernel duration in microseconds (roofline measurement). use_graph: the events
+ * are nodes of the captured step graph (the timed configuration); else eager launches. */
+OXE_API int oxe_mtp_device_probe(oxe_engine *e, int k, int kind, int use_graph, float *avg_us, int *n);
 /* steps, accepted drafts */
 OXE_API int oxe_mtp_stats(const oxe_engine *e, int64_t *st);
 OXE_API int oxe_engine_sync(oxe_engine *e);

@@ -511,8 +511,18 @@ struct oxo_driver {
     std::vector<float> cu_h;
     std::vector<float> hl;
     int64_t steps = 0, drafted = 0, accepted = 0, tokens_out = 0;
+    int64_t last_p0 = 0;
+    int last_n = 0;                // MtpDriver.last (mtp.rs:336)
+    std::vector<float> last_h;     // MtpDriver.last_h
 
     int mtp_lanes() const { return eng->max_lanes; }
+
+    void remember(int64_t p0, int n) {
+        last_p0 = p0;
+        last_n = n;
+        last_h.clear();
+        for (int i = 0; i < n; i++) last_h.insert(last_h.end(), eng->hout[i].begin(), eng->hout[i].end());
+    }
 
     void note(int64_t p0, const uint32_t *toks, int n) {
         const int64_t E = eng->d.n_embd;
@@ -564,6 +574,7 @@ struct oxo_driver {
             eng->verify(&x, 1, g);
             eng->commit(1);
             note(p, &x, 1);
+            remember(p, 1);
             out[0] = g[0];
             return 1;
         }
@@ -586,12 +597,39 @@ struct oxo_driver {
         while (a < k && drafts[a] == g[a]) a++;
         eng->commit(a + 1);
         note(p, vt, a + 1);
+        remember(p, a + 1);
         steps++;
         drafted += k;
         accepted += a;
         tokens_out += a + 1;
         for (int i = 0; i <= a; i++) out[i] = g[i];
         return a + 1;
+    }
+
+    // MtpDriver::step_plain (mtp.rs:504-515)
+    uint32_t step_plain(uint32_t x) {
+        const int64_t p = eng->pos;
+        uint32_t g[8];
+        eng->verify(&x, 1, g);
+        eng->commit(1);
+        note(p, &x, 1);
+        remember(p, 1);
+        flush(mtp_lanes() - 1);
+        return g[0];
+    }
+
+    // MtpDriver::rewind (mtp.rs:596-608)
+    int rewind(int m) {
+        if (last_n == 0 || m < 1 || m > last_n) return -1;
+        if (m == last_n) return 0;
+        eng->commit(m);
+        const int64_t E = eng->d.n_embd;
+        const size_t keep = std::min<size_t>((size_t)std::max<int64_t>(0, last_p0 + m - q), cu_tok.size());
+        cu_tok.resize(keep);
+        cu_h.resize(keep * E);
+        hl.assign(last_h.begin() + (m - 1) * E, last_h.begin() + m * E);
+        last_n = m;
+        return 0;
     }
 };
 
@@ -662,6 +700,8 @@ int oxo_driver_step(oxo_driver *d, uint32_t x, uint32_t *out, int64_t override_d
 void oxo_driver_stats(const oxo_driver *d, int64_t *st) {
     st[0] = d->steps; st[1] = d->drafted; st[2] = d->accepted; st[3] = d->tokens_out;
 }
+uint32_t oxo_driver_step_plain(oxo_driver *dr, uint32_t x) { return dr->step_plain(x); }
+int oxo_driver_rewind(oxo_driver *dr, int m) { return dr->rewind(m); }
 
 }  // extern "C"
 

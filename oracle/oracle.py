@@ -126,6 +126,8 @@ def lib():
             "oxo_driver_free": (None, [C.c_void_p]),
             "oxo_driver_prefill": (C.c_uint32, [C.c_void_p, u32p, C.c_int]),
             "oxo_driver_step": (C.c_int, [C.c_void_p, C.c_uint32, u32p, C.c_int64]),
+            "oxo_driver_step_plain": (C.c_uint32, [C.c_void_p, C.c_uint32]),
+            "oxo_driver_rewind": (C.c_int, [C.c_void_p, C.c_int]),
             "oxo_driver_stats": (None, [C.c_void_p, P(C.c_int64)]),
         }
         for name, (res, args) in sig.items():
@@ -265,6 +267,12 @@ class Driver:
         out = np.zeros(8, np.uint32)
         n = lib().oxo_driver_step(self.h, x, ptr(out, C.c_uint32), override_d1)
         return [int(v) for v in out[:n]]
+
+    def step_plain(self, x):
+        return int(lib().oxo_driver_step_plain(self.h, x))
+
+    def rewind(self, m):
+        return int(lib().oxo_driver_rewind(self.h, m))
 
     def stats(self):
         s = np.zeros(4, np.int64)

@@ -43,6 +43,8 @@ oxo_driver *oxo_driver_new(oxo_engine *e, int depth);                          /
 void oxo_driver_free(oxo_driver *d);
 uint32_t oxo_driver_prefill(oxo_driver *d, const uint32_t *toks, int n);      // mtp.rs:450-463
 int oxo_driver_step(oxo_driver *d, uint32_t x, uint32_t *out, int64_t override_d1); // mtp.rs:522-592
+uint32_t oxo_driver_step_plain(oxo_driver *d, uint32_t x);                           // mtp.rs:504-515
+int oxo_driver_rewind(oxo_driver *d, int m);                                        // mtp.rs:596-608
 void oxo_driver_stats(const oxo_driver *d, int64_t *st);
 #ifdef __cplusplus
 }

@@ -121,6 +121,13 @@ void MtpDriverHost::note(Engine &e, int p0, const uint32_t *toks, int n) {
     hl.assign(h.begin() + (size_t)(n - 1) * E, h.begin() + (size_t)n * E);
 }
 
+void MtpDriverHost::remember(Engine &e, int p0, int n) {
+    last_p0 = p0;
+    last_n = n;
+    last_h.resize((size_t)n * E);
+    for (int i = 0; i < n; i++) e.hidden_host(i, last_h.data() + (size_t)i * E);
+}
+
 int MtpDriverHost::flush(Engine &e, size_t keep) {
     while (cu_tok.size() > keep) {
         const int n = (int)std::min<size_t>(OXE_NL, cu_tok.size());
@@ -159,6 +166,7 @@ int MtpDriverHost::step(Engine &e, uint32_t x, uint32_t *out, int *n_out, int64_
         uint32_t g;
         if ((rc = e.verify(&x, 1, &g)) || (rc = e.commit(1))) return rc;
         note(e, p, &x, 1);
+        remember(e, p, 1);
         out[0] = g;
         *n_out = 1;
         return 0;
@@ -174,6 +182,7 @@ int MtpDriverHost::step(Engine &e, uint32_t x, uint32_t *out, int *n_out, int64_
     const int a = d1 == g[0] ? 1 : 0;
     if ((rc = e.commit(a + 1))) return rc;
     note(e, p, vt, a + 1);
+    remember(e, p, a + 1);
     steps++;
     accepted += a;
     for (int i = 0; i <= a; i++) out[i] = g[i];
@@ -181,8 +190,36 @@ int MtpDriverHost::step(Engine &e, uint32_t x, uint32_t *out, int *n_out, int64_
     return 0;
 }
 
+// MtpDriver::step_plain (mtp.rs:504-515): one target step that keeps the MTP catch-up in sync
+int MtpDriverHost::step_plain(Engine &e, uint32_t x, uint32_t *out) {
+    const int p = e.pos;
+    uint32_t g;
+    int rc;
+    if ((rc = e.verify(&x, 1, &g)) || (rc = e.commit(1))) return rc;
+    note(e, p, &x, 1);
+    remember(e, p, 1);
+    if ((rc = flush(e, 7))) return rc;
+    *out = g;
+    return 0;
+}
+
+// MtpDriver::rewind (mtp.rs:596-608): keep the first m committed tokens of the last step
+int MtpDriverHost::rewind(Engine &e, int m) {
+    if (last_n == 0 || m < 1 || m > last_n) return -1;
+    if (m == last_n) return 0;
+    int rc = e.commit(m);
+    if (rc) return rc;
+    const size_t keep = std::min<size_t>((size_t)std::max(0, last_p0 + m - q), cu_tok.size());
+    cu_tok.resize(keep);
+    cu_h.resize(keep * E);
+    hl.assign(last_h.begin() + (size_t)(m - 1) * E, last_h.begin() + (size_t)m * E);
+    last_n = m;
+    return 0;
+}
+
 // device-driven: hand the host driver state to the device, run K graph steps, read it back
 int MtpDriverHost::dev_begin(Engine &e, uint32_t x) {
+    last_n = 0;  // rewind applies to host-driven steps only
     int rc = flush(e, 0);  // at most the pair the next step seeds stays pending: none here
     if (rc) return rc;
     MtpState s{};
@@ -260,21 +297,50 @@ extern "C" {
 
 // Eagerly enqueue k device-driven MTP steps with HIP events around every launch of kernel `kind`
 // (engine stream); *avg_us = mean launch duration, *n = launches timed. For the bench's roofline.
-int oxe_mtp_device_probe(oxe_engine *e, int k, int kind, float *avg_us, int *n) {
+int oxe_mtp_device_probe(oxe_engine *e, int k, int kind, int use_graph, float *avg_us, int *n) {
     Engine *g = (Engine *)e;
-    g->probe_kind = kind;
-    g->probe_used = 0;
-    const int rc = g->mtp_steps_async(k, false);
-    g->probe_kind = -1;
-    if (rc) return rc;
-    if (hipStreamSynchronize(g->st) != hipSuccess) return -2;
+    if (k < 1 || kind < 0 || !avg_us || !n) return -1;
     double tot = 0.0;
     int cnt = 0;
-    for (size_t i = 0; i + 1 < g->probe_used; i += 2) {
-        float ms = 0.0f;
-        if (hipEventElapsedTime(&ms, g->probe_ev[i], g->probe_ev[i + 1]) != hipSuccess) return -2;
-        tot += ms;
-        cnt++;
+    auto collect = [&]() -> int {
+        if (hipStreamSynchronize(g->st) != hipSuccess) return -2;
+        for (size_t i = 0; i + 1 < g->probe_used; i += 2) {
+            float ms = 0.0f;
+            if (hipEventElapsedTime(&ms, g->probe_ev[i], g->probe_ev[i + 1]) != hipSuccess) return -2;
+            tot += ms;
+            cnt++;
+        }
+        return 0;
+    };
+    g->probe_kind = kind;
+    g->probe_used = 0;
+    if (!use_graph) {
+        // eager launches with events around each launch of the kind
+        int rc = g->mtp_steps_async(k, false);
+        g->probe_kind = -1;
+        if (rc) return rc;
+        if ((rc = collect())) return rc;
+    } else {
+        // the step graph with event-record nodes around each launch of the kind: the events time
+        // the kernels as they run inside the graph
+        hipGraph_t gr;
+        hipGraphExec_t ex = nullptr;
+        int rc = hipStreamBeginCapture(g->st, hipStreamCaptureModeThreadLocal) == hipSuccess ? 0 : -2;
+        if (!rc) {
+            g->enqueue_mtp_device_step();
+            rc = hipStreamEndCapture(g->st, &gr) == hipSuccess ? 0 : -2;
+            if (!rc) {
+                rc = hipGraphInstantiate(&ex, gr, nullptr, nullptr, 0) == hipSuccess ? 0 : -2;
+                (void)hipGraphDestroy(gr);
+            }
+        }
+        g->probe_kind = -1;
+        for (int i = 0; !rc && i < k; i++) {
+            rc = hipGraphLaunch(ex, g->st) == hipSuccess ? 0 : -2;
+            if (!rc) rc = collect();
+        }
+        if (ex) (void)hipGraphExecDestroy(ex);
+        if (rc) return rc;
     }
     *avg_us = cnt ? (float)(tot * 1000.0 / cnt) : 0.0f;
     *n = cnt;
@@ -291,6 +357,17 @@ int oxe_mtp_step(oxe_engine *e, uint32_t x, uint32_t *out, int *n_out, int64_t o
     Engine *g = (Engine *)e;
     if (!g->toks_ok(&x, 1) || override_d1 >= g->d.n_vocab || !out || !n_out) return -1;
     return g->drv.step(*g, x, out, n_out, override_d1);
+}
+
+int oxe_mtp_step_plain(oxe_engine *e, uint32_t x, uint32_t *out) {
+    Engine *g = (Engine *)e;
+    if (!g->toks_ok(&x, 1) || !out) return -1;
+    return g->drv.step_plain(*g, x, out);
+}
+
+int oxe_mtp_rewind(oxe_engine *e, int m) {
+    Engine *g = (Engine *)e;
+    return g->drv.rewind(*g, m);
 }
 
 int oxe_mtp_set_force(oxe_engine *e, const int32_t *force_d1, int n) {

@@ -33,10 +33,15 @@ struct MtpDriverHost {
     std::vector<float> cu_h;
     std::vector<float> hl = std::vector<float>(shp::E, 0.0f);  // target h_nextn of position pos-1
     int64_t steps = 0, accepted = 0;
+    int last_p0 = 0, last_n = 0;   // the last host-driven step's committed span (MtpDriver.last)
+    std::vector<float> last_h;     // h_nextn of each committed lane of that step (MtpDriver.last_h)
     void note(Engine &e, int p0, const uint32_t *toks, int n);
+    void remember(Engine &e, int p0, int n);
     int flush(Engine &e, size_t keep);
     int prefill(Engine &e, const uint32_t *toks, int n, uint32_t *next);
     int step(Engine &e, uint32_t x, uint32_t *out, int *n_out, int64_t override_d1);
+    int step_plain(Engine &e, uint32_t x, uint32_t *out);
+    int rewind(Engine &e, int m);
     int dev_begin(Engine &e, uint32_t x);
     int dev_end(Engine &e, uint32_t *out_tok, int cap, int *n_out, uint32_t *next_x);
 };

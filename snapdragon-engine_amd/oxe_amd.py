@@ -122,13 +122,15 @@ def _engine_sigs(L):
         "oxe_engine_device_bytes": (i64, [vp]),
         "oxe_mtp_prefill": (i32, [vp, u32p, i32, u32p]),
         "oxe_mtp_step": (i32, [vp, C.c_uint32, u32p, C.POINTER(C.c_int), i64]),
+        "oxe_mtp_step_plain": (i32, [vp, C.c_uint32, u32p]),
+        "oxe_mtp_rewind": (i32, [vp, i32]),
         "oxe_mtp_device_begin": (i32, [vp, C.c_uint32, i32]),
         "oxe_mtp_device_steps": (i32, [vp, i32, i32]),
         "oxe_mtp_device_end": (i32, [vp, u32p, i32, C.POINTER(C.c_int), u32p]),
         "oxe_mtp_set_force": (i32, [vp, C.POINTER(C.c_int32), i32]),
         "oxe_mtp_stats": (i32, [vp, C.POINTER(C.c_int64)]),
         "oxe_engine_sync": (i32, [vp]),
-        "oxe_mtp_device_probe": (i32, [vp, i32, i32, C.POINTER(C.c_float), C.POINTER(C.c_int)]),
+        "oxe_mtp_device_probe": (i32, [vp, i32, i32, i32, C.POINTER(C.c_float), C.POINTER(C.c_int)]),
         "oxe_engine_stream": (vp, [vp]),
     }
     for name, (res, args) in sig.items():
@@ -250,6 +252,14 @@ class Engine:
         check(lib().oxe_mtp_step(self.h, x, _np_ptr(out, C.c_uint32), C.byref(n), override_d1), "mtp_step")
         return [int(v) for v in out[: n.value]]
 
+    def mtp_step_plain(self, x):
+        out = (C.c_uint32 * 1)()
+        check(lib().oxe_mtp_step_plain(self.h, x, out), "mtp_step_plain")
+        return int(out[0])
+
+    def mtp_rewind(self, m):
+        check(lib().oxe_mtp_rewind(self.h, m), "mtp_rewind")
+
     def mtp_set_force(self, force):
         import numpy as np
         f = np.ascontiguousarray(force, np.int32)
@@ -276,10 +286,10 @@ class Engine:
         lib().oxe_mtp_stats(self.h, s.ctypes.data_as(C.POINTER(C.c_int64)))
         return dict(steps=int(s[0]), accepted=int(s[1]))
 
-    def mtp_device_probe(self, k, kind):
+    def mtp_device_probe(self, k, kind, use_graph=True):
         avg = C.c_float(0)
         n = C.c_int(0)
-        check(lib().oxe_mtp_device_probe(self.h, k, kind, C.byref(avg), C.byref(n)), "mtp_device_probe")
+        check(lib().oxe_mtp_device_probe(self.h, k, kind, int(use_graph), C.byref(avg), C.byref(n)), "mtp_device_probe")
         return float(avg.value), int(n.value)
 
     def sync(self):

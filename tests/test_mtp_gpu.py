@@ -98,3 +98,30 @@ def test_device_driver_natural_drafts_equal_plain(setup):
         g.close()
     assert outs[0] == outs[1]
     assert outs[0] == plain[1:1 + len(outs[0])]
+
+
+def test_rewind_and_step_plain_match_oracle(setup):
+    """Host-driven rewind (mtp.rs:596-608) and step_plain (504-515) against the oracle's driver,
+    tokens and h_nextn bit for bit."""
+    import oxe_amd as A
+    d, prompt, pattern, plain, forces = setup
+    g = A.Engine(d, seed=SEED, n_ctx=N_CTX)
+    o = O.Engine(d, seed=SEED, n_ctx=N_CTX)
+    od = O.Driver(o)
+    x = g.mtp_prefill(prompt)
+    assert od.prefill(prompt) == x
+    k = 0                                   # x == plain[k]: the greedy sequence is followed throughout
+    for acc in (1, 1, 0, 1):
+        f = plain[k + 1] if acc else (plain[k + 1] + 7) % d.n_vocab
+        rg, ro = g.mtp_step(x, f), od.step(x, f)
+        assert rg == ro == plain[k + 1: k + 2 + acc]
+        if acc:
+            g.mtp_rewind(1)                 # keep x only: the next token is plain[k + 1] again
+            assert od.rewind(1) == 0
+        x, k = plain[k + 1], k + 1
+        xg, xo = g.mtp_step_plain(x), od.step_plain(x)
+        assert xg == xo == plain[k + 1]
+        x, k = xg, k + 1
+        assert np.array_equal(g.hidden(0).view(np.uint32), o.hidden(0).view(np.uint32))
+    g.close()
+    o.close()

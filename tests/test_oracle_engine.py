@@ -86,3 +86,28 @@ def test_mtp_greedy_equals_plain_with_forced_drafts(desc):
     assert got[:n] == ref[:n]
     st = drv.stats()
     assert st["accepted"] == sum(pattern[j % len(pattern)] for j in range(i))
+
+
+def test_rewind_and_step_plain_equal_plain_greedy(desc):
+    """MtpDriver::rewind (mtp.rs:596-608): after an accepted step, keeping only x and continuing
+    from the first greedy token is plain greedy again; step_plain (mtp.rs:504-515) interleaves."""
+    prompt = (O.bench_prompt(5) % desc.n_vocab).tolist()
+    ref, _ = plain_greedy(desc, prompt, 12)
+    e = O.Engine(desc, seed=SEED, n_ctx=256)
+    drv = O.Driver(e)
+    x = drv.prefill(prompt)
+    got = [x]
+    out = drv.step(x, override_d1=ref[1])        # accepted: commits x and d1
+    assert out == ref[1:3]
+    assert drv.rewind(3) == -1                   # more than the step committed
+    assert drv.rewind(1) == 0                    # keep x only: the next token is ref[1] again
+    x = out[0]
+    got.append(x)
+    x = drv.step_plain(x)
+    got.append(x)
+    out = drv.step(x, override_d1=(ref[4] + 1) % desc.n_vocab)   # rejected draft
+    got += out
+    x = out[-1]
+    out = drv.step(x, override_d1=ref[5])
+    got += out
+    assert got == ref[: len(got)]
