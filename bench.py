@@ -43,18 +43,27 @@ KV_POS = 2 * 2 * 256 * 2                        # K + V bytes of one position (2
 SMALL = 8 * E * 4                               # norms and other f32 vectors per layer (upper bound)
 
 
-def step_bytes(pos, units_per_step, accepted_frac):
-    """Unique HBM bytes one MTP-1 step must move (weights once per run, state read once and
-    written per lane, KV of positions <= pos once per kv head), excluding cache re-reads."""
-    n_dn, n_att = 30, 10
-    verify = (n_dn * (DN_PROJ + MIX_OUT) + n_att * (ATT_PROJ + MIX_OUT)
-              + 40 * (ROUTER + SHARED + SMALL) + LM_HEAD + 2 * E * Q8
-              + n_dn * 3 * DN_STATE                       # read once, write 2 slots
-              + n_att * ((pos + 2) * KV_POS + 2 * KV_POS))
-    draft = EH_PROJ + ATT_PROJ + MIX_OUT + ROUTER + SHARED + SMALL + LM_HEAD + (pos + 1) * KV_POS + KV_POS
+def verify_bytes(pos, u_avg, n_dn=30, n_att=10):
+    """Unique HBM bytes of one 2-lane verify run (weights once, union experts at the measured mean
+    union size u_avg per MoE layer, DN state read once and written per lane, KV of positions <= pos
+    once per kv head), excluding cache re-reads."""
+    nl = n_dn + n_att
+    return (n_dn * (DN_PROJ + MIX_OUT) + n_att * (ATT_PROJ + MIX_OUT)
+            + nl * (ROUTER + SHARED + SMALL + u_avg * (EXPERT_GU + EXPERT_DOWN))
+            + LM_HEAD + 2 * E * Q8
+            + n_dn * 3 * DN_STATE
+            + n_att * ((pos + 2) * KV_POS + 2 * KV_POS))
+
+
+def draft_bytes(pos, u_avg):
+    return (EH_PROJ + ATT_PROJ + MIX_OUT + ROUTER + SHARED + SMALL + u_avg * (EXPERT_GU + EXPERT_DOWN) + LM_HEAD
+            + (pos + 1) * KV_POS + KV_POS)
+
+
+def step_bytes(pos, u_avg, accepted_frac):
+    """Unique HBM bytes one MTP-1 step must move: verify + draft + (accepted steps) MTP seeding."""
     seed = accepted_frac * (EH_PROJ + 1024 * E * Q8 + KV_POS)
-    experts = units_per_step * (EXPERT_GU + EXPERT_DOWN)
-    return verify + draft + seed + experts
+    return verify_bytes(pos, u_avg) + draft_bytes(pos, u_avg) + seed
 
 
 def cpu_baseline(seconds, prompt_len=8):
@@ -114,7 +123,10 @@ def main():
     ap.add_argument("--prompt", type=int, default=512)
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--probe-kind", type=int, default=1, help="kernel kind timed for the roofline (1 = experts gate/up)")
+    ap.add_argument("--probe-kind", type=int, default=-1,
+                    help="kernel kind timed for the roofline (default: 10 = the fused verify run, or 1 = experts "
+                         "gate/up with --per-phase)")
+    ap.add_argument("--per-phase", action="store_true", help="one launch per phase instead of the fused run kernel")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain device copy of known size (the PMC byte-counter calibration)")
     args = ap.parse_args()
@@ -134,6 +146,10 @@ def main():
     n_ctx = args.prompt + 2 * (args.steps + args.warmup) + 256 + 64
     t_setup = time.time()
     eng = A.Engine(d, seed=0, n_ctx=n_ctx)
+    if args.per_phase:
+        eng.set_fused(False)
+    fused = eng.fused
+    probe_kind = args.probe_kind if args.probe_kind >= 0 else (10 if fused else 1)
     prompt = O.bench_prompt(args.prompt)
     x = eng.mtp_prefill(prompt)
     eng.sync()
@@ -168,22 +184,32 @@ def main():
     tok_s = n_tok / (ms / 1e3)
     acc = (n_tok - args.steps) / max(args.steps, 1)
     mean_pos = (pos_start + pos_end) / 2
-    bytes_step = step_bytes(mean_pos, units / max(args.steps, 1), acc)
+    u_avg = units / max(calls, 1)
+    bytes_step = step_bytes(mean_pos, u_avg, acc)
     step_gbs = bytes_step / (ms / args.steps / 1e3) / 1e9
-    # roofline of the dominant kernel: live HIP-event timing of each launch in eager steps
+    # roofline of the dominant kernel: HIP events around each of its launches (eager steps; in the
+    # fused mode the verify run is one launch of ~a millisecond, so launch overhead is negligible)
     eng.mtp_device_begin(x, cap)
     uni1, calls1 = eng.counter(66), eng.counter(67)
+    pos_p0 = eng.pos
     probe_steps = 8
-    avg_us, n_launch = eng.mtp_device_probe(probe_steps, args.probe_kind, use_graph=True)
+    avg_us, n_launch = eng.mtp_device_probe(probe_steps, probe_kind)
     eng.mtp_device_end(cap)
-    u_per_launch = (eng.counter(66) - uni1) / max(eng.counter(67) - calls1, 1)
-    k_bytes = u_per_launch * EXPERT_GU
+    u_probe = (eng.counter(66) - uni1) / max(eng.counter(67) - calls1, 1)
+    if probe_kind == 10:
+        k_name = "fused_kernel, verify run (2 lanes x 40 layers + LM head, one launch)"
+        k_bytes = verify_bytes((pos_p0 + eng.pos) / 2, u_probe)
+        traffic_key = "fused_verify"
+    else:
+        k_name = "experts_kernel (routed gate/up GEMV + swiglu)"
+        k_bytes = u_probe * EXPERT_GU
+        traffic_key = "experts_kernel"
     k_gbs = k_bytes / (avg_us * 1e-6) / 1e9 if avg_us > 0 else 0.0
-    tr = load_traffic("experts_kernel")
+    tr = load_traffic(traffic_key)
     traffic = None
     if tr is not None:
-        # measured bytes per expert unit (a 16-row gate/up tile pair set of one union expert)
-        traffic = int(tr["hbm_bytes_per_unit"] * u_per_launch)
+        # measured HBM bytes per launch, scaled to this run's bytes (union size and context differ slightly)
+        traffic = int(tr["hbm_bytes_per_launch"] * k_bytes / tr["algorithmic_bytes_per_launch"])
     result = {
         "metric": "MTP-1 decode tok/s (35B-A3B shape, int8) + HBM GB/s as % of ~8 TB/s peak",
         "value": round(tok_s, 3),
@@ -206,9 +232,11 @@ def main():
         "hbm_GBs_step": round(step_gbs, 1),
         "hbm_frac_step": round(step_gbs / PEAK_HBM_GBS, 4),
         "expert_units_per_step": round(units / max(args.steps, 1), 3),
+        "union_experts_per_moe_layer": round(u_avg, 3),
+        "run_mode": "fused (one persistent launch per run)" if fused else "one launch per phase",
         "roofline": {"bound": "hbm", "achieved": round(k_gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(k_gbs / PEAK_HBM_GBS, 4), "traffic": traffic,
-                     "kernel": "experts_kernel (routed gate/up GEMV + swiglu)", "avg_us": round(avg_us, 3),
+                     "kernel": k_name, "avg_us": round(avg_us, 3),
                      "launches_timed": n_launch, "bytes_per_launch": int(k_bytes)},
         "setup_s": round(setup_s, 1),
     }

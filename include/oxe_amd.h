@@ -85,6 +85,17 @@ OXE_API int oxe_engine_counter(oxe_engine *e, int which, uint32_t *out);
 OXE_API int oxe_engine_state_copy(oxe_engine *e, int which, int dir, int64_t offset, void *host, int64_t nbytes);
 OXE_API int oxe_engine_set_pos(oxe_engine *e, int pos);
 OXE_API int64_t oxe_engine_device_bytes(const oxe_engine *e);
+/* Run mode (no counterpart in the reference, whose runs are thread-team phases): 1 = every run
+ * as one persistent launch of the fused run kernel (the default where the device has exactly 256
+ * CUs), 0 = one launch per phase. Both compute the same bits. -1 when 1 is not available. */
+OXE_API int oxe_engine_set_fused(oxe_engine *e, int on);
+OXE_API int oxe_engine_fused(const oxe_engine *e);
+/* Phase trace of the fused run kernel (diagnostic, no counterpart in the reference, whose Trace at
+ * crates/model/src/engine.rs:324-340 records tensors, not time): when on, every run records per workgroup and
+ * phase (phase id, start, barrier released, end) in device wall-clock ticks (100 MHz);
+ * read_trace copies the last run's records ([grid][512][4] u64) and returns their count. */
+OXE_API int oxe_engine_set_trace(oxe_engine *e, int on);
+OXE_API int64_t oxe_engine_read_trace(oxe_engine *e, unsigned long long *host, int64_t cap);
 
 /* ---- MTP depth-1 speculative decoding (crates/model/src/mtp.rs MtpDriver, depth 1) --------- */
 
@@ -110,11 +121,11 @@ OXE_API int oxe_mtp_device_steps(oxe_engine *e, int k, int use_graph);
 OXE_API int oxe_mtp_device_end(oxe_engine *e, uint32_t *out_tok, int cap, int *n_out, uint32_t *next_x);
 /* Forced drafts for the device-driven steps (test hook): force_d1[i] >= 0 replaces step i's draft. */
 OXE_API int oxe_mtp_set_force(oxe_engine *e, const int32_t *force_d1, int n);
-/* k device-driven steps with HIP events around each launch of one kernel kind (0 LM head,
+/* k eager device-driven steps with HIP events around each launch of one kernel kind (0 LM head,
  * 1 experts gate/up, 2 down, 3 projections, 4 mixer out, 5 delta-net, 6 router, 7 scores, 8 pv,
- * 9 MTP entry): mean kernel duration in microseconds (roofline measurement). use_graph: the events
- * are nodes of the captured step graph (the timed configuration); else eager launches. */
-OXE_API int oxe_mtp_device_probe(oxe_engine *e, int k, int kind, int use_graph, float *avg_us, int *n);
+ * 9 MTP entry; in the fused run mode 10 the verify run, 11 the draft run, each one launch): mean
+ * kernel duration in microseconds (roofline measurement). */
+OXE_API int oxe_mtp_device_probe(oxe_engine *e, int k, int kind, float *avg_us, int *n);
 /* steps, accepted drafts */
 OXE_API int oxe_mtp_stats(const oxe_engine *e, int64_t *st);
 OXE_API int oxe_engine_sync(oxe_engine *e);

@@ -120,3 +120,26 @@ int oxe_engine_set_pos(oxe_engine *e, int pos) {
 int64_t oxe_engine_device_bytes(const oxe_engine *e) { return (int64_t)((const Engine *)e)->bytes; }
 
 }  // extern "C"
+
+extern "C" int oxe_engine_set_fused(oxe_engine *e, int on) {
+    Engine *g = (Engine *)e;
+    if (g->set_fused(on != 0)) {
+        oxe::set_err("the fused run kernel is not available on this device");
+        return -1;
+    }
+    return 0;
+}
+
+extern "C" int oxe_engine_fused(const oxe_engine *e) { return ((const Engine *)e)->fused ? 1 : 0; }
+
+extern "C" int oxe_engine_set_trace(oxe_engine *e, int on) { return ((Engine *)e)->set_trace(on != 0); }
+
+extern "C" int64_t oxe_engine_read_trace(oxe_engine *e, unsigned long long *host, int64_t cap) {
+    Engine *g = (Engine *)e;
+    if (!g->fz_trace) return -1;
+    const int64_t n = (int64_t)g->fz_grid * oxe::FZ_TRACE_EV * 4;
+    if (cap < n) return -1;
+    if (hipMemcpyAsync(host, g->fz_trace, (size_t)n * 8, hipMemcpyDeviceToHost, g->st) != hipSuccess) return -2;
+    if (hipStreamSynchronize(g->st) != hipSuccess) return -2;
+    return n;
+}

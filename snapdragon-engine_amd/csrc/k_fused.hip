@@ -1,0 +1,1417 @@
+// The fused run kernel (see oxe_fused.h): every phase of one engine run in one persistent launch.
+//
+// Arithmetic is the per-phase kernels' (k_layer.hip, k_attn.hip, k_moe.hip) with the reference's
+// float order; only the distribution of work over threads differs:
+//   * 512-thread workgroups, one per CU; in the norm prologues lane l of the run is handled by
+//     threads [256 l, 256 l + 256) (8 elements each), and the exact double sums use the same
+//     bracket test, so their result does not depend on the reduction order;
+//   * Q8_0 GEMV slices: a workgroup owns a contiguous range of rows (or a fixed row list), loads all
+//     of its 16-byte code chunks and scale rows into registers before waiting at the barrier that
+//     releases the activations, then forms the exact int32 block dots and runs one serial fp32
+//     FMA chain per (row, lane) in block order, as the reference's NEON GEMV;
+//   * phase boundaries are grid barriers (per-XCD arrival counters, then one global counter; the
+//     last arrival publishes the round). Data a later phase of the same launch reads from another
+//     workgroup is stored and loaded with device-scope accesses.
+// Every spin is bounded: a stuck barrier sets the error word and every workgroup leaves.
+#include "oxe_fused.h"
+#include "oxe_gemv.h"
+#include "oxe_prologue.h"
+#include "oxe_route.h"
+#include "oxe_shape.h"
+
+namespace oxe {
+
+using namespace shp;
+
+namespace fz {
+
+constexpr int FT = 512;                       // threads per workgroup
+constexpr uint32_t SPIN_MAX = 400000;         // ~0.4 s at one device-scope load per iteration
+
+// ---- device-scope accesses for data exchanged inside the launch -----------------------------
+OXE_DEV void cst(float *p, float v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+OXE_DEV float cld(const float *p) { return __hip_atomic_load((float *)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+OXE_DEV void cst32(void *p, uint32_t v) { __hip_atomic_store((uint32_t *)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+OXE_DEV uint32_t cld32(const void *p) { return __hip_atomic_load((uint32_t *)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+OXE_DEV void cst16(uint16_t *p, uint16_t v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+OXE_DEV uint16_t cld16(const uint16_t *p) { return __hip_atomic_load((uint16_t *)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+OXE_DEV void cst64(void *p, unsigned long long v) {
+    __hip_atomic_store((unsigned long long *)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+OXE_DEV unsigned long long cld64(const void *p) {
+    return __hip_atomic_load((unsigned long long *)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+OXE_DEV uint4 cld128(const void *p) {
+    const unsigned long long a = cld64(p), b = cld64((const char *)p + 8);
+    return make_uint4((uint32_t)a, (uint32_t)(a >> 32), (uint32_t)b, (uint32_t)(b >> 32));
+}
+OXE_DEV void cst128(void *p, uint4 v) {
+    cst64(p, (unsigned long long)v.x | ((unsigned long long)v.y << 32));
+    cst64((char *)p + 8, (unsigned long long)v.z | ((unsigned long long)v.w << 32));
+}
+
+// ---- grid barrier -----------------------------------------------------------------------------
+struct Bar {
+    uint32_t *w;
+    uint32_t &round;   // thread 0's copy lives in LDS (only thread 0 reads or writes it)
+};
+
+// Arrival: every thread's stores of the phase are complete before the workgroup is counted.
+OXE_DEV void arrive(Bar b) {
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        b.round++;
+        const uint32_t x = blockIdx.x & (FZ_XCD - 1);
+        const uint32_t per = gridDim.x / FZ_XCD;
+        const uint32_t old = __hip_atomic_fetch_add(&b.w[32 * x], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (old == b.round * per - 1) {
+            const uint32_t og = __hip_atomic_fetch_add(&b.w[FZ_W_GLOB], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (og == b.round * FZ_XCD - 1) cst32(&b.w[FZ_W_FLAG], b.round);
+        }
+    }
+}
+
+// Wait until every workgroup arrived at the current round. false: the run was aborted.
+OXE_DEV bool wait(Bar b, int *s_ok) {
+    if (threadIdx.x == 0) {
+        int ok = 1;
+        uint32_t spins = 0;
+        while ((int32_t)(cld32(&b.w[FZ_W_FLAG]) - b.round) < 0) {
+            if (++spins > SPIN_MAX) {
+                cst32(&b.w[FZ_W_ERR], 1u);
+                ok = 0;
+                break;
+            }
+            if ((spins & 31) == 0 && cld32(&b.w[FZ_W_ERR])) {
+                ok = 0;
+                break;
+            }
+            __builtin_amdgcn_s_sleep(2);
+        }
+        *s_ok = ok;
+    }
+    __syncthreads();
+    return *s_ok != 0;
+}
+
+// ---- GEMV slices ------------------------------------------------------------------------------
+template <int K>
+struct KG {
+    static constexpr int NB = K / 32;          // blocks per row
+    static constexpr int KCH = K / 16;         // 16-byte code chunks per row
+    static constexpr int RPP = FT / KCH;       // rows per pass of the workgroup
+    static constexpr int SPR = K / 256;        // 16-byte scale chunks per row
+    static constexpr int WDS = NB / 2 + 1;     // LDS scale row stride in words (odd)
+};
+
+template <int K, int MAXP>
+struct WSlice {
+    uint4 w[MAXP];
+    uint4 s;
+};
+
+template <int K, int MAXR, int NL>
+struct GSm {
+    int32_t isum[NL][MAXR][KG<K>::NB + 1];
+    uint32_t wd[MAXR * KG<K>::WDS];
+    float out[NL][MAXR];
+};
+
+// codes of rows rowof(0..nr) and their scales into registers (plain loads: weights are read-only)
+template <int K, int MAXP, class RowOf>
+OXE_DEV void wload(WSlice<K, MAXP> &s, const int8_t *__restrict__ wq, const uint16_t *__restrict__ wd, int nr,
+                   RowOf rowof) {
+    using G = KG<K>;
+    const int t = threadIdx.x, c = t % G::KCH, rs = t / G::KCH;
+#pragma unroll
+    for (int p = 0; p < MAXP; p++) {
+        const int rl = p * G::RPP + rs;
+        s.w[p] = rl < nr ? *(const uint4 *)(wq + rowof(rl) * K + c * 16) : make_uint4(0, 0, 0, 0);
+    }
+    const int sr = t / G::SPR, sk = t % G::SPR;
+    s.s = sr < nr ? *(const uint4 *)(wd + rowof(sr) * G::NB + sk * 8) : make_uint4(0, 0, 0, 0);
+}
+
+// g.out[l][r] = row r . lane l for the slice's nr rows (activation codes xq [NL][xq_ld] and scales
+// xd [NL][xd_ld] in LDS). Ends with a barrier.
+template <int K, int MAXP, int NL>
+OXE_DEV void wdot(const WSlice<K, MAXP> &s, int nr, const int8_t *xq, int xq_ld, const uint16_t *xd, int xd_ld,
+                  GSm<K, MAXP * KG<K>::RPP, NL> &g) {
+    using G = KG<K>;
+    const int t = threadIdx.x, c = t % G::KCH, rs = t / G::KCH;
+    {
+        const int sr = t / G::SPR, sk = t % G::SPR;
+        if (sr < nr) {
+            uint32_t *d = &g.wd[sr * G::WDS + sk * 4];
+            d[0] = s.s.x; d[1] = s.s.y; d[2] = s.s.z; d[3] = s.s.w;
+        }
+    }
+    uint4 xa[NL];
+#pragma unroll
+    for (int l = 0; l < NL; l++) xa[l] = *(const uint4 *)(xq + l * xq_ld + c * 16);
+#pragma unroll
+    for (int p = 0; p < MAXP; p++) {
+        const int rl = p * G::RPP + rs;
+#pragma unroll
+        for (int l = 0; l < NL; l++) {
+            int32_t v = dot16(s.w[p], xa[l], 0);
+            v += shfl_xor_i(v, 1);  // the other half of the 32-code block sits in the adjacent lane
+            if ((c & 1) == 0 && rl < nr) g.isum[l][rl][c >> 1] = v;
+        }
+    }
+    __syncthreads();
+    if (t < nr * NL) {
+        const int rl = t % nr, l = t / nr;
+        const uint16_t *sw = (const uint16_t *)&g.wd[rl * G::WDS];
+        float acc = 0.0f;
+#pragma unroll 8
+        for (int b = 0; b < G::NB; b++)
+            acc = __builtin_fmaf((float)g.isum[l][rl][b], h2f(xd[l * xd_ld + b]) * h2f(sw[b]), acc);
+        g.out[l][rl] = acc;
+    }
+    __syncthreads();
+}
+
+// ---- norm prologue (oxe_rms_norm_mul_f32, oxe_ops.cpp:32-42), lane l on threads [256 l, 256 l + 256)
+struct NormSm {
+    double red[2][4];
+    float bc[2];
+};
+
+// v: this thread's 8 elements; xs: the lane's whole vector in LDS (sequential replay). All threads call.
+OXE_DEV void norm8(float v[8], const float *xs, const float *w, float eps, NormSm &ns) {
+    const int t = threadIdx.x, h = (t >> 8) & 1, tt = t & 255, wv = (t >> 6) & 3;
+    double p = 0.0;
+#pragma unroll
+    for (int i = 0; i < 8; i++) p += (double)(v[i] * v[i]);
+    for (int m = 32; m >= 1; m >>= 1) p += shfl_xor_d(p, m);
+    if ((t & 63) == 0) ns.red[h][wv] = p;
+    __syncthreads();
+    const double P = ((ns.red[h][0] + ns.red[h][1]) + ns.red[h][2]) + ns.red[h][3];
+    float mean;
+    const bool ok = bracket_ok_mean(P, P, E, (double)E, &mean);
+    if (!ok && tt == 0) {
+        double s = 0.0;
+        for (int i = 0; i < E; i++) s += (double)(xs[i] * xs[i]);
+        ns.bc[h] = (float)(s / (double)E);
+    }
+    __syncthreads();
+    if (!ok) mean = ns.bc[h];
+    const float scale = 1.0f / sqrtf(mean + eps);
+    const float4 w0 = *(const float4 *)(w + 8 * tt), w1 = *(const float4 *)(w + 8 * tt + 4);
+    const float wv8[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+    for (int i = 0; i < 8; i++) v[i] = (v[i] * scale) * wv8[i];
+}
+
+OXE_DEV void put8(float *x, const float *v) {
+    *(float4 *)x = make_float4(v[0], v[1], v[2], v[3]);
+    *(float4 *)(x + 4) = make_float4(v[4], v[5], v[6], v[7]);
+}
+OXE_DEV void get8(const float *x, float v[8]) {
+    const float4 a = *(const float4 *)x, b = *(const float4 *)(x + 4);
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+}
+OXE_DEV void cget8(const float *x, float v[8]) {
+#pragma unroll
+    for (int i = 0; i < 8; i++) v[i] = cld(x + i);
+}
+// dequantize_row_q8_0 (quants_base.c:64-78) of elements [8 tt, 8 tt + 8) of token row tok
+OXE_DEV void embed8t(const Q8W &emb, uint32_t tok, int tt, float v[8]) {
+    const int8_t *q = emb.q + (int64_t)tok * E + 8 * tt;
+    const float d = h2f(emb.d[(int64_t)tok * (E / 32) + (8 * tt) / 32]);
+    const uint2 c = *(const uint2 *)q;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        v[i] = (float)(int8_t)(c.x >> (8 * i)) * d;
+        v[i + 4] = (float)(int8_t)(c.y >> (8 * i)) * d;
+    }
+}
+
+// The run's lanes normalised with w and quantised to xq/xd (LDS). Source per lane: the token
+// embedding (emb != null), a vector written in this launch (coherent), or one from an earlier launch.
+// xf: LDS staging of the raw vectors; xn (optional): the normalised f32 vectors.
+template <int NL>
+OXE_DEV void prologue(int nl, const RunCtl *ctl, const Q8W *emb, const float *src, int64_t src_ld, bool coherent,
+                      const float *w, float eps, float (*xf)[E], int8_t *xq, int xq_ld, uint16_t *xd, int xd_ld,
+                      NormSm &ns, float (*xn)[E]) {
+    const int t = threadIdx.x, l = t >> 8, tt = t & 255;
+    float v[8];
+    const bool act = l < NL && l < nl;
+    if (act) {
+        if (emb) embed8t(*emb, ctl->tok[l], tt, v);
+        else if (coherent) cget8(src + l * src_ld + 8 * tt, v);
+        else get8(src + l * src_ld + 8 * tt, v);
+    } else {
+#pragma unroll
+        for (int i = 0; i < 8; i++) v[i] = 0.0f;
+    }
+    if (l < NL) put8(&xf[l][8 * tt], v);
+    __syncthreads();
+    norm8(v, xf[l < NL ? l : 0], w, eps, ns);
+    if (l < NL) {
+        if (act) {
+            quant8(v, xq + l * xq_ld + 8 * tt, xd + l * xd_ld + (8 * tt) / 32);
+            if (xn) put8(&xn[l][8 * tt], v);
+        } else {
+            *(uint2 *)(xq + l * xq_ld + 8 * tt) = make_uint2(0, 0);
+            if ((tt & 3) == 0) xd[l * xd_ld + (8 * tt) / 32] = 0;
+            if (xn) put8(&xn[l][8 * tt], v);
+        }
+    }
+    __syncthreads();
+}
+
+// ---- shared memory of the phases -------------------------------------------------------------
+template <int NL>
+struct ProjSm {
+    alignas(16) float xf[NL][E];
+    alignas(16) int8_t xq[NL][E];
+    uint16_t xd[NL][E / 32];
+    NormSm ns;
+    GSm<E, 52, NL> g;
+};
+template <int NL>
+struct DnSm {
+    float q[NL][DS], k[NL][DS], v[NL][HV], o[NL][HV];
+    float g[NL], b[NL];
+};
+template <int NL>
+struct OutSm {
+    alignas(16) int8_t xq[NL][MIX_W];
+    uint16_t xd[NL][MIX_W / 32];
+    GSm<MIX_W, 8, NL> g;
+};
+template <int NL>
+struct RouterSm {
+    alignas(16) float xf[NL][E];
+    alignas(16) float xn[NL][E];
+    alignas(16) int8_t xq[NL][E];
+    uint16_t xd[NL][E / 32];
+    NormSm ns;
+    alignas(16) float w[E];
+    alignas(16) float sg[E];
+    GSm<E, 8, NL> g;
+};
+template <int NL>
+struct ExpSm {
+    float lg[NL][NEXP];
+    alignas(16) int8_t xq[NL][E];
+    uint16_t xd[NL][E / 32];
+    GSm<E, 64, NL> g;
+    alignas(16) float h[NL][32];
+    alignas(16) int8_t hq[NL][32];
+    uint16_t hd[NL];
+};
+constexpr int DW_UNITS = OXE_MAX_UNION + 1;   // union experts + the shared expert
+template <int NL>
+struct DownSm {
+    alignas(16) int8_t hq[NL][DW_UNITS][FF];
+    uint16_t hd[NL][DW_UNITS][FF / 32];
+    alignas(16) float hs[NL][FFSH];
+    uint32_t wd[DW_UNITS][8 * (FF / 64 + 1)];
+    int32_t isum[DW_UNITS][NL][8][FF / 32 + 1];
+    float dn[DW_UNITS][NL][8];
+};
+template <int NL>
+struct ScSm {
+    alignas(16) uint16_t q[NL * GQA][HD];
+    float tmp[NL * GQA][HD];
+    float ktmp[NL][HD];
+    alignas(16) uint16_t knew[NL][HD];
+};
+template <int NL>
+struct HeadSm {
+    alignas(16) float xf[NL][E];
+    alignas(16) float xn[NL][E];
+    alignas(16) int8_t xq[NL][E];
+    uint16_t xd[NL][E / 32];
+    NormSm ns;
+    GSm<E, 32, NL> g;
+    unsigned long long key[FT / 64][NL];
+};
+template <int NL>
+struct EntrySm {
+    alignas(16) float xf[NL][E];
+    alignas(16) int8_t xq[NL][2 * E];
+    uint16_t xd[NL][2 * E / 32];
+    NormSm ns;
+    GSm<2 * E, 8, NL> g;
+};
+template <int NL>
+union PhaseSm {
+    ProjSm<NL> proj;
+    DnSm<NL> dn;
+    OutSm<NL> out;
+    RouterSm<NL> router;
+    ExpSm<NL> exp;
+    DownSm<NL> down;
+    ScSm<NL> sc;
+    HeadSm<NL> head;
+    EntrySm<NL> entry;
+};
+
+// state that lives across phases of one layer (static LDS)
+template <int NL>
+struct Persist {
+    RouteOut ro;
+    int32_t uni[OXE_MAX_UNION];
+    int32_t nu;
+    int32_t slot[NL][KUSED];   // union slot of each lane's rank-j expert
+    int ok;
+    uint32_t round;
+    uint32_t tev;                    // trace: next event index of this workgroup
+    unsigned long long t_start, t_pass;
+};
+
+}  // namespace fz
+
+// LDS of the fused kernel: the phases' union (dynamic) and the state that lives across phases
+extern __shared__ __align__(16) unsigned char fz_dyn[];
+__shared__ fz::Persist<OXE_NL> fz_ps;
+
+namespace fz {
+
+template <int NL>
+struct Ctx {
+    const RunCtl *ctl;
+    const FusedArgs *a;
+    PhaseSm<NL> *sm;
+    Persist<NL> *ps;
+    unsigned char *dyn;
+    Bar bar;
+    int nl, G, b;
+};
+
+template <int NL>
+OXE_DEV Ctx<NL> make_ctx(const RunCtl *ctl, const FusedArgs *a) {
+    static_assert(NL == OXE_NL, "one lane count");
+    Ctx<NL> c{ctl, a, (PhaseSm<NL> *)fz_dyn, &fz_ps, fz_dyn, Bar{a->sync, fz_ps.round}, 0, 0, 0};
+    c.nl = ctl->nl < 1 ? 1 : (ctl->nl > NL ? NL : ctl->nl);
+    c.G = gridDim.x;
+    c.b = blockIdx.x;
+    return c;
+}
+
+#define FZ_PHASE __device__ __attribute__((noinline))
+
+// phase trace (optional): thread 0 records the device wall clock (100 MHz) at the phase start,
+// when its barrier released, and at its arrival
+enum { TP_PROJ = 1, TP_DN, TP_SCORES, TP_PV, TP_OUT, TP_ROUTER, TP_EXPERTS, TP_DOWN, TP_ENTRY, TP_HEAD };
+template <int NL>
+OXE_DEV void tr_start(Ctx<NL> &c) {
+    if (c.a->trace && threadIdx.x == 0) c.ps->t_start = wall_clock64();
+}
+template <int NL>
+OXE_DEV void tr_pass(Ctx<NL> &c) {
+    if (c.a->trace && threadIdx.x == 0) c.ps->t_pass = wall_clock64();
+}
+// sub-step marker inside a phase: an event (id, previous mark, 0, now)
+template <int NL>
+OXE_DEV void tr_mark(Ctx<NL> &c, int id) {
+    if (c.a->trace && threadIdx.x == 0 && c.ps->tev < FZ_TRACE_EV) {
+        const unsigned long long now = wall_clock64();
+        unsigned long long *e = c.a->trace + ((size_t)c.b * FZ_TRACE_EV + c.ps->tev++) * 4;
+        e[0] = (unsigned long long)id;
+        e[1] = c.ps->t_pass;
+        e[2] = 0ull;
+        e[3] = now;
+        c.ps->t_pass = now;
+    }
+}
+template <int NL>
+OXE_DEV void tr_end(Ctx<NL> &c, int id) {
+    if (c.a->trace && threadIdx.x == 0 && c.ps->tev < FZ_TRACE_EV) {
+        unsigned long long *e = c.a->trace + ((size_t)c.b * FZ_TRACE_EV + c.ps->tev++) * 4;
+        e[0] = (unsigned long long)id;
+        e[1] = c.ps->t_start;
+        e[2] = c.ps->t_pass;
+        e[3] = wall_clock64();
+    }
+}
+
+// ---- phases ----------------------------------------------------------------------------------
+
+// proj: rows [r_begin, r_end) of the layer's input projection over the normalised lanes; V rows
+// (attention) also go to V^T at pos0 + l. Input: the embedding (layer 0 of a verify) or x.
+template <int NL>
+FZ_PHASE bool phase_proj(const RunCtl *ctl, const FusedArgs *ap, int il, bool embed, const float *x, int r_begin, int r_end) {
+    Ctx<NL> c = make_ctx<NL>(ctl, ap);
+    tr_start(c);
+    const LayerDev &L = ap->layers[il];
+    const FusedArgs &a = *c.a;
+    auto &s = c.sm->proj;
+    const int n = r_end - r_begin;
+    const int r0 = r_begin + (int)((int64_t)n * c.b / c.G), r1 = r_begin + (int)((int64_t)n * (c.b + 1) / c.G);
+    const int nr = r1 - r0;
+    WSlice<E, 13> ws;
+    wload<E, 13>(ws, L.proj.q, L.proj.d, nr, [&](int rl) { return (int64_t)(r0 + rl); });
+    if (!wait(c.bar, &c.ps->ok)) return false;
+    tr_pass(c);
+    prologue<NL>(c.nl, c.ctl, embed ? &a.m.tok_embd : nullptr, x, E, true, L.attn_norm, a.m.eps, s.xf, &s.xq[0][0], E,
+                 &s.xd[0][0], E / 32, s.ns, nullptr);
+    tr_mark(c, 111);
+    if (embed && c.b == 0) {
+        // the embedded input is the residual of layer 0
+        const int t = threadIdx.x, l = t >> 8, tt = t & 255;
+        if (l < c.nl)
+            for (int i = 0; i < 8; i++) cst(a.b.x + l * E + 8 * tt + i, s.xf[l][8 * tt + i]);
+    }
+    wdot<E, 13, NL>(ws, nr, &s.xq[0][0], E, &s.xd[0][0], E / 32, s.g);
+    tr_mark(c, 112);
+    const int t = threadIdx.x;
+    if (t < NL * 52) {
+        const int l = t / 52, rl = t % 52;
+        if (l < c.nl && rl < nr) {
+            const int row = r0 + rl;
+            const float v = s.g.out[l][rl];
+            cst(a.b.proj + (int64_t)l * DN_ROWS + row, v);
+            if (L.att && row >= AT_V) {
+                uint16_t *vt = a.m.vcache + (int64_t)L.index * NKV * HD * a.m.n_ctx;
+                cst16(vt + (int64_t)(row - AT_V) * a.m.n_ctx + c.ctl->pos0 + l, f2h(v));
+            }
+        }
+    }
+    tr_end(c, TP_PROJ);
+    arrive(c.bar);
+    return true;
+}
+
+// delta-net recurrence, one value head per workgroup b < 32 (k_layer.hip dn_kernel with 512
+// threads: thread (rg = t/16, c = t%16) owns state rows rg + 32 h, h < 4)
+OXE_DEV float dot16_tree_f(float acc) {
+    acc = acc + shfl_xor_f(acc, 8);
+    acc = acc + shfl_xor_f(acc, 4);
+    acc = acc + shfl_xor_f(acc, 1);
+    acc = acc + shfl_xor_f(acc, 2);
+    return acc;
+}
+OXE_DEV float conv4f(float s0, float s1, float s2, float xn, const float *c) {
+    const float p0 = s0 * c[0], p1 = s1 * c[1], p2 = s2 * c[2], p3 = xn * c[3];
+    float sumf = 0.0f;
+    sumf = sumf + p0;
+    sumf = sumf + p1;
+    sumf = sumf + p2;
+    sumf = sumf + p3;
+    return sumf;
+}
+
+template <int NL>
+FZ_PHASE bool phase_dn(const RunCtl *ctl, const FusedArgs *ap, int il) {
+    Ctx<NL> c = make_ctx<NL>(ctl, ap);
+    tr_start(c);
+    const LayerDev &L = ap->layers[il];
+    const FusedArgs &a = *c.a;
+    auto &s = c.sm->dn;
+    const int t = threadIdx.x, vh = c.b, kh = vh % NKH;
+    const bool worker = c.b < NVH;
+    const int cur = c.ctl->cur;
+    const int64_t conv_slot = (int64_t)a.m.n_rec * NCH * (KC - 1);
+    const int64_t ssm_slot = (int64_t)a.m.n_rec * NVH * HV * HV;
+    float *conv_state = a.m.conv_state + (int64_t)L.index * NCH * (KC - 1);
+    float *ssm = a.m.ssm_state + (int64_t)L.index * NVH * HV * HV;
+    const int rg = t >> 4, cc = t & 15;
+    float r[4][8];
+    if (worker) {
+#pragma unroll
+        for (int h = 0; h < 4; h++) {
+            const float *src = ssm + (int64_t)cur * ssm_slot + ((int64_t)vh * HV + rg + 32 * h) * HV;
+#pragma unroll
+            for (int q = 0; q < 8; q++) r[h][q] = src[cc + 16 * q];
+        }
+    }
+    if (!wait(c.bar, &c.ps->ok)) return false;
+    tr_pass(c);
+    if (worker) {
+        const int nl = c.nl;
+        if (t < 3 * DS) {
+            int ch;
+            bool writer;
+            if (t < DS) { ch = kh * DS + t; writer = vh < NKH; }
+            else if (t < 2 * DS) { ch = NKH * DS + kh * DS + (t - DS); writer = vh < NKH; }
+            else { ch = 2 * NKH * DS + vh * HV + (t - 2 * DS); writer = true; }
+            const float *cw = L.conv + (int64_t)ch * KC;
+            const float *st = conv_state + (int64_t)cur * conv_slot + (int64_t)ch * (KC - 1);
+            float s0 = st[0], s1 = st[1], s2 = st[2];
+            for (int l = 0; l < nl; l++) {
+                const float xn = cld(a.b.proj + (int64_t)l * DN_ROWS + ch);
+                const float y = v_silu(conv4f(s0, s1, s2, xn, cw));
+                s0 = s1; s1 = s2; s2 = xn;
+                if (writer) {
+                    float *dst = conv_state + (int64_t)((cur + l + 1) % OXE_NSLOTS) * conv_slot + (int64_t)ch * (KC - 1);
+                    dst[0] = s0; dst[1] = s1; dst[2] = s2;
+                }
+                if (t < DS) s.q[l][t] = y;
+                else if (t < 2 * DS) s.k[l][t - DS] = y;
+                else s.v[l][t - 2 * DS] = y;
+            }
+        }
+        __syncthreads();
+        tr_mark(c, 121);
+        {
+            const int w = t >> 6, lane = t & 63;
+            if (w < 2 * NL && (w >> 1) < nl) {
+                const int l = w >> 1;
+                float *xv = (w & 1) ? s.k[l] : s.q[l];
+                const float a0 = xv[lane], a1 = xv[lane + 64];
+                const float nf = (float)DS;
+                const float mean = wave_mean_sq_128(a0, a1, xv);
+                const float scale = 1.0f / sqrtf(mean + a.m.eps / nf);
+                const float s2 = 1.0f / sqrtf(nf);
+                xv[lane] = (a0 * scale) * s2;
+                xv[lane + 64] = (a1 * scale) * s2;
+            }
+            if (w == 2 * NL && lane < nl) {
+                const float ab = cld(a.b.proj + (int64_t)lane * DN_ROWS + DN_ALPHA + vh) + L.dt_bias[vh];
+                s.g[lane] = oxe_libm::expf_c(softplus_c(ab) * L.ssm_a[vh]);
+                s.b[lane] = sigmoid_c(cld(a.b.proj + (int64_t)lane * DN_ROWS + DN_BETA + vh));
+            }
+        }
+        __syncthreads();
+        tr_mark(c, 122);
+        const float scale = 1.0f / sqrtf((float)HV);
+        for (int l = 0; l < nl; l++) {
+            const float eg = s.g[l], beta = s.b[l];
+#pragma unroll
+            for (int h = 0; h < 4; h++) {
+                const int j = rg + 32 * h;
+                float acc = 0.0f;
+#pragma unroll
+                for (int q = 0; q < 8; q++) {
+                    r[h][q] = r[h][q] * eg;
+                    acc = __builtin_fmaf(r[h][q], s.k[l][cc + 16 * q], acc);
+                }
+                const float s1 = dot16_tree_f(acc);
+                const float delta = (s.v[l][j] - s1) * beta;
+                acc = 0.0f;
+#pragma unroll
+                for (int q = 0; q < 8; q++) {
+                    r[h][q] = __builtin_fmaf(s.k[l][cc + 16 * q], delta, r[h][q]);
+                    acc = __builtin_fmaf(r[h][q], s.q[l][cc + 16 * q], acc);
+                }
+                const float s2 = dot16_tree_f(acc);
+                float *dst = ssm + (int64_t)((cur + l + 1) % OXE_NSLOTS) * ssm_slot + ((int64_t)vh * HV + j) * HV;
+#pragma unroll
+                for (int q = 0; q < 8; q++) dst[cc + 16 * q] = r[h][q];
+                if (cc == 0) s.o[l][j] = s2 * scale;
+            }
+        }
+        __syncthreads();
+        tr_mark(c, 123);
+        {
+            const int w = t >> 6, lane = t & 63;
+            if (w < nl) {
+                const int l = w;
+                const float x0 = s.o[l][lane], x1 = s.o[l][lane + 64];
+                const float mean = wave_mean_sq_128(x0, x1, s.o[l]);
+                const float sc = 1.0f / sqrtf(mean + a.m.eps);
+                const float *z = a.b.proj + (int64_t)l * DN_ROWS + DN_Z + vh * HV;
+                const float o0 = ((x0 * sc) * L.ssm_norm[lane]) * v_silu(cld(z + lane));
+                const float o1 = ((x1 * sc) * L.ssm_norm[lane + 64]) * v_silu(cld(z + lane + 64));
+                float m0 = __builtin_fabsf(o0), m1 = __builtin_fabsf(o1);
+                for (int mm = 16; mm >= 1; mm >>= 1) {
+                    m0 = fmaxf(m0, shfl_xor_f(m0, mm));
+                    m1 = fmaxf(m1, shfl_xor_f(m1, mm));
+                }
+                const float d0 = m0 / 127.0f, d1 = m1 / 127.0f;
+                const float id0 = d0 != 0.0f ? 1.0f / d0 : 0.0f, id1 = d1 != 0.0f ? 1.0f / d1 : 0.0f;
+                const int32_t q0 = (int32_t)__builtin_rintf(o0 * id0), q1 = (int32_t)__builtin_rintf(o1 * id1);
+                // pack 4 consecutive codes per word: lanes 4k..4k+3
+                uint32_t p0 = (uint32_t)(q0 & 0xff), p1 = (uint32_t)(q1 & 0xff);
+                const int sh = 8 * (lane & 3);
+                p0 <<= sh;
+                p1 <<= sh;
+                p0 |= (uint32_t)shfl_xor_i((int)p0, 1);
+                p1 |= (uint32_t)shfl_xor_i((int)p1, 1);
+                p0 |= (uint32_t)shfl_xor_i((int)p0, 2);
+                p1 |= (uint32_t)shfl_xor_i((int)p1, 2);
+                int8_t *q = a.b.oq + (int64_t)l * DIN + vh * HV;
+                if ((lane & 3) == 0) {
+                    cst32(q + lane, p0);
+                    cst32(q + lane + 64, p1);
+                }
+                uint16_t *d = a.b.od + (int64_t)l * (DIN / 32) + vh * (HV / 32);
+                if (lane == 0) { cst16(d + 0, f2h(d0)); cst16(d + 2, f2h(d1)); }
+                if (lane == 32) { cst16(d + 1, f2h(d0)); cst16(d + 3, f2h(d1)); }
+            }
+        }
+    }
+    tr_end(c, TP_DN);
+    arrive(c.bar);
+    return true;
+}
+
+// out: rows [8 b, 8 b + 8) of ssm_out / attn_output over the quantised mixer output, + residual x
+template <int NL>
+FZ_PHASE bool phase_out(const RunCtl *ctl, const FusedArgs *ap, int il, const float *x) {
+    Ctx<NL> c = make_ctx<NL>(ctl, ap);
+    tr_start(c);
+    const LayerDev &L = ap->layers[il];
+    const FusedArgs &a = *c.a;
+    auto &s = c.sm->out;
+    const int t = threadIdx.x;
+    const int r0 = 8 * c.b;
+    WSlice<MIX_W, 4> ws;
+    wload<MIX_W, 4>(ws, L.out.q, L.out.d, 8, [&](int rl) { return (int64_t)(r0 + rl); });
+    if (!wait(c.bar, &c.ps->ok)) return false;
+    tr_pass(c);
+    {
+        const int l = t >> 8, tt = t & 255;
+        if (l < NL)
+            *(uint4 *)&s.xq[l][16 * tt] = l < c.nl ? cld128(a.b.oq + (int64_t)l * MIX_W + 16 * tt) : make_uint4(0, 0, 0, 0);
+        if (t < NL * (MIX_W / 32)) {
+            const int ll = t / (MIX_W / 32), bb = t % (MIX_W / 32);
+            s.xd[ll][bb] = ll < c.nl ? cld16(a.b.od + (int64_t)ll * (MIX_W / 32) + bb) : (uint16_t)0;
+        }
+    }
+    __syncthreads();
+    wdot<MIX_W, 4, NL>(ws, 8, &s.xq[0][0], MIX_W, &s.xd[0][0], MIX_W / 32, s.g);
+    if (t < NL * 8) {
+        const int l = t / 8, rl = t % 8;
+        if (l < c.nl) {
+            const int64_t i = (int64_t)l * E + r0 + rl;
+            cst(a.b.x1 + i, s.g.out[l][rl] + cld(x + i));
+        }
+    }
+    tr_end(c, TP_OUT);
+    arrive(c.bar);
+    return true;
+}
+
+// router: post_attention_norm + quantise (WG 0 publishes the quantised lanes for the experts),
+// router row b (f32, ggml_vec_dot_f32 order), the shared gate (last WG), shared gate/up half tiles
+// (WGs < 128: gate rows 16 tile + 4 half + i and the matching up rows) + swiglu
+template <int NL>
+FZ_PHASE bool phase_router(const RunCtl *ctl, const FusedArgs *ap, int il) {
+    Ctx<NL> c = make_ctx<NL>(ctl, ap);
+    tr_start(c);
+    const LayerDev &L = ap->layers[il];
+    const FusedArgs &a = *c.a;
+    auto &s = c.sm->router;
+    const int t = threadIdx.x;
+    const int b = c.b;
+    const bool shg = b == c.G - 1;
+    const bool gu = b < 2 * FFSH / 8;   // 128 half tiles
+    const int tile = b >> 1, hf = b & 1;
+    const float4 wrow = *(const float4 *)(L.router + (int64_t)b * E + 4 * t);
+    float4 wsg = make_float4(0, 0, 0, 0);
+    if (shg) wsg = *(const float4 *)(L.shexp_gate + 4 * t);
+    WSlice<E, 2> ws;
+    auto rowof = [&](int rl) { return (int64_t)(tile * 16 + (rl < 4 ? hf * 4 + rl : 8 + hf * 4 + (rl - 4))); };
+    wload<E, 2>(ws, L.shexp_gu.q, L.shexp_gu.d, gu ? 8 : 0, rowof);
+    if (!wait(c.bar, &c.ps->ok)) return false;
+    tr_pass(c);
+    *(float4 *)&s.w[4 * t] = wrow;
+    if (shg) *(float4 *)&s.sg[4 * t] = wsg;
+    prologue<NL>(c.nl, c.ctl, nullptr, a.b.x1, E, true, L.post_norm, a.m.eps, s.xf, &s.xq[0][0], E, &s.xd[0][0], E / 32,
+                 s.ns, s.xn);
+    tr_mark(c, 131);
+    if (b == 0) {
+        const int l = t >> 8, tt = t & 255;
+        if (l < c.nl) {
+            const uint2 v = *(const uint2 *)&s.xq[l][8 * tt];
+            cst64(a.b.xq + (int64_t)l * 2 * E + 8 * tt, (unsigned long long)v.x | ((unsigned long long)v.y << 32));
+            if ((tt & 3) == 0) cst16(a.b.xd + (int64_t)l * (2 * E / 32) + (8 * tt) / 32, s.xd[l][(8 * tt) / 32]);
+        }
+    }
+    // f32 dots: lane c of a 16-lane group runs chain c (elements c + 16 q); xor 8, 4, 1, 2 is the
+    // NEON reduction tree (vec.cpp:104-125)
+    if (t < 64) {
+        const int l = (t >> 4) & 1, cc = t & 15;
+        const bool sgd = t >= 32;
+        const float *wv = sgd ? s.sg : s.w;
+        float acc = 0.0f;
+        if (!sgd || shg) {
+#pragma unroll 8
+            for (int q = 0; q < E / 16; q++) acc = __builtin_fmaf(wv[cc + 16 * q], s.xn[l][cc + 16 * q], acc);
+        }
+        const float v = dot16_tree_f(acc);
+        if (cc == 0 && l < c.nl) {
+            if (!sgd) cst(a.b.router_lg + l * NEXP + b, v);
+            else if (shg) cst(a.b.sh_gate + l, sigmoid_c(v));
+        }
+    }
+    tr_mark(c, 132);
+    if (gu) {
+        wdot<E, 2, NL>(ws, 8, &s.xq[0][0], E, &s.xd[0][0], E / 32, s.g);
+        if (t < NL * 4) {
+            const int l = t / 4, i = t % 4;
+            if (l < c.nl) cst(a.b.hsh + l * FFSH + tile * 8 + hf * 4 + i, v_silu(s.g.out[l][i]) * s.g.out[l][4 + i]);
+        }
+    }
+    tr_end(c, TP_ROUTER);
+    arrive(c.bar);
+    return true;
+}
+
+// routing of every lane (each workgroup, from the published logits), then the routed experts'
+// gate/up (group b = (union slot u = b / 16, 64-row group b % 16): 4 tiles = 32 h values per lane,
+// one Q8_0 block), then the down projection + combine of rows [8 b, 8 b + 8)
+template <int NL>
+FZ_PHASE bool phase_moe(const RunCtl *ctl, const FusedArgs *ap, int il) {
+    Ctx<NL> c = make_ctx<NL>(ctl, ap);
+    tr_start(c);
+    const LayerDev &L = ap->layers[il];
+    const FusedArgs &a = *c.a;
+    auto &se = c.sm->exp;
+    auto &ps = *c.ps;
+    const int t = threadIdx.x, b = c.b, nl = c.nl;
+    if (!wait(c.bar, &ps.ok)) return false;
+    tr_pass(c);
+    // 1. routing (engine.rs:3414-3475)
+    if (t < NL * NEXP) {
+        const int l = t / NEXP, i = t % NEXP;
+        se.lg[l][i] = l < nl ? cld(a.b.router_lg + l * NEXP + i) : 0.0f;
+    }
+    if (t == 0) ps.ro.tie = 0;
+    __syncthreads();
+    if ((t >> 6) < nl) route_wave(se.lg[t >> 6], t >> 6, ps.ro);
+    __syncthreads();
+    if (t < 64) {
+        const int e = t < nl * KUSED ? ps.ro.ids[t / KUSED][t % KUSED] : -1;
+        bool isnew = e >= 0;
+#pragma unroll
+        for (int u = 0; u < NL * KUSED; u++) {
+            const int o = __shfl(e, u);
+            isnew &= !(u < t && o == e);
+        }
+        const unsigned long long mask = __ballot(isnew);
+        const int n = __popcll(mask);
+        const int pos = __popcll(mask & ((1ull << t) - 1));
+        if (isnew) ps.uni[pos] = e;
+        if (t == 0) ps.nu = n;
+        if (b == 0 && t == 0) {
+            if (ps.ro.tie) atomicAdd(a.b.counters + CNT_ERR_TIE, 1u);
+            atomicAdd(a.b.counters + CNT_UNI_SUM, (uint32_t)n);
+            atomicAdd(a.b.counters + CNT_EXP_CALLS, 1u);
+        }
+    }
+    __syncthreads();
+    const int nu = ps.nu < 0 ? 0 : (ps.nu > OXE_MAX_UNION ? OXE_MAX_UNION : ps.nu);
+    if (t < NL * KUSED) {
+        // union slot of each lane's rank-j expert
+        const int l = t / KUSED, j = t % KUSED;
+        int sl = 0;
+        if (l < nl)
+            for (int u = 0; u < nu; u++)
+                if (ps.uni[u] == ps.ro.ids[l][j]) sl = u;
+        ps.slot[l][j] = sl;
+    }
+    __syncthreads();
+    tr_mark(c, 101);
+    // 2. weight loads: this group's gate/up rows, and the down rows of every union expert + shared
+    const bool gw = b < nu * 16;
+    const int u_g = b >> 4, gq = b & 15;
+    int e_g = gw ? ps.uni[u_g] : 0;
+    e_g = e_g < 0 ? 0 : (e_g >= NEXP ? NEXP - 1 : e_g);
+    WSlice<E, 16> ew;
+    wload<E, 16>(ew, L.exp_gu.q + (int64_t)e_g * 2 * FF * E, L.exp_gu.d + (int64_t)e_g * 2 * FF * (E / 32), gw ? 64 : 0,
+                 [&](int rl) { return (int64_t)(gq * 64 + rl); });
+    const int r0 = 8 * b;
+    const int uh = t >> 8, rr = (t >> 5) & 7, ck = t & 31;
+    uint4 dw[9];
+#pragma unroll
+    for (int k = 0; k < 9; k++) {
+        const int u = 2 * k + uh;
+        dw[k] = make_uint4(0, 0, 0, 0);
+        if (u < DW_UNITS && (u == OXE_MAX_UNION || u < nu)) {
+            const int8_t *base;
+            if (u == OXE_MAX_UNION) base = L.shexp_down.q;
+            else {
+                int e = ps.uni[u];
+                e = e < 0 ? 0 : (e >= NEXP ? NEXP - 1 : e);
+                base = L.exp_down.q + (int64_t)e * E * FF;
+            }
+            dw[k] = *(const uint4 *)(base + (int64_t)(r0 + rr) * FF + 16 * ck);
+        }
+    }
+    uint4 dsc = make_uint4(0, 0, 0, 0);
+    const int su = t / 16, srr = (t % 16) / 2, shf = t % 2;
+    if (t < DW_UNITS * 16 && (su == OXE_MAX_UNION || su < nu)) {
+        const uint16_t *base;
+        if (su == OXE_MAX_UNION) base = L.shexp_down.d;
+        else {
+            int e = ps.uni[su];
+            e = e < 0 ? 0 : (e >= NEXP ? NEXP - 1 : e);
+            base = L.exp_down.d + (int64_t)e * E * (FF / 32);
+        }
+        dsc = *(const uint4 *)(base + (int64_t)(r0 + srr) * (FF / 32) + shf * 8);
+    }
+    tr_mark(c, 102);
+    // 3. gate/up + swiglu + Q8_0 of the group's 32 h values per lane
+    if (gw) {
+        {
+            const int l = t >> 8, tt = t & 255;
+            if (l < NL) {
+                const unsigned long long v = l < nl ? cld64(a.b.xq + (int64_t)l * 2 * E + 8 * tt) : 0ull;
+                *(uint2 *)&se.xq[l][8 * tt] = make_uint2((uint32_t)v, (uint32_t)(v >> 32));
+            }
+            if (t < NL * (E / 32)) {
+                const int ll = t / (E / 32), bb = t % (E / 32);
+                se.xd[ll][bb] = ll < nl ? cld16(a.b.xd + (int64_t)ll * (2 * E / 32) + bb) : (uint16_t)0;
+            }
+        }
+        __syncthreads();
+        tr_mark(c, 103);
+        wdot<E, 16, NL>(ew, 64, &se.xq[0][0], E, &se.xd[0][0], E / 32, se.g);
+        tr_mark(c, 104);
+        if (t < NL * 32) {
+            const int l = t / 32, i = t % 32, tl = i >> 3, r = i & 7;
+            se.h[l][i] = v_silu(se.g.out[l][tl * 16 + r]) * se.g.out[l][tl * 16 + 8 + r];
+        }
+        __syncthreads();
+        if (t < NL) quant_block_q8_0(se.h[t], se.hq[t], &se.hd[t]);
+        __syncthreads();
+        if (t < NL * 8) {
+            const int l = t / 8, k = t % 8;
+            if (l < nl) cst32(a.hq + ((int64_t)l * OXE_MAX_UNION + u_g) * FF + gq * 32 + 4 * k, *(const uint32_t *)&se.hq[l][4 * k]);
+        }
+        if (t < nl) cst16(a.hd + ((int64_t)t * OXE_MAX_UNION + u_g) * (FF / 32) + gq, se.hd[t]);
+    }
+    tr_end(c, TP_EXPERTS);
+    tr_start(c);
+    arrive(c.bar);
+    if (!wait(c.bar, &ps.ok)) return false;
+    tr_pass(c);
+    // 4. down + combine (engine.rs:3542-3624)
+    auto &sd = c.sm->down;
+    for (int i = t; i < NL * OXE_MAX_UNION * (FF / 16); i += FT) {
+        const int l = i / (OXE_MAX_UNION * (FF / 16)), u = (i / (FF / 16)) % OXE_MAX_UNION, k = i % (FF / 16);
+        uint4 v = make_uint4(0, 0, 0, 0);
+        if (l < nl && u < nu) v = cld128(a.hq + ((int64_t)l * OXE_MAX_UNION + u) * FF + 16 * k);
+        *(uint4 *)&sd.hq[l][u][16 * k] = v;
+    }
+    if (t < NL * OXE_MAX_UNION * (FF / 32)) {
+        const int l = t / (OXE_MAX_UNION * (FF / 32)), u = (t / (FF / 32)) % OXE_MAX_UNION, k = t % (FF / 32);
+        sd.hd[l][u][k] = (l < nl && u < nu) ? cld16(a.hd + ((int64_t)l * OXE_MAX_UNION + u) * (FF / 32) + k) : (uint16_t)0;
+    }
+    for (int i = t; i < NL * FFSH; i += FT) {
+        const int l = i / FFSH;
+        sd.hs[l][i % FFSH] = l < nl ? cld(a.b.hsh + i) : 0.0f;
+    }
+    if (t < DW_UNITS * 16) {
+        uint32_t *d = &sd.wd[su][srr * (FF / 64 + 1) + shf * 4];
+        d[0] = dsc.x; d[1] = dsc.y; d[2] = dsc.z; d[3] = dsc.w;
+    }
+    __syncthreads();
+    if (t < NL * (FFSH / 32)) {
+        const int l = t / (FFSH / 32), bb = t % (FFSH / 32);
+        quant_block_q8_0(&sd.hs[l][32 * bb], &sd.hq[l][OXE_MAX_UNION][32 * bb], &sd.hd[l][OXE_MAX_UNION][bb]);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < 9; k++) {
+        const int u = 2 * k + uh;
+        if (u < DW_UNITS && (u == OXE_MAX_UNION || u < nu)) {   // uniform within each wave
+#pragma unroll
+            for (int l = 0; l < NL; l++) {
+                const uint4 xa = *(const uint4 *)&sd.hq[l][u][16 * ck];
+                int32_t v = dot16(dw[k], xa, 0);
+                v += shfl_xor_i(v, 1);
+                if ((ck & 1) == 0) sd.isum[u][l][rr][ck >> 1] = v;
+            }
+        }
+    }
+    __syncthreads();
+    if (t < DW_UNITS * NL * 8) {
+        const int u = t / (NL * 8), l = (t / 8) % NL, r = t % 8;
+        if (u == OXE_MAX_UNION || u < nu) {
+            const uint16_t *sw = (const uint16_t *)&sd.wd[u][r * (FF / 64 + 1)];
+            float acc = 0.0f;
+#pragma unroll
+            for (int bb = 0; bb < FF / 32; bb++)
+                acc = __builtin_fmaf((float)sd.isum[u][l][r][bb], h2f(sd.hd[l][u][bb]) * h2f(sw[bb]), acc);
+            sd.dn[u][l][r] = acc;
+        }
+    }
+    __syncthreads();
+    if (t < NL * 8) {
+        const int l = t / 8, r = t % 8;
+        if (l < nl) {
+            float m = sd.dn[ps.slot[l][0]][l][r] * ps.ro.w[l][0];
+            for (int j = 1; j < KUSED; j++) {
+                const float p = sd.dn[ps.slot[l][j]][l][r] * ps.ro.w[l][j];
+                m = m + p;
+            }
+            const float sg = cld(a.b.sh_gate + l);
+            const float sh = sd.dn[OXE_MAX_UNION][l][r] * sg;
+            const float f = m + sh;
+            const int64_t i = (int64_t)l * E + r0 + r;
+            cst(a.b.x2 + i, f + cld(a.b.x1 + i));
+        }
+    }
+    tr_end(c, TP_DOWN);
+    arrive(c.bar);
+    return true;
+}
+
+// attention scores (workgroup = kv head x 128 positions) with the query prologue (q_norm, RoPE,
+// f16) and the run's own K rows computed in place (k_norm, RoPE); the workgroup whose range holds
+// a new position writes its K cache row
+OXE_DEV uint16_t *kcache_layer(const FusedArgs &a, const LayerDev &L) {
+    return a.m.kcache + (int64_t)L.index * NKV * a.m.n_ctx * HD;
+}
+
+typedef _Float16 h2t __attribute__((ext_vector_type(2)));
+OXE_DEV h2t u2h2f(uint32_t u) { return __builtin_bit_cast(h2t, u); }
+OXE_DEV uint32_t h22uf(h2t v) { return __builtin_bit_cast(uint32_t, v); }
+OXE_DEV float f16x8_reduce_q(h2t acc[4]) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) acc[i] = acc[i] + u2h2f(__shfl_xor(h22uf(acc[i]), 2, 64));
+#pragma unroll
+    for (int i = 0; i < 4; i++) acc[i] = acc[i] + u2h2f(__shfl_xor(h22uf(acc[i]), 1, 64));
+    const float t0 = (float)acc[0].x + (float)acc[2].x;
+    const float t1 = (float)acc[0].y + (float)acc[2].y;
+    const float t2 = (float)acc[1].x + (float)acc[3].x;
+    const float t3 = (float)acc[1].y + (float)acc[3].y;
+    return (t0 + t1) + (t2 + t3);
+}
+
+constexpr int SC_P = FT / 8;   // positions per scores workgroup (4 threads per position and lane)
+
+template <int NL>
+FZ_PHASE bool phase_scores(const RunCtl *ctl, const FusedArgs *ap, int il, bool seed_only) {
+    Ctx<NL> c = make_ctx<NL>(ctl, ap);
+    tr_start(c);
+    const LayerDev &L = ap->layers[il];
+    const FusedArgs &a = *c.a;
+    auto &s = c.sm->sc;
+    const int t = threadIdx.x, w = t >> 6, lane = t & 63, nl = c.nl;
+    const int pos0 = c.ctl->pos0, pmax = pos0 + nl - 1;
+    const int kvh = c.b % NKV, chunk = c.b / NKV;
+    const bool act = chunk * SC_P <= pmax;
+    if (!wait(c.bar, &c.ps->ok)) return false;
+    tr_pass(c);
+    // step 1: raw K rows of the run's positions in this range, and the raw queries, into LDS
+    // (one wave per vector); step 2: the norms; step 3: RoPE; step 4: f16 (and K cache rows)
+    const int kjob = w;                          // waves 0..NL-1: K row of lane w
+    const int pk = pos0 + kjob;
+    const bool kdo = act && kjob < nl && pk >= chunk * SC_P && pk < (chunk + 1) * SC_P;
+    float kv4[4], qv4[(NL * GQA + 7) / 8][4];
+    if (kdo) {
+        const float *kr = a.b.proj + (int64_t)kjob * DN_ROWS + AT_K + kvh * HD;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            kv4[i] = cld(kr + lane + 64 * i);
+            s.ktmp[kjob][lane + 64 * i] = kv4[i];
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < (NL * GQA + 7) / 8; k++) {
+        const int job = w + 8 * k, l = job / GQA, h = kvh * GQA + job % GQA;
+        if (act && !seed_only && job < NL * GQA && l < nl) {
+            const float *q = a.b.proj + (int64_t)l * DN_ROWS + h * 2 * HD;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                qv4[k][i] = cld(q + lane + 64 * i);
+                s.tmp[w + 8 * k][lane + 64 * i] = qv4[k][i];
+            }
+        }
+    }
+    __syncthreads();
+    if (kdo) {
+        const float mean = wave_mean_sq_256(kv4, s.ktmp[kjob]);
+        const float scale = 1.0f / sqrtf(mean + a.m.eps);
+#pragma unroll
+        for (int i = 0; i < 4; i++) kv4[i] = (kv4[i] * scale) * L.k_norm[lane + 64 * i];
+    }
+#pragma unroll
+    for (int k = 0; k < (NL * GQA + 7) / 8; k++) {
+        const int job = w + 8 * k, l = job / GQA;
+        if (act && !seed_only && job < NL * GQA && l < nl) {
+            const float mean = wave_mean_sq_256(qv4[k], s.tmp[job]);
+            const float scale = 1.0f / sqrtf(mean + a.m.eps);
+#pragma unroll
+            for (int i = 0; i < 4; i++) qv4[k][i] = (qv4[k][i] * scale) * L.q_norm[lane + 64 * i];
+        }
+    }
+    __syncthreads();
+    if (kdo)
+#pragma unroll
+        for (int i = 0; i < 4; i++) s.ktmp[kjob][lane + 64 * i] = kv4[i];
+#pragma unroll
+    for (int k = 0; k < (NL * GQA + 7) / 8; k++) {
+        const int job = w + 8 * k, l = job / GQA;
+        if (act && !seed_only && job < NL * GQA && l < nl)
+#pragma unroll
+            for (int i = 0; i < 4; i++) s.tmp[job][lane + 64 * i] = qv4[k][i];
+    }
+    __syncthreads();
+    if (kdo) rope_neox_lds(s.ktmp[kjob], a.m.rope + (int64_t)pk * NROT, lane);
+#pragma unroll
+    for (int k = 0; k < (NL * GQA + 7) / 8; k++) {
+        const int job = w + 8 * k, l = job / GQA;
+        if (act && !seed_only && job < NL * GQA && l < nl) rope_neox_lds(s.tmp[job], a.m.rope + (int64_t)(pos0 + l) * NROT, lane);
+    }
+    __syncthreads();
+    if (kdo) {
+        uint16_t *kc = kcache_layer(a, L);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint16_t h = f2h(s.ktmp[kjob][lane + 64 * i]);
+            s.knew[kjob][lane + 64 * i] = h;
+            kc[((int64_t)kvh * a.m.n_ctx + pk) * HD + lane + 64 * i] = h;
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < (NL * GQA + 7) / 8; k++) {
+        const int job = w + 8 * k, l = job / GQA;
+        if (act && !seed_only && job < NL * GQA)
+#pragma unroll
+            for (int i = 0; i < 4; i++) s.q[job][lane + 64 * i] = l < nl ? f2h(s.tmp[job][lane + 64 * i]) : (uint16_t)0;
+    }
+    __syncthreads();
+    if (act && !seed_only) {
+        // thread = (lane l, position p, chain quad j): the 8 heads of the group for one lane
+        const int l = t >> 8, tt = t & 255;
+        const int p = chunk * SC_P + (tt >> 2), j = tt & 3;
+        if (l < nl && p <= pos0 + l) {
+            const uint16_t *krow = p < pos0 ? kcache_layer(a, L) + ((int64_t)kvh * a.m.n_ctx + p) * HD : s.knew[p - pos0];
+            h2t acc[GQA][4];
+#pragma unroll
+            for (int q = 0; q < GQA; q++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) acc[q][i] = h2t{(_Float16)0.0f, (_Float16)0.0f};
+#pragma unroll 2
+            for (int sx = 0; sx < HD / 32; sx++) {
+                const uint4 kv = *(const uint4 *)(krow + 32 * sx + 8 * j);
+                const h2t k0 = u2h2f(kv.x), k1 = u2h2f(kv.y), k2 = u2h2f(kv.z), k3 = u2h2f(kv.w);
+#pragma unroll
+                for (int q = 0; q < GQA; q++) {
+                    const uint4 qv = *(const uint4 *)(&s.q[l * GQA + q][32 * sx + 8 * j]);
+                    acc[q][0] = __builtin_elementwise_fma(k0, u2h2f(qv.x), acc[q][0]);
+                    acc[q][1] = __builtin_elementwise_fma(k1, u2h2f(qv.y), acc[q][1]);
+                    acc[q][2] = __builtin_elementwise_fma(k2, u2h2f(qv.z), acc[q][2]);
+                    acc[q][3] = __builtin_elementwise_fma(k3, u2h2f(qv.w), acc[q][3]);
+                }
+            }
+#pragma unroll
+            for (int q = 0; q < GQA; q++) {
+                const float sc = f16x8_reduce_q(acc[q]);
+                if (j == 0) cst(a.b.scores + ((int64_t)l * NH + kvh * GQA + q) * a.m.n_ctx + p, sc);
+            }
+        }
+    }
+    tr_end(c, TP_SCORES);
+    arrive(c.bar);
+    return true;
+}
+
+// softmax + V^T . p + gate + Q8_0 (k_attn.hip pv_kernel), workgroup = (kv head, lane, 32 dims)
+template <int NL>
+FZ_PHASE bool phase_pv(const RunCtl *ctl, const FusedArgs *ap, int il) {
+    Ctx<NL> c = make_ctx<NL>(ctl, ap);
+    tr_start(c);
+    const LayerDev &L = ap->layers[il];
+    const FusedArgs &a = *c.a;
+    const int t = threadIdx.x, nl = c.nl;
+    constexpr int PVD = 32;
+    const int dchunk = c.b % (HD / PVD);
+    const int l = (c.b / (HD / PVD)) % NL;
+    const int kvh = c.b / ((HD / PVD) * NL);
+    const bool act = kvh < NKV && l < nl;
+    if (!wait(c.bar, &c.ps->ok)) return false;
+    tr_pass(c);
+    if (act) {
+        const int n_ctx = a.m.n_ctx;
+        uint16_t *s_p = (uint16_t *)c.dyn;                                  // [GQA][n_kv]
+        float *s_e = (float *)(c.dyn + (size_t)GQA * ((n_ctx + 1) & ~1) * 2);   // [n_kv]
+        float *s_gs = s_e + n_ctx;                                           // [n_kv / 4]
+        double *s_red = (double *)(((uintptr_t)(s_gs + n_ctx / 4) + 15) & ~(uintptr_t)15);   // [16]
+        float *s_mx = (float *)(s_red + 16);                                  // [16]
+        float *s_o = s_mx + 16;                                               // [GQA][PVD]
+        const int pos = c.ctl->pos0 + l;
+        const int pos0 = c.ctl->pos0;
+        int n_kv = (pos + 1 + 255) / 256 * 256;
+        if (n_kv < 256) n_kv = 256;
+        if (n_kv > n_ctx) n_kv = n_ctx;
+        const float scale = 1.0f / sqrtf((float)HD);
+        for (int hh = 0; hh < GQA; hh++) {
+            const int h = kvh * GQA + hh;
+            const float *sc = a.b.scores + ((int64_t)l * NH + h) * n_ctx;
+            float mx = -__builtin_inff();
+            for (int i = t; i < n_kv; i += FT) {
+                const float wv = i <= pos ? cld(sc + i) * scale : -__builtin_inff();
+                s_e[i] = wv;
+                mx = (mx > wv) ? mx : wv;
+            }
+            mx = block_max_f<FT>(mx, s_mx);
+            double part = 0.0;
+            for (int i0 = 0; i0 < n_kv; i0 += FT) {
+                const int i = i0 + t;
+                const float e = i < n_kv ? v_expf(s_e[i] - mx) : 0.0f;
+                if (i < n_kv) s_e[i] = e;
+                float g = e + shfl_xor_f(e, 1);
+                g = g + shfl_xor_f(g, 2);
+                if ((t & 3) == 0 && i < n_kv) {
+                    s_gs[i >> 2] = g;
+                    part += (double)g;
+                }
+            }
+            const double P = block_sum_d<FT>(part, s_red);
+            float f;
+            if (!bracket_ok_recip(P, P, n_kv / 4, &f)) {
+                if (t == 0) {
+                    double sum = 0.0;
+                    for (int g = 0; g < n_kv / 4; g++) sum += (double)s_gs[g];
+                    s_red[0] = sum;
+                }
+                __syncthreads();
+                f = (float)(1.0 / s_red[0]);
+                __syncthreads();
+            }
+            for (int i = t; i < n_kv; i += FT) s_p[hh * n_kv + i] = f2h(s_e[i] * f);
+            __syncthreads();
+        }
+        tr_mark(c, 141);
+        // V^T . p: thread = (head group hg of 2 heads, dim d, chain quad j)
+        const int j = t & 3, d = (t >> 2) & (PVD - 1), hg = t >> 7;
+        const int dg = dchunk * PVD + d;
+        const uint16_t *vrow = a.m.vcache + (int64_t)L.index * NKV * HD * n_ctx + (int64_t)(kvh * HD + dg) * n_ctx;
+        h2t acc[2][4];
+#pragma unroll
+        for (int q = 0; q < 2; q++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) acc[q][i] = h2t{(_Float16)0.0f, (_Float16)0.0f};
+        for (int sx = 0; sx < n_kv / 32; sx++) {
+            // chunks holding a position written in this launch are read device-coherently
+            const uint4 vv = 32 * sx + 31 >= pos0 ? cld128(vrow + 32 * sx + 8 * j) : *(const uint4 *)(vrow + 32 * sx + 8 * j);
+            const h2t v0 = u2h2f(vv.x), v1 = u2h2f(vv.y), v2 = u2h2f(vv.z), v3 = u2h2f(vv.w);
+#pragma unroll
+            for (int q = 0; q < 2; q++) {
+                const uint4 pv = *(const uint4 *)(&s_p[(hg * 2 + q) * n_kv + 32 * sx + 8 * j]);
+                acc[q][0] = __builtin_elementwise_fma(v0, u2h2f(pv.x), acc[q][0]);
+                acc[q][1] = __builtin_elementwise_fma(v1, u2h2f(pv.y), acc[q][1]);
+                acc[q][2] = __builtin_elementwise_fma(v2, u2h2f(pv.z), acc[q][2]);
+                acc[q][3] = __builtin_elementwise_fma(v3, u2h2f(pv.w), acc[q][3]);
+            }
+        }
+#pragma unroll
+        for (int q = 0; q < 2; q++) {
+            const float out = f16x8_reduce_q(acc[q]);
+            const int hh = hg * 2 + q, h = kvh * GQA + hh;
+            if (j == 0) {
+                const float gate = cld(a.b.proj + (int64_t)l * DN_ROWS + h * 2 * HD + HD + dg);
+                s_o[hh * PVD + d] = out * sigmoid_c(gate);
+            }
+        }
+        __syncthreads();
+        int8_t *sq = (int8_t *)(s_o + GQA * PVD);
+        uint16_t *sd = (uint16_t *)(sq + GQA * PVD);
+        if (t < GQA) quant_block_q8_0(s_o + t * PVD, sq + t * PVD, sd + t);
+        __syncthreads();
+        if (t < GQA * 8) {
+            const int hh = t / 8, k = t % 8, h = kvh * GQA + hh;
+            const int64_t off = (int64_t)l * MIX_W + h * HD + dchunk * PVD;
+            cst32(a.b.oq + off + 4 * k, *(const uint32_t *)(sq + hh * PVD + 4 * k));
+            if (k == 0) cst16(a.b.od + off / 32, sd[hh]);
+        }
+    }
+    tr_end(c, TP_PV);
+    arrive(c.bar);
+    return true;
+}
+
+// MTP entry: x2 = eh_proj . [enorm(embd(tok)); hnorm(h)], rows [8 b, 8 b + 8)
+template <int NL>
+FZ_PHASE bool phase_entry(const RunCtl *ctl, const FusedArgs *ap, int il) {
+    Ctx<NL> c = make_ctx<NL>(ctl, ap);
+    tr_start(c);
+    const LayerDev &L = ap->layers[il];
+    const FusedArgs &a = *c.a;
+    auto &s = c.sm->entry;
+    const int t = threadIdx.x, r0 = 8 * c.b;
+    WSlice<2 * E, 4> ws;
+    wload<2 * E, 4>(ws, L.eh_proj.q, L.eh_proj.d, 8, [&](int rl) { return (int64_t)(r0 + rl); });
+    // no barrier precedes the entry (its inputs come from earlier launches)
+    prologue<NL>(c.nl, c.ctl, &a.m.tok_embd, nullptr, 0, false, L.enorm, a.m.eps, s.xf, &s.xq[0][0], 2 * E, &s.xd[0][0],
+                 2 * E / 32, s.ns, nullptr);
+    {
+        // h of each lane: hid[hin_sel[l]]
+        const int l = t >> 8, tt = t & 255;
+        float v[8];
+        if (l < NL && l < c.nl) get8(a.b.hid + (int64_t)c.ctl->hin_sel[l] * E + 8 * tt, v);
+        else
+            for (int i = 0; i < 8; i++) v[i] = 0.0f;
+        if (l < NL) put8(&s.xf[l][8 * tt], v);
+        __syncthreads();
+        norm8(v, s.xf[l < NL ? l : 0], L.hnorm, a.m.eps, s.ns);
+        if (l < NL) {
+            if (l < c.nl) quant8(v, &s.xq[l][E + 8 * tt], &s.xd[l][(E + 8 * tt) / 32]);
+            else {
+                *(uint2 *)&s.xq[l][E + 8 * tt] = make_uint2(0, 0);
+                if ((tt & 3) == 0) s.xd[l][(E + 8 * tt) / 32] = 0;
+            }
+        }
+        __syncthreads();
+    }
+    wdot<2 * E, 4, NL>(ws, 8, &s.xq[0][0], 2 * E, &s.xd[0][0], 2 * E / 32, s.g);
+    if (t < NL * 8) {
+        const int l = t / 8, rl = t % 8;
+        if (l < c.nl) cst(a.b.x2 + (int64_t)l * E + r0 + rl, s.g.out[l][rl]);
+    }
+    tr_end(c, TP_ENTRY);
+    arrive(c.bar);
+    return true;
+}
+
+// output norm + LM head + per-workgroup argmax keys (first strict maximum, NaN never wins)
+OXE_DEV uint32_t ordered_bits_f(float f) {
+    const uint32_t u = __builtin_bit_cast(uint32_t, f);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+template <int NL>
+FZ_PHASE bool phase_head(const RunCtl *ctl, const FusedArgs *ap, const float *norm_w) {
+    Ctx<NL> c = make_ctx<NL>(ctl, ap);
+    tr_start(c);
+    const FusedArgs &a = *c.a;
+    auto &s = c.sm->head;
+    const int t = threadIdx.x, nl = c.nl, mask = c.ctl->head_mask;
+    const int64_t V = a.m.output.rows;
+    constexpr int TR = 32;                                   // rows per tile
+    const int64_t ntiles = (V + TR - 1) / TR;
+    const int64_t t0 = ntiles * c.b / c.G, t1 = ntiles * (c.b + 1) / c.G;
+    WSlice<E, 8> A, B;
+    auto rows_of = [&](int64_t tile) { const int64_t r = V - tile * TR; return (int)(r < TR ? r : TR); };
+    if (t0 < t1) wload<E, 8>(A, a.m.output.q, a.m.output.d, rows_of(t0), [&](int rl) { return t0 * TR + rl; });
+    if (!wait(c.bar, &c.ps->ok)) return false;
+    tr_pass(c);
+    prologue<NL>(nl, c.ctl, nullptr, a.b.x2, E, true, norm_w, a.m.eps, s.xf, &s.xq[0][0], E, &s.xd[0][0], E / 32, s.ns,
+                 s.xn);
+    if (c.b == 0) {
+        // h_nextn of each lane (Engine::hidden): the normalised x2
+        const int l = t >> 8, tt = t & 255;
+        if (l < nl) put8(a.b.hid + (int64_t)l * E + 8 * tt, &s.xn[l][8 * tt]);
+    }
+    if (mask == 0) return true;
+    float best = -__builtin_inff();
+    int64_t bi = -1;
+    const int rl = t % TR, l = t / TR;
+    for (int64_t tile = t0; tile < t1; tile += 2) {
+        const bool hb = tile + 1 < t1;
+        if (hb) wload<E, 8>(B, a.m.output.q, a.m.output.d, rows_of(tile + 1), [&](int r) { return (tile + 1) * TR + r; });
+        {
+            const int nr = rows_of(tile);
+            wdot<E, 8, NL>(A, nr, &s.xq[0][0], E, &s.xd[0][0], E / 32, s.g);
+            if (l < NL && l < nl && rl < nr) {
+                const float v = s.g.out[l][rl];
+                const int64_t row = tile * TR + rl;
+                if (a.keep_logits) a.b.logits[l * V + row] = v;
+                if (v > best) { best = v; bi = row; }
+            }
+        }
+        if (hb) {
+            if (tile + 2 < t1) wload<E, 8>(A, a.m.output.q, a.m.output.d, rows_of(tile + 2), [&](int r) { return (tile + 2) * TR + r; });
+            const int nr = rows_of(tile + 1);
+            wdot<E, 8, NL>(B, nr, &s.xq[0][0], E, &s.xd[0][0], E / 32, s.g);
+            if (l < NL && l < nl && rl < nr) {
+                const float v = s.g.out[l][rl];
+                const int64_t row = (tile + 1) * TR + rl;
+                if (a.keep_logits) a.b.logits[l * V + row] = v;
+                if (v > best) { best = v; bi = row; }
+            }
+        }
+    }
+    // per-lane key of this workgroup: the largest value, then the smallest row
+    unsigned long long key = 0ull;
+    if (l < NL && l < nl && ((mask >> l) & 1) && bi >= 0)
+        key = ((unsigned long long)ordered_bits_f(best) << 32) | (0xffffffffu - (uint32_t)bi);
+    if (t < NL * TR) {
+        for (int m = TR / 2; m >= 1; m >>= 1) {
+            const unsigned long long o = __shfl_xor(key, m, 64);
+            key = key > o ? key : o;
+        }
+        if (rl == 0 && l < NL) a.keys[(int64_t)l * c.G + c.b] = key;
+    }
+    tr_end(c, TP_HEAD);
+    return true;
+}
+
+template <int NL>
+OXE_DEV bool run_layer(const RunCtl *ctl, const FusedArgs *ap, int il, bool first) {
+    const LayerDev &L = ap->layers[il];
+    const float *x = first ? ap->b.x : ap->b.x2;
+    const int att = L.att;
+    if (!phase_proj<NL>(ctl, ap, il, first && ap->mode == FM_VERIFY, x, 0, att ? AT_ROWS : DN_ROWS)) return false;
+    if (!att) {
+        if (!phase_dn<NL>(ctl, ap, il)) return false;
+    } else {
+        if (!phase_scores<NL>(ctl, ap, il, false)) return false;
+        if (!phase_pv<NL>(ctl, ap, il)) return false;
+    }
+    if (!phase_out<NL>(ctl, ap, il, x)) return false;
+    if (!phase_router<NL>(ctl, ap, il)) return false;
+    if (!phase_moe<NL>(ctl, ap, il)) return false;
+    return true;
+}
+
+}  // namespace fz
+
+template <int NL>
+__global__ __launch_bounds__(fz::FT, 1) void fused_kernel(const RunCtl *__restrict__ ctl, const FusedArgs *__restrict__ ap) {
+    using namespace fz;
+    if (!ctl->active) return;
+    if (threadIdx.x == 0) {
+        fz_ps.round = cld32(&ap->sync[FZ_W_FLAG]);
+        fz_ps.tev = 0;
+    }
+    __syncthreads();
+    // the first phase of a run has no producer in this launch: its wait (the current round) passes at once
+    const int mode = ap->mode, nlay = ap->n_layer;
+    if (mode == FM_VERIFY) {
+        for (int il = 0; il < nlay; il++)
+            if (!run_layer<NL>(ctl, ap, il, il == 0)) return;
+        (void)phase_head<NL>(ctl, ap, ap->m.out_norm);
+    } else if (mode == FM_DRAFT) {
+        const int il = nlay;
+        if (!phase_entry<NL>(ctl, ap, il)) return;
+        // the MTP layer (attention) with input x2 (the entry output)
+        if (!phase_proj<NL>(ctl, ap, il, false, ap->b.x2, 0, AT_ROWS)) return;
+        if (!phase_scores<NL>(ctl, ap, il, false)) return;
+        if (!phase_pv<NL>(ctl, ap, il)) return;
+        if (!phase_out<NL>(ctl, ap, il, ap->b.x2)) return;
+        if (!phase_router<NL>(ctl, ap, il)) return;
+        if (!phase_moe<NL>(ctl, ap, il)) return;
+        (void)phase_head<NL>(ctl, ap, ap->layers[il].head_norm);
+    } else {
+        const int il = nlay;
+        if (!phase_entry<NL>(ctl, ap, il)) return;
+        if (!phase_proj<NL>(ctl, ap, il, false, ap->b.x2, AT_K, AT_ROWS)) return;
+        (void)phase_scores<NL>(ctl, ap, il, true);
+    }
+}
+
+size_t fused_lds_bytes(int n_ctx) {
+    const size_t base = sizeof(fz::PhaseSm<OXE_NL>);
+    const size_t pv = (size_t)GQA * ((n_ctx + 1) & ~1) * 2 + (size_t)n_ctx * 4 + (size_t)(n_ctx / 4) * 4 + 16 + 16 * 8 +
+                      16 * 4 + GQA * 32 * 4 + GQA * 32 + GQA * 2 + 256;
+    return (base > pv ? base : pv + 16) / 16 * 16 + 16;
+}
+
+int fused_blocks_per_cu(size_t lds) {
+    static size_t configured = 0;
+    if (lds > configured) {
+        if (hipFuncSetAttribute((const void *)fused_kernel<OXE_NL>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) !=
+            hipSuccess)
+            return 0;
+        configured = lds;
+    }
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fused_kernel<OXE_NL>, fz::FT, lds) != hipSuccess) return 0;
+    return n;
+}
+
+void launch_fused(const RunCtl *ctl, const FusedArgs *dev_args, int grid, size_t lds, hipStream_t st) {
+    hipLaunchKernelGGL(fused_kernel<OXE_NL>, dim3((unsigned)grid), dim3(fz::FT), lds, st, ctl, dev_args);
+}
+
+__global__ void fused_sync_reset_kernel(uint32_t *w) {
+    for (int i = threadIdx.x; i < FZ_SYNC_WORDS; i += blockDim.x) w[i] = 0u;
+}
+void launch_fused_sync_reset(uint32_t *sync, hipStream_t st) {
+    hipLaunchKernelGGL(fused_sync_reset_kernel, dim3(1), dim3(256), 0, st, sync);
+}
+
+}  // namespace oxe

@@ -48,9 +48,22 @@ __global__ void mtp_prep_draft_kernel(MtpState *ms, RunCtl *ctl, int n_ctx) {
     *ctl = r;
 }
 
-__global__ void mtp_prep_verify_kernel(MtpState *ms, RunCtl *ctl, const unsigned long long *keys, const int32_t *force_d1,
-                                       int force_n) {
-    uint32_t d1 = decode_key(keys[0]);
+// the largest of n argmax keys (one wave: lanes stride the keys, then a shuffle tree)
+__device__ unsigned long long wave_key_max(const unsigned long long *keys, int n) {
+    unsigned long long k = 0ull;
+    for (int i = threadIdx.x & 63; i < n; i += 64) k = keys[i] > k ? keys[i] : k;
+    for (int m = 32; m >= 1; m >>= 1) {
+        const unsigned long long o = __shfl_xor(k, m, 64);
+        k = o > k ? o : k;
+    }
+    return k;
+}
+
+__global__ void mtp_prep_verify_kernel(MtpState *ms, RunCtl *ctl, const unsigned long long *keys, int nkeys,
+                                       const int32_t *force_d1, int force_n) {
+    const unsigned long long k0 = wave_key_max(keys, nkeys);
+    if (threadIdx.x != 0) return;
+    uint32_t d1 = decode_key(k0);
     if (force_d1 && ms->steps < force_n && force_d1[ms->steps] >= 0) d1 = (uint32_t)force_d1[ms->steps];  // test hook (mtp.rs:554-558)
     ms->d1 = d1;
     RunCtl r{};
@@ -67,15 +80,20 @@ __global__ void mtp_prep_verify_kernel(MtpState *ms, RunCtl *ctl, const unsigned
 }
 
 // accept / commit / note (mtp.rs:564-591, engine.rs:2030-2039): a = (d1 == argmax lane 0)
-__global__ void mtp_commit_kernel(MtpState *ms, const unsigned long long *keys, float *hid, uint16_t *vcache,
+__global__ void mtp_commit_kernel(MtpState *ms, const unsigned long long *keys, int nkeys, float *hid, uint16_t *vcache,
                                   int64_t vrows, int n_ctx, uint32_t *out_tok, int out_cap) {
     __shared__ int s_a, s_ok, s_pos0;
+    __shared__ uint32_t s_g[2];
     const int t = threadIdx.x;
-    if (t == 0) {
-        s_ok = ms->err == 0;
-        const uint32_t g0 = decode_key(keys[0]);
-        s_a = s_ok && ms->d1 == g0;
-        s_pos0 = ms->pos;
+    if (t < 64) {
+        const unsigned long long k0 = wave_key_max(keys, nkeys), k1 = wave_key_max(keys + nkeys, nkeys);
+        if (t == 0) {
+            s_g[0] = decode_key(k0);
+            s_g[1] = decode_key(k1);
+            s_ok = ms->err == 0;
+            s_a = s_ok && ms->d1 == s_g[0];
+            s_pos0 = ms->pos;
+        }
     }
     __syncthreads();
     if (!s_ok) return;
@@ -90,7 +108,7 @@ __global__ void mtp_commit_kernel(MtpState *ms, const unsigned long long *keys, 
     if (!a)  // the rejected lane's V^T column of the main attention layers back to +0 (zero_v)
         for (int64_t r = t; r < vrows; r += blockDim.x) vcache[r * n_ctx + pos0 + 1] = 0;
     if (t == 0) {
-        const uint32_t g0 = decode_key(keys[0]), g1 = decode_key(keys[1]);
+        const uint32_t g0 = s_g[0], g1 = s_g[1];
         int n = ms->n_out;
         if (n < out_cap) out_tok[n++] = g0;
         if (a && n < out_cap) out_tok[n++] = g1;
@@ -237,6 +255,7 @@ int MtpDriverHost::dev_end(Engine &e, uint32_t *out_tok, int cap, int *n_out, ui
     MtpState s{};
     if (hipMemcpyAsync(&s, e.mtp_state, sizeof(s), hipMemcpyDeviceToHost, e.st) != hipSuccess) return -2;
     if (hipStreamSynchronize(e.st) != hipSuccess) return -2;
+    if (int rc = e.fused_check()) return rc;
     const int n = std::min(s.n_out, cap);
     if (n > 0 && hipMemcpy(out_tok, e.out_tok, (size_t)n * 4, hipMemcpyDeviceToHost) != hipSuccess) return -2;
     *n_out = n;
@@ -264,10 +283,10 @@ void Engine::enqueue_mtp_device_step() {
     enqueue_mtp_seed();
     hipLaunchKernelGGL(mtp_prep_draft_kernel, dim3(1), dim3(1), 0, st, mtp_state, ctl, m.n_ctx);
     enqueue_mtp_run();
-    hipLaunchKernelGGL(mtp_prep_verify_kernel, dim3(1), dim3(1), 0, st, mtp_state, ctl, (const unsigned long long *)b.amax_key,
+    hipLaunchKernelGGL(mtp_prep_verify_kernel, dim3(1), dim3(64), 0, st, mtp_state, ctl, keys(), nkeys(),
                        (const int32_t *)force_d1, force_n);
     enqueue_verify();
-    hipLaunchKernelGGL(mtp_commit_kernel, dim3(1), dim3(256), 0, st, mtp_state, (const unsigned long long *)b.amax_key, b.hid,
+    hipLaunchKernelGGL(mtp_commit_kernel, dim3(1), dim3(256), 0, st, mtp_state, keys(), nkeys(), b.hid,
                        m.vcache, (int64_t)n_att_main * NKV * HD, m.n_ctx, out_tok, out_cap);
 }
 
@@ -297,50 +316,23 @@ extern "C" {
 
 // Eagerly enqueue k device-driven MTP steps with HIP events around every launch of kernel `kind`
 // (engine stream); *avg_us = mean launch duration, *n = launches timed. For the bench's roofline.
-int oxe_mtp_device_probe(oxe_engine *e, int k, int kind, int use_graph, float *avg_us, int *n) {
+int oxe_mtp_device_probe(oxe_engine *e, int k, int kind, float *avg_us, int *n) {
     Engine *g = (Engine *)e;
     if (k < 1 || kind < 0 || !avg_us || !n) return -1;
-    double tot = 0.0;
-    int cnt = 0;
-    auto collect = [&]() -> int {
-        if (hipStreamSynchronize(g->st) != hipSuccess) return -2;
-        for (size_t i = 0; i + 1 < g->probe_used; i += 2) {
-            float ms = 0.0f;
-            if (hipEventElapsedTime(&ms, g->probe_ev[i], g->probe_ev[i + 1]) != hipSuccess) return -2;
-            tot += ms;
-            cnt++;
-        }
-        return 0;
-    };
     g->probe_kind = kind;
     g->probe_used = 0;
-    if (!use_graph) {
-        // eager launches with events around each launch of the kind
-        int rc = g->mtp_steps_async(k, false);
-        g->probe_kind = -1;
-        if (rc) return rc;
-        if ((rc = collect())) return rc;
-    } else {
-        // the step graph with event-record nodes around each launch of the kind: the events time
-        // the kernels as they run inside the graph
-        hipGraph_t gr;
-        hipGraphExec_t ex = nullptr;
-        int rc = hipStreamBeginCapture(g->st, hipStreamCaptureModeThreadLocal) == hipSuccess ? 0 : -2;
-        if (!rc) {
-            g->enqueue_mtp_device_step();
-            rc = hipStreamEndCapture(g->st, &gr) == hipSuccess ? 0 : -2;
-            if (!rc) {
-                rc = hipGraphInstantiate(&ex, gr, nullptr, nullptr, 0) == hipSuccess ? 0 : -2;
-                (void)hipGraphDestroy(gr);
-            }
-        }
-        g->probe_kind = -1;
-        for (int i = 0; !rc && i < k; i++) {
-            rc = hipGraphLaunch(ex, g->st) == hipSuccess ? 0 : -2;
-            if (!rc) rc = collect();
-        }
-        if (ex) (void)hipGraphExecDestroy(ex);
-        if (rc) return rc;
+    int rc = g->mtp_steps_async(k, false);
+    g->probe_kind = -1;
+    if (rc) return rc;
+    if (hipStreamSynchronize(g->st) != hipSuccess) return -2;
+    if ((rc = g->fused_check())) return rc;
+    double tot = 0.0;
+    int cnt = 0;
+    for (size_t i = 0; i + 1 < g->probe_used; i += 2) {
+        float ms = 0.0f;
+        if (hipEventElapsedTime(&ms, g->probe_ev[i], g->probe_ev[i + 1]) != hipSuccess) return -2;
+        tot += ms;
+        cnt++;
     }
     *avg_us = cnt ? (float)(tot * 1000.0 / cnt) : 0.0f;
     *n = cnt;

@@ -14,6 +14,7 @@
 #include "../../include/oxe_amd.h"
 #include "oxe_engine.h"
 #include "oxe_kernels.h"
+#include "oxe_fused.h"
 #include "oxe_model_kernels.h"
 #include "oxe_shape.h"
 
@@ -72,6 +73,20 @@ struct Engine {
     int32_t *force_d1 = nullptr;
     int force_n = 0;
     hipGraphExec_t graph_exec = nullptr;
+    // fused run kernel (one persistent launch per run) when the device supports it
+    bool fused = false, fused_ok = false;
+    int fz_grid = 0;
+    size_t fz_lds = 0;
+    uint32_t *fz_sync = nullptr;
+    int8_t *fz_hq = nullptr;
+    uint16_t *fz_hd = nullptr;
+    unsigned long long *fz_keys = nullptr;
+    LayerDev *fz_layers = nullptr;
+    FusedArgs *fz_args = nullptr;   // [3]: verify, draft, seed
+    unsigned long long *fz_trace = nullptr;
+    FusedArgs fz_host[3];
+    const unsigned long long *keys() const { return fused ? fz_keys : b.amax_key; }
+    int nkeys() const { return fused ? fz_grid : 1; }
     // kernel probe: HIP events around every launch of one kernel kind while enqueuing eagerly
     int probe_kind = -1;
     std::vector<hipEvent_t> probe_ev;
@@ -258,8 +273,106 @@ struct Engine {
         for (int p = 0; p < m.n_ctx; p++) mrope_cache(p, rope.data() + (size_t)p * NROT);
         (void)hipMemcpyAsync(m.rope, rope.data(), rope.size() * 4, hipMemcpyHostToDevice, st);
         (void)hipStreamSynchronize(st);
-        // the attention pv kernel keeps the group's probabilities in LDS: allow up to 160 KB
         if (hipGetLastError() != hipSuccess) throw std::runtime_error("HIP error during engine creation");
+        fused_init();
+    }
+
+    // The fused run kernel needs one workgroup per CU on exactly 256 CUs (its row splits assume
+    // 256 workgroups) with every workgroup resident.
+    void fused_init() {
+        int dev = 0, ncu = 0;
+        if (hipGetDevice(&dev) != hipSuccess) return;
+        if (hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return;
+        fz_lds = fused_lds_bytes(m.n_ctx);
+        if (ncu != 256 || fused_blocks_per_cu(fz_lds) < 1) return;
+        fz_grid = ncu;
+        fz_sync = alloc<uint32_t>(FZ_SYNC_WORDS);
+        fz_hq = alloc<int8_t>((size_t)OXE_NL * OXE_MAX_UNION * FF);
+        fz_hd = alloc<uint16_t>((size_t)OXE_NL * OXE_MAX_UNION * (FF / 32));
+        fz_keys = alloc<unsigned long long>((size_t)OXE_NL * fz_grid);
+        const int nl_total = d.n_layer + 1;
+        std::vector<LayerDev> ld(nl_total);
+        for (int il = 0; il < nl_total; il++) {
+            const LayerW &w = L[il];
+            LayerDev &x = ld[il];
+            x.att = w.att;
+            x.index = w.index;
+            x.attn_norm = w.attn_norm; x.post_norm = w.post_norm;
+            x.proj = w.proj; x.out = w.out;
+            x.conv = w.conv; x.ssm_a = w.ssm_a; x.dt_bias = w.dt_bias; x.ssm_norm = w.ssm_norm;
+            x.q_norm = w.q_norm; x.k_norm = w.k_norm;
+            x.router = w.router; x.shexp_gate = w.shexp_gate;
+            x.shexp_gu = w.shexp_gu; x.shexp_down = w.shexp_down; x.exp_gu = w.exp_gu; x.exp_down = w.exp_down;
+            x.eh_proj = w.eh_proj;
+            x.enorm = w.enorm; x.hnorm = w.hnorm; x.head_norm = w.head_norm;
+        }
+        fz_layers = alloc<LayerDev>(nl_total);
+        fz_args = alloc<FusedArgs>(3);
+        FusedArgs fa[3];
+        for (int mode = 0; mode < 3; mode++) {
+            FusedArgs &f = fa[mode];
+            f = FusedArgs{};
+            f.mode = mode;
+            f.n_layer = d.n_layer;
+            f.keep_logits = (mode == FM_VERIFY && keep_logits) ? 1 : 0;   // the MTP head keeps no logits
+            f.grid = fz_grid;
+            f.layers = fz_layers;
+            f.m = m;
+            f.b = b;
+            f.sync = fz_sync;
+            f.hq = fz_hq;
+            f.hd = fz_hd;
+            f.keys = fz_keys;
+        }
+        (void)hipMemsetAsync(fz_sync, 0, FZ_SYNC_WORDS * 4, st);
+        (void)hipMemsetAsync(fz_keys, 0, (size_t)OXE_NL * fz_grid * 8, st);
+        (void)hipMemcpyAsync(fz_layers, ld.data(), sizeof(LayerDev) * nl_total, hipMemcpyHostToDevice, st);
+        for (int mode = 0; mode < 3; mode++) fz_host[mode] = fa[mode];
+        (void)hipMemcpyAsync(fz_args, fa, sizeof(fa), hipMemcpyHostToDevice, st);
+        if (hipStreamSynchronize(st) != hipSuccess || hipGetLastError() != hipSuccess) return;
+        fused_ok = true;
+        fused = true;
+    }
+    int set_fused(bool on) {
+        if (on && !fused_ok) return -1;
+        if (on != fused) {
+            fused = on;
+            if (graph_exec) {
+                (void)hipGraphExecDestroy(graph_exec);
+                graph_exec = nullptr;
+            }
+        }
+        return 0;
+    }
+    // phase trace of the fused kernel: [grid][FZ_TRACE_EV][4] (phase id, start, barrier passed, end)
+    int set_trace(bool on) {
+        if (!fused_ok) return -1;
+        if (on && !fz_trace) {
+            try {
+                fz_trace = alloc<unsigned long long>((size_t)fz_grid * FZ_TRACE_EV * 4);
+            } catch (...) {
+                return -3;
+            }
+        }
+        for (int mode = 0; mode < 3; mode++) fz_host[mode].trace = on ? fz_trace : nullptr;
+        if (on) (void)hipMemsetAsync(fz_trace, 0, (size_t)fz_grid * FZ_TRACE_EV * 32, st);
+        if (hipMemcpyAsync(fz_args, fz_host, sizeof(fz_host), hipMemcpyHostToDevice, st) != hipSuccess) return -2;
+        return hipStreamSynchronize(st) == hipSuccess ? 0 : -2;
+    }
+    // after a run of the fused kernel was aborted (a barrier that never completed): reset the
+    // barrier words and report
+    int fused_check() {
+        if (!fused) return 0;
+        uint32_t err = 0;
+        if (hipMemcpyAsync(&err, fz_sync + FZ_W_ERR, 4, hipMemcpyDeviceToHost, st) != hipSuccess) return -2;
+        if (hipStreamSynchronize(st) != hipSuccess) return -2;
+        if (err) {
+            launch_fused_sync_reset(fz_sync, st);
+            (void)hipStreamSynchronize(st);
+            set_err("fused run aborted at a grid barrier (barrier words reset)");
+            return -4;
+        }
+        return 0;
     }
 
     // ggml_mrope_cache_init for a text position (IMRoPE sections, ext_factor 0, freq_scale 1)
@@ -337,7 +450,8 @@ struct Engine {
     }
 
     // ---- run sequences (device-side lanes/positions from RunCtl) ----
-    enum { K_HEAD = 0, K_EXPERTS = 1, K_DOWN = 2, K_PROJ = 3, K_OUT = 4, K_DN = 5, K_ROUTER = 6, K_SCORES = 7, K_PV = 8, K_ENTRY = 9 };
+    enum { K_HEAD = 0, K_EXPERTS = 1, K_DOWN = 2, K_PROJ = 3, K_OUT = 4, K_DN = 5, K_ROUTER = 6, K_SCORES = 7, K_PV = 8, K_ENTRY = 9,
+           K_FUSED = 10, K_FUSED_DRAFT = 11 };
     void enqueue_layer(int l, bool first) {
         const LayerW &w = L[l];
         const float *x = first ? b.x : b.x2;
@@ -359,10 +473,22 @@ struct Engine {
         probe(K_DOWN); launch_down(ctl, w, b, st); probe(K_DOWN);
     }
     void enqueue_verify() {
+        if (fused) {
+            probe(K_FUSED);
+            launch_fused(ctl, fz_args + FM_VERIFY, fz_grid, fz_lds, st);
+            probe(K_FUSED);
+            return;
+        }
         for (int l = 0; l < d.n_layer; l++) enqueue_layer(l, l == 0);
         probe(K_HEAD); launch_head(ctl, m, m.out_norm, b, keep_logits, st); probe(K_HEAD);
     }
     void enqueue_mtp_run() {
+        if (fused) {
+            probe(K_FUSED_DRAFT);
+            launch_fused(ctl, fz_args + FM_DRAFT, fz_grid, fz_lds, st);
+            probe(K_FUSED_DRAFT);
+            return;
+        }
         const LayerW &w = L[d.n_layer];
         probe(K_ENTRY); launch_entry(ctl, m, w, b, st); probe(K_ENTRY);
         // the MTP layer: input x2 (the entry output), as any layer > 0
@@ -375,6 +501,10 @@ struct Engine {
         probe(K_HEAD); launch_head(ctl, m, w.head_norm, b, false, st); probe(K_HEAD);
     }
     void enqueue_mtp_seed() {
+        if (fused) {
+            launch_fused(ctl, fz_args + FM_SEED, fz_grid, fz_lds, st);
+            return;
+        }
         const LayerW &w = L[d.n_layer];
         launch_entry(ctl, m, w, b, st);
         launch_proj(ctl, m, w, b.x2, false, nullptr, b, st, AT_K);  // K and V rows only
@@ -383,10 +513,16 @@ struct Engine {
 
     // ---- host-driven API (mirrors Engine::{verify, commit, mtp_run, mtp_seed}) ----
     int read_argmax(uint32_t *out, int n) {
-        unsigned long long keys[OXE_NL];
-        if (hipMemcpyAsync(keys, b.amax_key, sizeof(keys), hipMemcpyDeviceToHost, st) != hipSuccess) return -2;
+        const int nk = nkeys();
+        std::vector<unsigned long long> k((size_t)OXE_NL * nk);
+        if (hipMemcpyAsync(k.data(), keys(), k.size() * 8, hipMemcpyDeviceToHost, st) != hipSuccess) return -2;
         if (hipStreamSynchronize(st) != hipSuccess) return -2;
-        for (int i = 0; i < n; i++) out[i] = keys[i] == 0 ? 0u : 0xffffffffu - (uint32_t)(keys[i] & 0xffffffffu);
+        if (int rc = fused_check()) return rc;
+        for (int i = 0; i < n; i++) {
+            unsigned long long best = 0ull;
+            for (int j = 0; j < nk; j++) best = k[(size_t)i * nk + j] > best ? k[(size_t)i * nk + j] : best;
+            out[i] = best == 0 ? 0u : 0xffffffffu - (uint32_t)(best & 0xffffffffu);
+        }
         return 0;
     }
     RunCtl run(int nl, int pos0, const uint32_t *toks, int head_mask) const {
@@ -447,7 +583,8 @@ struct Engine {
         if (set_hidden(hs, n)) return -2;
         launch_set_run(ctl, run(n, pos0, toks, 0), st);
         enqueue_mtp_seed();
-        return hipStreamSynchronize(st) == hipSuccess ? 0 : -2;
+        if (hipStreamSynchronize(st) != hipSuccess) return -2;
+        return fused_check();
     }
 };
 

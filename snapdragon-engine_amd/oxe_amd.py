@@ -123,6 +123,10 @@ def _engine_sigs(L):
         "oxe_mtp_prefill": (i32, [vp, u32p, i32, u32p]),
         "oxe_mtp_step": (i32, [vp, C.c_uint32, u32p, C.POINTER(C.c_int), i64]),
         "oxe_mtp_step_plain": (i32, [vp, C.c_uint32, u32p]),
+        "oxe_engine_set_fused": (i32, [vp, i32]),
+        "oxe_engine_fused": (i32, [vp]),
+        "oxe_engine_set_trace": (i32, [vp, i32]),
+        "oxe_engine_read_trace": (i64, [vp, vp, i64]),
         "oxe_mtp_rewind": (i32, [vp, i32]),
         "oxe_mtp_device_begin": (i32, [vp, C.c_uint32, i32]),
         "oxe_mtp_device_steps": (i32, [vp, i32, i32]),
@@ -130,7 +134,7 @@ def _engine_sigs(L):
         "oxe_mtp_set_force": (i32, [vp, C.POINTER(C.c_int32), i32]),
         "oxe_mtp_stats": (i32, [vp, C.POINTER(C.c_int64)]),
         "oxe_engine_sync": (i32, [vp]),
-        "oxe_mtp_device_probe": (i32, [vp, i32, i32, i32, C.POINTER(C.c_float), C.POINTER(C.c_int)]),
+        "oxe_mtp_device_probe": (i32, [vp, i32, i32, C.POINTER(C.c_float), C.POINTER(C.c_int)]),
         "oxe_engine_stream": (vp, [vp]),
     }
     for name, (res, args) in sig.items():
@@ -252,6 +256,26 @@ class Engine:
         check(lib().oxe_mtp_step(self.h, x, _np_ptr(out, C.c_uint32), C.byref(n), override_d1), "mtp_step")
         return [int(v) for v in out[: n.value]]
 
+    def set_fused(self, on):
+        """1: each run is one persistent fused launch; 0: one launch per phase (same bits)."""
+        check(lib().oxe_engine_set_fused(self.h, int(on)), "set_fused")
+
+    @property
+    def fused(self):
+        return bool(lib().oxe_engine_fused(self.h))
+
+    def set_trace(self, on):
+        check(lib().oxe_engine_set_trace(self.h, int(on)), "set_trace")
+
+    def read_trace(self):
+        """Last fused run's phase records: array [grid, 512, 4] (phase id, start, passed, end), 100 MHz ticks."""
+        import numpy as np
+        buf = np.zeros(256 * 512 * 4, np.uint64)
+        n = lib().oxe_engine_read_trace(self.h, buf.ctypes.data_as(C.c_void_p), buf.size)
+        if n < 0:
+            raise RuntimeError("read_trace failed")
+        return buf[:n].reshape(-1, 512, 4)
+
     def mtp_step_plain(self, x):
         out = (C.c_uint32 * 1)()
         check(lib().oxe_mtp_step_plain(self.h, x, out), "mtp_step_plain")
@@ -286,10 +310,10 @@ class Engine:
         lib().oxe_mtp_stats(self.h, s.ctypes.data_as(C.POINTER(C.c_int64)))
         return dict(steps=int(s[0]), accepted=int(s[1]))
 
-    def mtp_device_probe(self, k, kind, use_graph=True):
+    def mtp_device_probe(self, k, kind):
         avg = C.c_float(0)
         n = C.c_int(0)
-        check(lib().oxe_mtp_device_probe(self.h, k, kind, int(use_graph), C.byref(avg), C.byref(n)), "mtp_device_probe")
+        check(lib().oxe_mtp_device_probe(self.h, k, kind, C.byref(avg), C.byref(n)), "mtp_device_probe")
         return float(avg.value), int(n.value)
 
     def sync(self):

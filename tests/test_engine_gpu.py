@@ -11,11 +11,17 @@ pytestmark = pytest.mark.gpu
 N_CTX = 512
 
 
-@pytest.fixture(scope="module")
-def small():
+@pytest.fixture(scope="module", params=["fused", "per_phase"])
+def small(request):
+    """Both run modes: one persistent fused launch per run, and one launch per phase."""
     import oxe_amd as A
     d = O.desc_small()
-    return d, A.Engine(d, seed=3, n_ctx=N_CTX), O.Engine(d, seed=3, n_ctx=N_CTX)
+    g = A.Engine(d, seed=3, n_ctx=N_CTX)
+    if request.param == "per_phase":
+        g.set_fused(False)
+    elif not g.fused:
+        pytest.skip("the fused run kernel needs a 256-CU device")
+    return d, g, O.Engine(d, seed=3, n_ctx=N_CTX)
 
 
 def bits(a):

@@ -37,6 +37,22 @@ def forced_drafts(plain, pattern):
     return forces
 
 
+@pytest.fixture(params=["fused", "per_phase"])
+def mode(request):
+    return request.param
+
+
+def engine(d, mode):
+    """A device engine in the given run mode (fused: one persistent launch per run)."""
+    import oxe_amd as A
+    g = A.Engine(d, seed=SEED, n_ctx=N_CTX)
+    if mode == "per_phase":
+        g.set_fused(False)
+    elif not g.fused:
+        pytest.skip("the fused run kernel needs a 256-CU device")
+    return g
+
+
 @pytest.fixture(scope="module")
 def setup():
     d = O.desc_small()
@@ -46,10 +62,9 @@ def setup():
     return d, prompt, pattern, plain, forced_drafts(plain, pattern)
 
 
-def test_host_driver_matches_oracle_and_plain_greedy(setup):
-    import oxe_amd as A
+def test_host_driver_matches_oracle_and_plain_greedy(setup, mode):
     d, prompt, pattern, plain, forces = setup
-    g = A.Engine(d, seed=SEED, n_ctx=N_CTX)
+    g = engine(d, mode)
     o = O.Engine(d, seed=SEED, n_ctx=N_CTX)
     od = O.Driver(o)
     xg, xo = g.mtp_prefill(prompt), od.prefill(prompt)
@@ -66,10 +81,9 @@ def test_host_driver_matches_oracle_and_plain_greedy(setup):
     assert g.pos == o.pos
 
 
-def test_device_driver_matches_host_driver(setup):
-    import oxe_amd as A
+def test_device_driver_matches_host_driver(setup, mode):
     d, prompt, pattern, plain, forces = setup
-    g = A.Engine(d, seed=SEED, n_ctx=N_CTX)
+    g = engine(d, mode)
     x = g.mtp_prefill(prompt)
     g.mtp_set_force(forces)
     g.mtp_device_begin(x, 64)
@@ -83,13 +97,12 @@ def test_device_driver_matches_host_driver(setup):
     assert r == plain[1 + len(toks): 1 + len(toks) + len(r)]
 
 
-def test_device_driver_natural_drafts_equal_plain(setup):
+def test_device_driver_natural_drafts_equal_plain(setup, mode):
     """No forced drafts (random weights: drafts are nearly always rejected); eager and graph agree."""
-    import oxe_amd as A
     d, prompt, pattern, plain, forces = setup
     outs = []
     for use_graph in (False, True):
-        g = A.Engine(d, seed=SEED, n_ctx=N_CTX)
+        g = engine(d, mode)
         x = g.mtp_prefill(prompt)
         g.mtp_device_begin(x, 64)
         g.mtp_device_steps(6, use_graph=use_graph)
