@@ -26,6 +26,7 @@ using namespace shp;
 namespace fz {
 
 constexpr int FT = 512;                       // threads per workgroup
+constexpr int SC_P = FT / 8;                  // positions per scores workgroup (4 threads per position and lane)
 constexpr uint32_t SPIN_MAX = 400000;         // ~0.4 s at one device-scope load per iteration
 
 // ---- device-scope accesses for data exchanged inside the launch -----------------------------
@@ -156,7 +157,7 @@ OXE_DEV void wdot(const WSlice<K, MAXP> &s, int nr, const int8_t *xq, int xq_ld,
 #pragma unroll
         for (int l = 0; l < NL; l++) {
             int32_t v = dot16(s.w[p], xa[l], 0);
-            v += shfl_xor_i(v, 1);  // the other half of the 32-code block sits in the adjacent lane
+            v += dpp_i<DPP_XOR1>(v);  // the other half of the 32-code block sits in the adjacent lane
             if ((c & 1) == 0 && rl < nr) g.isum[l][rl][c >> 1] = v;
         }
     }
@@ -173,19 +174,40 @@ OXE_DEV void wdot(const WSlice<K, MAXP> &s, int nr, const int8_t *xq, int xq_ld,
     __syncthreads();
 }
 
+// ---- cache warm-up -----------------------------------------------------------------------------
+// Workgroups with no work in a latency-bound phase read part `part` of `nparts` of a byte range the
+// next phase will stream, so it is served from the device's last-level (memory-side) cache. The
+// values are folded into one word that is stored (to an unused word) only when it equals an
+// arbitrary constant, which keeps the loads.
+OXE_DEV void warm(const void *base, size_t bytes, int part, int nparts, uint32_t *sink) {
+    const uint4 *p = (const uint4 *)base;
+    const size_t n16 = bytes / 16;
+    const size_t b0 = n16 * (size_t)part / nparts, b1 = n16 * (size_t)(part + 1) / nparts;
+    uint32_t x = 0;
+    for (size_t i = b0 + threadIdx.x; i < b1; i += 8 * FT) {
+        uint4 v[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) v[k] = i + (size_t)k * FT < b1 ? p[i + (size_t)k * FT] : make_uint4(0, 0, 0, 0);
+#pragma unroll
+        for (int k = 0; k < 8; k++) x ^= v[k].x ^ v[k].y ^ v[k].z ^ v[k].w;
+    }
+    if (x == 0x9e3779b9u) *sink = x;
+}
+
 // ---- norm prologue (oxe_rms_norm_mul_f32, oxe_ops.cpp:32-42), lane l on threads [256 l, 256 l + 256)
 struct NormSm {
     double red[2][4];
     float bc[2];
 };
 
-// v: this thread's 8 elements; xs: the lane's whole vector in LDS (sequential replay). All threads call.
-OXE_DEV void norm8(float v[8], const float *xs, const float *w, float eps, NormSm &ns) {
+// v: this thread's 8 elements; xs: the lane's whole vector in LDS (sequential replay); wv8: this
+// thread's 8 weights (loaded ahead by the caller). All threads call.
+OXE_DEV void norm8(float v[8], const float *xs, const float wv8[8], float eps, NormSm &ns) {
     const int t = threadIdx.x, h = (t >> 8) & 1, tt = t & 255, wv = (t >> 6) & 3;
-    double p = 0.0;
+    double q = 0.0;
 #pragma unroll
-    for (int i = 0; i < 8; i++) p += (double)(v[i] * v[i]);
-    for (int m = 32; m >= 1; m >>= 1) p += shfl_xor_d(p, m);
+    for (int i = 0; i < 8; i++) q += (double)(v[i] * v[i]);
+    const double p = wave_sum_d_any(q);
     if ((t & 63) == 0) ns.red[h][wv] = p;
     __syncthreads();
     const double P = ((ns.red[h][0] + ns.red[h][1]) + ns.red[h][2]) + ns.red[h][3];
@@ -199,10 +221,20 @@ OXE_DEV void norm8(float v[8], const float *xs, const float *w, float eps, NormS
     __syncthreads();
     if (!ok) mean = ns.bc[h];
     const float scale = 1.0f / sqrtf(mean + eps);
-    const float4 w0 = *(const float4 *)(w + 8 * tt), w1 = *(const float4 *)(w + 8 * tt + 4);
-    const float wv8[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
 #pragma unroll
     for (int i = 0; i < 8; i++) v[i] = (v[i] * scale) * wv8[i];
+}
+
+// this thread's 8 norm weights (elements [8 tt, 8 tt + 8) of w)
+struct W8 {
+    float v[8];
+};
+OXE_DEV W8 wload8(const float *w) {
+    W8 r;
+    const int tt = threadIdx.x & 255;
+    const float4 a = *(const float4 *)(w + 8 * tt), b = *(const float4 *)(w + 8 * tt + 4);
+    r.v[0] = a.x; r.v[1] = a.y; r.v[2] = a.z; r.v[3] = a.w; r.v[4] = b.x; r.v[5] = b.y; r.v[6] = b.z; r.v[7] = b.w;
+    return r;
 }
 
 OXE_DEV void put8(float *x, const float *v) {
@@ -215,7 +247,11 @@ OXE_DEV void get8(const float *x, float v[8]) {
 }
 OXE_DEV void cget8(const float *x, float v[8]) {
 #pragma unroll
-    for (int i = 0; i < 8; i++) v[i] = cld(x + i);
+    for (int i = 0; i < 4; i++) {
+        const unsigned long long u = cld64(x + 2 * i);
+        v[2 * i] = __builtin_bit_cast(float, (uint32_t)u);
+        v[2 * i + 1] = __builtin_bit_cast(float, (uint32_t)(u >> 32));
+    }
 }
 // dequantize_row_q8_0 (quants_base.c:64-78) of elements [8 tt, 8 tt + 8) of token row tok
 OXE_DEV void embed8t(const Q8W &emb, uint32_t tok, int tt, float v[8]) {
@@ -234,7 +270,7 @@ OXE_DEV void embed8t(const Q8W &emb, uint32_t tok, int tt, float v[8]) {
 // xf: LDS staging of the raw vectors; xn (optional): the normalised f32 vectors.
 template <int NL>
 OXE_DEV void prologue(int nl, const RunCtl *ctl, const Q8W *emb, const float *src, int64_t src_ld, bool coherent,
-                      const float *w, float eps, float (*xf)[E], int8_t *xq, int xq_ld, uint16_t *xd, int xd_ld,
+                      const W8 &w, float eps, float (*xf)[E], int8_t *xq, int xq_ld, uint16_t *xd, int xd_ld,
                       NormSm &ns, float (*xn)[E]) {
     const int t = threadIdx.x, l = t >> 8, tt = t & 255;
     float v[8];
@@ -249,7 +285,7 @@ OXE_DEV void prologue(int nl, const RunCtl *ctl, const Q8W *emb, const float *sr
     }
     if (l < NL) put8(&xf[l][8 * tt], v);
     __syncthreads();
-    norm8(v, xf[l < NL ? l : 0], w, eps, ns);
+    norm8(v, xf[l < NL ? l : 0], w.v, eps, ns);
     if (l < NL) {
         if (act) {
             quant8(v, xq + l * xq_ld + 8 * tt, xd + l * xd_ld + (8 * tt) / 32);
@@ -290,8 +326,9 @@ struct RouterSm {
     alignas(16) int8_t xq[NL][E];
     uint16_t xd[NL][E / 32];
     NormSm ns;
-    alignas(16) float w[E];
-    alignas(16) float sg[E];
+    alignas(16) float w[16][E / 16 + 4];    // chain-major: w[c][q] = row[c + 16 q]
+    alignas(16) float sg[16][E / 16 + 4];
+    alignas(16) float xc[NL][16][E / 16 + 4];
     GSm<E, 8, NL> g;
 };
 template <int NL>
@@ -320,6 +357,7 @@ struct ScSm {
     float tmp[NL * GQA][HD];
     float ktmp[NL][HD];
     alignas(16) uint16_t knew[NL][HD];
+    alignas(16) uint16_t krows[SC_P][HD];   // cached K rows of the workgroup's positions (DMA-loaded)
 };
 template <int NL>
 struct HeadSm {
@@ -362,7 +400,7 @@ struct Persist {
     int ok;
     uint32_t round;
     uint32_t tev;                    // trace: next event index of this workgroup
-    unsigned long long t_start, t_pass;
+    unsigned long long t_start, t_pass, t_mark;
 };
 
 }  // namespace fz
@@ -405,7 +443,7 @@ OXE_DEV void tr_start(Ctx<NL> &c) {
 }
 template <int NL>
 OXE_DEV void tr_pass(Ctx<NL> &c) {
-    if (c.a->trace && threadIdx.x == 0) c.ps->t_pass = wall_clock64();
+    if (c.a->trace && threadIdx.x == 0) c.ps->t_mark = c.ps->t_pass = wall_clock64();
 }
 // sub-step marker inside a phase: an event (id, previous mark, 0, now)
 template <int NL>
@@ -414,10 +452,10 @@ OXE_DEV void tr_mark(Ctx<NL> &c, int id) {
         const unsigned long long now = wall_clock64();
         unsigned long long *e = c.a->trace + ((size_t)c.b * FZ_TRACE_EV + c.ps->tev++) * 4;
         e[0] = (unsigned long long)id;
-        e[1] = c.ps->t_pass;
+        e[1] = c.ps->t_mark;
         e[2] = 0ull;
         e[3] = now;
-        c.ps->t_pass = now;
+        c.ps->t_mark = now;
     }
 }
 template <int NL>
@@ -447,9 +485,10 @@ FZ_PHASE bool phase_proj(const RunCtl *ctl, const FusedArgs *ap, int il, bool em
     const int nr = r1 - r0;
     WSlice<E, 13> ws;
     wload<E, 13>(ws, L.proj.q, L.proj.d, nr, [&](int rl) { return (int64_t)(r0 + rl); });
+    const W8 nw = wload8(L.attn_norm);
     if (!wait(c.bar, &c.ps->ok)) return false;
     tr_pass(c);
-    prologue<NL>(c.nl, c.ctl, embed ? &a.m.tok_embd : nullptr, x, E, true, L.attn_norm, a.m.eps, s.xf, &s.xq[0][0], E,
+    prologue<NL>(c.nl, c.ctl, embed ? &a.m.tok_embd : nullptr, x, E, true, nw, a.m.eps, s.xf, &s.xq[0][0], E,
                  &s.xd[0][0], E / 32, s.ns, nullptr);
     tr_mark(c, 111);
     if (embed && c.b == 0) {
@@ -480,13 +519,7 @@ FZ_PHASE bool phase_proj(const RunCtl *ctl, const FusedArgs *ap, int il, bool em
 
 // delta-net recurrence, one value head per workgroup b < 32 (k_layer.hip dn_kernel with 512
 // threads: thread (rg = t/16, c = t%16) owns state rows rg + 32 h, h < 4)
-OXE_DEV float dot16_tree_f(float acc) {
-    acc = acc + shfl_xor_f(acc, 8);
-    acc = acc + shfl_xor_f(acc, 4);
-    acc = acc + shfl_xor_f(acc, 1);
-    acc = acc + shfl_xor_f(acc, 2);
-    return acc;
-}
+OXE_DEV float dot16_tree_f(float acc) { return dot16_tree_dpp(acc); }
 OXE_DEV float conv4f(float s0, float s1, float s2, float xn, const float *c) {
     const float p0 = s0 * c[0], p1 = s1 * c[1], p2 = s2 * c[2], p3 = xn * c[3];
     float sumf = 0.0f;
@@ -521,19 +554,36 @@ FZ_PHASE bool phase_dn(const RunCtl *ctl, const FusedArgs *ap, int il) {
             for (int q = 0; q < 8; q++) r[h][q] = src[cc + 16 * q];
         }
     }
+    // this thread's conv channel: state (slot cur, an earlier launch) and weights, loaded ahead
+    int ch = 0;
+    bool writer = false;
+    if (t < DS) { ch = kh * DS + t; writer = vh < NKH; }
+    else if (t < 2 * DS) { ch = NKH * DS + kh * DS + (t - DS); writer = vh < NKH; }
+    else { ch = 2 * NKH * DS + vh * HV + (t - 2 * DS); writer = true; }
+    float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f;
+    float cw[KC] = {0.0f, 0.0f, 0.0f, 0.0f};
+    float dtb = 0.0f, sa = 0.0f;
+    if (worker && t < 3 * DS) {
+        const float *st = conv_state + (int64_t)cur * conv_slot + (int64_t)ch * (KC - 1);
+        s0 = st[0]; s1 = st[1]; s2 = st[2];
+        const float4 c4 = *(const float4 *)(L.conv + (int64_t)ch * KC);
+        cw[0] = c4.x; cw[1] = c4.y; cw[2] = c4.z; cw[3] = c4.w;
+    }
+    if (worker) {
+        dtb = L.dt_bias[vh];
+        sa = L.ssm_a[vh];
+    }
     if (!wait(c.bar, &c.ps->ok)) return false;
     tr_pass(c);
+    if (!worker && il + 1 < a.n_layer) {
+        const LayerDev &N = a.layers[il + 1];
+        const int64_t rows = N.att ? AT_ROWS : DN_ROWS;
+        warm(N.proj.q, (size_t)rows * E, c.b - NVH, c.G - NVH, a.sync + FZ_W_ERR + 32);
+        warm(N.proj.d, (size_t)rows * (E / 32) * 2, c.b - NVH, c.G - NVH, a.sync + FZ_W_ERR + 32);
+    }
     if (worker) {
         const int nl = c.nl;
         if (t < 3 * DS) {
-            int ch;
-            bool writer;
-            if (t < DS) { ch = kh * DS + t; writer = vh < NKH; }
-            else if (t < 2 * DS) { ch = NKH * DS + kh * DS + (t - DS); writer = vh < NKH; }
-            else { ch = 2 * NKH * DS + vh * HV + (t - 2 * DS); writer = true; }
-            const float *cw = L.conv + (int64_t)ch * KC;
-            const float *st = conv_state + (int64_t)cur * conv_slot + (int64_t)ch * (KC - 1);
-            float s0 = st[0], s1 = st[1], s2 = st[2];
             for (int l = 0; l < nl; l++) {
                 const float xn = cld(a.b.proj + (int64_t)l * DN_ROWS + ch);
                 const float y = v_silu(conv4f(s0, s1, s2, xn, cw));
@@ -563,8 +613,8 @@ FZ_PHASE bool phase_dn(const RunCtl *ctl, const FusedArgs *ap, int il) {
                 xv[lane + 64] = (a1 * scale) * s2;
             }
             if (w == 2 * NL && lane < nl) {
-                const float ab = cld(a.b.proj + (int64_t)lane * DN_ROWS + DN_ALPHA + vh) + L.dt_bias[vh];
-                s.g[lane] = oxe_libm::expf_c(softplus_c(ab) * L.ssm_a[vh]);
+                const float ab = cld(a.b.proj + (int64_t)lane * DN_ROWS + DN_ALPHA + vh) + dtb;
+                s.g[lane] = oxe_libm::expf_c(softplus_c(ab) * sa);
                 s.b[lane] = sigmoid_c(cld(a.b.proj + (int64_t)lane * DN_ROWS + DN_BETA + vh));
             }
         }
@@ -700,11 +750,20 @@ FZ_PHASE bool phase_router(const RunCtl *ctl, const FusedArgs *ap, int il) {
     WSlice<E, 2> ws;
     auto rowof = [&](int rl) { return (int64_t)(tile * 16 + (rl < 4 ? hf * 4 + rl : 8 + hf * 4 + (rl - 4))); };
     wload<E, 2>(ws, L.shexp_gu.q, L.shexp_gu.d, gu ? 8 : 0, rowof);
+    const W8 nw = wload8(L.post_norm);
     if (!wait(c.bar, &c.ps->ok)) return false;
     tr_pass(c);
-    *(float4 *)&s.w[4 * t] = wrow;
-    if (shg) *(float4 *)&s.sg[4 * t] = wsg;
-    prologue<NL>(c.nl, c.ctl, nullptr, a.b.x1, E, true, L.post_norm, a.m.eps, s.xf, &s.xq[0][0], E, &s.xd[0][0], E / 32,
+    {
+        // element e = 4 t + k goes to chain e % 16, step e / 16
+        const float wr[4] = {wrow.x, wrow.y, wrow.z, wrow.w}, gr[4] = {wsg.x, wsg.y, wsg.z, wsg.w};
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const int e = 4 * t + k;
+            s.w[e % 16][e / 16] = wr[k];
+            if (shg) s.sg[e % 16][e / 16] = gr[k];
+        }
+    }
+    prologue<NL>(c.nl, c.ctl, nullptr, a.b.x1, E, true, nw, a.m.eps, s.xf, &s.xq[0][0], E, &s.xd[0][0], E / 32,
                  s.ns, s.xn);
     tr_mark(c, 131);
     if (b == 0) {
@@ -717,14 +776,33 @@ FZ_PHASE bool phase_router(const RunCtl *ctl, const FusedArgs *ap, int il) {
     }
     // f32 dots: lane c of a 16-lane group runs chain c (elements c + 16 q); xor 8, 4, 1, 2 is the
     // NEON reduction tree (vec.cpp:104-125)
+    {
+        // the normalised lanes, chain-major as well
+        const int l = t >> 8, tt = t & 255;
+        if (l < NL) {
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                const int e = 8 * tt + k;
+                s.xc[l][e % 16][e / 16] = s.xn[l][e];
+            }
+        }
+    }
+    __syncthreads();
     if (t < 64) {
         const int l = (t >> 4) & 1, cc = t & 15;
         const bool sgd = t >= 32;
-        const float *wv = sgd ? s.sg : s.w;
+        const float *wv = sgd ? s.sg[cc] : s.w[cc];
+        const float *xv = s.xc[l][cc];
         float acc = 0.0f;
         if (!sgd || shg) {
-#pragma unroll 8
-            for (int q = 0; q < E / 16; q++) acc = __builtin_fmaf(wv[cc + 16 * q], s.xn[l][cc + 16 * q], acc);
+#pragma unroll 4
+            for (int q = 0; q < E / 16; q += 4) {
+                const float4 w4 = *(const float4 *)(wv + q), x4 = *(const float4 *)(xv + q);
+                acc = __builtin_fmaf(w4.x, x4.x, acc);
+                acc = __builtin_fmaf(w4.y, x4.y, acc);
+                acc = __builtin_fmaf(w4.z, x4.z, acc);
+                acc = __builtin_fmaf(w4.w, x4.w, acc);
+            }
         }
         const float v = dot16_tree_f(acc);
         if (cc == 0 && l < c.nl) {
@@ -759,6 +837,19 @@ FZ_PHASE bool phase_moe(const RunCtl *ctl, const FusedArgs *ap, int il) {
     const int t = threadIdx.x, b = c.b, nl = c.nl;
     if (!wait(c.bar, &ps.ok)) return false;
     tr_pass(c);
+    // the post-norm quantised lanes (published by the router phase) first: their latency overlaps
+    // the routing
+    {
+        const int l = t >> 8, tt = t & 255;
+        if (l < NL) {
+            const unsigned long long v = l < nl ? cld64(a.b.xq + (int64_t)l * 2 * E + 8 * tt) : 0ull;
+            *(uint2 *)&se.xq[l][8 * tt] = make_uint2((uint32_t)v, (uint32_t)(v >> 32));
+        }
+        if (t < NL * (E / 32)) {
+            const int ll = t / (E / 32), bb = t % (E / 32);
+            se.xd[ll][bb] = ll < nl ? cld16(a.b.xd + (int64_t)ll * (2 * E / 32) + bb) : (uint16_t)0;
+        }
+    }
     // 1. routing (engine.rs:3414-3475)
     if (t < NL * NEXP) {
         const int l = t / NEXP, i = t % NEXP;
@@ -808,6 +899,30 @@ FZ_PHASE bool phase_moe(const RunCtl *ctl, const FusedArgs *ap, int il) {
     WSlice<E, 16> ew;
     wload<E, 16>(ew, L.exp_gu.q + (int64_t)e_g * 2 * FF * E, L.exp_gu.d + (int64_t)e_g * 2 * FF * (E / 32), gw ? 64 : 0,
                  [&](int rl) { return (int64_t)(gq * 64 + rl); });
+    tr_mark(c, 102);
+    // 3. gate/up + swiglu + Q8_0 of the group's 32 h values per lane
+    if (gw) {
+        __syncthreads();
+        tr_mark(c, 103);
+        wdot<E, 16, NL>(ew, 64, &se.xq[0][0], E, &se.xd[0][0], E / 32, se.g);
+        tr_mark(c, 104);
+        if (t < NL * 32) {
+            const int l = t / 32, i = t % 32, tl = i >> 3, r = i & 7;
+            se.h[l][i] = v_silu(se.g.out[l][tl * 16 + r]) * se.g.out[l][tl * 16 + 8 + r];
+        }
+        __syncthreads();
+        if (t < NL) quant_block_q8_0(se.h[t], se.hq[t], &se.hd[t]);
+        __syncthreads();
+        if (t < NL * 8) {
+            const int l = t / 8, k = t % 8;
+            if (l < nl) cst32(a.hq + ((int64_t)l * OXE_MAX_UNION + u_g) * FF + gq * 32 + 4 * k, *(const uint32_t *)&se.hq[l][4 * k]);
+        }
+        if (t < nl) cst16(a.hd + ((int64_t)t * OXE_MAX_UNION + u_g) * (FF / 32) + gq, se.hd[t]);
+    }
+    tr_end(c, TP_EXPERTS);
+    tr_start(c);
+    arrive(c.bar);
+    // the down rows of every union expert and the shared expert, in flight across the barrier
     const int r0 = 8 * b;
     const int uh = t >> 8, rr = (t >> 5) & 7, ck = t & 31;
     uint4 dw[9];
@@ -838,40 +953,6 @@ FZ_PHASE bool phase_moe(const RunCtl *ctl, const FusedArgs *ap, int il) {
         }
         dsc = *(const uint4 *)(base + (int64_t)(r0 + srr) * (FF / 32) + shf * 8);
     }
-    tr_mark(c, 102);
-    // 3. gate/up + swiglu + Q8_0 of the group's 32 h values per lane
-    if (gw) {
-        {
-            const int l = t >> 8, tt = t & 255;
-            if (l < NL) {
-                const unsigned long long v = l < nl ? cld64(a.b.xq + (int64_t)l * 2 * E + 8 * tt) : 0ull;
-                *(uint2 *)&se.xq[l][8 * tt] = make_uint2((uint32_t)v, (uint32_t)(v >> 32));
-            }
-            if (t < NL * (E / 32)) {
-                const int ll = t / (E / 32), bb = t % (E / 32);
-                se.xd[ll][bb] = ll < nl ? cld16(a.b.xd + (int64_t)ll * (2 * E / 32) + bb) : (uint16_t)0;
-            }
-        }
-        __syncthreads();
-        tr_mark(c, 103);
-        wdot<E, 16, NL>(ew, 64, &se.xq[0][0], E, &se.xd[0][0], E / 32, se.g);
-        tr_mark(c, 104);
-        if (t < NL * 32) {
-            const int l = t / 32, i = t % 32, tl = i >> 3, r = i & 7;
-            se.h[l][i] = v_silu(se.g.out[l][tl * 16 + r]) * se.g.out[l][tl * 16 + 8 + r];
-        }
-        __syncthreads();
-        if (t < NL) quant_block_q8_0(se.h[t], se.hq[t], &se.hd[t]);
-        __syncthreads();
-        if (t < NL * 8) {
-            const int l = t / 8, k = t % 8;
-            if (l < nl) cst32(a.hq + ((int64_t)l * OXE_MAX_UNION + u_g) * FF + gq * 32 + 4 * k, *(const uint32_t *)&se.hq[l][4 * k]);
-        }
-        if (t < nl) cst16(a.hd + ((int64_t)t * OXE_MAX_UNION + u_g) * (FF / 32) + gq, se.hd[t]);
-    }
-    tr_end(c, TP_EXPERTS);
-    tr_start(c);
-    arrive(c.bar);
     if (!wait(c.bar, &ps.ok)) return false;
     tr_pass(c);
     // 4. down + combine (engine.rs:3542-3624)
@@ -908,7 +989,7 @@ FZ_PHASE bool phase_moe(const RunCtl *ctl, const FusedArgs *ap, int il) {
             for (int l = 0; l < NL; l++) {
                 const uint4 xa = *(const uint4 *)&sd.hq[l][u][16 * ck];
                 int32_t v = dot16(dw[k], xa, 0);
-                v += shfl_xor_i(v, 1);
+                v += dpp_i<DPP_XOR1>(v);
                 if ((ck & 1) == 0) sd.isum[u][l][rr][ck >> 1] = v;
             }
         }
@@ -968,7 +1049,6 @@ OXE_DEV float f16x8_reduce_q(h2t acc[4]) {
     return (t0 + t1) + (t2 + t3);
 }
 
-constexpr int SC_P = FT / 8;   // positions per scores workgroup (4 threads per position and lane)
 
 template <int NL>
 FZ_PHASE bool phase_scores(const RunCtl *ctl, const FusedArgs *ap, int il, bool seed_only) {
@@ -981,6 +1061,20 @@ FZ_PHASE bool phase_scores(const RunCtl *ctl, const FusedArgs *ap, int il, bool 
     const int pos0 = c.ctl->pos0, pmax = pos0 + nl - 1;
     const int kvh = c.b % NKV, chunk = c.b / NKV;
     const bool act = chunk * SC_P <= pmax;
+    // the K rows of this workgroup's cached positions (< pos0) go straight to LDS (one DMA load of
+    // 16 bytes per lane; 64 lanes fill 1 KB contiguous), shared by both lanes of the run
+    const int npre = act && !seed_only ? (pos0 - chunk * SC_P < SC_P ? pos0 - chunk * SC_P : SC_P) : 0;
+    if (npre > 0) {
+        const uint4 *src = (const uint4 *)(kcache_layer(a, L) + ((int64_t)kvh * a.m.n_ctx + chunk * SC_P) * HD);
+#pragma unroll
+        for (int k = 0; k < SC_P * HD / 8 / FT; k++) {
+            const int i = t + FT * k;                 // 16-byte chunk i: position i / 32, part i % 32
+            if (i / (HD / 8) < npre)
+                __builtin_amdgcn_global_load_lds((const void *)(src + i),
+                                                 (__attribute__((address_space(3))) void *)((uint4 *)&s.krows[0][0] + (i - (t & 63))),
+                                                 16, 0, 0);
+        }
+    }
     if (!wait(c.bar, &c.ps->ok)) return false;
     tr_pass(c);
     // step 1: raw K rows of the run's positions in this range, and the raw queries, into LDS
@@ -1062,12 +1156,14 @@ FZ_PHASE bool phase_scores(const RunCtl *ctl, const FusedArgs *ap, int il, bool 
             for (int i = 0; i < 4; i++) s.q[job][lane + 64 * i] = l < nl ? f2h(s.tmp[job][lane + 64 * i]) : (uint16_t)0;
     }
     __syncthreads();
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
     if (act && !seed_only) {
         // thread = (lane l, position p, chain quad j): the 8 heads of the group for one lane
         const int l = t >> 8, tt = t & 255;
         const int p = chunk * SC_P + (tt >> 2), j = tt & 3;
         if (l < nl && p <= pos0 + l) {
-            const uint16_t *krow = p < pos0 ? kcache_layer(a, L) + ((int64_t)kvh * a.m.n_ctx + p) * HD : s.knew[p - pos0];
+            const uint16_t *krow = p < pos0 ? s.krows[p - chunk * SC_P] : s.knew[p - pos0];
             h2t acc[GQA][4];
 #pragma unroll
             for (int q = 0; q < GQA; q++)
@@ -1111,59 +1207,89 @@ FZ_PHASE bool phase_pv(const RunCtl *ctl, const FusedArgs *ap, int il) {
     const int l = (c.b / (HD / PVD)) % NL;
     const int kvh = c.b / ((HD / PVD) * NL);
     const bool act = kvh < NKV && l < nl;
+    // the first V^T chunks of this thread's row that hold only earlier positions, before the barrier
+    constexpr int PV_PRE = 8;
+    uint4 vpre[PV_PRE];
+    const int vj = t & 3, vd = (t >> 2) & (PVD - 1);
+    const int pos0_ = c.ctl->pos0;
+    const uint16_t *vrow_ = a.m.vcache + (int64_t)L.index * NKV * HD * a.m.n_ctx +
+                            (int64_t)(kvh * HD + (dchunk * PVD + vd)) * a.m.n_ctx;
+#pragma unroll
+    for (int k = 0; k < PV_PRE; k++)
+        vpre[k] = (act && 32 * k + 31 < pos0_) ? *(const uint4 *)(vrow_ + 32 * k + 8 * vj) : make_uint4(0, 0, 0, 0);
     if (!wait(c.bar, &c.ps->ok)) return false;
     tr_pass(c);
+    if (!act && c.b >= NKV * NL * (HD / PVD) && il + 1 < a.n_layer) {
+        // idle during the attention: warm the next layer's input projection
+        const LayerDev &N = a.layers[il + 1];
+        const int64_t rows = N.att ? AT_ROWS : DN_ROWS;
+        const int idle0 = NKV * NL * (HD / PVD);
+        warm(N.proj.q, (size_t)rows * E, c.b - idle0, c.G - idle0, a.sync + FZ_W_ERR + 32);
+        warm(N.proj.d, (size_t)rows * (E / 32) * 2, c.b - idle0, c.G - idle0, a.sync + FZ_W_ERR + 32);
+    }
     if (act) {
         const int n_ctx = a.m.n_ctx;
-        uint16_t *s_p = (uint16_t *)c.dyn;                                  // [GQA][n_kv]
-        float *s_e = (float *)(c.dyn + (size_t)GQA * ((n_ctx + 1) & ~1) * 2);   // [n_kv]
-        float *s_gs = s_e + n_ctx;                                           // [n_kv / 4]
-        double *s_red = (double *)(((uintptr_t)(s_gs + n_ctx / 4) + 15) & ~(uintptr_t)15);   // [16]
-        float *s_mx = (float *)(s_red + 16);                                  // [16]
-        float *s_o = s_mx + 16;                                               // [GQA][PVD]
+        uint16_t *s_p = (uint16_t *)c.dyn;                                        // [GQA][n_kv] f16 probabilities
+        float *s_gs = (float *)(c.dyn + (size_t)GQA * ((n_ctx + 1) & ~1) * 2);    // [GQA][n_kv / 4] group sums
+        float *s_o = (float *)(((uintptr_t)(s_gs + (size_t)GQA * (n_ctx / 4)) + 15) & ~(uintptr_t)15);   // [GQA][PVD]
         const int pos = c.ctl->pos0 + l;
         const int pos0 = c.ctl->pos0;
         int n_kv = (pos + 1 + 255) / 256 * 256;
         if (n_kv < 256) n_kv = 256;
         if (n_kv > n_ctx) n_kv = n_ctx;
         const float scale = 1.0f / sqrtf((float)HD);
-        for (int hh = 0; hh < GQA; hh++) {
-            const int h = kvh * GQA + hh;
+        // softmax of head hh = wave w (oxe_soft_max_f32, oxe_ops.cpp:101-115): wp = s * scale
+        // (masked: -inf), max, e = v_expf(wp - max) with group sums (e0 + e1) + (e2 + e3) added in
+        // double, p = f16(e * f32(1 / sum)). Lane k owns groups k, k + 64, ... (4 consecutive positions).
+        {
+            const int hh = t >> 6, lane = t & 63, h = kvh * GQA + hh;
             const float *sc = a.b.scores + ((int64_t)l * NH + h) * n_ctx;
             float mx = -__builtin_inff();
-            for (int i = t; i < n_kv; i += FT) {
-                const float wv = i <= pos ? cld(sc + i) * scale : -__builtin_inff();
-                s_e[i] = wv;
-                mx = (mx > wv) ? mx : wv;
+            for (int g = lane; g < n_kv / 4; g += 64) {
+                const uint4 v = cld128(sc + 4 * g);
+                const float f4[4] = {__builtin_bit_cast(float, v.x), __builtin_bit_cast(float, v.y),
+                                     __builtin_bit_cast(float, v.z), __builtin_bit_cast(float, v.w)};
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    const float wv = 4 * g + k <= pos ? f4[k] * scale : -__builtin_inff();
+                    mx = (mx > wv) ? mx : wv;
+                }
             }
-            mx = block_max_f<FT>(mx, s_mx);
+            mx = wave_max_f(mx);
             double part = 0.0;
-            for (int i0 = 0; i0 < n_kv; i0 += FT) {
-                const int i = i0 + t;
-                const float e = i < n_kv ? v_expf(s_e[i] - mx) : 0.0f;
-                if (i < n_kv) s_e[i] = e;
-                float g = e + shfl_xor_f(e, 1);
-                g = g + shfl_xor_f(g, 2);
-                if ((t & 3) == 0 && i < n_kv) {
-                    s_gs[i >> 2] = g;
-                    part += (double)g;
-                }
+            float *gs = s_gs + (size_t)hh * (n_ctx / 4);
+            for (int g = lane; g < n_kv / 4; g += 64) {
+                const uint4 v = cld128(sc + 4 * g);
+                const float f4[4] = {__builtin_bit_cast(float, v.x), __builtin_bit_cast(float, v.y),
+                                     __builtin_bit_cast(float, v.z), __builtin_bit_cast(float, v.w)};
+                float e[4];
+#pragma unroll
+                for (int k = 0; k < 4; k++) e[k] = v_expf((4 * g + k <= pos ? f4[k] * scale : -__builtin_inff()) - mx);
+                const float gsum = (e[0] + e[1]) + (e[2] + e[3]);
+                gs[g] = gsum;
+                part += (double)gsum;
             }
-            const double P = block_sum_d<FT>(part, s_red);
+            for (int m = 32; m >= 1; m >>= 1) part += shfl_xor_d(part, m);
             float f;
-            if (!bracket_ok_recip(P, P, n_kv / 4, &f)) {
-                if (t == 0) {
-                    double sum = 0.0;
-                    for (int g = 0; g < n_kv / 4; g++) sum += (double)s_gs[g];
-                    s_red[0] = sum;
-                }
-                __syncthreads();
-                f = (float)(1.0 / s_red[0]);
-                __syncthreads();
+            if (!bracket_ok_recip(part, part, n_kv / 4, &f)) {
+                // sequential replay of the group sums in the reference order (wave-local data)
+                double sum = 0.0;
+                for (int g = 0; g < n_kv / 4; g++) sum += (double)gs[g];
+                f = (float)(1.0 / sum);
             }
-            for (int i = t; i < n_kv; i += FT) s_p[hh * n_kv + i] = f2h(s_e[i] * f);
-            __syncthreads();
+            uint16_t *pp = s_p + (size_t)hh * n_kv;
+            for (int g = lane; g < n_kv / 4; g += 64) {
+                const uint4 v = cld128(sc + 4 * g);
+                const float f4[4] = {__builtin_bit_cast(float, v.x), __builtin_bit_cast(float, v.y),
+                                     __builtin_bit_cast(float, v.z), __builtin_bit_cast(float, v.w)};
+                uint16_t q[4];
+#pragma unroll
+                for (int k = 0; k < 4; k++)
+                    q[k] = f2h(v_expf((4 * g + k <= pos ? f4[k] * scale : -__builtin_inff()) - mx) * f);
+                *(uint2 *)(pp + 4 * g) = make_uint2((uint32_t)q[0] | ((uint32_t)q[1] << 16), (uint32_t)q[2] | ((uint32_t)q[3] << 16));
+            }
         }
+        __syncthreads();
         tr_mark(c, 141);
         // V^T . p: thread = (head group hg of 2 heads, dim d, chain quad j)
         const int j = t & 3, d = (t >> 2) & (PVD - 1), hg = t >> 7;
@@ -1174,19 +1300,27 @@ FZ_PHASE bool phase_pv(const RunCtl *ctl, const FusedArgs *ap, int il) {
         for (int q = 0; q < 2; q++)
 #pragma unroll
             for (int i = 0; i < 4; i++) acc[q][i] = h2t{(_Float16)0.0f, (_Float16)0.0f};
-        for (int sx = 0; sx < n_kv / 32; sx++) {
-            // chunks holding a position written in this launch are read device-coherently
-            const uint4 vv = 32 * sx + 31 >= pos0 ? cld128(vrow + 32 * sx + 8 * j) : *(const uint4 *)(vrow + 32 * sx + 8 * j);
-            const h2t v0 = u2h2f(vv.x), v1 = u2h2f(vv.y), v2 = u2h2f(vv.z), v3 = u2h2f(vv.w);
+#define FZ_PV_STEP(SX, VV)                                                                              \
+    do {                                                                                                \
+        const uint4 vv_ = (VV);                                                                         \
+        const h2t v0 = u2h2f(vv_.x), v1 = u2h2f(vv_.y), v2 = u2h2f(vv_.z), v3 = u2h2f(vv_.w);           \
+        _Pragma("unroll") for (int q = 0; q < 2; q++) {                                                 \
+            const uint4 pv = *(const uint4 *)(&s_p[(hg * 2 + q) * n_kv + 32 * (SX) + 8 * j]);           \
+            acc[q][0] = __builtin_elementwise_fma(v0, u2h2f(pv.x), acc[q][0]);                          \
+            acc[q][1] = __builtin_elementwise_fma(v1, u2h2f(pv.y), acc[q][1]);                          \
+            acc[q][2] = __builtin_elementwise_fma(v2, u2h2f(pv.z), acc[q][2]);                          \
+            acc[q][3] = __builtin_elementwise_fma(v3, u2h2f(pv.w), acc[q][3]);                          \
+        }                                                                                               \
+    } while (0)
+        // chunks holding a position written in this launch are read device-coherently
 #pragma unroll
-            for (int q = 0; q < 2; q++) {
-                const uint4 pv = *(const uint4 *)(&s_p[(hg * 2 + q) * n_kv + 32 * sx + 8 * j]);
-                acc[q][0] = __builtin_elementwise_fma(v0, u2h2f(pv.x), acc[q][0]);
-                acc[q][1] = __builtin_elementwise_fma(v1, u2h2f(pv.y), acc[q][1]);
-                acc[q][2] = __builtin_elementwise_fma(v2, u2h2f(pv.z), acc[q][2]);
-                acc[q][3] = __builtin_elementwise_fma(v3, u2h2f(pv.w), acc[q][3]);
-            }
+        for (int sx = 0; sx < PV_PRE; sx++) {
+            if (sx < n_kv / 32) FZ_PV_STEP(sx, 32 * sx + 31 < pos0 ? vpre[sx] : cld128(vrow + 32 * sx + 8 * j));
         }
+#pragma unroll 4
+        for (int sx = PV_PRE; sx < n_kv / 32; sx++)
+            FZ_PV_STEP(sx, 32 * sx + 31 >= pos0 ? cld128(vrow + 32 * sx + 8 * j) : *(const uint4 *)(vrow + 32 * sx + 8 * j));
+#undef FZ_PV_STEP
 #pragma unroll
         for (int q = 0; q < 2; q++) {
             const float out = f16x8_reduce_q(acc[q]);
@@ -1224,8 +1358,9 @@ FZ_PHASE bool phase_entry(const RunCtl *ctl, const FusedArgs *ap, int il) {
     const int t = threadIdx.x, r0 = 8 * c.b;
     WSlice<2 * E, 4> ws;
     wload<2 * E, 4>(ws, L.eh_proj.q, L.eh_proj.d, 8, [&](int rl) { return (int64_t)(r0 + rl); });
+    const W8 nwe = wload8(L.enorm), nwh = wload8(L.hnorm);
     // no barrier precedes the entry (its inputs come from earlier launches)
-    prologue<NL>(c.nl, c.ctl, &a.m.tok_embd, nullptr, 0, false, L.enorm, a.m.eps, s.xf, &s.xq[0][0], 2 * E, &s.xd[0][0],
+    prologue<NL>(c.nl, c.ctl, &a.m.tok_embd, nullptr, 0, false, nwe, a.m.eps, s.xf, &s.xq[0][0], 2 * E, &s.xd[0][0],
                  2 * E / 32, s.ns, nullptr);
     {
         // h of each lane: hid[hin_sel[l]]
@@ -1236,7 +1371,7 @@ FZ_PHASE bool phase_entry(const RunCtl *ctl, const FusedArgs *ap, int il) {
             for (int i = 0; i < 8; i++) v[i] = 0.0f;
         if (l < NL) put8(&s.xf[l][8 * tt], v);
         __syncthreads();
-        norm8(v, s.xf[l < NL ? l : 0], L.hnorm, a.m.eps, s.ns);
+        norm8(v, s.xf[l < NL ? l : 0], nwh.v, a.m.eps, s.ns);
         if (l < NL) {
             if (l < c.nl) quant8(v, &s.xq[l][E + 8 * tt], &s.xd[l][(E + 8 * tt) / 32]);
             else {
@@ -1276,9 +1411,10 @@ FZ_PHASE bool phase_head(const RunCtl *ctl, const FusedArgs *ap, const float *no
     WSlice<E, 8> A, B;
     auto rows_of = [&](int64_t tile) { const int64_t r = V - tile * TR; return (int)(r < TR ? r : TR); };
     if (t0 < t1) wload<E, 8>(A, a.m.output.q, a.m.output.d, rows_of(t0), [&](int rl) { return t0 * TR + rl; });
+    const W8 nw = wload8(norm_w);
     if (!wait(c.bar, &c.ps->ok)) return false;
     tr_pass(c);
-    prologue<NL>(nl, c.ctl, nullptr, a.b.x2, E, true, norm_w, a.m.eps, s.xf, &s.xq[0][0], E, &s.xd[0][0], E / 32, s.ns,
+    prologue<NL>(nl, c.ctl, nullptr, a.b.x2, E, true, nw, a.m.eps, s.xf, &s.xq[0][0], E, &s.xd[0][0], E / 32, s.ns,
                  s.xn);
     if (c.b == 0) {
         // h_nextn of each lane (Engine::hidden): the normalised x2
@@ -1385,8 +1521,8 @@ __global__ __launch_bounds__(fz::FT, 1) void fused_kernel(const RunCtl *__restri
 
 size_t fused_lds_bytes(int n_ctx) {
     const size_t base = sizeof(fz::PhaseSm<OXE_NL>);
-    const size_t pv = (size_t)GQA * ((n_ctx + 1) & ~1) * 2 + (size_t)n_ctx * 4 + (size_t)(n_ctx / 4) * 4 + 16 + 16 * 8 +
-                      16 * 4 + GQA * 32 * 4 + GQA * 32 + GQA * 2 + 256;
+    const size_t pv = (size_t)GQA * ((n_ctx + 1) & ~1) * 2 + (size_t)GQA * (n_ctx / 4) * 4 + 16 + GQA * 32 * 4 + GQA * 32 +
+                      GQA * 2 + 256;
     return (base > pv ? base : pv + 16) / 16 * 16 + 16;
 }
 

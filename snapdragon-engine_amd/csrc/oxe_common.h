@@ -38,6 +38,60 @@ OXE_DEV float shfl_xor_f(float v, int m) { return __shfl_xor(v, m, 64); }
 OXE_DEV double shfl_xor_d(double v, int m) { return __shfl_xor(v, m, 64); }
 OXE_DEV int shfl_xor_i(int v, int m) { return __shfl_xor(v, m, 64); }
 
+// ---- DPP lane moves (no LDS round trip). Within a row of 16 lanes, row_ror:8 pairs lane c with
+// c ^ 8; after that step every value is symmetric under ^ 8, so row_ror:4 then pairs c with c ^ 4;
+// quad_perm gives ^ 1 and ^ 2 directly.
+constexpr int DPP_XOR1 = 0xB1;   // quad_perm [1, 0, 3, 2]
+constexpr int DPP_XOR2 = 0x4E;   // quad_perm [2, 3, 0, 1]
+constexpr int DPP_ROR1 = 0x121, DPP_ROR2 = 0x122, DPP_ROR4 = 0x124, DPP_ROR8 = 0x128;
+template <int CTRL>
+OXE_DEV int dpp_i(int v) { return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xf, 0xf, false); }
+template <int CTRL>
+OXE_DEV float dpp_f(float v) { return __builtin_bit_cast(float, dpp_i<CTRL>(__builtin_bit_cast(int, v))); }
+template <int CTRL>
+OXE_DEV double dpp_d(double v) {
+    const unsigned long long u = __builtin_bit_cast(unsigned long long, v);
+    const uint32_t lo = (uint32_t)dpp_i<CTRL>((int)(uint32_t)u), hi = (uint32_t)dpp_i<CTRL>((int)(uint32_t)(u >> 32));
+    return __builtin_bit_cast(double, ((unsigned long long)hi << 32) | lo);
+}
+OXE_DEV double readlane_d(double v, int lane) {
+    const unsigned long long u = __builtin_bit_cast(unsigned long long, v);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)u, lane);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(u >> 32), lane);
+    return __builtin_bit_cast(double, ((unsigned long long)hi << 32) | lo);
+}
+OXE_DEV float readlane_f(float v, int lane) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+}
+// Sum over the wave of a double whose summation order is free (the exact-sum bracket below accepts
+// any order): rows of 16 by rotation, then the four row sums. Uniform result.
+OXE_DEV double wave_sum_d_any(double v) {
+    v += dpp_d<DPP_ROR8>(v);
+    v += dpp_d<DPP_ROR4>(v);
+    v += dpp_d<DPP_ROR2>(v);
+    v += dpp_d<DPP_ROR1>(v);
+    return (readlane_d(v, 0) + readlane_d(v, 16)) + (readlane_d(v, 32) + readlane_d(v, 48));
+}
+// (v > o ? v : o) over the wave. Uniform result.
+OXE_DEV float wave_max_any(float v) {
+    float o;
+    o = dpp_f<DPP_ROR8>(v); v = v > o ? v : o;
+    o = dpp_f<DPP_ROR4>(v); v = v > o ? v : o;
+    o = dpp_f<DPP_ROR2>(v); v = v > o ? v : o;
+    o = dpp_f<DPP_ROR1>(v); v = v > o ? v : o;
+    const float a = readlane_f(v, 0), b = readlane_f(v, 16), c = readlane_f(v, 32), d = readlane_f(v, 48);
+    const float ab = a > b ? a : b, cd = c > d ? c : d;
+    return ab > cd ? ab : cd;
+}
+// the 16-lane tree of ggml_vec_dot_f32's NEON reduce (lane c = chain c): ^8, ^4, ^1, ^2
+OXE_DEV float dot16_tree_dpp(float acc) {
+    acc = acc + dpp_f<DPP_ROR8>(acc);
+    acc = acc + dpp_f<DPP_ROR4>(acc);
+    acc = acc + dpp_f<DPP_XOR1>(acc);
+    acc = acc + dpp_f<DPP_XOR2>(acc);
+    return acc;
+}
+
 // ggml_v_expf NEON (vendor/ggml-subset/generated/upstream/src/ggml-cpu/vec.h:1154-1175), one lane
 OXE_DEV float v_expf(float x) {
     const float r = 0x1.8p23f;

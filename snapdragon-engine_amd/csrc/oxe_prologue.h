@@ -92,8 +92,7 @@ OXE_DEV void embed8(const Q8W &emb, uint32_t tok, float v[8]) {
 // Exact sum of squares of a 128-element vector held 2 per lane by one wave, for the l2 / gated
 // norms (oxe_ops.cpp:19-49): returns f32(sum/n). All 64 lanes of the wave call it.
 OXE_DEV float wave_mean_sq_128(float a, float b, const float *x_replay) {
-    double p = (double)(a * a) + (double)(b * b);
-    for (int m = 32; m >= 1; m >>= 1) p += shfl_xor_d(p, m);
+    const double p = wave_sum_d_any((double)(a * a) + (double)(b * b));
     float mean;
     if (!bracket_ok_mean(p, p, 128, 128.0, &mean)) {
         double s = 0.0;
@@ -105,10 +104,10 @@ OXE_DEV float wave_mean_sq_128(float a, float b, const float *x_replay) {
 
 // The same for a 256-element vector held 4 per lane (q / k norms of attention).
 OXE_DEV float wave_mean_sq_256(const float v[4], const float *x_replay) {
-    double p = 0.0;
+    double q = 0.0;
 #pragma unroll
-    for (int i = 0; i < 4; i++) p += (double)(v[i] * v[i]);
-    for (int m = 32; m >= 1; m >>= 1) p += shfl_xor_d(p, m);
+    for (int i = 0; i < 4; i++) q += (double)(v[i] * v[i]);
+    const double p = wave_sum_d_any(q);
     float mean;
     if (!bracket_ok_mean(p, p, 256, 256.0, &mean)) {
         double s = 0.0;

@@ -40,8 +40,17 @@ struct RouteOut {
     int32_t ids[OXE_NL][KUSED];
     float w[OXE_NL][KUSED];
     float gs[OXE_NL][NEXP / 4];
+    float sv[OXE_NL][KUSED + 1];     // the selected top 9 (value, expert) of the fast path
+    int32_t si[OXE_NL][KUSED + 1];
+    float vs[OXE_NL][KUSED + 1];     // values in rank order
     int32_t tie;
 };
+
+OXE_DEV void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
 
 OXE_DEV void route_wave(const float *lg, int l, RouteOut &ro) {
     const int tl = threadIdx.x & 63;
@@ -51,15 +60,15 @@ OXE_DEV void route_wave(const float *lg, int l, RouteOut &ro) {
     float mx = p[0];
 #pragma unroll
     for (int k = 1; k < 4; k++) mx = (mx > p[k]) ? mx : p[k];
-    mx = wave_max_f(mx);
+    mx = wave_max_any(mx);
 #pragma unroll
     for (int k = 0; k < 4; k++) p[k] = v_expf(p[k] - mx);
     const float g = (p[0] + p[1]) + (p[2] + p[3]);
     ro.gs[l][tl] = g;
-    double P = (double)g;
-    for (int m = 32; m >= 1; m >>= 1) P += shfl_xor_d(P, m);
+    const double P = wave_sum_d_any((double)g);
     float f;
     if (!bracket_ok_recip(P, P, NEXP / 4, &f)) {
+        wave_lds_sync();
         double s = 0.0;
         for (int i = 0; i < NEXP / 4; i++) s += (double)ro.gs[l][i];
         f = (float)(1.0 / s);
@@ -70,45 +79,107 @@ OXE_DEV void route_wave(const float *lg, int l, RouteOut &ro) {
         p[k] = p[k] * f;
         nan |= p[k] != p[k];
     }
-    // top 9 by wave arg-max rounds
-    unsigned taken = 0;  // bit k: expert 4tl+k already picked
-    float vals[KUSED + 1];
-    int ids[KUSED + 1];
+    // Fast path: the probabilities are >= 0, so their bits order like their values. Radix-select
+    // the 9th largest bit pattern T (the largest T with at least 9 values >= T); when exactly 9
+    // values are >= T and they are pairwise distinct, their order by value is the reference's
+    // (no ties), found by ranking the 9 directly.
+    bool fast = !__ballot(nan);
+    if (fast) {
+        uint32_t b[4];
 #pragma unroll
-    for (int r = 0; r <= KUSED; r++) {
-        float bv = -__builtin_inff();
-        int bi = 0x7fffffff;
+        for (int k = 0; k < 4; k++) b[k] = __builtin_bit_cast(uint32_t, p[k]);
+        uint32_t T = 0;
+        for (int bit = 31; bit >= 0; bit--) {
+            const uint32_t cand = T | (1u << bit);
+            int cnt = 0;
 #pragma unroll
-        for (int k = 0; k < 4; k++)
-            if (!((taken >> k) & 1) && (p[k] > bv || bi == 0x7fffffff)) { bv = p[k]; bi = 4 * tl + k; }
-        const float m = wave_max_f(bv);
-        const int i = wave_min_i(bv == m ? bi : 0x7fffffff);
-        if ((i >> 2) == tl) taken |= 1u << (i & 3);
-        vals[r] = m;
-        ids[r] = i;
+            for (int k = 0; k < 4; k++) cnt += __popcll(__ballot(b[k] >= cand));
+            if (cnt >= KUSED + 1) T = cand;
+        }
+        unsigned long long m[4];
+        int nsel = 0;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            m[k] = __ballot(b[k] >= T);
+            nsel += __popcll(m[k]);
+        }
+        fast = nsel == KUSED + 1;
+        if (fast) {
+            const unsigned long long below = (1ull << tl) - 1;
+            int base = 0;
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                if (b[k] >= T) {
+                    const int slot = base + __popcll(m[k] & below);
+                    ro.sv[l][slot] = p[k];
+                    ro.si[l][slot] = 4 * tl + k;
+                }
+                base += __popcll(m[k]);
+            }
+            wave_lds_sync();
+            int dup = 0;
+            if (tl < KUSED + 1) {
+                const float v = ro.sv[l][tl];
+                const int id = ro.si[l][tl];
+                int rank = 0;
+#pragma unroll
+                for (int j = 0; j < KUSED + 1; j++) {
+                    const float o = ro.sv[l][j];
+                    rank += (o > v) ? 1 : 0;
+                    dup |= (j != tl && o == v) ? 1 : 0;
+                }
+                if (rank < KUSED) ro.ids[l][rank] = id;
+                ro.vs[l][rank] = v;
+                (void)id;
+            }
+            fast = !__ballot(dup != 0);
+            wave_lds_sync();
+        }
     }
-    bool tie = false;
+    if (!fast) {
+        // ties, NaN, or a repeated 9th value: the 9 wave arg-max rounds (largest value, then the
+        // lowest index), as the reference's std::sort order would need
+        unsigned taken = 0;  // bit k: expert 4tl+k already picked
+        float vals[KUSED + 1];
+        int ids[KUSED + 1];
 #pragma unroll
-    for (int r = 1; r <= KUSED; r++) tie |= !(vals[r - 1] > vals[r]);
-    int eq = 0;
+        for (int r = 0; r <= KUSED; r++) {
+            float bv = -__builtin_inff();
+            int bi = 0x7fffffff;
 #pragma unroll
-    for (int k = 0; k < 4; k++) eq += p[k] == vals[KUSED];
-    eq = wave_sum_i(eq);
-    tie |= eq != 1;
-    tie |= wave_sum_i(nan ? 1 : 0) != 0;
+            for (int k = 0; k < 4; k++)
+                if (!((taken >> k) & 1) && (p[k] > bv || bi == 0x7fffffff)) { bv = p[k]; bi = 4 * tl + k; }
+            const float mm = wave_max_f(bv);
+            const int i = wave_min_i(bv == mm ? bi : 0x7fffffff);
+            if ((i >> 2) == tl) taken |= 1u << (i & 3);
+            vals[r] = mm;
+            ids[r] = i;
+        }
+        bool tie = false;
+#pragma unroll
+        for (int r = 1; r <= KUSED; r++) tie |= !(vals[r - 1] > vals[r]);
+        int eq = 0;
+#pragma unroll
+        for (int k = 0; k < 4; k++) eq += p[k] == vals[KUSED];
+        eq = wave_sum_i(eq);
+        tie |= eq != 1;
+        tie |= wave_sum_i(nan ? 1 : 0) != 0;
+        if (tl == 0) {
+            for (int j = 0; j <= KUSED; j++) ro.vs[l][j] = vals[j];
+            for (int j = 0; j < KUSED; j++) ro.ids[l][j] = ids[j];
+            if (tie) ro.tie = 1;
+        }
+        wave_lds_sync();
+    }
     if (tl == 0) {
         double s = 0.0;
 #pragma unroll
-        for (int j = 0; j < KUSED; j++) s += (double)vals[j];
+        for (int j = 0; j < KUSED; j++) s += (double)ro.vs[l][j];
         float sf = (float)s;
         sf = sf < __builtin_inff() ? sf : __builtin_inff();
         sf = sf > 6.103515625e-5f ? sf : 6.103515625e-5f;
 #pragma unroll
-        for (int j = 0; j < KUSED; j++) {
-            ro.ids[l][j] = ids[j];
-            ro.w[l][j] = vals[j] / sf;
-        }
-        if (tie) ro.tie = 1;
+        for (int j = 0; j < KUSED; j++) ro.w[l][j] = ro.vs[l][j] / sf;
     }
 }
 
