@@ -9,9 +9,10 @@ committed tokens (accepted drafts + bonus).
 
 Timing: the prompt is prefilled first (not timed), W warm-up steps, then exactly K steps as K
 HIP-graph launches between two synchronised HIP events on the engine stream. The roofline object
-is for the kernel with the largest share of the step time (from the committed rocprof summary: the
-routed-expert gate/up kernel), timed live with HIP events around each of its launches in eager
-device-driven steps; its algorithmic bytes are the union experts' gate/up weights it streams.
+is for the kernel with the largest share of the step time: the fused run kernel's verify run (one
+launch per step, ~94 % of it), timed live with HIP events around its launch in eager device-driven
+steps; its algorithmic bytes are the verify run's unique weight, state and KV bytes at the
+measured union size.
 cpu_baseline: the C++ oracle (the reference algorithm restated, OpenMP over rows) timed on this
 host on a bounded sample of the same workload (see the `sample` field).
 """
@@ -139,10 +140,8 @@ def main():
         calibrate_copy(torch)
         return
     import oxe_amd as A
-    sys.path.insert(0, os.path.join(ROOT, "oracle"))
-    import oracle as O  # the model description struct and bench prompt only
 
-    d = O.desc_35b_a3b()
+    d = A.desc_35b_a3b()
     n_ctx = args.prompt + 2 * (args.steps + args.warmup) + 256 + 64
     t_setup = time.time()
     eng = A.Engine(d, seed=0, n_ctx=n_ctx)
@@ -150,7 +149,7 @@ def main():
         eng.set_fused(False)
     fused = eng.fused
     probe_kind = args.probe_kind if args.probe_kind >= 0 else (10 if fused else 1)
-    prompt = O.bench_prompt(args.prompt)
+    prompt = A.bench_prompt(args.prompt)
     x = eng.mtp_prefill(prompt)
     eng.sync()
     setup_s = time.time() - t_setup

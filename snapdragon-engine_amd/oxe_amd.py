@@ -40,6 +40,40 @@ def lib():
     return _lib
 
 
+class ModelDesc(C.Structure):
+    """oxe_model_desc of include/oxe_model.h (the reference's ModelDesc, crates/model/src/desc.rs:15-140)."""
+    _fields_ = [
+        ("n_layer", C.c_int32), ("n_embd", C.c_int32), ("n_vocab", C.c_int32),
+        ("n_head", C.c_int32), ("n_head_kv", C.c_int32), ("head_dim", C.c_int32),
+        ("n_expert", C.c_int32), ("n_expert_used", C.c_int32), ("ff_exp", C.c_int32), ("ff_shexp", C.c_int32),
+        ("ssm_conv_kernel", C.c_int32), ("ssm_d_state", C.c_int32), ("ssm_n_kheads", C.c_int32),
+        ("ssm_n_vheads", C.c_int32), ("ssm_d_inner", C.c_int32),
+        ("full_attention_interval", C.c_int32), ("n_rot", C.c_int32), ("rope_sections", C.c_int32 * 4),
+        ("rms_eps", C.c_float), ("rope_freq_base", C.c_float), ("n_ctx_train", C.c_int32), ("has_mtp", C.c_int32),
+    ]
+
+
+def desc_35b_a3b(**over):
+    """The qwen35moe 35B-A3B shape (40 layers, 3 delta-net : 1 attention, 256 experts top-8, vocab
+    151936, MTP block), as the reference reads it from GGUF metadata (desc.rs:69-140)."""
+    d = ModelDesc(n_layer=40, n_embd=2048, n_vocab=151936, n_head=16, n_head_kv=2, head_dim=256,
+                  n_expert=256, n_expert_used=8, ff_exp=512, ff_shexp=512, ssm_conv_kernel=4,
+                  ssm_d_state=128, ssm_n_kheads=16, ssm_n_vheads=32, ssm_d_inner=4096,
+                  full_attention_interval=4, n_rot=64, rms_eps=9.999999974752427e-07,
+                  rope_freq_base=1e7, n_ctx_train=262144, has_mtp=1)
+    d.rope_sections[:] = [11, 11, 10, 0]
+    for k, v in over.items():
+        setattr(d, k, v)
+    return d
+
+
+def bench_prompt(n):
+    """oxe bench's prompt ids (crates/oxe-cli/src/bin/oxe.rs:428-435): (i*2654435761 mod 2^32) % 150000 + 1000."""
+    import numpy as np
+    i = np.arange(n, dtype=np.uint64)
+    return (((i * 2654435761) & 0xFFFFFFFF) % 150000 + 1000).astype(np.uint32)
+
+
 def exported_symbols():
     """Names the header declares and the library must export."""
     hdr = os.path.join(HERE, "..", "include", "oxe_amd.h")
@@ -167,8 +201,8 @@ class Engine:
             check(L.oxe_engine_synth_weights(h), "synth_weights")
 
     def close(self):
-        if getattr(self, "h", None):
-            lib().oxe_engine_destroy(self.h)
+        if getattr(self, "h", None) and _lib is not None:
+            _lib.oxe_engine_destroy(self.h)
             self.h = None
 
     def __del__(self):

@@ -1,0 +1,88 @@
+"""Phase timing of the fused verify run (diagnostic).
+
+Builds the 35B-A3B-shaped synthetic model on the GPU, prefills the bench prompt, turns the fused
+kernel's phase trace on, runs host-driven 2-lane verify steps and prints, per phase kind, the mean
+time from the barrier release (first workgroup to pass) to the last workgroup done, the gap before
+it (previous phase done to this release) and the median sub-step marks. Times from the device wall
+clock (100 MHz).
+
+    python snapdragon-engine_amd/phase_trace.py [--prompt 512] [--steps 3]
+"""
+import argparse
+import os
+import sys
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+if HERE not in sys.path:
+    sys.path.insert(0, HERE)
+
+import oxe_amd as A  # noqa: E402
+
+PHASES = {1: "proj", 2: "dn", 3: "scores", 4: "pv", 5: "out", 6: "router", 7: "experts", 8: "down", 9: "entry",
+          10: "head"}
+MARKS = {101: "experts: routing", 102: "experts: gate/up loads issued", 103: "experts: issue drained",
+         104: "experts: gate/up dot", 111: "proj: norm prologue", 112: "proj: dot", 121: "dn: conv",
+         122: "dn: norms + gates", 123: "dn: delta rule", 131: "router: norm prologue", 132: "router: f32 dots",
+         141: "pv: softmax"}
+
+
+def analyse(tr):
+    """tr: [grid, events, 4] (id, start, passed, end). Returns (total_us, phase rows, mark rows)."""
+    G = tr.shape[0]
+    mains = []
+    for g in range(G):
+        ev = tr[g][(tr[g, :, 0] > 0) & (tr[g, :, 0] < 100)]
+        mains.append(ev)
+    n = min(len(m) for m in mains)
+    mm = np.stack([m[:n] for m in mains]).astype(np.int64)
+    ids = mm[0, :, 0]
+    start, pas, end = mm[:, :, 1], mm[:, :, 2], mm[:, :, 3]
+    rel = pas.min(axis=0)
+    done = end.max(axis=0)
+    total = (done[-1] - start.min()) / 100.0
+    agg = {}
+    for k in range(n):
+        name = PHASES.get(int(ids[k]), str(int(ids[k])))
+        a = agg.setdefault(name, [0, 0.0, 0.0])
+        a[0] += 1
+        a[1] += (done[k] - rel[k]) / 100.0
+        a[2] += (rel[k] - done[k - 1]) / 100.0 if k > 0 else 0.0
+    marks = {}
+    for g in range(G):
+        ev = tr[g][tr[g, :, 0] >= 100].astype(np.int64)
+        for e in ev:
+            marks.setdefault(int(e[0]), []).append((e[3] - e[1]) / 100.0)
+    return total, agg, marks
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--prompt", type=int, default=512)
+    ap.add_argument("--steps", type=int, default=3)
+    args = ap.parse_args()
+    d = A.desc_35b_a3b()
+    e = A.Engine(d, seed=0, n_ctx=args.prompt + 2 * args.steps + 256)
+    if not e.fused:
+        sys.exit("the fused run kernel is not available on this device")
+    x = e.mtp_prefill(A.bench_prompt(args.prompt))
+    e.set_trace(True)
+    for _ in range(args.steps):
+        g = e.verify([x, (x + 1) % d.n_vocab])
+        e.commit(1)
+        x = int(g[0])
+    total, agg, marks = analyse(e.read_trace())
+    print(f"verify run (2 lanes, 40 layers + LM head) at position {e.pos}: {total:.1f} us")
+    print(f"{'phase':10s} {'count':>5s} {'release->done us':>17s} {'gap before us':>14s} {'total us':>9s}")
+    for name, (cnt, dur, gap) in agg.items():
+        print(f"{name:10s} {cnt:5d} {dur / cnt:17.2f} {gap / cnt:14.2f} {dur + gap:9.1f}")
+    print("sub-steps (median over workgroups and layers, us):")
+    for i in sorted(marks):
+        v = np.array(marks[i])
+        print(f"  {MARKS.get(i, str(i)):32s} {np.median(v):6.2f}  (p90 {np.percentile(v, 90):.2f})")
+    e.close()
+
+
+if __name__ == "__main__":
+    main()
