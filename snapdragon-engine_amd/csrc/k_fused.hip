@@ -68,7 +68,12 @@ OXE_DEV void arrive(Bar b) {
         const uint32_t old = __hip_atomic_fetch_add(&b.w[32 * x], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if (old == b.round * per - 1) {
             const uint32_t og = __hip_atomic_fetch_add(&b.w[FZ_W_GLOB], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            if (og == b.round * FZ_XCD - 1) cst32(&b.w[FZ_W_FLAG], b.round);
+            if (og == b.round * FZ_XCD - 1) {
+                // release: one copy of the round per XCD line, then the launch-level copy
+#pragma unroll
+                for (int i = 0; i < FZ_XCD; i++) cst32(&b.w[FZ_W_REL + 32 * i], b.round);
+                cst32(&b.w[FZ_W_FLAG], b.round);
+            }
         }
     }
 }
@@ -78,7 +83,8 @@ OXE_DEV bool wait(Bar b, int *s_ok) {
     if (threadIdx.x == 0) {
         int ok = 1;
         uint32_t spins = 0;
-        while ((int32_t)(cld32(&b.w[FZ_W_FLAG]) - b.round) < 0) {
+        const uint32_t *rel = &b.w[FZ_W_REL + 32 * (blockIdx.x & (FZ_XCD - 1))];
+        while ((int32_t)(cld32(rel) - b.round) < 0) {
             if (++spins > SPIN_MAX) {
                 cst32(&b.w[FZ_W_ERR], 1u);
                 ok = 0;
@@ -88,7 +94,7 @@ OXE_DEV bool wait(Bar b, int *s_ok) {
                 ok = 0;
                 break;
             }
-            __builtin_amdgcn_s_sleep(2);
+            __builtin_amdgcn_s_sleep(1);
         }
         *s_ok = ok;
     }
@@ -706,6 +712,8 @@ FZ_PHASE bool phase_out(const RunCtl *ctl, const FusedArgs *ap, int il, const fl
     wload<MIX_W, 4>(ws, L.out.q, L.out.d, 8, [&](int rl) { return (int64_t)(r0 + rl); });
     if (!wait(c.bar, &c.ps->ok)) return false;
     tr_pass(c);
+    float xres = 0.0f;
+    if (t < NL * 8 && t / 8 < c.nl) xres = cld(x + (int64_t)(t / 8) * E + r0 + t % 8);
     {
         const int l = t >> 8, tt = t & 255;
         if (l < NL)
@@ -721,7 +729,7 @@ FZ_PHASE bool phase_out(const RunCtl *ctl, const FusedArgs *ap, int il, const fl
         const int l = t / 8, rl = t % 8;
         if (l < c.nl) {
             const int64_t i = (int64_t)l * E + r0 + rl;
-            cst(a.b.x1 + i, s.g.out[l][rl] + cld(x + i));
+            cst(a.b.x1 + i, s.g.out[l][rl] + xres);
         }
     }
     tr_end(c, TP_OUT);
@@ -857,8 +865,10 @@ FZ_PHASE bool phase_moe(const RunCtl *ctl, const FusedArgs *ap, int il) {
     }
     if (t == 0) ps.ro.tie = 0;
     __syncthreads();
+    tr_mark(c, 105);
     if ((t >> 6) < nl) route_wave(se.lg[t >> 6], t >> 6, ps.ro);
     __syncthreads();
+    tr_mark(c, 106);
     if (t < 64) {
         const int e = t < nl * KUSED ? ps.ro.ids[t / KUSED][t % KUSED] : -1;
         bool isnew = e >= 0;
@@ -955,21 +965,36 @@ FZ_PHASE bool phase_moe(const RunCtl *ctl, const FusedArgs *ap, int il) {
     }
     if (!wait(c.bar, &ps.ok)) return false;
     tr_pass(c);
-    // 4. down + combine (engine.rs:3542-3624)
+    // 4. down + combine (engine.rs:3542-3624). Loads in the order they are needed: the shared
+    // expert's h (quantised here), then the routed experts' quantised h, then the residual inputs.
     auto &sd = c.sm->down;
-    for (int i = t; i < NL * OXE_MAX_UNION * (FF / 16); i += FT) {
-        const int l = i / (OXE_MAX_UNION * (FF / 16)), u = (i / (FF / 16)) % OXE_MAX_UNION, k = i % (FF / 16);
-        uint4 v = make_uint4(0, 0, 0, 0);
-        if (l < nl && u < nu) v = cld128(a.hq + ((int64_t)l * OXE_MAX_UNION + u) * FF + 16 * k);
-        *(uint4 *)&sd.hq[l][u][16 * k] = v;
+    float hsv[NL * FFSH / FT];
+#pragma unroll
+    for (int k = 0; k < NL * FFSH / FT; k++) {
+        const int i = t + FT * k, l = i / FFSH;
+        hsv[k] = l < nl ? cld(a.b.hsh + i) : 0.0f;
     }
+    uint4 hqv[NL * OXE_MAX_UNION * (FF / 16) / FT];
+#pragma unroll
+    for (int k = 0; k < NL * OXE_MAX_UNION * (FF / 16) / FT; k++) {
+        const int i = t + FT * k;
+        const int l = i / (OXE_MAX_UNION * (FF / 16)), u = (i / (FF / 16)) % OXE_MAX_UNION, kk = i % (FF / 16);
+        hqv[k] = (l < nl && u < nu) ? cld128(a.hq + ((int64_t)l * OXE_MAX_UNION + u) * FF + 16 * kk) : make_uint4(0, 0, 0, 0);
+    }
+    uint16_t hdv = 0;
     if (t < NL * OXE_MAX_UNION * (FF / 32)) {
         const int l = t / (OXE_MAX_UNION * (FF / 32)), u = (t / (FF / 32)) % OXE_MAX_UNION, k = t % (FF / 32);
-        sd.hd[l][u][k] = (l < nl && u < nu) ? cld16(a.hd + ((int64_t)l * OXE_MAX_UNION + u) * (FF / 32) + k) : (uint16_t)0;
+        hdv = (l < nl && u < nu) ? cld16(a.hd + ((int64_t)l * OXE_MAX_UNION + u) * (FF / 32) + k) : (uint16_t)0;
     }
-    for (int i = t; i < NL * FFSH; i += FT) {
-        const int l = i / FFSH;
-        sd.hs[l][i % FFSH] = l < nl ? cld(a.b.hsh + i) : 0.0f;
+    float x1v = 0.0f, sgv = 0.0f;
+    if (t < NL * 8 && t / 8 < nl) {
+        x1v = cld(a.b.x1 + (int64_t)(t / 8) * E + r0 + t % 8);
+        sgv = cld(a.b.sh_gate + t / 8);
+    }
+#pragma unroll
+    for (int k = 0; k < NL * FFSH / FT; k++) {
+        const int i = t + FT * k;
+        sd.hs[i / FFSH][i % FFSH] = hsv[k];
     }
     if (t < DW_UNITS * 16) {
         uint32_t *d = &sd.wd[su][srr * (FF / 64 + 1) + shf * 4];
@@ -979,6 +1004,16 @@ FZ_PHASE bool phase_moe(const RunCtl *ctl, const FusedArgs *ap, int il) {
     if (t < NL * (FFSH / 32)) {
         const int l = t / (FFSH / 32), bb = t % (FFSH / 32);
         quant_block_q8_0(&sd.hs[l][32 * bb], &sd.hq[l][OXE_MAX_UNION][32 * bb], &sd.hd[l][OXE_MAX_UNION][bb]);
+    }
+#pragma unroll
+    for (int k = 0; k < NL * OXE_MAX_UNION * (FF / 16) / FT; k++) {
+        const int i = t + FT * k;
+        const int l = i / (OXE_MAX_UNION * (FF / 16)), u = (i / (FF / 16)) % OXE_MAX_UNION, kk = i % (FF / 16);
+        *(uint4 *)&sd.hq[l][u][16 * kk] = hqv[k];
+    }
+    if (t < NL * OXE_MAX_UNION * (FF / 32)) {
+        const int l = t / (OXE_MAX_UNION * (FF / 32)), u = (t / (FF / 32)) % OXE_MAX_UNION, k = t % (FF / 32);
+        sd.hd[l][u][k] = hdv;
     }
     __syncthreads();
 #pragma unroll
@@ -1015,11 +1050,10 @@ FZ_PHASE bool phase_moe(const RunCtl *ctl, const FusedArgs *ap, int il) {
                 const float p = sd.dn[ps.slot[l][j]][l][r] * ps.ro.w[l][j];
                 m = m + p;
             }
-            const float sg = cld(a.b.sh_gate + l);
-            const float sh = sd.dn[OXE_MAX_UNION][l][r] * sg;
+            const float sh = sd.dn[OXE_MAX_UNION][l][r] * sgv;
             const float f = m + sh;
             const int64_t i = (int64_t)l * E + r0 + r;
-            cst(a.b.x2 + i, f + cld(a.b.x1 + i));
+            cst(a.b.x2 + i, f + x1v);
         }
     }
     tr_end(c, TP_DOWN);

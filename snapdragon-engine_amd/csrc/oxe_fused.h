@@ -31,10 +31,11 @@ struct LayerDev {
 enum FusedMode { FM_VERIFY = 0, FM_DRAFT = 1, FM_SEED = 2 };
 
 // barrier words (uint32): per-XCD arrival counters at [32 x] (x = 0..7, one 128-byte line each),
-// the global arrival counter at [256], the release round at [288], the sticky error word at [320]
-constexpr int FZ_SYNC_WORDS = 512;
+// the global arrival counter at [256], the release round at [288] (read at launch), the sticky
+// error word at [320], and per-XCD copies of the release round at [384 + 32 x]
+constexpr int FZ_SYNC_WORDS = 640;
 constexpr int FZ_XCD = 8;
-constexpr int FZ_W_GLOB = 256, FZ_W_FLAG = 288, FZ_W_ERR = 320;
+constexpr int FZ_W_GLOB = 256, FZ_W_FLAG = 288, FZ_W_ERR = 320, FZ_W_REL = 384;
 
 struct FusedArgs {
     int32_t mode, n_layer, keep_logits, grid;
