@@ -26,7 +26,9 @@ using namespace shp;
 namespace fz {
 
 constexpr int FT = 512;                       // threads per workgroup
-constexpr int SC_P = FT / 8;                  // positions per scores workgroup (4 threads per position and lane)
+constexpr int SC_P = 16;                      // positions per scores chunk (workgroup step)
+constexpr int SC_KS = HD + 32;                // LDS row stride of cached K rows in halves (576 B: the 16 rows of a
+                                              // wave quarter fall on distinct banks)
 constexpr uint32_t SPIN_MAX = 400000;         // ~0.4 s at one device-scope load per iteration
 
 // ---- device-scope accesses for data exchanged inside the launch -----------------------------
@@ -318,6 +320,7 @@ template <int NL>
 struct DnSm {
     float q[NL][DS], k[NL][DS], v[NL][HV], o[NL][HV];
     float g[NL], b[NL];
+    int last;
 };
 template <int NL>
 struct OutSm {
@@ -343,16 +346,12 @@ struct ExpSm {
     alignas(16) int8_t xq[NL][E];
     uint16_t xd[NL][E / 32];
     GSm<E, 64, NL> g;
-    alignas(16) float h[NL][32];
-    alignas(16) int8_t hq[NL][32];
-    uint16_t hd[NL];
 };
 constexpr int DW_UNITS = OXE_MAX_UNION + 1;   // union experts + the shared expert
 template <int NL>
 struct DownSm {
     alignas(16) int8_t hq[NL][DW_UNITS][FF];
     uint16_t hd[NL][DW_UNITS][FF / 32];
-    alignas(16) float hs[NL][FFSH];
     uint32_t wd[DW_UNITS][8 * (FF / 64 + 1)];
     int32_t isum[DW_UNITS][NL][8][FF / 32 + 1];
     float dn[DW_UNITS][NL][8];
@@ -363,7 +362,7 @@ struct ScSm {
     float tmp[NL * GQA][HD];
     float ktmp[NL][HD];
     alignas(16) uint16_t knew[NL][HD];
-    alignas(16) uint16_t krows[SC_P][HD];   // cached K rows of the workgroup's positions (DMA-loaded)
+    alignas(16) uint16_t krows[SC_P][SC_KS];   // cached K rows of the chunk's positions (padded rows)
 };
 template <int NL>
 struct HeadSm {
@@ -523,8 +522,13 @@ FZ_PHASE bool phase_proj(const RunCtl *ctl, const FusedArgs *ap, int il, bool em
     return true;
 }
 
-// delta-net recurrence, one value head per workgroup b < 32 (k_layer.hip dn_kernel with 512
-// threads: thread (rg = t/16, c = t%16) owns state rows rg + 32 h, h < 4)
+// Delta-net recurrence (k_layer.hip dn_kernel's arithmetic) over DN_WPH workgroups per value head:
+// workgroup b takes value head vh = b / DN_WPH and state rows [16 (b % DN_WPH), +16); thread
+// (rg = t/16, c = t%16), t < 256, owns state row 16 (b % DN_WPH) + rg. Every workgroup of a head
+// forms the head's conv outputs and normalised q, k (gdn conv + l2 norms, oxe_ops.cpp:218-267) and
+// writes its 16 outputs; the last of the head's workgroups to count itself in (per-head arrival
+// counter) forms the gated norm of the head's 128 outputs and quantizes them.
+constexpr int DN_WPH = 8, DN_RPW = HV / DN_WPH;
 OXE_DEV float dot16_tree_f(float acc) { return dot16_tree_dpp(acc); }
 OXE_DEV float conv4f(float s0, float s1, float s2, float xn, const float *c) {
     const float p0 = s0 * c[0], p1 = s1 * c[1], p2 = s2 * c[2], p3 = xn * c[3];
@@ -535,6 +539,28 @@ OXE_DEV float conv4f(float s0, float s1, float s2, float xn, const float *c) {
     sumf = sumf + p3;
     return sumf;
 }
+// max over the 32-lane half of the wave holding this lane (exact, any order)
+OXE_DEV float half_max(float v) {
+    v = fmaxf(v, dpp_f<DPP_ROR8>(v));
+    v = fmaxf(v, dpp_f<DPP_ROR4>(v));
+    v = fmaxf(v, dpp_f<DPP_ROR2>(v));
+    v = fmaxf(v, dpp_f<DPP_ROR1>(v));
+    const float lo = fmaxf(readlane_f(v, 0), readlane_f(v, 16)), hi = fmaxf(readlane_f(v, 32), readlane_f(v, 48));
+    return (threadIdx.x & 63) < 32 ? lo : hi;
+}
+// quantize_row_q8_0 (NEON) of the 32-value block held one value per lane by each half of the
+// wave: *d = the block scale; returns in lane 4 i the codes of lanes 4 i .. 4 i + 3 (byte order)
+OXE_DEV uint32_t quant32_lanes(float v, float *d) {
+    const float m = half_max(__builtin_fabsf(v));
+    const float dd = m / 127.0f;
+    const float id = dd != 0.0f ? 1.0f / dd : 0.0f;
+    const int32_t q = (int32_t)__builtin_rintf(v * id);
+    int p = (int)((uint32_t)(q & 0xff) << (8 * (threadIdx.x & 3)));
+    p |= dpp_i<DPP_XOR1>(p);
+    p |= dpp_i<DPP_XOR2>(p);
+    *d = dd;
+    return (uint32_t)p;
+}
 
 template <int NL>
 FZ_PHASE bool phase_dn(const RunCtl *ctl, const FusedArgs *ap, int il) {
@@ -543,57 +569,62 @@ FZ_PHASE bool phase_dn(const RunCtl *ctl, const FusedArgs *ap, int il) {
     const LayerDev &L = ap->layers[il];
     const FusedArgs &a = *c.a;
     auto &s = c.sm->dn;
-    const int t = threadIdx.x, vh = c.b, kh = vh % NKH;
-    const bool worker = c.b < NVH;
+    const int t = threadIdx.x, w = t >> 6, lane = t & 63;
+    const int vh = c.b / DN_WPH, kh = vh % NKH, row0 = (c.b % DN_WPH) * DN_RPW;
+    const bool worker = c.b < NVH * DN_WPH;
     const int cur = c.ctl->cur;
     const int64_t conv_slot = (int64_t)a.m.n_rec * NCH * (KC - 1);
     const int64_t ssm_slot = (int64_t)a.m.n_rec * NVH * HV * HV;
     float *conv_state = a.m.conv_state + (int64_t)L.index * NCH * (KC - 1);
     float *ssm = a.m.ssm_state + (int64_t)L.index * NVH * HV * HV;
     const int rg = t >> 4, cc = t & 15;
-    float r[4][8];
-    if (worker) {
+    const bool dlt = worker && t < DN_RPW * 16;
+    float r[8];
+    if (dlt) {
+        const float *src = ssm + (int64_t)cur * ssm_slot + ((int64_t)vh * HV + row0 + rg) * HV;
 #pragma unroll
-        for (int h = 0; h < 4; h++) {
-            const float *src = ssm + (int64_t)cur * ssm_slot + ((int64_t)vh * HV + rg + 32 * h) * HV;
-#pragma unroll
-            for (int q = 0; q < 8; q++) r[h][q] = src[cc + 16 * q];
-        }
+        for (int q = 0; q < 8; q++) r[q] = src[cc + 16 * q];
     }
-    // this thread's conv channel: state (slot cur, an earlier launch) and weights, loaded ahead
+    // this thread's conv channel (q: t < 128, k: t < 256, the workgroup's 16 v rows: t < 272): state
+    // (slot cur, an earlier launch) and weights, loaded ahead. q/k states are written by the head's
+    // first workgroup of the first 16 value heads (value heads vh and vh + 16 share key head vh).
     int ch = 0;
-    bool writer = false;
-    if (t < DS) { ch = kh * DS + t; writer = vh < NKH; }
-    else if (t < 2 * DS) { ch = NKH * DS + kh * DS + (t - DS); writer = vh < NKH; }
-    else { ch = 2 * NKH * DS + vh * HV + (t - 2 * DS); writer = true; }
+    bool conv = false, writer = false;
+    if (t < DS) { ch = kh * DS + t; conv = worker; writer = vh < NKH && row0 == 0; }
+    else if (t < 2 * DS) { ch = NKH * DS + kh * DS + (t - DS); conv = worker; writer = vh < NKH && row0 == 0; }
+    else if (t < 2 * DS + DN_RPW) { ch = 2 * NKH * DS + vh * HV + row0 + (t - 2 * DS); conv = worker; writer = true; }
     float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f;
     float cw[KC] = {0.0f, 0.0f, 0.0f, 0.0f};
-    float dtb = 0.0f, sa = 0.0f;
-    if (worker && t < 3 * DS) {
+    if (conv) {
         const float *st = conv_state + (int64_t)cur * conv_slot + (int64_t)ch * (KC - 1);
         s0 = st[0]; s1 = st[1]; s2 = st[2];
         const float4 c4 = *(const float4 *)(L.conv + (int64_t)ch * KC);
         cw[0] = c4.x; cw[1] = c4.y; cw[2] = c4.z; cw[3] = c4.w;
     }
-    if (worker) {
-        dtb = L.dt_bias[vh];
-        sa = L.ssm_a[vh];
-    }
+    // gate thread of lane gl (wave 5) and the gated-norm weights (waves < NL)
+    const int gl = t - 5 * 64;
+    const bool gate = worker && gl >= 0 && gl < NL;
+    float dtb = 0.0f, sa = 0.0f;
+    if (gate) { dtb = L.dt_bias[vh]; sa = L.ssm_a[vh]; }
+    float nw0 = 0.0f, nw1 = 0.0f;
+    if (worker && w < NL) { nw0 = L.ssm_norm[lane]; nw1 = L.ssm_norm[lane + 64]; }
     if (!wait(c.bar, &c.ps->ok)) return false;
     tr_pass(c);
-    if (!worker && il + 1 < a.n_layer) {
-        const LayerDev &N = a.layers[il + 1];
-        const int64_t rows = N.att ? AT_ROWS : DN_ROWS;
-        warm(N.proj.q, (size_t)rows * E, c.b - NVH, c.G - NVH, a.sync + FZ_W_ERR + 32);
-        warm(N.proj.d, (size_t)rows * (E / 32) * 2, c.b - NVH, c.G - NVH, a.sync + FZ_W_ERR + 32);
-    }
     if (worker) {
         const int nl = c.nl;
-        if (t < 3 * DS) {
-            for (int l = 0; l < nl; l++) {
-                const float xn = cld(a.b.proj + (int64_t)l * DN_ROWS + ch);
-                const float y = v_silu(conv4f(s0, s1, s2, xn, cw));
-                s0 = s1; s1 = s2; s2 = xn;
+        float xin[NL], ga = 0.0f, gb = 0.0f;
+#pragma unroll
+        for (int l = 0; l < NL; l++) xin[l] = conv && l < nl ? cld(a.b.proj + (int64_t)l * DN_ROWS + ch) : 0.0f;
+        if (gate && gl < nl) {
+            ga = cld(a.b.proj + (int64_t)gl * DN_ROWS + DN_ALPHA + vh);
+            gb = cld(a.b.proj + (int64_t)gl * DN_ROWS + DN_BETA + vh);
+        }
+        if (conv) {
+#pragma unroll
+            for (int l = 0; l < NL; l++) {
+                if (l >= nl) break;
+                const float y = v_silu(conv4f(s0, s1, s2, xin[l], cw));
+                s0 = s1; s1 = s2; s2 = xin[l];
                 if (writer) {
                     float *dst = conv_state + (int64_t)((cur + l + 1) % OXE_NSLOTS) * conv_slot + (int64_t)ch * (KC - 1);
                     dst[0] = s0; dst[1] = s1; dst[2] = s2;
@@ -603,94 +634,99 @@ FZ_PHASE bool phase_dn(const RunCtl *ctl, const FusedArgs *ap, int il) {
                 else s.v[l][t - 2 * DS] = y;
             }
         }
+        if (gate && gl < nl) {
+            s.g[gl] = oxe_libm::expf_c(softplus_c(ga + dtb) * sa);
+            s.b[gl] = sigmoid_c(gb);
+        }
         __syncthreads();
         tr_mark(c, 121);
-        {
-            const int w = t >> 6, lane = t & 63;
-            if (w < 2 * NL && (w >> 1) < nl) {
-                const int l = w >> 1;
-                float *xv = (w & 1) ? s.k[l] : s.q[l];
-                const float a0 = xv[lane], a1 = xv[lane + 64];
-                const float nf = (float)DS;
-                const float mean = wave_mean_sq_128(a0, a1, xv);
-                const float scale = 1.0f / sqrtf(mean + a.m.eps / nf);
-                const float s2 = 1.0f / sqrtf(nf);
-                xv[lane] = (a0 * scale) * s2;
-                xv[lane + 64] = (a1 * scale) * s2;
-            }
-            if (w == 2 * NL && lane < nl) {
-                const float ab = cld(a.b.proj + (int64_t)lane * DN_ROWS + DN_ALPHA + vh) + dtb;
-                s.g[lane] = oxe_libm::expf_c(softplus_c(ab) * sa);
-                s.b[lane] = sigmoid_c(cld(a.b.proj + (int64_t)lane * DN_ROWS + DN_BETA + vh));
-            }
+        // l2 norms of q (wave 2 l) and k (wave 2 l + 1)
+        if (w < 2 * NL && (w >> 1) < nl) {
+            const int l = w >> 1;
+            float *xv = (w & 1) ? s.k[l] : s.q[l];
+            const float a0 = xv[lane], a1 = xv[lane + 64];
+            const float nf = (float)DS;
+            const float mean = wave_mean_sq_128(a0, a1, xv);
+            const float scale = 1.0f / sqrtf(mean + a.m.eps / nf);
+            const float sq = 1.0f / sqrtf(nf);
+            xv[lane] = (a0 * scale) * sq;
+            xv[lane + 64] = (a1 * scale) * sq;
         }
         __syncthreads();
         tr_mark(c, 122);
+        // delta rule per lane; the new states are kept in registers and stored after the count
         const float scale = 1.0f / sqrtf((float)HV);
-        for (int l = 0; l < nl; l++) {
-            const float eg = s.g[l], beta = s.b[l];
+        float stl[NL][8];
+        if (dlt) {
 #pragma unroll
-            for (int h = 0; h < 4; h++) {
-                const int j = rg + 32 * h;
+            for (int l = 0; l < NL; l++) {
+                if (l >= nl) break;
+                const float eg = s.g[l], beta = s.b[l];
                 float acc = 0.0f;
 #pragma unroll
                 for (int q = 0; q < 8; q++) {
-                    r[h][q] = r[h][q] * eg;
-                    acc = __builtin_fmaf(r[h][q], s.k[l][cc + 16 * q], acc);
+                    r[q] = r[q] * eg;
+                    acc = __builtin_fmaf(r[q], s.k[l][cc + 16 * q], acc);
                 }
-                const float s1 = dot16_tree_f(acc);
-                const float delta = (s.v[l][j] - s1) * beta;
+                const float sk = dot16_tree_f(acc);
+                const float delta = (s.v[l][rg] - sk) * beta;
                 acc = 0.0f;
 #pragma unroll
                 for (int q = 0; q < 8; q++) {
-                    r[h][q] = __builtin_fmaf(s.k[l][cc + 16 * q], delta, r[h][q]);
-                    acc = __builtin_fmaf(r[h][q], s.q[l][cc + 16 * q], acc);
+                    r[q] = __builtin_fmaf(s.k[l][cc + 16 * q], delta, r[q]);
+                    acc = __builtin_fmaf(r[q], s.q[l][cc + 16 * q], acc);
+                    stl[l][q] = r[q];
                 }
-                const float s2 = dot16_tree_f(acc);
-                float *dst = ssm + (int64_t)((cur + l + 1) % OXE_NSLOTS) * ssm_slot + ((int64_t)vh * HV + j) * HV;
-#pragma unroll
-                for (int q = 0; q < 8; q++) dst[cc + 16 * q] = r[h][q];
-                if (cc == 0) s.o[l][j] = s2 * scale;
+                const float sq = dot16_tree_f(acc);
+                if (cc == 0) cst(a.b.gdn + (int64_t)l * DIN + vh * HV + row0 + rg, sq * scale);
             }
         }
+        // count this workgroup in once its outputs are visible device-wide
+        __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
-        tr_mark(c, 123);
-        {
-            const int w = t >> 6, lane = t & 63;
-            if (w < nl) {
-                const int l = w;
-                const float x0 = s.o[l][lane], x1 = s.o[l][lane + 64];
-                const float mean = wave_mean_sq_128(x0, x1, s.o[l]);
-                const float sc = 1.0f / sqrtf(mean + a.m.eps);
-                const float *z = a.b.proj + (int64_t)l * DN_ROWS + DN_Z + vh * HV;
-                const float o0 = ((x0 * sc) * L.ssm_norm[lane]) * v_silu(cld(z + lane));
-                const float o1 = ((x1 * sc) * L.ssm_norm[lane + 64]) * v_silu(cld(z + lane + 64));
-                float m0 = __builtin_fabsf(o0), m1 = __builtin_fabsf(o1);
-                for (int mm = 16; mm >= 1; mm >>= 1) {
-                    m0 = fmaxf(m0, shfl_xor_f(m0, mm));
-                    m1 = fmaxf(m1, shfl_xor_f(m1, mm));
-                }
-                const float d0 = m0 / 127.0f, d1 = m1 / 127.0f;
-                const float id0 = d0 != 0.0f ? 1.0f / d0 : 0.0f, id1 = d1 != 0.0f ? 1.0f / d1 : 0.0f;
-                const int32_t q0 = (int32_t)__builtin_rintf(o0 * id0), q1 = (int32_t)__builtin_rintf(o1 * id1);
-                // pack 4 consecutive codes per word: lanes 4k..4k+3
-                uint32_t p0 = (uint32_t)(q0 & 0xff), p1 = (uint32_t)(q1 & 0xff);
-                const int sh = 8 * (lane & 3);
-                p0 <<= sh;
-                p1 <<= sh;
-                p0 |= (uint32_t)shfl_xor_i((int)p0, 1);
-                p1 |= (uint32_t)shfl_xor_i((int)p1, 1);
-                p0 |= (uint32_t)shfl_xor_i((int)p0, 2);
-                p1 |= (uint32_t)shfl_xor_i((int)p1, 2);
-                int8_t *q = a.b.oq + (int64_t)l * DIN + vh * HV;
-                if ((lane & 3) == 0) {
-                    cst32(q + lane, p0);
-                    cst32(q + lane + 64, p1);
-                }
-                uint16_t *d = a.b.od + (int64_t)l * (DIN / 32) + vh * (HV / 32);
-                if (lane == 0) { cst16(d + 0, f2h(d0)); cst16(d + 2, f2h(d1)); }
-                if (lane == 32) { cst16(d + 1, f2h(d0)); cst16(d + 3, f2h(d1)); }
+        if (t == 0) {
+            const uint32_t old =
+                __hip_atomic_fetch_add(&a.sync[FZ_W_HEAD + 32 * vh], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            s.last = (old % DN_WPH) == DN_WPH - 1;
+        }
+        __syncthreads();
+        const bool last = s.last != 0;
+        float x0 = 0.0f, x1 = 0.0f, z0 = 0.0f, z1 = 0.0f;
+        if (last && w < nl) {
+            const float *o = a.b.gdn + (int64_t)w * DIN + vh * HV;
+            const float *z = a.b.proj + (int64_t)w * DN_ROWS + DN_Z + vh * HV;
+            x0 = cld(o + lane); x1 = cld(o + lane + 64);
+            z0 = cld(z + lane); z1 = cld(z + lane + 64);
+        }
+        if (dlt) {
+#pragma unroll
+            for (int l = 0; l < NL; l++) {
+                if (l >= nl) break;
+                float *dst = ssm + (int64_t)((cur + l + 1) % OXE_NSLOTS) * ssm_slot + ((int64_t)vh * HV + row0 + rg) * HV;
+#pragma unroll
+                for (int q = 0; q < 8; q++) dst[cc + 16 * q] = stl[l][q];
             }
+        }
+        tr_mark(c, 123);
+        // gated norm (oxe_ops.cpp:19-49 rms + ssm_norm * silu(z)) and Q8_0 quantization of the head
+        if (last && w < nl) {
+            const int l = w;
+            s.o[l][lane] = x0;
+            s.o[l][lane + 64] = x1;
+            const float mean = wave_mean_sq_128(x0, x1, s.o[l]);
+            const float sc = 1.0f / sqrtf(mean + a.m.eps);
+            const float o0 = ((x0 * sc) * nw0) * v_silu(z0);
+            const float o1 = ((x1 * sc) * nw1) * v_silu(z1);
+            float d0, d1;
+            const uint32_t p0 = quant32_lanes(o0, &d0), p1 = quant32_lanes(o1, &d1);
+            int8_t *q = a.b.oq + (int64_t)l * DIN + vh * HV;
+            if ((lane & 3) == 0) {
+                cst32(q + lane, p0);
+                cst32(q + lane + 64, p1);
+            }
+            uint16_t *d = a.b.od + (int64_t)l * (DIN / 32) + vh * (HV / 32);
+            if (lane == 0) { cst16(d + 0, f2h(d0)); cst16(d + 2, f2h(d1)); }
+            if (lane == 32) { cst16(d + 1, f2h(d0)); cst16(d + 3, f2h(d1)); }
         }
     }
     tr_end(c, TP_DN);
@@ -870,17 +906,21 @@ FZ_PHASE bool phase_moe(const RunCtl *ctl, const FusedArgs *ap, int il) {
     __syncthreads();
     tr_mark(c, 106);
     if (t < 64) {
+        // union in first-use order (lane-major, engine.rs:3458-3475): entry t (lane t / 8, rank
+        // t % 8) is new when no earlier entry names its expert; its union slot is the number of
+        // new entries before its first occurrence
         const int e = t < nl * KUSED ? ps.ro.ids[t / KUSED][t % KUSED] : -1;
-        bool isnew = e >= 0;
+        int first = t;
 #pragma unroll
-        for (int u = 0; u < NL * KUSED; u++) {
-            const int o = __shfl(e, u);
-            isnew &= !(u < t && o == e);
+        for (int u = NL * KUSED - 1; u >= 0; u--) {
+            const int o = __builtin_amdgcn_readlane(e, u);
+            first = (o == e && u < first) ? u : first;
         }
+        const bool isnew = e >= 0 && first == t;
         const unsigned long long mask = __ballot(isnew);
         const int n = __popcll(mask);
-        const int pos = __popcll(mask & ((1ull << t) - 1));
-        if (isnew) ps.uni[pos] = e;
+        if (isnew) ps.uni[__popcll(mask & ((1ull << t) - 1))] = e;
+        if (t < NL * KUSED) ps.slot[t / KUSED][t % KUSED] = e >= 0 ? __popcll(mask & ((1ull << first) - 1)) : 0;
         if (t == 0) ps.nu = n;
         if (b == 0 && t == 0) {
             if (ps.ro.tie) atomicAdd(a.b.counters + CNT_ERR_TIE, 1u);
@@ -890,16 +930,6 @@ FZ_PHASE bool phase_moe(const RunCtl *ctl, const FusedArgs *ap, int il) {
     }
     __syncthreads();
     const int nu = ps.nu < 0 ? 0 : (ps.nu > OXE_MAX_UNION ? OXE_MAX_UNION : ps.nu);
-    if (t < NL * KUSED) {
-        // union slot of each lane's rank-j expert
-        const int l = t / KUSED, j = t % KUSED;
-        int sl = 0;
-        if (l < nl)
-            for (int u = 0; u < nu; u++)
-                if (ps.uni[u] == ps.ro.ids[l][j]) sl = u;
-        ps.slot[l][j] = sl;
-    }
-    __syncthreads();
     tr_mark(c, 101);
     // 2. weight loads: this group's gate/up rows, and the down rows of every union expert + shared
     const bool gw = b < nu * 16;
@@ -916,18 +946,16 @@ FZ_PHASE bool phase_moe(const RunCtl *ctl, const FusedArgs *ap, int il) {
         tr_mark(c, 103);
         wdot<E, 16, NL>(ew, 64, &se.xq[0][0], E, &se.xd[0][0], E / 32, se.g);
         tr_mark(c, 104);
-        if (t < NL * 32) {
+        if (t < 64) {
+            // swiglu of the group's 32 h values of lane l = t / 32 (half wave), then Q8_0
+            static_assert(NL * 32 <= 64, "one wave");
             const int l = t / 32, i = t % 32, tl = i >> 3, r = i & 7;
-            se.h[l][i] = v_silu(se.g.out[l][tl * 16 + r]) * se.g.out[l][tl * 16 + 8 + r];
+            const float hv = l < NL ? v_silu(se.g.out[l < NL ? l : 0][tl * 16 + r]) * se.g.out[l < NL ? l : 0][tl * 16 + 8 + r] : 0.0f;
+            float dd;
+            const uint32_t word = quant32_lanes(hv, &dd);
+            if (l < nl && (i & 3) == 0) cst32(a.hq + ((int64_t)l * OXE_MAX_UNION + u_g) * FF + gq * 32 + i, word);
+            if (l < nl && i == 0) cst16(a.hd + ((int64_t)l * OXE_MAX_UNION + u_g) * (FF / 32) + gq, f2h(dd));
         }
-        __syncthreads();
-        if (t < NL) quant_block_q8_0(se.h[t], se.hq[t], &se.hd[t]);
-        __syncthreads();
-        if (t < NL * 8) {
-            const int l = t / 8, k = t % 8;
-            if (l < nl) cst32(a.hq + ((int64_t)l * OXE_MAX_UNION + u_g) * FF + gq * 32 + 4 * k, *(const uint32_t *)&se.hq[l][4 * k]);
-        }
-        if (t < nl) cst16(a.hd + ((int64_t)t * OXE_MAX_UNION + u_g) * (FF / 32) + gq, se.hd[t]);
     }
     tr_end(c, TP_EXPERTS);
     tr_start(c);
@@ -991,19 +1019,18 @@ FZ_PHASE bool phase_moe(const RunCtl *ctl, const FusedArgs *ap, int il) {
         x1v = cld(a.b.x1 + (int64_t)(t / 8) * E + r0 + t % 8);
         sgv = cld(a.b.sh_gate + t / 8);
     }
+    // Q8_0 of the shared expert's h: element t of lane k in thread t, a block per half wave
+    static_assert(FFSH == FT, "one shared-expert element per thread and lane");
 #pragma unroll
-    for (int k = 0; k < NL * FFSH / FT; k++) {
-        const int i = t + FT * k;
-        sd.hs[i / FFSH][i % FFSH] = hsv[k];
+    for (int k = 0; k < NL; k++) {
+        float dd;
+        const uint32_t word = quant32_lanes(hsv[k], &dd);
+        if ((t & 3) == 0) *(uint32_t *)&sd.hq[k][OXE_MAX_UNION][t] = word;
+        if ((t & 31) == 0) sd.hd[k][OXE_MAX_UNION][t / 32] = f2h(dd);
     }
     if (t < DW_UNITS * 16) {
         uint32_t *d = &sd.wd[su][srr * (FF / 64 + 1) + shf * 4];
         d[0] = dsc.x; d[1] = dsc.y; d[2] = dsc.z; d[3] = dsc.w;
-    }
-    __syncthreads();
-    if (t < NL * (FFSH / 32)) {
-        const int l = t / (FFSH / 32), bb = t % (FFSH / 32);
-        quant_block_q8_0(&sd.hs[l][32 * bb], &sd.hq[l][OXE_MAX_UNION][32 * bb], &sd.hd[l][OXE_MAX_UNION][bb]);
     }
 #pragma unroll
     for (int k = 0; k < NL * OXE_MAX_UNION * (FF / 16) / FT; k++) {
@@ -1073,9 +1100,9 @@ OXE_DEV h2t u2h2f(uint32_t u) { return __builtin_bit_cast(h2t, u); }
 OXE_DEV uint32_t h22uf(h2t v) { return __builtin_bit_cast(uint32_t, v); }
 OXE_DEV float f16x8_reduce_q(h2t acc[4]) {
 #pragma unroll
-    for (int i = 0; i < 4; i++) acc[i] = acc[i] + u2h2f(__shfl_xor(h22uf(acc[i]), 2, 64));
+    for (int i = 0; i < 4; i++) acc[i] = acc[i] + u2h2f((uint32_t)dpp_i<DPP_XOR2>((int)h22uf(acc[i])));
 #pragma unroll
-    for (int i = 0; i < 4; i++) acc[i] = acc[i] + u2h2f(__shfl_xor(h22uf(acc[i]), 1, 64));
+    for (int i = 0; i < 4; i++) acc[i] = acc[i] + u2h2f((uint32_t)dpp_i<DPP_XOR1>((int)h22uf(acc[i])));
     const float t0 = (float)acc[0].x + (float)acc[2].x;
     const float t1 = (float)acc[0].y + (float)acc[2].y;
     const float t2 = (float)acc[1].x + (float)acc[3].x;
@@ -1093,134 +1120,126 @@ FZ_PHASE bool phase_scores(const RunCtl *ctl, const FusedArgs *ap, int il, bool 
     auto &s = c.sm->sc;
     const int t = threadIdx.x, w = t >> 6, lane = t & 63, nl = c.nl;
     const int pos0 = c.ctl->pos0, pmax = pos0 + nl - 1;
-    const int kvh = c.b % NKV, chunk = c.b / NKV;
-    const bool act = chunk * SC_P <= pmax;
-    // the K rows of this workgroup's cached positions (< pos0) go straight to LDS (one DMA load of
-    // 16 bytes per lane; 64 lanes fill 1 KB contiguous), shared by both lanes of the run
-    const int npre = act && !seed_only ? (pos0 - chunk * SC_P < SC_P ? pos0 - chunk * SC_P : SC_P) : 0;
-    if (npre > 0) {
-        const uint4 *src = (const uint4 *)(kcache_layer(a, L) + ((int64_t)kvh * a.m.n_ctx + chunk * SC_P) * HD);
+    // workgroup (kvh, chunk0) takes position chunks chunk0, chunk0 + G / 2, ... (16 positions each)
+    const int kvh = c.b % NKV, cstride = c.G / NKV, chunk0 = c.b / NKV;
+    const bool act = chunk0 * SC_P <= pmax;
+    // the first chunk's cached K rows (positions < pos0): thread = (position t / 32, 16-byte part)
+    const uint16_t *kcl = kcache_layer(a, L) + (int64_t)kvh * a.m.n_ctx * HD;
+    const int kp = t >> 5, kpart = t & 31;
+    uint4 kpre = make_uint4(0, 0, 0, 0);
+    if (act && !seed_only && chunk0 * SC_P + kp < pos0) kpre = *(const uint4 *)(kcl + (int64_t)(chunk0 * SC_P + kp) * HD + 8 * kpart);
+    // per wave, its vectors' norm weights and RoPE rows (read-only), before the barrier
+    const int kjob = w;                          // waves 0..NL-1: K row of lane w
+    const int pk = pos0 + kjob;
+    const int pkc = pk / SC_P;                   // the chunk holding position pk
+    const bool kdo = act && kjob < nl && pkc >= chunk0 && (pkc - chunk0) % cstride == 0;
+    const bool qdo = act && !seed_only;
+    float kw[4], qw[4];
 #pragma unroll
-        for (int k = 0; k < SC_P * HD / 8 / FT; k++) {
-            const int i = t + FT * k;                 // 16-byte chunk i: position i / 32, part i % 32
-            if (i / (HD / 8) < npre)
-                __builtin_amdgcn_global_load_lds((const void *)(src + i),
-                                                 (__attribute__((address_space(3))) void *)((uint4 *)&s.krows[0][0] + (i - (t & 63))),
-                                                 16, 0, 0);
-        }
+    for (int i = 0; i < 4; i++) {
+        kw[i] = kdo ? L.k_norm[lane + 64 * i] : 0.0f;
+        qw[i] = qdo ? L.q_norm[lane + 64 * i] : 0.0f;
+    }
+    const int rl = lane & (NROT / 2 - 1);
+    float kcs[2] = {0.0f, 0.0f}, qcs[(NL * GQA + 7) / 8][2];
+    if (kdo) { kcs[0] = a.m.rope[(int64_t)pk * NROT + 2 * rl]; kcs[1] = a.m.rope[(int64_t)pk * NROT + 2 * rl + 1]; }
+#pragma unroll
+    for (int k = 0; k < (NL * GQA + 7) / 8; k++) {
+        const int l = (w + 8 * k) / GQA;
+        const bool on = qdo && w + 8 * k < NL * GQA && l < nl;
+        qcs[k][0] = on ? a.m.rope[(int64_t)(pos0 + l) * NROT + 2 * rl] : 0.0f;
+        qcs[k][1] = on ? a.m.rope[(int64_t)(pos0 + l) * NROT + 2 * rl + 1] : 0.0f;
     }
     if (!wait(c.bar, &c.ps->ok)) return false;
     tr_pass(c);
-    // step 1: raw K rows of the run's positions in this range, and the raw queries, into LDS
-    // (one wave per vector); step 2: the norms; step 3: RoPE; step 4: f16 (and K cache rows)
-    const int kjob = w;                          // waves 0..NL-1: K row of lane w
-    const int pk = pos0 + kjob;
-    const bool kdo = act && kjob < nl && pk >= chunk * SC_P && pk < (chunk + 1) * SC_P;
+    // each wave takes its vectors (the K row of lane w on waves w < NL in range; queries job
+    // w + 8 k = (lane job / 8, head job % 8)) through raw -> rms norm * weight -> RoPE -> f16 on
+    // its own: lane c holds elements c + 64 i; RoPE pairs (c, c + 32) for c < 32 (slot 0)
     float kv4[4], qv4[(NL * GQA + 7) / 8][4];
     if (kdo) {
         const float *kr = a.b.proj + (int64_t)kjob * DN_ROWS + AT_K + kvh * HD;
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            kv4[i] = cld(kr + lane + 64 * i);
-            s.ktmp[kjob][lane + 64 * i] = kv4[i];
-        }
+        for (int i = 0; i < 4; i++) kv4[i] = cld(kr + lane + 64 * i);
     }
 #pragma unroll
     for (int k = 0; k < (NL * GQA + 7) / 8; k++) {
         const int job = w + 8 * k, l = job / GQA, h = kvh * GQA + job % GQA;
-        if (act && !seed_only && job < NL * GQA && l < nl) {
+        if (qdo && job < NL * GQA && l < nl) {
             const float *q = a.b.proj + (int64_t)l * DN_ROWS + h * 2 * HD;
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                qv4[k][i] = cld(q + lane + 64 * i);
-                s.tmp[w + 8 * k][lane + 64 * i] = qv4[k][i];
-            }
+            for (int i = 0; i < 4; i++) qv4[k][i] = cld(q + lane + 64 * i);
         }
     }
-    __syncthreads();
-    if (kdo) {
-        const float mean = wave_mean_sq_256(kv4, s.ktmp[kjob]);
+    auto finish = [&](float v[4], const float wt[4], const float cs[2], float *replay, uint16_t *dst) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) replay[lane + 64 * i] = v[i];
+        const float mean = wave_mean_sq_256(v, replay);
         const float scale = 1.0f / sqrtf(mean + a.m.eps);
 #pragma unroll
-        for (int i = 0; i < 4; i++) kv4[i] = (kv4[i] * scale) * L.k_norm[lane + 64 * i];
-    }
+        for (int i = 0; i < 4; i++) v[i] = (v[i] * scale) * wt[i];
+        const float o = __shfl_xor(v[0], NROT / 2, 64);
+        if (lane < NROT / 2) v[0] = __builtin_fmaf(v[0], cs[0], -(o * cs[1]));
+        else if (lane < NROT) v[0] = __builtin_fmaf(o, cs[1], v[0] * cs[0]);
 #pragma unroll
-    for (int k = 0; k < (NL * GQA + 7) / 8; k++) {
-        const int job = w + 8 * k, l = job / GQA;
-        if (act && !seed_only && job < NL * GQA && l < nl) {
-            const float mean = wave_mean_sq_256(qv4[k], s.tmp[job]);
-            const float scale = 1.0f / sqrtf(mean + a.m.eps);
-#pragma unroll
-            for (int i = 0; i < 4; i++) qv4[k][i] = (qv4[k][i] * scale) * L.q_norm[lane + 64 * i];
-        }
-    }
-    __syncthreads();
-    if (kdo)
-#pragma unroll
-        for (int i = 0; i < 4; i++) s.ktmp[kjob][lane + 64 * i] = kv4[i];
-#pragma unroll
-    for (int k = 0; k < (NL * GQA + 7) / 8; k++) {
-        const int job = w + 8 * k, l = job / GQA;
-        if (act && !seed_only && job < NL * GQA && l < nl)
-#pragma unroll
-            for (int i = 0; i < 4; i++) s.tmp[job][lane + 64 * i] = qv4[k][i];
-    }
-    __syncthreads();
-    if (kdo) rope_neox_lds(s.ktmp[kjob], a.m.rope + (int64_t)pk * NROT, lane);
-#pragma unroll
-    for (int k = 0; k < (NL * GQA + 7) / 8; k++) {
-        const int job = w + 8 * k, l = job / GQA;
-        if (act && !seed_only && job < NL * GQA && l < nl) rope_neox_lds(s.tmp[job], a.m.rope + (int64_t)(pos0 + l) * NROT, lane);
-    }
-    __syncthreads();
+        for (int i = 0; i < 4; i++) dst[lane + 64 * i] = f2h(v[i]);
+    };
     if (kdo) {
+        finish(kv4, kw, kcs, s.ktmp[kjob], s.knew[kjob]);
         uint16_t *kc = kcache_layer(a, L);
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const uint16_t h = f2h(s.ktmp[kjob][lane + 64 * i]);
-            s.knew[kjob][lane + 64 * i] = h;
-            kc[((int64_t)kvh * a.m.n_ctx + pk) * HD + lane + 64 * i] = h;
-        }
+        for (int i = 0; i < 4; i++) kc[((int64_t)kvh * a.m.n_ctx + pk) * HD + lane + 64 * i] = s.knew[kjob][lane + 64 * i];
     }
 #pragma unroll
     for (int k = 0; k < (NL * GQA + 7) / 8; k++) {
         const int job = w + 8 * k, l = job / GQA;
-        if (act && !seed_only && job < NL * GQA)
+        if (qdo && job < NL * GQA) {
+            if (l < nl) finish(qv4[k], qw, qcs[k], s.tmp[job], s.q[job]);
+            else
 #pragma unroll
-            for (int i = 0; i < 4; i++) s.q[job][lane + 64 * i] = l < nl ? f2h(s.tmp[job][lane + 64 * i]) : (uint16_t)0;
+                for (int i = 0; i < 4; i++) s.q[job][lane + 64 * i] = 0;
+        }
     }
     __syncthreads();
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
+    tr_mark(c, 151);
     if (act && !seed_only) {
-        // thread = (lane l, position p, chain quad j): the 8 heads of the group for one lane
-        const int l = t >> 8, tt = t & 255;
-        const int p = chunk * SC_P + (tt >> 2), j = tt & 3;
-        if (l < nl && p <= pos0 + l) {
-            const uint16_t *krow = p < pos0 ? s.krows[p - chunk * SC_P] : s.knew[p - pos0];
-            h2t acc[GQA][4];
+        // thread = (lane l, head pair hq, position pp of the chunk, chain quad j)
+        const int l = t >> 8, hq = (t >> 6) & 3, pp = (t >> 2) & (SC_P - 1), j = t & 3;
+        for (int chunk = chunk0; chunk * SC_P <= pmax; chunk += cstride) {
+            const int cb = chunk * SC_P;
+            if (chunk == chunk0) {
+                if (cb + kp < pos0) *(uint4 *)&s.krows[kp][8 * kpart] = kpre;
+            } else if (cb + kp < pos0) {
+                *(uint4 *)&s.krows[kp][8 * kpart] = *(const uint4 *)(kcl + (int64_t)(cb + kp) * HD + 8 * kpart);
+            }
+            __syncthreads();
+            const int p = cb + pp;
+            if (l < nl && p <= pos0 + l) {
+                const uint16_t *krow = p < pos0 ? s.krows[pp] : s.knew[p - pos0];
+                h2t acc[2][4];
 #pragma unroll
-            for (int q = 0; q < GQA; q++)
+                for (int q = 0; q < 2; q++)
 #pragma unroll
-                for (int i = 0; i < 4; i++) acc[q][i] = h2t{(_Float16)0.0f, (_Float16)0.0f};
-#pragma unroll 2
-            for (int sx = 0; sx < HD / 32; sx++) {
-                const uint4 kv = *(const uint4 *)(krow + 32 * sx + 8 * j);
-                const h2t k0 = u2h2f(kv.x), k1 = u2h2f(kv.y), k2 = u2h2f(kv.z), k3 = u2h2f(kv.w);
+                    for (int i = 0; i < 4; i++) acc[q][i] = h2t{(_Float16)0.0f, (_Float16)0.0f};
 #pragma unroll
-                for (int q = 0; q < GQA; q++) {
-                    const uint4 qv = *(const uint4 *)(&s.q[l * GQA + q][32 * sx + 8 * j]);
-                    acc[q][0] = __builtin_elementwise_fma(k0, u2h2f(qv.x), acc[q][0]);
-                    acc[q][1] = __builtin_elementwise_fma(k1, u2h2f(qv.y), acc[q][1]);
-                    acc[q][2] = __builtin_elementwise_fma(k2, u2h2f(qv.z), acc[q][2]);
-                    acc[q][3] = __builtin_elementwise_fma(k3, u2h2f(qv.w), acc[q][3]);
+                for (int sx = 0; sx < HD / 32; sx++) {
+                    const uint4 kv = *(const uint4 *)(krow + 32 * sx + 8 * j);
+                    const h2t k0 = u2h2f(kv.x), k1 = u2h2f(kv.y), k2 = u2h2f(kv.z), k3 = u2h2f(kv.w);
+#pragma unroll
+                    for (int q = 0; q < 2; q++) {
+                        const uint4 qv = *(const uint4 *)(&s.q[l * GQA + 2 * hq + q][32 * sx + 8 * j]);
+                        acc[q][0] = __builtin_elementwise_fma(k0, u2h2f(qv.x), acc[q][0]);
+                        acc[q][1] = __builtin_elementwise_fma(k1, u2h2f(qv.y), acc[q][1]);
+                        acc[q][2] = __builtin_elementwise_fma(k2, u2h2f(qv.z), acc[q][2]);
+                        acc[q][3] = __builtin_elementwise_fma(k3, u2h2f(qv.w), acc[q][3]);
+                    }
+                }
+#pragma unroll
+                for (int q = 0; q < 2; q++) {
+                    const float sc = f16x8_reduce_q(acc[q]);
+                    if (j == 0) cst(a.b.scores + ((int64_t)l * NH + kvh * GQA + 2 * hq + q) * a.m.n_ctx + p, sc);
                 }
             }
-#pragma unroll
-            for (int q = 0; q < GQA; q++) {
-                const float sc = f16x8_reduce_q(acc[q]);
-                if (j == 0) cst(a.b.scores + ((int64_t)l * NH + kvh * GQA + q) * a.m.n_ctx + p, sc);
-            }
+            __syncthreads();
         }
     }
     tr_end(c, TP_SCORES);
@@ -1228,7 +1247,17 @@ FZ_PHASE bool phase_scores(const RunCtl *ctl, const FusedArgs *ap, int il, bool 
     return true;
 }
 
-// softmax + V^T . p + gate + Q8_0 (k_attn.hip pv_kernel), workgroup = (kv head, lane, 32 dims)
+// Attention output (k_attn.hip pv_kernel's arithmetic): workgroup (kv head kvh, lane l, 32-dim
+// chunk) for the GQA group's 8 heads. Wave hh forms head hh's softmax (oxe_soft_max_f32,
+// oxe_ops.cpp:101-115) in one pass over its scores, held in registers (up to PV_SMK groups of 4
+// positions per lane; longer rows take three passes). Thread (d = t / 16, cp = t % 16) then runs
+// chain pair cp of ggml_vec_dot_f16 (positions 32 s + 2 cp and +1: accumulator cp / 4, halves
+// 2 (cp % 4) and +1) for dim d and all 8 heads; its V^T words of earlier launches are loaded
+// before the barrier. The F16x8 reduce is done by lane moves inside the 16-lane row of dim d.
+constexpr int PV_SMK = 8;    // softmax groups per lane in registers (n_kv <= 2048)
+constexpr int PV_VR = 32;    // V^T words per thread in registers (n_kv <= 1024)
+constexpr int PVD = 32;      // dims per workgroup (one Q8_0 block per head)
+
 template <int NL>
 FZ_PHASE bool phase_pv(const RunCtl *ctl, const FusedArgs *ap, int il) {
     Ctx<NL> c = make_ctx<NL>(ctl, ap);
@@ -1236,21 +1265,23 @@ FZ_PHASE bool phase_pv(const RunCtl *ctl, const FusedArgs *ap, int il) {
     const LayerDev &L = ap->layers[il];
     const FusedArgs &a = *c.a;
     const int t = threadIdx.x, nl = c.nl;
-    constexpr int PVD = 32;
     const int dchunk = c.b % (HD / PVD);
     const int l = (c.b / (HD / PVD)) % NL;
     const int kvh = c.b / ((HD / PVD) * NL);
     const bool act = kvh < NKV && l < nl;
-    // the first V^T chunks of this thread's row that hold only earlier positions, before the barrier
-    constexpr int PV_PRE = 8;
-    uint4 vpre[PV_PRE];
-    const int vj = t & 3, vd = (t >> 2) & (PVD - 1);
-    const int pos0_ = c.ctl->pos0;
-    const uint16_t *vrow_ = a.m.vcache + (int64_t)L.index * NKV * HD * a.m.n_ctx +
-                            (int64_t)(kvh * HD + (dchunk * PVD + vd)) * a.m.n_ctx;
+    const int n_ctx = a.m.n_ctx;
+    const int pos0 = c.ctl->pos0, pos = pos0 + l;
+    int n_kv = (pos + 1 + 255) / 256 * 256;
+    if (n_kv < 256) n_kv = 256;
+    if (n_kv > n_ctx) n_kv = n_ctx;
+    const int ns = n_kv / 32;
+    const int d = t >> 4, cp = t & 15, dg = dchunk * PVD + d;
+    const uint16_t *vrow = a.m.vcache + (int64_t)L.index * NKV * HD * n_ctx + (int64_t)(kvh * HD + dg) * n_ctx + 2 * cp;
+    // V^T words holding only positions written by earlier launches, before the barrier
+    uint32_t vr[PV_VR];
 #pragma unroll
-    for (int k = 0; k < PV_PRE; k++)
-        vpre[k] = (act && 32 * k + 31 < pos0_) ? *(const uint4 *)(vrow_ + 32 * k + 8 * vj) : make_uint4(0, 0, 0, 0);
+    for (int s = 0; s < PV_VR; s++)
+        vr[s] = (act && s < ns && 32 * s + 2 * cp + 1 < pos0) ? *(const uint32_t *)(vrow + 32 * s) : 0u;
     if (!wait(c.bar, &c.ps->ok)) return false;
     tr_pass(c);
     if (!act && c.b >= NKV * NL * (HD / PVD) && il + 1 < a.n_layer) {
@@ -1262,118 +1293,160 @@ FZ_PHASE bool phase_pv(const RunCtl *ctl, const FusedArgs *ap, int il) {
         warm(N.proj.d, (size_t)rows * (E / 32) * 2, c.b - idle0, c.G - idle0, a.sync + FZ_W_ERR + 32);
     }
     if (act) {
-        const int n_ctx = a.m.n_ctx;
-        uint16_t *s_p = (uint16_t *)c.dyn;                                        // [GQA][n_kv] f16 probabilities
-        float *s_gs = (float *)(c.dyn + (size_t)GQA * ((n_ctx + 1) & ~1) * 2);    // [GQA][n_kv / 4] group sums
-        float *s_o = (float *)(((uintptr_t)(s_gs + (size_t)GQA * (n_ctx / 4)) + 15) & ~(uintptr_t)15);   // [GQA][PVD]
-        const int pos = c.ctl->pos0 + l;
-        const int pos0 = c.ctl->pos0;
-        int n_kv = (pos + 1 + 255) / 256 * 256;
-        if (n_kv < 256) n_kv = 256;
-        if (n_kv > n_ctx) n_kv = n_ctx;
+        uint32_t *s_pp = (uint32_t *)c.dyn;                                  // [n_kv / 2][GQA] f16 pairs
+        float *s_gs = (float *)(c.dyn + (size_t)GQA * n_ctx * 2);           // [GQA][n_ctx / 4] group sums
+        float *s_o = s_gs + (size_t)GQA * (n_ctx / 4);                       // [GQA][PVD]
+        // this thread's gate (head cp < 8, dim dg) and the V^T words of this launch's positions
+        float sg = 0.0f;
+        if (cp < GQA) sg = cld(a.b.proj + (int64_t)l * DN_ROWS + (kvh * GQA + cp) * 2 * HD + HD + dg);
+#pragma unroll
+        for (int s = 0; s < PV_VR; s++)
+            if (s < ns && 32 * s + 2 * cp + 1 >= pos0) vr[s] = cld32(vrow + 32 * s);
         const float scale = 1.0f / sqrtf((float)HD);
-        // softmax of head hh = wave w (oxe_soft_max_f32, oxe_ops.cpp:101-115): wp = s * scale
-        // (masked: -inf), max, e = v_expf(wp - max) with group sums (e0 + e1) + (e2 + e3) added in
-        // double, p = f16(e * f32(1 / sum)). Lane k owns groups k, k + 64, ... (4 consecutive positions).
         {
+            // softmax of head hh = wave w: wp = s * scale (masked: -inf), max, e = v_expf(wp - max)
+            // with group sums (e0 + e1) + (e2 + e3) added in double, p = f16(e * f32(1 / sum))
             const int hh = t >> 6, lane = t & 63, h = kvh * GQA + hh;
             const float *sc = a.b.scores + ((int64_t)l * NH + h) * n_ctx;
+            float *gs = s_gs + (size_t)hh * (n_ctx / 4);
+            const int ng = n_kv / 4;
             float mx = -__builtin_inff();
-            for (int g = lane; g < n_kv / 4; g += 64) {
-                const uint4 v = cld128(sc + 4 * g);
-                const float f4[4] = {__builtin_bit_cast(float, v.x), __builtin_bit_cast(float, v.y),
-                                     __builtin_bit_cast(float, v.z), __builtin_bit_cast(float, v.w)};
+            double part = 0.0;
+            if (ng <= 64 * PV_SMK) {
+                float e[PV_SMK][4];
 #pragma unroll
-                for (int k = 0; k < 4; k++) {
-                    const float wv = 4 * g + k <= pos ? f4[k] * scale : -__builtin_inff();
-                    mx = (mx > wv) ? mx : wv;
+                for (int k = 0; k < PV_SMK; k++) {
+                    const int g = lane + 64 * k;
+                    const uint4 v = g < ng ? cld128(sc + 4 * g) : make_uint4(0, 0, 0, 0);
+                    const uint32_t u[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        e[k][i] = (g < ng && 4 * g + i <= pos) ? __builtin_bit_cast(float, u[i]) * scale : -__builtin_inff();
+                        mx = (mx > e[k][i]) ? mx : e[k][i];
+                    }
+                }
+                mx = wave_max_any(mx);
+#pragma unroll
+                for (int k = 0; k < PV_SMK; k++) {
+                    const int g = lane + 64 * k;
+                    if (g < ng) {
+#pragma unroll
+                        for (int i = 0; i < 4; i++) e[k][i] = v_expf(e[k][i] - mx);
+                        const float gsum = (e[k][0] + e[k][1]) + (e[k][2] + e[k][3]);
+                        gs[g] = gsum;
+                        part += (double)gsum;
+                    }
+                }
+                const double P = wave_sum_d_any(part);
+                float f;
+                if (!bracket_ok_recip(P, P, ng, &f)) {
+                    double sum = 0.0;
+                    for (int g = 0; g < ng; g++) sum += (double)gs[g];
+                    f = (float)(1.0 / sum);
+                }
+#pragma unroll
+                for (int k = 0; k < PV_SMK; k++) {
+                    const int g = lane + 64 * k;
+                    if (g < ng) {
+                        s_pp[(2 * g) * GQA + hh] = (uint32_t)f2h(e[k][0] * f) | ((uint32_t)f2h(e[k][1] * f) << 16);
+                        s_pp[(2 * g + 1) * GQA + hh] = (uint32_t)f2h(e[k][2] * f) | ((uint32_t)f2h(e[k][3] * f) << 16);
+                    }
+                }
+            } else {
+                // long rows: max, sums and probabilities in three passes over the scores
+                for (int g = lane; g < ng; g += 64) {
+                    const uint4 v = cld128(sc + 4 * g);
+                    const uint32_t u[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        const float wv = 4 * g + i <= pos ? __builtin_bit_cast(float, u[i]) * scale : -__builtin_inff();
+                        mx = (mx > wv) ? mx : wv;
+                    }
+                }
+                mx = wave_max_any(mx);
+                for (int g = lane; g < ng; g += 64) {
+                    const uint4 v = cld128(sc + 4 * g);
+                    const uint32_t u[4] = {v.x, v.y, v.z, v.w};
+                    float e[4];
+#pragma unroll
+                    for (int i = 0; i < 4; i++)
+                        e[i] = v_expf((4 * g + i <= pos ? __builtin_bit_cast(float, u[i]) * scale : -__builtin_inff()) - mx);
+                    const float gsum = (e[0] + e[1]) + (e[2] + e[3]);
+                    gs[g] = gsum;
+                    part += (double)gsum;
+                }
+                const double P = wave_sum_d_any(part);
+                float f;
+                if (!bracket_ok_recip(P, P, ng, &f)) {
+                    double sum = 0.0;
+                    for (int g = 0; g < ng; g++) sum += (double)gs[g];
+                    f = (float)(1.0 / sum);
+                }
+                for (int g = lane; g < ng; g += 64) {
+                    const uint4 v = cld128(sc + 4 * g);
+                    const uint32_t u[4] = {v.x, v.y, v.z, v.w};
+                    uint16_t q[4];
+#pragma unroll
+                    for (int i = 0; i < 4; i++)
+                        q[i] = f2h(v_expf((4 * g + i <= pos ? __builtin_bit_cast(float, u[i]) * scale : -__builtin_inff()) - mx) * f);
+                    s_pp[(2 * g) * GQA + hh] = (uint32_t)q[0] | ((uint32_t)q[1] << 16);
+                    s_pp[(2 * g + 1) * GQA + hh] = (uint32_t)q[2] | ((uint32_t)q[3] << 16);
                 }
             }
-            mx = wave_max_f(mx);
-            double part = 0.0;
-            float *gs = s_gs + (size_t)hh * (n_ctx / 4);
-            for (int g = lane; g < n_kv / 4; g += 64) {
-                const uint4 v = cld128(sc + 4 * g);
-                const float f4[4] = {__builtin_bit_cast(float, v.x), __builtin_bit_cast(float, v.y),
-                                     __builtin_bit_cast(float, v.z), __builtin_bit_cast(float, v.w)};
-                float e[4];
-#pragma unroll
-                for (int k = 0; k < 4; k++) e[k] = v_expf((4 * g + k <= pos ? f4[k] * scale : -__builtin_inff()) - mx);
-                const float gsum = (e[0] + e[1]) + (e[2] + e[3]);
-                gs[g] = gsum;
-                part += (double)gsum;
-            }
-            for (int m = 32; m >= 1; m >>= 1) part += shfl_xor_d(part, m);
-            float f;
-            if (!bracket_ok_recip(part, part, n_kv / 4, &f)) {
-                // sequential replay of the group sums in the reference order (wave-local data)
-                double sum = 0.0;
-                for (int g = 0; g < n_kv / 4; g++) sum += (double)gs[g];
-                f = (float)(1.0 / sum);
-            }
-            uint16_t *pp = s_p + (size_t)hh * n_kv;
-            for (int g = lane; g < n_kv / 4; g += 64) {
-                const uint4 v = cld128(sc + 4 * g);
-                const float f4[4] = {__builtin_bit_cast(float, v.x), __builtin_bit_cast(float, v.y),
-                                     __builtin_bit_cast(float, v.z), __builtin_bit_cast(float, v.w)};
-                uint16_t q[4];
-#pragma unroll
-                for (int k = 0; k < 4; k++)
-                    q[k] = f2h(v_expf((4 * g + k <= pos ? f4[k] * scale : -__builtin_inff()) - mx) * f);
-                *(uint2 *)(pp + 4 * g) = make_uint2((uint32_t)q[0] | ((uint32_t)q[1] << 16), (uint32_t)q[2] | ((uint32_t)q[3] << 16));
-            }
         }
+        if (cp < GQA) sg = sigmoid_c(sg);
         __syncthreads();
         tr_mark(c, 141);
-        // V^T . p: thread = (head group hg of 2 heads, dim d, chain quad j)
-        const int j = t & 3, d = (t >> 2) & (PVD - 1), hg = t >> 7;
-        const int dg = dchunk * PVD + d;
-        const uint16_t *vrow = a.m.vcache + (int64_t)L.index * NKV * HD * n_ctx + (int64_t)(kvh * HD + dg) * n_ctx;
-        h2t acc[2][4];
+        // V^T . p for dim d, chain pair cp, heads 0..7
+        h2t acc[GQA];
 #pragma unroll
-        for (int q = 0; q < 2; q++)
-#pragma unroll
-            for (int i = 0; i < 4; i++) acc[q][i] = h2t{(_Float16)0.0f, (_Float16)0.0f};
-#define FZ_PV_STEP(SX, VV)                                                                              \
-    do {                                                                                                \
-        const uint4 vv_ = (VV);                                                                         \
-        const h2t v0 = u2h2f(vv_.x), v1 = u2h2f(vv_.y), v2 = u2h2f(vv_.z), v3 = u2h2f(vv_.w);           \
-        _Pragma("unroll") for (int q = 0; q < 2; q++) {                                                 \
-            const uint4 pv = *(const uint4 *)(&s_p[(hg * 2 + q) * n_kv + 32 * (SX) + 8 * j]);           \
-            acc[q][0] = __builtin_elementwise_fma(v0, u2h2f(pv.x), acc[q][0]);                          \
-            acc[q][1] = __builtin_elementwise_fma(v1, u2h2f(pv.y), acc[q][1]);                          \
-            acc[q][2] = __builtin_elementwise_fma(v2, u2h2f(pv.z), acc[q][2]);                          \
-            acc[q][3] = __builtin_elementwise_fma(v3, u2h2f(pv.w), acc[q][3]);                          \
-        }                                                                                               \
+        for (int q = 0; q < GQA; q++) acc[q] = h2t{(_Float16)0.0f, (_Float16)0.0f};
+#define FZ_PV_STEP(S, VW)                                                                      \
+    do {                                                                                       \
+        const h2t v_ = u2h2f(VW);                                                              \
+        const uint4 pa_ = *(const uint4 *)&s_pp[(16 * (S) + cp) * GQA];                        \
+        const uint4 pb_ = *(const uint4 *)&s_pp[(16 * (S) + cp) * GQA + 4];                    \
+        acc[0] = __builtin_elementwise_fma(v_, u2h2f(pa_.x), acc[0]);                          \
+        acc[1] = __builtin_elementwise_fma(v_, u2h2f(pa_.y), acc[1]);                          \
+        acc[2] = __builtin_elementwise_fma(v_, u2h2f(pa_.z), acc[2]);                          \
+        acc[3] = __builtin_elementwise_fma(v_, u2h2f(pa_.w), acc[3]);                          \
+        acc[4] = __builtin_elementwise_fma(v_, u2h2f(pb_.x), acc[4]);                          \
+        acc[5] = __builtin_elementwise_fma(v_, u2h2f(pb_.y), acc[5]);                          \
+        acc[6] = __builtin_elementwise_fma(v_, u2h2f(pb_.z), acc[6]);                          \
+        acc[7] = __builtin_elementwise_fma(v_, u2h2f(pb_.w), acc[7]);                          \
     } while (0)
-        // chunks holding a position written in this launch are read device-coherently
 #pragma unroll
-        for (int sx = 0; sx < PV_PRE; sx++) {
-            if (sx < n_kv / 32) FZ_PV_STEP(sx, 32 * sx + 31 < pos0 ? vpre[sx] : cld128(vrow + 32 * sx + 8 * j));
-        }
+        for (int s = 0; s < PV_VR; s++)
+            if (s < ns) FZ_PV_STEP(s, vr[s]);
 #pragma unroll 4
-        for (int sx = PV_PRE; sx < n_kv / 32; sx++)
-            FZ_PV_STEP(sx, 32 * sx + 31 >= pos0 ? cld128(vrow + 32 * sx + 8 * j) : *(const uint4 *)(vrow + 32 * sx + 8 * j));
+        for (int s = PV_VR; s < ns; s++)
+            FZ_PV_STEP(s, 32 * s + 2 * cp + 1 >= pos0 ? cld32(vrow + 32 * s) : *(const uint32_t *)(vrow + 32 * s));
 #undef FZ_PV_STEP
+        // GGML_F16x8_REDUCE: accumulator j += j ^ 2 (cp ^ 8), j += j ^ 1 (cp ^ 4); widen halves
+        // (h0 + h4, h1 + h5 | h2 + h6, h3 + h7) and vaddvq ((t0 + t1) + (t2 + t3))
+        float mine = 0.0f;
 #pragma unroll
-        for (int q = 0; q < 2; q++) {
-            const float out = f16x8_reduce_q(acc[q]);
-            const int hh = hg * 2 + q, h = kvh * GQA + hh;
-            if (j == 0) {
-                const float gate = cld(a.b.proj + (int64_t)l * DN_ROWS + h * 2 * HD + HD + dg);
-                s_o[hh * PVD + d] = out * sigmoid_c(gate);
-            }
+        for (int q = 0; q < GQA; q++) {
+            h2t x = acc[q];
+            x = x + u2h2f((uint32_t)dpp_i<DPP_ROR8>((int)h22uf(x)));
+            x = x + u2h2f((uint32_t)dpp_i<DPP_ROR4>((int)h22uf(x)));
+            const float lo = (float)x.x, hi = (float)x.y;
+            const float tlo = lo + dpp_f<DPP_XOR2>(lo), thi = hi + dpp_f<DPP_XOR2>(hi);
+            const float s2 = tlo + thi;
+            const float out = s2 + dpp_f<DPP_XOR1>(s2);
+            mine = cp == q ? out : mine;
         }
+        if (cp < GQA) s_o[cp * PVD + d] = mine * sg;
+        tr_mark(c, 142);
         __syncthreads();
-        int8_t *sq = (int8_t *)(s_o + GQA * PVD);
-        uint16_t *sd = (uint16_t *)(sq + GQA * PVD);
-        if (t < GQA) quant_block_q8_0(s_o + t * PVD, sq + t * PVD, sd + t);
-        __syncthreads();
-        if (t < GQA * 8) {
-            const int hh = t / 8, k = t % 8, h = kvh * GQA + hh;
+        {
+            // Q8_0 of head hh's 32 outputs: wave hh, lanes 0..31
+            const int hh = t >> 6, lane = t & 63, h = kvh * GQA + hh;
+            float dd;
+            const uint32_t word = quant32_lanes(lane < PVD ? s_o[hh * PVD + lane] : 0.0f, &dd);
             const int64_t off = (int64_t)l * MIX_W + h * HD + dchunk * PVD;
-            cst32(a.b.oq + off + 4 * k, *(const uint32_t *)(sq + hh * PVD + 4 * k));
-            if (k == 0) cst16(a.b.od + off / 32, sd[hh]);
+            if (lane < PVD && (lane & 3) == 0) cst32(a.b.oq + off + lane, word);
+            if (lane == 0) cst16(a.b.od + off / 32, f2h(dd));
         }
     }
     tr_end(c, TP_PV);

@@ -32,10 +32,11 @@ enum FusedMode { FM_VERIFY = 0, FM_DRAFT = 1, FM_SEED = 2 };
 
 // barrier words (uint32): per-XCD arrival counters at [32 x] (x = 0..7, one 128-byte line each),
 // the global arrival counter at [256], the release round at [288] (read at launch), the sticky
-// error word at [320], and per-XCD copies of the release round at [384 + 32 x]
-constexpr int FZ_SYNC_WORDS = 640;
+// error word at [320], per-XCD copies of the release round at [384 + 32 x], and the delta-net
+// per-value-head arrival counters at [640 + 32 h] (h = 0..31)
+constexpr int FZ_SYNC_WORDS = 640 + 32 * 32;
 constexpr int FZ_XCD = 8;
-constexpr int FZ_W_GLOB = 256, FZ_W_FLAG = 288, FZ_W_ERR = 320, FZ_W_REL = 384;
+constexpr int FZ_W_GLOB = 256, FZ_W_FLAG = 288, FZ_W_ERR = 320, FZ_W_REL = 384, FZ_W_HEAD = 640;
 
 struct FusedArgs {
     int32_t mode, n_layer, keep_logits, grid;

@@ -51,8 +51,8 @@ OXE_DEV void quant8(const float v[8], int8_t *q, uint16_t *d) {
     float am = 0.0f;
 #pragma unroll
     for (int i = 0; i < 8; i++) am = fmaxf(am, __builtin_fabsf(v[i]));
-    am = fmaxf(am, shfl_xor_f(am, 1));
-    am = fmaxf(am, shfl_xor_f(am, 2));
+    am = fmaxf(am, dpp_f<DPP_XOR1>(am));
+    am = fmaxf(am, dpp_f<DPP_XOR2>(am));
     const float dd = am / 127.0f;
     const float id = dd != 0.0f ? 1.0f / dd : 0.0f;
     uint32_t lo = 0, hi = 0;

@@ -80,21 +80,25 @@ OXE_DEV void route_wave(const float *lg, int l, RouteOut &ro) {
         nan |= p[k] != p[k];
     }
     // Fast path: the probabilities are >= 0, so their bits order like their values. Radix-select
-    // the 9th largest bit pattern T (the largest T with at least 9 values >= T); when exactly 9
-    // values are >= T and they are pairwise distinct, their order by value is the reference's
-    // (no ties), found by ranking the 9 directly.
+    // a bit pattern T with exactly 9 values >= T, from the high bits down (T keeps at least 9
+    // values >= T at every step; the walk stops once exactly 9 are left). The probabilities are
+    // <= 1, so bits 31 and 30 are clear and the walk starts at bit 29 (were one not, T would still
+    // keep its invariant and the count test below decides). When exactly 9 values are >= T and
+    // they are pairwise distinct, their order by value is the reference's (no ties), found by
+    // ranking the 9 directly.
     bool fast = !__ballot(nan);
     if (fast) {
         uint32_t b[4];
 #pragma unroll
         for (int k = 0; k < 4; k++) b[k] = __builtin_bit_cast(uint32_t, p[k]);
         uint32_t T = 0;
-        for (int bit = 31; bit >= 0; bit--) {
+        int cntT = NEXP;
+        for (int bit = 29; bit >= 0 && cntT != KUSED + 1; bit--) {
             const uint32_t cand = T | (1u << bit);
             int cnt = 0;
 #pragma unroll
             for (int k = 0; k < 4; k++) cnt += __popcll(__ballot(b[k] >= cand));
-            if (cnt >= KUSED + 1) T = cand;
+            if (cnt >= KUSED + 1) { T = cand; cntT = cnt; }
         }
         unsigned long long m[4];
         int nsel = 0;
@@ -171,16 +175,14 @@ OXE_DEV void route_wave(const float *lg, int l, RouteOut &ro) {
         }
         wave_lds_sync();
     }
-    if (tl == 0) {
-        double s = 0.0;
+    // sum in rank order (every lane forms it), then lane j < 8 divides weight j
+    double s = 0.0;
 #pragma unroll
-        for (int j = 0; j < KUSED; j++) s += (double)ro.vs[l][j];
-        float sf = (float)s;
-        sf = sf < __builtin_inff() ? sf : __builtin_inff();
-        sf = sf > 6.103515625e-5f ? sf : 6.103515625e-5f;
-#pragma unroll
-        for (int j = 0; j < KUSED; j++) ro.w[l][j] = ro.vs[l][j] / sf;
-    }
+    for (int j = 0; j < KUSED; j++) s += (double)ro.vs[l][j];
+    float sf = (float)s;
+    sf = sf < __builtin_inff() ? sf : __builtin_inff();
+    sf = sf > 6.103515625e-5f ? sf : 6.103515625e-5f;
+    if (tl < KUSED) ro.w[l][tl] = ro.vs[l][tl] / sf;
 }
 
 }  // namespace oxe

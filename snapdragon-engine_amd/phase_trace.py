@@ -22,10 +22,11 @@ import oxe_amd as A  # noqa: E402
 
 PHASES = {1: "proj", 2: "dn", 3: "scores", 4: "pv", 5: "out", 6: "router", 7: "experts", 8: "down", 9: "entry",
           10: "head"}
-MARKS = {101: "experts: routing", 102: "experts: gate/up loads issued", 103: "experts: issue drained",
-         104: "experts: gate/up dot", 111: "proj: norm prologue", 112: "proj: dot", 121: "dn: conv",
-         122: "dn: norms + gates", 123: "dn: delta rule", 131: "router: norm prologue", 132: "router: f32 dots",
-         141: "pv: softmax"}
+MARKS = {101: "experts: union", 102: "experts: gate/up loads issued", 103: "experts: issue drained",
+         104: "experts: gate/up dot", 105: "experts: logits load", 106: "experts: route_wave",
+         111: "proj: norm prologue", 112: "proj: dot", 121: "dn: conv", 122: "dn: norms + gates",
+         123: "dn: delta rule", 131: "router: norm prologue", 132: "router: f32 dots", 141: "pv: softmax",
+         142: "pv: V.p + reduce", 151: "scores: q/k prologue"}
 
 
 def analyse(tr):
