@@ -130,6 +130,9 @@ def main():
     ap.add_argument("--per-phase", action="store_true", help="one launch per phase instead of the fused run kernel")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain device copy of known size (the PMC byte-counter calibration)")
+    ap.add_argument("--pmc-probe", action="store_true",
+                    help="only prefill and run the timed kernel's eager probe launches (for rocprofv3 --pmc), "
+                         "printing their algorithmic bytes")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build runs the whole MTP-1 step on a single MI355X "
@@ -154,6 +157,19 @@ def main():
     eng.sync()
     setup_s = time.time() - t_setup
     cap = 2 * (args.steps + args.warmup) + 16
+    if args.pmc_probe:
+        # eager launches only (no graph): the profiler counts every dispatch of the probe steps
+        eng.mtp_device_begin(x, cap)
+        uni1, calls1 = eng.counter(66), eng.counter(67)
+        pos_p0 = eng.pos
+        avg_us, n_launch = eng.mtp_device_probe(8, probe_kind)
+        eng.mtp_device_end(cap)
+        u_probe = (eng.counter(66) - uni1) / max(eng.counter(67) - calls1, 1)
+        kb = verify_bytes((pos_p0 + eng.pos) / 2, u_probe) if probe_kind == 10 else u_probe * EXPERT_GU
+        print(json.dumps({"pmc_probe": "fused_verify" if probe_kind == 10 else "experts_kernel",
+                          "launches": n_launch, "algorithmic_bytes_per_launch": int(kb), "avg_us": round(avg_us, 3),
+                          "positions": [pos_p0, eng.pos], "union_experts_per_moe_layer": round(u_probe, 3)}), flush=True)
+        return
     # warm-up (also captures the step graph)
     eng.mtp_device_begin(x, cap)
     eng.mtp_device_steps(args.warmup, use_graph=True)

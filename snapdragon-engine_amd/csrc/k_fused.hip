@@ -364,6 +364,8 @@ struct ScSm {
     alignas(16) uint16_t knew[NL][HD];
     alignas(16) uint16_t krows[SC_P][SC_KS];   // cached K rows of the chunk's positions (padded rows)
 };
+constexpr int HEAD_P = 8;                   // LM-head tile: 8 passes of 4 rows
+constexpr int HEAD_TR = HEAD_P * KG<E>::RPP;
 template <int NL>
 struct HeadSm {
     alignas(16) float xf[NL][E];
@@ -371,7 +373,7 @@ struct HeadSm {
     alignas(16) int8_t xq[NL][E];
     uint16_t xd[NL][E / 32];
     NormSm ns;
-    GSm<E, 32, NL> g;
+    GSm<E, HEAD_TR, NL> g;
     unsigned long long key[FT / 64][NL];
 };
 template <int NL>
@@ -750,7 +752,37 @@ FZ_PHASE bool phase_out(const RunCtl *ctl, const FusedArgs *ap, int il, const fl
     tr_pass(c);
     float xres = 0.0f;
     if (t < NL * 8 && t / 8 < c.nl) xres = cld(x + (int64_t)(t / 8) * E + r0 + t % 8);
-    {
+    if (L.att) {
+        // the attention's gated outputs (f32): thread (lane l, 16 elements at 16 tt), Q8_0 blocks of
+        // 32 over adjacent thread pairs (quantize_row_q8_0 NEON: amax, d = amax / 127, id from the
+        // f32 d, round-half-even codes)
+        const int l = t >> 8, tt = t & 255;
+        float v[16];
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const unsigned long long u = l < NL && l < c.nl ? cld64(a.b.gdn + (int64_t)l * MIX_W + 16 * tt + 2 * k) : 0ull;
+            v[2 * k] = __builtin_bit_cast(float, (uint32_t)u);
+            v[2 * k + 1] = __builtin_bit_cast(float, (uint32_t)(u >> 32));
+        }
+        float am = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 16; k++) am = fmaxf(am, __builtin_fabsf(v[k]));
+        am = fmaxf(am, dpp_f<DPP_XOR1>(am));
+        const float dd = am / 127.0f;
+        const float id = dd != 0.0f ? 1.0f / dd : 0.0f;
+        uint32_t w[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            uint32_t u = 0;
+#pragma unroll
+            for (int b = 0; b < 4; b++) u |= ((uint32_t)((int32_t)__builtin_rintf(v[4 * k + b] * id) & 0xff)) << (8 * b);
+            w[k] = u;
+        }
+        if (l < NL) {
+            *(uint4 *)&s.xq[l][16 * tt] = make_uint4(w[0], w[1], w[2], w[3]);
+            if ((tt & 1) == 0) s.xd[l][tt / 2] = f2h(dd);
+        }
+    } else {
         const int l = t >> 8, tt = t & 255;
         if (l < NL)
             *(uint4 *)&s.xq[l][16 * tt] = l < c.nl ? cld128(a.b.oq + (int64_t)l * MIX_W + 16 * tt) : make_uint4(0, 0, 0, 0);
@@ -960,12 +992,13 @@ FZ_PHASE bool phase_moe(const RunCtl *ctl, const FusedArgs *ap, int il) {
     tr_end(c, TP_EXPERTS);
     tr_start(c);
     arrive(c.bar);
-    // the down rows of every union expert and the shared expert, in flight across the barrier
+    // the down rows of every union expert and the shared expert: the first DW_PRE units per
+    // thread in flight across the barrier, the rest issued behind the phase's inputs (a barrier
+    // poll waits behind every load the workgroup has outstanding)
     const int r0 = 8 * b;
     const int uh = t >> 8, rr = (t >> 5) & 7, ck = t & 31;
     uint4 dw[9];
-#pragma unroll
-    for (int k = 0; k < 9; k++) {
+    auto dload = [&](int k) {
         const int u = 2 * k + uh;
         dw[k] = make_uint4(0, 0, 0, 0);
         if (u < DW_UNITS && (u == OXE_MAX_UNION || u < nu)) {
@@ -978,7 +1011,10 @@ FZ_PHASE bool phase_moe(const RunCtl *ctl, const FusedArgs *ap, int il) {
             }
             dw[k] = *(const uint4 *)(base + (int64_t)(r0 + rr) * FF + 16 * ck);
         }
-    }
+    };
+    constexpr int DW_PRE = 5;
+#pragma unroll
+    for (int k = 0; k < DW_PRE; k++) dload(k);
     uint4 dsc = make_uint4(0, 0, 0, 0);
     const int su = t / 16, srr = (t % 16) / 2, shf = t % 2;
     if (t < DW_UNITS * 16 && (su == OXE_MAX_UNION || su < nu)) {
@@ -1019,6 +1055,8 @@ FZ_PHASE bool phase_moe(const RunCtl *ctl, const FusedArgs *ap, int il) {
         x1v = cld(a.b.x1 + (int64_t)(t / 8) * E + r0 + t % 8);
         sgv = cld(a.b.sh_gate + t / 8);
     }
+#pragma unroll
+    for (int k = DW_PRE; k < 9; k++) dload(k);
     // Q8_0 of the shared expert's h: element t of lane k in thread t, a block per half wave
     static_assert(FFSH == FT, "one shared-expert element per thread and lane");
 #pragma unroll
@@ -1043,6 +1081,7 @@ FZ_PHASE bool phase_moe(const RunCtl *ctl, const FusedArgs *ap, int il) {
         sd.hd[l][u][k] = hdv;
     }
     __syncthreads();
+    tr_mark(c, 161);
 #pragma unroll
     for (int k = 0; k < 9; k++) {
         const int u = 2 * k + uh;
@@ -1057,6 +1096,7 @@ FZ_PHASE bool phase_moe(const RunCtl *ctl, const FusedArgs *ap, int il) {
         }
     }
     __syncthreads();
+    tr_mark(c, 162);
     if (t < DW_UNITS * NL * 8) {
         const int u = t / (NL * 8), l = (t / 8) % NL, r = t % 8;
         if (u == OXE_MAX_UNION || u < nu) {
@@ -1069,6 +1109,7 @@ FZ_PHASE bool phase_moe(const RunCtl *ctl, const FusedArgs *ap, int il) {
         }
     }
     __syncthreads();
+    tr_mark(c, 163);
     if (t < NL * 8) {
         const int l = t / 8, r = t % 8;
         if (l < nl) {
@@ -1247,16 +1288,22 @@ FZ_PHASE bool phase_scores(const RunCtl *ctl, const FusedArgs *ap, int il, bool 
     return true;
 }
 
-// Attention output (k_attn.hip pv_kernel's arithmetic): workgroup (kv head kvh, lane l, 32-dim
-// chunk) for the GQA group's 8 heads. Wave hh forms head hh's softmax (oxe_soft_max_f32,
-// oxe_ops.cpp:101-115) in one pass over its scores, held in registers (up to PV_SMK groups of 4
-// positions per lane; longer rows take three passes). Thread (d = t / 16, cp = t % 16) then runs
-// chain pair cp of ggml_vec_dot_f16 (positions 32 s + 2 cp and +1: accumulator cp / 4, halves
-// 2 (cp % 4) and +1) for dim d and all 8 heads; its V^T words of earlier launches are loaded
-// before the barrier. The F16x8 reduce is done by lane moves inside the 16-lane row of dim d.
-constexpr int PV_SMK = 8;    // softmax groups per lane in registers (n_kv <= 2048)
-constexpr int PV_VR = 32;    // V^T words per thread in registers (n_kv <= 1024)
-constexpr int PVD = 32;      // dims per workgroup (one Q8_0 block per head)
+// Attention output (k_attn.hip pv_kernel's arithmetic): workgroup (kv head kvh, lane l, 16-dim
+// chunk, head pair hp) for heads 2 hp, 2 hp + 1 of the GQA group; 256 workgroups. Head q of the
+// pair is handled by waves 4 q .. 4 q + 3: its softmax (oxe_soft_max_f32, oxe_ops.cpp:101-115)
+// in one pass over its scores held in registers (up to PV_SMK groups of 4 positions per thread;
+// longer rows take three passes), max and group-sum total combined over the four waves. The
+// chunk's V^T rows (16 dims x n_kv) are staged in LDS: 16-byte chunks holding only positions of
+// earlier launches are loaded before the barrier, the rest after it, device-coherently. Thread
+// (q = t / 256, dim d = (t / 16) % 16, cp = t % 16) runs chain pair cp of ggml_vec_dot_f16
+// (positions 32 s + 2 cp and +1: accumulator cp / 4, halves 2 (cp % 4) and +1) for dim d and head
+// q; the F16x8 reduce is done by lane moves inside the 16-lane row. The gated outputs (f32) go to
+// the mixer-output buffer; the output projection quantizes them.
+constexpr int PV_SMK = 2;    // softmax groups per thread in registers (n_kv <= 2048)
+constexpr int PVD = 16;      // dims per workgroup
+constexpr int PV_HP = GQA / 2;  // head pairs per kv head
+constexpr int PV_VK = 4;     // V^T 16-byte chunks per thread staged from registers (n_kv <= 1024)
+constexpr int PV_VMAX = 2048;   // positions of the V^T tile held in LDS (longer rows: the rest from memory)
 
 template <int NL>
 FZ_PHASE bool phase_pv(const RunCtl *ctl, const FusedArgs *ap, int il) {
@@ -1265,9 +1312,11 @@ FZ_PHASE bool phase_pv(const RunCtl *ctl, const FusedArgs *ap, int il) {
     const LayerDev &L = ap->layers[il];
     const FusedArgs &a = *c.a;
     const int t = threadIdx.x, nl = c.nl;
-    const int dchunk = c.b % (HD / PVD);
-    const int l = (c.b / (HD / PVD)) % NL;
-    const int kvh = c.b / ((HD / PVD) * NL);
+    constexpr int NCH = HD / PVD;
+    const int hp = c.b % PV_HP;
+    const int dchunk = (c.b / PV_HP) % NCH;
+    const int l = (c.b / (PV_HP * NCH)) % NL;
+    const int kvh = c.b / (PV_HP * NCH * NL);
     const bool act = kvh < NKV && l < nl;
     const int n_ctx = a.m.n_ctx;
     const int pos0 = c.ctl->pos0, pos = pos0 + l;
@@ -1275,179 +1324,176 @@ FZ_PHASE bool phase_pv(const RunCtl *ctl, const FusedArgs *ap, int il) {
     if (n_kv < 256) n_kv = 256;
     if (n_kv > n_ctx) n_kv = n_ctx;
     const int ns = n_kv / 32;
-    const int d = t >> 4, cp = t & 15, dg = dchunk * PVD + d;
-    const uint16_t *vrow = a.m.vcache + (int64_t)L.index * NKV * HD * n_ctx + (int64_t)(kvh * HD + dg) * n_ctx + 2 * cp;
-    // V^T words holding only positions written by earlier launches, before the barrier
-    uint32_t vr[PV_VR];
+    const int nst = n_kv < PV_VMAX ? n_kv : PV_VMAX;   // positions staged in LDS
+    const int nvc = nst / 8;                            // staged 16-byte chunks per V^T row
+    const int vs = nst + 32;                            // LDS row stride in halves
+    const uint16_t *vt = a.m.vcache + (int64_t)L.index * NKV * HD * n_ctx + (int64_t)(kvh * HD + dchunk * PVD) * n_ctx;
+    // staged chunk i = t + FT k: row i / nvc, chunk i % nvc; those of earlier launches only, now
+    uint4 vpre[PV_VK];
 #pragma unroll
-    for (int s = 0; s < PV_VR; s++)
-        vr[s] = (act && s < ns && 32 * s + 2 * cp + 1 < pos0) ? *(const uint32_t *)(vrow + 32 * s) : 0u;
+    for (int k = 0; k < PV_VK; k++) {
+        const int i = t + FT * k, r = i / nvc, ch = i % nvc;
+        vpre[k] = (act && i < PVD * nvc && 8 * ch + 7 < pos0) ? *(const uint4 *)(vt + (int64_t)r * n_ctx + 8 * ch)
+                                                              : make_uint4(0, 0, 0, 0);
+    }
     if (!wait(c.bar, &c.ps->ok)) return false;
     tr_pass(c);
-    if (!act && c.b >= NKV * NL * (HD / PVD) && il + 1 < a.n_layer) {
-        // idle during the attention: warm the next layer's input projection
-        const LayerDev &N = a.layers[il + 1];
-        const int64_t rows = N.att ? AT_ROWS : DN_ROWS;
-        const int idle0 = NKV * NL * (HD / PVD);
-        warm(N.proj.q, (size_t)rows * E, c.b - idle0, c.G - idle0, a.sync + FZ_W_ERR + 32);
-        warm(N.proj.d, (size_t)rows * (E / 32) * 2, c.b - idle0, c.G - idle0, a.sync + FZ_W_ERR + 32);
-    }
     if (act) {
-        uint32_t *s_pp = (uint32_t *)c.dyn;                                  // [n_kv / 2][GQA] f16 pairs
-        float *s_gs = (float *)(c.dyn + (size_t)GQA * n_ctx * 2);           // [GQA][n_ctx / 4] group sums
-        float *s_o = s_gs + (size_t)GQA * (n_ctx / 4);                       // [GQA][PVD]
-        // this thread's gate (head cp < 8, dim dg) and the V^T words of this launch's positions
-        float sg = 0.0f;
-        if (cp < GQA) sg = cld(a.b.proj + (int64_t)l * DN_ROWS + (kvh * GQA + cp) * 2 * HD + HD + dg);
+        uint32_t *s_pp = (uint32_t *)c.dyn;                                  // [n_kv / 2][2] f16 pairs
+        uint16_t *s_v = (uint16_t *)(c.dyn + (size_t)n_ctx * 4);            // [PVD][vs] V^T rows
+        float *s_mx = (float *)(s_v + (size_t)PVD * vs);                    // [2][4] wave maxima
+        double *s_ps = (double *)(((uintptr_t)(s_mx + 8) + 7) & ~(uintptr_t)7);   // [2][4] wave sums
+        float *s_f = (float *)(s_ps + 8);                                   // [2] 1 / sum
+        const int q = t >> 8, tq = t & 255, wq = (t >> 6) & 3;
+        const int cp = t & 15, d = (t >> 4) & (PVD - 1);
+        const int h = kvh * GQA + 2 * hp + q;
+        // the chunks with positions of this launch (or later), device-coherently; this thread's gate
 #pragma unroll
-        for (int s = 0; s < PV_VR; s++)
-            if (s < ns && 32 * s + 2 * cp + 1 >= pos0) vr[s] = cld32(vrow + 32 * s);
+        for (int k = 0; k < PV_VK; k++) {
+            const int i = t + FT * k, r = i / nvc, ch = i % nvc;
+            if (i < PVD * nvc && 8 * ch + 7 >= pos0) vpre[k] = cld128(vt + (int64_t)r * n_ctx + 8 * ch);
+        }
+        float sg = 0.0f;
+        if (cp == 0) sg = cld(a.b.proj + (int64_t)l * DN_ROWS + h * 2 * HD + HD + dchunk * PVD + d);
         const float scale = 1.0f / sqrtf((float)HD);
         {
-            // softmax of head hh = wave w: wp = s * scale (masked: -inf), max, e = v_expf(wp - max)
-            // with group sums (e0 + e1) + (e2 + e3) added in double, p = f16(e * f32(1 / sum))
-            const int hh = t >> 6, lane = t & 63, h = kvh * GQA + hh;
+            // softmax of head q: wp = s * scale (masked: -inf), max, e = v_expf(wp - max) with group
+            // sums (e0 + e1) + (e2 + e3) added in double, p = f16(e * f32(1 / sum))
             const float *sc = a.b.scores + ((int64_t)l * NH + h) * n_ctx;
-            float *gs = s_gs + (size_t)hh * (n_ctx / 4);
             const int ng = n_kv / 4;
+            auto wval = [&](uint32_t u, int p) { return p <= pos ? __builtin_bit_cast(float, u) * scale : -__builtin_inff(); };
+            auto group = [&](int g, float mx) {
+                const uint4 v = cld128(sc + 4 * g);
+                const float e0 = v_expf(wval(v.x, 4 * g) - mx), e1 = v_expf(wval(v.y, 4 * g + 1) - mx);
+                const float e2 = v_expf(wval(v.z, 4 * g + 2) - mx), e3 = v_expf(wval(v.w, 4 * g + 3) - mx);
+                return (e0 + e1) + (e2 + e3);
+            };
+            // max over the head's four waves (LDS), then the group-sum total
+            auto head_max = [&](float m) {
+                m = wave_max_any(m);
+                if ((t & 63) == 0) s_mx[q * 4 + wq] = m;
+                __syncthreads();
+                const float m01 = s_mx[q * 4] > s_mx[q * 4 + 1] ? s_mx[q * 4] : s_mx[q * 4 + 1];
+                const float m23 = s_mx[q * 4 + 2] > s_mx[q * 4 + 3] ? s_mx[q * 4 + 2] : s_mx[q * 4 + 3];
+                return m01 > m23 ? m01 : m23;
+            };
+            auto head_recip = [&](double part, float mx) {
+                part = wave_sum_d_any(part);
+                if ((t & 63) == 0) s_ps[q * 4 + wq] = part;
+                __syncthreads();
+                const double P = (s_ps[q * 4] + s_ps[q * 4 + 1]) + (s_ps[q * 4 + 2] + s_ps[q * 4 + 3]);
+                float f;
+                const bool ok = bracket_ok_recip(P, P, ng, &f);
+                if (!ok && tq == 0) {
+                    // the reference's sequential double sum of the group sums (rare: the parallel
+                    // sum's bracket straddles a rounding edge), recomputed from the scores
+                    double sum = 0.0;
+                    for (int g = 0; g < ng; g++) sum += (double)group(g, mx);
+                    s_f[q] = (float)(1.0 / sum);
+                }
+                __syncthreads();   // every wave of the workgroup (both heads) reaches it
+                if (!ok) f = s_f[q];
+                return f;
+            };
             float mx = -__builtin_inff();
             double part = 0.0;
-            if (ng <= 64 * PV_SMK) {
+            if (ng <= 256 * PV_SMK) {
                 float e[PV_SMK][4];
 #pragma unroll
                 for (int k = 0; k < PV_SMK; k++) {
-                    const int g = lane + 64 * k;
+                    const int g = tq + 256 * k;
                     const uint4 v = g < ng ? cld128(sc + 4 * g) : make_uint4(0, 0, 0, 0);
                     const uint32_t u[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
                     for (int i = 0; i < 4; i++) {
-                        e[k][i] = (g < ng && 4 * g + i <= pos) ? __builtin_bit_cast(float, u[i]) * scale : -__builtin_inff();
+                        e[k][i] = g < ng ? wval(u[i], 4 * g + i) : -__builtin_inff();
                         mx = (mx > e[k][i]) ? mx : e[k][i];
                     }
                 }
-                mx = wave_max_any(mx);
+                mx = head_max(mx);
+                tr_mark(c, 143);
 #pragma unroll
                 for (int k = 0; k < PV_SMK; k++) {
-                    const int g = lane + 64 * k;
+                    const int g = tq + 256 * k;
                     if (g < ng) {
 #pragma unroll
                         for (int i = 0; i < 4; i++) e[k][i] = v_expf(e[k][i] - mx);
-                        const float gsum = (e[k][0] + e[k][1]) + (e[k][2] + e[k][3]);
-                        gs[g] = gsum;
-                        part += (double)gsum;
+                        part += (double)((e[k][0] + e[k][1]) + (e[k][2] + e[k][3]));
                     }
                 }
-                const double P = wave_sum_d_any(part);
-                float f;
-                if (!bracket_ok_recip(P, P, ng, &f)) {
-                    double sum = 0.0;
-                    for (int g = 0; g < ng; g++) sum += (double)gs[g];
-                    f = (float)(1.0 / sum);
-                }
+                const float f = head_recip(part, mx);
 #pragma unroll
                 for (int k = 0; k < PV_SMK; k++) {
-                    const int g = lane + 64 * k;
+                    const int g = tq + 256 * k;
                     if (g < ng) {
-                        s_pp[(2 * g) * GQA + hh] = (uint32_t)f2h(e[k][0] * f) | ((uint32_t)f2h(e[k][1] * f) << 16);
-                        s_pp[(2 * g + 1) * GQA + hh] = (uint32_t)f2h(e[k][2] * f) | ((uint32_t)f2h(e[k][3] * f) << 16);
+                        s_pp[(2 * g) * 2 + q] = (uint32_t)f2h(e[k][0] * f) | ((uint32_t)f2h(e[k][1] * f) << 16);
+                        s_pp[(2 * g + 1) * 2 + q] = (uint32_t)f2h(e[k][2] * f) | ((uint32_t)f2h(e[k][3] * f) << 16);
                     }
                 }
             } else {
                 // long rows: max, sums and probabilities in three passes over the scores
-                for (int g = lane; g < ng; g += 64) {
+                for (int g = tq; g < ng; g += 256) {
                     const uint4 v = cld128(sc + 4 * g);
                     const uint32_t u[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
                     for (int i = 0; i < 4; i++) {
-                        const float wv = 4 * g + i <= pos ? __builtin_bit_cast(float, u[i]) * scale : -__builtin_inff();
+                        const float wv = wval(u[i], 4 * g + i);
                         mx = (mx > wv) ? mx : wv;
                     }
                 }
-                mx = wave_max_any(mx);
-                for (int g = lane; g < ng; g += 64) {
+                mx = head_max(mx);
+                for (int g = tq; g < ng; g += 256) part += (double)group(g, mx);
+                const float f = head_recip(part, mx);
+                for (int g = tq; g < ng; g += 256) {
                     const uint4 v = cld128(sc + 4 * g);
                     const uint32_t u[4] = {v.x, v.y, v.z, v.w};
-                    float e[4];
+                    uint16_t pq[4];
 #pragma unroll
-                    for (int i = 0; i < 4; i++)
-                        e[i] = v_expf((4 * g + i <= pos ? __builtin_bit_cast(float, u[i]) * scale : -__builtin_inff()) - mx);
-                    const float gsum = (e[0] + e[1]) + (e[2] + e[3]);
-                    gs[g] = gsum;
-                    part += (double)gsum;
-                }
-                const double P = wave_sum_d_any(part);
-                float f;
-                if (!bracket_ok_recip(P, P, ng, &f)) {
-                    double sum = 0.0;
-                    for (int g = 0; g < ng; g++) sum += (double)gs[g];
-                    f = (float)(1.0 / sum);
-                }
-                for (int g = lane; g < ng; g += 64) {
-                    const uint4 v = cld128(sc + 4 * g);
-                    const uint32_t u[4] = {v.x, v.y, v.z, v.w};
-                    uint16_t q[4];
-#pragma unroll
-                    for (int i = 0; i < 4; i++)
-                        q[i] = f2h(v_expf((4 * g + i <= pos ? __builtin_bit_cast(float, u[i]) * scale : -__builtin_inff()) - mx) * f);
-                    s_pp[(2 * g) * GQA + hh] = (uint32_t)q[0] | ((uint32_t)q[1] << 16);
-                    s_pp[(2 * g + 1) * GQA + hh] = (uint32_t)q[2] | ((uint32_t)q[3] << 16);
+                    for (int i = 0; i < 4; i++) pq[i] = f2h(v_expf(wval(u[i], 4 * g + i) - mx) * f);
+                    s_pp[(2 * g) * 2 + q] = (uint32_t)pq[0] | ((uint32_t)pq[1] << 16);
+                    s_pp[(2 * g + 1) * 2 + q] = (uint32_t)pq[2] | ((uint32_t)pq[3] << 16);
                 }
             }
         }
-        if (cp < GQA) sg = sigmoid_c(sg);
+        tr_mark(c, 144);
+        // the V^T tile into LDS
+#pragma unroll
+        for (int k = 0; k < PV_VK; k++) {
+            const int i = t + FT * k, r = i / nvc, ch = i % nvc;
+            if (i < PVD * nvc) *(uint4 *)(s_v + r * vs + 8 * ch) = vpre[k];
+        }
+        for (int i = t + FT * PV_VK; i < PVD * nvc; i += FT) {
+            const int r = i / nvc, ch = i % nvc;
+            const uint16_t *src = vt + (int64_t)r * n_ctx + 8 * ch;
+            *(uint4 *)(s_v + r * vs + 8 * ch) = 8 * ch + 7 < pos0 ? *(const uint4 *)src : cld128(src);
+        }
+        if (cp == 0) sg = sigmoid_c(sg);
         __syncthreads();
         tr_mark(c, 141);
-        // V^T . p for dim d, chain pair cp, heads 0..7
-        h2t acc[GQA];
-#pragma unroll
-        for (int q = 0; q < GQA; q++) acc[q] = h2t{(_Float16)0.0f, (_Float16)0.0f};
-#define FZ_PV_STEP(S, VW)                                                                      \
-    do {                                                                                       \
-        const h2t v_ = u2h2f(VW);                                                              \
-        const uint4 pa_ = *(const uint4 *)&s_pp[(16 * (S) + cp) * GQA];                        \
-        const uint4 pb_ = *(const uint4 *)&s_pp[(16 * (S) + cp) * GQA + 4];                    \
-        acc[0] = __builtin_elementwise_fma(v_, u2h2f(pa_.x), acc[0]);                          \
-        acc[1] = __builtin_elementwise_fma(v_, u2h2f(pa_.y), acc[1]);                          \
-        acc[2] = __builtin_elementwise_fma(v_, u2h2f(pa_.z), acc[2]);                          \
-        acc[3] = __builtin_elementwise_fma(v_, u2h2f(pa_.w), acc[3]);                          \
-        acc[4] = __builtin_elementwise_fma(v_, u2h2f(pb_.x), acc[4]);                          \
-        acc[5] = __builtin_elementwise_fma(v_, u2h2f(pb_.y), acc[5]);                          \
-        acc[6] = __builtin_elementwise_fma(v_, u2h2f(pb_.z), acc[6]);                          \
-        acc[7] = __builtin_elementwise_fma(v_, u2h2f(pb_.w), acc[7]);                          \
-    } while (0)
-#pragma unroll
-        for (int s = 0; s < PV_VR; s++)
-            if (s < ns) FZ_PV_STEP(s, vr[s]);
-#pragma unroll 4
-        for (int s = PV_VR; s < ns; s++)
-            FZ_PV_STEP(s, 32 * s + 2 * cp + 1 >= pos0 ? cld32(vrow + 32 * s) : *(const uint32_t *)(vrow + 32 * s));
-#undef FZ_PV_STEP
+        // V^T . p for dim d, chain pair cp, head q
+        h2t acc = h2t{(_Float16)0.0f, (_Float16)0.0f};
+        const uint16_t *vrow = s_v + d * vs + 2 * cp;
+        const uint32_t *prow = s_pp + cp * 2 + q;
+        const int nss = nst / 32;
+#pragma unroll 8
+        for (int s = 0; s < nss; s++)
+            acc = __builtin_elementwise_fma(u2h2f(*(const uint32_t *)(vrow + 32 * s)), u2h2f(prow[32 * s]), acc);
+        for (int s = nss; s < ns; s++) {
+            const uint16_t *src = vt + (int64_t)d * n_ctx + 32 * s + 2 * cp;
+            const uint32_t vw = 32 * s + 2 * cp + 1 >= pos0 ? cld32(src) : *(const uint32_t *)src;
+            acc = __builtin_elementwise_fma(u2h2f(vw), u2h2f(prow[32 * s]), acc);
+        }
         // GGML_F16x8_REDUCE: accumulator j += j ^ 2 (cp ^ 8), j += j ^ 1 (cp ^ 4); widen halves
         // (h0 + h4, h1 + h5 | h2 + h6, h3 + h7) and vaddvq ((t0 + t1) + (t2 + t3))
-        float mine = 0.0f;
-#pragma unroll
-        for (int q = 0; q < GQA; q++) {
-            h2t x = acc[q];
-            x = x + u2h2f((uint32_t)dpp_i<DPP_ROR8>((int)h22uf(x)));
-            x = x + u2h2f((uint32_t)dpp_i<DPP_ROR4>((int)h22uf(x)));
-            const float lo = (float)x.x, hi = (float)x.y;
-            const float tlo = lo + dpp_f<DPP_XOR2>(lo), thi = hi + dpp_f<DPP_XOR2>(hi);
-            const float s2 = tlo + thi;
-            const float out = s2 + dpp_f<DPP_XOR1>(s2);
-            mine = cp == q ? out : mine;
-        }
-        if (cp < GQA) s_o[cp * PVD + d] = mine * sg;
+        h2t x = acc;
+        x = x + u2h2f((uint32_t)dpp_i<DPP_ROR8>((int)h22uf(x)));
+        x = x + u2h2f((uint32_t)dpp_i<DPP_ROR4>((int)h22uf(x)));
+        const float lo = (float)x.x, hi = (float)x.y;
+        const float tlo = lo + dpp_f<DPP_XOR2>(lo), thi = hi + dpp_f<DPP_XOR2>(hi);
+        const float s2 = tlo + thi;
+        const float out = s2 + dpp_f<DPP_XOR1>(s2);
         tr_mark(c, 142);
-        __syncthreads();
-        {
-            // Q8_0 of head hh's 32 outputs: wave hh, lanes 0..31
-            const int hh = t >> 6, lane = t & 63, h = kvh * GQA + hh;
-            float dd;
-            const uint32_t word = quant32_lanes(lane < PVD ? s_o[hh * PVD + lane] : 0.0f, &dd);
-            const int64_t off = (int64_t)l * MIX_W + h * HD + dchunk * PVD;
-            if (lane < PVD && (lane & 3) == 0) cst32(a.b.oq + off + lane, word);
-            if (lane == 0) cst16(a.b.od + off / 32, f2h(dd));
-        }
+        if (cp == 0) cst(a.b.gdn + (int64_t)l * MIX_W + h * HD + dchunk * PVD + d, out * sg);
     }
     tr_end(c, TP_PV);
     arrive(c.bar);
@@ -1512,12 +1558,12 @@ FZ_PHASE bool phase_head(const RunCtl *ctl, const FusedArgs *ap, const float *no
     auto &s = c.sm->head;
     const int t = threadIdx.x, nl = c.nl, mask = c.ctl->head_mask;
     const int64_t V = a.m.output.rows;
-    constexpr int TR = 32;                                   // rows per tile
+    constexpr int TR = HEAD_TR;                              // rows per tile
     const int64_t ntiles = (V + TR - 1) / TR;
     const int64_t t0 = ntiles * c.b / c.G, t1 = ntiles * (c.b + 1) / c.G;
-    WSlice<E, 8> A, B;
+    WSlice<E, HEAD_P> A, B;
     auto rows_of = [&](int64_t tile) { const int64_t r = V - tile * TR; return (int)(r < TR ? r : TR); };
-    if (t0 < t1) wload<E, 8>(A, a.m.output.q, a.m.output.d, rows_of(t0), [&](int rl) { return t0 * TR + rl; });
+    if (t0 < t1) wload<E, HEAD_P>(A, a.m.output.q, a.m.output.d, rows_of(t0), [&](int rl) { return t0 * TR + rl; });
     const W8 nw = wload8(norm_w);
     if (!wait(c.bar, &c.ps->ok)) return false;
     tr_pass(c);
@@ -1534,10 +1580,10 @@ FZ_PHASE bool phase_head(const RunCtl *ctl, const FusedArgs *ap, const float *no
     const int rl = t % TR, l = t / TR;
     for (int64_t tile = t0; tile < t1; tile += 2) {
         const bool hb = tile + 1 < t1;
-        if (hb) wload<E, 8>(B, a.m.output.q, a.m.output.d, rows_of(tile + 1), [&](int r) { return (tile + 1) * TR + r; });
+        if (hb) wload<E, HEAD_P>(B, a.m.output.q, a.m.output.d, rows_of(tile + 1), [&](int r) { return (tile + 1) * TR + r; });
         {
             const int nr = rows_of(tile);
-            wdot<E, 8, NL>(A, nr, &s.xq[0][0], E, &s.xd[0][0], E / 32, s.g);
+            wdot<E, HEAD_P, NL>(A, nr, &s.xq[0][0], E, &s.xd[0][0], E / 32, s.g);
             if (l < NL && l < nl && rl < nr) {
                 const float v = s.g.out[l][rl];
                 const int64_t row = tile * TR + rl;
@@ -1546,9 +1592,9 @@ FZ_PHASE bool phase_head(const RunCtl *ctl, const FusedArgs *ap, const float *no
             }
         }
         if (hb) {
-            if (tile + 2 < t1) wload<E, 8>(A, a.m.output.q, a.m.output.d, rows_of(tile + 2), [&](int r) { return (tile + 2) * TR + r; });
+            if (tile + 2 < t1) wload<E, HEAD_P>(A, a.m.output.q, a.m.output.d, rows_of(tile + 2), [&](int r) { return (tile + 2) * TR + r; });
             const int nr = rows_of(tile + 1);
-            wdot<E, 8, NL>(B, nr, &s.xq[0][0], E, &s.xd[0][0], E / 32, s.g);
+            wdot<E, HEAD_P, NL>(B, nr, &s.xq[0][0], E, &s.xd[0][0], E / 32, s.g);
             if (l < NL && l < nl && rl < nr) {
                 const float v = s.g.out[l][rl];
                 const int64_t row = (tile + 1) * TR + rl;
@@ -1628,8 +1674,10 @@ __global__ __launch_bounds__(fz::FT, 1) void fused_kernel(const RunCtl *__restri
 
 size_t fused_lds_bytes(int n_ctx) {
     const size_t base = sizeof(fz::PhaseSm<OXE_NL>);
-    const size_t pv = (size_t)GQA * ((n_ctx + 1) & ~1) * 2 + (size_t)GQA * (n_ctx / 4) * 4 + 16 + GQA * 32 * 4 + GQA * 32 +
-                      GQA * 2 + 256;
+    // the attention-output phase: f16 probability pairs [n_ctx / 2][2], the V^T tile
+    // [PVD][min(n_ctx, PV_VMAX) + 32], and the softmax's cross-wave maxima and sums
+    const size_t vmax = (size_t)(n_ctx < fz::PV_VMAX ? n_ctx : fz::PV_VMAX);
+    const size_t pv = (size_t)n_ctx * 4 + (size_t)fz::PVD * (vmax + 32) * 2 + 256;
     return (base > pv ? base : pv + 16) / 16 * 16 + 16;
 }
 

@@ -18,8 +18,14 @@ namespace oxe {
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 
 OXE_DEV float h2f(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
-// v_cvt_f16_f32 under the default round-to-nearest-even mode (= __fp16 conversion on aarch64)
-OXE_DEV uint16_t f2h(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
+// v_cvt_f16_f32 under the default round-to-nearest-even mode (= __fp16 conversion on aarch64).
+// The empty asm pins f as a rounded f32 value: without it the compiler may fold a preceding f32
+// multiply into the conversion (v_fma_mixlo_f16, one rounding straight to f16), which differs from
+// the reference's f32 rounding followed by the f16 conversion in rare double-rounding cases.
+OXE_DEV uint16_t f2h(float f) {
+    asm volatile("" : "+v"(f));
+    return __builtin_bit_cast(uint16_t, (_Float16)f);
+}
 OXE_DEV _Float16 hbits(uint16_t h) { return __builtin_bit_cast(_Float16, h); }
 OXE_DEV uint16_t bitsh(_Float16 h) { return __builtin_bit_cast(uint16_t, h); }
 

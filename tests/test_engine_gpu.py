@@ -78,3 +78,32 @@ def test_mtp_run_and_seed_bitexact(small):
 def test_no_topk_ties(small):
     d, g, o = small
     assert g.counter(64) == 0
+
+
+@pytest.mark.parametrize("mode", ["fused", "per_phase"])
+def test_verify_sweep_bitexact(mode):
+    """Many short verify runs (one and two lanes) from several prompt lengths, each committed: every
+    lane's hidden row and logits bit-exact. Catches rare, value-dependent rounding differences (an
+    f32 product folded into its f16 conversion changed about one run in ten here)."""
+    import oxe_amd as A
+    d = O.desc_small()
+    for plen, nl in ((5, 2), (6, 1), (14, 2), (30, 2)):
+        prompt = [int(v) % d.n_vocab for v in O.bench_prompt(plen + 8)]
+        o = O.Engine(d, seed=0, n_ctx=256)
+        g = A.Engine(d, seed=0, n_ctx=256)
+        if mode == "per_phase":
+            g.set_fused(False)
+        elif not g.fused:
+            pytest.skip("the fused run kernel needs a 256-CU device")
+        for tk in prompt[:plen]:
+            assert g.step(tk) == o.step(tk)
+        for it in range(6):
+            toks = [prompt[plen + it], (prompt[it] * 7 + 11) % d.n_vocab][:nl]
+            assert list(g.verify(toks)) == list(o.verify(toks))
+            for ln in range(nl):
+                assert np.array_equal(bits(g.hidden(ln)), bits(o.hidden(ln))), (plen, it, ln, "hidden")
+                assert np.array_equal(bits(g.logits(ln)), bits(o.logits(ln))), (plen, it, ln, "logits")
+            g.commit(1)
+            o.commit(1)
+        g.close()
+        o.close()
