@@ -182,26 +182,6 @@ OXE_DEV void wdot(const WSlice<K, MAXP> &s, int nr, const int8_t *xq, int xq_ld,
     __syncthreads();
 }
 
-// ---- cache warm-up -----------------------------------------------------------------------------
-// Workgroups with no work in a latency-bound phase read part `part` of `nparts` of a byte range the
-// next phase will stream, so it is served from the device's last-level (memory-side) cache. The
-// values are folded into one word that is stored (to an unused word) only when it equals an
-// arbitrary constant, which keeps the loads.
-OXE_DEV void warm(const void *base, size_t bytes, int part, int nparts, uint32_t *sink) {
-    const uint4 *p = (const uint4 *)base;
-    const size_t n16 = bytes / 16;
-    const size_t b0 = n16 * (size_t)part / nparts, b1 = n16 * (size_t)(part + 1) / nparts;
-    uint32_t x = 0;
-    for (size_t i = b0 + threadIdx.x; i < b1; i += 8 * FT) {
-        uint4 v[8];
-#pragma unroll
-        for (int k = 0; k < 8; k++) v[k] = i + (size_t)k * FT < b1 ? p[i + (size_t)k * FT] : make_uint4(0, 0, 0, 0);
-#pragma unroll
-        for (int k = 0; k < 8; k++) x ^= v[k].x ^ v[k].y ^ v[k].z ^ v[k].w;
-    }
-    if (x == 0x9e3779b9u) *sink = x;
-}
-
 // ---- norm prologue (oxe_rms_norm_mul_f32, oxe_ops.cpp:32-42), lane l on threads [256 l, 256 l + 256)
 struct NormSm {
     double red[2][4];

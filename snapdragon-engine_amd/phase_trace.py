@@ -25,7 +25,7 @@ PHASES = {1: "proj", 2: "dn", 3: "scores", 4: "pv", 5: "out", 6: "router", 7: "e
 MARKS = {101: "experts: union", 102: "experts: gate/up loads issued", 103: "experts: issue drained",
          104: "experts: gate/up dot", 105: "experts: logits load", 106: "experts: route_wave",
          111: "proj: norm prologue", 112: "proj: dot", 121: "dn: conv", 122: "dn: norms + gates",
-         123: "dn: delta rule", 131: "router: norm prologue", 132: "router: f32 dots", 141: "pv: softmax",
+         123: "dn: delta rule", 131: "router: norm prologue", 132: "router: f32 dots", 141: "pv: V tile to LDS",
          142: "pv: V.p + reduce", 143: "pv: scores load + max", 144: "pv: exp, sum, probabilities", 151: "scores: q/k prologue",
          161: "down: inputs", 162: "down: block dots", 163: "down: chains"}
 
