@@ -4,7 +4,7 @@ Builds the 35B-A3B-shaped synthetic model on the GPU, prefills the bench prompt,
 kernel's phase trace on, runs host-driven 2-lane verify steps and prints, per phase kind, the mean
 time from the barrier release (first workgroup to pass) to the last workgroup done, the gap before
 it (previous phase done to this release) and the median sub-step marks. Times from the device wall
-clock (100 MHz).
+clock (100 MHz); "pass skew" is the time from the first to the last workgroup passing the barrier.
 
     python snapdragon-engine_amd/phase_trace.py [--prompt 512] [--steps 3]
 """
@@ -47,10 +47,11 @@ def analyse(tr):
     agg = {}
     for k in range(n):
         name = PHASES.get(int(ids[k]), str(int(ids[k])))
-        a = agg.setdefault(name, [0, 0.0, 0.0])
+        a = agg.setdefault(name, [0, 0.0, 0.0, 0.0])
         a[0] += 1
         a[1] += (done[k] - rel[k]) / 100.0
         a[2] += (rel[k] - done[k - 1]) / 100.0 if k > 0 else 0.0
+        a[3] += (pas[:, k].max() - rel[k]) / 100.0
     marks = {}
     for g in range(G):
         ev = tr[g][tr[g, :, 0] >= 100].astype(np.int64)
@@ -76,9 +77,10 @@ def main():
         x = int(g[0])
     total, agg, marks = analyse(e.read_trace())
     print(f"verify run (2 lanes, 40 layers + LM head) at position {e.pos}: {total:.1f} us")
-    print(f"{'phase':10s} {'count':>5s} {'release->done us':>17s} {'gap before us':>14s} {'total us':>9s}")
-    for name, (cnt, dur, gap) in agg.items():
-        print(f"{name:10s} {cnt:5d} {dur / cnt:17.2f} {gap / cnt:14.2f} {dur + gap:9.1f}")
+    print(f"{'phase':10s} {'count':>5s} {'release->done us':>17s} {'gap before us':>14s} {'pass skew us':>13s} "
+          f"{'total us':>9s}")
+    for name, (cnt, dur, gap, skew) in agg.items():
+        print(f"{name:10s} {cnt:5d} {dur / cnt:17.2f} {gap / cnt:14.2f} {skew / cnt:13.2f} {dur + gap:9.1f}")
     print("sub-steps (median over workgroups and layers, us):")
     for i in sorted(marks):
         v = np.array(marks[i])
