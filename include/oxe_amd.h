@@ -39,6 +39,15 @@ OXE_API int oxe_hip_quantize_row_q8_0(const float *x, int64_t k, int64_t nrows, 
 OXE_API int oxe_hip_gemv_q8_0(int64_t k, int64_t nr, int nl, const int8_t *wq, const uint16_t *wd, const int8_t *xq,
                               const uint16_t *xd, float *y, int32_t *isum, void *stream);
 
+/* Q8_0 GEMM for prefill: y[t][r] (row stride ldy >= nr) = W[r] . x[t] for nt token rows of
+ * activations (oxe_hip_quantize_row_q8_0 output) against nr weight rows (layout as in
+ * oxe_hip_gemv_q8_0); k a multiple of 256. Each output equals the GEMV's bit for bit (block dots
+ * on the int8 matrix cores, the fp32 chain over blocks in order). Replaces ggml_gemm_q8_0_4x8_q8_0
+ * (crates/kernels-sys/src/lib.rs:95; vendor/ggml-subset/generated/repack_subset.cpp:3804-3954).
+ * Returns 0, -1 (bad shape or null pointer) or -2 (launch error). */
+OXE_API int oxe_hip_gemm_q8_0(int64_t k, int64_t nr, int64_t nt, const int8_t *wq, const uint16_t *wd, const int8_t *xq,
+                              const uint16_t *xd, float *y, int64_t ldy, void *stream);
+
 /* Parity hook (no counterpart in the reference): y[i] = f(x) for the float x with bits
  * start + i*stride, i < n, on the device; f: 0 expf and 1 log1pf (the C library functions the
  * reference calls, oxe_ops.cpp:80-89), 2 ggml_v_expf (vec.h:1154-1175), 3 the sigmoid and

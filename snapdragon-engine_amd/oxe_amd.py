@@ -30,6 +30,7 @@ def lib():
         sig = {
             "oxe_hip_quantize_row_q8_0": (i32, [vp, i64, i64, vp, vp, vp]),
             "oxe_hip_gemv_q8_0": (i32, [i64, i64, i32, vp, vp, vp, vp, vp, vp, vp]),
+            "oxe_hip_gemm_q8_0": (i32, [i64, i64, i64, vp, vp, vp, vp, vp, i64, vp]),
             "oxe_hip_eval_unary": (i32, [i32, C.c_uint32, i64, i64, vp, vp]),
         }
         for name, (res, args) in sig.items():
@@ -123,6 +124,17 @@ def gemv_q8_0(wq, wd, xq, xd, y=None, isum=None):
     if y is None:
         y = torch.empty((nl, nr), dtype=torch.float32, device=wq.device)
     check(lib().oxe_hip_gemv_q8_0(k, nr, nl, _p(wq), _p(wd), _p(xq), _p(xd), _p(y), _p(isum), _stream()), "gemv_q8_0")
+    return y
+
+
+def gemm_q8_0(wq, wd, xq, xd, y=None):
+    """y[t, r] = Q8_0 GEMM of token rows t (any count) over weight rows r (prefill; int8 MFMA)."""
+    import torch
+    nr, k = wq.shape
+    nt = xq.shape[0]
+    if y is None:
+        y = torch.empty((nt, nr), dtype=torch.float32, device=wq.device)
+    check(lib().oxe_hip_gemm_q8_0(k, nr, nt, _p(wq), _p(wd), _p(xq), _p(xd), _p(y), y.stride(0), _stream()), "gemm_q8_0")
     return y
 
 
