@@ -106,11 +106,23 @@ OXE_API int oxe_engine_fused(const oxe_engine *e);
 OXE_API int oxe_engine_set_trace(oxe_engine *e, int on);
 OXE_API int64_t oxe_engine_read_trace(oxe_engine *e, unsigned long long *host, int64_t cap);
 
+/* Batched prefill of n prompt tokens at pos..pos+n-1 (all layers over the whole batch: int8
+ * matrix-core GEMMs for every weight matrix, token-parallel norms / routing / attention, the conv
+ * and delta-net recurrences token by token). KV cache, recurrent state, logits and hidden state of
+ * the last token are those of n decode steps, bit for bit; *next = argmax of the last token.
+ * hidden (optional host [n][n_embd]): every position's h_nextn. Replaces Engine::prefill_ext
+ * (crates/model/src/engine/prefill.rs:763). */
+OXE_API int oxe_engine_prefill(oxe_engine *e, const uint32_t *toks, int n, uint32_t *next, float *hidden);
+
 /* ---- MTP depth-1 speculative decoding (crates/model/src/mtp.rs MtpDriver, depth 1) --------- */
 
 /* Append prompt tokens through 2-token verify runs and the MTP catch-up (MtpDriver::prefill,
  * mtp.rs:450-463); *next = argmax after the last token. */
 OXE_API int oxe_mtp_prefill(oxe_engine *e, const uint32_t *toks, int n, uint32_t *next);
+/* Append a prompt with the batched prefill, then seed the MTP KV from every position's h_nextn in
+ * one batched pass (MtpDriver::prefill_batched, mtp.rs:468-500; one token: step_plain). Same
+ * engine state, MTP KV and *next as oxe_mtp_prefill. */
+OXE_API int oxe_mtp_prefill_batched(oxe_engine *e, const uint32_t *toks, int n, uint32_t *next);
 /* One speculative step from token x (MtpDriver::step, mtp.rs:522-592), host-driven: out[0..n_out)
  * = the greedy tokens that follow (accepted draft + bonus). override_d1 >= 0 replaces the draft
  * (the reference's draft_override test hook, mtp.rs:328-330). */

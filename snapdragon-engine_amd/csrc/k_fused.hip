@@ -521,29 +521,6 @@ OXE_DEV float conv4f(float s0, float s1, float s2, float xn, const float *c) {
     sumf = sumf + p3;
     return sumf;
 }
-// max over the 32-lane half of the wave holding this lane (exact, any order)
-OXE_DEV float half_max(float v) {
-    v = fmaxf(v, dpp_f<DPP_ROR8>(v));
-    v = fmaxf(v, dpp_f<DPP_ROR4>(v));
-    v = fmaxf(v, dpp_f<DPP_ROR2>(v));
-    v = fmaxf(v, dpp_f<DPP_ROR1>(v));
-    const float lo = fmaxf(readlane_f(v, 0), readlane_f(v, 16)), hi = fmaxf(readlane_f(v, 32), readlane_f(v, 48));
-    return (threadIdx.x & 63) < 32 ? lo : hi;
-}
-// quantize_row_q8_0 (NEON) of the 32-value block held one value per lane by each half of the
-// wave: *d = the block scale; returns in lane 4 i the codes of lanes 4 i .. 4 i + 3 (byte order)
-OXE_DEV uint32_t quant32_lanes(float v, float *d) {
-    const float m = half_max(__builtin_fabsf(v));
-    const float dd = m / 127.0f;
-    const float id = dd != 0.0f ? 1.0f / dd : 0.0f;
-    const int32_t q = (int32_t)__builtin_rintf(v * id);
-    int p = (int)((uint32_t)(q & 0xff) << (8 * (threadIdx.x & 3)));
-    p |= dpp_i<DPP_XOR1>(p);
-    p |= dpp_i<DPP_XOR2>(p);
-    *d = dd;
-    return (uint32_t)p;
-}
-
 template <int NL>
 FZ_PHASE bool phase_dn(const RunCtl *ctl, const FusedArgs *ap, int il) {
     Ctx<NL> c = make_ctx<NL>(ctl, ap);

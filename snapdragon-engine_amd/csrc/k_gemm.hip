@@ -16,6 +16,7 @@
 
 #include "../../include/oxe_amd.h"
 #include "oxe_common.h"
+#include "oxe_gemm.h"
 
 namespace oxe {
 
@@ -29,18 +30,32 @@ constexpr int NT = 256;                // threads
 
 typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
 
-__global__ __launch_bounds__(gm::NT) void gemm_q8_kernel(const int8_t *__restrict__ wq, const uint16_t *__restrict__ wd,
-                                                         const int8_t *__restrict__ xq, const uint16_t *__restrict__ xd,
-                                                         float *__restrict__ y, int64_t nr, int64_t nt, int64_t k,
-                                                         int64_t ldy) {
+__global__ __launch_bounds__(gm::NT) void gemm_q8_kernel(GemmArgs a) {
     using namespace gm;
     __shared__ __align__(16) int8_t sw[BM * LDR];
     __shared__ __align__(16) int8_t sx[BN * LDR];
     __shared__ __align__(16) float sdw[NBC][BM + 4];   // scales transposed: a lane's 4 rows are one 16-byte read
     __shared__ float sdx[NBC][BN + 4];
+    __shared__ int64_t sxr[BN];                          // activation row of each of the tile's output rows
     const int t = threadIdx.x, lane = t & 63, w = t >> 6;
-    const int64_t r0 = (int64_t)blockIdx.x * BM, t0 = (int64_t)blockIdx.y * BN;
-    const int64_t nb = k / 32;
+    const int64_t k = a.k, nr = a.nr, nb = k / 32;
+    const int64_t r0 = (int64_t)blockIdx.x * BM;
+    int64_t p0, pn;
+    const int8_t *wq = a.wq;
+    const uint16_t *wd = a.wd;
+    if (a.tiles) {
+        if (a.tile_count && (int)blockIdx.y >= *a.tile_count) return;   // uniform: before any barrier
+        const int4 tl = a.tiles[blockIdx.y];
+        wq += (int64_t)tl.x * a.wq_stride;
+        wd += (int64_t)tl.x * a.wd_stride;
+        p0 = tl.y;
+        pn = tl.z;
+    } else {
+        p0 = (int64_t)blockIdx.y * BN;
+        pn = a.nt - p0 < BN ? a.nt - p0 : BN;
+    }
+    if (t < BN) sxr[t] = t < pn ? (a.xrow ? (int64_t)a.xrow[p0 + t] : p0 + t) : -1;
+    __syncthreads();
     // wave w: rows 32 (w & 1) .., tokens 32 (w >> 1) ..; MFMA tile (i, j) at +16 i, +16 j
     const int wr = 32 * (w & 1), wt = 32 * (w >> 1);
     const int fr = lane & 15, fk = 8 * (lane >> 4);   // fragment row / token and its 8 k bytes
@@ -56,18 +71,18 @@ __global__ __launch_bounds__(gm::NT) void gemm_q8_kernel(const int8_t *__restric
 #pragma unroll
         for (int p = 0; p < BM * KC / 16 / NT; p++) {
             const int i = t + NT * p, row = i / (KC / 16), ch = i % (KC / 16);
-            const int64_t gr = r0 + row, gt = t0 + row;
-            const uint4 a = gr < nr ? *(const uint4 *)(wq + gr * k + kc + 16 * ch) : make_uint4(0, 0, 0, 0);
-            const uint4 b = gt < nt ? *(const uint4 *)(xq + gt * k + kc + 16 * ch) : make_uint4(0, 0, 0, 0);
-            *(uint4 *)(sw + row * LDR + 16 * ch) = a;
-            *(uint4 *)(sx + row * LDR + 16 * ch) = b;
+            const int64_t gr = r0 + row, xr = sxr[row];
+            const uint4 u = gr < nr ? *(const uint4 *)(wq + gr * k + kc + 16 * ch) : make_uint4(0, 0, 0, 0);
+            const uint4 v = xr >= 0 ? *(const uint4 *)(a.xq + xr * k + kc + 16 * ch) : make_uint4(0, 0, 0, 0);
+            *(uint4 *)(sw + row * LDR + 16 * ch) = u;
+            *(uint4 *)(sx + row * LDR + 16 * ch) = v;
         }
         // stage scales as f32: 64 rows x 8 blocks for W and X
         for (int i = t; i < BM * NBC; i += NT) {
             const int row = i / NBC, bb = i % NBC;
-            const int64_t gr = r0 + row, gt = t0 + row;
+            const int64_t gr = r0 + row, xr = sxr[row];
             sdw[bb][row] = gr < nr ? h2f(wd[gr * nb + kc / 32 + bb]) : 0.0f;
-            sdx[bb][row] = gt < nt ? h2f(xd[gt * nb + kc / 32 + bb]) : 0.0f;
+            sdx[bb][row] = xr >= 0 ? h2f(a.xd[xr * nb + kc / 32 + bb]) : 0.0f;
         }
         __syncthreads();
 #pragma unroll
@@ -104,9 +119,23 @@ __global__ __launch_bounds__(gm::NT) void gemm_q8_kernel(const int8_t *__restric
         for (int j = 0; j < 2; j++)
 #pragma unroll
             for (int v = 0; v < 4; v++) {
-                const int64_t gr = r0 + wr + 16 * i + 4 * (lane >> 4) + v, gt = t0 + wt + 16 * j + (lane & 15);
-                if (gr < nr && gt < nt) y[gt * ldy + gr] = acc[i][j][v];
+                const int64_t gr = r0 + wr + 16 * i + 4 * (lane >> 4) + v;
+                const int tt = wt + 16 * j + (lane & 15);
+                if (gr < nr && tt < pn) {
+                    const int64_t p = p0 + tt;
+                    a.y[p * a.ldy + gr] = a.res ? acc[i][j][v] + a.res[p * a.ldr + gr] : acc[i][j][v];
+                }
             }
+}
+
+int gemm_launch(const GemmArgs &a, int64_t ntiles, hipStream_t st) {
+    using namespace gm;
+    if (a.k <= 0 || a.k % KC != 0 || a.nr <= 0 || a.ldy < a.nr) return -1;
+    if (!a.wq || !a.wd || !a.xq || !a.xd || !a.y) return -1;
+    const int64_t ny = a.tiles ? ntiles : (a.nt + BN - 1) / BN;
+    if (ny <= 0) return 0;
+    hipLaunchKernelGGL(gemm_q8_kernel, dim3((unsigned)((a.nr + BM - 1) / BM), (unsigned)ny), dim3(NT), 0, st, a);
+    return hipGetLastError() == hipSuccess ? 0 : -2;
 }
 
 }  // namespace oxe
@@ -115,12 +144,9 @@ extern "C" {
 
 int oxe_hip_gemm_q8_0(int64_t k, int64_t nr, int64_t nt, const int8_t *wq, const uint16_t *wd, const int8_t *xq,
                       const uint16_t *xd, float *y, int64_t ldy, void *stream) {
-    using namespace oxe::gm;
-    if (k <= 0 || k % KC != 0 || nr <= 0 || nt <= 0 || ldy < nr) return -1;
-    if (!wq || !wd || !xq || !xd || !y) return -1;
-    const dim3 grid((unsigned)((nr + BM - 1) / BM), (unsigned)((nt + BN - 1) / BN));
-    hipLaunchKernelGGL(oxe::gemm_q8_kernel, grid, dim3(NT), 0, (hipStream_t)stream, wq, wd, xq, xd, y, nr, nt, k, ldy);
-    return hipGetLastError() == hipSuccess ? 0 : -2;
+    if (nt <= 0) return -1;
+    oxe::GemmArgs a{wq, wd, xq, xd, y, nullptr, nr, nt, k, ldy, 0, nullptr, 0, 0, nullptr};
+    return oxe::gemm_launch(a, 0, (hipStream_t)stream);
 }
 
 }  // extern "C"

@@ -1,0 +1,725 @@
+// Batched prefill (Engine::prefill / prefill_nextn, crates/model/src/engine/prefill.rs:752-773): the
+// prompt's tokens go through each layer together, the weight matrices as int8 matrix-core GEMMs
+// (k_gemm.hip, bitwise equal to the decode GEMV for Q8_0), everything else as token-parallel
+// kernels in the decode's float order. The recurrences (conv window, delta-rule state) run token
+// by token; each attention query sees exactly the positions a single-token step at its position
+// sees. So the KV cache, the recurrent state, every position's h_nextn and the last token's logits
+// are the bits of token-by-token decoding, which is what the reference's batched prefill gives
+// for Q8_0 weights (docs/lab-notes/M3-PREFILL.md:55-75). The recurrent state is read from and
+// written back to the engine's current slot.
+//
+// Also the batched MTP KV seeding (MtpDriver::flush of many pairs, mtp.rs:425-446): eh_proj entry
+// and the MTP layer's K / V rows for all pending (token, h) pairs in one pass.
+#include <algorithm>
+#include <vector>
+
+#include "oxe_engine_host.h"
+#include "oxe_gemm.h"
+#include "oxe_prologue.h"
+#include "oxe_route.h"
+#include "oxe_shape.h"
+
+namespace oxe {
+
+using namespace shp;
+
+namespace pf {
+
+// ---- per-token norm + Q8_0 (the decode prologue for T rows) ---------------------------------
+// row t: y = rms_norm(x_t) * w (oxe_ops.cpp:32-42); codes / scales to xq / xd (row stride xq_ld
+// bytes, xq_ld / 32 scales); optional f32 y to xn. toks (optional): x_t is the token's embedding,
+// stored to x first (the residual of layer 0, the replay source of the norm).
+__global__ __launch_bounds__(PT) void norm_quant_kernel(Q8W emb, const uint32_t *toks, float *x, const float *w, float eps,
+                                                        int8_t *xq, uint16_t *xd, int64_t xq_ld, float *xn) {
+    __shared__ NormScratch ns;
+    const int64_t t = blockIdx.x;
+    float v[EPT];
+    float *xr = x + t * E;
+    if (toks) {
+        embed8(emb, toks[t], v);
+        store8(xr, v);
+        __syncthreads();
+    } else {
+        load8(xr, v);
+    }
+    rms_norm_mul_e(v, xr, w, eps, ns);
+    quant8(v, xq + t * xq_ld + EPT * threadIdx.x, xd + t * (xq_ld / 32) + (EPT * threadIdx.x) / 32);
+    if (xn) store8(xn + t * E, v);
+}
+
+// ---- delta-net -----------------------------------------------------------------------------
+// causal conv + silu (oxe_ssm_conv_step_f32, oxe_ops.cpp:175-201, nc = 4): the window of token t is
+// (x_{t-3}, x_{t-2}, x_{t-1}, x_t), the positions before the chunk from the layer's state, so every
+// (token, channel) is independent; the four products are rounded, then added in order to +0.
+OXE_DEV float conv4_pf(float s0, float s1, float s2, float xn, const float *c) {
+    const float p0 = s0 * c[0], p1 = s1 * c[1], p2 = s2 * c[2], p3 = xn * c[3];
+    float sumf = 0.0f;
+    sumf = sumf + p0;
+    sumf = sumf + p1;
+    sumf = sumf + p2;
+    sumf = sumf + p3;
+    return sumf;
+}
+__global__ __launch_bounds__(256) void conv_kernel(const float *proj, int T, const float *conv_w, const float *state,
+                                                   float *cy) {
+    const int c = blockIdx.x * 256 + threadIdx.x;
+    const int64_t t = blockIdx.y;
+    float cw[KC];
+#pragma unroll
+    for (int i = 0; i < KC; i++) cw[i] = conv_w[(int64_t)c * KC + i];
+    const float *st = state + (int64_t)c * (KC - 1);
+    float s[KC];
+#pragma unroll
+    for (int i = 0; i < KC; i++) {
+        const int64_t tt = t - (KC - 1) + i;   // token of window slot i (< 0: the state's slot tt + 3)
+        s[i] = tt >= 0 ? proj[tt * DN_ROWS + c] : st[tt + (KC - 1)];
+    }
+    cy[t * NCH + c] = v_silu(conv4_pf(s[0], s[1], s[2], s[3], cw));
+}
+// the window after the chunk: the last three inputs (for T < 3 partly the older state)
+__global__ __launch_bounds__(256) void conv_state_kernel(const float *proj, int T, float *state) {
+    const int c = blockIdx.x * 256 + threadIdx.x;
+    float *st = state + (int64_t)c * (KC - 1);
+    float n[KC - 1];
+#pragma unroll
+    for (int i = 0; i < KC - 1; i++) {
+        const int tt = T - (KC - 1) + i;   // token of new slot i (< 0: old slot tt + 3)
+        n[i] = tt >= 0 ? proj[(int64_t)tt * DN_ROWS + c] : st[tt + (KC - 1)];
+    }
+#pragma unroll
+    for (int i = 0; i < KC - 1; i++) st[i] = n[i];
+}
+
+// l2 norms of q and k (oxe_gdn_l2_norm_f32: rms_norm with eps/n, then * 1/sqrt(n)), one wave per
+// (token, key head, q|k), in place; the gates of (token, value head) (engine.rs:2509-2524)
+__global__ __launch_bounds__(256) void dn_prep_kernel(float *cy, const float *proj, const float *dt_bias,
+                                                      const float *ssm_a, float eps, float *gg, float *gb) {
+    const int64_t t = blockIdx.x;
+    const int w = blockIdx.y * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;   // 0..31
+    const int kh = w >> 1;
+    float *xv = cy + t * NCH + ((w & 1) ? NKH * DS : 0) + kh * DS;
+    const float a0 = xv[lane], a1 = xv[lane + 64];
+    const float nf = (float)DS;
+    const float mean = wave_mean_sq_128(a0, a1, xv);
+    const float scale = 1.0f / sqrtf(mean + eps / nf);
+    const float sq = 1.0f / sqrtf(nf);
+    const float o0 = (a0 * scale) * sq, o1 = (a1 * scale) * sq;
+    xv[lane] = o0;
+    xv[lane + 64] = o1;
+    if (blockIdx.y == 0 && threadIdx.x < NVH) {
+        const int vh = threadIdx.x;
+        const float ab = proj[t * DN_ROWS + DN_ALPHA + vh] + dt_bias[vh];
+        gg[t * NVH + vh] = oxe_libm::expf_c(softplus_c(ab) * ssm_a[vh]);
+        gb[t * NVH + vh] = sigmoid_c(proj[t * DN_ROWS + DN_BETA + vh]);
+    }
+}
+
+// delta rule (oxe_gated_delta_net_step_f32_x4_from, oxe_ops.cpp:268-345) over the T tokens in order.
+// Workgroup = (value head vh = b / 8, state rows 16 (b % 8) ..); thread (row rg = t / 16, chain
+// c = t % 16) holds row elements c + 16 s in registers: chain c of ggml_vec_dot_f32, whose NEON
+// reduction tree is the DPP sequence of dot16_tree_dpp. Per token the inputs come from LDS, staged
+// DT_T tokens at a time. o[t][vh * 128 + row] = (S_row . q) / sqrt(128).
+constexpr int DT_T = 32;
+__global__ __launch_bounds__(256) void delta_kernel(const float *cy, const float *gg, const float *gb, float *ssm, float *o,
+                                                    int T) {
+    __shared__ float s_k[DT_T][DS], s_q[DT_T][DS], s_v[DT_T][16], s_g[DT_T], s_b[DT_T];
+    const int vh = blockIdx.x >> 3, row0 = (blockIdx.x & 7) * 16, kh = vh % NKH;
+    const int t = threadIdx.x, rg = t >> 4, cc = t & 15;
+    float *srow = ssm + ((int64_t)vh * HV + row0 + rg) * HV;
+    float r[8];
+#pragma unroll
+    for (int s = 0; s < 8; s++) r[s] = srow[cc + 16 * s];
+    const float scale = 1.0f / sqrtf((float)HV);
+    for (int t0 = 0; t0 < T; t0 += DT_T) {
+        const int nt = T - t0 < DT_T ? T - t0 : DT_T;
+        __syncthreads();
+        for (int i = t; i < nt * DS; i += 256) {
+            const int tt = i / DS, e = i % DS;
+            const float *row = cy + (int64_t)(t0 + tt) * NCH;
+            s_q[tt][e] = row[kh * DS + e];
+            s_k[tt][e] = row[NKH * DS + kh * DS + e];
+        }
+        for (int i = t; i < nt * 16; i += 256) {
+            const int tt = i / 16, e = i % 16;
+            s_v[tt][e] = cy[(int64_t)(t0 + tt) * NCH + 2 * NKH * DS + vh * HV + row0 + e];
+        }
+        if (t < nt) {
+            s_g[t] = gg[(int64_t)(t0 + t) * NVH + vh];
+            s_b[t] = gb[(int64_t)(t0 + t) * NVH + vh];
+        }
+        __syncthreads();
+        for (int tt = 0; tt < nt; tt++) {
+            const float eg = s_g[tt], beta = s_b[tt];
+            float acc = 0.0f;
+#pragma unroll
+            for (int s = 0; s < 8; s++) {
+                r[s] = r[s] * eg;
+                acc = __builtin_fmaf(r[s], s_k[tt][cc + 16 * s], acc);
+            }
+            const float sk = dot16_tree_dpp(acc);
+            const float delta = (s_v[tt][rg] - sk) * beta;
+            acc = 0.0f;
+#pragma unroll
+            for (int s = 0; s < 8; s++) {
+                r[s] = __builtin_fmaf(s_k[tt][cc + 16 * s], delta, r[s]);
+                acc = __builtin_fmaf(r[s], s_q[tt][cc + 16 * s], acc);
+            }
+            const float sq = dot16_tree_dpp(acc);
+            if (cc == 0) o[(int64_t)(t0 + tt) * DIN + vh * HV + row0 + rg] = sq * scale;
+        }
+    }
+#pragma unroll
+    for (int s = 0; s < 8; s++) srow[cc + 16 * s] = r[s];
+}
+
+// gated norm (rms_norm(o) * ssm_norm * silu(z), engine.rs:2560-2566) + Q8_0 of (token, value head),
+// one wave each
+__global__ __launch_bounds__(256) void gated_norm_kernel(const float *o, const float *proj, const float *ssm_norm, float eps,
+                                                         int8_t *oq, uint16_t *od) {
+    const int64_t t = blockIdx.x;
+    const int vh = blockIdx.y * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const float *orow = o + t * DIN + vh * HV;
+    const float x0 = orow[lane], x1 = orow[lane + 64];
+    const float mean = wave_mean_sq_128(x0, x1, orow);
+    const float sc = 1.0f / sqrtf(mean + eps);
+    const float *z = proj + t * DN_ROWS + DN_Z + vh * HV;
+    const float o0 = ((x0 * sc) * ssm_norm[lane]) * v_silu(z[lane]);
+    const float o1 = ((x1 * sc) * ssm_norm[lane + 64]) * v_silu(z[lane + 64]);
+    // Q8_0 blocks of 32: lanes 0..31 hold blocks 0 (o0) and 2 (o1), lanes 32..63 blocks 1 and 3
+    float d0, d1;
+    const uint32_t p0 = quant32_lanes(o0, &d0), p1 = quant32_lanes(o1, &d1);
+    int8_t *q = oq + t * DIN + vh * HV;
+    if ((lane & 3) == 0) {
+        *(uint32_t *)(q + lane) = p0;
+        *(uint32_t *)(q + lane + 64) = p1;
+    }
+    uint16_t *d = od + t * (DIN / 32) + vh * (HV / 32);
+    if (lane == 0) { d[0] = f2h(d0); d[2] = f2h(d1); }
+    if (lane == 32) { d[1] = f2h(d0); d[3] = f2h(d1); }
+}
+
+// ---- attention -------------------------------------------------------------------------------
+// q heads: rms_norm * q_norm, RoPE NEOX, f16 (engine.rs:2614-2703); K heads the same with k_norm
+// into the K cache at the token's position; the V rows f16 into V^T. One wave per vector: waves
+// 0..15 the q heads (skipped when kv_only), 16..17 the K heads, 18 the V rows.
+__global__ __launch_bounds__(256) void attn_prep_kernel(const float *proj, const float *q_norm, const float *k_norm,
+                                                        const float *rope, int pos0, float eps, uint16_t *qh,
+                                                        uint16_t *kc, uint16_t *vt, int n_ctx, int kv_only) {
+    const int64_t t = blockIdx.x;
+    const int w = blockIdx.y * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const int pos = pos0 + (int)t;
+    const float *pr = proj + t * DN_ROWS;
+    if (w < NH + NKV) {
+        if (w < NH && kv_only) return;
+        const bool isk = w >= NH;
+        const float *src = isk ? pr + AT_K + (w - NH) * HD : pr + w * 2 * HD;
+        const float *nw = isk ? k_norm : q_norm;
+        float v[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) v[i] = src[lane + 64 * i];
+        const float mean = wave_mean_sq_256(v, src);
+        const float scale = 1.0f / sqrtf(mean + eps);
+#pragma unroll
+        for (int i = 0; i < 4; i++) v[i] = (v[i] * scale) * nw[lane + 64 * i];
+        // rotate_pairs NEOX (oxe_ops.cpp:443-455) of pairs (i, i + 32), i < 32, as rope_neox_lds
+        const float *cs = rope + (int64_t)pos * NROT + 2 * (lane & (NROT / 2 - 1));
+        const float c = cs[0], s = cs[1];
+        const float oth = __shfl_xor(v[0], NROT / 2, 64);
+        if (lane < NROT / 2) v[0] = __builtin_fmaf(v[0], c, -(oth * s));
+        else v[0] = __builtin_fmaf(oth, s, v[0] * c);
+        uint16_t *dst = isk ? kc + ((int64_t)(w - NH) * n_ctx + pos) * HD : qh + (t * NH + w) * HD;
+#pragma unroll
+        for (int i = 0; i < 4; i++) dst[lane + 64 * i] = f2h(v[i]);
+    } else if (w == NH + NKV) {
+        for (int i = lane; i < NKV * HD; i += 64) vt[(int64_t)i * n_ctx + pos] = f2h(pr[AT_V + i]);
+    }
+}
+
+typedef _Float16 h2p __attribute__((ext_vector_type(2)));
+OXE_DEV h2p u2h(uint32_t u) { return __builtin_bit_cast(h2p, u); }
+OXE_DEV uint32_t h2u(h2p v) { return __builtin_bit_cast(uint32_t, v); }
+// GGML_F16x8_REDUCE of the 4 accumulators held by the 4 lanes of a quad, then the f32 widening and
+// vaddvq (the decode attention's reduce)
+OXE_DEV float f16x8_reduce_quad(h2p acc[4]) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) acc[i] = acc[i] + u2h((uint32_t)dpp_i<DPP_XOR2>((int)h2u(acc[i])));
+#pragma unroll
+    for (int i = 0; i < 4; i++) acc[i] = acc[i] + u2h((uint32_t)dpp_i<DPP_XOR1>((int)h2u(acc[i])));
+    const float t0 = (float)acc[0].x + (float)acc[2].x;
+    const float t1 = (float)acc[0].y + (float)acc[2].y;
+    const float t2 = (float)acc[1].x + (float)acc[3].x;
+    const float t3 = (float)acc[1].y + (float)acc[3].y;
+    return (t0 + t1) + (t2 + t3);
+}
+
+// One query (token t at position pos) and head h per workgroup (oxe_attn_head_f16,
+// oxe_ops.cpp:465-493): scores over positions <= pos (ggml_vec_dot_f16: 4 x 8 fp16 FMA chains,
+// chain (j, l) takes positions 32 s + 8 j + l), softmax over n_kv = pad256(pos + 1) with the -inf
+// mask (oxe_soft_max_f32, scale 1/16, the group sums added in double), f16 probabilities, then
+// V^T . p over n_kv (positions after pos contribute +0 . +0, as the zeroed cache rows of a
+// single-token step) and the sigmoid gate. f32 output o[t][h * 256 + d]. Dynamic LDS: scores
+// (f32) and probabilities (f16) of up to kv_cap positions.
+__global__ __launch_bounds__(256) void attn_kernel(const uint16_t *qh, const uint16_t *kc, const uint16_t *vt,
+                                                   const float *proj, int pos0, int n_ctx, int kv_cap, float *o) {
+    extern __shared__ __align__(16) float s_dyn[];
+    float *s_s = s_dyn;                             // [kv_cap]
+    uint16_t *s_p = (uint16_t *)(s_dyn + kv_cap);   // [kv_cap]
+    __shared__ __align__(16) uint16_t s_q[HD];
+    __shared__ double s_red[4];
+    __shared__ float s_mx[4];
+    __shared__ float s_f;
+    const int64_t t = blockIdx.x;
+    const int h = blockIdx.y, kvh = h / GQA, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int pos = pos0 + (int)t;
+    int n_kv = (pos + 1 + 255) / 256 * 256;
+    if (n_kv > n_ctx) n_kv = n_ctx;
+    if (tid < HD / 8) *(uint4 *)&s_q[8 * tid] = *(const uint4 *)(qh + (t * NH + h) * HD + 8 * tid);
+    __syncthreads();
+    // scores: thread (position pp = tid / 4 of a pass of 64, chain quad lane j = tid % 4)
+    {
+        const int pp = tid >> 2, j = tid & 3;
+        const uint16_t *kb = kc + (int64_t)kvh * n_ctx * HD;
+        for (int p0 = 0; p0 <= pos; p0 += 64) {
+            const int p = p0 + pp;
+            const uint16_t *krow = kb + (int64_t)(p <= pos ? p : pos) * HD;
+            h2p acc[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) acc[i] = h2p{(_Float16)0.0f, (_Float16)0.0f};
+#pragma unroll
+            for (int sx = 0; sx < HD / 32; sx++) {
+                const uint4 kv = *(const uint4 *)(krow + 32 * sx + 8 * j);
+                const uint4 qv = *(const uint4 *)(&s_q[32 * sx + 8 * j]);
+                acc[0] = __builtin_elementwise_fma(u2h(kv.x), u2h(qv.x), acc[0]);
+                acc[1] = __builtin_elementwise_fma(u2h(kv.y), u2h(qv.y), acc[1]);
+                acc[2] = __builtin_elementwise_fma(u2h(kv.z), u2h(qv.z), acc[2]);
+                acc[3] = __builtin_elementwise_fma(u2h(kv.w), u2h(qv.w), acc[3]);
+            }
+            const float sc = f16x8_reduce_quad(acc);
+            if (j == 0 && p <= pos) s_s[p] = sc;
+        }
+    }
+    __syncthreads();
+    const float scale = 1.0f / sqrtf((float)HD);
+    const int ng = n_kv / 4;
+    float mx = -__builtin_inff();
+    for (int g = tid; g < ng; g += 256)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int p = 4 * g + i;
+            const float wv = p <= pos ? s_s[p] * scale : -__builtin_inff();
+            mx = (mx > wv) ? mx : wv;
+        }
+    mx = wave_max_any(mx);
+    if (lane == 0) s_mx[w] = mx;
+    __syncthreads();
+    {
+        const float m01 = s_mx[0] > s_mx[1] ? s_mx[0] : s_mx[1], m23 = s_mx[2] > s_mx[3] ? s_mx[2] : s_mx[3];
+        mx = m01 > m23 ? m01 : m23;
+    }
+    // e = v_expf(w - max) kept in the score slots; group sums (e0 + e1) + (e2 + e3) added in double
+    double part = 0.0;
+    for (int g = tid; g < ng; g += 256) {
+        float e[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int p = 4 * g + i;
+            e[i] = v_expf((p <= pos ? s_s[p] * scale : -__builtin_inff()) - mx);
+        }
+        part += (double)((e[0] + e[1]) + (e[2] + e[3]));
+#pragma unroll
+        for (int i = 0; i < 4; i++) s_s[4 * g + i] = e[i];
+    }
+    part = wave_sum_d_any(part);
+    if (lane == 0) s_red[w] = part;
+    __syncthreads();
+    const double P = (s_red[0] + s_red[1]) + (s_red[2] + s_red[3]);
+    float f;
+    const bool ok = bracket_ok_recip(P, P, ng, &f);   // uniform
+    if (!ok) {
+        if (tid == 0) {
+            double sum = 0.0;
+            for (int g = 0; g < ng; g++) sum += (double)((s_s[4 * g] + s_s[4 * g + 1]) + (s_s[4 * g + 2] + s_s[4 * g + 3]));
+            s_f = (float)(1.0 / sum);
+        }
+        __syncthreads();
+        f = s_f;
+    }
+    for (int p = tid; p < n_kv; p += 256) s_p[p] = f2h(s_s[p] * f);
+    __syncthreads();
+    // V^T . p: thread (dim d0 + tid / 16, lane cp = tid % 16 of a 16-lane row): positions 32 s + 2 cp,
+    // + 1, i.e. chain quad j = cp / 4, accumulator cp % 4; the F16x8 reduce inside the row: ror 8 and
+    // ror 4 pair the quads as xor 2 / xor 1 of the reference tree, then the f32 tail in the quad
+    const int cp = tid & 15;
+    const uint16_t *vb = vt + (int64_t)kvh * HD * n_ctx;
+    for (int d0 = 0; d0 < HD; d0 += 16) {
+        const int d = d0 + (tid >> 4);
+        const uint16_t *vrow = vb + (int64_t)d * n_ctx;
+        h2p acc = h2p{(_Float16)0.0f, (_Float16)0.0f};
+        for (int s = 0; s < n_kv / 32; s++) {
+            const int p = 32 * s + 2 * cp;
+            uint32_t vw = *(const uint32_t *)(vrow + p);
+            if (p > pos) vw = 0u;
+            else if (p + 1 > pos) vw &= 0xffffu;
+            acc = __builtin_elementwise_fma(u2h(vw), u2h(*(const uint32_t *)&s_p[p]), acc);
+        }
+        h2p x = acc;
+        x = x + u2h((uint32_t)dpp_i<DPP_ROR8>((int)h2u(x)));
+        x = x + u2h((uint32_t)dpp_i<DPP_ROR4>((int)h2u(x)));
+        const float lo = (float)x.x, hi = (float)x.y;
+        const float tlo = lo + dpp_f<DPP_XOR2>(lo), thi = hi + dpp_f<DPP_XOR2>(hi);
+        const float s2 = tlo + thi;
+        const float out = s2 + dpp_f<DPP_XOR1>(s2);
+        if (cp == 0) {
+            const float gate = proj[t * DN_ROWS + h * 2 * HD + HD + d];
+            o[t * MIX_W + h * HD + d] = out * sigmoid_c(gate);
+        }
+    }
+}
+
+// ---- router, routing, MoE ------------------------------------------------------------------
+// router logits (ggml_vec_dot_f32: chain c of 16 over elements c + 16 q, then the NEON tree) of
+// (token, expert e < 256), and the shared-expert gate (e == 256: sigmoid of the dot with shexp_gate)
+__global__ __launch_bounds__(256) void router_kernel(const float *xn, const float *router, const float *shg, int T, float *lg,
+                                                     float *sg) {
+    const int64_t gid = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
+    const int cc = threadIdx.x & 15;
+    const int64_t t = gid / (NEXP + 1);
+    const int e = (int)(gid % (NEXP + 1));
+    const bool live = t < T;
+    const float *wv = e < NEXP ? router + (int64_t)e * E : shg;
+    const float *xv = xn + (live ? t : 0) * E;
+    float acc = 0.0f;
+    if (live)
+#pragma unroll 8
+        for (int q = 0; q < E / 16; q++) acc = __builtin_fmaf(wv[cc + 16 * q], xv[cc + 16 * q], acc);
+    const float v = dot16_tree_dpp(acc);
+    if (live && cc == 0) {
+        if (e < NEXP) lg[t * NEXP + e] = v;
+        else sg[t] = sigmoid_c(v);
+    }
+}
+
+// routing of one token per wave (softmax, top-8 with the reference's tie rules, renormalised
+// weights: route_wave, engine.rs:3414-3475)
+__global__ __launch_bounds__(256) void route_kernel(const float *lg, int T, int32_t *ids, float *wts, uint32_t *tie_count) {
+    __shared__ RouteOut ro[4];
+    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int64_t t = (int64_t)blockIdx.x * 4 + w;
+    if (t >= T) return;
+    if (lane == 0) ro[w].tie = 0;
+    wave_lds_sync();
+    route_wave(lg + t * NEXP, 0, ro[w]);
+    wave_lds_sync();
+    if (lane < KUSED) {
+        ids[t * KUSED + lane] = ro[w].ids[0][lane];
+        wts[t * KUSED + lane] = ro[w].w[0][lane];
+    }
+    if (lane == 0 && ro[w].tie) atomicAdd(tie_count, 1u);
+}
+
+// (token, rank) pairs grouped by expert: counts, then (one workgroup) offsets and the 64-pair tiles
+// of every expert, then the scatter. The order of pairs inside an expert's group is free: every
+// (pair, row) result of the grouped GEMMs is independent of its neighbours.
+constexpr int MO_CNT = 0, MO_OFF = NEXP, MO_FILL = 2 * NEXP, MO_NT = 3 * NEXP, MO_WORDS = 3 * NEXP + 1;
+__global__ void moe_count_kernel(const int32_t *ids, int np, int32_t *mo) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i < np) atomicAdd(&mo[MO_CNT + ids[i]], 1);
+}
+__global__ __launch_bounds__(NEXP) void moe_tiles_kernel(int32_t *mo, int4 *tiles) {
+    __shared__ int s_c[NEXP], s_t[NEXP];
+    const int e = threadIdx.x;
+    const int c = mo[MO_CNT + e], nt = (c + 63) / 64;
+    s_c[e] = c;
+    s_t[e] = nt;
+    __syncthreads();
+    for (int d = 1; d < NEXP; d <<= 1) {
+        const int a = e >= d ? s_c[e - d] : 0, b = e >= d ? s_t[e - d] : 0;
+        __syncthreads();
+        s_c[e] += a;
+        s_t[e] += b;
+        __syncthreads();
+    }
+    const int off = s_c[e] - c, tb = s_t[e] - nt;
+    mo[MO_OFF + e] = off;
+    mo[MO_FILL + e] = 0;
+    for (int s = 0; s < nt; s++) tiles[tb + s] = make_int4(e, off + 64 * s, min(64, c - 64 * s), 0);
+    if (e == NEXP - 1) mo[MO_NT] = s_t[e];
+}
+__global__ void moe_scatter_kernel(const int32_t *ids, int np, int32_t *mo, int32_t *ptok, int32_t *pair_of) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= np) return;
+    const int e = ids[i];
+    const int p = mo[MO_OFF + e] + atomicAdd(&mo[MO_FILL + e], 1);
+    ptok[p] = i / KUSED;
+    pair_of[i] = p;
+}
+
+// swiglu (ggml_vec_swiglu_f32: silu(gate) * up) of a gate/up output row with the 16-row interleave
+// (8 gate rows, then 8 up rows) and the Q8_0 of the 512 values: one workgroup per row
+__global__ __launch_bounds__(256) void swiglu_quant_kernel(const float *gu, int8_t *hq, uint16_t *hd) {
+    const int64_t r = blockIdx.x;
+    const float *g = gu + r * (2 * FF);
+#pragma unroll
+    for (int k = 0; k < 2; k++) {
+        const int i = threadIdx.x + 256 * k, tl = i >> 3, rr = i & 7;
+        const float h = v_silu(g[tl * 16 + rr]) * g[tl * 16 + 8 + rr];
+        float dd;
+        const uint32_t word = quant32_lanes(h, &dd);
+        if ((i & 3) == 0) *(uint32_t *)(hq + r * FF + i) = word;
+        if ((i & 31) == 0) hd[r * (FF / 32) + i / 32] = f2h(dd);
+    }
+}
+
+// combine (engine.rs:3591-3601): m = d_0 w_0, m = m + d_j w_j (j = 1..7), f = m + d_sh g_sh,
+// x2 = f + x1, per (token, row)
+__global__ __launch_bounds__(256) void combine_kernel(const float *dout, const int32_t *pair_of, const float *wts,
+                                                      const float *sh, const float *sg, const float *x1, float *x2,
+                                                      int T) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (int64_t)T * E) return;
+    const int64_t t = i / E, r = i % E;
+    float m = dout[(int64_t)pair_of[t * KUSED] * E + r] * wts[t * KUSED];
+    for (int j = 1; j < KUSED; j++) {
+        const float p = dout[(int64_t)pair_of[t * KUSED + j] * E + r] * wts[t * KUSED + j];
+        m = m + p;
+    }
+    const float s = sh[i] * sg[t];
+    const float f = m + s;
+    x2[i] = f + x1[i];
+}
+
+// ---- MTP entry for seeding -----------------------------------------------------------------
+// row t: [rms_norm(embd(tok)) * enorm ; rms_norm(h) * hnorm] quantised (K = 2 n_embd), as the
+// decode's entry prologue (engine.rs:2362-2390); the embedding goes to x (replay source) first
+__global__ __launch_bounds__(PT) void entry_in_kernel(Q8W emb, const uint32_t *toks, const float *h, float *x,
+                                                      const float *enorm, const float *hnorm, float eps, int8_t *xq,
+                                                      uint16_t *xd) {
+    __shared__ NormScratch ns;
+    const int64_t t = blockIdx.x;
+    float v[EPT];
+    embed8(emb, toks[t], v);
+    store8(x + t * E, v);
+    __syncthreads();
+    rms_norm_mul_e(v, x + t * E, enorm, eps, ns);
+    quant8(v, xq + t * 2 * E + EPT * threadIdx.x, xd + t * (2 * E / 32) + (EPT * threadIdx.x) / 32);
+    const float *hr = h + t * E;
+    load8(hr, v);
+    rms_norm_mul_e(v, hr, hnorm, eps, ns);
+    quant8(v, xq + t * 2 * E + E + EPT * threadIdx.x, xd + t * (2 * E / 32) + (E + EPT * threadIdx.x) / 32);
+}
+
+}  // namespace pf
+
+// ---- host ----------------------------------------------------------------------------------------
+
+int Engine::pf_alloc(int T) {
+    if (T <= pfb.cap) return 0;
+    try {
+        const size_t np = (size_t)T * KUSED;
+        pfb.x = alloc<float>((size_t)T * E);
+        pfb.x1 = alloc<float>((size_t)T * E);
+        pfb.xn = alloc<float>((size_t)T * E);
+        pfb.hin = alloc<float>((size_t)T * E);
+        pfb.xq = alloc<int8_t>((size_t)T * 2 * E);
+        pfb.xd = alloc<uint16_t>((size_t)T * (2 * E / 32));
+        pfb.proj = alloc<float>((size_t)T * DN_ROWS);
+        pfb.cy = alloc<float>((size_t)T * NCH);
+        pfb.gg = alloc<float>((size_t)T * NVH);
+        pfb.gb = alloc<float>((size_t)T * NVH);
+        pfb.o = alloc<float>((size_t)T * DIN);
+        pfb.oq = alloc<int8_t>((size_t)T * DIN);
+        pfb.od = alloc<uint16_t>((size_t)T * (DIN / 32));
+        pfb.qh = alloc<uint16_t>((size_t)T * NH * HD);
+        pfb.lg = alloc<float>((size_t)T * NEXP);
+        pfb.sg = alloc<float>((size_t)T);
+        pfb.ids = alloc<int32_t>(np);
+        pfb.wts = alloc<float>(np);
+        pfb.mo = alloc<int32_t>(pf::MO_WORDS);
+        pfb.ptok = alloc<int32_t>(np);
+        pfb.pair_of = alloc<int32_t>(np);
+        pfb.max_tiles = (int)(np / 64 + NEXP);
+        pfb.tiles = alloc<int4>((size_t)pfb.max_tiles);
+        pfb.gu = alloc<float>(np * 2 * FF);
+        pfb.hq = alloc<int8_t>(np * FF);
+        pfb.hd = alloc<uint16_t>(np * (FF / 32));
+        pfb.dout = alloc<float>(np * E);
+        pfb.sh = alloc<float>((size_t)T * E);
+        pfb.tok = alloc<uint32_t>((size_t)T);
+        pfb.cap = T;
+    } catch (...) {
+        set_err("out of device memory for the prefill buffers");
+        return -3;
+    }
+    return 0;
+}
+
+int Engine::pf_attn_lds(int kv_cap) {
+    const size_t lds = (size_t)kv_cap * 6;
+    if (lds > 160 * 1024 - 4096) {
+        set_err("prefill attention: context too long for the LDS-resident score row");
+        return -1;
+    }
+    if ((int)lds > pfb.attn_lds) {
+        if (hipFuncSetAttribute((const void *)pf::attn_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) !=
+            hipSuccess)
+            return -2;
+        pfb.attn_lds = (int)lds;
+    }
+    return 0;
+}
+
+// One chunk of T tokens at positions pos .. pos + T - 1 through every layer; h_out (optional, host)
+// receives every token's h_nextn; the last token's logits go to lane 0's logits, its h_nextn to
+// lane 0's hidden state.
+int Engine::pf_chunk(const uint32_t *toks, int T, float *h_out) {
+    using namespace pf;
+    const int p0 = pos, n_ctx = m.n_ctx;
+    const float eps = m.eps;
+    int kv_cap = (p0 + T + 255) / 256 * 256;
+    if (kv_cap > n_ctx) kv_cap = n_ctx;
+    int rc = pf_attn_lds(kv_cap);
+    if (rc) return rc;
+    if (hipMemcpyAsync(pfb.tok, toks, (size_t)T * 4, hipMemcpyHostToDevice, st) != hipSuccess) return -2;
+    const int64_t conv_slot = (int64_t)m.n_rec * NCH * (KC - 1), ssm_slot = (int64_t)m.n_rec * NVH * HV * HV;
+    const int np = T * KUSED;
+    auto gemm = [&](const Q8W &w, const int8_t *xq, const uint16_t *xd, int64_t k, float *y, int64_t ldy, const float *res,
+                    int64_t nt) {
+        GemmArgs g{};
+        g.wq = w.q; g.wd = w.d; g.xq = xq; g.xd = xd; g.y = y; g.res = res;
+        g.nr = w.rows; g.nt = nt; g.k = k; g.ldy = ldy; g.ldr = res ? E : 0;
+        return gemm_launch(g, 0, st);
+    };
+    auto grouped = [&](const Q8W &w, int64_t rows, int64_t k, const int8_t *xq, const uint16_t *xd, const int32_t *xrow,
+                       float *y) {
+        GemmArgs g{};
+        g.wq = w.q; g.wd = w.d; g.xq = xq; g.xd = xd; g.y = y;
+        g.nr = rows; g.nt = np; g.k = k; g.ldy = rows;
+        g.tiles = pfb.tiles; g.wq_stride = rows * k; g.wd_stride = rows * (k / 32); g.xrow = xrow;
+        g.tile_count = pfb.mo + MO_NT;
+        return gemm_launch(g, pfb.max_tiles, st);
+    };
+    for (int il = 0; il < d.n_layer; il++) {
+        const LayerW &w = L[il];
+        // input norm + Q8_0 (layer 0: the token embeddings, also the residual)
+        hipLaunchKernelGGL(norm_quant_kernel, dim3(T), dim3(PT), 0, st, m.tok_embd, il == 0 ? pfb.tok : nullptr, pfb.x,
+                           w.attn_norm, eps, pfb.xq, pfb.xd, (int64_t)E, nullptr);
+        if ((rc = gemm(w.proj, pfb.xq, pfb.xd, E, pfb.proj, DN_ROWS, nullptr, T))) return rc;
+        if (!w.att) {
+            float *cs = m.conv_state + (int64_t)cur * conv_slot + (int64_t)w.index * NCH * (KC - 1);
+            float *ss = m.ssm_state + (int64_t)cur * ssm_slot + (int64_t)w.index * NVH * HV * HV;
+            hipLaunchKernelGGL(conv_kernel, dim3(NCH / 256, T), dim3(256), 0, st, pfb.proj, T, w.conv, cs, pfb.cy);
+            hipLaunchKernelGGL(conv_state_kernel, dim3(NCH / 256), dim3(256), 0, st, pfb.proj, T, cs);
+            hipLaunchKernelGGL(dn_prep_kernel, dim3(T, 8), dim3(256), 0, st, pfb.cy, pfb.proj, w.dt_bias, w.ssm_a, eps,
+                               pfb.gg, pfb.gb);
+            hipLaunchKernelGGL(delta_kernel, dim3(NVH * 8), dim3(256), 0, st, pfb.cy, pfb.gg, pfb.gb, ss, pfb.o, T);
+            hipLaunchKernelGGL(gated_norm_kernel, dim3(T, NVH / 4), dim3(256), 0, st, pfb.o, pfb.proj, w.ssm_norm, eps,
+                               pfb.oq, pfb.od);
+        } else {
+            uint16_t *kcl = m.kcache + (int64_t)w.index * NKV * n_ctx * HD;
+            uint16_t *vtl = m.vcache + (int64_t)w.index * NKV * HD * n_ctx;
+            hipLaunchKernelGGL(attn_prep_kernel, dim3(T, 5), dim3(256), 0, st, pfb.proj, w.q_norm, w.k_norm, m.rope, p0,
+                               eps, pfb.qh, kcl, vtl, n_ctx, 0);
+            hipLaunchKernelGGL(attn_kernel, dim3(T, NH), dim3(256), (size_t)kv_cap * 6, st, pfb.qh, kcl, vtl, pfb.proj, p0,
+                               n_ctx, kv_cap, pfb.o);
+            if ((rc = quantize_q8_0(pfb.o, (int64_t)T * MIX_W, pfb.oq, pfb.od, st))) return rc;
+        }
+        // mixer output projection + residual
+        if ((rc = gemm(w.out, pfb.oq, pfb.od, MIX_W, pfb.x1, E, pfb.x, T))) return rc;
+        // post-attention norm: Q8_0 for the experts, f32 for the router
+        hipLaunchKernelGGL(norm_quant_kernel, dim3(T), dim3(PT), 0, st, m.tok_embd, nullptr, pfb.x1, w.post_norm, eps,
+                           pfb.xq, pfb.xd, (int64_t)E, pfb.xn);
+        hipLaunchKernelGGL(router_kernel, dim3((unsigned)(((int64_t)T * (NEXP + 1) + 15) / 16)), dim3(256), 0, st, pfb.xn,
+                           w.router, w.shexp_gate, T, pfb.lg, pfb.sg);
+        hipLaunchKernelGGL(route_kernel, dim3((T + 3) / 4), dim3(256), 0, st, pfb.lg, T, pfb.ids, pfb.wts,
+                           b.counters + CNT_ERR_TIE);
+        // shared expert over all tokens
+        if ((rc = gemm(w.shexp_gu, pfb.xq, pfb.xd, E, pfb.gu, 2 * FFSH, nullptr, T))) return rc;
+        hipLaunchKernelGGL(swiglu_quant_kernel, dim3(T), dim3(256), 0, st, pfb.gu, pfb.hq, pfb.hd);
+        if ((rc = gemm(w.shexp_down, pfb.hq, pfb.hd, FFSH, pfb.sh, E, nullptr, T))) return rc;
+        // routed experts: pairs grouped by expert, 64-pair tiles built on the device
+        if (hipMemsetAsync(pfb.mo, 0, NEXP * 4, st) != hipSuccess) return -2;
+        hipLaunchKernelGGL(moe_count_kernel, dim3((np + 255) / 256), dim3(256), 0, st, pfb.ids, np, pfb.mo);
+        hipLaunchKernelGGL(moe_tiles_kernel, dim3(1), dim3(NEXP), 0, st, pfb.mo, pfb.tiles);
+        hipLaunchKernelGGL(moe_scatter_kernel, dim3((np + 255) / 256), dim3(256), 0, st, pfb.ids, np, pfb.mo, pfb.ptok,
+                           pfb.pair_of);
+        if ((rc = grouped(w.exp_gu, 2 * FF, E, pfb.xq, pfb.xd, pfb.ptok, pfb.gu))) return rc;
+        hipLaunchKernelGGL(swiglu_quant_kernel, dim3(np), dim3(256), 0, st, pfb.gu, pfb.hq, pfb.hd);
+        if ((rc = grouped(w.exp_down, E, FF, pfb.hq, pfb.hd, nullptr, pfb.dout))) return rc;
+        hipLaunchKernelGGL(combine_kernel, dim3((unsigned)(((int64_t)T * E + 255) / 256)), dim3(256), 0, st, pfb.dout,
+                           pfb.pair_of, pfb.wts, pfb.sh, pfb.sg, pfb.x1, pfb.x, T);
+        if (hipGetLastError() != hipSuccess) return -2;
+    }
+    // h_nextn of every token (output norm of x2), the LM head of the last token
+    hipLaunchKernelGGL(norm_quant_kernel, dim3(T), dim3(PT), 0, st, m.tok_embd, nullptr, pfb.x, m.out_norm, eps, pfb.xq,
+                       pfb.xd, (int64_t)E, pfb.xn);
+    if ((rc = gemm(m.output, pfb.xq + (int64_t)(T - 1) * E, pfb.xd + (int64_t)(T - 1) * (E / 32), E, b.logits, d.n_vocab,
+                   nullptr, 1)))
+        return rc;
+    if (hipMemcpyAsync(b.hid, pfb.xn + (int64_t)(T - 1) * E, (size_t)E * 4, hipMemcpyDeviceToDevice, st) != hipSuccess)
+        return -2;
+    if (h_out && hipMemcpyAsync(h_out, pfb.xn, (size_t)T * E * 4, hipMemcpyDeviceToHost, st) != hipSuccess) return -2;
+    if (hipStreamSynchronize(st) != hipSuccess || hipGetLastError() != hipSuccess) return -2;
+    pos = p0 + T;
+    return 0;
+}
+
+int Engine::prefill(const uint32_t *toks, int n, uint32_t *next, float *h_all) {
+    if (n < 1 || pos + n > m.n_ctx || !toks_ok(toks, n)) return -1;
+    int rc = pf_alloc(std::min(n, PF_CHUNK));
+    if (rc) return rc;
+    pend_n = 0;
+    for (int c0 = 0; c0 < n; c0 += PF_CHUNK) {
+        const int c = std::min(PF_CHUNK, n - c0);
+        if ((rc = pf_chunk(toks + c0, c, h_all ? h_all + (size_t)c0 * E : nullptr))) return rc;
+    }
+    // greedy pick of the last token: the first strict maximum, NaN never wins, all -inf -> 0
+    // (engine.rs:1969-1987)
+    std::vector<float> lg(d.n_vocab);
+    if (hipMemcpy(lg.data(), b.logits, (size_t)d.n_vocab * 4, hipMemcpyDeviceToHost) != hipSuccess) return -2;
+    uint32_t best = 0;
+    float bv = -__builtin_inff();
+    for (int i = 0; i < d.n_vocab; i++)
+        if (lg[i] > bv) {
+            bv = lg[i];
+            best = (uint32_t)i;
+        }
+    if (next) *next = best;
+    return 0;
+}
+
+// MTP KV seeding of the pairs (toks[i], hs[i]) at positions pos0 + i, in batches (the decode's
+// mtp_seed for any number of pairs): entry eh_proj, then the MTP layer's K and V rows.
+int Engine::seed_batched(const uint32_t *toks, int n, int pos0, const float *hs) {
+    using namespace pf;
+    if (n < 1 || pos0 < 0 || pos0 + n > m.n_ctx || !toks_ok(toks, n) || !hs) return -1;
+    int rc = pf_alloc(std::min(n, PF_CHUNK));
+    if (rc) return rc;
+    const LayerW &w = L[d.n_layer];
+    uint16_t *kcl = m.kcache + (int64_t)w.index * NKV * m.n_ctx * HD;
+    uint16_t *vtl = m.vcache + (int64_t)w.index * NKV * HD * m.n_ctx;
+    for (int c0 = 0; c0 < n; c0 += PF_CHUNK) {
+        const int T = std::min(PF_CHUNK, n - c0);
+        if (hipMemcpyAsync(pfb.tok, toks + c0, (size_t)T * 4, hipMemcpyHostToDevice, st) != hipSuccess) return -2;
+        if (hipMemcpyAsync(pfb.hin, hs + (size_t)c0 * E, (size_t)T * E * 4, hipMemcpyHostToDevice, st) != hipSuccess)
+            return -2;
+        hipLaunchKernelGGL(entry_in_kernel, dim3(T), dim3(PT), 0, st, m.tok_embd, pfb.tok, pfb.hin, pfb.x, w.enorm, w.hnorm,
+                           m.eps, pfb.xq, pfb.xd);
+        GemmArgs g{};
+        g.wq = w.eh_proj.q; g.wd = w.eh_proj.d; g.xq = pfb.xq; g.xd = pfb.xd; g.y = pfb.x1;
+        g.nr = E; g.nt = T; g.k = 2 * E; g.ldy = E;
+        if ((rc = gemm_launch(g, 0, st))) return rc;
+        hipLaunchKernelGGL(norm_quant_kernel, dim3(T), dim3(PT), 0, st, m.tok_embd, nullptr, pfb.x1, w.attn_norm, m.eps,
+                           pfb.xq, pfb.xd, (int64_t)E, nullptr);
+        GemmArgs k{};
+        k.wq = w.proj.q + (int64_t)AT_K * E; k.wd = w.proj.d + (int64_t)AT_K * (E / 32);
+        k.xq = pfb.xq; k.xd = pfb.xd; k.y = pfb.proj + AT_K;
+        k.nr = AT_ROWS - AT_K; k.nt = T; k.k = E; k.ldy = DN_ROWS;
+        if ((rc = gemm_launch(k, 0, st))) return rc;
+        hipLaunchKernelGGL(attn_prep_kernel, dim3(T, 5), dim3(256), 0, st, pfb.proj, w.q_norm, w.k_norm, m.rope,
+                           pos0 + c0, m.eps, pfb.qh, kcl, vtl, m.n_ctx, 1);
+    }
+    if (hipStreamSynchronize(st) != hipSuccess || hipGetLastError() != hipSuccess) return -2;
+    return 0;
+}
+
+}  // namespace oxe

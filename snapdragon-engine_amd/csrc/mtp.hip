@@ -128,15 +128,21 @@ __global__ void mtp_commit_kernel(MtpState *ms, const unsigned long long *keys, 
 void MtpDriverHost::note(Engine &e, int p0, const uint32_t *toks, int n) {
     std::vector<float> h((size_t)n * E);
     for (int i = 0; i < n; i++) e.hidden_host(i, h.data() + (size_t)i * E);
+    note_h(p0, toks, n, h.data());
+}
+
+// MtpDriver::note_with (mtp.rs:415-432): the pairs (toks[i], h_nextn before toks[i]) of positions
+// not yet in the MTP KV join the catch-up; hl becomes the h_nextn of the last token
+void MtpDriverHost::note_h(int p0, const uint32_t *toks, int n, const float *h) {
     for (int i = 0; i < n; i++) {
         const int p = p0 + i;
         if (p >= q) {
             cu_tok.push_back(toks[i]);
             if (i == 0) cu_h.insert(cu_h.end(), hl.begin(), hl.end());
-            else cu_h.insert(cu_h.end(), h.begin() + (size_t)(i - 1) * E, h.begin() + (size_t)i * E);
+            else cu_h.insert(cu_h.end(), h + (size_t)(i - 1) * E, h + (size_t)i * E);
         }
     }
-    hl.assign(h.begin() + (size_t)(n - 1) * E, h.begin() + (size_t)n * E);
+    hl.assign(h + (size_t)(n - 1) * E, h + (size_t)n * E);
 }
 
 void MtpDriverHost::remember(Engine &e, int p0, int n) {
@@ -171,7 +177,43 @@ int MtpDriverHost::prefill(Engine &e, const uint32_t *toks, int n, uint32_t *nex
         note(e, p0, toks + c0, c);
         if ((rc = flush(e, 7))) return rc;  // the reference keeps up to mtp_lanes - 1 = 7 pairs pending
     }
+    last_n = 0;
     if (next) *next = nx;
+    return 0;
+}
+
+// MtpDriver::prefill_batched (mtp.rs:468-500): the batched prefill with every position's h_nextn,
+// then the catch-up pairs seeded into the MTP KV in one batched pass (the same K / V rows as
+// 2-lane seeding runs: every pair's rows depend on that pair only). One token: step_plain.
+int MtpDriverHost::prefill_batched(Engine &e, const uint32_t *toks, int n, uint32_t *next) {
+    if (n == 1) {
+        uint32_t g;
+        const int rc = step_plain(e, toks[0], &g);
+        if (rc) return rc;
+        last_n = 0;
+        if (next) *next = g;
+        return 0;
+    }
+    std::vector<float> h;
+    uint32_t g = 0;
+    for (int c0 = 0; c0 < n; c0 += PF_CHUNK) {
+        const int c = std::min(PF_CHUNK, n - c0);
+        const int p0 = e.pos;
+        h.resize((size_t)c * E);
+        int rc = e.prefill(toks + c0, c, &g, h.data());
+        if (rc) return rc;
+        note_h(p0, toks + c0, c, h.data());
+        const size_t keep = 7;
+        if (cu_tok.size() > keep) {
+            const int ns = (int)(cu_tok.size() - keep);
+            if ((rc = e.seed_batched(cu_tok.data(), ns, q, cu_h.data()))) return rc;
+            cu_tok.erase(cu_tok.begin(), cu_tok.begin() + ns);
+            cu_h.erase(cu_h.begin(), cu_h.begin() + (size_t)ns * E);
+            q += ns;
+        }
+    }
+    last_n = 0;
+    if (next) *next = g;
     return 0;
 }
 
@@ -343,6 +385,18 @@ int oxe_mtp_prefill(oxe_engine *e, const uint32_t *toks, int n, uint32_t *next) 
     Engine *g = (Engine *)e;
     if (n < 1 || !g->toks_ok(toks, n) || g->pos + n > g->m.n_ctx) return -1;
     return g->drv.prefill(*g, toks, n, next);
+}
+
+int oxe_mtp_prefill_batched(oxe_engine *e, const uint32_t *toks, int n, uint32_t *next) {
+    Engine *g = (Engine *)e;
+    if (n < 1 || !g->toks_ok(toks, n) || g->pos + n > g->m.n_ctx) return -1;
+    return g->drv.prefill_batched(*g, toks, n, next);
+}
+
+int oxe_engine_prefill(oxe_engine *e, const uint32_t *toks, int n, uint32_t *next, float *hidden) {
+    Engine *g = (Engine *)e;
+    if (n < 1 || !g->toks_ok(toks, n) || g->pos + n > g->m.n_ctx) return -1;
+    return g->prefill(toks, n, next, hidden);
 }
 
 int oxe_mtp_step(oxe_engine *e, uint32_t x, uint32_t *out, int *n_out, int64_t override_d1) {

@@ -156,6 +156,29 @@ OXE_DEV void quant_block_q8_0(const float *x, int8_t *q, uint16_t *d) {
     *(uint4 *)(q + 16) = make_uint4(packed[4], packed[5], packed[6], packed[7]);
 }
 
+// max over the 32-lane half of the wave holding this lane (exact, any order)
+OXE_DEV float half_max(float v) {
+    v = fmaxf(v, dpp_f<DPP_ROR8>(v));
+    v = fmaxf(v, dpp_f<DPP_ROR4>(v));
+    v = fmaxf(v, dpp_f<DPP_ROR2>(v));
+    v = fmaxf(v, dpp_f<DPP_ROR1>(v));
+    const float lo = fmaxf(readlane_f(v, 0), readlane_f(v, 16)), hi = fmaxf(readlane_f(v, 32), readlane_f(v, 48));
+    return (threadIdx.x & 63) < 32 ? lo : hi;
+}
+// quantize_row_q8_0 (NEON) of the 32-value block held one value per lane by each half of the
+// wave: *d = the block scale; returns in lane 4 i the codes of lanes 4 i .. 4 i + 3 (byte order)
+OXE_DEV uint32_t quant32_lanes(float v, float *d) {
+    const float m = half_max(__builtin_fabsf(v));
+    const float dd = m / 127.0f;
+    const float id = dd != 0.0f ? 1.0f / dd : 0.0f;
+    const int32_t q = (int32_t)__builtin_rintf(v * id);
+    int p = (int)((uint32_t)(q & 0xff) << (8 * (threadIdx.x & 3)));
+    p |= dpp_i<DPP_XOR1>(p);
+    p |= dpp_i<DPP_XOR2>(p);
+    *d = dd;
+    return (uint32_t)p;
+}
+
 // ---- block reductions (blockDim.x threads, all participating)
 
 template <int NT>

@@ -37,15 +37,29 @@ struct MtpDriverHost {
     int last_p0 = 0, last_n = 0;   // the last host-driven step's committed span (MtpDriver.last)
     std::vector<float> last_h;     // h_nextn of each committed lane of that step (MtpDriver.last_h)
     void note(Engine &e, int p0, const uint32_t *toks, int n);
+    void note_h(int p0, const uint32_t *toks, int n, const float *h);
     void remember(Engine &e, int p0, int n);
     int flush(Engine &e, size_t keep);
     int prefill(Engine &e, const uint32_t *toks, int n, uint32_t *next);
+    int prefill_batched(Engine &e, const uint32_t *toks, int n, uint32_t *next);
     int step(Engine &e, uint32_t x, uint32_t *out, int *n_out, int64_t override_d1);
     int step_plain(Engine &e, uint32_t x, uint32_t *out);
     int rewind(Engine &e, int m);
     int dev_begin(Engine &e, uint32_t x);
     int dev_end(Engine &e, uint32_t *out_tok, int cap, int *n_out, uint32_t *next_x);
 };
+
+// Buffers of the batched prefill, [T][...] for up to cap tokens (allocated on first use)
+struct PfBufs {
+    int cap = 0, max_tiles = 0, attn_lds = 0;
+    float *x, *x1, *xn, *hin, *proj, *cy, *gg, *gb, *o, *lg, *sg, *wts, *gu, *dout, *sh;
+    int8_t *xq, *oq, *hq;
+    uint16_t *xd, *od, *qh, *hd;
+    int32_t *ids, *mo, *ptok, *pair_of;
+    int4 *tiles;
+    uint32_t *tok;
+};
+constexpr int PF_CHUNK = 2048;   // tokens per batched pass
 
 inline thread_local std::string g_last_error;
 inline void set_err(const std::string &s) { g_last_error = s; }
@@ -87,6 +101,13 @@ struct Engine {
     FusedArgs fz_host[3];
     const unsigned long long *keys() const { return fused ? fz_keys : b.amax_key; }
     int nkeys() const { return fused ? fz_grid : 1; }
+    // batched prefill (k_prefill.hip)
+    PfBufs pfb{};
+    int pf_alloc(int T);
+    int pf_attn_lds(int kv_cap);
+    int pf_chunk(const uint32_t *toks, int T, float *h_out);
+    int prefill(const uint32_t *toks, int n, uint32_t *next, float *h_all);
+    int seed_batched(const uint32_t *toks, int n, int pos0, const float *hs);
     // kernel probe: HIP events around every launch of one kernel kind while enqueuing eagerly
     int probe_kind = -1;
     std::vector<hipEvent_t> probe_ev;

@@ -167,6 +167,8 @@ def _engine_sigs(L):
         "oxe_engine_set_pos": (i32, [vp, i32]),
         "oxe_engine_device_bytes": (i64, [vp]),
         "oxe_mtp_prefill": (i32, [vp, u32p, i32, u32p]),
+        "oxe_mtp_prefill_batched": (i32, [vp, u32p, i32, u32p]),
+        "oxe_engine_prefill": (i32, [vp, u32p, i32, u32p, f32p]),
         "oxe_mtp_step": (i32, [vp, C.c_uint32, u32p, C.POINTER(C.c_int), i64]),
         "oxe_mtp_step_plain": (i32, [vp, C.c_uint32, u32p]),
         "oxe_engine_set_fused": (i32, [vp, i32]),
@@ -287,7 +289,27 @@ class Engine:
     def set_pos(self, pos):
         check(lib().oxe_engine_set_pos(self.h, pos), "set_pos")
 
+    def prefill(self, toks, hidden=False):
+        """Batched prefill (Engine::prefill_ext, prefill.rs:763): argmax after the last token, and
+        with hidden=True also every position's h_nextn [n][n_embd]."""
+        import numpy as np
+        t = np.ascontiguousarray(toks, np.uint32)
+        nx = np.zeros(1, np.uint32)
+        h = np.empty((len(t), self.desc.n_embd), np.float32) if hidden else None
+        hp = _np_ptr(h, C.c_float) if hidden else None
+        check(lib().oxe_engine_prefill(self.h, _np_ptr(t, C.c_uint32), len(t), _np_ptr(nx, C.c_uint32), hp), "prefill")
+        return (int(nx[0]), h) if hidden else int(nx[0])
+
     # ---- MTP depth-1 driver (mtp.rs MtpDriver) ----
+    def mtp_prefill_batched(self, toks):
+        """MtpDriver::prefill_batched (mtp.rs:468-500)."""
+        import numpy as np
+        t = np.ascontiguousarray(toks, np.uint32)
+        nx = np.zeros(1, np.uint32)
+        check(lib().oxe_mtp_prefill_batched(self.h, _np_ptr(t, C.c_uint32), len(t), _np_ptr(nx, C.c_uint32)),
+              "mtp_prefill_batched")
+        return int(nx[0])
+
     def mtp_prefill(self, toks):
         import numpy as np
         t = np.ascontiguousarray(toks, np.uint32)
