@@ -26,6 +26,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "snapdragon-engine_amd"))
 
 PEAK_HBM_GBS = 8000.0
+PEAK_INT8_TOPS = 5000.0   # dense int8 matrix-core peak (5.0 POP/s)
 
 # ---- algorithmic bytes of the 35B-A3B all-Q8_0 shape (SURVEY 8(d) definition) ----
 Q8 = 34 / 32                                    # bytes per Q8_0 weight (32 codes + fp16 scale)
@@ -95,6 +96,102 @@ def cpu_baseline(seconds, prompt_len=8):
                       f"{wall:.1f} s wall minus {gen:.1f} s spent generating synthetic expert weights on first use"}
 
 
+def prefill_macs(T, n_dn=30, n_att=10):
+    """Multiply-accumulates of the batched prefill's matrix-core GEMMs over T tokens (projections,
+    mixer output, shared expert, the 8 routed experts of every token, the LM head of the last token)."""
+    shared = 3 * 512 * E
+    pair = 3 * 512 * E                          # one routed expert: gate + up + down
+    per_tok = (n_dn * (12352 * E + E * 4096 + shared + 8 * pair)
+               + n_att * (9216 * E + E * 4096 + shared + 8 * pair))
+    return T * per_tok + V * E
+
+
+def prefill_expert_macs(T, n_layer=40):
+    return T * n_layer * 8 * 3 * 512 * E
+
+
+def cpu_prefill_baseline(seconds):
+    """The oracle's prompt path (2-token verify runs, MtpDriver::prefill) on the 35B-A3B shape,
+    timed on this host for a bounded number of tokens."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+    O.build()
+    d = O.desc_35b_a3b()
+    e = O.Engine(d, seed=0, n_ctx=1024)
+    O.lib().oxo_set_keep_logits(e.h, 0)
+    toks = O.bench_prompt(512)
+    gen0 = O.lib().oxo_gen_seconds(e.h)
+    t0 = time.time()
+    n = 0
+    while (time.time() - t0 < seconds or n < 4) and n + 2 <= len(toks):
+        e.verify(toks[n:n + 2])
+        e.commit(2)
+        n += 2
+    wall = time.time() - t0
+    gen = O.lib().oxo_gen_seconds(e.h) - gen0
+    compute = max(wall - gen, 1e-9)
+    cores = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    e.close()
+    return {"value": round(n / compute, 4), "unit": "tok/s", "cores": cores, "kind": "port",
+            "sample": f"{n} prompt tokens of the 35B-A3B shape as 2-token verify runs (the reference's "
+                      f"MtpDriver::prefill path); {wall:.1f} s wall minus {gen:.1f} s generating synthetic expert "
+                      f"weights on first use"}
+
+
+def bench_prefill(args):
+    """batched prefill of a 2048-token prompt on the config-4 model."""
+    import oxe_amd as A
+    d = A.desc_35b_a3b()
+    T = args.prefill_tokens
+    eng = A.Engine(d, seed=0, n_ctx=T + 256)
+    prompt = A.bench_prompt(T)
+    for _ in range(max(args.warmup, 1)):
+        eng.set_pos(0)
+        eng.prefill(prompt)
+    times = []
+    for _ in range(args.steps):
+        eng.set_pos(0)
+        t0 = time.perf_counter()
+        eng.prefill(prompt)
+        times.append(time.perf_counter() - t0)
+    ms = 1e3 * sum(times) / len(times)
+    kinds = {}
+    for kind, name in ((12, "gemm_all"), (13, "gemm_experts"), (14, "attention"), (15, "delta_rule")):
+        eng.set_pos(0)
+        us, n = eng.prefill_probe(prompt, kind)
+        kinds[name] = {"total_us": round(us, 1), "launches": n}
+    macs = prefill_macs(T)
+    g_us = kinds["gemm_all"]["total_us"]
+    tops = 2 * macs / (g_us * 1e-6) / 1e12 if g_us > 0 else 0.0
+    e_us = kinds["gemm_experts"]["total_us"]
+    e_tops = 2 * prefill_expert_macs(T) / (e_us * 1e-6) / 1e12 if e_us > 0 else 0.0
+    result = {
+        "metric": "batched prefill tok/s (35B-A3B shape, int8, 2048-token prompt)",
+        "value": round(T / (ms / 1e3), 1),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": max(args.warmup, 1),
+        "ms_per_step": round(ms, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8 (Q8_0 weights and activations, int32 block dots on the matrix cores, fp32 chains; fp16 KV)",
+        "data": "synthetic: seeded random Q8_0 weights (include/oxe_model.h), reference bench prompt ids",
+        "config": {"workload": "BASELINE config 5: batched prefill of a 2048-token prompt, config-4 model "
+                               "(40 layers, vocab 151936, all Q8_0)", "prompt_tokens": T,
+                   "parallelism": "single GPU"},
+        "roofline": {"bound": "mfma", "achieved": round(tops, 2), "peak": PEAK_INT8_TOPS, "unit": "TOP/s",
+                     "frac": round(tops / PEAK_INT8_TOPS, 4), "traffic": None,
+                     "kernel": "gemm_q8_kernel (every matrix-core GEMM of the prefill, summed)",
+                     "total_us": g_us, "launches_timed": kinds["gemm_all"]["launches"], "int_ops": int(2 * macs)},
+        "experts_TOPs": round(e_tops, 2),
+        "breakdown_us": kinds,
+    }
+    result["cpu_baseline"] = None if args.no_cpu else cpu_prefill_baseline(args.cpu_seconds)
+    print(json.dumps(result), flush=True)
+
+
 def calibrate_copy(torch, mib=1024, reps=4):
     """A plain copy of `mib` MiB, `reps` times: under rocprofv3 --pmc its FETCH_SIZE / WRITE_SIZE
     per dispatch calibrate the byte counters (bytes moved are known exactly)."""
@@ -133,6 +230,10 @@ def main():
     ap.add_argument("--pmc-probe", action="store_true",
                     help="only prefill and run the timed kernel's eager probe launches (for rocprofv3 --pmc), "
                          "printing their algorithmic bytes")
+    ap.add_argument("--prefill", action="store_true",
+                    help="BASELINE config 5 instead: batched prefill of --prefill-tokens prompt tokens "
+                         "(--steps timed prefills after --warmup untimed ones)")
+    ap.add_argument("--prefill-tokens", type=int, default=2048)
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build runs the whole MTP-1 step on a single MI355X "
@@ -141,6 +242,13 @@ def main():
     import torch
     if args.calibrate_copy:
         calibrate_copy(torch)
+        return
+    if args.prefill:
+        if args.steps == ap.get_default("steps"):
+            args.steps = 5
+        if args.warmup == ap.get_default("warmup"):
+            args.warmup = 1
+        bench_prefill(args)
         return
     import oxe_amd as A
 
@@ -153,7 +261,7 @@ def main():
     fused = eng.fused
     probe_kind = args.probe_kind if args.probe_kind >= 0 else (10 if fused else 1)
     prompt = A.bench_prompt(args.prompt)
-    x = eng.mtp_prefill(prompt)
+    x = eng.mtp_prefill_batched(prompt)
     eng.sync()
     setup_s = time.time() - t_setup
     cap = 2 * (args.steps + args.warmup) + 16

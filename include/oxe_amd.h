@@ -113,6 +113,12 @@ OXE_API int64_t oxe_engine_read_trace(oxe_engine *e, unsigned long long *host, i
  * hidden (optional host [n][n_embd]): every position's h_nextn. Replaces Engine::prefill_ext
  * (crates/model/src/engine/prefill.rs:763). */
 OXE_API int oxe_engine_prefill(oxe_engine *e, const uint32_t *toks, int n, uint32_t *next, float *hidden);
+/* oxe_engine_prefill with HIP events around every launch of one kernel kind (12 every matrix-core
+ * GEMM, 13 the grouped expert GEMMs, 14 attention, 15 the delta rule): *total_us = their summed
+ * duration, *n_launch = launches timed (diagnostic for the prefill roofline; no counterpart in the
+ * reference). */
+OXE_API int oxe_engine_prefill_probe(oxe_engine *e, const uint32_t *toks, int n, int kind, float *total_us,
+                                     int *n_launch);
 
 /* ---- MTP depth-1 speculative decoding (crates/model/src/mtp.rs MtpDriver, depth 1) --------- */
 

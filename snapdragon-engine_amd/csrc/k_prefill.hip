@@ -587,7 +587,10 @@ int Engine::pf_chunk(const uint32_t *toks, int T, float *h_out) {
         GemmArgs g{};
         g.wq = w.q; g.wd = w.d; g.xq = xq; g.xd = xd; g.y = y; g.res = res;
         g.nr = w.rows; g.nt = nt; g.k = k; g.ldy = ldy; g.ldr = res ? E : 0;
-        return gemm_launch(g, 0, st);
+        probe(K_PF_GEMM);
+        const int r = gemm_launch(g, 0, st);
+        probe(K_PF_GEMM);
+        return r;
     };
     auto grouped = [&](const Q8W &w, int64_t rows, int64_t k, const int8_t *xq, const uint16_t *xd, const int32_t *xrow,
                        float *y) {
@@ -596,7 +599,10 @@ int Engine::pf_chunk(const uint32_t *toks, int T, float *h_out) {
         g.nr = rows; g.nt = np; g.k = k; g.ldy = rows;
         g.tiles = pfb.tiles; g.wq_stride = rows * k; g.wd_stride = rows * (k / 32); g.xrow = xrow;
         g.tile_count = pfb.mo + MO_NT;
-        return gemm_launch(g, pfb.max_tiles, st);
+        probe(K_PF_GEMM); probe(K_PF_EXPERT);
+        const int r = gemm_launch(g, pfb.max_tiles, st);
+        probe(K_PF_EXPERT); probe(K_PF_GEMM);
+        return r;
     };
     for (int il = 0; il < d.n_layer; il++) {
         const LayerW &w = L[il];
@@ -611,7 +617,9 @@ int Engine::pf_chunk(const uint32_t *toks, int T, float *h_out) {
             hipLaunchKernelGGL(conv_state_kernel, dim3(NCH / 256), dim3(256), 0, st, pfb.proj, T, cs);
             hipLaunchKernelGGL(dn_prep_kernel, dim3(T, 8), dim3(256), 0, st, pfb.cy, pfb.proj, w.dt_bias, w.ssm_a, eps,
                                pfb.gg, pfb.gb);
+            probe(K_PF_DELTA);
             hipLaunchKernelGGL(delta_kernel, dim3(NVH * 8), dim3(256), 0, st, pfb.cy, pfb.gg, pfb.gb, ss, pfb.o, T);
+            probe(K_PF_DELTA);
             hipLaunchKernelGGL(gated_norm_kernel, dim3(T, NVH / 4), dim3(256), 0, st, pfb.o, pfb.proj, w.ssm_norm, eps,
                                pfb.oq, pfb.od);
         } else {
@@ -619,8 +627,10 @@ int Engine::pf_chunk(const uint32_t *toks, int T, float *h_out) {
             uint16_t *vtl = m.vcache + (int64_t)w.index * NKV * HD * n_ctx;
             hipLaunchKernelGGL(attn_prep_kernel, dim3(T, 5), dim3(256), 0, st, pfb.proj, w.q_norm, w.k_norm, m.rope, p0,
                                eps, pfb.qh, kcl, vtl, n_ctx, 0);
+            probe(K_PF_ATTN);
             hipLaunchKernelGGL(attn_kernel, dim3(T, NH), dim3(256), (size_t)kv_cap * 6, st, pfb.qh, kcl, vtl, pfb.proj, p0,
                                n_ctx, kv_cap, pfb.o);
+            probe(K_PF_ATTN);
             if ((rc = quantize_q8_0(pfb.o, (int64_t)T * MIX_W, pfb.oq, pfb.od, st))) return rc;
         }
         // mixer output projection + residual
@@ -723,3 +733,34 @@ int Engine::seed_batched(const uint32_t *toks, int n, int pos0, const float *hs)
 }
 
 }  // namespace oxe
+
+extern "C" {
+
+// A batched prefill with HIP events around every launch of one kernel kind (12 every matrix-core
+// GEMM, 13 the grouped expert GEMMs, 14 attention, 15 the delta rule): *total_us = their summed
+// duration, *n = launches timed. Diagnostic for the prefill roofline (no counterpart in the
+// reference).
+int oxe_engine_prefill_probe(oxe_engine *e, const uint32_t *toks, int n, int kind, float *total_us, int *n_launch) {
+    oxe::Engine *g = (oxe::Engine *)e;
+    if (n < 1 || !g->toks_ok(toks, n) || g->pos + n > g->m.n_ctx || kind < 12 || kind > 15 || !total_us || !n_launch)
+        return -1;
+    g->probe_kind = kind;
+    g->probe_used = 0;
+    uint32_t next;
+    const int rc = g->prefill(toks, n, &next, nullptr);
+    g->probe_kind = -1;
+    if (rc) return rc;
+    double tot = 0.0;
+    int cnt = 0;
+    for (size_t i = 0; i + 1 < g->probe_used; i += 2) {
+        float ms = 0.0f;
+        if (hipEventElapsedTime(&ms, g->probe_ev[i], g->probe_ev[i + 1]) != hipSuccess) return -2;
+        tot += ms;
+        cnt++;
+    }
+    *total_us = (float)(tot * 1000.0);
+    *n_launch = cnt;
+    return 0;
+}
+
+}  // extern "C"

@@ -472,7 +472,9 @@ struct Engine {
 
     // ---- run sequences (device-side lanes/positions from RunCtl) ----
     enum { K_HEAD = 0, K_EXPERTS = 1, K_DOWN = 2, K_PROJ = 3, K_OUT = 4, K_DN = 5, K_ROUTER = 6, K_SCORES = 7, K_PV = 8, K_ENTRY = 9,
-           K_FUSED = 10, K_FUSED_DRAFT = 11 };
+           K_FUSED = 10, K_FUSED_DRAFT = 11,
+           // batched prefill: every matrix-core GEMM, the grouped expert GEMMs, attention, delta rule
+           K_PF_GEMM = 12, K_PF_EXPERT = 13, K_PF_ATTN = 14, K_PF_DELTA = 15 };
     void enqueue_layer(int l, bool first) {
         const LayerW &w = L[l];
         const float *x = first ? b.x : b.x2;

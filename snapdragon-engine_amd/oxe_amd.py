@@ -169,6 +169,7 @@ def _engine_sigs(L):
         "oxe_mtp_prefill": (i32, [vp, u32p, i32, u32p]),
         "oxe_mtp_prefill_batched": (i32, [vp, u32p, i32, u32p]),
         "oxe_engine_prefill": (i32, [vp, u32p, i32, u32p, f32p]),
+        "oxe_engine_prefill_probe": (i32, [vp, u32p, i32, i32, C.POINTER(C.c_float), C.POINTER(C.c_int)]),
         "oxe_mtp_step": (i32, [vp, C.c_uint32, u32p, C.POINTER(C.c_int), i64]),
         "oxe_mtp_step_plain": (i32, [vp, C.c_uint32, u32p]),
         "oxe_engine_set_fused": (i32, [vp, i32]),
@@ -299,6 +300,16 @@ class Engine:
         hp = _np_ptr(h, C.c_float) if hidden else None
         check(lib().oxe_engine_prefill(self.h, _np_ptr(t, C.c_uint32), len(t), _np_ptr(nx, C.c_uint32), hp), "prefill")
         return (int(nx[0]), h) if hidden else int(nx[0])
+
+    def prefill_probe(self, toks, kind):
+        """A prefill with HIP events around every launch of one kernel kind (12 every GEMM, 13 grouped
+        expert GEMMs, 14 attention, 15 delta rule): (summed microseconds, launches)."""
+        import numpy as np
+        t = np.ascontiguousarray(toks, np.uint32)
+        us, n = C.c_float(0), C.c_int(0)
+        check(lib().oxe_engine_prefill_probe(self.h, _np_ptr(t, C.c_uint32), len(t), kind, C.byref(us), C.byref(n)),
+              "prefill_probe")
+        return float(us.value), int(n.value)
 
     # ---- MTP depth-1 driver (mtp.rs MtpDriver) ----
     def mtp_prefill_batched(self, toks):
