@@ -117,12 +117,17 @@ __global__ __launch_bounds__(256) void dn_prep_kernel(float *cy, const float *pr
 // delta rule (oxe_gated_delta_net_step_f32_x4_from, oxe_ops.cpp:268-345) over the T tokens in order.
 // Workgroup = (value head vh = b / 8, state rows 16 (b % 8) ..); thread (row rg = t / 16, chain
 // c = t % 16) holds row elements c + 16 s in registers: chain c of ggml_vec_dot_f32, whose NEON
-// reduction tree is the DPP sequence of dot16_tree_dpp. Per token the inputs come from LDS, staged
-// DT_T tokens at a time. o[t][vh * 128 + row] = (S_row . q) / sqrt(128).
+// reduction tree is the DPP sequence of dot16_tree_dpp. The token inputs (q, k, the 16 v rows,
+// gates) are staged through LDS DT_T tokens at a time, double-buffered: the next stage's global
+// loads are in flight while the current stage runs, and each token's q / k values are read from
+// LDS one token ahead. o[t][vh * 128 + row] = (S_row . q) / sqrt(128).
 constexpr int DT_T = 32;
 __global__ __launch_bounds__(256) void delta_kernel(const float *cy, const float *gg, const float *gb, float *ssm, float *o,
                                                     int T) {
-    __shared__ float s_k[DT_T][DS], s_q[DT_T][DS], s_v[DT_T][16], s_g[DT_T], s_b[DT_T];
+    // q and k of a token, transposed per chain: [q|k][c][s] = element c + 16 s (a lane's 8 values are
+    // two 16-byte reads)
+    __shared__ __align__(16) float s_qk[2][DT_T][2][16][8];
+    __shared__ float s_v[2][DT_T][16], s_g[2][DT_T], s_b[2][DT_T], s_out[2][DT_T][16];
     const int vh = blockIdx.x >> 3, row0 = (blockIdx.x & 7) * 16, kh = vh % NKH;
     const int t = threadIdx.x, rg = t >> 4, cc = t & 15;
     float *srow = ssm + ((int64_t)vh * HV + row0 + rg) * HV;
@@ -130,43 +135,92 @@ __global__ __launch_bounds__(256) void delta_kernel(const float *cy, const float
 #pragma unroll
     for (int s = 0; s < 8; s++) r[s] = srow[cc + 16 * s];
     const float scale = 1.0f / sqrtf((float)HV);
-    for (int t0 = 0; t0 < T; t0 += DT_T) {
+    // this thread's share of a stage: element t of every token's [q | k], and two v values
+    const int64_t qk_off = t < DS ? kh * DS + t : NKH * DS + kh * DS + (t - DS);
+    const int vt0 = t >> 4, ve = t & 15;   // v: tokens vt0 and vt0 + 16, row row0 + ve
+    const int64_t v_off = 2 * NKH * DS + vh * HV + row0 + ve;
+    float pf[DT_T], pv[2], pg = 0.0f, pb = 0.0f;
+    auto fetch = [&](int t0) {
         const int nt = T - t0 < DT_T ? T - t0 : DT_T;
-        __syncthreads();
-        for (int i = t; i < nt * DS; i += 256) {
-            const int tt = i / DS, e = i % DS;
-            const float *row = cy + (int64_t)(t0 + tt) * NCH;
-            s_q[tt][e] = row[kh * DS + e];
-            s_k[tt][e] = row[NKH * DS + kh * DS + e];
-        }
-        for (int i = t; i < nt * 16; i += 256) {
-            const int tt = i / 16, e = i % 16;
-            s_v[tt][e] = cy[(int64_t)(t0 + tt) * NCH + 2 * NKH * DS + vh * HV + row0 + e];
-        }
+#pragma unroll
+        for (int j = 0; j < DT_T; j++) pf[j] = j < nt ? cy[(int64_t)(t0 + j) * NCH + qk_off] : 0.0f;
+#pragma unroll
+        for (int j = 0; j < 2; j++) pv[j] = vt0 + 16 * j < nt ? cy[(int64_t)(t0 + vt0 + 16 * j) * NCH + v_off] : 0.0f;
         if (t < nt) {
-            s_g[t] = gg[(int64_t)(t0 + t) * NVH + vh];
-            s_b[t] = gb[(int64_t)(t0 + t) * NVH + vh];
+            pg = gg[(int64_t)(t0 + t) * NVH + vh];
+            pb = gb[(int64_t)(t0 + t) * NVH + vh];
         }
-        __syncthreads();
-        for (int tt = 0; tt < nt; tt++) {
-            const float eg = s_g[tt], beta = s_b[tt];
+    };
+    auto put = [&](int buf) {
+#pragma unroll
+        for (int j = 0; j < DT_T; j++) s_qk[buf][j][t >> 7][t & 15][(t >> 4) & 7] = pf[j];
+#pragma unroll
+        for (int j = 0; j < 2; j++) s_v[buf][vt0 + 16 * j][ve] = pv[j];
+        if (t < DT_T) {
+            s_g[buf][t] = pg;
+            s_b[buf][t] = pb;
+        }
+    };
+    fetch(0);
+    put(0);
+    __syncthreads();
+    int buf = 0;
+    for (int t0 = 0; t0 < T; t0 += DT_T, buf ^= 1) {
+        const int nt = T - t0 < DT_T ? T - t0 : DT_T;
+        const bool more = t0 + DT_T < T;
+        if (more) fetch(t0 + DT_T);
+        auto ld8 = [&](const float *p, float v[8]) {
+            const float4 a = *(const float4 *)p, b = *(const float4 *)(p + 4);
+            v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+        };
+        // g, beta, v of a token, read with its q / k one token ahead
+        auto gbv = [&](int tt, float &eg, float &beta, float &vv) {
+            eg = s_g[buf][tt];
+            beta = s_b[buf][tt];
+            vv = s_v[buf][tt][rg];
+        };
+        auto step = [&](int tt, const float kc[8], const float qc[8], float eg, float beta, float vv) {
             float acc = 0.0f;
 #pragma unroll
             for (int s = 0; s < 8; s++) {
                 r[s] = r[s] * eg;
-                acc = __builtin_fmaf(r[s], s_k[tt][cc + 16 * s], acc);
+                acc = __builtin_fmaf(r[s], kc[s], acc);
             }
             const float sk = dot16_tree_dpp(acc);
-            const float delta = (s_v[tt][rg] - sk) * beta;
+            const float delta = (vv - sk) * beta;
             acc = 0.0f;
 #pragma unroll
             for (int s = 0; s < 8; s++) {
-                r[s] = __builtin_fmaf(s_k[tt][cc + 16 * s], delta, r[s]);
-                acc = __builtin_fmaf(r[s], s_q[tt][cc + 16 * s], acc);
+                r[s] = __builtin_fmaf(kc[s], delta, r[s]);
+                acc = __builtin_fmaf(r[s], qc[s], acc);
             }
             const float sq = dot16_tree_dpp(acc);
-            if (cc == 0) o[(int64_t)(t0 + tt) * DIN + vh * HV + row0 + rg] = sq * scale;
+            if (cc == 0) s_out[buf][tt][rg] = sq * scale;
+        };
+        // tokens in pairs, each token's q / k read from LDS while the previous one runs
+        float ka[8], qa[8], kb[8], qb[8], ga, ba, va, gb2, bb, vb;
+        ld8(s_qk[buf][0][0][cc], qa);
+        ld8(s_qk[buf][0][1][cc], ka);
+        gbv(0, ga, ba, va);
+        for (int tt = 0; tt < nt; tt += 2) {
+            const int t1 = tt + 1 < DT_T ? tt + 1 : DT_T - 1;
+            ld8(s_qk[buf][t1][0][cc], qb);
+            ld8(s_qk[buf][t1][1][cc], kb);
+            gbv(t1, gb2, bb, vb);
+            step(tt, ka, qa, ga, ba, va);
+            if (tt + 1 < nt) {
+                const int t2 = tt + 2 < DT_T ? tt + 2 : DT_T - 1;
+                ld8(s_qk[buf][t2][0][cc], qa);
+                ld8(s_qk[buf][t2][1][cc], ka);
+                gbv(t2, ga, ba, va);
+                step(tt + 1, kb, qb, gb2, bb, vb);
+            }
         }
+        if (more) put(buf ^ 1);
+        __syncthreads();
+        // the stage's outputs, coalesced (the buffer is rewritten two stages later, after a barrier)
+        for (int i = t; i < nt * 16; i += 256)
+            o[(int64_t)(t0 + (i >> 4)) * DIN + vh * HV + row0 + (i & 15)] = s_out[buf][i >> 4][i & 15];
     }
 #pragma unroll
     for (int s = 0; s < 8; s++) srow[cc + 16 * s] = r[s];
@@ -376,26 +430,199 @@ __global__ __launch_bounds__(256) void attn_kernel(const uint16_t *qh, const uin
     }
 }
 
+// The same per (query, head) arithmetic with the 8 query heads of one KV head in one workgroup
+// (grid (token, kv head)): each K row and V^T chunk is loaded once for the 8 heads. Scores: thread
+// (position pp = tid / 4 of a pass of 64, chain quad lane j) keeps the 8 heads' accumulators;
+// softmax: wave w takes heads 2 w and 2 w + 1 (wave-level reductions only), the f16 probabilities
+// overwrite the front half of the head's f32 score row (in lane order: a write only reaches score
+// slots the wave has already read); V^T . p: thread (dim, chain quad lane j) keeps the 8 heads'
+// 4 accumulators, as the decode's pv kernel. Dynamic LDS: [8][kv_cap] f32.
+constexpr int AQ_LDS_MAX = 150 * 1024;   // dynamic LDS cap of attn_gqa_kernel (32 bytes per position)
+constexpr int AQ_BYTES_PER_POS = 4 * GQA;
+__global__ __launch_bounds__(256, 2) void attn_gqa_kernel(const uint16_t *qh, const uint16_t *kc, const uint16_t *vt,
+                                                          const float *proj, int pos0, int n_ctx, int kv_cap, float *o) {
+    extern __shared__ __align__(16) float s_dyn[];
+    float *s_s = s_dyn;   // [GQA][kv_cap] f32 scores, then f16 probabilities in the first half of each row
+    __shared__ __align__(16) uint16_t s_q[GQA][HD];
+    const int64_t t = blockIdx.x;
+    const int kvh = blockIdx.y, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int pos = pos0 + (int)t;
+    int n_kv = (pos + 1 + 255) / 256 * 256;
+    if (n_kv > n_ctx) n_kv = n_ctx;
+    *(uint4 *)&s_q[tid >> 5][8 * (tid & 31)] = *(const uint4 *)(qh + (t * NH + kvh * GQA + (tid >> 5)) * HD + 8 * (tid & 31));
+    __syncthreads();
+    const int j = tid & 3;
+    {
+        const int pp = tid >> 2;
+        const uint16_t *kb = kc + (int64_t)kvh * n_ctx * HD;
+        for (int p0 = 0; p0 <= pos; p0 += 64) {
+            const int p = p0 + pp;
+            const uint16_t *krow = kb + (int64_t)(p <= pos ? p : pos) * HD;
+            h2p acc[GQA][4];
+#pragma unroll
+            for (int h = 0; h < GQA; h++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) acc[h][i] = h2p{(_Float16)0.0f, (_Float16)0.0f};
+#pragma unroll 2
+            for (int sx = 0; sx < HD / 32; sx++) {
+                const uint4 kv = *(const uint4 *)(krow + 32 * sx + 8 * j);
+#pragma unroll
+                for (int h = 0; h < GQA; h++) {
+                    const uint4 qv = *(const uint4 *)(&s_q[h][32 * sx + 8 * j]);
+                    acc[h][0] = __builtin_elementwise_fma(u2h(kv.x), u2h(qv.x), acc[h][0]);
+                    acc[h][1] = __builtin_elementwise_fma(u2h(kv.y), u2h(qv.y), acc[h][1]);
+                    acc[h][2] = __builtin_elementwise_fma(u2h(kv.z), u2h(qv.z), acc[h][2]);
+                    acc[h][3] = __builtin_elementwise_fma(u2h(kv.w), u2h(qv.w), acc[h][3]);
+                }
+            }
+#pragma unroll
+            for (int h = 0; h < GQA; h++) {
+                const float sc = f16x8_reduce_quad(acc[h]);
+                if (j == 0 && p <= pos) s_s[h * kv_cap + p] = sc;
+            }
+        }
+    }
+    __syncthreads();
+    const float scale = 1.0f / sqrtf((float)HD);
+    const int ng = n_kv / 4;
+#pragma unroll 1
+    for (int hh = 0; hh < 2; hh++) {
+        const int h = 2 * w + hh;
+        float *ss = s_s + h * kv_cap;
+        float mx = -__builtin_inff();
+        for (int p = lane; p < n_kv; p += 64) {
+            const float wv = p <= pos ? ss[p] * scale : -__builtin_inff();
+            mx = (mx > wv) ? mx : wv;
+        }
+        mx = wave_max_any(mx);
+        double part = 0.0;
+        for (int g = lane; g < ng; g += 64) {
+            float e[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int p = 4 * g + i;
+                e[i] = v_expf((p <= pos ? ss[p] * scale : -__builtin_inff()) - mx);
+            }
+            part += (double)((e[0] + e[1]) + (e[2] + e[3]));
+#pragma unroll
+            for (int i = 0; i < 4; i++) ss[4 * g + i] = e[i];
+        }
+        const double P = wave_sum_d_any(part);
+        float f;
+        wave_lds_sync();
+        if (!bracket_ok_recip(P, P, ng, &f)) {   // wave-uniform
+            double sum = 0.0;
+            for (int g = 0; g < ng; g++) sum += (double)((ss[4 * g] + ss[4 * g + 1]) + (ss[4 * g + 2] + ss[4 * g + 3]));
+            f = (float)(1.0 / sum);
+            wave_lds_sync();
+        }
+        // iteration k reads score slots [64 k, 64 k + 64) and writes f16 slots [64 k, 64 k + 64), i.e.
+        // bytes [128 k, 128 k + 128): score slots of iteration k / 2 <= k, already read
+        uint16_t *sp = (uint16_t *)ss;
+        for (int p = lane; p < n_kv; p += 64) sp[p] = f2h(ss[p] * f);
+    }
+    __syncthreads();
+    const uint16_t *vb = vt + (int64_t)kvh * HD * n_ctx;
+    const float *gate = proj + t * DN_ROWS + kvh * GQA * 2 * HD + HD;
+    for (int d0 = 0; d0 < HD; d0 += 64) {
+        const int d = d0 + (tid >> 2);
+        const uint16_t *vrow = vb + (int64_t)d * n_ctx;
+        h2p acc[GQA][4];
+#pragma unroll
+        for (int h = 0; h < GQA; h++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) acc[h][i] = h2p{(_Float16)0.0f, (_Float16)0.0f};
+        for (int sx = 0; sx < n_kv / 32; sx++) {
+            const int p = 32 * sx + 8 * j;   // this lane's 8 positions p .. p + 7 (chain quad j of block sx)
+            uint4 vv = *(const uint4 *)(vrow + p);
+            if (p + 7 > pos) {   // V^T of positions after pos is +0 in a single-token step
+                uint32_t m[4];
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int q0 = p + 2 * i;
+                    m[i] = q0 > pos ? 0u : (q0 + 1 > pos ? 0xffffu : 0xffffffffu);
+                }
+                vv.x &= m[0]; vv.y &= m[1]; vv.z &= m[2]; vv.w &= m[3];
+            }
+#pragma unroll
+            for (int h = 0; h < GQA; h++) {
+                const uint4 pv = *(const uint4 *)((const uint16_t *)(s_s + h * kv_cap) + p);
+                acc[h][0] = __builtin_elementwise_fma(u2h(vv.x), u2h(pv.x), acc[h][0]);
+                acc[h][1] = __builtin_elementwise_fma(u2h(vv.y), u2h(pv.y), acc[h][1]);
+                acc[h][2] = __builtin_elementwise_fma(u2h(vv.z), u2h(pv.z), acc[h][2]);
+                acc[h][3] = __builtin_elementwise_fma(u2h(vv.w), u2h(pv.w), acc[h][3]);
+            }
+        }
+#pragma unroll
+        for (int h = 0; h < GQA; h++) {
+            const float out = f16x8_reduce_quad(acc[h]);
+            if (j == 0) o[t * MIX_W + (kvh * GQA + h) * HD + d] = out * sigmoid_c(gate[h * 2 * HD + d]);
+        }
+    }
+}
+
 // ---- router, routing, MoE ------------------------------------------------------------------
 // router logits (ggml_vec_dot_f32: chain c of 16 over elements c + 16 q, then the NEON tree) of
-// (token, expert e < 256), and the shared-expert gate (e == 256: sigmoid of the dot with shexp_gate)
+// (token, expert e < 256), and the shared-expert gate (e == 256: sigmoid of the dot with shexp_gate).
+// Workgroup = 16 tokens x 16 rows (row 256 is the shared gate); lane group g (16 lanes, lane = chain
+// c) holds the chains of 4 tokens x 4 rows; token and weight rows are staged through LDS 256
+// elements at a time. Every dot keeps the reference's 16 chains in order and its reduction tree.
+constexpr int RT_TB = 16, RT_KC = 256, RT_LD = RT_KC + 16, RT_NR = NEXP + 1;
 __global__ __launch_bounds__(256) void router_kernel(const float *xn, const float *router, const float *shg, int T, float *lg,
                                                      float *sg) {
-    const int64_t gid = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
-    const int cc = threadIdx.x & 15;
-    const int64_t t = gid / (NEXP + 1);
-    const int e = (int)(gid % (NEXP + 1));
-    const bool live = t < T;
-    const float *wv = e < NEXP ? router + (int64_t)e * E : shg;
-    const float *xv = xn + (live ? t : 0) * E;
-    float acc = 0.0f;
-    if (live)
-#pragma unroll 8
-        for (int q = 0; q < E / 16; q++) acc = __builtin_fmaf(wv[cc + 16 * q], xv[cc + 16 * q], acc);
-    const float v = dot16_tree_dpp(acc);
-    if (live && cc == 0) {
-        if (e < NEXP) lg[t * NEXP + e] = v;
-        else sg[t] = sigmoid_c(v);
+    __shared__ __align__(16) float s_x[RT_TB][RT_LD], s_w[RT_TB][RT_LD];
+    const int tid = threadIdx.x, g = tid >> 4, c = tid & 15, tb = g & 3, eb = g >> 2;
+    const int64_t t0 = (int64_t)blockIdx.x * RT_TB;
+    const int e0 = blockIdx.y * RT_TB;
+    float acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int e = 0; e < 4; e++) acc[i][e] = 0.0f;
+    for (int k0 = 0; k0 < E; k0 += RT_KC) {
+        __syncthreads();
+#pragma unroll
+        for (int r = 0; r < RT_TB * RT_KC / 4 / 256; r++) {
+            const int i = tid + 256 * r, row = i / (RT_KC / 4), c4 = i % (RT_KC / 4);
+            const int64_t tt = t0 + row;
+            const int ee = e0 + row;
+            const float4 xv = tt < T ? *(const float4 *)(xn + tt * E + k0 + 4 * c4) : make_float4(0, 0, 0, 0);
+            const float *wr = ee < NEXP ? router + (int64_t)ee * E : shg;
+            const float4 wv = ee < RT_NR ? *(const float4 *)(wr + k0 + 4 * c4) : make_float4(0, 0, 0, 0);
+            *(float4 *)&s_x[row][4 * c4] = xv;
+            *(float4 *)&s_w[row][4 * c4] = wv;
+        }
+        __syncthreads();
+#pragma unroll 4
+        for (int q = 0; q < RT_KC / 16; q++) {
+            float xv[4], wv[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) xv[i] = s_x[4 * tb + i][16 * q + c];
+#pragma unroll
+            for (int e = 0; e < 4; e++) wv[e] = s_w[4 * eb + e][16 * q + c];
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+#pragma unroll
+                for (int e = 0; e < 4; e++) acc[i][e] = __builtin_fmaf(wv[e], xv[i], acc[i][e]);
+        }
+    }
+    float v[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int e = 0; e < 4; e++) v[i][e] = dot16_tree_dpp(acc[i][e]);
+    // every lane of the group holds all 16 sums; lane c writes (token c / 4, row c % 4)
+    float mine = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+            if (c == 4 * i + e) mine = v[i][e];
+    const int64_t tt = t0 + 4 * tb + (c >> 2);
+    const int ee = e0 + 4 * eb + (c & 3);
+    if (tt < T && ee < RT_NR) {
+        if (ee < NEXP) lg[tt * NEXP + ee] = mine;
+        else sg[tt] = sigmoid_c(mine);
     }
 }
 
@@ -553,17 +780,20 @@ int Engine::pf_alloc(int T) {
     return 0;
 }
 
+// dynamic LDS of the prefill attention for score rows of kv_cap positions: the kv-head-shared kernel
+// where its 8 rows fit, else the per-head kernel
 int Engine::pf_attn_lds(int kv_cap) {
-    const size_t lds = (size_t)kv_cap * 6;
+    const bool gqa = (size_t)kv_cap * pf::AQ_BYTES_PER_POS <= (size_t)pf::AQ_LDS_MAX;
+    const size_t lds = (size_t)kv_cap * (gqa ? pf::AQ_BYTES_PER_POS : 6);
     if (lds > 160 * 1024 - 4096) {
         set_err("prefill attention: context too long for the LDS-resident score row");
         return -1;
     }
-    if ((int)lds > pfb.attn_lds) {
-        if (hipFuncSetAttribute((const void *)pf::attn_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) !=
-            hipSuccess)
-            return -2;
-        pfb.attn_lds = (int)lds;
+    int &have = gqa ? pfb.attn_lds_gqa : pfb.attn_lds;
+    if ((int)lds > have) {
+        const void *f = gqa ? (const void *)pf::attn_gqa_kernel : (const void *)pf::attn_kernel;
+        if (hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess) return -2;
+        have = (int)lds;
     }
     return 0;
 }
@@ -628,8 +858,12 @@ int Engine::pf_chunk(const uint32_t *toks, int T, float *h_out) {
             hipLaunchKernelGGL(attn_prep_kernel, dim3(T, 5), dim3(256), 0, st, pfb.proj, w.q_norm, w.k_norm, m.rope, p0,
                                eps, pfb.qh, kcl, vtl, n_ctx, 0);
             probe(K_PF_ATTN);
-            hipLaunchKernelGGL(attn_kernel, dim3(T, NH), dim3(256), (size_t)kv_cap * 6, st, pfb.qh, kcl, vtl, pfb.proj, p0,
-                               n_ctx, kv_cap, pfb.o);
+            if ((size_t)kv_cap * AQ_BYTES_PER_POS <= (size_t)AQ_LDS_MAX)
+                hipLaunchKernelGGL(attn_gqa_kernel, dim3(T, NKV), dim3(256), (size_t)kv_cap * AQ_BYTES_PER_POS, st, pfb.qh, kcl, vtl,
+                                   pfb.proj, p0, n_ctx, kv_cap, pfb.o);
+            else
+                hipLaunchKernelGGL(attn_kernel, dim3(T, NH), dim3(256), (size_t)kv_cap * 6, st, pfb.qh, kcl, vtl, pfb.proj,
+                                   p0, n_ctx, kv_cap, pfb.o);
             probe(K_PF_ATTN);
             if ((rc = quantize_q8_0(pfb.o, (int64_t)T * MIX_W, pfb.oq, pfb.od, st))) return rc;
         }
@@ -638,8 +872,8 @@ int Engine::pf_chunk(const uint32_t *toks, int T, float *h_out) {
         // post-attention norm: Q8_0 for the experts, f32 for the router
         hipLaunchKernelGGL(norm_quant_kernel, dim3(T), dim3(PT), 0, st, m.tok_embd, nullptr, pfb.x1, w.post_norm, eps,
                            pfb.xq, pfb.xd, (int64_t)E, pfb.xn);
-        hipLaunchKernelGGL(router_kernel, dim3((unsigned)(((int64_t)T * (NEXP + 1) + 15) / 16)), dim3(256), 0, st, pfb.xn,
-                           w.router, w.shexp_gate, T, pfb.lg, pfb.sg);
+        hipLaunchKernelGGL(router_kernel, dim3((T + RT_TB - 1) / RT_TB, (RT_NR + RT_TB - 1) / RT_TB), dim3(256), 0, st,
+                           pfb.xn, w.router, w.shexp_gate, T, pfb.lg, pfb.sg);
         hipLaunchKernelGGL(route_kernel, dim3((T + 3) / 4), dim3(256), 0, st, pfb.lg, T, pfb.ids, pfb.wts,
                            b.counters + CNT_ERR_TIE);
         // shared expert over all tokens

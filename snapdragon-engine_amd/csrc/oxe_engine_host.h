@@ -51,7 +51,7 @@ struct MtpDriverHost {
 
 // Buffers of the batched prefill, [T][...] for up to cap tokens (allocated on first use)
 struct PfBufs {
-    int cap = 0, max_tiles = 0, attn_lds = 0;
+    int cap = 0, max_tiles = 0, attn_lds = 0, attn_lds_gqa = 0;
     float *x, *x1, *xn, *hin, *proj, *cy, *gg, *gb, *o, *lg, *sg, *wts, *gu, *dout, *sh;
     int8_t *xq, *oq, *hq;
     uint16_t *xd, *od, *qh, *hd;
