@@ -93,6 +93,16 @@ OXE_API int oxe_engine_counter(oxe_engine *e, int which, uint32_t *out);
 /* State copy for parity checks / hand-off (see engine.hip for the regions). */
 OXE_API int oxe_engine_state_copy(oxe_engine *e, int which, int dir, int64_t offset, void *host, int64_t nbytes);
 OXE_API int oxe_engine_set_pos(oxe_engine *e, int pos);
+/* Sequence state in the reference's byte order (prefix store / prefill hand-off): Engine::state_bytes
+ * (engine.rs:1570-1576); Engine::write_state (1682-1722): per attention layer (the MTP layer's
+ * included) the f16 K rows of positions < pos per KV head, then the f16 V^T rows (kv head *
+ * head_dim + dim) of those positions, then the current slot's conv state [n_rec][8192][3] and
+ * delta-net S [n_rec][32][128][128] (s[j*128+i] = S[i][j]), f32; write_state needs cap >=
+ * state_bytes (-1 otherwise). Engine::read_state (1819-1871): the same bytes for n_pos positions
+ * (nbytes must match exactly); V^T of positions [n_pos, pos) zeroed, position = n_pos. */
+OXE_API int64_t oxe_engine_state_bytes(const oxe_engine *e);
+OXE_API int oxe_engine_write_state(oxe_engine *e, void *host, int64_t cap);
+OXE_API int oxe_engine_read_state(oxe_engine *e, const void *host, int64_t nbytes, int n_pos);
 OXE_API int64_t oxe_engine_device_bytes(const oxe_engine *e);
 /* Run mode (no counterpart in the reference, whose runs are thread-team phases): 1 = every run
  * as one persistent launch of the fused run kernel (the default where the device has exactly 256

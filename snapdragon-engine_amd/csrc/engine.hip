@@ -119,6 +119,82 @@ int oxe_engine_set_pos(oxe_engine *e, int pos) {
 
 int64_t oxe_engine_device_bytes(const oxe_engine *e) { return (int64_t)((const Engine *)e)->bytes; }
 
+// Engine::state_bytes (engine.rs:1570-1576): K and V^T of the positions < pos of every attention
+// layer (the MTP layer's included), f16, then the current slot's conv and delta-net state, f32.
+int64_t oxe_engine_state_bytes(const oxe_engine *e) {
+    const Engine *g = (const Engine *)e;
+    using namespace oxe::shp;
+    const int64_t rec = (int64_t)g->m.n_rec * (NCH * (KC - 1) + NVH * HV * HV) * 4;
+    return (int64_t)g->m.n_att * NKV * (2 * HD + 2 * HD) * g->pos + rec;
+}
+
+// Engine::write_state (engine.rs:1682-1722): per attention layer, the K rows of positions < pos of
+// each KV head, then the V^T rows (kv head * head_dim + dim) of those positions; then conv and S of
+// the current slot. Little-endian raw bits into host memory of cap bytes.
+int oxe_engine_write_state(oxe_engine *e, void *host, int64_t cap) {
+    Engine *g = (Engine *)e;
+    using namespace oxe::shp;
+    const int64_t need = oxe_engine_state_bytes(e);
+    if (!host || cap < need) return -1;
+    const int n = g->pos, n_ctx = g->m.n_ctx;
+    char *o = (char *)host;
+    for (int ai = 0; ai < g->m.n_att; ai++) {
+        for (int h = 0; h < NKV; h++) {
+            const uint16_t *src = g->m.kcache + ((int64_t)ai * NKV + h) * n_ctx * HD;
+            if (n && hipMemcpyAsync(o, src, (size_t)n * HD * 2, hipMemcpyDeviceToHost, g->st) != hipSuccess) return -2;
+            o += (size_t)n * HD * 2;
+        }
+        const uint16_t *vt = g->m.vcache + (int64_t)ai * NKV * HD * n_ctx;
+        if (n && hipMemcpy2DAsync(o, (size_t)n * 2, vt, (size_t)n_ctx * 2, (size_t)n * 2, NKV * HD, hipMemcpyDeviceToHost,
+                                  g->st) != hipSuccess)
+            return -2;
+        o += (size_t)NKV * HD * n * 2;
+    }
+    const size_t conv = (size_t)g->m.n_rec * NCH * (KC - 1) * 4, ssm = (size_t)g->m.n_rec * NVH * HV * HV * 4;
+    if (hipMemcpyAsync(o, (const char *)g->m.conv_state + g->cur * conv, conv, hipMemcpyDeviceToHost, g->st) != hipSuccess)
+        return -2;
+    o += conv;
+    if (hipMemcpyAsync(o, (const char *)g->m.ssm_state + g->cur * ssm, ssm, hipMemcpyDeviceToHost, g->st) != hipSuccess)
+        return -2;
+    return hipStreamSynchronize(g->st) == hipSuccess ? 0 : -2;
+}
+
+// Engine::read_state (engine.rs:1819-1871): the inverse of write_state for n_pos positions; V^T
+// columns [n_pos, pos) of a longer current sequence are zeroed (zero_v), the position becomes n_pos
+// and any uncommitted verify is dropped.
+int oxe_engine_read_state(oxe_engine *e, const void *host, int64_t nbytes, int n_pos) {
+    Engine *g = (Engine *)e;
+    using namespace oxe::shp;
+    if (!host || n_pos < 0 || n_pos > g->m.n_ctx) return -1;
+    const int n_ctx = g->m.n_ctx;
+    const size_t conv = (size_t)g->m.n_rec * NCH * (KC - 1) * 4, ssm = (size_t)g->m.n_rec * NVH * HV * HV * 4;
+    const int64_t need = (int64_t)g->m.n_att * NKV * 4 * HD * n_pos + (int64_t)(conv + ssm);
+    if (nbytes != need) return -1;
+    const char *in = (const char *)host;
+    for (int ai = 0; ai < g->m.n_att; ai++) {
+        for (int h = 0; h < NKV; h++) {
+            uint16_t *dst = g->m.kcache + ((int64_t)ai * NKV + h) * n_ctx * HD;
+            if (n_pos && hipMemcpyAsync(dst, in, (size_t)n_pos * HD * 2, hipMemcpyHostToDevice, g->st) != hipSuccess) return -2;
+            in += (size_t)n_pos * HD * 2;
+        }
+        uint16_t *vt = g->m.vcache + (int64_t)ai * NKV * HD * n_ctx;
+        if (n_pos && hipMemcpy2DAsync(vt, (size_t)n_ctx * 2, in, (size_t)n_pos * 2, (size_t)n_pos * 2, NKV * HD,
+                                      hipMemcpyHostToDevice, g->st) != hipSuccess)
+            return -2;
+        in += (size_t)NKV * HD * n_pos * 2;
+    }
+    if (hipMemcpyAsync((char *)g->m.conv_state + g->cur * conv, in, conv, hipMemcpyHostToDevice, g->st) != hipSuccess)
+        return -2;
+    in += conv;
+    if (hipMemcpyAsync((char *)g->m.ssm_state + g->cur * ssm, in, ssm, hipMemcpyHostToDevice, g->st) != hipSuccess)
+        return -2;
+    // every attention layer's V^T of the positions the old sequence held beyond n_pos back to +0
+    if (g->pos > n_pos) oxe::launch_zero_v(g->m, g->m.n_att, n_pos, g->pos, g->st);
+    g->pos = n_pos;
+    g->pend_n = 0;
+    return hipStreamSynchronize(g->st) == hipSuccess ? 0 : -2;
+}
+
 }  // extern "C"
 
 extern "C" int oxe_engine_set_fused(oxe_engine *e, int on) {

@@ -166,6 +166,9 @@ def _engine_sigs(L):
         "oxe_engine_state_copy": (i32, [vp, i32, i32, i64, vp, i64]),
         "oxe_engine_set_pos": (i32, [vp, i32]),
         "oxe_engine_device_bytes": (i64, [vp]),
+        "oxe_engine_state_bytes": (i64, [vp]),
+        "oxe_engine_write_state": (i32, [vp, vp, i64]),
+        "oxe_engine_read_state": (i32, [vp, vp, i64, i32]),
         "oxe_mtp_prefill": (i32, [vp, u32p, i32, u32p]),
         "oxe_mtp_prefill_batched": (i32, [vp, u32p, i32, u32p]),
         "oxe_engine_prefill": (i32, [vp, u32p, i32, u32p, f32p]),
@@ -289,6 +292,20 @@ class Engine:
 
     def set_pos(self, pos):
         check(lib().oxe_engine_set_pos(self.h, pos), "set_pos")
+
+    def write_state(self):
+        """Engine::write_state bytes (reference order) as a numpy uint8 array."""
+        import numpy as np
+        n = int(lib().oxe_engine_state_bytes(self.h))
+        buf = np.empty(n, np.uint8)
+        check(lib().oxe_engine_write_state(self.h, buf.ctypes.data_as(C.c_void_p), n), "write_state")
+        return buf
+
+    def read_state(self, buf, n_pos):
+        """Engine::read_state of write_state bytes for n_pos positions."""
+        import numpy as np
+        b = np.ascontiguousarray(buf, np.uint8)
+        check(lib().oxe_engine_read_state(self.h, b.ctypes.data_as(C.c_void_p), b.nbytes, n_pos), "read_state")
 
     def prefill(self, toks, hidden=False):
         """Batched prefill (Engine::prefill_ext, prefill.rs:763): argmax after the last token, and

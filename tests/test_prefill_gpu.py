@@ -184,3 +184,77 @@ def test_prefill_rejects_bad_arguments():
             g.prefill(toks)
     assert g.pos == 0
     g.close()
+
+
+def oracle_state_bytes(o, d):
+    """Engine::write_state (engine.rs:1682-1722) assembled from the oracle's arrays: per attention
+    layer the K rows of positions < pos per KV head, then the V^T rows; then the current slot's conv
+    state and S."""
+    n, n_ctx = o.pos, int(o.n_ctx)
+    n_att = sum(1 for i in range(d.n_layer) if (i + 1) % d.full_attention_interval == 0) + 1
+    n_rec = d.n_layer - (n_att - 1)
+    kc = np.ctypeslib.as_array(O.lib().oxo_kcache(o.h), (n_att * NKV * n_ctx * HD,)).reshape(n_att, NKV, n_ctx, HD)
+    vc = np.ctypeslib.as_array(O.lib().oxo_vcache(o.h), (n_att * NKV * HD * n_ctx,)).reshape(n_att, NKV * HD, n_ctx)
+    conv_len, ssm_len = n_rec * NCH * 3, n_rec * NVH * HV * HV
+    cur = O.lib().oxo_cur_slot(o.h)
+    conv = np.ctypeslib.as_array(O.lib().oxo_conv_state(o.h), (2 * conv_len,))[cur * conv_len:(cur + 1) * conv_len]
+    ssm = np.ctypeslib.as_array(O.lib().oxo_ssm_state(o.h), (2 * ssm_len,))[cur * ssm_len:(cur + 1) * ssm_len]
+    parts = []
+    for ai in range(n_att):
+        for h in range(NKV):
+            parts.append(kc[ai, h, :n].tobytes())
+        parts.append(np.ascontiguousarray(vc[ai, :, :n]).tobytes())
+    parts += [conv.tobytes(), ssm.tobytes()]
+    return np.frombuffer(b"".join(parts), np.uint8)
+
+
+def test_write_state_reference_order():
+    """write_state after a batched prefill = the oracle's state after token-by-token steps, in the
+    reference's byte order; state_bytes is the reference's formula"""
+    d = O.desc_small()
+    toks = prompt(d, 23, salt=9)
+    g, o = engine(d, 256), O.Engine(d, seed=SEED, n_ctx=256)
+    print("write_state n=23", flush=True)
+    g.prefill(toks)
+    for t in toks:
+        o.step(t)
+    got, want = g.write_state(), oracle_state_bytes(o, d)
+    assert got.size == want.size == 2 * NKV * 4 * HD * 23 + 4 * 3 * (NCH * 3 + NVH * HV * HV)
+    assert np.array_equal(got, want), f"first differing byte {np.flatnonzero(got != want)[:4]}"
+    g.close()
+    o.close()
+
+
+def test_read_state_handoff_continues_exactly():
+    """prefill on one engine, hand the state to another (read_state), decode on both: identical
+    tokens and logits; a shorter state read into an engine that held a longer sequence zeroes the
+    tail of V^T and decodes like a fresh engine"""
+    d = O.desc_small()
+    toks = prompt(d, 140, salt=2)
+    a, b, c = engine(d, 512), engine(d, 512), engine(d, 512)
+    print("read_state hand-off n=140", flush=True)
+    nx = a.prefill(toks)
+    blob = a.write_state()
+    b.read_state(blob, len(toks))
+    assert b.pos == a.pos == 140
+    x = nx
+    for _ in range(4):
+        x1, x2 = a.step(x), b.step(x)
+        assert x1 == x2
+        assert np.array_equal(bits(a.logits(0)), bits(b.logits(0)))
+        x = x1
+    # c runs a longer sequence first, then takes the 140-token state: same continuation as a fresh read
+    c.prefill(prompt(d, 300, salt=7))
+    c.read_state(blob, len(toks))
+    fresh = engine(d, 512)
+    fresh.read_state(blob, len(toks))
+    # the state of positions < 140 and every V^T column (the tail back to +0) match a fresh read;
+    # K rows past the position are never read and are not cleared (as in the reference)
+    assert np.array_equal(c.write_state(), fresh.write_state())
+    assert np.array_equal(state(c, d)[1], state(fresh, d)[1])
+    assert c.step(nx) == fresh.step(nx)
+    assert np.array_equal(bits(c.logits(0)), bits(fresh.logits(0)))
+    with pytest.raises(RuntimeError):
+        c.read_state(blob[:-1], len(toks))
+    for g in (a, b, c, fresh):
+        g.close()
