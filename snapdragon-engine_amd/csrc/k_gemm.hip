@@ -14,6 +14,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "../../include/oxe_amd.h"
 #include "oxe_common.h"
 #include "oxe_gemm.h"
@@ -59,6 +61,8 @@ __global__ __launch_bounds__(gm::NT) void gemm_q8_kernel(GemmArgs a) {
     // wave w: rows 32 (w & 1) .., tokens 32 (w >> 1) ..; MFMA tile (i, j) at +16 i, +16 j
     const int wr = 32 * (w & 1), wt = 32 * (w >> 1);
     const int fr = lane & 15, fk = 8 * (lane >> 4);   // fragment row / token and its 8 k bytes
+    const int64_t wrem = pn - wt;   // tokens of the tile in this wave's column range and beyond
+    const int nj = wrem > 16 ? 2 : (wrem > 0 ? 1 : 0);
     float acc[2][2][4];
 #pragma unroll
     for (int i = 0; i < 2; i++)
@@ -85,32 +89,40 @@ __global__ __launch_bounds__(gm::NT) void gemm_q8_kernel(GemmArgs a) {
             sdx[bb][row] = xr >= 0 ? h2f(a.xd[xr * nb + kc / 32 + bb]) : 0.0f;
         }
         __syncthreads();
+        // the wave's 16-token sub-tiles that hold tokens (a per-expert group fills a tile partly):
+        // empty ones are skipped, wave-uniformly
+        auto blocks = [&](auto njc) {
+            constexpr int NJ = decltype(njc)::value;
 #pragma unroll
-        for (int bb = 0; bb < NBC; bb++) {
-            long fa[2], fb[2];
+            for (int bb = 0; bb < NBC; bb++) {
+                long fa[2], fb[NJ];
 #pragma unroll
-            for (int i = 0; i < 2; i++) fa[i] = *(const long *)(sw + (wr + 16 * i + fr) * LDR + 32 * bb + fk);
+                for (int i = 0; i < 2; i++) fa[i] = *(const long *)(sw + (wr + 16 * i + fr) * LDR + 32 * bb + fk);
 #pragma unroll
-            for (int j = 0; j < 2; j++) fb[j] = *(const long *)(sx + (wt + 16 * j + fr) * LDR + 32 * bb + fk);
-            // this lane's outputs: rows wr + 16 i + 4 (lane >> 4) + v, token wt + 16 j + (lane & 15)
-            float dxs[2], dws[2][4];
+                for (int j = 0; j < NJ; j++) fb[j] = *(const long *)(sx + (wt + 16 * j + fr) * LDR + 32 * bb + fk);
+                // this lane's outputs: rows wr + 16 i + 4 (lane >> 4) + v, token wt + 16 j + (lane & 15)
+                float dxs[NJ], dws[2][4];
 #pragma unroll
-            for (int j = 0; j < 2; j++) dxs[j] = sdx[bb][wt + 16 * j + fr];
+                for (int j = 0; j < NJ; j++) dxs[j] = sdx[bb][wt + 16 * j + fr];
 #pragma unroll
-            for (int i = 0; i < 2; i++) {
-                const float4 d4 = *(const float4 *)&sdw[bb][wr + 16 * i + 4 * (lane >> 4)];
-                dws[i][0] = d4.x; dws[i][1] = d4.y; dws[i][2] = d4.z; dws[i][3] = d4.w;
-            }
-#pragma unroll
-            for (int i = 0; i < 2; i++)
-#pragma unroll
-                for (int j = 0; j < 2; j++) {
-                    const i32x4 zero = {0, 0, 0, 0};
-                    const i32x4 s = __builtin_amdgcn_mfma_i32_16x16x32_i8(fa[i], fb[j], zero, 0, 0, 0);
-#pragma unroll
-                    for (int v = 0; v < 4; v++) acc[i][j][v] = __builtin_fmaf((float)s[v], dxs[j] * dws[i][v], acc[i][j][v]);
+                for (int i = 0; i < 2; i++) {
+                    const float4 d4 = *(const float4 *)&sdw[bb][wr + 16 * i + 4 * (lane >> 4)];
+                    dws[i][0] = d4.x; dws[i][1] = d4.y; dws[i][2] = d4.z; dws[i][3] = d4.w;
                 }
-        }
+#pragma unroll
+                for (int i = 0; i < 2; i++)
+#pragma unroll
+                    for (int j = 0; j < NJ; j++) {
+                        const i32x4 zero = {0, 0, 0, 0};
+                        const i32x4 s = __builtin_amdgcn_mfma_i32_16x16x32_i8(fa[i], fb[j], zero, 0, 0, 0);
+#pragma unroll
+                        for (int v = 0; v < 4; v++)
+                            acc[i][j][v] = __builtin_fmaf((float)s[v], dxs[j] * dws[i][v], acc[i][j][v]);
+                    }
+            }
+        };
+        if (nj == 2) blocks(std::integral_constant<int, 2>{});
+        else if (nj == 1) blocks(std::integral_constant<int, 1>{});
         __syncthreads();
     }
 #pragma unroll

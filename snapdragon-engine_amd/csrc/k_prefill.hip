@@ -896,8 +896,9 @@ int Engine::pf_chunk(const uint32_t *toks, int T, float *h_out) {
     // h_nextn of every token (output norm of x2), the LM head of the last token
     hipLaunchKernelGGL(norm_quant_kernel, dim3(T), dim3(PT), 0, st, m.tok_embd, nullptr, pfb.x, m.out_norm, eps, pfb.xq,
                        pfb.xd, (int64_t)E, pfb.xn);
-    if ((rc = gemm(m.output, pfb.xq + (int64_t)(T - 1) * E, pfb.xd + (int64_t)(T - 1) * (E / 32), E, b.logits, d.n_vocab,
-                   nullptr, 1)))
+    // the LM head of one token is a weight stream: the lane GEMV (HBM-bound), not the GEMM
+    if ((rc = oxe_hip_gemv_q8_0(E, m.output.rows, 1, m.output.q, m.output.d, pfb.xq + (int64_t)(T - 1) * E,
+                                pfb.xd + (int64_t)(T - 1) * (E / 32), b.logits, nullptr, st)))
         return rc;
     if (hipMemcpyAsync(b.hid, pfb.xn + (int64_t)(T - 1) * E, (size_t)E * 4, hipMemcpyDeviceToDevice, st) != hipSuccess)
         return -2;
