@@ -130,6 +130,49 @@ OXE_API int oxe_engine_prefill(oxe_engine *e, const uint32_t *toks, int n, uint3
 OXE_API int oxe_engine_prefill_probe(oxe_engine *e, const uint32_t *toks, int n, int kind, float *total_us,
                                      int *n_launch);
 
+/* ---- GGUF model files (crates/gguf/src/lib.rs, crates/model/src/desc.rs, weights.rs) --------- */
+
+typedef struct oxe_gguf oxe_gguf;
+
+/* Memory-map and parse a GGUF v2/v3 file: header, metadata, tensor table, data alignment
+ * (general.alignment, default 32, a power of two), every tensor inside the file. Replaces
+ * Gguf::open (gguf/src/lib.rs:345-355) with parse_header (268-316) and check_bounds (320-330):
+ * the same checks and the same error cases (bad magic, version, counts the file cannot hold, more
+ * than 4 dimensions, dimensions above 2^63, unknown types, element counts not a multiple of the
+ * type's block, overflowing sizes, data beyond the end of the file). -1 with oxe_last_error(). */
+OXE_API int oxe_gguf_open(const char *path, oxe_gguf **out);
+/* parse_header of an in-memory file image (no bounds check; file_bytes = len) */
+OXE_API int oxe_gguf_parse(const void *buf, uint64_t len, oxe_gguf **out);
+/* check_bounds against a file of file_bytes bytes */
+OXE_API int oxe_gguf_check_bounds(const oxe_gguf *g, uint64_t file_bytes);
+OXE_API void oxe_gguf_close(oxe_gguf *g);
+OXE_API int oxe_gguf_info(const oxe_gguf *g, uint32_t *version, uint64_t *n_tensors, uint64_t *n_meta,
+                          uint64_t *data_offset, uint64_t *header_bytes, uint64_t *file_bytes);
+/* tensor i: name (valid until close), ggml type id, dims, shape (unused dims 1), offset in the data
+ * section, bytes (TensorInfo, lib.rs:136-166) */
+OXE_API int oxe_gguf_tensor(const oxe_gguf *g, uint64_t i, const char **name, uint32_t *type, uint32_t *n_dims,
+                            uint64_t *shape4, uint64_t *offset, uint64_t *bytes);
+/* metadata entry i: key and GGUF value type; typed lookups by key (first match, Header::get), with
+ * Value::as_u64 / as_f64 semantics (lib.rs:113-134); arrays: item type, length, and whether the
+ * items were kept (arrays longer than 4096 items are counted only) */
+OXE_API int oxe_gguf_meta(const oxe_gguf *g, uint64_t i, const char **key, uint32_t *type);
+OXE_API int oxe_gguf_meta_u64(const oxe_gguf *g, const char *key, uint64_t *out);
+OXE_API int oxe_gguf_meta_f64(const oxe_gguf *g, const char *key, double *out);
+OXE_API int oxe_gguf_meta_str(const oxe_gguf *g, const char *key, const char **out);
+OXE_API int oxe_gguf_meta_array(const oxe_gguf *g, const char *key, uint32_t *item_type, uint64_t *len, int *kept);
+OXE_API int oxe_gguf_meta_array_f64(const oxe_gguf *g, const char *key, uint64_t i, double *out);
+/* ModelDesc::from_header + check (desc.rs:69-178): qwen35moe only, layer kinds from the tensors
+ * (ssm_a / attn_q) checked against full_attention_interval, shape cross-checks. */
+OXE_API int oxe_gguf_model_desc(const oxe_gguf *g, oxe_model_desc *out);
+/* Every weight of the engine from the file (WeightStore::load, weights.rs:556-700): Q8_0 matmul
+ * weights split on the device into this build's codes + scales layout (the reference repacks into
+ * 4-row interleaved blocks, oxe_repack_q8_0_4x8, lib.rs:59), F32 norms, routers and state
+ * parameters copied. Other tensor types are refused by name (-1): the kernels run Q8_0 matmul
+ * weights and F32 vectors only (k-quants and BF16 routers are not built). */
+OXE_API int oxe_engine_load_gguf(oxe_engine *e, const oxe_gguf *g);
+/* open + model_desc + engine_create + load_gguf */
+OXE_API int oxe_engine_create_from_gguf(const char *path, int n_ctx, oxe_engine **out);
+
 /* ---- MTP depth-1 speculative decoding (crates/model/src/mtp.rs MtpDriver, depth 1) --------- */
 
 /* Append prompt tokens through 2-token verify runs and the MTP catch-up (MtpDriver::prefill,

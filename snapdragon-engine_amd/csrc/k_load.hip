@@ -1,0 +1,218 @@
+// Weight loader (WeightStore::load, crates/model/src/weights.rs:556-700, for the device): every
+// tensor the engine reads is taken from a GGUF file (gguf.cpp) into the engine's device arrays in
+// the kernels' layout. Q8_0 matmul weights are split on the device from ggml's 34-byte blocks
+// (fp16 d, 32 int8 codes) into codes [rows][k] + fp16 scales [rows][k/32] (the form every GEMV /
+// GEMM kernel here reads, in place of the reference's 4-row interleave, oxe_shim.cpp:9-29),
+// concatenated per projection ([qkv | z | beta | alpha], [q+gate | k | v]) and, for gate / up
+// pairs, interleaved per 16-row tile (8 gate rows, then 8 up rows). F32 vectors and matrices are
+// copied. Any other tensor type is refused with the tensor's name: the kernels of this build run
+// Q8_0 matmul weights and F32 routers / norms only.
+#include <algorithm>
+#include <string>
+
+#include "oxe_engine_host.h"
+#include "oxe_gguf.h"
+
+namespace oxe {
+
+namespace ld {
+
+// rows of raw Q8_0 blocks -> codes + scales; source row R (of `rows`, `grp_rows` per group, e.g.
+// per expert) goes to destination row dst0 + (R / grp_rows) * dst_grp + map(R % grp_rows), map =
+// identity, or the gate / up tile interleave 16 (r / 8) + il + r % 8 (il 0 gate, 8 up)
+__global__ void q8_split_kernel(const uint8_t *src, int64_t rows, int64_t k, int64_t grp_rows, int64_t dst_grp,
+                                int64_t dst0, int il, int8_t *q, uint16_t *d) {
+    const int64_t nbr = k / 32, nb = rows * nbr;
+    for (int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; b < nb; b += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t R = b / nbr, kb = b % nbr, g = R / grp_rows, r = R % grp_rows;
+        const int64_t dr = dst0 + g * dst_grp + (il < 0 ? r : 16 * (r / 8) + il + r % 8);
+        const uint16_t *blk = (const uint16_t *)(src + b * 34);   // 34-byte blocks: 2-byte aligned
+        uint32_t w[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) w[i] = (uint32_t)blk[1 + 2 * i] | ((uint32_t)blk[2 + 2 * i] << 16);
+        uint4 *dst = (uint4 *)(q + dr * k + kb * 32);
+        dst[0] = make_uint4(w[0], w[1], w[2], w[3]);
+        dst[1] = make_uint4(w[4], w[5], w[6], w[7]);
+        d[dr * nbr + kb] = blk[0];
+    }
+}
+
+}  // namespace ld
+
+// host-visible status of a load: "" or the first problem
+static std::string tensor_check(const GgufTensor *t, const std::string &name, uint32_t type,
+                                std::initializer_list<uint64_t> shape) {
+    if (!t) return "missing tensor " + name;
+    GgmlTypeInfo ti{};
+    ggml_type_info(t->type, &ti);
+    if (t->type != type) {
+        GgmlTypeInfo want{};
+        ggml_type_info(type, &want);
+        return name + ": type " + (ti.name ? ti.name : "unknown") + " has no kernel in this build (expected " +
+               want.name + ": Q8_0 matmul weights, F32 vectors and routers)";
+    }
+    if (t->shape != std::vector<uint64_t>(shape)) return name + ": unexpected shape";
+    return "";
+}
+
+int Engine::load_gguf(const Gguf &g) {
+    constexpr int64_t CHUNK = 256ll << 20;   // staging bytes per upload
+    uint8_t *stage = nullptr;
+    if (hipMalloc(&stage, CHUNK) != hipSuccess) {
+        set_err("out of device memory for the load staging buffer");
+        return -3;
+    }
+    std::string err;
+    int rc = 0;
+    // Q8_0 tensor of rows x k (x n_grp groups) into (q, d) with the row mapping of q8_split_kernel
+    auto q8 = [&](const std::string &name, int64_t k, int64_t rows, int64_t n_grp, int8_t *q, uint16_t *d,
+                  int64_t dst0, int64_t dst_grp, int il) {
+        if (!err.empty()) return;
+        const GgufTensor *t = g.tensor(name);
+        err = n_grp > 1 ? tensor_check(t, name, GGML_Q8_0, {(uint64_t)k, (uint64_t)rows, (uint64_t)n_grp})
+                        : tensor_check(t, name, GGML_Q8_0, {(uint64_t)k, (uint64_t)rows});
+        if (!err.empty()) return;
+        const int64_t row_bytes = k / 32 * 34, grp_bytes = rows * row_bytes;
+        const uint8_t *src = g.data(*t);
+        auto launch = [&](int64_t off, int64_t n_rows, int64_t grp_rows, int64_t d0) {
+            if (hipMemcpyAsync(stage, src + off, (size_t)(n_rows * row_bytes), hipMemcpyHostToDevice, st) != hipSuccess) {
+                rc = -2;
+                return;
+            }
+            const int64_t nb = n_rows * (k / 32);
+            hipLaunchKernelGGL(ld::q8_split_kernel, dim3((unsigned)std::min<int64_t>((nb + 255) / 256, 65535)), dim3(256),
+                               0, st, stage, n_rows, k, grp_rows, dst_grp, d0, il, q, d);
+            if (hipGetLastError() != hipSuccess) rc = -2;
+        };
+        if (n_grp == 1) {
+            // one matrix, in row chunks (an interleaved gate / up matrix is one chunk: the tile
+            // mapping needs the matrix-local row)
+            if (il >= 0 && grp_bytes > CHUNK) {
+                err = name + ": interleaved matrix larger than the staging buffer";
+                return;
+            }
+            const int64_t per = std::max<int64_t>(1, CHUNK / row_bytes);
+            for (int64_t r0 = 0; r0 < rows && !rc; r0 += per) {
+                const int64_t n = std::min(per, rows - r0);
+                launch(r0 * row_bytes, n, il >= 0 ? rows : ((int64_t)1 << 62), dst0 + (il >= 0 ? 0 : r0));
+            }
+        } else {
+            // per-expert groups, whole groups per chunk
+            const int64_t per = std::max<int64_t>(1, CHUNK / grp_bytes);
+            if (grp_bytes > CHUNK) {
+                err = name + ": expert matrix larger than the staging buffer";
+                return;
+            }
+            for (int64_t g0 = 0; g0 < n_grp && !rc; g0 += per) {
+                const int64_t n = std::min(per, n_grp - g0);
+                launch(g0 * grp_bytes, n * rows, rows, dst0 + g0 * dst_grp);
+            }
+        }
+    };
+    auto f32 = [&](const std::string &name, std::initializer_list<uint64_t> shape, float *dst) {
+        if (!err.empty()) return;
+        const GgufTensor *t = g.tensor(name);
+        err = tensor_check(t, name, GGML_F32, shape);
+        if (!err.empty()) return;
+        if (hipMemcpyAsync(dst, g.data(*t), (size_t)t->bytes(), hipMemcpyHostToDevice, st) != hipSuccess) rc = -2;
+    };
+    const int nl_total = d.n_layer + 1;
+    for (int il = 0; il < nl_total && err.empty() && !rc; il++) {
+        LayerW &w = L[il];
+        const std::string p = "blk." + std::to_string(il) + ".";
+        f32(p + "attn_norm.weight", {E}, w.attn_norm);
+        f32(p + "post_attention_norm.weight", {E}, w.post_norm);
+        if (!w.att) {
+            q8(p + "attn_qkv.weight", E, NCH, 1, w.proj.q, w.proj.d, 0, 0, -1);
+            q8(p + "attn_gate.weight", E, DIN, 1, w.proj.q, w.proj.d, DN_Z, 0, -1);
+            q8(p + "ssm_beta.weight", E, NVH, 1, w.proj.q, w.proj.d, DN_BETA, 0, -1);
+            q8(p + "ssm_alpha.weight", E, NVH, 1, w.proj.q, w.proj.d, DN_ALPHA, 0, -1);
+            q8(p + "ssm_out.weight", DIN, E, 1, w.out.q, w.out.d, 0, 0, -1);
+            f32(p + "ssm_conv1d.weight", {KC, NCH}, w.conv);
+            f32(p + "ssm_a", {NVH}, w.ssm_a);
+            f32(p + "ssm_dt.bias", {NVH}, w.dt_bias);
+            f32(p + "ssm_norm.weight", {HV}, w.ssm_norm);
+        } else {
+            q8(p + "attn_q.weight", E, NH * 2 * HD, 1, w.proj.q, w.proj.d, 0, 0, -1);
+            q8(p + "attn_k.weight", E, NKV * HD, 1, w.proj.q, w.proj.d, AT_K, 0, -1);
+            q8(p + "attn_v.weight", E, NKV * HD, 1, w.proj.q, w.proj.d, AT_V, 0, -1);
+            q8(p + "attn_output.weight", NH * HD, E, 1, w.out.q, w.out.d, 0, 0, -1);
+            f32(p + "attn_q_norm.weight", {HD}, w.q_norm);
+            f32(p + "attn_k_norm.weight", {HD}, w.k_norm);
+        }
+        f32(p + "ffn_gate_inp.weight", {E, NEXP}, w.router);
+        f32(p + "ffn_gate_inp_shexp.weight", {E}, w.shexp_gate);
+        q8(p + "ffn_gate_shexp.weight", E, FFSH, 1, w.shexp_gu.q, w.shexp_gu.d, 0, 0, 0);
+        q8(p + "ffn_up_shexp.weight", E, FFSH, 1, w.shexp_gu.q, w.shexp_gu.d, 0, 0, 8);
+        q8(p + "ffn_down_shexp.weight", FFSH, E, 1, w.shexp_down.q, w.shexp_down.d, 0, 0, -1);
+        q8(p + "ffn_gate_exps.weight", E, FF, NEXP, w.exp_gu.q, w.exp_gu.d, 0, 2 * FF, 0);
+        q8(p + "ffn_up_exps.weight", E, FF, NEXP, w.exp_gu.q, w.exp_gu.d, 0, 2 * FF, 8);
+        q8(p + "ffn_down_exps.weight", FF, E, NEXP, w.exp_down.q, w.exp_down.d, 0, E, -1);
+        if (il == d.n_layer) {
+            q8(p + "nextn.eh_proj.weight", 2 * E, E, 1, w.eh_proj.q, w.eh_proj.d, 0, 0, -1);
+            f32(p + "nextn.enorm.weight", {E}, w.enorm);
+            f32(p + "nextn.hnorm.weight", {E}, w.hnorm);
+            f32(p + "nextn.shared_head_norm.weight", {E}, w.head_norm);
+        }
+    }
+    q8("token_embd.weight", E, d.n_vocab, 1, m.tok_embd.q, m.tok_embd.d, 0, 0, -1);
+    q8("output.weight", E, d.n_vocab, 1, m.output.q, m.output.d, 0, 0, -1);
+    f32("output_norm.weight", {E}, m.out_norm);
+    const hipError_t se = hipStreamSynchronize(st);
+    (void)hipFree(stage);
+    if (!err.empty()) {
+        set_err(err);
+        return -1;
+    }
+    if (rc || se != hipSuccess) return -2;
+    return 0;
+}
+
+}  // namespace oxe
+
+extern "C" {
+
+int oxe_engine_load_gguf(oxe_engine *e, const oxe_gguf *gg) {
+    oxe::Engine *g = (oxe::Engine *)e;
+    const oxe::Gguf *f = (const oxe::Gguf *)gg;
+    if (!g || !f) return -1;
+    oxe_model_desc d;
+    if (oxe_gguf_model_desc(gg, &d)) return -1;
+    if (d.n_layer != g->d.n_layer || d.n_vocab != g->d.n_vocab || !d.has_mtp) {
+        oxe::set_err("the file's model (layers, vocabulary, MTP block) differs from the engine's");
+        return -1;
+    }
+    return g->load_gguf(*f);
+}
+
+int oxe_engine_create_from_gguf(const char *path, int n_ctx, oxe_engine **out) {
+    if (!out) return -1;
+    oxe_gguf *f = nullptr;
+    int rc = oxe_gguf_open(path, &f);
+    if (rc) return rc;
+    oxe_model_desc d;
+    if ((rc = oxe_gguf_model_desc(f, &d))) {
+        oxe_gguf_close(f);
+        return rc;
+    }
+    if (!d.has_mtp) {
+        oxe::set_err("the file has no nextn (MTP) block: this engine runs MTP depth-1 decoding");
+        oxe_gguf_close(f);
+        return -1;
+    }
+    oxe_engine *e = nullptr;
+    if ((rc = oxe_engine_create(&d, 0, n_ctx, &e))) {
+        oxe_gguf_close(f);
+        return rc;
+    }
+    rc = oxe_engine_load_gguf(e, f);
+    oxe_gguf_close(f);
+    if (rc) {
+        oxe_engine_destroy(e);
+        return rc;
+    }
+    *out = e;
+    return 0;
+}
+
+}  // extern "C"

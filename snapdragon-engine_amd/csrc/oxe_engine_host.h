@@ -25,6 +25,7 @@ namespace oxe {
 using namespace shp;
 
 struct Engine;
+struct Gguf;
 
 // MtpDriver (crates/model/src/mtp.rs:314-608) at depth 1, host-driven; dev_begin / dev_end hand its
 // state to and from the device-driven step.
@@ -108,6 +109,8 @@ struct Engine {
     int pf_chunk(const uint32_t *toks, int T, float *h_out);
     int prefill(const uint32_t *toks, int n, uint32_t *next, float *h_all);
     int seed_batched(const uint32_t *toks, int n, int pos0, const float *hs);
+    // weights from a GGUF file (k_load.hip)
+    int load_gguf(const Gguf &g);
     // kernel probe: HIP events around every launch of one kernel kind while enqueuing eagerly
     int probe_kind = -1;
     std::vector<hipEvent_t> probe_ev;

@@ -188,6 +188,24 @@ def _engine_sigs(L):
         "oxe_engine_sync": (i32, [vp]),
         "oxe_mtp_device_probe": (i32, [vp, i32, i32, C.POINTER(C.c_float), C.POINTER(C.c_int)]),
         "oxe_engine_stream": (vp, [vp]),
+        "oxe_gguf_open": (i32, [C.c_char_p, C.POINTER(C.c_void_p)]),
+        "oxe_gguf_parse": (i32, [vp, C.c_uint64, C.POINTER(C.c_void_p)]),
+        "oxe_gguf_check_bounds": (i32, [vp, C.c_uint64]),
+        "oxe_gguf_close": (None, [vp]),
+        "oxe_gguf_info": (i32, [vp, C.POINTER(C.c_uint32)] + [C.POINTER(C.c_uint64)] * 5),
+        "oxe_gguf_tensor": (i32, [vp, C.c_uint64, C.POINTER(C.c_char_p), C.POINTER(C.c_uint32),
+                                  C.POINTER(C.c_uint32), C.POINTER(C.c_uint64), C.POINTER(C.c_uint64),
+                                  C.POINTER(C.c_uint64)]),
+        "oxe_gguf_meta": (i32, [vp, C.c_uint64, C.POINTER(C.c_char_p), C.POINTER(C.c_uint32)]),
+        "oxe_gguf_meta_u64": (i32, [vp, C.c_char_p, C.POINTER(C.c_uint64)]),
+        "oxe_gguf_meta_f64": (i32, [vp, C.c_char_p, C.POINTER(C.c_double)]),
+        "oxe_gguf_meta_str": (i32, [vp, C.c_char_p, C.POINTER(C.c_char_p)]),
+        "oxe_gguf_meta_array": (i32, [vp, C.c_char_p, C.POINTER(C.c_uint32), C.POINTER(C.c_uint64),
+                                      C.POINTER(C.c_int)]),
+        "oxe_gguf_meta_array_f64": (i32, [vp, C.c_char_p, C.c_uint64, C.POINTER(C.c_double)]),
+        "oxe_gguf_model_desc": (i32, [vp, vp]),
+        "oxe_engine_load_gguf": (i32, [vp, vp]),
+        "oxe_engine_create_from_gguf": (i32, [C.c_char_p, i32, C.POINTER(C.c_void_p)]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -197,6 +215,116 @@ def _engine_sigs(L):
 
 def _np_ptr(a, ct):
     return a.ctypes.data_as(C.POINTER(ct))
+
+
+def _sigs():
+    L = lib()
+    if not hasattr(L, "_engine_sigs"):
+        _engine_sigs(L)
+        L._engine_sigs = True
+    return L
+
+
+def _last_error():
+    e = _sigs().oxe_last_error()
+    return e.decode(errors="replace") if e else ""
+
+
+class GgufError(RuntimeError):
+    pass
+
+
+class Gguf:
+    """A parsed GGUF file (crates/gguf Gguf / Header): metadata and tensor table; the payload is
+    read only by the weight loader."""
+
+    def __init__(self, path=None, data=None):
+        L = _sigs()
+        h = C.c_void_p()
+        if data is not None:
+            self._buf = bytes(data)
+            rc = L.oxe_gguf_parse(self._buf, len(self._buf), C.byref(h))
+        else:
+            rc = L.oxe_gguf_open(os.fsencode(path), C.byref(h))
+        if rc != 0:
+            raise GgufError(_last_error())
+        self.h = h
+
+    def close(self):
+        if getattr(self, "h", None) and _lib is not None:
+            _lib.oxe_gguf_close(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()
+
+    def check_bounds(self, file_bytes):
+        if lib().oxe_gguf_check_bounds(self.h, file_bytes) != 0:
+            raise GgufError(_last_error())
+
+    def info(self):
+        v = C.c_uint32()
+        n = [C.c_uint64() for _ in range(5)]
+        check(lib().oxe_gguf_info(self.h, C.byref(v), *[C.byref(x) for x in n]), "gguf_info")
+        keys = ("n_tensors", "n_meta", "data_offset", "header_bytes", "file_bytes")
+        return dict(version=v.value, **{k: x.value for k, x in zip(keys, n)})
+
+    def tensors(self):
+        """[(name, ggml type id, shape, offset, bytes)] in file order"""
+        out = []
+        for i in range(self.info()["n_tensors"]):
+            name, ty, nd = C.c_char_p(), C.c_uint32(), C.c_uint32()
+            shape, off, nb = (C.c_uint64 * 4)(), C.c_uint64(), C.c_uint64()
+            check(lib().oxe_gguf_tensor(self.h, i, C.byref(name), C.byref(ty), C.byref(nd), shape, C.byref(off),
+                                        C.byref(nb)), "gguf_tensor")
+            out.append((name.value.decode(), ty.value, list(shape[: nd.value]), off.value, nb.value))
+        return out
+
+    def meta_keys(self):
+        out = []
+        for i in range(self.info()["n_meta"]):
+            k, t = C.c_char_p(), C.c_uint32()
+            check(lib().oxe_gguf_meta(self.h, i, C.byref(k), C.byref(t)), "gguf_meta")
+            out.append((k.value.decode(), t.value))
+        return out
+
+    def u64(self, key):
+        v = C.c_uint64()
+        return v.value if lib().oxe_gguf_meta_u64(self.h, key.encode(), C.byref(v)) == 0 else None
+
+    def f64(self, key):
+        v = C.c_double()
+        return v.value if lib().oxe_gguf_meta_f64(self.h, key.encode(), C.byref(v)) == 0 else None
+
+    def str(self, key):
+        v = C.c_char_p()
+        return v.value.decode() if lib().oxe_gguf_meta_str(self.h, key.encode(), C.byref(v)) == 0 else None
+
+    def array(self, key):
+        """(item type, length, items as floats or None when only counted)"""
+        it, n, kept = C.c_uint32(), C.c_uint64(), C.c_int()
+        if lib().oxe_gguf_meta_array(self.h, key.encode(), C.byref(it), C.byref(n), C.byref(kept)) != 0:
+            return None
+        items = None
+        if kept.value:
+            items = []
+            for i in range(n.value):
+                x = C.c_double()
+                items.append(x.value if lib().oxe_gguf_meta_array_f64(self.h, key.encode(), i, C.byref(x)) == 0
+                             else None)
+        return it.value, n.value, items
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def model_desc(self):
+        d = ModelDesc()
+        if lib().oxe_gguf_model_desc(self.h, C.byref(d)) != 0:
+            raise GgufError(_last_error())
+        return d
 
 
 class Engine:
@@ -217,6 +345,26 @@ class Engine:
         self.n_ctx = L.oxe_engine_n_ctx(h)
         if synth:
             check(L.oxe_engine_synth_weights(h), "synth_weights")
+
+    @classmethod
+    def from_gguf(cls, path, n_ctx=1024):
+        """An engine with every weight from a GGUF file (oxe_engine_create_from_gguf)."""
+        L = _sigs()
+        h = C.c_void_p()
+        rc = L.oxe_engine_create_from_gguf(os.fsencode(path), n_ctx, C.byref(h))
+        if rc != 0:
+            raise GgufError(f"oxe_engine_create_from_gguf: {rc} {_last_error()}")
+        e = cls.__new__(cls)
+        e.h = h
+        e.n_ctx = L.oxe_engine_n_ctx(h)
+        with Gguf(path) as g:
+            e.desc = g.model_desc()
+        return e
+
+    def load_gguf(self, g):
+        rc = lib().oxe_engine_load_gguf(self.h, g.h)
+        if rc != 0:
+            raise GgufError(f"oxe_engine_load_gguf: {rc} {_last_error()}")
 
     def close(self):
         if getattr(self, "h", None) and _lib is not None:

@@ -111,7 +111,25 @@ def engine_small():
 MAKERS = dict(config1_slice=config1_slice, route=route, dn_step=dn_step, attn_head=attn_head,
               engine_small=engine_small)
 
+# GGUF header fixtures: the fields the tests use of the reference's own test fixtures
+# tests/fixtures/{qwen36,ornith}.json (model_inspect.py's reading of the real Qwen3.6 and Ornith
+# files: metadata, tensor table, layer / expert layout), copied as data
+GGUF_FIXTURE_KEYS = ["source", "file", "file_bytes", "gguf_version", "data_offset", "header_bytes_read",
+                     "n_metadata", "architecture", "layers", "experts", "kv_bytes_per_token_f16",
+                     "recurrent_state_bytes", "tensor_bytes", "metadata", "tensors"]
+
+
+def gguf_headers(ref="/root/reference/tests/fixtures"):
+    import json
+    for name in ("qwen36", "ornith"):
+        fx = json.load(open(os.path.join(ref, name + ".json")))
+        with open(os.path.join(HERE, f"gguf_header_{name}.json"), "w") as f:
+            json.dump({k: fx[k] for k in GGUF_FIXTURE_KEYS}, f, separators=(",", ":"))
+        print("wrote", f"gguf_header_{name}.json")
+
+
 if __name__ == "__main__":
     for name, fn in MAKERS.items():
         np.savez_compressed(os.path.join(HERE, name + ".npz"), **fn())
         print("wrote", name)
+    gguf_headers()

@@ -1,0 +1,95 @@
+"""Weights from a GGUF file on the GPU (Gguf::open + ModelDesc::from_header + WeightStore::load,
+crates/gguf/src/lib.rs, crates/model/src/desc.rs, weights.rs).
+
+The synthetic model is written as a qwen35moe GGUF file with the reference's tensor names and ggml
+layouts (tests/gguf_writer.py, from the oracle's generator); an engine created from the file must
+decode bit for bit like the engine that generates the same weights on the device (prefill,
+logits, hidden states, speculative steps), which checks every tensor's name, shape, Q8_0 block
+split, projection concatenation and gate / up interleave at once. A real Qwen3.6 file (its header
+rebuilt from the reference's fixture, a sparse file of the real size) is refused by name at its
+first tensor type without a kernel here."""
+import json
+import os
+
+import numpy as np
+import pytest
+
+import gguf_writer as W
+import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+SEED = 5
+
+
+def bits(a):
+    return np.ascontiguousarray(a, np.float32).view(np.uint32)
+
+
+def scratch_dir():
+    return "/dev/shm" if os.path.isdir("/dev/shm") and os.access("/dev/shm", os.W_OK) else "/tmp"
+
+
+def test_engine_from_gguf_decodes_like_the_synthetic_engine():
+    import oxe_amd as A
+    d = O.desc_small()
+    path = os.path.join(scratch_dir(), f"oxe_test_synth_{os.getpid()}.gguf")
+    try:
+        print("writing the synthetic model as GGUF", flush=True)
+        W.write_synth_model(path, O, d, SEED)
+        print(f"wrote {os.path.getsize(path) >> 20} MiB; loading", flush=True)
+        g = A.Engine.from_gguf(path, n_ctx=512)
+        s = A.Engine(d, seed=SEED, n_ctx=512)
+        for f, _ in d._fields_:
+            a, b = getattr(g.desc, f), getattr(d, f)
+            assert (list(a) == list(b)) if f == "rope_sections" else a == b, f
+        toks = [int(v) % d.n_vocab for v in O.bench_prompt(40)]
+        print("prefill and steps", flush=True)
+        assert g.prefill(toks) == s.prefill(toks)
+        assert np.array_equal(bits(g.logits(0)), bits(s.logits(0)))
+        assert np.array_equal(bits(g.hidden(0)), bits(s.hidden(0)))
+        x = s.step(7)
+        assert g.step(7) == x
+        assert np.array_equal(bits(g.logits(0)), bits(s.logits(0)))
+        # MTP head: draft, verify, accept through the loaded nextn block
+        for _ in range(4):
+            og, os_ = g.mtp_step(x), s.mtp_step(x)
+            assert og == os_
+            x = os_[-1]
+        assert np.array_equal(bits(g.hidden(0)), bits(s.hidden(0)))
+        g.close()
+        s.close()
+    finally:
+        if os.path.exists(path):
+            os.remove(path)
+
+
+def test_real_qwen36_file_is_refused_by_tensor_type():
+    """the reference's Qwen3.6 file (header from its fixture, a sparse file of the real size):
+    F32 ssm_beta (and k-quant experts) have no kernel in this build -> -1 with the tensor's name"""
+    import oxe_amd as A
+    fx = json.load(open(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden",
+                                     "gguf_header_qwen36.json")))
+    ids = {"F32": 0, "Q8_0": 8, "Q4_K": 12, "Q5_K": 13, "Q6_K": 14, "BF16": 30}
+
+    def typed(k, v):
+        if isinstance(v, str):
+            return (k, "str", v)
+        if isinstance(v, int):
+            return (k, "u32", v)
+        if isinstance(v, float):
+            return (k, "f32", v)
+        return (k, "arr", ("i32", v))
+
+    hdr, data_offset = W.header_at([typed(k, v) for k, v in fx["metadata"].items()],
+                                   [(n, ids[t], s, o) for n, t, s, o, _ in fx["tensors"]])
+    path = os.path.join("/tmp", f"oxe_test_qwen36_{os.getpid()}.gguf")
+    try:
+        with open(path, "wb") as f:
+            f.write(hdr)
+            f.truncate(data_offset + fx["tensor_bytes"])   # sparse: no data written
+        with pytest.raises(A.GgufError, match="blk.0.ssm_beta.weight: type F32 has no kernel"):
+            A.Engine.from_gguf(path, n_ctx=256)
+    finally:
+        if os.path.exists(path):
+            os.remove(path)
