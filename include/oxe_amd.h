@@ -48,6 +48,13 @@ OXE_API int oxe_hip_gemv_q8_0(int64_t k, int64_t nr, int nl, const int8_t *wq, c
 OXE_API int oxe_hip_gemm_q8_0(int64_t k, int64_t nr, int64_t nt, const int8_t *wq, const uint16_t *wd, const int8_t *xq,
                               const uint16_t *xd, float *y, int64_t ldy, void *stream);
 
+/* Q8_0 weight repack: nrows rows of ggml Q8_0 blocks (34 bytes: fp16 d, 32 int8 codes; device memory)
+ * into this build's layout, int8 codes [nrows][k] + fp16 scales [nrows][k/32], which every GEMV /
+ * GEMM entry point here reads. Replaces oxe_repack_q8_0_4x8 (crates/kernels-sys/src/lib.rs:59, the
+ * reference's 4-row interleave for its NEON GEMV); -1 on a bad shape (k not a multiple of 32),
+ * nothing written. */
+OXE_API int oxe_hip_repack_q8_0(const void *src, int64_t nrows, int64_t k, int8_t *q, uint16_t *d, void *stream);
+
 /* Parity hook (no counterpart in the reference): y[i] = f(x) for the float x with bits
  * start + i*stride, i < n, on the device; f: 0 expf and 1 log1pf (the C library functions the
  * reference calls, oxe_ops.cpp:80-89), 2 ggml_v_expf (vec.h:1154-1175), 3 the sigmoid and

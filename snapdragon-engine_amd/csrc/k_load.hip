@@ -172,6 +172,15 @@ int Engine::load_gguf(const Gguf &g) {
 
 extern "C" {
 
+int oxe_hip_repack_q8_0(const void *src, int64_t nrows, int64_t k, int8_t *q, uint16_t *d, void *stream) {
+    if (!src || !q || !d || nrows <= 0 || k <= 0 || k % 32 != 0) return -1;
+    const int64_t nb = nrows * (k / 32);
+    hipLaunchKernelGGL(oxe::ld::q8_split_kernel, dim3((unsigned)std::min<int64_t>((nb + 255) / 256, 65535)), dim3(256), 0,
+                       (hipStream_t)stream, (const uint8_t *)src, nrows, k, (int64_t)1 << 62, (int64_t)0, (int64_t)0, -1,
+                       q, d);
+    return hipGetLastError() == hipSuccess ? 0 : -2;
+}
+
 int oxe_engine_load_gguf(oxe_engine *e, const oxe_gguf *gg) {
     oxe::Engine *g = (oxe::Engine *)e;
     const oxe::Gguf *f = (const oxe::Gguf *)gg;

@@ -30,6 +30,7 @@ def lib():
         sig = {
             "oxe_hip_quantize_row_q8_0": (i32, [vp, i64, i64, vp, vp, vp]),
             "oxe_hip_gemv_q8_0": (i32, [i64, i64, i32, vp, vp, vp, vp, vp, vp, vp]),
+            "oxe_hip_repack_q8_0": (i32, [vp, i64, i64, vp, vp, vp]),
             "oxe_hip_gemm_q8_0": (i32, [i64, i64, i64, vp, vp, vp, vp, vp, i64, vp]),
             "oxe_hip_eval_unary": (i32, [i32, C.c_uint32, i64, i64, vp, vp]),
         }
@@ -136,6 +137,17 @@ def gemm_q8_0(wq, wd, xq, xd, y=None):
         y = torch.empty((nt, nr), dtype=torch.float32, device=wq.device)
     check(lib().oxe_hip_gemm_q8_0(k, nr, nt, _p(wq), _p(wd), _p(xq), _p(xd), _p(y), y.stride(0), _stream()), "gemm_q8_0")
     return y
+
+
+def repack_q8_0(blocks, k):
+    """ggml Q8_0 blocks (uint8 [nrows, k/32*34] on the GPU) -> (codes int8 [nrows, k], scales int16
+    [nrows, k/32]) in this build's layout (oxe_hip_repack_q8_0)"""
+    import torch
+    nrows = blocks.shape[0]
+    q = torch.empty((nrows, k), dtype=torch.int8, device=blocks.device)
+    d = torch.empty((nrows, k // 32), dtype=torch.int16, device=blocks.device)
+    check(lib().oxe_hip_repack_q8_0(_p(blocks), nrows, k, _p(q), _p(d), _stream()), "repack_q8_0")
+    return q, d
 
 
 def eval_unary(fn, start, n, stride, y):

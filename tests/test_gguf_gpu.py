@@ -93,3 +93,25 @@ def test_real_qwen36_file_is_refused_by_tensor_type():
     finally:
         if os.path.exists(path):
             os.remove(path)
+
+
+def test_repack_q8_0_splits_ggml_blocks(dev):
+    """oxe_hip_repack_q8_0: ggml Q8_0 blocks -> codes + scales, exactly the oracle's arrays; the
+    repacked weights run the GEMV to the oracle's bits; k not a multiple of 32 is refused"""
+    import oxe_amd as A
+    import torch
+    for rows, k in ((300, 2048), (7, 512), (1, 32)):
+        q, d = O.synth_q8(9, 2, O.T["DN_OUT"], rows, k)
+        blocks = torch.from_numpy(np.frombuffer(W.q8_blocks(q, d), np.uint8).reshape(rows, k // 32 * 34).copy()).to(dev)
+        gq, gd = A.repack_q8_0(blocks, k)
+        assert np.array_equal(gq.cpu().numpy(), q)
+        assert np.array_equal(gd.cpu().numpy().view(np.uint16), d)
+    x = (O.synth_normal(9, 11, 2 * 2048).reshape(2, 2048)).astype(np.float32)
+    xq, xd = O.quantize_q8_0(x)
+    q, d = O.synth_q8(9, 3, O.T["DN_OUT"], 256, 2048)
+    blocks = torch.from_numpy(np.frombuffer(W.q8_blocks(q, d), np.uint8).reshape(256, 64 * 34).copy()).to(dev)
+    gq, gd = A.repack_q8_0(blocks, 2048)
+    y = A.gemv_q8_0(gq, gd, torch.from_numpy(xq).to(dev), torch.from_numpy(xd.view(np.int16)).to(dev))
+    assert np.array_equal(y.cpu().numpy().view(np.uint32), O.gemv_q8_0(q, d, xq, xd).view(np.uint32))
+    with pytest.raises(RuntimeError):
+        A.repack_q8_0(torch.zeros((2, 34), dtype=torch.uint8, device=dev), 48)
