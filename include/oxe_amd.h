@@ -110,6 +110,13 @@ OXE_API int oxe_engine_set_pos(oxe_engine *e, int pos);
 OXE_API int64_t oxe_engine_state_bytes(const oxe_engine *e);
 OXE_API int oxe_engine_write_state(oxe_engine *e, void *host, int64_t cap);
 OXE_API int oxe_engine_read_state(oxe_engine *e, const void *host, int64_t nbytes, int n_pos);
+/* KV rows of positions [a, b) in the write_state order (the prefix store's row segments):
+ * Engine::kv_row_bytes (engine.rs:1812-1814) = bytes per position; Engine::write_kv_rows
+ * (1727-1767), b <= pos, cap >= (b - a) * kv_row_bytes; Engine::read_kv_rows (1769-1810), b <=
+ * n_ctx, nbytes == (b - a) * kv_row_bytes, the position does not change. */
+OXE_API int64_t oxe_engine_kv_row_bytes(const oxe_engine *e);
+OXE_API int oxe_engine_write_kv_rows(oxe_engine *e, int a, int b, void *host, int64_t cap);
+OXE_API int oxe_engine_read_kv_rows(oxe_engine *e, int a, int b, const void *host, int64_t nbytes);
 OXE_API int64_t oxe_engine_device_bytes(const oxe_engine *e);
 /* Run mode (no counterpart in the reference, whose runs are thread-team phases): 1 = every run
  * as one persistent launch of the fused run kernel (the default where the device has exactly 256
@@ -218,6 +225,86 @@ OXE_API int oxe_mtp_stats(const oxe_engine *e, int64_t *st);
 OXE_API int oxe_engine_sync(oxe_engine *e);
 /* the engine's HIP stream (hipStream_t) */
 OXE_API void *oxe_engine_stream(oxe_engine *e);
+
+/* ---- the server's engine (crates/server/src/engine.rs:28-190 trait Engine, implemented for oxe
+ * by crates/server/src/oxe_engine.rs:317-634 OxeEngine) ---------------------------------------
+ * An oxe_srv borrows an engine (destroy the oxe_srv first) and, with mtp != 0, drives it through
+ * the MTP depth-1 driver. Errors: -1 with oxe_last_error() (the reference's EngineError text),
+ * -2 HIP error; 1 = "not supported here" (the trait's Ok(None)). */
+typedef struct oxe_srv oxe_srv;
+typedef struct oxe_snapshot oxe_snapshot;
+
+OXE_API int oxe_srv_create(oxe_engine *engine, int mtp, oxe_srv **out);
+OXE_API void oxe_srv_destroy(oxe_srv *s);
+OXE_API oxe_engine *oxe_srv_engine(oxe_srv *s);
+/* n_ctx / n_vocab / n_past (Engine::n_ctx, n_vocab, n_past) */
+OXE_API int oxe_srv_n_ctx(const oxe_srv *s);
+OXE_API int oxe_srv_n_vocab(const oxe_srv *s);
+OXE_API int oxe_srv_n_past(const oxe_srv *s);
+/* reset (OxeEngine::reset, oxe_engine.rs:336-341; Engine::reset, engine.rs:1491-1509): empty
+ * sequence, recurrent state and V^T zeroed, MTP driver re-synced with h_prev = 0 */
+OXE_API int oxe_srv_reset(oxe_srv *s);
+/* prefill (oxe_engine.rs:342-374): append n >= 1 tokens ("empty prefill", "context full", "token
+ * T out of vocab"); with MTP the batched prefill seeds the MTP KV (one token: step_plain); logits
+ * (optional, host [n_vocab]) = the last token's row. logits NULL = prefill_quiet (375-390). */
+OXE_API int oxe_srv_prefill(oxe_srv *s, const uint32_t *toks, int n, float *logits);
+/* decode (the trait's default: prefill of one token) */
+OXE_API int oxe_srv_decode(oxe_srv *s, uint32_t tok, float *logits);
+/* decode_argmax (oxe_engine.rs:544-562): one step (MTP: step_plain), *out = the first maximum of
+ * the logits row */
+OXE_API int oxe_srv_decode_argmax(oxe_srv *s, uint32_t tok, uint32_t *out);
+/* decode_spec_argmax (oxe_engine.rs:563-578): one MTP step from tok; extra[0..n_extra) = accepted
+ * drafts (in the state), argmax[0..n_argmax) = the argmax of every committed row (the last is the
+ * bonus token, not yet in the state); arrays of 2 (the verify lanes). 1 without MTP. */
+OXE_API int oxe_srv_decode_spec_argmax(oxe_srv *s, uint32_t tok, uint32_t *extra, int *n_extra, uint32_t *argmax,
+                                       int *n_argmax);
+/* decode_spec (oxe_engine.rs:530-543): as decode_spec_argmax with the committed rows' logits,
+ * rows = host [n_extra + 1][n_vocab] */
+OXE_API int oxe_srv_decode_spec(oxe_srv *s, uint32_t tok, uint32_t *extra, int *n_extra, float *rows);
+/* spec_rewind (oxe_engine.rs:579-592): keep the first `keep` tokens the last lookup verify or MTP
+ * step committed (MtpDriver::rewind, mtp.rs:596-608) */
+OXE_API int oxe_srv_spec_rewind(oxe_srv *s, int keep);
+/* decode_verify (oxe_engine.rs:593-619): caller drafts on the plain engine (1 with MTP on, no
+ * drafts or no room): verify [tok, drafts[0..k)], k = min(n_drafts, verify lanes - 1 = 1, room), accept the prefix
+ * equal to greedy decoding, commit it; accepted[0..n_acc), argmax[0..n_acc] as decode_spec_argmax */
+OXE_API int oxe_srv_decode_verify(oxe_srv *s, uint32_t tok, const uint32_t *drafts, int n_drafts, uint32_t *accepted,
+                                  int *n_acc, uint32_t *argmax, int *n_argmax);
+/* spec_max_depth / spec_counters (oxe_engine.rs:620-633): MTP (drafted, accepted) or the lookup
+ * counts of decode_verify */
+OXE_API int oxe_srv_spec_max_depth(const oxe_srv *s);
+OXE_API int oxe_srv_spec_counters(const oxe_srv *s, uint64_t *drafted, uint64_t *accepted);
+/* snapshot / snapshot_reuse (oxe_engine.rs:391-397; Engine::save_recurrent, engine.rs:1525-1531):
+ * the current slot's conv + delta-net state (a device copy) and the position, plus the MTP
+ * driver's state; *inout NULL allocates a snapshot, else it is reused. restore (oxe_engine.rs:
+ * 402-409; Engine::restore_recurrent, engine.rs:1643-1659): refused for a snapshot ahead of the
+ * position; V^T of the positions beyond it back to +0; the MTP driver imports the snapshot's
+ * state when it fits (MtpDriver::import_state, mtp.rs:391-401), else re-syncs (363-382). */
+OXE_API int oxe_srv_snapshot(oxe_srv *s, oxe_snapshot **inout);
+OXE_API int oxe_srv_restore(oxe_srv *s, const oxe_snapshot *snap);
+/* snapshot_bytes (oxe_engine.rs:410-412), the snapshot's position, free */
+OXE_API int64_t oxe_snapshot_bytes(const oxe_snapshot *snap);
+OXE_API int oxe_snapshot_pos(const oxe_snapshot *snap);
+OXE_API void oxe_snapshot_free(oxe_snapshot *snap);
+/* state_size_hint (oxe_engine.rs:398-401); save_state / load_state (oxe_engine.rs:492-529):
+ * Engine::write_state bytes, then with MTP u64 q, u64 n, n u32 catch-up tokens, their n h rows and
+ * h_prev (f32); save_bytes = the exact size save_state writes; load_state checks the whole buffer
+ * before it changes any state */
+OXE_API int64_t oxe_srv_state_size_hint(const oxe_srv *s);
+OXE_API int64_t oxe_srv_save_bytes(const oxe_srv *s);
+OXE_API int oxe_srv_save_state(oxe_srv *s, void *buf, int64_t cap, int64_t *written);
+OXE_API int oxe_srv_load_state(oxe_srv *s, const void *buf, int64_t nbytes, int n_pos);
+/* snapshot files (snap_save / snap_save_live / snap_load, oxe_engine.rs:428-467):
+ * RecurrentSnapshot::write_to (engine.rs:572-582) + tag byte (0 / 2) + MtpState::write
+ * (oxe_engine.rs:108-119); snap_load needs the KV rows of positions < n_pos in place
+ * (oxe_engine_read_kv_rows) and the file's position equal to n_pos */
+OXE_API int64_t oxe_srv_snap_file_bytes(const oxe_srv *s, const oxe_snapshot *snap);
+OXE_API int oxe_srv_snap_save(oxe_srv *s, const oxe_snapshot *snap, void *buf, int64_t cap, int64_t *written);
+OXE_API int64_t oxe_srv_snap_live_bytes(const oxe_srv *s);
+OXE_API int oxe_srv_snap_save_live(oxe_srv *s, void *buf, int64_t cap, int64_t *written);
+OXE_API int oxe_srv_snap_load(oxe_srv *s, const void *buf, int64_t nbytes, int n_pos);
+/* Engine::state_layout (engine.rs:1669-1677), f16 KV: "att=A kv_heads=H head_dim=D conv=C ssm=S
+ * f16kv"; returns 0, or the bytes needed when cap is too small */
+OXE_API int oxe_srv_state_layout(const oxe_srv *s, char *buf, int cap);
 
 #ifdef __cplusplus
 }

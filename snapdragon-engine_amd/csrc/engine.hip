@@ -128,28 +128,77 @@ int64_t oxe_engine_state_bytes(const oxe_engine *e) {
     return (int64_t)g->m.n_att * NKV * (2 * HD + 2 * HD) * g->pos + rec;
 }
 
-// Engine::write_state (engine.rs:1682-1722): per attention layer, the K rows of positions < pos of
-// each KV head, then the V^T rows (kv head * head_dim + dim) of those positions; then conv and S of
+// K and V^T rows of positions [a, b) of every attention layer (the MTP layer's included), in the
+// order of Engine::write_kv_rows / read_kv_rows (engine.rs:1727-1810): per layer the K rows of
+// each KV head, then the V^T rows (kv head * head_dim + dim), f16 bits. to_host: device -> host.
+static int kv_rows_copy(Engine *g, int a, int b, char *host, bool to_host) {
+    using namespace oxe::shp;
+    const int n = b - a, n_ctx = g->m.n_ctx;
+    if (n == 0) return 0;
+    const hipMemcpyKind kind = to_host ? hipMemcpyDeviceToHost : hipMemcpyHostToDevice;
+    for (int ai = 0; ai < g->m.n_att; ai++) {
+        for (int h = 0; h < NKV; h++) {
+            uint16_t *k = g->m.kcache + ((int64_t)ai * NKV + h) * n_ctx * HD + (int64_t)a * HD;
+            if (hipMemcpyAsync(to_host ? (void *)host : (void *)k, to_host ? (const void *)k : (const void *)host,
+                               (size_t)n * HD * 2, kind, g->st) != hipSuccess)
+                return -2;
+            host += (size_t)n * HD * 2;
+        }
+        uint16_t *vt = g->m.vcache + (int64_t)ai * NKV * HD * n_ctx + a;
+        const hipError_t r = to_host ? hipMemcpy2DAsync(host, (size_t)n * 2, vt, (size_t)n_ctx * 2, (size_t)n * 2,
+                                                        NKV * HD, kind, g->st)
+                                     : hipMemcpy2DAsync(vt, (size_t)n_ctx * 2, host, (size_t)n * 2, (size_t)n * 2,
+                                                        NKV * HD, kind, g->st);
+        if (r != hipSuccess) return -2;
+        host += (size_t)NKV * HD * n * 2;
+    }
+    return 0;
+}
+
+// Engine::kv_row_bytes (engine.rs:1812-1814): K + V bytes per position over every attention layer
+int64_t oxe_engine_kv_row_bytes(const oxe_engine *e) {
+    using namespace oxe::shp;
+    return (int64_t)((const Engine *)e)->m.n_att * NKV * 4 * HD;
+}
+
+// Engine::write_kv_rows (engine.rs:1727-1767): rows of positions [a, b), b <= pos
+int oxe_engine_write_kv_rows(oxe_engine *e, int a, int b, void *host, int64_t cap) {
+    Engine *g = (Engine *)e;
+    if (a < 0 || a > b || b > g->pos) {
+        oxe::set_err("kv rows beyond the current position");
+        return -1;
+    }
+    if (!host || cap < oxe_engine_kv_row_bytes(e) * (b - a)) return -1;
+    int rc = kv_rows_copy(g, a, b, (char *)host, true);
+    if (rc) return rc;
+    return hipStreamSynchronize(g->st) == hipSuccess ? 0 : -2;
+}
+
+// Engine::read_kv_rows (engine.rs:1769-1810): rows of positions [a, b), b <= n_ctx; the position
+// does not change (a recurrent snapshot sets it after the rows)
+int oxe_engine_read_kv_rows(oxe_engine *e, int a, int b, const void *host, int64_t nbytes) {
+    Engine *g = (Engine *)e;
+    if (a < 0 || a > b || b > g->m.n_ctx) {
+        oxe::set_err("kv rows beyond the context");
+        return -1;
+    }
+    if (!host || nbytes != oxe_engine_kv_row_bytes(e) * (b - a)) return -1;
+    int rc = kv_rows_copy(g, a, b, (char *)host, false);
+    if (rc) return rc;
+    return hipStreamSynchronize(g->st) == hipSuccess ? 0 : -2;
+}
+
+// Engine::write_state (engine.rs:1682-1722): the KV rows of positions < pos, then conv and S of
 // the current slot. Little-endian raw bits into host memory of cap bytes.
 int oxe_engine_write_state(oxe_engine *e, void *host, int64_t cap) {
     Engine *g = (Engine *)e;
     using namespace oxe::shp;
     const int64_t need = oxe_engine_state_bytes(e);
     if (!host || cap < need) return -1;
-    const int n = g->pos, n_ctx = g->m.n_ctx;
     char *o = (char *)host;
-    for (int ai = 0; ai < g->m.n_att; ai++) {
-        for (int h = 0; h < NKV; h++) {
-            const uint16_t *src = g->m.kcache + ((int64_t)ai * NKV + h) * n_ctx * HD;
-            if (n && hipMemcpyAsync(o, src, (size_t)n * HD * 2, hipMemcpyDeviceToHost, g->st) != hipSuccess) return -2;
-            o += (size_t)n * HD * 2;
-        }
-        const uint16_t *vt = g->m.vcache + (int64_t)ai * NKV * HD * n_ctx;
-        if (n && hipMemcpy2DAsync(o, (size_t)n * 2, vt, (size_t)n_ctx * 2, (size_t)n * 2, NKV * HD, hipMemcpyDeviceToHost,
-                                  g->st) != hipSuccess)
-            return -2;
-        o += (size_t)NKV * HD * n * 2;
-    }
+    int rc = kv_rows_copy(g, 0, g->pos, o, true);
+    if (rc) return rc;
+    o += oxe_engine_kv_row_bytes(e) * g->pos;
     const size_t conv = (size_t)g->m.n_rec * NCH * (KC - 1) * 4, ssm = (size_t)g->m.n_rec * NVH * HV * HV * 4;
     if (hipMemcpyAsync(o, (const char *)g->m.conv_state + g->cur * conv, conv, hipMemcpyDeviceToHost, g->st) != hipSuccess)
         return -2;
@@ -166,23 +215,13 @@ int oxe_engine_read_state(oxe_engine *e, const void *host, int64_t nbytes, int n
     Engine *g = (Engine *)e;
     using namespace oxe::shp;
     if (!host || n_pos < 0 || n_pos > g->m.n_ctx) return -1;
-    const int n_ctx = g->m.n_ctx;
     const size_t conv = (size_t)g->m.n_rec * NCH * (KC - 1) * 4, ssm = (size_t)g->m.n_rec * NVH * HV * HV * 4;
-    const int64_t need = (int64_t)g->m.n_att * NKV * 4 * HD * n_pos + (int64_t)(conv + ssm);
+    const int64_t need = oxe_engine_kv_row_bytes(e) * n_pos + (int64_t)(conv + ssm);
     if (nbytes != need) return -1;
     const char *in = (const char *)host;
-    for (int ai = 0; ai < g->m.n_att; ai++) {
-        for (int h = 0; h < NKV; h++) {
-            uint16_t *dst = g->m.kcache + ((int64_t)ai * NKV + h) * n_ctx * HD;
-            if (n_pos && hipMemcpyAsync(dst, in, (size_t)n_pos * HD * 2, hipMemcpyHostToDevice, g->st) != hipSuccess) return -2;
-            in += (size_t)n_pos * HD * 2;
-        }
-        uint16_t *vt = g->m.vcache + (int64_t)ai * NKV * HD * n_ctx;
-        if (n_pos && hipMemcpy2DAsync(vt, (size_t)n_ctx * 2, in, (size_t)n_pos * 2, (size_t)n_pos * 2, NKV * HD,
-                                      hipMemcpyHostToDevice, g->st) != hipSuccess)
-            return -2;
-        in += (size_t)NKV * HD * n_pos * 2;
-    }
+    int rc = kv_rows_copy(g, 0, n_pos, (char *)in, false);
+    if (rc) return rc;
+    in += oxe_engine_kv_row_bytes(e) * n_pos;
     if (hipMemcpyAsync((char *)g->m.conv_state + g->cur * conv, in, conv, hipMemcpyHostToDevice, g->st) != hipSuccess)
         return -2;
     in += conv;

@@ -218,6 +218,41 @@ def _engine_sigs(L):
         "oxe_gguf_model_desc": (i32, [vp, vp]),
         "oxe_engine_load_gguf": (i32, [vp, vp]),
         "oxe_engine_create_from_gguf": (i32, [C.c_char_p, i32, C.POINTER(C.c_void_p)]),
+        "oxe_engine_kv_row_bytes": (i64, [vp]),
+        "oxe_engine_write_kv_rows": (i32, [vp, i32, i32, vp, i64]),
+        "oxe_engine_read_kv_rows": (i32, [vp, i32, i32, vp, i64]),
+        "oxe_srv_create": (i32, [vp, i32, C.POINTER(C.c_void_p)]),
+        "oxe_srv_destroy": (None, [vp]),
+        "oxe_srv_engine": (vp, [vp]),
+        "oxe_srv_n_ctx": (i32, [vp]),
+        "oxe_srv_n_vocab": (i32, [vp]),
+        "oxe_srv_n_past": (i32, [vp]),
+        "oxe_srv_reset": (i32, [vp]),
+        "oxe_srv_prefill": (i32, [vp, u32p, i32, f32p]),
+        "oxe_srv_decode": (i32, [vp, C.c_uint32, f32p]),
+        "oxe_srv_decode_argmax": (i32, [vp, C.c_uint32, u32p]),
+        "oxe_srv_decode_spec_argmax": (i32, [vp, C.c_uint32, u32p, C.POINTER(C.c_int), u32p, C.POINTER(C.c_int)]),
+        "oxe_srv_decode_spec": (i32, [vp, C.c_uint32, u32p, C.POINTER(C.c_int), f32p]),
+        "oxe_srv_spec_rewind": (i32, [vp, i32]),
+        "oxe_srv_decode_verify": (i32, [vp, C.c_uint32, u32p, i32, u32p, C.POINTER(C.c_int), u32p,
+                                        C.POINTER(C.c_int)]),
+        "oxe_srv_spec_max_depth": (i32, [vp]),
+        "oxe_srv_spec_counters": (i32, [vp, C.POINTER(C.c_uint64), C.POINTER(C.c_uint64)]),
+        "oxe_srv_snapshot": (i32, [vp, C.POINTER(C.c_void_p)]),
+        "oxe_srv_restore": (i32, [vp, vp]),
+        "oxe_snapshot_bytes": (i64, [vp]),
+        "oxe_snapshot_pos": (i32, [vp]),
+        "oxe_snapshot_free": (None, [vp]),
+        "oxe_srv_state_size_hint": (i64, [vp]),
+        "oxe_srv_save_bytes": (i64, [vp]),
+        "oxe_srv_save_state": (i32, [vp, vp, i64, C.POINTER(C.c_int64)]),
+        "oxe_srv_load_state": (i32, [vp, vp, i64, i32]),
+        "oxe_srv_snap_file_bytes": (i64, [vp, vp]),
+        "oxe_srv_snap_save": (i32, [vp, vp, vp, i64, C.POINTER(C.c_int64)]),
+        "oxe_srv_snap_live_bytes": (i64, [vp]),
+        "oxe_srv_snap_save_live": (i32, [vp, vp, i64, C.POINTER(C.c_int64)]),
+        "oxe_srv_snap_load": (i32, [vp, vp, i64, i32]),
+        "oxe_srv_state_layout": (i32, [vp, C.c_char_p, i32]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -467,6 +502,25 @@ class Engine:
         b = np.ascontiguousarray(buf, np.uint8)
         check(lib().oxe_engine_read_state(self.h, b.ctypes.data_as(C.c_void_p), b.nbytes, n_pos), "read_state")
 
+    def kv_row_bytes(self):
+        return int(lib().oxe_engine_kv_row_bytes(self.h))
+
+    def write_kv_rows(self, a, b):
+        """Engine::write_kv_rows: K and V^T rows of positions [a, b) as a numpy uint8 array."""
+        import numpy as np
+        buf = np.empty(self.kv_row_bytes() * (b - a), np.uint8)
+        rc = lib().oxe_engine_write_kv_rows(self.h, a, b, buf.ctypes.data_as(C.c_void_p), buf.nbytes)
+        if rc != 0:
+            raise EngineError(f"save kv rows: {_last_error() or rc}")
+        return buf
+
+    def read_kv_rows(self, a, b, buf):
+        import numpy as np
+        x = np.ascontiguousarray(buf, np.uint8)
+        rc = lib().oxe_engine_read_kv_rows(self.h, a, b, x.ctypes.data_as(C.c_void_p), x.nbytes)
+        if rc != 0:
+            raise EngineError(f"load kv rows: {_last_error() or rc}")
+
     def prefill(self, toks, hidden=False):
         """Batched prefill (Engine::prefill_ext, prefill.rs:763): argmax after the last token, and
         with hidden=True also every position's h_nextn [n][n_embd]."""
@@ -577,3 +631,200 @@ class Engine:
 
     def stream(self):
         return lib().oxe_engine_stream(self.h)
+
+
+class EngineError(RuntimeError):
+    """The server engine's error (crates/server/src/engine.rs EngineError) with its message."""
+
+
+class Snapshot:
+    """OxeSnapshot: the recurrent state of the current slot (device copy), the position and the
+    MTP driver's state."""
+
+    def __init__(self, h):
+        self.h = h
+
+    @property
+    def pos(self):
+        return int(lib().oxe_snapshot_pos(self.h))
+
+    def close(self):
+        if getattr(self, "h", None) and _lib is not None:
+            _lib.oxe_snapshot_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()
+
+
+class ServerEngine:
+    """The reference server's `Engine` trait for oxe (crates/server/src/engine.rs:28-190,
+    OxeEngine in crates/server/src/oxe_engine.rs:317-634) over an Engine, with or without the MTP
+    depth-1 driver: the same method names, argument meaning, return values (None where the trait
+    returns Ok(None)) and error messages (EngineError)."""
+
+    def __init__(self, engine, mtp=True):
+        L = _sigs()
+        self.engine = engine
+        self.mtp = bool(mtp)
+        h = C.c_void_p()
+        check(L.oxe_srv_create(engine.h, int(self.mtp), C.byref(h)), "oxe_srv_create")
+        self.h = h
+        self.n_vocab = int(L.oxe_srv_n_vocab(h))
+
+    def close(self):
+        if getattr(self, "h", None) and _lib is not None:
+            _lib.oxe_srv_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()
+
+    def _rc(self, rc, what):
+        if rc < 0:
+            raise EngineError(_last_error() if rc == -1 and _last_error() else f"{what}: status {rc}")
+        return rc
+
+    def n_ctx(self):
+        return int(lib().oxe_srv_n_ctx(self.h))
+
+    def n_past(self):
+        return int(lib().oxe_srv_n_past(self.h))
+
+    def reset(self):
+        self._rc(lib().oxe_srv_reset(self.h), "reset")
+
+    def prefill(self, tokens):
+        import numpy as np
+        t = np.ascontiguousarray(tokens, np.uint32)
+        out = np.empty(self.n_vocab, np.float32)
+        self._rc(lib().oxe_srv_prefill(self.h, _np_ptr(t, C.c_uint32), len(t), _np_ptr(out, C.c_float)), "prefill")
+        return out
+
+    def prefill_quiet(self, tokens):
+        import numpy as np
+        t = np.ascontiguousarray(tokens, np.uint32)
+        self._rc(lib().oxe_srv_prefill(self.h, _np_ptr(t, C.c_uint32), len(t), None), "prefill")
+
+    def decode(self, token):
+        import numpy as np
+        out = np.empty(self.n_vocab, np.float32)
+        self._rc(lib().oxe_srv_decode(self.h, token, _np_ptr(out, C.c_float)), "decode")
+        return out
+
+    def decode_argmax(self, token):
+        import numpy as np
+        out = np.zeros(1, np.uint32)
+        self._rc(lib().oxe_srv_decode_argmax(self.h, token, _np_ptr(out, C.c_uint32)), "decode_argmax")
+        return int(out[0])
+
+    def decode_spec_argmax(self, token):
+        import numpy as np
+        ex, g = np.zeros(8, np.uint32), np.zeros(8, np.uint32)
+        ne, ng = C.c_int(0), C.c_int(0)
+        rc = self._rc(lib().oxe_srv_decode_spec_argmax(self.h, token, _np_ptr(ex, C.c_uint32), C.byref(ne),
+                                                        _np_ptr(g, C.c_uint32), C.byref(ng)), "decode_spec_argmax")
+        if rc == 1:
+            return None
+        return [int(v) for v in ex[: ne.value]], [int(v) for v in g[: ng.value]]
+
+    def decode_spec(self, token):
+        import numpy as np
+        ex = np.zeros(8, np.uint32)
+        ne = C.c_int(0)
+        rows = np.empty((8, self.n_vocab), np.float32)
+        rc = self._rc(lib().oxe_srv_decode_spec(self.h, token, _np_ptr(ex, C.c_uint32), C.byref(ne),
+                                                 _np_ptr(rows, C.c_float)), "decode_spec")
+        if rc == 1:
+            return None
+        return [int(v) for v in ex[: ne.value]], [rows[i].copy() for i in range(ne.value + 1)]
+
+    def spec_rewind(self, keep):
+        self._rc(lib().oxe_srv_spec_rewind(self.h, keep), "spec_rewind")
+
+    def decode_verify(self, token, drafts):
+        import numpy as np
+        d = np.ascontiguousarray(drafts, np.uint32)
+        acc, g = np.zeros(8, np.uint32), np.zeros(8, np.uint32)
+        na, ng = C.c_int(0), C.c_int(0)
+        rc = self._rc(lib().oxe_srv_decode_verify(self.h, token, _np_ptr(d, C.c_uint32), len(d), _np_ptr(acc, C.c_uint32),
+                                                   C.byref(na), _np_ptr(g, C.c_uint32), C.byref(ng)), "decode_verify")
+        if rc == 1:
+            return None
+        return [int(v) for v in acc[: na.value]], [int(v) for v in g[: ng.value]]
+
+    def spec_max_depth(self):
+        return int(lib().oxe_srv_spec_max_depth(self.h))
+
+    def spec_counters(self):
+        a, b = C.c_uint64(0), C.c_uint64(0)
+        self._rc(lib().oxe_srv_spec_counters(self.h, C.byref(a), C.byref(b)), "spec_counters")
+        return int(a.value), int(b.value)
+
+    def snapshot(self):
+        h = C.c_void_p()
+        self._rc(lib().oxe_srv_snapshot(self.h, C.byref(h)), "snapshot")
+        return Snapshot(h)
+
+    def snapshot_reuse(self, old):
+        h = C.c_void_p(old.h.value if isinstance(old.h, C.c_void_p) else old.h)
+        self._rc(lib().oxe_srv_snapshot(self.h, C.byref(h)), "snapshot")
+        old.h = None
+        return Snapshot(h)
+
+    def restore(self, snap):
+        self._rc(lib().oxe_srv_restore(self.h, snap.h), "restore")
+
+    @staticmethod
+    def snapshot_bytes(snap):
+        return int(lib().oxe_snapshot_bytes(snap.h))
+
+    def state_size_hint(self):
+        return int(lib().oxe_srv_state_size_hint(self.h))
+
+    def state_id(self):
+        buf = C.create_string_buffer(256)
+        self._rc(lib().oxe_srv_state_layout(self.h, buf, 256), "state_layout")
+        return f"oxe-state-v1 {buf.value.decode()} mtp={'true' if self.mtp else 'false'}"
+
+    def save_state_vec(self):
+        import numpy as np
+        buf = np.empty(int(lib().oxe_srv_save_bytes(self.h)), np.uint8)
+        w = C.c_int64(0)
+        self._rc(lib().oxe_srv_save_state(self.h, buf.ctypes.data_as(C.c_void_p), buf.nbytes, C.byref(w)), "save_state")
+        return buf[: w.value]
+
+    def load_state(self, buf, n_pos):
+        import numpy as np
+        b = np.ascontiguousarray(buf, np.uint8)
+        self._rc(lib().oxe_srv_load_state(self.h, b.ctypes.data_as(C.c_void_p), b.nbytes, n_pos), "load_state")
+
+    def kv_row_bytes(self):
+        return self.engine.kv_row_bytes()
+
+    def kv_rows_save(self, a, b):
+        return self.engine.write_kv_rows(a, b)
+
+    def kv_rows_load(self, a, b, buf):
+        self.engine.read_kv_rows(a, b, buf)
+
+    def snap_save(self, snap):
+        import numpy as np
+        buf = np.empty(int(lib().oxe_srv_snap_file_bytes(self.h, snap.h)), np.uint8)
+        w = C.c_int64(0)
+        self._rc(lib().oxe_srv_snap_save(self.h, snap.h, buf.ctypes.data_as(C.c_void_p), buf.nbytes, C.byref(w)),
+                 "snap_save")
+        return buf[: w.value]
+
+    def snap_save_live(self):
+        import numpy as np
+        buf = np.empty(int(lib().oxe_srv_snap_live_bytes(self.h)), np.uint8)
+        w = C.c_int64(0)
+        self._rc(lib().oxe_srv_snap_save_live(self.h, buf.ctypes.data_as(C.c_void_p), buf.nbytes, C.byref(w)),
+                 "snap_save_live")
+        return buf[: w.value]
+
+    def snap_load(self, buf, n_pos):
+        import numpy as np
+        b = np.ascontiguousarray(buf, np.uint8)
+        self._rc(lib().oxe_srv_snap_load(self.h, b.ctypes.data_as(C.c_void_p), b.nbytes, n_pos), "snap_load")
