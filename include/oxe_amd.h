@@ -55,6 +55,25 @@ OXE_API int oxe_hip_gemm_q8_0(int64_t k, int64_t nr, int64_t nt, const int8_t *w
  * nothing written. */
 OXE_API int oxe_hip_repack_q8_0(const void *src, int64_t nrows, int64_t k, int8_t *q, uint16_t *d, void *stream);
 
+/* K-quant activation quantizer: nrows rows of k floats (k a multiple of 256; x 16-byte aligned) ->
+ * ggml block_q8_K blocks (float d, int8 qs[256], int16 bsums[16]; 292 bytes each) [nrows][k/256].
+ * Replaces quantize_row_q8_K (on ARM the reference's is quantize_row_q8_K_ref,
+ * vendor/ggml-subset/generated/quants_base.c:14-48, ggml_subset.h:18-19); an all-zero block gets
+ * zero sums (the reference leaves them unwritten). 0, -1 bad shape, -2 launch error. */
+OXE_API int oxe_hip_quantize_row_q8_K(const float *x, int64_t k, int64_t nrows, void *y, void *stream);
+
+/* K-quant lane GEMV: s[l][r] = W[r] . y[l] for nl = 1..4 lanes, bit for bit the reference's
+ * per-lane result. type 3 Q3_K, 4 Q4_K, 5 Q5_K, 6 Q6_K; w = nr rows of k/256 ggml blocks of the type
+ * (the GGUF file's bytes, 4-byte aligned; no repack), y = nl lanes of k/256 block_q8_K (as
+ * oxe_hip_quantize_row_q8_K writes them: the kernels use their bsums), s = float [nl][nr]. Replaces
+ * oxe_vl_gemv (crates/kernels-sys/src/lib.rs:113; csrc/oxe_vl.inc:78-107 and oxe_vl_q{3,4,5,6}k.inc),
+ * whose weights are its 8-row interleaved repack, and its per-lane fallback ggml_gemv_q*_K_8x8_q8_K.
+ * Returns as the reference: 1 = done, 0 = not handled, nothing written (another type, nl outside
+ * 1..4, k not a multiple of 256 or above 65536, Q3_K / Q6_K with an odd number of blocks per row);
+ * -2 launch error. */
+OXE_API int oxe_hip_vl_gemv(int type, int64_t k, int64_t nr, int nl, const void *w, const void *y, float *s,
+                            void *stream);
+
 /* Parity hook (no counterpart in the reference): y[i] = f(x) for the float x with bits
  * start + i*stride, i < n, on the device; f: 0 expf and 1 log1pf (the C library functions the
  * reference calls, oxe_ops.cpp:80-89), 2 ggml_v_expf (vec.h:1154-1175), 3 the sigmoid and

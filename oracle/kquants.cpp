@@ -1,0 +1,238 @@
+// TEST INFRASTRUCTURE ONLY (see oxo.h): the K-quant activation quantizer and the K-quant lane GEMVs
+// of the reference, restated per (lane, row) in the reference's float order.
+//
+// Blocks are ggml's (vendor/ggml-subset/generated/ggml-common.h:315-376): the GGUF file's bytes.
+// The reference repacks them into 8-row interleaved blocks (block_q*_Kx8) for its NEON kernels;
+// the repack moves bytes only, so every weight code, scale and min below is the same number.
+#include <math.h>
+#include <string.h>
+
+#include "oxo.h"
+
+namespace {
+
+constexpr int QK = 256;
+
+struct BQ8K {   // block_q8_K, ggml-common.h:371-375
+    float d;
+    int8_t qs[QK];
+    int16_t bsums[QK / 16];
+};
+static_assert(sizeof(BQ8K) == 292, "block_q8_K");
+
+// nearest_int (vendor/ggml-subset/generated/quants_base.c:5-11): round half to even through the
+// float add of 1.5 * 2^23
+int nearest_int(float fval) {
+    float val = fval + 12582912.f;
+    int i;
+    memcpy(&i, &val, sizeof(int));
+    return (i & 0x007fffff) - 0x00400000;
+}
+
+// get_scale_min_k4 (quants_base.c:50-57): the 6-bit scale and min of sub-block j of a Q4_K / Q5_K block
+void scale_min_k4(int j, const uint8_t *q, int *d, int *m) {
+    if (j < 4) {
+        *d = q[j] & 63;
+        *m = q[j + 4] & 63;
+    } else {
+        *d = (q[j + 4] & 0xF) | ((q[j - 4] >> 6) << 4);
+        *m = (q[j + 4] >> 4) | ((q[j - 0] >> 6) << 4);
+    }
+}
+
+// q3k_raw_scales (repack_subset.cpp:575-587): the 16 raw 6-bit scales of a Q3_K block (scale = raw - 32)
+void q3k_raw(const uint8_t *sc12, uint8_t raw[16]) {
+    const uint32_t kmask1 = 0x03030303, kmask2 = 0x0f0f0f0f;
+    uint32_t aux[4];
+    memcpy(aux, sc12, 12);
+    const uint32_t tmp = aux[2];
+    aux[2] = ((aux[0] >> 4) & kmask2) | (((tmp >> 4) & kmask1) << 4);
+    aux[3] = ((aux[1] >> 4) & kmask2) | (((tmp >> 6) & kmask1) << 4);
+    aux[0] = (aux[0] & kmask2) | (((tmp >> 0) & kmask1) << 4);
+    aux[1] = (aux[1] & kmask2) | (((tmp >> 2) & kmask1) << 4);
+    memcpy(raw, aux, 16);
+}
+
+// the 32-value sums of the q8_K bsums (the reference's vpaddq_s16 of the 16-value sums)
+int bsum32(const BQ8K &y, int j) { return (int16_t)(y.bsums[2 * j] + y.bsums[2 * j + 1]); }
+
+// Q4_K (oxe_vl_q4k.inc:1-7, ggml_gemv_q4_K_8x8_q8_K dotprod branch): per 64-weight step sb,
+//   acc = fma(d_w * d_x, f32(sc_lo * I_lo), acc); acc = fma(d_w * d_x, f32(sc_hi * I_hi), acc)
+// and once per block acc = acc - f32(sum_j min_j * bsum32_j) * (dmin_w * d_x), unfused (vmlsq_f32).
+float row_q4_K(const uint8_t *w, const BQ8K *y, int nb) {
+    float acc = 0.0f;
+    for (int b = 0; b < nb; b++, w += 144) {
+        const float dw = oxo_f16_to_f32((uint16_t)(w[0] | w[1] << 8));
+        const float dm = oxo_f16_to_f32((uint16_t)(w[2] | w[3] << 8));
+        const uint8_t *sc = w + 4, *qs = w + 16;
+        const float sbs = dw * y[b].d, sbm = dm * y[b].d;
+        int32_t bias = 0;
+        for (int sb = 0; sb < 4; sb++) {
+            int s_lo, m_lo, s_hi, m_hi;
+            scale_min_k4(2 * sb, sc, &s_lo, &m_lo);
+            scale_min_k4(2 * sb + 1, sc, &s_hi, &m_hi);
+            int32_t lo = 0, hi = 0;
+            for (int l = 0; l < 32; l++) {
+                lo += (qs[32 * sb + l] & 15) * y[b].qs[64 * sb + l];
+                hi += (qs[32 * sb + l] >> 4) * y[b].qs[64 * sb + 32 + l];
+            }
+            acc = fmaf(sbs, (float)(s_lo * lo), acc);
+            acc = fmaf(sbs, (float)(s_hi * hi), acc);
+            bias += m_lo * bsum32(y[b], 2 * sb) + m_hi * bsum32(y[b], 2 * sb + 1);
+        }
+        const float t = (float)bias * sbm;
+        acc = acc - t;
+    }
+    return acc;
+}
+
+// Q5_K (oxe_vl_q5k.inc:1-12, ggml_gemv_q5_K_8x8_q8_K): the 5th bit of a code is bit 2 sb (low
+// sub-block) or 2 sb + 1 (high) of qh[l]; per step sb: fma lo, fma hi, then
+// acc = acc - (dmin_w * d_x) * f32(min_lo * bsum_lo + min_hi * bsum_hi), unfused (vmlsq_f32).
+float row_q5_K(const uint8_t *w, const BQ8K *y, int nb) {
+    float acc = 0.0f;
+    for (int b = 0; b < nb; b++, w += 176) {
+        const float dw = oxo_f16_to_f32((uint16_t)(w[0] | w[1] << 8));
+        const float dm = oxo_f16_to_f32((uint16_t)(w[2] | w[3] << 8));
+        const uint8_t *sc = w + 4, *qh = w + 16, *qs = w + 48;
+        const float sbs = dw * y[b].d, sbm = dm * y[b].d;
+        for (int sb = 0; sb < 4; sb++) {
+            int s_lo, m_lo, s_hi, m_hi;
+            scale_min_k4(2 * sb, sc, &s_lo, &m_lo);
+            scale_min_k4(2 * sb + 1, sc, &s_hi, &m_hi);
+            int32_t lo = 0, hi = 0;
+            for (int l = 0; l < 32; l++) {
+                const int cl = (qs[32 * sb + l] & 15) | (((qh[l] >> (2 * sb)) & 1) << 4);
+                const int ch = (qs[32 * sb + l] >> 4) | (((qh[l] >> (2 * sb + 1)) & 1) << 4);
+                lo += cl * y[b].qs[64 * sb + l];
+                hi += ch * y[b].qs[64 * sb + 32 + l];
+            }
+            acc = fmaf(sbs, (float)(s_lo * lo), acc);
+            acc = fmaf(sbs, (float)(s_hi * hi), acc);
+            const int32_t bias = m_lo * bsum32(y[b], 2 * sb) + m_hi * bsum32(y[b], 2 * sb + 1);
+            const float t = sbm * (float)bias;
+            acc = acc - t;
+        }
+    }
+    return acc;
+}
+
+// Q6_K (oxe_vl_q6k.inc:1-8, ggml_gemv_q6_K_8x8_q8_K): I = sum over the 16 sub-blocks of
+// scale_i * (16 codes - 32) . q8, exact int32; per block acc = acc + f32(I) * (d_w * d_x), unfused
+// (vmlaq_f32, oxe_vl_q6k.inc:107-113).
+float row_q6_K(const uint8_t *w, const BQ8K *y, int nb) {
+    float acc = 0.0f;
+    for (int b = 0; b < nb; b++, w += 210) {
+        const uint8_t *ql = w, *qh = w + 128;
+        const int8_t *sc = (const int8_t *)(w + 192);
+        const float dw = oxo_f16_to_f32((uint16_t)(w[208] | w[209] << 8));
+        const float sbs = dw * y[b].d;
+        int32_t sub[16] = {0};
+        for (int n = 0; n < 2; n++) {
+            for (int l = 0; l < 32; l++) {
+                const int e = 128 * n + l;
+                const uint8_t lo = ql[64 * n + l], lo2 = ql[64 * n + 32 + l], h = qh[32 * n + l];
+                const int q1 = ((lo & 15) | ((h & 3) << 4)) - 32;
+                const int q2 = ((lo2 & 15) | (((h >> 2) & 3) << 4)) - 32;
+                const int q3 = ((lo >> 4) | (((h >> 4) & 3) << 4)) - 32;
+                const int q4 = ((lo2 >> 4) | (((h >> 6) & 3) << 4)) - 32;
+                sub[(e + 0) / 16] += q1 * y[b].qs[e + 0];
+                sub[(e + 32) / 16] += q2 * y[b].qs[e + 32];
+                sub[(e + 64) / 16] += q3 * y[b].qs[e + 64];
+                sub[(e + 96) / 16] += q4 * y[b].qs[e + 96];
+            }
+        }
+        int32_t I = 0;
+        for (int i = 0; i < 16; i++) I += sc[i] * sub[i];
+        const float t = (float)I * sbs;
+        acc = acc + t;
+    }
+    return acc;
+}
+
+// Q3_K (oxe_vl_q3k.inc:1-10, ggml_q3x8_dot_row_dotprod): code of element 128 n + 32 s + l =
+// ((qs[32 n + l] >> 2 s) & 3) - (bit 4 n + s of hmask[l] ? 0 : 4); isum = sum over the 16
+// sub-blocks of (raw_i - 32) * dot16_i; per block acc = fma(f32(isum), d_x * d_w, acc).
+float row_q3_K(const uint8_t *w, const BQ8K *y, int nb) {
+    float acc = 0.0f;
+    for (int b = 0; b < nb; b++, w += 110) {
+        const uint8_t *hm = w, *qs = w + 32;
+        uint8_t raw[16];
+        q3k_raw(w + 96, raw);
+        const float dw = oxo_f16_to_f32((uint16_t)(w[108] | w[109] << 8));
+        const float sbd = y[b].d * dw;
+        int32_t sub[16] = {0};
+        for (int n = 0; n < 2; n++)
+            for (int s = 0; s < 4; s++)
+                for (int l = 0; l < 32; l++) {
+                    const int e = 128 * n + 32 * s + l;
+                    const int q = ((qs[32 * n + l] >> (2 * s)) & 3) - (((hm[l] >> (4 * n + s)) & 1) ? 0 : 4);
+                    sub[e / 16] += q * y[b].qs[e];
+                }
+        int32_t isum = 0;
+        for (int i = 0; i < 16; i++) isum += (raw[i] - 32) * sub[i];
+        acc = fmaf((float)isum, sbd, acc);
+    }
+    return acc;
+}
+
+}  // namespace
+
+extern "C" {
+
+// quantize_row_q8_K_ref (vendor/ggml-subset/generated/quants_base.c:14-48; on ARM the reference's
+// quantize_row_q8_K is this function, ggml_subset.h:18-19)
+void oxo_quantize_row_q8_K(const float *x, void *vy, int64_t k) {
+    BQ8K *y = (BQ8K *)vy;
+    for (int64_t i = 0; i < k / QK; i++, x += QK) {
+        float max = 0, amax = 0;
+        for (int j = 0; j < QK; ++j) {
+            const float ax = fabsf(x[j]);
+            if (ax > amax) {
+                amax = ax;
+                max = x[j];
+            }
+        }
+        if (!amax) {
+            y[i].d = 0;
+            memset(y[i].qs, 0, QK);
+            memset(y[i].bsums, 0, sizeof(y[i].bsums));   // the reference leaves them as they were
+            continue;
+        }
+        const float iscale = -127.f / max;
+        for (int j = 0; j < QK; ++j) {
+            const float v = iscale * x[j];
+            const int q = nearest_int(v);
+            y[i].qs[j] = (int8_t)(q < 127 ? q : 127);
+        }
+        for (int j = 0; j < QK / 16; ++j) {
+            int sum = 0;
+            for (int ii = 0; ii < 16; ++ii) sum += y[i].qs[j * 16 + ii];
+            y[i].bsums[j] = (int16_t)sum;
+        }
+        y[i].d = 1 / iscale;
+    }
+}
+
+// oxe_vl_gemv (crates/kernels-sys/csrc/oxe_vl.inc:78-107) per lane: s[l*nr + r] = row r of w
+// (nb = k/256 blocks of the type, rows contiguous) . lane l of y (nb q8_K blocks per lane).
+// type 3 Q3_K, 4 Q4_K, 5 Q5_K, 6 Q6_K. Returns 1, or 0 (nothing written) for another type.
+int oxo_vl_gemv(int type, int64_t k, int64_t nr, int nl, const void *w, const void *y, float *s) {
+    const int nb = (int)(k / QK);
+    int bb;
+    float (*row)(const uint8_t *, const BQ8K *, int);
+    switch (type) {
+        case 3: bb = 110; row = row_q3_K; break;
+        case 4: bb = 144; row = row_q4_K; break;
+        case 5: bb = 176; row = row_q5_K; break;
+        case 6: bb = 210; row = row_q6_K; break;
+        default: return 0;
+    }
+#pragma omp parallel for schedule(static) if (nr * nl > 64)
+    for (int64_t r = 0; r < nr; r++)
+        for (int l = 0; l < nl; l++)
+            s[(int64_t)l * nr + r] = row((const uint8_t *)w + r * (int64_t)nb * bb, (const BQ8K *)y + (int64_t)l * nb, nb);
+    return 1;
+}
+
+}  // extern "C"

@@ -129,6 +129,8 @@ def lib():
             "oxo_driver_step_plain": (C.c_uint32, [C.c_void_p, C.c_uint32]),
             "oxo_driver_rewind": (C.c_int, [C.c_void_p, C.c_int]),
             "oxo_driver_stats": (None, [C.c_void_p, P(C.c_int64)]),
+            "oxo_quantize_row_q8_K": (None, [f32p, C.c_void_p, C.c_int64]),
+            "oxo_vl_gemv": (C.c_int, [C.c_int, C.c_int64, C.c_int64, C.c_int, C.c_void_p, C.c_void_p, f32p]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -153,6 +155,35 @@ def quantize_q8_0(x):
     for i in range(rows.shape[0]):
         lib().oxo_quantize_row_q8_0(ptr(rows[i], C.c_float), k, ptr(q[i], C.c_int8), ptr(d[i], C.c_uint16))
     return q.reshape(x.shape), d.reshape(x.shape[:-1] + (k // 32,))
+
+
+# ggml block_q8_K (ggml-common.h:371-375) and the K-quant block sizes (315-368)
+Q8K = np.dtype([("d", "<f4"), ("qs", "i1", (256,)), ("bsums", "<i2", (16,))])
+KQ_BYTES = {3: 110, 4: 144, 5: 176, 6: 210}
+
+
+def quantize_q8_K(x):
+    """quantize_row_q8_K_ref per row: float rows [..., k] -> uint8 [..., k/256 * 292]"""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    k = x.shape[-1]
+    rows = x.reshape(-1, k)
+    y = np.zeros((rows.shape[0], k // 256 * 292), np.uint8)
+    for i in range(rows.shape[0]):
+        lib().oxo_quantize_row_q8_K(ptr(rows[i], C.c_float), y[i].ctypes.data_as(C.c_void_p), k)
+    return y.reshape(x.shape[:-1] + (k // 256 * 292,))
+
+
+def vl_gemv(ty, w, k, y):
+    """oxe_vl_gemv per lane: w uint8 [nr][k/256 * block bytes] (ggml blocks), y uint8 [nl][k/256 * 292]
+    -> f32 [nl][nr]"""
+    w = np.ascontiguousarray(w, np.uint8)
+    y = np.ascontiguousarray(y, np.uint8)
+    nr, nl = w.shape[0], y.shape[0]
+    s = np.empty((nl, nr), np.float32)
+    rc = lib().oxo_vl_gemv(ty, k, nr, nl, w.ctypes.data_as(C.c_void_p), y.ctypes.data_as(C.c_void_p), ptr(s, C.c_float))
+    if rc != 1:
+        raise ValueError(f"vl_gemv: type {ty} not handled")
+    return s
 
 
 def gemv_q8_0(wq, wd, xq, xd, want_isum=False):

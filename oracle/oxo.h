@@ -37,6 +37,13 @@ void oxo_dequantize_row_q8_0(const int8_t *q, const uint16_t *d, int64_t k, floa
 void oxo_gemv_q8_0(int64_t k, int64_t nr, int nl, const int8_t *wq, const uint16_t *wd,
                    const int8_t *xq, const uint16_t *xd, float *y, int32_t *isum);
 
+// ---- K-quants (kquants.cpp): quantize_row_q8_K_ref (quants_base.c:14-48) into ggml block_q8_K
+// (float d, int8 qs[256], int16 bsums[16]; 292 bytes); the lane GEMV contract of oxe_vl_gemv
+// (crates/kernels-sys/csrc/oxe_vl.inc:78-107, oxe_vl_q{3,4,5,6}k.inc) per lane over ggml blocks:
+// s[l*nr + r] = W[r] . y[l]; type 3 Q3_K, 4 Q4_K, 5 Q5_K, 6 Q6_K; returns 0 for another type.
+void oxo_quantize_row_q8_K(const float *x, void *y, int64_t k);
+int  oxo_vl_gemv(int type, int64_t k, int64_t nr, int nl, const void *w, const void *y, float *s);
+
 // ---- f32 / f16 vector helpers (vendor/ggml-subset/generated/upstream/src/ggml-cpu/vec.{h,cpp})
 float oxo_vec_dot_f32(int n, const float *x, const float *y);            // vec.cpp:104-125
 float oxo_vec_dot_f16(int n, const uint16_t *x, const uint16_t *y);      // vec.cpp:345-371

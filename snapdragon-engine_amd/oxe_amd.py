@@ -33,6 +33,8 @@ def lib():
             "oxe_hip_repack_q8_0": (i32, [vp, i64, i64, vp, vp, vp]),
             "oxe_hip_gemm_q8_0": (i32, [i64, i64, i64, vp, vp, vp, vp, vp, i64, vp]),
             "oxe_hip_eval_unary": (i32, [i32, C.c_uint32, i64, i64, vp, vp]),
+            "oxe_hip_quantize_row_q8_K": (i32, [vp, i64, i64, vp, vp]),
+            "oxe_hip_vl_gemv": (i32, [i32, i64, i64, i32, vp, vp, vp, vp]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -148,6 +150,32 @@ def repack_q8_0(blocks, k):
     d = torch.empty((nrows, k // 32), dtype=torch.int16, device=blocks.device)
     check(lib().oxe_hip_repack_q8_0(_p(blocks), nrows, k, _p(q), _p(d), _stream()), "repack_q8_0")
     return q, d
+
+
+def quantize_q8_K(x):
+    """x: float32 [..., k] on the GPU (k a multiple of 256) -> ggml block_q8_K bytes, uint8
+    [..., k/256 * 292] (quantize_row_q8_K)"""
+    import torch
+    x = x.contiguous()
+    k = x.shape[-1]
+    nrows = x.numel() // k
+    y = torch.empty(x.shape[:-1] + (k // 256 * 292,), dtype=torch.uint8, device=x.device)
+    check(lib().oxe_hip_quantize_row_q8_K(_p(x), k, nrows, _p(y), _stream()), "quantize_q8_K")
+    return y
+
+
+def vl_gemv(ty, w, k, y, s=None):
+    """K-quant lane GEMV (oxe_vl_gemv): w uint8 [nr, k/256 * block bytes] (ggml blocks of type ty:
+    3 Q3_K, 4 Q4_K, 5 Q5_K, 6 Q6_K), y uint8 [nl, k/256 * 292] (q8_K lanes) -> float32 [nl, nr];
+    None when the type / shape is not handled (the reference's 0 return)"""
+    import torch
+    nr, nl = w.shape[0], y.shape[0]
+    if s is None:
+        s = torch.empty((nl, nr), dtype=torch.float32, device=w.device)
+    rc = lib().oxe_hip_vl_gemv(ty, k, nr, nl, _p(w), _p(y), _p(s), _stream())
+    if rc < 0:
+        raise RuntimeError(f"vl_gemv failed with status {rc}")
+    return s if rc == 1 else None
 
 
 def eval_unary(fn, start, n, stride, y):
