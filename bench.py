@@ -192,6 +192,104 @@ def bench_prefill(args):
     print(json.dumps(result), flush=True)
 
 
+KQ_BYTES = {3: 110, 4: 144, 5: 176, 6: 210}
+KQ_D_OFF = {3: (108,), 4: (0, 2), 5: (0, 2), 6: (208,)}   # fp16 d (and dmin) inside a block
+
+
+def kq_weights(torch, ty, rows, k, seed):
+    """random K-quant blocks on the device: random code / scale bytes, fp16 d (dmin) in [1e-3, 1e-2]"""
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    nb, bb = k // 256, KQ_BYTES[ty]
+    w = torch.randint(0, 256, (rows, nb, bb), dtype=torch.uint8, device="cuda", generator=g)
+    for off in KQ_D_OFF[ty]:
+        d = (torch.rand((rows, nb), device="cuda", generator=g) * 9e-3 + 1e-3).half().view(torch.int16)
+        w[:, :, off] = (d & 0xFF).to(torch.uint8)
+        w[:, :, off + 1] = ((d >> 8) & 0xFF).to(torch.uint8)
+    return w.view(rows, nb * bb)
+
+
+def cpu_kquant_baseline(seconds, ty, k, rows_total):
+    """the oracle's lane GEMV (OpenMP over rows) on this host: 2 lanes over a bounded row sample"""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import numpy as np
+    import oracle as O
+    O.build()
+    rng = np.random.default_rng(0)
+    rows = 4096
+    w = rng.integers(0, 256, size=(rows, k // 256 * KQ_BYTES[ty]), dtype=np.uint8)
+    for off in KQ_D_OFF[ty]:
+        h = rng.uniform(1e-3, 1e-2, size=(rows, k // 256)).astype(np.float16).view(np.uint16)
+        v = w.reshape(rows, k // 256, KQ_BYTES[ty])
+        v[:, :, off] = h & 0xFF
+        v[:, :, off + 1] = h >> 8
+    y = O.quantize_q8_K(rng.standard_normal((2, k)).astype(np.float32))
+    t0, n = time.time(), 0
+    while time.time() - t0 < seconds or n == 0:
+        O.vl_gemv(ty, w, k, y)
+        n += rows
+    dt = time.time() - t0
+    bytes_per_row = k // 256 * KQ_BYTES[ty]
+    cores = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    return {"value": round(n * bytes_per_row / dt / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": "port",
+            "sample": f"{n} rows ({n / rows_total:.2f} x the full matrix) of the same type and k, 2 lanes, "
+                      f"in {dt:.1f} s"}
+
+
+def bench_kquant(args):
+    """The K-quant lane GEMV (oxe_hip_vl_gemv) on the real Qwen3.6 file's shapes (its header fixture):
+    the Q6_K LM head [248320 x 2048] (the dominant single matrix, 417 MB, beyond the 256 MB
+    memory-side cache) with the 2 verify lanes; the Q4_K expert gate / up and Q5_K expert down of a
+    16-expert union, rotated over enough copies to stream from HBM."""
+    import torch
+    import oxe_amd as A
+    V36 = 248320
+
+    def timed(ty, k, rows, copies, reps):
+        ws = [kq_weights(torch, ty, rows, k, seed=c) for c in range(copies)]
+        x = torch.randn((2, k), device="cuda")
+        y = A.quantize_q8_K(x)
+        s = torch.empty((2, rows), device="cuda")
+        for w in ws:
+            assert A.vl_gemv(ty, w, k, y, s) is not None
+        torch.cuda.synchronize()
+        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        ev0.record()
+        for i in range(reps):
+            A.vl_gemv(ty, ws[i % copies], k, y, s)
+        ev1.record()
+        torch.cuda.synchronize()
+        us = ev0.elapsed_time(ev1) * 1e3 / reps
+        nbytes = rows * (k // 256) * KQ_BYTES[ty] + 2 * (k // 256) * 292 + 2 * rows * 4
+        del ws
+        return us, nbytes
+
+    parts = {}
+    for name, ty, k, rows, copies in (("lm_head_q6_K", 6, 2048, V36, 1),
+                                      ("experts_gate_up_q4_K", 4, 2048, 16 * 1024, 24),
+                                      ("experts_down_q5_K", 5, 512, 16 * 2048, 40)):
+        us, nbytes = timed(ty, k, rows, copies, max(args.steps, 4))
+        parts[name] = {"us": round(us, 2), "bytes": nbytes, "GBs": round(nbytes / (us * 1e-6) / 1e9, 1),
+                       "type": ty, "k": k, "rows": rows}
+    head = parts["lm_head_q6_K"]
+    result = {
+        "metric": "K-quant lane GEMV GB/s (Qwen3.6 Q6_K LM head, 2 lanes)",
+        "value": head["GBs"], "unit": "GB/s", "n_gpus": 1, "steps": max(args.steps, 4), "warmup": 1,
+        "ms_per_step": round(head["us"] / 1e3, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int (K-quant codes x q8_K codes, int32 sub-block dots) then the reference's fp32 chain",
+        "data": "synthetic: random K-quant blocks (fp16 scales in [1e-3, 1e-2]), random activations",
+        "config": {"workload": "oxe_vl_gemv on the Qwen3.6 file's tensor shapes and types "
+                               "(tests/golden/gguf_header_qwen36.json): output.weight Q6_K [248320 x 2048]",
+                   "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "achieved": head["GBs"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(head["GBs"] / PEAK_HBM_GBS, 4), "traffic": None,
+                     "kernel": "vl_gemv_kernel<6>", "bytes_per_launch": head["bytes"]},
+        "breakdown": parts,
+    }
+    result["cpu_baseline"] = None if args.no_cpu else cpu_kquant_baseline(args.cpu_seconds, 6, 2048, V36)
+    print(json.dumps(result), flush=True)
+
+
 def calibrate_copy(torch, mib=1024, reps=4):
     """A plain copy of `mib` MiB, `reps` times: under rocprofv3 --pmc its FETCH_SIZE / WRITE_SIZE
     per dispatch calibrate the byte counters (bytes moved are known exactly)."""
@@ -234,6 +332,8 @@ def main():
                     help="BASELINE config 5 instead: batched prefill of --prefill-tokens prompt tokens "
                          "(--steps timed prefills after --warmup untimed ones)")
     ap.add_argument("--prefill-tokens", type=int, default=2048)
+    ap.add_argument("--kquant", action="store_true",
+                    help="the K-quant lane GEMV on the Qwen3.6 shapes instead (--steps timed launches each)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build runs the whole MTP-1 step on a single MI355X "
@@ -242,6 +342,11 @@ def main():
     import torch
     if args.calibrate_copy:
         calibrate_copy(torch)
+        return
+    if args.kquant:
+        if args.steps == ap.get_default("steps"):
+            args.steps = 40
+        bench_kquant(args)
         return
     if args.prefill:
         if args.steps == ap.get_default("steps"):

@@ -3,12 +3,11 @@
 // oxe_vl.inc:78-107, types 3..6), bit for bit per (lane, row).
 //
 // Weights are the GGUF file's ggml blocks (no repack: the reference's 8-row interleave only serves
-// its NEON SMMLA tiles). A workgroup of 256 threads owns rpw rows and walks k in chunks of kch
-// blocks: the chunk's weight bytes and the lanes' q8_K blocks are staged in LDS with coalesced
-// dword loads; thread (row, unit) forms the exact integers of one half block (128 weights) for
-// every lane with v_dot4_i32_i8 (codes repacked 4 per dword); then one thread per (row, lane)
-// runs the reference's float chain over the chunk's blocks in order. Integer parts are exact, so
-// only the chain (the order and fusion the reference documents per type) fixes the bits.
+// its NEON SMMLA tiles). Integer parts are exact (codes repacked 4 per dword into v_dot4_i32_i8),
+// so only the float chain per (lane, row), in the order and fusion the reference documents per
+// type, fixes the bits; the kernel layout is free otherwise (see vl_gemv_kernel).
+#include <algorithm>
+
 #include "oxe_common.h"
 
 namespace oxe {
@@ -17,8 +16,6 @@ namespace kq {
 constexpr int QK = 256;
 constexpr int Q8K_BYTES = 292;   // block_q8_K: float d, int8 qs[256], int16 bsums[16]
 constexpr int Q8K_QS = 4, Q8K_BS = 260;
-constexpr int NT = 256;          // threads per workgroup
-constexpr int KCH = 8;           // blocks per chunk (at most)
 constexpr int RES = 6;           // ints per (unit, lane)
 constexpr int MAX_LANES = 4;
 
@@ -88,7 +85,8 @@ __global__ __launch_bounds__(256) void quant_q8_K_kernel(const float *__restrict
     if (lane == 0) *(float *)yb = am != 0.0f ? 1 / iscale : 0.0f;
 }
 
-// ---- integers of one half block (unit h: weights 128 h .. 128 h + 127) for one lane -------------
+// ---- integers of one half block (unit h: weights 128 h .. 128 h + 127), every lane ---------------
+// yb: the lanes' q8_K blocks of this block position, ystride bytes apart; out[l * RES + ...]
 
 // get_scale_min_k4 (quants_base.c:50-57)
 OXE_DEV void scale_min_k4(int j, const uint8_t *q, int &d, int &m) {
@@ -103,16 +101,20 @@ OXE_DEV void scale_min_k4(int j, const uint8_t *q, int &d, int &m) {
 
 // Q4_K / Q5_K: for the unit's two 64-weight steps g: sc_lo * I_lo, sc_hi * I_hi (out[0..3]); Q4_K:
 // out[4] = the unit's part of sum min_j * bsum32_j; Q5_K: out[4 + g'] = that sum per step
-template <int TY>
-OXE_DEV void unit_k45(const uint8_t *wb, const uint8_t *yb, int h, int *out) {
+template <int TY, int NL>
+OXE_DEV void unit_k45(const uint8_t *wb, const uint8_t *yb, int ystride, int h, int *out) {
     const uint8_t *sc = wb + 4;
     const uint8_t *qs = wb + (TY == 4 ? 16 : 48);
     const uint8_t *qh = wb + 16;
-    const uint8_t *yq = yb + Q8K_QS;
-    int bias4 = 0;
+    int bias4[NL];
+#pragma unroll
+    for (int l = 0; l < NL; l++) bias4[l] = 0;
+#pragma unroll
     for (int gg = 0; gg < 2; gg++) {
         const int g = 2 * h + gg;
-        int lo = 0, hi = 0;
+        int lo[NL], hi[NL];
+#pragma unroll
+        for (int l = 0; l < NL; l++) lo[l] = hi[l] = 0;
 #pragma unroll
         for (int i = 0; i < 8; i++) {
             const uint32_t w = ld32(qs + 32 * g + 4 * i);
@@ -122,28 +124,41 @@ OXE_DEV void unit_k45(const uint8_t *wb, const uint8_t *yb, int h, int *out) {
                 cl |= ((hb >> (2 * g)) & 0x01010101u) << 4;
                 ch |= ((hb >> (2 * g + 1)) & 0x01010101u) << 4;
             }
-            lo = dot4(cl, ld32(yq + 64 * g + 4 * i), lo);
-            hi = dot4(ch, ld32(yq + 64 * g + 32 + 4 * i), hi);
+#pragma unroll
+            for (int l = 0; l < NL; l++) {
+                const uint8_t *yq = yb + l * ystride + Q8K_QS;
+                lo[l] = dot4(cl, ld32(yq + 64 * g + 4 * i), lo[l]);
+                hi[l] = dot4(ch, ld32(yq + 64 * g + 32 + 4 * i), hi[l]);
+            }
         }
         int s_lo, m_lo, s_hi, m_hi;
         scale_min_k4(2 * g, sc, s_lo, m_lo);
         scale_min_k4(2 * g + 1, sc, s_hi, m_hi);
-        out[2 * gg] = s_lo * lo;
-        out[2 * gg + 1] = s_hi * hi;
-        const int bias = m_lo * (bsum16(yb, 4 * g) + bsum16(yb, 4 * g + 1)) +
-                         m_hi * (bsum16(yb, 4 * g + 2) + bsum16(yb, 4 * g + 3));
-        if (TY == 5) out[4 + gg] = bias;
-        bias4 += bias;
+#pragma unroll
+        for (int l = 0; l < NL; l++) {
+            const uint8_t *y = yb + l * ystride;
+            out[l * RES + 2 * gg] = s_lo * lo[l];
+            out[l * RES + 2 * gg + 1] = s_hi * hi[l];
+            const int bias = m_lo * (bsum16(y, 4 * g) + bsum16(y, 4 * g + 1)) + m_hi * (bsum16(y, 4 * g + 2) + bsum16(y, 4 * g + 3));
+            if (TY == 5) out[l * RES + 4 + gg] = bias;
+            bias4[l] += bias;
+        }
     }
-    if (TY == 4) out[4] = bias4;
+    if (TY == 4)
+#pragma unroll
+        for (int l = 0; l < NL; l++) out[l * RES + 4] = bias4[l];
 }
 
 // Q6_K: the unit's part of I = sum_i scale_i * (16 codes - 32) . q8 (the -32 through the q8 sums)
-OXE_DEV void unit_q6(const uint8_t *wb, const uint8_t *yb, int n, int *out) {
+template <int NL>
+OXE_DEV void unit_q6(const uint8_t *wb, const uint8_t *yb, int ystride, int n, int *out) {
     const uint8_t *ql = wb + 64 * n, *qh = wb + 128 + 32 * n;
     const int8_t *sc = (const int8_t *)(wb + 192);
-    const uint8_t *yq = yb + Q8K_QS + 128 * n;
-    int d[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    int d[NL][8];
+#pragma unroll
+    for (int l = 0; l < NL; l++)
+#pragma unroll
+        for (int i = 0; i < 8; i++) d[l][i] = 0;
 #pragma unroll
     for (int i = 0; i < 8; i++) {
         const uint32_t a = ld32h(ql + 4 * i), a2 = ld32h(ql + 32 + 4 * i), hb = ld32h(qh + 4 * i);
@@ -152,15 +167,22 @@ OXE_DEV void unit_q6(const uint8_t *wb, const uint8_t *yb, int n, int *out) {
         const uint32_t c2 = ((a >> 4) & 0x0F0F0F0Fu) | (((hb >> 4) & 0x03030303u) << 4);
         const uint32_t c3 = ((a2 >> 4) & 0x0F0F0F0Fu) | (((hb >> 6) & 0x03030303u) << 4);
         const int s = i >> 2;   // which 16 of the 32
-        d[0 + s] = dot4(c0, ld32(yq + 4 * i), d[0 + s]);
-        d[2 + s] = dot4(c1, ld32(yq + 32 + 4 * i), d[2 + s]);
-        d[4 + s] = dot4(c2, ld32(yq + 64 + 4 * i), d[4 + s]);
-        d[6 + s] = dot4(c3, ld32(yq + 96 + 4 * i), d[6 + s]);
-    }
-    int I = 0;
 #pragma unroll
-    for (int i = 0; i < 8; i++) I += (int)sc[8 * n + i] * (d[i] - 32 * bsum16(yb, 8 * n + i));
-    out[0] = I;
+        for (int l = 0; l < NL; l++) {
+            const uint8_t *yq = yb + l * ystride + Q8K_QS + 128 * n;
+            d[l][0 + s] = dot4(c0, ld32(yq + 4 * i), d[l][0 + s]);
+            d[l][2 + s] = dot4(c1, ld32(yq + 32 + 4 * i), d[l][2 + s]);
+            d[l][4 + s] = dot4(c2, ld32(yq + 64 + 4 * i), d[l][4 + s]);
+            d[l][6 + s] = dot4(c3, ld32(yq + 96 + 4 * i), d[l][6 + s]);
+        }
+    }
+#pragma unroll
+    for (int l = 0; l < NL; l++) {
+        int I = 0;
+#pragma unroll
+        for (int i = 0; i < 8; i++) I += (int)sc[8 * n + i] * (d[l][i] - 32 * bsum16(yb + l * ystride, 8 * n + i));
+        out[l * RES] = I;
+    }
 }
 
 // q3k_raw_scales (repack_subset.cpp:575-587): raw 6-bit scale i of a Q3_K block
@@ -171,10 +193,14 @@ OXE_DEV int q3_raw(const uint8_t *s12, int i) {
 }
 
 // Q3_K: the unit's part of isum = sum_i (raw_i - 32) * dot16_i, codes (low 2 bits | hmask bit << 2) - 4
-OXE_DEV void unit_q3(const uint8_t *wb, const uint8_t *yb, int n, int *out) {
+template <int NL>
+OXE_DEV void unit_q3(const uint8_t *wb, const uint8_t *yb, int ystride, int n, int *out) {
     const uint8_t *hm = wb, *qs = wb + 32 + 32 * n;
-    const uint8_t *yq = yb + Q8K_QS + 128 * n;
-    int d[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    int d[NL][8];
+#pragma unroll
+    for (int l = 0; l < NL; l++)
+#pragma unroll
+        for (int i = 0; i < 8; i++) d[l][i] = 0;
 #pragma unroll
     for (int i = 0; i < 8; i++) {
         const uint32_t qw = ld32h(qs + 4 * i), hw = ld32h(hm + 4 * i);
@@ -182,20 +208,30 @@ OXE_DEV void unit_q3(const uint8_t *wb, const uint8_t *yb, int n, int *out) {
 #pragma unroll
         for (int s = 0; s < 4; s++) {
             const uint32_t c = ((qw >> (2 * s)) & 0x03030303u) | (((hw >> (4 * n + s)) & 0x01010101u) << 2);
-            d[2 * s + half] = dot4(c, ld32(yq + 32 * s + 4 * i), d[2 * s + half]);
+#pragma unroll
+            for (int l = 0; l < NL; l++) {
+                const uint8_t *yq = yb + l * ystride + Q8K_QS + 128 * n;
+                d[l][2 * s + half] = dot4(c, ld32(yq + 32 * s + 4 * i), d[l][2 * s + half]);
+            }
         }
     }
-    int I = 0;
+    int sc[8];
 #pragma unroll
-    for (int i = 0; i < 8; i++) I += (q3_raw(wb + 96, 8 * n + i) - 32) * (d[i] - 4 * bsum16(yb, 8 * n + i));
-    out[0] = I;
+    for (int i = 0; i < 8; i++) sc[i] = q3_raw(wb + 96, 8 * n + i) - 32;
+#pragma unroll
+    for (int l = 0; l < NL; l++) {
+        int I = 0;
+#pragma unroll
+        for (int i = 0; i < 8; i++) I += sc[i] * (d[l][i] - 4 * bsum16(yb + l * ystride, 8 * n + i));
+        out[l * RES] = I;
+    }
 }
 
-template <int TY>
-OXE_DEV void unit(const uint8_t *wb, const uint8_t *yb, int h, int *out) {
-    if (TY == 4 || TY == 5) unit_k45<TY>(wb, yb, h, out);
-    else if (TY == 6) unit_q6(wb, yb, h, out);
-    else unit_q3(wb, yb, h, out);
+template <int TY, int NL>
+OXE_DEV void unit(const uint8_t *wb, const uint8_t *yb, int ystride, int h, int *out) {
+    if (TY == 4 || TY == 5) unit_k45<TY, NL>(wb, yb, ystride, h, out);
+    else if (TY == 6) unit_q6<NL>(wb, yb, ystride, h, out);
+    else unit_q3<NL>(wb, yb, ystride, h, out);
 }
 
 // ---- the reference's float chain over one block (units r0: weights 0..127, r1: 128..255) ---------
@@ -232,78 +268,120 @@ OXE_DEV float chain(float acc, const uint8_t *wb, const uint8_t *yb, const int *
 }
 
 // ---- the lane GEMV --------------------------------------------------------------------------------
-// s[l * nr + r] = W[r] . y[l]; w: nr rows of nb blocks; y: nl lanes of nb q8_K blocks. kch blocks
-// per chunk (a power of two; every chunk's byte count and offset a multiple of 4), rpw = NT / (2 kch)
-// rows per workgroup, thread (ri, u): row ri, unit u = half u % 2 of the chunk's block u / 2.
-template <int TY>
-__global__ __launch_bounds__(NT) void vl_gemv_kernel(const uint8_t *__restrict__ w, int nb, int64_t nr,
-                                                     const uint8_t *__restrict__ y, int nl, float *__restrict__ s,
-                                                     int kch) {
+// s[l * nr + r] = W[r] . y[l]; w: nr rows of nb blocks (row bytes a multiple of 4, w 16-byte
+// aligned); y: NL lanes of nb q8_K blocks. One wave per workgroup, persistent over groups of 4 rows
+// (16 threads per row). Per group: the 4 rows' bytes (contiguous) go to LDS with 16-byte loads,
+// the first PF x 1 KiB of them loaded into registers one group ahead; then per chunk of up to 8
+// blocks thread (row ri, unit u) forms half block u % 2 of block u / 2 for every lane, and threads
+// u < NL of each row run lane u's chain over the chunk's blocks in order.
+constexpr int GR = 4;     // rows per group
+constexpr int PF = 8;     // prefetched 16-byte pieces per thread
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));   // a plain vector (HIP's uint4 is a union
+                                                              // type that keeps arrays of it in scratch)
+
+__host__ __device__ inline int align16(int n) { return (n + 15) / 16 * 16; }
+
+// the first PF x 1 KiB of group g's bytes into registers (16-byte loads)
+OXE_DEV void pf_load(u32x4 (&pf)[PF], const uint8_t *w, int64_t g, int64_t nr, int row_bytes, int t) {
+    const u32x4 *src = (const u32x4 *)(w + g * GR * row_bytes);
+    const int n16 = (int)(min((int64_t)GR, nr - g * GR) * row_bytes) / 16;
+#pragma unroll
+    for (int j = 0; j < PF; j++)
+        if (t + 64 * j < n16) pf[j] = src[t + 64 * j];
+}
+
+// one group of 4 rows: its prefetched bytes (pf) and the rest to LDS, pf refilled with group
+// g_next, then the units and the chains
+template <int TY, int NL>
+OXE_DEV void vl_group(u32x4 (&pf)[PF], int64_t g, int64_t g_next, const uint8_t *__restrict__ w, int nb, int64_t nr,
+                      float *__restrict__ s, uint8_t *wl, const uint8_t *yl, int *res) {
     constexpr int BB = BT<TY>::B;
-    extern __shared__ __align__(16) uint8_t lds[];
-    const int U = 2 * kch, rpw = NT / U;
-    uint8_t *wl = lds;                                         // [rpw][kch * BB]
-    uint8_t *yl = lds + (rpw * kch * BB + 15) / 16 * 16;       // [nl][kch][292]
-    int *res = (int *)(yl + (nl * kch * Q8K_BYTES + 15) / 16 * 16);   // [NT][MAX_LANES][RES]
-    const int t = threadIdx.x, ri = t / U, u = t % U;
-    const int64_t row0 = (int64_t)blockIdx.x * rpw, r = row0 + ri;
-    const int64_t row_bytes = (int64_t)nb * BB;
-    float acc[2] = {0.0f, 0.0f};
-    for (int b0 = 0; b0 < nb; b0 += kch) {
-        const int kc = min(kch, nb - b0);
-        const int seg = kc * BB / 4;
-        for (int i = t; i < rpw * seg; i += NT) {
-            const int rr = i / seg, o = i - rr * seg;
-            if (row0 + rr < nr)
-                ((uint32_t *)(wl + rr * kch * BB))[o] = ((const uint32_t *)(w + (row0 + rr) * row_bytes + (int64_t)b0 * BB))[o];
-        }
-        const int yseg = kc * Q8K_BYTES / 4;
-        for (int i = t; i < nl * yseg; i += NT) {
-            const int l = i / yseg, o = i - l * yseg;
-            ((uint32_t *)(yl + l * kch * Q8K_BYTES))[o] = ((const uint32_t *)(y + ((int64_t)l * nb + b0) * Q8K_BYTES))[o];
-        }
+    constexpr int RS = NL * RES + 1;   // odd per-thread stride: no bank conflicts between threads
+    const int row_bytes = nb * BB, ystride = nb * Q8K_BYTES;
+    const int t = threadIdx.x, ri = t >> 4, u = t & 15;
+    const int64_t ngroups = (nr + GR - 1) / GR;
+    const int sp = (int)(min((int64_t)GR, nr - g * GR) * row_bytes), n16 = sp / 16;
+    const u32x4 *src = (const u32x4 *)(w + g * GR * row_bytes);
+    __syncthreads();   // the previous group's LDS reads are done
+#pragma unroll
+    for (int j = 0; j < PF; j++)
+        if (t + 64 * j < n16) ((u32x4 *)wl)[t + 64 * j] = pf[j];
+    for (int i = t + 64 * PF; i < n16; i += 64) ((u32x4 *)wl)[i] = src[i];
+    for (int i = n16 * 4 + t; i < sp / 4; i += 64) ((uint32_t *)wl)[i] = ((const uint32_t *)src)[i];   // tail
+    __syncthreads();
+    if (g_next < ngroups) pf_load(pf, w, g_next, nr, row_bytes, t);   // in flight while this group computes
+    const int64_t r = g * GR + ri;
+    const bool live = r < nr;
+    float acc = 0.0f;
+    for (int b0 = 0; b0 < nb; b0 += 8) {
+        const int kc = min(8, nb - b0);
+        const int bi = b0 + (u >> 1);
+        if ((u >> 1) < kc && live)
+            unit<TY, NL>(wl + ri * row_bytes + bi * BB, yl + bi * Q8K_BYTES, ystride, u & 1, res + t * RS);
         __syncthreads();
-        const int bi = u >> 1, h = u & 1;
-        if (bi < kc && ri < rpw && r < nr)
-            for (int l = 0; l < nl; l++)
-                unit<TY>(wl + ri * kch * BB + bi * BB, yl + (l * kch + bi) * Q8K_BYTES, h, res + (t * MAX_LANES + l) * RES);
-        __syncthreads();
-        if (ri < rpw && r < nr)
-            for (int j = 0; j < 2; j++) {
-                const int l = u + j * U;
-                if (l >= nl) continue;
-                for (int b = 0; b < kc; b++) {
-                    const int *r0 = res + ((ri * U + 2 * b) * MAX_LANES + l) * RES;
-                    const int *r1 = res + ((ri * U + 2 * b + 1) * MAX_LANES + l) * RES;
-                    acc[j] = chain<TY>(acc[j], wl + ri * kch * BB + b * BB, yl + (l * kch + b) * Q8K_BYTES, r0, r1);
-                }
+        if (u < NL && live)
+            for (int b = 0; b < kc; b++) {
+                const int *r0 = res + (ri * 16 + 2 * b) * RS + u * RES;
+                const int *r1 = res + (ri * 16 + 2 * b + 1) * RS + u * RES;
+                acc = chain<TY>(acc, wl + ri * row_bytes + (b0 + b) * BB, yl + u * ystride + (b0 + b) * Q8K_BYTES, r0, r1);
             }
         __syncthreads();
     }
-    if (ri < rpw && r < nr)
-        for (int j = 0; j < 2; j++) {
-            const int l = u + j * U;
-            if (l < nl) s[(int64_t)l * nr + r] = acc[j];
-        }
+    if (u < NL && live) s[(int64_t)u * nr + r] = acc;
 }
 
-size_t vl_gemv_lds(int bb, int kch, int nl) {
-    const int rpw = NT / (2 * kch);
-    return (size_t)(rpw * kch * bb + 15) / 16 * 16 + (size_t)(nl * kch * Q8K_BYTES + 15) / 16 * 16 +
-           (size_t)NT * MAX_LANES * RES * 4;
+template <int TY, int NL>
+__global__ __launch_bounds__(64) void vl_gemv_kernel(const uint8_t *__restrict__ w, int nb, int64_t nr,
+                                                     const uint8_t *__restrict__ y, float *__restrict__ s) {
+    constexpr int BB = BT<TY>::B;
+    extern __shared__ __align__(16) uint8_t lds[];
+    const int row_bytes = nb * BB, ystride = nb * Q8K_BYTES;
+    uint8_t *wl = lds;                                           // [GR][row_bytes]
+    uint8_t *yl = lds + align16(GR * row_bytes);                 // [NL][nb][292]
+    int *res = (int *)(yl + align16(NL * ystride));              // [64][NL * RES + 1]
+    const int t = threadIdx.x;
+    const int64_t ngroups = (nr + GR - 1) / GR, G = gridDim.x;
+    for (int i = t; i < NL * ystride / 4; i += 64) ((uint32_t *)yl)[i] = ((const uint32_t *)y)[i];
+    // the register buffer holds the next group's first bytes (fixed indices only: it stays in
+    // registers; a second buffer two groups ahead measured no faster)
+    u32x4 pf[PF];
+    if ((int64_t)blockIdx.x < ngroups) pf_load(pf, w, blockIdx.x, nr, row_bytes, t);
+    for (int64_t g = blockIdx.x; g < ngroups; g += G) vl_group<TY, NL>(pf, g, g + G, w, nb, nr, s, wl, yl, res);
+}
+
+size_t vl_gemv_lds(int bb, int nb, int nl) {
+    return (size_t)align16(GR * nb * bb) + (size_t)align16(nl * nb * Q8K_BYTES) + (size_t)64 * (nl * RES + 1) * 4;
+}
+
+template <int TY, int NL>
+int vl_gemv_launch(const uint8_t *w, int nb, int64_t nr, const uint8_t *y, float *s, hipStream_t st) {
+    constexpr int BB = BT<TY>::B;
+    const size_t lds = vl_gemv_lds(BB, nb, NL);
+    static bool attr = false;   // above 64 KiB of LDS the kernel needs the attribute (160 KiB per CU)
+    if (lds > 65536 && !attr) {
+        if (hipFuncSetAttribute((const void *)vl_gemv_kernel<TY, NL>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                (int)lds) != hipSuccess)
+            return -2;
+        attr = true;
+    }
+    int dev = 0, ncu = 256;
+    (void)hipGetDevice(&dev);
+    (void)hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev);
+    const int per_cu = (int)std::max<size_t>(1, std::min<size_t>(16, (160 * 1024) / lds));
+    const int64_t ngroups = (nr + GR - 1) / GR;
+    const int64_t grid = std::min<int64_t>(ngroups, (int64_t)ncu * per_cu);
+    hipLaunchKernelGGL((vl_gemv_kernel<TY, NL>), dim3((unsigned)grid), dim3(64), lds, st, w, nb, nr, y, s);
+    return hipGetLastError() == hipSuccess ? 1 : -2;
 }
 
 template <int TY>
-int vl_gemv_launch(const uint8_t *w, int nb, int64_t nr, const uint8_t *y, int nl, float *s, hipStream_t st) {
-    constexpr int BB = BT<TY>::B;
-    int kch = KCH;   // a power of two (so 2 kch divides the workgroup), at most nb
-    while (kch > nb) kch >>= 1;
-    const int rpw = NT / (2 * kch);
-    const int64_t grid = (nr + rpw - 1) / rpw;
-    if (grid > 0x7fffffff) return 0;
-    const size_t lds = vl_gemv_lds(BB, kch, nl);
-    hipLaunchKernelGGL(vl_gemv_kernel<TY>, dim3((unsigned)grid), dim3(NT), lds, st, w, nb, nr, y, nl, s, kch);
-    return hipGetLastError() == hipSuccess ? 1 : -2;
+int vl_gemv_type(const uint8_t *w, int nb, int64_t nr, const uint8_t *y, int nl, float *s, hipStream_t st) {
+    switch (nl) {
+        case 1: return vl_gemv_launch<TY, 1>(w, nb, nr, y, s, st);
+        case 2: return vl_gemv_launch<TY, 2>(w, nb, nr, y, s, st);
+        case 3: return vl_gemv_launch<TY, 3>(w, nb, nr, y, s, st);
+        default: return vl_gemv_launch<TY, 4>(w, nb, nr, y, s, st);
+    }
 }
 
 }  // namespace kq
@@ -322,17 +400,17 @@ int oxe_hip_quantize_row_q8_K(const float *x, int64_t k, int64_t nrows, void *y,
 
 int oxe_hip_vl_gemv(int type, int64_t k, int64_t nr, int nl, const void *w, const void *y, float *s, void *stream) {
     using namespace oxe::kq;
-    if (nl < 1 || nl > MAX_LANES || nr <= 0 || k <= 0 || k % QK != 0 || k > 65536 || !w || !y || !s) return 0;
-    if (((uintptr_t)w & 3) != 0 || ((uintptr_t)y & 3) != 0) return 0;
+    if (nl < 1 || nl > MAX_LANES || nr <= 0 || k <= 0 || k % QK != 0 || k > 8192 || !w || !y || !s) return 0;
+    if (((uintptr_t)w & 15) != 0 || ((uintptr_t)y & 3) != 0) return 0;
     const int nb = (int)(k / QK);
     const hipStream_t st = (hipStream_t)stream;
     const uint8_t *wb = (const uint8_t *)w, *yb = (const uint8_t *)y;
     switch (type) {
-        case 4: return vl_gemv_launch<4>(wb, nb, nr, yb, nl, s, st);
-        case 5: return vl_gemv_launch<5>(wb, nb, nr, yb, nl, s, st);
-        // 110- and 210-byte blocks: dword staging needs an even block count
-        case 3: return nb % 2 ? 0 : vl_gemv_launch<3>(wb, nb, nr, yb, nl, s, st);
-        case 6: return nb % 2 ? 0 : vl_gemv_launch<6>(wb, nb, nr, yb, nl, s, st);
+        case 4: return vl_gemv_type<4>(wb, nb, nr, yb, nl, s, st);
+        case 5: return vl_gemv_type<5>(wb, nb, nr, yb, nl, s, st);
+        // 110- and 210-byte blocks: rows of an even block count keep every 4-row group 16-byte aligned
+        case 3: return nb % 2 ? 0 : vl_gemv_type<3>(wb, nb, nr, yb, nl, s, st);
+        case 6: return nb % 2 ? 0 : vl_gemv_type<6>(wb, nb, nr, yb, nl, s, st);
         default: return 0;
     }
 }
