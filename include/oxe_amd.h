@@ -222,6 +222,14 @@ OXE_API int oxe_mtp_step(oxe_engine *e, uint32_t x, uint32_t *out, int *n_out, i
 /* One plain target step from x that keeps the MTP catch-up in sync (MtpDriver::step_plain,
  * mtp.rs:504-515); *out = argmax after x. */
 OXE_API int oxe_mtp_step_plain(oxe_engine *e, uint32_t x, uint32_t *out);
+/* Drafts per host-driven step, 1..3 (MtpDriver.depth, mtp.rs:314-360; the reference's MAX_LANES
+ * verify of depth + 1 lanes runs here as pieces of at most 2 lanes, each committed before the next,
+ * stopping at the first rejected draft: the same committed state, tokens, hidden rows and logits).
+ * The device-driven step (oxe_mtp_device_*) is depth 1 and refuses other depths. */
+OXE_API int oxe_mtp_set_depth(oxe_engine *e, int depth);
+/* oxe_mtp_step with force[i] >= 0 (i < nforce) replacing draft i + 1 after the draft chain is formed
+ * (the reference's draft_override hook, mtp.rs:328-330, 554-558); out has room for depth + 1 tokens */
+OXE_API int oxe_mtp_step_force(oxe_engine *e, uint32_t x, uint32_t *out, int *n_out, const int64_t *force, int nforce);
 /* Keep only the first m (1..committed) tokens of the last host-driven step (MtpDriver::rewind,
  * mtp.rs:596-608; the server's spec_rewind, crates/server/src/engine.rs:100-104). -1 without a
  * step to rewind. */
@@ -239,7 +247,7 @@ OXE_API int oxe_mtp_set_force(oxe_engine *e, const int32_t *force_d1, int n);
  * 9 MTP entry; in the fused run mode 10 the verify run, 11 the draft run, each one launch): mean
  * kernel duration in microseconds (roofline measurement). */
 OXE_API int oxe_mtp_device_probe(oxe_engine *e, int k, int kind, float *avg_us, int *n);
-/* steps, accepted drafts */
+/* st[0] steps, st[1] accepted drafts, st[2] drafted tokens (MtpStats, mtp.rs:273-290) */
 OXE_API int oxe_mtp_stats(const oxe_engine *e, int64_t *st);
 OXE_API int oxe_engine_sync(oxe_engine *e);
 /* the engine's HIP stream (hipStream_t) */
@@ -274,7 +282,7 @@ OXE_API int oxe_srv_decode(oxe_srv *s, uint32_t tok, float *logits);
 OXE_API int oxe_srv_decode_argmax(oxe_srv *s, uint32_t tok, uint32_t *out);
 /* decode_spec_argmax (oxe_engine.rs:563-578): one MTP step from tok; extra[0..n_extra) = accepted
  * drafts (in the state), argmax[0..n_argmax) = the argmax of every committed row (the last is the
- * bonus token, not yet in the state); arrays of 2 (the verify lanes). 1 without MTP. */
+ * bonus token, not yet in the state); arrays of depth + 1 (at most 4). 1 without MTP. */
 OXE_API int oxe_srv_decode_spec_argmax(oxe_srv *s, uint32_t tok, uint32_t *extra, int *n_extra, uint32_t *argmax,
                                        int *n_argmax);
 /* decode_spec (oxe_engine.rs:530-543): as decode_spec_argmax with the committed rows' logits,
@@ -288,9 +296,11 @@ OXE_API int oxe_srv_spec_rewind(oxe_srv *s, int keep);
  * equal to greedy decoding, commit it; accepted[0..n_acc), argmax[0..n_acc] as decode_spec_argmax */
 OXE_API int oxe_srv_decode_verify(oxe_srv *s, uint32_t tok, const uint32_t *drafts, int n_drafts, uint32_t *accepted,
                                   int *n_acc, uint32_t *argmax, int *n_argmax);
-/* spec_max_depth / spec_counters (oxe_engine.rs:620-633): MTP (drafted, accepted) or the lookup
+/* spec_set_depth (oxe_engine.rs:623-627): drafts per step, clamped to 1..spec_max_depth (3 with MTP);
+ * spec_max_depth / spec_counters (oxe_engine.rs:620-633): MTP (drafted, accepted) or the lookup
  * counts of decode_verify */
 OXE_API int oxe_srv_spec_max_depth(const oxe_srv *s);
+OXE_API int oxe_srv_spec_set_depth(oxe_srv *s, int depth);
 OXE_API int oxe_srv_spec_counters(const oxe_srv *s, uint64_t *drafted, uint64_t *accepted);
 /* snapshot / snapshot_reuse (oxe_engine.rs:391-397; Engine::save_recurrent, engine.rs:1525-1531):
  * the current slot's conv + delta-net state (a device copy) and the position, plus the MTP

@@ -564,8 +564,10 @@ struct oxo_driver {
         return next;
     }
 
-    // MtpDriver::step (mtp.rs:522-592); `override_d1` >= 0 replaces the draft (test hook, mtp.rs:554-558)
-    int step(uint32_t x, uint32_t *out, int64_t override_d1) {
+    // MtpDriver::step (mtp.rs:522-592); force[i] >= 0 (i < nforce) replaces draft i after the draft
+    // chain is formed, as the reference's draft_override hook does (mtp.rs:554-558)
+    int step(uint32_t x, uint32_t *out, int64_t override_d1) { return step_force(x, out, &override_d1, 1); }
+    int step_force(uint32_t x, uint32_t *out, const int64_t *force, int nforce) {
         const int64_t p = eng->pos;
         const int64_t k = std::min<int64_t>(depth, std::max<int64_t>(0, eng->n_ctx - (p + 1)));
         flush(mtp_lanes() - 1);
@@ -587,7 +589,8 @@ struct oxo_driver {
             drafts[i] = eng->mtp_run(&drafts[i - 1], 1, p + i, h.data(), 1);
             h = eng->hout[0];
         }
-        if (override_d1 >= 0) drafts[0] = (uint32_t)override_d1;
+        for (int64_t i = 0; i < k && i < nforce; i++)
+            if (force[i] >= 0) drafts[i] = (uint32_t)force[i];
         uint32_t vt[8];
         vt[0] = x;
         for (int64_t i = 0; i < k; i++) vt[1 + i] = drafts[i];
@@ -637,6 +640,14 @@ extern "C" {
 
 oxo_engine *oxo_engine_new(const oxe_model_desc *d, uint64_t seed, int64_t n_ctx) {
     oxo_engine *e = new oxo_engine();
+    e->init(*d, seed, n_ctx);
+    return e;
+}
+// n_slots recurrent slots = verify lanes (the reference's verify width for MTP depth n_slots - 1)
+oxo_engine *oxo_engine_new_lanes(const oxe_model_desc *d, uint64_t seed, int64_t n_ctx, int n_slots) {
+    if (n_slots < 1 || n_slots > 8) return nullptr;
+    oxo_engine *e = new oxo_engine();
+    e->n_slots = n_slots;
     e->init(*d, seed, n_ctx);
     return e;
 }
@@ -697,6 +708,9 @@ oxo_driver *oxo_driver_new(oxo_engine *e, int depth) {
 void oxo_driver_free(oxo_driver *d) { delete d; }
 uint32_t oxo_driver_prefill(oxo_driver *d, const uint32_t *toks, int n) { return d->prefill(toks, n); }
 int oxo_driver_step(oxo_driver *d, uint32_t x, uint32_t *out, int64_t override_d1) { return d->step(x, out, override_d1); }
+int oxo_driver_step_force(oxo_driver *d, uint32_t x, uint32_t *out, const int64_t *force, int nforce) {
+    return d->step_force(x, out, force, nforce);
+}
 void oxo_driver_stats(const oxo_driver *d, int64_t *st) {
     st[0] = d->steps; st[1] = d->drafted; st[2] = d->accepted; st[3] = d->tokens_out;
 }

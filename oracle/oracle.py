@@ -96,6 +96,7 @@ def lib():
             "oxo_eval_unary": (None, [C.c_int, C.c_uint32, C.c_int64, C.c_int64, f32p]),
             "oxo_engine_new": (C.c_void_p, [P(ModelDesc), C.c_uint64, C.c_int64]),
             "oxo_engine_free": (None, [C.c_void_p]),
+            "oxo_engine_new_lanes": (C.c_void_p, [P(ModelDesc), C.c_uint64, C.c_int64, C.c_int]),
             "oxo_engine_reset": (None, [C.c_void_p]),
             "oxo_verify": (C.c_int, [C.c_void_p, u32p, C.c_int, u32p]),
             "oxo_commit": (C.c_int, [C.c_void_p, C.c_int]),
@@ -127,6 +128,7 @@ def lib():
             "oxo_driver_prefill": (C.c_uint32, [C.c_void_p, u32p, C.c_int]),
             "oxo_driver_step": (C.c_int, [C.c_void_p, C.c_uint32, u32p, C.c_int64]),
             "oxo_driver_step_plain": (C.c_uint32, [C.c_void_p, C.c_uint32]),
+            "oxo_driver_step_force": (C.c_int, [C.c_void_p, C.c_uint32, u32p, P(C.c_int64), C.c_int]),
             "oxo_driver_rewind": (C.c_int, [C.c_void_p, C.c_int]),
             "oxo_driver_stats": (None, [C.c_void_p, P(C.c_int64)]),
             "oxo_quantize_row_q8_K": (None, [f32p, C.c_void_p, C.c_int64]),
@@ -236,9 +238,10 @@ def config1_inputs(seed=0):
 class Engine:
     """Oracle engine (engine.rs semantics) on the synthetic model."""
 
-    def __init__(self, desc, seed=0, n_ctx=1024):
+    def __init__(self, desc, seed=0, n_ctx=1024, lanes=2):
         self.desc = desc
-        self.h = lib().oxo_engine_new(C.byref(desc), seed, n_ctx)
+        self.h = (lib().oxo_engine_new(C.byref(desc), seed, n_ctx) if lanes == 2 else
+                  lib().oxo_engine_new_lanes(C.byref(desc), seed, n_ctx, lanes))
         self.n_ctx = lib().oxo_n_ctx(self.h)
 
     def close(self):
@@ -294,9 +297,14 @@ class Driver:
         t = np.asarray(toks, np.uint32)
         return int(lib().oxo_driver_prefill(self.h, ptr(t, C.c_uint32), len(t)))
 
-    def step(self, x, override_d1=-1):
+    def step(self, x, override_d1=-1, force=None):
+        """one speculative step; override_d1 / force[i] >= 0 replace draft 1 / draft i + 1"""
         out = np.zeros(8, np.uint32)
-        n = lib().oxo_driver_step(self.h, x, ptr(out, C.c_uint32), override_d1)
+        if force is not None:
+            f = np.asarray(force, np.int64)
+            n = lib().oxo_driver_step_force(self.h, x, ptr(out, C.c_uint32), ptr(f, C.c_int64), len(f))
+        else:
+            n = lib().oxo_driver_step(self.h, x, ptr(out, C.c_uint32), override_d1)
         return [int(v) for v in out[:n]]
 
     def step_plain(self, x):

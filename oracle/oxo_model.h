@@ -10,6 +10,8 @@ typedef struct oxo_engine oxo_engine;
 typedef struct oxo_driver oxo_driver;
 
 oxo_engine *oxo_engine_new(const oxe_model_desc *d, uint64_t seed, int64_t n_ctx);
+// with n_slots recurrent slots (verify lanes; 2 by default, 4 for MTP depth 3)
+oxo_engine *oxo_engine_new_lanes(const oxe_model_desc *d, uint64_t seed, int64_t n_ctx, int n_slots);
 void oxo_engine_free(oxo_engine *e);
 void oxo_engine_reset(oxo_engine *e);
 int oxo_verify(oxo_engine *e, const uint32_t *toks, int n, uint32_t *out);      // engine.rs:2002-2025
@@ -43,6 +45,8 @@ oxo_driver *oxo_driver_new(oxo_engine *e, int depth);                          /
 void oxo_driver_free(oxo_driver *d);
 uint32_t oxo_driver_prefill(oxo_driver *d, const uint32_t *toks, int n);      // mtp.rs:450-463
 int oxo_driver_step(oxo_driver *d, uint32_t x, uint32_t *out, int64_t override_d1); // mtp.rs:522-592
+// the same with force[i] >= 0 replacing draft i (i < nforce) after the chain (draft_override, mtp.rs:554-558)
+int oxo_driver_step_force(oxo_driver *d, uint32_t x, uint32_t *out, const int64_t *force, int nforce);
 uint32_t oxo_driver_step_plain(oxo_driver *d, uint32_t x);                           // mtp.rs:504-515
 int oxo_driver_rewind(oxo_driver *d, int m);                                        // mtp.rs:596-608
 void oxo_driver_stats(const oxo_driver *d, int64_t *st);

@@ -146,6 +146,7 @@ void MtpDriverHost::note_h(int p0, const uint32_t *toks, int n, const float *h) 
 }
 
 void MtpDriverHost::remember(Engine &e, int p0, int n) {
+    last_cur0 = (e.cur - n % OXE_NSLOTS + OXE_NSLOTS) % OXE_NSLOTS;   // n lanes committed from there
     last_p0 = p0;
     last_n = n;
     last_h.resize((size_t)n * E);
@@ -218,8 +219,21 @@ int MtpDriverHost::prefill_batched(Engine &e, const uint32_t *toks, int n, uint3
 }
 
 int MtpDriverHost::step(Engine &e, uint32_t x, uint32_t *out, int *n_out, int64_t override_d1) {
-    const int p = e.pos;
-    const int k = std::min(1, std::max(0, e.m.n_ctx - (p + 1)));
+    return step_k(e, x, out, n_out, &override_d1, 1, nullptr);
+}
+
+// MtpDriver::step (mtp.rs:522-592) at depth k = min(depth, room): the catch-up seeded, the draft
+// chain d_1 = MTP(x, h_prev) at p, d_i = MTP(d_{i-1}, h of the previous MTP run) at p + i - 1;
+// force[i] >= 0 replaces d_{i+1} after the chain (the draft_override hook, mtp.rs:554-558); then
+// the verify of [x, d_1..d_k] with greedy acceptance. The verify runs in pieces of at most OXE_NL
+// lanes, each committed before the next, and stops at the first rejected draft: a run of n lanes
+// computes exactly n steps, so the committed state, argmaxes, hidden rows and logits are those of
+// the reference's single (k+1)-lane verify and commit(a+1). rows (optional, host [k+1][n_vocab]):
+// the logits of every committed lane.
+int MtpDriverHost::step_k(Engine &e, uint32_t x, uint32_t *out, int *n_out, const int64_t *force, int nforce,
+                          float *rows) {
+    const int p = e.pos, cur0 = e.cur;
+    const int k = std::min(depth, std::max(0, e.m.n_ctx - (p + 1)));
     int rc = flush(e, 7);
     if (rc) return rc;
     if (k == 0) {
@@ -227,23 +241,55 @@ int MtpDriverHost::step(Engine &e, uint32_t x, uint32_t *out, int *n_out, int64_
         if ((rc = e.verify(&x, 1, &g)) || (rc = e.commit(1))) return rc;
         note(e, p, &x, 1);
         remember(e, p, 1);
+        if (rows && hipMemcpy(rows, e.b.logits, (size_t)e.d.n_vocab * 4, hipMemcpyDeviceToHost) != hipSuccess) return -2;
         out[0] = g;
         *n_out = 1;
         return 0;
     }
     if ((rc = flush(e, 0))) return rc;
-    uint32_t d1;
-    if ((rc = e.mtp_run(&x, 1, p, hl.data(), 1, &d1))) return rc;
+    uint32_t d[MTP_MAX_DEPTH];
+    if ((rc = e.mtp_run(&x, 1, p, hl.data(), 1, &d[0]))) return rc;
     q = p + 1;
-    if (override_d1 >= 0) d1 = (uint32_t)override_d1;
-    const uint32_t vt[2] = {x, d1};
-    uint32_t g[2];
-    if ((rc = e.verify(vt, 2, g))) return rc;
-    const int a = d1 == g[0] ? 1 : 0;
-    if ((rc = e.commit(a + 1))) return rc;
-    note(e, p, vt, a + 1);
-    remember(e, p, a + 1);
+    std::vector<float> h(E);
+    for (int i = 1; i < k; i++) {
+        if ((rc = e.hidden_host(0, h.data()))) return rc;
+        if ((rc = e.mtp_run(&d[i - 1], 1, p + i, h.data(), 1, &d[i]))) return rc;
+    }
+    for (int i = 0; i < k && i < nforce; i++)
+        if (force[i] >= 0) d[i] = (uint32_t)force[i];
+    uint32_t vt[MTP_MAX_DEPTH + 1], g[MTP_MAX_DEPTH + 1];
+    vt[0] = x;
+    for (int i = 0; i < k; i++) vt[1 + i] = d[i];
+    std::vector<float> hs((size_t)(k + 1) * E);
+    int done = 0;
+    for (bool more = true; more;) {
+        const int n = std::min(OXE_NL, k + 1 - done);
+        if ((rc = e.verify(vt + done, n, g + done))) return rc;
+        int m = 0;   // lanes of this piece to commit: lane j, then j + 1 while d_{j+1} == g_j
+        for (int j = done; j < done + n; j++) {
+            m++;
+            if (j >= k || vt[j + 1] != g[j]) {
+                more = false;
+                break;
+            }
+        }
+        for (int j = 0; j < m; j++) {
+            if ((rc = e.hidden_host(j, hs.data() + (size_t)(done + j) * E))) return rc;
+            if (rows && hipMemcpy(rows + (size_t)(done + j) * e.d.n_vocab, e.b.logits + (size_t)j * e.d.n_vocab,
+                                  (size_t)e.d.n_vocab * 4, hipMemcpyDeviceToHost) != hipSuccess)
+                return -2;
+        }
+        if ((rc = e.commit(m))) return rc;
+        done += m;
+    }
+    const int a = done - 1;
+    note_h(p, vt, a + 1, hs.data());
+    last_p0 = p;
+    last_n = a + 1;
+    last_cur0 = cur0;
+    last_h.assign(hs.begin(), hs.begin() + (size_t)(a + 1) * E);
     steps++;
+    drafted += k;
     accepted += a;
     for (int i = 0; i <= a; i++) out[i] = g[i];
     *n_out = a + 1;
@@ -263,11 +309,15 @@ int MtpDriverHost::step_plain(Engine &e, uint32_t x, uint32_t *out) {
     return 0;
 }
 
-// MtpDriver::rewind (mtp.rs:596-608): keep the first m committed tokens of the last step
+// MtpDriver::rewind (mtp.rs:596-608): keep the first m committed tokens of the last step. Inside
+// the step's last verify piece this is a smaller commit; before it, a rollback to the slot that
+// holds the state after token m (the step began at slot last_cur0; lane j wrote slot + j + 1).
 int MtpDriverHost::rewind(Engine &e, int m) {
     if (last_n == 0 || m < 1 || m > last_n) return -1;
     if (m == last_n) return 0;
-    int rc = e.commit(m);
+    const int target = last_p0 + m;
+    int rc = (e.pend_n > 0 && target > e.pend_pos0) ? e.commit(target - e.pend_pos0)
+                                                     : e.rollback(target, (last_cur0 + m) % OXE_NSLOTS);
     if (rc) return rc;
     const size_t keep = std::min<size_t>((size_t)std::max(0, last_p0 + m - q), cu_tok.size());
     cu_tok.resize(keep);
@@ -317,6 +367,7 @@ int MtpDriverHost::dev_end(Engine &e, uint32_t *out_tok, int cap, int *n_out, ui
     e.pend_n = 0;
     steps += s.steps;
     accepted += s.accepted;
+    drafted += s.steps;   // one draft per device-driven step
     return s.err ? -4 : 0;
 }
 
@@ -405,6 +456,21 @@ int oxe_mtp_step(oxe_engine *e, uint32_t x, uint32_t *out, int *n_out, int64_t o
     return g->drv.step(*g, x, out, n_out, override_d1);
 }
 
+int oxe_mtp_step_force(oxe_engine *e, uint32_t x, uint32_t *out, int *n_out, const int64_t *force, int nforce) {
+    Engine *g = (Engine *)e;
+    if (!g->toks_ok(&x, 1) || !out || !n_out || nforce < 0 || (nforce > 0 && !force)) return -1;
+    for (int i = 0; i < nforce; i++)
+        if (force[i] >= g->d.n_vocab) return -1;
+    return g->drv.step_k(*g, x, out, n_out, force, nforce, nullptr);
+}
+
+int oxe_mtp_set_depth(oxe_engine *e, int depth) {
+    Engine *g = (Engine *)e;
+    if (depth < 1 || depth > oxe::MTP_MAX_DEPTH) return -1;
+    g->drv.depth = depth;
+    return 0;
+}
+
 int oxe_mtp_step_plain(oxe_engine *e, uint32_t x, uint32_t *out) {
     Engine *g = (Engine *)e;
     if (!g->toks_ok(&x, 1) || !out) return -1;
@@ -424,6 +490,10 @@ int oxe_mtp_set_force(oxe_engine *e, const int32_t *force_d1, int n) {
 int oxe_mtp_device_begin(oxe_engine *e, uint32_t x, int out_cap) {
     Engine *g = (Engine *)e;
     if (out_cap < 1 || !g->toks_ok(&x, 1)) return -1;
+    if (g->drv.depth != 1) {
+        oxe::set_err("device-driven MTP steps are depth 1");
+        return -1;
+    }
     if (g->ensure_out(out_cap)) return -3;
     return g->drv.dev_begin(*g, x);
 }
@@ -443,6 +513,7 @@ int oxe_mtp_stats(const oxe_engine *e, int64_t *st) {
     const Engine *g = (const Engine *)e;
     st[0] = g->drv.steps;
     st[1] = g->drv.accepted;
+    st[2] = g->drv.drafted;
     return 0;
 }
 

@@ -24,7 +24,10 @@ struct Q8W {
     int64_t rows = 0, k = 0;
 };
 
-constexpr int OXE_NSLOTS = OXE_NL + 1;  // recurrent slots: lane i reads slot cur+i, writes cur+i+1 (never in place)
+// recurrent slots: lane i reads slot cur+i, writes cur+i+1 (never in place). Five keep the state
+// after every position of an MTP depth-3 step (4 lanes verified in pieces of OXE_NL), so a rewind
+// can return to any committed prefix of it.
+constexpr int OXE_NSLOTS = 5;
 
 // Run control (device memory). Written by the host through a tiny kernel for host-driven calls and
 // by the commit kernel for the device-driven MTP step; read by every kernel of a run.

@@ -27,15 +27,18 @@ using namespace shp;
 struct Engine;
 struct Gguf;
 
-// MtpDriver (crates/model/src/mtp.rs:314-608) at depth 1, host-driven; dev_begin / dev_end hand its
-// state to and from the device-driven step.
+// MtpDriver (crates/model/src/mtp.rs:314-608), host-driven, depth 1..MTP_MAX_DEPTH; dev_begin /
+// dev_end hand its state to and from the device-driven step (depth 1).
+constexpr int MTP_MAX_DEPTH = 3;
 struct MtpDriverHost {
+    int depth = 1;               // drafts per step (MtpDriver.depth)
     int q = 0;                   // MTP KV holds correct pairs for positions < q
     std::vector<uint32_t> cu_tok;  // pending catch-up pairs for positions q, q+1, ...
     std::vector<float> cu_h;
     std::vector<float> hl = std::vector<float>(shp::E, 0.0f);  // target h_nextn of position pos-1
-    int64_t steps = 0, accepted = 0;
+    int64_t steps = 0, accepted = 0, drafted = 0;
     int last_p0 = 0, last_n = 0;   // the last host-driven step's committed span (MtpDriver.last)
+    int last_cur0 = 0;             // the recurrent slot before that span
     std::vector<float> last_h;     // h_nextn of each committed lane of that step (MtpDriver.last_h)
     void note(Engine &e, int p0, const uint32_t *toks, int n);
     void note_h(int p0, const uint32_t *toks, int n, const float *h);
@@ -44,6 +47,7 @@ struct MtpDriverHost {
     int prefill(Engine &e, const uint32_t *toks, int n, uint32_t *next);
     int prefill_batched(Engine &e, const uint32_t *toks, int n, uint32_t *next);
     int step(Engine &e, uint32_t x, uint32_t *out, int *n_out, int64_t override_d1);
+    int step_k(Engine &e, uint32_t x, uint32_t *out, int *n_out, const int64_t *force, int nforce, float *rows);
     int step_plain(Engine &e, uint32_t x, uint32_t *out);
     int rewind(Engine &e, int m);
     int dev_begin(Engine &e, uint32_t x);
@@ -579,6 +583,17 @@ struct Engine {
         pend_n = n;
         pend_done = 0;
         return read_argmax(out, n);
+    }
+    // back to position p_new < pos of the current host-driven step, whose state after position
+    // p_new - 1 is in slot cur_new (an earlier verify piece of the step): V^T of the positions
+    // after it back to +0, no pending verify
+    int rollback(int p_new, int cur_new) {
+        if (p_new < 0 || p_new > pos || cur_new < 0 || cur_new >= OXE_NSLOTS) return -1;
+        launch_zero_v(m, n_att_main, p_new, pos, st);
+        pos = p_new;
+        cur = cur_new;
+        pend_n = 0;
+        return hipStreamSynchronize(st) == hipSuccess ? 0 : -2;
     }
     int commit(int mm) {
         if (pend_n == 0) return -1;

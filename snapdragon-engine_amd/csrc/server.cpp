@@ -122,14 +122,16 @@ struct SrvEngine {
     }
 
     // decode_spec_argmax: `extra` = accepted drafts (now in the state), `argmax` = the argmax of
-    // every committed row (the last one is the bonus token, not yet in the state)
-    int decode_spec_argmax(uint32_t tok, uint32_t *extra, int *n_extra, uint32_t *argmax, int *n_argmax) {
+    // every committed row (the last one is the bonus token, not yet in the state); rows (optional):
+    // those rows' logits (decode_spec)
+    int decode_spec_argmax(uint32_t tok, uint32_t *extra, int *n_extra, uint32_t *argmax, int *n_argmax,
+                           float *rows = nullptr) {
         if (!mtp) return 1;   // unsupported: the caller decodes one token
         int rc = check_one(tok);
         if (rc) return rc;
-        uint32_t out[OXE_NL];
+        uint32_t out[MTP_MAX_DEPTH + 1];
         int n = 0;
-        if ((rc = e->drv.step(*e, tok, out, &n, -1))) return rc;
+        if ((rc = e->drv.step_k(*e, tok, out, &n, nullptr, 0, rows))) return rc;
         for (int i = 0; i < n; i++) argmax[i] = out[i];
         for (int i = 0; i + 1 < n; i++) extra[i] = out[i];
         *n_argmax = n;
@@ -448,14 +450,9 @@ int oxe_srv_decode_spec_argmax(oxe_srv *s, uint32_t tok, uint32_t *extra, int *n
 }
 int oxe_srv_decode_spec(oxe_srv *s, uint32_t tok, uint32_t *extra, int *n_extra, float *rows) {
     if (!extra || !n_extra || !rows) return -1;
-    SrvEngine *v = srv(s);
-    uint32_t g[oxe::OXE_NL];
+    uint32_t g[oxe::MTP_MAX_DEPTH + 1];
     int ng = 0;
-    int rc = v->decode_spec_argmax(tok, extra, n_extra, g, &ng);
-    if (rc) return rc;
-    for (int i = 0; i < ng; i++)
-        if ((rc = oxe_engine_logits((oxe_engine *)v->e, i, rows + (size_t)i * v->e->d.n_vocab))) return rc;
-    return 0;
+    return srv(s)->decode_spec_argmax(tok, extra, n_extra, g, &ng, rows);
 }
 int oxe_srv_spec_rewind(oxe_srv *s, int keep) { return srv(s)->spec_rewind(keep); }
 int oxe_srv_decode_verify(oxe_srv *s, uint32_t tok, const uint32_t *drafts, int n_drafts, uint32_t *accepted, int *n_acc,
@@ -463,12 +460,18 @@ int oxe_srv_decode_verify(oxe_srv *s, uint32_t tok, const uint32_t *drafts, int 
     if (!drafts || !accepted || !n_acc || !argmax || !n_argmax) return -1;
     return srv(s)->decode_verify(tok, drafts, n_drafts, accepted, n_acc, argmax, n_argmax);
 }
-int oxe_srv_spec_max_depth(const oxe_srv *s) { return ((const SrvEngine *)s)->mtp ? 1 : 0; }
+int oxe_srv_spec_max_depth(const oxe_srv *s) { return ((const SrvEngine *)s)->mtp ? oxe::MTP_MAX_DEPTH : 0; }
+// spec_set_depth (oxe_engine.rs:623-627): clamped to 1..max; no effect without MTP
+int oxe_srv_spec_set_depth(oxe_srv *s, int depth) {
+    SrvEngine *v = srv(s);
+    if (v->mtp) v->e->drv.depth = depth < 1 ? 1 : (depth > oxe::MTP_MAX_DEPTH ? oxe::MTP_MAX_DEPTH : depth);
+    return 0;
+}
 int oxe_srv_spec_counters(const oxe_srv *s, uint64_t *drafted, uint64_t *accepted) {
     const SrvEngine *v = (const SrvEngine *)s;
     if (!drafted || !accepted) return -1;
     if (v->mtp) {
-        *drafted = (uint64_t)v->e->drv.steps;
+        *drafted = (uint64_t)v->e->drv.drafted;
         *accepted = (uint64_t)v->e->drv.accepted;
     } else {
         *drafted = v->lookup_drafted;

@@ -225,6 +225,9 @@ def _engine_sigs(L):
         "oxe_mtp_device_end": (i32, [vp, u32p, i32, C.POINTER(C.c_int), u32p]),
         "oxe_mtp_set_force": (i32, [vp, C.POINTER(C.c_int32), i32]),
         "oxe_mtp_stats": (i32, [vp, C.POINTER(C.c_int64)]),
+        "oxe_mtp_step_force": (i32, [vp, C.c_uint32, u32p, C.POINTER(C.c_int), C.POINTER(C.c_int64), i32]),
+        "oxe_mtp_set_depth": (i32, [vp, i32]),
+        "oxe_srv_spec_set_depth": (i32, [vp, i32]),
         "oxe_engine_sync": (i32, [vp]),
         "oxe_mtp_device_probe": (i32, [vp, i32, i32, C.POINTER(C.c_float), C.POINTER(C.c_int)]),
         "oxe_engine_stream": (vp, [vp]),
@@ -614,6 +617,20 @@ class Engine:
             raise RuntimeError("read_trace failed")
         return buf[:n].reshape(-1, 1024, 4)
 
+    def mtp_set_depth(self, depth):
+        """drafts per host-driven MTP step (MtpDriver.depth; the device-driven step is depth 1)"""
+        check(lib().oxe_mtp_set_depth(self.h, depth), "mtp_set_depth")
+
+    def mtp_step_force(self, x, force):
+        """one host-driven MTP step with force[i] >= 0 replacing draft i + 1 (draft_override)"""
+        import numpy as np
+        f = np.ascontiguousarray(force, np.int64)
+        out = np.zeros(8, np.uint32)
+        n = C.c_int(0)
+        check(lib().oxe_mtp_step_force(self.h, x, _np_ptr(out, C.c_uint32), C.byref(n), _np_ptr(f, C.c_int64), len(f)),
+              "mtp_step_force")
+        return [int(v) for v in out[: n.value]]
+
     def mtp_step_plain(self, x):
         out = (C.c_uint32 * 1)()
         check(lib().oxe_mtp_step_plain(self.h, x, out), "mtp_step_plain")
@@ -644,9 +661,9 @@ class Engine:
 
     def mtp_stats(self):
         import numpy as np
-        s = np.zeros(2, np.int64)
+        s = np.zeros(3, np.int64)
         lib().oxe_mtp_stats(self.h, s.ctypes.data_as(C.POINTER(C.c_int64)))
-        return dict(steps=int(s[0]), accepted=int(s[1]))
+        return dict(steps=int(s[0]), accepted=int(s[1]), drafted=int(s[2]))
 
     def mtp_device_probe(self, k, kind):
         avg = C.c_float(0)
@@ -783,6 +800,9 @@ class ServerEngine:
 
     def spec_max_depth(self):
         return int(lib().oxe_srv_spec_max_depth(self.h))
+
+    def spec_set_depth(self, depth):
+        lib().oxe_srv_spec_set_depth(self.h, depth)
 
     def spec_counters(self):
         a, b = C.c_uint64(0), C.c_uint64(0)

@@ -111,3 +111,42 @@ def test_rewind_and_step_plain_equal_plain_greedy(desc):
     out = drv.step(x, override_d1=ref[5])
     got += out
     assert got == ref[: len(got)]
+
+
+def test_four_lane_verify_equals_steps(desc):
+    """the reference's verify width for MTP depth 3 (4 recurrent slots): verify(n) == n steps for
+    n = 3, 4, and a partial commit leaves the state of the committed prefix"""
+    a = O.Engine(desc, seed=SEED, n_ctx=256, lanes=4)
+    b = O.Engine(desc, seed=SEED, n_ctx=256)
+    for toks, m in (([17, 3001, 9], 3), ([5, 6, 7, 8], 4), ([40, 41, 42, 43], 2)):
+        g = a.verify(toks)
+        la = [a.logits(i) for i in range(m)]
+        a.commit(m)
+        for i, t in enumerate(toks[:m]):
+            assert b.step(t) == g[i]
+            assert np.array_equal(bits(b.logits(0)), bits(la[i]))
+    assert a.pos == b.pos
+    assert a.step(100) == b.step(100)
+    assert np.array_equal(bits(a.logits(0)), bits(b.logits(0)))
+
+
+@pytest.mark.parametrize("depth", [2, 3])
+def test_mtp_depth_k_greedy_equals_plain(desc, depth):
+    """MtpDriver at depth k (mtp.rs:522-592) with forced drafts through every acceptance count
+    equals plain greedy decoding (crates/model/src/tests.rs:1033-1117)"""
+    prompt = [int(v) % desc.n_vocab for v in O.bench_prompt(9)]
+    ref, _ = plain_greedy(desc, prompt, 30)
+    e = O.Engine(desc, seed=SEED, n_ctx=256, lanes=depth + 1)
+    drv = O.Driver(e, depth)
+    x = drv.prefill(prompt)
+    out, k = [x], 0
+    for a in [depth, 0, 1, depth, depth - 1, 0]:
+        f = [ref[k + 1 + i] for i in range(a)] + ([(ref[k + 1 + a] + 1) % desc.n_vocab] if a < depth else [])
+        r = drv.step(x, force=f + [-1] * (depth - len(f)))
+        assert len(r) == a + 1
+        out += r
+        k += a + 1
+        x = r[-1]
+    assert out == ref[:len(out)]
+    st = drv.stats()
+    assert st["drafted"] == 6 * depth and st["accepted"] == sum([depth, 0, 1, depth, depth - 1, 0])

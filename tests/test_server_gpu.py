@@ -84,7 +84,7 @@ def test_prefill_logits_and_decode_argmax_plain_and_mtp(d, prompt, plain):
     # decode = prefill of one token: the row of that token
     row = sp.decode(xp)
     assert first_max(row) == plain[9] and sp.n_past() == len(prompt) + 9
-    assert sp.spec_max_depth() == 0 and sm.spec_max_depth() == 1
+    assert sp.spec_max_depth() == 0 and sm.spec_max_depth() == 3
 
 
 def test_decode_spec_argmax_is_greedy(d, prompt, plain):
