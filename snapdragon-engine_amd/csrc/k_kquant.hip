@@ -27,9 +27,19 @@ template <> struct BT<6> { static constexpr int B = 210; };
 
 OXE_DEV uint32_t ld32(const uint8_t *p) { return *(const uint32_t *)p; }
 OXE_DEV uint16_t ld16(const uint8_t *p) { return *(const uint16_t *)p; }
-// 4 bytes at a 2-byte aligned LDS address (Q3_K / Q6_K blocks are 110 / 210 bytes, so every other
-// block of a row starts 2 bytes off a dword boundary)
-OXE_DEV uint32_t ld32h(const uint8_t *p) { return (uint32_t)ld16(p) | (uint32_t)ld16(p + 2) << 16; }
+// N dwords from a 2-byte aligned LDS address (Q3_K / Q6_K blocks are 110 / 210 bytes, so every other
+// block of a row starts 2 bytes off a dword boundary): N + 1 aligned dword reads, then each dword
+// cut out of a neighbouring pair (v_alignbyte_b32)
+template <int N>
+OXE_DEV void ld_run(const uint8_t *p, uint32_t (&out)[N]) {
+    const uint32_t sh = (uint32_t)(uintptr_t)p & 3u;
+    const uint32_t *a = (const uint32_t *)(p - sh);
+    uint32_t w[N + 1];
+#pragma unroll
+    for (int i = 0; i <= N; i++) w[i] = a[i];
+#pragma unroll
+    for (int i = 0; i < N; i++) out[i] = __builtin_amdgcn_alignbyte(w[i + 1], w[i], sh);
+}
 OXE_DEV int bsum16(const uint8_t *yb, int i) { return (int)*(const int16_t *)(yb + Q8K_BS + 2 * i); }
 
 // ---- quantize_row_q8_K_ref (vendor/ggml-subset/generated/quants_base.c:14-48) --------------------
@@ -152,8 +162,10 @@ OXE_DEV void unit_k45(const uint8_t *wb, const uint8_t *yb, int ystride, int h, 
 // Q6_K: the unit's part of I = sum_i scale_i * (16 codes - 32) . q8 (the -32 through the q8 sums)
 template <int NL>
 OXE_DEV void unit_q6(const uint8_t *wb, const uint8_t *yb, int ystride, int n, int *out) {
-    const uint8_t *ql = wb + 64 * n, *qh = wb + 128 + 32 * n;
     const int8_t *sc = (const int8_t *)(wb + 192);
+    uint32_t qlw[16], qhw[8];   // ql[64 n .. 64 n + 63], qh[32 n .. 32 n + 31]
+    ld_run<16>(wb + 64 * n, qlw);
+    ld_run<8>(wb + 128 + 32 * n, qhw);
     int d[NL][8];
 #pragma unroll
     for (int l = 0; l < NL; l++)
@@ -161,7 +173,7 @@ OXE_DEV void unit_q6(const uint8_t *wb, const uint8_t *yb, int ystride, int n, i
         for (int i = 0; i < 8; i++) d[l][i] = 0;
 #pragma unroll
     for (int i = 0; i < 8; i++) {
-        const uint32_t a = ld32h(ql + 4 * i), a2 = ld32h(ql + 32 + 4 * i), hb = ld32h(qh + 4 * i);
+        const uint32_t a = qlw[i], a2 = qlw[8 + i], hb = qhw[i];
         const uint32_t c0 = (a & 0x0F0F0F0Fu) | ((hb & 0x03030303u) << 4);
         const uint32_t c1 = (a2 & 0x0F0F0F0Fu) | (((hb >> 2) & 0x03030303u) << 4);
         const uint32_t c2 = ((a >> 4) & 0x0F0F0F0Fu) | (((hb >> 4) & 0x03030303u) << 4);
@@ -195,7 +207,9 @@ OXE_DEV int q3_raw(const uint8_t *s12, int i) {
 // Q3_K: the unit's part of isum = sum_i (raw_i - 32) * dot16_i, codes (low 2 bits | hmask bit << 2) - 4
 template <int NL>
 OXE_DEV void unit_q3(const uint8_t *wb, const uint8_t *yb, int ystride, int n, int *out) {
-    const uint8_t *hm = wb, *qs = wb + 32 + 32 * n;
+    uint32_t qsw[8], hmw[8];   // qs[32 n .. 32 n + 31], hmask[0..31]
+    ld_run<8>(wb + 32 + 32 * n, qsw);
+    ld_run<8>(wb, hmw);
     int d[NL][8];
 #pragma unroll
     for (int l = 0; l < NL; l++)
@@ -203,7 +217,7 @@ OXE_DEV void unit_q3(const uint8_t *wb, const uint8_t *yb, int ystride, int n, i
         for (int i = 0; i < 8; i++) d[l][i] = 0;
 #pragma unroll
     for (int i = 0; i < 8; i++) {
-        const uint32_t qw = ld32h(qs + 4 * i), hw = ld32h(hm + 4 * i);
+        const uint32_t qw = qsw[i], hw = hmw[i];
         const int half = i >> 2;
 #pragma unroll
         for (int s = 0; s < 4; s++) {
