@@ -10,7 +10,8 @@
 //
 // Workgroup tile: 64 weight rows x 64 tokens, 4 waves of 32 x 32 (2 x 2 MFMA tiles). The K
 // dimension is staged through LDS 8 blocks (256 bytes per row) at a time with 16-byte coalesced
-// loads; LDS rows are padded to 272 bytes so a wave's 8-byte fragment reads fall on distinct banks.
+// loads, the next stage's held in registers while the current one computes; LDS rows are padded to
+// 272 bytes so a wave's 8-byte fragment reads fall on distinct banks.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -70,25 +71,43 @@ __global__ __launch_bounds__(gm::NT) void gemm_q8_kernel(GemmArgs a) {
         for (int j = 0; j < 2; j++)
 #pragma unroll
             for (int v = 0; v < 4; v++) acc[i][j][v] = 0.0f;
-    for (int64_t kc = 0; kc < k; kc += KC) {
-        // stage codes: 64 rows x 256 bytes each for W and X, 16 bytes per thread and pass
+    // the next stage's codes and scales are loaded into registers while the current stage computes
+    constexpr int NP = BM * KC / 16 / NT;   // 16-byte code chunks per thread and matrix
+    uint4 pu[NP], pv[NP];
+    float pdw[BM * NBC / NT], pdx[BM * NBC / NT];
+    auto fetch = [&](int64_t kc) {
 #pragma unroll
-        for (int p = 0; p < BM * KC / 16 / NT; p++) {
+        for (int p = 0; p < NP; p++) {
             const int i = t + NT * p, row = i / (KC / 16), ch = i % (KC / 16);
             const int64_t gr = r0 + row, xr = sxr[row];
-            const uint4 u = gr < nr ? *(const uint4 *)(wq + gr * k + kc + 16 * ch) : make_uint4(0, 0, 0, 0);
-            const uint4 v = xr >= 0 ? *(const uint4 *)(a.xq + xr * k + kc + 16 * ch) : make_uint4(0, 0, 0, 0);
-            *(uint4 *)(sw + row * LDR + 16 * ch) = u;
-            *(uint4 *)(sx + row * LDR + 16 * ch) = v;
+            pu[p] = gr < nr ? *(const uint4 *)(wq + gr * k + kc + 16 * ch) : make_uint4(0, 0, 0, 0);
+            pv[p] = xr >= 0 ? *(const uint4 *)(a.xq + xr * k + kc + 16 * ch) : make_uint4(0, 0, 0, 0);
         }
-        // stage scales as f32: 64 rows x 8 blocks for W and X
-        for (int i = t; i < BM * NBC; i += NT) {
-            const int row = i / NBC, bb = i % NBC;
+#pragma unroll
+        for (int p = 0; p < BM * NBC / NT; p++) {
+            const int i = t + NT * p, row = i / NBC, bb = i % NBC;
             const int64_t gr = r0 + row, xr = sxr[row];
-            sdw[bb][row] = gr < nr ? h2f(wd[gr * nb + kc / 32 + bb]) : 0.0f;
-            sdx[bb][row] = xr >= 0 ? h2f(a.xd[xr * nb + kc / 32 + bb]) : 0.0f;
+            pdw[p] = gr < nr ? h2f(wd[gr * nb + kc / 32 + bb]) : 0.0f;
+            pdx[p] = xr >= 0 ? h2f(a.xd[xr * nb + kc / 32 + bb]) : 0.0f;
+        }
+    };
+    fetch(0);
+    for (int64_t kc = 0; kc < k; kc += KC) {
+        // stage codes (64 rows x 256 bytes of W and X) and scales (as f32) from the registers
+#pragma unroll
+        for (int p = 0; p < NP; p++) {
+            const int i = t + NT * p, row = i / (KC / 16), ch = i % (KC / 16);
+            *(uint4 *)(sw + row * LDR + 16 * ch) = pu[p];
+            *(uint4 *)(sx + row * LDR + 16 * ch) = pv[p];
+        }
+#pragma unroll
+        for (int p = 0; p < BM * NBC / NT; p++) {
+            const int i = t + NT * p, row = i / NBC, bb = i % NBC;
+            sdw[bb][row] = pdw[p];
+            sdx[bb][row] = pdx[p];
         }
         __syncthreads();
+        if (kc + KC < k) fetch(kc + KC);
         // the wave's 16-token sub-tiles that hold tokens (a per-expert group fills a tile partly):
         // empty ones are skipped, wave-uniformly
         auto blocks = [&](auto njc) {
