@@ -200,8 +200,9 @@ OXE_API int oxe_gguf_model_desc(const oxe_gguf *g, oxe_model_desc *out);
 /* Every weight of the engine from the file (WeightStore::load, weights.rs:556-700): Q8_0 matmul
  * weights split on the device into this build's codes + scales layout (the reference repacks into
  * 4-row interleaved blocks, oxe_repack_q8_0_4x8, lib.rs:59), F32 norms, routers and state
- * parameters copied. Other tensor types are refused by name (-1): the kernels run Q8_0 matmul
- * weights and F32 vectors only (k-quants and BF16 routers are not built). */
+ * parameters copied, BF16 ones widened to f32 (as the reference converts BF16 small tensors,
+ * crates/model/src/mtp.rs:109-128). Other tensor types are refused by name (-1): the engine's runs
+ * take Q8_0 matmul weights (the K-quant GEMVs exist at kernel level, oxe_hip_vl_gemv). */
 OXE_API int oxe_engine_load_gguf(oxe_engine *e, const oxe_gguf *g);
 /* open + model_desc + engine_create + load_gguf */
 OXE_API int oxe_engine_create_from_gguf(const char *path, int n_ctx, oxe_engine **out);

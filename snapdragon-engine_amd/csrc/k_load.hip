@@ -49,7 +49,7 @@ static std::string tensor_check(const GgufTensor *t, const std::string &name, ui
         GgmlTypeInfo want{};
         ggml_type_info(type, &want);
         return name + ": type " + (ti.name ? ti.name : "unknown") + " has no kernel in this build (expected " +
-               want.name + ": Q8_0 matmul weights, F32 vectors and routers)";
+               want.name + ": Q8_0 matmul weights, F32 or BF16 vectors and routers)";
     }
     if (t->shape != std::vector<uint64_t>(shape)) return name + ": unexpected shape";
     return "";
@@ -109,9 +109,21 @@ int Engine::load_gguf(const Gguf &g) {
             }
         }
     };
+    // F32 vectors and routers; BF16 ones widened to f32 (exact: the bf16 bits are the high half of
+    // the f32), as the reference converts BF16 small tensors at load (crates/model/src/mtp.rs:109-128)
     auto f32 = [&](const std::string &name, std::initializer_list<uint64_t> shape, float *dst) {
         if (!err.empty()) return;
         const GgufTensor *t = g.tensor(name);
+        if (t && t->type == GGML_BF16) {
+            err = tensor_check(t, name, GGML_BF16, shape);
+            if (!err.empty()) return;
+            const uint16_t *src = (const uint16_t *)g.data(*t);
+            const size_t n = (size_t)t->bytes() / 2;
+            std::vector<uint32_t> wide(n);
+            for (size_t i = 0; i < n; i++) wide[i] = (uint32_t)src[i] << 16;
+            if (hipMemcpy(dst, wide.data(), n * 4, hipMemcpyHostToDevice) != hipSuccess) rc = -2;
+            return;
+        }
         err = tensor_check(t, name, GGML_F32, shape);
         if (!err.empty()) return;
         if (hipMemcpyAsync(dst, g.data(*t), (size_t)t->bytes(), hipMemcpyHostToDevice, st) != hipSuccess) rc = -2;

@@ -115,3 +115,54 @@ def test_repack_q8_0_splits_ggml_blocks(dev):
     assert np.array_equal(y.cpu().numpy().view(np.uint32), O.gemv_q8_0(q, d, xq, xd).view(np.uint32))
     with pytest.raises(RuntimeError):
         A.repack_q8_0(torch.zeros((2, 34), dtype=torch.uint8, device=dev), 48)
+
+
+def test_bf16_routers_load_as_their_f32_widening():
+    """BF16 routers (the Qwen3.6 file's MTP layer has them) are widened to f32 at load, as the
+    reference converts BF16 small tensors (crates/model/src/mtp.rs:109-128): a file with BF16 routers
+    decodes bit for bit like the same file with those values stored as F32"""
+    import oxe_amd as A
+    d = O.desc_small()
+    conv = {f"blk.{il}.{n}" for il in (0, d.n_layer) for n in ("ffn_gate_inp.weight", "ffn_gate_inp_shexp.weight")}
+
+    def bf16_bits(x):
+        u = np.ascontiguousarray(x, np.float32).view(np.uint32).astype(np.uint64)
+        r = (u + 0x7FFF + ((u >> 16) & 1)) >> 16          # round to nearest even
+        return r.astype(np.uint16)
+
+    def variant(as_bf16):
+        out = []
+        for name, ty, shape, payload in W.synth_model_tensors(O, d, SEED):
+            if name in conv:
+                import io
+                buf = io.BytesIO()
+                payload(buf)
+                b = bf16_bits(np.frombuffer(buf.getvalue(), np.float32))
+                data = b.tobytes() if as_bf16 else (b.astype(np.uint32) << 16).tobytes()
+                out.append((name, W.GGML["BF16"] if as_bf16 else ty, shape, (lambda data: lambda f: f.write(data))(data)))
+            else:
+                out.append((name, ty, shape, payload))
+        return out
+
+    paths = [os.path.join(scratch_dir(), f"oxe_test_bf16_{i}_{os.getpid()}.gguf") for i in range(2)]
+    try:
+        for p, as_bf16 in zip(paths, (False, True)):
+            print(f"writing {'BF16' if as_bf16 else 'F32'} routers", flush=True)
+            W.write(p, W.qwen35moe_meta(d), variant(as_bf16))
+        ga, gb = A.Engine.from_gguf(paths[0], n_ctx=512), A.Engine.from_gguf(paths[1], n_ctx=512)
+        toks = [int(v) % d.n_vocab for v in O.bench_prompt(24)]
+        assert ga.prefill(toks) == gb.prefill(toks)
+        x = ga.step(3)
+        assert gb.step(3) == x
+        for _ in range(3):
+            ra, rb = ga.mtp_step(x), gb.mtp_step(x)
+            assert ra == rb
+            x = ra[-1]
+        assert np.array_equal(bits(ga.logits(0)), bits(gb.logits(0)))
+        assert np.array_equal(bits(ga.hidden(0)), bits(gb.hidden(0)))
+        ga.close()
+        gb.close()
+    finally:
+        for p in paths:
+            if os.path.exists(p):
+                os.remove(p)
