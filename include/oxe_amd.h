@@ -217,8 +217,8 @@ OXE_API int oxe_mtp_prefill(oxe_engine *e, const uint32_t *toks, int n, uint32_t
  * engine state, MTP KV and *next as oxe_mtp_prefill. */
 OXE_API int oxe_mtp_prefill_batched(oxe_engine *e, const uint32_t *toks, int n, uint32_t *next);
 /* One speculative step from token x (MtpDriver::step, mtp.rs:522-592), host-driven: out[0..n_out)
- * = the greedy tokens that follow (accepted drafts + bonus; room for depth + 1). override_d1 >= 0 replaces the draft
- * (the reference's draft_override test hook, mtp.rs:328-330). */
+ * = the greedy tokens that follow (accepted drafts + bonus; room for depth + 1). override_d1 >= 0
+ * replaces the first draft (the reference's draft_override test hook, mtp.rs:328-330). */
 OXE_API int oxe_mtp_step(oxe_engine *e, uint32_t x, uint32_t *out, int *n_out, int64_t override_d1);
 /* One plain target step from x that keeps the MTP catch-up in sync (MtpDriver::step_plain,
  * mtp.rs:504-515); *out = argmax after x. */
