@@ -155,6 +155,29 @@ def test_prefill_across_chunks():
     b.close()
 
 
+def test_prefill_per_head_attention_path():
+    """5000 tokens: the third chunk's score rows reach 5120 positions, beyond the kv-head-shared
+    kernel's LDS (4800), so its attention runs on the per-head kernel; equal to 2-token verify
+    decoding bit for bit (logits, hidden state, KV and recurrent state)"""
+    d = O.desc_small()
+    n = 5000
+    toks = prompt(d, n, salt=3)
+    a, b = engine(d, 5120), engine(d, 5120)
+    print(f"prefill n={n}", flush=True)
+    nx = a.prefill(toks)
+    x = None
+    for i in range(0, n, 2):
+        g = b.verify(toks[i:i + 2])
+        b.commit(2)
+        x = int(g[-1])
+    assert nx == x
+    assert np.array_equal(bits(a.logits(0)), bits(b.logits(1)))
+    assert np.array_equal(bits(a.hidden(0)), bits(b.hidden(1)))
+    assert_same_state(a, b, d, f"{n} tokens")
+    a.close()
+    b.close()
+
+
 def test_mtp_prefill_batched_equals_mtp_prefill():
     """MtpDriver::prefill_batched: the same target state, MTP KV and speculative steps as the
     2-token-verify prompt path"""
