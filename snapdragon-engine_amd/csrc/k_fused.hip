@@ -31,18 +31,43 @@ constexpr int SC_KS = HD + 32;                // LDS row stride of cached K rows
                                               // wave quarter fall on distinct banks)
 constexpr uint32_t SPIN_MAX = 400000;         // ~0.4 s at one device-scope load per iteration
 
+// ---- address-space views ------------------------------------------------------------------------
+// The phases are separate (non-inlined) functions, so pointers reach them as generic pointers and
+// plain accesses compile to flat instructions. A flat access counts on both the vector-memory and
+// the LDS wait counters, so an LDS wait would also wait for every weight load in flight. Device
+// memory is therefore read and written through global-space views, and the run's arguments (not
+// written during the launch) through a uniform constant-space view (scalar loads).
+#define FZ_GAS __attribute__((address_space(1)))
+#define FZ_CAS __attribute__((address_space(4)))
+template <int N> struct RawOf;   // a plain type of N bytes (no constructors, so it loads from any space)
+template <> struct RawOf<2> { using T = uint16_t; };
+template <> struct RawOf<4> { using T = uint32_t; };
+template <> struct RawOf<8> { using T = uint32_t __attribute__((ext_vector_type(2))); };
+template <> struct RawOf<16> { using T = uint32_t __attribute__((ext_vector_type(4))); };
+template <class T>
+OXE_DEV T gld(const T *p) {
+    using R = typename RawOf<sizeof(T)>::T;
+    return __builtin_bit_cast(T, *(const FZ_GAS R *)p);
+}
+template <class T>
+OXE_DEV const FZ_CAS T *uni(const T *p) {
+    const uint64_t v = (uint64_t)p;
+    return (const FZ_CAS T *)(((uint64_t)__builtin_amdgcn_readfirstlane((uint32_t)(v >> 32)) << 32) |
+                              (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)v));
+}
+
 // ---- device-scope accesses for data exchanged inside the launch -----------------------------
-OXE_DEV void cst(float *p, float v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
-OXE_DEV float cld(const float *p) { return __hip_atomic_load((float *)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
-OXE_DEV void cst32(void *p, uint32_t v) { __hip_atomic_store((uint32_t *)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
-OXE_DEV uint32_t cld32(const void *p) { return __hip_atomic_load((uint32_t *)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
-OXE_DEV void cst16(uint16_t *p, uint16_t v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
-OXE_DEV uint16_t cld16(const uint16_t *p) { return __hip_atomic_load((uint16_t *)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+OXE_DEV void cst(float *p, float v) { __hip_atomic_store((FZ_GAS float *)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+OXE_DEV float cld(const float *p) { return __hip_atomic_load((FZ_GAS float *)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+OXE_DEV void cst32(void *p, uint32_t v) { __hip_atomic_store((FZ_GAS uint32_t *)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+OXE_DEV uint32_t cld32(const void *p) { return __hip_atomic_load((FZ_GAS uint32_t *)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+OXE_DEV void cst16(uint16_t *p, uint16_t v) { __hip_atomic_store((FZ_GAS uint16_t *)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+OXE_DEV uint16_t cld16(const uint16_t *p) { return __hip_atomic_load((FZ_GAS uint16_t *)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
 OXE_DEV void cst64(void *p, unsigned long long v) {
-    __hip_atomic_store((unsigned long long *)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store((FZ_GAS unsigned long long *)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 OXE_DEV unsigned long long cld64(const void *p) {
-    return __hip_atomic_load((unsigned long long *)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return __hip_atomic_load((FZ_GAS unsigned long long *)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 OXE_DEV uint4 cld128(const void *p) {
     const unsigned long long a = cld64(p), b = cld64((const char *)p + 8);
@@ -133,13 +158,16 @@ OXE_DEV void wload(WSlice<K, MAXP> &s, const int8_t *__restrict__ wq, const uint
                    RowOf rowof) {
     using G = KG<K>;
     const int t = threadIdx.x, c = t % G::KCH, rs = t / G::KCH;
+    // rows past nr load row nr - 1 again (wdot ignores them): no per-load branch, so the loads are
+    // issued back to back without a wait between them; nothing is loaded (or read) when nr = 0
+    if (nr <= 0) return;
 #pragma unroll
     for (int p = 0; p < MAXP; p++) {
         const int rl = p * G::RPP + rs;
-        s.w[p] = rl < nr ? *(const uint4 *)(wq + rowof(rl) * K + c * 16) : make_uint4(0, 0, 0, 0);
+        s.w[p] = gld((const uint4 *)(wq + rowof(rl < nr ? rl : nr - 1) * K + c * 16));
     }
     const int sr = t / G::SPR, sk = t % G::SPR;
-    s.s = sr < nr ? *(const uint4 *)(wd + rowof(sr) * G::NB + sk * 8) : make_uint4(0, 0, 0, 0);
+    s.s = gld((const uint4 *)(wd + rowof(sr < nr ? sr : nr - 1) * G::NB + sk * 8));
 }
 
 // g.out[l][r] = row r . lane l for the slice's nr rows (activation codes xq [NL][xq_ld] and scales
@@ -149,13 +177,8 @@ OXE_DEV void wdot(const WSlice<K, MAXP> &s, int nr, const int8_t *xq, int xq_ld,
                   GSm<K, MAXP * KG<K>::RPP, NL> &g) {
     using G = KG<K>;
     const int t = threadIdx.x, c = t % G::KCH, rs = t / G::KCH;
-    {
-        const int sr = t / G::SPR, sk = t % G::SPR;
-        if (sr < nr) {
-            uint32_t *d = &g.wd[sr * G::WDS + sk * 4];
-            d[0] = s.s.x; d[1] = s.s.y; d[2] = s.s.z; d[3] = s.s.w;
-        }
-    }
+    // codes first, in load order: each pass waits only for its own chunk; the scales (loaded last)
+    // go to LDS after the dots
     uint4 xa[NL];
 #pragma unroll
     for (int l = 0; l < NL; l++) xa[l] = *(const uint4 *)(xq + l * xq_ld + c * 16);
@@ -167,6 +190,13 @@ OXE_DEV void wdot(const WSlice<K, MAXP> &s, int nr, const int8_t *xq, int xq_ld,
             int32_t v = dot16(s.w[p], xa[l], 0);
             v += dpp_i<DPP_XOR1>(v);  // the other half of the 32-code block sits in the adjacent lane
             if ((c & 1) == 0 && rl < nr) g.isum[l][rl][c >> 1] = v;
+        }
+    }
+    {
+        const int sr = t / G::SPR, sk = t % G::SPR;
+        if (sr < nr) {
+            uint32_t *d = &g.wd[sr * G::WDS + sk * 4];
+            d[0] = s.s.x; d[1] = s.s.y; d[2] = s.s.z; d[3] = s.s.w;
         }
     }
     __syncthreads();
@@ -220,7 +250,7 @@ struct W8 {
 OXE_DEV W8 wload8(const float *w) {
     W8 r;
     const int tt = threadIdx.x & 255;
-    const float4 a = *(const float4 *)(w + 8 * tt), b = *(const float4 *)(w + 8 * tt + 4);
+    const float4 a = gld((const float4 *)(w + 8 * tt)), b = gld((const float4 *)(w + 8 * tt + 4));
     r.v[0] = a.x; r.v[1] = a.y; r.v[2] = a.z; r.v[3] = a.w; r.v[4] = b.x; r.v[5] = b.y; r.v[6] = b.z; r.v[7] = b.w;
     return r;
 }
@@ -244,8 +274,8 @@ OXE_DEV void cget8(const float *x, float v[8]) {
 // dequantize_row_q8_0 (quants_base.c:64-78) of elements [8 tt, 8 tt + 8) of token row tok
 OXE_DEV void embed8t(const Q8W &emb, uint32_t tok, int tt, float v[8]) {
     const int8_t *q = emb.q + (int64_t)tok * E + 8 * tt;
-    const float d = h2f(emb.d[(int64_t)tok * (E / 32) + (8 * tt) / 32]);
-    const uint2 c = *(const uint2 *)q;
+    const float d = h2f(gld(emb.d + (int64_t)tok * (E / 32) + (8 * tt) / 32));
+    const uint2 c = gld((const uint2 *)q);
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         v[i] = (float)(int8_t)(c.x >> (8 * i)) * d;
@@ -401,22 +431,30 @@ namespace fz {
 template <int NL>
 struct Ctx {
     const RunCtl *ctl;
-    const FusedArgs *a;
+    const FZ_CAS FusedArgs *a;
     PhaseSm<NL> *sm;
     Persist<NL> *ps;
     unsigned char *dyn;
     Bar bar;
+    unsigned long long *trace;
     int nl, G, b;
 };
 
 template <int NL>
-OXE_DEV Ctx<NL> make_ctx(const RunCtl *ctl, const FusedArgs *a) {
+OXE_DEV Ctx<NL> make_ctx(const RunCtl *ctl, const FusedArgs *ap) {
     static_assert(NL == OXE_NL, "one lane count");
-    Ctx<NL> c{ctl, a, (PhaseSm<NL> *)fz_dyn, &fz_ps, fz_dyn, Bar{a->sync, fz_ps.round}, 0, 0, 0};
+    const FZ_CAS FusedArgs *a = uni(ap);
+    Ctx<NL> c{ctl, a, (PhaseSm<NL> *)fz_dyn, &fz_ps, fz_dyn, Bar{a->sync, fz_ps.round}, a->trace, 0, 0, 0};
     c.nl = ctl->nl < 1 ? 1 : (ctl->nl > NL ? NL : ctl->nl);
     c.G = gridDim.x;
     c.b = blockIdx.x;
     return c;
+}
+
+// layer il's tensors (il is uniform: read with scalar loads)
+template <int NL>
+OXE_DEV const FZ_CAS LayerDev &layer_of(const Ctx<NL> &c, int il) {
+    return *(uni(c.a->layers) + __builtin_amdgcn_readfirstlane(il));
 }
 
 #define FZ_PHASE __device__ __attribute__((noinline))
@@ -426,18 +464,18 @@ OXE_DEV Ctx<NL> make_ctx(const RunCtl *ctl, const FusedArgs *a) {
 enum { TP_PROJ = 1, TP_DN, TP_SCORES, TP_PV, TP_OUT, TP_ROUTER, TP_EXPERTS, TP_DOWN, TP_ENTRY, TP_HEAD };
 template <int NL>
 OXE_DEV void tr_start(Ctx<NL> &c) {
-    if (c.a->trace && threadIdx.x == 0) c.ps->t_start = wall_clock64();
+    if (c.trace && threadIdx.x == 0) c.ps->t_start = wall_clock64();
 }
 template <int NL>
 OXE_DEV void tr_pass(Ctx<NL> &c) {
-    if (c.a->trace && threadIdx.x == 0) c.ps->t_mark = c.ps->t_pass = wall_clock64();
+    if (c.trace && threadIdx.x == 0) c.ps->t_mark = c.ps->t_pass = wall_clock64();
 }
 // sub-step marker inside a phase: an event (id, previous mark, 0, now)
 template <int NL>
 OXE_DEV void tr_mark(Ctx<NL> &c, int id) {
-    if (c.a->trace && threadIdx.x == 0 && c.ps->tev < FZ_TRACE_EV) {
+    if (c.trace && threadIdx.x == 0 && c.ps->tev < FZ_TRACE_EV) {
         const unsigned long long now = wall_clock64();
-        unsigned long long *e = c.a->trace + ((size_t)c.b * FZ_TRACE_EV + c.ps->tev++) * 4;
+        unsigned long long *e = c.trace + ((size_t)c.b * FZ_TRACE_EV + c.ps->tev++) * 4;
         e[0] = (unsigned long long)id;
         e[1] = c.ps->t_mark;
         e[2] = 0ull;
@@ -447,8 +485,8 @@ OXE_DEV void tr_mark(Ctx<NL> &c, int id) {
 }
 template <int NL>
 OXE_DEV void tr_end(Ctx<NL> &c, int id) {
-    if (c.a->trace && threadIdx.x == 0 && c.ps->tev < FZ_TRACE_EV) {
-        unsigned long long *e = c.a->trace + ((size_t)c.b * FZ_TRACE_EV + c.ps->tev++) * 4;
+    if (c.trace && threadIdx.x == 0 && c.ps->tev < FZ_TRACE_EV) {
+        unsigned long long *e = c.trace + ((size_t)c.b * FZ_TRACE_EV + c.ps->tev++) * 4;
         e[0] = (unsigned long long)id;
         e[1] = c.ps->t_start;
         e[2] = c.ps->t_pass;
@@ -464,8 +502,8 @@ template <int NL>
 FZ_PHASE bool phase_proj(const RunCtl *ctl, const FusedArgs *ap, int il, bool embed, const float *x, int r_begin, int r_end) {
     Ctx<NL> c = make_ctx<NL>(ctl, ap);
     tr_start(c);
-    const LayerDev &L = ap->layers[il];
-    const FusedArgs &a = *c.a;
+    const FZ_CAS FusedArgs &a = *c.a;
+    const FZ_CAS LayerDev &L = layer_of(c, il);
     auto &s = c.sm->proj;
     const int n = r_end - r_begin;
     const int r0 = r_begin + (int)((int64_t)n * c.b / c.G), r1 = r_begin + (int)((int64_t)n * (c.b + 1) / c.G);
@@ -475,7 +513,8 @@ FZ_PHASE bool phase_proj(const RunCtl *ctl, const FusedArgs *ap, int il, bool em
     const W8 nw = wload8(L.attn_norm);
     if (!wait(c.bar, &c.ps->ok)) return false;
     tr_pass(c);
-    prologue<NL>(c.nl, c.ctl, embed ? &a.m.tok_embd : nullptr, x, E, true, nw, a.m.eps, s.xf, &s.xq[0][0], E,
+    const Q8W emb{a.m.tok_embd.q, a.m.tok_embd.d};
+    prologue<NL>(c.nl, c.ctl, embed ? &emb : nullptr, x, E, true, nw, a.m.eps, s.xf, &s.xq[0][0], E,
                  &s.xd[0][0], E / 32, s.ns, nullptr);
     tr_mark(c, 111);
     if (embed && c.b == 0) {
@@ -525,8 +564,8 @@ template <int NL>
 FZ_PHASE bool phase_dn(const RunCtl *ctl, const FusedArgs *ap, int il) {
     Ctx<NL> c = make_ctx<NL>(ctl, ap);
     tr_start(c);
-    const LayerDev &L = ap->layers[il];
-    const FusedArgs &a = *c.a;
+    const FZ_CAS FusedArgs &a = *c.a;
+    const FZ_CAS LayerDev &L = layer_of(c, il);
     auto &s = c.sm->dn;
     const int t = threadIdx.x, w = t >> 6, lane = t & 63;
     const int vh = c.b / DN_WPH, kh = vh % NKH, row0 = (c.b % DN_WPH) * DN_RPW;
@@ -557,7 +596,7 @@ FZ_PHASE bool phase_dn(const RunCtl *ctl, const FusedArgs *ap, int il) {
     if (conv) {
         const float *st = conv_state + (int64_t)cur * conv_slot + (int64_t)ch * (KC - 1);
         s0 = st[0]; s1 = st[1]; s2 = st[2];
-        const float4 c4 = *(const float4 *)(L.conv + (int64_t)ch * KC);
+        const float4 c4 = gld((const float4 *)(L.conv + (int64_t)ch * KC));
         cw[0] = c4.x; cw[1] = c4.y; cw[2] = c4.z; cw[3] = c4.w;
     }
     // gate thread of lane gl (wave 5) and the gated-norm weights (waves < NL)
@@ -698,8 +737,8 @@ template <int NL>
 FZ_PHASE bool phase_out(const RunCtl *ctl, const FusedArgs *ap, int il, const float *x) {
     Ctx<NL> c = make_ctx<NL>(ctl, ap);
     tr_start(c);
-    const LayerDev &L = ap->layers[il];
-    const FusedArgs &a = *c.a;
+    const FZ_CAS FusedArgs &a = *c.a;
+    const FZ_CAS LayerDev &L = layer_of(c, il);
     auto &s = c.sm->out;
     const int t = threadIdx.x;
     const int r0 = 8 * c.b;
@@ -769,17 +808,17 @@ template <int NL>
 FZ_PHASE bool phase_router(const RunCtl *ctl, const FusedArgs *ap, int il) {
     Ctx<NL> c = make_ctx<NL>(ctl, ap);
     tr_start(c);
-    const LayerDev &L = ap->layers[il];
-    const FusedArgs &a = *c.a;
+    const FZ_CAS FusedArgs &a = *c.a;
+    const FZ_CAS LayerDev &L = layer_of(c, il);
     auto &s = c.sm->router;
     const int t = threadIdx.x;
     const int b = c.b;
     const bool shg = b == c.G - 1;
     const bool gu = b < 2 * FFSH / 8;   // 128 half tiles
     const int tile = b >> 1, hf = b & 1;
-    const float4 wrow = *(const float4 *)(L.router + (int64_t)b * E + 4 * t);
+    const float4 wrow = gld((const float4 *)(L.router + (int64_t)b * E + 4 * t));
     float4 wsg = make_float4(0, 0, 0, 0);
-    if (shg) wsg = *(const float4 *)(L.shexp_gate + 4 * t);
+    if (shg) wsg = gld((const float4 *)(L.shexp_gate + 4 * t));
     WSlice<E, 2> ws;
     auto rowof = [&](int rl) { return (int64_t)(tile * 16 + (rl < 4 ? hf * 4 + rl : 8 + hf * 4 + (rl - 4))); };
     wload<E, 2>(ws, L.shexp_gu.q, L.shexp_gu.d, gu ? 8 : 0, rowof);
@@ -863,8 +902,8 @@ template <int NL>
 FZ_PHASE bool phase_moe(const RunCtl *ctl, const FusedArgs *ap, int il) {
     Ctx<NL> c = make_ctx<NL>(ctl, ap);
     tr_start(c);
-    const LayerDev &L = ap->layers[il];
-    const FusedArgs &a = *c.a;
+    const FZ_CAS FusedArgs &a = *c.a;
+    const FZ_CAS LayerDev &L = layer_of(c, il);
     auto &se = c.sm->exp;
     auto &ps = *c.ps;
     const int t = threadIdx.x, b = c.b, nl = c.nl;
@@ -931,7 +970,6 @@ FZ_PHASE bool phase_moe(const RunCtl *ctl, const FusedArgs *ap, int il) {
     tr_mark(c, 102);
     // 3. gate/up + swiglu + Q8_0 of the group's 32 h values per lane
     if (gw) {
-        __syncthreads();
         tr_mark(c, 103);
         wdot<E, 16, NL>(ew, 64, &se.xq[0][0], E, &se.xd[0][0], E / 32, se.g);
         tr_mark(c, 104);
@@ -966,7 +1004,7 @@ FZ_PHASE bool phase_moe(const RunCtl *ctl, const FusedArgs *ap, int il) {
                 e = e < 0 ? 0 : (e >= NEXP ? NEXP - 1 : e);
                 base = L.exp_down.q + (int64_t)e * E * FF;
             }
-            dw[k] = *(const uint4 *)(base + (int64_t)(r0 + rr) * FF + 16 * ck);
+            dw[k] = gld((const uint4 *)(base + (int64_t)(r0 + rr) * FF + 16 * ck));
         }
     };
     constexpr int DW_PRE = 5;
@@ -982,7 +1020,7 @@ FZ_PHASE bool phase_moe(const RunCtl *ctl, const FusedArgs *ap, int il) {
             e = e < 0 ? 0 : (e >= NEXP ? NEXP - 1 : e);
             base = L.exp_down.d + (int64_t)e * E * (FF / 32);
         }
-        dsc = *(const uint4 *)(base + (int64_t)(r0 + srr) * (FF / 32) + shf * 8);
+        dsc = gld((const uint4 *)(base + (int64_t)(r0 + srr) * (FF / 32) + shf * 8));
     }
     if (!wait(c.bar, &ps.ok)) return false;
     tr_pass(c);
@@ -1089,7 +1127,7 @@ FZ_PHASE bool phase_moe(const RunCtl *ctl, const FusedArgs *ap, int il) {
 // attention scores (workgroup = kv head x 128 positions) with the query prologue (q_norm, RoPE,
 // f16) and the run's own K rows computed in place (k_norm, RoPE); the workgroup whose range holds
 // a new position writes its K cache row
-OXE_DEV uint16_t *kcache_layer(const FusedArgs &a, const LayerDev &L) {
+OXE_DEV uint16_t *kcache_layer(const FZ_CAS FusedArgs &a, const FZ_CAS LayerDev &L) {
     return a.m.kcache + (int64_t)L.index * NKV * a.m.n_ctx * HD;
 }
 
@@ -1113,8 +1151,8 @@ template <int NL>
 FZ_PHASE bool phase_scores(const RunCtl *ctl, const FusedArgs *ap, int il, bool seed_only) {
     Ctx<NL> c = make_ctx<NL>(ctl, ap);
     tr_start(c);
-    const LayerDev &L = ap->layers[il];
-    const FusedArgs &a = *c.a;
+    const FZ_CAS FusedArgs &a = *c.a;
+    const FZ_CAS LayerDev &L = layer_of(c, il);
     auto &s = c.sm->sc;
     const int t = threadIdx.x, w = t >> 6, lane = t & 63, nl = c.nl;
     const int pos0 = c.ctl->pos0, pmax = pos0 + nl - 1;
@@ -1125,7 +1163,7 @@ FZ_PHASE bool phase_scores(const RunCtl *ctl, const FusedArgs *ap, int il, bool 
     const uint16_t *kcl = kcache_layer(a, L) + (int64_t)kvh * a.m.n_ctx * HD;
     const int kp = t >> 5, kpart = t & 31;
     uint4 kpre = make_uint4(0, 0, 0, 0);
-    if (act && !seed_only && chunk0 * SC_P + kp < pos0) kpre = *(const uint4 *)(kcl + (int64_t)(chunk0 * SC_P + kp) * HD + 8 * kpart);
+    if (act && !seed_only && chunk0 * SC_P + kp < pos0) kpre = gld((const uint4 *)(kcl + (int64_t)(chunk0 * SC_P + kp) * HD + 8 * kpart));
     // per wave, its vectors' norm weights and RoPE rows (read-only), before the barrier
     const int kjob = w;                          // waves 0..NL-1: K row of lane w
     const int pk = pos0 + kjob;
@@ -1207,7 +1245,7 @@ FZ_PHASE bool phase_scores(const RunCtl *ctl, const FusedArgs *ap, int il, bool 
             if (chunk == chunk0) {
                 if (cb + kp < pos0) *(uint4 *)&s.krows[kp][8 * kpart] = kpre;
             } else if (cb + kp < pos0) {
-                *(uint4 *)&s.krows[kp][8 * kpart] = *(const uint4 *)(kcl + (int64_t)(cb + kp) * HD + 8 * kpart);
+                *(uint4 *)&s.krows[kp][8 * kpart] = gld((const uint4 *)(kcl + (int64_t)(cb + kp) * HD + 8 * kpart));
             }
             __syncthreads();
             const int p = cb + pp;
@@ -1266,8 +1304,8 @@ template <int NL>
 FZ_PHASE bool phase_pv(const RunCtl *ctl, const FusedArgs *ap, int il) {
     Ctx<NL> c = make_ctx<NL>(ctl, ap);
     tr_start(c);
-    const LayerDev &L = ap->layers[il];
-    const FusedArgs &a = *c.a;
+    const FZ_CAS FusedArgs &a = *c.a;
+    const FZ_CAS LayerDev &L = layer_of(c, il);
     const int t = threadIdx.x, nl = c.nl;
     constexpr int NCH = HD / PVD;
     const int hp = c.b % PV_HP;
@@ -1290,7 +1328,7 @@ FZ_PHASE bool phase_pv(const RunCtl *ctl, const FusedArgs *ap, int il) {
 #pragma unroll
     for (int k = 0; k < PV_VK; k++) {
         const int i = t + FT * k, r = i / nvc, ch = i % nvc;
-        vpre[k] = (act && i < PVD * nvc && 8 * ch + 7 < pos0) ? *(const uint4 *)(vt + (int64_t)r * n_ctx + 8 * ch)
+        vpre[k] = (act && i < PVD * nvc && 8 * ch + 7 < pos0) ? gld((const uint4 *)(vt + (int64_t)r * n_ctx + 8 * ch))
                                                               : make_uint4(0, 0, 0, 0);
     }
     if (!wait(c.bar, &c.ps->ok)) return false;
@@ -1422,7 +1460,7 @@ FZ_PHASE bool phase_pv(const RunCtl *ctl, const FusedArgs *ap, int il) {
         for (int i = t + FT * PV_VK; i < PVD * nvc; i += FT) {
             const int r = i / nvc, ch = i % nvc;
             const uint16_t *src = vt + (int64_t)r * n_ctx + 8 * ch;
-            *(uint4 *)(s_v + r * vs + 8 * ch) = 8 * ch + 7 < pos0 ? *(const uint4 *)src : cld128(src);
+            *(uint4 *)(s_v + r * vs + 8 * ch) = 8 * ch + 7 < pos0 ? gld((const uint4 *)src) : cld128(src);
         }
         if (cp == 0) sg = sigmoid_c(sg);
         __syncthreads();
@@ -1437,7 +1475,7 @@ FZ_PHASE bool phase_pv(const RunCtl *ctl, const FusedArgs *ap, int il) {
             acc = __builtin_elementwise_fma(u2h2f(*(const uint32_t *)(vrow + 32 * s)), u2h2f(prow[32 * s]), acc);
         for (int s = nss; s < ns; s++) {
             const uint16_t *src = vt + (int64_t)d * n_ctx + 32 * s + 2 * cp;
-            const uint32_t vw = 32 * s + 2 * cp + 1 >= pos0 ? cld32(src) : *(const uint32_t *)src;
+            const uint32_t vw = 32 * s + 2 * cp + 1 >= pos0 ? cld32(src) : gld((const uint32_t *)src);
             acc = __builtin_elementwise_fma(u2h2f(vw), u2h2f(prow[32 * s]), acc);
         }
         // GGML_F16x8_REDUCE: accumulator j += j ^ 2 (cp ^ 8), j += j ^ 1 (cp ^ 4); widen halves
@@ -1462,15 +1500,16 @@ template <int NL>
 FZ_PHASE bool phase_entry(const RunCtl *ctl, const FusedArgs *ap, int il) {
     Ctx<NL> c = make_ctx<NL>(ctl, ap);
     tr_start(c);
-    const LayerDev &L = ap->layers[il];
-    const FusedArgs &a = *c.a;
+    const FZ_CAS FusedArgs &a = *c.a;
+    const FZ_CAS LayerDev &L = layer_of(c, il);
     auto &s = c.sm->entry;
     const int t = threadIdx.x, r0 = 8 * c.b;
     WSlice<2 * E, 4> ws;
     wload<2 * E, 4>(ws, L.eh_proj.q, L.eh_proj.d, 8, [&](int rl) { return (int64_t)(r0 + rl); });
     const W8 nwe = wload8(L.enorm), nwh = wload8(L.hnorm);
     // no barrier precedes the entry (its inputs come from earlier launches)
-    prologue<NL>(c.nl, c.ctl, &a.m.tok_embd, nullptr, 0, false, nwe, a.m.eps, s.xf, &s.xq[0][0], 2 * E, &s.xd[0][0],
+    const Q8W emb{a.m.tok_embd.q, a.m.tok_embd.d};
+    prologue<NL>(c.nl, c.ctl, &emb, nullptr, 0, false, nwe, a.m.eps, s.xf, &s.xq[0][0], 2 * E, &s.xd[0][0],
                  2 * E / 32, s.ns, nullptr);
     {
         // h of each lane: hid[hin_sel[l]]
@@ -1511,7 +1550,7 @@ template <int NL>
 FZ_PHASE bool phase_head(const RunCtl *ctl, const FusedArgs *ap, const float *norm_w) {
     Ctx<NL> c = make_ctx<NL>(ctl, ap);
     tr_start(c);
-    const FusedArgs &a = *c.a;
+    const FZ_CAS FusedArgs &a = *c.a;
     auto &s = c.sm->head;
     const int t = threadIdx.x, nl = c.nl, mask = c.ctl->head_mask;
     const int64_t V = a.m.output.rows;
