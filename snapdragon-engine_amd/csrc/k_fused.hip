@@ -989,37 +989,30 @@ FZ_PHASE bool phase_moe(const RunCtl *ctl, const FusedArgs *ap, int il) {
     arrive(c.bar);
     // the down rows of every union expert and the shared expert: the first DW_PRE units per
     // thread in flight across the barrier, the rest issued behind the phase's inputs (a barrier
-    // poll waits behind every load the workgroup has outstanding)
+    // poll waits behind every load the workgroup has outstanding). Every load of this phase is
+    // unconditional (a load skipped on some path makes the compiler's wait for an earlier one
+    // conservative, i.e. a wait for all): units past the union re-read the shared expert's rows
+    // (cached), absent lanes and union slots read stale buffer contents, and nothing reads those.
     const int r0 = 8 * b;
     const int uh = t >> 8, rr = (t >> 5) & 7, ck = t & 31;
+    auto unit_q = [&](int u) -> const int8_t * {
+        int e = ps.uni[u < OXE_MAX_UNION ? u : 0];
+        e = e < 0 ? 0 : (e >= NEXP ? NEXP - 1 : e);
+        return u < nu && u < OXE_MAX_UNION ? L.exp_down.q + (int64_t)e * E * FF : L.shexp_down.q;
+    };
     uint4 dw[9];
     auto dload = [&](int k) {
-        const int u = 2 * k + uh;
-        dw[k] = make_uint4(0, 0, 0, 0);
-        if (u < DW_UNITS && (u == OXE_MAX_UNION || u < nu)) {
-            const int8_t *base;
-            if (u == OXE_MAX_UNION) base = L.shexp_down.q;
-            else {
-                int e = ps.uni[u];
-                e = e < 0 ? 0 : (e >= NEXP ? NEXP - 1 : e);
-                base = L.exp_down.q + (int64_t)e * E * FF;
-            }
-            dw[k] = gld((const uint4 *)(base + (int64_t)(r0 + rr) * FF + 16 * ck));
-        }
+        dw[k] = gld((const uint4 *)(unit_q(2 * k + uh) + (int64_t)(r0 + rr) * FF + 16 * ck));
     };
     constexpr int DW_PRE = 5;
 #pragma unroll
     for (int k = 0; k < DW_PRE; k++) dload(k);
-    uint4 dsc = make_uint4(0, 0, 0, 0);
-    const int su = t / 16, srr = (t % 16) / 2, shf = t % 2;
-    if (t < DW_UNITS * 16 && (su == OXE_MAX_UNION || su < nu)) {
-        const uint16_t *base;
-        if (su == OXE_MAX_UNION) base = L.shexp_down.d;
-        else {
-            int e = ps.uni[su];
-            e = e < 0 ? 0 : (e >= NEXP ? NEXP - 1 : e);
-            base = L.exp_down.d + (int64_t)e * E * (FF / 32);
-        }
+    const int su = t / 16 < DW_UNITS ? t / 16 : OXE_MAX_UNION, srr = (t % 16) / 2, shf = t % 2;
+    uint4 dsc;
+    {
+        int e = ps.uni[su < OXE_MAX_UNION ? su : 0];
+        e = e < 0 ? 0 : (e >= NEXP ? NEXP - 1 : e);
+        const uint16_t *base = su < nu && su < OXE_MAX_UNION ? L.exp_down.d + (int64_t)e * E * (FF / 32) : L.shexp_down.d;
         dsc = gld((const uint4 *)(base + (int64_t)(r0 + srr) * (FF / 32) + shf * 8));
     }
     if (!wait(c.bar, &ps.ok)) return false;
@@ -1029,27 +1022,15 @@ FZ_PHASE bool phase_moe(const RunCtl *ctl, const FusedArgs *ap, int il) {
     auto &sd = c.sm->down;
     float hsv[NL * FFSH / FT];
 #pragma unroll
-    for (int k = 0; k < NL * FFSH / FT; k++) {
-        const int i = t + FT * k, l = i / FFSH;
-        hsv[k] = l < nl ? cld(a.b.hsh + i) : 0.0f;
-    }
+    for (int k = 0; k < NL * FFSH / FT; k++) hsv[k] = cld(a.b.hsh + t + FT * k);
     uint4 hqv[NL * OXE_MAX_UNION * (FF / 16) / FT];
 #pragma unroll
-    for (int k = 0; k < NL * OXE_MAX_UNION * (FF / 16) / FT; k++) {
-        const int i = t + FT * k;
-        const int l = i / (OXE_MAX_UNION * (FF / 16)), u = (i / (FF / 16)) % OXE_MAX_UNION, kk = i % (FF / 16);
-        hqv[k] = (l < nl && u < nu) ? cld128(a.hq + ((int64_t)l * OXE_MAX_UNION + u) * FF + 16 * kk) : make_uint4(0, 0, 0, 0);
-    }
-    uint16_t hdv = 0;
-    if (t < NL * OXE_MAX_UNION * (FF / 32)) {
-        const int l = t / (OXE_MAX_UNION * (FF / 32)), u = (t / (FF / 32)) % OXE_MAX_UNION, k = t % (FF / 32);
-        hdv = (l < nl && u < nu) ? cld16(a.hd + ((int64_t)l * OXE_MAX_UNION + u) * (FF / 32) + k) : (uint16_t)0;
-    }
-    float x1v = 0.0f, sgv = 0.0f;
-    if (t < NL * 8 && t / 8 < nl) {
-        x1v = cld(a.b.x1 + (int64_t)(t / 8) * E + r0 + t % 8);
-        sgv = cld(a.b.sh_gate + t / 8);
-    }
+    for (int k = 0; k < NL * OXE_MAX_UNION * (FF / 16) / FT; k++) hqv[k] = cld128(a.hq + 16 * (t + FT * k));
+    constexpr int NHD = NL * OXE_MAX_UNION * (FF / 32);
+    const uint16_t hdv = cld16(a.hd + (t < NHD ? t : NHD - 1));
+    const int tx = t < NL * 8 ? t : NL * 8 - 1;
+    const float x1v = cld(a.b.x1 + (int64_t)(tx / 8) * E + r0 + tx % 8);
+    const float sgv = cld(a.b.sh_gate + tx / 8);
 #pragma unroll
     for (int k = DW_PRE; k < 9; k++) dload(k);
     // Q8_0 of the shared expert's h: element t of lane k in thread t, a block per half wave
