@@ -272,9 +272,9 @@ OXE_DEV void cget8(const float *x, float v[8]) {
     }
 }
 // dequantize_row_q8_0 (quants_base.c:64-78) of elements [8 tt, 8 tt + 8) of token row tok
-OXE_DEV void embed8t(const Q8W &emb, uint32_t tok, int tt, float v[8]) {
-    const int8_t *q = emb.q + (int64_t)tok * E + 8 * tt;
-    const float d = h2f(gld(emb.d + (int64_t)tok * (E / 32) + (8 * tt) / 32));
+OXE_DEV void embed8t(const int8_t *eq, const uint16_t *ed, uint32_t tok, int tt, float v[8]) {
+    const int8_t *q = eq + (int64_t)tok * E + 8 * tt;
+    const float d = h2f(gld(ed + (int64_t)tok * (E / 32) + (8 * tt) / 32));
     const uint2 c = gld((const uint2 *)q);
 #pragma unroll
     for (int i = 0; i < 4; i++) {
@@ -283,18 +283,34 @@ OXE_DEV void embed8t(const Q8W &emb, uint32_t tok, int tt, float v[8]) {
     }
 }
 
+// entry l (divergent) of a per-lane array of the run control, from uniform scalar loads
+// (each entry made wave-uniform first, so the selection stays a register select and the reads stay
+// scalar loads)
+template <int NL, class T>
+OXE_DEV T lane_pick(const FZ_CAS T *v, int l) {
+    static_assert(sizeof(T) == 4, "32-bit entries");
+    T r = (T)__builtin_amdgcn_readfirstlane((int)v[0]);
+#pragma unroll
+    for (int i = 1; i < NL; i++) {
+        const T vi = (T)__builtin_amdgcn_readfirstlane((int)v[i]);
+        r = l == i ? vi : r;
+    }
+    return r;
+}
+
 // The run's lanes normalised with w and quantised to xq/xd (LDS). Source per lane: the token
-// embedding (emb != null), a vector written in this launch (coherent), or one from an earlier launch.
+// embedding (eq != null), a vector written in this launch (coherent), or one from an earlier launch.
 // xf: LDS staging of the raw vectors; xn (optional): the normalised f32 vectors.
 template <int NL>
-OXE_DEV void prologue(int nl, const RunCtl *ctl, const Q8W *emb, const float *src, int64_t src_ld, bool coherent,
+OXE_DEV void prologue(int nl, const FZ_CAS RunCtl *ctl, const int8_t *eq, const uint16_t *ed, const float *src,
+                      int64_t src_ld, bool coherent,
                       const W8 &w, float eps, float (*xf)[E], int8_t *xq, int xq_ld, uint16_t *xd, int xd_ld,
                       NormSm &ns, float (*xn)[E]) {
     const int t = threadIdx.x, l = t >> 8, tt = t & 255;
     float v[8];
     const bool act = l < NL && l < nl;
     if (act) {
-        if (emb) embed8t(*emb, ctl->tok[l], tt, v);
+        if (eq) embed8t(eq, ed, lane_pick<NL>(ctl->tok, l), tt, v);
         else if (coherent) cget8(src + l * src_ld + 8 * tt, v);
         else get8(src + l * src_ld + 8 * tt, v);
     } else {
@@ -430,7 +446,7 @@ namespace fz {
 
 template <int NL>
 struct Ctx {
-    const RunCtl *ctl;
+    const FZ_CAS RunCtl *ctl;   // written by the control kernels before the launch, read-only in it
     const FZ_CAS FusedArgs *a;
     PhaseSm<NL> *sm;
     Persist<NL> *ps;
@@ -444,8 +460,8 @@ template <int NL>
 OXE_DEV Ctx<NL> make_ctx(const RunCtl *ctl, const FusedArgs *ap) {
     static_assert(NL == OXE_NL, "one lane count");
     const FZ_CAS FusedArgs *a = uni(ap);
-    Ctx<NL> c{ctl, a, (PhaseSm<NL> *)fz_dyn, &fz_ps, fz_dyn, Bar{a->sync, fz_ps.round}, a->trace, 0, 0, 0};
-    c.nl = ctl->nl < 1 ? 1 : (ctl->nl > NL ? NL : ctl->nl);
+    Ctx<NL> c{uni(ctl), a, (PhaseSm<NL> *)fz_dyn, &fz_ps, fz_dyn, Bar{a->sync, fz_ps.round}, a->trace, 0, 0, 0};
+    c.nl = c.ctl->nl < 1 ? 1 : (c.ctl->nl > NL ? NL : c.ctl->nl);
     c.G = gridDim.x;
     c.b = blockIdx.x;
     return c;
@@ -513,8 +529,7 @@ FZ_PHASE bool phase_proj(const RunCtl *ctl, const FusedArgs *ap, int il, bool em
     const W8 nw = wload8(L.attn_norm);
     if (!wait(c.bar, &c.ps->ok)) return false;
     tr_pass(c);
-    const Q8W emb{a.m.tok_embd.q, a.m.tok_embd.d};
-    prologue<NL>(c.nl, c.ctl, embed ? &emb : nullptr, x, E, true, nw, a.m.eps, s.xf, &s.xq[0][0], E,
+    prologue<NL>(c.nl, c.ctl, embed ? a.m.tok_embd.q : nullptr, a.m.tok_embd.d, x, E, true, nw, a.m.eps, s.xf, &s.xq[0][0], E,
                  &s.xd[0][0], E / 32, s.ns, nullptr);
     tr_mark(c, 111);
     if (embed && c.b == 0) {
@@ -835,7 +850,7 @@ FZ_PHASE bool phase_router(const RunCtl *ctl, const FusedArgs *ap, int il) {
             if (shg) s.sg[e % 16][e / 16] = gr[k];
         }
     }
-    prologue<NL>(c.nl, c.ctl, nullptr, a.b.x1, E, true, nw, a.m.eps, s.xf, &s.xq[0][0], E, &s.xd[0][0], E / 32,
+    prologue<NL>(c.nl, c.ctl, nullptr, nullptr, a.b.x1, E, true, nw, a.m.eps, s.xf, &s.xq[0][0], E, &s.xd[0][0], E / 32,
                  s.ns, s.xn);
     tr_mark(c, 131);
     if (b == 0) {
@@ -1489,14 +1504,13 @@ FZ_PHASE bool phase_entry(const RunCtl *ctl, const FusedArgs *ap, int il) {
     wload<2 * E, 4>(ws, L.eh_proj.q, L.eh_proj.d, 8, [&](int rl) { return (int64_t)(r0 + rl); });
     const W8 nwe = wload8(L.enorm), nwh = wload8(L.hnorm);
     // no barrier precedes the entry (its inputs come from earlier launches)
-    const Q8W emb{a.m.tok_embd.q, a.m.tok_embd.d};
-    prologue<NL>(c.nl, c.ctl, &emb, nullptr, 0, false, nwe, a.m.eps, s.xf, &s.xq[0][0], 2 * E, &s.xd[0][0],
+    prologue<NL>(c.nl, c.ctl, a.m.tok_embd.q, a.m.tok_embd.d, nullptr, 0, false, nwe, a.m.eps, s.xf, &s.xq[0][0], 2 * E, &s.xd[0][0],
                  2 * E / 32, s.ns, nullptr);
     {
         // h of each lane: hid[hin_sel[l]]
         const int l = t >> 8, tt = t & 255;
         float v[8];
-        if (l < NL && l < c.nl) get8(a.b.hid + (int64_t)c.ctl->hin_sel[l] * E + 8 * tt, v);
+        if (l < NL && l < c.nl) get8(a.b.hid + (int64_t)lane_pick<NL>(c.ctl->hin_sel, l) * E + 8 * tt, v);
         else
             for (int i = 0; i < 8; i++) v[i] = 0.0f;
         if (l < NL) put8(&s.xf[l][8 * tt], v);
@@ -1544,7 +1558,7 @@ FZ_PHASE bool phase_head(const RunCtl *ctl, const FusedArgs *ap, const float *no
     const W8 nw = wload8(norm_w);
     if (!wait(c.bar, &c.ps->ok)) return false;
     tr_pass(c);
-    prologue<NL>(nl, c.ctl, nullptr, a.b.x2, E, true, nw, a.m.eps, s.xf, &s.xq[0][0], E, &s.xd[0][0], E / 32, s.ns,
+    prologue<NL>(nl, c.ctl, nullptr, nullptr, a.b.x2, E, true, nw, a.m.eps, s.xf, &s.xq[0][0], E, &s.xd[0][0], E / 32, s.ns,
                  s.xn);
     if (c.b == 0) {
         // h_nextn of each lane (Engine::hidden): the normalised x2
