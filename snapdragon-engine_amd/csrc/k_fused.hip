@@ -39,6 +39,7 @@ constexpr uint32_t SPIN_MAX = 400000;         // ~0.4 s at one device-scope load
 // written during the launch) through a uniform constant-space view (scalar loads).
 #define FZ_GAS __attribute__((address_space(1)))
 #define FZ_CAS __attribute__((address_space(4)))
+#define FZ_LDS __attribute__((address_space(3)))
 template <int N> struct RawOf;   // a plain type of N bytes (no constructors, so it loads from any space)
 template <> struct RawOf<2> { using T = uint16_t; };
 template <> struct RawOf<4> { using T = uint32_t; };
@@ -153,14 +154,14 @@ struct GSm {
 };
 
 // codes of rows rowof(0..nr) and their scales into registers (plain loads: weights are read-only)
-template <int K, int MAXP, class RowOf>
+template <int K, int MAXP, bool NONEMPTY = false, class RowOf>
 OXE_DEV void wload(WSlice<K, MAXP> &s, const int8_t *__restrict__ wq, const uint16_t *__restrict__ wd, int nr,
                    RowOf rowof) {
     using G = KG<K>;
     const int t = threadIdx.x, c = t % G::KCH, rs = t / G::KCH;
     // rows past nr load row nr - 1 again (wdot ignores them): no per-load branch, so the loads are
     // issued back to back without a wait between them; nothing is loaded (or read) when nr = 0
-    if (nr <= 0) return;
+    if (!NONEMPTY && nr <= 0) return;   // NONEMPTY: the caller guarantees nr >= 1 (no branch)
 #pragma unroll
     for (int p = 0; p < MAXP; p++) {
         const int rl = p * G::RPP + rs;
@@ -433,6 +434,7 @@ struct Persist {
     int ok;
     uint32_t round;
     uint32_t tev;                    // trace: next event index of this workgroup
+    uint32_t dyn_off;                // LDS offset of the dynamic LDS (fz_dyn), set by the kernel
     unsigned long long t_start, t_pass, t_mark;
 };
 
@@ -460,7 +462,10 @@ template <int NL>
 OXE_DEV Ctx<NL> make_ctx(const RunCtl *ctl, const FusedArgs *ap) {
     static_assert(NL == OXE_NL, "one lane count");
     const FZ_CAS FusedArgs *a = uni(ap);
-    Ctx<NL> c{uni(ctl), a, (PhaseSm<NL> *)fz_dyn, &fz_ps, fz_dyn, Bar{a->sync, fz_ps.round}, a->trace, 0, 0, 0};
+    // the dynamic LDS from its offset (a non-kernel function would otherwise look its base up in a
+    // per-kernel table in device memory, a load that may be repeated behind the weight loads in flight)
+    unsigned char *dyn = (unsigned char *)(FZ_LDS unsigned char *)(uintptr_t)fz_ps.dyn_off;
+    Ctx<NL> c{uni(ctl), a, (PhaseSm<NL> *)dyn, &fz_ps, dyn, Bar{a->sync, fz_ps.round}, a->trace, 0, 0, 0};
     c.nl = c.ctl->nl < 1 ? 1 : (c.ctl->nl > NL ? NL : c.ctl->nl);
     c.G = gridDim.x;
     c.b = blockIdx.x;
@@ -1569,30 +1574,24 @@ FZ_PHASE bool phase_head(const RunCtl *ctl, const FusedArgs *ap, const float *no
     float best = -__builtin_inff();
     int64_t bi = -1;
     const int rl = t % TR, l = t / TR;
+    // two register buffers; both reload every iteration, past the range the last tile again (read from
+    // cache), so no load sits behind a branch and the compiler's waits stay counts of loads in flight
+    auto dot_tile = [&](WSlice<E, HEAD_P> &W, int64_t tile) {
+        const int nr = rows_of(tile);
+        wdot<E, HEAD_P, NL>(W, nr, &s.xq[0][0], E, &s.xd[0][0], E / 32, s.g);
+        if (l < NL && l < nl && rl < nr) {
+            const float v = s.g.out[l][rl];
+            const int64_t row = tile * TR + rl;
+            if (a.keep_logits) a.b.logits[l * V + row] = v;
+            if (v > best) { best = v; bi = row; }
+        }
+    };
     for (int64_t tile = t0; tile < t1; tile += 2) {
-        const bool hb = tile + 1 < t1;
-        if (hb) wload<E, HEAD_P>(B, a.m.output.q, a.m.output.d, rows_of(tile + 1), [&](int r) { return (tile + 1) * TR + r; });
-        {
-            const int nr = rows_of(tile);
-            wdot<E, HEAD_P, NL>(A, nr, &s.xq[0][0], E, &s.xd[0][0], E / 32, s.g);
-            if (l < NL && l < nl && rl < nr) {
-                const float v = s.g.out[l][rl];
-                const int64_t row = tile * TR + rl;
-                if (a.keep_logits) a.b.logits[l * V + row] = v;
-                if (v > best) { best = v; bi = row; }
-            }
-        }
-        if (hb) {
-            if (tile + 2 < t1) wload<E, HEAD_P>(A, a.m.output.q, a.m.output.d, rows_of(tile + 2), [&](int r) { return (tile + 2) * TR + r; });
-            const int nr = rows_of(tile + 1);
-            wdot<E, HEAD_P, NL>(B, nr, &s.xq[0][0], E, &s.xd[0][0], E / 32, s.g);
-            if (l < NL && l < nl && rl < nr) {
-                const float v = s.g.out[l][rl];
-                const int64_t row = (tile + 1) * TR + rl;
-                if (a.keep_logits) a.b.logits[l * V + row] = v;
-                if (v > best) { best = v; bi = row; }
-            }
-        }
+        const int64_t tb = tile + 1 < t1 ? tile + 1 : t1 - 1, ta = tile + 2 < t1 ? tile + 2 : t1 - 1;
+        wload<E, HEAD_P, true>(B, a.m.output.q, a.m.output.d, rows_of(tb), [&](int r) { return tb * TR + r; });
+        dot_tile(A, tile);
+        wload<E, HEAD_P, true>(A, a.m.output.q, a.m.output.d, rows_of(ta), [&](int r) { return ta * TR + r; });
+        if (tile + 1 < t1) dot_tile(B, tile + 1);
     }
     // per-lane key of this workgroup: the largest value, then the smallest row
     unsigned long long key = 0ull;
@@ -1636,6 +1635,7 @@ __global__ __launch_bounds__(fz::FT, 1) void fused_kernel(const RunCtl *__restri
     if (threadIdx.x == 0) {
         fz_ps.round = cld32(&ap->sync[FZ_W_FLAG]);
         fz_ps.tev = 0;
+        fz_ps.dyn_off = (uint32_t)(uintptr_t)(FZ_LDS unsigned char *)fz_dyn;
     }
     __syncthreads();
     // the first phase of a run has no producer in this launch: its wait (the current round) passes at once
