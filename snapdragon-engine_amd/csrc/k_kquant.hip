@@ -40,7 +40,17 @@ OXE_DEV void ld_run(const uint8_t *p, uint32_t (&out)[N]) {
 #pragma unroll
     for (int i = 0; i < N; i++) out[i] = __builtin_amdgcn_alignbyte(w[i + 1], w[i], sh);
 }
-OXE_DEV int bsum16(const uint8_t *yb, int i) { return (int)*(const int16_t *)(yb + Q8K_BS + 2 * i); }
+// Activations in LDS: each q8_K block repacked as two halves (codes 128 h .. 128 h + 127 and their 8
+// sums of 16), YH = 37 dwords apart (odd: the 16 threads of a row read one half each, at the same
+// offset, on distinct banks), lanes YL(nb) dwords apart; the block scales in a separate array.
+constexpr int YH = 37;
+__host__ __device__ inline int y_lane_words(int nb) { return nb * 2 * YH; }
+struct YView {
+    const uint32_t *h;   // half (b, h) of lane 0
+    int ls;              // lane stride in dwords
+    OXE_DEV uint32_t q(int l, int j) const { return h[l * ls + j]; }   // code dword j (0..31)
+    OXE_DEV int bsum(int l, int i) const { return (int)((const int16_t *)(h + l * ls + 32))[i]; }   // sum i (0..7)
+};
 
 // ---- quantize_row_q8_K_ref (vendor/ggml-subset/generated/quants_base.c:14-48) --------------------
 // One wave per 256-value block; thread t holds values 4 t .. 4 t + 3. The block maximum is the
@@ -96,7 +106,7 @@ __global__ __launch_bounds__(256) void quant_q8_K_kernel(const float *__restrict
 }
 
 // ---- integers of one half block (unit h: weights 128 h .. 128 h + 127), every lane ---------------
-// yb: the lanes' q8_K blocks of this block position, ystride bytes apart; out[l * RES + ...]
+// y: the lanes' halves h of this block position (YView); out[l * RES + ...]
 
 // get_scale_min_k4 (quants_base.c:50-57)
 OXE_DEV void scale_min_k4(int j, const uint8_t *q, int &d, int &m) {
@@ -112,7 +122,7 @@ OXE_DEV void scale_min_k4(int j, const uint8_t *q, int &d, int &m) {
 // Q4_K / Q5_K: for the unit's two 64-weight steps g: sc_lo * I_lo, sc_hi * I_hi (out[0..3]); Q4_K:
 // out[4] = the unit's part of sum min_j * bsum32_j; Q5_K: out[4 + g'] = that sum per step
 template <int TY, int NL>
-OXE_DEV void unit_k45(const uint8_t *wb, const uint8_t *yb, int ystride, int h, int *out) {
+OXE_DEV void unit_k45(const uint8_t *wb, YView y, int h, int *out) {
     const uint8_t *sc = wb + 4;
     const uint8_t *qs = wb + (TY == 4 ? 16 : 48);
     const uint8_t *qh = wb + 16;
@@ -136,9 +146,8 @@ OXE_DEV void unit_k45(const uint8_t *wb, const uint8_t *yb, int ystride, int h, 
             }
 #pragma unroll
             for (int l = 0; l < NL; l++) {
-                const uint8_t *yq = yb + l * ystride + Q8K_QS;
-                lo[l] = dot4(cl, ld32(yq + 64 * g + 4 * i), lo[l]);
-                hi[l] = dot4(ch, ld32(yq + 64 * g + 32 + 4 * i), hi[l]);
+                lo[l] = dot4(cl, y.q(l, 16 * gg + i), lo[l]);
+                hi[l] = dot4(ch, y.q(l, 16 * gg + 8 + i), hi[l]);
             }
         }
         int s_lo, m_lo, s_hi, m_hi;
@@ -146,10 +155,9 @@ OXE_DEV void unit_k45(const uint8_t *wb, const uint8_t *yb, int ystride, int h, 
         scale_min_k4(2 * g + 1, sc, s_hi, m_hi);
 #pragma unroll
         for (int l = 0; l < NL; l++) {
-            const uint8_t *y = yb + l * ystride;
             out[l * RES + 2 * gg] = s_lo * lo[l];
             out[l * RES + 2 * gg + 1] = s_hi * hi[l];
-            const int bias = m_lo * (bsum16(y, 4 * g) + bsum16(y, 4 * g + 1)) + m_hi * (bsum16(y, 4 * g + 2) + bsum16(y, 4 * g + 3));
+            const int bias = m_lo * (y.bsum(l, 4 * gg) + y.bsum(l, 4 * gg + 1)) + m_hi * (y.bsum(l, 4 * gg + 2) + y.bsum(l, 4 * gg + 3));
             if (TY == 5) out[l * RES + 4 + gg] = bias;
             bias4[l] += bias;
         }
@@ -161,7 +169,7 @@ OXE_DEV void unit_k45(const uint8_t *wb, const uint8_t *yb, int ystride, int h, 
 
 // Q6_K: the unit's part of I = sum_i scale_i * (16 codes - 32) . q8 (the -32 through the q8 sums)
 template <int NL>
-OXE_DEV void unit_q6(const uint8_t *wb, const uint8_t *yb, int ystride, int n, int *out) {
+OXE_DEV void unit_q6(const uint8_t *wb, YView y, int n, int *out) {
     const int8_t *sc = (const int8_t *)(wb + 192);
     uint32_t qlw[16], qhw[8];   // ql[64 n .. 64 n + 63], qh[32 n .. 32 n + 31]
     ld_run<16>(wb + 64 * n, qlw);
@@ -181,18 +189,17 @@ OXE_DEV void unit_q6(const uint8_t *wb, const uint8_t *yb, int ystride, int n, i
         const int s = i >> 2;   // which 16 of the 32
 #pragma unroll
         for (int l = 0; l < NL; l++) {
-            const uint8_t *yq = yb + l * ystride + Q8K_QS + 128 * n;
-            d[l][0 + s] = dot4(c0, ld32(yq + 4 * i), d[l][0 + s]);
-            d[l][2 + s] = dot4(c1, ld32(yq + 32 + 4 * i), d[l][2 + s]);
-            d[l][4 + s] = dot4(c2, ld32(yq + 64 + 4 * i), d[l][4 + s]);
-            d[l][6 + s] = dot4(c3, ld32(yq + 96 + 4 * i), d[l][6 + s]);
+            d[l][0 + s] = dot4(c0, y.q(l, i), d[l][0 + s]);
+            d[l][2 + s] = dot4(c1, y.q(l, 8 + i), d[l][2 + s]);
+            d[l][4 + s] = dot4(c2, y.q(l, 16 + i), d[l][4 + s]);
+            d[l][6 + s] = dot4(c3, y.q(l, 24 + i), d[l][6 + s]);
         }
     }
 #pragma unroll
     for (int l = 0; l < NL; l++) {
         int I = 0;
 #pragma unroll
-        for (int i = 0; i < 8; i++) I += (int)sc[8 * n + i] * (d[l][i] - 32 * bsum16(yb + l * ystride, 8 * n + i));
+        for (int i = 0; i < 8; i++) I += (int)sc[8 * n + i] * (d[l][i] - 32 * y.bsum(l, i));
         out[l * RES] = I;
     }
 }
@@ -206,7 +213,7 @@ OXE_DEV int q3_raw(const uint8_t *s12, int i) {
 
 // Q3_K: the unit's part of isum = sum_i (raw_i - 32) * dot16_i, codes (low 2 bits | hmask bit << 2) - 4
 template <int NL>
-OXE_DEV void unit_q3(const uint8_t *wb, const uint8_t *yb, int ystride, int n, int *out) {
+OXE_DEV void unit_q3(const uint8_t *wb, YView y, int n, int *out) {
     uint32_t qsw[8], hmw[8];   // qs[32 n .. 32 n + 31], hmask[0..31]
     ld_run<8>(wb + 32 + 32 * n, qsw);
     ld_run<8>(wb, hmw);
@@ -223,10 +230,7 @@ OXE_DEV void unit_q3(const uint8_t *wb, const uint8_t *yb, int ystride, int n, i
         for (int s = 0; s < 4; s++) {
             const uint32_t c = ((qw >> (2 * s)) & 0x03030303u) | (((hw >> (4 * n + s)) & 0x01010101u) << 2);
 #pragma unroll
-            for (int l = 0; l < NL; l++) {
-                const uint8_t *yq = yb + l * ystride + Q8K_QS + 128 * n;
-                d[l][2 * s + half] = dot4(c, ld32(yq + 32 * s + 4 * i), d[l][2 * s + half]);
-            }
+            for (int l = 0; l < NL; l++) d[l][2 * s + half] = dot4(c, y.q(l, 8 * s + i), d[l][2 * s + half]);
         }
     }
     int sc[8];
@@ -236,22 +240,21 @@ OXE_DEV void unit_q3(const uint8_t *wb, const uint8_t *yb, int ystride, int n, i
     for (int l = 0; l < NL; l++) {
         int I = 0;
 #pragma unroll
-        for (int i = 0; i < 8; i++) I += sc[i] * (d[l][i] - 4 * bsum16(yb + l * ystride, 8 * n + i));
+        for (int i = 0; i < 8; i++) I += sc[i] * (d[l][i] - 4 * y.bsum(l, i));
         out[l * RES] = I;
     }
 }
 
 template <int TY, int NL>
-OXE_DEV void unit(const uint8_t *wb, const uint8_t *yb, int ystride, int h, int *out) {
-    if (TY == 4 || TY == 5) unit_k45<TY, NL>(wb, yb, ystride, h, out);
-    else if (TY == 6) unit_q6<NL>(wb, yb, ystride, h, out);
-    else unit_q3<NL>(wb, yb, ystride, h, out);
+OXE_DEV void unit(const uint8_t *wb, YView y, int h, int *out) {
+    if (TY == 4 || TY == 5) unit_k45<TY, NL>(wb, y, h, out);
+    else if (TY == 6) unit_q6<NL>(wb, y, h, out);
+    else unit_q3<NL>(wb, y, h, out);
 }
 
 // ---- the reference's float chain over one block (units r0: weights 0..127, r1: 128..255) ---------
 template <int TY>
-OXE_DEV float chain(float acc, const uint8_t *wb, const uint8_t *yb, const int *r0, const int *r1) {
-    const float dx = *(const float *)yb;
+OXE_DEV float chain(float acc, const uint8_t *wb, float dx, const int *r0, const int *r1) {
     if (TY == 4 || TY == 5) {
         // oxe_vl_q4k.inc:1-7 / oxe_vl_q5k.inc:6-12
         const float sbs = h2f(ld16(wb)) * dx, sbm = h2f(ld16(wb + 2)) * dx;
@@ -308,10 +311,10 @@ OXE_DEV void pf_load(u32x4 (&pf)[PF], const uint8_t *w, int64_t g, int64_t nr, i
 // g_next, then the units and the chains
 template <int TY, int NL>
 OXE_DEV void vl_group(u32x4 (&pf)[PF], int64_t g, int64_t g_next, const uint8_t *__restrict__ w, int nb, int64_t nr,
-                      float *__restrict__ s, uint8_t *wl, const uint8_t *yl, int *res) {
+                      float *__restrict__ s, uint8_t *wl, const uint32_t *yh, const float *yd, int *res) {
     constexpr int BB = BT<TY>::B;
     constexpr int RS = NL * RES + 1;   // odd per-thread stride: no bank conflicts between threads
-    const int row_bytes = nb * BB, ystride = nb * Q8K_BYTES;
+    const int row_bytes = nb * BB, ls = y_lane_words(nb);
     const int t = threadIdx.x, ri = t >> 4, u = t & 15;
     const int64_t ngroups = (nr + GR - 1) / GR;
     const int sp = (int)(min((int64_t)GR, nr - g * GR) * row_bytes), n16 = sp / 16;
@@ -331,13 +334,13 @@ OXE_DEV void vl_group(u32x4 (&pf)[PF], int64_t g, int64_t g_next, const uint8_t 
         const int kc = min(8, nb - b0);
         const int bi = b0 + (u >> 1);
         if ((u >> 1) < kc && live)
-            unit<TY, NL>(wl + ri * row_bytes + bi * BB, yl + bi * Q8K_BYTES, ystride, u & 1, res + t * RS);
+            unit<TY, NL>(wl + ri * row_bytes + bi * BB, YView{yh + (2 * bi + (u & 1)) * YH, ls}, u & 1, res + t * RS);
         __syncthreads();
         if (u < NL && live)
             for (int b = 0; b < kc; b++) {
                 const int *r0 = res + (ri * 16 + 2 * b) * RS + u * RES;
                 const int *r1 = res + (ri * 16 + 2 * b + 1) * RS + u * RES;
-                acc = chain<TY>(acc, wl + ri * row_bytes + (b0 + b) * BB, yl + u * ystride + (b0 + b) * Q8K_BYTES, r0, r1);
+                acc = chain<TY>(acc, wl + ri * row_bytes + (b0 + b) * BB, yd[u * nb + b0 + b], r0, r1);
             }
         __syncthreads();
     }
@@ -349,22 +352,29 @@ __global__ __launch_bounds__(64) void vl_gemv_kernel(const uint8_t *__restrict__
                                                      const uint8_t *__restrict__ y, float *__restrict__ s) {
     constexpr int BB = BT<TY>::B;
     extern __shared__ __align__(16) uint8_t lds[];
-    const int row_bytes = nb * BB, ystride = nb * Q8K_BYTES;
-    uint8_t *wl = lds;                                           // [GR][row_bytes]
-    uint8_t *yl = lds + align16(GR * row_bytes);                 // [NL][nb][292]
-    int *res = (int *)(yl + align16(NL * ystride));              // [64][NL * RES + 1]
+    const int row_bytes = nb * BB;
+    uint8_t *wl = lds;                                                   // [GR][row_bytes]
+    uint32_t *yh = (uint32_t *)(lds + align16(GR * row_bytes));         // [NL][nb][2][YH]
+    float *yd = (float *)(yh + NL * y_lane_words(nb));                   // [NL][nb]
+    int *res = (int *)((uint8_t *)yh + align16(NL * nb * (2 * YH + 1) * 4));   // [64][NL * RES + 1]
     const int t = threadIdx.x;
     const int64_t ngroups = (nr + GR - 1) / GR, G = gridDim.x;
-    for (int i = t; i < NL * ystride / 4; i += 64) ((uint32_t *)yl)[i] = ((const uint32_t *)y)[i];
+    // the lanes' q8_K blocks (lane l block b is block l nb + b) repacked into halves and scales
+    for (int i = t; i < NL * nb * 2 * 36; i += 64) {
+        const int wd = i % 36, hb = i / 36, h = hb & 1;
+        const uint32_t *src = (const uint32_t *)(y + (int64_t)(hb >> 1) * Q8K_BYTES);
+        yh[hb * YH + wd] = wd < 32 ? src[1 + 32 * h + wd] : src[65 + 4 * h + (wd - 32)];
+    }
+    for (int i = t; i < NL * nb; i += 64) yd[i] = *(const float *)(y + (int64_t)i * Q8K_BYTES);
     // the register buffer holds the next group's first bytes (fixed indices only: it stays in
     // registers; a second buffer two groups ahead measured no faster)
     u32x4 pf[PF];
     if ((int64_t)blockIdx.x < ngroups) pf_load(pf, w, blockIdx.x, nr, row_bytes, t);
-    for (int64_t g = blockIdx.x; g < ngroups; g += G) vl_group<TY, NL>(pf, g, g + G, w, nb, nr, s, wl, yl, res);
+    for (int64_t g = blockIdx.x; g < ngroups; g += G) vl_group<TY, NL>(pf, g, g + G, w, nb, nr, s, wl, yh, yd, res);
 }
 
 size_t vl_gemv_lds(int bb, int nb, int nl) {
-    return (size_t)align16(GR * nb * bb) + (size_t)align16(nl * nb * Q8K_BYTES) + (size_t)64 * (nl * RES + 1) * 4;
+    return (size_t)align16(GR * nb * bb) + (size_t)align16(nl * nb * (2 * YH + 1) * 4) + (size_t)64 * (nl * RES + 1) * 4;
 }
 
 template <int TY, int NL>
