@@ -35,8 +35,10 @@ constexpr uint32_t SPIN_MAX = 400000;         // ~0.4 s at one device-scope load
 // The phases are separate (non-inlined) functions, so pointers reach them as generic pointers and
 // plain accesses compile to flat instructions. A flat access counts on both the vector-memory and
 // the LDS wait counters, so an LDS wait would also wait for every weight load in flight. Device
-// memory is therefore read and written through global-space views, and the run's arguments (not
-// written during the launch) through a uniform constant-space view (scalar loads).
+// memory is therefore read and written through global-space views, and the run's arguments and run
+// control (written by the host or the control kernels before the launch, never during it) through a
+// uniform constant-space view (scalar loads; every dispatch starts with the scalar cache invalidated,
+// so the values written before the launch are the ones read).
 #define FZ_GAS __attribute__((address_space(1)))
 #define FZ_CAS __attribute__((address_space(4)))
 #define FZ_LDS __attribute__((address_space(3)))
