@@ -33,11 +33,21 @@ OXE_API int oxe_hip_quantize_row_q8_0(const float *x, int64_t k, int64_t nrows, 
 
 /* Q8_0 lane GEMV: y[l][r] = W[r] . x[l] for nl = 1 or 2 lanes in one weight pass; weights as int8
  * codes [nr][k] + fp16 scales [nr][k/32] (this build's layout; see oxe_hip_repack_q8_0), lanes as
- * produced by oxe_hip_quantize_row_q8_0; k in {512, 2048, 4096}. isum (optional, may be NULL):
+ * produced by oxe_hip_quantize_row_q8_0; k any multiple of 32 up to 65536 (tuned kernels for 512,
+ * 2048 and 4096, a one-wave-per-row kernel otherwise). isum (optional, may be NULL):
  * the exact int32 block dots [nl][nr][k/32]. Replaces oxe_vl_gemv (lib.rs:113, type 80) and
  * ggml_gemv_q8_0_4x8_q8_0 (lib.rs:75). */
 OXE_API int oxe_hip_gemv_q8_0(int64_t k, int64_t nr, int nl, const int8_t *wq, const uint16_t *wd, const int8_t *xq,
                               const uint16_t *xd, float *y, int32_t *isum, void *stream);
+
+/* Routing of n_rows rows of 256 router logits (f32): probabilities = softmax, the top 8 expert ids
+ * (ids [n_rows][8]) in the reference's order, including libstdc++ std::sort's order of tied
+ * probabilities, and their weights renormalised by the clamped sum (w [n_rows][8]). *tie_count
+ * (device memory) is incremented once per row that took the sort path. Replaces Engine::route
+ * (crates/model/src/engine.rs:3414-3429) over oxe_soft_max_f32 and oxe_argsort_top_k_f32
+ * (crates/kernels-sys/src/lib.rs:129-130; oxe_ops.cpp:101-165). */
+OXE_API int oxe_hip_route_f32(const float *logits, int64_t n_rows, int32_t *ids, float *w, uint32_t *tie_count,
+                              void *stream);
 
 /* Q8_0 GEMM for prefill: y[t][r] (row stride ldy >= nr) = W[r] . x[t] for nt token rows of
  * activations (oxe_hip_quantize_row_q8_0 output) against nr weight rows (layout as in
@@ -114,7 +124,10 @@ OXE_API int oxe_engine_n_ctx(const oxe_engine *e);
 OXE_API int oxe_engine_hidden(oxe_engine *e, int lane, float *out);
 /* Logits of lane `lane` of the last verify (Engine::logits_lane, engine.rs:1934-1937), host copy. */
 OXE_API int oxe_engine_logits(oxe_engine *e, int lane, float *out);
-/* Diagnostic counters (64: top-k ties met, where the reference would sort). */
+/* Overwrite router rows [row0, row0 + nrows) of layer `layer` (n_layer: the MTP block) with host f32
+ * rows of n_embd values (a test hook for exact routing ties; no counterpart in the reference). */
+OXE_API int oxe_engine_set_router(oxe_engine *e, int layer, int row0, int nrows, const float *host);
+/* Diagnostic counters (64: routings that took the reference's std::sort path for tied probabilities). */
 OXE_API int oxe_engine_counter(oxe_engine *e, int which, uint32_t *out);
 /* State copy for parity checks / hand-off (see engine.hip for the regions). */
 OXE_API int oxe_engine_state_copy(oxe_engine *e, int which, int dir, int64_t offset, void *host, int64_t nbytes);
@@ -283,12 +296,14 @@ OXE_API int oxe_srv_decode(oxe_srv *s, uint32_t tok, float *logits);
 OXE_API int oxe_srv_decode_argmax(oxe_srv *s, uint32_t tok, uint32_t *out);
 /* decode_spec_argmax (oxe_engine.rs:563-578): one MTP step from tok; extra[0..n_extra) = accepted
  * drafts (in the state), argmax[0..n_argmax) = the argmax of every committed row (the last is the
- * bonus token, not yet in the state); arrays of depth + 1 (at most 4). 1 without MTP. */
+ * bonus token, not yet in the state); both arrays sized spec_max_depth() + 1 (4). 1 without MTP. */
 OXE_API int oxe_srv_decode_spec_argmax(oxe_srv *s, uint32_t tok, uint32_t *extra, int *n_extra, uint32_t *argmax,
                                        int *n_argmax);
-/* decode_spec (oxe_engine.rs:530-543): as decode_spec_argmax with the committed rows' logits,
- * rows = host [n_extra + 1][n_vocab] */
-OXE_API int oxe_srv_decode_spec(oxe_srv *s, uint32_t tok, uint32_t *extra, int *n_extra, float *rows);
+/* decode_spec (oxe_engine.rs:530-543): as decode_spec_argmax with the committed rows' logits in
+ * rows = host [rows_cap][n_vocab]; rows [0, n_extra] are written. A step commits up to depth + 1
+ * rows, so rows_cap must be at least the current depth + 1 (spec_max_depth() + 1 covers every depth):
+ * a smaller buffer is refused (-1) before any work. extra holds up to depth values. */
+OXE_API int oxe_srv_decode_spec(oxe_srv *s, uint32_t tok, uint32_t *extra, int *n_extra, float *rows, int rows_cap);
 /* spec_rewind (oxe_engine.rs:579-592): keep the first `keep` tokens the last lookup verify or MTP
  * step committed (MtpDriver::rewind, mtp.rs:596-608) */
 OXE_API int oxe_srv_spec_rewind(oxe_srv *s, int keep);

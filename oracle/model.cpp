@@ -691,6 +691,16 @@ void oxo_mixer(oxo_engine *e, int l, int nl, int64_t pos0, const float *x, float
     else e->recurrent(l, nl);
     for (int ln = 0; ln < nl; ln++) std::memcpy(out + ln * e->d.n_embd, e->x1[ln].data(), e->d.n_embd * 4);
 }
+// router rows [row0, row0 + nrows) of layer l replaced (test hook for exact routing ties)
+void oxo_engine_set_router(oxo_engine *e, int l, int row0, int nrows, const float *src) {
+    std::memcpy(e->layers[l].router.data() + (size_t)row0 * e->d.n_embd, src, (size_t)nrows * e->d.n_embd * 4);
+}
+// the MTP entry alone (engine.rs:2362-2390): x[nl][E] = eh_proj . [enorm(embd(tok)); hnorm(h)]
+void oxo_mtp_entry(oxo_engine *e, const uint32_t *toks, int nl, const float *hs, float *x) {
+    for (int ln = 0; ln < nl; ln++) std::memcpy(e->hin[ln].data(), hs + ln * e->d.n_embd, e->d.n_embd * 4);
+    e->mtp_entry(nl, toks);
+    for (int ln = 0; ln < nl; ln++) std::memcpy(x + ln * e->d.n_embd, e->x2[ln].data(), e->d.n_embd * 4);
+}
 void oxo_moe(oxo_engine *e, int l, int nl, const float *x1, float *x2) {
     for (int ln = 0; ln < nl; ln++) std::memcpy(e->x1[ln].data(), x1 + ln * e->d.n_embd, e->d.n_embd * 4);
     e->moe(l, nl);

@@ -120,6 +120,8 @@ def lib():
             "oxo_set_pos": (None, [C.c_void_p, C.c_int64]),
             "oxo_mixer": (None, [C.c_void_p, C.c_int, C.c_int, C.c_int64, f32p, f32p]),
             "oxo_moe": (None, [C.c_void_p, C.c_int, C.c_int, f32p, f32p]),
+            "oxo_mtp_entry": (None, [C.c_void_p, u32p, C.c_int, f32p, f32p]),
+            "oxo_engine_set_router": (None, [C.c_void_p, C.c_int, C.c_int, C.c_int, f32p]),
             "oxo_synth_q8": (None, [C.c_uint64, C.c_int, C.c_int, C.c_int64, C.c_int64, C.c_int64, i8p, u16p]),
             "oxo_synth_f32": (None, [C.c_uint64, C.c_int, C.c_int, C.c_int64, f32p]),
             "oxo_synth_normal": (None, [C.c_uint64, C.c_uint64, C.c_int64, C.c_float, C.c_float, f32p]),
@@ -278,6 +280,10 @@ class Engine:
     @property
     def pos(self):
         return int(lib().oxo_pos(self.h))
+
+    def set_router(self, layer, row0, rows):
+        r = np.ascontiguousarray(rows, np.float32)
+        lib().oxo_engine_set_router(self.h, layer, row0, r.shape[0], ptr(r, C.c_float))
 
     def hidden(self, lane):
         return np.ctypeslib.as_array(lib().oxo_hidden(self.h, lane), (self.desc.n_embd,)).copy()

@@ -36,6 +36,8 @@ uint16_t *oxo_vcache_mut(oxo_engine *e);
 void oxo_set_pos(oxo_engine *e, int64_t pos);
 void oxo_mixer(oxo_engine *e, int l, int nl, int64_t pos0, const float *x, float *x1);
 void oxo_moe(oxo_engine *e, int l, int nl, const float *x1, float *x2);
+void oxo_engine_set_router(oxo_engine *e, int l, int row0, int nrows, const float *src);
+void oxo_mtp_entry(oxo_engine *e, const uint32_t *toks, int nl, const float *hs, float *x);
 
 void oxo_synth_q8(uint64_t seed, int layer, int kind, int64_t expert, int64_t rows, int64_t k, int8_t *q, uint16_t *d);
 void oxo_synth_f32(uint64_t seed, int layer, int kind, int64_t n, float *out);

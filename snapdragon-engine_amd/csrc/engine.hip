@@ -117,6 +117,14 @@ int oxe_engine_set_pos(oxe_engine *e, int pos) {
     return 0;
 }
 
+int oxe_engine_set_router(oxe_engine *e, int layer, int row0, int nrows, const float *host) {
+    Engine *g = (Engine *)e;
+    if (layer < 0 || layer > g->d.n_layer || row0 < 0 || nrows < 1 || row0 + nrows > oxe::NEXP || !host) return -1;
+    float *dst = g->L[layer].router + (int64_t)row0 * oxe::E;
+    if (hipMemcpyAsync(dst, host, (size_t)nrows * oxe::E * sizeof(float), hipMemcpyHostToDevice, g->st) != hipSuccess) return -2;
+    return hipStreamSynchronize(g->st) == hipSuccess ? 0 : -2;
+}
+
 int64_t oxe_engine_device_bytes(const oxe_engine *e) { return (int64_t)((const Engine *)e)->bytes; }
 
 // Engine::state_bytes (engine.rs:1570-1576): K and V^T of the positions < pos of every attention

@@ -57,6 +57,12 @@ static std::string tensor_check(const GgufTensor *t, const std::string &name, ui
 
 int Engine::load_gguf(const Gguf &g) {
     constexpr int64_t CHUNK = 256ll << 20;   // staging bytes per upload
+    // the reference's MTP loader refuses a draft head with its own embedding or LM head (mtp.rs:97-99)
+    const std::string mp = "blk." + std::to_string(d.n_layer) + ".";
+    if (g.tensor(mp + "nextn.embed_tokens.weight") || g.tensor(mp + "nextn.shared_head_head.weight")) {
+        set_err("MTP head with its own embedding/head is not supported (both GGUFs share the target's)");
+        return -1;
+    }
     uint8_t *stage = nullptr;
     if (hipMalloc(&stage, CHUNK) != hipSuccess) {
         set_err("out of device memory for the load staging buffer");
@@ -199,8 +205,18 @@ int oxe_engine_load_gguf(oxe_engine *e, const oxe_gguf *gg) {
     if (!g || !f) return -1;
     oxe_model_desc d;
     if (oxe_gguf_model_desc(gg, &d)) return -1;
-    if (d.n_layer != g->d.n_layer || d.n_vocab != g->d.n_vocab || !d.has_mtp) {
-        oxe::set_err("the file's model (layers, vocabulary, MTP block) differs from the engine's");
+    // every descriptor field the kernels and the RoPE table depend on must equal the engine's
+    const oxe_model_desc &c = g->d;
+    bool same = d.n_layer == c.n_layer && d.n_embd == c.n_embd && d.n_vocab == c.n_vocab && d.n_head == c.n_head &&
+                d.n_head_kv == c.n_head_kv && d.head_dim == c.head_dim && d.n_expert == c.n_expert &&
+                d.n_expert_used == c.n_expert_used && d.ff_exp == c.ff_exp && d.ff_shexp == c.ff_shexp &&
+                d.ssm_conv_kernel == c.ssm_conv_kernel && d.ssm_d_state == c.ssm_d_state &&
+                d.ssm_n_kheads == c.ssm_n_kheads && d.ssm_n_vheads == c.ssm_n_vheads && d.ssm_d_inner == c.ssm_d_inner &&
+                d.full_attention_interval == c.full_attention_interval && d.n_rot == c.n_rot &&
+                d.rms_eps == c.rms_eps && d.rope_freq_base == c.rope_freq_base && d.has_mtp && c.has_mtp;
+    for (int i = 0; i < 4; i++) same = same && d.rope_sections[i] == c.rope_sections[i];
+    if (!same) {
+        oxe::set_err("the file's model descriptor (shape, norms' eps, RoPE, layer pattern, MTP block) differs from the engine's");
         return -1;
     }
     return g->load_gguf(*f);

@@ -971,6 +971,16 @@ int Engine::seed_batched(const uint32_t *toks, int n, int pos0, const float *hs)
 
 extern "C" {
 
+// Routing of n_rows rows of n_expert (= 256) router logits: softmax, top-8 (libstdc++ std::sort order
+// on ties), weights renormalised by their clamped sum. Replaces Engine::route (engine.rs:3414-3429)
+// over oxe_soft_max_f32 and oxe_argsort_top_k_f32 (crates/kernels-sys/src/lib.rs:129-130).
+int oxe_hip_route_f32(const float *logits, int64_t n_rows, int32_t *ids, float *w, uint32_t *tie_count, void *stream) {
+    if (n_rows <= 0 || n_rows > (int64_t)1 << 30 || !logits || !ids || !w || !tie_count) return -1;
+    hipLaunchKernelGGL(oxe::pf::route_kernel, dim3((unsigned)((n_rows + 3) / 4)), dim3(256), 0, (hipStream_t)stream, logits,
+                       (int)n_rows, ids, w, tie_count);
+    return hipGetLastError() == hipSuccess ? 0 : -2;
+}
+
 // A batched prefill with HIP events around every launch of one kernel kind (12 every matrix-core
 // GEMM, 13 the grouped expert GEMMs, 14 attention, 15 the delta rule): *total_us = their summed
 // duration, *n = launches timed. Diagnostic for the prefill roofline (no counterpart in the

@@ -4,6 +4,7 @@
 #include "oxe_common.h"
 #include "oxe_engine.h"
 #include "oxe_shape.h"
+#include "oxe_stdsort.h"
 
 namespace oxe {
 
@@ -14,28 +15,11 @@ using namespace shp;
 //           groups of 4 with the group sum (v0+v1)+(v2+v3) added in double, scale by f32(1/sum)
 //   ids   = oxe_argsort_top_k_f32(probs, 8)              (oxe_ops.cpp:121-165)
 //   w_j   = probs[ids_j] / clamp(ggml_vec_sum_f32(w), 6.103515625e-5, inf)
-// The top 9 are taken by 9 wave arg-max rounds (largest value, then lowest index). When the 9 are
-// not strictly decreasing or the 9th value repeats (where the reference runs std::sort), the
-// lane's tie flag is set; the order used is then descending value, ascending index.
-OXE_DEV float wave_max_f(float v) {
-    for (int m = 32; m >= 1; m >>= 1) {
-        const float o = shfl_xor_f(v, m);
-        v = (v > o) ? v : o;
-    }
-    return v;
-}
-OXE_DEV int wave_min_i(int v) {
-    for (int m = 32; m >= 1; m >>= 1) {
-        const int o = shfl_xor_i(v, m);
-        v = v < o ? v : o;
-    }
-    return v;
-}
-OXE_DEV int wave_sum_i(int v) {
-    for (int m = 32; m >= 1; m >>= 1) v += shfl_xor_i(v, m);
-    return v;
-}
-
+// Fast path: a radix select of the top 9, ranked directly when they are pairwise distinct. When
+// the 9 largest are not strictly distinct, the 9th repeats, or a value is NaN (where the reference
+// runs std::sort over all 256 indices with x[a] > x[b]), one thread of the wave runs libstdc++'s
+// std::sort algorithm (oxe_stdsort.h) over the 256 probabilities in LDS, so tied experts come out in
+// the reference's order; the lane's tie flag counts these runs.
 struct RouteOut {
     int32_t ids[OXE_NL][KUSED];
     float w[OXE_NL][KUSED];
@@ -43,6 +27,9 @@ struct RouteOut {
     float sv[OXE_NL][KUSED + 1];     // the selected top 9 (value, expert) of the fast path
     int32_t si[OXE_NL][KUSED + 1];
     float vs[OXE_NL][KUSED + 1];     // values in rank order
+    float pv[OXE_NL][NEXP];          // the tie path: probabilities, sorted expert indices, sort stack
+    uint8_t sx[OXE_NL][NEXP];
+    oxe_sort::Range stk[OXE_NL][OXE_SORT_STACK];
     int32_t tie;
 };
 
@@ -141,37 +128,23 @@ OXE_DEV void route_wave(const float *lg, int l, RouteOut &ro) {
         }
     }
     if (!fast) {
-        // ties, NaN, or a repeated 9th value: the 9 wave arg-max rounds (largest value, then the
-        // lowest index), as the reference's std::sort order would need
-        unsigned taken = 0;  // bit k: expert 4tl+k already picked
-        float vals[KUSED + 1];
-        int ids[KUSED + 1];
+        // ties, NaN, or a repeated 9th value: std::sort of all 256 indices (oxe_ops.cpp:157-164)
+        static_assert(NEXP == 256, "8-bit expert indices");
 #pragma unroll
-        for (int r = 0; r <= KUSED; r++) {
-            float bv = -__builtin_inff();
-            int bi = 0x7fffffff;
-#pragma unroll
-            for (int k = 0; k < 4; k++)
-                if (!((taken >> k) & 1) && (p[k] > bv || bi == 0x7fffffff)) { bv = p[k]; bi = 4 * tl + k; }
-            const float mm = wave_max_f(bv);
-            const int i = wave_min_i(bv == mm ? bi : 0x7fffffff);
-            if ((i >> 2) == tl) taken |= 1u << (i & 3);
-            vals[r] = mm;
-            ids[r] = i;
+        for (int k = 0; k < 4; k++) {
+            ro.pv[l][4 * tl + k] = p[k];
+            ro.sx[l][4 * tl + k] = (uint8_t)(4 * tl + k);
         }
-        bool tie = false;
-#pragma unroll
-        for (int r = 1; r <= KUSED; r++) tie |= !(vals[r - 1] > vals[r]);
-        int eq = 0;
-#pragma unroll
-        for (int k = 0; k < 4; k++) eq += p[k] == vals[KUSED];
-        eq = wave_sum_i(eq);
-        tie |= eq != 1;
-        tie |= wave_sum_i(nan ? 1 : 0) != 0;
+        wave_lds_sync();
         if (tl == 0) {
-            for (int j = 0; j <= KUSED; j++) ro.vs[l][j] = vals[j];
-            for (int j = 0; j < KUSED; j++) ro.ids[l][j] = ids[j];
-            if (tie) ro.tie = 1;
+            oxe_sort::sort_desc(ro.sx[l], ro.pv[l], NEXP, ro.stk[l]);
+            ro.tie = 1;
+        }
+        wave_lds_sync();
+        if (tl <= KUSED) {
+            const int e = ro.sx[l][tl];
+            if (tl < KUSED) ro.ids[l][tl] = e;
+            ro.vs[l][tl] = ro.pv[l][e];
         }
         wave_lds_sync();
     }

@@ -320,7 +320,8 @@ struct SrvEngine {
             if (nbytes < (int64_t)(t - in) + 16) return fail(-1, "load snapshot: truncated");
             std::memcpy(&q, t, 8);
             std::memcpy(&n, t + 8, 8);
-            if (n > 4096 || q + n != (uint64_t)n_pos)
+            // each term bounded first, so the sum cannot wrap (as load_state checks it)
+            if (n > 4096 || n > (uint64_t)n_pos || q > (uint64_t)n_pos || q + n != (uint64_t)n_pos)
                 return fail(-1, "load snapshot: MTP state does not match the snapshot position");
             t += 16;
         }
@@ -448,8 +449,15 @@ int oxe_srv_decode_spec_argmax(oxe_srv *s, uint32_t tok, uint32_t *extra, int *n
     if (!extra || !n_extra || !argmax || !n_argmax) return -1;
     return srv(s)->decode_spec_argmax(tok, extra, n_extra, argmax, n_argmax);
 }
-int oxe_srv_decode_spec(oxe_srv *s, uint32_t tok, uint32_t *extra, int *n_extra, float *rows) {
+int oxe_srv_decode_spec(oxe_srv *s, uint32_t tok, uint32_t *extra, int *n_extra, float *rows, int rows_cap) {
     if (!extra || !n_extra || !rows) return -1;
+    // a step commits up to depth + 1 rows: refuse a buffer that could not hold them, before any work
+    const SrvEngine *v = srv(s);
+    if (v->mtp && rows_cap < v->e->drv.depth + 1) {
+        oxe::set_err("decode_spec: rows buffer holds " + std::to_string(rows_cap) + " rows, a depth-" +
+                  std::to_string(v->e->drv.depth) + " step needs " + std::to_string(v->e->drv.depth + 1));
+        return -1;
+    }
     uint32_t g[oxe::MTP_MAX_DEPTH + 1];
     int ng = 0;
     return srv(s)->decode_spec_argmax(tok, extra, n_extra, g, &ng, rows);

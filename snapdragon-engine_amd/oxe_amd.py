@@ -35,6 +35,7 @@ def lib():
             "oxe_hip_eval_unary": (i32, [i32, C.c_uint32, i64, i64, vp, vp]),
             "oxe_hip_quantize_row_q8_K": (i32, [vp, i64, i64, vp, vp]),
             "oxe_hip_vl_gemv": (i32, [i32, i64, i64, i32, vp, vp, vp, vp]),
+            "oxe_hip_route_f32": (i32, [vp, i64, vp, vp, vp, vp]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -178,6 +179,21 @@ def vl_gemv(ty, w, k, y, s=None):
     return s if rc == 1 else None
 
 
+def route_f32(logits, tie_count=None):
+    """Routing of rows of 256 router logits (float32 [n, 256] on the GPU): top-8 ids int32 [n, 8] and
+    renormalised weights float32 [n, 8] (Engine::route; std::sort order on tied probabilities);
+    tie_count (uint32 [1] on the GPU, optional) counts rows that took the sort path."""
+    import torch
+    logits = logits.contiguous()
+    n = logits.shape[0]
+    ids = torch.empty((n, 8), dtype=torch.int32, device=logits.device)
+    w = torch.empty((n, 8), dtype=torch.float32, device=logits.device)
+    if tie_count is None:
+        tie_count = torch.zeros(1, dtype=torch.int32, device=logits.device)
+    check(lib().oxe_hip_route_f32(_p(logits), n, _p(ids), _p(w), _p(tie_count), _stream()), "route_f32")
+    return ids, w
+
+
 def eval_unary(fn, start, n, stride, y):
     """y[i] = device scalar function fn at the float with bits start + i*stride (parity hook)."""
     check(lib().oxe_hip_eval_unary(fn, start, n, stride, _p(y), _stream()), "eval_unary")
@@ -205,6 +221,7 @@ def _engine_sigs(L):
         "oxe_engine_counter": (i32, [vp, i32, u32p]),
         "oxe_engine_state_copy": (i32, [vp, i32, i32, i64, vp, i64]),
         "oxe_engine_set_pos": (i32, [vp, i32]),
+        "oxe_engine_set_router": (i32, [vp, i32, i32, i32, f32p]),
         "oxe_engine_device_bytes": (i64, [vp]),
         "oxe_engine_state_bytes": (i64, [vp]),
         "oxe_engine_write_state": (i32, [vp, vp, i64]),
@@ -263,7 +280,7 @@ def _engine_sigs(L):
         "oxe_srv_decode": (i32, [vp, C.c_uint32, f32p]),
         "oxe_srv_decode_argmax": (i32, [vp, C.c_uint32, u32p]),
         "oxe_srv_decode_spec_argmax": (i32, [vp, C.c_uint32, u32p, C.POINTER(C.c_int), u32p, C.POINTER(C.c_int)]),
-        "oxe_srv_decode_spec": (i32, [vp, C.c_uint32, u32p, C.POINTER(C.c_int), f32p]),
+        "oxe_srv_decode_spec": (i32, [vp, C.c_uint32, u32p, C.POINTER(C.c_int), f32p, i32]),
         "oxe_srv_spec_rewind": (i32, [vp, i32]),
         "oxe_srv_decode_verify": (i32, [vp, C.c_uint32, u32p, i32, u32p, C.POINTER(C.c_int), u32p,
                                         C.POINTER(C.c_int)]),
@@ -518,6 +535,13 @@ class Engine:
 
     def set_pos(self, pos):
         check(lib().oxe_engine_set_pos(self.h, pos), "set_pos")
+
+    def set_router(self, layer, row0, rows):
+        """Overwrite router rows [row0, row0 + len(rows)) of `layer` (test hook for routing ties)."""
+        import numpy as np
+        r = np.ascontiguousarray(rows, np.float32)
+        check(lib().oxe_engine_set_router(self.h, layer, row0, r.shape[0], r.ctypes.data_as(C.POINTER(C.c_float))),
+              "set_router")
 
     def write_state(self):
         """Engine::write_state bytes (reference order) as a numpy uint8 array."""
@@ -779,7 +803,7 @@ class ServerEngine:
         ne = C.c_int(0)
         rows = np.empty((8, self.n_vocab), np.float32)
         rc = self._rc(lib().oxe_srv_decode_spec(self.h, token, _np_ptr(ex, C.c_uint32), C.byref(ne),
-                                                 _np_ptr(rows, C.c_float)), "decode_spec")
+                                                 _np_ptr(rows, C.c_float), rows.shape[0]), "decode_spec")
         if rc == 1:
             return None
         return [int(v) for v in ex[: ne.value]], [rows[i].copy() for i in range(ne.value + 1)]

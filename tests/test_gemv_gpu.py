@@ -30,7 +30,10 @@ def test_quantize_matches_oracle(dev):
     assert np.array_equal(d.cpu().numpy().view(np.uint16), d_ref)
 
 
-@pytest.mark.parametrize("k,nr,nl", [(2048, 4096, 2), (2048, 4096, 1), (4096, 2048, 2), (512, 2048, 2), (2048, 40, 2)])
+# the tuned shapes (k 512, 2048, 4096) and the any-k kernel (k a multiple of 32: the reference GEMV's
+# contract, crates/kernels-sys/src/lib.rs:75, 113)
+@pytest.mark.parametrize("k,nr,nl", [(2048, 4096, 2), (2048, 4096, 1), (4096, 2048, 2), (512, 2048, 2), (2048, 40, 2),
+                                     (32, 7, 2), (96, 130, 1), (1024, 257, 2), (3200, 64, 2), (8192, 33, 1)])
 def test_gemv_bitexact(dev, k, nr, nl):
     import oxe_amd as A
     import torch
@@ -43,6 +46,19 @@ def test_gemv_bitexact(dev, k, nr, nl):
     torch.cuda.synchronize()
     assert np.array_equal(isum.cpu().numpy(), isum_ref)
     assert np.array_equal(y.cpu().numpy().view(np.uint32), y_ref.view(np.uint32))
+
+
+def test_gemv_bad_shapes_write_nothing(dev):
+    import ctypes as C
+    import oxe_amd as A
+    import torch
+    y = torch.full((2, 8), 7.0, device=dev)
+    z = torch.zeros(64, dtype=torch.int8, device=dev)
+    for k, nr, nl in ((48, 8, 2), (0, 8, 2), (64, 0, 2), (64, 8, 3)):
+        rc = A.lib().oxe_hip_gemv_q8_0(k, nr, nl, A._p(z), A._p(z), A._p(z), A._p(z), A._p(y), None, A._stream())
+        assert rc == -1, (k, nr, nl)
+    torch.cuda.synchronize()
+    assert bool((y == 7.0).all())
 
 
 def test_config1_gemv(dev):

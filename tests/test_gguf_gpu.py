@@ -166,3 +166,53 @@ def test_bf16_routers_load_as_their_f32_widening():
         for p in paths:
             if os.path.exists(p):
                 os.remove(p)
+
+
+def _sparse_synth_file(path, desc, extra=(), meta_over=None):
+    """the synthetic model's header (+ extra tensors) over a sparse data region: enough for every
+    check the loader makes before reading a payload"""
+    tensors = [(n, t, s) for n, t, s, _ in W.synth_model_tensors(O, desc, 0)] + list(extra)
+    meta = W.qwen35moe_meta(desc)
+    if meta_over:
+        meta = [(k, vt, meta_over.get(k, v)) for k, vt, v in meta]
+    hdr, data_offset, offs = W.header(meta, tensors)
+    end = max(o + W.tensor_bytes(t, s) for o, (_, t, s) in zip(offs, tensors))
+    with open(path, "wb") as f:
+        f.write(hdr)
+        f.truncate(data_offset + end)
+
+
+def test_mtp_head_with_own_embedding_or_head_is_refused():
+    """the reference's MTP loader refuses nextn.embed_tokens / nextn.shared_head_head (mtp.rs:97-99)"""
+    import oxe_amd as A
+    d = O.desc_small()
+    for name in ("nextn.embed_tokens.weight", "nextn.shared_head_head.weight"):
+        path = os.path.join("/tmp", f"oxe_test_nextn_{os.getpid()}.gguf")
+        try:
+            _sparse_synth_file(path, d, [(f"blk.{d.n_layer}.{name}", W.GGML["Q8_0"], [d.n_embd, d.n_vocab])])
+            with pytest.raises(A.GgufError, match="MTP head with its own embedding/head is not supported"):
+                A.Engine.from_gguf(path, n_ctx=256)
+        finally:
+            if os.path.exists(path):
+                os.remove(path)
+
+
+def test_load_into_engine_with_another_descriptor_is_refused():
+    """oxe_engine_load_gguf: a file whose norms' eps or RoPE base differs from the engine's is refused"""
+    import oxe_amd as A
+    d = O.desc_small()
+    g = A.Engine(d, seed=0, n_ctx=256)
+    try:
+        for key, val in (("qwen35moe.attention.layer_norm_rms_epsilon", 1e-5), ("qwen35moe.rope.freq_base", 5e6)):
+            path = os.path.join("/tmp", f"oxe_test_desc_{os.getpid()}.gguf")
+            try:
+                _sparse_synth_file(path, d, meta_over={key: val})
+                f = A.Gguf(path)
+                with pytest.raises(A.GgufError, match="descriptor"):
+                    g.load_gguf(f)
+                f.close()
+            finally:
+                if os.path.exists(path):
+                    os.remove(path)
+    finally:
+        g.close()

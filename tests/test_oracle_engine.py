@@ -150,3 +150,22 @@ def test_mtp_depth_k_greedy_equals_plain(desc, depth):
     assert out == ref[:len(out)]
     st = drv.stats()
     assert st["drafted"] == 6 * depth and st["accepted"] == sum([depth, 0, 1, depth, depth - 1, 0])
+
+
+def test_tied_router_rows_take_the_sort_path(desc):
+    # router rows duplicated in pairs: every probability appears twice, so every routing sorts; the
+    # engine invariants still hold on that path
+    a = O.Engine(desc, seed=SEED, n_ctx=256)
+    b = O.Engine(desc, seed=SEED, n_ctx=256)
+    for layer in range(desc.n_layer + 1):
+        r = O.synth_f32(SEED, layer, O.T["ROUTER"], 256 * desc.n_embd).reshape(256, desc.n_embd)
+        r[1::2] = r[0::2]
+        a.set_router(layer, 0, r)
+        b.set_router(layer, 0, r)
+    g = a.verify([17, 3001])
+    la = a.logits(1)
+    a.commit(2)
+    assert b.step(17) == g[0]
+    assert b.step(3001) == g[1]
+    assert np.array_equal(bits(b.logits(0)), bits(la))
+    assert O.lib().oxo_tie_count(a.h) >= desc.n_layer * 2

@@ -477,15 +477,155 @@ def test_attention_head():
         return out.copy()
 
     o1 = run(kc, vt, k_last)
-    keys = kc[: pos + 1].astype(np.float64).copy()
+    # float64 attention with the reference's fp16 formats: q and the probabilities rounded to fp16,
+    # both dot products accumulated in fp16 chains (f64_model.dot_f16, the NEON ggml_vec_dot_f16
+    # structure pinned bit for bit by test_vec_dot_f16_reduce_tree_separating)
+    from f64_model import dot_f16, f16
+    keys = kc[:n_kv].astype(np.float64).copy()
     keys[pos] = k_last
-    sc = keys @ q.astype(np.float16).astype(np.float64) / 16
+    sc = dot_f16(keys[: pos + 1], f16(q)) / 16
     p = np.exp(sc - sc.max())
-    p /= p.sum()
-    want = vt[:, : pos + 1].astype(np.float64) @ p
-    assert np.allclose(o1, want, atol=2e-2 * np.abs(want).max())
+    p16 = np.zeros(n_kv)
+    p16[: pos + 1] = f16(p / p.sum())
+    want = dot_f16(vt[:, :n_kv].astype(np.float64), p16)
+    assert np.abs(o1 - want).max() <= 1e-3 * np.abs(want).max()
+    # an exact-math reference (no fp16 accumulation) is further away than the bar: the fp16 chains matter
+    exact = vt[:, : pos + 1].astype(np.float64) @ (p / p.sum())
+    assert np.abs(exact - want).max() > np.abs(o1 - want).max()
     # masked positions and the cache's own row at pos_last do not matter
     kc2, vt2 = kc.copy(), vt.copy()
     kc2[pos:] = 7
     vt2[:, pos + 1:] = 3
     assert np.array_equal(run(kc2, vt2, k_last), o1)
+
+
+# ---- bit-separating cases for the double-precision sums and the fp16 reduce tree ---------------
+# Each expected value is derived with exact rationals rounded once per operation in the reference's
+# structure; each case is chosen so that a plausible other structure gives different bits (asserted).
+def to_f64(fr):
+    return round_binary(fr, 53, -1022, 1023)
+
+
+def rms_ref(x, w, eps, square="f32", acc="f64"):
+    """oxe_rms_norm_mul_f32 (oxe_ops.cpp:32-42): sum += (double)(x*x) in element order; mean = f32(sum / n);
+    scale = 1 / sqrtf(mean + eps); y = (x * scale) * w. `square` / `acc` select plausible other forms."""
+    s = Fraction(0)
+    for v in x:
+        sq = Fraction(float(v)) ** 2
+        sq = Fraction(to_f32(sq)) if square == "f32" else sq
+        s = Fraction(to_f32(s + sq)) if acc == "f32" else Fraction(to_f64(s + sq))
+    mean = np.float32(to_f32(s / len(x)))
+    scale = np.float32(1.0) / np.sqrt(np.float32(mean + np.float32(eps)))   # f32 ops, correctly rounded
+    return (x * scale) * w
+
+
+def rms_oracle(x, w, eps):
+    y = np.empty_like(x)
+    L.oxo_rms_norm_mul_f32(fp(x), fp(w), fp(y), len(x), np.float32(eps))
+    return y
+
+
+def test_rms_norm_double_sum_separating():
+    eps = np.float32(1e-6)
+    # (1) one large square and 2047 squares of 2^-26: a double sum keeps them (mean 2^-11 (1 + 2047 2^-26)),
+    # an f32 sum loses every one of them (mean 2^-11)
+    x = np.full(2048, 2.0 ** -13, np.float32)
+    x[0] = 1.0
+    w = np.ones(2048, np.float32)
+    want = rms_ref(x, w, eps)
+    assert not np.array_equal(want, rms_ref(x, w, eps, acc="f32"))
+    assert np.array_equal(rms_oracle(x, w, eps).view(np.uint32), want.view(np.uint32))
+    # (2) squares rounded to f32 before the double sum: a seeded search for a row on which the
+    # unrounded (double) squares give other bits
+    rng = np.random.default_rng(31)
+    for _ in range(200):
+        x = (1 + rng.integers(0, 2 ** 12, 256) * 2.0 ** -12 + rng.integers(0, 2, 256) * 2.0 ** -23).astype(np.float32)
+        w = np.ones(256, np.float32)
+        want = rms_ref(x, w, eps)
+        if not np.array_equal(want, rms_ref(x, w, eps, square="f64")):
+            break
+    else:
+        raise AssertionError("no separating row found")
+    assert np.array_equal(rms_oracle(x, w, eps).view(np.uint32), want.view(np.uint32))
+
+
+def softmax_ref(x, e, group="pairwise", acc="f64"):
+    """oxe_soft_max_f32 with scale 1 and no mask over n % 4 == 0 values whose exponentials are e
+    (ggml_vec_soft_max_f32, NEON: per group of 4, sum += (double)vaddvq_f32(e0..e3); then
+    y = e * f32(1.0 / sum))."""
+    s = Fraction(0)
+    for g in range(0, len(e), 4):
+        a = [Fraction(float(v)) for v in e[g:g + 4]]
+        if group == "pairwise":
+            gs = to_f32(Fraction(to_f32(a[0] + a[1])) + Fraction(to_f32(a[2] + a[3])))
+        elif group == "sequential":
+            gs = to_f32(Fraction(to_f32(Fraction(to_f32(a[0] + a[1])) + a[2])) + a[3])
+        else:                                   # the group added to the double sum element by element
+            for v in a:
+                s = Fraction(to_f64(s + v))
+            continue
+        s = Fraction(to_f32(s + Fraction(gs))) if acc == "f32" else Fraction(to_f64(s + Fraction(gs)))
+    r = np.float32(to_f32(Fraction(to_f64(1 / s))))
+    return np.asarray(e, np.float32) * r
+
+
+def test_soft_max_group_sums_separating():
+    n = 256
+    x = np.full(n, -20.5, np.float32)
+    x[0] = 0.0                                  # the maximum: e = 1
+    x[1:4] = -16.54                             # e ~ 1.1 * 2^-24: the group's add order decides its last bit
+    # the tail (e ~ 1e-9 each, lost in an f32 sum next to 1) shifts 1 / sum; the first tail value on
+    # which every other structure gives other bits is taken
+    for tail in np.arange(-21.0, -19.0, 0.05, dtype=np.float32):
+        x[4:] = tail
+        e = np.array([L.oxo_v_expf(float(v)) for v in x], np.float32)
+        want = softmax_ref(x, e)
+        if all(not np.array_equal(want, softmax_ref(x, e, **o))
+               for o in (dict(group="sequential"), dict(group="none"), dict(acc="f32"))):
+            break
+    else:
+        raise AssertionError("no separating tail found")
+    y = np.empty(n, np.float32)
+    w = np.empty(n, np.float32)
+    L.oxo_soft_max_f32(n, fp(y), fp(x), np.float32(1.0), None, fp(w))
+    assert np.array_equal(y.view(np.uint32), want.view(np.uint32))
+
+
+def f16x8_reduce_ref(chains, tree="ref"):
+    """GGML_F16x8_REDUCE (simd-mappings.h:410-428) over accumulators a0..a3 of 8 fp16 lanes:
+    a0 += a2, a1 += a3, a0 += a1 (fp16 adds per lane); t = f32(lanes 0-3) + f32(lanes 4-7);
+    vaddvq: (t0 + t1) + (t2 + t3)."""
+    a = [[Fraction(float(v)) for v in chains[8 * j:8 * j + 8]] for j in range(4)]
+    add16 = lambda p, q: [Fraction(to_f16(u + v)) for u, v in zip(p, q)]
+    if tree == "ref":
+        a0 = add16(add16(a[0], a[2]), add16(a[1], a[3]))
+    elif tree == "sequential":
+        a0 = add16(add16(add16(a[0], a[1]), a[2]), a[3])
+    else:                                       # "adjacent": (a0 + a1) + (a2 + a3)
+        a0 = add16(add16(a[0], a[1]), add16(a[2], a[3]))
+    if tree == "lanes_adjacent":
+        a0 = add16(add16(a[0], a[2]), add16(a[1], a[3]))
+        t = [Fraction(to_f32(a0[2 * i] + a0[2 * i + 1])) for i in range(4)]
+    else:
+        t = [Fraction(to_f32(a0[i] + a0[i + 4])) for i in range(4)]
+    if tree == "lanes_sequential":
+        return to_f32(Fraction(to_f32(Fraction(to_f32(t[0] + t[1])) + t[2])) + t[3])
+    return to_f32(Fraction(to_f32(t[0] + t[1])) + Fraction(to_f32(t[2] + t[3])))
+
+
+def test_vec_dot_f16_reduce_tree_separating():
+    # n = 32 with y = 1: chain c (accumulator c // 8, lane c % 8) holds exactly x_c. The chain values
+    # are drawn (seeded) from values whose fp16 and f32 sums round, until every other tree gives
+    # other bits.
+    rng = np.random.default_rng(37)
+    pool = np.array([0, 0, 0, 1, 1, 2, 3, 2048, 2048, 1024, 2.0 ** -13, 2.0 ** -12, 0.5], np.float64)
+    for _ in range(5000):
+        c = rng.choice(pool, 32).astype(np.float16)
+        want = f16x8_reduce_ref(c)
+        if all(f16x8_reduce_ref(c, o) != want for o in ("sequential", "adjacent", "lanes_adjacent", "lanes_sequential")):
+            break
+    else:
+        raise AssertionError("no separating chain values found")
+    one = np.ones(32, np.float16)
+    got = L.oxo_vec_dot_f16(32, O.ptr(c.view(np.uint16), C.c_uint16), O.ptr(one.view(np.uint16), C.c_uint16))
+    assert got == want
