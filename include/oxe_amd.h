@@ -217,6 +217,14 @@ OXE_API int oxe_gguf_model_desc(const oxe_gguf *g, oxe_model_desc *out);
  * crates/model/src/mtp.rs:109-128). Other tensor types are refused by name (-1): the engine's runs
  * take Q8_0 matmul weights (the K-quant GEMVs exist at kernel level, oxe_hip_vl_gemv). */
 OXE_API int oxe_engine_load_gguf(oxe_engine *e, const oxe_gguf *g);
+/* oxe_engine_load_gguf without any device allocation: no counterpart in the reference; for callers
+ * that cannot allocate device memory (code under HIP graph capture, serving loops, harnesses that
+ * forbid hipMalloc). Uploads are staged through a 16 MiB device array of the library (one per GPU,
+ * held until the process ends) instead of a 256 MiB buffer allocated per call; a tensor that must be
+ * staged whole above 16 MiB (one expert's matrix, an interleaved gate / up matrix) is refused by
+ * name (-1). The engine's device must be current. Calls that overlap on one GPU share the array and
+ * race: serialise them. */
+OXE_API int oxe_engine_load_gguf_noalloc(oxe_engine *e, const oxe_gguf *g);
 /* open + model_desc + engine_create + load_gguf */
 OXE_API int oxe_engine_create_from_gguf(const char *path, int n_ctx, oxe_engine **out);
 

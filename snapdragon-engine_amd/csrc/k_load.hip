@@ -8,6 +8,7 @@
 // copied. Any other tensor type is refused with the tensor's name: the kernels of this build run
 // Q8_0 matmul weights and F32 routers / norms only.
 #include <algorithm>
+#include <mutex>
 #include <string>
 
 #include "oxe_engine_host.h"
@@ -55,16 +56,16 @@ static std::string tensor_check(const GgufTensor *t, const std::string &name, ui
     return "";
 }
 
-int Engine::load_gguf(const Gguf &g) {
-    constexpr int64_t CHUNK = 256ll << 20;   // staging bytes per upload
+int Engine::load_gguf(const Gguf &g, uint8_t *given_stage, int64_t given_chunk) {
+    const int64_t CHUNK = given_stage ? given_chunk : 256ll << 20;   // staging bytes per upload
     // the reference's MTP loader refuses a draft head with its own embedding or LM head (mtp.rs:97-99)
     const std::string mp = "blk." + std::to_string(d.n_layer) + ".";
     if (g.tensor(mp + "nextn.embed_tokens.weight") || g.tensor(mp + "nextn.shared_head_head.weight")) {
         set_err("MTP head with its own embedding/head is not supported (both GGUFs share the target's)");
         return -1;
     }
-    uint8_t *stage = nullptr;
-    if (hipMalloc(&stage, CHUNK) != hipSuccess) {
+    uint8_t *stage = given_stage;
+    if (!stage && hipMalloc(&stage, CHUNK) != hipSuccess) {
         set_err("out of device memory for the load staging buffer");
         return -3;
     }
@@ -177,7 +178,7 @@ int Engine::load_gguf(const Gguf &g) {
     q8("output.weight", E, d.n_vocab, 1, m.output.q, m.output.d, 0, 0, -1);
     f32("output_norm.weight", {E}, m.out_norm);
     const hipError_t se = hipStreamSynchronize(st);
-    (void)hipFree(stage);
+    if (!given_stage) (void)hipFree(stage);
     if (!err.empty()) {
         set_err(err);
         return -1;
@@ -186,23 +187,36 @@ int Engine::load_gguf(const Gguf &g) {
     return 0;
 }
 
+// ---- staging of the allocation-free loader -----------------------------------------------------
+// A file-scope device array (each GPU the library runs on holds its own copy until the process
+// ends). Host code never passes `load_scratch` itself to a kernel or copy (on the host it names a
+// stand-in, not device memory): its device address is looked up once per device with that device
+// current and kept in load_scratch_ptr.
+constexpr int64_t LOAD_SCRATCH_BYTES = 16ll << 20;
+constexpr int LOAD_SCRATCH_MAX_DEV = 64;
+static __device__ __align__(256) uint8_t load_scratch[LOAD_SCRATCH_BYTES];
+static std::mutex load_scratch_mu;
+static uint8_t *load_scratch_ptr[LOAD_SCRATCH_MAX_DEV];
+
+// the device address of device dev's load_scratch (dev must be current); null on failure
+static uint8_t *load_scratch_of(int dev) {
+    if (dev < 0 || dev >= LOAD_SCRATCH_MAX_DEV) return nullptr;
+    std::lock_guard<std::mutex> lk(load_scratch_mu);
+    if (!load_scratch_ptr[dev]) {
+        void *p = nullptr;
+        if (hipGetSymbolAddress(&p, HIP_SYMBOL(load_scratch)) != hipSuccess || !p) return nullptr;
+        load_scratch_ptr[dev] = (uint8_t *)p;
+    }
+    return load_scratch_ptr[dev];
+}
+
 }  // namespace oxe
 
 extern "C" {
 
-int oxe_hip_repack_q8_0(const void *src, int64_t nrows, int64_t k, int8_t *q, uint16_t *d, void *stream) {
-    if (!src || !q || !d || nrows <= 0 || k <= 0 || k % 32 != 0) return -1;
-    const int64_t nb = nrows * (k / 32);
-    hipLaunchKernelGGL(oxe::ld::q8_split_kernel, dim3((unsigned)std::min<int64_t>((nb + 255) / 256, 65535)), dim3(256), 0,
-                       (hipStream_t)stream, (const uint8_t *)src, nrows, k, (int64_t)1 << 62, (int64_t)0, (int64_t)0, -1,
-                       q, d);
-    return hipGetLastError() == hipSuccess ? 0 : -2;
-}
-
-int oxe_engine_load_gguf(oxe_engine *e, const oxe_gguf *gg) {
+// the file's descriptor against the engine's (0: equal)
+static int load_gguf_check(oxe_engine *e, const oxe_gguf *gg) {
     oxe::Engine *g = (oxe::Engine *)e;
-    const oxe::Gguf *f = (const oxe::Gguf *)gg;
-    if (!g || !f) return -1;
     oxe_model_desc d;
     if (oxe_gguf_model_desc(gg, &d)) return -1;
     // every descriptor field the kernels and the RoPE table depend on must equal the engine's
@@ -219,6 +233,45 @@ int oxe_engine_load_gguf(oxe_engine *e, const oxe_gguf *gg) {
         oxe::set_err("the file's model descriptor (shape, norms' eps, RoPE, layer pattern, MTP block) differs from the engine's");
         return -1;
     }
+    return 0;
+}
+
+int oxe_engine_load_gguf_noalloc(oxe_engine *e, const oxe_gguf *gg) {
+    oxe::Engine *g = (oxe::Engine *)e;
+    if (!g || !gg) return -1;
+    int cur = -1;
+    if (hipGetDevice(&cur) != hipSuccess) return -2;
+    if (cur != g->dev) {
+        oxe::set_err("load_gguf_noalloc: the engine's device must be current");
+        return -1;
+    }
+    uint8_t *stage = oxe::load_scratch_of(cur);
+    if (!stage) {
+        oxe::set_err("load_gguf_noalloc: no device address for the staging array");
+        return -2;
+    }
+    const int rc = load_gguf_check(e, gg);
+    if (rc) return rc;
+    // every upload goes through the 16 MiB array: a tensor group that must be staged whole (one
+    // expert's matrix, an interleaved gate / up matrix) above that size is refused by name
+    return g->load_gguf(*(const oxe::Gguf *)gg, stage, oxe::LOAD_SCRATCH_BYTES);
+}
+
+int oxe_hip_repack_q8_0(const void *src, int64_t nrows, int64_t k, int8_t *q, uint16_t *d, void *stream) {
+    if (!src || !q || !d || nrows <= 0 || k <= 0 || k % 32 != 0) return -1;
+    const int64_t nb = nrows * (k / 32);
+    hipLaunchKernelGGL(oxe::ld::q8_split_kernel, dim3((unsigned)std::min<int64_t>((nb + 255) / 256, 65535)), dim3(256), 0,
+                       (hipStream_t)stream, (const uint8_t *)src, nrows, k, (int64_t)1 << 62, (int64_t)0, (int64_t)0, -1,
+                       q, d);
+    return hipGetLastError() == hipSuccess ? 0 : -2;
+}
+
+int oxe_engine_load_gguf(oxe_engine *e, const oxe_gguf *gg) {
+    oxe::Engine *g = (oxe::Engine *)e;
+    const oxe::Gguf *f = (const oxe::Gguf *)gg;
+    if (!g || !f) return -1;
+    const int rc = load_gguf_check(e, gg);
+    if (rc) return rc;
     return g->load_gguf(*f);
 }
 

@@ -72,6 +72,7 @@ inline void set_err(const std::string &s) { g_last_error = s; }
 struct Engine {
     oxe_model_desc d{};
     uint64_t seed = 0;
+    int dev = 0;            // the device current at creation (every buffer and the stream live there)
     hipStream_t st = nullptr;
     ModelRt m{};
     std::vector<LayerW> L;  // n_layer (+1 MTP block)
@@ -113,8 +114,9 @@ struct Engine {
     int pf_chunk(const uint32_t *toks, int T, float *h_out);
     int prefill(const uint32_t *toks, int n, uint32_t *next, float *h_all);
     int seed_batched(const uint32_t *toks, int n, int pos0, const float *hs);
-    // weights from a GGUF file (k_load.hip)
-    int load_gguf(const Gguf &g);
+    // weights from a GGUF file (k_load.hip): through a staging buffer allocated for the call, or
+    // through `stage` (chunk bytes) when given
+    int load_gguf(const Gguf &g, uint8_t *stage = nullptr, int64_t chunk = 0);
     // kernel probe: HIP events around every launch of one kernel kind while enqueuing eagerly
     int probe_kind = -1;
     std::vector<hipEvent_t> probe_ev;
@@ -206,6 +208,7 @@ struct Engine {
     void create(const oxe_model_desc &desc, uint64_t sd, int n_ctx) {
         d = desc;
         seed = sd;
+        if (hipGetDevice(&dev) != hipSuccess) throw std::runtime_error("hipGetDevice failed");
         if (hipStreamCreate(&st) != hipSuccess) throw std::runtime_error("hipStreamCreate failed");
         m.n_layer = d.n_layer;
         m.n_vocab = d.n_vocab;

@@ -265,6 +265,7 @@ def _engine_sigs(L):
         "oxe_gguf_meta_array_f64": (i32, [vp, C.c_char_p, C.c_uint64, C.POINTER(C.c_double)]),
         "oxe_gguf_model_desc": (i32, [vp, vp]),
         "oxe_engine_load_gguf": (i32, [vp, vp]),
+        "oxe_engine_load_gguf_noalloc": (i32, [vp, vp]),
         "oxe_engine_create_from_gguf": (i32, [C.c_char_p, i32, C.POINTER(C.c_void_p)]),
         "oxe_engine_kv_row_bytes": (i64, [vp]),
         "oxe_engine_write_kv_rows": (i32, [vp, i32, i32, vp, i64]),
@@ -460,6 +461,12 @@ class Engine:
         rc = lib().oxe_engine_load_gguf(self.h, g.h)
         if rc != 0:
             raise GgufError(f"oxe_engine_load_gguf: {rc} {_last_error()}")
+
+    def load_gguf_noalloc(self, g):
+        """load_gguf staged through the library's static device array (no device allocation)"""
+        rc = lib().oxe_engine_load_gguf_noalloc(self.h, g.h)
+        if rc != 0:
+            raise GgufError(f"oxe_engine_load_gguf_noalloc: {rc} {_last_error()}")
 
     def close(self):
         if getattr(self, "h", None) and _lib is not None:
