@@ -14,7 +14,9 @@ launch per step, ~94 % of it), timed live with HIP events around its launch in e
 steps; its algorithmic bytes are the verify run's unique weight, state and KV bytes at the
 measured union size.
 cpu_baseline: the C++ oracle (the reference algorithm restated, OpenMP over rows) timed on this
-host on a bounded sample of the same workload (see the `sample` field).
+host on a bounded sample of the same workload, resumed from the GPU run's own sequence state (see
+the `sample` field). parity: the run's generated ids against the oracle's for the same model and
+prompt (tests/golden/config4_ids.npz) and the reference bench's generated_hash of them.
 """
 import argparse
 import json
@@ -68,16 +70,36 @@ def step_bytes(pos, u_avg, accepted_frac):
     return verify_bytes(pos, u_avg) + draft_bytes(pos, u_avg) + seed
 
 
-def cpu_baseline(seconds, prompt_len=8):
-    """Time the oracle's MTP-1 steps on the full 35B-A3B shape (bounded sample)."""
+def host_cores():
+    """(threads the oracle uses, the process's core list, the host CPU model)"""
+    aff = sorted(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else list(range(os.cpu_count() or 1))
+    threads = int(os.environ.get("OMP_NUM_THREADS", len(aff)))
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return min(threads, len(aff)), aff, model
+
+
+def cpu_baseline(seconds, state, n_pos, hl, x):
+    """Time the oracle's MTP-1 steps on the full 35B-A3B shape (bounded sample) from the GPU run's own
+    state: the sequence state after the 512-token prompt and the warm-up steps (Engine::write_state
+    bytes read into the oracle engine, the MTP driver resumed at that position), so the CPU steps run
+    at the GPU's context positions."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as O
     O.build()
     d = O.desc_35b_a3b()
-    e = O.Engine(d, seed=0, n_ctx=prompt_len + 256)
+    e = O.Engine(d, seed=0, n_ctx=n_pos + 256)
     O.lib().oxo_set_keep_logits(e.h, 0)
+    e.read_state(state, n_pos)
     drv = O.Driver(e)
-    x = drv.prefill(O.bench_prompt(prompt_len))
+    drv.import_state(n_pos, hl)
     gen0 = O.lib().oxo_gen_seconds(e.h)
     t0 = time.time()
     toks = steps = 0
@@ -89,11 +111,33 @@ def cpu_baseline(seconds, prompt_len=8):
     wall = time.time() - t0
     gen = O.lib().oxo_gen_seconds(e.h) - gen0
     compute = max(wall - gen, 1e-9)
-    cores = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    threads, aff, model = host_cores()
     e.close()
-    return {"value": round(toks / compute, 4), "unit": "tok/s", "cores": cores, "kind": "port",
-            "sample": f"{steps} MTP-1 steps ({toks} tokens) of the 35B-A3B shape after an {prompt_len}-token prompt; "
-                      f"{wall:.1f} s wall minus {gen:.1f} s spent generating synthetic expert weights on first use"}
+    return {"value": round(toks / compute, 4), "unit": "tok/s", "cores": threads, "kind": "port",
+            "cpu": model, "affinity": f"{len(aff)} cores [{aff[0]}..{aff[-1]}]" if aff else "",
+            "sample": f"{steps} MTP-1 steps ({toks} tokens) of the 35B-A3B shape at positions {n_pos}..{n_pos + steps}, "
+                      f"from the GPU run's state after its {n_pos}-position prefix; the reference algorithm "
+                      f"restated in C++ with OpenMP over rows on {threads} threads (not the reference's pinned "
+                      f"thread team with one barrier per plan phase); {wall:.1f} s wall minus {gen:.1f} s spent "
+                      f"generating synthetic expert weights on first use"}
+
+
+def golden_parity(gen):
+    """The run's generated ids (as the reference's bench records them, oxe.rs:2108-2133) against the
+    oracle's for the same model and prompt (tests/golden/config4_ids.npz, make_golden.py)."""
+    import numpy as np
+    import oxe_amd as A
+    path = os.path.join(ROOT, "tests", "golden", "config4_ids.npz")
+    out = {"generated_hash": A.hash_ids(gen), "ids": len(gen)}
+    if not os.path.exists(path):
+        out["oracle_ids"] = None
+        return out
+    want = np.load(path)["ids"]
+    n = min(len(gen), len(want))
+    same = bool(np.array_equal(np.asarray(gen[:n], np.uint32), want[:n]))
+    out.update({"oracle_ids_compared": n, "identical_to_oracle": same,
+                "oracle_generated_hash": A.hash_ids(want[:n]) if n else None})
+    return out
 
 
 def prefill_macs(T, n_dn=30, n_att=10):
@@ -130,7 +174,7 @@ def cpu_prefill_baseline(seconds):
     wall = time.time() - t0
     gen = O.lib().oxo_gen_seconds(e.h) - gen0
     compute = max(wall - gen, 1e-9)
-    cores = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    cores = host_cores()[0]
     e.close()
     return {"value": round(n / compute, 4), "unit": "tok/s", "cores": cores, "kind": "port",
             "sample": f"{n} prompt tokens of the 35B-A3B shape as 2-token verify runs (the reference's "
@@ -229,7 +273,7 @@ def cpu_kquant_baseline(seconds, ty, k, rows_total):
         n += rows
     dt = time.time() - t0
     bytes_per_row = k // 256 * KQ_BYTES[ty]
-    cores = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    cores = host_cores()[0]
     return {"value": round(n * bytes_per_row / dt / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": "port",
             "sample": f"{n} rows ({n / rows_total:.2f} x the full matrix) of the same type and k, 2 lanes, "
                       f"in {dt:.1f} s"}
@@ -384,9 +428,11 @@ def main():
                           "positions": [pos_p0, eng.pos], "union_experts_per_moe_layer": round(u_probe, 3)}), flush=True)
         return
     # warm-up (also captures the step graph)
+    gen = [int(x)]
     eng.mtp_device_begin(x, cap)
     eng.mtp_device_steps(args.warmup, use_graph=True)
     warm_toks, x = eng.mtp_device_end(cap)
+    gen += [int(t) for t in warm_toks]
     # timed region: K graph steps between events on the engine stream
     uni0 = eng.counter(66)
     calls0 = eng.counter(67)
@@ -404,6 +450,10 @@ def main():
     torch.cuda.synchronize()
     ms = ev0.elapsed_time(ev1)
     toks, x = eng.mtp_device_end(cap)
+    gen += [int(t) for t in toks]
+    parity = golden_parity(gen)
+    # the CPU baseline resumes from this state (after the prompt, warm-up and timed steps)
+    cpu_state = None if args.no_cpu else (eng.write_state(), eng.pos, eng.hidden(0), int(x))
     stats = eng.mtp_stats()
     units = eng.counter(66) - uni0
     calls = eng.counter(67) - calls0
@@ -467,9 +517,10 @@ def main():
                      "kernel": k_name, "avg_us": round(avg_us, 3),
                      "launches_timed": n_launch, "bytes_per_launch": int(k_bytes)},
         "setup_s": round(setup_s, 1),
+        "parity": parity,
     }
-    if not args.no_cpu:
-        result["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+    if cpu_state is not None:
+        result["cpu_baseline"] = cpu_baseline(args.cpu_seconds, *cpu_state)
     else:
         result["cpu_baseline"] = None
     print(json.dumps(result), flush=True)

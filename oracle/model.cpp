@@ -716,6 +716,38 @@ oxo_driver *oxo_driver_new(oxo_engine *e, int depth) {
     return d;
 }
 void oxo_driver_free(oxo_driver *d) { delete d; }
+// a driver state imported from elsewhere (MtpDriver::import_state with no pending pairs): the MTP
+// head's KV seeded below q, h_{P-1} = hl
+void oxo_driver_import(oxo_driver *d, int64_t q, const float *hl) {
+    d->q = q;
+    d->cu_tok.clear();
+    d->cu_h.clear();
+    d->hl.assign(hl, hl + d->eng->d.n_embd);
+}
+// the engine's state in Engine::write_state's byte order (K rows, V^T rows per attention layer, then
+// the current slot's conv state and S) for n_pos positions; the position becomes n_pos
+int oxo_engine_read_state(oxo_engine *e, const uint8_t *buf, int64_t nbytes, int64_t n_pos) {
+    const int64_t hd = e->d.head_dim, nkv = e->d.n_head_kv;
+    const int64_t need = (int64_t)e->n_att * nkv * 2 * hd * 2 * n_pos + (e->conv_len + e->ssm_len) * e->n_rec * 4;
+    if (n_pos < 0 || n_pos > e->n_ctx || nbytes != need) return -1;
+    const uint8_t *p = buf;
+    for (int a = 0; a < e->n_att; a++) {
+        for (int64_t h = 0; h < nkv; h++) {
+            std::memcpy(e->kcache.data() + ((size_t)(a * nkv + h) * e->n_ctx) * hd, p, (size_t)n_pos * hd * 2);
+            p += n_pos * hd * 2;
+        }
+        for (int64_t r = 0; r < nkv * hd; r++) {
+            std::memcpy(e->vcache.data() + ((size_t)a * nkv * hd + r) * e->v_stride, p, (size_t)n_pos * 2);
+            p += n_pos * 2;
+        }
+    }
+    std::memcpy(e->conv_state.data() + (size_t)e->cur_slot * e->n_rec * e->conv_len, p, (size_t)e->n_rec * e->conv_len * 4);
+    p += e->n_rec * e->conv_len * 4;
+    std::memcpy(e->ssm_state.data() + (size_t)e->cur_slot * e->n_rec * e->ssm_len, p, (size_t)e->n_rec * e->ssm_len * 4);
+    e->pos = n_pos;
+    e->pend_n = 0;
+    return 0;
+}
 uint32_t oxo_driver_prefill(oxo_driver *d, const uint32_t *toks, int n) { return d->prefill(toks, n); }
 int oxo_driver_step(oxo_driver *d, uint32_t x, uint32_t *out, int64_t override_d1) { return d->step(x, out, override_d1); }
 int oxo_driver_step_force(oxo_driver *d, uint32_t x, uint32_t *out, const int64_t *force, int nforce) {

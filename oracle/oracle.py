@@ -127,6 +127,8 @@ def lib():
             "oxo_synth_normal": (None, [C.c_uint64, C.c_uint64, C.c_int64, C.c_float, C.c_float, f32p]),
             "oxo_driver_new": (C.c_void_p, [C.c_void_p, C.c_int]),
             "oxo_driver_free": (None, [C.c_void_p]),
+            "oxo_driver_import": (None, [C.c_void_p, C.c_int64, f32p]),
+            "oxo_engine_read_state": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int64, C.c_int64]),
             "oxo_driver_prefill": (C.c_uint32, [C.c_void_p, u32p, C.c_int]),
             "oxo_driver_step": (C.c_int, [C.c_void_p, C.c_uint32, u32p, C.c_int64]),
             "oxo_driver_step_plain": (C.c_uint32, [C.c_void_p, C.c_uint32]),
@@ -281,6 +283,11 @@ class Engine:
     def pos(self):
         return int(lib().oxo_pos(self.h))
 
+    def read_state(self, buf, n_pos):
+        """Engine::read_state (engine.rs:1819-1871) of write_state bytes"""
+        b = np.ascontiguousarray(buf, np.uint8)
+        assert lib().oxo_engine_read_state(self.h, b.ctypes.data_as(C.c_void_p), b.nbytes, n_pos) == 0, "read_state"
+
     def set_router(self, layer, row0, rows):
         r = np.ascontiguousarray(rows, np.float32)
         lib().oxo_engine_set_router(self.h, layer, row0, r.shape[0], ptr(r, C.c_float))
@@ -312,6 +319,10 @@ class Driver:
         else:
             n = lib().oxo_driver_step(self.h, x, ptr(out, C.c_uint32), override_d1)
         return [int(v) for v in out[:n]]
+
+    def import_state(self, q, hl):
+        h = np.ascontiguousarray(hl, np.float32)
+        lib().oxo_driver_import(self.h, q, ptr(h, C.c_float))
 
     def step_plain(self, x):
         return int(lib().oxo_driver_step_plain(self.h, x))

@@ -45,6 +45,8 @@ void oxo_synth_normal(uint64_t seed, uint64_t uid, int64_t n, float mu, float si
 
 oxo_driver *oxo_driver_new(oxo_engine *e, int depth);                          // mtp.rs:348-362
 void oxo_driver_free(oxo_driver *d);
+void oxo_driver_import(oxo_driver *d, int64_t q, const float *hl);
+int oxo_engine_read_state(oxo_engine *e, const uint8_t *buf, int64_t nbytes, int64_t n_pos);
 uint32_t oxo_driver_prefill(oxo_driver *d, const uint32_t *toks, int n);      // mtp.rs:450-463
 int oxo_driver_step(oxo_driver *d, uint32_t x, uint32_t *out, int64_t override_d1); // mtp.rs:522-592
 // the same with force[i] >= 0 replacing draft i (i < nforce) after the chain (draft_override, mtp.rs:554-558)

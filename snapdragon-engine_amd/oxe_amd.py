@@ -79,6 +79,33 @@ def bench_prompt(n):
     return (((i * 2654435761) & 0xFFFFFFFF) % 150000 + 1000).astype(np.uint32)
 
 
+def hash_bytes(b):
+    """The reference's 64-bit content hash (crates/model/src/weights.rs:254-272): four multiply-rotate
+    lanes over 32-byte words, a tail lane over the remaining bytes, then the lanes folded."""
+    M = 0xFFFFFFFFFFFFFFFF
+    K = (0x9E3779B97F4A7C15, 0xC2B2AE3D27D4EB4F, 0x165667B19E3779F9, 0xD6E8FEB86659FD93)
+    rotl = lambda v, r: ((v << r) | (v >> (64 - r))) & M  # noqa: E731
+    h = [0x243F6A8885A308D3, 0x13198A2E03707344, 0xA4093822299F31D0, 0x082EFA98EC4E6C89]
+    words = len(b) // 32
+    for i in range(words):
+        for l in range(4):
+            w = int.from_bytes(b[i * 32 + l * 8:i * 32 + l * 8 + 8], "little")
+            h[l] = rotl(((h[l] ^ w) * K[l]) & M, 31)
+    x = (len(b) * K[0]) & M
+    for v in b[words * 32:]:
+        x = rotl(((x ^ v) * K[1]) & M, 17)
+    for l, v in enumerate(h):
+        x = rotl(((x ^ v) * K[l]) & M, 23)
+    return x ^ (x >> 29)
+
+
+def hash_ids(ids):
+    """`generated_hash` of the reference's bench (sha_ids, crates/oxe-cli/src/bin/oxe.rs:417-419):
+    hash_bytes of the ids as little-endian u32, as 16 hex digits."""
+    b = b"".join(int(v).to_bytes(4, "little") for v in ids)
+    return f"{hash_bytes(b):016x}"
+
+
 def exported_symbols():
     """Names the header declares and the library must export."""
     hdr = os.path.join(HERE, "..", "include", "oxe_amd.h")

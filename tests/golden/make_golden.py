@@ -11,8 +11,17 @@ device path shows up as a diff against committed data:
   attn_head.npz      one attention head (head_dim 256, n_kv 256, pos_last 200)
   engine_small.npz   argmax ids and FNV-1a-64 hashes of logits / h_nextn of the 4-layer model over
                      a prompt and 6 greedy steps
-Run: python tests/golden/make_golden.py
+  config4_ids.npz    BASELINE config 4 at its stated size: the 35B-A3B model (seed 0), the reference
+                     bench prompt of 512 ids prefilled through MtpDriver::prefill, then 264 greedy
+                     MTP-1 steps; the generated ids as the reference's bench records them (every
+                     token fed to the target, oxe.rs:2108-2133) and their generated_hash
+  config5_state.npz  BASELINE config 5 on the 4-layer model (seed 7): 2048 prompt tokens decoded token
+                     by token; SHA-256 of Engine::write_state's bytes (K rows, V^T rows, conv state, S),
+                     of the last token's logits and h_nextn, and the next token
+Run: python tests/golden/make_golden.py [name ...]   (no name: the small fixtures; config4_ids needs
+~40 GB of host memory and several minutes on 16 threads)
 """
+import hashlib
 import ctypes as C
 import os
 import sys
@@ -108,8 +117,65 @@ def engine_small():
                 hidden_fnv=np.array(hh, np.uint64))
 
 
+def config4_ids(n_prompt=512, n_steps=264):
+    sys.path.insert(0, os.path.join(HERE, "..", "..", "snapdragon-engine_amd"))
+    import oxe_amd as A
+    d = O.desc_35b_a3b()
+    e = O.Engine(d, seed=0, n_ctx=n_prompt + 2 * n_steps + 64)
+    O.lib().oxo_set_keep_logits(e.h, 0)
+    drv = O.Driver(e)
+    prompt = O.bench_prompt(n_prompt)
+    x = drv.prefill(prompt)
+    gen = []
+    for i in range(n_steps):
+        gen.append(x)
+        out = drv.step(x)
+        gen += out[:-1]
+        x = out[-1]
+        if i % 16 == 0:
+            print(f"config4: step {i} pos {e.pos}", flush=True)
+    gen.append(x)
+    ids = np.array(gen, np.uint32)
+    return dict(prompt=prompt, steps=np.int32(n_steps), ids=ids, generated_hash=np.array(A.hash_ids(ids)),
+                stats=np.array(list(drv.stats().values()), np.int64))
+
+
+def config5_state(n=2048):
+    d = O.desc_small()
+    e = O.Engine(d, seed=7, n_ctx=n + 256)
+    toks = (O.bench_prompt(n) % d.n_vocab).astype(np.uint32)
+    x = None
+    for i, t in enumerate(toks):
+        x = e.step(int(t))
+        if i % 256 == 0:
+            print(f"config5: token {i}", flush=True)
+    HD, NKV, NCH, NVH, HV = d.head_dim, d.n_head_kv, 8192, d.ssm_n_vheads, 128
+    n_ctx = int(e.n_ctx)
+    n_att = d.n_layer // d.full_attention_interval + 1
+    n_rec = d.n_layer - (n_att - 1)
+    L = O.lib()
+    kc = np.ctypeslib.as_array(L.oxo_kcache(e.h), (n_att * NKV * n_ctx * HD,)).reshape(n_att, NKV, n_ctx, HD)
+    vc = np.ctypeslib.as_array(L.oxo_vcache(e.h), (n_att * NKV * HD * n_ctx,)).reshape(n_att, NKV * HD, n_ctx)
+    conv_len, ssm_len = n_rec * NCH * 3, n_rec * NVH * HV * HV
+    cur = L.oxo_cur_slot(e.h)
+    conv = np.ctypeslib.as_array(L.oxo_conv_state(e.h), (2 * conv_len,))[cur * conv_len:(cur + 1) * conv_len]
+    ssm = np.ctypeslib.as_array(L.oxo_ssm_state(e.h), (2 * ssm_len,))[cur * ssm_len:(cur + 1) * ssm_len]
+    kv = []
+    for ai in range(n_att):
+        for h in range(NKV):
+            kv.append(kc[ai, h, :n].tobytes())
+        kv.append(np.ascontiguousarray(vc[ai, :, :n]).tobytes())
+    sha = lambda b: hashlib.sha256(b).hexdigest()  # noqa: E731
+    state = b"".join(kv) + conv.tobytes() + ssm.tobytes()
+    return dict(prompt=toks, state_sha=np.array(sha(state)), kv_sha=np.array(sha(b"".join(kv))),
+                conv_sha=np.array(sha(conv.tobytes())), ssm_sha=np.array(sha(ssm.tobytes())),
+                logits_sha=np.array(sha(e.logits(0).tobytes())), hidden_sha=np.array(sha(e.hidden(0).tobytes())),
+                next=np.uint32(x), state_bytes=np.int64(len(state)))
+
+
 MAKERS = dict(config1_slice=config1_slice, route=route, dn_step=dn_step, attn_head=attn_head,
               engine_small=engine_small)
+LARGE = dict(config4_ids=config4_ids, config5_state=config5_state)
 
 # GGUF header fixtures: the fields the tests use of the reference's own test fixtures
 # tests/fixtures/{qwen36,ornith}.json (model_inspect.py's reading of the real Qwen3.6 and Ornith
@@ -129,7 +195,13 @@ def gguf_headers(ref="/root/reference/tests/fixtures"):
 
 
 if __name__ == "__main__":
-    for name, fn in MAKERS.items():
+    names = sys.argv[1:]
+    if not names:
+        for name, fn in MAKERS.items():
+            np.savez_compressed(os.path.join(HERE, name + ".npz"), **fn())
+            print("wrote", name)
+        gguf_headers()
+    for name in names:
+        fn = {**MAKERS, **LARGE}[name]
         np.savez_compressed(os.path.join(HERE, name + ".npz"), **fn())
         print("wrote", name)
-    gguf_headers()

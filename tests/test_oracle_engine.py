@@ -169,3 +169,34 @@ def test_tied_router_rows_take_the_sort_path(desc):
     assert b.step(3001) == g[1]
     assert np.array_equal(bits(b.logits(0)), bits(la))
     assert O.lib().oxo_tie_count(a.h) >= desc.n_layer * 2
+
+
+def test_read_state_handoff(desc):
+    # Engine::read_state of write_state-ordered bytes continues exactly like the original engine
+    import ctypes as C
+    L = O.lib()
+    a = O.Engine(desc, seed=SEED, n_ctx=256)
+    for t in (5, 900, 31, 4000, 12):
+        a.step(t)
+    n, nc, hd, nkv = a.pos, int(a.n_ctx), desc.head_dim, desc.n_head_kv
+    n_att = desc.n_layer // desc.full_attention_interval + 1
+    n_rec = desc.n_layer - (n_att - 1)
+    kc = np.ctypeslib.as_array(L.oxo_kcache(a.h), (n_att * nkv * nc * hd,)).reshape(n_att, nkv, nc, hd)
+    vc = np.ctypeslib.as_array(L.oxo_vcache(a.h), (n_att * nkv * hd * nc,)).reshape(n_att, nkv * hd, nc)
+    conv_len, ssm_len = n_rec * 8192 * 3, n_rec * 32 * 128 * 128
+    cur = L.oxo_cur_slot(a.h)
+    conv = np.ctypeslib.as_array(L.oxo_conv_state(a.h), (2 * conv_len,))[cur * conv_len:(cur + 1) * conv_len]
+    ssm = np.ctypeslib.as_array(L.oxo_ssm_state(a.h), (2 * ssm_len,))[cur * ssm_len:(cur + 1) * ssm_len]
+    parts = []
+    for ai in range(n_att):
+        for h in range(nkv):
+            parts.append(kc[ai, h, :n].tobytes())
+        parts.append(np.ascontiguousarray(vc[ai, :, :n]).tobytes())
+    blob = np.frombuffer(b"".join(parts) + conv.tobytes() + ssm.tobytes(), np.uint8)
+    b = O.Engine(desc, seed=SEED, n_ctx=256)
+    b.read_state(blob, n)
+    assert b.pos == n
+    assert L.oxo_engine_read_state(b.h, blob.ctypes.data_as(C.c_void_p), blob.nbytes - 1, n) == -1
+    for t in (77, 3):
+        assert a.step(t) == b.step(t)
+        assert np.array_equal(bits(a.logits(0)), bits(b.logits(0)))
