@@ -6,13 +6,15 @@
 //     threads [256 l, 256 l + 256) (8 elements each), and the exact double sums use the same
 //     bracket test, so their result does not depend on the reduction order;
 //   * Q8_0 GEMV slices: a workgroup owns a contiguous range of rows (or a fixed row list), loads all
-//     of its 16-byte code chunks and scale rows into registers before waiting at the barrier that
-//     releases the activations, then forms the exact int32 block dots and runs one serial fp32
-//     FMA chain per (row, lane) in block order, as the reference's NEON GEMV;
-//   * phase boundaries are grid barriers (per-XCD arrival counters, then one global counter; the
-//     last arrival publishes the round). Data a later phase of the same launch reads from another
-//     workgroup is stored and loaded with device-scope accesses.
-// Every spin is bounded: a stuck barrier sets the error word and every workgroup leaves.
+//     of its 16-byte code chunks and scale rows into registers before it polls for the activations,
+//     then forms the exact int32 block dots and runs one serial fp32 FMA chain per (row, lane) in
+//     block order, as the reference's NEON GEMV;
+//   * no grid barrier: every value a phase passes to another workgroup is a tagged 64-bit word
+//     (FzXch, oxe_fused.h), and a reader polls the words it needs until they carry the tag of the
+//     phase that writes them. A workgroup therefore waits only for its own inputs, and a phase of
+//     one workgroup overlaps the previous phase of the others.
+// Every poll is bounded: a poll that times out sets the sticky error word, and every workgroup
+// that sees it leaves the run.
 #include "oxe_fused.h"
 #include "oxe_gemv.h"
 #include "oxe_prologue.h"
@@ -81,55 +83,63 @@ OXE_DEV void cst128(void *p, uint4 v) {
     cst64((char *)p + 8, (unsigned long long)v.z | ((unsigned long long)v.w << 32));
 }
 
-// ---- grid barrier -----------------------------------------------------------------------------
-struct Bar {
-    uint32_t *w;
-    uint32_t &round;   // thread 0's copy lives in LDS (only thread 0 reads or writes it)
-};
+// ---- tagged exchange (FzXch) ----------------------------------------------------------------
+// phases of run layer k (the verify's layer il: k = il; the MTP layer of a draft / seed run: k = 1,
+// its entry acting as the "down" phase of k = 0)
+enum { PH_PROJ = 0, PH_MIX = 1, PH_PV = 2, PH_OUT = 3, PH_ROUTER = 4, PH_EXP = 5, PH_DOWN = 6 };
 
-// Arrival: every thread's stores of the phase are complete before the workgroup is counted.
-OXE_DEV void arrive(Bar b) {
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        b.round++;
-        const uint32_t x = blockIdx.x & (FZ_XCD - 1);
-        const uint32_t per = gridDim.x / FZ_XCD;
-        const uint32_t old = __hip_atomic_fetch_add(&b.w[32 * x], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (old == b.round * per - 1) {
-            const uint32_t og = __hip_atomic_fetch_add(&b.w[FZ_W_GLOB], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            if (og == b.round * FZ_XCD - 1) {
-                // release: one copy of the round per XCD line, then the launch-level copy
+OXE_DEV unsigned long long ll_pack(uint32_t v, uint32_t tag) { return ((unsigned long long)tag << 32) | v; }
+OXE_DEV void ll_st(uint64_t *p, uint32_t v, uint32_t tag) { cst64(p, ll_pack(v, tag)); }
+OXE_DEV void ll_stf(uint64_t *p, float v, uint32_t tag) { ll_st(p, __builtin_bit_cast(uint32_t, v), tag); }
+OXE_DEV bool ll_ok(unsigned long long w, uint32_t tag) { return (uint32_t)(w >> 32) == tag; }
+
+// Spin until the N words at p (consecutive) carry `tag`; their values to v. Every spin is bounded:
+// past SPIN_MAX polls the sticky error word is set; a poll also stops when another workgroup set it.
+// false: the run was aborted.
+template <int N>
+OXE_DEV bool ll_ld(const uint64_t *p, uint32_t tag, uint32_t v[N], uint32_t *err) {
+    unsigned long long w[N];
 #pragma unroll
-                for (int i = 0; i < FZ_XCD; i++) cst32(&b.w[FZ_W_REL + 32 * i], b.round);
-                cst32(&b.w[FZ_W_FLAG], b.round);
-            }
+    for (int i = 0; i < N; i++) w[i] = cld64(p + i);
+    uint32_t spins = 0;
+    while (true) {
+        bool ok = true;
+#pragma unroll
+        for (int i = 0; i < N; i++) ok = ok && ll_ok(w[i], tag);
+        if (ok) break;
+        if (++spins > SPIN_MAX) {
+            cst32(err, 1u);
+            return false;
         }
+        if ((spins & 31) == 0 && cld32(err)) return false;
+        __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+        for (int i = 0; i < N; i++)
+            if (!ll_ok(w[i], tag)) w[i] = cld64(p + i);
     }
+#pragma unroll
+    for (int i = 0; i < N; i++) v[i] = (uint32_t)w[i];
+    return true;
+}
+template <int N>
+OXE_DEV bool ll_ldf(const uint64_t *p, uint32_t tag, float v[N], uint32_t *err) {
+    uint32_t u[N];
+    const bool ok = ll_ld<N>(p, tag, u, err);
+#pragma unroll
+    for (int i = 0; i < N; i++) v[i] = __builtin_bit_cast(float, u[i]);
+    return ok;
 }
 
-// Wait until every workgroup arrived at the current round. false: the run was aborted.
-OXE_DEV bool wait(Bar b, int *s_ok) {
-    if (threadIdx.x == 0) {
-        int ok = 1;
-        uint32_t spins = 0;
-        const uint32_t *rel = &b.w[FZ_W_REL + 32 * (blockIdx.x & (FZ_XCD - 1))];
-        while ((int32_t)(cld32(rel) - b.round) < 0) {
-            if (++spins > SPIN_MAX) {
-                cst32(&b.w[FZ_W_ERR], 1u);
-                ok = 0;
-                break;
-            }
-            if ((spins & 31) == 0 && cld32(&b.w[FZ_W_ERR])) {
-                ok = 0;
-                break;
-            }
-            __builtin_amdgcn_s_sleep(1);
-        }
-        *s_ok = ok;
-    }
+// every thread's verdict of its polls combined (all threads call): false if any thread of the
+// workgroup saw the run aborted. s_fail is sticky (cleared at the launch's start; an aborted
+// workgroup leaves the run), and the second barrier keeps a later call's update from reaching a
+// thread still reading this one's result.
+OXE_DEV bool all_ok(bool ok, int *s_fail) {
+    if (!ok) *s_fail = 1;
     __syncthreads();
-    return *s_ok != 0;
+    const bool r = *s_fail == 0;
+    __syncthreads();
+    return r;
 }
 
 // ---- GEMV slices ------------------------------------------------------------------------------
@@ -266,14 +276,6 @@ OXE_DEV void get8(const float *x, float v[8]) {
     const float4 a = *(const float4 *)x, b = *(const float4 *)(x + 4);
     v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
 }
-OXE_DEV void cget8(const float *x, float v[8]) {
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const unsigned long long u = cld64(x + 2 * i);
-        v[2 * i] = __builtin_bit_cast(float, (uint32_t)u);
-        v[2 * i + 1] = __builtin_bit_cast(float, (uint32_t)(u >> 32));
-    }
-}
 // dequantize_row_q8_0 (quants_base.c:64-78) of elements [8 tt, 8 tt + 8) of token row tok
 OXE_DEV void embed8t(const int8_t *eq, const uint16_t *ed, uint32_t tok, int tt, float v[8]) {
     const int8_t *q = eq + (int64_t)tok * E + 8 * tt;
@@ -302,24 +304,26 @@ OXE_DEV T lane_pick(const FZ_CAS T *v, int l) {
 }
 
 // The run's lanes normalised with w and quantised to xq/xd (LDS). Source per lane: the token
-// embedding (eq != null), a vector written in this launch (coherent), or one from an earlier launch.
-// xf: LDS staging of the raw vectors; xn (optional): the normalised f32 vectors.
+// embedding (eq != null) or a tagged exchange buffer (src: [NL][E] words with tag `tag`; thread
+// (lane l, tt) reads elements [8 tt, 8 tt + 8), one producing workgroup's rows). xf: LDS staging of
+// the raw vectors; xn (optional): the normalised f32 vectors. false: the run was aborted.
 template <int NL>
-OXE_DEV void prologue(int nl, const FZ_CAS RunCtl *ctl, const int8_t *eq, const uint16_t *ed, const float *src,
-                      int64_t src_ld, bool coherent,
+OXE_DEV bool prologue(int nl, const FZ_CAS RunCtl *ctl, const int8_t *eq, const uint16_t *ed, const uint64_t *src,
+                      uint32_t tag, uint32_t *err,
                       const W8 &w, float eps, float (*xf)[E], int8_t *xq, int xq_ld, uint16_t *xd, int xd_ld,
-                      NormSm &ns, float (*xn)[E]) {
+                      NormSm &ns, float (*xn)[E], int *s_ok) {
     const int t = threadIdx.x, l = t >> 8, tt = t & 255;
     float v[8];
     const bool act = l < NL && l < nl;
+    bool ok = true;
     if (act) {
         if (eq) embed8t(eq, ed, lane_pick<NL>(ctl->tok, l), tt, v);
-        else if (coherent) cget8(src + l * src_ld + 8 * tt, v);
-        else get8(src + l * src_ld + 8 * tt, v);
+        else ok = ll_ldf<8>(src + l * E + 8 * tt, tag, v, err);
     } else {
 #pragma unroll
         for (int i = 0; i < 8; i++) v[i] = 0.0f;
     }
+    if (!all_ok(ok, s_ok)) return false;
     if (l < NL) put8(&xf[l][8 * tt], v);
     __syncthreads();
     norm8(v, xf[l < NL ? l : 0], w.v, eps, ns);
@@ -334,6 +338,7 @@ OXE_DEV void prologue(int nl, const FZ_CAS RunCtl *ctl, const int8_t *eq, const 
         }
     }
     __syncthreads();
+    return true;
 }
 
 // ---- shared memory of the phases -------------------------------------------------------------
@@ -349,7 +354,6 @@ template <int NL>
 struct DnSm {
     float q[NL][DS], k[NL][DS], v[NL][HV], o[NL][HV];
     float g[NL], b[NL];
-    int last;
 };
 template <int NL>
 struct OutSm {
@@ -433,8 +437,10 @@ struct Persist {
     int32_t uni[OXE_MAX_UNION];
     int32_t nu;
     int32_t slot[NL][KUSED];   // union slot of each lane's rank-j expert
-    int ok;
-    uint32_t round;
+    alignas(16) int8_t xq[NL][E];    // the post-attention-norm lanes, Q8_0 (router phase -> experts)
+    uint16_t xd[NL][E / 32];
+    int fail;                        // a poll of this workgroup saw the run aborted (sticky)
+    uint32_t base;                   // tag base of the launch
     uint32_t tev;                    // trace: next event index of this workgroup
     uint32_t dyn_off;                // LDS offset of the dynamic LDS (fz_dyn), set by the kernel
     unsigned long long t_start, t_pass, t_mark;
@@ -455,19 +461,28 @@ struct Ctx {
     PhaseSm<NL> *sm;
     Persist<NL> *ps;
     unsigned char *dyn;
-    Bar bar;
+    uint32_t *err;              // the sticky error word
+    uint32_t base;              // tag base of the launch
+    int k;                      // run layer index: exchange buffer parity k & 1
     unsigned long long *trace;
     int nl, G, b;
+    // tag of phase ph of run layer kk
+    OXE_DEV uint32_t tag(int kk, int ph) const { return base + 1u + 8u * (uint32_t)kk + (uint32_t)ph; }
+    OXE_DEV int par() const { return k & 1; }
 };
 
 template <int NL>
-OXE_DEV Ctx<NL> make_ctx(const RunCtl *ctl, const FusedArgs *ap) {
+OXE_DEV Ctx<NL> make_ctx(const RunCtl *ctl, const FusedArgs *ap, int k) {
     static_assert(NL == OXE_NL, "one lane count");
     const FZ_CAS FusedArgs *a = uni(ap);
     // the dynamic LDS from its offset (a non-kernel function would otherwise look its base up in a
     // per-kernel table in device memory, a load that may be repeated behind the weight loads in flight)
     unsigned char *dyn = (unsigned char *)(FZ_LDS unsigned char *)(uintptr_t)fz_ps.dyn_off;
-    Ctx<NL> c{uni(ctl), a, (PhaseSm<NL> *)dyn, &fz_ps, dyn, Bar{a->sync, fz_ps.round}, a->trace, 0, 0, 0};
+    // the phase's LDS aliases the previous phase's: no thread writes it before every thread is done
+    // with the previous phase
+    __syncthreads();
+    Ctx<NL> c{uni(ctl), a, (PhaseSm<NL> *)dyn, &fz_ps, dyn, a->sync + FZ_W_ERR,
+              (uint32_t)__builtin_amdgcn_readfirstlane((int)fz_ps.base), k, a->trace, 0, 0, 0};
     c.nl = c.ctl->nl < 1 ? 1 : (c.ctl->nl > NL ? NL : c.ctl->nl);
     c.G = gridDim.x;
     c.b = blockIdx.x;
@@ -520,10 +535,11 @@ OXE_DEV void tr_end(Ctx<NL> &c, int id) {
 // ---- phases ----------------------------------------------------------------------------------
 
 // proj: rows [r_begin, r_end) of the layer's input projection over the normalised lanes; V rows
-// (attention) also go to V^T at pos0 + l. Input: the embedding (layer 0 of a verify) or x.
+// (attention) also go to V^T at pos0 + l (read by later launches; this launch's attention takes the
+// new positions' V from the projection outputs). Input: the embedding (layer 0 of a verify) or x.
 template <int NL>
-FZ_PHASE bool phase_proj(const RunCtl *ctl, const FusedArgs *ap, int il, bool embed, const float *x, int r_begin, int r_end) {
-    Ctx<NL> c = make_ctx<NL>(ctl, ap);
+FZ_PHASE bool phase_proj(const RunCtl *ctl, const FusedArgs *ap, int il, int k, bool embed, int r_begin, int r_end) {
+    Ctx<NL> c = make_ctx<NL>(ctl, ap, k);
     tr_start(c);
     const FZ_CAS FusedArgs &a = *c.a;
     const FZ_CAS LayerDev &L = layer_of(c, il);
@@ -534,34 +550,35 @@ FZ_PHASE bool phase_proj(const RunCtl *ctl, const FusedArgs *ap, int il, bool em
     WSlice<E, 13> ws;
     wload<E, 13>(ws, L.proj.q, L.proj.d, nr, [&](int rl) { return (int64_t)(r0 + rl); });
     const W8 nw = wload8(L.attn_norm);
-    if (!wait(c.bar, &c.ps->ok)) return false;
+    uint64_t *xin = a.xc.x + (size_t)c.par() * NL * E;
+    if (!prologue<NL>(c.nl, c.ctl, embed ? a.m.tok_embd.q : nullptr, a.m.tok_embd.d, xin, k > 0 ? c.tag(k - 1, PH_DOWN) : 0u,
+                      c.err, nw, a.m.eps, s.xf, &s.xq[0][0], E, &s.xd[0][0], E / 32, s.ns, nullptr, &c.ps->fail))
+        return false;
     tr_pass(c);
-    prologue<NL>(c.nl, c.ctl, embed ? a.m.tok_embd.q : nullptr, a.m.tok_embd.d, x, E, true, nw, a.m.eps, s.xf, &s.xq[0][0], E,
-                 &s.xd[0][0], E / 32, s.ns, nullptr);
     tr_mark(c, 111);
     if (embed && c.b == 0) {
         // the embedded input is the residual of layer 0
         const int t = threadIdx.x, l = t >> 8, tt = t & 255;
         if (l < c.nl)
-            for (int i = 0; i < 8; i++) cst(a.b.x + l * E + 8 * tt + i, s.xf[l][8 * tt + i]);
+            for (int i = 0; i < 8; i++) ll_stf(xin + l * E + 8 * tt + i, s.xf[l][8 * tt + i], c.tag(k, PH_PROJ));
     }
     wdot<E, 13, NL>(ws, nr, &s.xq[0][0], E, &s.xd[0][0], E / 32, s.g);
     tr_mark(c, 112);
     const int t = threadIdx.x;
+    uint64_t *po = a.xc.p + (size_t)c.par() * NL * DN_ROWS;
     if (t < NL * 52) {
         const int l = t / 52, rl = t % 52;
         if (l < c.nl && rl < nr) {
             const int row = r0 + rl;
             const float v = s.g.out[l][rl];
-            cst(a.b.proj + (int64_t)l * DN_ROWS + row, v);
+            ll_stf(po + (int64_t)l * DN_ROWS + row, v, c.tag(k, PH_PROJ));
             if (L.att && row >= AT_V) {
                 uint16_t *vt = a.m.vcache + (int64_t)L.index * NKV * HD * a.m.n_ctx;
-                cst16(vt + (int64_t)(row - AT_V) * a.m.n_ctx + c.ctl->pos0 + l, f2h(v));
+                vt[(int64_t)(row - AT_V) * a.m.n_ctx + c.ctl->pos0 + l] = f2h(v);
             }
         }
     }
     tr_end(c, TP_PROJ);
-    arrive(c.bar);
     return true;
 }
 
@@ -569,8 +586,8 @@ FZ_PHASE bool phase_proj(const RunCtl *ctl, const FusedArgs *ap, int il, bool em
 // workgroup b takes value head vh = b / DN_WPH and state rows [16 (b % DN_WPH), +16); thread
 // (rg = t/16, c = t%16), t < 256, owns state row 16 (b % DN_WPH) + rg. Every workgroup of a head
 // forms the head's conv outputs and normalised q, k (gdn conv + l2 norms, oxe_ops.cpp:218-267) and
-// writes its 16 outputs; the last of the head's workgroups to count itself in (per-head arrival
-// counter) forms the gated norm of the head's 128 outputs and quantizes them.
+// writes its 16 outputs; the head's first workgroup then reads the head's 128 outputs back (tagged)
+// and forms their gated norm and Q8_0 quantisation.
 constexpr int DN_WPH = 8, DN_RPW = HV / DN_WPH;
 OXE_DEV float dot16_tree_f(float acc) { return dot16_tree_dpp(acc); }
 OXE_DEV float conv4f(float s0, float s1, float s2, float xn, const float *c) {
@@ -583,8 +600,8 @@ OXE_DEV float conv4f(float s0, float s1, float s2, float xn, const float *c) {
     return sumf;
 }
 template <int NL>
-FZ_PHASE bool phase_dn(const RunCtl *ctl, const FusedArgs *ap, int il) {
-    Ctx<NL> c = make_ctx<NL>(ctl, ap);
+FZ_PHASE bool phase_dn(const RunCtl *ctl, const FusedArgs *ap, int il, int k) {
+    Ctx<NL> c = make_ctx<NL>(ctl, ap, k);
     tr_start(c);
     const FZ_CAS FusedArgs &a = *c.a;
     const FZ_CAS LayerDev &L = layer_of(c, il);
@@ -628,17 +645,24 @@ FZ_PHASE bool phase_dn(const RunCtl *ctl, const FusedArgs *ap, int il) {
     if (gate) { dtb = L.dt_bias[vh]; sa = L.ssm_a[vh]; }
     float nw0 = 0.0f, nw1 = 0.0f;
     if (worker && w < NL) { nw0 = L.ssm_norm[lane]; nw1 = L.ssm_norm[lane + 64]; }
-    if (!wait(c.bar, &c.ps->ok)) return false;
-    tr_pass(c);
+    const uint64_t *pin = a.xc.p + (size_t)c.par() * NL * DN_ROWS;
+    uint64_t *gx = a.xc.g + (size_t)c.par() * NL * MIX_W;
+    const uint32_t tp = c.tag(k, PH_PROJ), tg = c.tag(k, PH_MIX);
     if (worker) {
         const int nl = c.nl;
         float xin[NL], ga = 0.0f, gb = 0.0f;
+        bool ok = true;
 #pragma unroll
-        for (int l = 0; l < NL; l++) xin[l] = conv && l < nl ? cld(a.b.proj + (int64_t)l * DN_ROWS + ch) : 0.0f;
-        if (gate && gl < nl) {
-            ga = cld(a.b.proj + (int64_t)gl * DN_ROWS + DN_ALPHA + vh);
-            gb = cld(a.b.proj + (int64_t)gl * DN_ROWS + DN_BETA + vh);
+        for (int l = 0; l < NL; l++) {
+            xin[l] = 0.0f;
+            if (conv && l < nl) ok = ok && ll_ldf<1>(pin + (int64_t)l * DN_ROWS + ch, tp, &xin[l], c.err);
         }
+        if (gate && gl < nl) {
+            ok = ok && ll_ldf<1>(pin + (int64_t)gl * DN_ROWS + DN_ALPHA + vh, tp, &ga, c.err);
+            ok = ok && ll_ldf<1>(pin + (int64_t)gl * DN_ROWS + DN_BETA + vh, tp, &gb, c.err);
+        }
+        if (!all_ok(ok, &c.ps->fail)) return false;
+        tr_pass(c);
         if (conv) {
 #pragma unroll
             for (int l = 0; l < NL; l++) {
@@ -698,25 +722,18 @@ FZ_PHASE bool phase_dn(const RunCtl *ctl, const FusedArgs *ap, int il) {
                     stl[l][q] = r[q];
                 }
                 const float sq = dot16_tree_f(acc);
-                if (cc == 0) cst(a.b.gdn + (int64_t)l * DIN + vh * HV + row0 + rg, sq * scale);
+                if (cc == 0) ll_stf(gx + (int64_t)l * DIN + vh * HV + row0 + rg, sq * scale, tg);
             }
         }
-        // count this workgroup in once its outputs are visible device-wide
-        __builtin_amdgcn_s_waitcnt(0);
-        __syncthreads();
-        if (t == 0) {
-            const uint32_t old =
-                __hip_atomic_fetch_add(&a.sync[FZ_W_HEAD + 32 * vh], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            s.last = (old % DN_WPH) == DN_WPH - 1;
-        }
-        __syncthreads();
-        const bool last = s.last != 0;
+        // the head's first workgroup reads the head's 128 outputs of every lane back
+        const bool last = row0 == 0;
         float x0 = 0.0f, x1 = 0.0f, z0 = 0.0f, z1 = 0.0f;
+        ok = true;
         if (last && w < nl) {
-            const float *o = a.b.gdn + (int64_t)w * DIN + vh * HV;
-            const float *z = a.b.proj + (int64_t)w * DN_ROWS + DN_Z + vh * HV;
-            x0 = cld(o + lane); x1 = cld(o + lane + 64);
-            z0 = cld(z + lane); z1 = cld(z + lane + 64);
+            const uint64_t *o = gx + (int64_t)w * DIN + vh * HV;
+            const uint64_t *z = pin + (int64_t)w * DN_ROWS + DN_Z + vh * HV;
+            ok = ll_ldf<1>(z + lane, tp, &z0, c.err) && ll_ldf<1>(z + lane + 64, tp, &z1, c.err) &&
+                 ll_ldf<1>(o + lane, tg, &x0, c.err) && ll_ldf<1>(o + lane + 64, tg, &x1, c.err);
         }
         if (dlt) {
 #pragma unroll
@@ -739,25 +756,26 @@ FZ_PHASE bool phase_dn(const RunCtl *ctl, const FusedArgs *ap, int il) {
             const float o1 = ((x1 * sc) * nw1) * v_silu(z1);
             float d0, d1;
             const uint32_t p0 = quant32_lanes(o0, &d0), p1 = quant32_lanes(o1, &d1);
-            int8_t *q = a.b.oq + (int64_t)l * DIN + vh * HV;
+            uint64_t *q = a.xc.o + ((size_t)c.par() * NL + l) * (DIN / 4) + (vh * HV) / 4;
             if ((lane & 3) == 0) {
-                cst32(q + lane, p0);
-                cst32(q + lane + 64, p1);
+                ll_st(q + lane / 4, p0, tg);
+                ll_st(q + (lane + 64) / 4, p1, tg);
             }
-            uint16_t *d = a.b.od + (int64_t)l * (DIN / 32) + vh * (HV / 32);
-            if (lane == 0) { cst16(d + 0, f2h(d0)); cst16(d + 2, f2h(d1)); }
-            if (lane == 32) { cst16(d + 1, f2h(d0)); cst16(d + 3, f2h(d1)); }
+            uint64_t *d = a.xc.od + ((size_t)c.par() * NL + l) * (DIN / 32) + vh * (HV / 32);
+            if (lane == 0) { ll_st(d + 0, f2h(d0), tg); ll_st(d + 2, f2h(d1), tg); }
+            if (lane == 32) { ll_st(d + 1, f2h(d0), tg); ll_st(d + 3, f2h(d1), tg); }
         }
+        if (!all_ok(ok, &c.ps->fail)) return false;
     }
     tr_end(c, TP_DN);
-    arrive(c.bar);
     return true;
 }
 
-// out: rows [8 b, 8 b + 8) of ssm_out / attn_output over the quantised mixer output, + residual x
+// out: rows [8 b, 8 b + 8) of ssm_out / attn_output over the quantised mixer output, + the residual
+// (x of the layer, tag xtag); the sums go to x1
 template <int NL>
-FZ_PHASE bool phase_out(const RunCtl *ctl, const FusedArgs *ap, int il, const float *x) {
-    Ctx<NL> c = make_ctx<NL>(ctl, ap);
+FZ_PHASE bool phase_out(const RunCtl *ctl, const FusedArgs *ap, int il, int k, uint32_t xtag) {
+    Ctx<NL> c = make_ctx<NL>(ctl, ap, k);
     tr_start(c);
     const FZ_CAS FusedArgs &a = *c.a;
     const FZ_CAS LayerDev &L = layer_of(c, il);
@@ -766,69 +784,68 @@ FZ_PHASE bool phase_out(const RunCtl *ctl, const FusedArgs *ap, int il, const fl
     const int r0 = 8 * c.b;
     WSlice<MIX_W, 4> ws;
     wload<MIX_W, 4>(ws, L.out.q, L.out.d, 8, [&](int rl) { return (int64_t)(r0 + rl); });
-    if (!wait(c.bar, &c.ps->ok)) return false;
-    tr_pass(c);
+    const uint64_t *xin = a.xc.x + (size_t)c.par() * NL * E;
+    const uint32_t tm = c.tag(k, L.att ? PH_PV : PH_MIX);
+    bool ok = true;
     float xres = 0.0f;
-    if (t < NL * 8 && t / 8 < c.nl) xres = cld(x + (int64_t)(t / 8) * E + r0 + t % 8);
+    if (t < NL * 8 && t / 8 < c.nl) ok = ll_ldf<1>(xin + (int64_t)(t / 8) * E + r0 + t % 8, xtag, &xres, c.err);
+    const int l = t >> 8, tt = t & 255;
+    const bool act = l < NL && l < c.nl;
     if (L.att) {
         // the attention's gated outputs (f32): thread (lane l, 16 elements at 16 tt), Q8_0 blocks of
         // 32 over adjacent thread pairs (quantize_row_q8_0 NEON: amax, d = amax / 127, id from the
         // f32 d, round-half-even codes)
-        const int l = t >> 8, tt = t & 255;
         float v[16];
 #pragma unroll
-        for (int k = 0; k < 8; k++) {
-            const unsigned long long u = l < NL && l < c.nl ? cld64(a.b.gdn + (int64_t)l * MIX_W + 16 * tt + 2 * k) : 0ull;
-            v[2 * k] = __builtin_bit_cast(float, (uint32_t)u);
-            v[2 * k + 1] = __builtin_bit_cast(float, (uint32_t)(u >> 32));
-        }
+        for (int q = 0; q < 16; q++) v[q] = 0.0f;
+        if (act) ok = ll_ldf<16>(a.xc.g + ((size_t)c.par() * NL + l) * MIX_W + 16 * tt, tm, v, c.err) && ok;
         float am = 0.0f;
 #pragma unroll
-        for (int k = 0; k < 16; k++) am = fmaxf(am, __builtin_fabsf(v[k]));
+        for (int q = 0; q < 16; q++) am = fmaxf(am, __builtin_fabsf(v[q]));
         am = fmaxf(am, dpp_f<DPP_XOR1>(am));
         const float dd = am / 127.0f;
         const float id = dd != 0.0f ? 1.0f / dd : 0.0f;
         uint32_t w[4];
 #pragma unroll
-        for (int k = 0; k < 4; k++) {
+        for (int q = 0; q < 4; q++) {
             uint32_t u = 0;
 #pragma unroll
-            for (int b = 0; b < 4; b++) u |= ((uint32_t)((int32_t)__builtin_rintf(v[4 * k + b] * id) & 0xff)) << (8 * b);
-            w[k] = u;
+            for (int bb = 0; bb < 4; bb++) u |= ((uint32_t)((int32_t)__builtin_rintf(v[4 * q + bb] * id) & 0xff)) << (8 * bb);
+            w[q] = u;
         }
         if (l < NL) {
             *(uint4 *)&s.xq[l][16 * tt] = make_uint4(w[0], w[1], w[2], w[3]);
             if ((tt & 1) == 0) s.xd[l][tt / 2] = f2h(dd);
         }
     } else {
-        const int l = t >> 8, tt = t & 255;
-        if (l < NL)
-            *(uint4 *)&s.xq[l][16 * tt] = l < c.nl ? cld128(a.b.oq + (int64_t)l * MIX_W + 16 * tt) : make_uint4(0, 0, 0, 0);
+        uint32_t w[4] = {0u, 0u, 0u, 0u};
+        if (act) ok = ll_ld<4>(a.xc.o + ((size_t)c.par() * NL + l) * (MIX_W / 4) + 4 * tt, tm, w, c.err) && ok;
+        if (l < NL) *(uint4 *)&s.xq[l][16 * tt] = make_uint4(w[0], w[1], w[2], w[3]);
         if (t < NL * (MIX_W / 32)) {
             const int ll = t / (MIX_W / 32), bb = t % (MIX_W / 32);
-            s.xd[ll][bb] = ll < c.nl ? cld16(a.b.od + (int64_t)ll * (MIX_W / 32) + bb) : (uint16_t)0;
+            uint32_t d = 0u;
+            if (ll < c.nl) ok = ll_ld<1>(a.xc.od + ((size_t)c.par() * NL + ll) * (MIX_W / 32) + bb, tm, &d, c.err) && ok;
+            s.xd[ll][bb] = (uint16_t)d;
         }
     }
-    __syncthreads();
+    if (!all_ok(ok, &c.ps->fail)) return false;
+    tr_pass(c);
     wdot<MIX_W, 4, NL>(ws, 8, &s.xq[0][0], MIX_W, &s.xd[0][0], MIX_W / 32, s.g);
     if (t < NL * 8) {
-        const int l = t / 8, rl = t % 8;
-        if (l < c.nl) {
-            const int64_t i = (int64_t)l * E + r0 + rl;
-            cst(a.b.x1 + i, s.g.out[l][rl] + xres);
-        }
+        const int ll = t / 8, rl = t % 8;
+        if (ll < c.nl)
+            ll_stf(a.xc.x1 + ((size_t)c.par() * NL + ll) * E + r0 + rl, s.g.out[ll][rl] + xres, c.tag(k, PH_OUT));
     }
     tr_end(c, TP_OUT);
-    arrive(c.bar);
     return true;
 }
 
-// router: post_attention_norm + quantise (WG 0 publishes the quantised lanes for the experts),
+// router: post_attention_norm + quantise (kept in this workgroup's persistent LDS for the experts),
 // router row b (f32, ggml_vec_dot_f32 order), the shared gate (last WG), shared gate/up half tiles
 // (WGs < 128: gate rows 16 tile + 4 half + i and the matching up rows) + swiglu
 template <int NL>
-FZ_PHASE bool phase_router(const RunCtl *ctl, const FusedArgs *ap, int il) {
-    Ctx<NL> c = make_ctx<NL>(ctl, ap);
+FZ_PHASE bool phase_router(const RunCtl *ctl, const FusedArgs *ap, int il, int k) {
+    Ctx<NL> c = make_ctx<NL>(ctl, ap, k);
     tr_start(c);
     const FZ_CAS FusedArgs &a = *c.a;
     const FZ_CAS LayerDev &L = layer_of(c, il);
@@ -845,27 +862,25 @@ FZ_PHASE bool phase_router(const RunCtl *ctl, const FusedArgs *ap, int il) {
     auto rowof = [&](int rl) { return (int64_t)(tile * 16 + (rl < 4 ? hf * 4 + rl : 8 + hf * 4 + (rl - 4))); };
     wload<E, 2>(ws, L.shexp_gu.q, L.shexp_gu.d, gu ? 8 : 0, rowof);
     const W8 nw = wload8(L.post_norm);
-    if (!wait(c.bar, &c.ps->ok)) return false;
-    tr_pass(c);
     {
-        // element e = 4 t + k goes to chain e % 16, step e / 16
+        // element e = 4 t + q goes to chain e % 16, step e / 16
         const float wr[4] = {wrow.x, wrow.y, wrow.z, wrow.w}, gr[4] = {wsg.x, wsg.y, wsg.z, wsg.w};
 #pragma unroll
-        for (int k = 0; k < 4; k++) {
-            const int e = 4 * t + k;
-            s.w[e % 16][e / 16] = wr[k];
-            if (shg) s.sg[e % 16][e / 16] = gr[k];
+        for (int q = 0; q < 4; q++) {
+            const int e = 4 * t + q;
+            s.w[e % 16][e / 16] = wr[q];
+            if (shg) s.sg[e % 16][e / 16] = gr[q];
         }
     }
-    prologue<NL>(c.nl, c.ctl, nullptr, nullptr, a.b.x1, E, true, nw, a.m.eps, s.xf, &s.xq[0][0], E, &s.xd[0][0], E / 32,
-                 s.ns, s.xn);
-    tr_mark(c, 131);
-    if (b == 0) {
+    if (!prologue<NL>(c.nl, c.ctl, nullptr, nullptr, a.xc.x1 + (size_t)c.par() * NL * E, c.tag(k, PH_OUT), c.err, nw,
+                      a.m.eps, s.xf, &s.xq[0][0], E, &s.xd[0][0], E / 32, s.ns, s.xn, &c.ps->fail))
+        return false;
+    tr_pass(c);
+    {
         const int l = t >> 8, tt = t & 255;
-        if (l < c.nl) {
-            const uint2 v = *(const uint2 *)&s.xq[l][8 * tt];
-            cst64(a.b.xq + (int64_t)l * 2 * E + 8 * tt, (unsigned long long)v.x | ((unsigned long long)v.y << 32));
-            if ((tt & 3) == 0) cst16(a.b.xd + (int64_t)l * (2 * E / 32) + (8 * tt) / 32, s.xd[l][(8 * tt) / 32]);
+        if (l < NL) {
+            *(uint2 *)&c.ps->xq[l][8 * tt] = *(const uint2 *)&s.xq[l][8 * tt];
+            if ((tt & 3) == 0) c.ps->xd[l][(8 * tt) / 32] = s.xd[l][(8 * tt) / 32];
         }
     }
     // f32 dots: lane c of a 16-lane group runs chain c (elements c + 16 q); xor 8, 4, 1, 2 is the
@@ -875,8 +890,8 @@ FZ_PHASE bool phase_router(const RunCtl *ctl, const FusedArgs *ap, int il) {
         const int l = t >> 8, tt = t & 255;
         if (l < NL) {
 #pragma unroll
-            for (int k = 0; k < 8; k++) {
-                const int e = 8 * tt + k;
+            for (int q = 0; q < 8; q++) {
+                const int e = 8 * tt + q;
                 s.xc[l][e % 16][e / 16] = s.xn[l][e];
             }
         }
@@ -900,8 +915,8 @@ FZ_PHASE bool phase_router(const RunCtl *ctl, const FusedArgs *ap, int il) {
         }
         const float v = dot16_tree_f(acc);
         if (cc == 0 && l < c.nl) {
-            if (!sgd) cst(a.b.router_lg + l * NEXP + b, v);
-            else if (shg) cst(a.b.sh_gate + l, sigmoid_c(v));
+            if (!sgd) ll_stf(a.xc.lg + ((size_t)c.par() * NL + l) * NEXP + b, v, c.tag(k, PH_ROUTER));
+            else if (shg) ll_stf(a.xc.sg + (size_t)c.par() * NL + l, sigmoid_c(v), c.tag(k, PH_ROUTER));
         }
     }
     tr_mark(c, 132);
@@ -909,48 +924,41 @@ FZ_PHASE bool phase_router(const RunCtl *ctl, const FusedArgs *ap, int il) {
         wdot<E, 2, NL>(ws, 8, &s.xq[0][0], E, &s.xd[0][0], E / 32, s.g);
         if (t < NL * 4) {
             const int l = t / 4, i = t % 4;
-            if (l < c.nl) cst(a.b.hsh + l * FFSH + tile * 8 + hf * 4 + i, v_silu(s.g.out[l][i]) * s.g.out[l][4 + i]);
+            if (l < c.nl)
+                ll_stf(a.xc.hsh + ((size_t)c.par() * NL + l) * FFSH + tile * 8 + hf * 4 + i,
+                       v_silu(s.g.out[l][i]) * s.g.out[l][4 + i], c.tag(k, PH_ROUTER));
         }
     }
     tr_end(c, TP_ROUTER);
-    arrive(c.bar);
     return true;
 }
 
 // routing of every lane (each workgroup, from the published logits), then the routed experts'
 // gate/up (group b = (union slot u = b / 16, 64-row group b % 16): 4 tiles = 32 h values per lane,
-// one Q8_0 block), then the down projection + combine of rows [8 b, 8 b + 8)
+// one Q8_0 block), then the down projection + combine of rows [8 b, 8 b + 8), written to x of the
+// next run layer
 template <int NL>
-FZ_PHASE bool phase_moe(const RunCtl *ctl, const FusedArgs *ap, int il) {
-    Ctx<NL> c = make_ctx<NL>(ctl, ap);
+FZ_PHASE bool phase_moe(const RunCtl *ctl, const FusedArgs *ap, int il, int k) {
+    Ctx<NL> c = make_ctx<NL>(ctl, ap, k);
     tr_start(c);
     const FZ_CAS FusedArgs &a = *c.a;
     const FZ_CAS LayerDev &L = layer_of(c, il);
     auto &se = c.sm->exp;
     auto &ps = *c.ps;
     const int t = threadIdx.x, b = c.b, nl = c.nl;
-    if (!wait(c.bar, &ps.ok)) return false;
-    tr_pass(c);
-    // the post-norm quantised lanes (published by the router phase) first: their latency overlaps
-    // the routing
-    {
-        const int l = t >> 8, tt = t & 255;
-        if (l < NL) {
-            const unsigned long long v = l < nl ? cld64(a.b.xq + (int64_t)l * 2 * E + 8 * tt) : 0ull;
-            *(uint2 *)&se.xq[l][8 * tt] = make_uint2((uint32_t)v, (uint32_t)(v >> 32));
-        }
-        if (t < NL * (E / 32)) {
-            const int ll = t / (E / 32), bb = t % (E / 32);
-            se.xd[ll][bb] = ll < nl ? cld16(a.b.xd + (int64_t)ll * (2 * E / 32) + bb) : (uint16_t)0;
-        }
-    }
-    // 1. routing (engine.rs:3414-3475)
+    const uint32_t trt = c.tag(k, PH_ROUTER), tet = c.tag(k, PH_EXP);
+    // 1. routing (engine.rs:3414-3475) of the published logits; the post-norm quantised lanes are
+    // this workgroup's own (router phase, persistent LDS)
+    bool ok = true;
     if (t < NL * NEXP) {
         const int l = t / NEXP, i = t % NEXP;
-        se.lg[l][i] = l < nl ? cld(a.b.router_lg + l * NEXP + i) : 0.0f;
+        float v = 0.0f;
+        if (l < nl) ok = ll_ldf<1>(a.xc.lg + ((size_t)c.par() * NL + l) * NEXP + i, trt, &v, c.err);
+        se.lg[l][i] = v;
     }
     if (t == 0) ps.ro.tie = 0;
-    __syncthreads();
+    if (!all_ok(ok, &ps.fail)) return false;
+    tr_pass(c);
     tr_mark(c, 105);
     if ((t >> 6) < nl) route_wave(se.lg[t >> 6], t >> 6, ps.ro);
     __syncthreads();
@@ -993,7 +1001,7 @@ FZ_PHASE bool phase_moe(const RunCtl *ctl, const FusedArgs *ap, int il) {
     // 3. gate/up + swiglu + Q8_0 of the group's 32 h values per lane
     if (gw) {
         tr_mark(c, 103);
-        wdot<E, 16, NL>(ew, 64, &se.xq[0][0], E, &se.xd[0][0], E / 32, se.g);
+        wdot<E, 16, NL>(ew, 64, &ps.xq[0][0], E, &ps.xd[0][0], E / 32, se.g);
         tr_mark(c, 104);
         if (t < 64) {
             // swiglu of the group's 32 h values of lane l = t / 32 (half wave), then Q8_0
@@ -1002,19 +1010,19 @@ FZ_PHASE bool phase_moe(const RunCtl *ctl, const FusedArgs *ap, int il) {
             const float hv = l < NL ? v_silu(se.g.out[l < NL ? l : 0][tl * 16 + r]) * se.g.out[l < NL ? l : 0][tl * 16 + 8 + r] : 0.0f;
             float dd;
             const uint32_t word = quant32_lanes(hv, &dd);
-            if (l < nl && (i & 3) == 0) cst32(a.hq + ((int64_t)l * OXE_MAX_UNION + u_g) * FF + gq * 32 + i, word);
-            if (l < nl && i == 0) cst16(a.hd + ((int64_t)l * OXE_MAX_UNION + u_g) * (FF / 32) + gq, f2h(dd));
+            const size_t hi = ((size_t)c.par() * NL + (l < NL ? l : 0)) * OXE_MAX_UNION + u_g;
+            if (l < nl && (i & 3) == 0) ll_st(a.xc.hq + hi * (FF / 4) + (gq * 32 + i) / 4, word, tet);
+            if (l < nl && i == 0) ll_st(a.xc.hd + hi * (FF / 32) + gq, f2h(dd), tet);
         }
     }
     tr_end(c, TP_EXPERTS);
     tr_start(c);
-    arrive(c.bar);
+    __syncthreads();   // the down phase's LDS aliases the experts'
     // the down rows of every union expert and the shared expert: the first DW_PRE units per
-    // thread in flight across the barrier, the rest issued behind the phase's inputs (a barrier
-    // poll waits behind every load the workgroup has outstanding). Every load of this phase is
-    // unconditional (a load skipped on some path makes the compiler's wait for an earlier one
-    // conservative, i.e. a wait for all): units past the union re-read the shared expert's rows
-    // (cached), absent lanes and union slots read stale buffer contents, and nothing reads those.
+    // thread issued before the phase's inputs are polled, the rest behind them (a poll waits behind
+    // every load the thread has outstanding). The weight loads are unconditional (a load skipped on
+    // some path makes the compiler's wait for an earlier one conservative, i.e. a wait for all):
+    // units past the union re-read the shared expert's rows (cached).
     const int r0 = 8 * b;
     const int uh = t >> 8, rr = (t >> 5) & 7, ck = t & 31;
     auto unit_q = [&](int u) -> const int8_t * {
@@ -1023,12 +1031,12 @@ FZ_PHASE bool phase_moe(const RunCtl *ctl, const FusedArgs *ap, int il) {
         return u < nu && u < OXE_MAX_UNION ? L.exp_down.q + (int64_t)e * E * FF : L.shexp_down.q;
     };
     uint4 dw[9];
-    auto dload = [&](int k) {
-        dw[k] = gld((const uint4 *)(unit_q(2 * k + uh) + (int64_t)(r0 + rr) * FF + 16 * ck));
+    auto dload = [&](int q) {
+        dw[q] = gld((const uint4 *)(unit_q(2 * q + uh) + (int64_t)(r0 + rr) * FF + 16 * ck));
     };
     constexpr int DW_PRE = 5;
 #pragma unroll
-    for (int k = 0; k < DW_PRE; k++) dload(k);
+    for (int q = 0; q < DW_PRE; q++) dload(q);
     const int su = t / 16 < DW_UNITS ? t / 16 : OXE_MAX_UNION, srr = (t % 16) / 2, shf = t % 2;
     uint4 dsc;
     {
@@ -1037,57 +1045,74 @@ FZ_PHASE bool phase_moe(const RunCtl *ctl, const FusedArgs *ap, int il) {
         const uint16_t *base = su < nu && su < OXE_MAX_UNION ? L.exp_down.d + (int64_t)e * E * (FF / 32) : L.shexp_down.d;
         dsc = gld((const uint4 *)(base + (int64_t)(r0 + srr) * (FF / 32) + shf * 8));
     }
-    if (!wait(c.bar, &ps.ok)) return false;
-    tr_pass(c);
-    // 4. down + combine (engine.rs:3542-3624). Loads in the order they are needed: the shared
-    // expert's h (quantised here), then the routed experts' quantised h, then the residual inputs.
+    // 4. down + combine (engine.rs:3542-3624). Inputs in the order they are published: the shared
+    // expert's h (quantised here), the residual rows and the shared gate (router / out phases), then
+    // the routed experts' quantised h of the union's live slots.
     auto &sd = c.sm->down;
-    float hsv[NL * FFSH / FT];
+    const size_t pl = (size_t)c.par() * NL;
+    float hsv[NL];
 #pragma unroll
-    for (int k = 0; k < NL * FFSH / FT; k++) hsv[k] = cld(a.b.hsh + t + FT * k);
-    uint4 hqv[NL * OXE_MAX_UNION * (FF / 16) / FT];
-#pragma unroll
-    for (int k = 0; k < NL * OXE_MAX_UNION * (FF / 16) / FT; k++) hqv[k] = cld128(a.hq + 16 * (t + FT * k));
-    constexpr int NHD = NL * OXE_MAX_UNION * (FF / 32);
-    const uint16_t hdv = cld16(a.hd + (t < NHD ? t : NHD - 1));
+    for (int l = 0; l < NL; l++) {
+        hsv[l] = 0.0f;
+        if (l < nl) ok = ll_ldf<1>(a.xc.hsh + (pl + l) * FFSH + t, trt, &hsv[l], c.err) && ok;
+    }
     const int tx = t < NL * 8 ? t : NL * 8 - 1;
-    const float x1v = cld(a.b.x1 + (int64_t)(tx / 8) * E + r0 + tx % 8);
-    const float sgv = cld(a.b.sh_gate + tx / 8);
+    float x1v = 0.0f, sgv = 0.0f;
+    if (t < NL * 8 && tx / 8 < nl) {
+        ok = ll_ldf<1>(a.xc.x1 + (pl + tx / 8) * E + r0 + tx % 8, c.tag(k, PH_OUT), &x1v, c.err) && ok;
+        ok = ll_ldf<1>(a.xc.sg + pl + tx / 8, trt, &sgv, c.err) && ok;
+    }
+    constexpr int NHQ = NL * OXE_MAX_UNION * (FF / 16) / FT;   // 16-code items per thread
+    uint32_t hqv[NHQ][4];
 #pragma unroll
-    for (int k = DW_PRE; k < 9; k++) dload(k);
-    // Q8_0 of the shared expert's h: element t of lane k in thread t, a block per half wave
+    for (int q = 0; q < NHQ; q++) {
+        const int i = t + FT * q;
+        const int l = i / (OXE_MAX_UNION * (FF / 16)), u = (i / (FF / 16)) % OXE_MAX_UNION, kk = i % (FF / 16);
+        hqv[q][0] = hqv[q][1] = hqv[q][2] = hqv[q][3] = 0u;
+        if (l < nl && u < nu) ok = ll_ld<4>(a.xc.hq + ((pl + l) * OXE_MAX_UNION + u) * (FF / 4) + 4 * kk, tet, hqv[q], c.err) && ok;
+    }
+    static_assert(NL * OXE_MAX_UNION * (FF / 32) == FT, "one scale per thread");
+    uint32_t hdv = 0u;
+    {
+        const int l = t / (OXE_MAX_UNION * (FF / 32)), u = (t / (FF / 32)) % OXE_MAX_UNION;
+        if (l < nl && u < nu) ok = ll_ld<1>(a.xc.hd + (pl * OXE_MAX_UNION) * (FF / 32) + t, tet, &hdv, c.err) && ok;
+    }
+#pragma unroll
+    for (int q = DW_PRE; q < 9; q++) dload(q);
+    // Q8_0 of the shared expert's h: element t of lane l in thread t, a block per half wave
     static_assert(FFSH == FT, "one shared-expert element per thread and lane");
 #pragma unroll
-    for (int k = 0; k < NL; k++) {
+    for (int l = 0; l < NL; l++) {
         float dd;
-        const uint32_t word = quant32_lanes(hsv[k], &dd);
-        if ((t & 3) == 0) *(uint32_t *)&sd.hq[k][OXE_MAX_UNION][t] = word;
-        if ((t & 31) == 0) sd.hd[k][OXE_MAX_UNION][t / 32] = f2h(dd);
+        const uint32_t word = quant32_lanes(hsv[l], &dd);
+        if ((t & 3) == 0) *(uint32_t *)&sd.hq[l][OXE_MAX_UNION][t] = word;
+        if ((t & 31) == 0) sd.hd[l][OXE_MAX_UNION][t / 32] = f2h(dd);
     }
     if (t < DW_UNITS * 16) {
         uint32_t *d = &sd.wd[su][srr * (FF / 64 + 1) + shf * 4];
         d[0] = dsc.x; d[1] = dsc.y; d[2] = dsc.z; d[3] = dsc.w;
     }
 #pragma unroll
-    for (int k = 0; k < NL * OXE_MAX_UNION * (FF / 16) / FT; k++) {
-        const int i = t + FT * k;
+    for (int q = 0; q < NHQ; q++) {
+        const int i = t + FT * q;
         const int l = i / (OXE_MAX_UNION * (FF / 16)), u = (i / (FF / 16)) % OXE_MAX_UNION, kk = i % (FF / 16);
-        *(uint4 *)&sd.hq[l][u][16 * kk] = hqv[k];
+        *(uint4 *)&sd.hq[l][u][16 * kk] = make_uint4(hqv[q][0], hqv[q][1], hqv[q][2], hqv[q][3]);
     }
-    if (t < NL * OXE_MAX_UNION * (FF / 32)) {
-        const int l = t / (OXE_MAX_UNION * (FF / 32)), u = (t / (FF / 32)) % OXE_MAX_UNION, k = t % (FF / 32);
-        sd.hd[l][u][k] = hdv;
+    {
+        const int l = t / (OXE_MAX_UNION * (FF / 32)), u = (t / (FF / 32)) % OXE_MAX_UNION, kb = t % (FF / 32);
+        sd.hd[l][u][kb] = (uint16_t)hdv;
     }
-    __syncthreads();
+    if (!all_ok(ok, &ps.fail)) return false;
+    tr_pass(c);
     tr_mark(c, 161);
 #pragma unroll
-    for (int k = 0; k < 9; k++) {
-        const int u = 2 * k + uh;
+    for (int q = 0; q < 9; q++) {
+        const int u = 2 * q + uh;
         if (u < DW_UNITS && (u == OXE_MAX_UNION || u < nu)) {   // uniform within each wave
 #pragma unroll
             for (int l = 0; l < NL; l++) {
                 const uint4 xa = *(const uint4 *)&sd.hq[l][u][16 * ck];
-                int32_t v = dot16(dw[k], xa, 0);
+                int32_t v = dot16(dw[q], xa, 0);
                 v += dpp_i<DPP_XOR1>(v);
                 if ((ck & 1) == 0) sd.isum[u][l][rr][ck >> 1] = v;
             }
@@ -1118,12 +1143,10 @@ FZ_PHASE bool phase_moe(const RunCtl *ctl, const FusedArgs *ap, int il) {
             }
             const float sh = sd.dn[OXE_MAX_UNION][l][r] * sgv;
             const float f = m + sh;
-            const int64_t i = (int64_t)l * E + r0 + r;
-            cst(a.b.x2 + i, f + x1v);
+            ll_stf(a.xc.x + ((size_t)((k + 1) & 1) * NL + l) * E + r0 + r, f + x1v, c.tag(k, PH_DOWN));
         }
     }
     tr_end(c, TP_DOWN);
-    arrive(c.bar);
     return true;
 }
 
@@ -1151,8 +1174,8 @@ OXE_DEV float f16x8_reduce_q(h2t acc[4]) {
 
 
 template <int NL>
-FZ_PHASE bool phase_scores(const RunCtl *ctl, const FusedArgs *ap, int il, bool seed_only) {
-    Ctx<NL> c = make_ctx<NL>(ctl, ap);
+FZ_PHASE bool phase_scores(const RunCtl *ctl, const FusedArgs *ap, int il, int k, bool seed_only) {
+    Ctx<NL> c = make_ctx<NL>(ctl, ap, k);
     tr_start(c);
     const FZ_CAS FusedArgs &a = *c.a;
     const FZ_CAS LayerDev &L = layer_of(c, il);
@@ -1183,32 +1206,35 @@ FZ_PHASE bool phase_scores(const RunCtl *ctl, const FusedArgs *ap, int il, bool 
     float kcs[2] = {0.0f, 0.0f}, qcs[(NL * GQA + 7) / 8][2];
     if (kdo) { kcs[0] = a.m.rope[(int64_t)pk * NROT + 2 * rl]; kcs[1] = a.m.rope[(int64_t)pk * NROT + 2 * rl + 1]; }
 #pragma unroll
-    for (int k = 0; k < (NL * GQA + 7) / 8; k++) {
-        const int l = (w + 8 * k) / GQA;
-        const bool on = qdo && w + 8 * k < NL * GQA && l < nl;
-        qcs[k][0] = on ? a.m.rope[(int64_t)(pos0 + l) * NROT + 2 * rl] : 0.0f;
-        qcs[k][1] = on ? a.m.rope[(int64_t)(pos0 + l) * NROT + 2 * rl + 1] : 0.0f;
+    for (int q = 0; q < (NL * GQA + 7) / 8; q++) {
+        const int l = (w + 8 * q) / GQA;
+        const bool on = qdo && w + 8 * q < NL * GQA && l < nl;
+        qcs[q][0] = on ? a.m.rope[(int64_t)(pos0 + l) * NROT + 2 * rl] : 0.0f;
+        qcs[q][1] = on ? a.m.rope[(int64_t)(pos0 + l) * NROT + 2 * rl + 1] : 0.0f;
     }
-    if (!wait(c.bar, &c.ps->ok)) return false;
-    tr_pass(c);
     // each wave takes its vectors (the K row of lane w on waves w < NL in range; queries job
-    // w + 8 k = (lane job / 8, head job % 8)) through raw -> rms norm * weight -> RoPE -> f16 on
+    // w + 8 q = (lane job / 8, head job % 8)) through raw -> rms norm * weight -> RoPE -> f16 on
     // its own: lane c holds elements c + 64 i; RoPE pairs (c, c + 32) for c < 32 (slot 0)
+    const uint64_t *pin = a.xc.p + (size_t)c.par() * NL * DN_ROWS;
+    const uint32_t tp = c.tag(k, PH_PROJ);
+    bool ok = true;
     float kv4[4], qv4[(NL * GQA + 7) / 8][4];
     if (kdo) {
-        const float *kr = a.b.proj + (int64_t)kjob * DN_ROWS + AT_K + kvh * HD;
+        const uint64_t *kr = pin + (int64_t)kjob * DN_ROWS + AT_K + kvh * HD;
 #pragma unroll
-        for (int i = 0; i < 4; i++) kv4[i] = cld(kr + lane + 64 * i);
+        for (int i = 0; i < 4; i++) ok = ll_ldf<1>(kr + lane + 64 * i, tp, &kv4[i], c.err) && ok;
     }
 #pragma unroll
-    for (int k = 0; k < (NL * GQA + 7) / 8; k++) {
-        const int job = w + 8 * k, l = job / GQA, h = kvh * GQA + job % GQA;
+    for (int q = 0; q < (NL * GQA + 7) / 8; q++) {
+        const int job = w + 8 * q, l = job / GQA, h = kvh * GQA + job % GQA;
         if (qdo && job < NL * GQA && l < nl) {
-            const float *q = a.b.proj + (int64_t)l * DN_ROWS + h * 2 * HD;
+            const uint64_t *qr = pin + (int64_t)l * DN_ROWS + h * 2 * HD;
 #pragma unroll
-            for (int i = 0; i < 4; i++) qv4[k][i] = cld(q + lane + 64 * i);
+            for (int i = 0; i < 4; i++) ok = ll_ldf<1>(qr + lane + 64 * i, tp, &qv4[q][i], c.err) && ok;
         }
     }
+    if (!all_ok(ok, &c.ps->fail)) return false;
+    tr_pass(c);
     auto finish = [&](float v[4], const float wt[4], const float cs[2], float *replay, uint16_t *dst) {
 #pragma unroll
         for (int i = 0; i < 4; i++) replay[lane + 64 * i] = v[i];
@@ -1229,10 +1255,10 @@ FZ_PHASE bool phase_scores(const RunCtl *ctl, const FusedArgs *ap, int il, bool 
         for (int i = 0; i < 4; i++) kc[((int64_t)kvh * a.m.n_ctx + pk) * HD + lane + 64 * i] = s.knew[kjob][lane + 64 * i];
     }
 #pragma unroll
-    for (int k = 0; k < (NL * GQA + 7) / 8; k++) {
-        const int job = w + 8 * k, l = job / GQA;
+    for (int q = 0; q < (NL * GQA + 7) / 8; q++) {
+        const int job = w + 8 * q, l = job / GQA;
         if (qdo && job < NL * GQA) {
-            if (l < nl) finish(qv4[k], qw, qcs[k], s.tmp[job], s.q[job]);
+            if (l < nl) finish(qv4[q], qw, qcs[q], s.tmp[job], s.q[job]);
             else
 #pragma unroll
                 for (int i = 0; i < 4; i++) s.q[job][lane + 64 * i] = 0;
@@ -1241,8 +1267,12 @@ FZ_PHASE bool phase_scores(const RunCtl *ctl, const FusedArgs *ap, int il, bool 
     __syncthreads();
     tr_mark(c, 151);
     if (act && !seed_only) {
-        // thread = (lane l, head pair hq, position pp of the chunk, chain quad j)
+        // thread = (lane l, head pair hq, position pp of the chunk, chain quad j). Positions of a
+        // chunk past the lane's own (masked in the softmax) get the tag with value 0, so the
+        // softmax polls whole groups of 4.
         const int l = t >> 8, hq = (t >> 6) & 3, pp = (t >> 2) & (SC_P - 1), j = t & 3;
+        uint64_t *scx = a.xc.sc + ((size_t)c.par() * NL + (l < NL ? l : 0)) * NH * a.m.n_ctx;
+        const uint32_t ts = c.tag(k, PH_MIX);
         for (int chunk = chunk0; chunk * SC_P <= pmax; chunk += cstride) {
             const int cb = chunk * SC_P;
             if (chunk == chunk0) {
@@ -1275,14 +1305,16 @@ FZ_PHASE bool phase_scores(const RunCtl *ctl, const FusedArgs *ap, int il, bool 
 #pragma unroll
                 for (int q = 0; q < 2; q++) {
                     const float sc = f16x8_reduce_q(acc[q]);
-                    if (j == 0) cst(a.b.scores + ((int64_t)l * NH + kvh * GQA + 2 * hq + q) * a.m.n_ctx + p, sc);
+                    if (j == 0) ll_stf(scx + (int64_t)(kvh * GQA + 2 * hq + q) * a.m.n_ctx + p, sc, ts);
                 }
+            } else if (l < nl && j == 0 && p < a.m.n_ctx) {
+#pragma unroll
+                for (int q = 0; q < 2; q++) ll_stf(scx + (int64_t)(kvh * GQA + 2 * hq + q) * a.m.n_ctx + p, 0.0f, ts);
             }
             __syncthreads();
         }
     }
     tr_end(c, TP_SCORES);
-    arrive(c.bar);
     return true;
 }
 
@@ -1295,8 +1327,10 @@ FZ_PHASE bool phase_scores(const RunCtl *ctl, const FusedArgs *ap, int il, bool 
 // earlier launches are loaded before the barrier, the rest after it, device-coherently. Thread
 // (q = t / 256, dim d = (t / 16) % 16, cp = t % 16) runs chain pair cp of ggml_vec_dot_f16
 // (positions 32 s + 2 cp and +1: accumulator cp / 4, halves 2 (cp % 4) and +1) for dim d and head
-// q; the F16x8 reduce is done by lane moves inside the 16-lane row. The gated outputs (f32) go to
-// the mixer-output buffer; the output projection quantizes them.
+// q; the F16x8 reduce is done by lane moves inside the 16-lane row. The V^T entries of this run's
+// own positions are taken from the projection outputs (f16 of the f32 V rows, the value the
+// projection phase writes to V^T for later runs); every other entry is the cache's. The gated
+// outputs (f32) go to the mixer-output buffer; the output projection quantizes them.
 constexpr int PV_SMK = 2;    // softmax groups per thread in registers (n_kv <= 2048)
 constexpr int PVD = 16;      // dims per workgroup
 constexpr int PV_HP = GQA / 2;  // head pairs per kv head
@@ -1304,8 +1338,8 @@ constexpr int PV_VK = 4;     // V^T 16-byte chunks per thread staged from regist
 constexpr int PV_VMAX = 2048;   // positions of the V^T tile held in LDS (longer rows: the rest from memory)
 
 template <int NL>
-FZ_PHASE bool phase_pv(const RunCtl *ctl, const FusedArgs *ap, int il) {
-    Ctx<NL> c = make_ctx<NL>(ctl, ap);
+FZ_PHASE bool phase_pv(const RunCtl *ctl, const FusedArgs *ap, int il, int k) {
+    Ctx<NL> c = make_ctx<NL>(ctl, ap, k);
     tr_start(c);
     const FZ_CAS FusedArgs &a = *c.a;
     const FZ_CAS LayerDev &L = layer_of(c, il);
@@ -1326,42 +1360,56 @@ FZ_PHASE bool phase_pv(const RunCtl *ctl, const FusedArgs *ap, int il) {
     const int nvc = nst / 8;                            // staged 16-byte chunks per V^T row
     const int vs = nst + 32;                            // LDS row stride in halves
     const uint16_t *vt = a.m.vcache + (int64_t)L.index * NKV * HD * n_ctx + (int64_t)(kvh * HD + dchunk * PVD) * n_ctx;
-    // staged chunk i = t + FT k: row i / nvc, chunk i % nvc; those of earlier launches only, now
+    // staged chunk i = t + FT q: row i / nvc, chunk i % nvc (this run's positions are patched in
+    // LDS afterwards)
     uint4 vpre[PV_VK];
 #pragma unroll
-    for (int k = 0; k < PV_VK; k++) {
-        const int i = t + FT * k, r = i / nvc, ch = i % nvc;
-        vpre[k] = (act && i < PVD * nvc && 8 * ch + 7 < pos0) ? gld((const uint4 *)(vt + (int64_t)r * n_ctx + 8 * ch))
-                                                              : make_uint4(0, 0, 0, 0);
+    for (int q = 0; q < PV_VK; q++) {
+        const int i = t + FT * q, r = i / nvc, ch = i % nvc;
+        vpre[q] = (act && i < PVD * nvc) ? gld((const uint4 *)(vt + (int64_t)r * n_ctx + 8 * ch)) : make_uint4(0, 0, 0, 0);
     }
-    if (!wait(c.bar, &c.ps->ok)) return false;
-    tr_pass(c);
+    const uint64_t *pin = a.xc.p + (size_t)c.par() * NL * DN_ROWS;
+    const uint32_t tp = c.tag(k, PH_PROJ), ts = c.tag(k, PH_MIX);
     if (act) {
         uint32_t *s_pp = (uint32_t *)c.dyn;                                  // [n_kv / 2][2] f16 pairs
         uint16_t *s_v = (uint16_t *)(c.dyn + (size_t)n_ctx * 4);            // [PVD][vs] V^T rows
         float *s_mx = (float *)(s_v + (size_t)PVD * vs);                    // [2][4] wave maxima
         double *s_ps = (double *)(((uintptr_t)(s_mx + 8) + 7) & ~(uintptr_t)7);   // [2][4] wave sums
         float *s_f = (float *)(s_ps + 8);                                   // [2] 1 / sum
+        uint16_t *s_vn = (uint16_t *)(s_f + 2);                             // [NL][PVD] this run's V
         const int q = t >> 8, tq = t & 255, wq = (t >> 6) & 3;
         const int cp = t & 15, d = (t >> 4) & (PVD - 1);
         const int h = kvh * GQA + 2 * hp + q;
-        // the chunks with positions of this launch (or later), device-coherently; this thread's gate
-#pragma unroll
-        for (int k = 0; k < PV_VK; k++) {
-            const int i = t + FT * k, r = i / nvc, ch = i % nvc;
-            if (i < PVD * nvc && 8 * ch + 7 >= pos0) vpre[k] = cld128(vt + (int64_t)r * n_ctx + 8 * ch);
+        bool ok = true;
+        // this run's V entries of the chunk's 16 dims, and this thread's gate
+        if (t < NL * PVD) {
+            const int vl = t / PVD, vd = t % PVD;
+            float v = 0.0f;
+            if (vl < nl) ok = ll_ldf<1>(pin + (int64_t)vl * DN_ROWS + AT_V + kvh * HD + dchunk * PVD + vd, tp, &v, c.err);
+            s_vn[vl * PVD + vd] = f2h(v);
         }
         float sg = 0.0f;
-        if (cp == 0) sg = cld(a.b.proj + (int64_t)l * DN_ROWS + h * 2 * HD + HD + dchunk * PVD + d);
+        if (cp == 0) ok = ll_ldf<1>(pin + (int64_t)l * DN_ROWS + h * 2 * HD + HD + dchunk * PVD + d, tp, &sg, c.err) && ok;
         const float scale = 1.0f / sqrtf((float)HD);
+        // the scores of head q: groups of 4 positions up to the one holding pos (the scores phase
+        // tags every position of its chunks); later groups are masked and not read
+        const uint64_t *sc = a.xc.sc + ((size_t)c.par() * NL + l) * NH * n_ctx + (int64_t)h * n_ctx;
+        auto sget = [&](int g, uint32_t u[4]) -> bool {
+            if (4 * g > pos) {
+                u[0] = u[1] = u[2] = u[3] = 0u;
+                return true;
+            }
+            return ll_ld<4>(sc + 4 * g, ts, u, c.err);
+        };
         {
             // softmax of head q: wp = s * scale (masked: -inf), max, e = v_expf(wp - max) with group
             // sums (e0 + e1) + (e2 + e3) added in double, p = f16(e * f32(1 / sum))
-            const float *sc = a.b.scores + ((int64_t)l * NH + h) * n_ctx;
             const int ng = n_kv / 4;
             auto wval = [&](uint32_t u, int p) { return p <= pos ? __builtin_bit_cast(float, u) * scale : -__builtin_inff(); };
             auto group = [&](int g, float mx) {
-                const uint4 v = cld128(sc + 4 * g);
+                uint32_t u[4];
+                (void)sget(g, u);   // polled before (the same groups, first pass)
+                const uint4 v = make_uint4(u[0], u[1], u[2], u[3]);
                 const float e0 = v_expf(wval(v.x, 4 * g) - mx), e1 = v_expf(wval(v.y, 4 * g + 1) - mx);
                 const float e2 = v_expf(wval(v.z, 4 * g + 2) - mx), e3 = v_expf(wval(v.w, 4 * g + 3) - mx);
                 return (e0 + e1) + (e2 + e3);
@@ -1398,53 +1446,57 @@ FZ_PHASE bool phase_pv(const RunCtl *ctl, const FusedArgs *ap, int il) {
             if (ng <= 256 * PV_SMK) {
                 float e[PV_SMK][4];
 #pragma unroll
-                for (int k = 0; k < PV_SMK; k++) {
-                    const int g = tq + 256 * k;
-                    const uint4 v = g < ng ? cld128(sc + 4 * g) : make_uint4(0, 0, 0, 0);
-                    const uint32_t u[4] = {v.x, v.y, v.z, v.w};
+                for (int k2 = 0; k2 < PV_SMK; k2++) {
+                    const int g = tq + 256 * k2;
+                    uint32_t u[4] = {0u, 0u, 0u, 0u};
+                    if (g < ng) ok = sget(g, u) && ok;
 #pragma unroll
                     for (int i = 0; i < 4; i++) {
-                        e[k][i] = g < ng ? wval(u[i], 4 * g + i) : -__builtin_inff();
-                        mx = (mx > e[k][i]) ? mx : e[k][i];
+                        e[k2][i] = g < ng ? wval(u[i], 4 * g + i) : -__builtin_inff();
+                        mx = (mx > e[k2][i]) ? mx : e[k2][i];
                     }
                 }
+                if (!all_ok(ok, &c.ps->fail)) return false;
+                tr_pass(c);
                 mx = head_max(mx);
                 tr_mark(c, 143);
 #pragma unroll
-                for (int k = 0; k < PV_SMK; k++) {
-                    const int g = tq + 256 * k;
+                for (int k2 = 0; k2 < PV_SMK; k2++) {
+                    const int g = tq + 256 * k2;
                     if (g < ng) {
 #pragma unroll
-                        for (int i = 0; i < 4; i++) e[k][i] = v_expf(e[k][i] - mx);
-                        part += (double)((e[k][0] + e[k][1]) + (e[k][2] + e[k][3]));
+                        for (int i = 0; i < 4; i++) e[k2][i] = v_expf(e[k2][i] - mx);
+                        part += (double)((e[k2][0] + e[k2][1]) + (e[k2][2] + e[k2][3]));
                     }
                 }
                 const float f = head_recip(part, mx);
 #pragma unroll
-                for (int k = 0; k < PV_SMK; k++) {
-                    const int g = tq + 256 * k;
+                for (int k2 = 0; k2 < PV_SMK; k2++) {
+                    const int g = tq + 256 * k2;
                     if (g < ng) {
-                        s_pp[(2 * g) * 2 + q] = (uint32_t)f2h(e[k][0] * f) | ((uint32_t)f2h(e[k][1] * f) << 16);
-                        s_pp[(2 * g + 1) * 2 + q] = (uint32_t)f2h(e[k][2] * f) | ((uint32_t)f2h(e[k][3] * f) << 16);
+                        s_pp[(2 * g) * 2 + q] = (uint32_t)f2h(e[k2][0] * f) | ((uint32_t)f2h(e[k2][1] * f) << 16);
+                        s_pp[(2 * g + 1) * 2 + q] = (uint32_t)f2h(e[k2][2] * f) | ((uint32_t)f2h(e[k2][3] * f) << 16);
                     }
                 }
             } else {
                 // long rows: max, sums and probabilities in three passes over the scores
                 for (int g = tq; g < ng; g += 256) {
-                    const uint4 v = cld128(sc + 4 * g);
-                    const uint32_t u[4] = {v.x, v.y, v.z, v.w};
+                    uint32_t u[4];
+                    ok = sget(g, u) && ok;
 #pragma unroll
                     for (int i = 0; i < 4; i++) {
                         const float wv = wval(u[i], 4 * g + i);
                         mx = (mx > wv) ? mx : wv;
                     }
                 }
+                if (!all_ok(ok, &c.ps->fail)) return false;
+                tr_pass(c);
                 mx = head_max(mx);
                 for (int g = tq; g < ng; g += 256) part += (double)group(g, mx);
                 const float f = head_recip(part, mx);
                 for (int g = tq; g < ng; g += 256) {
-                    const uint4 v = cld128(sc + 4 * g);
-                    const uint32_t u[4] = {v.x, v.y, v.z, v.w};
+                    uint32_t u[4];
+                    (void)sget(g, u);
                     uint16_t pq[4];
 #pragma unroll
                     for (int i = 0; i < 4; i++) pq[i] = f2h(v_expf(wval(u[i], 4 * g + i) - mx) * f);
@@ -1454,18 +1506,22 @@ FZ_PHASE bool phase_pv(const RunCtl *ctl, const FusedArgs *ap, int il) {
             }
         }
         tr_mark(c, 144);
-        // the V^T tile into LDS
+        // the V^T tile into LDS, then this run's positions patched in
 #pragma unroll
-        for (int k = 0; k < PV_VK; k++) {
-            const int i = t + FT * k, r = i / nvc, ch = i % nvc;
-            if (i < PVD * nvc) *(uint4 *)(s_v + r * vs + 8 * ch) = vpre[k];
+        for (int q2 = 0; q2 < PV_VK; q2++) {
+            const int i = t + FT * q2, r = i / nvc, ch = i % nvc;
+            if (i < PVD * nvc) *(uint4 *)(s_v + r * vs + 8 * ch) = vpre[q2];
         }
         for (int i = t + FT * PV_VK; i < PVD * nvc; i += FT) {
             const int r = i / nvc, ch = i % nvc;
-            const uint16_t *src = vt + (int64_t)r * n_ctx + 8 * ch;
-            *(uint4 *)(s_v + r * vs + 8 * ch) = 8 * ch + 7 < pos0 ? gld((const uint4 *)src) : cld128(src);
+            *(uint4 *)(s_v + r * vs + 8 * ch) = gld((const uint4 *)(vt + (int64_t)r * n_ctx + 8 * ch));
         }
         if (cp == 0) sg = sigmoid_c(sg);
+        __syncthreads();
+        if (t < NL * PVD) {
+            const int vl = t / PVD, vd = t % PVD;
+            if (vl < nl && pos0 + vl < nst) s_v[vd * vs + pos0 + vl] = s_vn[vl * PVD + vd];
+        }
         __syncthreads();
         tr_mark(c, 141);
         // V^T . p for dim d, chain pair cp, head q
@@ -1477,8 +1533,11 @@ FZ_PHASE bool phase_pv(const RunCtl *ctl, const FusedArgs *ap, int il) {
         for (int s = 0; s < nss; s++)
             acc = __builtin_elementwise_fma(u2h2f(*(const uint32_t *)(vrow + 32 * s)), u2h2f(prow[32 * s]), acc);
         for (int s = nss; s < ns; s++) {
-            const uint16_t *src = vt + (int64_t)d * n_ctx + 32 * s + 2 * cp;
-            const uint32_t vw = 32 * s + 2 * cp + 1 >= pos0 ? cld32(src) : gld((const uint32_t *)src);
+            const int p0 = 32 * s + 2 * cp;
+            uint32_t vw = gld((const uint32_t *)(vt + (int64_t)d * n_ctx + p0));
+            // this run's positions from the projection outputs
+            if (p0 >= pos0 && p0 < pos0 + nl) vw = (vw & 0xffff0000u) | s_vn[(p0 - pos0) * PVD + d];
+            if (p0 + 1 >= pos0 && p0 + 1 < pos0 + nl) vw = (vw & 0xffffu) | ((uint32_t)s_vn[(p0 + 1 - pos0) * PVD + d] << 16);
             acc = __builtin_elementwise_fma(u2h2f(vw), u2h2f(prow[32 * s]), acc);
         }
         // GGML_F16x8_REDUCE: accumulator j += j ^ 2 (cp ^ 8), j += j ^ 1 (cp ^ 4); widen halves
@@ -1491,17 +1550,17 @@ FZ_PHASE bool phase_pv(const RunCtl *ctl, const FusedArgs *ap, int il) {
         const float s2 = tlo + thi;
         const float out = s2 + dpp_f<DPP_XOR1>(s2);
         tr_mark(c, 142);
-        if (cp == 0) cst(a.b.gdn + (int64_t)l * MIX_W + h * HD + dchunk * PVD + d, out * sg);
+        if (cp == 0) ll_stf(a.xc.g + ((size_t)c.par() * NL + l) * MIX_W + h * HD + dchunk * PVD + d, out * sg, c.tag(k, PH_PV));
     }
     tr_end(c, TP_PV);
-    arrive(c.bar);
     return true;
 }
 
-// MTP entry: x2 = eh_proj . [enorm(embd(tok)); hnorm(h)], rows [8 b, 8 b + 8)
+// MTP entry: eh_proj . [enorm(embd(tok)); hnorm(h)], rows [8 b, 8 b + 8), written as the "down"
+// output of run layer 0 (the input x of the MTP layer, run layer 1)
 template <int NL>
 FZ_PHASE bool phase_entry(const RunCtl *ctl, const FusedArgs *ap, int il) {
-    Ctx<NL> c = make_ctx<NL>(ctl, ap);
+    Ctx<NL> c = make_ctx<NL>(ctl, ap, 0);
     tr_start(c);
     const FZ_CAS FusedArgs &a = *c.a;
     const FZ_CAS LayerDev &L = layer_of(c, il);
@@ -1510,9 +1569,9 @@ FZ_PHASE bool phase_entry(const RunCtl *ctl, const FusedArgs *ap, int il) {
     WSlice<2 * E, 4> ws;
     wload<2 * E, 4>(ws, L.eh_proj.q, L.eh_proj.d, 8, [&](int rl) { return (int64_t)(r0 + rl); });
     const W8 nwe = wload8(L.enorm), nwh = wload8(L.hnorm);
-    // no barrier precedes the entry (its inputs come from earlier launches)
-    prologue<NL>(c.nl, c.ctl, a.m.tok_embd.q, a.m.tok_embd.d, nullptr, 0, false, nwe, a.m.eps, s.xf, &s.xq[0][0], 2 * E, &s.xd[0][0],
-                 2 * E / 32, s.ns, nullptr);
+    // the entry's inputs come from earlier launches (nothing to poll)
+    (void)prologue<NL>(c.nl, c.ctl, a.m.tok_embd.q, a.m.tok_embd.d, nullptr, 0u, c.err, nwe, a.m.eps, s.xf, &s.xq[0][0], 2 * E,
+                       &s.xd[0][0], 2 * E / 32, s.ns, nullptr, &c.ps->fail);
     {
         // h of each lane: hid[hin_sel[l]]
         const int l = t >> 8, tt = t & 255;
@@ -1535,10 +1594,9 @@ FZ_PHASE bool phase_entry(const RunCtl *ctl, const FusedArgs *ap, int il) {
     wdot<2 * E, 4, NL>(ws, 8, &s.xq[0][0], 2 * E, &s.xd[0][0], 2 * E / 32, s.g);
     if (t < NL * 8) {
         const int l = t / 8, rl = t % 8;
-        if (l < c.nl) cst(a.b.x2 + (int64_t)l * E + r0 + rl, s.g.out[l][rl]);
+        if (l < c.nl) ll_stf(a.xc.x + ((size_t)1 * NL + l) * E + r0 + rl, s.g.out[l][rl], c.tag(0, PH_DOWN));
     }
     tr_end(c, TP_ENTRY);
-    arrive(c.bar);
     return true;
 }
 
@@ -1548,9 +1606,10 @@ OXE_DEV uint32_t ordered_bits_f(float f) {
     return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
+// k: the run layer after the last (its input x is the head's input)
 template <int NL>
-FZ_PHASE bool phase_head(const RunCtl *ctl, const FusedArgs *ap, const float *norm_w) {
-    Ctx<NL> c = make_ctx<NL>(ctl, ap);
+FZ_PHASE bool phase_head(const RunCtl *ctl, const FusedArgs *ap, const float *norm_w, int k) {
+    Ctx<NL> c = make_ctx<NL>(ctl, ap, k);
     tr_start(c);
     const FZ_CAS FusedArgs &a = *c.a;
     auto &s = c.sm->head;
@@ -1563,10 +1622,10 @@ FZ_PHASE bool phase_head(const RunCtl *ctl, const FusedArgs *ap, const float *no
     auto rows_of = [&](int64_t tile) { const int64_t r = V - tile * TR; return (int)(r < TR ? r : TR); };
     if (t0 < t1) wload<E, HEAD_P>(A, a.m.output.q, a.m.output.d, rows_of(t0), [&](int rl) { return t0 * TR + rl; });
     const W8 nw = wload8(norm_w);
-    if (!wait(c.bar, &c.ps->ok)) return false;
+    if (!prologue<NL>(nl, c.ctl, nullptr, nullptr, a.xc.x + (size_t)c.par() * NL * E, c.tag(k - 1, PH_DOWN), c.err, nw, a.m.eps,
+                      s.xf, &s.xq[0][0], E, &s.xd[0][0], E / 32, s.ns, s.xn, &c.ps->fail))
+        return false;
     tr_pass(c);
-    prologue<NL>(nl, c.ctl, nullptr, nullptr, a.b.x2, E, true, nw, a.m.eps, s.xf, &s.xq[0][0], E, &s.xd[0][0], E / 32, s.ns,
-                 s.xn);
     if (c.b == 0) {
         // h_nextn of each lane (Engine::hidden): the normalised x2
         const int l = t >> 8, tt = t & 255;
@@ -1610,22 +1669,45 @@ FZ_PHASE bool phase_head(const RunCtl *ctl, const FusedArgs *ap, const float *no
     return true;
 }
 
+// layer il as run layer k (embed: its input is the token embedding)
 template <int NL>
-OXE_DEV bool run_layer(const RunCtl *ctl, const FusedArgs *ap, int il, bool first) {
+OXE_DEV bool run_layer(const RunCtl *ctl, const FusedArgs *ap, int il, int k, bool embed, uint32_t base) {
     const LayerDev &L = ap->layers[il];
-    const float *x = first ? ap->b.x : ap->b.x2;
     const int att = L.att;
-    if (!phase_proj<NL>(ctl, ap, il, first && ap->mode == FM_VERIFY, x, 0, att ? AT_ROWS : DN_ROWS)) return false;
+    // the residual: the embedding (written by the projection phase) or the previous layer's output
+    const uint32_t xtag = base + 1u + (embed ? 8u * (uint32_t)k + PH_PROJ : 8u * (uint32_t)(k - 1) + PH_DOWN);
+    if (!phase_proj<NL>(ctl, ap, il, k, embed, 0, att ? AT_ROWS : DN_ROWS)) return false;
     if (!att) {
-        if (!phase_dn<NL>(ctl, ap, il)) return false;
+        if (!phase_dn<NL>(ctl, ap, il, k)) return false;
     } else {
-        if (!phase_scores<NL>(ctl, ap, il, false)) return false;
-        if (!phase_pv<NL>(ctl, ap, il)) return false;
+        if (!phase_scores<NL>(ctl, ap, il, k, false)) return false;
+        if (!phase_pv<NL>(ctl, ap, il, k)) return false;
     }
-    if (!phase_out<NL>(ctl, ap, il, x)) return false;
-    if (!phase_router<NL>(ctl, ap, il)) return false;
-    if (!phase_moe<NL>(ctl, ap, il)) return false;
+    if (!phase_out<NL>(ctl, ap, il, k, xtag)) return false;
+    if (!phase_router<NL>(ctl, ap, il, k)) return false;
+    if (!phase_moe<NL>(ctl, ap, il, k)) return false;
     return true;
+}
+
+template <int NL>
+OXE_DEV void run_all(const RunCtl *ctl, const FusedArgs *ap, uint32_t base) {
+    const int mode = ap->mode, nlay = ap->n_layer;
+    if (mode == FM_VERIFY) {
+        for (int il = 0; il < nlay; il++)
+            if (!run_layer<NL>(ctl, ap, il, il, il == 0, base)) return;
+        (void)phase_head<NL>(ctl, ap, ap->m.out_norm, nlay);
+    } else if (mode == FM_DRAFT) {
+        const int il = nlay;
+        if (!phase_entry<NL>(ctl, ap, il)) return;
+        // the MTP layer (attention) as run layer 1, its input the entry output
+        if (!run_layer<NL>(ctl, ap, il, 1, false, base)) return;
+        (void)phase_head<NL>(ctl, ap, ap->layers[il].head_norm, 2);
+    } else {
+        const int il = nlay;
+        if (!phase_entry<NL>(ctl, ap, il)) return;
+        if (!phase_proj<NL>(ctl, ap, il, 1, false, AT_K, AT_ROWS)) return;
+        (void)phase_scores<NL>(ctl, ap, il, 1, true);
+    }
 }
 
 }  // namespace fz
@@ -1635,33 +1717,24 @@ __global__ __launch_bounds__(fz::FT, 1) void fused_kernel(const RunCtl *__restri
     using namespace fz;
     if (!ctl->active) return;
     if (threadIdx.x == 0) {
-        fz_ps.round = cld32(&ap->sync[FZ_W_FLAG]);
+        fz_ps.base = cld32(&ap->sync[FZ_W_FLAG]);
+        fz_ps.fail = 0;
         fz_ps.tev = 0;
         fz_ps.dyn_off = (uint32_t)(uintptr_t)(FZ_LDS unsigned char *)fz_dyn;
     }
     __syncthreads();
-    // the first phase of a run has no producer in this launch: its wait (the current round) passes at once
-    const int mode = ap->mode, nlay = ap->n_layer;
-    if (mode == FM_VERIFY) {
-        for (int il = 0; il < nlay; il++)
-            if (!run_layer<NL>(ctl, ap, il, il == 0)) return;
-        (void)phase_head<NL>(ctl, ap, ap->m.out_norm);
-    } else if (mode == FM_DRAFT) {
-        const int il = nlay;
-        if (!phase_entry<NL>(ctl, ap, il)) return;
-        // the MTP layer (attention) with input x2 (the entry output)
-        if (!phase_proj<NL>(ctl, ap, il, false, ap->b.x2, 0, AT_ROWS)) return;
-        if (!phase_scores<NL>(ctl, ap, il, false)) return;
-        if (!phase_pv<NL>(ctl, ap, il)) return;
-        if (!phase_out<NL>(ctl, ap, il, ap->b.x2)) return;
-        if (!phase_router<NL>(ctl, ap, il)) return;
-        if (!phase_moe<NL>(ctl, ap, il)) return;
-        (void)phase_head<NL>(ctl, ap, ap->layers[il].head_norm);
-    } else {
-        const int il = nlay;
-        if (!phase_entry<NL>(ctl, ap, il)) return;
-        if (!phase_proj<NL>(ctl, ap, il, false, ap->b.x2, AT_K, AT_ROWS)) return;
-        (void)phase_scores<NL>(ctl, ap, il, true);
+    const uint32_t base = (uint32_t)__builtin_amdgcn_readfirstlane((int)fz_ps.base);
+    run_all<NL>(ctl, ap, base);
+    // every workgroup counts itself out, aborted or not; the last one moves the tag base past this
+    // launch's tags and re-arms the counter (the next launch on the stream starts after this one ends)
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint32_t *sync = ap->sync;
+        const uint32_t old = __hip_atomic_fetch_add(sync + FZ_W_DONE, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (old == gridDim.x - 1) {
+            cst32(sync + FZ_W_DONE, 0u);
+            cst32(sync + FZ_W_FLAG, base + FZ_TAG_STRIDE);
+        }
     }
 }
 
@@ -1691,11 +1764,25 @@ void launch_fused(const RunCtl *ctl, const FusedArgs *dev_args, int grid, size_t
     hipLaunchKernelGGL(fused_kernel<OXE_NL>, dim3((unsigned)grid), dim3(fz::FT), lds, st, ctl, dev_args);
 }
 
+// after an aborted run: the error word and the finished counter cleared, the tag base moved past
+// every tag the aborted launch may have written
 __global__ void fused_sync_reset_kernel(uint32_t *w) {
-    for (int i = threadIdx.x; i < FZ_SYNC_WORDS; i += blockDim.x) w[i] = 0u;
+    const uint32_t base = w[FZ_W_FLAG];
+    __syncthreads();
+    for (int i = threadIdx.x; i < FZ_SYNC_WORDS; i += blockDim.x) w[i] = i == FZ_W_FLAG ? base + FZ_TAG_STRIDE : 0u;
 }
 void launch_fused_sync_reset(uint32_t *sync, hipStream_t st) {
     hipLaunchKernelGGL(fused_sync_reset_kernel, dim3(1), dim3(256), 0, st, sync);
+}
+
+// every exchange word back to tag 0 (never a live tag) and the tag base to 0
+__global__ void fused_xch_clear_kernel(uint64_t *x, size_t n, uint32_t *sync) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) x[i] = 0ull;
+    if (blockIdx.x == 0)
+        for (int i = threadIdx.x; i < FZ_SYNC_WORDS; i += blockDim.x) sync[i] = 0u;
+}
+void launch_fused_xch_clear(uint64_t *xch, size_t words, uint32_t *sync, hipStream_t st) {
+    hipLaunchKernelGGL(fused_xch_clear_kernel, dim3(256), dim3(256), 0, st, xch, words, sync);
 }
 
 }  // namespace oxe

@@ -390,14 +390,18 @@ int Engine::mtp_steps_async(int k, bool use_graph) {
     }
     if (!graph_exec) {
         if (hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal) != hipSuccess) return -2;
+        fz_capturing = true;
         enqueue_mtp_device_step();
+        fz_capturing = false;
         hipGraph_t g;
         if (hipStreamEndCapture(st, &g) != hipSuccess) return -2;
         if (hipGraphInstantiate(&graph_exec, g, nullptr, nullptr, 0) != hipSuccess) return -2;
         (void)hipGraphDestroy(g);
     }
-    for (int i = 0; i < k; i++)
+    for (int i = 0; i < k; i++) {
+        if (fused) fz_account(3);   // seed, draft and verify launches of one step
         if (hipGraphLaunch(graph_exec, st) != hipSuccess) return -2;
+    }
     return 0;
 }
 

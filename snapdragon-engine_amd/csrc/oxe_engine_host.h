@@ -98,8 +98,10 @@ struct Engine {
     int fz_grid = 0;
     size_t fz_lds = 0;
     uint32_t *fz_sync = nullptr;
-    int8_t *fz_hq = nullptr;
-    uint16_t *fz_hd = nullptr;
+    uint64_t *fz_xch = nullptr;     // the tagged exchange buffers (FzXch), one allocation
+    size_t fz_xch_words = 0;
+    uint64_t fz_launches = 0;       // fused launches (an upper bound) since the tag base was last zeroed
+    bool fz_capturing = false;      // launches being captured into a graph are counted per replay
     unsigned long long *fz_keys = nullptr;
     LayerDev *fz_layers = nullptr;
     FusedArgs *fz_args = nullptr;   // [3]: verify, draft, seed
@@ -318,8 +320,23 @@ struct Engine {
         if (ncu != 256 || fused_blocks_per_cu(fz_lds) < 1) return;
         fz_grid = ncu;
         fz_sync = alloc<uint32_t>(FZ_SYNC_WORDS);
-        fz_hq = alloc<int8_t>((size_t)OXE_NL * OXE_MAX_UNION * FF);
-        fz_hd = alloc<uint16_t>((size_t)OXE_NL * OXE_MAX_UNION * (FF / 32));
+        // tags of a launch are base + 1 + 8 k + phase for run layers k <= n_layer
+        if (8 * (d.n_layer + 2) >= (int64_t)FZ_TAG_STRIDE) return;
+        const size_t NLs = OXE_NL;
+        const size_t xw[12] = {2 * NLs * E, 2 * NLs * E, 2 * NLs * DN_ROWS, 2 * NLs * MIX_W, 2 * NLs * (MIX_W / 4),
+                               2 * NLs * (MIX_W / 32), 2 * NLs * NEXP, 2 * NLs, 2 * NLs * FFSH,
+                               2 * NLs * OXE_MAX_UNION * (FF / 4), 2 * NLs * OXE_MAX_UNION * (FF / 32),
+                               2 * NLs * NH * (size_t)m.n_ctx};
+        size_t off[12], tot = 0;
+        for (int i = 0; i < 12; i++) {
+            off[i] = tot;
+            tot += (xw[i] + 31) / 32 * 32;   // 256-byte aligned parts
+        }
+        fz_xch = alloc<uint64_t>(tot);
+        fz_xch_words = tot;
+        FzXch xc;
+        uint64_t **parts[12] = {&xc.x, &xc.x1, &xc.p, &xc.g, &xc.o, &xc.od, &xc.lg, &xc.sg, &xc.hsh, &xc.hq, &xc.hd, &xc.sc};
+        for (int i = 0; i < 12; i++) *parts[i] = fz_xch + off[i];
         fz_keys = alloc<unsigned long long>((size_t)OXE_NL * fz_grid);
         const int nl_total = d.n_layer + 1;
         std::vector<LayerDev> ld(nl_total);
@@ -351,11 +368,11 @@ struct Engine {
             f.m = m;
             f.b = b;
             f.sync = fz_sync;
-            f.hq = fz_hq;
-            f.hd = fz_hd;
+            f.xc = xc;
             f.keys = fz_keys;
         }
         (void)hipMemsetAsync(fz_sync, 0, FZ_SYNC_WORDS * 4, st);
+        (void)hipMemsetAsync(fz_xch, 0, fz_xch_words * 8, st);
         (void)hipMemsetAsync(fz_keys, 0, (size_t)OXE_NL * fz_grid * 8, st);
         (void)hipMemcpyAsync(fz_layers, ld.data(), sizeof(LayerDev) * nl_total, hipMemcpyHostToDevice, st);
         for (int mode = 0; mode < 3; mode++) fz_host[mode] = fa[mode];
@@ -390,8 +407,19 @@ struct Engine {
         if (hipMemcpyAsync(fz_args, fz_host, sizeof(fz_host), hipMemcpyHostToDevice, st) != hipSuccess) return -2;
         return hipStreamSynchronize(st) == hipSuccess ? 0 : -2;
     }
-    // after a run of the fused kernel was aborted (a barrier that never completed): reset the
-    // barrier words and report
+    // n more fused launches about to be enqueued (outside graph capture). The tag base grows by
+    // FZ_TAG_STRIDE per launch; long before it wraps, every exchange word and the base go back to
+    // zero (a fill kernel on the engine stream, ordered before the launches).
+    static constexpr uint64_t FZ_CLEAR_EVERY = 1ull << 20;
+    void fz_account(int n) {
+        if (fz_launches + (uint64_t)n > FZ_CLEAR_EVERY) {
+            launch_fused_xch_clear(fz_xch, fz_xch_words, fz_sync, st);
+            fz_launches = 0;
+        }
+        fz_launches += (uint64_t)n;
+    }
+    // after a run of the fused kernel was aborted (a poll that timed out): clear the error word,
+    // move the tag base on, and report
     int fused_check() {
         if (!fused) return 0;
         uint32_t err = 0;
@@ -400,7 +428,8 @@ struct Engine {
         if (err) {
             launch_fused_sync_reset(fz_sync, st);
             (void)hipStreamSynchronize(st);
-            set_err("fused run aborted at a grid barrier (barrier words reset)");
+            fz_account(1);
+            set_err("fused run aborted: an exchange poll timed out (sync words reset)");
             return -4;
         }
         return 0;
@@ -507,6 +536,7 @@ struct Engine {
     }
     void enqueue_verify() {
         if (fused) {
+            if (!fz_capturing) fz_account(1);
             probe(K_FUSED);
             launch_fused(ctl, fz_args + FM_VERIFY, fz_grid, fz_lds, st);
             probe(K_FUSED);
@@ -517,6 +547,7 @@ struct Engine {
     }
     void enqueue_mtp_run() {
         if (fused) {
+            if (!fz_capturing) fz_account(1);
             probe(K_FUSED_DRAFT);
             launch_fused(ctl, fz_args + FM_DRAFT, fz_grid, fz_lds, st);
             probe(K_FUSED_DRAFT);
@@ -535,6 +566,7 @@ struct Engine {
     }
     void enqueue_mtp_seed() {
         if (fused) {
+            if (!fz_capturing) fz_account(1);
             launch_fused(ctl, fz_args + FM_SEED, fz_grid, fz_lds, st);
             return;
         }
