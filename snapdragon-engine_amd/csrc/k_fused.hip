@@ -32,9 +32,12 @@ constexpr int SC_P = 16;                      // positions per scores chunk (wor
 constexpr int SC_KS = HD + 32;                // LDS row stride of cached K rows in halves (576 B: the 16 rows of a
                                               // wave quarter fall on distinct banks)
 constexpr uint32_t SPIN_MAX = 400000;         // ~0.4 s at one device-scope load per iteration
+#ifndef FZ_POLL_SLEEP
+#define FZ_POLL_SLEEP 1                       // s_sleep between polls of a missing word (units of 64 clocks)
+#endif
 
 // ---- address-space views ------------------------------------------------------------------------
-// The phases are separate (non-inlined) functions, so pointers reach them as generic pointers and
+// Each layer's phases form one non-inlined function, so pointers reach it as generic pointers and
 // plain accesses compile to flat instructions. A flat access counts on both the vector-memory and
 // the LDS wait counters, so an LDS wait would also wait for every weight load in flight. Device
 // memory is therefore read and written through global-space views, and the run's arguments and run
@@ -93,41 +96,127 @@ OXE_DEV void ll_st(uint64_t *p, uint32_t v, uint32_t tag) { cst64(p, ll_pack(v, 
 OXE_DEV void ll_stf(uint64_t *p, float v, uint32_t tag) { ll_st(p, __builtin_bit_cast(uint32_t, v), tag); }
 OXE_DEV bool ll_ok(unsigned long long w, uint32_t tag) { return (uint32_t)(w >> 32) == tag; }
 
-// Spin until the N words at p (consecutive) carry `tag`; their values to v. Every spin is bounded:
-// past SPIN_MAX polls the sticky error word is set; a poll also stops when another workgroup set it.
-// false: the run was aborted.
-template <int N>
-OXE_DEV bool ll_ld(const uint64_t *p, uint32_t tag, uint32_t v[N], uint32_t *err) {
-    unsigned long long w[N];
-#pragma unroll
-    for (int i = 0; i < N; i++) w[i] = cld64(p + i);
-    uint32_t spins = 0;
-    while (true) {
-        bool ok = true;
-#pragma unroll
-        for (int i = 0; i < N; i++) ok = ok && ll_ok(w[i], tag);
-        if (ok) break;
-        if (++spins > SPIN_MAX) {
-            cst32(err, 1u);
-            return false;
-        }
-        if ((spins & 31) == 0 && cld32(err)) return false;
-        __builtin_amdgcn_s_sleep(1);
-#pragma unroll
-        for (int i = 0; i < N; i++)
-            if (!ll_ok(w[i], tag)) w[i] = cld64(p + i);
+// A thread's tagged inputs: word i at at(i).p with tag at(i).tag, wanted when at(i).on. While word 0
+// (list the word expected last first) is missing, only it is polled (one load in flight per thread,
+// so waiting workgroups do not flood the memory system with re-reads of data they already hold);
+// every wanted word is loaded once, and missing ones again until all are there. SENT: poll word 0
+// before the first load of the others (inputs that are usually not ready yet); otherwise every word
+// is loaded at once first (inputs that usually are). Every poll is bounded: past SPIN_MAX polls the
+// sticky error word is set; a poll also stops when another workgroup set it. false: the run was
+// aborted.
+struct LLW {
+    const uint64_t *p;
+    uint32_t tag;
+    bool on;
+};
+// err[0]: the sticky error word; on a timeout err[1..4] note the word polled (expected tag, the tag
+// seen, the low 32 bits of its address, the workgroup)
+OXE_DEV bool ll_spin(uint32_t &spins, uint32_t *err, const uint64_t *p, uint32_t tag, unsigned long long seen) {
+    if (++spins > SPIN_MAX) {
+        cst32(err + 1, tag);
+        cst32(err + 2, (uint32_t)(seen >> 32));
+        cst32(err + 3, (uint32_t)(uintptr_t)p);
+        cst32(err + 4, blockIdx.x);
+        cst32(err, 1u);
+        return false;
     }
-#pragma unroll
-    for (int i = 0; i < N; i++) v[i] = (uint32_t)w[i];
+    if ((spins & 31) == 0 && cld32(err)) return false;
+    __builtin_amdgcn_s_sleep(FZ_POLL_SLEEP);
     return true;
 }
-template <int N>
-OXE_DEV bool ll_ldf(const uint64_t *p, uint32_t tag, float v[N], uint32_t *err) {
-    uint32_t u[N];
-    const bool ok = ll_ld<N>(p, tag, u, err);
+// The exchange buffers as a buffer resource: two adjacent tagged words in one 16-byte device-scope
+// load. A wave's loads of 8 bytes per lane are served at about a third of the rate of 16-byte ones
+// when every workgroup reads the same words (measured: 32 KB read by 255 workgroups in 2.4 us with
+// 8-byte loads, 0.7 us with 16-byte loads). Each 8-byte half is written by one 8-byte store and
+// checked against its own tag, so a load that sees one half before the other only polls again.
+struct XR {
+    __amdgpu_buffer_rsrc_t r;
+    const uint64_t *base;
+};
+OXE_DEV XR make_xr(const uint64_t *base, uint32_t bytes) {
+    return XR{__builtin_amdgcn_make_buffer_rsrc((void *)base, (short)0, (int)bytes, 0x00020000), base};
+}
+OXE_DEV void cld128x(const XR &xr, const uint64_t *p, unsigned long long &w0, unsigned long long &w1) {
+    typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+    // cache policy 16: sc1 (device scope, as the relaxed agent-scope atomic loads above)
+    const u4 v = __builtin_amdgcn_raw_buffer_load_b128(xr.r, (int)((const char *)p - (const char *)xr.base), 0, 16);
+    w0 = ((unsigned long long)v.y << 32) | v.x;
+    w1 = ((unsigned long long)v.w << 32) | v.z;
+}
+
+// NP: words [0, 2 NP) come in adjacent pairs (at(2 m + 1).p == at(2 m).p + 1, 16-byte aligned, the
+// same `on`), loaded 16 bytes at a time through xr in the first round.
+template <int N, int NP, bool SENT, class At>
+OXE_DEV bool ll_gather(At at, uint32_t (&v)[N], uint32_t *err, const XR *xr) {
+    static_assert(N <= 32 && 2 * NP <= N, "mask of 32 words");
+    uint32_t miss = 0;
+    if (SENT && at(0).on) {
+        const LLW x = at(0);
+        uint32_t spins = 0;
+        unsigned long long y;
+        while (!ll_ok(y = cld64(x.p), x.tag))
+            if (!ll_spin(spins, err, x.p, x.tag, y)) return false;
+    }
+    {
+        unsigned long long w[N];
+        // pairs through xr (without it, word by word)
+        const int np = xr ? NP : 0;
 #pragma unroll
-    for (int i = 0; i < N; i++) v[i] = __builtin_bit_cast(float, u[i]);
-    return ok;
+        for (int m = 0; m < NP; m++) {
+            w[2 * m] = w[2 * m + 1] = 0ull;
+            if (m < np && at(2 * m).on) cld128x(*xr, at(2 * m).p, w[2 * m], w[2 * m + 1]);
+        }
+#pragma unroll
+        for (int i = 0; i < N; i++)
+            if (i >= 2 * np) w[i] = at(i).on ? cld64(at(i).p) : 0ull;
+#pragma unroll
+        for (int i = 0; i < N; i++) {
+            v[i] = (uint32_t)w[i];
+            if (at(i).on && !ll_ok(w[i], at(i).tag)) miss |= 1u << i;
+        }
+    }
+    if (miss == 0) return true;
+    uint32_t spins = 0;
+    if (miss & 1u) {
+        const LLW x = at(0);
+        unsigned long long y;
+        while (!ll_ok(y = cld64(x.p), x.tag))
+            if (!ll_spin(spins, err, x.p, x.tag, y)) return false;
+        v[0] = (uint32_t)y;
+        miss &= ~1u;
+    }
+    while (miss) {
+        unsigned long long w[N];
+#pragma unroll
+        for (int i = 1; i < N; i++) w[i] = ((miss >> i) & 1u) ? cld64(at(i).p) : 0ull;
+#pragma unroll
+        for (int i = 1; i < N; i++)
+            if (((miss >> i) & 1u) && ll_ok(w[i], at(i).tag)) {
+                v[i] = (uint32_t)w[i];
+                miss &= ~(1u << i);
+            }
+        if (miss) {
+            // the first word still missing, for the timeout note
+            const uint64_t *mp = nullptr;
+            uint32_t mt = 0;
+            unsigned long long mw = 0;
+#pragma unroll
+            for (int i = N - 1; i >= 1; i--)
+                if ((miss >> i) & 1u) { mp = at(i).p; mt = at(i).tag; mw = w[i]; }
+            if (!ll_spin(spins, err, mp, mt, mw)) return false;
+        }
+    }
+    return true;
+}
+OXE_DEV float u2f(uint32_t u) { return __builtin_bit_cast(float, u); }
+
+// wait until at most n of this wave's vector memory operations are in flight (the other counters
+// unconstrained): the weight loads issued before an input gather are left to finish in part, so
+// the gather is issued when its inputs are more likely to be there
+template <int N>
+OXE_DEV void wait_vm() {
+    static_assert(N >= 0 && N < 64, "vmcnt field");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
 // every thread's verdict of its polls combined (all threads call): false if any thread of the
@@ -149,7 +238,7 @@ struct KG {
     static constexpr int KCH = K / 16;         // 16-byte code chunks per row
     static constexpr int RPP = FT / KCH;       // rows per pass of the workgroup
     static constexpr int SPR = K / 256;        // 16-byte scale chunks per row
-    static constexpr int WDS = NB / 2 + 1;     // LDS scale row stride in words (odd)
+    static constexpr int FS = NB + 4;          // LDS row stride of the chain operands (16-byte rows)
 };
 
 template <int K, int MAXP>
@@ -160,10 +249,29 @@ struct WSlice {
 
 template <int K, int MAXR, int NL>
 struct GSm {
-    int32_t isum[NL][MAXR][KG<K>::NB + 1];
-    uint32_t wd[MAXR * KG<K>::WDS];
+    // the serial chain's operands per (lane, row, block): f32 of the int32 block dot, and the scale
+    // product h2f(activation scale) * h2f(weight scale)
+    alignas(16) float f[NL][MAXR][KG<K>::FS];
+    alignas(16) float d[NL][MAXR][KG<K>::FS];
     float out[NL][MAXR];
 };
+
+// passes [P0, P1) of the codes (and the scales when SC) into registers, as wload; nr >= 1
+template <int K, int MAXP, int P0, int P1, bool SC, class RowOf>
+OXE_DEV void wload_part(WSlice<K, MAXP> &s, const int8_t *__restrict__ wq, const uint16_t *__restrict__ wd, int nr,
+                        RowOf rowof) {
+    using G = KG<K>;
+    const int t = threadIdx.x, c = t % G::KCH, rs = t / G::KCH;
+#pragma unroll
+    for (int p = P0; p < P1; p++) {
+        const int rl = p * G::RPP + rs;
+        s.w[p] = gld((const uint4 *)(wq + rowof(rl < nr ? rl : nr - 1) * K + c * 16));
+    }
+    if (SC) {
+        const int sr = t / G::SPR, sk = t % G::SPR;
+        s.s = gld((const uint4 *)(wd + rowof(sr < nr ? sr : nr - 1) * G::NB + sk * 8));
+    }
+}
 
 // codes of rows rowof(0..nr) and their scales into registers (plain loads: weights are read-only)
 template <int K, int MAXP, bool NONEMPTY = false, class RowOf>
@@ -185,13 +293,16 @@ OXE_DEV void wload(WSlice<K, MAXP> &s, const int8_t *__restrict__ wq, const uint
 
 // g.out[l][r] = row r . lane l for the slice's nr rows (activation codes xq [NL][xq_ld] and scales
 // xd [NL][xd_ld] in LDS). Ends with a barrier.
-template <int K, int MAXP, int NL>
+struct NoMid {
+    OXE_DEV void operator()() const {}
+};
+template <int K, int MAXP, int NL, class Mid = NoMid>
 OXE_DEV void wdot(const WSlice<K, MAXP> &s, int nr, const int8_t *xq, int xq_ld, const uint16_t *xd, int xd_ld,
-                  GSm<K, MAXP * KG<K>::RPP, NL> &g) {
+                  GSm<K, MAXP * KG<K>::RPP, NL> &g, Mid mid = Mid()) {
     using G = KG<K>;
     const int t = threadIdx.x, c = t % G::KCH, rs = t / G::KCH;
     // codes first, in load order: each pass waits only for its own chunk; the scales (loaded last)
-    // go to LDS after the dots
+    // after the dots
     uint4 xa[NL];
 #pragma unroll
     for (int l = 0; l < NL; l++) xa[l] = *(const uint4 *)(xq + l * xq_ld + c * 16);
@@ -202,24 +313,42 @@ OXE_DEV void wdot(const WSlice<K, MAXP> &s, int nr, const int8_t *xq, int xq_ld,
         for (int l = 0; l < NL; l++) {
             int32_t v = dot16(s.w[p], xa[l], 0);
             v += dpp_i<DPP_XOR1>(v);  // the other half of the 32-code block sits in the adjacent lane
-            if ((c & 1) == 0 && rl < nr) g.isum[l][rl][c >> 1] = v;
+            if ((c & 1) == 0 && rl < nr) g.f[l][rl][c >> 1] = (float)v;
         }
     }
     {
+        // thread (row sr, scale chunk sk) holds the weight scales of blocks [8 sk, 8 sk + 8)
         const int sr = t / G::SPR, sk = t % G::SPR;
         if (sr < nr) {
-            uint32_t *d = &g.wd[sr * G::WDS + sk * 4];
-            d[0] = s.s.x; d[1] = s.s.y; d[2] = s.s.z; d[3] = s.s.w;
+            const uint32_t sw[4] = {s.s.x, s.s.y, s.s.z, s.s.w};
+#pragma unroll
+            for (int l = 0; l < NL; l++) {
+                float dv[8];
+#pragma unroll
+                for (int q = 0; q < 8; q++) {
+                    const uint16_t wsc = (uint16_t)(sw[q / 2] >> (16 * (q & 1)));
+                    dv[q] = h2f(xd[l * xd_ld + 8 * sk + q]) * h2f(wsc);
+                }
+                *(float4 *)&g.d[l][sr][8 * sk] = make_float4(dv[0], dv[1], dv[2], dv[3]);
+                *(float4 *)&g.d[l][sr][8 * sk + 4] = make_float4(dv[4], dv[5], dv[6], dv[7]);
+            }
         }
     }
     __syncthreads();
+    mid();
     if (t < nr * NL) {
+        // one serial FMA chain per (row, lane) in block order, four blocks per LDS read
         const int rl = t % nr, l = t / nr;
-        const uint16_t *sw = (const uint16_t *)&g.wd[rl * G::WDS];
+        const float *fr = &g.f[l][rl][0], *dr = &g.d[l][rl][0];
         float acc = 0.0f;
-#pragma unroll 8
-        for (int b = 0; b < G::NB; b++)
-            acc = __builtin_fmaf((float)g.isum[l][rl][b], h2f(xd[l * xd_ld + b]) * h2f(sw[b]), acc);
+#pragma unroll 4
+        for (int b = 0; b < G::NB; b += 4) {
+            const float4 f4 = *(const float4 *)(fr + b), d4 = *(const float4 *)(dr + b);
+            acc = __builtin_fmaf(f4.x, d4.x, acc);
+            acc = __builtin_fmaf(f4.y, d4.y, acc);
+            acc = __builtin_fmaf(f4.z, d4.z, acc);
+            acc = __builtin_fmaf(f4.w, d4.w, acc);
+        }
         g.out[l][rl] = acc;
     }
     __syncthreads();
@@ -304,28 +433,43 @@ OXE_DEV T lane_pick(const FZ_CAS T *v, int l) {
 }
 
 // The run's lanes normalised with w and quantised to xq/xd (LDS). Source per lane: the token
-// embedding (eq != null) or a tagged exchange buffer (src: [NL][E] words with tag `tag`; thread
-// (lane l, tt) reads elements [8 tt, 8 tt + 8), one producing workgroup's rows). xf: LDS staging of
-// the raw vectors; xn (optional): the normalised f32 vectors. false: the run was aborted.
-template <int NL>
+// embedding (eq != null) or a tagged exchange buffer (src: [NL][E] words with tag `tag`, read
+// coalesced: word t + FT j by thread t, staged in xf). xf: LDS staging of the raw vectors; xn
+// (optional): the normalised f32 vectors. false: the run was aborted.
+template <int NL, bool SENT = false, class Mid = NoMid>
 OXE_DEV bool prologue(int nl, const FZ_CAS RunCtl *ctl, const int8_t *eq, const uint16_t *ed, const uint64_t *src,
                       uint32_t tag, uint32_t *err,
                       const W8 &w, float eps, float (*xf)[E], int8_t *xq, int xq_ld, uint16_t *xd, int xd_ld,
-                      NormSm &ns, float (*xn)[E], int *s_ok) {
+                      NormSm &ns, float (*xn)[E], int *s_ok, const XR *xr = nullptr, Mid mid = Mid()) {
     const int t = threadIdx.x, l = t >> 8, tt = t & 255;
     float v[8];
     const bool act = l < NL && l < nl;
     bool ok = true;
-    if (act) {
-        if (eq) embed8t(eq, ed, lane_pick<NL>(ctl->tok, l), tt, v);
-        else ok = ll_ldf<8>(src + l * E + 8 * tt, tag, v, err);
-    } else {
+    if (eq) {
+        if (act) embed8t(eq, ed, lane_pick<NL>(ctl->tok, l), tt, v);
+        else
 #pragma unroll
-        for (int i = 0; i < 8; i++) v[i] = 0.0f;
+            for (int i = 0; i < 8; i++) v[i] = 0.0f;
+        if (l < NL) put8(&xf[l][8 * tt], v);
+        __syncthreads();
+    } else {
+        static_assert(NL * E == 8 * FT, "8 words per thread");
+        // word 2 (t + FT m) + h is u[2 m + h]
+        auto wi = [&](int j) { return 2 * (t + FT * (j / 2)) + (j & 1); };
+        uint32_t u[8];
+        ok = ll_gather<8, 4, SENT>([&](int j) { return LLW{src + wi(j), tag, wi(j) / E < nl}; }, u, err, xr);
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const int i = wi(j);
+            xf[i / E][i % E] = i / E < nl ? u2f(u[j]) : 0.0f;
+        }
+        if (!all_ok(ok, s_ok)) return false;
+        mid();   // inputs arrived
+        if (l < NL) get8(&xf[l][8 * tt], v);
+        else
+#pragma unroll
+            for (int i = 0; i < 8; i++) v[i] = 0.0f;
     }
-    if (!all_ok(ok, s_ok)) return false;
-    if (l < NL) put8(&xf[l][8 * tt], v);
-    __syncthreads();
     norm8(v, xf[l < NL ? l : 0], w.v, eps, ns);
     if (l < NL) {
         if (act) {
@@ -360,6 +504,7 @@ struct OutSm {
     alignas(16) int8_t xq[NL][MIX_W];
     uint16_t xd[NL][MIX_W / 32];
     GSm<MIX_W, 8, NL> g;
+    alignas(16) float stg[NL][MIX_W];   // the attention's f32 outputs, staged from the coalesced reads
 };
 template <int NL>
 struct RouterSm {
@@ -385,8 +530,9 @@ template <int NL>
 struct DownSm {
     alignas(16) int8_t hq[NL][DW_UNITS][FF];
     uint16_t hd[NL][DW_UNITS][FF / 32];
-    uint32_t wd[DW_UNITS][8 * (FF / 64 + 1)];
-    int32_t isum[DW_UNITS][NL][8][FF / 32 + 1];
+    // chain operands per (unit, lane, row, block): f32 of the int32 block dot, scale product
+    alignas(16) float f[DW_UNITS][NL][8][FF / 32 + 4];
+    alignas(16) float d[DW_UNITS][NL][8][FF / 32 + 4];
     float dn[DW_UNITS][NL][8];
 };
 template <int NL>
@@ -495,7 +641,12 @@ OXE_DEV const FZ_CAS LayerDev &layer_of(const Ctx<NL> &c, int il) {
     return *(uni(c.a->layers) + __builtin_amdgcn_readfirstlane(il));
 }
 
-#define FZ_PHASE __device__ __attribute__((noinline))
+// Phases are inlined into one non-inlined function per layer (run_layer). A call boundary costs a
+// wait for every memory operation in flight (the callee's entry waits for all counters), which at a
+// phase boundary would hold the next phase's weight loads behind the previous phase's output stores;
+// inlining the whole run instead leaves the register allocator with one function too large to
+// allocate without spills.
+#define FZ_PHASE __device__ __attribute__((always_inline)) inline
 
 // phase trace (optional): thread 0 records the device wall clock (100 MHz) at the phase start,
 // when its barrier released, and at its arrival
@@ -537,24 +688,68 @@ OXE_DEV void tr_end(Ctx<NL> &c, int id) {
 // proj: rows [r_begin, r_end) of the layer's input projection over the normalised lanes; V rows
 // (attention) also go to V^T at pos0 + l (read by later launches; this launch's attention takes the
 // new positions' V from the projection outputs). Input: the embedding (layer 0 of a verify) or x.
+// A workgroup's projection slice: rows [r0, r0 + nr) of rows [r_begin, r_end) of the layer's
+// matrix, its weights and the attention-norm weights, loaded into registers. The down phase of the
+// layer before loads it once its own inputs are in, so the slice streams during the down phase's
+// work and the exchange of its outputs.
+struct ProjPre {
+    WSlice<E, 13> ws;
+    W8 nw;
+    int r0, nr;
+};
+OXE_DEV void proj_load(const FZ_CAS LayerDev &L, int b, int G, int r_begin, int r_end, ProjPre &pp) {
+    const int n = r_end - r_begin;
+    pp.r0 = r_begin + (int)((int64_t)n * b / G);
+    pp.nr = r_begin + (int)((int64_t)n * (b + 1) / G) - pp.r0;
+    const int r0 = pp.r0;
+    wload<E, 13>(pp.ws, L.proj.q, L.proj.d, pp.nr, [&](int rl) { return (int64_t)(r0 + rl); });
+    pp.nw = wload8(L.attn_norm);
+}
+OXE_DEV int proj_rows(const FZ_CAS LayerDev &L) { return L.att ? AT_ROWS : DN_ROWS; }
+// the same in four parts (passes 0-3, 4-7, 8-11, then 12 with the scales and norm weights), issued
+// between steps of the down phase: a wave that issues more loads than the memory pipeline takes at
+// once stalls at the issue until earlier ones complete, which would hold the down phase's own work
+template <int PART>
+OXE_DEV void proj_load_part(const FZ_CAS LayerDev &L, int b, int G, int r_begin, int r_end, ProjPre &pp) {
+    if (PART == 0) {
+        const int n = r_end - r_begin;
+        pp.r0 = r_begin + (int)((int64_t)n * b / G);
+        pp.nr = r_begin + (int)((int64_t)n * (b + 1) / G) - pp.r0;
+    }
+    const int r0 = pp.r0;
+    auto rowof = [&](int rl) { return (int64_t)(r0 + rl); };
+    if (PART == 0) wload_part<E, 13, 0, 4, false>(pp.ws, L.proj.q, L.proj.d, pp.nr, rowof);
+    if (PART == 1) wload_part<E, 13, 4, 8, false>(pp.ws, L.proj.q, L.proj.d, pp.nr, rowof);
+    if (PART == 2) wload_part<E, 13, 8, 12, false>(pp.ws, L.proj.q, L.proj.d, pp.nr, rowof);
+    if (PART == 3) {
+        wload_part<E, 13, 12, 13, true>(pp.ws, L.proj.q, L.proj.d, pp.nr, rowof);
+        pp.nw = wload8(L.attn_norm);
+    }
+}
+
+// pp: the slice (loaded: by the down phase before; otherwise loaded here)
 template <int NL>
-FZ_PHASE bool phase_proj(const RunCtl *ctl, const FusedArgs *ap, int il, int k, bool embed, int r_begin, int r_end) {
+FZ_PHASE bool phase_proj(const RunCtl *ctl, const FusedArgs *ap, int il, int k, bool embed, int r_begin, int r_end,
+                         ProjPre &pp, bool loaded) {
     Ctx<NL> c = make_ctx<NL>(ctl, ap, k);
     tr_start(c);
     const FZ_CAS FusedArgs &a = *c.a;
     const FZ_CAS LayerDev &L = layer_of(c, il);
     auto &s = c.sm->proj;
-    const int n = r_end - r_begin;
-    const int r0 = r_begin + (int)((int64_t)n * c.b / c.G), r1 = r_begin + (int)((int64_t)n * (c.b + 1) / c.G);
-    const int nr = r1 - r0;
-    WSlice<E, 13> ws;
-    wload<E, 13>(ws, L.proj.q, L.proj.d, nr, [&](int rl) { return (int64_t)(r0 + rl); });
-    const W8 nw = wload8(L.attn_norm);
+    if (!loaded) {
+        proj_load(L, c.b, c.G, r_begin, r_end, pp);
+        if (!embed) wait_vm<8>();   // about half of the 16 loads above
+    }
+    const WSlice<E, 13> &ws = pp.ws;
+    const W8 &nw = pp.nw;
+    const int r0 = pp.r0, nr = pp.nr;
     uint64_t *xin = a.xc.x + (size_t)c.par() * NL * E;
+    const XR xr = make_xr(a.xbase, a.xbytes);
     if (!prologue<NL>(c.nl, c.ctl, embed ? a.m.tok_embd.q : nullptr, a.m.tok_embd.d, xin, k > 0 ? c.tag(k - 1, PH_DOWN) : 0u,
-                      c.err, nw, a.m.eps, s.xf, &s.xq[0][0], E, &s.xd[0][0], E / 32, s.ns, nullptr, &c.ps->fail))
+                      c.err, nw, a.m.eps, s.xf, &s.xq[0][0], E, &s.xd[0][0], E / 32, s.ns, nullptr, &c.ps->fail, &xr,
+                      [&] { tr_pass(c); }))
         return false;
-    tr_pass(c);
+    if (embed) tr_pass(c);
     tr_mark(c, 111);
     if (embed && c.b == 0) {
         // the embedded input is the residual of layer 0
@@ -562,7 +757,7 @@ FZ_PHASE bool phase_proj(const RunCtl *ctl, const FusedArgs *ap, int il, int k, 
         if (l < c.nl)
             for (int i = 0; i < 8; i++) ll_stf(xin + l * E + 8 * tt + i, s.xf[l][8 * tt + i], c.tag(k, PH_PROJ));
     }
-    wdot<E, 13, NL>(ws, nr, &s.xq[0][0], E, &s.xd[0][0], E / 32, s.g);
+    wdot<E, 13, NL>(ws, nr, &s.xq[0][0], E, &s.xd[0][0], E / 32, s.g, [&] { tr_mark(c, 113); });
     tr_mark(c, 112);
     const int t = threadIdx.x;
     uint64_t *po = a.xc.p + (size_t)c.par() * NL * DN_ROWS;
@@ -650,16 +845,21 @@ FZ_PHASE bool phase_dn(const RunCtl *ctl, const FusedArgs *ap, int il, int k) {
     const uint32_t tp = c.tag(k, PH_PROJ), tg = c.tag(k, PH_MIX);
     if (worker) {
         const int nl = c.nl;
-        float xin[NL], ga = 0.0f, gb = 0.0f;
-        bool ok = true;
+        float xin[NL], ga, gb;
+        bool ok;
+        {
+            uint32_t u[NL + 2];
+            const int gl1 = gl < 0 ? 0 : (gl >= NL ? NL - 1 : gl);
+            ok = ll_gather<NL + 2, 0, true>(
+                [&](int i) {
+                    if (i < NL) return LLW{pin + (int64_t)i * DN_ROWS + ch, tp, conv && i < nl};
+                    return LLW{pin + (int64_t)gl1 * DN_ROWS + (i == NL ? DN_ALPHA : DN_BETA) + vh, tp, gate && gl < nl};
+                },
+                u, c.err, nullptr);
 #pragma unroll
-        for (int l = 0; l < NL; l++) {
-            xin[l] = 0.0f;
-            if (conv && l < nl) ok = ok && ll_ldf<1>(pin + (int64_t)l * DN_ROWS + ch, tp, &xin[l], c.err);
-        }
-        if (gate && gl < nl) {
-            ok = ok && ll_ldf<1>(pin + (int64_t)gl * DN_ROWS + DN_ALPHA + vh, tp, &ga, c.err);
-            ok = ok && ll_ldf<1>(pin + (int64_t)gl * DN_ROWS + DN_BETA + vh, tp, &gb, c.err);
+            for (int l = 0; l < NL; l++) xin[l] = u2f(u[l]);
+            ga = u2f(u[NL]);
+            gb = u2f(u[NL + 1]);
         }
         if (!all_ok(ok, &c.ps->fail)) return false;
         tr_pass(c);
@@ -727,14 +927,22 @@ FZ_PHASE bool phase_dn(const RunCtl *ctl, const FusedArgs *ap, int il, int k) {
         }
         // the head's first workgroup reads the head's 128 outputs of every lane back
         const bool last = row0 == 0;
-        float x0 = 0.0f, x1 = 0.0f, z0 = 0.0f, z1 = 0.0f;
-        ok = true;
-        if (last && w < nl) {
-            const uint64_t *o = gx + (int64_t)w * DIN + vh * HV;
-            const uint64_t *z = pin + (int64_t)w * DN_ROWS + DN_Z + vh * HV;
-            ok = ll_ldf<1>(z + lane, tp, &z0, c.err) && ll_ldf<1>(z + lane + 64, tp, &z1, c.err) &&
-                 ll_ldf<1>(o + lane, tg, &x0, c.err) && ll_ldf<1>(o + lane + 64, tg, &x1, c.err);
+        float x0, x1, z0, z1;
+        {
+            const int wl = w < NL ? w : 0;
+            const uint64_t *o = gx + (int64_t)wl * DIN + vh * HV;
+            const uint64_t *z = pin + (int64_t)wl * DN_ROWS + DN_Z + vh * HV;
+            const bool on = last && w < nl;
+            uint32_t u[4];
+            ok = ll_gather<4, 0, true>(
+                [&](int i) {
+                    const int off = lane + 64 * (i & 1);
+                    return i < 2 ? LLW{o + off, tg, on} : LLW{z + off, tp, on};
+                },
+                u, c.err, nullptr);
+            x0 = u2f(u[0]); x1 = u2f(u[1]); z0 = u2f(u[2]); z1 = u2f(u[3]);
         }
+        if (last) tr_mark(c, 124);
         if (dlt) {
 #pragma unroll
             for (int l = 0; l < NL; l++) {
@@ -765,6 +973,7 @@ FZ_PHASE bool phase_dn(const RunCtl *ctl, const FusedArgs *ap, int il, int k) {
             if (lane == 0) { ll_st(d + 0, f2h(d0), tg); ll_st(d + 2, f2h(d1), tg); }
             if (lane == 32) { ll_st(d + 1, f2h(d0), tg); ll_st(d + 3, f2h(d1), tg); }
         }
+        if (last) tr_mark(c, 125);
         if (!all_ok(ok, &c.ps->fail)) return false;
     }
     tr_end(c, TP_DN);
@@ -786,19 +995,41 @@ FZ_PHASE bool phase_out(const RunCtl *ctl, const FusedArgs *ap, int il, int k, u
     wload<MIX_W, 4>(ws, L.out.q, L.out.d, 8, [&](int rl) { return (int64_t)(r0 + rl); });
     const uint64_t *xin = a.xc.x + (size_t)c.par() * NL * E;
     const uint32_t tm = c.tag(k, L.att ? PH_PV : PH_MIX);
-    bool ok = true;
-    float xres = 0.0f;
-    if (t < NL * 8 && t / 8 < c.nl) ok = ll_ldf<1>(xin + (int64_t)(t / 8) * E + r0 + t % 8, xtag, &xres, c.err);
+    bool ok;
+    float xres;
     const int l = t >> 8, tt = t & 255;
     const bool act = l < NL && l < c.nl;
+    const int l1 = l < NL ? l : 0;
+    const bool xon = t < NL * 8 && t / 8 < c.nl;
+    const uint64_t *xr = xin + (int64_t)((t / 8) % NL) * E + r0 + t % 8;
+    const XR xrs = make_xr(a.xbase, a.xbytes);
     if (L.att) {
-        // the attention's gated outputs (f32): thread (lane l, 16 elements at 16 tt), Q8_0 blocks of
-        // 32 over adjacent thread pairs (quantize_row_q8_0 NEON: amax, d = amax / 127, id from the
-        // f32 d, round-half-even codes)
+        // the attention's gated outputs (f32), read coalesced (word t + FT j) into LDS; then thread
+        // (lane l, 16 elements at 16 tt), Q8_0 blocks of 32 over adjacent thread pairs
+        // (quantize_row_q8_0 NEON: amax, d = amax / 127, id from the f32 d, round-half-even codes)
+        static_assert(NL * MIX_W == 16 * FT, "16 words per thread");
+        {
+            // word 2 (t + FT m) + h is u[2 m + h]
+            auto wi = [&](int j) { return 2 * (t + FT * (j / 2)) + (j & 1); };
+            uint32_t u[17];
+            const uint64_t *gi = a.xc.g + (size_t)c.par() * NL * MIX_W;
+            ok = ll_gather<17, 8, true>(
+                [&](int j) { return j < 16 ? LLW{gi + wi(j), tm, wi(j) / MIX_W < c.nl} : LLW{xr, xtag, xon}; }, u, c.err,
+                &xrs);
+#pragma unroll
+            for (int j = 0; j < 16; j++) {
+                const int i = wi(j);
+                s.stg[i / MIX_W][i % MIX_W] = i / MIX_W < c.nl ? u2f(u[j]) : 0.0f;
+            }
+            xres = u2f(u[16]);
+        }
+        if (!all_ok(ok, &c.ps->fail)) return false;
         float v[16];
 #pragma unroll
-        for (int q = 0; q < 16; q++) v[q] = 0.0f;
-        if (act) ok = ll_ldf<16>(a.xc.g + ((size_t)c.par() * NL + l) * MIX_W + 16 * tt, tm, v, c.err) && ok;
+        for (int q = 0; q < 16; q += 4) {
+            const float4 f = *(const float4 *)&s.stg[l1][16 * tt + q];
+            v[q] = f.x; v[q + 1] = f.y; v[q + 2] = f.z; v[q + 3] = f.w;
+        }
         float am = 0.0f;
 #pragma unroll
         for (int q = 0; q < 16; q++) am = fmaxf(am, __builtin_fabsf(v[q]));
@@ -817,20 +1048,36 @@ FZ_PHASE bool phase_out(const RunCtl *ctl, const FusedArgs *ap, int il, int k, u
             *(uint4 *)&s.xq[l][16 * tt] = make_uint4(w[0], w[1], w[2], w[3]);
             if ((tt & 1) == 0) s.xd[l][tt / 2] = f2h(dd);
         }
+        __syncthreads();
     } else {
-        uint32_t w[4] = {0u, 0u, 0u, 0u};
-        if (act) ok = ll_ld<4>(a.xc.o + ((size_t)c.par() * NL + l) * (MIX_W / 4) + 4 * tt, tm, w, c.err) && ok;
-        if (l < NL) *(uint4 *)&s.xq[l][16 * tt] = make_uint4(w[0], w[1], w[2], w[3]);
-        if (t < NL * (MIX_W / 32)) {
-            const int ll = t / (MIX_W / 32), bb = t % (MIX_W / 32);
-            uint32_t d = 0u;
-            if (ll < c.nl) ok = ll_ld<1>(a.xc.od + ((size_t)c.par() * NL + ll) * (MIX_W / 32) + bb, tm, &d, c.err) && ok;
-            s.xd[ll][bb] = (uint16_t)d;
+        // the quantised delta-net output (4 codes per word), read coalesced: word t + FT j by thread
+        // t; scale word t by threads t < NL * MIX_W / 32
+        static_assert(NL * MIX_W / 4 == 4 * FT, "4 words per thread");
+        const int ll = (t / (MIX_W / 32)) % NL, bb = t % (MIX_W / 32);
+        const bool don = t < NL * (MIX_W / 32) && t / (MIX_W / 32) < c.nl;
+        const uint64_t *oi = a.xc.o + (size_t)c.par() * NL * (MIX_W / 4);
+        const uint64_t *di = a.xc.od + ((size_t)c.par() * NL + ll) * (MIX_W / 32) + bb;
+        // word 2 (t + FT m) + h is u[2 m + h]
+        auto wi = [&](int j) { return 2 * (t + FT * (j / 2)) + (j & 1); };
+        uint32_t u[6];
+        ok = ll_gather<6, 2, true>(
+            [&](int j) {
+                return j < 4 ? LLW{oi + wi(j), tm, wi(j) / (MIX_W / 4) < c.nl}
+                             : (j == 4 ? LLW{di, tm, don} : LLW{xr, xtag, xon});
+            },
+            u, c.err, &xrs);
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int i = wi(j), li = i / (MIX_W / 4);
+            ((uint32_t *)&s.xq[li][0])[i % (MIX_W / 4)] = li < c.nl ? u[j] : 0u;
         }
+        if (t < NL * (MIX_W / 32)) s.xd[ll][bb] = don ? (uint16_t)u[4] : (uint16_t)0;
+        xres = u2f(u[5]);
+        if (!all_ok(ok, &c.ps->fail)) return false;
     }
-    if (!all_ok(ok, &c.ps->fail)) return false;
     tr_pass(c);
-    wdot<MIX_W, 4, NL>(ws, 8, &s.xq[0][0], MIX_W, &s.xd[0][0], MIX_W / 32, s.g);
+    wdot<MIX_W, 4, NL>(ws, 8, &s.xq[0][0], MIX_W, &s.xd[0][0], MIX_W / 32, s.g, [&] { tr_mark(c, 171); });
+    tr_mark(c, 172);
     if (t < NL * 8) {
         const int ll = t / 8, rl = t % 8;
         if (ll < c.nl)
@@ -872,10 +1119,11 @@ FZ_PHASE bool phase_router(const RunCtl *ctl, const FusedArgs *ap, int il, int k
             if (shg) s.sg[e % 16][e / 16] = gr[q];
         }
     }
-    if (!prologue<NL>(c.nl, c.ctl, nullptr, nullptr, a.xc.x1 + (size_t)c.par() * NL * E, c.tag(k, PH_OUT), c.err, nw,
-                      a.m.eps, s.xf, &s.xq[0][0], E, &s.xd[0][0], E / 32, s.ns, s.xn, &c.ps->fail))
+    const XR xr = make_xr(a.xbase, a.xbytes);
+    if (!prologue<NL, true>(c.nl, c.ctl, nullptr, nullptr, a.xc.x1 + (size_t)c.par() * NL * E, c.tag(k, PH_OUT), c.err, nw,
+                      a.m.eps, s.xf, &s.xq[0][0], E, &s.xd[0][0], E / 32, s.ns, s.xn, &c.ps->fail, &xr, [&] { tr_pass(c); }))
         return false;
-    tr_pass(c);
+    tr_mark(c, 131);
     {
         const int l = t >> 8, tt = t & 255;
         if (l < NL) {
@@ -937,8 +1185,10 @@ FZ_PHASE bool phase_router(const RunCtl *ctl, const FusedArgs *ap, int il, int k
 // gate/up (group b = (union slot u = b / 16, 64-row group b % 16): 4 tiles = 32 h values per lane,
 // one Q8_0 block), then the down projection + combine of rows [8 b, 8 b + 8), written to x of the
 // next run layer
+// il_next >= 0: once the down phase's inputs are in, the projection slice of layer il_next goes
+// to pp
 template <int NL>
-FZ_PHASE bool phase_moe(const RunCtl *ctl, const FusedArgs *ap, int il, int k) {
+FZ_PHASE bool phase_moe(const RunCtl *ctl, const FusedArgs *ap, int il, int k, int il_next, ProjPre &pp) {
     Ctx<NL> c = make_ctx<NL>(ctl, ap, k);
     tr_start(c);
     const FZ_CAS FusedArgs &a = *c.a;
@@ -952,9 +1202,9 @@ FZ_PHASE bool phase_moe(const RunCtl *ctl, const FusedArgs *ap, int il, int k) {
     bool ok = true;
     if (t < NL * NEXP) {
         const int l = t / NEXP, i = t % NEXP;
-        float v = 0.0f;
-        if (l < nl) ok = ll_ldf<1>(a.xc.lg + ((size_t)c.par() * NL + l) * NEXP + i, trt, &v, c.err);
-        se.lg[l][i] = v;
+        uint32_t u[1];
+        ok = ll_gather<1, 0, false>([&](int) { return LLW{a.xc.lg + ((size_t)c.par() * NL + l) * NEXP + i, trt, l < nl}; }, u, c.err, nullptr);
+        se.lg[l][i] = l < nl ? u2f(u[0]) : 0.0f;
     }
     if (t == 0) ps.ro.tie = 0;
     if (!all_ok(ok, &ps.fail)) return false;
@@ -997,6 +1247,40 @@ FZ_PHASE bool phase_moe(const RunCtl *ctl, const FusedArgs *ap, int il, int k) {
     WSlice<E, 16> ew;
     wload<E, 16>(ew, L.exp_gu.q + (int64_t)e_g * 2 * FF * E, L.exp_gu.d + (int64_t)e_g * 2 * FF * (E / 32), gw ? 64 : 0,
                  [&](int rl) { return (int64_t)(gq * 64 + rl); });
+    // the down rows of every union expert and the shared expert (rows [8 b, 8 b + 8) of each unit):
+    // the first DW_EARLY units per thread right behind the gate/up rows, the rest in the down phase
+    // (measured: any issued here slow the gate/up stream more than they save). The weight loads are
+    // unconditional (a load skipped on some path makes the compiler's wait for an earlier one
+    // conservative, i.e. a wait for all): units past the union re-read the shared expert's rows.
+    const int r0 = 8 * b;
+    const int uh = t >> 8, rr = (t >> 5) & 7, ck = t & 31;
+    auto unit_q = [&](int u) -> const int8_t * {
+        int e = ps.uni[u < OXE_MAX_UNION ? u : 0];
+        e = e < 0 ? 0 : (e >= NEXP ? NEXP - 1 : e);
+        return u < nu && u < OXE_MAX_UNION ? L.exp_down.q + (int64_t)e * E * FF : L.shexp_down.q;
+    };
+    uint4 dw[9];
+    auto dload = [&](int q) {
+        dw[q] = gld((const uint4 *)(unit_q(2 * q + uh) + (int64_t)(r0 + rr) * FF + 16 * ck));
+    };
+    const int su = t / 16 < DW_UNITS ? t / 16 : OXE_MAX_UNION, srr = (t % 16) / 2, shf = t % 2;
+    uint4 dsc;
+    auto sload = [&]() {
+        int e = ps.uni[su < OXE_MAX_UNION ? su : 0];
+        e = e < 0 ? 0 : (e >= NEXP ? NEXP - 1 : e);
+        const uint16_t *base = su < nu && su < OXE_MAX_UNION ? L.exp_down.d + (int64_t)e * E * (FF / 32) : L.shexp_down.d;
+        dsc = gld((const uint4 *)(base + (int64_t)(r0 + srr) * (FF / 32) + shf * 8));
+    };
+#ifndef FZ_DW_EARLY
+#define FZ_DW_EARLY 0
+#endif
+#ifndef FZ_DW_PRE
+#define FZ_DW_PRE 5
+#endif
+    constexpr int DW_EARLY = FZ_DW_EARLY, DW_PRE = FZ_DW_PRE > FZ_DW_EARLY ? FZ_DW_PRE : FZ_DW_EARLY;
+#pragma unroll
+    for (int q = 0; q < DW_EARLY; q++) dload(q);
+    if (DW_EARLY > 0) sload();
     tr_mark(c, 102);
     // 3. gate/up + swiglu + Q8_0 of the group's 32 h values per lane
     if (gw) {
@@ -1018,67 +1302,64 @@ FZ_PHASE bool phase_moe(const RunCtl *ctl, const FusedArgs *ap, int il, int k) {
     tr_end(c, TP_EXPERTS);
     tr_start(c);
     __syncthreads();   // the down phase's LDS aliases the experts'
-    // the down rows of every union expert and the shared expert: the first DW_PRE units per
-    // thread issued before the phase's inputs are polled, the rest behind them (a poll waits behind
-    // every load the thread has outstanding). The weight loads are unconditional (a load skipped on
-    // some path makes the compiler's wait for an earlier one conservative, i.e. a wait for all):
-    // units past the union re-read the shared expert's rows (cached).
-    const int r0 = 8 * b;
-    const int uh = t >> 8, rr = (t >> 5) & 7, ck = t & 31;
-    auto unit_q = [&](int u) -> const int8_t * {
-        int e = ps.uni[u < OXE_MAX_UNION ? u : 0];
-        e = e < 0 ? 0 : (e >= NEXP ? NEXP - 1 : e);
-        return u < nu && u < OXE_MAX_UNION ? L.exp_down.q + (int64_t)e * E * FF : L.shexp_down.q;
-    };
-    uint4 dw[9];
-    auto dload = [&](int q) {
-        dw[q] = gld((const uint4 *)(unit_q(2 * q + uh) + (int64_t)(r0 + rr) * FF + 16 * ck));
-    };
-    constexpr int DW_PRE = 5;
+    // down units [DW_EARLY, DW_PRE) issued before the phase's inputs are polled, the rest behind them
+    // (a poll waits behind every load the thread has outstanding)
 #pragma unroll
-    for (int q = 0; q < DW_PRE; q++) dload(q);
-    const int su = t / 16 < DW_UNITS ? t / 16 : OXE_MAX_UNION, srr = (t % 16) / 2, shf = t % 2;
-    uint4 dsc;
-    {
-        int e = ps.uni[su < OXE_MAX_UNION ? su : 0];
-        e = e < 0 ? 0 : (e >= NEXP ? NEXP - 1 : e);
-        const uint16_t *base = su < nu && su < OXE_MAX_UNION ? L.exp_down.d + (int64_t)e * E * (FF / 32) : L.shexp_down.d;
-        dsc = gld((const uint4 *)(base + (int64_t)(r0 + srr) * (FF / 32) + shf * 8));
-    }
+    for (int q = DW_EARLY; q < DW_PRE; q++) dload(q);
+    if (DW_EARLY == 0) sload();
     // 4. down + combine (engine.rs:3542-3624). Inputs in the order they are published: the shared
     // expert's h (quantised here), the residual rows and the shared gate (router / out phases), then
     // the routed experts' quantised h of the union's live slots.
     auto &sd = c.sm->down;
     const size_t pl = (size_t)c.par() * NL;
+    // this thread's inputs, latest producers first: the routed experts' h (4 codes per word; word
+    // t + FT m of [lane][union slot][FF / 4], read coalesced) and its scale word t, then the shared
+    // expert's h (element t of each lane), the residual row and the shared gate (t < NL * 8)
+    constexpr int NHW = NL * OXE_MAX_UNION * (FF / 4) / FT;   // h words per thread
+    static_assert(NL * OXE_MAX_UNION * (FF / 4) == NHW * FT && NL * OXE_MAX_UNION * (FF / 32) == FT, "word split");
+    const int ld_ = t / (OXE_MAX_UNION * (FF / 32)), ud = (t / (FF / 32)) % OXE_MAX_UNION;
+    const int tx = t < NL * 8 ? t : NL * 8 - 1;
+    const bool xon = t < NL * 8 && tx / 8 < nl;
+    // h word 2 (t + FT m) + h of [lane][union slot][FF / 4] is u[2 m + h]
+    auto hwi = [&](int j) { return 2 * (t + FT * (j / 2)) + (j & 1); };
+    auto hq_on = [&](int j) {
+        const int i = hwi(j), q = i / (OXE_MAX_UNION * (FF / 4)), u = (i / (FF / 4)) % OXE_MAX_UNION;
+        return q < nl && u < nu;
+    };
+    constexpr int NW = NHW + 1 + NL + 2;
+    const XR xr = make_xr(a.xbase, a.xbytes);
+    uint32_t u[NW];
+    ok = ll_gather<NW, NHW / 2, true>(
+        [&](int i) {
+            if (i < NHW) return LLW{a.xc.hq + pl * OXE_MAX_UNION * (FF / 4) + hwi(i), tet, hq_on(i)};
+            if (i == NHW) return LLW{a.xc.hd + (pl * OXE_MAX_UNION) * (FF / 32) + t, tet, ld_ < nl && ud < nu};
+            if (i < NHW + 1 + NL) {
+                const int l = i - NHW - 1;
+                return LLW{a.xc.hsh + (pl + l) * FFSH + t, trt, l < nl};
+            }
+            if (i == NHW + 1 + NL) return LLW{a.xc.x1 + (pl + tx / 8) * E + r0 + tx % 8, c.tag(k, PH_OUT), xon};
+            return LLW{a.xc.sg + pl + tx / 8, trt, xon};
+        },
+        u, c.err, &xr);
+    const uint32_t hdv = u[NHW];
     float hsv[NL];
 #pragma unroll
-    for (int l = 0; l < NL; l++) {
-        hsv[l] = 0.0f;
-        if (l < nl) ok = ll_ldf<1>(a.xc.hsh + (pl + l) * FFSH + t, trt, &hsv[l], c.err) && ok;
-    }
-    const int tx = t < NL * 8 ? t : NL * 8 - 1;
-    float x1v = 0.0f, sgv = 0.0f;
-    if (t < NL * 8 && tx / 8 < nl) {
-        ok = ll_ldf<1>(a.xc.x1 + (pl + tx / 8) * E + r0 + tx % 8, c.tag(k, PH_OUT), &x1v, c.err) && ok;
-        ok = ll_ldf<1>(a.xc.sg + pl + tx / 8, trt, &sgv, c.err) && ok;
-    }
-    constexpr int NHQ = NL * OXE_MAX_UNION * (FF / 16) / FT;   // 16-code items per thread
-    uint32_t hqv[NHQ][4];
-#pragma unroll
-    for (int q = 0; q < NHQ; q++) {
-        const int i = t + FT * q;
-        const int l = i / (OXE_MAX_UNION * (FF / 16)), u = (i / (FF / 16)) % OXE_MAX_UNION, kk = i % (FF / 16);
-        hqv[q][0] = hqv[q][1] = hqv[q][2] = hqv[q][3] = 0u;
-        if (l < nl && u < nu) ok = ll_ld<4>(a.xc.hq + ((pl + l) * OXE_MAX_UNION + u) * (FF / 4) + 4 * kk, tet, hqv[q], c.err) && ok;
-    }
-    static_assert(NL * OXE_MAX_UNION * (FF / 32) == FT, "one scale per thread");
-    uint32_t hdv = 0u;
-    {
-        const int l = t / (OXE_MAX_UNION * (FF / 32)), u = (t / (FF / 32)) % OXE_MAX_UNION;
-        if (l < nl && u < nu) ok = ll_ld<1>(a.xc.hd + (pl * OXE_MAX_UNION) * (FF / 32) + t, tet, &hdv, c.err) && ok;
-    }
+    for (int l = 0; l < NL; l++) hsv[l] = l < nl ? u2f(u[NHW + 1 + l]) : 0.0f;
+    const float x1v = u2f(u[NHW + 1 + NL]), sgv = u2f(u[NHW + 2 + NL]);
 #pragma unroll
     for (int q = DW_PRE; q < 9; q++) dload(q);
+#ifndef FZ_NO_PREFETCH
+    const bool pf = il_next >= 0;
+#else
+    const bool pf = false;
+#endif
+    const FZ_CAS LayerDev &Ln = layer_of(c, pf ? il_next : il);
+    const int pre_rows = proj_rows(Ln);
+#ifdef FZ_PREFETCH_ONCE
+    if (pf) proj_load(Ln, b, c.G, 0, pre_rows, pp);
+#else
+    if (pf) proj_load_part<0>(Ln, b, c.G, 0, pre_rows, pp);
+#endif
     // Q8_0 of the shared expert's h: element t of lane l in thread t, a block per half wave
     static_assert(FFSH == FT, "one shared-expert element per thread and lane");
 #pragma unroll
@@ -1088,23 +1369,31 @@ FZ_PHASE bool phase_moe(const RunCtl *ctl, const FusedArgs *ap, int il, int k) {
         if ((t & 3) == 0) *(uint32_t *)&sd.hq[l][OXE_MAX_UNION][t] = word;
         if ((t & 31) == 0) sd.hd[l][OXE_MAX_UNION][t / 32] = f2h(dd);
     }
-    if (t < DW_UNITS * 16) {
-        uint32_t *d = &sd.wd[su][srr * (FF / 64 + 1) + shf * 4];
-        d[0] = dsc.x; d[1] = dsc.y; d[2] = dsc.z; d[3] = dsc.w;
-    }
 #pragma unroll
-    for (int q = 0; q < NHQ; q++) {
-        const int i = t + FT * q;
-        const int l = i / (OXE_MAX_UNION * (FF / 16)), u = (i / (FF / 16)) % OXE_MAX_UNION, kk = i % (FF / 16);
-        *(uint4 *)&sd.hq[l][u][16 * kk] = make_uint4(hqv[q][0], hqv[q][1], hqv[q][2], hqv[q][3]);
+    for (int m = 0; m < NHW; m++) {
+        const int i = hwi(m), q = i / (OXE_MAX_UNION * (FF / 4)), uu = (i / (FF / 4)) % OXE_MAX_UNION;
+        ((uint32_t *)&sd.hq[q][uu][0])[i % (FF / 4)] = hq_on(m) ? u[m] : 0u;
     }
-    {
-        const int l = t / (OXE_MAX_UNION * (FF / 32)), u = (t / (FF / 32)) % OXE_MAX_UNION, kb = t % (FF / 32);
-        sd.hd[l][u][kb] = (uint16_t)hdv;
-    }
+    sd.hd[ld_][ud][t % (FF / 32)] = (uint16_t)hdv;
     if (!all_ok(ok, &ps.fail)) return false;
     tr_pass(c);
+#ifndef FZ_PREFETCH_ONCE
+    if (pf) proj_load_part<1>(Ln, b, c.G, 0, pre_rows, pp);
+#endif
     tr_mark(c, 161);
+    if (t < DW_UNITS * 16) {
+        // scale products of (unit su, row srr, blocks [8 shf, 8 shf + 8)) for every lane
+        const uint32_t sw[4] = {dsc.x, dsc.y, dsc.z, dsc.w};
+#pragma unroll
+        for (int l = 0; l < NL; l++) {
+            float dv[8];
+#pragma unroll
+            for (int q = 0; q < 8; q++)
+                dv[q] = h2f(sd.hd[l][su][8 * shf + q]) * h2f((uint16_t)(sw[q / 2] >> (16 * (q & 1))));
+            *(float4 *)&sd.d[su][l][srr][8 * shf] = make_float4(dv[0], dv[1], dv[2], dv[3]);
+            *(float4 *)&sd.d[su][l][srr][8 * shf + 4] = make_float4(dv[4], dv[5], dv[6], dv[7]);
+        }
+    }
 #pragma unroll
     for (int q = 0; q < 9; q++) {
         const int u = 2 * q + uh;
@@ -1114,24 +1403,35 @@ FZ_PHASE bool phase_moe(const RunCtl *ctl, const FusedArgs *ap, int il, int k) {
                 const uint4 xa = *(const uint4 *)&sd.hq[l][u][16 * ck];
                 int32_t v = dot16(dw[q], xa, 0);
                 v += dpp_i<DPP_XOR1>(v);
-                if ((ck & 1) == 0) sd.isum[u][l][rr][ck >> 1] = v;
+                if ((ck & 1) == 0) sd.f[u][l][rr][ck >> 1] = (float)v;
             }
         }
     }
     __syncthreads();
+#ifndef FZ_PREFETCH_ONCE
+    if (pf) proj_load_part<2>(Ln, b, c.G, 0, pre_rows, pp);
+#endif
     tr_mark(c, 162);
     if (t < DW_UNITS * NL * 8) {
         const int u = t / (NL * 8), l = (t / 8) % NL, r = t % 8;
         if (u == OXE_MAX_UNION || u < nu) {
-            const uint16_t *sw = (const uint16_t *)&sd.wd[u][r * (FF / 64 + 1)];
+            const float *fr = &sd.f[u][l][r][0], *dr = &sd.d[u][l][r][0];
             float acc = 0.0f;
 #pragma unroll
-            for (int bb = 0; bb < FF / 32; bb++)
-                acc = __builtin_fmaf((float)sd.isum[u][l][r][bb], h2f(sd.hd[l][u][bb]) * h2f(sw[bb]), acc);
+            for (int bb = 0; bb < FF / 32; bb += 4) {
+                const float4 f4 = *(const float4 *)(fr + bb), d4 = *(const float4 *)(dr + bb);
+                acc = __builtin_fmaf(f4.x, d4.x, acc);
+                acc = __builtin_fmaf(f4.y, d4.y, acc);
+                acc = __builtin_fmaf(f4.z, d4.z, acc);
+                acc = __builtin_fmaf(f4.w, d4.w, acc);
+            }
             sd.dn[u][l][r] = acc;
         }
     }
     __syncthreads();
+#ifndef FZ_PREFETCH_ONCE
+    if (pf) proj_load_part<3>(Ln, b, c.G, 0, pre_rows, pp);
+#endif
     tr_mark(c, 163);
     if (t < NL * 8) {
         const int l = t / 8, r = t % 8;
@@ -1217,23 +1517,29 @@ FZ_PHASE bool phase_scores(const RunCtl *ctl, const FusedArgs *ap, int il, int k
     // its own: lane c holds elements c + 64 i; RoPE pairs (c, c + 32) for c < 32 (slot 0)
     const uint64_t *pin = a.xc.p + (size_t)c.par() * NL * DN_ROWS;
     const uint32_t tp = c.tag(k, PH_PROJ);
-    bool ok = true;
-    float kv4[4], qv4[(NL * GQA + 7) / 8][4];
-    if (kdo) {
-        const uint64_t *kr = pin + (int64_t)kjob * DN_ROWS + AT_K + kvh * HD;
+    constexpr int NQJ = (NL * GQA + 7) / 8;
+    float kv4[4], qv4[NQJ][4];
+    {
+        // the query rows of this wave's jobs and the K row, 4 words each (elements lane + 64 i)
+        uint32_t u[4 * NQJ + 4];
+        const bool ok = ll_gather<4 * NQJ + 4, 0, true>(
+            [&](int i) {
+                const int q = i / 4, e = lane + 64 * (i % 4);
+                if (q < NQJ) {
+                    const int job = w + 8 * q, l = (job / GQA) % NL, h = kvh * GQA + job % GQA;
+                    return LLW{pin + (int64_t)l * DN_ROWS + h * 2 * HD + e, tp, qdo && job < NL * GQA && job / GQA < nl};
+                }
+                return LLW{pin + (int64_t)(kjob % NL) * DN_ROWS + AT_K + kvh * HD + e, tp, kdo};
+            },
+            u, c.err, nullptr);
 #pragma unroll
-        for (int i = 0; i < 4; i++) ok = ll_ldf<1>(kr + lane + 64 * i, tp, &kv4[i], c.err) && ok;
+        for (int q = 0; q < NQJ; q++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) qv4[q][i] = u2f(u[4 * q + i]);
+#pragma unroll
+        for (int i = 0; i < 4; i++) kv4[i] = u2f(u[4 * NQJ + i]);
+        if (!all_ok(ok, &c.ps->fail)) return false;
     }
-#pragma unroll
-    for (int q = 0; q < (NL * GQA + 7) / 8; q++) {
-        const int job = w + 8 * q, l = job / GQA, h = kvh * GQA + job % GQA;
-        if (qdo && job < NL * GQA && l < nl) {
-            const uint64_t *qr = pin + (int64_t)l * DN_ROWS + h * 2 * HD;
-#pragma unroll
-            for (int i = 0; i < 4; i++) ok = ll_ldf<1>(qr + lane + 64 * i, tp, &qv4[q][i], c.err) && ok;
-        }
-    }
-    if (!all_ok(ok, &c.ps->fail)) return false;
     tr_pass(c);
     auto finish = [&](float v[4], const float wt[4], const float cs[2], float *replay, uint16_t *dst) {
 #pragma unroll
@@ -1380,31 +1686,47 @@ FZ_PHASE bool phase_pv(const RunCtl *ctl, const FusedArgs *ap, int il, int k) {
         const int q = t >> 8, tq = t & 255, wq = (t >> 6) & 3;
         const int cp = t & 15, d = (t >> 4) & (PVD - 1);
         const int h = kvh * GQA + 2 * hp + q;
-        bool ok = true;
-        // this run's V entries of the chunk's 16 dims, and this thread's gate
-        if (t < NL * PVD) {
-            const int vl = t / PVD, vd = t % PVD;
-            float v = 0.0f;
-            if (vl < nl) ok = ll_ldf<1>(pin + (int64_t)vl * DN_ROWS + AT_V + kvh * HD + dchunk * PVD + vd, tp, &v, c.err);
-            s_vn[vl * PVD + vd] = f2h(v);
-        }
-        float sg = 0.0f;
-        if (cp == 0) ok = ll_ldf<1>(pin + (int64_t)l * DN_ROWS + h * 2 * HD + HD + dchunk * PVD + d, tp, &sg, c.err) && ok;
-        const float scale = 1.0f / sqrtf((float)HD);
         // the scores of head q: groups of 4 positions up to the one holding pos (the scores phase
         // tags every position of its chunks); later groups are masked and not read
         const uint64_t *sc = a.xc.sc + ((size_t)c.par() * NL + l) * NH * n_ctx + (int64_t)h * n_ctx;
-        auto sget = [&](int g, uint32_t u[4]) -> bool {
-            if (4 * g > pos) {
-                u[0] = u[1] = u[2] = u[3] = 0u;
-                return true;
-            }
-            return ll_ld<4>(sc + 4 * g, ts, u, c.err);
+        auto sget = [&](int g, uint32_t (&u)[4]) -> bool {
+            return ll_gather<4, 0, false>([&](int i) { return LLW{sc + 4 * g + i, ts, 4 * g <= pos}; }, u, c.err, nullptr);
         };
+        const int ng = n_kv / 4;
+        const bool shortrow = ng <= 256 * PV_SMK;
+        // this thread's scores of head q (short rows: positions tq + 256 j, read coalesced and staged
+        // in LDS, where the V^T tile goes later), this run's V entries of the chunk's 16 dims
+        // (t < NL * PVD) and this thread's gate, in one gather
+        constexpr int NSC = 4 * PV_SMK;
+        float *s_raw = (float *)s_v;                                        // [2][n_kv] staged scores
+        const int vl = (t / PVD) % NL, vd = t % PVD;
+        // position 2 (tq + 256 m) + h is u0[2 m + h]; a pair is wanted when its first position is
+        auto pi = [&](int i) { return 2 * (tq + 256 * (i / 2)) + (i & 1); };
+        const XR xr = make_xr(a.xbase, a.xbytes);
+        uint32_t u0[NSC + 2];
+        bool ok = ll_gather<NSC + 2, NSC / 2, true>(
+            [&](int i) {
+                if (i < NSC) {
+                    const int p0 = pi(i & ~1);
+                    return LLW{sc + pi(i), ts, shortrow && p0 < n_kv && p0 <= pos};
+                }
+                if (i == NSC)
+                    return LLW{pin + (int64_t)vl * DN_ROWS + AT_V + kvh * HD + dchunk * PVD + vd, tp, t < NL * PVD && vl < nl};
+                return LLW{pin + (int64_t)l * DN_ROWS + h * 2 * HD + HD + dchunk * PVD + d, tp, cp == 0};
+            },
+            u0, c.err, &xr);
+        if (shortrow)
+#pragma unroll
+            for (int i = 0; i < NSC; i++) {
+                const int p = pi(i);
+                if (p < n_kv) s_raw[q * n_kv + p] = u2f(u0[i]);
+            }
+        if (t < NL * PVD) s_vn[vl * PVD + vd] = f2h(vl < nl ? u2f(u0[NSC]) : 0.0f);
+        float sg = cp == 0 ? u2f(u0[NSC + 1]) : 0.0f;
+        const float scale = 1.0f / sqrtf((float)HD);
         {
             // softmax of head q: wp = s * scale (masked: -inf), max, e = v_expf(wp - max) with group
             // sums (e0 + e1) + (e2 + e3) added in double, p = f16(e * f32(1 / sum))
-            const int ng = n_kv / 4;
             auto wval = [&](uint32_t u, int p) { return p <= pos ? __builtin_bit_cast(float, u) * scale : -__builtin_inff(); };
             auto group = [&](int g, float mx) {
                 uint32_t u[4];
@@ -1443,21 +1765,22 @@ FZ_PHASE bool phase_pv(const RunCtl *ctl, const FusedArgs *ap, int il, int k) {
             };
             float mx = -__builtin_inff();
             double part = 0.0;
-            if (ng <= 256 * PV_SMK) {
+            if (shortrow) {
+                if (!all_ok(ok, &c.ps->fail)) return false;
+                tr_pass(c);
                 float e[PV_SMK][4];
 #pragma unroll
                 for (int k2 = 0; k2 < PV_SMK; k2++) {
                     const int g = tq + 256 * k2;
-                    uint32_t u[4] = {0u, 0u, 0u, 0u};
-                    if (g < ng) ok = sget(g, u) && ok;
+                    float4 f = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                    if (g < ng) f = *(const float4 *)&s_raw[q * n_kv + 4 * g];
+                    const float fr[4] = {f.x, f.y, f.z, f.w};
 #pragma unroll
                     for (int i = 0; i < 4; i++) {
-                        e[k2][i] = g < ng ? wval(u[i], 4 * g + i) : -__builtin_inff();
+                        e[k2][i] = g < ng ? wval(__builtin_bit_cast(uint32_t, fr[i]), 4 * g + i) : -__builtin_inff();
                         mx = (mx > e[k2][i]) ? mx : e[k2][i];
                     }
                 }
-                if (!all_ok(ok, &c.ps->fail)) return false;
-                tr_pass(c);
                 mx = head_max(mx);
                 tr_mark(c, 143);
 #pragma unroll
@@ -1622,8 +1945,10 @@ FZ_PHASE bool phase_head(const RunCtl *ctl, const FusedArgs *ap, const float *no
     auto rows_of = [&](int64_t tile) { const int64_t r = V - tile * TR; return (int)(r < TR ? r : TR); };
     if (t0 < t1) wload<E, HEAD_P>(A, a.m.output.q, a.m.output.d, rows_of(t0), [&](int rl) { return t0 * TR + rl; });
     const W8 nw = wload8(norm_w);
+    wait_vm<5>();   // about half of the 11 loads above
+    const XR xr = make_xr(a.xbase, a.xbytes);
     if (!prologue<NL>(nl, c.ctl, nullptr, nullptr, a.xc.x + (size_t)c.par() * NL * E, c.tag(k - 1, PH_DOWN), c.err, nw, a.m.eps,
-                      s.xf, &s.xq[0][0], E, &s.xd[0][0], E / 32, s.ns, s.xn, &c.ps->fail))
+                      s.xf, &s.xq[0][0], E, &s.xd[0][0], E / 32, s.ns, s.xn, &c.ps->fail, &xr))
         return false;
     tr_pass(c);
     if (c.b == 0) {
@@ -1669,14 +1994,25 @@ FZ_PHASE bool phase_head(const RunCtl *ctl, const FusedArgs *ap, const float *no
     return true;
 }
 
-// layer il as run layer k (embed: its input is the token embedding)
+// One call per layer boundary: the MoE tail (experts, down) of layer ilp as run layer kp (ilp >= 0),
+// then the projection, mixer, output and router phases of layer il as run layer k (il >= 0; embed:
+// its input is the token embedding). The call boundary sits between the router and experts phases,
+// so the down phase can load the next layer's projection slice into registers.
 template <int NL>
-OXE_DEV bool run_layer(const RunCtl *ctl, const FusedArgs *ap, int il, int k, bool embed, uint32_t base) {
+__device__ __attribute__((noinline)) bool run_step(const RunCtl *ctl, const FusedArgs *ap, int ilp, int kp, int il, int k,
+                                                   bool embed, uint32_t base) {
+    ProjPre pre;
+    if (ilp >= 0 && !phase_moe<NL>(ctl, ap, ilp, kp, il, pre)) return false;
+    if (il < 0) return true;
     const LayerDev &L = ap->layers[il];
     const int att = L.att;
     // the residual: the embedding (written by the projection phase) or the previous layer's output
     const uint32_t xtag = base + 1u + (embed ? 8u * (uint32_t)k + PH_PROJ : 8u * (uint32_t)(k - 1) + PH_DOWN);
-    if (!phase_proj<NL>(ctl, ap, il, k, embed, 0, att ? AT_ROWS : DN_ROWS)) return false;
+#ifndef FZ_NO_PREFETCH
+    if (!phase_proj<NL>(ctl, ap, il, k, embed, 0, att ? AT_ROWS : DN_ROWS, pre, ilp >= 0)) return false;
+#else
+    if (!phase_proj<NL>(ctl, ap, il, k, embed, 0, att ? AT_ROWS : DN_ROWS, pre, false)) return false;
+#endif
     if (!att) {
         if (!phase_dn<NL>(ctl, ap, il, k)) return false;
     } else {
@@ -1685,7 +2021,6 @@ OXE_DEV bool run_layer(const RunCtl *ctl, const FusedArgs *ap, int il, int k, bo
     }
     if (!phase_out<NL>(ctl, ap, il, k, xtag)) return false;
     if (!phase_router<NL>(ctl, ap, il, k)) return false;
-    if (!phase_moe<NL>(ctl, ap, il, k)) return false;
     return true;
 }
 
@@ -1693,19 +2028,21 @@ template <int NL>
 OXE_DEV void run_all(const RunCtl *ctl, const FusedArgs *ap, uint32_t base) {
     const int mode = ap->mode, nlay = ap->n_layer;
     if (mode == FM_VERIFY) {
-        for (int il = 0; il < nlay; il++)
-            if (!run_layer<NL>(ctl, ap, il, il, il == 0, base)) return;
+        for (int il = 0; il <= nlay; il++)
+            if (!run_step<NL>(ctl, ap, il - 1, il - 1, il < nlay ? il : -1, il, il == 0, base)) return;
         (void)phase_head<NL>(ctl, ap, ap->m.out_norm, nlay);
     } else if (mode == FM_DRAFT) {
         const int il = nlay;
         if (!phase_entry<NL>(ctl, ap, il)) return;
         // the MTP layer (attention) as run layer 1, its input the entry output
-        if (!run_layer<NL>(ctl, ap, il, 1, false, base)) return;
+        if (!run_step<NL>(ctl, ap, -1, 0, il, 1, false, base)) return;
+        if (!run_step<NL>(ctl, ap, il, 1, -1, 2, false, base)) return;
         (void)phase_head<NL>(ctl, ap, ap->layers[il].head_norm, 2);
     } else {
         const int il = nlay;
         if (!phase_entry<NL>(ctl, ap, il)) return;
-        if (!phase_proj<NL>(ctl, ap, il, 1, false, AT_K, AT_ROWS)) return;
+        ProjPre pre;
+        if (!phase_proj<NL>(ctl, ap, il, 1, false, AT_K, AT_ROWS, pre, false)) return;
         (void)phase_scores<NL>(ctl, ap, il, 1, true);
     }
 }

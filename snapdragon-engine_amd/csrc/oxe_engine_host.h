@@ -332,6 +332,7 @@ struct Engine {
             off[i] = tot;
             tot += (xw[i] + 31) / 32 * 32;   // 256-byte aligned parts
         }
+        if (tot * 8 > 0x7fffffffull) return;   // buffer offsets are 31-bit
         fz_xch = alloc<uint64_t>(tot);
         fz_xch_words = tot;
         FzXch xc;
@@ -369,6 +370,8 @@ struct Engine {
             f.b = b;
             f.sync = fz_sync;
             f.xc = xc;
+            f.xbase = fz_xch;
+            f.xbytes = (uint32_t)(fz_xch_words * 8);
             f.keys = fz_keys;
         }
         (void)hipMemsetAsync(fz_sync, 0, FZ_SYNC_WORDS * 4, st);
@@ -422,14 +425,21 @@ struct Engine {
     // move the tag base on, and report
     int fused_check() {
         if (!fused) return 0;
-        uint32_t err = 0;
-        if (hipMemcpyAsync(&err, fz_sync + FZ_W_ERR, 4, hipMemcpyDeviceToHost, st) != hipSuccess) return -2;
+        uint32_t err[5] = {0, 0, 0, 0, 0};
+        if (hipMemcpyAsync(err, fz_sync + FZ_W_ERR, sizeof(err), hipMemcpyDeviceToHost, st) != hipSuccess) return -2;
         if (hipStreamSynchronize(st) != hipSuccess) return -2;
-        if (err) {
+        if (err[0]) {
             launch_fused_sync_reset(fz_sync, st);
             (void)hipStreamSynchronize(st);
             fz_account(1);
-            set_err("fused run aborted: an exchange poll timed out (sync words reset)");
+            // the word that timed out: its byte offset in the exchange allocation, the tags
+            const int64_t off = (int64_t)(uint32_t)(err[3] - (uint32_t)(uintptr_t)fz_xch);
+            char msg[256];
+            snprintf(msg, sizeof msg,
+                     "fused run aborted: an exchange poll timed out (workgroup %u, byte offset %lld, tag %u expected, "
+                     "%u seen; sync words reset)",
+                     err[4], (long long)off, err[1], err[2]);
+            set_err(msg);
             return -4;
         }
         return 0;

@@ -68,6 +68,8 @@ struct FusedArgs {
     ActBufs b;
     uint32_t *sync;                // [FZ_SYNC_WORDS]
     FzXch xc;                      // tagged exchange buffers
+    const uint64_t *xbase;         // the one allocation holding every exchange buffer, and its size
+    uint32_t xbytes;
     unsigned long long *keys;      // [NL][grid] per-workgroup argmax keys of the LM head
     unsigned long long *trace;     // optional [grid][FZ_TRACE_EV][4]: phase id, start, barrier passed, end
 };

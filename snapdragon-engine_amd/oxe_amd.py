@@ -130,7 +130,8 @@ def _stream():
 
 def check(rc, what):
     if rc != 0:
-        raise RuntimeError(f"{what} failed with status {rc}")
+        msg = _last_error()
+        raise RuntimeError(f"{what} failed with status {rc}" + (f": {msg}" if msg else ""))
 
 
 # ---- kernel-level entry points (torch tensors on cuda)

@@ -2,9 +2,11 @@
 
 Builds the 35B-A3B-shaped synthetic model on the GPU, prefills the bench prompt, turns the fused
 kernel's phase trace on, runs host-driven 2-lane verify steps and prints, per phase kind, the mean
-time from the barrier release (first workgroup to pass) to the last workgroup done, the gap before
-it (previous phase done to this release) and the median sub-step marks. Times from the device wall
-clock (100 MHz); "pass skew" is the time from the first to the last workgroup passing the barrier.
+time from the first workgroup to receive its inputs to the last workgroup done, the gap before it
+(previous phase done to that first arrival), per workgroup the wait for inputs and the work after
+them, the median sub-step marks, and the timeline of one DN and one attention layer. Times from the
+device wall clock (100 MHz); "pass skew" is the time from the first to the last workgroup to receive
+its inputs.
 
     python snapdragon-engine_amd/phase_trace.py [--prompt 512] [--steps 3]
 """
@@ -24,8 +26,8 @@ PHASES = {1: "proj", 2: "dn", 3: "scores", 4: "pv", 5: "out", 6: "router", 7: "e
           10: "head"}
 MARKS = {101: "experts: union", 102: "experts: gate/up loads issued", 103: "experts: issue drained",
          104: "experts: gate/up dot", 105: "experts: logits load", 106: "experts: route_wave",
-         111: "proj: norm prologue", 112: "proj: dot", 121: "dn: conv", 122: "dn: norms + gates",
-         123: "dn: delta rule", 131: "router: norm prologue", 132: "router: f32 dots", 141: "pv: V tile to LDS",
+         111: "proj: norm prologue", 113: "proj: int dots", 112: "proj: chains", 171: "out: int dots", 172: "out: chains", 121: "dn: conv", 122: "dn: norms + gates",
+         123: "dn: delta rule", 124: "dn: head leader inputs", 125: "dn: head leader norm + store", 131: "router: norm prologue", 132: "router: f32 dots", 141: "pv: V tile to LDS",
          142: "pv: V.p + reduce", 143: "pv: scores load + max", 144: "pv: exp, sum, probabilities", 151: "scores: q/k prologue",
          161: "down: inputs", 162: "down: block dots", 163: "down: chains"}
 
@@ -57,7 +59,27 @@ def analyse(tr):
         ev = tr[g][tr[g, :, 0] >= 100].astype(np.int64)
         for e in ev:
             marks.setdefault(int(e[0]), []).append((e[3] - e[1]) / 100.0)
-    return total, agg, marks
+    # per workgroup: start -> inputs arrived ("wait") and inputs arrived -> end ("work")
+    for k in range(n):
+        name = PHASES.get(int(ids[k]), str(int(ids[k])))
+        a = agg[name]
+        if len(a) == 4:
+            a += [[], []]
+        a[4].append(np.median(pas[:, k] - start[:, k]) / 100.0)
+        a[5].append(np.median(end[:, k] - pas[:, k]) / 100.0)
+    return total, agg, marks, (ids, start, pas, end)
+
+
+def timeline(ids, start, pas, end, k0, k1):
+    """Rows (phase, start, pass, end) as min / median / max over workgroups, us from event k0's
+    earliest start, for events [k0, k1)."""
+    t0 = start[:, k0].min()
+    rows = []
+    for k in range(k0, k1):
+        name = PHASES.get(int(ids[k]), str(int(ids[k])))
+        q = [np.percentile((v[:, k] - t0) / 100.0, (0, 50, 100)) for v in (start, pas, end)]
+        rows.append((name, q))
+    return rows
 
 
 def main():
@@ -75,12 +97,25 @@ def main():
         g = e.verify([x, (x + 1) % d.n_vocab])
         e.commit(1)
         x = int(g[0])
-    total, agg, marks = analyse(e.read_trace())
+    total, agg, marks, ev = analyse(e.read_trace())
     print(f"verify run (2 lanes, 40 layers + LM head) at position {e.pos}: {total:.1f} us")
     print(f"{'phase':10s} {'count':>5s} {'release->done us':>17s} {'gap before us':>14s} {'pass skew us':>13s} "
-          f"{'total us':>9s}")
-    for name, (cnt, dur, gap, skew) in agg.items():
-        print(f"{name:10s} {cnt:5d} {dur / cnt:17.2f} {gap / cnt:14.2f} {skew / cnt:13.2f} {dur + gap:9.1f}")
+          f"{'total us':>9s} {'wait med':>9s} {'work med':>9s}")
+    for name, (cnt, dur, gap, skew, wt, wk) in agg.items():
+        print(f"{name:10s} {cnt:5d} {dur / cnt:17.2f} {gap / cnt:14.2f} {skew / cnt:13.2f} {dur + gap:9.1f} "
+              f"{np.mean(wt):9.2f} {np.mean(wk):9.2f}")
+    ids = ev[0]
+    # one DN layer and one attention layer in the middle of the run: start / inputs / end per phase
+    for want in (2, 3):
+        ks = [k for k in range(len(ids)) if ids[k] == want]
+        if len(ks) < 2:
+            continue
+        k0 = ks[len(ks) // 2] - 1
+        k1 = min(k0 + 6, len(ids))
+        print(f"timeline of one {'DN' if want == 2 else 'attention'} layer (us; min / median / max over workgroups):")
+        for name, q in timeline(*ev, k0, k1):
+            print(f"  {name:8s} start {q[0][0]:6.2f} {q[0][1]:6.2f} {q[0][2]:6.2f} | inputs {q[1][0]:6.2f} {q[1][1]:6.2f} "
+                  f"{q[1][2]:6.2f} | end {q[2][0]:6.2f} {q[2][1]:6.2f} {q[2][2]:6.2f}")
     print("sub-steps (median over workgroups and layers, us):")
     for i in sorted(marks):
         v = np.array(marks[i])
