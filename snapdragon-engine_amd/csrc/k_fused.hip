@@ -57,6 +57,18 @@ OXE_DEV T gld(const T *p) {
     using R = typename RawOf<sizeof(T)>::T;
     return __builtin_bit_cast(T, *(const FZ_GAS R *)p);
 }
+// streamed once per run (weights, cache rows): a non-temporal load. Measured on MI355X: 256
+// workgroups each reading 136 KB never read before take 14 us with plain loads and 6.5 us with
+// non-temporal ones (the L2 does not allocate the lines).
+template <class T>
+OXE_DEV T gldn(const T *p) {
+    using R = typename RawOf<sizeof(T)>::T;
+#ifdef FZ_NO_NT
+    return __builtin_bit_cast(T, *(const FZ_GAS R *)p);
+#else
+    return __builtin_bit_cast(T, __builtin_nontemporal_load((const FZ_GAS R *)p));
+#endif
+}
 template <class T>
 OXE_DEV const FZ_CAS T *uni(const T *p) {
     const uint64_t v = (uint64_t)p;
@@ -265,11 +277,11 @@ OXE_DEV void wload_part(WSlice<K, MAXP> &s, const int8_t *__restrict__ wq, const
 #pragma unroll
     for (int p = P0; p < P1; p++) {
         const int rl = p * G::RPP + rs;
-        s.w[p] = gld((const uint4 *)(wq + rowof(rl < nr ? rl : nr - 1) * K + c * 16));
+        s.w[p] = gldn((const uint4 *)(wq + rowof(rl < nr ? rl : nr - 1) * K + c * 16));
     }
     if (SC) {
         const int sr = t / G::SPR, sk = t % G::SPR;
-        s.s = gld((const uint4 *)(wd + rowof(sr < nr ? sr : nr - 1) * G::NB + sk * 8));
+        s.s = gldn((const uint4 *)(wd + rowof(sr < nr ? sr : nr - 1) * G::NB + sk * 8));
     }
 }
 
@@ -285,10 +297,10 @@ OXE_DEV void wload(WSlice<K, MAXP> &s, const int8_t *__restrict__ wq, const uint
 #pragma unroll
     for (int p = 0; p < MAXP; p++) {
         const int rl = p * G::RPP + rs;
-        s.w[p] = gld((const uint4 *)(wq + rowof(rl < nr ? rl : nr - 1) * K + c * 16));
+        s.w[p] = gldn((const uint4 *)(wq + rowof(rl < nr ? rl : nr - 1) * K + c * 16));
     }
     const int sr = t / G::SPR, sk = t % G::SPR;
-    s.s = gld((const uint4 *)(wd + rowof(sr < nr ? sr : nr - 1) * G::NB + sk * 8));
+    s.s = gldn((const uint4 *)(wd + rowof(sr < nr ? sr : nr - 1) * G::NB + sk * 8));
 }
 
 // g.out[l][r] = row r . lane l for the slice's nr rows (activation codes xq [NL][xq_ld] and scales
@@ -1102,9 +1114,9 @@ FZ_PHASE bool phase_router(const RunCtl *ctl, const FusedArgs *ap, int il, int k
     const bool shg = b == c.G - 1;
     const bool gu = b < 2 * FFSH / 8;   // 128 half tiles
     const int tile = b >> 1, hf = b & 1;
-    const float4 wrow = gld((const float4 *)(L.router + (int64_t)b * E + 4 * t));
+    const float4 wrow = gldn((const float4 *)(L.router + (int64_t)b * E + 4 * t));
     float4 wsg = make_float4(0, 0, 0, 0);
-    if (shg) wsg = gld((const float4 *)(L.shexp_gate + 4 * t));
+    if (shg) wsg = gldn((const float4 *)(L.shexp_gate + 4 * t));
     WSlice<E, 2> ws;
     auto rowof = [&](int rl) { return (int64_t)(tile * 16 + (rl < 4 ? hf * 4 + rl : 8 + hf * 4 + (rl - 4))); };
     wload<E, 2>(ws, L.shexp_gu.q, L.shexp_gu.d, gu ? 8 : 0, rowof);
@@ -1144,29 +1156,34 @@ FZ_PHASE bool phase_router(const RunCtl *ctl, const FusedArgs *ap, int il, int k
             }
         }
     }
-    __syncthreads();
-    if (t < 64) {
-        const int l = (t >> 4) & 1, cc = t & 15;
-        const bool sgd = t >= 32;
-        const float *wv = sgd ? s.sg[cc] : s.w[cc];
-        const float *xv = s.xc[l][cc];
-        float acc = 0.0f;
-        if (!sgd || shg) {
+    // f32 dots on wave 0 (measured: on a wave of their own beside the shared gate/up GEMV's chains,
+    // the phase is no faster)
+    auto f32_dots = [&]() {
+        if (t < 64) {
+            const int tw = t, l = (tw >> 4) & 1, cc = tw & 15;
+            const bool sgd = tw >= 32;
+            const float *wv = sgd ? s.sg[cc] : s.w[cc];
+            const float *xv = s.xc[l][cc];
+            float acc = 0.0f;
+            if (!sgd || shg) {
 #pragma unroll 4
-            for (int q = 0; q < E / 16; q += 4) {
-                const float4 w4 = *(const float4 *)(wv + q), x4 = *(const float4 *)(xv + q);
-                acc = __builtin_fmaf(w4.x, x4.x, acc);
-                acc = __builtin_fmaf(w4.y, x4.y, acc);
-                acc = __builtin_fmaf(w4.z, x4.z, acc);
-                acc = __builtin_fmaf(w4.w, x4.w, acc);
+                for (int q = 0; q < E / 16; q += 4) {
+                    const float4 w4 = *(const float4 *)(wv + q), x4 = *(const float4 *)(xv + q);
+                    acc = __builtin_fmaf(w4.x, x4.x, acc);
+                    acc = __builtin_fmaf(w4.y, x4.y, acc);
+                    acc = __builtin_fmaf(w4.z, x4.z, acc);
+                    acc = __builtin_fmaf(w4.w, x4.w, acc);
+                }
+            }
+            const float v = dot16_tree_f(acc);
+            if (cc == 0 && l < c.nl) {
+                if (!sgd) ll_stf(a.xc.lg + ((size_t)c.par() * NL + l) * NEXP + b, v, c.tag(k, PH_ROUTER));
+                else if (shg) ll_stf(a.xc.sg + (size_t)c.par() * NL + l, sigmoid_c(v), c.tag(k, PH_ROUTER));
             }
         }
-        const float v = dot16_tree_f(acc);
-        if (cc == 0 && l < c.nl) {
-            if (!sgd) ll_stf(a.xc.lg + ((size_t)c.par() * NL + l) * NEXP + b, v, c.tag(k, PH_ROUTER));
-            else if (shg) ll_stf(a.xc.sg + (size_t)c.par() * NL + l, sigmoid_c(v), c.tag(k, PH_ROUTER));
-        }
-    }
+    };
+    __syncthreads();
+    f32_dots();
     tr_mark(c, 132);
     if (gu) {
         wdot<E, 2, NL>(ws, 8, &s.xq[0][0], E, &s.xd[0][0], E / 32, s.g);
@@ -1210,6 +1227,20 @@ FZ_PHASE bool phase_moe(const RunCtl *ctl, const FusedArgs *ap, int il, int k, i
     if (!all_ok(ok, &ps.fail)) return false;
     tr_pass(c);
     tr_mark(c, 105);
+    // the first part of the next layer's projection slice streams while the routing computes (the
+    // memory pipeline is otherwise idle until the experts are known)
+#ifndef FZ_NO_PREFETCH
+    const bool pf = il_next >= 0;
+#else
+    const bool pf = false;
+#endif
+    const FZ_CAS LayerDev &Ln = layer_of(c, pf ? il_next : il);
+    const int pre_rows = proj_rows(Ln);
+#ifdef FZ_PREFETCH_ONCE
+    if (pf) proj_load(Ln, b, c.G, 0, pre_rows, pp);
+#elif defined(FZ_PF_IN_ROUTING)
+    if (pf) proj_load_part<0>(Ln, b, c.G, 0, pre_rows, pp);
+#endif
     if ((t >> 6) < nl) route_wave(se.lg[t >> 6], t >> 6, ps.ro);
     __syncthreads();
     tr_mark(c, 106);
@@ -1261,7 +1292,7 @@ FZ_PHASE bool phase_moe(const RunCtl *ctl, const FusedArgs *ap, int il, int k, i
     };
     uint4 dw[9];
     auto dload = [&](int q) {
-        dw[q] = gld((const uint4 *)(unit_q(2 * q + uh) + (int64_t)(r0 + rr) * FF + 16 * ck));
+        dw[q] = gldn((const uint4 *)(unit_q(2 * q + uh) + (int64_t)(r0 + rr) * FF + 16 * ck));
     };
     const int su = t / 16 < DW_UNITS ? t / 16 : OXE_MAX_UNION, srr = (t % 16) / 2, shf = t % 2;
     uint4 dsc;
@@ -1269,7 +1300,7 @@ FZ_PHASE bool phase_moe(const RunCtl *ctl, const FusedArgs *ap, int il, int k, i
         int e = ps.uni[su < OXE_MAX_UNION ? su : 0];
         e = e < 0 ? 0 : (e >= NEXP ? NEXP - 1 : e);
         const uint16_t *base = su < nu && su < OXE_MAX_UNION ? L.exp_down.d + (int64_t)e * E * (FF / 32) : L.shexp_down.d;
-        dsc = gld((const uint4 *)(base + (int64_t)(r0 + srr) * (FF / 32) + shf * 8));
+        dsc = gldn((const uint4 *)(base + (int64_t)(r0 + srr) * (FF / 32) + shf * 8));
     };
 #ifndef FZ_DW_EARLY
 #define FZ_DW_EARLY 0
@@ -1348,16 +1379,7 @@ FZ_PHASE bool phase_moe(const RunCtl *ctl, const FusedArgs *ap, int il, int k, i
     const float x1v = u2f(u[NHW + 1 + NL]), sgv = u2f(u[NHW + 2 + NL]);
 #pragma unroll
     for (int q = DW_PRE; q < 9; q++) dload(q);
-#ifndef FZ_NO_PREFETCH
-    const bool pf = il_next >= 0;
-#else
-    const bool pf = false;
-#endif
-    const FZ_CAS LayerDev &Ln = layer_of(c, pf ? il_next : il);
-    const int pre_rows = proj_rows(Ln);
-#ifdef FZ_PREFETCH_ONCE
-    if (pf) proj_load(Ln, b, c.G, 0, pre_rows, pp);
-#else
+#if !defined(FZ_PREFETCH_ONCE) && !defined(FZ_PF_IN_ROUTING)
     if (pf) proj_load_part<0>(Ln, b, c.G, 0, pre_rows, pp);
 #endif
     // Q8_0 of the shared expert's h: element t of lane l in thread t, a block per half wave
@@ -1489,7 +1511,7 @@ FZ_PHASE bool phase_scores(const RunCtl *ctl, const FusedArgs *ap, int il, int k
     const uint16_t *kcl = kcache_layer(a, L) + (int64_t)kvh * a.m.n_ctx * HD;
     const int kp = t >> 5, kpart = t & 31;
     uint4 kpre = make_uint4(0, 0, 0, 0);
-    if (act && !seed_only && chunk0 * SC_P + kp < pos0) kpre = gld((const uint4 *)(kcl + (int64_t)(chunk0 * SC_P + kp) * HD + 8 * kpart));
+    if (act && !seed_only && chunk0 * SC_P + kp < pos0) kpre = gldn((const uint4 *)(kcl + (int64_t)(chunk0 * SC_P + kp) * HD + 8 * kpart));
     // per wave, its vectors' norm weights and RoPE rows (read-only), before the barrier
     const int kjob = w;                          // waves 0..NL-1: K row of lane w
     const int pk = pos0 + kjob;
@@ -1584,7 +1606,7 @@ FZ_PHASE bool phase_scores(const RunCtl *ctl, const FusedArgs *ap, int il, int k
             if (chunk == chunk0) {
                 if (cb + kp < pos0) *(uint4 *)&s.krows[kp][8 * kpart] = kpre;
             } else if (cb + kp < pos0) {
-                *(uint4 *)&s.krows[kp][8 * kpart] = gld((const uint4 *)(kcl + (int64_t)(cb + kp) * HD + 8 * kpart));
+                *(uint4 *)&s.krows[kp][8 * kpart] = gldn((const uint4 *)(kcl + (int64_t)(cb + kp) * HD + 8 * kpart));
             }
             __syncthreads();
             const int p = cb + pp;
@@ -1672,7 +1694,7 @@ FZ_PHASE bool phase_pv(const RunCtl *ctl, const FusedArgs *ap, int il, int k) {
 #pragma unroll
     for (int q = 0; q < PV_VK; q++) {
         const int i = t + FT * q, r = i / nvc, ch = i % nvc;
-        vpre[q] = (act && i < PVD * nvc) ? gld((const uint4 *)(vt + (int64_t)r * n_ctx + 8 * ch)) : make_uint4(0, 0, 0, 0);
+        vpre[q] = (act && i < PVD * nvc) ? gldn((const uint4 *)(vt + (int64_t)r * n_ctx + 8 * ch)) : make_uint4(0, 0, 0, 0);
     }
     const uint64_t *pin = a.xc.p + (size_t)c.par() * NL * DN_ROWS;
     const uint32_t tp = c.tag(k, PH_PROJ), ts = c.tag(k, PH_MIX);
@@ -1837,7 +1859,7 @@ FZ_PHASE bool phase_pv(const RunCtl *ctl, const FusedArgs *ap, int il, int k) {
         }
         for (int i = t + FT * PV_VK; i < PVD * nvc; i += FT) {
             const int r = i / nvc, ch = i % nvc;
-            *(uint4 *)(s_v + r * vs + 8 * ch) = gld((const uint4 *)(vt + (int64_t)r * n_ctx + 8 * ch));
+            *(uint4 *)(s_v + r * vs + 8 * ch) = gldn((const uint4 *)(vt + (int64_t)r * n_ctx + 8 * ch));
         }
         if (cp == 0) sg = sigmoid_c(sg);
         __syncthreads();
@@ -1857,7 +1879,7 @@ FZ_PHASE bool phase_pv(const RunCtl *ctl, const FusedArgs *ap, int il, int k) {
             acc = __builtin_elementwise_fma(u2h2f(*(const uint32_t *)(vrow + 32 * s)), u2h2f(prow[32 * s]), acc);
         for (int s = nss; s < ns; s++) {
             const int p0 = 32 * s + 2 * cp;
-            uint32_t vw = gld((const uint32_t *)(vt + (int64_t)d * n_ctx + p0));
+            uint32_t vw = gldn((const uint32_t *)(vt + (int64_t)d * n_ctx + p0));
             // this run's positions from the projection outputs
             if (p0 >= pos0 && p0 < pos0 + nl) vw = (vw & 0xffff0000u) | s_vn[(p0 - pos0) * PVD + d];
             if (p0 + 1 >= pos0 && p0 + 1 < pos0 + nl) vw = (vw & 0xffffu) | ((uint32_t)s_vn[(p0 + 1 - pos0) * PVD + d] << 16);
