@@ -318,6 +318,8 @@ OXE_DEV void wdot(const WSlice<K, MAXP> &s, int nr, const int8_t *xq, int xq_ld,
     uint4 xa[NL];
 #pragma unroll
     for (int l = 0; l < NL; l++) xa[l] = *(const uint4 *)(xq + l * xq_ld + c * 16);
+    // branch-free, so the independent dots interleave: both lanes of a pair hold the block's sum and
+    // store it to the same word; rows past nr (< MAXP * RPP, inside g) get values nobody reads
 #pragma unroll
     for (int p = 0; p < MAXP; p++) {
         const int rl = p * G::RPP + rs;
@@ -325,7 +327,7 @@ OXE_DEV void wdot(const WSlice<K, MAXP> &s, int nr, const int8_t *xq, int xq_ld,
         for (int l = 0; l < NL; l++) {
             int32_t v = dot16(s.w[p], xa[l], 0);
             v += dpp_i<DPP_XOR1>(v);  // the other half of the 32-code block sits in the adjacent lane
-            if ((c & 1) == 0 && rl < nr) g.f[l][rl][c >> 1] = (float)v;
+            g.f[l][rl][c >> 1] = (float)v;
         }
     }
     {
@@ -370,6 +372,7 @@ OXE_DEV void wdot(const WSlice<K, MAXP> &s, int nr, const int8_t *xq, int xq_ld,
 struct NormSm {
     double red[2][4];
     float bc[2];
+    double part[2][FT / 64];   // per-wave partial sums of squares of each lane (gathered inputs)
 };
 
 // v: this thread's 8 elements; xs: the lane's whole vector in LDS (sequential replay); wv8: this
@@ -464,25 +467,57 @@ OXE_DEV bool prologue(int nl, const FZ_CAS RunCtl *ctl, const int8_t *eq, const 
             for (int i = 0; i < 8; i++) v[i] = 0.0f;
         if (l < NL) put8(&xf[l][8 * tt], v);
         __syncthreads();
+        norm8(v, xf[l < NL ? l : 0], w.v, eps, ns);
     } else {
-        static_assert(NL * E == 8 * FT, "8 words per thread");
-        // word 2 (t + FT m) + h is u[2 m + h]
+        static_assert(NL * E == 8 * FT && NL == 2, "8 words per thread, 4 of each lane");
+        // word 2 (t + FT m) + h is u[2 m + h]: m < 2 are lane 0's, m >= 2 lane 1's
         auto wi = [&](int j) { return 2 * (t + FT * (j / 2)) + (j & 1); };
         uint32_t u[8];
         ok = ll_gather<8, 4, SENT>([&](int j) { return LLW{src + wi(j), tag, wi(j) / E < nl}; }, u, err, xr);
+        // the exact parallel sum of squares (any order: the bracket below decides) from the
+        // gathered words; the abort flag and the per-wave partials share one barrier
+        double q[2] = {0.0, 0.0};
 #pragma unroll
         for (int j = 0; j < 8; j++) {
             const int i = wi(j);
-            xf[i / E][i % E] = i / E < nl ? u2f(u[j]) : 0.0f;
+            const float x = i / E < nl ? u2f(u[j]) : 0.0f;
+            xf[i / E][i % E] = x;
+            q[j / 4] += (double)(x * x);
         }
-        if (!all_ok(ok, s_ok)) return false;
+        const double p0 = wave_sum_d_any(q[0]), p1 = wave_sum_d_any(q[1]);
+        if (!ok) *s_ok = 1;
+        if ((t & 63) == 0) { ns.part[0][t >> 6] = p0; ns.part[1][t >> 6] = p1; }
+        __syncthreads();
+        // no thread writes the sticky flag again before the barrier at the end of this prologue
+        if (*s_ok != 0) return false;
         mid();   // inputs arrived
+        float mean[2];
+        bool replay = false;
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            double P = 0.0;
+#pragma unroll
+            for (int i = 0; i < FT / 64; i++) P += ns.part[h][i];
+            replay |= !bracket_ok_mean(P, P, E, (double)E, &mean[h]);
+        }
+        if (replay) {   // uniform: every thread tested both lanes
+            if (tt == 0 && l < NL) {
+                double sq = 0.0;
+                for (int i = 0; i < E; i++) sq += (double)(xf[l][i] * xf[l][i]);
+                ns.bc[l] = (float)(sq / (double)E);
+            }
+            __syncthreads();
+#pragma unroll
+            for (int h = 0; h < 2; h++) mean[h] = ns.bc[h];
+        }
         if (l < NL) get8(&xf[l][8 * tt], v);
         else
 #pragma unroll
             for (int i = 0; i < 8; i++) v[i] = 0.0f;
+        const float scale = 1.0f / sqrtf((l == 1 ? mean[1] : mean[0]) + eps);
+#pragma unroll
+        for (int i = 0; i < 8; i++) v[i] = (v[i] * scale) * w.v[i];
     }
-    norm8(v, xf[l < NL ? l : 0], w.v, eps, ns);
     if (l < NL) {
         if (act) {
             quant8(v, xq + l * xq_ld + 8 * tt, xd + l * xd_ld + (8 * tt) / 32);
@@ -601,6 +636,7 @@ struct Persist {
     uint32_t base;                   // tag base of the launch
     uint32_t tev;                    // trace: next event index of this workgroup
     uint32_t dyn_off;                // LDS offset of the dynamic LDS (fz_dyn), set by the kernel
+    uint64_t exp2tab[32];            // the C-library expf's table (oxe_libm), read from LDS by the gates
     unsigned long long t_start, t_pass, t_mark;
 };
 
@@ -611,6 +647,9 @@ extern __shared__ __align__(16) unsigned char fz_dyn[];
 __shared__ fz::Persist<OXE_NL> fz_ps;
 
 namespace fz {
+
+// the expf table's LDS copy as an LDS-space pointer (its reads compile to LDS loads)
+OXE_DEV const FZ_LDS uint64_t *exp_tab() { return (const FZ_LDS uint64_t *)&fz_ps.exp2tab[0]; }
 
 template <int NL>
 struct Ctx {
@@ -890,13 +929,13 @@ FZ_PHASE bool phase_dn(const RunCtl *ctl, const FusedArgs *ap, int il, int k) {
                 else s.v[l][t - 2 * DS] = y;
             }
         }
-        if (gate && gl < nl) {
-            s.g[gl] = oxe_libm::expf_c(softplus_c(ga + dtb) * sa);
-            s.b[gl] = sigmoid_c(gb);
-        }
         __syncthreads();
         tr_mark(c, 121);
-        // l2 norms of q (wave 2 l) and k (wave 2 l + 1)
+        // the gates (wave 5) beside the l2 norms of q (wave 2 l) and k (wave 2 l + 1)
+        if (gate && gl < nl) {
+            s.g[gl] = oxe_libm::expf_t(softplus_t(ga + dtb, exp_tab()) * sa, exp_tab());
+            s.b[gl] = sigmoid_t(gb, exp_tab());
+        }
         if (w < 2 * NL && (w >> 1) < nl) {
             const int l = w >> 1;
             float *xv = (w & 1) ? s.k[l] : s.q[l];
@@ -1178,7 +1217,7 @@ FZ_PHASE bool phase_router(const RunCtl *ctl, const FusedArgs *ap, int il, int k
             const float v = dot16_tree_f(acc);
             if (cc == 0 && l < c.nl) {
                 if (!sgd) ll_stf(a.xc.lg + ((size_t)c.par() * NL + l) * NEXP + b, v, c.tag(k, PH_ROUTER));
-                else if (shg) ll_stf(a.xc.sg + (size_t)c.par() * NL + l, sigmoid_c(v), c.tag(k, PH_ROUTER));
+                else if (shg) ll_stf(a.xc.sg + (size_t)c.par() * NL + l, sigmoid_t(v, exp_tab()), c.tag(k, PH_ROUTER));
             }
         }
     };
@@ -1416,16 +1455,19 @@ FZ_PHASE bool phase_moe(const RunCtl *ctl, const FusedArgs *ap, int il, int k, i
             *(float4 *)&sd.d[su][l][srr][8 * shf + 4] = make_float4(dv[4], dv[5], dv[6], dv[7]);
         }
     }
+    // branch-free but for the one unit slot past DW_UNITS (uniform per wave), so the dots interleave:
+    // units past the union dot zeros with the shared expert's rows (never read); both lanes of a pair
+    // hold the block's sum and store it to the same word
 #pragma unroll
     for (int q = 0; q < 9; q++) {
         const int u = 2 * q + uh;
-        if (u < DW_UNITS && (u == OXE_MAX_UNION || u < nu)) {   // uniform within each wave
+        if (2 * q + 1 < DW_UNITS || u < DW_UNITS) {
 #pragma unroll
             for (int l = 0; l < NL; l++) {
                 const uint4 xa = *(const uint4 *)&sd.hq[l][u][16 * ck];
                 int32_t v = dot16(dw[q], xa, 0);
                 v += dpp_i<DPP_XOR1>(v);
-                if ((ck & 1) == 0) sd.f[u][l][rr][ck >> 1] = (float)v;
+                sd.f[u][l][rr][ck >> 1] = (float)v;
             }
         }
     }
@@ -1861,7 +1903,7 @@ FZ_PHASE bool phase_pv(const RunCtl *ctl, const FusedArgs *ap, int il, int k) {
             const int r = i / nvc, ch = i % nvc;
             *(uint4 *)(s_v + r * vs + 8 * ch) = gldn((const uint4 *)(vt + (int64_t)r * n_ctx + 8 * ch));
         }
-        if (cp == 0) sg = sigmoid_c(sg);
+        if (cp == 0) sg = sigmoid_t(sg, exp_tab());
         __syncthreads();
         if (t < NL * PVD) {
             const int vl = t / PVD, vd = t % PVD;
@@ -2081,6 +2123,7 @@ __global__ __launch_bounds__(fz::FT, 1) void fused_kernel(const RunCtl *__restri
         fz_ps.tev = 0;
         fz_ps.dyn_off = (uint32_t)(uintptr_t)(FZ_LDS unsigned char *)fz_dyn;
     }
+    if (threadIdx.x < 32) fz_ps.exp2tab[threadIdx.x] = oxe_libm::kExp2fTab[threadIdx.x];
     __syncthreads();
     const uint32_t base = (uint32_t)__builtin_amdgcn_readfirstlane((int)fz_ps.base);
     run_all<NL>(ctl, ap, base);

@@ -124,6 +124,11 @@ OXE_DEV float v_silu(float x) { return x / (1.0f + v_expf(0.0f - x)); }
 OXE_DEV float sigmoid_c(float x) { return 1.f / (1.f + oxe_libm::expf_c(-x)); }
 // op_softplus (oxe_ops.cpp:85-89)
 OXE_DEV float softplus_c(float x) { return (x > 20.0f) ? x : oxe_libm::log1pf_c(oxe_libm::expf_c(x)); }
+// the same two with the expf table passed in (an LDS copy)
+template <class Tab>
+OXE_DEV float sigmoid_t(float x, Tab tab) { return 1.f / (1.f + oxe_libm::expf_t(-x, tab)); }
+template <class Tab>
+OXE_DEV float softplus_t(float x, Tab tab) { return (x > 20.0f) ? x : oxe_libm::log1pf_c(oxe_libm::expf_t(x, tab)); }
 
 // quantize_row_q8_0, NEON branch (vendor/ggml-subset/generated/quants_subset.c:6-42), one thread
 // per 32-value block: amax (exact), d = amax/127, id = d ? 1/d : 0 from the f32 d, fp16(d) by RNE,

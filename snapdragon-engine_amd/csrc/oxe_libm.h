@@ -43,7 +43,10 @@ static const uint64_t kExp2fTab[32] = {
     0x3fef5818dcfba487ULL, 0x3fef7c97337b9b5fULL, 0x3fefa4afa2a490daULL, 0x3fefd0765b6e4540ULL,
 };
 
-OXE_HD float expf_c(float x) {
+// tab: the 32 entries above, from any address space (a device caller may pass a copy in LDS so the
+// lookup is an LDS read instead of a global load behind the memory operations in flight)
+template <class Tab>
+OXE_HD float expf_t(float x, Tab tab) {
     const double xd = (double)x;
     const uint32_t abstop = (f2u(x) >> 20) & 0x7ff;
     if (abstop >= (f2u(88.0f) >> 20)) {
@@ -59,7 +62,7 @@ OXE_HD float expf_c(float x) {
     const uint64_t ki = d2u(kd);
     kd -= shift;
     const double r = __builtin_fma(invln2n, xd, -kd);
-    uint64_t t = kExp2fTab[ki % 32];
+    uint64_t t = tab[ki % 32];
     t += ki << 47;
     const double s = u2d(t);
     const double c0 = 0x1.c6af84b912394p-5 / 32 / 32 / 32;
@@ -72,6 +75,7 @@ OXE_HD float expf_c(float x) {
     y = y * s;
     return (float)y;
 }
+OXE_HD float expf_c(float x) { return expf_t(x, kExp2fTab); }
 
 // log1pf by the classic fdlibm single-precision method (s_log1pf.c, glibc <= 2.40): reduce
 // 1+x = 2^k (1+f) with a correction term c for the rounding of 1+x, then
