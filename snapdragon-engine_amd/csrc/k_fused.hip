@@ -778,10 +778,60 @@ OXE_DEV void proj_load_part(const FZ_CAS LayerDev &L, int b, int G, int r_begin,
     }
 }
 
+// ---- delta-net inputs known ahead (the projection phase loads them for the delta-net phase)
+constexpr int DN_WPH = 8, DN_RPW = HV / DN_WPH;
+// conv channel of thread t (q: t < 128, k: t < 256, the workgroup's 16 v rows: t < 272; others
+// re-read the last v row)
+OXE_DEV int dn_channel(int vh, int row0, int t) {
+    const int kh = vh % NKH;
+    if (t < DS) return kh * DS + t;
+    if (t < 2 * DS) return NKH * DS + kh * DS + (t - DS);
+    const int i = t - 2 * DS < DN_RPW ? t - 2 * DS : DN_RPW - 1;
+    return 2 * NKH * DS + vh * HV + row0 + i;
+}
+// the delta-net phase's inputs known before the layer runs: the thread's state row (slot cur, an
+// earlier launch), its conv channel's state and weights, the head's gate constants and the
+// gated-norm weights. The projection phase loads them after its block dots (no later wait of that
+// phase depends on the count of loads in flight, so the loads may be conditional).
+struct DnPre {
+    float r[8];
+    float s0, s1, s2;
+    float4 cw;
+    float dtb, sa, nw0, nw1;
+};
+OXE_DEV void dn_load(const FZ_CAS FusedArgs &a, const FZ_CAS LayerDev &L, int b, int cur, DnPre &dp) {
+    const int t = threadIdx.x, lane = t & 63;
+    const int vh = (b / DN_WPH) % NVH, row0 = (b % DN_WPH) * DN_RPW;
+    const int64_t conv_slot = (int64_t)a.m.n_rec * NCH * (KC - 1);
+    const int64_t ssm_slot = (int64_t)a.m.n_rec * NVH * HV * HV;
+    const float *conv_state = a.m.conv_state + (int64_t)L.index * NCH * (KC - 1);
+    const float *ssm = a.m.ssm_state + (int64_t)L.index * NVH * HV * HV;
+    const int rg = (t >> 4) % DN_RPW, cc = t & 15;
+    if (t < DN_RPW * 16) {
+        const float *src = ssm + (int64_t)cur * ssm_slot + ((int64_t)vh * HV + row0 + rg) * HV;
+#pragma unroll
+        for (int q = 0; q < 8; q++) dp.r[q] = gldn(src + cc + 16 * q);
+    }
+    if (t < 2 * DS + DN_RPW) {
+        const int ch = dn_channel(vh, row0, t);
+        const float *st = conv_state + (int64_t)cur * conv_slot + (int64_t)ch * (KC - 1);
+        dp.s0 = gldn(st); dp.s1 = gldn(st + 1); dp.s2 = gldn(st + 2);
+        dp.cw = gld((const float4 *)(L.conv + (int64_t)ch * KC));
+    }
+    if ((t >> 6) == 5) {
+        dp.dtb = gld(L.dt_bias + vh);
+        dp.sa = gld(L.ssm_a + vh);
+    }
+    if ((t >> 6) < 2) {
+        dp.nw0 = gld(L.ssm_norm + lane);
+        dp.nw1 = gld(L.ssm_norm + lane + 64);
+    }
+}
+
 // pp: the slice (loaded: by the down phase before; otherwise loaded here)
 template <int NL>
 FZ_PHASE bool phase_proj(const RunCtl *ctl, const FusedArgs *ap, int il, int k, bool embed, int r_begin, int r_end,
-                         ProjPre &pp, bool loaded) {
+                         ProjPre &pp, bool loaded, DnPre &dp) {
     Ctx<NL> c = make_ctx<NL>(ctl, ap, k);
     tr_start(c);
     const FZ_CAS FusedArgs &a = *c.a;
@@ -801,6 +851,7 @@ FZ_PHASE bool phase_proj(const RunCtl *ctl, const FusedArgs *ap, int il, int k, 
                       [&] { tr_pass(c); }))
         return false;
     if (embed) tr_pass(c);
+    // a delta-net layer's next phase inputs that do not depend on this one
     tr_mark(c, 111);
     if (embed && c.b == 0) {
         // the embedded input is the residual of layer 0
@@ -808,7 +859,12 @@ FZ_PHASE bool phase_proj(const RunCtl *ctl, const FusedArgs *ap, int il, int k, 
         if (l < c.nl)
             for (int i = 0; i < 8; i++) ll_stf(xin + l * E + 8 * tt + i, s.xf[l][8 * tt + i], c.tag(k, PH_PROJ));
     }
-    wdot<E, 13, NL>(ws, nr, &s.xq[0][0], E, &s.xd[0][0], E / 32, s.g, [&] { tr_mark(c, 113); });
+    // after the block dots (every weight wait of this phase done): a delta-net layer's inputs of the
+    // next phase that do not depend on this one
+    wdot<E, 13, NL>(ws, nr, &s.xq[0][0], E, &s.xd[0][0], E / 32, s.g, [&] {
+        tr_mark(c, 113);
+        if (!L.att) dn_load(a, L, c.b, c.ctl->cur, dp);
+    });
     tr_mark(c, 112);
     const int t = threadIdx.x;
     uint64_t *po = a.xc.p + (size_t)c.par() * NL * DN_ROWS;
@@ -834,7 +890,6 @@ FZ_PHASE bool phase_proj(const RunCtl *ctl, const FusedArgs *ap, int il, int k, 
 // forms the head's conv outputs and normalised q, k (gdn conv + l2 norms, oxe_ops.cpp:218-267) and
 // writes its 16 outputs; the head's first workgroup then reads the head's 128 outputs back (tagged)
 // and forms their gated norm and Q8_0 quantisation.
-constexpr int DN_WPH = 8, DN_RPW = HV / DN_WPH;
 OXE_DEV float dot16_tree_f(float acc) { return dot16_tree_dpp(acc); }
 OXE_DEV float conv4f(float s0, float s1, float s2, float xn, const float *c) {
     const float p0 = s0 * c[0], p1 = s1 * c[1], p2 = s2 * c[2], p3 = xn * c[3];
@@ -846,14 +901,14 @@ OXE_DEV float conv4f(float s0, float s1, float s2, float xn, const float *c) {
     return sumf;
 }
 template <int NL>
-FZ_PHASE bool phase_dn(const RunCtl *ctl, const FusedArgs *ap, int il, int k) {
+FZ_PHASE bool phase_dn(const RunCtl *ctl, const FusedArgs *ap, int il, int k, const DnPre &dp) {
     Ctx<NL> c = make_ctx<NL>(ctl, ap, k);
     tr_start(c);
     const FZ_CAS FusedArgs &a = *c.a;
     const FZ_CAS LayerDev &L = layer_of(c, il);
     auto &s = c.sm->dn;
     const int t = threadIdx.x, w = t >> 6, lane = t & 63;
-    const int vh = c.b / DN_WPH, kh = vh % NKH, row0 = (c.b % DN_WPH) * DN_RPW;
+    const int vh = c.b / DN_WPH, row0 = (c.b % DN_WPH) * DN_RPW;
     const bool worker = c.b < NVH * DN_WPH;
     const int cur = c.ctl->cur;
     const int64_t conv_slot = (int64_t)a.m.n_rec * NCH * (KC - 1);
@@ -862,35 +917,18 @@ FZ_PHASE bool phase_dn(const RunCtl *ctl, const FusedArgs *ap, int il, int k) {
     float *ssm = a.m.ssm_state + (int64_t)L.index * NVH * HV * HV;
     const int rg = t >> 4, cc = t & 15;
     const bool dlt = worker && t < DN_RPW * 16;
+    const int ch = dn_channel(vh, row0, t);
+    const bool conv = worker && t < 2 * DS + DN_RPW;
+    const bool writer = t < 2 * DS ? (vh < NKH && row0 == 0) : true;
     float r[8];
-    if (dlt) {
-        const float *src = ssm + (int64_t)cur * ssm_slot + ((int64_t)vh * HV + row0 + rg) * HV;
 #pragma unroll
-        for (int q = 0; q < 8; q++) r[q] = src[cc + 16 * q];
-    }
-    // this thread's conv channel (q: t < 128, k: t < 256, the workgroup's 16 v rows: t < 272): state
-    // (slot cur, an earlier launch) and weights, loaded ahead. q/k states are written by the head's
-    // first workgroup of the first 16 value heads (value heads vh and vh + 16 share key head vh).
-    int ch = 0;
-    bool conv = false, writer = false;
-    if (t < DS) { ch = kh * DS + t; conv = worker; writer = vh < NKH && row0 == 0; }
-    else if (t < 2 * DS) { ch = NKH * DS + kh * DS + (t - DS); conv = worker; writer = vh < NKH && row0 == 0; }
-    else if (t < 2 * DS + DN_RPW) { ch = 2 * NKH * DS + vh * HV + row0 + (t - 2 * DS); conv = worker; writer = true; }
-    float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f;
-    float cw[KC] = {0.0f, 0.0f, 0.0f, 0.0f};
-    if (conv) {
-        const float *st = conv_state + (int64_t)cur * conv_slot + (int64_t)ch * (KC - 1);
-        s0 = st[0]; s1 = st[1]; s2 = st[2];
-        const float4 c4 = gld((const float4 *)(L.conv + (int64_t)ch * KC));
-        cw[0] = c4.x; cw[1] = c4.y; cw[2] = c4.z; cw[3] = c4.w;
-    }
+    for (int q = 0; q < 8; q++) r[q] = dp.r[q];
+    float s0 = dp.s0, s1 = dp.s1, s2 = dp.s2;
+    const float cw[KC] = {dp.cw.x, dp.cw.y, dp.cw.z, dp.cw.w};
     // gate thread of lane gl (wave 5) and the gated-norm weights (waves < NL)
     const int gl = t - 5 * 64;
     const bool gate = worker && gl >= 0 && gl < NL;
-    float dtb = 0.0f, sa = 0.0f;
-    if (gate) { dtb = L.dt_bias[vh]; sa = L.ssm_a[vh]; }
-    float nw0 = 0.0f, nw1 = 0.0f;
-    if (worker && w < NL) { nw0 = L.ssm_norm[lane]; nw1 = L.ssm_norm[lane + 64]; }
+    const float dtb = dp.dtb, sa = dp.sa, nw0 = dp.nw0, nw1 = dp.nw1;
     const uint64_t *pin = a.xc.p + (size_t)c.par() * NL * DN_ROWS;
     uint64_t *gx = a.xc.g + (size_t)c.par() * NL * MIX_W;
     const uint32_t tp = c.tag(k, PH_PROJ), tg = c.tag(k, PH_MIX);
@@ -2072,13 +2110,14 @@ __device__ __attribute__((noinline)) bool run_step(const RunCtl *ctl, const Fuse
     const int att = L.att;
     // the residual: the embedding (written by the projection phase) or the previous layer's output
     const uint32_t xtag = base + 1u + (embed ? 8u * (uint32_t)k + PH_PROJ : 8u * (uint32_t)(k - 1) + PH_DOWN);
+    DnPre dp;
 #ifndef FZ_NO_PREFETCH
-    if (!phase_proj<NL>(ctl, ap, il, k, embed, 0, att ? AT_ROWS : DN_ROWS, pre, ilp >= 0)) return false;
+    if (!phase_proj<NL>(ctl, ap, il, k, embed, 0, att ? AT_ROWS : DN_ROWS, pre, ilp >= 0, dp)) return false;
 #else
-    if (!phase_proj<NL>(ctl, ap, il, k, embed, 0, att ? AT_ROWS : DN_ROWS, pre, false)) return false;
+    if (!phase_proj<NL>(ctl, ap, il, k, embed, 0, att ? AT_ROWS : DN_ROWS, pre, false, dp)) return false;
 #endif
     if (!att) {
-        if (!phase_dn<NL>(ctl, ap, il, k)) return false;
+        if (!phase_dn<NL>(ctl, ap, il, k, dp)) return false;
     } else {
         if (!phase_scores<NL>(ctl, ap, il, k, false)) return false;
         if (!phase_pv<NL>(ctl, ap, il, k)) return false;
@@ -2106,7 +2145,8 @@ OXE_DEV void run_all(const RunCtl *ctl, const FusedArgs *ap, uint32_t base) {
         const int il = nlay;
         if (!phase_entry<NL>(ctl, ap, il)) return;
         ProjPre pre;
-        if (!phase_proj<NL>(ctl, ap, il, 1, false, AT_K, AT_ROWS, pre, false)) return;
+        DnPre dp;   // the MTP layer is an attention layer: not loaded
+        if (!phase_proj<NL>(ctl, ap, il, 1, false, AT_K, AT_ROWS, pre, false, dp)) return;
         (void)phase_scores<NL>(ctl, ap, il, 1, true);
     }
 }
