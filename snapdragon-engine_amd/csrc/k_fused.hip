@@ -303,6 +303,37 @@ OXE_DEV void wload(WSlice<K, MAXP> &s, const int8_t *__restrict__ wq, const uint
     s.s = gldn((const uint4 *)(wd + rowof(sr < nr ? sr : nr - 1) * G::NB + sk * 8));
 }
 
+// the serial chain acc = fma(a[i], b[i], acc) for i = 0..N-1 in order, from +0 (N a multiple of 16;
+// a, b 16-byte aligned, in LDS): the next sixteen operands of each are read while the current
+// sixteen multiply-add, so the chain does not wait for an LDS read every step
+template <int N>
+OXE_DEV float chain_fma(const float *a, const float *b) {
+    static_assert(N % 16 == 0, "sixteen per step");
+    constexpr int S = 4;   // float4 pairs per step
+    const float4 *a4 = (const float4 *)a, *b4 = (const float4 *)b;
+    float4 x[S], y[S];
+#pragma unroll
+    for (int i = 0; i < S; i++) { x[i] = a4[i]; y[i] = b4[i]; }
+    float acc = 0.0f;
+    for (int q = 0; q < N / 4; q += S) {
+        const int qn = q + S < N / 4 ? q + S : q;   // the last step reads its own operands again
+        float4 u[S], v[S];
+#pragma unroll
+        for (int i = 0; i < S; i++) { u[i] = a4[qn + i]; v[i] = b4[qn + i]; }
+        __builtin_amdgcn_sched_barrier(0);   // the reads stay ahead of this step's multiply-adds
+#pragma unroll
+        for (int i = 0; i < S; i++) {
+            acc = __builtin_fmaf(x[i].x, y[i].x, acc);
+            acc = __builtin_fmaf(x[i].y, y[i].y, acc);
+            acc = __builtin_fmaf(x[i].z, y[i].z, acc);
+            acc = __builtin_fmaf(x[i].w, y[i].w, acc);
+        }
+#pragma unroll
+        for (int i = 0; i < S; i++) { x[i] = u[i]; y[i] = v[i]; }
+    }
+    return acc;
+}
+
 // g.out[l][r] = row r . lane l for the slice's nr rows (activation codes xq [NL][xq_ld] and scales
 // xd [NL][xd_ld] in LDS). Ends with a barrier.
 struct NoMid {
@@ -353,17 +384,7 @@ OXE_DEV void wdot(const WSlice<K, MAXP> &s, int nr, const int8_t *xq, int xq_ld,
     if (t < nr * NL) {
         // one serial FMA chain per (row, lane) in block order, four blocks per LDS read
         const int rl = t % nr, l = t / nr;
-        const float *fr = &g.f[l][rl][0], *dr = &g.d[l][rl][0];
-        float acc = 0.0f;
-#pragma unroll 4
-        for (int b = 0; b < G::NB; b += 4) {
-            const float4 f4 = *(const float4 *)(fr + b), d4 = *(const float4 *)(dr + b);
-            acc = __builtin_fmaf(f4.x, d4.x, acc);
-            acc = __builtin_fmaf(f4.y, d4.y, acc);
-            acc = __builtin_fmaf(f4.z, d4.z, acc);
-            acc = __builtin_fmaf(f4.w, d4.w, acc);
-        }
-        g.out[l][rl] = acc;
+        g.out[l][rl] = chain_fma<G::NB>(&g.f[l][rl][0], &g.d[l][rl][0]);
     }
     __syncthreads();
 }
@@ -1242,16 +1263,7 @@ FZ_PHASE bool phase_router(const RunCtl *ctl, const FusedArgs *ap, int il, int k
             const float *wv = sgd ? s.sg[cc] : s.w[cc];
             const float *xv = s.xc[l][cc];
             float acc = 0.0f;
-            if (!sgd || shg) {
-#pragma unroll 4
-                for (int q = 0; q < E / 16; q += 4) {
-                    const float4 w4 = *(const float4 *)(wv + q), x4 = *(const float4 *)(xv + q);
-                    acc = __builtin_fmaf(w4.x, x4.x, acc);
-                    acc = __builtin_fmaf(w4.y, x4.y, acc);
-                    acc = __builtin_fmaf(w4.z, x4.z, acc);
-                    acc = __builtin_fmaf(w4.w, x4.w, acc);
-                }
-            }
+            if (!sgd || shg) acc = chain_fma<E / 16>(wv, xv);
             const float v = dot16_tree_f(acc);
             if (cc == 0 && l < c.nl) {
                 if (!sgd) ll_stf(a.xc.lg + ((size_t)c.par() * NL + l) * NEXP + b, v, c.tag(k, PH_ROUTER));
