@@ -197,10 +197,18 @@ OXE_DEV bool ll_gather(At at, uint32_t (&v)[N], uint32_t *err, const XR *xr) {
         v[0] = (uint32_t)y;
         miss &= ~1u;
     }
+    const int np = xr ? NP : 0;
     while (miss) {
         unsigned long long w[N];
+        // pairs with a missing half again 16 bytes at a time, the other words one by one
 #pragma unroll
-        for (int i = 1; i < N; i++) w[i] = ((miss >> i) & 1u) ? cld64(at(i).p) : 0ull;
+        for (int m = 0; m < NP; m++) {
+            w[2 * m] = w[2 * m + 1] = 0ull;
+            if (m < np && ((miss >> (2 * m)) & 3u)) cld128x(*xr, at(2 * m).p, w[2 * m], w[2 * m + 1]);
+        }
+#pragma unroll
+        for (int i = 1; i < N; i++)
+            if (i >= 2 * np) w[i] = ((miss >> i) & 1u) ? cld64(at(i).p) : 0ull;
 #pragma unroll
         for (int i = 1; i < N; i++)
             if (((miss >> i) & 1u) && ll_ok(w[i], at(i).tag)) {
