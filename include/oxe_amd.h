@@ -158,7 +158,7 @@ OXE_API int oxe_engine_fused(const oxe_engine *e);
 /* Phase trace of the fused run kernel (diagnostic, no counterpart in the reference, whose Trace at
  * crates/model/src/engine.rs:324-340 records tensors, not time): when on, every run records per workgroup and
  * phase (phase id, start, barrier released, end) in device wall-clock ticks (100 MHz);
- * read_trace copies the last run's records ([grid][1024][4] u64) and returns their count. */
+ * read_trace copies the last run's records ([grid][2048][4] u64) and returns their count. */
 OXE_API int oxe_engine_set_trace(oxe_engine *e, int on);
 OXE_API int64_t oxe_engine_read_trace(oxe_engine *e, unsigned long long *host, int64_t cap);
 

@@ -74,7 +74,7 @@ struct FusedArgs {
     unsigned long long *trace;     // optional [grid][FZ_TRACE_EV][4]: phase id, start, barrier passed, end
 };
 
-constexpr int FZ_TRACE_EV = 1024;  // trace events per workgroup and run
+constexpr int FZ_TRACE_EV = 2048;  // trace events per workgroup and run
 
 size_t fused_lds_bytes(int n_ctx);
 // workgroups of the fused kernel one CU holds with `lds` bytes of dynamic LDS (must be >= 1)

@@ -668,13 +668,13 @@ class Engine:
         check(lib().oxe_engine_set_trace(self.h, int(on)), "set_trace")
 
     def read_trace(self):
-        """Last fused run's phase records: array [grid, 1024, 4] (phase id, start, passed, end), 100 MHz ticks."""
+        """Last fused run's phase records: array [grid, 2048, 4] (phase id, start, passed, end), 100 MHz ticks."""
         import numpy as np
-        buf = np.zeros(256 * 1024 * 4, np.uint64)
+        buf = np.zeros(256 * 2048 * 4, np.uint64)
         n = lib().oxe_engine_read_trace(self.h, buf.ctypes.data_as(C.c_void_p), buf.size)
         if n < 0:
             raise RuntimeError("read_trace failed")
-        return buf[:n].reshape(-1, 1024, 4)
+        return buf[:n].reshape(-1, 2048, 4)
 
     def mtp_set_depth(self, depth):
         """drafts per host-driven MTP step (MtpDriver.depth; the device-driven step is depth 1)"""

@@ -70,6 +70,29 @@ def analyse(tr):
     return total, agg, marks, (ids, start, pas, end)
 
 
+def phase_bytes(d, union, pos):
+    """Algorithmic HBM bytes of one instance of each phase kind (Q8_0 rows: codes + fp16 scale per 32),
+    for the run's two lanes at context position pos; union: routed experts per MoE layer (both lanes)."""
+    q8 = lambda rows, k: rows * (k + k // 32 * 2)
+    E, F, FF = d.n_embd, d.ff_exp, d.ff_shexp
+    conv = d.ssm_d_inner + 2 * d.ssm_n_kheads * d.ssm_d_state        # q, k, v channels
+    dn_rows = conv + d.ssm_d_inner + 2 * d.ssm_n_vheads               # [qkv; z; beta; alpha]
+    at_rows = 2 * d.n_head * d.head_dim + 2 * d.n_head_kv * d.head_dim  # [q + gate; k; v]
+    state = d.ssm_n_vheads * (d.ssm_d_inner // d.ssm_n_vheads) ** 2 * 4
+    kv_row = d.n_head_kv * d.head_dim * 2
+    return {
+        "proj": (30 * q8(dn_rows, E) + 10 * q8(at_rows, E)) / 40.0,
+        "dn": state * 3 + conv * 3 * 4 * 3 + conv * 4 * 4,
+        "out": q8(E, d.ssm_d_inner),
+        "router": d.n_expert * E * 4 + E * 4 + q8(2 * FF, E),
+        "experts": union * q8(2 * F, E),
+        "down": (union + 1) * q8(E, F),
+        "scores": (pos + 2) * kv_row,
+        "pv": (pos + 2) * kv_row,
+        "head": q8(d.n_vocab, E),
+    }
+
+
 def timeline(ids, start, pas, end, k0, k1):
     """Rows (phase, start, pass, end) as min / median / max over workgroups, us from event k0's
     earliest start, for events [k0, k1)."""
@@ -93,17 +116,24 @@ def main():
         sys.exit("the fused run kernel is not available on this device")
     x = e.mtp_prefill(A.bench_prompt(args.prompt))
     e.set_trace(True)
+    u0, c0 = e.counter(66), e.counter(67)
     for _ in range(args.steps):
         g = e.verify([x, (x + 1) % d.n_vocab])
         e.commit(1)
         x = int(g[0])
+    union = (e.counter(66) - u0) / max(1, e.counter(67) - c0)
     total, agg, marks, ev = analyse(e.read_trace())
-    print(f"verify run (2 lanes, 40 layers + LM head) at position {e.pos}: {total:.1f} us")
+    pb = phase_bytes(d, union, e.pos)
+    print(f"verify run (2 lanes, 40 layers + LM head) at position {e.pos}: {total:.1f} us; "
+          f"routed experts per MoE layer (union of the lanes) {union:.2f}")
     print(f"{'phase':10s} {'count':>5s} {'release->done us':>17s} {'gap before us':>14s} {'pass skew us':>13s} "
-          f"{'total us':>9s} {'wait med':>9s} {'work med':>9s}")
+          f"{'total us':>9s} {'wait med':>9s} {'work med':>9s} {'MB each':>8s} {'GB/s':>7s}")
     for name, (cnt, dur, gap, skew, wt, wk) in agg.items():
+        mb = pb.get(name, 0.0) / 1e6
+        gbs = mb * cnt / (dur + gap) * 1e3 if dur + gap > 0 else 0.0
         print(f"{name:10s} {cnt:5d} {dur / cnt:17.2f} {gap / cnt:14.2f} {skew / cnt:13.2f} {dur + gap:9.1f} "
-              f"{np.mean(wt):9.2f} {np.mean(wk):9.2f}")
+              f"{np.mean(wt):9.2f} {np.mean(wk):9.2f} {mb:8.2f} {gbs:7.0f}")
+    print("GB/s: the phase kind's algorithmic bytes over its total (release->done plus the gap before it)")
     ids = ev[0]
     # one DN layer and one attention layer in the middle of the run: start / inputs / end per phase
     for want in (2, 3):
