@@ -1799,12 +1799,16 @@ FZ_PHASE bool phase_pv(const RunCtl *ctl, const FusedArgs *ap, int il, int k) {
     const uint64_t *pin = a.xc.p + (size_t)c.par() * NL * DN_ROWS;
     const uint32_t tp = c.tag(k, PH_PROJ), ts = c.tag(k, PH_MIX);
     if (act) {
+        // byte offsets from the LDS base (pointer arithmetic only: an integer round trip would lose
+        // the LDS address space, and generic accesses wait for every memory operation in flight)
+        const size_t o_v = (size_t)n_ctx * 4, o_mx = o_v + (size_t)PVD * vs * 2;
+        const size_t o_ps = (o_mx + 8 * sizeof(float) + 7) & ~(size_t)7, o_f = o_ps + 8 * sizeof(double);
         uint32_t *s_pp = (uint32_t *)c.dyn;                                  // [n_kv / 2][2] f16 pairs
-        uint16_t *s_v = (uint16_t *)(c.dyn + (size_t)n_ctx * 4);            // [PVD][vs] V^T rows
-        float *s_mx = (float *)(s_v + (size_t)PVD * vs);                    // [2][4] wave maxima
-        double *s_ps = (double *)(((uintptr_t)(s_mx + 8) + 7) & ~(uintptr_t)7);   // [2][4] wave sums
-        float *s_f = (float *)(s_ps + 8);                                   // [2] 1 / sum
-        uint16_t *s_vn = (uint16_t *)(s_f + 2);                             // [NL][PVD] this run's V
+        uint16_t *s_v = (uint16_t *)(c.dyn + o_v);                          // [PVD][vs] V^T rows
+        float *s_mx = (float *)(c.dyn + o_mx);                              // [2][4] wave maxima
+        double *s_ps = (double *)(c.dyn + o_ps);                            // [2][4] wave sums
+        float *s_f = (float *)(c.dyn + o_f);                                // [2] 1 / sum
+        uint16_t *s_vn = (uint16_t *)(c.dyn + o_f + 2 * sizeof(float));     // [NL][PVD] this run's V
         const int q = t >> 8, tq = t & 255, wq = (t >> 6) & 3;
         const int cp = t & 15, d = (t >> 4) & (PVD - 1);
         const int h = kvh * GQA + 2 * hp + q;
