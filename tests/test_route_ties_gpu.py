@@ -8,8 +8,10 @@ device restates the algorithm, oxe_stdsort.h, itself checked against std::sort i
     repeated 9th value, few distinct levels — ids and weights against the oracle's softmax, top-k
     and renormalisation;
   * engine level, both run modes: every layer's router rows duplicated in pairs (row 2i + 1 = row
-    2i, so every probability appears twice and each routing takes the sort path); the MTP prefill and
-    device-driven steps return the oracle's tokens, logits and hidden rows bit for bit.
+    2i, so every probability appears twice and each routing takes the sort path) or in threes (the
+    8th and 9th probabilities are then always equal: the sort decides which experts run, not only
+    their order); the MTP prefill and device-driven steps return the oracle's tokens, logits and
+    hidden rows bit for bit.
 """
 import ctypes as C
 
@@ -77,14 +79,16 @@ def test_route_kernel_ties_bitexact(dev):
     assert ties == len(lg) - 1 and int(tc.item()) == ties
 
 
-def paired_router(d, layer):
+def copied_router(d, layer, copies):
     r = O.synth_f32(SEED, layer, O.T["ROUTER"], 256 * d.n_embd).reshape(256, d.n_embd)
-    r[1::2] = r[0::2]
+    for j in range(1, copies):
+        r[j::copies] = r[0::copies][: len(r[j::copies])]
     return r
 
 
+@pytest.mark.parametrize("copies", [2, 3])
 @pytest.mark.parametrize("mode", ["fused", "per_phase"])
-def test_engine_with_tied_routers_bitexact(dev, mode):
+def test_engine_with_tied_routers_bitexact(dev, mode, copies):
     import oxe_amd as A
     d = O.desc_small()
     g = A.Engine(d, seed=SEED, n_ctx=256)
@@ -94,7 +98,7 @@ def test_engine_with_tied_routers_bitexact(dev, mode):
         pytest.skip("the fused run kernel needs a 256-CU device")
     o = O.Engine(d, seed=SEED, n_ctx=256)
     for layer in range(d.n_layer + 1):
-        r = paired_router(d, layer)
+        r = copied_router(d, layer, copies)
         g.set_router(layer, 0, r)
         o.set_router(layer, 0, r)
     prompt = O.bench_prompt(7) % d.n_vocab
