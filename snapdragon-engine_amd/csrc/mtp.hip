@@ -23,7 +23,8 @@ OXE_HOST_DEV_INLINE uint32_t decode_key(unsigned long long k) { return k == 0 ? 
 
 // ---- device-driven step kernels ----------------------------------------------------------------
 
-__global__ void mtp_prep_seed_kernel(MtpState *ms, RunCtl *ctl) {
+// the seed run's control block of the step about to start: active when a pair is pending
+__device__ RunCtl seed_ctl(const MtpState *ms) {
     RunCtl r{};
     r.nl = 1;
     r.pos0 = ms->pos - 1;
@@ -32,11 +33,12 @@ __global__ void mtp_prep_seed_kernel(MtpState *ms, RunCtl *ctl) {
     r.hin_sel[0] = HID_PEND;
     r.head_mask = 0;
     r.active = ms->pending != 0 && ms->err == 0;
-    *ctl = r;
+    return r;
 }
 
-__global__ void mtp_prep_draft_kernel(MtpState *ms, RunCtl *ctl, int n_ctx) {
-    if (ms->pos + 2 > n_ctx) ms->err |= 1;  // no room for the 2-lane verify: stop (reference: k = 0)
+// the draft run's: inactive when the 2-lane verify has no room (the step then stops the driver, as
+// the reference's k = 0; mtp_prep_verify_kernel records it)
+__device__ RunCtl draft_ctl(const MtpState *ms, int n_ctx) {
     RunCtl r{};
     r.nl = 1;
     r.pos0 = ms->pos;
@@ -44,8 +46,17 @@ __global__ void mtp_prep_draft_kernel(MtpState *ms, RunCtl *ctl, int n_ctx) {
     r.tok[0] = ms->x;
     r.hin_sel[0] = HID_HL;
     r.head_mask = 1;
-    r.active = ms->err == 0;
-    *ctl = r;
+    r.active = ms->err == 0 && ms->pos + 2 <= n_ctx;
+    return r;
+}
+
+// per-phase runs: the step's seed and draft runs read ctl, one after the other
+__global__ void mtp_prep_seed_kernel(MtpState *ms, RunCtl *ctl) { *ctl = seed_ctl(ms); }
+__global__ void mtp_prep_draft_kernel(MtpState *ms, RunCtl *ctl, int n_ctx) { *ctl = draft_ctl(ms, n_ctx); }
+// fused runs: both control blocks of the first step (the commit kernel fills them for the next)
+__global__ void mtp_prep_step_kernel(MtpState *ms, RunCtl *cs, RunCtl *cd, int n_ctx) {
+    *cs = seed_ctl(ms);
+    *cd = draft_ctl(ms, n_ctx);
 }
 
 // the largest of n argmax keys (one wave: lanes stride the keys, then a shuffle tree)
@@ -60,9 +71,10 @@ __device__ unsigned long long wave_key_max(const unsigned long long *keys, int n
 }
 
 __global__ void mtp_prep_verify_kernel(MtpState *ms, RunCtl *ctl, const unsigned long long *keys, int nkeys,
-                                       const int32_t *force_d1, int force_n) {
+                                       const int32_t *force_d1, int force_n, int n_ctx) {
     const unsigned long long k0 = wave_key_max(keys, nkeys);
     if (threadIdx.x != 0) return;
+    if (ms->pos + 2 > n_ctx) ms->err |= 1;  // no room for the 2-lane verify: stop (reference: k = 0)
     uint32_t d1 = decode_key(k0);
     if (force_d1 && ms->steps < force_n && force_d1[ms->steps] >= 0) d1 = (uint32_t)force_d1[ms->steps];  // test hook (mtp.rs:554-558)
     ms->d1 = d1;
@@ -80,8 +92,9 @@ __global__ void mtp_prep_verify_kernel(MtpState *ms, RunCtl *ctl, const unsigned
 }
 
 // accept / commit / note (mtp.rs:564-591, engine.rs:2030-2039): a = (d1 == argmax lane 0)
+// Then the next step's seed and draft control blocks (cs, cd), from the updated state.
 __global__ void mtp_commit_kernel(MtpState *ms, const unsigned long long *keys, int nkeys, float *hid, uint16_t *vcache,
-                                  int64_t vrows, int n_ctx, uint32_t *out_tok, int out_cap) {
+                                  int64_t vrows, int n_ctx, uint32_t *out_tok, int out_cap, RunCtl *cs, RunCtl *cd) {
     __shared__ int s_a, s_ok, s_pos0;
     __shared__ uint32_t s_g[2];
     const int t = threadIdx.x;
@@ -96,7 +109,13 @@ __global__ void mtp_commit_kernel(MtpState *ms, const unsigned long long *keys, 
         }
     }
     __syncthreads();
-    if (!s_ok) return;
+    if (!s_ok) {
+        if (t == 0) {
+            *cs = seed_ctl(ms);
+            *cd = draft_ctl(ms, n_ctx);
+        }
+        return;
+    }
     const int a = s_a, pos0 = s_pos0;
     // hl = h_nextn after the last committed token; the accepted draft's pair (d1, h after x)
     // waits for MTP seeding
@@ -120,6 +139,8 @@ __global__ void mtp_commit_kernel(MtpState *ms, const unsigned long long *keys, 
         ms->cur = (ms->cur + a + 1) % OXE_NSLOTS;
         ms->steps += 1;
         ms->accepted += a;
+        *cs = seed_ctl(ms);
+        *cd = draft_ctl(ms, n_ctx);
     }
 }
 
@@ -340,6 +361,7 @@ int MtpDriverHost::dev_begin(Engine &e, uint32_t x) {
     s.n_out = 0;
     if (hipMemcpyAsync(e.mtp_state, &s, sizeof(s), hipMemcpyHostToDevice, e.st) != hipSuccess) return -2;
     if (hipMemcpyAsync(e.b.hid + (size_t)HID_HL * E, hl.data(), (size_t)E * 4, hipMemcpyHostToDevice, e.st) != hipSuccess) return -2;
+    hipLaunchKernelGGL(mtp_prep_step_kernel, dim3(1), dim3(1), 0, e.st, e.mtp_state, e.ctl_seed, e.ctl_draft, e.m.n_ctx);
     return hipStreamSynchronize(e.st) == hipSuccess ? 0 : -2;
 }
 
@@ -372,15 +394,22 @@ int MtpDriverHost::dev_end(Engine &e, uint32_t *out_tok, int cap, int *n_out, ui
 }
 
 void Engine::enqueue_mtp_device_step() {
-    hipLaunchKernelGGL(mtp_prep_seed_kernel, dim3(1), dim3(1), 0, st, mtp_state, ctl);
-    enqueue_mtp_seed();
-    hipLaunchKernelGGL(mtp_prep_draft_kernel, dim3(1), dim3(1), 0, st, mtp_state, ctl, m.n_ctx);
-    enqueue_mtp_run();
+    if (fused) {
+        // the seed and draft runs read their own control blocks, filled by the previous step's
+        // commit (or dev_begin): two launches fewer per step
+        enqueue_mtp_seed(ctl_seed);
+        enqueue_mtp_run(ctl_draft);
+    } else {
+        hipLaunchKernelGGL(mtp_prep_seed_kernel, dim3(1), dim3(1), 0, st, mtp_state, ctl);
+        enqueue_mtp_seed();
+        hipLaunchKernelGGL(mtp_prep_draft_kernel, dim3(1), dim3(1), 0, st, mtp_state, ctl, m.n_ctx);
+        enqueue_mtp_run();
+    }
     hipLaunchKernelGGL(mtp_prep_verify_kernel, dim3(1), dim3(64), 0, st, mtp_state, ctl, keys(), nkeys(),
-                       (const int32_t *)force_d1, force_n);
+                       (const int32_t *)force_d1, force_n, m.n_ctx);
     enqueue_verify();
     hipLaunchKernelGGL(mtp_commit_kernel, dim3(1), dim3(256), 0, st, mtp_state, keys(), nkeys(), b.hid,
-                       m.vcache, (int64_t)n_att_main * NKV * HD, m.n_ctx, out_tok, out_cap);
+                       m.vcache, (int64_t)n_att_main * NKV * HD, m.n_ctx, out_tok, out_cap, ctl_seed, ctl_draft);
 }
 
 int Engine::mtp_steps_async(int k, bool use_graph) {

@@ -78,6 +78,9 @@ struct Engine {
     std::vector<LayerW> L;  // n_layer (+1 MTP block)
     ActBufs b{};
     RunCtl *ctl = nullptr;  // device
+    // the device-driven step's seed and draft control blocks (fused runs), filled by the previous
+    // step's commit kernel or by dev_begin
+    RunCtl *ctl_seed = nullptr, *ctl_draft = nullptr;
     std::vector<void *> allocs;
     size_t bytes = 0;
     // host mirror of the engine position (host-driven API)
@@ -290,7 +293,9 @@ struct Engine {
         b.logits = alloc<float>((size_t)OXE_NL * d.n_vocab);
         b.amax_key = alloc<unsigned long long>(OXE_NL);
         b.counters = alloc<uint32_t>(CNT_N);
-        ctl = alloc<RunCtl>(1);
+        ctl = alloc<RunCtl>(3);
+        ctl_seed = ctl + 1;
+        ctl_draft = ctl + 2;
         mtp_state = alloc<MtpState>(1);
         (void)hipMemsetAsync(mtp_state, 0, sizeof(MtpState), st);
         // zero what must start at zero (before any graph capture)
@@ -555,11 +560,12 @@ struct Engine {
         for (int l = 0; l < d.n_layer; l++) enqueue_layer(l, l == 0);
         probe(K_HEAD); launch_head(ctl, m, m.out_norm, b, keep_logits, st); probe(K_HEAD);
     }
-    void enqueue_mtp_run() {
+    // rc: the fused run's control block (default: ctl)
+    void enqueue_mtp_run(const RunCtl *rc = nullptr) {
         if (fused) {
             if (!fz_capturing) fz_account(1);
             probe(K_FUSED_DRAFT);
-            launch_fused(ctl, fz_args + FM_DRAFT, fz_grid, fz_lds, st);
+            launch_fused(rc ? rc : ctl, fz_args + FM_DRAFT, fz_grid, fz_lds, st);
             probe(K_FUSED_DRAFT);
             return;
         }
@@ -574,10 +580,10 @@ struct Engine {
         enqueue_moe(w);
         probe(K_HEAD); launch_head(ctl, m, w.head_norm, b, false, st); probe(K_HEAD);
     }
-    void enqueue_mtp_seed() {
+    void enqueue_mtp_seed(const RunCtl *rc = nullptr) {
         if (fused) {
             if (!fz_capturing) fz_account(1);
-            launch_fused(ctl, fz_args + FM_SEED, fz_grid, fz_lds, st);
+            launch_fused(rc ? rc : ctl, fz_args + FM_SEED, fz_grid, fz_lds, st);
             return;
         }
         const LayerW &w = L[d.n_layer];
