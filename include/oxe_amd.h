@@ -247,7 +247,8 @@ OXE_API int oxe_mtp_step_plain(oxe_engine *e, uint32_t x, uint32_t *out);
 /* Drafts per host-driven step, 1..3 (MtpDriver.depth, mtp.rs:314-360; the reference's MAX_LANES
  * verify of depth + 1 lanes runs here as pieces of at most 2 lanes, each committed before the next,
  * stopping at the first rejected draft: the same committed state, tokens, hidden rows and logits).
- * The device-driven step (oxe_mtp_device_*) is depth 1 and refuses other depths. */
+ * The device-driven step (oxe_mtp_device_*) runs depth 1 or 2 (the depth set when begin is called)
+ * and refuses depth 3. */
 OXE_API int oxe_mtp_set_depth(oxe_engine *e, int depth);
 /* oxe_mtp_step with force[i] >= 0 (i < nforce) replacing draft i + 1 after the draft chain is formed
  * (the reference's draft_override hook, mtp.rs:328-330, 554-558); out has room for depth + 1 tokens */
@@ -258,11 +259,16 @@ OXE_API int oxe_mtp_step_force(oxe_engine *e, uint32_t x, uint32_t *out, int *n_
 OXE_API int oxe_mtp_rewind(oxe_engine *e, int m);
 /* Device-driven steps: begin hands the driver state to the GPU; each of the k steps then runs
  * seed -> draft -> 2-lane verify -> greedy accept/commit on the GPU (one HIP graph per step, no
- * host round-trip); end synchronises and returns the emitted tokens and the next x. */
+ * host round-trip); end synchronises and returns the emitted tokens and the next x. At depth 2 a step
+ * runs two drafts and verifies x, d1 and then d2 in pieces of at most two lanes, the second piece
+ * only when d1 was accepted and d2 matches (mtp.rs:522-592). A step that does not fit the context
+ * (depth 1: 2 positions, depth 2: 3) stops the steps: end returns -4, and the caller continues with
+ * host-driven steps (which shorten the draft chain to the room left, as the reference does). */
 OXE_API int oxe_mtp_device_begin(oxe_engine *e, uint32_t x, int out_cap);
 OXE_API int oxe_mtp_device_steps(oxe_engine *e, int k, int use_graph);
 OXE_API int oxe_mtp_device_end(oxe_engine *e, uint32_t *out_tok, int cap, int *n_out, uint32_t *next_x);
-/* Forced drafts for the device-driven steps (test hook): force_d1[i] >= 0 replaces step i's draft. */
+/* Forced drafts for the device-driven steps (test hook): force_d1[i * depth + j] >= 0 replaces draft
+ * j + 1 of step i. */
 OXE_API int oxe_mtp_set_force(oxe_engine *e, const int32_t *force_d1, int n);
 /* k eager device-driven steps with HIP events around each launch of one kernel kind (0 LM head,
  * 1 experts gate/up, 2 down, 3 projections, 4 mixer out, 5 delta-net, 6 router, 7 scores, 8 pv,

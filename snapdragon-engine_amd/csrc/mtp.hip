@@ -1,9 +1,10 @@
-// MTP depth-1 speculative decoding (crates/model/src/mtp.rs:314-608, MtpDriver with depth 1):
-//  * a host-driven driver with the reference's semantics (catch-up pairs, draft, 2-lane verify,
-//    greedy accept, commit, rewind) over the engine's host-driven calls, and
-//  * the device-driven step: the same state machine held in device memory (MtpState), one step
-//    = seed (if a pair is pending) -> draft -> verify -> accept/commit, all decided on the GPU and
-//    captured once as a HIP graph; K steps are K graph launches with no host round-trip.
+// MTP speculative decoding (crates/model/src/mtp.rs:314-608, MtpDriver):
+//  * a host-driven driver with the reference's semantics (catch-up pairs, draft chain, verify,
+//    greedy accept, commit, rewind) over the engine's host-driven calls, depth 1..3, and
+//  * the device-driven step at depth 1 or 2: the same state machine held in device memory
+//    (MtpState), one step = seed (the pending pairs) -> draft(s) -> verify -> accept/commit, all
+//    decided on the GPU and captured once as a HIP graph; K steps are K graph launches with no host
+//    round-trip.
 #include <hip/hip_runtime.h>
 
 #include <cstring>
@@ -141,6 +142,185 @@ __global__ void mtp_commit_kernel(MtpState *ms, const unsigned long long *keys, 
         ms->accepted += a;
         *cs = seed_ctl(ms);
         *cd = draft_ctl(ms, n_ctx);
+    }
+}
+
+// ---- the device-driven step at depth 2 (mtp.rs:522-592 with k = 2) --------------------------------
+// seed (the pending pairs, up to 2) -> draft 1 (x, hl) at p -> draft 2 (d1, draft 1's MTP h) at p + 1
+// -> verify piece 1 (x, d1) at p, p + 1 -> commit 1 -> verify piece 2 (d2 at p + 2; active when d1
+// was accepted and d2 equals piece 1's second argmax) -> commit 2. The reference's 3-lane verify runs
+// as these two pieces (the kernels' lane count), committed one after the other and stopped at the
+// first rejected draft, as the host driver's step_k does. Every run reads ctl, written just before it.
+
+// draft i of the current step, or the test hook's forced value (force[steps * 2 + i] >= 0)
+__device__ uint32_t forced2(const MtpState *ms, const int32_t *force, int force_n, int i, uint32_t d) {
+    const int j = ms->steps * 2 + i;
+    return (force && j < force_n && force[j] >= 0) ? (uint32_t)force[j] : d;
+}
+
+__global__ void mtp2_prep_seed_kernel(MtpState *ms, RunCtl *ctl) {
+    const int np = ms->pending;
+    RunCtl r{};
+    r.nl = np > 1 ? 2 : 1;
+    r.pos0 = ms->pos - np;
+    r.cur = ms->cur;
+    r.tok[0] = ms->pend_tok;
+    r.tok[1] = ms->pend_tok2;
+    r.hin_sel[0] = HID_PEND;
+    r.hin_sel[1] = HID_PEND2;
+    r.head_mask = 0;
+    r.active = np > 0 && ms->err == 0;
+    *ctl = r;
+}
+
+__global__ void mtp2_prep_draft1_kernel(MtpState *ms, RunCtl *ctl, int n_ctx) {
+    if (ms->pos + 3 > n_ctx) ms->err |= 2;  // no room for the 3 positions of a depth-2 step: stop
+    RunCtl r{};
+    r.nl = 1;
+    r.pos0 = ms->pos;
+    r.cur = ms->cur;
+    r.tok[0] = ms->x;
+    r.hin_sel[0] = HID_HL;
+    r.head_mask = 1;
+    r.active = ms->err == 0;
+    *ctl = r;
+}
+
+// d1 from draft 1's argmax; draft 1's MTP h (hid[0]) kept in HID_M as draft 2's input
+__global__ void mtp2_prep_draft2_kernel(MtpState *ms, RunCtl *ctl, const unsigned long long *keys, int nkeys, float *hid,
+                                        const int32_t *force, int force_n) {
+    const int t = threadIdx.x;
+    if (t < 64) {
+        const unsigned long long k0 = wave_key_max(keys, nkeys);
+        if (t == 0) {
+            const uint32_t d1 = forced2(ms, force, force_n, 0, decode_key(k0));
+            ms->d1 = d1;
+            RunCtl r{};
+            r.nl = 1;
+            r.pos0 = ms->pos + 1;
+            r.cur = ms->cur;
+            r.tok[0] = d1;
+            r.hin_sel[0] = HID_M;
+            r.head_mask = 1;
+            r.active = ms->err == 0;
+            *ctl = r;
+        }
+    }
+    for (int i = t; i < E; i += blockDim.x) hid[(int64_t)HID_M * E + i] = hid[i];
+}
+
+__global__ void mtp2_prep_verify1_kernel(MtpState *ms, RunCtl *ctl, const unsigned long long *keys, int nkeys,
+                                         const int32_t *force, int force_n) {
+    const unsigned long long k0 = wave_key_max(keys, nkeys);
+    if (threadIdx.x != 0) return;
+    ms->d2 = forced2(ms, force, force_n, 1, decode_key(k0));
+    RunCtl r{};
+    r.nl = 2;
+    r.pos0 = ms->pos;
+    r.cur = ms->cur;
+    r.tok[0] = ms->x;
+    r.tok[1] = ms->d1;
+    r.head_mask = 3;
+    r.hin_sel[0] = HID_HL;
+    r.hin_sel[1] = HID_PEND;
+    r.active = ms->err == 0;
+    *ctl = r;
+}
+
+// piece 1: lane 0 is committed; lane 1 when d1 == g0 (else its V^T column goes back to +0). The
+// pairs of the committed drafts wait for seeding (note_with: (d1, h after x), (d2, h after d1)).
+// Writes piece 2's control block: d2 at p + 2 when d1 was accepted and d2 == g1.
+__global__ void mtp2_commit1_kernel(MtpState *ms, RunCtl *ctl, const unsigned long long *keys, int nkeys, float *hid,
+                                    uint16_t *vcache, int64_t vrows, int n_ctx, uint32_t *out_tok, int out_cap) {
+    __shared__ int s_a, s_p2, s_ok, s_pos0;
+    __shared__ uint32_t s_g[2];
+    const int t = threadIdx.x;
+    if (t < 64) {
+        const unsigned long long k0 = wave_key_max(keys, nkeys), k1 = wave_key_max(keys + nkeys, nkeys);
+        if (t == 0) {
+            s_g[0] = decode_key(k0);
+            s_g[1] = decode_key(k1);
+            s_ok = ms->err == 0;
+            s_a = s_ok && ms->d1 == s_g[0];
+            s_p2 = s_a && ms->d2 == s_g[1];
+            s_pos0 = ms->pos;
+        }
+    }
+    __syncthreads();
+    if (!s_ok) {
+        if (t == 0) {
+            ms->piece2 = 0;
+            RunCtl r{};
+            r.nl = 1;
+            r.active = 0;
+            *ctl = r;
+        }
+        return;
+    }
+    const int a = s_a, p2 = s_p2, pos0 = s_pos0;
+    for (int i = t; i < E; i += blockDim.x) {
+        const float h0 = hid[i], h1 = hid[E + i];
+        if (!a) hid[(int64_t)HID_HL * E + i] = h0;
+        if (a) hid[(int64_t)HID_PEND * E + i] = h0;
+        if (a && !p2) hid[(int64_t)HID_HL * E + i] = h1;
+        if (p2) hid[(int64_t)HID_PEND2 * E + i] = h1;
+    }
+    if (!a)
+        for (int64_t r = t; r < vrows; r += blockDim.x) vcache[r * n_ctx + pos0 + 1] = 0;
+    if (t == 0) {
+        int n = ms->n_out;
+        if (n < out_cap) out_tok[n++] = s_g[0];
+        if (a && n < out_cap) out_tok[n++] = s_g[1];
+        ms->n_out = n;
+        ms->pending = a ? 1 + p2 : 0;
+        ms->pend_tok = ms->d1;
+        ms->pend_tok2 = ms->d2;
+        ms->pos = pos0 + a + 1;
+        ms->cur = (ms->cur + a + 1) % OXE_NSLOTS;
+        ms->piece2 = p2;
+        if (!p2) {
+            ms->x = a ? s_g[1] : s_g[0];
+            ms->steps += 1;
+            ms->accepted += a;
+        }
+        RunCtl r{};
+        r.nl = 1;
+        r.pos0 = ms->pos;
+        r.cur = ms->cur;
+        r.tok[0] = ms->d2;
+        r.head_mask = 1;
+        r.hin_sel[0] = HID_HL;
+        r.active = p2;
+        *ctl = r;
+    }
+}
+
+// piece 2 (one lane, always committed): g2 is the bonus token, hl the h after d2
+__global__ void mtp2_commit2_kernel(MtpState *ms, const unsigned long long *keys, int nkeys, float *hid, uint32_t *out_tok,
+                                    int out_cap) {
+    __shared__ int s_on;
+    __shared__ uint32_t s_g;
+    const int t = threadIdx.x;
+    if (t < 64) {
+        const unsigned long long k0 = wave_key_max(keys, nkeys);
+        if (t == 0) {
+            s_on = ms->piece2 != 0 && ms->err == 0;
+            s_g = decode_key(k0);
+        }
+    }
+    __syncthreads();
+    if (!s_on) return;
+    for (int i = t; i < E; i += blockDim.x) hid[(int64_t)HID_HL * E + i] = hid[i];
+    if (t == 0) {
+        int n = ms->n_out;
+        if (n < out_cap) out_tok[n++] = s_g;
+        ms->n_out = n;
+        ms->x = s_g;
+        ms->pos += 1;
+        ms->cur = (ms->cur + 1) % OXE_NSLOTS;
+        ms->piece2 = 0;
+        ms->steps += 1;
+        ms->accepted += 2;
     }
 }
 
@@ -351,8 +531,13 @@ int MtpDriverHost::rewind(Engine &e, int m) {
 // device-driven: hand the host driver state to the device, run K graph steps, read it back
 int MtpDriverHost::dev_begin(Engine &e, uint32_t x) {
     last_n = 0;  // rewind applies to host-driven steps only
-    int rc = flush(e, 0);  // at most the pair the next step seeds stays pending: none here
+    int rc = flush(e, 0);  // at most the pairs the next step seeds stay pending: none here
     if (rc) return rc;
+    if (e.dev_depth != depth) {  // a captured step is for one depth
+        if (e.graph_exec) (void)hipGraphExecDestroy(e.graph_exec);
+        e.graph_exec = nullptr;
+        e.dev_depth = depth;
+    }
     MtpState s{};
     s.pos = e.pos;
     s.cur = e.cur;
@@ -378,18 +563,25 @@ int MtpDriverHost::dev_end(Engine &e, uint32_t *out_tok, int cap, int *n_out, ui
     if (hipMemcpy(hl.data(), e.b.hid + (size_t)HID_HL * E, (size_t)E * 4, hipMemcpyDeviceToHost) != hipSuccess) return -2;
     cu_tok.clear();
     cu_h.clear();
-    if (s.pending) {
-        cu_tok.push_back(s.pend_tok);
-        cu_h.resize(E);
-        if (hipMemcpy(cu_h.data(), e.b.hid + (size_t)HID_PEND * E, (size_t)E * 4, hipMemcpyDeviceToHost) != hipSuccess) return -2;
+    const int np = std::max(0, std::min(s.pending, 2));
+    if (np > 0) {
+        const uint32_t pt[2] = {s.pend_tok, s.pend_tok2};
+        const int hb[2] = {HID_PEND, HID_PEND2};
+        cu_h.resize((size_t)np * E);
+        for (int i = 0; i < np; i++) {
+            cu_tok.push_back(pt[i]);
+            if (hipMemcpy(cu_h.data() + (size_t)i * E, e.b.hid + (size_t)hb[i] * E, (size_t)E * 4, hipMemcpyDeviceToHost) !=
+                hipSuccess)
+                return -2;
+        }
     }
-    q = s.pos - (s.pending ? 1 : 0);
+    q = s.pos - np;
     e.pos = s.pos;
     e.cur = s.cur;
     e.pend_n = 0;
     steps += s.steps;
     accepted += s.accepted;
-    drafted += s.steps;   // one draft per device-driven step
+    drafted += (int64_t)s.steps * e.dev_depth;   // dev_depth drafts per device-driven step
     return s.err ? -4 : 0;
 }
 
@@ -412,15 +604,36 @@ void Engine::enqueue_mtp_device_step() {
                        m.vcache, (int64_t)n_att_main * NKV * HD, m.n_ctx, out_tok, out_cap, ctl_seed, ctl_draft);
 }
 
+void Engine::enqueue_mtp_device_step2() {
+    const int32_t *force = (const int32_t *)force_d1;
+    hipLaunchKernelGGL(mtp2_prep_seed_kernel, dim3(1), dim3(1), 0, st, mtp_state, ctl);
+    enqueue_mtp_seed();
+    hipLaunchKernelGGL(mtp2_prep_draft1_kernel, dim3(1), dim3(1), 0, st, mtp_state, ctl, m.n_ctx);
+    enqueue_mtp_run();
+    hipLaunchKernelGGL(mtp2_prep_draft2_kernel, dim3(1), dim3(256), 0, st, mtp_state, ctl, keys(), nkeys(), b.hid, force,
+                       force_n);
+    enqueue_mtp_run();
+    hipLaunchKernelGGL(mtp2_prep_verify1_kernel, dim3(1), dim3(64), 0, st, mtp_state, ctl, keys(), nkeys(), force, force_n);
+    enqueue_verify();
+    hipLaunchKernelGGL(mtp2_commit1_kernel, dim3(1), dim3(256), 0, st, mtp_state, ctl, keys(), nkeys(), b.hid, m.vcache,
+                       (int64_t)n_att_main * NKV * HD, m.n_ctx, out_tok, out_cap);
+    enqueue_verify();
+    hipLaunchKernelGGL(mtp2_commit2_kernel, dim3(1), dim3(256), 0, st, mtp_state, keys(), nkeys(), b.hid, out_tok, out_cap);
+}
+
 int Engine::mtp_steps_async(int k, bool use_graph) {
     if (!use_graph) {
-        for (int i = 0; i < k; i++) enqueue_mtp_device_step();
+        for (int i = 0; i < k; i++) {
+            if (dev_depth == 2) enqueue_mtp_device_step2();
+            else enqueue_mtp_device_step();
+        }
         return hipGetLastError() == hipSuccess ? 0 : -2;
     }
     if (!graph_exec) {
         if (hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal) != hipSuccess) return -2;
         fz_capturing = true;
-        enqueue_mtp_device_step();
+        if (dev_depth == 2) enqueue_mtp_device_step2();
+        else enqueue_mtp_device_step();
         fz_capturing = false;
         hipGraph_t g;
         if (hipStreamEndCapture(st, &g) != hipSuccess) return -2;
@@ -428,7 +641,7 @@ int Engine::mtp_steps_async(int k, bool use_graph) {
         (void)hipGraphDestroy(g);
     }
     for (int i = 0; i < k; i++) {
-        if (fused) fz_account(3);   // seed, draft and verify launches of one step
+        if (fused) fz_account(dev_depth == 2 ? 5 : 3);   // seed, draft(s) and verify launches of one step
         if (hipGraphLaunch(graph_exec, st) != hipSuccess) return -2;
     }
     return 0;
@@ -523,8 +736,8 @@ int oxe_mtp_set_force(oxe_engine *e, const int32_t *force_d1, int n) {
 int oxe_mtp_device_begin(oxe_engine *e, uint32_t x, int out_cap) {
     Engine *g = (Engine *)e;
     if (out_cap < 1 || !g->toks_ok(&x, 1)) return -1;
-    if (g->drv.depth != 1) {
-        oxe::set_err("device-driven MTP steps are depth 1");
+    if (g->drv.depth != 1 && g->drv.depth != 2) {
+        oxe::set_err("device-driven MTP steps are depth 1 or 2");
         return -1;
     }
     if (g->ensure_out(out_cap)) return -3;

@@ -42,24 +42,31 @@ struct RunCtl {
     int32_t pad;
 };
 
-// Device-driven MTP depth-1 state (crates/model/src/mtp.rs:314-340 MtpDriver, depth 1)
+// Device-driven MTP state (crates/model/src/mtp.rs:314-340 MtpDriver, depth 1 or 2)
 struct MtpState {
     int32_t pos;         // committed position P (tokens in the target)
     int32_t cur;         // current recurrent slot
     uint32_t x;          // next token (not yet in the target)
-    int32_t pending;     // 1: pair (pend_tok, hidden buffer HID_PEND) waits for MTP seeding at pos-1
-    uint32_t pend_tok;
+    int32_t pending;     // pairs waiting for MTP seeding at pos - pending .. pos - 1 (0..depth):
+    uint32_t pend_tok;   // (pend_tok, hidden buffer HID_PEND), then (pend_tok2, HID_PEND2)
     int32_t n_out;       // tokens emitted so far (ring position in out_tok)
     int32_t steps, accepted;
-    uint32_t d1;         // draft of the current step
-    int32_t err;         // sticky error bits (1: context full)
+    uint32_t d1;         // drafts of the current step
+    int32_t err;         // sticky error bits (1: context full; 2: no room for a depth-2 step)
+    uint32_t pend_tok2;
+    uint32_t d2;
+    int32_t piece2;      // depth 2: the current step verifies d2 in a second piece
+    int32_t pad;
 };
 
-// hidden-state buffers ([OXE_NL + 2][n_embd] floats): 0..NL-1 h_nextn per lane of the last run,
-// HID_HL the target h of position pos-1 (MtpDriver.hl), HID_PEND the pending catch-up pair's h.
+// hidden-state buffers ([HID_N][n_embd] floats): 0..NL-1 h_nextn per lane of the last run, HID_HL
+// the target h of position pos-1 (MtpDriver.hl), HID_PEND / HID_PEND2 the pending catch-up pairs'
+// h, HID_M the first draft run's MTP h (the second draft's input at depth 2).
 constexpr int HID_HL = OXE_NL;
 constexpr int HID_PEND = OXE_NL + 1;
-constexpr int HID_N = OXE_NL + 2;
+constexpr int HID_PEND2 = OXE_NL + 2;
+constexpr int HID_M = OXE_NL + 3;
+constexpr int HID_N = OXE_NL + 4;
 
 struct LayerW {
     int att = 0;    // 1: full attention (+ MTP block), 0: gated delta-net

@@ -28,7 +28,7 @@ struct Engine;
 struct Gguf;
 
 // MtpDriver (crates/model/src/mtp.rs:314-608), host-driven, depth 1..MTP_MAX_DEPTH; dev_begin /
-// dev_end hand its state to and from the device-driven step (depth 1).
+// dev_end hand its state to and from the device-driven step (depth 1 or 2).
 constexpr int MTP_MAX_DEPTH = 3;
 struct MtpDriverHost {
     int depth = 1;               // drafts per step (MtpDriver.depth)
@@ -136,7 +136,9 @@ struct Engine {
         (void)hipEventRecord(probe_ev[probe_used++], st);
     }
 
+    int dev_depth = 1;   // drafts per device-driven step (1 or 2), set by dev_begin
     void enqueue_mtp_device_step();
+    void enqueue_mtp_device_step2();
     int mtp_steps_async(int k, bool use_graph);
     int ensure_out(int cap) {
         if (cap <= out_cap) return 0;

@@ -677,7 +677,7 @@ class Engine:
         return buf[:n].reshape(-1, 2048, 4)
 
     def mtp_set_depth(self, depth):
-        """drafts per host-driven MTP step (MtpDriver.depth; the device-driven step is depth 1)"""
+        """drafts per MTP step (MtpDriver.depth): host-driven steps 1..3, device-driven steps 1 or 2"""
         check(lib().oxe_mtp_set_depth(self.h, depth), "mtp_set_depth")
 
     def mtp_step_force(self, x, force):

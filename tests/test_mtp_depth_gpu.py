@@ -130,6 +130,87 @@ def test_server_spec_depth(setup):
             assert np.array_equal(sp.decode(t).view(np.uint32), r.view(np.uint32))
         x = int(np.argmax(rows[-1]))
     g = A.Engine(d, seed=SEED, n_ctx=N_CTX)
-    g.mtp_set_depth(2)
+    g.mtp_set_depth(3)   # the device-driven step runs depth 1 or 2
     with pytest.raises(RuntimeError):
         g.mtp_device_begin(plain[0], 8)
+
+
+def depth2_engine(d, mode):
+    import oxe_amd as A
+    g = A.Engine(d, seed=SEED, n_ctx=N_CTX)
+    if mode == "per_phase":
+        g.set_fused(False)
+    elif not g.fused:
+        g.close()
+        pytest.skip("the fused run kernel needs a 256-CU device")
+    g.mtp_set_depth(2)
+    return g
+
+
+@pytest.mark.parametrize("mode", ["fused", "per_phase"])
+def test_device_depth2_forced_matches_oracle(setup, mode):
+    """Device-driven depth-2 steps (two drafts, verify pieces (x, d1) then (d2), all decided on the
+    GPU) with forced drafts through every acceptance count, against the oracle's depth-2 driver:
+    tokens, counters and position; then host-driven steps continue from the handed-back state (its
+    pending catch-up pairs) exactly as the oracle's driver does."""
+    d, prompt, plain = setup
+    g = depth2_engine(d, mode)
+    o = O.Engine(d, seed=SEED, n_ctx=N_CTX, lanes=3)
+    od = O.Driver(o, 2)
+    x = g.mtp_prefill(prompt)
+    assert od.prefill(prompt) == x == plain[0]
+    pattern = [2, 0, 1, 2, 1, 0, 2, 2, 1, 1]
+    forces, want, k, xo = [], [], 0, x
+    for a in pattern:
+        f = forces_for(plain, k, a, 2, d.n_vocab)
+        forces += f
+        ro = od.step(xo, force=f)
+        assert ro == plain[k + 1: k + 2 + a]
+        want += ro
+        k += a + 1
+        xo = ro[-1]
+    g.mtp_set_force(forces)
+    g.mtp_device_begin(x, 64)
+    g.mtp_device_steps(len(pattern), use_graph=True)
+    toks, nx = g.mtp_device_end(64)
+    assert toks == want
+    assert nx == xo
+    st, so = g.mtp_stats(), od.stats()
+    assert (st["steps"], st["drafted"], st["accepted"]) == (so["steps"], so["drafted"], so["accepted"])
+    assert g.pos == o.pos
+    g.mtp_set_force([])
+    for _ in range(3):
+        rg, ro = g.mtp_step_force(nx, []), od.step(xo, force=[])
+        assert rg == ro == plain[k + 1: k + 1 + len(rg)]
+        k += len(rg)
+        nx, xo = rg[-1], ro[-1]
+    assert np.array_equal(np.asarray(g.hidden(0), np.float32).view(np.uint32), o.hidden(0).view(np.uint32))
+    g.close()
+    o.close()
+
+
+@pytest.mark.parametrize("mode", ["fused", "per_phase"])
+def test_device_depth2_natural_drafts(setup, mode):
+    """Unforced device-driven depth-2 steps (the head's own drafts): eager and graph launches agree,
+    and both equal the oracle's depth-2 driver and plain greedy decoding."""
+    d, prompt, plain = setup
+    o = O.Engine(d, seed=SEED, n_ctx=N_CTX, lanes=3)
+    od = O.Driver(o, 2)
+    xo = od.prefill(prompt)
+    want = []
+    for _ in range(6):
+        ro = od.step(xo, force=[])
+        want += ro
+        xo = ro[-1]
+    o.close()
+    for use_graph in (False, True):
+        g = depth2_engine(d, mode)
+        x = g.mtp_prefill(prompt)
+        g.mtp_device_begin(x, 64)
+        g.mtp_device_steps(6, use_graph=use_graph)
+        toks, nx = g.mtp_device_end(64)
+        assert toks == want == plain[1:1 + len(want)]
+        assert nx == xo
+        assert g.mtp_stats()["drafted"] == 12
+        g.close()
+
