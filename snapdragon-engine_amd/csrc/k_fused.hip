@@ -630,6 +630,7 @@ struct HeadSm {
     NormSm ns;
     GSm<E, HEAD_TR, NL> g;
     unsigned long long key[FT / 64][NL];
+    int64_t claim[4];   // first tile of claimed pair k in claim[k & 3]
 };
 template <int NL>
 struct EntrySm {
@@ -2066,7 +2067,15 @@ FZ_PHASE bool phase_head(const RunCtl *ctl, const FusedArgs *ap, const float *no
     const int64_t V = a.m.output.rows;
     constexpr int TR = HEAD_TR;                              // rows per tile
     const int64_t ntiles = (V + TR - 1) / TR;
-    const int64_t t0 = ntiles * c.b / c.G, t1 = ntiles * (c.b + 1) / c.G;
+    // Tiles: `per` (even) in a contiguous range per workgroup, then pairs of the remaining tiles
+    // claimed from a counter, so the workgroups that stream faster take more of the tail (the HBM
+    // gives some XCDs' CUs less than others). Fewer than 4 tiles per workgroup: a static split only.
+#ifndef FZ_HEAD_SPCT
+#define FZ_HEAD_SPCT 90
+#endif
+    const int64_t per = 2 * ((ntiles * FZ_HEAD_SPCT / 100) / (2 * c.G));
+    const bool dyn = per >= 4;
+    const int64_t t0 = dyn ? per * c.b : ntiles * c.b / c.G, t1 = dyn ? t0 + per : ntiles * (c.b + 1) / c.G;
     WSlice<E, HEAD_P> A, B;
     auto rows_of = [&](int64_t tile) { const int64_t r = V - tile * TR; return (int)(r < TR ? r : TR); };
     if (t0 < t1) wload<E, HEAD_P>(A, a.m.output.q, a.m.output.d, rows_of(t0), [&](int rl) { return t0 * TR + rl; });
@@ -2098,12 +2107,42 @@ FZ_PHASE bool phase_head(const RunCtl *ctl, const FusedArgs *ap, const float *no
             if (v > best) { best = v; bi = row; }
         }
     };
-    for (int64_t tile = t0; tile < t1; tile += 2) {
-        const int64_t tb = tile + 1 < t1 ? tile + 1 : t1 - 1, ta = tile + 2 < t1 ? tile + 2 : t1 - 1;
-        wload<E, HEAD_P, true>(B, a.m.output.q, a.m.output.d, rows_of(tb), [&](int r) { return tb * TR + r; });
-        dot_tile(A, tile);
-        wload<E, HEAD_P, true>(A, a.m.output.q, a.m.output.d, rows_of(ta), [&](int r) { return ta * TR + r; });
-        if (tile + 1 < t1) dot_tile(B, tile + 1);
+    if (!dyn) {
+        for (int64_t tile = t0; tile < t1; tile += 2) {
+            const int64_t tb = tile + 1 < t1 ? tile + 1 : t1 - 1, ta = tile + 2 < t1 ? tile + 2 : t1 - 1;
+            wload<E, HEAD_P, true>(B, a.m.output.q, a.m.output.d, rows_of(tb), [&](int r) { return tb * TR + r; });
+            dot_tile(A, tile);
+            wload<E, HEAD_P, true>(A, a.m.output.q, a.m.output.d, rows_of(ta), [&](int r) { return ta * TR + r; });
+            if (tile + 1 < t1) dot_tile(B, tile + 1);
+        }
+    } else {
+        // the i-th tile of this workgroup: i < per its own, then pair k = (i - per) / 2 of its claims
+        // (tiles ns + d, ns + d + 1 for the counter's value d), -1 past the last tile. Claim k is
+        // issued by thread 0 two iterations before pair k is reached (at i = per + 2 k - 4), its value
+        // written to LDS mid-iteration and published by the next barrier; every claim issued is read
+        // before the workgroup leaves, so no atomic is in flight at the launch's end (when the last
+        // workgroup out clears the counter). Tiles are visited in increasing order (claims increase).
+        const int64_t ns = per * c.G;
+        uint32_t *hq = a.sync + FZ_W_HEADQ;
+        auto seq = [&](int64_t i) -> int64_t {
+            if (i < per) return t0 + i;
+            const int64_t f = s.claim[((i - per) >> 1) & 3] + ((i - per) & 1);
+            return f < ntiles ? f : -1;
+        };
+        uint32_t rv = 0;
+        for (int64_t i = 0;; i += 2) {
+            const int64_t tc = seq(i);
+            if (tc < 0) break;
+            const bool claim = i >= per - 4;
+            if (claim && t == 0) rv = __hip_atomic_fetch_add(hq, 2u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            const int64_t sb = seq(i + 1), sa = seq(i + 2);
+            const int64_t tb = sb < 0 ? tc : sb, ta = sa < 0 ? tb : sa;   // past the end: a reload
+            wload<E, HEAD_P, true>(B, a.m.output.q, a.m.output.d, rows_of(tb), [&](int r) { return tb * TR + r; });
+            dot_tile(A, tc);
+            if (claim && t == 0) s.claim[((i - per + 4) >> 1) & 3] = ns + (int64_t)rv;
+            wload<E, HEAD_P, true>(A, a.m.output.q, a.m.output.d, rows_of(ta), [&](int r) { return ta * TR + r; });
+            if (sb >= 0) dot_tile(B, tb);
+        }
     }
     // per-lane key of this workgroup: the largest value, then the smallest row
     unsigned long long key = 0ull;
@@ -2199,6 +2238,7 @@ __global__ __launch_bounds__(fz::FT, 1) void fused_kernel(const RunCtl *__restri
         const uint32_t old = __hip_atomic_fetch_add(sync + FZ_W_DONE, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if (old == gridDim.x - 1) {
             cst32(sync + FZ_W_DONE, 0u);
+            cst32(sync + FZ_W_HEADQ, 0u);
             cst32(sync + FZ_W_FLAG, base + FZ_TAG_STRIDE);
         }
     }

@@ -36,6 +36,7 @@ enum FusedMode { FM_VERIFY = 0, FM_DRAFT = 1, FM_SEED = 2 };
 // the sticky error word at [320]
 constexpr int FZ_SYNC_WORDS = 384;
 constexpr int FZ_W_DONE = 256, FZ_W_FLAG = 288, FZ_W_ERR = 320;
+constexpr int FZ_W_HEADQ = 352;   // the LM head's tile-pair counter (cleared by the last workgroup out)
 constexpr uint32_t FZ_TAG_STRIDE = 1024;   // > 8 phases x (n_layer + 2)
 
 // Tagged exchange buffers of the fused kernel. Every 32-bit value one workgroup passes to another
