@@ -2,9 +2,9 @@
 //  * a host-driven driver with the reference's semantics (catch-up pairs, draft chain, verify,
 //    greedy accept, commit, rewind) over the engine's host-driven calls, depth 1..3, and
 //  * the device-driven step at depth 1 or 2: the same state machine held in device memory
-//    (MtpState), one step = seed (the pending pairs) -> draft(s) -> verify -> accept/commit, all
-//    decided on the GPU and captured once as a HIP graph; K steps are K graph launches with no host
-//    round-trip.
+//    (MtpState), one step = draft(s) (depth 1: with the pending pair as an extra lane; depth 2: after
+//    a seeding run) -> verify -> accept/commit, all decided on the GPU and captured once as a HIP
+//    graph; K steps are K graph launches with no host round-trip.
 #include <hip/hip_runtime.h>
 
 #include <cstring>
@@ -24,41 +24,32 @@ OXE_HOST_DEV_INLINE uint32_t decode_key(unsigned long long k) { return k == 0 ? 
 
 // ---- device-driven step kernels ----------------------------------------------------------------
 
-// the seed run's control block of the step about to start: active when a pair is pending
-__device__ RunCtl seed_ctl(const MtpState *ms) {
-    RunCtl r{};
-    r.nl = 1;
-    r.pos0 = ms->pos - 1;
-    r.cur = ms->cur;
-    r.tok[0] = ms->pend_tok;
-    r.hin_sel[0] = HID_PEND;
-    r.head_mask = 0;
-    r.active = ms->pending != 0 && ms->err == 0;
-    return r;
-}
-
-// the draft run's: inactive when the 2-lane verify has no room (the step then stops the driver, as
-// the reference's k = 0; mtp_prep_verify_kernel records it)
+// The draft run's control block of the step about to start. A pending catch-up pair (the accepted
+// draft of the previous step with the target h before it) rides along as lane 0 at pos - 1 and the
+// draft (x, hl) is the last lane: the pair's MTP K / V rows are written by the same run that reads
+// them (lanes are independent but for the attention over earlier positions, which includes the
+// run's own rows), as the reference's batched MTP call takes its pending pairs with the draft. Only
+// the last lane's LM-head argmax is wanted. Inactive when the 2-lane verify has no room (the step
+// then stops the driver, as the reference's k = 0; mtp_prep_verify_kernel records it).
 __device__ RunCtl draft_ctl(const MtpState *ms, int n_ctx) {
+    const int np = ms->pending != 0 ? 1 : 0;
     RunCtl r{};
-    r.nl = 1;
-    r.pos0 = ms->pos;
+    r.nl = 1 + np;
+    r.pos0 = ms->pos - np;
     r.cur = ms->cur;
-    r.tok[0] = ms->x;
-    r.hin_sel[0] = HID_HL;
-    r.head_mask = 1;
+    r.tok[0] = np ? ms->pend_tok : ms->x;
+    r.tok[1] = ms->x;
+    r.hin_sel[0] = np ? HID_PEND : HID_HL;
+    r.hin_sel[1] = HID_HL;
+    r.head_mask = 1 << np;
     r.active = ms->err == 0 && ms->pos + 2 <= n_ctx;
     return r;
 }
 
-// per-phase runs: the step's seed and draft runs read ctl, one after the other
-__global__ void mtp_prep_seed_kernel(MtpState *ms, RunCtl *ctl) { *ctl = seed_ctl(ms); }
+// per-phase runs: the draft run reads ctl
 __global__ void mtp_prep_draft_kernel(MtpState *ms, RunCtl *ctl, int n_ctx) { *ctl = draft_ctl(ms, n_ctx); }
-// fused runs: both control blocks of the first step (the commit kernel fills them for the next)
-__global__ void mtp_prep_step_kernel(MtpState *ms, RunCtl *cs, RunCtl *cd, int n_ctx) {
-    *cs = seed_ctl(ms);
-    *cd = draft_ctl(ms, n_ctx);
-}
+// fused runs: the first step's draft control block (the commit kernel fills it for the next)
+__global__ void mtp_prep_step_kernel(MtpState *ms, RunCtl *cd, int n_ctx) { *cd = draft_ctl(ms, n_ctx); }
 
 // the largest of n argmax keys (one wave: lanes stride the keys, then a shuffle tree)
 __device__ unsigned long long wave_key_max(const unsigned long long *keys, int n) {
@@ -73,7 +64,7 @@ __device__ unsigned long long wave_key_max(const unsigned long long *keys, int n
 
 __global__ void mtp_prep_verify_kernel(MtpState *ms, RunCtl *ctl, const unsigned long long *keys, int nkeys,
                                        const int32_t *force_d1, int force_n, int n_ctx) {
-    const unsigned long long k0 = wave_key_max(keys, nkeys);
+    const unsigned long long k0 = wave_key_max(keys + (ms->pending != 0 ? nkeys : 0), nkeys);  // the draft's lane
     if (threadIdx.x != 0) return;
     if (ms->pos + 2 > n_ctx) ms->err |= 1;  // no room for the 2-lane verify: stop (reference: k = 0)
     uint32_t d1 = decode_key(k0);
@@ -93,9 +84,9 @@ __global__ void mtp_prep_verify_kernel(MtpState *ms, RunCtl *ctl, const unsigned
 }
 
 // accept / commit / note (mtp.rs:564-591, engine.rs:2030-2039): a = (d1 == argmax lane 0)
-// Then the next step's seed and draft control blocks (cs, cd), from the updated state.
+// Then the next step's draft control block (cd), from the updated state.
 __global__ void mtp_commit_kernel(MtpState *ms, const unsigned long long *keys, int nkeys, float *hid, uint16_t *vcache,
-                                  int64_t vrows, int n_ctx, uint32_t *out_tok, int out_cap, RunCtl *cs, RunCtl *cd) {
+                                  int64_t vrows, int n_ctx, uint32_t *out_tok, int out_cap, RunCtl *cd) {
     __shared__ int s_a, s_ok, s_pos0;
     __shared__ uint32_t s_g[2];
     const int t = threadIdx.x;
@@ -111,10 +102,7 @@ __global__ void mtp_commit_kernel(MtpState *ms, const unsigned long long *keys, 
     }
     __syncthreads();
     if (!s_ok) {
-        if (t == 0) {
-            *cs = seed_ctl(ms);
-            *cd = draft_ctl(ms, n_ctx);
-        }
+        if (t == 0) *cd = draft_ctl(ms, n_ctx);
         return;
     }
     const int a = s_a, pos0 = s_pos0;
@@ -140,7 +128,6 @@ __global__ void mtp_commit_kernel(MtpState *ms, const unsigned long long *keys, 
         ms->cur = (ms->cur + a + 1) % OXE_NSLOTS;
         ms->steps += 1;
         ms->accepted += a;
-        *cs = seed_ctl(ms);
         *cd = draft_ctl(ms, n_ctx);
     }
 }
@@ -546,7 +533,7 @@ int MtpDriverHost::dev_begin(Engine &e, uint32_t x) {
     s.n_out = 0;
     if (hipMemcpyAsync(e.mtp_state, &s, sizeof(s), hipMemcpyHostToDevice, e.st) != hipSuccess) return -2;
     if (hipMemcpyAsync(e.b.hid + (size_t)HID_HL * E, hl.data(), (size_t)E * 4, hipMemcpyHostToDevice, e.st) != hipSuccess) return -2;
-    hipLaunchKernelGGL(mtp_prep_step_kernel, dim3(1), dim3(1), 0, e.st, e.mtp_state, e.ctl_seed, e.ctl_draft, e.m.n_ctx);
+    hipLaunchKernelGGL(mtp_prep_step_kernel, dim3(1), dim3(1), 0, e.st, e.mtp_state, e.ctl_draft, e.m.n_ctx);
     return hipStreamSynchronize(e.st) == hipSuccess ? 0 : -2;
 }
 
@@ -587,13 +574,10 @@ int MtpDriverHost::dev_end(Engine &e, uint32_t *out_tok, int cap, int *n_out, ui
 
 void Engine::enqueue_mtp_device_step() {
     if (fused) {
-        // the seed and draft runs read their own control blocks, filled by the previous step's
-        // commit (or dev_begin): two launches fewer per step
-        enqueue_mtp_seed(ctl_seed);
+        // the draft run (with the pending pair, if any) reads its own control block, filled by the
+        // previous step's commit (or dev_begin)
         enqueue_mtp_run(ctl_draft);
     } else {
-        hipLaunchKernelGGL(mtp_prep_seed_kernel, dim3(1), dim3(1), 0, st, mtp_state, ctl);
-        enqueue_mtp_seed();
         hipLaunchKernelGGL(mtp_prep_draft_kernel, dim3(1), dim3(1), 0, st, mtp_state, ctl, m.n_ctx);
         enqueue_mtp_run();
     }
@@ -601,7 +585,7 @@ void Engine::enqueue_mtp_device_step() {
                        (const int32_t *)force_d1, force_n, m.n_ctx);
     enqueue_verify();
     hipLaunchKernelGGL(mtp_commit_kernel, dim3(1), dim3(256), 0, st, mtp_state, keys(), nkeys(), b.hid,
-                       m.vcache, (int64_t)n_att_main * NKV * HD, m.n_ctx, out_tok, out_cap, ctl_seed, ctl_draft);
+                       m.vcache, (int64_t)n_att_main * NKV * HD, m.n_ctx, out_tok, out_cap, ctl_draft);
 }
 
 void Engine::enqueue_mtp_device_step2() {
@@ -641,7 +625,7 @@ int Engine::mtp_steps_async(int k, bool use_graph) {
         (void)hipGraphDestroy(g);
     }
     for (int i = 0; i < k; i++) {
-        if (fused) fz_account(dev_depth == 2 ? 5 : 3);   // seed, draft(s) and verify launches of one step
+        if (fused) fz_account(dev_depth == 2 ? 5 : 2);   // the fused launches of one step
         if (hipGraphLaunch(graph_exec, st) != hipSuccess) return -2;
     }
     return 0;

@@ -78,9 +78,9 @@ struct Engine {
     std::vector<LayerW> L;  // n_layer (+1 MTP block)
     ActBufs b{};
     RunCtl *ctl = nullptr;  // device
-    // the device-driven step's seed and draft control blocks (fused runs), filled by the previous
-    // step's commit kernel or by dev_begin
-    RunCtl *ctl_seed = nullptr, *ctl_draft = nullptr;
+    // the device-driven step's draft control block (fused runs), filled by the previous step's
+    // commit kernel or by dev_begin
+    RunCtl *ctl_draft = nullptr;
     std::vector<void *> allocs;
     size_t bytes = 0;
     // host mirror of the engine position (host-driven API)
@@ -295,9 +295,8 @@ struct Engine {
         b.logits = alloc<float>((size_t)OXE_NL * d.n_vocab);
         b.amax_key = alloc<unsigned long long>(OXE_NL);
         b.counters = alloc<uint32_t>(CNT_N);
-        ctl = alloc<RunCtl>(3);
-        ctl_seed = ctl + 1;
-        ctl_draft = ctl + 2;
+        ctl = alloc<RunCtl>(2);
+        ctl_draft = ctl + 1;
         mtp_state = alloc<MtpState>(1);
         (void)hipMemsetAsync(mtp_state, 0, sizeof(MtpState), st);
         // zero what must start at zero (before any graph capture)
