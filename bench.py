@@ -334,6 +334,33 @@ def bench_kquant(args):
     print(json.dumps(result), flush=True)
 
 
+def gemm_probe(torch, reps):
+    """The batched prefill's Q8_0 GEMM (oxe_hip_gemm_q8_0, the kernel of every prefill projection) on
+    its 2048-token shapes, timed with HIP events on torch's stream: for rocprofv3 --pmc counter runs
+    (matrix-core busy cycles) over a launch list with nothing else of the engine in it."""
+    import oxe_amd as A
+    dev = "cuda"
+    g = torch.Generator(device=dev)
+    g.manual_seed(0)
+    # (K, weight rows, tokens): DN projection, output projection, an expert group's gate / up rows
+    for k, nr, nt in ((2048, 12352, 2048), (4096, 2048, 2048), (2048, 1024, 2048)):
+        wq = torch.randint(-127, 128, (nr, k), dtype=torch.int8, device=dev, generator=g)
+        wd = (torch.rand(nr, k // 32, device=dev, generator=g) * 0.019 + 0.001).half().view(torch.int16)
+        xq, xd = A.quantize_q8_0(torch.randn(nt, k, device=dev, generator=g))
+        y = A.gemm_q8_0(wq, wd, xq, xd)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            A.gemm_q8_0(wq, wd, xq, xd, y)
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1000 / reps
+        print(json.dumps({"gemm_probe": {"k": k, "rows": nr, "tokens": nt, "launches": reps + 1,
+                                         "avg_us": round(us, 1), "int8_TOPs": round(2 * nr * nt * k / us / 1e6, 1)}}),
+              flush=True)
+
+
 def calibrate_copy(torch, mib=1024, reps=4):
     """A plain copy of `mib` MiB, `reps` times: under rocprofv3 --pmc its FETCH_SIZE / WRITE_SIZE
     per dispatch calibrate the byte counters (bytes moved are known exactly)."""
@@ -378,6 +405,8 @@ def main():
     ap.add_argument("--prefill-tokens", type=int, default=2048)
     ap.add_argument("--kquant", action="store_true",
                     help="the K-quant lane GEMV on the Qwen3.6 shapes instead (--steps timed launches each)")
+    ap.add_argument("--gemm-probe", action="store_true",
+                    help="only the prefill's Q8_0 GEMM on its 2048-token shapes (for rocprofv3 --pmc)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build runs the whole MTP-1 step on a single MI355X "
@@ -386,6 +415,9 @@ def main():
     import torch
     if args.calibrate_copy:
         calibrate_copy(torch)
+        return
+    if args.gemm_probe:
+        gemm_probe(torch, 4)
         return
     if args.kquant:
         if args.steps == ap.get_default("steps"):
