@@ -17,6 +17,7 @@
 // that sees it leaves the run.
 #include "oxe_fused.h"
 #include "oxe_gemv.h"
+#include "oxe_mtp_dev.h"
 #include "oxe_prologue.h"
 #include "oxe_route.h"
 #include "oxe_shape.h"
@@ -101,7 +102,7 @@ OXE_DEV void cst128(void *p, uint4 v) {
 // ---- tagged exchange (FzXch) ----------------------------------------------------------------
 // phases of run layer k (the verify's layer il: k = il; the MTP layer of a draft / seed run: k = 1,
 // its entry acting as the "down" phase of k = 0)
-enum { PH_PROJ = 0, PH_MIX = 1, PH_PV = 2, PH_OUT = 3, PH_ROUTER = 4, PH_EXP = 5, PH_DOWN = 6 };
+enum { PH_PROJ = 0, PH_MIX = 1, PH_PV = 2, PH_OUT = 3, PH_ROUTER = 4, PH_EXP = 5, PH_DOWN = 6, PH_HEAD = 7 };
 
 OXE_DEV unsigned long long ll_pack(uint32_t v, uint32_t tag) { return ((unsigned long long)tag << 32) | v; }
 OXE_DEV void ll_st(uint64_t *p, uint32_t v, uint32_t tag) { cst64(p, ll_pack(v, tag)); }
@@ -2153,7 +2154,13 @@ FZ_PHASE bool phase_head(const RunCtl *ctl, const FusedArgs *ap, const float *no
             const unsigned long long o = __shfl_xor(key, m, 64);
             key = key > o ? key : o;
         }
-        if (rl == 0 && l < NL) a.keys[(int64_t)l * c.G + c.b] = key;
+        if (rl == 0 && l < NL) {
+            a.keys[(int64_t)l * c.G + c.b] = key;
+            // and as two tagged halves, for the launch's last stage (the device-driven MTP step)
+            uint64_t *kx = a.xc.kx + ((size_t)l * c.G + c.b) * 2;
+            ll_st(kx, (uint32_t)key, c.tag(k, PH_HEAD));
+            ll_st(kx + 1, (uint32_t)(key >> 32), c.tag(k, PH_HEAD));
+        }
     }
     tr_end(c, TP_HEAD);
     return true;
@@ -2216,10 +2223,73 @@ OXE_DEV void run_all(const RunCtl *ctl, const FusedArgs *ap, uint32_t base) {
 
 }  // namespace fz
 
+// The device-driven MTP step's decision at the end of its fused draft (stage 1) or verify (stage 2)
+// run, by workgroup 0 once every other workgroup has left (done: the run's phases ran; false for an
+// inactive run, whose step still decides to stop). The LM head's per-workgroup keys are read as
+// tagged words (their stores may still be in flight); hid rows are workgroup 0's own writes.
+template <int NL>
+OXE_DEV void mtp_stage(const RunCtl *ctl, const FusedArgs *ap, uint32_t base, bool done) {
+    using namespace fz;
+    const FZ_CAS FusedArgs &a = *uni(ap);
+    const MtpHooks &h = *a.mh;
+    const int stage = uni(ctl)->stage, t = threadIdx.x, G = gridDim.x;
+    struct StageSm {
+        unsigned long long k[FT / 64];
+        CommitSm cs;
+        int aborted;
+    };
+    StageSm &sm = *(StageSm *)fz_dyn;
+    if (t == 0) sm.aborted = done && cld32(a.sync + FZ_W_ERR) != 0;
+    __syncthreads();
+    const bool ran = done && !sm.aborted;
+    unsigned long long key = 0ull;
+    if (ran) {
+        static_assert(NL * 256 == FT, "a key per thread: lane t / 256, workgroup t % 256");
+        const int l = t / 256, bb = t % 256;
+        const int kh = a.mode == FM_VERIFY ? a.n_layer : 2;   // the head's run layer (run_all)
+        const uint32_t tag = base + 1u + 8u * (uint32_t)kh + (uint32_t)PH_HEAD;
+        uint32_t u[2];
+        const bool ok = ll_gather<2, 0, false>(
+            [&](int i) { return LLW{a.xc.kx + ((size_t)l * G + bb) * 2 + i, tag, bb < G}; }, u, a.sync + FZ_W_ERR,
+            nullptr);
+        key = ok && bb < G ? ((unsigned long long)u[1] << 32) | u[0] : 0ull;
+#pragma unroll
+        for (int m = 32; m >= 1; m >>= 1) {
+            const unsigned long long o = __shfl_xor(key, m, 64);
+            key = o > key ? o : key;
+        }
+        if ((t & 63) == 0) sm.k[t >> 6] = key;
+        (void)ok;   // a failed gather leaves the sticky error word set (checked below)
+    }
+    __syncthreads();
+    if (t == 0 && ran && cld32(a.sync + FZ_W_ERR) != 0) sm.aborted = 1;
+    __syncthreads();
+    auto lane_max = [&](int l) {
+        unsigned long long m = 0ull;
+        for (int w = 4 * l; w < 4 * l + 4; w++) m = sm.k[w] > m ? sm.k[w] : m;
+        return m;
+    };
+    const bool good = ran && !sm.aborted;
+    if (stage == 1) {
+        if (t == 0) {
+            if (done && !good) h.ms->err |= 4;   // the draft run aborted: the steps stop
+            const int dl = uni(ctl)->nl - 1;     // the draft is the run's last lane
+            *h.ctl_verify = mtp_after_draft(h.ms, good ? lane_max(dl < NL ? dl : NL - 1) : 0ull, h.force, h.force_n, h.n_ctx);
+        }
+    } else if (stage == 2) {
+        if (t == 0 && done && !good) h.ms->err |= 4;   // the verify run aborted: the steps stop
+        const uint32_t g0 = decode_key(good ? lane_max(0) : 0ull), g1 = decode_key(good ? lane_max(1) : 0ull);
+        mtp_commit(h.ms, good, g0, g1, a.b.hid, h.n_ctx, h.out_tok, h.out_cap, h.ctl_draft, sm.cs);
+    }
+}
+
 template <int NL>
 __global__ __launch_bounds__(fz::FT, 1) void fused_kernel(const RunCtl *__restrict__ ctl, const FusedArgs *__restrict__ ap) {
     using namespace fz;
-    if (!ctl->active) return;
+    if (!ctl->active) {
+        if (ctl->stage != 0 && blockIdx.x == 0) mtp_stage<NL>(ctl, ap, 0u, false);
+        return;
+    }
     if (threadIdx.x == 0) {
         fz_ps.base = cld32(&ap->sync[FZ_W_FLAG]);
         fz_ps.fail = 0;
@@ -2233,6 +2303,24 @@ __global__ __launch_bounds__(fz::FT, 1) void fused_kernel(const RunCtl *__restri
     // every workgroup counts itself out, aborted or not; the last one moves the tag base past this
     // launch's tags and re-arms the counter (the next launch on the stream starts after this one ends)
     __syncthreads();
+    if (ctl->stage != 0 && blockIdx.x == 0) {
+        // a run of the device-driven MTP step: workgroup 0 leaves last, after the step's decision
+        uint32_t *sync = ap->sync;
+        if (threadIdx.x == 0) {
+            uint32_t spins = 0;
+            while (cld32(sync + FZ_W_DONE) != gridDim.x - 1 && ++spins < 4u * SPIN_MAX) __builtin_amdgcn_s_sleep(2);
+            if (spins >= 4u * SPIN_MAX) cst32(sync + FZ_W_ERR, 1u);
+        }
+        __syncthreads();
+        mtp_stage<NL>(ctl, ap, base, true);
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            cst32(sync + FZ_W_DONE, 0u);
+            cst32(sync + FZ_W_HEADQ, 0u);
+            cst32(sync + FZ_W_FLAG, base + FZ_TAG_STRIDE);
+        }
+        return;
+    }
     if (threadIdx.x == 0) {
         uint32_t *sync = ap->sync;
         const uint32_t old = __hip_atomic_fetch_add(sync + FZ_W_DONE, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

@@ -14,37 +14,15 @@
 #include "oxe_engine.h"
 #include "oxe_engine_host.h"
 #include "oxe_model_kernels.h"
+#include "oxe_mtp_dev.h"
 #include "oxe_shape.h"
 
 namespace oxe {
 
 using namespace shp;
 
-OXE_HOST_DEV_INLINE uint32_t decode_key(unsigned long long k) { return k == 0 ? 0u : 0xffffffffu - (uint32_t)(k & 0xffffffffu); }
 
 // ---- device-driven step kernels ----------------------------------------------------------------
-
-// The draft run's control block of the step about to start. A pending catch-up pair (the accepted
-// draft of the previous step with the target h before it) rides along as lane 0 at pos - 1 and the
-// draft (x, hl) is the last lane: the pair's MTP K / V rows are written by the same run that reads
-// them (lanes are independent but for the attention over earlier positions, which includes the
-// run's own rows), as the reference's batched MTP call takes its pending pairs with the draft. Only
-// the last lane's LM-head argmax is wanted. Inactive when the 2-lane verify has no room (the step
-// then stops the driver, as the reference's k = 0; mtp_prep_verify_kernel records it).
-__device__ RunCtl draft_ctl(const MtpState *ms, int n_ctx) {
-    const int np = ms->pending != 0 ? 1 : 0;
-    RunCtl r{};
-    r.nl = 1 + np;
-    r.pos0 = ms->pos - np;
-    r.cur = ms->cur;
-    r.tok[0] = np ? ms->pend_tok : ms->x;
-    r.tok[1] = ms->x;
-    r.hin_sel[0] = np ? HID_PEND : HID_HL;
-    r.hin_sel[1] = HID_HL;
-    r.head_mask = 1 << np;
-    r.active = ms->err == 0 && ms->pos + 2 <= n_ctx;
-    return r;
-}
 
 // per-phase runs: the draft run reads ctl
 __global__ void mtp_prep_draft_kernel(MtpState *ms, RunCtl *ctl, int n_ctx) { *ctl = draft_ctl(ms, n_ctx); }
@@ -62,32 +40,19 @@ __device__ unsigned long long wave_key_max(const unsigned long long *keys, int n
     return k;
 }
 
+// per-phase runs: the verify's control block from the draft's argmax (the fused draft run does this
+// in its last stage)
 __global__ void mtp_prep_verify_kernel(MtpState *ms, RunCtl *ctl, const unsigned long long *keys, int nkeys,
                                        const int32_t *force_d1, int force_n, int n_ctx) {
     const unsigned long long k0 = wave_key_max(keys + (ms->pending != 0 ? nkeys : 0), nkeys);  // the draft's lane
-    if (threadIdx.x != 0) return;
-    if (ms->pos + 2 > n_ctx) ms->err |= 1;  // no room for the 2-lane verify: stop (reference: k = 0)
-    uint32_t d1 = decode_key(k0);
-    if (force_d1 && ms->steps < force_n && force_d1[ms->steps] >= 0) d1 = (uint32_t)force_d1[ms->steps];  // test hook (mtp.rs:554-558)
-    ms->d1 = d1;
-    RunCtl r{};
-    r.nl = 2;
-    r.pos0 = ms->pos;
-    r.cur = ms->cur;
-    r.tok[0] = ms->x;
-    r.tok[1] = d1;
-    r.head_mask = 3;
-    r.hin_sel[0] = HID_HL;
-    r.hin_sel[1] = HID_PEND;
-    r.active = ms->err == 0;
-    *ctl = r;
+    if (threadIdx.x == 0) *ctl = mtp_after_draft(ms, k0, force_d1, force_n, n_ctx);
 }
 
-// accept / commit / note (mtp.rs:564-591, engine.rs:2030-2039): a = (d1 == argmax lane 0)
-// Then the next step's draft control block (cd), from the updated state.
-__global__ void mtp_commit_kernel(MtpState *ms, const unsigned long long *keys, int nkeys, float *hid, uint16_t *vcache,
-                                  int64_t vrows, int n_ctx, uint32_t *out_tok, int out_cap, RunCtl *cd) {
-    __shared__ int s_a, s_ok, s_pos0;
+// per-phase runs: accept / commit after the verify (the fused verify run does this in its last
+// stage), then the next step's draft control block (cd)
+__global__ void mtp_commit_kernel(MtpState *ms, const unsigned long long *keys, int nkeys, float *hid, int n_ctx,
+                                  uint32_t *out_tok, int out_cap, RunCtl *cd) {
+    __shared__ CommitSm sm;
     __shared__ uint32_t s_g[2];
     const int t = threadIdx.x;
     if (t < 64) {
@@ -95,41 +60,10 @@ __global__ void mtp_commit_kernel(MtpState *ms, const unsigned long long *keys, 
         if (t == 0) {
             s_g[0] = decode_key(k0);
             s_g[1] = decode_key(k1);
-            s_ok = ms->err == 0;
-            s_a = s_ok && ms->d1 == s_g[0];
-            s_pos0 = ms->pos;
         }
     }
     __syncthreads();
-    if (!s_ok) {
-        if (t == 0) *cd = draft_ctl(ms, n_ctx);
-        return;
-    }
-    const int a = s_a, pos0 = s_pos0;
-    // hl = h_nextn after the last committed token; the accepted draft's pair (d1, h after x)
-    // waits for MTP seeding
-    for (int i = t; i < E; i += blockDim.x) {
-        const float h0 = hid[i], h1 = hid[E + i];
-        hid[(int64_t)HID_HL * E + i] = a ? h1 : h0;
-        if (a) hid[(int64_t)HID_PEND * E + i] = h0;
-    }
-    if (!a)  // the rejected lane's V^T column of the main attention layers back to +0 (zero_v)
-        for (int64_t r = t; r < vrows; r += blockDim.x) vcache[r * n_ctx + pos0 + 1] = 0;
-    if (t == 0) {
-        const uint32_t g0 = s_g[0], g1 = s_g[1];
-        int n = ms->n_out;
-        if (n < out_cap) out_tok[n++] = g0;
-        if (a && n < out_cap) out_tok[n++] = g1;
-        ms->n_out = n;
-        ms->x = a ? g1 : g0;
-        ms->pending = a;
-        ms->pend_tok = ms->d1;
-        ms->pos = pos0 + a + 1;
-        ms->cur = (ms->cur + a + 1) % OXE_NSLOTS;
-        ms->steps += 1;
-        ms->accepted += a;
-        *cd = draft_ctl(ms, n_ctx);
-    }
+    mtp_commit(ms, true, s_g[0], s_g[1], hid, n_ctx, out_tok, out_cap, cd, sm);
 }
 
 // ---- the device-driven step at depth 2 (mtp.rs:522-592 with k = 2) --------------------------------
@@ -531,6 +465,7 @@ int MtpDriverHost::dev_begin(Engine &e, uint32_t x) {
     s.x = x;
     s.pending = 0;
     s.n_out = 0;
+    s.zcol = -1;
     if (hipMemcpyAsync(e.mtp_state, &s, sizeof(s), hipMemcpyHostToDevice, e.st) != hipSuccess) return -2;
     if (hipMemcpyAsync(e.b.hid + (size_t)HID_HL * E, hl.data(), (size_t)E * 4, hipMemcpyHostToDevice, e.st) != hipSuccess) return -2;
     hipLaunchKernelGGL(mtp_prep_step_kernel, dim3(1), dim3(1), 0, e.st, e.mtp_state, e.ctl_draft, e.m.n_ctx);
@@ -542,6 +477,10 @@ int MtpDriverHost::dev_end(Engine &e, uint32_t *out_tok, int cap, int *n_out, ui
     if (hipMemcpyAsync(&s, e.mtp_state, sizeof(s), hipMemcpyDeviceToHost, e.st) != hipSuccess) return -2;
     if (hipStreamSynchronize(e.st) != hipSuccess) return -2;
     if (int rc = e.fused_check()) return rc;
+    if (s.zcol >= 0 && s.zcol < e.m.n_ctx) {   // the last rejected lane's V^T column (zero_v)
+        launch_zero_v(e.m, e.n_att_main, s.zcol, s.zcol + 1, e.st);
+        if (hipStreamSynchronize(e.st) != hipSuccess) return -2;
+    }
     const int n = std::min(s.n_out, cap);
     if (n > 0 && hipMemcpy(out_tok, e.out_tok, (size_t)n * 4, hipMemcpyDeviceToHost) != hipSuccess) return -2;
     *n_out = n;
@@ -574,18 +513,20 @@ int MtpDriverHost::dev_end(Engine &e, uint32_t *out_tok, int cap, int *n_out, ui
 
 void Engine::enqueue_mtp_device_step() {
     if (fused) {
-        // the draft run (with the pending pair, if any) reads its own control block, filled by the
-        // previous step's commit (or dev_begin)
+        // two launches: the draft run (with the pending pair, if any) reads its control block, filled
+        // by the previous step's verify run (or dev_begin), and its last stage prepares the verify's;
+        // the verify run's last stage accepts / commits and fills the next draft's
         enqueue_mtp_run(ctl_draft);
-    } else {
-        hipLaunchKernelGGL(mtp_prep_draft_kernel, dim3(1), dim3(1), 0, st, mtp_state, ctl, m.n_ctx);
-        enqueue_mtp_run();
+        enqueue_verify();
+        return;
     }
+    hipLaunchKernelGGL(mtp_prep_draft_kernel, dim3(1), dim3(1), 0, st, mtp_state, ctl, m.n_ctx);
+    enqueue_mtp_run();
     hipLaunchKernelGGL(mtp_prep_verify_kernel, dim3(1), dim3(64), 0, st, mtp_state, ctl, keys(), nkeys(),
                        (const int32_t *)force_d1, force_n, m.n_ctx);
     enqueue_verify();
-    hipLaunchKernelGGL(mtp_commit_kernel, dim3(1), dim3(256), 0, st, mtp_state, keys(), nkeys(), b.hid,
-                       m.vcache, (int64_t)n_att_main * NKV * HD, m.n_ctx, out_tok, out_cap, ctl_draft);
+    hipLaunchKernelGGL(mtp_commit_kernel, dim3(1), dim3(256), 0, st, mtp_state, keys(), nkeys(), b.hid, m.n_ctx,
+                       out_tok, out_cap, ctl_draft);
 }
 
 void Engine::enqueue_mtp_device_step2() {

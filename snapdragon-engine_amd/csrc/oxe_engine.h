@@ -39,7 +39,8 @@ struct RunCtl {
     uint32_t tok[OXE_NL];
     int32_t hin_sel[OXE_NL]; // MTP entry: which hidden buffer feeds lane i (index into hid[])
     int32_t active;      // 0: every kernel of this run returns at once (conditional MTP seeding)
-    int32_t pad;
+    int32_t stage;       // fused runs of the device-driven MTP step: 1 after a draft run (prepare the
+                         // verify), 2 after a verify run (accept / commit); 0 otherwise
 };
 
 // Device-driven MTP state (crates/model/src/mtp.rs:314-340 MtpDriver, depth 1 or 2)
@@ -56,7 +57,8 @@ struct MtpState {
     uint32_t pend_tok2;
     uint32_t d2;
     int32_t piece2;      // depth 2: the current step verifies d2 in a second piece
-    int32_t pad;
+    int32_t zcol;        // depth 1: a rejected lane's V^T column not yet back to +0 (-1: none); the
+                         // next step's verify overwrites it, dev_end zeroes it if no step did
 };
 
 // hidden-state buffers ([HID_N][n_embd] floats): 0..NL-1 h_nextn per lane of the last run, HID_HL

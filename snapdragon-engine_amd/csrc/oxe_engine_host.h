@@ -106,6 +106,7 @@ struct Engine {
     uint64_t fz_launches = 0;       // fused launches (an upper bound) since the tag base was last zeroed
     bool fz_capturing = false;      // launches being captured into a graph are counted per replay
     unsigned long long *fz_keys = nullptr;
+    MtpHooks *fz_hooks = nullptr;   // the device-driven MTP step's stages in the fused runs
     LayerDev *fz_layers = nullptr;
     FusedArgs *fz_args = nullptr;   // [3]: verify, draft, seed
     unsigned long long *fz_trace = nullptr;
@@ -152,7 +153,22 @@ struct Engine {
             (void)hipGraphExecDestroy(graph_exec);
             graph_exec = nullptr;
         }
-        return 0;
+        return hooks_upload();
+    }
+    // the fused runs' view of the device-driven step (MtpHooks), after any of its buffers changes
+    int hooks_upload() {
+        if (!fz_hooks) return 0;
+        MtpHooks h{};
+        h.ms = mtp_state;
+        h.ctl_verify = ctl;
+        h.ctl_draft = ctl_draft;
+        h.out_tok = out_tok;
+        h.out_cap = out_cap;
+        h.force = force_d1;
+        h.force_n = force_n;
+        h.n_ctx = m.n_ctx;
+        if (hipMemcpyAsync(fz_hooks, &h, sizeof(h), hipMemcpyHostToDevice, st) != hipSuccess) return -2;
+        return hipStreamSynchronize(st) == hipSuccess ? 0 : -2;
     }
     int set_force(const int32_t *f, int n) {
         for (int i = 0; i < n; i++)
@@ -173,7 +189,7 @@ struct Engine {
             (void)hipGraphExecDestroy(graph_exec);
             graph_exec = nullptr;
         }
-        return 0;
+        return hooks_upload();
     }
     int hidden_host(int lane, float *out) {
         if (hipMemcpyAsync(out, b.hid + (size_t)lane * E, E * 4, hipMemcpyDeviceToHost, st) != hipSuccess) return -2;
@@ -329,12 +345,12 @@ struct Engine {
         // tags of a launch are base + 1 + 8 k + phase for run layers k <= n_layer
         if (8 * (d.n_layer + 2) >= (int64_t)FZ_TAG_STRIDE) return;
         const size_t NLs = OXE_NL;
-        const size_t xw[12] = {2 * NLs * E, 2 * NLs * E, 2 * NLs * DN_ROWS, 2 * NLs * MIX_W, 2 * NLs * (MIX_W / 4),
+        const size_t xw[13] = {2 * NLs * E, 2 * NLs * E, 2 * NLs * DN_ROWS, 2 * NLs * MIX_W, 2 * NLs * (MIX_W / 4),
                                2 * NLs * (MIX_W / 32), 2 * NLs * NEXP, 2 * NLs, 2 * NLs * FFSH,
                                2 * NLs * OXE_MAX_UNION * (FF / 4), 2 * NLs * OXE_MAX_UNION * (FF / 32),
-                               2 * NLs * NH * (size_t)m.n_ctx};
-        size_t off[12], tot = 0;
-        for (int i = 0; i < 12; i++) {
+                               2 * NLs * NH * (size_t)m.n_ctx, NLs * (size_t)fz_grid * 2};
+        size_t off[13], tot = 0;
+        for (int i = 0; i < 13; i++) {
             off[i] = tot;
             tot += (xw[i] + 31) / 32 * 32;   // 256-byte aligned parts
         }
@@ -342,8 +358,9 @@ struct Engine {
         fz_xch = alloc<uint64_t>(tot);
         fz_xch_words = tot;
         FzXch xc;
-        uint64_t **parts[12] = {&xc.x, &xc.x1, &xc.p, &xc.g, &xc.o, &xc.od, &xc.lg, &xc.sg, &xc.hsh, &xc.hq, &xc.hd, &xc.sc};
-        for (int i = 0; i < 12; i++) *parts[i] = fz_xch + off[i];
+        uint64_t **parts[13] = {&xc.x, &xc.x1, &xc.p, &xc.g, &xc.o, &xc.od, &xc.lg, &xc.sg, &xc.hsh, &xc.hq, &xc.hd, &xc.sc, &xc.kx};
+        for (int i = 0; i < 13; i++) *parts[i] = fz_xch + off[i];
+        fz_hooks = alloc<MtpHooks>(1);
         fz_keys = alloc<unsigned long long>((size_t)OXE_NL * fz_grid);
         const int nl_total = d.n_layer + 1;
         std::vector<LayerDev> ld(nl_total);
@@ -379,7 +396,9 @@ struct Engine {
             f.xbase = fz_xch;
             f.xbytes = (uint32_t)(fz_xch_words * 8);
             f.keys = fz_keys;
+            f.mh = fz_hooks;
         }
+        if (hooks_upload()) return;
         (void)hipMemsetAsync(fz_sync, 0, FZ_SYNC_WORDS * 4, st);
         (void)hipMemsetAsync(fz_xch, 0, fz_xch_words * 8, st);
         (void)hipMemsetAsync(fz_keys, 0, (size_t)OXE_NL * fz_grid * 8, st);

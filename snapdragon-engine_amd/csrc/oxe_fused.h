@@ -60,6 +60,19 @@ struct FzXch {
     uint64_t *hq;     // [2][NL][MAX_UNION][FF/4] routed experts' h, Q8_0 codes, 4 per word
     uint64_t *hd;     // [2][NL][MAX_UNION][FF/32] their fp16 scales
     uint64_t *sc;     // [2][NL][NH][n_ctx]       attention scores
+    uint64_t *kx;     // [NL][grid][2]            the LM head's per-workgroup argmax keys (low, high half)
+};
+
+// The device-driven MTP step's state and outputs, for the last stage of a fused draft or verify run
+// whose control block has stage 1 or 2 (device memory; the host rewrites it when out_tok or the
+// forced drafts change)
+struct MtpHooks {
+    MtpState *ms;
+    RunCtl *ctl_verify;       // stage 1 writes the verify's control block here
+    RunCtl *ctl_draft;        // stage 2 writes the next step's draft control block here
+    uint32_t *out_tok;
+    const int32_t *force;
+    int32_t out_cap, force_n, n_ctx, pad;
 };
 
 struct FusedArgs {
@@ -73,6 +86,7 @@ struct FusedArgs {
     uint32_t xbytes;
     unsigned long long *keys;      // [NL][grid] per-workgroup argmax keys of the LM head
     unsigned long long *trace;     // optional [grid][FZ_TRACE_EV][4]: phase id, start, barrier passed, end
+    const MtpHooks *mh;            // the device-driven MTP step's stages
 };
 
 constexpr int FZ_TRACE_EV = 2048;  // trace events per workgroup and run
