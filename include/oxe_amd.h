@@ -258,8 +258,9 @@ OXE_API int oxe_mtp_step_force(oxe_engine *e, uint32_t x, uint32_t *out, int *n_
  * step to rewind. */
 OXE_API int oxe_mtp_rewind(oxe_engine *e, int m);
 /* Device-driven steps: begin hands the driver state to the GPU; each of the k steps then runs
- * seed -> draft -> 2-lane verify -> greedy accept/commit on the GPU (one HIP graph per step, no
- * host round-trip); end synchronises and returns the emitted tokens and the next x. At depth 2 a step
+ * draft (the pending catch-up pair, if any, as an extra lane) -> 2-lane verify -> greedy
+ * accept/commit on the GPU (one HIP graph per step, no host round-trip); end synchronises and
+ * returns the emitted tokens and the next x. At depth 2 a step
  * runs two drafts and verifies x, d1 and then d2 in pieces of at most two lanes, the second piece
  * only when d1 was accepted and d2 matches (mtp.rs:522-592). A step that does not fit the context
  * (depth 1: 2 positions, depth 2: 3) stops the steps: end returns -4, and the caller continues with

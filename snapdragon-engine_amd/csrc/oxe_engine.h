@@ -29,8 +29,9 @@ struct Q8W {
 // can return to any committed prefix of it.
 constexpr int OXE_NSLOTS = 5;
 
-// Run control (device memory). Written by the host through a tiny kernel for host-driven calls and
-// by the commit kernel for the device-driven MTP step; read by every kernel of a run.
+// Run control (device memory). Written by the host through a tiny kernel for host-driven calls and,
+// for the device-driven MTP step, by the step's decision code (the control kernels of per-phase runs,
+// the last stage of fused draft and verify runs); read by every kernel of a run.
 struct RunCtl {
     int32_t nl;          // lanes of this run (1..OXE_NL)
     int32_t pos0;        // position of lane 0
