@@ -107,3 +107,25 @@ def test_verify_sweep_bitexact(mode):
             o.commit(1)
         g.close()
         o.close()
+
+
+def test_lm_head_claimed_tail_bitexact():
+    """The fused LM head with its tail claimed from a counter (a vocabulary of 40000 rows: 4 tiles of
+    32 rows per workgroup, then 226 tiles in claimed pairs): every logit of both lanes and the
+    argmaxes against the oracle, over several runs (the counter is re-armed by each launch's last
+    workgroup)."""
+    import oxe_amd as A
+    d = O.desc_small(n_vocab=40000)
+    g = A.Engine(d, seed=11, n_ctx=N_CTX)
+    if not g.fused:
+        pytest.skip("the fused run kernel needs a 256-CU device")
+    o = O.Engine(d, seed=11, n_ctx=N_CTX)
+    for toks in ([39999, 12], [5, 31000], [20000]):
+        ag, ao = g.verify(toks), o.verify(toks)
+        assert list(ag) == list(ao), toks
+        for ln in range(len(toks)):
+            assert np.array_equal(bits(g.logits(ln)), bits(o.logits(ln))), (toks, ln)
+        g.commit(1)
+        o.commit(1)
+    g.close()
+    o.close()
