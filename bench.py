@@ -19,6 +19,7 @@ the `sample` field). parity: the run's generated ids against the oracle's for th
 prompt (tests/golden/config4_ids.npz) and the reference bench's generated_hash of them.
 """
 import argparse
+import contextlib
 import json
 import os
 import sys
@@ -86,6 +87,26 @@ def host_cores():
     return min(threads, len(aff)), aff, model
 
 
+@contextlib.contextmanager
+def pinned_team(O):
+    """The oracle's OpenMP team pinned like the reference's worker pool (crates/sched/src/lib.rs:1-11):
+    thread i on the i-th core of this process's affinity set, caller included; the caller's mask is
+    restored on exit. Yields the team size, 0 if pinning failed."""
+    team = O.lib().oxo_pin_team(1)
+    try:
+        yield max(team, 0)
+    finally:
+        O.lib().oxo_pin_team(0)
+
+
+def team_text(team, threads):
+    if team > 0:
+        return (f"a persistent OpenMP team of {team} threads, thread i pinned to the i-th core of the "
+                f"process's affinity set like the reference's worker pool, with a barrier at the end of "
+                f"each parallel row loop (not the reference's static plan with one barrier per phase)")
+    return f"OpenMP over rows on {threads} unpinned threads (pinning failed)"
+
+
 def cpu_baseline(seconds, state, n_pos, hl, x):
     """Time the oracle's MTP-1 steps on the full 35B-A3B shape (bounded sample) from the GPU run's own
     state: the sequence state after the 512-token prompt and the warm-up steps (Engine::write_state
@@ -94,6 +115,11 @@ def cpu_baseline(seconds, state, n_pos, hl, x):
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as O
     O.build()
+    with pinned_team(O) as team:
+        return _cpu_steps(O, seconds, state, n_pos, hl, x, team)
+
+
+def _cpu_steps(O, seconds, state, n_pos, hl, x, team):
     d = O.desc_35b_a3b()
     e = O.Engine(d, seed=0, n_ctx=n_pos + 256)
     O.lib().oxo_set_keep_logits(e.h, 0)
@@ -113,12 +139,11 @@ def cpu_baseline(seconds, state, n_pos, hl, x):
     compute = max(wall - gen, 1e-9)
     threads, aff, model = host_cores()
     e.close()
-    return {"value": round(toks / compute, 4), "unit": "tok/s", "cores": threads, "kind": "port",
-            "cpu": model, "affinity": f"{len(aff)} cores [{aff[0]}..{aff[-1]}]" if aff else "",
+    return {"value": round(toks / compute, 4), "unit": "tok/s", "cores": team if team > 0 else threads,
+            "kind": "port", "cpu": model, "affinity": f"{len(aff)} cores [{aff[0]}..{aff[-1]}]" if aff else "",
             "sample": f"{steps} MTP-1 steps ({toks} tokens) of the 35B-A3B shape at positions {n_pos}..{n_pos + steps}, "
                       f"from the GPU run's state after its {n_pos}-position prefix; the reference algorithm "
-                      f"restated in C++ with OpenMP over rows on {threads} threads (not the reference's pinned "
-                      f"thread team with one barrier per plan phase); {wall:.1f} s wall minus {gen:.1f} s spent "
+                      f"restated in C++ on {team_text(team, threads)}; {wall:.1f} s wall minus {gen:.1f} s spent "
                       f"generating synthetic expert weights on first use"}
 
 
@@ -160,6 +185,11 @@ def cpu_prefill_baseline(seconds):
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as O
     O.build()
+    with pinned_team(O) as team:
+        return _cpu_prefill(O, seconds, team)
+
+
+def _cpu_prefill(O, seconds, team):
     d = O.desc_35b_a3b()
     e = O.Engine(d, seed=0, n_ctx=1024)
     O.lib().oxo_set_keep_logits(e.h, 0)
@@ -176,10 +206,10 @@ def cpu_prefill_baseline(seconds):
     compute = max(wall - gen, 1e-9)
     cores = host_cores()[0]
     e.close()
-    return {"value": round(n / compute, 4), "unit": "tok/s", "cores": cores, "kind": "port",
+    return {"value": round(n / compute, 4), "unit": "tok/s", "cores": team or cores, "kind": "port",
             "sample": f"{n} prompt tokens of the 35B-A3B shape as 2-token verify runs (the reference's "
-                      f"MtpDriver::prefill path); {wall:.1f} s wall minus {gen:.1f} s generating synthetic expert "
-                      f"weights on first use"}
+                      f"MtpDriver::prefill path) on {team_text(team, cores)}; {wall:.1f} s wall minus "
+                      f"{gen:.1f} s generating synthetic expert weights on first use"}
 
 
 def bench_prefill(args):
@@ -267,16 +297,17 @@ def cpu_kquant_baseline(seconds, ty, k, rows_total):
         v[:, :, off] = h & 0xFF
         v[:, :, off + 1] = h >> 8
     y = O.quantize_q8_K(rng.standard_normal((2, k)).astype(np.float32))
-    t0, n = time.time(), 0
-    while time.time() - t0 < seconds or n == 0:
-        O.vl_gemv(ty, w, k, y)
-        n += rows
-    dt = time.time() - t0
+    with pinned_team(O) as team:
+        t0, n = time.time(), 0
+        while time.time() - t0 < seconds or n == 0:
+            O.vl_gemv(ty, w, k, y)
+            n += rows
+        dt = time.time() - t0
     bytes_per_row = k // 256 * KQ_BYTES[ty]
     cores = host_cores()[0]
-    return {"value": round(n * bytes_per_row / dt / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": "port",
+    return {"value": round(n * bytes_per_row / dt / 1e9, 3), "unit": "GB/s", "cores": team or cores, "kind": "port",
             "sample": f"{n} rows ({n / rows_total:.2f} x the full matrix) of the same type and k, 2 lanes, "
-                      f"in {dt:.1f} s"}
+                      f"in {dt:.1f} s on {team_text(team, cores)}"}
 
 
 def bench_kquant(args):

@@ -16,6 +16,9 @@
 #include <mutex>
 #include <vector>
 
+#include <omp.h>
+#include <sched.h>
+
 namespace {
 
 struct Q8 {
@@ -673,6 +676,47 @@ const float *oxo_logits(const oxo_engine *e, int lane) { return e->logits[lane].
 int64_t oxo_n_ctx(const oxo_engine *e) { return e->n_ctx; }
 void oxo_set_keep_logits(oxo_engine *e, int on) { e->keep_logits = on != 0; }
 double oxo_gen_seconds(const oxo_engine *e) { return e->gen_seconds; }
+
+// Pin the OpenMP team the way the reference's worker pool is pinned (crates/sched/src/lib.rs:1-11,
+// 137-147, 233-249): team thread i on the i-th CPU of the calling thread's affinity set, the caller
+// (thread 0) included, its previous mask kept and restored by oxo_pin_team(0). libgomp keeps the
+// team's threads alive between parallel regions, so the pinned threads serve every later region of
+// the same size. Returns the team size pinned (0 after unpinning), or -1 if a mask call failed.
+namespace {
+cpu_set_t g_caller_mask;
+bool g_pinned = false;
+}  // namespace
+
+int oxo_pin_team(int on) {
+    if (!on) {
+        if (!g_pinned) return 0;
+        int bad = 0;
+#pragma omp parallel reduction(+ : bad)
+        bad += sched_setaffinity(0, sizeof(cpu_set_t), &g_caller_mask) != 0;
+        g_pinned = false;
+        return bad ? -1 : 0;
+    }
+    cpu_set_t mask;
+    CPU_ZERO(&mask);
+    if (sched_getaffinity(0, sizeof(cpu_set_t), &mask) != 0) return -1;
+    std::vector<int> cpus;
+    for (int c = 0; c < CPU_SETSIZE; c++)
+        if (CPU_ISSET(c, &mask)) cpus.push_back(c);
+    if (cpus.empty()) return -1;
+    if (!g_pinned) g_caller_mask = mask;
+    int bad = 0, team = 0;
+#pragma omp parallel reduction(+ : bad)
+    {
+        const int t = omp_get_thread_num();
+        if (t == 0) team = omp_get_num_threads();
+        cpu_set_t one;
+        CPU_ZERO(&one);
+        CPU_SET(cpus[t % cpus.size()], &one);
+        bad += sched_setaffinity(0, sizeof(cpu_set_t), &one) != 0;
+    }
+    g_pinned = true;
+    return bad ? -1 : team;
+}
 
 // raw state views for parity checks: K cache [att][kvh][n_ctx][hd] f16, V^T [att][kvh*hd][n_ctx] f16,
 // conv [slot][rec][(kc-1)*channels], S [slot][rec][nv][hv][hv]

@@ -111,6 +111,7 @@ def lib():
             "oxo_n_ctx": (C.c_int64, [C.c_void_p]),
             "oxo_set_keep_logits": (None, [C.c_void_p, C.c_int]),
             "oxo_gen_seconds": (C.c_double, [C.c_void_p]),
+            "oxo_pin_team": (C.c_int, [C.c_int]),
             "oxo_kcache": (u16p, [C.c_void_p]),
             "oxo_vcache": (u16p, [C.c_void_p]),
             "oxo_conv_state": (f32p, [C.c_void_p]),

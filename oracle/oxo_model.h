@@ -27,6 +27,7 @@ const float *oxo_logits(const oxo_engine *e, int lane);
 int64_t oxo_n_ctx(const oxo_engine *e);
 void oxo_set_keep_logits(oxo_engine *e, int on);
 double oxo_gen_seconds(const oxo_engine *e);  // time spent generating synthetic experts
+int oxo_pin_team(int on);  // pin (1) / unpin (0) the OpenMP team, one thread per CPU of the caller's mask
 const uint16_t *oxo_kcache(const oxo_engine *e);
 const uint16_t *oxo_vcache(const oxo_engine *e);
 float *oxo_conv_state(oxo_engine *e);

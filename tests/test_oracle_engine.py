@@ -200,3 +200,26 @@ def test_read_state_handoff(desc):
     for t in (77, 3):
         assert a.step(t) == b.step(t)
         assert np.array_equal(bits(a.logits(0)), bits(b.logits(0)))
+
+
+def test_pinned_team_same_bits_and_restores_mask(desc):
+    # oxo_pin_team pins team thread i to the i-th CPU of the caller's mask (the reference's pool,
+    # crates/sched/src/lib.rs:1-11) and restores the caller's mask; placement never changes a value
+    import os
+    L = O.lib()
+    before = os.sched_getaffinity(0)
+    a = O.Engine(desc, seed=SEED, n_ctx=64)
+    b = O.Engine(desc, seed=SEED, n_ctx=64)
+    want = [a.step(t) for t in (5, 900, 31)]
+    try:
+        team = L.oxo_pin_team(1)
+        assert team >= 1
+        if len(before) > 1:
+            assert os.sched_getaffinity(0) == {sorted(before)[0]}
+        got = [b.step(t) for t in (5, 900, 31)]
+    finally:
+        assert L.oxo_pin_team(0) == 0
+    assert os.sched_getaffinity(0) == before
+    assert got == want
+    assert np.array_equal(bits(a.logits(0)), bits(b.logits(0)))
+    assert np.array_equal(bits(a.hidden(0)), bits(b.hidden(0)))
