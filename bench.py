@@ -115,11 +115,12 @@ def cpu_baseline(seconds, state, n_pos, hl, x):
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as O
     O.build()
+    hc = host_cores()                           # before pinning narrows this thread's mask
     with pinned_team(O) as team:
-        return _cpu_steps(O, seconds, state, n_pos, hl, x, team)
+        return _cpu_steps(O, seconds, state, n_pos, hl, x, team, hc)
 
 
-def _cpu_steps(O, seconds, state, n_pos, hl, x, team):
+def _cpu_steps(O, seconds, state, n_pos, hl, x, team, hc):
     d = O.desc_35b_a3b()
     e = O.Engine(d, seed=0, n_ctx=n_pos + 256)
     O.lib().oxo_set_keep_logits(e.h, 0)
@@ -137,7 +138,7 @@ def _cpu_steps(O, seconds, state, n_pos, hl, x, team):
     wall = time.time() - t0
     gen = O.lib().oxo_gen_seconds(e.h) - gen0
     compute = max(wall - gen, 1e-9)
-    threads, aff, model = host_cores()
+    threads, aff, model = hc
     e.close()
     return {"value": round(toks / compute, 4), "unit": "tok/s", "cores": team if team > 0 else threads,
             "kind": "port", "cpu": model, "affinity": f"{len(aff)} cores [{aff[0]}..{aff[-1]}]" if aff else "",
@@ -185,11 +186,12 @@ def cpu_prefill_baseline(seconds):
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as O
     O.build()
+    cores = host_cores()[0]
     with pinned_team(O) as team:
-        return _cpu_prefill(O, seconds, team)
+        return _cpu_prefill(O, seconds, team, cores)
 
 
-def _cpu_prefill(O, seconds, team):
+def _cpu_prefill(O, seconds, team, cores):
     d = O.desc_35b_a3b()
     e = O.Engine(d, seed=0, n_ctx=1024)
     O.lib().oxo_set_keep_logits(e.h, 0)
@@ -204,7 +206,6 @@ def _cpu_prefill(O, seconds, team):
     wall = time.time() - t0
     gen = O.lib().oxo_gen_seconds(e.h) - gen0
     compute = max(wall - gen, 1e-9)
-    cores = host_cores()[0]
     e.close()
     return {"value": round(n / compute, 4), "unit": "tok/s", "cores": team or cores, "kind": "port",
             "sample": f"{n} prompt tokens of the 35B-A3B shape as 2-token verify runs (the reference's "
