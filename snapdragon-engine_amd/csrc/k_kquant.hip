@@ -287,29 +287,32 @@ OXE_DEV float chain(float acc, const uint8_t *wb, float dx, const int *r0, const
 // ---- the lane GEMV --------------------------------------------------------------------------------
 // s[l * nr + r] = W[r] . y[l]; w: nr rows of nb blocks (row bytes a multiple of 4, w 16-byte
 // aligned); y: NL lanes of nb q8_K blocks. One wave per workgroup, persistent over groups of 4 rows
-// (16 threads per row). Per group: the 4 rows' bytes (contiguous) go to LDS with 16-byte loads,
-// the first PF x 1 KiB of them loaded into registers one group ahead; then per chunk of up to 8
-// blocks thread (row ri, unit u) forms half block u % 2 of block u / 2 for every lane, and threads
-// u < NL of each row run lane u's chain over the chunk's blocks in order.
+// (16 threads per row). Per group: the 4 rows' bytes (contiguous) go to LDS with 16-byte loads, the
+// first PF x 1 KiB of them held in registers, two groups ahead (buffers a and b, alternating); then
+// per chunk of up to 8 blocks thread (row ri, unit u) forms half block u % 2 of block u / 2 for
+// every lane, and threads u < NL of each row run lane u's chain over the chunk's blocks in order.
+// The register loads are unconditional (indices clamped into the group; a group past the end
+// re-reads the last one and writes nothing): a load under a per-thread condition makes the
+// compiler wait for every outstanding load before the first LDS store, which drains the second
+// buffer (measured: 2-deep conditional 143.8 us, unconditional 130.6 us for the Q6_K LM head).
 constexpr int GR = 4;     // rows per group
-constexpr int PF = 8;     // prefetched 16-byte pieces per thread
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));   // a plain vector (HIP's uint4 is a union
                                                               // type that keeps arrays of it in scratch)
 
 __host__ __device__ inline int align16(int n) { return (n + 15) / 16 * 16; }
 
-// the first PF x 1 KiB of group g's bytes into registers (16-byte loads)
+// the first PF x 1 KiB of group g's bytes (g < ngroups) into registers, non-temporal 16-byte loads
+template <int PF>
 OXE_DEV void pf_load(u32x4 (&pf)[PF], const uint8_t *w, int64_t g, int64_t nr, int row_bytes, int t) {
     const u32x4 *src = (const u32x4 *)(w + g * GR * row_bytes);
     const int n16 = (int)(min((int64_t)GR, nr - g * GR) * row_bytes) / 16;
 #pragma unroll
-    for (int j = 0; j < PF; j++)
-        if (t + 64 * j < n16) pf[j] = src[t + 64 * j];
+    for (int j = 0; j < PF; j++) pf[j] = __builtin_nontemporal_load(src + min(t + 64 * j, n16 - 1));
 }
 
-// one group of 4 rows: its prefetched bytes (pf) and the rest to LDS, pf refilled with group
-// g_next, then the units and the chains
-template <int TY, int NL>
+// one group of 4 rows (g may be past the end: then nothing is written): its prefetched bytes (pf)
+// and the rest to LDS, pf refilled with group g_next, then the units and the chains
+template <int TY, int NL, int PF>
 OXE_DEV void vl_group(u32x4 (&pf)[PF], int64_t g, int64_t g_next, const uint8_t *__restrict__ w, int nb, int64_t nr,
                       float *__restrict__ s, uint8_t *wl, const uint32_t *yh, const float *yd, int *res) {
     constexpr int BB = BT<TY>::B;
@@ -317,18 +320,19 @@ OXE_DEV void vl_group(u32x4 (&pf)[PF], int64_t g, int64_t g_next, const uint8_t 
     const int row_bytes = nb * BB, ls = y_lane_words(nb);
     const int t = threadIdx.x, ri = t >> 4, u = t & 15;
     const int64_t ngroups = (nr + GR - 1) / GR;
-    const int sp = (int)(min((int64_t)GR, nr - g * GR) * row_bytes), n16 = sp / 16;
-    const u32x4 *src = (const u32x4 *)(w + g * GR * row_bytes);
+    const bool gin = g < ngroups;
+    const int64_t gd = gin ? g : ngroups - 1;   // the group whose bytes pf holds
+    const int sp = (int)(min((int64_t)GR, nr - gd * GR) * row_bytes), n16 = sp / 16;
+    const u32x4 *src = (const u32x4 *)(w + gd * GR * row_bytes);
     __syncthreads();   // the previous group's LDS reads are done
 #pragma unroll
-    for (int j = 0; j < PF; j++)
-        if (t + 64 * j < n16) ((u32x4 *)wl)[t + 64 * j] = pf[j];
+    for (int j = 0; j < PF; j++) ((u32x4 *)wl)[min(t + 64 * j, n16 - 1)] = pf[j];   // clamped: same bytes
     for (int i = t + 64 * PF; i < n16; i += 64) ((u32x4 *)wl)[i] = src[i];
     for (int i = n16 * 4 + t; i < sp / 4; i += 64) ((uint32_t *)wl)[i] = ((const uint32_t *)src)[i];   // tail
     __syncthreads();
-    if (g_next < ngroups) pf_load(pf, w, g_next, nr, row_bytes, t);   // in flight while this group computes
-    const int64_t r = g * GR + ri;
-    const bool live = r < nr;
+    pf_load(pf, w, g_next < ngroups ? g_next : ngroups - 1, nr, row_bytes, t);   // in flight meanwhile
+    const int64_t r = gd * GR + ri;
+    const bool live = gin && r < nr;
     float acc = 0.0f;
     for (int b0 = 0; b0 < nb; b0 += 8) {
         const int kc = min(8, nb - b0);
@@ -347,7 +351,7 @@ OXE_DEV void vl_group(u32x4 (&pf)[PF], int64_t g, int64_t g_next, const uint8_t 
     if (u < NL && live) s[(int64_t)u * nr + r] = acc;
 }
 
-template <int TY, int NL>
+template <int TY, int NL, int PF>
 __global__ __launch_bounds__(64) void vl_gemv_kernel(const uint8_t *__restrict__ w, int nb, int64_t nr,
                                                      const uint8_t *__restrict__ y, float *__restrict__ s) {
     constexpr int BB = BT<TY>::B;
@@ -366,24 +370,31 @@ __global__ __launch_bounds__(64) void vl_gemv_kernel(const uint8_t *__restrict__
         yh[hb * YH + wd] = wd < 32 ? src[1 + 32 * h + wd] : src[65 + 4 * h + (wd - 32)];
     }
     for (int i = t; i < NL * nb; i += 64) yd[i] = *(const float *)(y + (int64_t)i * Q8K_BYTES);
-    // the register buffer holds the next group's first bytes (fixed indices only: it stays in
-    // registers; a second buffer two groups ahead measured no faster)
-    u32x4 pf[PF];
-    if ((int64_t)blockIdx.x < ngroups) pf_load(pf, w, blockIdx.x, nr, row_bytes, t);
-    for (int64_t g = blockIdx.x; g < ngroups; g += G) vl_group<TY, NL>(pf, g, g + G, w, nb, nr, s, wl, yh, yd, res);
+    // two register buffers (fixed indices only: they stay in registers), groups g and g + G in
+    // flight from the start; the scheduling barrier keeps buffer a's loads ahead of b's, so the
+    // first LDS stores wait for a's only
+    u32x4 pa[PF], pb[PF];
+    if ((int64_t)blockIdx.x >= ngroups) return;
+    pf_load(pa, w, blockIdx.x, nr, row_bytes, t);
+    __builtin_amdgcn_sched_barrier(0);
+    pf_load(pb, w, min((int64_t)blockIdx.x + G, ngroups - 1), nr, row_bytes, t);
+    for (int64_t g = blockIdx.x; g < ngroups; g += 2 * G) {
+        vl_group<TY, NL, PF>(pa, g, g + 2 * G, w, nb, nr, s, wl, yh, yd, res);
+        vl_group<TY, NL, PF>(pb, g + G, g + 3 * G, w, nb, nr, s, wl, yh, yd, res);
+    }
 }
 
 size_t vl_gemv_lds(int bb, int nb, int nl) {
     return (size_t)align16(GR * nb * bb) + (size_t)align16(nl * nb * (2 * YH + 1) * 4) + (size_t)64 * (nl * RES + 1) * 4;
 }
 
-template <int TY, int NL>
-int vl_gemv_launch(const uint8_t *w, int nb, int64_t nr, const uint8_t *y, float *s, hipStream_t st) {
+template <int TY, int NL, int PF>
+int vl_gemv_launch_pf(const uint8_t *w, int nb, int64_t nr, const uint8_t *y, float *s, hipStream_t st) {
     constexpr int BB = BT<TY>::B;
     const size_t lds = vl_gemv_lds(BB, nb, NL);
     static bool attr = false;   // above 64 KiB of LDS the kernel needs the attribute (160 KiB per CU)
     if (lds > 65536 && !attr) {
-        if (hipFuncSetAttribute((const void *)vl_gemv_kernel<TY, NL>, hipFuncAttributeMaxDynamicSharedMemorySize,
+        if (hipFuncSetAttribute((const void *)vl_gemv_kernel<TY, NL, PF>, hipFuncAttributeMaxDynamicSharedMemorySize,
                                 (int)lds) != hipSuccess)
             return -2;
         attr = true;
@@ -394,8 +405,18 @@ int vl_gemv_launch(const uint8_t *w, int nb, int64_t nr, const uint8_t *y, float
     const int per_cu = (int)std::max<size_t>(1, std::min<size_t>(16, (160 * 1024) / lds));
     const int64_t ngroups = (nr + GR - 1) / GR;
     const int64_t grid = std::min<int64_t>(ngroups, (int64_t)ncu * per_cu);
-    hipLaunchKernelGGL((vl_gemv_kernel<TY, NL>), dim3((unsigned)grid), dim3(64), lds, st, w, nb, nr, y, s);
+    hipLaunchKernelGGL((vl_gemv_kernel<TY, NL, PF>), dim3((unsigned)grid), dim3(64), lds, st, w, nb, nr, y, s);
     return hipGetLastError() == hipSuccess ? 1 : -2;
+}
+
+// registers per prefetch buffer: the smallest of 2, 4, 8 KiB-per-wave steps that holds a whole group
+// (the rest of a larger group is copied to LDS directly)
+template <int TY, int NL>
+int vl_gemv_launch(const uint8_t *w, int nb, int64_t nr, const uint8_t *y, float *s, hipStream_t st) {
+    const int n16 = GR * nb * BT<TY>::B / 16;
+    if (n16 <= 128) return vl_gemv_launch_pf<TY, NL, 2>(w, nb, nr, y, s, st);
+    if (n16 <= 256) return vl_gemv_launch_pf<TY, NL, 4>(w, nb, nr, y, s, st);
+    return vl_gemv_launch_pf<TY, NL, 8>(w, nb, nr, y, s, st);
 }
 
 template <int TY>
