@@ -16,14 +16,15 @@ namespace kq {
 constexpr int QK = 256;
 constexpr int Q8K_BYTES = 292;   // block_q8_K: float d, int8 qs[256], int16 bsums[16]
 constexpr int Q8K_QS = 4, Q8K_BS = 260;
-constexpr int RES = 6;           // ints per (unit, lane)
 constexpr int MAX_LANES = 4;
 
+// B: block bytes; R: integers per (unit, lane) that the chain reads (kept in LDS between the units
+// and the chains, so a smaller R leaves room for more waves per CU)
 template <int TY> struct BT;
-template <> struct BT<3> { static constexpr int B = 110; };
-template <> struct BT<4> { static constexpr int B = 144; };
-template <> struct BT<5> { static constexpr int B = 176; };
-template <> struct BT<6> { static constexpr int B = 210; };
+template <> struct BT<3> { static constexpr int B = 110, R = 1; };
+template <> struct BT<4> { static constexpr int B = 144, R = 5; };
+template <> struct BT<5> { static constexpr int B = 176, R = 6; };
+template <> struct BT<6> { static constexpr int B = 210, R = 1; };
 
 OXE_DEV uint32_t ld32(const uint8_t *p) { return *(const uint32_t *)p; }
 OXE_DEV uint16_t ld16(const uint8_t *p) { return *(const uint16_t *)p; }
@@ -106,7 +107,7 @@ __global__ __launch_bounds__(256) void quant_q8_K_kernel(const float *__restrict
 }
 
 // ---- integers of one half block (unit h: weights 128 h .. 128 h + 127), every lane ---------------
-// y: the lanes' halves h of this block position (YView); out[l * RES + ...]
+// y: the lanes' halves h of this block position (YView); out[l * BT<TY>::R + ...]
 
 // get_scale_min_k4 (quants_base.c:50-57)
 OXE_DEV void scale_min_k4(int j, const uint8_t *q, int &d, int &m) {
@@ -123,6 +124,7 @@ OXE_DEV void scale_min_k4(int j, const uint8_t *q, int &d, int &m) {
 // out[4] = the unit's part of sum min_j * bsum32_j; Q5_K: out[4 + g'] = that sum per step
 template <int TY, int NL>
 OXE_DEV void unit_k45(const uint8_t *wb, YView y, int h, int *out) {
+    constexpr int RES = BT<TY>::R;
     const uint8_t *sc = wb + 4;
     const uint8_t *qs = wb + (TY == 4 ? 16 : 48);
     const uint8_t *qh = wb + 16;
@@ -170,6 +172,7 @@ OXE_DEV void unit_k45(const uint8_t *wb, YView y, int h, int *out) {
 // Q6_K: the unit's part of I = sum_i scale_i * (16 codes - 32) . q8 (the -32 through the q8 sums)
 template <int NL>
 OXE_DEV void unit_q6(const uint8_t *wb, YView y, int n, int *out) {
+    constexpr int RES = BT<6>::R;
     const int8_t *sc = (const int8_t *)(wb + 192);
     uint32_t qlw[16], qhw[8];   // ql[64 n .. 64 n + 63], qh[32 n .. 32 n + 31]
     ld_run<16>(wb + 64 * n, qlw);
@@ -214,6 +217,7 @@ OXE_DEV int q3_raw(const uint8_t *s12, int i) {
 // Q3_K: the unit's part of isum = sum_i (raw_i - 32) * dot16_i, codes (low 2 bits | hmask bit << 2) - 4
 template <int NL>
 OXE_DEV void unit_q3(const uint8_t *wb, YView y, int n, int *out) {
+    constexpr int RES = BT<3>::R;
     uint32_t qsw[8], hmw[8];   // qs[32 n .. 32 n + 31], hmask[0..31]
     ld_run<8>(wb + 32 + 32 * n, qsw);
     ld_run<8>(wb, hmw);
@@ -316,7 +320,8 @@ template <int TY, int NL, int PF>
 OXE_DEV void vl_group(u32x4 (&pf)[PF], int64_t g, int64_t g_next, const uint8_t *__restrict__ w, int nb, int64_t nr,
                       float *__restrict__ s, uint8_t *wl, const uint32_t *yh, const float *yd, int *res) {
     constexpr int BB = BT<TY>::B;
-    constexpr int RS = NL * RES + 1;   // odd per-thread stride: no bank conflicts between threads
+    constexpr int RES = BT<TY>::R;
+    constexpr int RS = (NL * RES) | 1;   // odd per-thread stride: no bank conflicts between threads
     const int row_bytes = nb * BB, ls = y_lane_words(nb);
     const int t = threadIdx.x, ri = t >> 4, u = t & 15;
     const int64_t ngroups = (nr + GR - 1) / GR;
@@ -360,7 +365,7 @@ __global__ __launch_bounds__(64) void vl_gemv_kernel(const uint8_t *__restrict__
     uint8_t *wl = lds;                                                   // [GR][row_bytes]
     uint32_t *yh = (uint32_t *)(lds + align16(GR * row_bytes));         // [NL][nb][2][YH]
     float *yd = (float *)(yh + NL * y_lane_words(nb));                   // [NL][nb]
-    int *res = (int *)((uint8_t *)yh + align16(NL * nb * (2 * YH + 1) * 4));   // [64][NL * RES + 1]
+    int *res = (int *)((uint8_t *)yh + align16(NL * nb * (2 * YH + 1) * 4));   // [64][(NL * R) | 1]
     const int t = threadIdx.x;
     const int64_t ngroups = (nr + GR - 1) / GR, G = gridDim.x;
     // the lanes' q8_K blocks (lane l block b is block l nb + b) repacked into halves and scales
@@ -384,14 +389,14 @@ __global__ __launch_bounds__(64) void vl_gemv_kernel(const uint8_t *__restrict__
     }
 }
 
-size_t vl_gemv_lds(int bb, int nb, int nl) {
-    return (size_t)align16(GR * nb * bb) + (size_t)align16(nl * nb * (2 * YH + 1) * 4) + (size_t)64 * (nl * RES + 1) * 4;
+size_t vl_gemv_lds(int bb, int rr, int nb, int nl) {
+    return (size_t)align16(GR * nb * bb) + (size_t)align16(nl * nb * (2 * YH + 1) * 4) + (size_t)64 * ((nl * rr) | 1) * 4;
 }
 
 template <int TY, int NL, int PF>
 int vl_gemv_launch_pf(const uint8_t *w, int nb, int64_t nr, const uint8_t *y, float *s, hipStream_t st) {
     constexpr int BB = BT<TY>::B;
-    const size_t lds = vl_gemv_lds(BB, nb, NL);
+    const size_t lds = vl_gemv_lds(BB, BT<TY>::R, nb, NL);
     static bool attr = false;   // above 64 KiB of LDS the kernel needs the attribute (160 KiB per CU)
     if (lds > 65536 && !attr) {
         if (hipFuncSetAttribute((const void *)vl_gemv_kernel<TY, NL, PF>, hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -402,7 +407,13 @@ int vl_gemv_launch_pf(const uint8_t *w, int nb, int64_t nr, const uint8_t *y, fl
     int dev = 0, ncu = 256;
     (void)hipGetDevice(&dev);
     (void)hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev);
-    const int per_cu = (int)std::max<size_t>(1, std::min<size_t>(16, (160 * 1024) / lds));
+    // exactly the waves a CU holds, by LDS and registers both: a grid beyond them leaves its last
+    // waves to start after others finish, one below them leaves SIMDs short of a wave (measured on
+    // the Q6_K LM head, 12 resident per CU: 11 per CU 131 us, 13 per CU 116 us, 12 per CU 92.5 us)
+    int occ = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, vl_gemv_kernel<TY, NL, PF>, 64, lds) != hipSuccess || occ < 1)
+        occ = (int)std::max<size_t>(1, (160 * 1024) / lds);
+    const int per_cu = std::min(16, occ);
     const int64_t ngroups = (nr + GR - 1) / GR;
     const int64_t grid = std::min<int64_t>(ngroups, (int64_t)ncu * per_cu);
     hipLaunchKernelGGL((vl_gemv_kernel<TY, NL, PF>), dim3((unsigned)grid), dim3(64), lds, st, w, nb, nr, y, s);
