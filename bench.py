@@ -347,6 +347,8 @@ def bench_kquant(args):
         parts[name] = {"us": round(us, 2), "bytes": nbytes, "GBs": round(nbytes / (us * 1e-6) / 1e9, 1),
                        "type": ty, "k": k, "rows": rows}
     head = parts["lm_head_q6_K"]
+    tr = load_traffic("kquant_lm_head")   # the same shape and kernel, counted in a rocprofv3 --pmc run
+    traffic = tr["hbm_bytes_per_launch"] if tr and tr.get("algorithmic_bytes_per_launch") == head["bytes"] else None
     result = {
         "metric": "K-quant lane GEMV GB/s (Qwen3.6 Q6_K LM head, 2 lanes)",
         "value": head["GBs"], "unit": "GB/s", "n_gpus": 1, "steps": max(args.steps, 4), "warmup": 1,
@@ -358,7 +360,7 @@ def bench_kquant(args):
                                "(tests/golden/gguf_header_qwen36.json): output.weight Q6_K [248320 x 2048]",
                    "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": head["GBs"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                     "frac": round(head["GBs"] / PEAK_HBM_GBS, 4), "traffic": None,
+                     "frac": round(head["GBs"] / PEAK_HBM_GBS, 4), "traffic": traffic,
                      "kernel": "vl_gemv_kernel<6>", "bytes_per_launch": head["bytes"]},
         "breakdown": parts,
     }

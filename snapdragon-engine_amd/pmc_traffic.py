@@ -8,6 +8,13 @@ measured/true ratio and writes profiles/<key>_traffic.json, which bench.py uses 
 
     python snapdragon-engine_amd/pmc_traffic.py --probe-fetch DIR --probe-write DIR \\
         --copy-fetch DIR --copy-write DIR --probe-json FILE [--out profiles/fused_verify_traffic.json]
+
+For a kernel launched outside the engine (a fixed shape, e.g. the K-quant GEMV of `bench.py --kquant`),
+--algorithmic BYTES replaces --probe-json and every dispatch of --kernel (a name substring) counts:
+
+    python snapdragon-engine_amd/pmc_traffic.py --probe-fetch DIR --probe-write DIR --copy-fetch DIR \\
+        --copy-write DIR --kernel "vl_gemv_kernel<6, 2, 8>" --algorithmic 419168832 \\
+        --out profiles/kquant_lm_head_traffic.json
 """
 import argparse
 import csv
@@ -44,14 +51,22 @@ def largest(vals, n):
 
 def main():
     ap = argparse.ArgumentParser()
-    for k in ("probe-fetch", "probe-write", "copy-fetch", "copy-write", "probe-json"):
+    for k in ("probe-fetch", "probe-write", "copy-fetch", "copy-write"):
         ap.add_argument("--" + k, required=True)
+    ap.add_argument("--probe-json")
+    ap.add_argument("--algorithmic", type=int)
     ap.add_argument("--kernel", default="fused_kernel")
     ap.add_argument("--out", default=os.path.join(os.path.dirname(os.path.abspath(__file__)), "..", "profiles",
                                                   "fused_verify_traffic.json"))
     a = ap.parse_args()
-    with open(a.probe_json) as f:
-        probe = next(json.loads(line) for line in f if line.startswith("{") and "pmc_probe" in line)
+    if a.probe_json:
+        with open(a.probe_json) as f:
+            probe = next(json.loads(line) for line in f if line.startswith("{") and "pmc_probe" in line)
+    elif a.algorithmic:
+        probe = {"pmc_probe": a.kernel, "algorithmic_bytes_per_launch": a.algorithmic,
+                 "launches": len(per_dispatch(a.probe_fetch, "FETCH_SIZE", a.kernel))}
+    else:
+        raise SystemExit("--probe-json or --algorithmic is required")
     n = probe["launches"]
     copy_bytes = 1 << 30
     cf = largest(per_dispatch(a.copy_fetch, "FETCH_SIZE", ""), 1)[0] * 1024
@@ -70,9 +85,10 @@ def main():
         "hbm_bytes_per_launch": int(fetch + write),
         "algorithmic_bytes_per_launch": probe["algorithmic_bytes_per_launch"],
         "traffic_over_algorithmic": round((fetch + write) / probe["algorithmic_bytes_per_launch"], 4),
-        "positions": probe["positions"],
-        "union_experts_per_moe_layer": probe["union_experts_per_moe_layer"],
     }
+    for k in ("positions", "union_experts_per_moe_layer"):
+        if k in probe:
+            res[k] = probe[k]
     os.makedirs(os.path.dirname(os.path.abspath(a.out)), exist_ok=True)
     with open(a.out, "w") as f:
         json.dump(res, f, indent=1)
