@@ -63,20 +63,23 @@ int oxe_hip_quantize_row_q8_0(const float *x, int64_t k, int64_t nrows, int8_t *
     return oxe::quantize_q8_0(x, k * nrows, q, d, (hipStream_t)stream);
 }
 
+// oxe_vl_gemv's contract (crates/kernels-sys/csrc/oxe_vl.inc:78-107, bound as `!= 0` by
+// gemv_lanes_raw, crates/kernels-sys/src/lib.rs:652-666): 1 when done; 0 with nothing written when
+// there is no kernel for the call (lanes outside 1..4, no rows, k not a positive multiple of 32 or
+// past the one-wave-per-row kernel's LDS); -2 on a launch error
 int oxe_hip_gemv_q8_0(int64_t k, int64_t nr, int nl, const int8_t *wq, const uint16_t *wd, const int8_t *xq,
                       const uint16_t *xd, float *y, int32_t *isum, void *stream) {
-    if (nr <= 0 || nl < 1 || nl > 2 || k <= 0 || k % 32 != 0) return -1;
+    if (nr <= 0 || nl < 1 || nl > oxe::GEMV_MAX_LANES || k <= 0 || k % 32 != 0) return 0;
     if (k != 512 && k != 2048 && k != 4096) {
         const size_t lds = (size_t)oxe::GG_ROWS * nl * (k / 32) * sizeof(int32_t);
-        if (lds > 64 * 1024) return -1;   // k > 65536 with 2 lanes (131072 with 1)
+        if (lds > 64 * 1024) return 0;   // k > 32768 with 4 lanes, 65536 with 2, 131072 with 1
         hipLaunchKernelGGL(oxe::gemv_any_kernel, dim3((unsigned)((nr + oxe::GG_ROWS - 1) / oxe::GG_ROWS)),
                            dim3(64 * oxe::GG_ROWS), lds, (hipStream_t)stream, k, nr, nl, wq, wd, xq, xd, y, isum);
-        return hipGetLastError() == hipSuccess ? 0 : -2;
+        return hipGetLastError() == hipSuccess ? 1 : -2;
     }
     oxe::EpiStore epi{y, nr, nullptr, 0};
-    const int rc = oxe::gemv_launch_k(k, nl, wq, wd, nr, oxe::Acts{xq, xd}, isum, epi, (hipStream_t)stream);
-    if (rc != 0) return rc;
-    return hipGetLastError() == hipSuccess ? 0 : -2;
+    if (oxe::gemv_launch_k(k, nl, wq, wd, nr, oxe::Acts{xq, xd}, isum, epi, (hipStream_t)stream) != 0) return 0;
+    return hipGetLastError() == hipSuccess ? 1 : -2;
 }
 
 }  // extern "C"

@@ -897,9 +897,9 @@ int Engine::pf_chunk(const uint32_t *toks, int T, float *h_out) {
     hipLaunchKernelGGL(norm_quant_kernel, dim3(T), dim3(PT), 0, st, m.tok_embd, nullptr, pfb.x, m.out_norm, eps, pfb.xq,
                        pfb.xd, (int64_t)E, pfb.xn);
     // the LM head of one token is a weight stream: the lane GEMV (HBM-bound), not the GEMM
-    if ((rc = oxe_hip_gemv_q8_0(E, m.output.rows, 1, m.output.q, m.output.d, pfb.xq + (int64_t)(T - 1) * E,
-                                pfb.xd + (int64_t)(T - 1) * (E / 32), b.logits, nullptr, st)))
-        return rc;
+    rc = oxe_hip_gemv_q8_0(E, m.output.rows, 1, m.output.q, m.output.d, pfb.xq + (int64_t)(T - 1) * E,
+                           pfb.xd + (int64_t)(T - 1) * (E / 32), b.logits, nullptr, st);
+    if (rc != 1) return rc == 0 ? -1 : rc;   // 1: done (oxe_vl_gemv's convention)
     if (hipMemcpyAsync(b.hid, pfb.xn + (int64_t)(T - 1) * E, (size_t)E * 4, hipMemcpyDeviceToDevice, st) != hipSuccess)
         return -2;
     if (h_out && hipMemcpyAsync(h_out, pfb.xn, (size_t)T * E * 4, hipMemcpyDeviceToHost, st) != hipSuccess) return -2;

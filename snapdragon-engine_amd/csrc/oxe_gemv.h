@@ -1,4 +1,4 @@
-// Q8_0 GEMV tile for 1-2 activation lanes in one weight pass (gfx950), shared by every kernel that
+// Q8_0 GEMV tile for 1-4 activation lanes in one weight pass (gfx950), shared by every kernel that
 // reads Q8_0 weights (dense projections, experts, the LM head).
 //
 // Contract (reference: ggml_gemv_q8_0_4x8_q8_0 NEON+dotprod, vendor/ggml-subset/generated/
@@ -20,6 +20,7 @@
 namespace oxe {
 
 constexpr int GEMV_THREADS = 256;
+constexpr int GEMV_MAX_LANES = 4;   // the reference's OXE_VL_MAX_LANES
 
 template <int K>
 struct GemvGeom {
@@ -161,6 +162,8 @@ inline int gemv_launch(int nl, const int8_t *wq, const uint16_t *wd, int64_t nro
     const unsigned nb = (unsigned)((nrows + R - 1) / R);
     if (nl == 1) hipLaunchKernelGGL((gemv_kernel<K, 1, Epi>), dim3(nb), dim3(GEMV_THREADS), 0, st, wq, wd, nrows, a, isum_out, epi);
     else if (nl == 2) hipLaunchKernelGGL((gemv_kernel<K, 2, Epi>), dim3(nb), dim3(GEMV_THREADS), 0, st, wq, wd, nrows, a, isum_out, epi);
+    else if (nl == 3) hipLaunchKernelGGL((gemv_kernel<K, 3, Epi>), dim3(nb), dim3(GEMV_THREADS), 0, st, wq, wd, nrows, a, isum_out, epi);
+    else if (nl == 4) hipLaunchKernelGGL((gemv_kernel<K, 4, Epi>), dim3(nb), dim3(GEMV_THREADS), 0, st, wq, wd, nrows, a, isum_out, epi);
     else return -1;
     return 0;
 }
