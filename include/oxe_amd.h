@@ -7,7 +7,10 @@
  * (hipStream_t passed as void*), int status codes. No allocation inside kernel-level calls.
  *
  * Status codes: 0 ok, -1 bad shape/argument (nothing written, like the reference's
- * oxe_repack_q8_0_4x8 returning -1), -2 HIP launch/runtime error, -3 out of device memory.
+ * oxe_repack_q8_0_4x8 returning -1), -2 HIP launch/runtime error, -3 out of device memory,
+ * -4 device-side stop (a device-driven step that does not fit the context), -5 a fused run aborted
+ * (one of its exchange polls timed out; oxe_last_error() names the word): the run commits nothing,
+ * the engine keeps the state before it, and the call may be repeated.
  *
  * Every declaration names the reference interface it replaces (file:line in the reference tree).
  */
@@ -31,12 +34,14 @@ typedef struct oxe_engine oxe_engine;
  * vendor/ggml-subset/generated/quants_subset.c:6-42). */
 OXE_API int oxe_hip_quantize_row_q8_0(const float *x, int64_t k, int64_t nrows, int8_t *q, uint16_t *d, void *stream);
 
-/* Q8_0 lane GEMV: y[l][r] = W[r] . x[l] for nl = 1 or 2 lanes in one weight pass; weights as int8
- * codes [nr][k] + fp16 scales [nr][k/32] (this build's layout; see oxe_hip_repack_q8_0), lanes as
- * produced by oxe_hip_quantize_row_q8_0; k any multiple of 32 up to 65536 (tuned kernels for 512,
- * 2048 and 4096, a one-wave-per-row kernel otherwise). isum (optional, may be NULL):
- * the exact int32 block dots [nl][nr][k/32]. Replaces oxe_vl_gemv (lib.rs:113, type 80) and
- * ggml_gemv_q8_0_4x8_q8_0 (lib.rs:75). */
+/* Q8_0 lane GEMV: y[l][r] = W[r] . x[l] for nl = 1..4 lanes in one weight pass, each lane bit for
+ * bit the per-lane GEMV; weights as int8 codes [nr][k] + fp16 scales [nr][k/32] (this build's
+ * layout; see oxe_hip_repack_q8_0), lanes as produced by oxe_hip_quantize_row_q8_0; k any multiple
+ * of 32 (tuned kernels for 512, 2048 and 4096, a one-wave-per-row kernel otherwise, up to 131072 /
+ * nl ... 32768 at 4 lanes). isum (optional, may be NULL): the exact int32 block dots [nl][nr][k/32].
+ * Replaces oxe_vl_gemv type 80 (lib.rs:113; csrc/oxe_vl.inc:78-107) with its return convention:
+ * 1 = done, 0 = not handled with nothing written (nl outside 1..4, nr <= 0, k not a positive
+ * multiple of 32 or past the limit), -2 launch error; and ggml_gemv_q8_0_4x8_q8_0 (lib.rs:75). */
 OXE_API int oxe_hip_gemv_q8_0(int64_t k, int64_t nr, int nl, const int8_t *wq, const uint16_t *wd, const int8_t *xq,
                               const uint16_t *xd, float *y, int32_t *isum, void *stream);
 
@@ -79,7 +84,7 @@ OXE_API int oxe_hip_quantize_row_q8_K(const float *x, int64_t k, int64_t nrows, 
  * oxe_vl_gemv (crates/kernels-sys/src/lib.rs:113; csrc/oxe_vl.inc:78-107 and oxe_vl_q{3,4,5,6}k.inc),
  * whose weights are its 8-row interleaved repack, and its per-lane fallback ggml_gemv_q*_K_8x8_q8_K.
  * Returns as the reference: 1 = done, 0 = not handled, nothing written (another type, nl outside
- * 1..4, k not a multiple of 256 or above 65536, Q3_K / Q6_K with an odd number of blocks per row);
+ * 1..4, k not a multiple of 256 or above 8192, Q3_K / Q6_K with an odd number of blocks per row);
  * -2 launch error. */
 OXE_API int oxe_hip_vl_gemv(int type, int64_t k, int64_t nr, int nl, const void *w, const void *y, float *s,
                             void *stream);
@@ -100,6 +105,13 @@ OXE_API const char *oxe_last_error(void);
  * device memory. Replaces Engine::with_options (crates/model/src/engine.rs:869-1000) with
  * verify_lanes 2 and an MTP head. */
 OXE_API int oxe_engine_create(const oxe_model_desc *desc, uint64_t seed, int n_ctx, oxe_engine **out);
+/* oxe_engine_create on the caller's stream (hipStream_t as void*, the null stream included; the
+ * device-driven steps' graph capture needs a created stream): every launch and copy of the engine,
+ * weight synthesis and loading included, goes to it, and destroy leaves it to the caller. The
+ * reference's engine runs on the caller's thread (Engine::with_options, engine.rs:869); this is its
+ * device counterpart. */
+OXE_API int oxe_engine_create_on(const oxe_model_desc *desc, uint64_t seed, int n_ctx, void *stream,
+                                 oxe_engine **out);
 OXE_API void oxe_engine_destroy(oxe_engine *e);
 /* Fill every weight with the synthetic model of include/oxe_model.h (the benchmark's model). */
 OXE_API int oxe_engine_synth_weights(oxe_engine *e);
@@ -222,8 +234,8 @@ OXE_API int oxe_engine_load_gguf(oxe_engine *e, const oxe_gguf *g);
  * forbid hipMalloc). Uploads are staged through a 16 MiB device array of the library (one per GPU,
  * held until the process ends) instead of a 256 MiB buffer allocated per call; a tensor that must be
  * staged whole above 16 MiB (one expert's matrix, an interleaved gate / up matrix) is refused by
- * name (-1). The engine's device must be current. Calls that overlap on one GPU share the array and
- * race: serialise them. */
+ * name (-1). The engine's device must be current. Calls on one GPU share the array: a per-device
+ * lock makes overlapping calls (other threads, other streams) run one after another. */
 OXE_API int oxe_engine_load_gguf_noalloc(oxe_engine *e, const oxe_gguf *g);
 /* open + model_desc + engine_create + load_gguf */
 OXE_API int oxe_engine_create_from_gguf(const char *path, int n_ctx, oxe_engine **out);
@@ -264,7 +276,9 @@ OXE_API int oxe_mtp_rewind(oxe_engine *e, int m);
  * runs two drafts and verifies x, d1 and then d2 in pieces of at most two lanes, the second piece
  * only when d1 was accepted and d2 matches (mtp.rs:522-592). A step that does not fit the context
  * (depth 1: 2 positions, depth 2: 3) stops the steps: end returns -4, and the caller continues with
- * host-driven steps (which shorten the draft chain to the room left, as the reference does). */
+ * host-driven steps (which shorten the draft chain to the room left, as the reference does). A run
+ * that aborted stops the steps as well: end returns -5 after handing back the state of the last step
+ * that ran (tokens, position, pending pairs), so decoding continues from there. */
 OXE_API int oxe_mtp_device_begin(oxe_engine *e, uint32_t x, int out_cap);
 OXE_API int oxe_mtp_device_steps(oxe_engine *e, int k, int use_graph);
 OXE_API int oxe_mtp_device_end(oxe_engine *e, uint32_t *out_tok, int cap, int *n_out, uint32_t *next_x);

@@ -14,7 +14,7 @@ extern "C" {
 
 const char *oxe_last_error(void) { return oxe::g_last_error.c_str(); }
 
-int oxe_engine_create(const oxe_model_desc *desc, uint64_t seed, int n_ctx, oxe_engine **out) {
+static int engine_create(const oxe_model_desc *desc, uint64_t seed, int n_ctx, bool caller, void *stream, oxe_engine **out) {
     // the attention kernel keeps a kv group's f16 probabilities in LDS: contexts up to 6144
     if (!desc || !out || n_ctx < 1 || n_ctx > 6144) {
         oxe::set_err("n_ctx must be in [1, 6144]");
@@ -26,7 +26,7 @@ int oxe_engine_create(const oxe_model_desc *desc, uint64_t seed, int n_ctx, oxe_
     }
     Engine *e = new Engine();
     try {
-        e->create(*desc, seed, n_ctx);
+        e->create(*desc, seed, n_ctx, caller, (hipStream_t)stream);
     } catch (const std::exception &ex) {
         oxe::set_err(ex.what());
         delete e;
@@ -34,6 +34,14 @@ int oxe_engine_create(const oxe_model_desc *desc, uint64_t seed, int n_ctx, oxe_
     }
     *out = (oxe_engine *)e;
     return 0;
+}
+
+int oxe_engine_create(const oxe_model_desc *desc, uint64_t seed, int n_ctx, oxe_engine **out) {
+    return engine_create(desc, seed, n_ctx, false, nullptr, out);
+}
+
+int oxe_engine_create_on(const oxe_model_desc *desc, uint64_t seed, int n_ctx, void *stream, oxe_engine **out) {
+    return engine_create(desc, seed, n_ctx, true, stream, out);
 }
 
 void oxe_engine_destroy(oxe_engine *e) { delete (Engine *)e; }

@@ -197,6 +197,9 @@ constexpr int LOAD_SCRATCH_MAX_DEV = 64;
 static __device__ __align__(256) uint8_t load_scratch[LOAD_SCRATCH_BYTES];
 static std::mutex load_scratch_mu;
 static uint8_t *load_scratch_ptr[LOAD_SCRATCH_MAX_DEV];
+// held by an allocation-free load from its first upload until its final stream synchronisation, so
+// overlapping calls on one GPU (other threads, other streams) take turns with the array
+static std::mutex load_stage_mu[LOAD_SCRATCH_MAX_DEV];
 
 // the device address of device dev's load_scratch (dev must be current); null on failure
 static uint8_t *load_scratch_of(int dev) {
@@ -253,7 +256,10 @@ int oxe_engine_load_gguf_noalloc(oxe_engine *e, const oxe_gguf *gg) {
     const int rc = load_gguf_check(e, gg);
     if (rc) return rc;
     // every upload goes through the 16 MiB array: a tensor group that must be staged whole (one
-    // expert's matrix, an interleaved gate / up matrix) above that size is refused by name
+    // expert's matrix, an interleaved gate / up matrix) above that size is refused by name. The
+    // device's staging lock is held until load_gguf has synchronised its stream (every copy out of
+    // the array has completed).
+    std::lock_guard<std::mutex> lk(oxe::load_stage_mu[cur]);
     return g->load_gguf(*(const oxe::Gguf *)gg, stage, oxe::LOAD_SCRATCH_BYTES);
 }
 

@@ -476,9 +476,18 @@ int MtpDriverHost::dev_end(Engine &e, uint32_t *out_tok, int cap, int *n_out, ui
     MtpState s{};
     if (hipMemcpyAsync(&s, e.mtp_state, sizeof(s), hipMemcpyDeviceToHost, e.st) != hipSuccess) return -2;
     if (hipStreamSynchronize(e.st) != hipSuccess) return -2;
-    if (int rc = e.fused_check()) return rc;
+    // An aborted run (-5) commits nothing, and every step after it in this batch is inactive: the
+    // device state is that of the last step that ran, and is handed back below like any other.
+    const int abort_rc = e.fused_check();
+    if (abort_rc != 0 && abort_rc != -5) return abort_rc;
+    const bool aborted = abort_rc == -5 || (s.err & 4) != 0;
     if (s.zcol >= 0 && s.zcol < e.m.n_ctx) {   // the last rejected lane's V^T column (zero_v)
         launch_zero_v(e.m, e.n_att_main, s.zcol, s.zcol + 1, e.st);
+        if (hipStreamSynchronize(e.st) != hipSuccess) return -2;
+    }
+    if (aborted && s.pos < e.m.n_ctx) {
+        // the V^T columns an aborted verify (up to 3 lanes from pos) may have written go back to +0
+        launch_zero_v(e.m, e.n_att_main, s.pos, std::min(s.pos + 3, e.m.n_ctx), e.st);
         if (hipStreamSynchronize(e.st) != hipSuccess) return -2;
     }
     const int n = std::min(s.n_out, cap);
@@ -508,6 +517,10 @@ int MtpDriverHost::dev_end(Engine &e, uint32_t *out_tok, int cap, int *n_out, ui
     steps += s.steps;
     accepted += s.accepted;
     drafted += (int64_t)s.steps * e.dev_depth;   // dev_depth drafts per device-driven step
+    if (aborted) {
+        if (abort_rc == 0) set_err("fused run aborted: an exchange poll timed out (nothing committed)");
+        return -5;
+    }
     return s.err ? -4 : 0;
 }
 
@@ -555,6 +568,10 @@ int Engine::mtp_steps_async(int k, bool use_graph) {
         return hipGetLastError() == hipSuccess ? 0 : -2;
     }
     if (!graph_exec) {
+        if (!st) {
+            set_err("graph steps need a created stream: this engine runs on the null stream");
+            return -1;
+        }
         if (hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal) != hipSuccess) return -2;
         fz_capturing = true;
         if (dev_depth == 2) enqueue_mtp_device_step2();

@@ -74,6 +74,7 @@ struct Engine {
     uint64_t seed = 0;
     int dev = 0;            // the device current at creation (every buffer and the stream live there)
     hipStream_t st = nullptr;
+    bool own_stream = true; // st created by the engine (destroyed with it), else the caller's
     ModelRt m{};
     std::vector<LayerW> L;  // n_layer (+1 MTP block)
     ActBufs b{};
@@ -215,9 +216,9 @@ struct Engine {
     ~Engine() {
         for (hipEvent_t ev : probe_ev) (void)hipEventDestroy(ev);
         if (graph_exec) (void)hipGraphExecDestroy(graph_exec);
-        if (st) (void)hipStreamSynchronize(st);
+        (void)hipStreamSynchronize(st);
         for (void *p : allocs) (void)hipFree(p);
-        if (st) (void)hipStreamDestroy(st);
+        if (st && own_stream) (void)hipStreamDestroy(st);
     }
 
     static bool shape_ok(const oxe_model_desc &d) {
@@ -228,11 +229,18 @@ struct Engine {
                d.full_attention_interval >= 1 && d.has_mtp == 1;
     }
 
-    void create(const oxe_model_desc &desc, uint64_t sd, int n_ctx) {
+    // caller: every launch and copy of this engine goes to the caller's `stream` (the null stream
+    // included); otherwise to a stream of its own
+    void create(const oxe_model_desc &desc, uint64_t sd, int n_ctx, bool caller = false, hipStream_t stream = nullptr) {
         d = desc;
         seed = sd;
         if (hipGetDevice(&dev) != hipSuccess) throw std::runtime_error("hipGetDevice failed");
-        if (hipStreamCreate(&st) != hipSuccess) throw std::runtime_error("hipStreamCreate failed");
+        if (caller) {
+            st = stream;
+            own_stream = false;
+        } else if (hipStreamCreate(&st) != hipSuccess) {
+            throw std::runtime_error("hipStreamCreate failed");
+        }
         m.n_layer = d.n_layer;
         m.n_vocab = d.n_vocab;
         m.n_ctx = (n_ctx + 255) / 256 * 256;
@@ -358,7 +366,8 @@ struct Engine {
         fz_xch = alloc<uint64_t>(tot);
         fz_xch_words = tot;
         FzXch xc;
-        uint64_t **parts[13] = {&xc.x, &xc.x1, &xc.p, &xc.g, &xc.o, &xc.od, &xc.lg, &xc.sg, &xc.hsh, &xc.hq, &xc.hd, &xc.sc, &xc.kx};
+        uint64_t **parts[13] = {&xc.x, &xc.x1, &xc.p, &xc.g, &xc.o, &xc.od, &xc.lg, &xc.sg, &xc.hsh, &xc.hq, &xc.hd,
+                                &xc.sc, &xc.kx};
         for (int i = 0; i < 13; i++) *parts[i] = fz_xch + off[i];
         fz_hooks = alloc<MtpHooks>(1);
         fz_keys = alloc<unsigned long long>((size_t)OXE_NL * fz_grid);
@@ -447,7 +456,9 @@ struct Engine {
         fz_launches += (uint64_t)n;
     }
     // after a run of the fused kernel was aborted (a poll that timed out): clear the error word,
-    // move the tag base on, and report
+    // move the tag base on, and report -5 (OXE_E_ABORT). An aborted run commits nothing: its lanes
+    // write only the recurrent slots after the current one and the K / V^T rows of their own
+    // positions, which the next run that reaches those positions writes again.
     int fused_check() {
         if (!fused) return 0;
         uint32_t err[5] = {0, 0, 0, 0, 0};
@@ -462,10 +473,10 @@ struct Engine {
             char msg[256];
             snprintf(msg, sizeof msg,
                      "fused run aborted: an exchange poll timed out (workgroup %u, byte offset %lld, tag %u expected, "
-                     "%u seen; sync words reset)",
+                     "%u seen; sync words reset, nothing committed)",
                      err[4], (long long)off, err[1], err[2]);
             set_err(msg);
-            return -4;
+            return -5;
         }
         return 0;
     }

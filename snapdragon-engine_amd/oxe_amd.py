@@ -149,13 +149,15 @@ def quantize_q8_0(x):
 
 
 def gemv_q8_0(wq, wd, xq, xd, y=None, isum=None):
-    """y[l, r] = Q8_0 GEMV of lanes l (1 or 2) over rows r; optional int32 block sums [nl, nr, k/32]."""
+    """y[l, r] = Q8_0 GEMV of lanes l (1..4) over rows r; optional int32 block sums [nl, nr, k/32]."""
     import torch
     nr, k = wq.shape
     nl = xq.shape[0]
     if y is None:
         y = torch.empty((nl, nr), dtype=torch.float32, device=wq.device)
-    check(lib().oxe_hip_gemv_q8_0(k, nr, nl, _p(wq), _p(wd), _p(xq), _p(xd), _p(y), _p(isum), _stream()), "gemv_q8_0")
+    rc = lib().oxe_hip_gemv_q8_0(k, nr, nl, _p(wq), _p(wd), _p(xq), _p(xd), _p(y), _p(isum), _stream())
+    if rc != 1:   # oxe_vl_gemv's convention: 1 done, 0 not handled (nothing written)
+        raise RuntimeError(f"gemv_q8_0 failed with status {rc}" + (": not handled" if rc == 0 else ""))
     return y
 
 
@@ -235,6 +237,7 @@ def _engine_sigs(L):
     sig = {
         "oxe_last_error": (C.c_char_p, []),
         "oxe_engine_create": (i32, [vp, C.c_uint64, i32, C.POINTER(C.c_void_p)]),
+        "oxe_engine_create_on": (i32, [vp, C.c_uint64, i32, vp, C.POINTER(C.c_void_p)]),
         "oxe_engine_destroy": (None, [vp]),
         "oxe_engine_synth_weights": (i32, [vp]),
         "oxe_engine_verify": (i32, [vp, u32p, i32, u32p]),
@@ -454,7 +457,9 @@ class Gguf:
 class Engine:
     """MI355X engine through the C ABI (Engine::{verify, commit, step, mtp_run, mtp_seed})."""
 
-    def __init__(self, desc, seed=0, n_ctx=1024, synth=True):
+    def __init__(self, desc, seed=0, n_ctx=1024, synth=True, stream=None):
+        """stream: a caller's hipStream_t (an int, e.g. torch.cuda.Stream().cuda_stream) that every
+        launch and copy of the engine then goes to (oxe_engine_create_on); None: the engine's own."""
         import numpy as np  # noqa: F401
         L = lib()
         if not hasattr(L, "_engine_sigs"):
@@ -462,7 +467,10 @@ class Engine:
             L._engine_sigs = True
         self.desc = desc
         h = C.c_void_p()
-        rc = L.oxe_engine_create(C.byref(desc), seed, n_ctx, C.byref(h))
+        if stream is None:
+            rc = L.oxe_engine_create(C.byref(desc), seed, n_ctx, C.byref(h))
+        else:
+            rc = L.oxe_engine_create_on(C.byref(desc), seed, n_ctx, C.c_void_p(int(stream)), C.byref(h))
         if rc != 0:
             raise RuntimeError(f"oxe_engine_create: {rc} {L.oxe_last_error()}")
         self.h = h

@@ -129,3 +129,33 @@ def test_lm_head_claimed_tail_bitexact():
         o.commit(1)
     g.close()
     o.close()
+
+
+@pytest.mark.parametrize("which", ["created", "null"])
+def test_engine_on_caller_stream(which):
+    """oxe_engine_create_on: an engine whose launches and copies all go to the caller's stream (a
+    torch stream, or the null stream) decodes bit for bit like one on its own stream: a batched
+    prompt, verify runs and device-driven MTP steps (graph steps on the created stream, eager ones
+    on the null stream, which cannot be captured)."""
+    import oxe_amd as A
+    import torch
+    d = O.desc_small()
+    ref = A.Engine(d, seed=5, n_ctx=N_CTX)
+    st = torch.cuda.Stream() if which == "created" else None
+    g = A.Engine(d, seed=5, n_ctx=N_CTX, stream=st.cuda_stream if st is not None else 0)
+    assert (g.stream() or 0) == (st.cuda_stream if st is not None else 0)
+    prompt = [int(v) % d.n_vocab for v in O.bench_prompt(20)]
+    xr, xg = ref.mtp_prefill_batched(prompt), g.mtp_prefill_batched(prompt)
+    assert xr == xg
+    assert np.array_equal(bits(g.hidden(0)), bits(ref.hidden(0)))
+    graph = which == "created"
+    out = []
+    for e, x in ((ref, xr), (g, xg)):
+        e.mtp_device_begin(x, 64)
+        e.mtp_device_steps(6, use_graph=graph)
+        out.append(e.mtp_device_end(64))
+    assert list(out[0][0]) == list(out[1][0]) and out[0][1] == out[1][1]
+    for ln in range(2):
+        assert np.array_equal(bits(g.logits(ln)), bits(ref.logits(ln))), ln
+    g.close()
+    ref.close()
