@@ -431,8 +431,8 @@ def main():
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain device copy of known size (the PMC byte-counter calibration)")
     ap.add_argument("--pmc-probe", action="store_true",
-                    help="only prefill and run the timed kernel's eager probe launches (for rocprofv3 --pmc), "
-                         "printing their algorithmic bytes")
+                    help="refused: counter collection over the engine's launches faults inside rocprofv3 "
+                         "(the fused verify run's `traffic` stays null)")
     ap.add_argument("--prefill", action="store_true",
                     help="BASELINE config 5 instead: batched prefill of --prefill-tokens prompt tokens "
                          "(--steps timed prefills after --warmup untimed ones)")
@@ -444,8 +444,17 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build runs the whole MTP-1 step on a single MI355X "
-              f"(--gpus {args.gpus} is not supported; see DESIGN.md for how the path would shard)", file=sys.stderr)
+              f"(--gpus {args.gpus} is not supported; the scaling unit is one engine per GPU on independent "
+              f"sequences)", file=sys.stderr)
         sys.exit(2)
+    if args.pmc_probe:
+        # Two runs of this mode under rocprofv3 --pmc FETCH_SIZE took a host SIGSEGV inside the
+        # profiler's dispatch interception at the engine's first kernel launch (synth_q8), once with
+        # the engine on a stream of its own and once on the caller's (torch's) stream; the cause is
+        # not in this program's reach, so counter collection over the engine is not run again.
+        sys.exit("--pmc-probe: counter collection over the engine's launches faults inside rocprofv3 "
+                 "(host SIGSEGV at the first launch, on the engine's own stream and on the caller's); "
+                 "not run. Counter runs over kernel-level launches (--kquant, --gemm-probe) work.")
     import torch
     if args.calibrate_copy:
         calibrate_copy(torch)
@@ -480,19 +489,6 @@ def main():
     eng.sync()
     setup_s = time.time() - t_setup
     cap = 2 * (args.steps + args.warmup) + 16
-    if args.pmc_probe:
-        # eager launches only (no graph): the profiler counts every dispatch of the probe steps
-        eng.mtp_device_begin(x, cap)
-        uni1, calls1 = eng.counter(66), eng.counter(67)
-        pos_p0 = eng.pos
-        avg_us, n_launch = eng.mtp_device_probe(8, probe_kind)
-        eng.mtp_device_end(cap)
-        u_probe = (eng.counter(66) - uni1) / max(eng.counter(67) - calls1, 1)
-        kb = verify_bytes((pos_p0 + eng.pos) / 2, u_probe) if probe_kind == 10 else u_probe * EXPERT_GU
-        print(json.dumps({"pmc_probe": "fused_verify" if probe_kind == 10 else "experts_kernel",
-                          "launches": n_launch, "algorithmic_bytes_per_launch": int(kb), "avg_us": round(avg_us, 3),
-                          "positions": [pos_p0, eng.pos], "union_experts_per_moe_layer": round(u_probe, 3)}), flush=True)
-        return
     # warm-up (also captures the step graph)
     gen = [int(x)]
     eng.mtp_device_begin(x, cap)

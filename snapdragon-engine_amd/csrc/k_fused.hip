@@ -33,9 +33,7 @@ constexpr int SC_P = 16;                      // positions per scores chunk (wor
 constexpr int SC_KS = HD + 32;                // LDS row stride of cached K rows in halves (576 B: the 16 rows of a
                                               // wave quarter fall on distinct banks)
 constexpr uint32_t SPIN_MAX = 400000;         // ~0.4 s at one device-scope load per iteration
-#ifndef FZ_POLL_SLEEP
-#define FZ_POLL_SLEEP 1                       // s_sleep between polls of a missing word (units of 64 clocks)
-#endif
+constexpr int POLL_SLEEP = 1;                 // s_sleep between polls of a missing word (units of 64 clocks)
 
 // ---- address-space views ------------------------------------------------------------------------
 // Each layer's phases form one non-inlined function, so pointers reach it as generic pointers and
@@ -64,11 +62,7 @@ OXE_DEV T gld(const T *p) {
 template <class T>
 OXE_DEV T gldn(const T *p) {
     using R = typename RawOf<sizeof(T)>::T;
-#ifdef FZ_NO_NT
-    return __builtin_bit_cast(T, *(const FZ_GAS R *)p);
-#else
     return __builtin_bit_cast(T, __builtin_nontemporal_load((const FZ_GAS R *)p));
-#endif
 }
 template <class T>
 OXE_DEV const FZ_CAS T *uni(const T *p) {
@@ -134,7 +128,7 @@ OXE_DEV bool ll_spin(uint32_t &spins, uint32_t *err, const uint64_t *p, uint32_t
         return false;
     }
     if ((spins & 31) == 0 && cld32(err)) return false;
-    __builtin_amdgcn_s_sleep(FZ_POLL_SLEEP);
+    __builtin_amdgcn_s_sleep(POLL_SLEEP);
     return true;
 }
 // The exchange buffers as a buffer resource: two adjacent tagged words in one 16-byte device-scope
@@ -1326,20 +1320,10 @@ FZ_PHASE bool phase_moe(const RunCtl *ctl, const FusedArgs *ap, int il, int k, i
     if (!all_ok(ok, &ps.fail)) return false;
     tr_pass(c);
     tr_mark(c, 105);
-    // the first part of the next layer's projection slice streams while the routing computes (the
-    // memory pipeline is otherwise idle until the experts are known)
-#ifndef FZ_NO_PREFETCH
+    // the next layer's projection slice is loaded in parts between the down phase's steps
     const bool pf = il_next >= 0;
-#else
-    const bool pf = false;
-#endif
     const FZ_CAS LayerDev &Ln = layer_of(c, pf ? il_next : il);
     const int pre_rows = proj_rows(Ln);
-#ifdef FZ_PREFETCH_ONCE
-    if (pf) proj_load(Ln, b, c.G, 0, pre_rows, pp);
-#elif defined(FZ_PF_IN_ROUTING)
-    if (pf) proj_load_part<0>(Ln, b, c.G, 0, pre_rows, pp);
-#endif
     if ((t >> 6) < nl) route_wave(se.lg[t >> 6], t >> 6, ps.ro);
     __syncthreads();
     tr_mark(c, 106);
@@ -1401,13 +1385,8 @@ FZ_PHASE bool phase_moe(const RunCtl *ctl, const FusedArgs *ap, int il, int k, i
         const uint16_t *base = su < nu && su < OXE_MAX_UNION ? L.exp_down.d + (int64_t)e * E * (FF / 32) : L.shexp_down.d;
         dsc = gldn((const uint4 *)(base + (int64_t)(r0 + srr) * (FF / 32) + shf * 8));
     };
-#ifndef FZ_DW_EARLY
-#define FZ_DW_EARLY 0
-#endif
-#ifndef FZ_DW_PRE
-#define FZ_DW_PRE 5
-#endif
-    constexpr int DW_EARLY = FZ_DW_EARLY, DW_PRE = FZ_DW_PRE > FZ_DW_EARLY ? FZ_DW_PRE : FZ_DW_EARLY;
+    // measured best: none behind the gate / up rows, five of the nine before the inputs are polled
+    constexpr int DW_EARLY = 0, DW_PRE = 5;
 #pragma unroll
     for (int q = 0; q < DW_EARLY; q++) dload(q);
     if (DW_EARLY > 0) sload();
@@ -1478,9 +1457,7 @@ FZ_PHASE bool phase_moe(const RunCtl *ctl, const FusedArgs *ap, int il, int k, i
     const float x1v = u2f(u[NHW + 1 + NL]), sgv = u2f(u[NHW + 2 + NL]);
 #pragma unroll
     for (int q = DW_PRE; q < 9; q++) dload(q);
-#if !defined(FZ_PREFETCH_ONCE) && !defined(FZ_PF_IN_ROUTING)
     if (pf) proj_load_part<0>(Ln, b, c.G, 0, pre_rows, pp);
-#endif
     // Q8_0 of the shared expert's h: element t of lane l in thread t, a block per half wave
     static_assert(FFSH == FT, "one shared-expert element per thread and lane");
 #pragma unroll
@@ -1498,9 +1475,7 @@ FZ_PHASE bool phase_moe(const RunCtl *ctl, const FusedArgs *ap, int il, int k, i
     sd.hd[ld_][ud][t % (FF / 32)] = (uint16_t)hdv;
     if (!all_ok(ok, &ps.fail)) return false;
     tr_pass(c);
-#ifndef FZ_PREFETCH_ONCE
     if (pf) proj_load_part<1>(Ln, b, c.G, 0, pre_rows, pp);
-#endif
     tr_mark(c, 161);
     if (t < DW_UNITS * 16) {
         // scale products of (unit su, row srr, blocks [8 shf, 8 shf + 8)) for every lane
@@ -1532,9 +1507,7 @@ FZ_PHASE bool phase_moe(const RunCtl *ctl, const FusedArgs *ap, int il, int k, i
         }
     }
     __syncthreads();
-#ifndef FZ_PREFETCH_ONCE
     if (pf) proj_load_part<2>(Ln, b, c.G, 0, pre_rows, pp);
-#endif
     tr_mark(c, 162);
     if (t < DW_UNITS * NL * 8) {
         const int u = t / (NL * 8), l = (t / 8) % NL, r = t % 8;
@@ -1553,9 +1526,7 @@ FZ_PHASE bool phase_moe(const RunCtl *ctl, const FusedArgs *ap, int il, int k, i
         }
     }
     __syncthreads();
-#ifndef FZ_PREFETCH_ONCE
     if (pf) proj_load_part<3>(Ln, b, c.G, 0, pre_rows, pp);
-#endif
     tr_mark(c, 163);
     if (t < NL * 8) {
         const int l = t / 8, r = t % 8;
@@ -2071,10 +2042,8 @@ FZ_PHASE bool phase_head(const RunCtl *ctl, const FusedArgs *ap, const float *no
     // Tiles: `per` (even) in a contiguous range per workgroup, then pairs of the remaining tiles
     // claimed from a counter, so the workgroups that stream faster take more of the tail (the HBM
     // gives some XCDs' CUs less than others). Fewer than 4 tiles per workgroup: a static split only.
-#ifndef FZ_HEAD_SPCT
-#define FZ_HEAD_SPCT 90
-#endif
-    const int64_t per = 2 * ((ntiles * FZ_HEAD_SPCT / 100) / (2 * c.G));
+    constexpr int64_t STATIC_PCT = 90;   // share of the tiles split statically (measured best)
+    const int64_t per = 2 * ((ntiles * STATIC_PCT / 100) / (2 * c.G));
     const bool dyn = per >= 4;
     const int64_t t0 = dyn ? per * c.b : ntiles * c.b / c.G, t1 = dyn ? t0 + per : ntiles * (c.b + 1) / c.G;
     WSlice<E, HEAD_P> A, B;
@@ -2181,11 +2150,7 @@ __device__ __attribute__((noinline)) bool run_step(const RunCtl *ctl, const Fuse
     // the residual: the embedding (written by the projection phase) or the previous layer's output
     const uint32_t xtag = base + 1u + (embed ? 8u * (uint32_t)k + PH_PROJ : 8u * (uint32_t)(k - 1) + PH_DOWN);
     DnPre dp;
-#ifndef FZ_NO_PREFETCH
     if (!phase_proj<NL>(ctl, ap, il, k, embed, 0, att ? AT_ROWS : DN_ROWS, pre, ilp >= 0, dp)) return false;
-#else
-    if (!phase_proj<NL>(ctl, ap, il, k, embed, 0, att ? AT_ROWS : DN_ROWS, pre, false, dp)) return false;
-#endif
     if (!att) {
         if (!phase_dn<NL>(ctl, ap, il, k, dp)) return false;
     } else {

@@ -26,8 +26,9 @@ PHASES = {1: "proj", 2: "dn", 3: "scores", 4: "pv", 5: "out", 6: "router", 7: "e
           10: "head"}
 MARKS = {101: "experts: union", 102: "experts: gate/up loads issued", 103: "experts: issue drained",
          104: "experts: gate/up dot", 105: "experts: logits load", 106: "experts: route_wave",
-         111: "proj: norm prologue", 113: "proj: int dots", 112: "proj: chains", 171: "out: int dots", 172: "out: chains", 121: "dn: conv", 122: "dn: norms + gates",
-         123: "dn: delta rule", 124: "dn: head leader inputs", 125: "dn: head leader norm + store", 131: "router: norm prologue", 132: "router: f32 dots", 141: "pv: V tile to LDS",
+         111: "proj: norm prologue", 113: "proj: int dots", 112: "proj: chains",
+         117: "proj: int dots (again)", 118: "proj: chains (again)", 171: "out: int dots", 172: "out: chains", 121: "dn: conv", 122: "dn: norms + gates",
+         123: "dn: delta rule", 124: "dn: head's partial sums", 125: "dn: gated norm + codes", 131: "router: norm prologue", 132: "router: f32 dots", 141: "pv: V tile to LDS",
          142: "pv: V.p + reduce", 143: "pv: scores load + max", 144: "pv: exp, sum, probabilities", 151: "scores: q/k prologue",
          161: "down: inputs", 162: "down: block dots", 163: "down: chains"}
 
@@ -42,7 +43,11 @@ def analyse(tr):
     n = min(len(m) for m in mains)
     mm = np.stack([m[:n] for m in mains]).astype(np.int64)
     ids = mm[0, :, 0]
-    start, pas, end = mm[:, :, 1], mm[:, :, 2], mm[:, :, 3]
+    # a workgroup that takes no part in a phase records it with pass = 0: masked out below
+    on = mm[:, :, 2] > 0
+    start = np.ma.masked_array(mm[:, :, 1], ~on)
+    pas = np.ma.masked_array(mm[:, :, 2], ~on)
+    end = np.ma.masked_array(mm[:, :, 3], ~on)
     rel = pas.min(axis=0)
     done = end.max(axis=0)
     total = (done[-1] - start.min()) / 100.0
@@ -65,8 +70,8 @@ def analyse(tr):
         a = agg[name]
         if len(a) == 4:
             a += [[], []]
-        a[4].append(np.median(pas[:, k] - start[:, k]) / 100.0)
-        a[5].append(np.median(end[:, k] - pas[:, k]) / 100.0)
+        a[4].append(np.ma.median(pas[:, k] - start[:, k]) / 100.0)
+        a[5].append(np.ma.median(end[:, k] - pas[:, k]) / 100.0)
     return total, agg, marks, (ids, start, pas, end)
 
 
@@ -100,7 +105,7 @@ def timeline(ids, start, pas, end, k0, k1):
     rows = []
     for k in range(k0, k1):
         name = PHASES.get(int(ids[k]), str(int(ids[k])))
-        q = [np.percentile((v[:, k] - t0) / 100.0, (0, 50, 100)) for v in (start, pas, end)]
+        q = [np.percentile((v[:, k].compressed() - t0) / 100.0, (0, 50, 100)) for v in (start, pas, end)]
         rows.append((name, q))
     return rows
 
@@ -141,7 +146,7 @@ def main():
         if len(ks) < 2:
             continue
         k0 = ks[len(ks) // 2] - 1
-        k1 = min(k0 + 6, len(ids))
+        k1 = min(k0 + 7, len(ids))
         print(f"timeline of one {'DN' if want == 2 else 'attention'} layer (us; min / median / max over workgroups):")
         for name, q in timeline(*ev, k0, k1):
             print(f"  {name:8s} start {q[0][0]:6.2f} {q[0][1]:6.2f} {q[0][2]:6.2f} | inputs {q[1][0]:6.2f} {q[1][1]:6.2f} "

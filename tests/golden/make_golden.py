@@ -18,6 +18,8 @@ device path shows up as a diff against committed data:
   config5_state.npz  BASELINE config 5 on the 4-layer model (seed 7): 2048 prompt tokens decoded token
                      by token; SHA-256 of Engine::write_state's bytes (K rows, V^T rows, conv state, S),
                      of the last token's logits and h_nextn, and the next token
+  config5_full_state.npz  the same on the config-4 model (35B-A3B, 40 layers, seed 0), config 5's
+                     stated model (~40 GB of host memory, tens of minutes on 8 threads)
 Run: python tests/golden/make_golden.py [name ...]   (no name: the small fixtures; config4_ids needs
 ~40 GB of host memory and several minutes on 16 threads)
 """
@@ -140,9 +142,10 @@ def config4_ids(n_prompt=512, n_steps=264):
                 stats=np.array(list(drv.stats().values()), np.int64))
 
 
-def config5_state(n=2048):
-    d = O.desc_small()
-    e = O.Engine(d, seed=7, n_ctx=n + 256)
+def config5_state(n=2048, d=None, seed=7):
+    d = O.desc_small() if d is None else d
+    e = O.Engine(d, seed=seed, n_ctx=n + 256)
+    O.lib().oxo_set_keep_logits(e.h, 1)
     toks = (O.bench_prompt(n) % d.n_vocab).astype(np.uint32)
     x = None
     for i, t in enumerate(toks):
@@ -173,9 +176,14 @@ def config5_state(n=2048):
                 next=np.uint32(x), state_bytes=np.int64(len(state)))
 
 
+def config5_full_state(n=2048):
+    """config 5 at its stated size: the config-4 model (35B-A3B, 40 layers, seed 0)"""
+    return config5_state(n, O.desc_35b_a3b(), 0)
+
+
 MAKERS = dict(config1_slice=config1_slice, route=route, dn_step=dn_step, attn_head=attn_head,
               engine_small=engine_small)
-LARGE = dict(config4_ids=config4_ids, config5_state=config5_state)
+LARGE = dict(config4_ids=config4_ids, config5_state=config5_state, config5_full_state=config5_full_state)
 
 # GGUF header fixtures: the fields the tests use of the reference's own test fixtures
 # tests/fixtures/{qwen36,ornith}.json (model_inspect.py's reading of the real Qwen3.6 and Ornith
