@@ -10,6 +10,8 @@
 
 #include "oxe_common.h"
 
+#include <mutex>
+
 namespace oxe {
 namespace kq {
 
@@ -393,26 +395,56 @@ size_t vl_gemv_lds(int bb, int rr, int nb, int nl) {
     return (size_t)align16(GR * nb * bb) + (size_t)align16(nl * nb * (2 * YH + 1) * 4) + (size_t)64 * ((nl * rr) | 1) * 4;
 }
 
+constexpr int KQ_MAX_DEV = 64;
 template <int TY, int NL, int PF>
 int vl_gemv_launch_pf(const uint8_t *w, int nb, int64_t nr, const uint8_t *y, float *s, hipStream_t st) {
     constexpr int BB = BT<TY>::B;
     const size_t lds = vl_gemv_lds(BB, BT<TY>::R, nb, NL);
-    static bool attr = false;   // above 64 KiB of LDS the kernel needs the attribute (160 KiB per CU)
-    if (lds > 65536 && !attr) {
-        if (hipFuncSetAttribute((const void *)vl_gemv_kernel<TY, NL, PF>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                (int)lds) != hipSuccess)
-            return -2;
-        attr = true;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= KQ_MAX_DEV) return -2;
+    // per instantiation and device: the dynamic LDS the kernel is configured for (above 64 KiB it
+    // needs the attribute; 160 KiB per CU), the CU count, and the occupancy per LDS size, each asked
+    // of the runtime once (a query per launch would sit on the decode path)
+    struct Cache {
+        size_t configured = 65536;
+        int ncu = 0;
+        size_t lds[8] = {};
+        int occ[8] = {};
+    };
+    static Cache cache[KQ_MAX_DEV];
+    static std::mutex mu;
+    int ncu = 256, occ = 0;
+    {
+        std::lock_guard<std::mutex> lk(mu);
+        Cache &cc = cache[dev];
+        if (lds > cc.configured) {
+            if (hipFuncSetAttribute((const void *)vl_gemv_kernel<TY, NL, PF>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                    (int)lds) != hipSuccess)
+                return -2;
+            cc.configured = lds;
+        }
+        if (cc.ncu == 0 && hipDeviceGetAttribute(&cc.ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+            cc.ncu = 256;
+        ncu = cc.ncu;
+        int slot = -1;
+        for (int i = 0; i < 8 && slot < 0; i++)
+            if (cc.lds[i] == lds || cc.lds[i] == 0) slot = i;
+        if (slot >= 0 && cc.lds[slot] == lds) {
+            occ = cc.occ[slot];
+        } else {
+            // exactly the waves a CU holds, by LDS and registers both: a grid beyond them leaves its
+            // last waves to start after others finish, one below them leaves SIMDs short of a wave
+            // (measured on the Q6_K LM head, 12 resident per CU: 11 per CU 131 us, 13 per CU 116 us,
+            // 12 per CU 92.5 us)
+            if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, vl_gemv_kernel<TY, NL, PF>, 64, lds) != hipSuccess ||
+                occ < 1)
+                occ = (int)std::max<size_t>(1, (160 * 1024) / lds);
+            if (slot >= 0) {
+                cc.lds[slot] = lds;
+                cc.occ[slot] = occ;
+            }
+        }
     }
-    int dev = 0, ncu = 256;
-    (void)hipGetDevice(&dev);
-    (void)hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev);
-    // exactly the waves a CU holds, by LDS and registers both: a grid beyond them leaves its last
-    // waves to start after others finish, one below them leaves SIMDs short of a wave (measured on
-    // the Q6_K LM head, 12 resident per CU: 11 per CU 131 us, 13 per CU 116 us, 12 per CU 92.5 us)
-    int occ = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, vl_gemv_kernel<TY, NL, PF>, 64, lds) != hipSuccess || occ < 1)
-        occ = (int)std::max<size_t>(1, (160 * 1024) / lds);
     const int per_cu = std::min(16, occ);
     const int64_t ngroups = (nr + GR - 1) / GR;
     const int64_t grid = std::min<int64_t>(ngroups, (int64_t)ncu * per_cu);

@@ -418,6 +418,27 @@ def test_delta_rule_math():
     assert np.allclose(out, want_out, rtol=1e-4, atol=1e-5)
 
 
+def test_delta_rule_update_is_fused():
+    """The rank-1 update row += k * delta is one fused multiply-add per element (ggml_vec_mad_f32's
+    vfmaq_f32, oxe_ops.cpp:324), not a rounded product then a sum. Hand-derived case: S = 0 but
+    S[0][0] = -1, k = e0 * (1 + 2^-12), v = 0, beta = 1, g = 0 (decay 1). Then sk = -(1 + 2^-12) and
+    delta = 1 + 2^-12 exactly; the fused update gives (1 + 2^-12)^2 - 1 = 2^-11 + 2^-24 exactly,
+    where the unfused one rounds the product to 1 + 2^-11 (a tie, to even) and gives 2^-11."""
+    sv = 16
+    s = np.zeros((sv, sv), np.float32)
+    s[0, 0] = -1.0
+    k = np.zeros(sv, np.float32)
+    k[0] = np.float32(1.0 + 2.0 ** -12)
+    q = np.zeros(sv, np.float32)
+    q[0] = 1.0
+    v = np.zeros(sv, np.float32)
+    so, out = dn_step(s, q, k, v, 0.0, 1.0)
+    fused = np.float32(2.0 ** -11 + 2.0 ** -24)
+    assert so[0, 0] == fused, (so[0, 0], fused, np.float32(2.0 ** -11))
+    assert np.array_equal(so[1:], s[1:]) and np.array_equal(so[0, 1:], s[0, 1:])
+    assert out[0] == fused / np.float32(4.0) and not out[1:].any()
+
+
 def test_delta_rule_special_cases():
     rng = np.random.default_rng(12)
     sv = 16
