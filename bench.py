@@ -368,6 +368,147 @@ def bench_kquant(args):
     print(json.dumps(result), flush=True)
 
 
+def config_line(args, n, value_gbs, us, nbytes, floor_us, workload, dtype, kernel, parts, parity):
+    return {
+        "metric": f"BASELINE config {n} GB/s (% of ~8 TB/s HBM)", "value": round(value_gbs, 1), "unit": "GB/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": 1, "ms_per_step": round(us / 1e3, 5), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": dtype, "data": "synthetic (seeded)",
+        "config": {"workload": workload, "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "achieved": round(value_gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(value_gbs / PEAK_HBM_GBS, 4), "traffic": None, "kernel": kernel,
+                     "bytes_per_launch": int(nbytes)},
+        "floor_us_at_8TBs": floor_us, "us": round(us, 2), "breakdown": parts, "parity": parity,
+        "cpu_baseline": None,
+    }
+
+
+def bench_config1(args):
+    """the Q8_0 lane GEMV W [4096 x 2048], 2 lanes (oxe_hip_gemv_q8_0), timed
+    over back-to-back calls rotating 40 weight copies (356 MB: beyond the 256 MB memory-side cache),
+    HIP events on torch's stream. Parity: the config-1 golden slice (64 rows of the seed-0 matrix,
+    tests/golden/config1_slice.npz), quantizer and GEMV bit for bit."""
+    import numpy as np
+    import torch
+    import oxe_amd as A
+    k, nr, copies = 2048, 4096, 40
+    g1 = np.load(os.path.join(ROOT, "tests", "golden", "config1_slice.npz"))
+    xq, xd = A.quantize_q8_0(torch.from_numpy(g1["x"]).cuda())
+    y = A.gemv_q8_0(torch.from_numpy(g1["wq"]).cuda(), torch.from_numpy(g1["wd"].view(np.int16)).cuda(), xq, xd)
+    parity = {"golden_rows": int(g1["wq"].shape[0]),
+              "identical_to_oracle": bool(np.array_equal(xq.cpu().numpy(), g1["xq"])
+                                          and np.array_equal(y.cpu().numpy().view(np.uint32), g1["y"].view(np.uint32)))}
+    ws = []
+    for c in range(copies):
+        g = torch.Generator(device="cuda").manual_seed(c)
+        q = torch.randint(-127, 128, (nr, k), dtype=torch.int8, device="cuda", generator=g)
+        d = torch.empty((nr, k // 32), dtype=torch.float16, device="cuda").uniform_(0.001, 0.02, generator=g)
+        ws.append((q, d.view(torch.int16)))
+    out = torch.empty((2, nr), device="cuda")
+    for q, d in ws:
+        A.gemv_q8_0(q, d, xq, xd, y=out)
+    torch.cuda.synchronize()
+    reps = max(args.steps, 400)
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ev0.record()
+    for i in range(reps):
+        q, d = ws[i % copies]
+        A.gemv_q8_0(q, d, xq, xd, y=out)
+    ev1.record()
+    torch.cuda.synchronize()
+    us = ev0.elapsed_time(ev1) * 1e3 / reps
+    nbytes = nr * k * Q8 + 2 * k * Q8 + 2 * nr * 4
+    args.steps = reps
+    return config_line(args, 1, nbytes / (us * 1e-6) / 1e9, us, nbytes, 1.12,
+                       "BASELINE config 1: Q8_0 GEMV W [4096 x 2048], 2 lanes, back-to-back calls over 40 copies",
+                       "int8 (Q8_0 codes, int32 block dots, fp32 chain)", "gemv_kernel<2048, 2>",
+                       {"calls": reps, "copies": copies}, parity)
+
+
+def _per_phase_probe(eng, toks_fn, kinds, reps):
+    """mean duration (us) and launches per verify of each kernel kind, over reps verifies of fresh
+    tokens (per-phase run mode)"""
+    res = {}
+    for kind in kinds:
+        tot, cnt = 0.0, 0
+        for r in range(reps):
+            us, n = eng.verify_probe(toks_fn(r), kind)
+            tot += us * n
+            cnt += n
+        res[kind] = (tot / max(cnt, 1), cnt / reps)
+    return res
+
+
+def bench_config2(args):
+    """one MoE layer with 2 lanes (router + shared gate, routing, the union's
+    gate / up + swiglu, down + combine), the per-phase kernels of the 35B-A3B model (router_kernel,
+    experts_kernel, down_kernel) timed with HIP events in 2-lane verifies of fresh token pairs; per
+    MoE layer = the sum of the three kernels' mean durations."""
+    import oxe_amd as A
+    d = A.desc_35b_a3b()
+    eng = A.Engine(d, seed=0, n_ctx=1024)
+    eng.set_fused(False)
+    eng.mtp_prefill_batched(A.bench_prompt(512))
+    reps = max(2, min(args.steps, 8))
+    toks = lambda r: [(r * 7919 + 17) % 150000 + 1000, (r * 104729 + 3) % 150000 + 1000]  # noqa: E731
+    u0, c0 = eng.counter(66), eng.counter(67)
+    res = _per_phase_probe(eng, toks, (6, 1, 2), reps)
+    union = (eng.counter(66) - u0) / max(eng.counter(67) - c0, 1)
+    us = sum(res[k][0] for k in (6, 1, 2))
+    nbytes = ROUTER + SHARED + union * (EXPERT_GU + EXPERT_DOWN) + 4 * E * 4
+    parts = {"router_us": round(res[6][0], 2), "experts_us": round(res[1][0], 2), "down_us": round(res[2][0], 2),
+             "union_experts": round(union, 2), "verifies": 3 * reps, "layers_per_verify": res[1][1]}
+    eng.close()
+    args.steps = reps
+    return config_line(args, 2, nbytes / (us * 1e-6) / 1e9, us, nbytes, 7.3,
+                       "BASELINE config 2: one MoE layer (256 + 1 experts), 2 lanes, per-phase kernels of the "
+                       "35B-A3B model, mean over its 40 layers", "int8 (Q8_0) experts, f32 router",
+                       "router_kernel + experts_kernel + down_kernel", parts,
+                       {"note": "tests/test_engine_gpu.py and test_configs_gpu.py check these kernels bit for bit"})
+
+
+def bench_config3(args):
+    """the mixers of a 3:1 stack (3 delta-net + 1 attention layers) for one token
+    at 4096 prior positions (KV, conv and S state handed over by read_state), the per-phase mixer
+    kernels (projections, delta rule, scores, attention output, output projections) timed with HIP
+    events in 1-lane verifies; the sum over the 4 layers."""
+    import numpy as np
+    import oxe_amd as A
+    d = A.desc_35b_a3b(n_layer=4, n_vocab=4096)   # 3 delta-net + 1 attention layers
+    n_pos = 4096
+    rng = np.random.default_rng(3)
+    n_att = d.n_layer // d.full_attention_interval + 1
+    n_rec = d.n_layer - (n_att - 1)
+    K = rng.standard_normal((n_att, 2, n_pos, 256)).astype(np.float16)
+    VT = rng.standard_normal((n_att, 2 * 256, n_pos)).astype(np.float16)
+    conv = (0.5 * rng.standard_normal((n_rec, 8192, 3))).astype(np.float32)
+    S = (0.1 * rng.standard_normal((n_rec, 32, 128, 128))).astype(np.float32)
+    parts_b = []
+    for ai in range(n_att):
+        for h in range(2):
+            parts_b.append(K[ai, h].tobytes())
+        parts_b.append(VT[ai].tobytes())
+    blob = np.frombuffer(b"".join(parts_b) + conv.tobytes() + S.tobytes(), np.uint8)
+    eng = A.Engine(d, seed=3, n_ctx=n_pos + 256)
+    eng.set_fused(False)
+    eng.read_state(blob, n_pos)
+    reps = max(2, min(args.steps, 8))
+    res = _per_phase_probe(eng, lambda r: [(r * 7919 + 17) % d.n_vocab], (3, 5, 7, 8, 4), reps)
+    # per token: the sum over the layers of every mixer kernel (count launches per verify)
+    us = sum(res[k][0] * res[k][1] for k in res)
+    n_dn = n_rec
+    nbytes = (n_dn * (DN_PROJ + MIX_OUT + 2 * DN_STATE) + (ATT_PROJ + MIX_OUT + (n_pos + 1) * KV_POS))
+    names = {3: "proj", 5: "delta_net", 7: "scores", 8: "attn_out", 4: "out_proj"}
+    parts = {names[k]: {"us_each": round(res[k][0], 2), "per_token": res[k][1]} for k in res}
+    eng.close()
+    args.steps = reps
+    return config_line(args, 3, nbytes / (us * 1e-6) / 1e9, us, nbytes, 19.8,
+                       "BASELINE config 3: mixers of 3 delta-net + 1 attention layers, one token, 4096 prior "
+                       "positions, per-phase kernels", "int8 (Q8_0) projections, fp32 state, fp16 KV",
+                       "proj + delta-net + scores + pv + out kernels", parts,
+                       {"note": "tests/test_configs_gpu.py::test_config3_mixers_at_4096_positions checks them bit "
+                                "for bit at this size"})
+
+
 def gemm_probe(torch, reps):
     """The batched prefill's Q8_0 GEMM (oxe_hip_gemm_q8_0, the kernel of every prefill projection) on
     its 2048-token shapes, timed with HIP events on torch's stream: for rocprofv3 --pmc counter runs
@@ -439,6 +580,9 @@ def main():
     ap.add_argument("--prefill-tokens", type=int, default=2048)
     ap.add_argument("--kquant", action="store_true",
                     help="the K-quant lane GEMV on the Qwen3.6 shapes instead (--steps timed launches each)")
+    ap.add_argument("--config", type=int, default=0, choices=(0, 1, 2, 3),
+                    help="a bench line for BASELINE config 1 (GEMV), 2 (one MoE layer) or 3 (mixers at 4096 "
+                         "positions) instead of the decode step")
     ap.add_argument("--gemm-probe", action="store_true",
                     help="only the prefill's Q8_0 GEMM on its 2048-token shapes (for rocprofv3 --pmc)")
     args = ap.parse_args()
@@ -466,6 +610,10 @@ def main():
         if args.steps == ap.get_default("steps"):
             args.steps = 40
         bench_kquant(args)
+        return
+    if args.config:
+        fn = {1: bench_config1, 2: bench_config2, 3: bench_config3}[args.config]
+        print(json.dumps(fn(args)), flush=True)
         return
     if args.prefill:
         if args.steps == ap.get_default("steps"):

@@ -290,6 +290,10 @@ OXE_API int oxe_mtp_set_force(oxe_engine *e, const int32_t *force_d1, int n);
  * 9 MTP entry; in the fused run mode 10 the verify run, 11 the draft run, each one launch): mean
  * kernel duration in microseconds (roofline measurement). */
 OXE_API int oxe_mtp_device_probe(oxe_engine *e, int k, int kind, float *avg_us, int *n);
+/* oxe_engine_verify with the same HIP-event timing of one kernel kind (*count launches timed):
+ * the bench's per-config lines. No counterpart in the reference (a measurement hook). */
+OXE_API int oxe_engine_verify_probe(oxe_engine *e, const uint32_t *toks, int n, int kind, uint32_t *argmax_out,
+                                    float *avg_us, int *count);
 /* st[0] steps, st[1] accepted drafts, st[2] drafted tokens (MtpStats, mtp.rs:273-290) */
 OXE_API int oxe_mtp_stats(const oxe_engine *e, int64_t *st);
 OXE_API int oxe_engine_sync(oxe_engine *e);

@@ -52,6 +52,30 @@ int oxe_engine_verify(oxe_engine *e, const uint32_t *toks, int n, uint32_t *argm
     return ((Engine *)e)->verify(toks, n, argmax_out);
 }
 
+// oxe_engine_verify with HIP events around every launch of kernel kind `kind` (the kinds of
+// oxe_mtp_device_probe); *avg_us = their mean duration, *count = launches timed
+int oxe_engine_verify_probe(oxe_engine *e, const uint32_t *toks, int n, int kind, uint32_t *argmax_out, float *avg_us,
+                            int *count) {
+    Engine *g = (Engine *)e;
+    if (kind < 0 || !avg_us || !count) return -1;
+    g->probe_kind = kind;
+    g->probe_used = 0;
+    const int rc = g->verify(toks, n, argmax_out);
+    g->probe_kind = -1;
+    if (rc) return rc;
+    double tot = 0.0;
+    int cnt = 0;
+    for (size_t i = 0; i + 1 < g->probe_used; i += 2) {
+        float ms = 0.0f;
+        if (hipEventElapsedTime(&ms, g->probe_ev[i], g->probe_ev[i + 1]) != hipSuccess) return -2;
+        tot += ms;
+        cnt++;
+    }
+    *avg_us = cnt ? (float)(tot * 1000.0 / cnt) : 0.0f;
+    *count = cnt;
+    return 0;
+}
+
 int oxe_engine_commit(oxe_engine *e, int m) { return ((Engine *)e)->commit(m); }
 
 int oxe_engine_step(oxe_engine *e, uint32_t tok, uint32_t *argmax_out) {

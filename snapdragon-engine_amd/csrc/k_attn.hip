@@ -134,31 +134,34 @@ struct PvArgs {
     int n_ctx;
 };
 
-constexpr int PV_D = 32;            // output dims per workgroup (one Q8_0 block per head)
-constexpr int PV_MAX_KV = 8192;     // LDS holds the 8 heads' f16 probabilities for n_kv <= this
+constexpr int PV_D = 32;            // output dims per workgroup (one Q8_0 block of one head)
+constexpr int PV_MAX_KV = 8192;     // LDS holds the head's f16 probabilities for n_kv <= this
 
+// workgroup (kv head kvh, lane l, 32-dim chunk, head hh of the GQA group): 256 workgroups, the
+// chunk's V^T rows shared through the cache by the group's 8 heads
 template <int NL>
 __global__ __launch_bounds__(256) void pv_kernel(const RunCtl *__restrict__ ctl, PvArgs a) {
     extern __shared__ uint16_t s_dyn[];
-    uint16_t *s_p = s_dyn;                                        // [GQA][n_kv]
-    float *s_e = (float *)(s_dyn + GQA * ((a.n_ctx + 1) & ~1));   // [n_kv]
+    uint16_t *s_p = s_dyn;                                        // [n_kv]
+    float *s_e = (float *)(s_dyn + ((a.n_ctx + 1) & ~1));         // [n_kv]
     __shared__ float s_gs[PV_MAX_KV / 4];
     __shared__ double s_red[8];
-    __shared__ float s_o[GQA][PV_D];
+    __shared__ float s_o[PV_D];
     if (!ctl->active) return;
     const int t = threadIdx.x;
-    const int dchunk = blockIdx.x % (HD / PV_D);
-    const int l = (blockIdx.x / (HD / PV_D)) % NL;
-    const int kvh = blockIdx.x / ((HD / PV_D) * NL);
+    const int hh = blockIdx.x % GQA;
+    const int dchunk = (blockIdx.x / GQA) % (HD / PV_D);
+    const int l = (blockIdx.x / (GQA * (HD / PV_D))) % NL;
+    const int kvh = blockIdx.x / (GQA * (HD / PV_D) * NL);
     if (l >= ctl->nl) return;
     const int pos = ctl->pos0 + l;
     int n_kv = (pos + 1 + 255) / 256 * 256;
     if (n_kv < 256) n_kv = 256;
     if (n_kv > a.n_ctx) n_kv = a.n_ctx;
     const float scale = 1.0f / sqrtf((float)HD);
-    // softmax rows of the group's 8 heads (oxe_soft_max_f32, oxe_ops.cpp:101-115)
-    for (int hh = 0; hh < GQA; hh++) {
-        const int h = kvh * GQA + hh;
+    const int h = kvh * GQA + hh;
+    // softmax of the head's row (oxe_soft_max_f32, oxe_ops.cpp:101-115)
+    {
         const float *sc = a.scores + ((int64_t)l * NH + h) * a.n_ctx;
         float mx = -__builtin_inff();
         for (int i = t; i < n_kv; i += 256) {
@@ -192,44 +195,36 @@ __global__ __launch_bounds__(256) void pv_kernel(const RunCtl *__restrict__ ctl,
             f = (float)(1.0 / s_red[0]);
             __syncthreads();
         }
-        for (int i = t; i < n_kv; i += 256) s_p[hh * n_kv + i] = f2h(s_e[i] * f);
+        for (int i = t; i < n_kv; i += 256) s_p[i] = f2h(s_e[i] * f);
         __syncthreads();
     }
-    // V^T . p: thread = (head group hg of 4 heads, dim d, chain octet j)
-    const int j = t & 3, d = (t >> 2) & (PV_D - 1), hg = t >> 7;
+    // V^T . p: thread = (dim d, chain octet j) of ggml_vec_dot_f16 (threads >= 128 idle)
+    const int j = t & 3, d = (t >> 2) & (PV_D - 1);
     const int dg = dchunk * PV_D + d;
-    const uint16_t *vrow = a.vt + (int64_t)(kvh * HD + dg) * a.n_ctx;
-    h2 acc[4][4];
+    if (t < 4 * PV_D) {
+        const uint16_t *vrow = a.vt + (int64_t)(kvh * HD + dg) * a.n_ctx;
+        h2 acc[4];
 #pragma unroll
-    for (int q = 0; q < 4; q++)
-#pragma unroll
-        for (int i = 0; i < 4; i++) acc[q][i] = h2{(_Float16)0.0f, (_Float16)0.0f};
-    for (int s = 0; s < n_kv / 32; s++) {
-        const uint4 vv = *(const uint4 *)(vrow + 32 * s + 8 * j);
-        const h2 v0 = u2h2(vv.x), v1 = u2h2(vv.y), v2 = u2h2(vv.z), v3 = u2h2(vv.w);
-#pragma unroll
-        for (int q = 0; q < 4; q++) {
-            const uint4 pv = *(const uint4 *)(&s_p[(hg * 4 + q) * n_kv + 32 * s + 8 * j]);
-            acc[q][0] = __builtin_elementwise_fma(v0, u2h2(pv.x), acc[q][0]);
-            acc[q][1] = __builtin_elementwise_fma(v1, u2h2(pv.y), acc[q][1]);
-            acc[q][2] = __builtin_elementwise_fma(v2, u2h2(pv.z), acc[q][2]);
-            acc[q][3] = __builtin_elementwise_fma(v3, u2h2(pv.w), acc[q][3]);
+        for (int i = 0; i < 4; i++) acc[i] = h2{(_Float16)0.0f, (_Float16)0.0f};
+#pragma unroll 4
+        for (int s = 0; s < n_kv / 32; s++) {
+            const uint4 vv = *(const uint4 *)(vrow + 32 * s + 8 * j);
+            const uint4 pv = *(const uint4 *)(&s_p[32 * s + 8 * j]);
+            acc[0] = __builtin_elementwise_fma(u2h2(vv.x), u2h2(pv.x), acc[0]);
+            acc[1] = __builtin_elementwise_fma(u2h2(vv.y), u2h2(pv.y), acc[1]);
+            acc[2] = __builtin_elementwise_fma(u2h2(vv.z), u2h2(pv.z), acc[2]);
+            acc[3] = __builtin_elementwise_fma(u2h2(vv.w), u2h2(pv.w), acc[3]);
         }
-    }
-#pragma unroll
-    for (int q = 0; q < 4; q++) {
-        const float out = f16x8_reduce_quad(acc[q]);
-        const int hh = hg * 4 + q, h = kvh * GQA + hh;
+        const float out = f16x8_reduce_quad(acc);
         if (j == 0) {
             const float gate = a.proj[(int64_t)l * DN_ROWS + h * 2 * HD + HD + dg];
-            s_o[hh][d] = out * sigmoid_c(gate);
+            s_o[d] = out * sigmoid_c(gate);
         }
     }
     __syncthreads();
-    if (t < GQA) {
-        const int h = kvh * GQA + t;
+    if (t == 0) {
         const int64_t off = (int64_t)l * MIX_W + h * HD + dchunk * PV_D;
-        quant_block_q8_0(s_o[t], a.oq + off, a.od + off / 32);
+        quant_block_q8_0(s_o, a.oq + off, a.od + off / 32);
     }
 }
 
@@ -241,13 +236,13 @@ void launch_pv(const RunCtl *ctl, const ModelRt &m, const LayerW &w, const ActBu
     a.oq = b.oq;
     a.od = b.od;
     a.n_ctx = m.n_ctx;
-    const size_t lds = (size_t)GQA * ((m.n_ctx + 1) & ~1) * 2 + (size_t)m.n_ctx * 4;
+    const size_t lds = (size_t)((m.n_ctx + 1) & ~1) * 2 + (size_t)m.n_ctx * 4;
     static size_t configured = 0;
     if (lds > configured) {
         (void)hipFuncSetAttribute((const void *)pv_kernel<OXE_NL>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         configured = lds;
     }
-    hipLaunchKernelGGL(pv_kernel<OXE_NL>, dim3(NKV * OXE_NL * (HD / PV_D)), dim3(256), lds, st, ctl, a);
+    hipLaunchKernelGGL(pv_kernel<OXE_NL>, dim3(NKV * OXE_NL * (HD / PV_D) * GQA), dim3(256), lds, st, ctl, a);
 }
 
 }  // namespace oxe

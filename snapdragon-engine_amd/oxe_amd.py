@@ -238,6 +238,7 @@ def _engine_sigs(L):
         "oxe_last_error": (C.c_char_p, []),
         "oxe_engine_create": (i32, [vp, C.c_uint64, i32, C.POINTER(C.c_void_p)]),
         "oxe_engine_create_on": (i32, [vp, C.c_uint64, i32, vp, C.POINTER(C.c_void_p)]),
+        "oxe_engine_verify_probe": (i32, [vp, u32p, i32, i32, u32p, C.POINTER(C.c_float), C.POINTER(C.c_int)]),
         "oxe_engine_destroy": (None, [vp]),
         "oxe_engine_synth_weights": (i32, [vp]),
         "oxe_engine_verify": (i32, [vp, u32p, i32, u32p]),
@@ -518,6 +519,16 @@ class Engine:
         out = np.zeros(8, np.uint32)
         check(lib().oxe_engine_verify(self.h, _np_ptr(t, C.c_uint32), len(t), _np_ptr(out, C.c_uint32)), "verify")
         return out[: len(t)].copy()
+
+    def verify_probe(self, toks, kind):
+        """verify(toks) with HIP events around each launch of kernel kind `kind`: (mean us, launches)"""
+        import numpy as np
+        t = np.ascontiguousarray(toks, np.uint32)
+        out = np.zeros(8, np.uint32)
+        us, n = C.c_float(0.0), C.c_int(0)
+        check(lib().oxe_engine_verify_probe(self.h, _np_ptr(t, C.c_uint32), len(t), kind, _np_ptr(out, C.c_uint32),
+                                             C.byref(us), C.byref(n)), "verify_probe")
+        return float(us.value), int(n.value)
 
     def commit(self, m):
         check(lib().oxe_engine_commit(self.h, m), "commit")
