@@ -7,21 +7,19 @@
 // The int32 block dots are int8 matrix-core products (v_mfma_i32_32x32x32_i8: a 32 x 32 tile of one
 // block's dots per instruction, exact in any order; any split of the block's 32 codes over the
 // lanes gives the same sums as long as weights and activations use the same split). The scale
-// products d_x[t][b] * d_w[r][b] of the same tile are a rank-1 fp32 matrix-core product
-// (v_mfma_f32_32x32x2_f32 with the second k column zero: one product and an exact zero added, so
-// each element is the correctly rounded fp32 product, the value a VALU multiply gives), in the same
+// products d_x[t][b] * d_w[r][b] of both 32-token tiles of a block are one two-block fp32 matrix-core
+// outer product (v_mfma_f32_32x32x1_2b_f32: one product per element and nothing added, so each
+// element is the correctly rounded fp32 product, the value a VALU multiply gives), in the same
 // 32 x 32 output layout as the dots. What is left for the VALU is the chain itself, two operations
 // per output and block (convert the block sum, fused multiply-add), one value per (row, token) per
-// lane, block by block in order, so the chain is the reference's. The VALU is the kernel's bound;
-// each wave issues a tile's matrix-core products for the next block as soon as the tile's chain of
-// the current block has read them, so they run under the other tile's chain.
+// lane, block by block in order, so the chain is the reference's. The VALU is the kernel's bound.
 //
 // Workgroup tile: 128 weight rows x 64 tokens, 4 waves of 32 rows x 64 tokens (two 32 x 32 tiles).
-// The K dimension is staged through LDS 8 blocks (256 bytes per row) at a time with 16-byte
-// coalesced loads, the next stage's held in registers while the current one computes; LDS rows are
-// padded to 272 bytes so the 16-byte fragment reads of 8 consecutive rows fall on distinct banks.
-// Scales are staged as f32 by one thread per row (8 blocks from one 16-byte load), so each LDS
-// store instruction writes 64 consecutive words.
+// K is staged 4 blocks (128 bytes per row) at a time, double-buffered in LDS and filled by
+// direct global-to-LDS loads (global_load_lds_dwordx4 / _dword: no staging registers), so three
+// workgroups fit a CU. Code rows are stored unpadded with their 16-byte chunks XOR-swizzled by the
+// row's low 3 bits, so the 16-byte fragment reads of 8 consecutive rows fall on distinct banks.
+// Scales are staged as the raw f16 (4 per row and stage) and converted when read.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -35,25 +33,38 @@ namespace oxe {
 
 namespace gm {
 constexpr int BM = 128, BN = 64;       // rows, tokens per workgroup
-constexpr int KC = 256;                // K bytes (8 blocks) per LDS stage
+constexpr int KC = 128;                // K bytes (4 blocks) per stage
 constexpr int NBC = KC / 32;           // blocks per stage
-constexpr int LDR = KC + 16;           // LDS row stride (bytes)
 constexpr int NT = 256;                // threads
 constexpr int WR = 32;                 // weight rows per wave
-constexpr int SDW = BM + 32;           // weight-scale row of one block: BM scales, then 32 zeros
 }  // namespace gm
+
+// one stage of LDS: codes [row][KC] with chunk c of row r at slot c ^ (r & 7); scales [row][NBC] f16
+struct GemmStage {
+    int8_t w[gm::BM * gm::KC];
+    int8_t x[gm::BN * gm::KC];
+    uint16_t dw[gm::BM * gm::NBC];
+    uint16_t dx[gm::BN * gm::NBC];
+};
 
 typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
 typedef int32_t i32x16 __attribute__((ext_vector_type(16)));
-typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x32 __attribute__((ext_vector_type(32)));
+typedef __attribute__((address_space(3))) void lds_void;
+typedef __attribute__((address_space(1))) void glb_void;
 
-__global__ __launch_bounds__(gm::NT, 2) void gemm_q8_kernel(GemmArgs a, int vec4) {
+// global -> LDS, 16 or 4 bytes per lane; lane i's bytes land at dst + 16 i (4 i), dst wave-uniform
+__device__ __forceinline__ void to_lds16(const void *src, void *dst) {
+    __builtin_amdgcn_global_load_lds((glb_void *)src, (lds_void *)dst, 16, 0, 0);
+}
+__device__ __forceinline__ void to_lds4(const void *src, void *dst) {
+    __builtin_amdgcn_global_load_lds((glb_void *)src, (lds_void *)dst, 4, 0, 0);
+}
+
+__global__ __launch_bounds__(gm::NT, 3) void gemm_q8_kernel(GemmArgs a, int vec4) {
     using namespace gm;
-    __shared__ __align__(16) int8_t sw[BM * LDR];
-    __shared__ __align__(16) int8_t sx[BN * LDR];
-    __shared__ __align__(16) float sdw[NBC][SDW];   // [block][row] weight scales as f32; [.][BM ..] stay 0
-    __shared__ __align__(16) float sdx[NBC][BN];    // [block][token] activation scales as f32
-    __shared__ int64_t sxr[BN];                     // activation row of each of the tile's output rows
+    __shared__ __align__(16) GemmStage st0, st1;
+    __shared__ int64_t sxr[BN];   // activation row of each of the tile's output rows (-1: none)
     const int t = threadIdx.x, lane = t & 63, w = t >> 6;
     const int64_t k = a.k, nr = a.nr, nb = k / 32;
     const int64_t r0 = (int64_t)blockIdx.x * BM;
@@ -71,103 +82,116 @@ __global__ __launch_bounds__(gm::NT, 2) void gemm_q8_kernel(GemmArgs a, int vec4
         p0 = (int64_t)blockIdx.y * BN;
         pn = a.nt - p0 < BN ? a.nt - p0 : BN;
     }
+    if (pn <= 0) return;   // uniform
     if (t < BN) sxr[t] = t < pn ? (a.xrow ? (int64_t)a.xrow[p0 + t] : p0 + t) : -1;
-    for (int i = t; i < NBC * 32; i += NT) sdw[i / 32][BM + i % 32] = 0.0f;
     __syncthreads();
-    // wave w: rows 32 w .. 32 w + 31 of the tile; tile j: tokens 32 j .. 32 j + 31
+    // Loads of one stage. Rows past the matrix (weights) or the tile (tokens) read a valid row
+    // instead (the last weight row, the tile's first token): their outputs are never stored, and
+    // each output element depends only on its own row's and token's codes and scales.
+    // Wave w fills weight rows 32 w .. + 31 (4 x 8 rows of 128 bytes), token rows 16 w .. + 15 (2 x 8
+    // rows), the weight scales of its 32 rows and (waves 0, 1) the token scales of rows 32 w .. + 31.
+    // Lane L of a code load: row 8 q + (L >> 3) of the group, chunk (L & 7) ^ (L >> 3) of the 128
+    // bytes, stored at slot L & 7; lane L of a scale load: row L >> 1, f16 pair L & 1.
+    const int lr8 = lane >> 3, cch = (lane & 7) ^ lr8;
+    const int64_t wlast = nr - 1;
+    uint32_t wofs[4], xofs[2], wsofs, xsofs = 0;
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        const int64_t gr = r0 + WR * w + 8 * q + lr8;
+        wofs[q] = (uint32_t)((gr < wlast ? gr : wlast) * k + 16 * cch);
+    }
+#pragma unroll
+    for (int q = 0; q < 2; q++) {
+        const int64_t xr = sxr[16 * w + 8 * q + lr8];
+        xofs[q] = (uint32_t)((xr >= 0 ? xr : sxr[0]) * k + 16 * cch);
+    }
+    {
+        const int64_t gr = r0 + WR * w + (lane >> 1);
+        wsofs = (uint32_t)(((gr < wlast ? gr : wlast) * nb) * 2 + 4 * (lane & 1));
+        if (w < 2) {
+            const int64_t xr = sxr[32 * w + (lane >> 1)];
+            xsofs = (uint32_t)(((xr >= 0 ? xr : sxr[0]) * nb) * 2 + 4 * (lane & 1));
+        }
+    }
+    auto fetch = [&](GemmStage &S, int64_t kc) {
+        const int8_t *wb = wq + kc, *xb = a.xq + kc;
+        const int8_t *wsb = (const int8_t *)wd + kc / 16, *xsb = (const int8_t *)a.xd + kc / 16;
+#pragma unroll
+        for (int q = 0; q < 4; q++) to_lds16(wb + wofs[q], S.w + (WR * w + 8 * q) * KC);
+#pragma unroll
+        for (int q = 0; q < 2; q++) to_lds16(xb + xofs[q], S.x + (16 * w + 8 * q) * KC);
+        to_lds4(wsb + wsofs, S.dw + WR * w * NBC);
+        if (w < 2) to_lds4(xsb + xsofs, S.dx + 32 * w * NBC);
+    };
+    // wave w: rows 32 w .. + 31 of the tile; tile j: tokens 32 j .. + 31. Fragment of a code row:
+    // row / token lane & 31, the 16 bytes 16 (lane >> 5) .. of the block, at slot (2 b + (lane >> 5))
+    // ^ (row & 7); row & 7 = lane & 7 for both operands.
     const int wr = WR * w, fr = lane & 31, fh = lane >> 5;
+    int fofs[NBC];
+#pragma unroll
+    for (int bb = 0; bb < NBC; bb++) fofs[bb] = fr * KC + 16 * ((2 * bb + fh) ^ (fr & 7));
     float acc[2][16];
 #pragma unroll
     for (int j = 0; j < 2; j++)
 #pragma unroll
         for (int v = 0; v < 16; v++) acc[j][v] = 0.0f;
-    // the next stage's codes and scales are loaded into registers while the current stage computes:
-    // thread t stages 16-byte chunk t % 16 of rows t / 16 + 16 p; threads 0-127 the scales of weight
-    // row t, threads 128-191 those of token row t - 128 (wave-uniform roles)
-    constexpr int NPW = BM * KC / 16 / NT, NPX = BN * KC / 16 / NT;   // 16-byte chunks per thread
-    const int crow = t / (KC / 16), cch = t % (KC / 16);
-    const int64_t wrows = nr - r0;   // rows of W left from the tile's first
-    const int8_t *wqt = wq + (r0 + crow) * k + 16 * cch;
-    const int srow = t < BM ? t : t - BM;
-    uint4 pu[NPW], pv[NPX], ps;
-    auto fetch = [&](int64_t kc) {
-#pragma unroll
-        for (int p = 0; p < NPW; p++)
-            pu[p] = crow + 16 * p < wrows ? *(const uint4 *)(wqt + (int64_t)(16 * p) * k + kc) : make_uint4(0, 0, 0, 0);
-#pragma unroll
-        for (int p = 0; p < NPX; p++) {
-            const int64_t xr = sxr[crow + 16 * p];
-            pv[p] = xr >= 0 ? *(const uint4 *)(a.xq + xr * k + 16 * cch + kc) : make_uint4(0, 0, 0, 0);
-        }
-        ps = make_uint4(0, 0, 0, 0);
-        if (t < BM) {
-            if (t < wrows) ps = *(const uint4 *)(wd + (r0 + t) * nb + kc / 32);
-        } else if (t < BM + BN) {
-            const int64_t xr = sxr[srow];
-            if (xr >= 0) ps = *(const uint4 *)(a.xd + xr * nb + kc / 32);
-        }
-    };
-    fetch(0);
-    // tokens of the tile: a per-expert group fills a tile partly; an empty second tile is skipped
-    // (uniform across the workgroup)
-    auto run = [&](auto njc) {
+    // one stage's chain: tile j's outputs in this lane are rows wr + 8 q + 4 (lane >> 5) + e
+    // (v = 4 q + e), token 32 j + (lane & 31); the two-block scale product's block j is tile j
+    auto compute = [&](const GemmStage &S, auto njc) {
         constexpr int NJ = decltype(njc)::value;
-        for (int64_t kc = 0; kc < k; kc += KC) {
+        const uint2 hw = *(const uint2 *)&S.dw[(wr + fr) * NBC];   // this lane's weight row, 4 blocks
+        const uint2 hx = *(const uint2 *)&S.dx[lane * NBC];        // token `lane`, 4 blocks
+        auto dots = [&](int bb, int j) {
+            const i32x4 fa = *(const i32x4 *)(S.w + wr * KC + fofs[bb]);
+            const i32x4 fb = *(const i32x4 *)(S.x + 32 * KC * j + fofs[bb]);
+            const i32x16 zero = {};
+            return __builtin_amdgcn_mfma_i32_32x32x32_i8(fa, fb, zero, 0, 0, 0);
+        };
+        auto scales = [&](int bb) {
+            const uint32_t pw = bb < 2 ? hw.x : hw.y, px = bb < 2 ? hx.x : hx.y;
+            const float dw = h2f((uint16_t)(pw >> (16 * (bb & 1)))), dx = h2f((uint16_t)(px >> (16 * (bb & 1))));
+            const f32x32 zero = {};
+            return __builtin_amdgcn_mfma_f32_32x32x1f32(dw, dx, zero, 0, 0, 0);
+        };
+        i32x16 s[NJ];
 #pragma unroll
-            for (int p = 0; p < NPW; p++) *(uint4 *)(sw + (crow + 16 * p) * LDR + 16 * cch) = pu[p];
+        for (int j = 0; j < NJ; j++) s[j] = dots(0, j);
+        f32x32 d = scales(0);
 #pragma unroll
-            for (int p = 0; p < NPX; p++) *(uint4 *)(sx + (crow + 16 * p) * LDR + 16 * cch) = pv[p];
-            if (t < BM + BN) {
-                const uint32_t h[4] = {ps.x, ps.y, ps.z, ps.w};
-                float *dst = t < BM ? &sdw[0][srow] : &sdx[0][srow];
-                const int st = t < BM ? SDW : BN;
-#pragma unroll
-                for (int bb = 0; bb < NBC; bb++) dst[bb * st] = h2f((uint16_t)(h[bb / 2] >> (16 * (bb % 2))));
-            }
-            __syncthreads();
-            if (kc + KC < k) fetch(kc + KC);
-            // fragments: row / token lane & 31, codes 16 (lane >> 5) .. + 15 of the block; scale
-            // operands: lanes 0-31 the row's / token's scale (k column 0), lanes 32-63 a zero weight
-            // scale (k column 1)
-            const int8_t *fa_p = sw + (wr + fr) * LDR + 16 * fh;
-            const int8_t *fb_p = sx + fr * LDR + 16 * fh;
-            const float *sa_p = &sdw[0][fh ? BM + fr : wr + fr];
-            const float *sb_p = &sdx[0][fr];
-            auto dots = [&](int bb, int j) {
-                const i32x4 fa = *(const i32x4 *)(fa_p + 32 * bb);
-                const i32x4 fb = *(const i32x4 *)(fb_p + 32 * LDR * j + 32 * bb);
-                const i32x16 zero = {};
-                return __builtin_amdgcn_mfma_i32_32x32x32_i8(fa, fb, zero, 0, 0, 0);
-            };
-            auto scales = [&](int bb, int j) {
-                const f32x16 zero = {};
-                return __builtin_amdgcn_mfma_f32_32x32x2f32(sa_p[bb * SDW], sb_p[bb * BN + 32 * j], zero, 0, 0, 0);
-            };
-            i32x16 s[NJ];
-            f32x16 d[NJ];
+        for (int bb = 0; bb < NBC; bb++) {
 #pragma unroll
             for (int j = 0; j < NJ; j++) {
-                s[j] = dots(0, j);
-                d[j] = scales(0, j);
+#pragma unroll
+                for (int v = 0; v < 16; v++) acc[j][v] = __builtin_fmaf((float)s[j][v], d[16 * j + v], acc[j][v]);
+                if (bb + 1 < NBC) s[j] = dots(bb + 1, j);
             }
-#pragma unroll
-            for (int bb = 0; bb < NBC; bb++) {
-                // tile j's outputs in this lane: rows wr + 8 q + 4 (lane >> 5) + e (v = 4 q + e), token 32 j + (lane & 31)
-#pragma unroll
-                for (int j = 0; j < NJ; j++) {
-#pragma unroll
-                    for (int v = 0; v < 16; v++) acc[j][v] = __builtin_fmaf((float)s[j][v], d[j][v], acc[j][v]);
-                    if (bb + 1 < NBC) {
-                        s[j] = dots(bb + 1, j);
-                        d[j] = scales(bb + 1, j);
-                    }
-                }
-            }
-            __syncthreads();
+            if (bb + 1 < NBC) d = scales(bb + 1);
         }
     };
+    // every wave's loads of a stage done and visible before any wave reads it; every wave done with a
+    // stage before it is refilled
+    auto stage_sync = [&]() {
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+    };
+    auto run = [&](auto njc) {
+        const int64_t ns = k / KC;
+        fetch(st0, 0);
+        stage_sync();
+        for (int64_t i = 0; i < ns; i += 2) {
+            if (i + 1 < ns) fetch(st1, (i + 1) * KC);
+            compute(st0, njc);
+            stage_sync();
+            if (i + 1 >= ns) break;
+            if (i + 2 < ns) fetch(st0, (i + 2) * KC);
+            compute(st1, njc);
+            stage_sync();
+        }
+    };
+    // tokens of the tile: a per-expert group fills a tile partly; an empty second tile is skipped
+    // (uniform across the workgroup)
     if (pn > 32) run(std::integral_constant<int, 2>{});
-    else if (pn > 0) run(std::integral_constant<int, 1>{});
+    else run(std::integral_constant<int, 1>{});
 #pragma unroll
     for (int j = 0; j < 2; j++) {
         const int tt = 32 * j + fr;
@@ -198,8 +222,10 @@ int gemm_launch(const GemmArgs &a, int64_t ntiles, hipStream_t st) {
     using namespace gm;
     if (a.k <= 0 || a.k % KC != 0 || a.nr <= 0 || a.ldy < a.nr) return -1;
     if (!a.wq || !a.wd || !a.xq || !a.xd || !a.y) return -1;
-    // 16-byte loads of codes and of 8 scales at a time
+    // 16-byte loads of codes
     if (((uintptr_t)a.wq | (uintptr_t)a.wd | (uintptr_t)a.xq | (uintptr_t)a.xd) % 16 != 0) return -1;
+    // the kernel addresses one weight group's and the activations' codes with 32-bit offsets
+    if ((uint64_t)a.nr * (uint64_t)a.k > UINT32_MAX || (uint64_t)a.nt * (uint64_t)a.k > UINT32_MAX) return -1;
     const int64_t ny = a.tiles ? ntiles : (a.nt + BN - 1) / BN;
     if (ny <= 0) return 0;
     // 16-byte output (and residual) accesses where every row group of 4 starts 16-byte aligned
