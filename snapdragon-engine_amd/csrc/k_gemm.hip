@@ -17,8 +17,10 @@
 // Workgroup tile: 128 weight rows x 64 tokens, 4 waves of 32 rows x 64 tokens (two 32 x 32 tiles).
 // K is staged 4 blocks (128 bytes per row) at a time, double-buffered in LDS and filled by
 // direct global-to-LDS loads (global_load_lds_dwordx4 / _dword: no staging registers), so three
-// workgroups fit a CU. Code rows are stored unpadded with their 16-byte chunks XOR-swizzled by the
-// row's low 3 bits, so the 16-byte fragment reads of 8 consecutive rows fall on distinct banks.
+// workgroups fit a CU. Code rows (128 bytes) are stored unpadded with their 16-byte chunks
+// XOR-swizzled by f(r) = (r & 7) ^ ((r >> 3) & 1): the 16-byte fragment reads of 8 consecutive rows
+// cover 8 distinct chunk slots of 128 bytes, and those of 16 consecutive rows 16 distinct 16-byte
+// slots of 256 bytes, so neither a 32-bank nor a 64-bank LDS sees a conflict.
 // Scales are staged as the raw f16 (4 per row and stage) and converted when read.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -39,7 +41,7 @@ constexpr int NT = 256;                // threads
 constexpr int WR = 32;                 // weight rows per wave
 }  // namespace gm
 
-// one stage of LDS: codes [row][KC] with chunk c of row r at slot c ^ (r & 7); scales [row][NBC] f16
+// one stage of LDS: codes [row][KC] with chunk c of row r at slot c ^ f(r); scales [row][NBC] f16
 struct GemmStage {
     int8_t w[gm::BM * gm::KC];
     int8_t x[gm::BN * gm::KC];
@@ -90,20 +92,21 @@ __global__ __launch_bounds__(gm::NT, 3) void gemm_q8_kernel(GemmArgs a, int vec4
     // each output element depends only on its own row's and token's codes and scales.
     // Wave w fills weight rows 32 w .. + 31 (4 x 8 rows of 128 bytes), token rows 16 w .. + 15 (2 x 8
     // rows), the weight scales of its 32 rows and (waves 0, 1) the token scales of rows 32 w .. + 31.
-    // Lane L of a code load: row 8 q + (L >> 3) of the group, chunk (L & 7) ^ (L >> 3) of the 128
-    // bytes, stored at slot L & 7; lane L of a scale load: row L >> 1, f16 pair L & 1.
+    // Lane L of a code load: row 8 q + (L >> 3) of the group, chunk (L & 7) ^ f(row) of the 128
+    // bytes, stored at slot L & 7 (f(row) = (L >> 3) ^ (q & 1): each group starts at a multiple of
+    // 8 rows, odd groups at an odd multiple); lane L of a scale load: row L >> 1, f16 pair L & 1.
     const int lr8 = lane >> 3, cch = (lane & 7) ^ lr8;
     const int64_t wlast = nr - 1;
     uint32_t wofs[4], xofs[2], wsofs, xsofs = 0;
 #pragma unroll
     for (int q = 0; q < 4; q++) {
         const int64_t gr = r0 + WR * w + 8 * q + lr8;
-        wofs[q] = (uint32_t)((gr < wlast ? gr : wlast) * k + 16 * cch);
+        wofs[q] = (uint32_t)((gr < wlast ? gr : wlast) * k + 16 * (cch ^ (q & 1)));
     }
 #pragma unroll
     for (int q = 0; q < 2; q++) {
         const int64_t xr = sxr[16 * w + 8 * q + lr8];
-        xofs[q] = (uint32_t)((xr >= 0 ? xr : sxr[0]) * k + 16 * cch);
+        xofs[q] = (uint32_t)((xr >= 0 ? xr : sxr[0]) * k + 16 * (cch ^ (q & 1)));
     }
     {
         const int64_t gr = r0 + WR * w + (lane >> 1);
@@ -125,11 +128,11 @@ __global__ __launch_bounds__(gm::NT, 3) void gemm_q8_kernel(GemmArgs a, int vec4
     };
     // wave w: rows 32 w .. + 31 of the tile; tile j: tokens 32 j .. + 31. Fragment of a code row:
     // row / token lane & 31, the 16 bytes 16 (lane >> 5) .. of the block, at slot (2 b + (lane >> 5))
-    // ^ (row & 7); row & 7 = lane & 7 for both operands.
+    // ^ f(row); f(row) = f(lane & 31) for both operands (their row bases are multiples of 16).
     const int wr = WR * w, fr = lane & 31, fh = lane >> 5;
     int fofs[NBC];
 #pragma unroll
-    for (int bb = 0; bb < NBC; bb++) fofs[bb] = fr * KC + 16 * ((2 * bb + fh) ^ (fr & 7));
+    for (int bb = 0; bb < NBC; bb++) fofs[bb] = fr * KC + 16 * ((2 * bb + fh) ^ (fr & 7) ^ ((fr >> 3) & 1));
     float acc[2][16];
 #pragma unroll
     for (int j = 0; j < 2; j++)
