@@ -151,3 +151,35 @@ def test_config5_prefill_2048_state_hashes(dev):
     assert sha(np.asarray(g.hidden(0), np.float32).tobytes()) == str(gold["hidden_sha"])
     assert nx == int(gold["next"])
     g.close()
+
+
+def test_config5_prefill_2048_full_model_state_hashes(dev):
+    """Config 5 at its stated size: the config-4 model (35B-A3B shape, 40 layers, seed 0) prefills the
+    2048-token bench prompt in one batched call; the whole recurrent state in the reference's byte
+    order (every attention layer's K rows and V^T columns, then the conv and delta-net states), the
+    last token's logits and hidden state and the next id equal the oracle's after 2048 single-token
+    steps (tests/golden/make_golden.py config5_full_state)."""
+    import oxe_amd as A
+    gold = np.load(os.path.join(GOLDEN, "config5_full_state.npz"))
+    d = A.desc_35b_a3b()
+    toks = gold["prompt"]
+    n = len(toks)
+    g = A.Engine(d, seed=0, n_ctx=n + 256)
+    print("config 5 (40 layers): prefill 2048", flush=True)
+    nx = g.prefill(toks)
+    sha = lambda b: hashlib.sha256(b).hexdigest()  # noqa: E731
+    state = g.write_state().tobytes()
+    assert len(state) == int(gold["state_bytes"])
+    n_att = d.n_layer // d.full_attention_interval + 1
+    kv_bytes = n_att * 2 * d.n_head_kv * n * d.head_dim * 2
+    n_rec = d.n_layer - (n_att - 1)
+    conv_bytes = n_rec * 8192 * 3 * 4
+    parts = dict(kv_sha=state[:kv_bytes], conv_sha=state[kv_bytes:kv_bytes + conv_bytes],
+                 ssm_sha=state[kv_bytes + conv_bytes:])
+    bad = [name for name, b in parts.items() if sha(b) != str(gold[name])]
+    assert not bad, f"state parts differing from the oracle: {bad}"
+    assert sha(state) == str(gold["state_sha"])
+    assert sha(np.asarray(g.logits(0), np.float32).tobytes()) == str(gold["logits_sha"])
+    assert sha(np.asarray(g.hidden(0), np.float32).tobytes()) == str(gold["hidden_sha"])
+    assert nx == int(gold["next"])
+    g.close()
