@@ -107,45 +107,67 @@ def team_text(team, threads):
     return f"OpenMP over rows on {threads} unpinned threads (pinning failed)"
 
 
+def plan_text(team):
+    return (f"the reference's static plan (crates/model/src/plan.rs:171-249) on a persistent team of {team} "
+            f"threads, thread i pinned to the i-th core of the process's affinity set, one sense-reversing "
+            f"spin barrier after each phase (crates/sched/src/lib.rs:43-84, 320-345)")
+
+
 def cpu_baseline(seconds, state, n_pos, hl, x):
     """Time the oracle's MTP-1 steps on the full 35B-A3B shape (bounded sample) from the GPU run's own
     state: the sequence state after the 512-token prompt and the warm-up steps (Engine::write_state
     bytes read into the oracle engine, the MTP driver resumed at that position), so the CPU steps run
-    at the GPU's context positions."""
+    at the GPU's context positions. The figure is the oracle's plan mode (the reference's static
+    per-phase plan on a pinned team); the OpenMP row-loop figure of the same sample is kept beside it."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as O
     O.build()
     hc = host_cores()                           # before pinning narrows this thread's mask
+    res = _cpu_steps(O, seconds, state, n_pos, hl, x, hc, plan=True)
     with pinned_team(O) as team:
-        return _cpu_steps(O, seconds, state, n_pos, hl, x, team, hc)
+        omp = _cpu_steps(O, seconds / 2, state, n_pos, hl, x, hc, team=team)
+    res["openmp_rows"] = {k: omp[k] for k in ("value", "unit", "cores", "sample")}
+    return res
 
 
-def _cpu_steps(O, seconds, state, n_pos, hl, x, team, hc):
+def _cpu_steps(O, seconds, state, n_pos, hl, x, hc, team=0, plan=False):
     d = O.desc_35b_a3b()
     e = O.Engine(d, seed=0, n_ctx=n_pos + 256)
     O.lib().oxo_set_keep_logits(e.h, 0)
     e.read_state(state, n_pos)
+    threads, aff, model = hc
+    if plan:
+        team = max(e.set_plan(threads), 0)
     drv = O.Driver(e)
     drv.import_state(n_pos, hl)
     gen0 = O.lib().oxo_gen_seconds(e.h)
+    b0 = e.plan_barriers()
     t0 = time.time()
     toks = steps = 0
-    while time.time() - t0 < seconds or steps < 2:
+    # the budget is compute time (wall minus first-use weight generation), capped at 4x in wall time
+    while steps < 2 or (time.time() - t0 - (O.lib().oxo_gen_seconds(e.h) - gen0) < seconds
+                        and time.time() - t0 < 4 * seconds):
         out = drv.step(x)
         toks += len(out)
         steps += 1
         x = out[-1]
     wall = time.time() - t0
     gen = O.lib().oxo_gen_seconds(e.h) - gen0
+    bars = e.plan_barriers() - b0 if plan else None
     compute = max(wall - gen, 1e-9)
-    threads, aff, model = hc
+    if plan:
+        e.set_plan(0)
     e.close()
-    return {"value": round(toks / compute, 4), "unit": "tok/s", "cores": team if team > 0 else threads,
-            "kind": "port", "cpu": model, "affinity": f"{len(aff)} cores [{aff[0]}..{aff[-1]}]" if aff else "",
-            "sample": f"{steps} MTP-1 steps ({toks} tokens) of the 35B-A3B shape at positions {n_pos}..{n_pos + steps}, "
-                      f"from the GPU run's state after its {n_pos}-position prefix; the reference algorithm "
-                      f"restated in C++ on {team_text(team, threads)}; {wall:.1f} s wall minus {gen:.1f} s spent "
-                      f"generating synthetic expert weights on first use"}
+    how = plan_text(team) if plan else team_text(team, threads)
+    out = {"value": round(toks / compute, 4), "unit": "tok/s", "cores": team if team > 0 else threads,
+           "kind": "port", "cpu": model, "affinity": f"{len(aff)} cores [{aff[0]}..{aff[-1]}]" if aff else "",
+           "sample": f"{steps} MTP-1 steps ({toks} tokens) of the 35B-A3B shape at positions {n_pos}..{n_pos + steps}, "
+                     f"from the GPU run's state after its {n_pos}-position prefix; the reference algorithm "
+                     f"restated in C++ on {how}; {wall:.1f} s wall minus {gen:.1f} s spent "
+                     f"generating synthetic expert weights on first use"}
+    if plan:
+        out["barriers_per_step"] = round(bars / max(steps, 1), 1)
+    return out
 
 
 def golden_parity(gen):
@@ -182,34 +204,43 @@ def prefill_expert_macs(T, n_layer=40):
 
 def cpu_prefill_baseline(seconds):
     """The oracle's prompt path (2-token verify runs, MtpDriver::prefill) on the 35B-A3B shape,
-    timed on this host for a bounded number of tokens."""
+    timed on this host for a bounded number of tokens: plan mode, the OpenMP figure beside it."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as O
     O.build()
     cores = host_cores()[0]
+    res = _cpu_prefill(O, seconds, 0, cores, plan=True)
     with pinned_team(O) as team:
-        return _cpu_prefill(O, seconds, team, cores)
+        omp = _cpu_prefill(O, seconds / 2, team, cores)
+    res["openmp_rows"] = {k: omp[k] for k in ("value", "unit", "cores", "sample")}
+    return res
 
 
-def _cpu_prefill(O, seconds, team, cores):
+def _cpu_prefill(O, seconds, team, cores, plan=False):
     d = O.desc_35b_a3b()
     e = O.Engine(d, seed=0, n_ctx=1024)
     O.lib().oxo_set_keep_logits(e.h, 0)
+    if plan:
+        team = max(e.set_plan(cores), 0)
     toks = O.bench_prompt(512)
     gen0 = O.lib().oxo_gen_seconds(e.h)
     t0 = time.time()
     n = 0
-    while (time.time() - t0 < seconds or n < 4) and n + 2 <= len(toks):
+    while (n < 4 or (time.time() - t0 - (O.lib().oxo_gen_seconds(e.h) - gen0) < seconds
+                     and time.time() - t0 < 4 * seconds)) and n + 2 <= len(toks):
         e.verify(toks[n:n + 2])
         e.commit(2)
         n += 2
     wall = time.time() - t0
     gen = O.lib().oxo_gen_seconds(e.h) - gen0
     compute = max(wall - gen, 1e-9)
+    if plan:
+        e.set_plan(0)
     e.close()
+    how = plan_text(team) if plan else team_text(team, cores)
     return {"value": round(n / compute, 4), "unit": "tok/s", "cores": team or cores, "kind": "port",
             "sample": f"{n} prompt tokens of the 35B-A3B shape as 2-token verify runs (the reference's "
-                      f"MtpDriver::prefill path) on {team_text(team, cores)}; {wall:.1f} s wall minus "
+                      f"MtpDriver::prefill path) on {how}; {wall:.1f} s wall minus "
                       f"{gen:.1f} s generating synthetic expert weights on first use"}
 
 
@@ -563,7 +594,7 @@ def main():
     ap.add_argument("--steps", type=int, default=256)
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--prompt", type=int, default=512)
-    ap.add_argument("--cpu-seconds", type=float, default=20.0)
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--probe-kind", type=int, default=-1,
                     help="kernel kind timed for the roofline (default: 10 = the fused verify run, or 1 = experts "

@@ -9,11 +9,14 @@
 #include "oxo_model.h"
 
 #include <algorithm>
+#include <atomic>
 #include <chrono>
 #include <cmath>
 #include <cstring>
+#include <functional>
 #include <memory>
 #include <mutex>
+#include <thread>
 #include <vector>
 
 #include <omp.h>
@@ -27,6 +30,9 @@ struct Q8 {
     std::vector<uint16_t> d;
 };
 
+// set on the threads of a plan run: their work is their share, so nothing inside spawns a team
+thread_local bool tl_in_plan = false;
+
 // Generate rows [r0, r0+n) of expert e of a Q8_0 tensor [experts][rows][k] into m.
 void gen_q8(uint64_t seed, int layer, int kind, int64_t rows, int64_t k, int64_t e, Q8 &m) {
     m.rows = rows;
@@ -37,8 +43,21 @@ void gen_q8(uint64_t seed, int layer, int kind, int64_t rows, int64_t k, int64_t
     const uint64_t skey = oxe_tensor_key(seed, layer, kind + OXE_T_SCALE_OFFSET);
     const oxe_synth_param p = oxe_synth_param_of(kind);
     const uint64_t base = (uint64_t)e * rows * k;
-#pragma omp parallel for schedule(static)
+#pragma omp parallel for schedule(static) if (!tl_in_plan)
     for (int64_t r = 0; r < rows; r++) {
+        for (int64_t i = 0; i < k; i++) m.q[r * k + i] = oxe_synth_code(key, base + r * k + i);
+        for (int64_t b = 0; b < k / 32; b++)
+            m.d[r * (k / 32) + b] = oxe_synth_scale(skey, (base + r * k) / 32 + b, p);
+    }
+}
+
+// rows [r0, r1) of expert e's matrix m (already sized rows x k), on the calling thread
+void gen_q8_rows(uint64_t seed, int layer, int kind, int64_t rows, int64_t k, int64_t e, int64_t r0, int64_t r1, Q8 &m) {
+    const uint64_t key = oxe_tensor_key(seed, layer, kind);
+    const uint64_t skey = oxe_tensor_key(seed, layer, kind + OXE_T_SCALE_OFFSET);
+    const oxe_synth_param p = oxe_synth_param_of(kind);
+    const uint64_t base = (uint64_t)e * rows * k;
+    for (int64_t r = r0; r < r1; r++) {
         for (int64_t i = 0; i < k; i++) m.q[r * k + i] = oxe_synth_code(key, base + r * k + i);
         for (int64_t b = 0; b < k / 32; b++)
             m.d[r * (k / 32) + b] = oxe_synth_scale(skey, (base + r * k) / 32 + b, p);
@@ -70,6 +89,127 @@ struct Layer {
     std::vector<float> enorm, hnorm, head_norm;
     int index = 0;  // recurrent or attention index
 };
+
+// ---- The reference's worker pool (crates/sched/src/lib.rs:1-11, 43-84, 320-345): a persistent
+// team, thread i pinned to the i-th CPU of the creating thread's affinity set (the creator is
+// thread 0 and gets its mask back when the pool goes), jobs published through an epoch, and a
+// centralised sense-reversing spin barrier whose episodes are counted. Idle workers spin on the
+// epoch for a while and then yield.
+struct PlanPool {
+    struct alignas(128) Line {
+        std::atomic<uint32_t> v{0};
+    };
+    int n = 1;
+    std::vector<std::thread> th;
+    Line epoch, arrived, sense, stop;
+    std::atomic<uint64_t> episodes{0};
+    std::vector<Line> lsense;   // per-thread barrier sense (each slot touched by its owner only)
+    const std::function<void(int)> *job = nullptr;
+    cpu_set_t caller_mask;
+    bool pinned = false;
+
+    static void pin(int cpu) {
+        cpu_set_t one;
+        CPU_ZERO(&one);
+        CPU_SET(cpu, &one);
+        sched_setaffinity(0, sizeof(one), &one);
+    }
+    // team of n threads (n <= CPUs of the caller's mask); returns false if the mask is unreadable
+    bool start(int nthreads) {
+        CPU_ZERO(&caller_mask);
+        if (sched_getaffinity(0, sizeof(caller_mask), &caller_mask) != 0) return false;
+        std::vector<int> cpus;
+        for (int c = 0; c < CPU_SETSIZE; c++)
+            if (CPU_ISSET(c, &caller_mask)) cpus.push_back(c);
+        if (cpus.empty()) return false;
+        n = std::max(1, std::min<int>(nthreads, (int)cpus.size()));
+        lsense = std::vector<Line>(n);
+        pin(cpus[0]);
+        pinned = true;
+        for (int t = 1; t < n; t++) th.emplace_back([this, t, c = cpus[t]] { worker(t, c); });
+        return true;
+    }
+    ~PlanPool() {
+        stop.v.store(1, std::memory_order_release);
+        epoch.v.fetch_add(1, std::memory_order_release);
+        for (auto &t : th) t.join();
+        if (pinned) sched_setaffinity(0, sizeof(caller_mask), &caller_mask);
+    }
+    // counted: false for the barriers of synthetic-weight generation (not part of the plan)
+    void barrier(int tid, bool counted = true) {
+        const uint32_t s = lsense[tid].v.load(std::memory_order_relaxed) ^ 1u;
+        lsense[tid].v.store(s, std::memory_order_relaxed);
+        if (n == 1) {
+            if (counted) episodes.fetch_add(1, std::memory_order_relaxed);
+            return;
+        }
+        if (arrived.v.fetch_add(1, std::memory_order_acq_rel) + 1 == (uint32_t)n) {
+            arrived.v.store(0, std::memory_order_relaxed);
+            if (counted) episodes.fetch_add(1, std::memory_order_relaxed);
+            sense.v.store(s, std::memory_order_release);
+        } else {
+            while (sense.v.load(std::memory_order_acquire) != s) __builtin_ia32_pause();
+        }
+    }
+    void worker(int tid, int cpu) {
+        pin(cpu);
+        tl_in_plan = true;
+        uint32_t seen = 0;
+        for (;;) {
+            uint32_t e;
+            int spins = 0;
+            while ((e = epoch.v.load(std::memory_order_acquire)) == seen) {
+                if (++spins < (1 << 16)) __builtin_ia32_pause();
+                else std::this_thread::yield();
+            }
+            seen = e;
+            if (stop.v.load(std::memory_order_acquire)) return;
+            (*job)(tid);
+            barrier(tid);   // the join
+        }
+    }
+    // run f on every thread (the caller is thread 0); returns after the join barrier
+    void run(const std::function<void(int)> &f) {
+        job = &f;
+        epoch.v.fetch_add(1, std::memory_order_release);
+        tl_in_plan = true;
+        f(0);
+        barrier(0);
+        tl_in_plan = false;
+    }
+};
+
+// plan::split / split_rows (crates/model/src/plan.rs:156-164)
+inline void split(int64_t n, int parts, int i, int64_t &a, int64_t &b) {
+    a = n * i / parts;
+    b = n * (i + 1) / parts;
+}
+inline void split_rows(int64_t rows, int parts, int i, int64_t &a, int64_t &b) {
+    split(rows / 8, parts, i, a, b);
+    a *= 8;
+    b *= 8;
+}
+
+// rows [r0, r1) of a Q8_0 matrix for nl lanes, y[l][r - r0], on the calling thread: the same
+// per-(row, lane) block chain as oxo_gemv_q8_0
+void gemv_rows(const int8_t *wq, const uint16_t *wd, int64_t k, int64_t r0, int64_t r1, int nl, const int8_t *const *xq,
+               const uint16_t *const *xd, float *const *y) {
+    const int64_t nb = k / 32;
+    for (int64_t r = r0; r < r1; r++) {
+        const int8_t *w = wq + r * k;
+        for (int l = 0; l < nl; l++) {
+            const int8_t *x = xq[l];
+            float acc = 0.0f;
+            for (int64_t b = 0; b < nb; b++) {
+                int32_t s = 0;
+                for (int j = 0; j < 32; j++) s += (int32_t)w[b * 32 + j] * (int32_t)x[b * 32 + j];
+                const float prod = oxo_f16_to_f32(xd[l][b]) * oxo_f16_to_f32(wd[r * nb + b]);
+                acc = std::fma((float)s, prod, acc);
+            }
+            y[l][r - r0] = acc;
+        }
+    }
+}
 
 inline int64_t padded_n_kv(int64_t pos, int64_t n_ctx) {
     return std::min(n_ctx, std::max<int64_t>(256, (pos + 1 + 255) / 256 * 256));
@@ -435,8 +575,501 @@ struct oxo_engine {
         moe(l, nl);
     }
 
+    // ---- the static plan on the pinned team (crates/model/src/plan.rs:171-249, engine.rs:2137-2190):
+    // every thread walks the run's phases and does its share of each; one barrier after each phase.
+    // Each row, head, unit and logit is computed by one thread with the same arithmetic as the
+    // methods above, so a plan run gives the same bits as they do.
+    struct TS {
+        std::vector<std::vector<float>> xin, xn, qkv, z, beta, alpha, conv, qg, cat, dtmp, probs, w;
+        std::vector<std::vector<int8_t>> xq, oq;
+        std::vector<std::vector<uint16_t>> xd, od;
+        std::vector<std::vector<int32_t>> ids;
+        std::vector<float> gate, beta_s, gdn, tmpn, zs, tmp, q, aout, gs, kn, g, u, wp, sh_gate;
+        std::vector<int32_t> iscr;
+        std::vector<std::pair<uint32_t, uint32_t>> uni_u;   // union units (expert, 256-row block)
+        std::vector<uint32_t> uni_e;
+    };
+    std::unique_ptr<PlanPool> pool;
+    std::vector<TS> pts;
+    std::vector<std::vector<float>> p_router, p_hsh, p_h, p_kraw;
+    std::vector<std::vector<int8_t>> p_hq, p_hshq;
+    std::vector<std::vector<uint16_t>> p_hd, p_hshd;
+    std::vector<std::vector<std::pair<float, uint32_t>>> p_best;   // [lane][thread]
+
+    int set_plan(int nthreads) {
+        pool.reset();
+        pts.clear();
+        if (nthreads <= 0) return 0;
+        pool.reset(new PlanPool());
+        if (!pool->start(nthreads)) {
+            pool.reset();
+            return -1;
+        }
+        const int nt = pool->n, L = max_lanes;
+        const int64_t E = d.n_embd, nk = d.ssm_n_kheads, ds = d.ssm_d_state, K = d.n_expert_used, F = d.ff_exp;
+        const int64_t nch = d.ssm_d_inner + 2 * nk * ds, W = std::max<int64_t>(d.ssm_d_inner, d.n_head * d.head_dim);
+        auto vv = [&](int64_t n) { return std::vector<std::vector<float>>(L, std::vector<float>(n, 0.0f)); };
+        pts.resize(nt);
+        for (TS &t : pts) {
+            t.xin = vv(E); t.xn = vv(E); t.qkv = vv(nch); t.z = vv(d.ssm_d_inner); t.beta = vv(d.ssm_n_vheads);
+            t.alpha = vv(d.ssm_n_vheads); t.conv = vv(nch); t.qg = vv(2 * d.n_head * d.head_dim); t.cat = vv(2 * E);
+            t.dtmp = vv((K + 1) * E); t.probs = vv(d.n_expert); t.w = vv(K);
+            t.xq.assign(L, std::vector<int8_t>(2 * E)); t.xd.assign(L, std::vector<uint16_t>(2 * E / 32));
+            t.oq.assign(L, std::vector<int8_t>(W)); t.od.assign(L, std::vector<uint16_t>(W / 32));
+            t.ids.assign(L, std::vector<int32_t>(K));
+            t.gate.assign(d.ssm_n_vheads, 0.f); t.beta_s.assign(d.ssm_n_vheads, 0.f);
+            const int64_t hv = d.ssm_d_inner / d.ssm_n_vheads;
+            t.gdn.assign(hv, 0.f); t.tmpn.assign(hv, 0.f); t.zs.assign(hv, 0.f);
+            t.tmp.assign(std::max<int64_t>(nch, 256), 0.f);
+            t.q.assign(d.head_dim, 0.f); t.aout.assign(d.head_dim, 0.f); t.gs.assign(d.head_dim, 0.f);
+            t.kn.assign(d.head_dim, 0.f); t.g.assign(256, 0.f); t.u.assign(256, 0.f);
+            t.wp.assign(d.n_expert, 0.f); t.sh_gate.assign(L, 0.f); t.iscr.assign(d.n_expert, 0);
+        }
+        p_router = vv(d.n_expert); p_hsh = vv(d.ff_shexp); p_h = vv(K * F); p_kraw = vv(d.n_head_kv * d.head_dim);
+        p_hq.assign(L, std::vector<int8_t>(K * F)); p_hd.assign(L, std::vector<uint16_t>(K * F / 32));
+        p_hshq.assign(L, std::vector<int8_t>(d.ff_shexp)); p_hshd.assign(L, std::vector<uint16_t>(d.ff_shexp / 32));
+        p_best.assign(L, std::vector<std::pair<float, uint32_t>>(nt));
+        return nt;
+    }
+
+    // thread `tid`'s rows of w for its lanes: y[ln] + 0 .. (r1 - r0)
+    static void rows_of(const Q8 &w, int64_t r0, int64_t r1, int nl, std::vector<std::vector<int8_t>> &xq,
+                        std::vector<std::vector<uint16_t>> &xd, const std::function<float *(int)> &y) {
+        if (r1 <= r0) return;
+        const int8_t *q[8];
+        const uint16_t *dd[8];
+        float *ys[8];
+        for (int ln = 0; ln < nl; ln++) { q[ln] = xq[ln].data(); dd[ln] = xd[ln].data(); ys[ln] = y(ln); }
+        gemv_rows(w.q.data(), w.d.data(), w.k, r0, r1, nl, q, dd, ys);
+    }
+    // the layer input and its norm on this thread (layer_entry + norm, engine.rs:2239-2266)
+    void p_entry(TS &ts, int l, int nl, const uint32_t *toks, const std::vector<float> &normw) {
+        for (int ln = 0; ln < nl; ln++) {
+            if (l == 0) ts.xin[ln] = embed(toks[ln]);
+            else std::memcpy(ts.xin[ln].data(), x2[ln].data(), d.n_embd * 4);
+            oxo_rms_norm_mul_f32(ts.xin[ln].data(), normw.data(), ts.xn[ln].data(), d.n_embd, d.rms_eps);
+            oxo_quantize_row_q8_0(ts.xn[ln].data(), d.n_embd, ts.xq[ln].data(), ts.xd[ln].data());
+        }
+    }
+
+    // RecMix (engine.rs:2394-2570): key heads [kh0, kh1) of this thread, their value heads
+    void p_rec_mix(TS &ts, int tid, int nt, int l, int nl, const uint32_t *toks) {
+        Layer &L = layers[l];
+        p_entry(ts, l, nl, toks, L.attn_norm);
+        const int64_t ds = d.ssm_d_state, nk = d.ssm_n_kheads, nv = d.ssm_n_vheads, hv = d.ssm_d_inner / nv;
+        const int64_t kc = d.ssm_conv_kernel, vpk = nv / nk;
+        int64_t kh0, kh1;
+        split(nk, nt, tid, kh0, kh1);
+        if (kh1 <= kh0) return;
+        std::vector<std::pair<int64_t, int64_t>> rg;
+        rg.push_back({kh0 * ds, kh1 * ds});
+        rg.push_back({nk * ds + kh0 * ds, nk * ds + kh1 * ds});
+        for (int64_t m = 0; m < vpk; m++) rg.push_back({2 * nk * ds + (kh0 + m * nk) * hv, 2 * nk * ds + (kh1 + m * nk) * hv});
+        for (auto &r : rg) rows_of(L.qkv, r.first, r.second, nl, ts.xq, ts.xd, [&](int ln) { return ts.qkv[ln].data() + r.first; });
+        for (int64_t m = 0; m < vpk; m++) {
+            const int64_t v0 = kh0 + m * nk, v1 = kh1 + m * nk;
+            rows_of(L.z, v0 * hv, v1 * hv, nl, ts.xq, ts.xd, [&](int ln) { return ts.z[ln].data() + v0 * hv; });
+            rows_of(L.beta, v0, v1, nl, ts.xq, ts.xd, [&](int ln) { return ts.beta[ln].data() + v0; });
+            rows_of(L.alpha, v0, v1, nl, ts.xq, ts.xd, [&](int ln) { return ts.alpha[ln].data() + v0; });
+        }
+        const int ri = L.index;
+        for (int ln = 0; ln < nl; ln++) {
+            const int dst = (cur_slot + ln) % n_slots;
+            const int src = ln == 0 ? dst : (cur_slot + ln - 1) % n_slots;
+            float *cs = conv_state.data() + ((size_t)dst * n_rec + ri) * conv_len;
+            const float *cs_src = conv_state.data() + ((size_t)src * n_rec + ri) * conv_len;
+            float *cv = ts.conv[ln].data();
+            for (auto &r : rg) {
+                if (src != dst) std::memcpy(cs + r.first * (kc - 1), cs_src + r.first * (kc - 1), (r.second - r.first) * (kc - 1) * 4);
+                oxo_ssm_conv_step_f32(cs + r.first * (kc - 1), ts.qkv[ln].data() + r.first, L.conv.data() + r.first * kc,
+                                      (int)(r.second - r.first), (int)kc, cv + r.first);
+                oxo_silu_f32((int)(r.second - r.first), ts.tmp.data(), cv + r.first);
+                std::memcpy(cv + r.first, ts.tmp.data(), (r.second - r.first) * 4);
+            }
+            for (int64_t g = kh0; g < kh1; g++) {
+                oxo_gdn_l2_norm_f32(cv + g * ds, ds, d.rms_eps);
+                oxo_gdn_l2_norm_f32(cv + nk * ds + g * ds, ds, d.rms_eps);
+            }
+            for (int64_t m = 0; m < vpk; m++)
+                for (int64_t vh = kh0 + m * nk; vh < kh1 + m * nk; vh++) {
+                    const float ab = ts.alpha[ln][vh] + L.dt[vh];
+                    float sp;
+                    oxo_softplus_f32(1, &sp, &ab);
+                    ts.gate[vh] = sp * L.a[vh];
+                    oxo_sigmoid_f32(1, &ts.beta_s[vh], &ts.beta[ln][vh]);
+                }
+            for (int64_t m = 0; m < vpk; m++)
+                for (int64_t vh = kh0 + m * nk; vh < kh1 + m * nk; vh++) {
+                    const int64_t kh = vh % nk;
+                    float *st = ssm_state.data() + ((size_t)dst * n_rec + ri) * ssm_len + vh * hv * hv;
+                    const float *s_in = ssm_state.data() + ((size_t)src * n_rec + ri) * ssm_len + vh * hv * hv;
+                    oxo_gated_delta_net_step_f32_from(st, s_in, cv + kh * ds, cv + nk * ds + kh * ds, cv + 2 * nk * ds + vh * hv,
+                                                      ts.gate[vh], ts.beta_s[vh], hv, ts.gdn.data());
+                    oxo_rms_norm_mul_f32(ts.gdn.data(), L.ssm_norm.data(), ts.tmpn.data(), hv, d.rms_eps);
+                    oxo_silu_f32((int)hv, ts.zs.data(), ts.z[ln].data() + vh * hv);
+                    for (int64_t j = 0; j < hv; j++) o[ln][vh * hv + j] = ts.tmpn[j] * ts.zs[j];
+                }
+        }
+    }
+    // RecOut / AttnOut (engine.rs:2573-2609): this thread's rows of the output projection + residual
+    void p_mix_out_lanes(TS &ts, int tid, int nt, int l, int nl, int64_t width) {
+        int64_t r0, r1;
+        split_rows(d.n_embd, nt, tid, r0, r1);
+        if (r1 <= r0) return;
+        for (int ln = 0; ln < nl; ln++) oxo_quantize_row_q8_0(o[ln].data(), width, ts.oq[ln].data(), ts.od[ln].data());
+        rows_of(layers[l].out, r0, r1, nl, ts.oq, ts.od, [&](int ln) { return ts.dtmp[ln].data(); });
+        for (int ln = 0; ln < nl; ln++)
+            for (int64_t r = r0; r < r1; r++) x1[ln][r] = ts.dtmp[ln][r - r0] + ts.xin[ln][r];
+    }
+    // AttnQkv (engine.rs:2614-2705): query heads [qh0, qh1) (q + gate rows, q norm, RoPE), raw K
+    // rows k_rows, V rows v_rows (the reversed split) into V^T at pos0 + lane
+    void p_attn_qkv(TS &ts, int tid, int nt, int l, int nl, int64_t pos0, const uint32_t *toks, bool with_q) {
+        Layer &L = layers[l];
+        if (with_q) p_entry(ts, l, nl, toks, L.attn_norm);
+        const int64_t hd = d.head_dim, nkv = d.n_head_kv;
+        const int ai = L.index;
+        if (with_q) {
+            int64_t qh0, qh1;
+            split(d.n_head, nt, tid, qh0, qh1);
+            rows_of(L.wq, qh0 * 2 * hd, qh1 * 2 * hd, nl, ts.xq, ts.xd, [&](int ln) { return ts.qg[ln].data() + qh0 * 2 * hd; });
+        }
+        int64_t k0, k1, v0, v1;
+        split_rows(nkv * hd, nt, tid, k0, k1);
+        split_rows(nkv * hd, nt, nt - 1 - tid, v0, v1);
+        rows_of(L.wk, k0, k1, nl, ts.xq, ts.xd, [&](int ln) { return p_kraw[ln].data() + k0; });
+        if (v1 > v0) {
+            rows_of(L.wv, v0, v1, nl, ts.xq, ts.xd, [&](int ln) { return ts.dtmp[ln].data(); });
+            for (int ln = 0; ln < nl; ln++)
+                for (int64_t r = v0; r < v1; r++)
+                    vcache[((size_t)ai * nkv * hd + r) * v_stride + pos0 + ln] = oxo_f32_to_f16(ts.dtmp[ln][r - v0]);
+        }
+    }
+    // write_k (engine.rs:2709-2745): the owners of query head kvh * group write K rows of every lane
+    void p_write_k(TS &ts, int tid, int nt, int l, int nl, int64_t pos0) {
+        Layer &L = layers[l];
+        const int64_t hd = d.head_dim, nkv = d.n_head_kv, group = d.n_head / nkv;
+        int64_t qh0, qh1;
+        split(d.n_head, nt, tid, qh0, qh1);
+        for (int64_t kvh = 0; kvh < nkv; kvh++) {
+            if (kvh * group < qh0 || kvh * group >= qh1) continue;
+            for (int ln = 0; ln < nl; ln++) {
+                const int64_t p = pos0 + ln;
+                oxo_rms_norm_mul_f32(p_kraw[ln].data() + kvh * hd, L.k_norm.data(), ts.kn.data(), hd, d.rms_eps);
+                oxo_rope_neox_inplace(ts.kn.data(), d.n_rot, rope_tab.data() + p * d.n_rot);
+                uint16_t *kr = kcache.data() + (((size_t)L.index * nkv + kvh) * n_ctx + p) * hd;
+                for (int64_t i = 0; i < hd; i++) kr[i] = oxo_f32_to_f16(ts.kn[i]);
+            }
+        }
+    }
+    // AttnCore (engine.rs:2748-2830) after the K rows are written: query heads [qh0, qh1), every lane
+    void p_attn_core(TS &ts, int tid, int nt, int l, int nl, int64_t pos0) {
+        Layer &L = layers[l];
+        const int64_t hd = d.head_dim, nkv = d.n_head_kv, group = d.n_head / nkv;
+        const int ai = L.index;
+        const float scale = 1.0f / sqrtf((float)hd);
+        int64_t qh0, qh1;
+        split(d.n_head, nt, tid, qh0, qh1);
+        for (int ln = 0; ln < nl; ln++) {
+            const int64_t p = pos0 + ln;
+            const int n_kv = (int)padded_n_kv(p, n_ctx);
+            for (int64_t h = qh0; h < qh1; h++) {
+                oxo_rms_norm_mul_f32(ts.qg[ln].data() + h * 2 * hd, L.q_norm.data(), ts.q.data(), hd, d.rms_eps);
+                oxo_rope_neox_inplace(ts.q.data(), d.n_rot, rope_tab.data() + p * d.n_rot);
+                const int64_t kvh = h / group;
+                const uint16_t *kb = kcache.data() + ((size_t)ai * nkv + kvh) * n_ctx * hd;
+                const uint16_t *vb = vcache.data() + ((size_t)ai * nkv * hd + kvh * hd) * v_stride;
+                oxo_attn_head_f16(ts.q.data(), kb, hd, kb + p * hd, vb, v_stride, n_kv, (int)p, (int)hd, scale, ts.aout.data());
+                oxo_sigmoid_f32(hd, ts.gs.data(), ts.qg[ln].data() + h * 2 * hd + hd);
+                for (int64_t j = 0; j < hd; j++) o[ln][h * hd + j] = ts.aout[j] * ts.gs[j];
+            }
+        }
+    }
+    // MoeRouter (engine.rs:3372-3410): router rows, the shared gate (every thread), shared gate/up rows
+    void p_moe_router(TS &ts, int tid, int nt, int l, int nl) {
+        Layer &L = layers[l];
+        const int64_t E = d.n_embd;
+        int64_t e0, e1, s0, s1;
+        split(d.n_expert, nt, tid, e0, e1);
+        split_rows(d.ff_shexp, nt, tid, s0, s1);
+        for (int ln = 0; ln < nl; ln++) {
+            oxo_rms_norm_mul_f32(x1[ln].data(), L.post_norm.data(), ts.xn[ln].data(), E, d.rms_eps);
+            oxo_quantize_row_q8_0(ts.xn[ln].data(), E, ts.xq[ln].data(), ts.xd[ln].data());
+            for (int64_t e = e0; e < e1; e++) p_router[ln][e] = oxo_vec_dot_f32((int)E, L.router.data() + e * E, ts.xn[ln].data());
+            const float sgd = oxo_vec_dot_f32((int)E, L.shexp_gate.data(), ts.xn[ln].data());
+            oxo_sigmoid_f32(1, &ts.sh_gate[ln], &sgd);
+        }
+        if (s1 > s0) {
+            for (int ln = 0; ln < nl; ln++) {
+                const int8_t *q[1] = {ts.xq[ln].data()};
+                const uint16_t *dd[1] = {ts.xd[ln].data()};
+                float *yg[1] = {ts.tmp.data()}, *yu[1] = {ts.tmp.data() + (s1 - s0)};
+                gemv_rows(L.gate_sh.q.data(), L.gate_sh.d.data(), E, s0, s1, 1, q, dd, yg);
+                gemv_rows(L.up_sh.q.data(), L.up_sh.d.data(), E, s0, s1, 1, q, dd, yu);
+                oxo_swiglu_f32((int)(s1 - s0), p_hsh[ln].data() + s0, ts.tmp.data(), ts.tmp.data() + (s1 - s0));
+            }
+        }
+    }
+    // route (engine.rs:3414-3429), on every thread for every lane
+    void p_route(TS &ts, int nl) {
+        const int64_t NE = d.n_expert, K = d.n_expert_used;
+        for (int ln = 0; ln < nl; ln++) {
+            oxo_soft_max_f32((int)NE, ts.probs[ln].data(), p_router[ln].data(), 1.0f, nullptr, ts.wp.data());
+            int tie = 0;
+            oxo_argsort_top_k_f32(ts.probs[ln].data(), (int)NE, (int)K, ts.ids[ln].data(), ts.iscr.data(), &tie);
+            for (int64_t j = 0; j < K; j++) ts.w[ln][j] = ts.probs[ln][ts.ids[ln][j]];
+            float s = oxo_vec_sum_f32((int)K, ts.w[ln].data());
+            s = std::max(std::min(s, INFINITY), 6.103515625e-5f);
+            for (int64_t j = 0; j < K; j++) ts.w[ln][j] = ts.w[ln][j] / s;
+        }
+    }
+    // Synthetic expert weights this run routes to and nothing has generated yet, made by the whole
+    // team (rows split) before the units run; its time counts as generation, its barriers do not
+    // count. Every thread sees the same list: the units are the same on every thread and nothing
+    // generates experts between the previous barrier and the first one here.
+    void p_gen_experts(TS &ts, int tid, int nt, int l) {
+        Layer &L = layers[l];
+        std::vector<uint32_t> miss;
+        for (auto &u : ts.uni_u)
+            if (u.second == 0 && !L.experts[u.first]) miss.push_back(u.first);
+        if (miss.empty()) return;
+        const auto t0 = std::chrono::steady_clock::now();
+        pool->barrier(tid, false);
+        if (tid == 0)
+            for (uint32_t e : miss) {
+                std::unique_ptr<Q8[]> m(new Q8[3]);
+                const int64_t E = d.n_embd, F = d.ff_exp;
+                const int64_t rk[3][2] = {{F, E}, {F, E}, {E, F}};
+                for (int w = 0; w < 3; w++) {
+                    m[w].rows = rk[w][0];
+                    m[w].k = rk[w][1];
+                    m[w].q.resize(rk[w][0] * rk[w][1]);
+                    m[w].d.resize(rk[w][0] * rk[w][1] / 32);
+                }
+                L.experts[e] = std::move(m);
+            }
+        pool->barrier(tid, false);
+        const int kinds[3] = {OXE_T_GATE_EXPS, OXE_T_UP_EXPS, OXE_T_DOWN_EXPS};
+        for (uint32_t e : miss)
+            for (int w = 0; w < 3; w++) {
+                Q8 &m = L.experts[e][w];
+                int64_t r0, r1;
+                split(m.rows, nt, tid, r0, r1);
+                gen_q8_rows(seed, l, kinds[w], m.rows, m.k, e, r0, r1, m);
+            }
+        pool->barrier(tid, false);
+        if (tid == 0) gen_seconds += std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
+    }
+    // MoeGateUp (engine.rs:3437-3539): units (expert, 256-row block); several lanes: the union of
+    // the lanes' experts in lane-major first use, split evenly, each unit for every lane that routed there
+    void p_moe_gate_up(TS &ts, int tid, int nt, int l, int nl) {
+        const int64_t E = d.n_embd, F = d.ff_exp, K = d.n_expert_used, bpe = F / 256;
+        p_route(ts, nl);
+        ts.uni_u.clear();
+        ts.uni_e.clear();
+        if (nl == 1) {
+            for (int64_t j = 0; j < K; j++)
+                for (int64_t b = 0; b < bpe; b++) ts.uni_u.push_back({(uint32_t)ts.ids[0][j], (uint32_t)b});
+        } else {
+            for (int ln = 0; ln < nl; ln++)
+                for (int64_t j = 0; j < K; j++) {
+                    const uint32_t e = (uint32_t)ts.ids[ln][j];
+                    if (std::find(ts.uni_e.begin(), ts.uni_e.end(), e) == ts.uni_e.end()) {
+                        ts.uni_e.push_back(e);
+                        for (int64_t b = 0; b < bpe; b++) ts.uni_u.push_back({e, (uint32_t)b});
+                    }
+                }
+        }
+        p_gen_experts(ts, tid, nt, l);
+        int64_t u0, u1;
+        split((int64_t)ts.uni_u.size(), nt, tid, u0, u1);
+        for (int64_t uu = u0; uu < u1; uu++) {
+            const uint32_t e = ts.uni_u[uu].first;
+            const int64_t b = ts.uni_u[uu].second;
+            const Q8 &wg = expert(l, (int)e, 0), &wu = expert(l, (int)e, 1);
+            for (int ln = 0; ln < nl; ln++) {
+                int64_t j = -1;
+                for (int64_t i = 0; i < K; i++)
+                    if ((uint32_t)ts.ids[ln][i] == e) { j = i; break; }
+                if (j < 0) continue;
+                const int8_t *q[1] = {ts.xq[ln].data()};
+                const uint16_t *dd[1] = {ts.xd[ln].data()};
+                float *yg[1] = {ts.g.data()}, *yu[1] = {ts.u.data()};
+                gemv_rows(wg.q.data(), wg.d.data(), E, b * 256, (b + 1) * 256, 1, q, dd, yg);
+                gemv_rows(wu.q.data(), wu.d.data(), E, b * 256, (b + 1) * 256, 1, q, dd, yu);
+                const int64_t off = j * F + b * 256;
+                oxo_swiglu_f32(256, p_h[ln].data() + off, ts.g.data(), ts.u.data());
+                oxo_quantize_row_q8_0(p_h[ln].data() + off, 256, p_hq[ln].data() + off, p_hd[ln].data() + off / 32);
+            }
+        }
+        for (int64_t b = 0; b < d.ff_shexp / 256; b++)
+            if (nt - 1 - (int)(b % nt) == tid)
+                for (int ln = 0; ln < nl; ln++)
+                    oxo_quantize_row_q8_0(p_hsh[ln].data() + b * 256, 256, p_hshq[ln].data() + b * 256, p_hshd[ln].data() + b * 8);
+    }
+    // MoeDown (engine.rs:3542-3625): this thread's output rows of every routed expert and the shared
+    // expert, combined in the reference's order, + residual
+    void p_moe_down(TS &ts, int tid, int nt, int l, int nl) {
+        Layer &L = layers[l];
+        const int64_t E = d.n_embd, F = d.ff_exp, K = d.n_expert_used;
+        int64_t r0, r1;
+        split_rows(E, nt, tid, r0, r1);
+        const int64_t nr = r1 - r0;
+        if (nr <= 0) return;
+        for (int ln = 0; ln < nl; ln++) {
+            float *dt = ts.dtmp[ln].data();
+            for (int64_t j = 0; j < K; j++) {
+                const Q8 &wdn = expert(l, ts.ids[ln][j], 2);
+                const int8_t *q[1] = {p_hq[ln].data() + j * F};
+                const uint16_t *dd[1] = {p_hd[ln].data() + j * F / 32};
+                float *y[1] = {dt + j * nr};
+                gemv_rows(wdn.q.data(), wdn.d.data(), F, r0, r1, 1, q, dd, y);
+            }
+            const int8_t *q[1] = {p_hshq[ln].data()};
+            const uint16_t *dd[1] = {p_hshd[ln].data()};
+            float *y[1] = {dt + K * nr};
+            gemv_rows(L.down_sh.q.data(), L.down_sh.d.data(), d.ff_shexp, r0, r1, 1, q, dd, y);
+            const float sg = ts.sh_gate[ln];
+            for (int64_t i = 0; i < nr; i++) {
+                float m = dt[i] * ts.w[ln][0];
+                for (int64_t j = 1; j < K; j++) {
+                    const float pp = dt[j * nr + i] * ts.w[ln][j];
+                    m = m + pp;
+                }
+                const float sh = dt[K * nr + i] * sg;
+                const float f = m + sh;
+                x2[ln][r0 + i] = f + x1[ln][r0 + i];
+            }
+        }
+    }
+    // Head (engine.rs:3630-3715): this thread's vocabulary rows in chunks of 256, the first strict
+    // maximum per lane; thread 0 keeps the normed hidden state
+    void p_head(TS &ts, int tid, int nt, int nl, uint32_t mask, const std::vector<float> &norm) {
+        const int64_t E = d.n_embd, V = d.n_vocab;
+        int64_t r0, r1;
+        split_rows(V, nt, tid, r0, r1);
+        for (int ln = 0; ln < nl; ln++) {
+            oxo_rms_norm_mul_f32(x2[ln].data(), norm.data(), ts.xn[ln].data(), E, d.rms_eps);
+            if (tid == 0) std::memcpy(hout[ln].data(), ts.xn[ln].data(), E * 4);
+            std::pair<float, uint32_t> b{-INFINITY, UINT32_MAX};
+            if (mask & (1u << ln)) {
+                oxo_quantize_row_q8_0(ts.xn[ln].data(), E, ts.xq[ln].data(), ts.xd[ln].data());
+                for (int64_t r = r0; r < r1; r += 256) {
+                    const int64_t c = std::min<int64_t>(256, r1 - r);
+                    const int8_t *q[1] = {ts.xq[ln].data()};
+                    const uint16_t *dd[1] = {ts.xd[ln].data()};
+                    float *y[1] = {ts.tmp.data()};
+                    gemv_rows(output.q.data(), output.d.data(), E, r, r + c, 1, q, dd, y);
+                    for (int64_t i = 0; i < c; i++)
+                        if (ts.tmp[i] > b.first) b = {ts.tmp[i], (uint32_t)(r + i)};
+                    if (keep_logits) std::memcpy(logits[ln].data() + r, ts.tmp.data(), c * 4);
+                }
+            }
+            p_best[ln][tid] = b;
+        }
+    }
+    void p_gather_argmax(int nl) {
+        for (int ln = 0; ln < nl; ln++) {
+            std::pair<float, uint32_t> b{-INFINITY, UINT32_MAX};
+            for (auto &t : p_best[ln])
+                if (t.first > b.first) b = t;
+            argmax[ln] = b.second == UINT32_MAX ? 0 : b.second;
+        }
+    }
+    // the MoE phases of layer l (three barriers)
+    void p_moe(TS &ts, int tid, int nt, int l, int nl) {
+        p_moe_router(ts, tid, nt, l, nl);
+        pool->barrier(tid);
+        p_moe_gate_up(ts, tid, nt, l, nl);
+        pool->barrier(tid);
+        p_moe_down(ts, tid, nt, l, nl);
+        pool->barrier(tid);
+    }
+    // the attention layer's mixer phases (AttnQkv, AttnCore with write_k + its inner barrier, AttnOut)
+    void p_attention(TS &ts, int tid, int nt, int l, int nl, int64_t pos0, const uint32_t *toks) {
+        p_attn_qkv(ts, tid, nt, l, nl, pos0, toks, true);
+        pool->barrier(tid);
+        p_write_k(ts, tid, nt, l, nl, pos0);
+        pool->barrier(tid);
+        p_attn_core(ts, tid, nt, l, nl, pos0);
+        pool->barrier(tid);
+        p_mix_out_lanes(ts, tid, nt, l, nl, d.n_head * d.head_dim);
+        pool->barrier(tid);
+    }
+    int verify_plan(const uint32_t *toks, int n, uint32_t *out) {
+        pend_pos0 = pos;
+        pend_cur = cur_slot;
+        pend_n = n;
+        pend_done = 0;
+        const int nt = pool->n;
+        const int64_t p0 = pos;
+        std::function<void(int)> job = [&](int tid) {
+            TS &ts = pts[tid];
+            for (int l = 0; l < d.n_layer; l++) {
+                if (layers[l].att) {
+                    p_attention(ts, tid, nt, l, n, p0, toks);
+                } else {
+                    p_rec_mix(ts, tid, nt, l, n, toks);
+                    pool->barrier(tid);
+                    p_mix_out_lanes(ts, tid, nt, l, n, d.ssm_d_inner);
+                    pool->barrier(tid);
+                }
+                p_moe(ts, tid, nt, l, n);
+            }
+            p_head(ts, tid, nt, n, (1u << n) - 1, out_norm);
+        };
+        pool->run(job);
+        p_gather_argmax(n);
+        for (int ln = 0; ln < n; ln++) out[ln] = argmax[ln];
+        return 0;
+    }
+    // MtpEntry (engine.rs:2362-2390) as its own phase: eh_proj rows of this thread for every lane
+    void p_mtp_entry(TS &ts, int tid, int nt, int nl, const uint32_t *toks) {
+        Layer &L = layers[d.n_layer];
+        const int64_t E = d.n_embd;
+        int64_t r0, r1;
+        split_rows(E, nt, tid, r0, r1);
+        for (int ln = 0; ln < nl; ln++) {
+            std::vector<float> e = embed(toks[ln]);
+            oxo_rms_norm_mul_f32(e.data(), L.enorm.data(), ts.cat[ln].data(), E, d.rms_eps);
+            oxo_rms_norm_mul_f32(hin[ln].data(), L.hnorm.data(), ts.cat[ln].data() + E, E, d.rms_eps);
+            oxo_quantize_row_q8_0(ts.cat[ln].data(), 2 * E, ts.xq[ln].data(), ts.xd[ln].data());
+        }
+        rows_of(L.eh_proj, r0, r1, nl, ts.xq, ts.xd, [&](int ln) { return x2[ln].data() + r0; });
+    }
+    uint32_t mtp_run_plan(const uint32_t *toks, int n, int64_t pos0, int head_last) {
+        const int l = d.n_layer, nt = pool->n;
+        std::function<void(int)> job = [&](int tid) {
+            TS &ts = pts[tid];
+            p_mtp_entry(ts, tid, nt, n, toks);
+            pool->barrier(tid);
+            p_attention(ts, tid, nt, l, n, pos0, toks);
+            p_moe(ts, tid, nt, l, n);
+            p_head(ts, tid, nt, n, head_last ? 1u << (n - 1) : 0u, layers[l].head_norm);
+        };
+        pool->run(job);
+        p_gather_argmax(n);
+        return head_last ? argmax[n - 1] : UINT32_MAX;
+    }
+    void mtp_seed_plan(const uint32_t *toks, int n, int64_t pos0) {
+        const int l = d.n_layer, nt = pool->n;
+        std::function<void(int)> job = [&](int tid) {
+            TS &ts = pts[tid];
+            p_mtp_entry(ts, tid, nt, n, toks);
+            pool->barrier(tid);
+            for (int ln = 0; ln < n; ln++) {
+                oxo_rms_norm_mul_f32(x2[ln].data(), layers[l].attn_norm.data(), ts.xn[ln].data(), d.n_embd, d.rms_eps);
+                oxo_quantize_row_q8_0(ts.xn[ln].data(), d.n_embd, ts.xq[ln].data(), ts.xd[ln].data());
+            }
+            p_attn_qkv(ts, tid, nt, l, n, pos0, toks, false);
+            pool->barrier(tid);
+            p_write_k(ts, tid, nt, l, n, pos0);
+        };
+        pool->run(job);
+    }
+
     int verify(const uint32_t *toks, int n, uint32_t *out) {
         if (n < 1 || n > n_slots || pos + n > n_ctx) return -1;
+        if (pool) return verify_plan(toks, n, out);
         pend_pos0 = pos;
         pend_cur = cur_slot;
         pend_n = n;
@@ -485,6 +1118,7 @@ struct oxo_engine {
     uint32_t mtp_run(const uint32_t *toks, int n, int64_t pos0, const float *hs, int head_last) {
         const int l = d.n_layer;
         for (int ln = 0; ln < n; ln++) std::memcpy(hin[ln].data(), hs + ln * d.n_embd, d.n_embd * 4);
+        if (pool) return mtp_run_plan(toks, n, pos0, head_last);
         mtp_entry(n, toks);
         for (int ln = 0; ln < n; ln++) xin[ln] = x2[ln];
         attention(l, n, pos0);
@@ -497,6 +1131,10 @@ struct oxo_engine {
     void mtp_seed(const uint32_t *toks, int n, int64_t pos0, const float *hs) {
         const int l = d.n_layer;
         for (int ln = 0; ln < n; ln++) std::memcpy(hin[ln].data(), hs + ln * d.n_embd, d.n_embd * 4);
+        if (pool) {
+            mtp_seed_plan(toks, n, pos0);
+            return;
+        }
         mtp_entry(n, toks);
         std::vector<std::vector<float>> xn(n, std::vector<float>(d.n_embd));
         for (int ln = 0; ln < n; ln++)
@@ -676,6 +1314,12 @@ const float *oxo_logits(const oxo_engine *e, int lane) { return e->logits[lane].
 int64_t oxo_n_ctx(const oxo_engine *e) { return e->n_ctx; }
 void oxo_set_keep_logits(oxo_engine *e, int on) { e->keep_logits = on != 0; }
 double oxo_gen_seconds(const oxo_engine *e) { return e->gen_seconds; }
+// Runs from now on go through the reference's static plan on a pinned team of `nthreads` threads
+// (at most the CPUs of the caller's mask; the caller is thread 0 and is pinned to the first of
+// them until the plan is dropped); 0 drops the plan and its team. Returns the team size, 0, or -1.
+int oxo_set_plan(oxo_engine *e, int nthreads) { return e->set_plan(nthreads); }
+// barrier episodes of the plan's team so far (the reference's barriers/token counter)
+int64_t oxo_plan_barriers(const oxo_engine *e) { return e->pool ? (int64_t)e->pool->episodes.load() : -1; }
 
 // Pin the OpenMP team the way the reference's worker pool is pinned (crates/sched/src/lib.rs:1-11,
 // 137-147, 233-249): team thread i on the i-th CPU of the calling thread's affinity set, the caller

@@ -111,6 +111,8 @@ def lib():
             "oxo_n_ctx": (C.c_int64, [C.c_void_p]),
             "oxo_set_keep_logits": (None, [C.c_void_p, C.c_int]),
             "oxo_gen_seconds": (C.c_double, [C.c_void_p]),
+            "oxo_set_plan": (C.c_int, [C.c_void_p, C.c_int]),
+            "oxo_plan_barriers": (C.c_int64, [C.c_void_p]),
             "oxo_pin_team": (C.c_int, [C.c_int]),
             "oxo_kcache": (u16p, [C.c_void_p]),
             "oxo_vcache": (u16p, [C.c_void_p]),
@@ -266,6 +268,14 @@ class Engine:
 
     def commit(self, m):
         assert lib().oxo_commit(self.h, m) == 0
+
+    def set_plan(self, nthreads):
+        """run through the reference's static plan on a pinned team of nthreads (0: the default
+        path); returns the team size"""
+        return int(lib().oxo_set_plan(self.h, nthreads))
+
+    def plan_barriers(self):
+        return int(lib().oxo_plan_barriers(self.h))
 
     def step(self, tok):
         return int(lib().oxo_step(self.h, tok))
