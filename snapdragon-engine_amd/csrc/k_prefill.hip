@@ -444,7 +444,8 @@ __global__ __launch_bounds__(256, 2) void attn_gqa_kernel(const uint16_t *qh, co
     extern __shared__ __align__(16) float s_dyn[];
     float *s_s = s_dyn;   // [GQA][kv_cap] f32 scores, then f16 probabilities in the first half of each row
     __shared__ __align__(16) uint16_t s_q[GQA][HD];
-    const int64_t t = blockIdx.x;
+    // the chunk's tokens from the last: the longest causal rows start first
+    const int64_t t = (int64_t)gridDim.x - 1 - blockIdx.x;
     const int kvh = blockIdx.y, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int pos = pos0 + (int)t;
     int n_kv = (pos + 1 + 255) / 256 * 256;
@@ -458,26 +459,26 @@ __global__ __launch_bounds__(256, 2) void attn_gqa_kernel(const uint16_t *qh, co
         for (int p0 = 0; p0 <= pos; p0 += 64) {
             const int p = p0 + pp;
             const uint16_t *krow = kb + (int64_t)(p <= pos ? p : pos) * HD;
-            h2p acc[GQA][4];
+            uint4 kvs[HD / 32];
 #pragma unroll
-            for (int h = 0; h < GQA; h++)
-#pragma unroll
-                for (int i = 0; i < 4; i++) acc[h][i] = h2p{(_Float16)0.0f, (_Float16)0.0f};
+            for (int sx = 0; sx < HD / 32; sx++) kvs[sx] = *(const uint4 *)(krow + 32 * sx + 8 * j);
+            // one query head at a time (two in flight): its score is finished and stored before the
+            // next head's query chunks are read, so only the K chunks stay in registers
 #pragma unroll 2
-            for (int sx = 0; sx < HD / 32; sx++) {
-                const uint4 kv = *(const uint4 *)(krow + 32 * sx + 8 * j);
-#pragma unroll
-                for (int h = 0; h < GQA; h++) {
-                    const uint4 qv = *(const uint4 *)(&s_q[h][32 * sx + 8 * j]);
-                    acc[h][0] = __builtin_elementwise_fma(u2h(kv.x), u2h(qv.x), acc[h][0]);
-                    acc[h][1] = __builtin_elementwise_fma(u2h(kv.y), u2h(qv.y), acc[h][1]);
-                    acc[h][2] = __builtin_elementwise_fma(u2h(kv.z), u2h(qv.z), acc[h][2]);
-                    acc[h][3] = __builtin_elementwise_fma(u2h(kv.w), u2h(qv.w), acc[h][3]);
-                }
-            }
-#pragma unroll
             for (int h = 0; h < GQA; h++) {
-                const float sc = f16x8_reduce_quad(acc[h]);
+                h2p acc[4];
+#pragma unroll
+                for (int i = 0; i < 4; i++) acc[i] = h2p{(_Float16)0.0f, (_Float16)0.0f};
+#pragma unroll
+                for (int sx = 0; sx < HD / 32; sx++) {
+                    const uint4 kv = kvs[sx];
+                    const uint4 qv = *(const uint4 *)(&s_q[h][32 * sx + 8 * j]);
+                    acc[0] = __builtin_elementwise_fma(u2h(kv.x), u2h(qv.x), acc[0]);
+                    acc[1] = __builtin_elementwise_fma(u2h(kv.y), u2h(qv.y), acc[1]);
+                    acc[2] = __builtin_elementwise_fma(u2h(kv.z), u2h(qv.z), acc[2]);
+                    acc[3] = __builtin_elementwise_fma(u2h(kv.w), u2h(qv.w), acc[3]);
+                }
+                const float sc = f16x8_reduce_quad(acc);
                 if (j == 0 && p <= pos) s_s[h * kv_cap + p] = sc;
             }
         }
@@ -532,9 +533,16 @@ __global__ __launch_bounds__(256, 2) void attn_gqa_kernel(const uint16_t *qh, co
         for (int h = 0; h < GQA; h++)
 #pragma unroll
             for (int i = 0; i < 4; i++) acc[h][i] = h2p{(_Float16)0.0f, (_Float16)0.0f};
-        for (int sx = 0; sx < n_kv / 32; sx++) {
+        // n_kv is a multiple of 256: blocks of 32 positions in groups of 4, the group's V^T loads first
+        for (int sx0 = 0; sx0 < n_kv / 32; sx0 += 4) {
+          uint4 vvs[4];
+#pragma unroll
+          for (int u = 0; u < 4; u++) vvs[u] = *(const uint4 *)(vrow + 32 * (sx0 + u) + 8 * j);
+#pragma unroll
+          for (int u = 0; u < 4; u++) {
+            const int sx = sx0 + u;
             const int p = 32 * sx + 8 * j;   // this lane's 8 positions p .. p + 7 (chain quad j of block sx)
-            uint4 vv = *(const uint4 *)(vrow + p);
+            uint4 vv = vvs[u];
             if (p + 7 > pos) {   // V^T of positions after pos is +0 in a single-token step
                 uint32_t m[4];
 #pragma unroll
@@ -552,6 +560,7 @@ __global__ __launch_bounds__(256, 2) void attn_gqa_kernel(const uint16_t *qh, co
                 acc[h][2] = __builtin_elementwise_fma(u2h(vv.z), u2h(pv.z), acc[h][2]);
                 acc[h][3] = __builtin_elementwise_fma(u2h(vv.w), u2h(pv.w), acc[h][3]);
             }
+          }
         }
 #pragma unroll
         for (int h = 0; h < GQA; h++) {
