@@ -69,7 +69,24 @@ __global__ __launch_bounds__(gm::NT, 3) void gemm_q8_kernel(GemmArgs a, int vec4
     __shared__ int64_t sxr[BN];   // activation row of each of the tile's output rows (-1: none)
     const int t = threadIdx.x, lane = t & 63, w = t >> 6;
     const int64_t k = a.k, nr = a.nr, nb = k / 32;
-    const int64_t r0 = (int64_t)blockIdx.x * BM;
+    // plain GEMMs with a partial last row tile dispatch its workgroups after all full ones, and its
+    // waves without a valid row skip the arithmetic: the round that holds them is short
+    int64_t bx = blockIdx.x, by = blockIdx.y;
+    if (!a.tiles) {
+        const int64_t nfull = nr / BM;
+        if (nfull < (int64_t)gridDim.x) {
+            const int64_t L = (int64_t)blockIdx.y * gridDim.x + blockIdx.x, nf = nfull * gridDim.y;
+            if (L < nf) {
+                bx = L % nfull;
+                by = L / nfull;
+            } else {
+                bx = nfull;
+                by = L - nf;
+            }
+        }
+    }
+    const int64_t r0 = bx * BM;
+    const bool wave_on = r0 + WR * w < nr;   // wave-uniform
     int64_t p0, pn;
     const int8_t *wq = a.wq;
     const uint16_t *wd = a.wd;
@@ -81,7 +98,7 @@ __global__ __launch_bounds__(gm::NT, 3) void gemm_q8_kernel(GemmArgs a, int vec4
         p0 = tl.y;
         pn = tl.z;
     } else {
-        p0 = (int64_t)blockIdx.y * BN;
+        p0 = by * BN;
         pn = a.nt - p0 < BN ? a.nt - p0 : BN;
     }
     if (pn <= 0) return;   // uniform
@@ -119,11 +136,13 @@ __global__ __launch_bounds__(gm::NT, 3) void gemm_q8_kernel(GemmArgs a, int vec4
     auto fetch = [&](GemmStage &S, int64_t kc) {
         const int8_t *wb = wq + kc, *xb = a.xq + kc;
         const int8_t *wsb = (const int8_t *)wd + kc / 16, *xsb = (const int8_t *)a.xd + kc / 16;
+        if (wave_on) {
 #pragma unroll
-        for (int q = 0; q < 4; q++) to_lds16(wb + wofs[q], S.w + (WR * w + 8 * q) * KC);
+            for (int q = 0; q < 4; q++) to_lds16(wb + wofs[q], S.w + (WR * w + 8 * q) * KC);
+            to_lds4(wsb + wsofs, S.dw + WR * w * NBC);
+        }
 #pragma unroll
         for (int q = 0; q < 2; q++) to_lds16(xb + xofs[q], S.x + (16 * w + 8 * q) * KC);
-        to_lds4(wsb + wsofs, S.dw + WR * w * NBC);
         if (w < 2) to_lds4(xsb + xsofs, S.dx + 32 * w * NBC);
     };
     // wave w: rows 32 w .. + 31 of the tile; tile j: tokens 32 j .. + 31. Fragment of a code row:
@@ -142,6 +161,7 @@ __global__ __launch_bounds__(gm::NT, 3) void gemm_q8_kernel(GemmArgs a, int vec4
     // (v = 4 q + e), token 32 j + (lane & 31); the two-block scale product's block j is tile j
     auto compute = [&](const GemmStage &S, auto njc) {
         constexpr int NJ = decltype(njc)::value;
+        if (!wave_on) return;
         const uint2 hw = *(const uint2 *)&S.dw[(wr + fr) * NBC];   // this lane's weight row, 4 blocks
         const uint2 hx = *(const uint2 *)&S.dx[lane * NBC];        // token `lane`, 4 blocks
         auto dots = [&](int bb, int j) {
