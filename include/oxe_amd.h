@@ -56,10 +56,12 @@ OXE_API int oxe_hip_route_f32(const float *logits, int64_t n_rows, int32_t *ids,
 
 /* Q8_0 GEMM for prefill: y[t][r] (row stride ldy >= nr) = W[r] . x[t] for nt token rows of
  * activations (oxe_hip_quantize_row_q8_0 output) against nr weight rows (layout as in
- * oxe_hip_gemv_q8_0); k a multiple of 256. Each output equals the GEMV's bit for bit (block dots
- * on the int8 matrix cores, the fp32 chain over blocks in order). Replaces ggml_gemm_q8_0_4x8_q8_0
- * (crates/kernels-sys/src/lib.rs:95; vendor/ggml-subset/generated/repack_subset.cpp:3804-3954).
- * Returns 0, -1 (bad shape or null pointer) or -2 (launch error). */
+ * oxe_hip_gemv_q8_0); k a multiple of 128. Each output equals the GEMV's bit for bit (block dots
+ * and scale products on the matrix cores, the fp32 chain over blocks in order). Replaces
+ * ggml_gemm_q8_0_4x8_q8_0 (crates/kernels-sys/src/lib.rs:95;
+ * vendor/ggml-subset/generated/repack_subset.cpp:3804-3954). wq, wd, xq and xd must be 16-byte
+ * aligned, and nr * k and nt * k below 2^32 (the kernel addresses codes with 32-bit offsets).
+ * Returns 0, -1 (bad shape, alignment or null pointer) or -2 (launch error). */
 OXE_API int oxe_hip_gemm_q8_0(int64_t k, int64_t nr, int64_t nt, const int8_t *wq, const uint16_t *wd, const int8_t *xq,
                               const uint16_t *xd, float *y, int64_t ldy, void *stream);
 

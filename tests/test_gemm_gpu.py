@@ -51,8 +51,16 @@ def test_gemm_equals_gemv_large(dev):
 def test_gemm_rejects_bad_shapes(dev):
     import oxe_amd as A
     import torch
-    wq = torch.zeros((64, 300), dtype=torch.int8, device=dev)   # k not a multiple of 256
+    wq = torch.zeros((64, 300), dtype=torch.int8, device=dev)   # k not a multiple of 128
     wd = torch.zeros((64, 300 // 32), dtype=torch.int16, device=dev)
     with pytest.raises(RuntimeError):
         A.gemm_q8_0(wq, wd, torch.zeros((4, 300), dtype=torch.int8, device=dev),
                     torch.zeros((4, 300 // 32), dtype=torch.int16, device=dev))
+    # codes not 16-byte aligned (the kernel's 16-byte global-to-LDS loads): refused, nothing launched
+    k = 256
+    buf = torch.zeros(64 * k + 16, dtype=torch.int8, device=dev)
+    wq = buf[1:1 + 64 * k].view(64, k)
+    wd = torch.zeros((64, k // 32), dtype=torch.int16, device=dev)
+    with pytest.raises(RuntimeError):
+        A.gemm_q8_0(wq, wd, torch.zeros((4, k), dtype=torch.int8, device=dev),
+                    torch.zeros((4, k // 32), dtype=torch.int16, device=dev))
