@@ -16,7 +16,9 @@ def _t(a, dev):
 
 
 @pytest.mark.parametrize("k,nr,nt", [(2048, 256, 64), (2048, 1000, 37), (512, 2048, 100), (4096, 130, 5),
-                                     (2048, 40, 1), (2048, 4096, 200)])
+                                     (2048, 40, 1), (2048, 4096, 200),
+                                     # one and three 128-byte stages (the double-buffered loop's odd ends)
+                                     (128, 64, 3), (384, 200, 70)])
 def test_gemm_bitexact_vs_oracle(dev, k, nr, nt):
     import oxe_amd as A
     wq, wd = O.synth_q8(11, 3, O.T["OUTPUT"], nr, k)
