@@ -576,10 +576,13 @@ __global__ __launch_bounds__(256, 2) void attn_gqa_kernel(const uint16_t *qh, co
 // Workgroup = 16 tokens x 16 rows (row 256 is the shared gate); lane group g (16 lanes, lane = chain
 // c) holds the chains of 4 tokens x 4 rows; token and weight rows are staged through LDS 256
 // elements at a time. Every dot keeps the reference's 16 chains in order and its reduction tree.
-constexpr int RT_TB = 16, RT_KC = 256, RT_LD = RT_KC + 16, RT_NR = NEXP + 1;
+constexpr int RT_TB = 16, RT_KC = 256, RT_Q = RT_KC / 16, RT_QP = RT_Q + 4, RT_NR = NEXP + 1;
+// LDS rows are stored chain-major: element 16 q + c of a stage at [row][c][q] (rows of RT_QP floats,
+// padded so that 16-byte reads of 16 consecutive chains fall on distinct banks), so a thread reads
+// four consecutive steps of its chain in one 16-byte load
 __global__ __launch_bounds__(256) void router_kernel(const float *xn, const float *router, const float *shg, int T, float *lg,
                                                      float *sg) {
-    __shared__ __align__(16) float s_x[RT_TB][RT_LD], s_w[RT_TB][RT_LD];
+    __shared__ __align__(16) float s_x[RT_TB][16][RT_QP], s_w[RT_TB][16][RT_QP];
     const int tid = threadIdx.x, g = tid >> 4, c = tid & 15, tb = g & 3, eb = g >> 2;
     const int64_t t0 = (int64_t)blockIdx.x * RT_TB;
     const int e0 = blockIdx.y * RT_TB;
@@ -598,21 +601,29 @@ __global__ __launch_bounds__(256) void router_kernel(const float *xn, const floa
             const float4 xv = tt < T ? *(const float4 *)(xn + tt * E + k0 + 4 * c4) : make_float4(0, 0, 0, 0);
             const float *wr = ee < NEXP ? router + (int64_t)ee * E : shg;
             const float4 wv = ee < RT_NR ? *(const float4 *)(wr + k0 + 4 * c4) : make_float4(0, 0, 0, 0);
-            *(float4 *)&s_x[row][4 * c4] = xv;
-            *(float4 *)&s_w[row][4 * c4] = wv;
+            // elements 4 c4 .. 4 c4 + 3 of the stage: step q = c4 / 4, chains 4 (c4 % 4) ..
+            const int q = c4 >> 2, cb = 4 * (c4 & 3);
+            s_x[row][cb][q] = xv.x; s_x[row][cb + 1][q] = xv.y; s_x[row][cb + 2][q] = xv.z; s_x[row][cb + 3][q] = xv.w;
+            s_w[row][cb][q] = wv.x; s_w[row][cb + 1][q] = wv.y; s_w[row][cb + 2][q] = wv.z; s_w[row][cb + 3][q] = wv.w;
         }
         __syncthreads();
-#pragma unroll 4
-        for (int q = 0; q < RT_KC / 16; q++) {
-            float xv[4], wv[4];
 #pragma unroll
-            for (int i = 0; i < 4; i++) xv[i] = s_x[4 * tb + i][16 * q + c];
+        for (int q4 = 0; q4 < RT_Q / 4; q4++) {
+            float4 xv[4], wv[4];
 #pragma unroll
-            for (int e = 0; e < 4; e++) wv[e] = s_w[4 * eb + e][16 * q + c];
+            for (int i = 0; i < 4; i++) xv[i] = *(const float4 *)&s_x[4 * tb + i][c][4 * q4];
 #pragma unroll
-            for (int i = 0; i < 4; i++)
+            for (int e = 0; e < 4; e++) wv[e] = *(const float4 *)&s_w[4 * eb + e][c][4 * q4];
 #pragma unroll
-                for (int e = 0; e < 4; e++) acc[i][e] = __builtin_fmaf(wv[e], xv[i], acc[i][e]);
+            for (int qq = 0; qq < 4; qq++)
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        const float xs = qq == 0 ? xv[i].x : qq == 1 ? xv[i].y : qq == 2 ? xv[i].z : xv[i].w;
+                        const float ws = qq == 0 ? wv[e].x : qq == 1 ? wv[e].y : qq == 2 ? wv[e].z : wv[e].w;
+                        acc[i][e] = __builtin_fmaf(ws, xs, acc[i][e]);
+                    }
         }
     }
     float v[4][4];
