@@ -28,7 +28,7 @@ MARKS = {101: "experts: union", 102: "experts: gate/up loads issued", 103: "expe
          104: "experts: gate/up dot", 105: "experts: logits load", 106: "experts: route_wave",
          111: "proj: norm prologue", 113: "proj: int dots", 112: "proj: chains",
          117: "proj: int dots (again)", 118: "proj: chains (again)", 171: "out: int dots", 172: "out: chains", 121: "dn: conv", 122: "dn: norms + gates",
-         123: "dn: delta rule", 124: "dn: head's partial sums", 125: "dn: gated norm + codes", 131: "router: norm prologue", 132: "router: f32 dots", 141: "pv: V tile to LDS",
+         123: "dn: delta rule", 124: "dn: head leader inputs", 125: "dn: head leader norm + store", 131: "router: norm prologue", 132: "router: f32 dots", 141: "pv: V tile to LDS",
          142: "pv: V.p + reduce", 143: "pv: scores load + max", 144: "pv: exp, sum, probabilities", 151: "scores: q/k prologue",
          161: "down: inputs", 162: "down: block dots", 163: "down: chains"}
 
