@@ -228,8 +228,13 @@ OXE_API int oxe_gguf_model_desc(const oxe_gguf *g, oxe_model_desc *out);
  * weights split on the device into this build's codes + scales layout (the reference repacks into
  * 4-row interleaved blocks, oxe_repack_q8_0_4x8, lib.rs:59), F32 norms, routers and state
  * parameters copied, BF16 ones widened to f32 (as the reference converts BF16 small tensors,
- * crates/model/src/mtp.rs:109-128). Other tensor types are refused by name (-1): the engine's runs
- * take Q8_0 matmul weights (the K-quant GEMVs exist at kernel level, oxe_hip_vl_gemv). */
+ * crates/model/src/mtp.rs:109-128). K-quant (Q3_K..Q6_K) expert, shared-expert and output matrices
+ * and F32 ssm_beta / ssm_alpha (a Qwen3.6 file's types; the reference's mv dispatches every type,
+ * engine.rs:2270-2343) are copied in the file's blocks into an engine created with those types,
+ * which oxe_engine_create_from_gguf reads from the file; into an engine created for Q8_0 they are
+ * refused by name (-1), as is any other tensor type. An engine with such matrices runs its runs per
+ * phase (oxe_engine_set_fused(e, 1) returns -1: the fused run kernel reads Q8_0 matrices only) and
+ * its batched prefill as decode runs of two positions (the same state and h_nextn). */
 OXE_API int oxe_engine_load_gguf(oxe_engine *e, const oxe_gguf *g);
 /* oxe_engine_load_gguf without any device allocation: no counterpart in the reference; for callers
  * that cannot allocate device memory (code under HIP graph capture, serving loops, harnesses that
@@ -239,7 +244,7 @@ OXE_API int oxe_engine_load_gguf(oxe_engine *e, const oxe_gguf *g);
  * name (-1). The engine's device must be current. Calls on one GPU share the array: a per-device
  * lock makes overlapping calls (other threads, other streams) run one after another. */
 OXE_API int oxe_engine_load_gguf_noalloc(oxe_engine *e, const oxe_gguf *g);
-/* open + model_desc + engine_create + load_gguf */
+/* open + model_desc + engine_create with the file's matrix types + load_gguf */
 OXE_API int oxe_engine_create_from_gguf(const char *path, int n_ctx, oxe_engine **out);
 
 /* ---- MTP depth-1 speculative decoding (crates/model/src/mtp.rs MtpDriver, depth 1) --------- */

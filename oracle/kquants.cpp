@@ -8,6 +8,7 @@
 #include <string.h>
 
 #include "oxo.h"
+#include "../include/oxe_model.h"
 
 namespace {
 
@@ -233,6 +234,62 @@ int oxo_vl_gemv(int type, int64_t k, int64_t nr, int nl, const void *w, const vo
         for (int l = 0; l < nl; l++)
             s[(int64_t)l * nr + r] = row((const uint8_t *)w + r * (int64_t)nb * bb, (const BQ8K *)y + (int64_t)l * nb, nb);
     return 1;
+}
+
+// Synthetic K-quant tensors for the tests' model files (not the reference's: its models come from
+// files). Block i of tensor (seed, layer, kind), flat over [expert][row][k / 256], is filled with
+// the 64-bit words oxe_rng(key, 32 i + j), then its fp16 fields are set from the scale key:
+// Q4_K / Q5_K d, dmin in [0.0005, 0.004); Q6_K d in [0.00005, 0.0003); Q3_K d in [0.0005, 0.004).
+// Codes, 6-bit scales and mins stay whatever the words hold (every bit pattern is a valid block).
+// type: 11 Q3_K, 12 Q4_K, 13 Q5_K, 14 Q6_K (ggml ids). Returns the bytes written, or 0.
+int64_t oxo_synth_kq(uint64_t seed, int layer, int kind, int type, int64_t expert, int64_t rows, int64_t k, uint8_t *out) {
+    int bb;
+    switch (type) {
+        case 11: bb = 110; break;
+        case 12: bb = 144; break;
+        case 13: bb = 176; break;
+        case 14: bb = 210; break;
+        default: return 0;
+    }
+    if (k % QK != 0 || rows < 0 || expert < 0) return 0;
+    const int64_t nb = rows * (k / QK);
+    const uint64_t key = oxe_tensor_key(seed, layer, kind);
+    const uint64_t skey = oxe_tensor_key(seed, layer, kind + OXE_T_SCALE_OFFSET);
+    const uint64_t base = (uint64_t)expert * (uint64_t)nb;
+    auto f16_in = [&](uint64_t i, float lo, float hi) {
+        const float u = oxe_synth_unit(skey, i);
+        const float t = u * (hi - lo);
+        return oxe_f32_to_f16_rne(lo + t);
+    };
+#pragma omp parallel for schedule(static) if (nb > 4096)
+    for (int64_t b = 0; b < nb; b++) {
+        const uint64_t bi = base + (uint64_t)b;
+        uint8_t *blk = out + b * bb;
+        uint8_t tmp[256];
+        for (int j = 0; j < 32; j++) {
+            const uint64_t w = oxe_rng(key, 32 * bi + (uint64_t)j);
+            memcpy(tmp + 8 * j, &w, 8);
+        }
+        memcpy(blk, tmp, bb);
+        uint16_t h0, h1;
+        switch (type) {
+            case 12: case 13:
+                h0 = f16_in(2 * bi, 0.0005f, 0.004f);
+                h1 = f16_in(2 * bi + 1, 0.0005f, 0.004f);
+                memcpy(blk, &h0, 2);
+                memcpy(blk + 2, &h1, 2);
+                break;
+            case 14:
+                h0 = f16_in(2 * bi, 0.00005f, 0.0003f);
+                memcpy(blk + 208, &h0, 2);
+                break;
+            default:
+                h0 = f16_in(2 * bi, 0.0005f, 0.004f);
+                memcpy(blk + 108, &h0, 2);
+                break;
+        }
+    }
+    return nb * bb;
 }
 
 }  // extern "C"

@@ -24,17 +24,31 @@
 
 namespace {
 
-struct Q8 {
+// A weight matrix [rows][k]: Q8_0 (codes q and fp16 block scales d), a K-quant (the file's ggml
+// blocks in raw, rows contiguous) or F32 (rows in raw as floats); type is the ggml type id.
+struct Mat {
     int64_t rows = 0, k = 0;
+    int type = 8;   // 0 F32, 8 Q8_0, 11 Q3_K, 12 Q4_K, 13 Q5_K, 14 Q6_K
     std::vector<int8_t> q;
     std::vector<uint16_t> d;
+    std::vector<uint8_t> raw;
 };
+
+int kq_block_bytes(int type) {
+    switch (type) {
+        case 11: return 110;
+        case 12: return 144;
+        case 13: return 176;
+        case 14: return 210;
+        default: return 0;
+    }
+}
 
 // set on the threads of a plan run: their work is their share, so nothing inside spawns a team
 thread_local bool tl_in_plan = false;
 
 // Generate rows [r0, r0+n) of expert e of a Q8_0 tensor [experts][rows][k] into m.
-void gen_q8(uint64_t seed, int layer, int kind, int64_t rows, int64_t k, int64_t e, Q8 &m) {
+void gen_q8(uint64_t seed, int layer, int kind, int64_t rows, int64_t k, int64_t e, Mat &m) {
     m.rows = rows;
     m.k = k;
     m.q.resize(rows * k);
@@ -52,7 +66,7 @@ void gen_q8(uint64_t seed, int layer, int kind, int64_t rows, int64_t k, int64_t
 }
 
 // rows [r0, r1) of expert e's matrix m (already sized rows x k), on the calling thread
-void gen_q8_rows(uint64_t seed, int layer, int kind, int64_t rows, int64_t k, int64_t e, int64_t r0, int64_t r1, Q8 &m) {
+void gen_q8_rows(uint64_t seed, int layer, int kind, int64_t rows, int64_t k, int64_t e, int64_t r0, int64_t r1, Mat &m) {
     const uint64_t key = oxe_tensor_key(seed, layer, kind);
     const uint64_t skey = oxe_tensor_key(seed, layer, kind + OXE_T_SCALE_OFFSET);
     const oxe_synth_param p = oxe_synth_param_of(kind);
@@ -75,17 +89,17 @@ struct Layer {
     bool att = false;
     std::vector<float> attn_norm, post_norm;
     // delta-net
-    Q8 qkv, z, beta, alpha, out;
+    Mat qkv, z, beta, alpha, out;
     std::vector<float> conv, a, dt, ssm_norm;
     // attention
-    Q8 wq, wk, wv;
+    Mat wq, wk, wv;
     std::vector<float> q_norm, k_norm;
     // MoE
     std::vector<float> router, shexp_gate;
-    Q8 gate_sh, up_sh, down_sh;
-    std::vector<std::unique_ptr<Q8[]>> experts;  // [expert] -> {gate, up, down}, lazily generated
+    Mat gate_sh, up_sh, down_sh;
+    std::vector<std::unique_ptr<Mat[]>> experts;  // [expert] -> {gate, up, down}, lazily generated
     // MTP block
-    Q8 eh_proj;
+    Mat eh_proj;
     std::vector<float> enorm, hnorm, head_norm;
     int index = 0;  // recurrent or attention index
 };
@@ -224,8 +238,32 @@ struct oxo_engine {
     int n_slots = 2, max_lanes = 8;
     std::vector<Layer> layers;  // n_layer (+1 MTP)
     std::vector<float> out_norm;
-    Q8 output;
+    Mat output;
     std::mutex gen_mu;
+    // ggml type of each matrix: [layer (OXE_GLOBAL_LAYER for the global tensors)][tensor kind];
+    // 8 (Q8_0) unless set at creation
+    std::vector<int32_t> types = std::vector<int32_t>(64 * 64, 8);
+    bool typed = false;   // some matrix is not Q8_0 (the plan mode takes Q8_0 models only)
+    int type_of(int layer, int kind) const { return types[(size_t)layer * 64 + kind]; }
+    void gen_mat(int layer, int kind, int64_t rows, int64_t k, int64_t e, Mat &m) const {
+        const int ty = type_of(layer, kind);
+        if (ty == 8) {
+            gen_q8(seed, layer, kind, rows, k, e, m);
+            m.type = 8;
+            return;
+        }
+        m.rows = rows;
+        m.k = k;
+        m.type = ty;
+        if (ty == 0) {
+            const std::vector<float> v = gen_f32(seed, layer, kind, rows * k);
+            m.raw.resize(v.size() * 4);
+            std::memcpy(m.raw.data(), v.data(), m.raw.size());
+        } else {
+            m.raw.resize((size_t)rows * (k / 256) * kq_block_bytes(ty));
+            oxo_synth_kq(seed, layer, kind, ty, e, rows, k, m.raw.data());
+        }
+    }
 
     int n_rec = 0, n_att = 0;  // n_att includes the MTP layer
     int64_t conv_len = 0, ssm_len = 0, v_stride = 0;
@@ -244,16 +282,16 @@ struct oxo_engine {
     bool keep_logits = true;
 
     double gen_seconds = 0.0;
-    const Q8 &expert(int l, int e, int which) {
+    const Mat &expert(int l, int e, int which) {
         Layer &L = layers[l];
         std::lock_guard<std::mutex> g(gen_mu);
         if (!L.experts[e]) {
             const auto t0 = std::chrono::steady_clock::now();
-            std::unique_ptr<Q8[]> m(new Q8[3]);
+            std::unique_ptr<Mat[]> m(new Mat[3]);
             const int64_t E = d.n_embd, F = d.ff_exp;
-            gen_q8(seed, l, OXE_T_GATE_EXPS, F, E, e, m[0]);
-            gen_q8(seed, l, OXE_T_UP_EXPS, F, E, e, m[1]);
-            gen_q8(seed, l, OXE_T_DOWN_EXPS, E, F, e, m[2]);
+            gen_mat(l, OXE_T_GATE_EXPS, F, E, e, m[0]);
+            gen_mat(l, OXE_T_UP_EXPS, F, E, e, m[1]);
+            gen_mat(l, OXE_T_DOWN_EXPS, E, F, e, m[2]);
             L.experts[e] = std::move(m);
             gen_seconds += std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
         }
@@ -274,9 +312,26 @@ struct oxo_engine {
         return y;
     }
 
-    // y[nl][rows] = W . quantize(x[l]) for each lane
-    static void mv(const Q8 &w, const std::vector<const float *> &xs, std::vector<float *> ys) {
+    // y[nl][rows] = W . x[l] for each lane (the reference's mv / mv_lanes, engine.rs:2270-2343): F32
+    // rows by oxe_vec_dot_f32 on x itself; K-quants by the lane GEMV on x quantised to q8_K; Q8_0 by
+    // the block chain on x quantised to Q8_0
+    static void mv(const Mat &w, const std::vector<const float *> &xs, std::vector<float *> ys) {
         const int nl = (int)xs.size();
+        if (w.type == 0) {
+            const float *rows = (const float *)w.raw.data();
+            for (int l = 0; l < nl; l++)
+                for (int64_t r = 0; r < w.rows; r++) ys[l][r] = oxo_vec_dot_f32((int)w.k, rows + r * w.k, xs[l]);
+            return;
+        }
+        if (w.type != 8) {
+            const int64_t nb = w.k / 256;
+            std::vector<uint8_t> y((size_t)nl * nb * 292);
+            for (int l = 0; l < nl; l++) oxo_quantize_row_q8_K(xs[l], y.data() + (size_t)l * nb * 292, w.k);
+            std::vector<float> s((size_t)nl * w.rows);
+            oxo_vl_gemv(w.type - 8, w.k, w.rows, nl, w.raw.data(), y.data(), s.data());
+            for (int l = 0; l < nl; l++) std::memcpy(ys[l], s.data() + (size_t)l * w.rows, w.rows * sizeof(float));
+            return;
+        }
         std::vector<int8_t> xq(nl * w.k);
         std::vector<uint16_t> xd(nl * w.k / 32);
         for (int l = 0; l < nl; l++) oxo_quantize_row_q8_0(xs[l], w.k, xq.data() + l * w.k, xd.data() + l * w.k / 32);
@@ -302,38 +357,38 @@ struct oxo_engine {
             L.attn_norm = gen_f32(seed, il, OXE_T_ATTN_NORM, E);
             L.post_norm = gen_f32(seed, il, OXE_T_POST_NORM, E);
             if (!L.att) {
-                gen_q8(seed, il, OXE_T_DN_QKV, nch, E, 0, L.qkv);
-                gen_q8(seed, il, OXE_T_DN_Z, d.ssm_d_inner, E, 0, L.z);
-                gen_q8(seed, il, OXE_T_DN_BETA, nv, E, 0, L.beta);
-                gen_q8(seed, il, OXE_T_DN_ALPHA, nv, E, 0, L.alpha);
-                gen_q8(seed, il, OXE_T_DN_OUT, E, d.ssm_d_inner, 0, L.out);
+                gen_mat(il, OXE_T_DN_QKV, nch, E, 0, L.qkv);
+                gen_mat(il, OXE_T_DN_Z, d.ssm_d_inner, E, 0, L.z);
+                gen_mat(il, OXE_T_DN_BETA, nv, E, 0, L.beta);
+                gen_mat(il, OXE_T_DN_ALPHA, nv, E, 0, L.alpha);
+                gen_mat(il, OXE_T_DN_OUT, E, d.ssm_d_inner, 0, L.out);
                 L.conv = gen_f32(seed, il, OXE_T_DN_CONV, nch * d.ssm_conv_kernel);
                 L.a = gen_f32(seed, il, OXE_T_DN_A, nv);
                 L.dt = gen_f32(seed, il, OXE_T_DN_DT, nv);
                 L.ssm_norm = gen_f32(seed, il, OXE_T_DN_NORM, hv);
             } else {
-                gen_q8(seed, il, OXE_T_ATT_Q, d.n_head * 2 * hd, E, 0, L.wq);
-                gen_q8(seed, il, OXE_T_ATT_K, d.n_head_kv * hd, E, 0, L.wk);
-                gen_q8(seed, il, OXE_T_ATT_V, d.n_head_kv * hd, E, 0, L.wv);
-                gen_q8(seed, il, OXE_T_ATT_OUT, E, d.n_head * hd, 0, L.out);
+                gen_mat(il, OXE_T_ATT_Q, d.n_head * 2 * hd, E, 0, L.wq);
+                gen_mat(il, OXE_T_ATT_K, d.n_head_kv * hd, E, 0, L.wk);
+                gen_mat(il, OXE_T_ATT_V, d.n_head_kv * hd, E, 0, L.wv);
+                gen_mat(il, OXE_T_ATT_OUT, E, d.n_head * hd, 0, L.out);
                 L.q_norm = gen_f32(seed, il, OXE_T_ATT_QNORM, hd);
                 L.k_norm = gen_f32(seed, il, OXE_T_ATT_KNORM, hd);
             }
             L.router = gen_f32(seed, il, OXE_T_ROUTER, (int64_t)d.n_expert * E);
             L.shexp_gate = gen_f32(seed, il, OXE_T_SHEXP_GATE, E);
-            gen_q8(seed, il, OXE_T_GATE_SHEXP, d.ff_shexp, E, 0, L.gate_sh);
-            gen_q8(seed, il, OXE_T_UP_SHEXP, d.ff_shexp, E, 0, L.up_sh);
-            gen_q8(seed, il, OXE_T_DOWN_SHEXP, E, d.ff_shexp, 0, L.down_sh);
+            gen_mat(il, OXE_T_GATE_SHEXP, d.ff_shexp, E, 0, L.gate_sh);
+            gen_mat(il, OXE_T_UP_SHEXP, d.ff_shexp, E, 0, L.up_sh);
+            gen_mat(il, OXE_T_DOWN_SHEXP, E, d.ff_shexp, 0, L.down_sh);
             L.experts.resize(d.n_expert);
             if (mtp) {
-                gen_q8(seed, il, OXE_T_EH_PROJ, E, 2 * E, 0, L.eh_proj);
+                gen_mat(il, OXE_T_EH_PROJ, E, 2 * E, 0, L.eh_proj);
                 L.enorm = gen_f32(seed, il, OXE_T_ENORM, E);
                 L.hnorm = gen_f32(seed, il, OXE_T_HNORM, E);
                 L.head_norm = gen_f32(seed, il, OXE_T_HEAD_NORM, E);
             }
         }
         out_norm = gen_f32(seed, OXE_GLOBAL_LAYER, OXE_T_OUT_NORM, E);
-        gen_q8(seed, OXE_GLOBAL_LAYER, OXE_T_OUTPUT, d.n_vocab, E, 0, output);
+        gen_mat(OXE_GLOBAL_LAYER, OXE_T_OUTPUT, d.n_vocab, E, 0, output);
         conv_len = (d.ssm_conv_kernel - 1) * nch;
         ssm_len = nv * hv * hv;
         conv_state.assign((size_t)n_slots * n_rec * conv_len, 0.0f);
@@ -526,7 +581,7 @@ struct oxo_engine {
             // experts
             std::vector<std::vector<float>> dn(K, std::vector<float>(E));
             for (int64_t j = 0; j < K; j++) {
-                const Q8 &wg = expert(l, ids[j], 0), &wu = expert(l, ids[j], 1), &wdn = expert(l, ids[j], 2);
+                const Mat &wg = expert(l, ids[j], 0), &wu = expert(l, ids[j], 1), &wdn = expert(l, ids[j], 2);
                 std::vector<float> g(F), u(F), h(F);
                 mv(wg, {xn.data()}, {g.data()});
                 mv(wu, {xn.data()}, {u.data()});
@@ -600,6 +655,7 @@ struct oxo_engine {
         pool.reset();
         pts.clear();
         if (nthreads <= 0) return 0;
+        if (typed) return -1;
         pool.reset(new PlanPool());
         if (!pool->start(nthreads)) {
             pool.reset();
@@ -633,7 +689,7 @@ struct oxo_engine {
     }
 
     // thread `tid`'s rows of w for its lanes: y[ln] + 0 .. (r1 - r0)
-    static void rows_of(const Q8 &w, int64_t r0, int64_t r1, int nl, std::vector<std::vector<int8_t>> &xq,
+    static void rows_of(const Mat &w, int64_t r0, int64_t r1, int nl, std::vector<std::vector<int8_t>> &xq,
                         std::vector<std::vector<uint16_t>> &xd, const std::function<float *(int)> &y) {
         if (r1 <= r0) return;
         const int8_t *q[8];
@@ -836,7 +892,7 @@ struct oxo_engine {
         pool->barrier(tid, false);
         if (tid == 0)
             for (uint32_t e : miss) {
-                std::unique_ptr<Q8[]> m(new Q8[3]);
+                std::unique_ptr<Mat[]> m(new Mat[3]);
                 const int64_t E = d.n_embd, F = d.ff_exp;
                 const int64_t rk[3][2] = {{F, E}, {F, E}, {E, F}};
                 for (int w = 0; w < 3; w++) {
@@ -851,7 +907,7 @@ struct oxo_engine {
         const int kinds[3] = {OXE_T_GATE_EXPS, OXE_T_UP_EXPS, OXE_T_DOWN_EXPS};
         for (uint32_t e : miss)
             for (int w = 0; w < 3; w++) {
-                Q8 &m = L.experts[e][w];
+                Mat &m = L.experts[e][w];
                 int64_t r0, r1;
                 split(m.rows, nt, tid, r0, r1);
                 gen_q8_rows(seed, l, kinds[w], m.rows, m.k, e, r0, r1, m);
@@ -885,7 +941,7 @@ struct oxo_engine {
         for (int64_t uu = u0; uu < u1; uu++) {
             const uint32_t e = ts.uni_u[uu].first;
             const int64_t b = ts.uni_u[uu].second;
-            const Q8 &wg = expert(l, (int)e, 0), &wu = expert(l, (int)e, 1);
+            const Mat &wg = expert(l, (int)e, 0), &wu = expert(l, (int)e, 1);
             for (int ln = 0; ln < nl; ln++) {
                 int64_t j = -1;
                 for (int64_t i = 0; i < K; i++)
@@ -918,7 +974,7 @@ struct oxo_engine {
         for (int ln = 0; ln < nl; ln++) {
             float *dt = ts.dtmp[ln].data();
             for (int64_t j = 0; j < K; j++) {
-                const Q8 &wdn = expert(l, ts.ids[ln][j], 2);
+                const Mat &wdn = expert(l, ts.ids[ln][j], 2);
                 const int8_t *q[1] = {p_hq[ln].data() + j * F};
                 const uint16_t *dd[1] = {p_hd[ln].data() + j * F / 32};
                 float *y[1] = {dt + j * nr};
@@ -1292,6 +1348,31 @@ oxo_engine *oxo_engine_new_lanes(const oxe_model_desc *d, uint64_t seed, int64_t
     e->init(*d, seed, n_ctx);
     return e;
 }
+// with each matrix's ggml type from types[layer * 64 + kind] (layer OXE_GLOBAL_LAYER: the global
+// tensors): Q8_0 (8) anywhere; K-quants (11..14) for the expert, shared-expert and output matrices;
+// F32 (0) for ssm_beta / ssm_alpha. Null for another combination.
+oxo_engine *oxo_engine_new_typed(const oxe_model_desc *d, uint64_t seed, int64_t n_ctx, int n_slots, const int32_t *types) {
+    if (n_slots < 1 || n_slots > 8 || !types) return nullptr;
+    oxo_engine *e = new oxo_engine();
+    e->n_slots = n_slots;
+    for (int l = 0; l < 64; l++)
+        for (int k = 0; k < 64; k++) {
+            const int32_t t = types[l * 64 + k];
+            if (!oxe_kind_is_q8(k)) continue;
+            const bool kq = t >= 11 && t <= 14, ok = t == 8 ||
+                (kq && (k == OXE_T_GATE_EXPS || k == OXE_T_UP_EXPS || k == OXE_T_DOWN_EXPS || k == OXE_T_GATE_SHEXP ||
+                        k == OXE_T_UP_SHEXP || k == OXE_T_DOWN_SHEXP || k == OXE_T_OUTPUT)) ||
+                (t == 0 && (k == OXE_T_DN_BETA || k == OXE_T_DN_ALPHA));
+            if (!ok) {
+                delete e;
+                return nullptr;
+            }
+            e->types[(size_t)l * 64 + k] = t;
+            e->typed |= t != 8;
+        }
+    e->init(*d, seed, n_ctx);
+    return e;
+}
 void oxo_engine_free(oxo_engine *e) { delete e; }
 void oxo_engine_reset(oxo_engine *e) { e->reset(); }
 int oxo_verify(oxo_engine *e, const uint32_t *toks, int n, uint32_t *out) { return e->verify(toks, n, out); }
@@ -1452,7 +1533,7 @@ int oxo_driver_rewind(oxo_driver *dr, int m) { return dr->rewind(m); }
 extern "C" {
 // Synthetic tensors of include/oxe_model.h on the host (inputs for parity tests).
 void oxo_synth_q8(uint64_t seed, int layer, int kind, int64_t expert, int64_t rows, int64_t k, int8_t *q, uint16_t *d) {
-    Q8 m;
+    Mat m;
     gen_q8(seed, layer, kind, rows, k, expert, m);
     std::memcpy(q, m.q.data(), m.q.size());
     std::memcpy(d, m.d.data(), m.d.size() * 2);

@@ -97,6 +97,7 @@ def lib():
             "oxo_engine_new": (C.c_void_p, [P(ModelDesc), C.c_uint64, C.c_int64]),
             "oxo_engine_free": (None, [C.c_void_p]),
             "oxo_engine_new_lanes": (C.c_void_p, [P(ModelDesc), C.c_uint64, C.c_int64, C.c_int]),
+            "oxo_engine_new_typed": (C.c_void_p, [P(ModelDesc), C.c_uint64, C.c_int64, C.c_int, i32p]),
             "oxo_engine_reset": (None, [C.c_void_p]),
             "oxo_verify": (C.c_int, [C.c_void_p, u32p, C.c_int, u32p]),
             "oxo_commit": (C.c_int, [C.c_void_p, C.c_int]),
@@ -126,6 +127,8 @@ def lib():
             "oxo_mtp_entry": (None, [C.c_void_p, u32p, C.c_int, f32p, f32p]),
             "oxo_engine_set_router": (None, [C.c_void_p, C.c_int, C.c_int, C.c_int, f32p]),
             "oxo_synth_q8": (None, [C.c_uint64, C.c_int, C.c_int, C.c_int64, C.c_int64, C.c_int64, i8p, u16p]),
+            "oxo_synth_kq": (C.c_int64, [C.c_uint64, C.c_int, C.c_int, C.c_int, C.c_int64, C.c_int64, C.c_int64,
+                                         C.POINTER(C.c_uint8)]),
             "oxo_synth_f32": (None, [C.c_uint64, C.c_int, C.c_int, C.c_int64, f32p]),
             "oxo_synth_normal": (None, [C.c_uint64, C.c_uint64, C.c_int64, C.c_float, C.c_float, f32p]),
             "oxo_driver_new": (C.c_void_p, [C.c_void_p, C.c_int]),
@@ -213,6 +216,17 @@ def synth_q8(seed, layer, kind, rows, k, expert=0):
     return q, d
 
 
+KQ_BLOCK = {11: 110, 12: 144, 13: 176, 14: 210}   # ggml type id -> bytes per 256 weights
+
+
+def synth_kq(seed, layer, kind, ty, rows, k, expert=0):
+    """synthetic K-quant tensor (ggml type 11..14): rows x k/256 blocks as uint8 [rows][row bytes]"""
+    out = np.empty((rows, k // 256 * KQ_BLOCK[ty]), np.uint8)
+    n = lib().oxo_synth_kq(seed, layer, kind, ty, expert, rows, k, ptr(out, C.c_uint8))
+    assert n == out.size
+    return out
+
+
 def synth_f32(seed, layer, kind, n):
     v = np.empty(n, np.float32)
     lib().oxo_synth_f32(seed, layer, kind, n, ptr(v, C.c_float))
@@ -245,10 +259,20 @@ def config1_inputs(seed=0):
 class Engine:
     """Oracle engine (engine.rs semantics) on the synthetic model."""
 
-    def __init__(self, desc, seed=0, n_ctx=1024, lanes=2):
+    def __init__(self, desc, seed=0, n_ctx=1024, lanes=2, types=None):
+        """types: {(layer, kind): ggml type id} for matrices that are not Q8_0 (layer GLOBAL_LAYER
+        for the LM head)"""
         self.desc = desc
-        self.h = (lib().oxo_engine_new(C.byref(desc), seed, n_ctx) if lanes == 2 else
-                  lib().oxo_engine_new_lanes(C.byref(desc), seed, n_ctx, lanes))
+        if types:
+            tt = np.full(64 * 64, 8, np.int32)
+            for (layer, kind), ty in types.items():
+                tt[layer * 64 + kind] = ty
+            self.h = lib().oxo_engine_new_typed(C.byref(desc), seed, n_ctx, lanes, ptr(tt, C.c_int32))
+            if not self.h:
+                raise ValueError("a matrix type this model cannot take there")
+        else:
+            self.h = (lib().oxo_engine_new(C.byref(desc), seed, n_ctx) if lanes == 2 else
+                      lib().oxo_engine_new_lanes(C.byref(desc), seed, n_ctx, lanes))
         self.n_ctx = lib().oxo_n_ctx(self.h)
 
     def close(self):

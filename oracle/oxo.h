@@ -43,6 +43,9 @@ void oxo_gemv_q8_0(int64_t k, int64_t nr, int nl, const int8_t *wq, const uint16
 // s[l*nr + r] = W[r] . y[l]; type 3 Q3_K, 4 Q4_K, 5 Q5_K, 6 Q6_K; returns 0 for another type.
 void oxo_quantize_row_q8_K(const float *x, void *y, int64_t k);
 int  oxo_vl_gemv(int type, int64_t k, int64_t nr, int nl, const void *w, const void *y, float *s);
+// synthetic K-quant tensor bytes (ggml type 11..14, rows x k/256 blocks of expert `expert`) for the
+// tests' model files; returns the bytes written or 0
+int64_t oxo_synth_kq(uint64_t seed, int layer, int kind, int type, int64_t expert, int64_t rows, int64_t k, uint8_t *out);
 
 // ---- f32 / f16 vector helpers (vendor/ggml-subset/generated/upstream/src/ggml-cpu/vec.{h,cpp})
 float oxo_vec_dot_f32(int n, const float *x, const float *y);            // vec.cpp:104-125

@@ -12,6 +12,9 @@ typedef struct oxo_driver oxo_driver;
 oxo_engine *oxo_engine_new(const oxe_model_desc *d, uint64_t seed, int64_t n_ctx);
 // with n_slots recurrent slots (verify lanes; 2 by default, 4 for MTP depth 3)
 oxo_engine *oxo_engine_new_lanes(const oxe_model_desc *d, uint64_t seed, int64_t n_ctx, int n_slots);
+// with per-matrix ggml types types[layer * 64 + kind] (K-quant experts, shared experts and LM head;
+// F32 ssm_beta / ssm_alpha; Q8_0 elsewhere); null for a type this model cannot take there
+oxo_engine *oxo_engine_new_typed(const oxe_model_desc *d, uint64_t seed, int64_t n_ctx, int n_slots, const int32_t *types);
 void oxo_engine_free(oxo_engine *e);
 void oxo_engine_reset(oxo_engine *e);
 int oxo_verify(oxo_engine *e, const uint32_t *toks, int n, uint32_t *out);      // engine.rs:2002-2025

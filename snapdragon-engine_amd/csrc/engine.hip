@@ -14,7 +14,11 @@ extern "C" {
 
 const char *oxe_last_error(void) { return oxe::g_last_error.c_str(); }
 
-static int engine_create(const oxe_model_desc *desc, uint64_t seed, int n_ctx, bool caller, void *stream, oxe_engine **out) {
+}  // extern "C"
+
+namespace oxe {
+int create_engine(const oxe_model_desc *desc, uint64_t seed, int n_ctx, bool caller, void *stream, const ModelTypes *mt,
+                  oxe_engine **out) {
     // the attention kernel keeps a kv group's f16 probabilities in LDS: contexts up to 6144
     if (!desc || !out || n_ctx < 1 || n_ctx > 6144) {
         oxe::set_err("n_ctx must be in [1, 6144]");
@@ -26,7 +30,7 @@ static int engine_create(const oxe_model_desc *desc, uint64_t seed, int n_ctx, b
     }
     Engine *e = new Engine();
     try {
-        e->create(*desc, seed, n_ctx, caller, (hipStream_t)stream);
+        e->create(*desc, seed, n_ctx, caller, (hipStream_t)stream, mt);
     } catch (const std::exception &ex) {
         oxe::set_err(ex.what());
         delete e;
@@ -35,13 +39,16 @@ static int engine_create(const oxe_model_desc *desc, uint64_t seed, int n_ctx, b
     *out = (oxe_engine *)e;
     return 0;
 }
+}  // namespace oxe
+
+extern "C" {
 
 int oxe_engine_create(const oxe_model_desc *desc, uint64_t seed, int n_ctx, oxe_engine **out) {
-    return engine_create(desc, seed, n_ctx, false, nullptr, out);
+    return oxe::create_engine(desc, seed, n_ctx, false, nullptr, nullptr, out);
 }
 
 int oxe_engine_create_on(const oxe_model_desc *desc, uint64_t seed, int n_ctx, void *stream, oxe_engine **out) {
-    return engine_create(desc, seed, n_ctx, true, stream, out);
+    return oxe::create_engine(desc, seed, n_ctx, true, stream, nullptr, out);
 }
 
 void oxe_engine_destroy(oxe_engine *e) { delete (Engine *)e; }
@@ -279,7 +286,8 @@ int oxe_engine_read_state(oxe_engine *e, const void *host, int64_t nbytes, int n
 extern "C" int oxe_engine_set_fused(oxe_engine *e, int on) {
     Engine *g = (Engine *)e;
     if (g->set_fused(on != 0)) {
-        oxe::set_err("the fused run kernel is not available on this device");
+        oxe::set_err(g->kq ? "the fused run kernel reads Q8_0 matrices only: this engine's K-quant / F32 matrices run per phase"
+                           : "the fused run kernel is not available on this device");
         return -1;
     }
     return 0;

@@ -9,6 +9,8 @@
 #include <algorithm>
 
 #include "oxe_common.h"
+#include "oxe_model_kernels.h"
+#include "oxe_prologue.h"
 
 #include <mutex>
 
@@ -472,7 +474,438 @@ int vl_gemv_type(const uint8_t *w, int nb, int64_t nr, const uint8_t *y, int nl,
     }
 }
 
+
+// ==== K-quant and F32 matrices in the engine's per-phase runs ======================================
+// (the reference's mv / mv_lanes over any qtype, crates/model/src/engine.rs:2270-2343; MoE phases
+// engine.rs:3437-3625; LM head 3630-3715). Every (lane, row) value is the lane GEMV's: the same
+// block units and float chain as vl_gemv_kernel, on the activation quantised as the weight's type
+// asks (q8_K for K-quants, Q8_0 for Q8_0, the f32 vector itself for F32 rows).
+
+// ggml type id (11..14) -> the units / chain of that type
+template <int NL>
+OXE_DEV void unit_rt(int type, const uint8_t *wb, YView y, int h, int *out) {
+    switch (type) {
+        case 11: unit<3, NL>(wb, y, h, out); break;
+        case 12: unit<4, NL>(wb, y, h, out); break;
+        case 13: unit<5, NL>(wb, y, h, out); break;
+        default: unit<6, NL>(wb, y, h, out); break;
+    }
+}
+OXE_DEV float chain_rt(int type, float acc, const uint8_t *wb, float dx, const int *r0, const int *r1) {
+    switch (type) {
+        case 11: return chain<3>(acc, wb, dx, r0, r1);
+        case 12: return chain<4>(acc, wb, dx, r0, r1);
+        case 13: return chain<5>(acc, wb, dx, r0, r1);
+        default: return chain<6>(acc, wb, dx, r0, r1);
+    }
+}
+OXE_DEV int res_of(int type) { return type == 12 ? BT<4>::R : type == 13 ? BT<5>::R : 1; }
+constexpr int RES_MAX = 6;
+
+// nblk q8_K blocks (292 bytes each, from y) into LDS as halves (YH words apart) and scales
+OXE_DEV void stage_q8k(const uint8_t *y, int nblk, uint32_t *yh, float *yd) {
+    for (int i = threadIdx.x; i < nblk * 2 * 36; i += blockDim.x) {
+        const int wd = i % 36, hb = i / 36, h = hb & 1;
+        const uint32_t *src = (const uint32_t *)(y + (int64_t)(hb >> 1) * Q8K_BYTES);
+        yh[hb * YH + wd] = wd < 32 ? src[1 + 32 * h + wd] : src[65 + 4 * h + (wd - 32)];
+    }
+    for (int i = threadIdx.x; i < nblk; i += blockDim.x) yd[i] = *(const float *)(y + (int64_t)i * Q8K_BYTES);
+}
+
+OXE_DEV uint32_t ordered_bits(float f) {
+    const uint32_t u = __builtin_bit_cast(uint32_t, f);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+// ---- F32 ssm_beta / ssm_alpha rows: x -> rms_norm * attn_norm (every workgroup, exact), then
+// oxe_vec_dot_f32 per (row, lane) in ggml_vec_dot_f32's order (vec.cpp:104-125): lane c of a
+// 16-lane group runs chain c over elements c + 16 s; xor 8, 4, 1, 2 is the NEON reduction tree.
+// Workgroup b: rows 16 b .. 16 b + 15 of [beta rows | alpha rows]; outputs into the projection
+// buffer at DN_BETA / DN_ALPHA, where the delta-net phase reads them.
+template <int NL>
+__global__ __launch_bounds__(256) void ba_f32_kernel(const RunCtl *__restrict__ ctl, const float *x, const float *norm_w,
+                                                     float eps, const float *beta, const float *alpha, float *proj) {
+    __shared__ float s_xn[NL][shp::E];
+    __shared__ NormScratch ns;
+    if (!ctl->active) return;
+    const int nl = ctl->nl, t = threadIdx.x;
+#pragma unroll
+    for (int l = 0; l < NL; l++) {
+        float v[EPT];
+        if (l < nl) {
+            load8(x + (int64_t)l * shp::E, v);
+            rms_norm_mul_e(v, x + (int64_t)l * shp::E, norm_w, eps, ns);
+        } else {
+#pragma unroll
+            for (int i = 0; i < EPT; i++) v[i] = 0.0f;
+        }
+        store8(s_xn[l], v);
+    }
+    __syncthreads();
+    const int c = t & 15, row = blockIdx.x * 16 + (t >> 4);
+    const bool is_beta = row < shp::NVH;
+    const float *w = (is_beta ? beta + (int64_t)row * shp::E : alpha + (int64_t)(row - shp::NVH) * shp::E);
+    float acc[NL];
+#pragma unroll
+    for (int l = 0; l < NL; l++) acc[l] = 0.0f;
+#pragma unroll 8
+    for (int s = 0; s < shp::E / 16; s++) {
+        const float wv = w[c + 16 * s];
+#pragma unroll
+        for (int l = 0; l < NL; l++) acc[l] = __builtin_fmaf(wv, s_xn[l][c + 16 * s], acc[l]);
+    }
+#pragma unroll
+    for (int l = 0; l < NL; l++) {
+        float v = acc[l];
+        v = v + shfl_xor_f(v, 8);
+        v = v + shfl_xor_f(v, 4);
+        v = v + shfl_xor_f(v, 1);
+        v = v + shfl_xor_f(v, 2);
+        if (c == 0 && l < nl) proj[(int64_t)l * shp::DN_ROWS + (is_beta ? shp::DN_BETA + row : shp::DN_ALPHA + row - shp::NVH)] = v;
+    }
+}
+
+// ---- MoE gate / up over K-quant matrices: workgroup (unit u, tile of 16 rows), u < OXE_MAX_UNION
+// the union's expert u, u = OXE_MAX_UNION the shared expert. Thread (row t / 16, half block t % 16)
+// forms its half block's integers for every lane; threads t % 16 < NL then run lane t % 16's chain
+// over the row's 8 blocks; gate first, then up, then silu(g) * u (ggml_v_silu, as swiglu) for
+// every lane that routed to the expert (the shared expert: every lane).
+struct KqGuArgs {
+    const uint8_t *xk;          // [NL][E / 256] q8_K blocks of xn
+    RawW gate, up, sh_gate, sh_up;
+    const int32_t *uni, *route_ids;
+    float *hexp;                // [NL][KUSED][FF]
+    float *hsh;                 // [NL][FFSH]
+    int do_exp, do_sh;
+};
+constexpr int GU_NB = shp::E / QK;   // 8 blocks per row
+static_assert(GU_NB * 2 == 16 && shp::FF == shp::FFSH, "16 half blocks per row; one tiling for both");
+
+template <int NL>
+__global__ __launch_bounds__(256) void kq_gu_kernel(const RunCtl *__restrict__ ctl, KqGuArgs a) {
+    constexpr int RS = (NL * RES_MAX) | 1;
+    __shared__ uint32_t yh[NL * GU_NB * 2 * YH];
+    __shared__ float yd[NL * GU_NB];
+    __shared__ int res[256 * RS];
+    if (!ctl->active) return;
+    const int nl = ctl->nl, t = threadIdx.x, ri = t >> 4, hu = t & 15;
+    const int u = blockIdx.x / (shp::FF / 16), tile = blockIdx.x % (shp::FF / 16);
+    const bool sh = u == OXE_MAX_UNION;
+    if (sh ? !a.do_sh : !a.do_exp) return;
+    int e = 0;
+    if (!sh) {
+        int nu = a.uni[0];
+        nu = nu < 0 ? 0 : (nu > OXE_MAX_UNION ? OXE_MAX_UNION : nu);
+        if (u >= nu) return;
+        e = a.uni[1 + u];
+        e = e < 0 ? 0 : (e >= shp::NEXP ? shp::NEXP - 1 : e);
+    }
+    stage_q8k(a.xk, NL * GU_NB, yh, yd);
+    __syncthreads();
+    const int row = tile * 16 + ri;
+    float g = 0.0f, v = 0.0f;
+    for (int which = 0; which < 2; which++) {
+        const RawW &W = sh ? (which ? a.sh_up : a.sh_gate) : (which ? a.up : a.gate);
+        const int type = W.type, rs = res_of(type);
+        const int64_t rb = raw_row_bytes(W);
+        const uint8_t *wr = W.w + ((int64_t)e * W.rows + row) * rb;
+        unit_rt<NL>(type, wr + (hu >> 1) * kq_block_bytes(type), YView{yh + (2 * (hu >> 1) + (hu & 1)) * YH, GU_NB * 2 * YH},
+                    hu & 1, res + t * RS);
+        __syncthreads();
+        if (hu < NL) {
+            float acc = 0.0f;
+            for (int b = 0; b < GU_NB; b++) {
+                const int *r0 = res + (ri * 16 + 2 * b) * RS + hu * rs, *r1 = res + (ri * 16 + 2 * b + 1) * RS + hu * rs;
+                acc = chain_rt(type, acc, wr + b * kq_block_bytes(type), yd[hu * GU_NB + b], r0, r1);
+            }
+            if (which) v = acc;
+            else g = acc;
+        }
+        __syncthreads();
+    }
+    if (hu < NL && hu < nl) {
+        const float h = v_silu(g) * v;
+        if (sh) {
+            a.hsh[(int64_t)hu * shp::FFSH + row] = h;
+        } else {
+            int j = -1;
+            for (int jj = 0; jj < shp::KUSED; jj++)
+                if (a.route_ids[hu * shp::KUSED + jj] == e) j = jj;
+            if (j >= 0) a.hexp[((int64_t)hu * shp::KUSED + j) * shp::FF + row] = h;
+        }
+    }
+}
+
+// ---- MoE down + combine with any mix of K-quant and Q8_0 down matrices: workgroup = 16 output
+// rows; units 0..nu-1 the union's experts, unit OXE_MAX_UNION the shared expert. Each (unit, lane,
+// row) value is that matrix's row dot with the lane's h (slot j of the lane's top-k, or the shared
+// h): K-quants on h's q8_K blocks (2 per row of 512), four units per pass with 64 threads each
+// (row, half block); Q8_0 on h quantised to Q8_0 in LDS, one thread per (unit, lane, row) running
+// the block chain. Then the reference's combine (engine.rs:3591-3601):
+// m = d0 w0; m += dj wj; f = m + dsh * g; x2 = f + x1.
+struct KqDownArgs {
+    const int32_t *uni, *route_ids;
+    const float *route_w, *sh_gate;
+    const float *hexp, *hsh;        // f32 h (Q8_0 matrices quantise it here)
+    const uint8_t *hk, *hshk;       // q8_K blocks of h (K-quant matrices)
+    Q8W exp_down, shexp_down;
+    RawW exp_down_r, sh_down_r;
+    const float *x1;
+    float *x2;
+    unsigned long long *amax_key;
+};
+constexpr int DN_R = 16;                     // output rows per workgroup
+constexpr int DN_NB = shp::FF / QK;          // 2 blocks per down row
+constexpr int DN_U = OXE_MAX_UNION + 1;
+constexpr int DN_A = shp::KUSED + 1;         // activation rows per lane: the k slots, then the shared h
+
+template <int NL>
+__global__ __launch_bounds__(256) void kq_down_kernel(const RunCtl *__restrict__ ctl, KqDownArgs a) {
+    constexpr int RS = (NL * RES_MAX) | 1;   // odd per-thread stride of the unit integers
+    __shared__ uint32_t yh[NL * DN_A * DN_NB * 2 * YH];
+    __shared__ float yd[NL * DN_A * DN_NB];
+    __shared__ int8_t s_q[NL * DN_A][shp::FF];
+    __shared__ uint16_t s_d[NL * DN_A][shp::FF / 32];
+    __shared__ int res[256 * RS];
+    __shared__ float s_dn[NL][DN_A][DN_R];
+    __shared__ int32_t s_e[DN_U], s_slot[DN_U][NL];
+    __shared__ float s_w[NL][shp::KUSED], s_sg[NL];
+    if (!ctl->active) return;
+    const int nl = ctl->nl, t = threadIdx.x;
+    const int64_t row0 = (int64_t)blockIdx.x * DN_R;
+    if (blockIdx.x == 0 && t < NL) a.amax_key[t] = 0ull;   // the LM head that follows starts clean
+    int nu = a.uni[0];
+    nu = nu < 0 ? 0 : (nu > OXE_MAX_UNION ? OXE_MAX_UNION : nu);
+    const bool exp_kq = a.exp_down_r.type != 8, sh_kq = a.sh_down_r.type != 8;
+    if (t < DN_U) {
+        const int e = t < OXE_MAX_UNION ? (t < nu ? a.uni[1 + t] : -1) : 0;
+        s_e[t] = e < 0 ? 0 : (e < shp::NEXP ? e : shp::NEXP - 1);   // slots below compare the unclamped id
+        for (int l = 0; l < NL; l++) {
+            int j = -1;
+            if (l < nl) {
+                if (t == OXE_MAX_UNION) j = shp::KUSED;
+                else if (e >= 0)
+                    for (int jj = 0; jj < shp::KUSED; jj++)
+                        if (a.route_ids[l * shp::KUSED + jj] == e) j = jj;
+            }
+            s_slot[t][l] = j;
+        }
+    }
+    if (t < NL * shp::KUSED) s_w[t / shp::KUSED][t % shp::KUSED] = t / shp::KUSED < nl ? a.route_w[t] : 0.0f;
+    if (t < NL) s_sg[t] = t < nl ? a.sh_gate[t] : 0.0f;
+    // activations: activation row ar = l * DN_A + j (j = KUSED: the shared h)
+    if (exp_kq || sh_kq) {
+        for (int l = 0; l < NL; l++) {
+            if (exp_kq) stage_q8k(a.hk + (int64_t)l * shp::KUSED * DN_NB * Q8K_BYTES, shp::KUSED * DN_NB,
+                                  yh + l * DN_A * DN_NB * 2 * YH, yd + l * DN_A * DN_NB);
+            if (sh_kq) stage_q8k(a.hshk + (int64_t)l * DN_NB * Q8K_BYTES, DN_NB, yh + (l * DN_A + shp::KUSED) * DN_NB * 2 * YH,
+                                 yd + (l * DN_A + shp::KUSED) * DN_NB);
+        }
+    }
+    if (!exp_kq || !sh_kq) {
+        for (int i = t; i < NL * DN_A * (shp::FF / 32); i += 256) {
+            const int ar = i / (shp::FF / 32), b = i % (shp::FF / 32), l = ar / DN_A, j = ar % DN_A;
+            const bool want = j < shp::KUSED ? !exp_kq : !sh_kq;
+            if (want && l < nl) {
+                const float *src = j < shp::KUSED ? a.hexp + ((int64_t)l * shp::KUSED + j) * shp::FF + 32 * b
+                                                  : a.hsh + (int64_t)l * shp::FFSH + 32 * b;
+                quant_block_q8_0(src, &s_q[ar][32 * b], &s_d[ar][b]);
+            }
+        }
+    }
+    __syncthreads();
+    // K-quant units, four per pass: thread (unit u0 + t / 64, row t / 4 % 16, half block t % 4) forms
+    // its half block's integers for every lane with a slot there; threads t % 4 < NL then run lane
+    // t % 4's chain over the row's two blocks
+    {
+        const int p = t >> 6, rr = (t >> 2) & 15, hu = t & 3;
+        for (int u0 = 0; u0 < DN_U; u0 += 4) {
+            const int u = u0 + p;
+            const bool live = u < DN_U && (u == OXE_MAX_UNION ? sh_kq : (exp_kq && u < nu));
+            const RawW &W = u == OXE_MAX_UNION ? a.sh_down_r : a.exp_down_r;
+            const int type = W.type, rs = res_of(type), bb = kq_block_bytes(type);
+            const uint8_t *wr = live ? W.w + ((int64_t)s_e[u] * W.rows + row0 + rr) * raw_row_bytes(W) : nullptr;
+            if (live)
+                for (int l = 0; l < NL; l++) {
+                    const int j = s_slot[u][l];
+                    if (j >= 0)
+                        unit_rt<1>(type, wr + (hu >> 1) * bb, YView{yh + ((l * DN_A + j) * DN_NB * 2 + hu) * YH, 0}, hu & 1,
+                                   res + t * RS + l * rs);
+                }
+            __syncthreads();
+            if (live && hu < NL && s_slot[u][hu] >= 0) {
+                const int ar = hu * DN_A + s_slot[u][hu];
+                float acc = 0.0f;
+                for (int b = 0; b < DN_NB; b++) {
+                    const int *r0 = res + ((t & ~3) + 2 * b) * RS + hu * rs, *r1 = res + ((t & ~3) + 2 * b + 1) * RS + hu * rs;
+                    acc = chain_rt(type, acc, wr + b * bb, yd[ar * DN_NB + b], r0, r1);
+                }
+                s_dn[hu][s_slot[u][hu]][rr] = acc;
+            }
+            __syncthreads();
+        }
+    }
+    // Q8_0 units: one thread per (unit, lane, row), the block chain of the Q8_0 GEMV
+    for (int i = t; i < DN_U * NL * DN_R; i += 256) {
+        const int u = i / (NL * DN_R), l = (i / DN_R) % NL, rr = i % DN_R;
+        const bool sh = u == OXE_MAX_UNION;
+        if (sh ? sh_kq : (exp_kq || u >= nu)) continue;
+        const int j = s_slot[u][l];
+        if (j < 0) continue;
+        const int64_t row = row0 + rr;
+        const int8_t *wq = sh ? a.shexp_down.q + row * shp::FFSH : a.exp_down.q + ((int64_t)s_e[u] * shp::E + row) * shp::FF;
+        const uint16_t *wd = sh ? a.shexp_down.d + row * (shp::FFSH / 32)
+                                : a.exp_down.d + ((int64_t)s_e[u] * shp::E + row) * (shp::FF / 32);
+        const int ar = l * DN_A + j;
+        float acc = 0.0f;
+        for (int b = 0; b < shp::FF / 32; b++) {
+            int32_t s = 0;
+#pragma unroll
+            for (int k = 0; k < 8; k++)
+                s = dot4(*(const uint32_t *)(wq + 32 * b + 4 * k), *(const uint32_t *)&s_q[ar][32 * b + 4 * k], s);
+            acc = __builtin_fmaf((float)s, h2f(s_d[ar][b]) * h2f(wd[b]), acc);
+        }
+        s_dn[l][j][rr] = acc;
+    }
+    __syncthreads();
+    if (t < NL * DN_R) {
+        const int l = t / DN_R, rr = t % DN_R;
+        if (l < nl) {
+            float m = s_dn[l][0][rr] * s_w[l][0];
+            for (int j = 1; j < shp::KUSED; j++) {
+                const float pp = s_dn[l][j][rr] * s_w[l][j];
+                m = m + pp;
+            }
+            const float sv = s_dn[l][shp::KUSED][rr] * s_sg[l];
+            const float f = m + sv;
+            a.x2[(int64_t)l * shp::E + row0 + rr] = f + a.x1[(int64_t)l * shp::E + row0 + rr];
+        }
+    }
+}
+
+// ---- LM head over a K-quant matrix: the normed x2 (h_nextn) of every lane, q8_K blocks of it, the
+// lane GEMV into the logits, then the first strict maximum per wanted lane (NaN never wins; all
+// -inf: no key, argmax 0), packed as the per-phase head packs it: (ordered value << 32) | ~row.
+template <int NL>
+__global__ __launch_bounds__(256) void kq_head_norm_kernel(const RunCtl *__restrict__ ctl, const float *x2,
+                                                           const float *norm_w, float eps, float *hid, float *xn) {
+    __shared__ NormScratch ns;
+    if (!ctl->active) return;
+    const int nl = ctl->nl, t = threadIdx.x;
+#pragma unroll
+    for (int l = 0; l < NL; l++) {
+        float v[EPT];
+        if (l < nl) {
+            load8(x2 + (int64_t)l * shp::E, v);
+            rms_norm_mul_e(v, x2 + (int64_t)l * shp::E, norm_w, eps, ns);
+            store8(hid + (int64_t)l * shp::E, v);
+        } else {
+#pragma unroll
+            for (int i = 0; i < EPT; i++) v[i] = 0.0f;
+        }
+        store8(xn + (int64_t)l * shp::E, v);
+    }
+}
+
+template <int NL>
+__global__ __launch_bounds__(1024) void kq_argmax_kernel(const RunCtl *__restrict__ ctl, const float *logits, int64_t nv,
+                                                         unsigned long long *amax_key) {
+    __shared__ unsigned long long red[16];
+    if (!ctl->active) return;
+    const int l = blockIdx.x, t = threadIdx.x;
+    if (l >= ctl->nl || !((ctl->head_mask >> l) & 1)) return;
+    float best = -__builtin_inff();
+    int64_t bi = -1;
+    for (int64_t r = t; r < nv; r += 1024) {
+        const float v = logits[(int64_t)l * nv + r];
+        if (v > best) { best = v; bi = r; }
+    }
+    unsigned long long key = bi >= 0 ? ((unsigned long long)ordered_bits(best) << 32) | (0xffffffffu - (uint32_t)bi) : 0ull;
+    for (int m = 32; m >= 1; m >>= 1) {
+        const unsigned long long o = __shfl_xor(key, m, 64);
+        key = o > key ? o : key;
+    }
+    if ((t & 63) == 0) red[t >> 6] = key;
+    __syncthreads();
+    if (t == 0) {
+        unsigned long long k = 0ull;
+        for (int i = 0; i < 16; i++) k = red[i] > k ? red[i] : k;
+        if (k) atomicMax(&amax_key[l], k);
+    }
+}
+
 }  // namespace kq
+
+int launch_ba_f32(const RunCtl *ctl, const ModelRt &m, const LayerW &w, const float *x, const ActBufs &b, hipStream_t st) {
+    hipLaunchKernelGGL(kq::ba_f32_kernel<OXE_NL>, dim3(2 * shp::NVH / 16), dim3(256), 0, st, ctl, x, w.attn_norm, m.eps,
+                       (const float *)w.beta_r.w, (const float *)w.alpha_r.w, b.proj);
+    return hipGetLastError() == hipSuccess ? 0 : -2;
+}
+
+// q8_K blocks of nblk consecutive 256-value blocks of x (every lane of a [NL][n] buffer at once)
+static void quant_k(const float *x, int64_t nblk, uint8_t *y, hipStream_t st) {
+    hipLaunchKernelGGL(kq::quant_q8_K_kernel, dim3((unsigned)((nblk + 3) / 4)), dim3(256), 0, st, x, nblk, y);
+}
+
+int launch_kq_moe(const RunCtl *ctl, const ModelRt &m, const LayerW &w, const ActBufs &b, hipStream_t st) {
+    (void)m;
+    const bool exp_gu = w.exp_gate_r.type != 8, sh_gu = w.sh_gate_r.type != 8;
+    if (exp_gu || sh_gu) quant_k(b.xn, (int64_t)OXE_NL * shp::E / kq::QK, b.xk, st);
+    if (!exp_gu) launch_experts(ctl, w, b, st);
+    if (exp_gu || sh_gu) {
+        kq::KqGuArgs a{};
+        a.xk = b.xk;
+        a.gate = w.exp_gate_r;
+        a.up = w.exp_up_r;
+        a.sh_gate = w.sh_gate_r;
+        a.sh_up = w.sh_up_r;
+        a.uni = b.uni;
+        a.route_ids = b.route_ids;
+        a.hexp = b.hexp;
+        a.hsh = b.hsh;
+        a.do_exp = exp_gu;
+        a.do_sh = sh_gu;
+        hipLaunchKernelGGL(kq::kq_gu_kernel<OXE_NL>, dim3((OXE_MAX_UNION + 1) * (shp::FF / 16)), dim3(256), 0, st, ctl, a);
+    }
+    if (w.exp_down_r.type != 8) quant_k(b.hexp, (int64_t)OXE_NL * shp::KUSED * shp::FF / kq::QK, b.hk, st);
+    if (w.sh_down_r.type != 8) quant_k(b.hsh, (int64_t)OXE_NL * shp::FFSH / kq::QK, b.hshk, st);
+    kq::KqDownArgs d{};
+    d.uni = b.uni;
+    d.route_ids = b.route_ids;
+    d.route_w = b.route_w;
+    d.sh_gate = b.sh_gate;
+    d.hexp = b.hexp;
+    d.hsh = b.hsh;
+    d.hk = b.hk;
+    d.hshk = b.hshk;
+    d.exp_down = w.exp_down;
+    d.shexp_down = w.shexp_down;
+    d.exp_down_r = w.exp_down_r;
+    d.sh_down_r = w.sh_down_r;
+    d.x1 = b.x1;
+    d.x2 = b.x2;
+    d.amax_key = b.amax_key;
+    hipLaunchKernelGGL(kq::kq_down_kernel<OXE_NL>, dim3(shp::E / kq::DN_R), dim3(256), 0, st, ctl, d);
+    return hipGetLastError() == hipSuccess ? 0 : -2;
+}
+
+int launch_kq_head(const RunCtl *ctl, const ModelRt &m, const float *norm_w, const ActBufs &b, hipStream_t st) {
+    hipLaunchKernelGGL(kq::kq_head_norm_kernel<OXE_NL>, dim3(1), dim3(256), 0, st, ctl, b.x2, norm_w, m.eps, b.hid, b.xn);
+    quant_k(b.xn, (int64_t)OXE_NL * shp::E / kq::QK, b.xk, st);
+    const int nb = shp::E / kq::QK;
+    const RawW &o = m.output_r;
+    int rc;
+    switch (o.type) {
+        case 11: rc = kq::vl_gemv_type<3>(o.w, nb, o.rows, b.xk, OXE_NL, b.logits, st); break;
+        case 12: rc = kq::vl_gemv_type<4>(o.w, nb, o.rows, b.xk, OXE_NL, b.logits, st); break;
+        case 13: rc = kq::vl_gemv_type<5>(o.w, nb, o.rows, b.xk, OXE_NL, b.logits, st); break;
+        default: rc = kq::vl_gemv_type<6>(o.w, nb, o.rows, b.xk, OXE_NL, b.logits, st); break;
+    }
+    if (rc != 1) return -2;
+    hipLaunchKernelGGL(kq::kq_argmax_kernel<OXE_NL>, dim3(OXE_NL), dim3(1024), 0, st, ctl, b.logits, o.rows, b.amax_key);
+    return hipGetLastError() == hipSuccess ? 0 : -2;
+}
+
 }  // namespace oxe
 
 extern "C" {

@@ -5,8 +5,10 @@
 // GEMM kernel here reads, in place of the reference's 4-row interleave, oxe_shim.cpp:9-29),
 // concatenated per projection ([qkv | z | beta | alpha], [q+gate | k | v]) and, for gate / up
 // pairs, interleaved per 16-row tile (8 gate rows, then 8 up rows). F32 vectors and matrices are
-// copied. Any other tensor type is refused with the tensor's name: the kernels of this build run
-// Q8_0 matmul weights and F32 routers / norms only.
+// copied. The expert, shared-expert and output matrices may also be K-quants (Q3_K..Q6_K) and
+// ssm_beta / ssm_alpha F32 (the types a Qwen3.6 file holds there): those are copied in the file's
+// own blocks, for an engine created with those types (model_types reads them from the file). Any
+// other tensor type is refused with the tensor's name.
 #include <algorithm>
 #include <mutex>
 #include <string>
@@ -49,11 +51,41 @@ static std::string tensor_check(const GgufTensor *t, const std::string &name, ui
     if (t->type != type) {
         GgmlTypeInfo want{};
         ggml_type_info(type, &want);
+        const bool kq = t->type >= 11 && t->type <= 14;
+        if ((kq || t->type == GGML_F32) && type == GGML_Q8_0)
+            return name + ": type " + (ti.name ? ti.name : "unknown") + " has no kernel for this tensor here (Q8_0 " +
+                   "expected; K-quants load for the expert, shared-expert and output matrices, F32 for ssm_beta / " +
+                   "ssm_alpha, of an engine created from the file)";
         return name + ": type " + (ti.name ? ti.name : "unknown") + " has no kernel in this build (expected " +
-               want.name + ": Q8_0 matmul weights, F32 or BF16 vectors and routers)";
+               want.name + ": Q8_0 or K-quant matmul weights, F32 or BF16 vectors and routers)";
     }
     if (t->shape != std::vector<uint64_t>(shape)) return name + ": unexpected shape";
     return "";
+}
+
+// The types of the matrices that may be other than Q8_0, as the file holds them: gate / up of the
+// experts (or of the shared expert) both Q8_0 or both K-quants, down Q8_0 or a K-quant, ssm_beta /
+// ssm_alpha both Q8_0 or both F32, the LM head Q8_0 or a K-quant. A tensor of any other type keeps
+// Q8_0 here, and the load refuses it by name.
+ModelTypes model_types(const Gguf &g, const oxe_model_desc &d) {
+    ModelTypes mt;
+    mt.layer.assign(d.n_layer + 1, LayerTypes{});
+    auto ty = [&](const std::string &name) { const GgufTensor *t = g.tensor(name); return t ? (int)t->type : -1; };
+    auto kq = [](int t) { return t >= 11 && t <= 14; };
+    for (int il = 0; il <= d.n_layer; il++) {
+        LayerTypes &lt = mt.layer[il];
+        const std::string p = "blk." + std::to_string(il) + ".";
+        const int g0 = ty(p + "ffn_gate_exps.weight"), u0 = ty(p + "ffn_up_exps.weight"), d0 = ty(p + "ffn_down_exps.weight");
+        if (kq(g0) && kq(u0)) { lt.gate = g0; lt.up = u0; }
+        if (kq(d0)) lt.down = d0;
+        const int g1 = ty(p + "ffn_gate_shexp.weight"), u1 = ty(p + "ffn_up_shexp.weight"), d1 = ty(p + "ffn_down_shexp.weight");
+        if (kq(g1) && kq(u1)) { lt.sh_gate = g1; lt.sh_up = u1; }
+        if (kq(d1)) lt.sh_down = d1;
+        if (ty(p + "ssm_beta.weight") == (int)GGML_F32 && ty(p + "ssm_alpha.weight") == (int)GGML_F32) lt.beta = lt.alpha = 0;
+    }
+    const int o = ty("output.weight");
+    if (kq(o)) mt.output = o;
+    return mt;
 }
 
 int Engine::load_gguf(const Gguf &g, uint8_t *given_stage, int64_t given_chunk) {
@@ -116,6 +148,18 @@ int Engine::load_gguf(const Gguf &g, uint8_t *given_stage, int64_t given_chunk) 
             }
         }
     };
+    // a matrix kept in the file's blocks (K-quant or F32): copied as it is, in chunks
+    auto raw = [&](const std::string &name, const RawW &r, std::initializer_list<uint64_t> shape) {
+        if (!err.empty()) return;
+        const GgufTensor *t = g.tensor(name);
+        err = tensor_check(t, name, (uint32_t)r.type, shape);
+        if (!err.empty()) return;
+        const uint8_t *src = g.data(*t);
+        const int64_t n = (int64_t)t->bytes();
+        for (int64_t off = 0; off < n && !rc; off += CHUNK)
+            if (hipMemcpyAsync(r.w + off, src + off, (size_t)std::min(CHUNK, n - off), hipMemcpyHostToDevice, st) != hipSuccess)
+                rc = -2;
+    };
     // F32 vectors and routers; BF16 ones widened to f32 (exact: the bf16 bits are the high half of
     // the f32), as the reference converts BF16 small tensors at load (crates/model/src/mtp.rs:109-128)
     auto f32 = [&](const std::string &name, std::initializer_list<uint64_t> shape, float *dst) {
@@ -144,8 +188,13 @@ int Engine::load_gguf(const Gguf &g, uint8_t *given_stage, int64_t given_chunk) 
         if (!w.att) {
             q8(p + "attn_qkv.weight", E, NCH, 1, w.proj.q, w.proj.d, 0, 0, -1);
             q8(p + "attn_gate.weight", E, DIN, 1, w.proj.q, w.proj.d, DN_Z, 0, -1);
-            q8(p + "ssm_beta.weight", E, NVH, 1, w.proj.q, w.proj.d, DN_BETA, 0, -1);
-            q8(p + "ssm_alpha.weight", E, NVH, 1, w.proj.q, w.proj.d, DN_ALPHA, 0, -1);
+            if (w.beta_r.type == 8) {
+                q8(p + "ssm_beta.weight", E, NVH, 1, w.proj.q, w.proj.d, DN_BETA, 0, -1);
+                q8(p + "ssm_alpha.weight", E, NVH, 1, w.proj.q, w.proj.d, DN_ALPHA, 0, -1);
+            } else {
+                raw(p + "ssm_beta.weight", w.beta_r, {E, NVH});
+                raw(p + "ssm_alpha.weight", w.alpha_r, {E, NVH});
+            }
             q8(p + "ssm_out.weight", DIN, E, 1, w.out.q, w.out.d, 0, 0, -1);
             f32(p + "ssm_conv1d.weight", {KC, NCH}, w.conv);
             f32(p + "ssm_a", {NVH}, w.ssm_a);
@@ -161,12 +210,24 @@ int Engine::load_gguf(const Gguf &g, uint8_t *given_stage, int64_t given_chunk) 
         }
         f32(p + "ffn_gate_inp.weight", {E, NEXP}, w.router);
         f32(p + "ffn_gate_inp_shexp.weight", {E}, w.shexp_gate);
-        q8(p + "ffn_gate_shexp.weight", E, FFSH, 1, w.shexp_gu.q, w.shexp_gu.d, 0, 0, 0);
-        q8(p + "ffn_up_shexp.weight", E, FFSH, 1, w.shexp_gu.q, w.shexp_gu.d, 0, 0, 8);
-        q8(p + "ffn_down_shexp.weight", FFSH, E, 1, w.shexp_down.q, w.shexp_down.d, 0, 0, -1);
-        q8(p + "ffn_gate_exps.weight", E, FF, NEXP, w.exp_gu.q, w.exp_gu.d, 0, 2 * FF, 0);
-        q8(p + "ffn_up_exps.weight", E, FF, NEXP, w.exp_gu.q, w.exp_gu.d, 0, 2 * FF, 8);
-        q8(p + "ffn_down_exps.weight", FF, E, NEXP, w.exp_down.q, w.exp_down.d, 0, E, -1);
+        if (w.sh_gate_r.type == 8) {
+            q8(p + "ffn_gate_shexp.weight", E, FFSH, 1, w.shexp_gu.q, w.shexp_gu.d, 0, 0, 0);
+            q8(p + "ffn_up_shexp.weight", E, FFSH, 1, w.shexp_gu.q, w.shexp_gu.d, 0, 0, 8);
+        } else {
+            raw(p + "ffn_gate_shexp.weight", w.sh_gate_r, {E, FFSH});
+            raw(p + "ffn_up_shexp.weight", w.sh_up_r, {E, FFSH});
+        }
+        if (w.sh_down_r.type == 8) q8(p + "ffn_down_shexp.weight", FFSH, E, 1, w.shexp_down.q, w.shexp_down.d, 0, 0, -1);
+        else raw(p + "ffn_down_shexp.weight", w.sh_down_r, {FFSH, E});
+        if (w.exp_gate_r.type == 8) {
+            q8(p + "ffn_gate_exps.weight", E, FF, NEXP, w.exp_gu.q, w.exp_gu.d, 0, 2 * FF, 0);
+            q8(p + "ffn_up_exps.weight", E, FF, NEXP, w.exp_gu.q, w.exp_gu.d, 0, 2 * FF, 8);
+        } else {
+            raw(p + "ffn_gate_exps.weight", w.exp_gate_r, {E, FF, NEXP});
+            raw(p + "ffn_up_exps.weight", w.exp_up_r, {E, FF, NEXP});
+        }
+        if (w.exp_down_r.type == 8) q8(p + "ffn_down_exps.weight", FF, E, NEXP, w.exp_down.q, w.exp_down.d, 0, E, -1);
+        else raw(p + "ffn_down_exps.weight", w.exp_down_r, {FF, E, NEXP});
         if (il == d.n_layer) {
             q8(p + "nextn.eh_proj.weight", 2 * E, E, 1, w.eh_proj.q, w.eh_proj.d, 0, 0, -1);
             f32(p + "nextn.enorm.weight", {E}, w.enorm);
@@ -175,7 +236,8 @@ int Engine::load_gguf(const Gguf &g, uint8_t *given_stage, int64_t given_chunk) 
         }
     }
     q8("token_embd.weight", E, d.n_vocab, 1, m.tok_embd.q, m.tok_embd.d, 0, 0, -1);
-    q8("output.weight", E, d.n_vocab, 1, m.output.q, m.output.d, 0, 0, -1);
+    if (m.output_r.type == 8) q8("output.weight", E, d.n_vocab, 1, m.output.q, m.output.d, 0, 0, -1);
+    else raw("output.weight", m.output_r, {E, (uint64_t)d.n_vocab});
     f32("output_norm.weight", {E}, m.out_norm);
     const hipError_t se = hipStreamSynchronize(st);
     if (!given_stage) (void)hipFree(stage);
@@ -297,7 +359,8 @@ int oxe_engine_create_from_gguf(const char *path, int n_ctx, oxe_engine **out) {
         return -1;
     }
     oxe_engine *e = nullptr;
-    if ((rc = oxe_engine_create(&d, 0, n_ctx, &e))) {
+    const oxe::ModelTypes mt = oxe::model_types(*(const oxe::Gguf *)f, d);
+    if ((rc = oxe::create_engine(&d, 0, n_ctx, false, nullptr, &mt, &e))) {
         oxe_gguf_close(f);
         return rc;
     }

@@ -149,7 +149,9 @@ void launch_router(const RunCtl *ctl, const ModelRt &m, const LayerW &w, const A
         (void)hipFuncSetAttribute((const void *)router_kernel<OXE_NL>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         configured = true;
     }
-    hipLaunchKernelGGL(router_kernel<OXE_NL>, dim3(RT_ROW_WG + RT_SH_WG + RT_GU_TILES), dim3(256), lds, st, ctl, a);
+    // a K-quant shared gate / up runs in the MoE's K-quant kernels instead of these tiles
+    const int tiles = w.sh_gate_r.type == 8 ? RT_GU_TILES : 0;
+    hipLaunchKernelGGL(router_kernel<OXE_NL>, dim3(RT_ROW_WG + RT_SH_WG + tiles), dim3(256), lds, st, ctl, a);
 }
 
 // routing of every lane (one wave each) and the union of the lanes' experts in first-use order,

@@ -930,6 +930,21 @@ int Engine::pf_chunk(const uint32_t *toks, int T, float *h_out) {
 
 int Engine::prefill(const uint32_t *toks, int n, uint32_t *next, float *h_all) {
     if (n < 1 || pos + n > m.n_ctx || !toks_ok(toks, n)) return -1;
+    if (kq) {
+        // the batched pass's GEMMs take Q8_0 matrices: a model with K-quant / F32 matrices runs the
+        // decode runs two positions at a time (every position's state and h_nextn are the same)
+        uint32_t g[OXE_NL] = {};
+        for (int c0 = 0; c0 < n; c0 += OXE_NL) {
+            const int c = std::min(OXE_NL, n - c0);
+            int rc = verify(toks + c0, c, g);
+            if (!rc) rc = commit(c);
+            if (rc) return rc;
+            for (int i = 0; i < c && h_all; i++)
+                if ((rc = hidden_host(i, h_all + (size_t)(c0 + i) * E))) return rc;
+        }
+        if (next) *next = g[(n - 1) % OXE_NL];
+        return 0;
+    }
     int rc = pf_alloc(std::min(n, PF_CHUNK));
     if (rc) return rc;
     pend_n = 0;

@@ -9,6 +9,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <vector>
+
 #include "../../include/oxe_model.h"
 
 namespace oxe {
@@ -22,6 +24,37 @@ struct Q8W {
     int8_t *q = nullptr;
     uint16_t *d = nullptr;
     int64_t rows = 0, k = 0;
+};
+
+// A matrix kept in a model file's own blocks: K-quant rows of k / 256 ggml blocks (type 11..14), or
+// F32 rows (type 0). type 8: not used (the matrix is Q8_0, in the Q8W beside it).
+struct RawW {
+    uint8_t *w = nullptr;
+    int type = 8;
+    int64_t rows = 0, k = 0;   // per expert for the expert tensors
+};
+__host__ __device__ inline int kq_block_bytes(int type) {
+    return type == 11 ? 110 : type == 12 ? 144 : type == 13 ? 176 : type == 14 ? 210 : 0;
+}
+__host__ __device__ inline int64_t raw_row_bytes(const RawW &r) {
+    return r.type == 0 ? r.k * 4 : r.k / 256 * kq_block_bytes(r.type);
+}
+
+// ggml types of the matrices that may be other than Q8_0 (the reference's mv dispatches every type,
+// crates/model/src/engine.rs:2270-2343): K-quant experts, shared expert and LM head; F32 ssm_beta /
+// ssm_alpha. Gate and up of one expert kind are both Q8_0 or both K-quants.
+struct LayerTypes {
+    int gate = 8, up = 8, down = 8, sh_gate = 8, sh_up = 8, sh_down = 8, beta = 8, alpha = 8;
+    bool any() const { return gate != 8 || up != 8 || down != 8 || sh_gate != 8 || sh_up != 8 || sh_down != 8 || beta != 8 || alpha != 8; }
+};
+struct ModelTypes {
+    std::vector<LayerTypes> layer;   // n_layer + 1 (the MTP block last)
+    int output = 8;
+    bool any() const {
+        for (const LayerTypes &t : layer)
+            if (t.any()) return true;
+        return output != 8;
+    }
 };
 
 // recurrent slots: lane i reads slot cur+i, writes cur+i+1 (never in place). Five keep the state
@@ -86,6 +119,12 @@ struct LayerW {
     Q8W exp_down;   // [n_expert][n_embd][ff_exp]
     Q8W eh_proj;    // MTP block only: [n_embd][2*n_embd]
     float *enorm = nullptr, *hnorm = nullptr, *head_norm = nullptr;
+    // matrices of other types (a model file's), used in place of the Q8W ones above when their type
+    // is not 8: experts [n_expert][rows][k], the shared expert, ssm_beta / ssm_alpha [n_vheads][n_embd]
+    RawW exp_gate_r, exp_up_r, exp_down_r, sh_gate_r, sh_up_r, sh_down_r, beta_r, alpha_r;
+    bool kq_moe() const {
+        return exp_gate_r.type != 8 || exp_down_r.type != 8 || sh_gate_r.type != 8 || sh_down_r.type != 8;
+    }
 };
 
 // Per-lane activation buffers, all [OXE_NL][...]
@@ -111,6 +150,9 @@ struct ActBufs {
     float *hid;           // [HID_N][n_embd]
     float *logits;        // [NL][n_vocab] (optional)
     unsigned long long *amax_key;  // [NL] packed argmax keys
+    uint8_t *xk;          // q8_K blocks of xn [NL][n_embd / 256] (K-quant matrices)
+    uint8_t *hk;          // q8_K blocks of hexp [NL][k_used][ff_exp / 256]
+    uint8_t *hshk;        // q8_K blocks of hsh [NL][ff_shexp / 256]
     uint32_t *counters;   // per-kernel completion counters (zeroed at allocation; self-resetting)
 };
 

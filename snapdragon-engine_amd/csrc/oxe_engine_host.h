@@ -66,6 +66,11 @@ struct PfBufs {
 };
 constexpr int PF_CHUNK = 2048;   // tokens per batched pass
 
+// engine creation behind oxe_engine_create / _create_on / _create_from_gguf (engine.hip); mt: the
+// matrices' types, Q8_0 everywhere when null
+int create_engine(const oxe_model_desc *desc, uint64_t seed, int n_ctx, bool caller, void *stream, const ModelTypes *mt,
+                  oxe_engine **out);
+
 inline thread_local std::string g_last_error;
 inline void set_err(const std::string &s) { g_last_error = s; }
 
@@ -77,6 +82,8 @@ struct Engine {
     bool own_stream = true; // st created by the engine (destroyed with it), else the caller's
     ModelRt m{};
     std::vector<LayerW> L;  // n_layer (+1 MTP block)
+    ModelTypes types;       // the matrices' types
+    bool kq = false;        // some matrix is not Q8_0: per-phase runs, token-by-token prefill
     ActBufs b{};
     RunCtl *ctl = nullptr;  // device
     // the device-driven step's draft control block (fused runs), filled by the previous step's
@@ -230,10 +237,16 @@ struct Engine {
     }
 
     // caller: every launch and copy of this engine goes to the caller's `stream` (the null stream
-    // included); otherwise to a stream of its own
-    void create(const oxe_model_desc &desc, uint64_t sd, int n_ctx, bool caller = false, hipStream_t stream = nullptr) {
+    // included); otherwise to a stream of its own. mt: the matrices' types (a model file's), Q8_0
+    // everywhere when null
+    void create(const oxe_model_desc &desc, uint64_t sd, int n_ctx, bool caller = false, hipStream_t stream = nullptr,
+                const ModelTypes *mt = nullptr) {
         d = desc;
         seed = sd;
+        types.layer.assign(d.n_layer + 1, LayerTypes{});
+        types.output = 8;
+        if (mt && (int)mt->layer.size() == d.n_layer + 1) types = *mt;
+        kq = types.any();
         if (hipGetDevice(&dev) != hipSuccess) throw std::runtime_error("hipGetDevice failed");
         if (caller) {
             st = stream;
@@ -276,10 +289,28 @@ struct Engine {
             }
             w.router = alloc<float>((size_t)NEXP * E);
             w.shexp_gate = alloc<float>(E);
-            w.shexp_gu = q8(2 * FFSH, E);
-            w.shexp_down = q8(E, FFSH);
-            w.exp_gu = q8((int64_t)NEXP * 2 * FF, E);
-            w.exp_down = q8((int64_t)NEXP * E, FF);
+            const LayerTypes &ty = types.layer[il];
+            // a matrix of another type lives in its file blocks; its Q8_0 array is not allocated
+            auto raw = [&](RawW &r, int type, int64_t n_grp, int64_t rows, int64_t k) {
+                r.type = type;
+                r.rows = rows;
+                r.k = k;
+                if (type != 8) r.w = alloc<uint8_t>((size_t)(n_grp * rows * raw_row_bytes(r)));
+            };
+            raw(w.sh_gate_r, ty.sh_gate, 1, FFSH, E);
+            raw(w.sh_up_r, ty.sh_up, 1, FFSH, E);
+            raw(w.sh_down_r, ty.sh_down, 1, E, FFSH);
+            raw(w.exp_gate_r, ty.gate, NEXP, FF, E);
+            raw(w.exp_up_r, ty.up, NEXP, FF, E);
+            raw(w.exp_down_r, ty.down, NEXP, E, FF);
+            if (!w.att) {
+                raw(w.beta_r, ty.beta, 1, NVH, E);
+                raw(w.alpha_r, ty.alpha, 1, NVH, E);
+            }
+            if (ty.sh_gate == 8) w.shexp_gu = q8(2 * FFSH, E);
+            if (ty.sh_down == 8) w.shexp_down = q8(E, FFSH);
+            if (ty.gate == 8) w.exp_gu = q8((int64_t)NEXP * 2 * FF, E);
+            if (ty.down == 8) w.exp_down = q8((int64_t)NEXP * E, FF);
             if (il == d.n_layer) {
                 w.eh_proj = q8(E, 2 * E);
                 w.enorm = alloc<float>(E);
@@ -288,7 +319,17 @@ struct Engine {
             }
         }
         m.tok_embd = q8(d.n_vocab, E);
-        m.output = q8(d.n_vocab, E);
+        m.output_r = RawW{};
+        if (types.output != 8) {
+            m.output_r.type = types.output;
+            m.output_r.rows = d.n_vocab;
+            m.output_r.k = E;
+            m.output_r.w = alloc<uint8_t>((size_t)(d.n_vocab * raw_row_bytes(m.output_r)));
+            m.output.rows = d.n_vocab;   // the vocabulary size every head reads; no Q8_0 array
+            m.output.k = E;
+        } else {
+            m.output = q8(d.n_vocab, E);
+        }
         m.out_norm = alloc<float>(E);
         // state
         m.conv_state = alloc<float>((size_t)OXE_NSLOTS * n_rec * NCH * (KC - 1));
@@ -318,6 +359,9 @@ struct Engine {
         b.hid = alloc<float>((size_t)HID_N * E);
         b.logits = alloc<float>((size_t)OXE_NL * d.n_vocab);
         b.amax_key = alloc<unsigned long long>(OXE_NL);
+        b.xk = alloc<uint8_t>((size_t)OXE_NL * (E / 256) * 292);
+        b.hk = alloc<uint8_t>((size_t)OXE_NL * KUSED * (FF / 256) * 292);
+        b.hshk = alloc<uint8_t>((size_t)OXE_NL * (FFSH / 256) * 292);
         b.counters = alloc<uint32_t>(CNT_N);
         ctl = alloc<RunCtl>(2);
         ctl_draft = ctl + 1;
@@ -343,6 +387,7 @@ struct Engine {
     // The fused run kernel needs one workgroup per CU on exactly 256 CUs (its row splits assume
     // 256 workgroups) with every workgroup resident.
     void fused_init() {
+        if (kq) return;   // the fused run kernel reads Q8_0 matrices only: such models run per phase
         int dev = 0, ncu = 0;
         if (hipGetDevice(&dev) != hipSuccess) return;
         if (hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return;
@@ -506,6 +551,10 @@ struct Engine {
     }
 
     int synth_weights() {
+        if (kq) {
+            set_err("synth_weights: the engine holds K-quant / F32 matrices, which come from a model file");
+            return -1;
+        }
         int rc = 0;
         auto chk = [&](int r) { if (r) rc = r; };
         const int nl_total = d.n_layer + 1;
@@ -564,6 +613,8 @@ struct Engine {
         const LayerW &w = L[l];
         const float *x = first ? b.x : b.x2;
         probe(K_PROJ); launch_proj(ctl, m, w, first ? nullptr : b.x2, first, first ? b.x : nullptr, b, st); probe(K_PROJ);
+        // F32 ssm_beta / ssm_alpha: their rows of the projection output (the Q8_0 pass's are unused)
+        if (!w.att && w.beta_r.type != 8) (void)launch_ba_f32(ctl, m, w, first ? b.x : b.x2, b, st);
         if (!w.att) {
             probe(K_DN); launch_dn(ctl, m, w, b, st); probe(K_DN);
         } else {
@@ -577,8 +628,16 @@ struct Engine {
     void enqueue_moe(const LayerW &w) {
         probe(K_ROUTER); launch_router(ctl, m, w, b, st); probe(K_ROUTER);
         launch_route(ctl, b, st);
+        if (w.kq_moe()) {
+            probe(K_EXPERTS); (void)launch_kq_moe(ctl, m, w, b, st); probe(K_EXPERTS);
+            return;
+        }
         probe(K_EXPERTS); launch_experts(ctl, w, b, st); probe(K_EXPERTS);
         probe(K_DOWN); launch_down(ctl, w, b, st); probe(K_DOWN);
+    }
+    void enqueue_head(const float *norm_w, bool store_logits) {
+        if (m.output_r.type != 8) (void)launch_kq_head(ctl, m, norm_w, b, st);
+        else launch_head(ctl, m, norm_w, b, store_logits, st);
     }
     void enqueue_verify() {
         if (fused) {
@@ -589,7 +648,7 @@ struct Engine {
             return;
         }
         for (int l = 0; l < d.n_layer; l++) enqueue_layer(l, l == 0);
-        probe(K_HEAD); launch_head(ctl, m, m.out_norm, b, keep_logits, st); probe(K_HEAD);
+        probe(K_HEAD); enqueue_head(m.out_norm, keep_logits); probe(K_HEAD);
     }
     // rc: the fused run's control block (default: ctl)
     void enqueue_mtp_run(const RunCtl *rc = nullptr) {
@@ -609,7 +668,7 @@ struct Engine {
         probe(K_PV); launch_pv(ctl, m, w, b, st); probe(K_PV);
         probe(K_OUT); launch_out(ctl, w, b.x2, b, st); probe(K_OUT);
         enqueue_moe(w);
-        probe(K_HEAD); launch_head(ctl, m, w.head_norm, b, false, st); probe(K_HEAD);
+        probe(K_HEAD); enqueue_head(w.head_norm, false); probe(K_HEAD);
     }
     void enqueue_mtp_seed(const RunCtl *rc = nullptr) {
         if (fused) {

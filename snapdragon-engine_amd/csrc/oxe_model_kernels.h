@@ -18,6 +18,7 @@ struct ModelRt {
     float eps;
     // global tensors
     Q8W tok_embd, output;
+    RawW output_r;         // the LM head in another type (output_r.type != 8), else unused
     float *out_norm;
     // state
     float *conv_state;     // [NSLOTS][n_rec][NCH][KC-1]
@@ -46,5 +47,12 @@ void launch_down(const RunCtl *ctl, const LayerW &w, const ActBufs &b, hipStream
 void launch_head(const RunCtl *ctl, const ModelRt &m, const float *norm_w, const ActBufs &b, bool store_logits,
                  hipStream_t st);
 void launch_entry(const RunCtl *ctl, const ModelRt &m, const LayerW &w, const ActBufs &b, hipStream_t st);
+
+// K-quant / F32 matrices in the per-phase runs (k_kquant.hip): F32 ssm_beta / ssm_alpha rows after
+// the projection; the MoE's gate / up and down of a layer with any K-quant expert or shared matrix;
+// the LM head over a K-quant output matrix. Each returns 0 or -2 (a launch failed).
+int launch_ba_f32(const RunCtl *ctl, const ModelRt &m, const LayerW &w, const float *x, const ActBufs &b, hipStream_t st);
+int launch_kq_moe(const RunCtl *ctl, const ModelRt &m, const LayerW &w, const ActBufs &b, hipStream_t st);
+int launch_kq_head(const RunCtl *ctl, const ModelRt &m, const float *norm_w, const ActBufs &b, hipStream_t st);
 
 }  // namespace oxe

@@ -126,63 +126,81 @@ def qwen35moe_meta(desc):
     ]
 
 
-def synth_model_tensors(O, desc, seed):
+def synth_model_tensors(O, desc, seed, types=None):
     """(name, type, shape, payload) of every tensor of the synthetic model, generated by the
-    oracle from the same counter-based generator the device uses"""
+    oracle from the same counter-based generator the device uses. types: {(layer, kind): ggml type}
+    for matrices written as K-quants (11..14, the oracle's synthetic blocks) or F32 (0) instead of
+    Q8_0 (layer GLOBAL_LAYER: the LM head), as the oracle's typed engine builds them."""
     T, G = O.T, O.GLOBAL_LAYER
     E, V = desc.n_embd, desc.n_vocab
     NCH = desc.ssm_d_inner + 2 * desc.ssm_n_kheads * desc.ssm_d_state
     NH, HD, NKV, NEXP, FF = desc.n_head, desc.head_dim, desc.n_head_kv, desc.n_expert, desc.ff_exp
-    Q8, F32 = GGML["Q8_0"], GGML["F32"]
+    F32 = GGML["F32"]
+    types = types or {}
 
-    def q8(layer, kind, rows, k):
-        return lambda f: f.write(q8_blocks(*O.synth_q8(seed, layer, kind, rows, k)))
+    def ty(layer, kind):
+        return types.get((layer, kind), GGML["Q8_0"])
 
-    def q8x(layer, kind, rows, k):
+    def mat(layer, kind, rows, k):
+        t = ty(layer, kind)
+        if t == GGML["Q8_0"]:
+            return lambda f: f.write(q8_blocks(*O.synth_q8(seed, layer, kind, rows, k)))
+        if t == F32:
+            return lambda f: f.write(O.synth_f32(seed, layer, kind, rows * k).tobytes())
+        return lambda f: f.write(O.synth_kq(seed, layer, kind, t, rows, k).tobytes())
+
+    def matx(layer, kind, rows, k):
+        t = ty(layer, kind)
+
         def w(f):
             for e in range(NEXP):
-                f.write(q8_blocks(*O.synth_q8(seed, layer, kind, rows, k, expert=e)))
+                if t == GGML["Q8_0"]:
+                    f.write(q8_blocks(*O.synth_q8(seed, layer, kind, rows, k, expert=e)))
+                else:
+                    f.write(O.synth_kq(seed, layer, kind, t, rows, k, expert=e).tobytes())
         return w
+
+    q8, q8x = mat, matx
 
     def f32(layer, kind, n):
         return lambda f: f.write(O.synth_f32(seed, layer, kind, n).tobytes())
 
-    out = [("output.weight", Q8, [E, V], q8(G, T["OUTPUT"], V, E)),
+    out = [("output.weight", ty(G, T["OUTPUT"]), [E, V], q8(G, T["OUTPUT"], V, E)),
            ("output_norm.weight", F32, [E], f32(G, T["OUT_NORM"], E)),
-           ("token_embd.weight", Q8, [E, V], q8(G, T["TOK_EMBD"], V, E))]
+           ("token_embd.weight", GGML["Q8_0"], [E, V], q8(G, T["TOK_EMBD"], V, E))]
     for il in range(desc.n_layer + 1):
         p = f"blk.{il}."
         att = il == desc.n_layer or (il + 1) % desc.full_attention_interval == 0
         t = [(p + "attn_norm.weight", F32, [E], f32(il, T["ATTN_NORM"], E)),
              (p + "post_attention_norm.weight", F32, [E], f32(il, T["POST_NORM"], E))]
         if not att:
-            t += [(p + "attn_qkv.weight", Q8, [E, NCH], q8(il, T["DN_QKV"], NCH, E)),
-                  (p + "attn_gate.weight", Q8, [E, desc.ssm_d_inner], q8(il, T["DN_Z"], desc.ssm_d_inner, E)),
-                  (p + "ssm_beta.weight", Q8, [E, desc.ssm_n_vheads], q8(il, T["DN_BETA"], desc.ssm_n_vheads, E)),
-                  (p + "ssm_alpha.weight", Q8, [E, desc.ssm_n_vheads], q8(il, T["DN_ALPHA"], desc.ssm_n_vheads, E)),
-                  (p + "ssm_out.weight", Q8, [desc.ssm_d_inner, E], q8(il, T["DN_OUT"], E, desc.ssm_d_inner)),
+            t += [(p + "attn_qkv.weight", ty(il, T["DN_QKV"]), [E, NCH], q8(il, T["DN_QKV"], NCH, E)),
+                  (p + "attn_gate.weight", ty(il, T["DN_Z"]), [E, desc.ssm_d_inner], q8(il, T["DN_Z"], desc.ssm_d_inner, E)),
+                  (p + "ssm_beta.weight", ty(il, T["DN_BETA"]), [E, desc.ssm_n_vheads], q8(il, T["DN_BETA"], desc.ssm_n_vheads, E)),
+                  (p + "ssm_alpha.weight", ty(il, T["DN_ALPHA"]), [E, desc.ssm_n_vheads], q8(il, T["DN_ALPHA"], desc.ssm_n_vheads, E)),
+                  (p + "ssm_out.weight", ty(il, T["DN_OUT"]), [desc.ssm_d_inner, E], q8(il, T["DN_OUT"], E, desc.ssm_d_inner)),
                   (p + "ssm_conv1d.weight", F32, [desc.ssm_conv_kernel, NCH],
                    f32(il, T["DN_CONV"], NCH * desc.ssm_conv_kernel)),
                   (p + "ssm_a", F32, [desc.ssm_n_vheads], f32(il, T["DN_A"], desc.ssm_n_vheads)),
                   (p + "ssm_dt.bias", F32, [desc.ssm_n_vheads], f32(il, T["DN_DT"], desc.ssm_n_vheads)),
                   (p + "ssm_norm.weight", F32, [desc.ssm_d_state], f32(il, T["DN_NORM"], desc.ssm_d_state))]
         else:
-            t += [(p + "attn_q.weight", Q8, [E, 2 * NH * HD], q8(il, T["ATT_Q"], 2 * NH * HD, E)),
-                  (p + "attn_k.weight", Q8, [E, NKV * HD], q8(il, T["ATT_K"], NKV * HD, E)),
-                  (p + "attn_v.weight", Q8, [E, NKV * HD], q8(il, T["ATT_V"], NKV * HD, E)),
-                  (p + "attn_output.weight", Q8, [NH * HD, E], q8(il, T["ATT_OUT"], E, NH * HD)),
+            t += [(p + "attn_q.weight", ty(il, T["ATT_Q"]), [E, 2 * NH * HD], q8(il, T["ATT_Q"], 2 * NH * HD, E)),
+                  (p + "attn_k.weight", ty(il, T["ATT_K"]), [E, NKV * HD], q8(il, T["ATT_K"], NKV * HD, E)),
+                  (p + "attn_v.weight", ty(il, T["ATT_V"]), [E, NKV * HD], q8(il, T["ATT_V"], NKV * HD, E)),
+                  (p + "attn_output.weight", ty(il, T["ATT_OUT"]), [NH * HD, E], q8(il, T["ATT_OUT"], E, NH * HD)),
                   (p + "attn_q_norm.weight", F32, [HD], f32(il, T["ATT_QNORM"], HD)),
                   (p + "attn_k_norm.weight", F32, [HD], f32(il, T["ATT_KNORM"], HD))]
         t += [(p + "ffn_gate_inp.weight", F32, [E, NEXP], f32(il, T["ROUTER"], NEXP * E)),
               (p + "ffn_gate_inp_shexp.weight", F32, [E], f32(il, T["SHEXP_GATE"], E)),
-              (p + "ffn_gate_shexp.weight", Q8, [E, desc.ff_shexp], q8(il, T["GATE_SHEXP"], desc.ff_shexp, E)),
-              (p + "ffn_up_shexp.weight", Q8, [E, desc.ff_shexp], q8(il, T["UP_SHEXP"], desc.ff_shexp, E)),
-              (p + "ffn_down_shexp.weight", Q8, [desc.ff_shexp, E], q8(il, T["DOWN_SHEXP"], E, desc.ff_shexp)),
-              (p + "ffn_gate_exps.weight", Q8, [E, FF, NEXP], q8x(il, T["GATE_EXPS"], FF, E)),
-              (p + "ffn_up_exps.weight", Q8, [E, FF, NEXP], q8x(il, T["UP_EXPS"], FF, E)),
-              (p + "ffn_down_exps.weight", Q8, [FF, E, NEXP], q8x(il, T["DOWN_EXPS"], E, FF))]
+              (p + "ffn_gate_shexp.weight", ty(il, T["GATE_SHEXP"]), [E, desc.ff_shexp], q8(il, T["GATE_SHEXP"], desc.ff_shexp, E)),
+              (p + "ffn_up_shexp.weight", ty(il, T["UP_SHEXP"]), [E, desc.ff_shexp], q8(il, T["UP_SHEXP"], desc.ff_shexp, E)),
+              (p + "ffn_down_shexp.weight", ty(il, T["DOWN_SHEXP"]), [desc.ff_shexp, E], q8(il, T["DOWN_SHEXP"], E, desc.ff_shexp)),
+              (p + "ffn_gate_exps.weight", ty(il, T["GATE_EXPS"]), [E, FF, NEXP], q8x(il, T["GATE_EXPS"], FF, E)),
+              (p + "ffn_up_exps.weight", ty(il, T["UP_EXPS"]), [E, FF, NEXP], q8x(il, T["UP_EXPS"], FF, E)),
+              (p + "ffn_down_exps.weight", ty(il, T["DOWN_EXPS"]), [FF, E, NEXP], q8x(il, T["DOWN_EXPS"], E, FF))]
         if il == desc.n_layer:
-            t += [(p + "nextn.eh_proj.weight", Q8, [2 * E, E], q8(il, T["EH_PROJ"], E, 2 * E)),
+            t += [(p + "nextn.eh_proj.weight", ty(il, T["EH_PROJ"]), [2 * E, E], q8(il, T["EH_PROJ"], E, 2 * E)),
                   (p + "nextn.enorm.weight", F32, [E], f32(il, T["ENORM"], E)),
                   (p + "nextn.hnorm.weight", F32, [E], f32(il, T["HNORM"], E)),
                   (p + "nextn.shared_head_norm.weight", F32, [E], f32(il, T["HEAD_NORM"], E))]
@@ -190,5 +208,5 @@ def synth_model_tensors(O, desc, seed):
     return out
 
 
-def write_synth_model(path, O, desc, seed):
-    return write(path, qwen35moe_meta(desc), synth_model_tensors(O, desc, seed))
+def write_synth_model(path, O, desc, seed, types=None):
+    return write(path, qwen35moe_meta(desc), synth_model_tensors(O, desc, seed, types))

@@ -5,9 +5,10 @@ The synthetic model is written as a qwen35moe GGUF file with the reference's ten
 layouts (tests/gguf_writer.py, from the oracle's generator); an engine created from the file must
 decode bit for bit like the engine that generates the same weights on the device (prefill,
 logits, hidden states, speculative steps), which checks every tensor's name, shape, Q8_0 block
-split, projection concatenation and gate / up interleave at once. A real Qwen3.6 file (its header
-rebuilt from the reference's fixture, a sparse file of the real size) is refused by name at its
-first tensor type without a kernel here."""
+split, projection concatenation and gate / up interleave at once. The reference's real Qwen3.6 and
+Ornith files (headers rebuilt from its fixtures, sparse files of the real size): the Qwen3.6 file's
+types all load and run; the Ornith file is refused by name at its first tensor type without a
+kernel here."""
 import json
 import os
 
@@ -64,13 +65,11 @@ def test_engine_from_gguf_decodes_like_the_synthetic_engine():
             os.remove(path)
 
 
-def test_real_qwen36_file_is_refused_by_tensor_type():
-    """the reference's Qwen3.6 file (header from its fixture, a sparse file of the real size):
-    F32 ssm_beta (and k-quant experts) have no kernel in this build -> -1 with the tensor's name"""
-    import oxe_amd as A
-    fx = json.load(open(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden",
-                                     "gguf_header_qwen36.json")))
-    ids = {"F32": 0, "Q8_0": 8, "Q4_K": 12, "Q5_K": 13, "Q6_K": 14, "BF16": 30}
+def real_header_file(name):
+    """the reference's real model file rebuilt from its header fixture: the header, then a sparse
+    data section of the real size (every weight byte zero)"""
+    fx = json.load(open(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", f"gguf_header_{name}.json")))
+    ids = {"F32": 0, "Q8_0": 8, "Q3_K": 11, "Q4_K": 12, "Q5_K": 13, "Q6_K": 14, "BF16": 30}
 
     def typed(k, v):
         if isinstance(v, str):
@@ -83,12 +82,40 @@ def test_real_qwen36_file_is_refused_by_tensor_type():
 
     hdr, data_offset = W.header_at([typed(k, v) for k, v in fx["metadata"].items()],
                                    [(n, ids[t], s, o) for n, t, s, o, _ in fx["tensors"]])
-    path = os.path.join("/tmp", f"oxe_test_qwen36_{os.getpid()}.gguf")
+    path = os.path.join(scratch_dir(), f"oxe_test_{name}_{os.getpid()}.gguf")
+    with open(path, "wb") as f:
+        f.write(hdr)
+        f.truncate(data_offset + fx["tensor_bytes"])   # sparse: no data written
+    return path
+
+
+def test_real_qwen36_file_loads_and_decodes():
+    """the reference's Qwen3.6 file (header from its fixture, a sparse 21 GiB file of the real size):
+    K-quant experts (Q4_K gate / up, Q5_K and Q6_K down), F32 ssm_beta / ssm_alpha, the Q6_K LM
+    head and the MTP layer's BF16 routers all load; with every weight zero each logit is +0, so the
+    first strict maximum is row 0"""
+    import oxe_amd as A
+    path = real_header_file("qwen36")
     try:
-        with open(path, "wb") as f:
-            f.write(hdr)
-            f.truncate(data_offset + fx["tensor_bytes"])   # sparse: no data written
-        with pytest.raises(A.GgufError, match="blk.0.ssm_beta.weight: type F32 has no kernel"):
+        print("loading the sparse Qwen3.6 file", flush=True)
+        g = A.Engine.from_gguf(path, n_ctx=256)
+        assert not g.fused
+        assert g.step(1) == 0
+        lg = np.asarray(g.logits(0), np.float32)
+        assert lg.shape[0] == g.desc.n_vocab and not np.any(bits(lg))
+        g.close()
+    finally:
+        if os.path.exists(path):
+            os.remove(path)
+
+
+def test_real_ornith_file_is_refused_by_tensor_type():
+    """the reference's Ornith file: its Q4_K delta-net projections have no kernel in this build (the
+    engine takes K-quants for the expert, shared-expert and output matrices) -> -1 with the name"""
+    import oxe_amd as A
+    path = real_header_file("ornith")
+    try:
+        with pytest.raises(A.GgufError, match="blk.0.attn_qkv.weight: type Q4_K"):
             A.Engine.from_gguf(path, n_ctx=256)
     finally:
         if os.path.exists(path):
