@@ -607,6 +607,75 @@ def load_traffic(kernel):
         return json.load(f)
 
 
+def bench_forced(args):
+    """MTP device steps with every draft accepted: the drafts are forced (mtp_set_force, the
+    reference's draft_override hook, mtp.rs:554-558) to the target's own greedy ids, taken first from
+    a second engine's plain steps, so each step emits depth + 1 ids and the output must equal that
+    greedy sequence. Depth 2 verifies (x, d1) and then (d2) as two pieces of at most two lanes: its
+    verify reads the weights twice per step (the reference's 3-lane verify reads them once)."""
+    import torch
+    import oxe_amd as A
+    depth, K, W = args.depth, args.steps, args.warmup
+    d = A.desc_35b_a3b()
+    n_need = (depth + 1) * (K + W) + 8
+    n_ctx = args.prompt + n_need + 256 + 64
+    prompt = A.bench_prompt(args.prompt)
+    # the target's greedy continuation (every emitted id of a device step is a greedy target id)
+    ga = A.Engine(d, seed=0, n_ctx=n_ctx)
+    x0 = ga.mtp_prefill_batched(prompt)
+    cap = n_need + 16
+    ga.mtp_device_begin(x0, cap)
+    ga.mtp_device_steps(n_need, use_graph=True)
+    toks, _ = ga.mtp_device_end(cap)
+    ga.close()
+    g = [int(x0)] + [int(t) for t in toks]
+    assert len(g) >= (depth + 1) * (K + W) + 1
+    force = []
+    for i in range(K + W):
+        force += [g[(depth + 1) * i + 1 + j] for j in range(depth)]
+    eng = A.Engine(d, seed=0, n_ctx=n_ctx)
+    assert eng.mtp_prefill_batched(prompt) == x0
+    eng.mtp_set_depth(depth)
+    eng.mtp_set_force(force)
+    cap = (depth + 1) * (K + W) + 16
+    eng.mtp_device_begin(x0, cap)
+    eng.mtp_device_steps(W, use_graph=True)     # also captures the step graph
+    stream = torch.cuda.ExternalStream(eng.stream())
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    eng.sync()
+    torch.cuda.synchronize()
+    ev0.record(stream)
+    eng.mtp_device_steps(K, use_graph=True)
+    ev1.record(stream)
+    eng.sync()
+    torch.cuda.synchronize()
+    ms = ev0.elapsed_time(ev1)
+    out, _ = eng.mtp_device_end(cap)
+    out = [int(t) for t in out]
+    n_tok = (depth + 1) * K
+    return {
+        "metric": f"MTP-{depth} decode tok/s with every draft accepted (forced to the target's greedy ids), 35B-A3B shape, int8",
+        "value": round(n_tok / (ms / 1e3), 3),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": W,
+        "ms_per_step": round(ms / K, 4),
+        "tokens_per_step": depth + 1,
+        "verify_weight_passes_per_step": 1 if depth == 1 else 2,
+        "higher_is_better": True,
+        "vs_baseline": None,
+        "dtype": "int8 (Q8_0 weights and activations, int32 block dots, fp32 chains; fp16 KV)",
+        "data": "synthetic: seeded random Q8_0 weights, reference bench prompt ids; drafts forced",
+        "config": {"workload": f"BASELINE config 4 model, device-driven MTP depth {depth}, every draft accepted",
+                   "prompt_tokens": args.prompt, "parallelism": "single GPU"},
+        "run_mode": "fused (one persistent launch per run)" if eng.fused else "one launch per phase",
+        "parity": {"emitted_equal_greedy": out == g[1:1 + len(out)], "emitted": len(out),
+                   "expected": (depth + 1) * (K + W)},
+    }
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -633,6 +702,8 @@ def main():
     ap.add_argument("--config", type=int, default=0, choices=(0, 1, 2, 3),
                     help="a bench line for BASELINE config 1 (GEMV), 2 (one MoE layer) or 3 (mixers at 4096 "
                          "positions) instead of the decode step")
+    ap.add_argument("--depth", type=int, default=0, choices=(0, 1, 2),
+                    help="MTP depth 1 or 2 with every draft accepted (forced to the greedy ids): one JSON line")
     ap.add_argument("--gemm-probe", action="store_true",
                     help="only the prefill's Q8_0 GEMM on its 2048-token shapes (for rocprofv3 --pmc)")
     args = ap.parse_args()
@@ -660,6 +731,11 @@ def main():
         if args.steps == ap.get_default("steps"):
             args.steps = 40
         bench_kquant(args)
+        return
+    if args.depth:
+        if args.steps == ap.get_default("steps"):
+            args.steps = 64
+        print(json.dumps(bench_forced(args)), flush=True)
         return
     if args.config:
         fn = {1: bench_config1, 2: bench_config2, 3: bench_config3}[args.config]
