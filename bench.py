@@ -60,15 +60,16 @@ def verify_bytes(pos, u_avg, n_dn=30, n_att=10):
             + n_att * ((pos + 2) * KV_POS + 2 * KV_POS))
 
 
-def draft_bytes(pos, u_avg):
-    return (EH_PROJ + ATT_PROJ + MIX_OUT + ROUTER + SHARED + SMALL + u_avg * (EXPERT_GU + EXPERT_DOWN) + LM_HEAD
-            + (pos + 1) * KV_POS + KV_POS)
+def draft_bytes(pos, u_avg, head_rows=V):
+    """one draft run; head_rows: rows of its LM head (a restricted draft head's, else the vocabulary)"""
+    return (EH_PROJ + ATT_PROJ + MIX_OUT + ROUTER + SHARED + SMALL + u_avg * (EXPERT_GU + EXPERT_DOWN)
+            + head_rows * E * Q8 + (pos + 1) * KV_POS + KV_POS)
 
 
-def step_bytes(pos, u_avg, accepted_frac):
+def step_bytes(pos, u_avg, accepted_frac, head_rows=V):
     """Unique HBM bytes one MTP-1 step must move: verify + draft + (accepted steps) MTP seeding."""
     seed = accepted_frac * (EH_PROJ + 1024 * E * Q8 + KV_POS)
-    return verify_bytes(pos, u_avg) + draft_bytes(pos, u_avg) + seed
+    return verify_bytes(pos, u_avg) + draft_bytes(pos, u_avg, head_rows) + seed
 
 
 def host_cores():
@@ -702,6 +703,9 @@ def main():
     ap.add_argument("--config", type=int, default=0, choices=(0, 1, 2, 3),
                     help="a bench line for BASELINE config 1 (GEMV), 2 (one MoE layer) or 3 (mixers at 4096 "
                          "positions) instead of the decode step")
+    ap.add_argument("--draft-vocab", type=int, default=0,
+                    help="restrict the MTP draft head to token ids 0..K-1 (MtpWeights::set_draft_vocab); "
+                         "verify, and so the output, is unchanged")
     ap.add_argument("--depth", type=int, default=0, choices=(0, 1, 2),
                     help="MTP depth 1 or 2 with every draft accepted (forced to the greedy ids): one JSON line")
     ap.add_argument("--gemm-probe", action="store_true",
@@ -756,6 +760,7 @@ def main():
     eng = A.Engine(d, seed=0, n_ctx=n_ctx)
     if args.per_phase:
         eng.set_fused(False)
+    draft_rows = eng.mtp_set_draft_vocab(list(range(args.draft_vocab))) if args.draft_vocab > 0 else 0
     fused = eng.fused
     probe_kind = args.probe_kind if args.probe_kind >= 0 else (10 if fused else 1)
     prompt = A.bench_prompt(args.prompt)
@@ -799,7 +804,7 @@ def main():
     acc = (n_tok - args.steps) / max(args.steps, 1)
     mean_pos = (pos_start + pos_end) / 2
     u_avg = units / max(calls, 1)
-    bytes_step = step_bytes(mean_pos, u_avg, acc)
+    bytes_step = step_bytes(mean_pos, u_avg, acc, draft_rows or V)
     step_gbs = bytes_step / (ms / args.steps / 1e3) / 1e9
     # roofline of the dominant kernel: HIP events around each of its launches (eager steps; in the
     # fused mode the verify run is one launch of ~a millisecond, so launch overhead is negligible)
@@ -839,7 +844,8 @@ def main():
         "data": "synthetic: seeded random Q8_0 weights (include/oxe_model.h), reference bench prompt ids",
         "config": {"workload": "BASELINE config 4: 35B-A3B-shaped MTP-1 decode, 40 layers (30 DN + 10 GQA) + MTP block, "
                                "vocab 151936, all Q8_0",
-                   "prompt_tokens": args.prompt, "ctx_positions": [pos_start, pos_end], "parallelism": "single GPU"},
+                   "prompt_tokens": args.prompt, "ctx_positions": [pos_start, pos_end], "parallelism": "single GPU",
+                   **({"draft_head_rows": draft_rows} if draft_rows else {})},
         "tokens": n_tok,
         "accepted_drafts": n_tok - args.steps,
         "hbm_bytes_per_step": int(bytes_step),

@@ -292,6 +292,13 @@ OXE_API int oxe_mtp_device_end(oxe_engine *e, uint32_t *out_tok, int cap, int *n
 /* Forced drafts for the device-driven steps (test hook): force_d1[i * depth + j] >= 0 replaces draft
  * j + 1 of step i. */
 OXE_API int oxe_mtp_set_force(oxe_engine *e, const int32_t *force_d1, int n);
+/* Restricted-vocabulary draft head (MtpWeights::set_draft_vocab, crates/model/src/mtp.rs:166-197,
+ * WP-D3b): the output matrix's rows of `ids` (ids >= n_vocab dropped, sorted, duplicates removed,
+ * padded by repeating the last id) become every MTP draft run's LM head, its argmax mapped back to
+ * token ids; verify runs keep the whole head, so the output is unchanged and only the drafts (and
+ * acceptance) can differ. n = 0 restores the whole head. Returns the draft head's rows (0 after a
+ * restore), -1 (no id below n_vocab: "empty draft vocabulary"), -2 or -3. */
+OXE_API int oxe_mtp_set_draft_vocab(oxe_engine *e, const uint32_t *ids, int n);
 /* k eager device-driven steps with HIP events around each launch of one kernel kind (0 LM head,
  * 1 experts gate/up, 2 down, 3 projections, 4 mixer out, 5 delta-net, 6 router, 7 scores, 8 pv,
  * 9 MTP entry; in the fused run mode 10 the verify run, 11 the draft run, each one launch): mean
@@ -310,7 +317,9 @@ OXE_API void *oxe_engine_stream(oxe_engine *e);
 /* ---- the server's engine (crates/server/src/engine.rs:28-190 trait Engine, implemented for oxe
  * by crates/server/src/oxe_engine.rs:317-634 OxeEngine) ---------------------------------------
  * An oxe_srv borrows an engine (destroy the oxe_srv first) and, with mtp != 0, drives it through
- * the MTP depth-1 driver. Errors: -1 with oxe_last_error() (the reference's EngineError text),
+ * the MTP depth-1 driver; then OXE_MTP_DRAFT_VOCAB=<ranking file> [OXE_MTP_DRAFT_K=<k>] restricts
+ * the engine's draft head as the reference's adapter does (oxe_engine.rs:215-222; see
+ * oxe_mtp_set_draft_vocab). Errors: -1 with oxe_last_error() (the reference's EngineError text),
  * -2 HIP error; 1 = "not supported here" (the trait's Ok(None)). */
 typedef struct oxe_srv oxe_srv;
 typedef struct oxe_snapshot oxe_snapshot;

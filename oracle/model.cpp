@@ -603,8 +603,27 @@ struct oxo_engine {
         }
     }
 
-    // head (engine.rs:3630-3715) + gather_argmax (1969-1987)
-    void head(int nl, uint32_t mask, const std::vector<float> &norm) {
+    // restricted-vocabulary draft head (MtpWeights::set_draft_vocab, mtp.rs:166-197): the draft
+    // runs' argmax over these ids only (ascending, unique); empty: the whole head
+    std::vector<uint32_t> draft_ids;
+    std::vector<char> draft_mask;
+    int set_draft_vocab(const uint32_t *ids, int n) {
+        std::vector<uint32_t> v;
+        for (int i = 0; i < n; i++)
+            if (ids[i] < (uint32_t)d.n_vocab) v.push_back(ids[i]);
+        if (n > 0 && v.empty()) return -1;
+        std::sort(v.begin(), v.end());
+        v.erase(std::unique(v.begin(), v.end()), v.end());
+        draft_ids = v;
+        draft_mask.assign(v.empty() ? 0 : d.n_vocab, 0);
+        for (uint32_t i : v) draft_mask[i] = 1;
+        return (int)v.size();
+    }
+
+    // head (engine.rs:3630-3715) + gather_argmax (1969-1987); draft: an MTP draft run's head (the
+    // restricted one when set: its rows are the ids ascending, so the first maximum over them is
+    // the first by id)
+    void head(int nl, uint32_t mask, const std::vector<float> &norm, bool draft = false) {
         const int64_t E = d.n_embd, V = d.n_vocab;
         for (int ln = 0; ln < nl; ln++) {
             oxo_rms_norm_mul_f32(x2[ln].data(), norm.data(), hout[ln].data(), E, d.rms_eps);
@@ -613,8 +632,13 @@ struct oxo_engine {
             mv(output, {hout[ln].data()}, {lg.data()});
             float best = -INFINITY;
             uint32_t bi = UINT32_MAX;
-            for (int64_t r = 0; r < V; r++)
-                if (lg[r] > best) { best = lg[r]; bi = (uint32_t)r; }
+            if (draft && !draft_ids.empty()) {
+                for (uint32_t r : draft_ids)
+                    if (lg[r] > best) { best = lg[r]; bi = r; }
+            } else {
+                for (int64_t r = 0; r < V; r++)
+                    if (lg[r] > best) { best = lg[r]; bi = (uint32_t)r; }
+            }
             argmax[ln] = bi == UINT32_MAX ? 0 : bi;
             if (keep_logits) logits[ln] = lg;
         }
@@ -999,7 +1023,8 @@ struct oxo_engine {
     }
     // Head (engine.rs:3630-3715): this thread's vocabulary rows in chunks of 256, the first strict
     // maximum per lane; thread 0 keeps the normed hidden state
-    void p_head(TS &ts, int tid, int nt, int nl, uint32_t mask, const std::vector<float> &norm) {
+    void p_head(TS &ts, int tid, int nt, int nl, uint32_t mask, const std::vector<float> &norm, bool draft = false) {
+        const bool restricted = draft && !draft_ids.empty();
         const int64_t E = d.n_embd, V = d.n_vocab;
         int64_t r0, r1;
         split_rows(V, nt, tid, r0, r1);
@@ -1016,7 +1041,7 @@ struct oxo_engine {
                     float *y[1] = {ts.tmp.data()};
                     gemv_rows(output.q.data(), output.d.data(), E, r, r + c, 1, q, dd, y);
                     for (int64_t i = 0; i < c; i++)
-                        if (ts.tmp[i] > b.first) b = {ts.tmp[i], (uint32_t)(r + i)};
+                        if (ts.tmp[i] > b.first && (!restricted || draft_mask[r + i])) b = {ts.tmp[i], (uint32_t)(r + i)};
                     if (keep_logits) std::memcpy(logits[ln].data() + r, ts.tmp.data(), c * 4);
                 }
             }
@@ -1100,7 +1125,7 @@ struct oxo_engine {
             pool->barrier(tid);
             p_attention(ts, tid, nt, l, n, pos0, toks);
             p_moe(ts, tid, nt, l, n);
-            p_head(ts, tid, nt, n, head_last ? 1u << (n - 1) : 0u, layers[l].head_norm);
+            p_head(ts, tid, nt, n, head_last ? 1u << (n - 1) : 0u, layers[l].head_norm, true);
         };
         pool->run(job);
         p_gather_argmax(n);
@@ -1179,7 +1204,7 @@ struct oxo_engine {
         for (int ln = 0; ln < n; ln++) xin[ln] = x2[ln];
         attention(l, n, pos0);
         moe(l, n);
-        head(n, head_last ? 1u << (n - 1) : 0u, layers[l].head_norm);
+        head(n, head_last ? 1u << (n - 1) : 0u, layers[l].head_norm, true);
         return head_last ? argmax[n - 1] : UINT32_MAX;
     }
 
@@ -1399,6 +1424,9 @@ double oxo_gen_seconds(const oxo_engine *e) { return e->gen_seconds; }
 // (at most the CPUs of the caller's mask; the caller is thread 0 and is pinned to the first of
 // them until the plan is dropped); 0 drops the plan and its team. Returns the team size, 0, or -1.
 int oxo_set_plan(oxo_engine *e, int nthreads) { return e->set_plan(nthreads); }
+// the restricted draft head's ids (below n_vocab, sorted, unique); n = 0 restores the whole head.
+// Returns the ids kept, or -1 when none is below n_vocab
+int oxo_set_draft_vocab(oxo_engine *e, const uint32_t *ids, int n) { return e->set_draft_vocab(ids, n); }
 // barrier episodes of the plan's team so far (the reference's barriers/token counter)
 int64_t oxo_plan_barriers(const oxo_engine *e) { return e->pool ? (int64_t)e->pool->episodes.load() : -1; }
 

@@ -113,6 +113,7 @@ def lib():
             "oxo_set_keep_logits": (None, [C.c_void_p, C.c_int]),
             "oxo_gen_seconds": (C.c_double, [C.c_void_p]),
             "oxo_set_plan": (C.c_int, [C.c_void_p, C.c_int]),
+            "oxo_set_draft_vocab": (C.c_int, [C.c_void_p, u32p, C.c_int]),
             "oxo_plan_barriers": (C.c_int64, [C.c_void_p]),
             "oxo_pin_team": (C.c_int, [C.c_int]),
             "oxo_kcache": (u16p, [C.c_void_p]),
@@ -292,6 +293,13 @@ class Engine:
 
     def commit(self, m):
         assert lib().oxo_commit(self.h, m) == 0
+
+    def set_draft_vocab(self, ids):
+        v = np.ascontiguousarray(ids, np.uint32)
+        n = lib().oxo_set_draft_vocab(self.h, ptr(v, C.c_uint32), len(v))
+        if n < 0:
+            raise ValueError("empty draft vocabulary")
+        return n
 
     def set_plan(self, nthreads):
         """run through the reference's static plan on a pinned team of nthreads (0: the default

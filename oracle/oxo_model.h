@@ -14,6 +14,8 @@ oxo_engine *oxo_engine_new(const oxe_model_desc *d, uint64_t seed, int64_t n_ctx
 oxo_engine *oxo_engine_new_lanes(const oxe_model_desc *d, uint64_t seed, int64_t n_ctx, int n_slots);
 // with per-matrix ggml types types[layer * 64 + kind] (K-quant experts, shared experts and LM head;
 // F32 ssm_beta / ssm_alpha; Q8_0 elsewhere); null for a type this model cannot take there
+// restricted-vocabulary draft head (mtp.rs:166-197): MTP draft runs' argmax over `ids` only
+int oxo_set_draft_vocab(oxo_engine *e, const uint32_t *ids, int n);
 oxo_engine *oxo_engine_new_typed(const oxe_model_desc *d, uint64_t seed, int64_t n_ctx, int n_slots, const int32_t *types);
 void oxo_engine_free(oxo_engine *e);
 void oxo_engine_reset(oxo_engine *e);

@@ -17,6 +17,76 @@ const char *oxe_last_error(void) { return oxe::g_last_error.c_str(); }
 }  // extern "C"
 
 namespace oxe {
+
+// rows ids[0..n) of a row-major matrix (row_bytes per row, a multiple of 4) into dst, one thread per
+// 4-byte word
+__global__ void gather_rows_kernel(const uint8_t *src, int64_t row_bytes, const uint32_t *ids, int64_t n, uint8_t *dst) {
+    const int64_t wpr = row_bytes / 4, nw = n * wpr;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < nw; i += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t r = i / wpr, c = i % wpr;
+        ((uint32_t *)dst)[i] = ((const uint32_t *)(src + (int64_t)ids[r] * row_bytes))[c];
+    }
+}
+
+int Engine::set_draft_vocab(const uint32_t *ids, int n) {
+    if (n < 0 || (n > 0 && !ids)) return -1;
+    std::vector<uint32_t> v;
+    for (int i = 0; i < n; i++)
+        if (ids[i] < (uint32_t)d.n_vocab) v.push_back(ids[i]);
+    if (n > 0 && v.empty()) {
+        set_err("empty draft vocabulary");
+        return -1;
+    }
+    std::sort(v.begin(), v.end());
+    v.erase(std::unique(v.begin(), v.end()), v.end());
+    while (!v.empty() && v.size() % 16 != 0) v.push_back(v.back());
+    const int64_t rows = (int64_t)v.size();
+    if (graph_exec) {   // a captured draft run holds the old head
+        (void)hipGraphExecDestroy(graph_exec);
+        graph_exec = nullptr;
+    }
+    if (rows > 0) {
+        try {
+            if (rows > draft_cap) {   // arrays of the largest head so far (kept until the engine goes)
+                draft_ids = alloc<uint32_t>((size_t)rows);
+                if (m.output_r.type != 8) {
+                    draft_r = m.output_r;
+                    draft_r.w = alloc<uint8_t>((size_t)(rows * raw_row_bytes(m.output_r)));
+                } else {
+                    draft_w.q = alloc<int8_t>((size_t)rows * E);
+                    draft_w.d = alloc<uint16_t>((size_t)rows * (E / 32));
+                }
+                draft_cap = rows;
+            }
+        } catch (...) {
+            return -3;
+        }
+        if (hipMemcpyAsync(draft_ids, v.data(), (size_t)rows * 4, hipMemcpyHostToDevice, st) != hipSuccess) return -2;
+        auto gather = [&](const void *src, int64_t rb, void *dst) {
+            const int64_t nw = rows * rb / 4;
+            hipLaunchKernelGGL(gather_rows_kernel, dim3((unsigned)std::min<int64_t>((nw + 255) / 256, 65535)), dim3(256), 0, st,
+                               (const uint8_t *)src, rb, draft_ids, rows, (uint8_t *)dst);
+        };
+        if (m.output_r.type != 8) {
+            draft_r.rows = rows;
+            gather(m.output_r.w, raw_row_bytes(m.output_r), draft_r.w);
+        } else {
+            draft_w.rows = rows;
+            draft_w.k = E;
+            gather(m.output.q, E, draft_w.q);
+            gather(m.output.d, (E / 32) * 2, draft_w.d);
+        }
+    }
+    draft_rows = rows;
+    if (fused_ok) {
+        fz_host[FM_DRAFT].head_w = rows > 0 ? draft_w : m.output;
+        fz_host[FM_DRAFT].head_ids = rows > 0 ? draft_ids : nullptr;
+        if (hipMemcpyAsync(fz_args, fz_host, sizeof(fz_host), hipMemcpyHostToDevice, st) != hipSuccess) return -2;
+    }
+    if (hipStreamSynchronize(st) != hipSuccess || hipGetLastError() != hipSuccess) return -2;
+    return (int)rows;
+}
+
 int create_engine(const oxe_model_desc *desc, uint64_t seed, int n_ctx, bool caller, void *stream, const ModelTypes *mt,
                   oxe_engine **out) {
     // the attention kernel keeps a kv group's f16 probabilities in LDS: contexts up to 6144

@@ -2036,7 +2036,7 @@ FZ_PHASE bool phase_head(const RunCtl *ctl, const FusedArgs *ap, const float *no
     const FZ_CAS FusedArgs &a = *c.a;
     auto &s = c.sm->head;
     const int t = threadIdx.x, nl = c.nl, mask = c.ctl->head_mask;
-    const int64_t V = a.m.output.rows;
+    const int64_t V = a.head_w.rows;
     constexpr int TR = HEAD_TR;                              // rows per tile
     const int64_t ntiles = (V + TR - 1) / TR;
     // Tiles: `per` (even) in a contiguous range per workgroup, then pairs of the remaining tiles
@@ -2048,7 +2048,7 @@ FZ_PHASE bool phase_head(const RunCtl *ctl, const FusedArgs *ap, const float *no
     const int64_t t0 = dyn ? per * c.b : ntiles * c.b / c.G, t1 = dyn ? t0 + per : ntiles * (c.b + 1) / c.G;
     WSlice<E, HEAD_P> A, B;
     auto rows_of = [&](int64_t tile) { const int64_t r = V - tile * TR; return (int)(r < TR ? r : TR); };
-    if (t0 < t1) wload<E, HEAD_P>(A, a.m.output.q, a.m.output.d, rows_of(t0), [&](int rl) { return t0 * TR + rl; });
+    if (t0 < t1) wload<E, HEAD_P>(A, a.head_w.q, a.head_w.d, rows_of(t0), [&](int rl) { return t0 * TR + rl; });
     const W8 nw = wload8(norm_w);
     wait_vm<5>();   // about half of the 11 loads above
     const XR xr = make_xr(a.xbase, a.xbytes);
@@ -2080,9 +2080,9 @@ FZ_PHASE bool phase_head(const RunCtl *ctl, const FusedArgs *ap, const float *no
     if (!dyn) {
         for (int64_t tile = t0; tile < t1; tile += 2) {
             const int64_t tb = tile + 1 < t1 ? tile + 1 : t1 - 1, ta = tile + 2 < t1 ? tile + 2 : t1 - 1;
-            wload<E, HEAD_P, true>(B, a.m.output.q, a.m.output.d, rows_of(tb), [&](int r) { return tb * TR + r; });
+            wload<E, HEAD_P, true>(B, a.head_w.q, a.head_w.d, rows_of(tb), [&](int r) { return tb * TR + r; });
             dot_tile(A, tile);
-            wload<E, HEAD_P, true>(A, a.m.output.q, a.m.output.d, rows_of(ta), [&](int r) { return ta * TR + r; });
+            wload<E, HEAD_P, true>(A, a.head_w.q, a.head_w.d, rows_of(ta), [&](int r) { return ta * TR + r; });
             if (tile + 1 < t1) dot_tile(B, tile + 1);
         }
     } else {
@@ -2107,17 +2107,21 @@ FZ_PHASE bool phase_head(const RunCtl *ctl, const FusedArgs *ap, const float *no
             if (claim && t == 0) rv = __hip_atomic_fetch_add(hq, 2u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             const int64_t sb = seq(i + 1), sa = seq(i + 2);
             const int64_t tb = sb < 0 ? tc : sb, ta = sa < 0 ? tb : sa;   // past the end: a reload
-            wload<E, HEAD_P, true>(B, a.m.output.q, a.m.output.d, rows_of(tb), [&](int r) { return tb * TR + r; });
+            wload<E, HEAD_P, true>(B, a.head_w.q, a.head_w.d, rows_of(tb), [&](int r) { return tb * TR + r; });
             dot_tile(A, tc);
             if (claim && t == 0) s.claim[((i - per + 4) >> 1) & 3] = ns + (int64_t)rv;
-            wload<E, HEAD_P, true>(A, a.m.output.q, a.m.output.d, rows_of(ta), [&](int r) { return ta * TR + r; });
+            wload<E, HEAD_P, true>(A, a.head_w.q, a.head_w.d, rows_of(ta), [&](int r) { return ta * TR + r; });
             if (sb >= 0) dot_tile(B, tb);
         }
     }
     // per-lane key of this workgroup: the largest value, then the smallest row
     unsigned long long key = 0ull;
-    if (l < NL && l < nl && ((mask >> l) & 1) && bi >= 0)
-        key = ((unsigned long long)ordered_bits_f(best) << 32) | (0xffffffffu - (uint32_t)bi);
+    if (l < NL && l < nl && ((mask >> l) & 1) && bi >= 0) {
+        // a restricted draft head's rows are ascending token ids: the first maximum by row is the
+        // first by id
+        const uint32_t id = a.head_ids ? a.head_ids[bi] : (uint32_t)bi;
+        key = ((unsigned long long)ordered_bits_f(best) << 32) | (0xffffffffu - id);
+    }
     if (t < NL * TR) {
         for (int m = TR / 2; m >= 1; m >>= 1) {
             const unsigned long long o = __shfl_xor(key, m, 64);

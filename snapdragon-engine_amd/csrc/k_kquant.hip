@@ -809,7 +809,7 @@ __global__ __launch_bounds__(256) void kq_head_norm_kernel(const RunCtl *__restr
 
 template <int NL>
 __global__ __launch_bounds__(1024) void kq_argmax_kernel(const RunCtl *__restrict__ ctl, const float *logits, int64_t nv,
-                                                         unsigned long long *amax_key) {
+                                                         unsigned long long *amax_key, const uint32_t *ids) {
     __shared__ unsigned long long red[16];
     if (!ctl->active) return;
     const int l = blockIdx.x, t = threadIdx.x;
@@ -820,7 +820,9 @@ __global__ __launch_bounds__(1024) void kq_argmax_kernel(const RunCtl *__restric
         const float v = logits[(int64_t)l * nv + r];
         if (v > best) { best = v; bi = r; }
     }
-    unsigned long long key = bi >= 0 ? ((unsigned long long)ordered_bits(best) << 32) | (0xffffffffu - (uint32_t)bi) : 0ull;
+    // a restricted draft head's rows are ascending token ids: the first maximum by row is the first by id
+    const uint32_t id = bi < 0 ? 0u : (ids ? ids[bi] : (uint32_t)bi);
+    unsigned long long key = bi >= 0 ? ((unsigned long long)ordered_bits(best) << 32) | (0xffffffffu - id) : 0ull;
     for (int m = 32; m >= 1; m >>= 1) {
         const unsigned long long o = __shfl_xor(key, m, 64);
         key = o > key ? o : key;
@@ -889,11 +891,12 @@ int launch_kq_moe(const RunCtl *ctl, const ModelRt &m, const LayerW &w, const Ac
     return hipGetLastError() == hipSuccess ? 0 : -2;
 }
 
-int launch_kq_head(const RunCtl *ctl, const ModelRt &m, const float *norm_w, const ActBufs &b, hipStream_t st) {
+int launch_kq_head(const RunCtl *ctl, const ModelRt &m, const float *norm_w, const ActBufs &b, hipStream_t st,
+                   const RawW *w, const uint32_t *ids) {
     hipLaunchKernelGGL(kq::kq_head_norm_kernel<OXE_NL>, dim3(1), dim3(256), 0, st, ctl, b.x2, norm_w, m.eps, b.hid, b.xn);
     quant_k(b.xn, (int64_t)OXE_NL * shp::E / kq::QK, b.xk, st);
     const int nb = shp::E / kq::QK;
-    const RawW &o = m.output_r;
+    const RawW &o = w ? *w : m.output_r;
     int rc;
     switch (o.type) {
         case 11: rc = kq::vl_gemv_type<3>(o.w, nb, o.rows, b.xk, OXE_NL, b.logits, st); break;
@@ -902,7 +905,7 @@ int launch_kq_head(const RunCtl *ctl, const ModelRt &m, const float *norm_w, con
         default: rc = kq::vl_gemv_type<6>(o.w, nb, o.rows, b.xk, OXE_NL, b.logits, st); break;
     }
     if (rc != 1) return -2;
-    hipLaunchKernelGGL(kq::kq_argmax_kernel<OXE_NL>, dim3(OXE_NL), dim3(1024), 0, st, ctl, b.logits, o.rows, b.amax_key);
+    hipLaunchKernelGGL(kq::kq_argmax_kernel<OXE_NL>, dim3(OXE_NL), dim3(1024), 0, st, ctl, b.logits, o.rows, b.amax_key, ids);
     return hipGetLastError() == hipSuccess ? 0 : -2;
 }
 

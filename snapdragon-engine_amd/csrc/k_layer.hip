@@ -440,7 +440,7 @@ template <int NL>
 __global__ __launch_bounds__(GEMV_THREADS) void head_kernel(const RunCtl *__restrict__ ctl, const float *x2,
                                                             const float *norm_w, float eps, Q8W w, int64_t ntiles,
                                                             float *hid, float *logits,
-                                                            unsigned long long *amax_key) {
+                                                            unsigned long long *amax_key, const uint32_t *ids) {
     constexpr int R = GemvR<E>::R;
     __shared__ int8_t s_xq[NL][E];
     __shared__ uint16_t s_xd[NL][E / 32];
@@ -484,16 +484,20 @@ __global__ __launch_bounds__(GEMV_THREADS) void head_kernel(const RunCtl *__rest
         }
     }
     if (t < NL && t < nl && ((mask >> t) & 1) && bi >= 0) {
-        const unsigned long long key = ((unsigned long long)ordered_bits(best) << 32) | (0xffffffffu - (uint32_t)bi);
+        // a restricted draft head's rows are ascending token ids (ids[row]): the first maximum by
+        // row is the first by id
+        const uint32_t id = ids ? ids[bi] : (uint32_t)bi;
+        const unsigned long long key = ((unsigned long long)ordered_bits(best) << 32) | (0xffffffffu - id);
         atomicMax(&amax_key[t], key);
     }
 }
 
 void launch_head(const RunCtl *ctl, const ModelRt &m, const float *norm_w, const ActBufs &b, bool store_logits,
-                 hipStream_t st) {
-    const int64_t ntiles = (m.output.rows + GemvR<E>::R - 1) / GemvR<E>::R;
+                 hipStream_t st, const Q8W *w, const uint32_t *ids) {
+    const Q8W &hw = w ? *w : m.output;
+    const int64_t ntiles = (hw.rows + GemvR<E>::R - 1) / GemvR<E>::R;
     hipLaunchKernelGGL(head_kernel<OXE_NL>, dim3(grid_for(ntiles, 2048)), dim3(GEMV_THREADS), 0, st, ctl, b.x2,
-                       norm_w, m.eps, m.output, ntiles, b.hid, store_logits ? b.logits : nullptr, b.amax_key);
+                       norm_w, m.eps, hw, ntiles, b.hid, store_logits ? b.logits : nullptr, b.amax_key, ids);
 }
 
 }  // namespace oxe

@@ -675,6 +675,12 @@ int oxe_mtp_set_force(oxe_engine *e, const int32_t *force_d1, int n) {
     return g->set_force(force_d1, n);
 }
 
+int oxe_mtp_set_draft_vocab(oxe_engine *e, const uint32_t *ids, int n) {
+    Engine *g = (Engine *)e;
+    if (!g) return -1;
+    return g->set_draft_vocab(ids, n);
+}
+
 int oxe_mtp_device_begin(oxe_engine *e, uint32_t x, int out_cap) {
     Engine *g = (Engine *)e;
     if (out_cap < 1 || !g->toks_ok(&x, 1)) return -1;

@@ -451,6 +451,8 @@ struct Engine {
             f.xbytes = (uint32_t)(fz_xch_words * 8);
             f.keys = fz_keys;
             f.mh = fz_hooks;
+            f.head_w = m.output;
+            f.head_ids = nullptr;
         }
         if (hooks_upload()) return;
         (void)hipMemsetAsync(fz_sync, 0, FZ_SYNC_WORDS * 4, st);
@@ -635,10 +637,23 @@ struct Engine {
         probe(K_EXPERTS); launch_experts(ctl, w, b, st); probe(K_EXPERTS);
         probe(K_DOWN); launch_down(ctl, w, b, st); probe(K_DOWN);
     }
-    void enqueue_head(const float *norm_w, bool store_logits) {
-        if (m.output_r.type != 8) (void)launch_kq_head(ctl, m, norm_w, b, st);
-        else launch_head(ctl, m, norm_w, b, store_logits, st);
+    // draft: an MTP draft run's head (the restricted draft head when one is set)
+    void enqueue_head(const float *norm_w, bool store_logits, bool draft = false) {
+        const uint32_t *ids = draft ? draft_ids : nullptr;
+        if (m.output_r.type != 8) (void)launch_kq_head(ctl, m, norm_w, b, st, draft ? &draft_r : nullptr, ids);
+        else launch_head(ctl, m, norm_w, b, store_logits, st, draft ? &draft_w : nullptr, ids);
     }
+    // ---- restricted-vocabulary draft head (MtpWeights::set_draft_vocab, mtp.rs:166-197): the
+    // output matrix's rows of `ids` (below n_vocab, sorted, duplicates dropped, padded to a multiple
+    // of 16 rows by repeating the last id), gathered on the device; every MTP draft run's argmax
+    // runs over them and maps local row r back to token ids[r]. Drafts only: verify runs keep the
+    // whole head, so the output is unchanged. n = 0: drafts use the whole head again. Returns the
+    // draft head's rows (0 when cleared) or -1 (no id in range), -2, -3.
+    Q8W draft_w{};
+    RawW draft_r{};
+    uint32_t *draft_ids = nullptr;
+    int64_t draft_rows = 0, draft_cap = 0;
+    int set_draft_vocab(const uint32_t *ids, int n);
     void enqueue_verify() {
         if (fused) {
             if (!fz_capturing) fz_account(1);
@@ -668,7 +683,7 @@ struct Engine {
         probe(K_PV); launch_pv(ctl, m, w, b, st); probe(K_PV);
         probe(K_OUT); launch_out(ctl, w, b.x2, b, st); probe(K_OUT);
         enqueue_moe(w);
-        probe(K_HEAD); enqueue_head(w.head_norm, false); probe(K_HEAD);
+        probe(K_HEAD); enqueue_head(w.head_norm, false, draft_rows > 0); probe(K_HEAD);
     }
     void enqueue_mtp_seed(const RunCtl *rc = nullptr) {
         if (fused) {

@@ -87,6 +87,10 @@ struct FusedArgs {
     unsigned long long *keys;      // [NL][grid] per-workgroup argmax keys of the LM head
     unsigned long long *trace;     // optional [grid][FZ_TRACE_EV][4]: phase id, start, barrier passed, end
     const MtpHooks *mh;            // the device-driven MTP step's stages
+    // the LM head of this run: the output matrix, or (draft runs) the restricted draft head's rows,
+    // whose local row r is token head_ids[r] (null: row r is token r)
+    Q8W head_w;
+    const uint32_t *head_ids;
 };
 
 constexpr int FZ_TRACE_EV = 2048;  // trace events per workgroup and run

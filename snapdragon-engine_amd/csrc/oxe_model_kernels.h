@@ -44,8 +44,10 @@ void launch_router(const RunCtl *ctl, const ModelRt &m, const LayerW &w, const A
 void launch_route(const RunCtl *ctl, const ActBufs &b, hipStream_t st);
 void launch_experts(const RunCtl *ctl, const LayerW &w, const ActBufs &b, hipStream_t st);
 void launch_down(const RunCtl *ctl, const LayerW &w, const ActBufs &b, hipStream_t st);
+// w / ids: a restricted draft head (rows of the output matrix, local row r = token ids[r]); null: the
+// output matrix, row r = token r
 void launch_head(const RunCtl *ctl, const ModelRt &m, const float *norm_w, const ActBufs &b, bool store_logits,
-                 hipStream_t st);
+                 hipStream_t st, const Q8W *w = nullptr, const uint32_t *ids = nullptr);
 void launch_entry(const RunCtl *ctl, const ModelRt &m, const LayerW &w, const ActBufs &b, hipStream_t st);
 
 // K-quant / F32 matrices in the per-phase runs (k_kquant.hip): F32 ssm_beta / ssm_alpha rows after
@@ -53,6 +55,7 @@ void launch_entry(const RunCtl *ctl, const ModelRt &m, const LayerW &w, const Ac
 // the LM head over a K-quant output matrix. Each returns 0 or -2 (a launch failed).
 int launch_ba_f32(const RunCtl *ctl, const ModelRt &m, const LayerW &w, const float *x, const ActBufs &b, hipStream_t st);
 int launch_kq_moe(const RunCtl *ctl, const ModelRt &m, const LayerW &w, const ActBufs &b, hipStream_t st);
-int launch_kq_head(const RunCtl *ctl, const ModelRt &m, const float *norm_w, const ActBufs &b, hipStream_t st);
+int launch_kq_head(const RunCtl *ctl, const ModelRt &m, const float *norm_w, const ActBufs &b, hipStream_t st,
+                   const RawW *w = nullptr, const uint32_t *ids = nullptr);
 
 }  // namespace oxe

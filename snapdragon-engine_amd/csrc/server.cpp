@@ -9,6 +9,13 @@
 //   snapshot / restore  recurrent state + position (+ the MTP driver's catch-up state); KV in place
 //   save_state / load_state  Engine::write_state / read_state bytes + the MTP driver's state
 // Snapshots are kept in device memory (the state is 63 MB per slot; a device copy is ~20 us).
+// With MTP on, OXE_MTP_DRAFT_VOCAB=<ranking> [OXE_MTP_DRAFT_K=<k>] restricts the draft head to the
+// ranking file's ids (one per line, most frequent first, cut to k), as the reference's adapter does
+// at load (oxe_engine.rs:215-222, MtpWeights::apply_draft_vocab, mtp.rs:199-222).
+#include <cstdlib>
+#include <fstream>
+#include <sstream>
+
 #include "../../include/oxe_amd.h"
 #include "oxe_engine_host.h"
 
@@ -425,10 +432,54 @@ static SrvEngine *srv(oxe_srv *s) {
 
 extern "C" {
 
+// the ranking file's ids: the first field of each line that parses as an unsigned integer, in file
+// order, the first k of them when k >= 0 (apply_draft_vocab, mtp.rs:199-212)
+static int read_ranking(const char *path, long long k, std::vector<uint32_t> &ids) {
+    std::ifstream f(path);
+    if (!f) {
+        oxe::set_err(std::string(path) + ": cannot be read");
+        return -1;
+    }
+    std::string line;
+    while (std::getline(f, line)) {
+        std::istringstream ls(line);
+        std::string w;
+        if (!(ls >> w) || w.empty() || w.size() > 10 || w.find_first_not_of("0123456789") != std::string::npos) continue;
+        const unsigned long long v = std::stoull(w);
+        if (v > 0xffffffffull) continue;
+        ids.push_back((uint32_t)v);
+    }
+    if (k >= 0 && (long long)ids.size() > k) ids.resize((size_t)k);
+    return 0;
+}
+
 int oxe_srv_create(oxe_engine *engine, int mtp, oxe_srv **out) {
     if (!engine || !out) return -1;
+    oxe::Engine *e = (oxe::Engine *)engine;
+    if (mtp) {
+        if (const char *rk = std::getenv("OXE_MTP_DRAFT_VOCAB")) {
+            long long k = -1;
+            if (const char *ks = std::getenv("OXE_MTP_DRAFT_K")) {
+                char *end = nullptr;
+                const long long v = std::strtoll(ks, &end, 10);
+                if (end && *end == 0 && v >= 0) k = v;   // unparsable: no cut, as the reference's .ok()
+            }
+            std::vector<uint32_t> ids;
+            if (read_ranking(rk, k, ids)) return -1;
+            if (ids.empty()) {
+                oxe::set_err("empty draft vocabulary");
+                return -1;
+            }
+            const int rows = e->set_draft_vocab(ids.data(), (int)ids.size());
+            if (rows < 0) {
+                if (rows == -1) oxe::set_err("empty draft vocabulary");
+                return rows;
+            }
+            if (rows > 0) fprintf(stderr, "oxe-server: MTP draft head restricted to %d rows\n", rows);
+        }
+    }
     SrvEngine *s = new SrvEngine();
-    s->e = (oxe::Engine *)engine;
+    s->e = e;
     s->mtp = mtp != 0;
     if (s->mtp) s->mtp_sync(nullptr);
     *out = (oxe_srv *)s;

@@ -273,6 +273,7 @@ def _engine_sigs(L):
         "oxe_mtp_device_steps": (i32, [vp, i32, i32]),
         "oxe_mtp_device_end": (i32, [vp, u32p, i32, C.POINTER(C.c_int), u32p]),
         "oxe_mtp_set_force": (i32, [vp, C.POINTER(C.c_int32), i32]),
+        "oxe_mtp_set_draft_vocab": (i32, [vp, C.POINTER(C.c_uint32), i32]),
         "oxe_mtp_stats": (i32, [vp, C.POINTER(C.c_int64)]),
         "oxe_mtp_step_force": (i32, [vp, C.c_uint32, u32p, C.POINTER(C.c_int), C.POINTER(C.c_int64), i32]),
         "oxe_mtp_set_depth": (i32, [vp, i32]),
@@ -716,6 +717,16 @@ class Engine:
 
     def mtp_rewind(self, m):
         check(lib().oxe_mtp_rewind(self.h, m), "mtp_rewind")
+
+    def mtp_set_draft_vocab(self, ids):
+        """restrict every MTP draft run's LM head to the output rows of `ids` (MtpWeights::set_draft_vocab);
+        an empty list restores the whole head. Returns the draft head's rows."""
+        import numpy as np
+        v = np.ascontiguousarray(ids, np.uint32)
+        rc = lib().oxe_mtp_set_draft_vocab(self.h, v.ctypes.data_as(C.POINTER(C.c_uint32)), len(v))
+        if rc < 0:
+            raise EngineError(f"mtp_set_draft_vocab: {_last_error() or rc}")
+        return rc
 
     def mtp_set_force(self, force):
         import numpy as np

@@ -125,3 +125,23 @@ def test_typed_engine_mtp_steps_match_oracle_driver(typed_file):
     assert [int(t) for t in gen] == want
     assert nxt == x
     g.close()
+
+
+def test_typed_engine_restricted_draft_head_matches_oracle(typed_file):
+    """the restricted draft head over a Q6_K LM head (rows gathered from the file's blocks)"""
+    import oxe_amd as A
+    d, ty, path = typed_file
+    g = A.Engine.from_gguf(path, n_ctx=512)
+    ref = O.Engine(d, seed=SEED, n_ctx=512, types=ty)
+    vocab = [i for i in range(d.n_vocab) if i % 5 == 1]
+    assert g.mtp_set_draft_vocab(vocab) == (len(vocab) + 15) // 16 * 16
+    ref.set_draft_vocab(vocab)
+    for t in (3, 17, 42):
+        assert g.step(t) == ref.step(t)
+    h = np.asarray(ref.hidden(0), np.float32).copy()
+    for i, tok in enumerate((77, 1234, 9)):
+        got = g.mtp_run([tok], 3 + i, h[None, :])
+        want = ref.mtp_run([tok], 3 + i, h[None, :])
+        assert got == want and got % 5 == 1, i
+        h = np.asarray(ref.hidden(0), np.float32).copy()
+    g.close()

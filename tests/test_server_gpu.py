@@ -323,3 +323,33 @@ def test_trait_errors(d, prompt):
     with pytest.raises(A.EngineError, match="rewind without a step"):
         s.spec_rewind(1)
     assert s.n_past() == 0
+
+
+def test_draft_vocab_from_the_environment(d, prompt, plain, tmp_path, monkeypatch):
+    """OXE_MTP_DRAFT_VOCAB=<ranking> [OXE_MTP_DRAFT_K=<k>] (oxe_engine.rs:215-222): the draft head is
+    restricted to the ranking's first k ids (lines that do not start with an id are skipped); the
+    output is still the greedy sequence. A missing file or a ranking with no id is refused."""
+    import oxe_amd as A
+    rk = tmp_path / "ranking.txt"
+    ids = [i for i in range(d.n_vocab) if i % 3 == 0]
+    rk.write_text("# most frequent first\n" + "\n".join(f"{i} {100 - j}" for j, i in enumerate(ids)) + "\n")
+    monkeypatch.setenv("OXE_MTP_DRAFT_VOCAB", str(rk))
+    monkeypatch.setenv("OXE_MTP_DRAFT_K", "500")
+    s = server(d, True)
+    x = first_max(s.prefill(prompt))
+    out = [x]
+    while len(out) < 24:
+        _, g = s.decode_spec_argmax(x)
+        out += g
+        x = g[-1]
+    assert out == plain[:len(out)]
+    s.close()
+    monkeypatch.setenv("OXE_MTP_DRAFT_VOCAB", str(tmp_path / "missing.txt"))
+    e = A.Engine(d, seed=SEED, n_ctx=N_CTX)
+    with pytest.raises(RuntimeError, match="cannot be read"):
+        A.ServerEngine(e, mtp=True)
+    (tmp_path / "empty.txt").write_text("not an id\n")
+    monkeypatch.setenv("OXE_MTP_DRAFT_VOCAB", str(tmp_path / "empty.txt"))
+    with pytest.raises(RuntimeError, match="empty draft vocabulary"):
+        A.ServerEngine(e, mtp=True)
+    e.close()
