@@ -215,6 +215,94 @@ void oxo_quantize_row_q8_K(const float *x, void *vy, int64_t k) {
     }
 }
 
+// dequantize_row_q{3,4,5,6}_K (vendor/ggml-subset/generated/quants_base.c:80-230), as the reference
+// builds them: GCC with its default -ffp-contract=fast (crates/kernels-sys/build.rs:5-7), so the
+// Q4_K / Q5_K element d1 * q - m1 is one fused multiply-subtract; Q3_K and Q6_K are products only.
+// type: 11 Q3_K, 12 Q4_K, 13 Q5_K, 14 Q6_K. Returns 1, or 0 for another type.
+int oxo_dequantize_row_kq(int type, const void *vx, float *y, int64_t k) {
+    const uint8_t *x = (const uint8_t *)vx;
+    const int64_t nb = k / QK;
+    auto f16 = [](const uint8_t *p) { uint16_t h; memcpy(&h, p, 2); return oxo_f16_to_f32(h); };
+    switch (type) {
+        case 12: case 13: {
+            const int bb = type == 12 ? 144 : 176;
+            for (int64_t i = 0; i < nb; i++) {
+                const uint8_t *b = x + i * bb;
+                const float d = f16(b), mn = f16(b + 2);
+                const uint8_t *sc = b + 4, *qh = b + 16, *q = b + (type == 12 ? 16 : 48);
+                for (int j = 0, is = 0; j < QK; j += 64, is += 2) {
+                    int s1, m1i, s2, m2i;
+                    scale_min_k4(is, sc, &s1, &m1i);
+                    scale_min_k4(is + 1, sc, &s2, &m2i);
+                    const float d1 = d * (float)s1, m1 = mn * (float)m1i;
+                    const float d2 = d * (float)s2, m2 = mn * (float)m2i;
+                    const int u1 = 1 << (j / 32), u2 = 2 << (j / 32);
+                    for (int l = 0; l < 32; ++l) {
+                        const int qq = (q[l] & 0xF) + (type == 13 && (qh[l] & u1) ? 16 : 0);
+                        *y++ = fmaf(d1, (float)qq, -m1);
+                    }
+                    for (int l = 0; l < 32; ++l) {
+                        const int qq = (q[l] >> 4) + (type == 13 && (qh[l] & u2) ? 16 : 0);
+                        *y++ = fmaf(d2, (float)qq, -m2);
+                    }
+                    q += 32;
+                }
+            }
+            return 1;
+        }
+        case 14:
+            for (int64_t i = 0; i < nb; i++) {
+                const uint8_t *b = x + i * 210;
+                const float d = f16(b + 208);
+                const uint8_t *ql = b, *qh = b + 128;
+                const int8_t *sc = (const int8_t *)(b + 192);
+                for (int n = 0; n < QK; n += 128) {
+                    for (int l = 0; l < 32; ++l) {
+                        const int is = l / 16;
+                        const int8_t q1 = (int8_t)((ql[l + 0] & 0xF) | (((qh[l] >> 0) & 3) << 4)) - 32;
+                        const int8_t q2 = (int8_t)((ql[l + 32] & 0xF) | (((qh[l] >> 2) & 3) << 4)) - 32;
+                        const int8_t q3 = (int8_t)((ql[l + 0] >> 4) | (((qh[l] >> 4) & 3) << 4)) - 32;
+                        const int8_t q4 = (int8_t)((ql[l + 32] >> 4) | (((qh[l] >> 6) & 3) << 4)) - 32;
+                        y[l + 0] = d * (float)sc[is + 0] * (float)q1;
+                        y[l + 32] = d * (float)sc[is + 2] * (float)q2;
+                        y[l + 64] = d * (float)sc[is + 4] * (float)q3;
+                        y[l + 96] = d * (float)sc[is + 6] * (float)q4;
+                    }
+                    y += 128;
+                    ql += 64;
+                    qh += 32;
+                    sc += 8;
+                }
+            }
+            return 1;
+        case 11:
+            for (int64_t i = 0; i < nb; i++) {
+                const uint8_t *b = x + i * 110;
+                const float d_all = f16(b + 108);
+                const uint8_t *q = b + 32, *hm = b;
+                uint8_t raw[16];
+                q3k_raw(b + 96, raw);
+                int is = 0;
+                uint8_t m = 1;
+                for (int n = 0; n < QK; n += 128) {
+                    int shift = 0;
+                    for (int j = 0; j < 4; ++j) {
+                        float dl = d_all * (float)(raw[is++] - 32);
+                        for (int l = 0; l < 16; ++l) *y++ = dl * (float)((int)((q[l + 0] >> shift) & 3) - ((hm[l + 0] & m) ? 0 : 4));
+                        dl = d_all * (float)(raw[is++] - 32);
+                        for (int l = 0; l < 16; ++l) *y++ = dl * (float)((int)((q[l + 16] >> shift) & 3) - ((hm[l + 16] & m) ? 0 : 4));
+                        shift += 2;
+                        m <<= 1;
+                    }
+                    q += 32;
+                }
+            }
+            return 1;
+        default:
+            return 0;
+    }
+}
+
 // oxe_vl_gemv (crates/kernels-sys/csrc/oxe_vl.inc:78-107) per lane: s[l*nr + r] = row r of w
 // (nb = k/256 blocks of the type, rows contiguous) . lane l of y (nb q8_K blocks per lane).
 // type 3 Q3_K, 4 Q4_K, 5 Q5_K, 6 Q6_K. Returns 1, or 0 (nothing written) for another type.
@@ -239,8 +327,10 @@ int oxo_vl_gemv(int type, int64_t k, int64_t nr, int nl, const void *w, const vo
 // Synthetic K-quant tensors for the tests' model files (not the reference's: its models come from
 // files). Block i of tensor (seed, layer, kind), flat over [expert][row][k / 256], is filled with
 // the 64-bit words oxe_rng(key, 32 i + j), then its fp16 fields are set from the scale key:
-// Q4_K / Q5_K d, dmin in [0.0005, 0.004); Q6_K d in [0.00005, 0.0003); Q3_K d in [0.0005, 0.004).
-// Codes, 6-bit scales and mins stay whatever the words hold (every bit pattern is a valid block).
+// Q4_K / Q5_K d in [0.0005, 0.004) and dmin = fp16(d * mean code) (7.5 for Q4_K, 15.5 for Q5_K, so
+// the block's weights d * scale * code - dmin * min average about zero, as a trained model's do);
+// Q6_K d in [0.00005, 0.0003); Q3_K d in [0.0005, 0.004). Codes, 6-bit scales and mins stay
+// whatever the words hold (every bit pattern is a valid block).
 // type: 11 Q3_K, 12 Q4_K, 13 Q5_K, 14 Q6_K (ggml ids). Returns the bytes written, or 0.
 int64_t oxo_synth_kq(uint64_t seed, int layer, int kind, int type, int64_t expert, int64_t rows, int64_t k, uint8_t *out) {
     int bb;
@@ -273,12 +363,14 @@ int64_t oxo_synth_kq(uint64_t seed, int layer, int kind, int type, int64_t exper
         memcpy(blk, tmp, bb);
         uint16_t h0, h1;
         switch (type) {
-            case 12: case 13:
+            case 12: case 13: {
                 h0 = f16_in(2 * bi, 0.0005f, 0.004f);
-                h1 = f16_in(2 * bi + 1, 0.0005f, 0.004f);
+                const float dv = oxo_f16_to_f32(h0) * (type == 12 ? 7.5f : 15.5f);
+                h1 = oxe_f32_to_f16_rne(dv);
                 memcpy(blk, &h0, 2);
                 memcpy(blk + 2, &h1, 2);
                 break;
+            }
             case 14:
                 h0 = f16_in(2 * bi, 0.00005f, 0.0003f);
                 memcpy(blk + 208, &h0, 2);

@@ -298,8 +298,16 @@ struct oxo_engine {
         return L.experts[e][which];
     }
 
+    Mat tok_embd_k;   // a K-quant token embedding (its rows dequantised per token)
     std::vector<float> embed(uint32_t tok) {
         const int64_t E = d.n_embd;
+        if (tok_embd_k.type != 8) {
+            // dequantize_row of the token's row (engine.rs:2251-2256)
+            std::vector<float> y(E);
+            const size_t rb = (size_t)(E / 256) * kq_block_bytes(tok_embd_k.type);
+            oxo_dequantize_row_kq(tok_embd_k.type, tok_embd_k.raw.data() + (size_t)tok * rb, y.data(), E);
+            return y;
+        }
         std::vector<int8_t> q(E);
         std::vector<uint16_t> dd(E / 32);
         const uint64_t key = oxe_tensor_key(seed, OXE_GLOBAL_LAYER, OXE_T_TOK_EMBD);
@@ -389,6 +397,7 @@ struct oxo_engine {
         }
         out_norm = gen_f32(seed, OXE_GLOBAL_LAYER, OXE_T_OUT_NORM, E);
         gen_mat(OXE_GLOBAL_LAYER, OXE_T_OUTPUT, d.n_vocab, E, 0, output);
+        if (type_of(OXE_GLOBAL_LAYER, OXE_T_TOK_EMBD) != 8) gen_mat(OXE_GLOBAL_LAYER, OXE_T_TOK_EMBD, d.n_vocab, E, 0, tok_embd_k);
         conv_len = (d.ssm_conv_kernel - 1) * nch;
         ssm_len = nv * hv * hv;
         conv_state.assign((size_t)n_slots * n_rec * conv_len, 0.0f);
@@ -1374,8 +1383,8 @@ oxo_engine *oxo_engine_new_lanes(const oxe_model_desc *d, uint64_t seed, int64_t
     return e;
 }
 // with each matrix's ggml type from types[layer * 64 + kind] (layer OXE_GLOBAL_LAYER: the global
-// tensors): Q8_0 (8) anywhere; K-quants (11..14) for the expert, shared-expert and output matrices;
-// F32 (0) for ssm_beta / ssm_alpha. Null for another combination.
+// tensors): Q8_0 (8) anywhere; K-quants (11..14) anywhere but the MTP entry's eh_proj; F32 (0) for
+// ssm_beta / ssm_alpha. Null for another combination.
 oxo_engine *oxo_engine_new_typed(const oxe_model_desc *d, uint64_t seed, int64_t n_ctx, int n_slots, const int32_t *types) {
     if (n_slots < 1 || n_slots > 8 || !types) return nullptr;
     oxo_engine *e = new oxo_engine();
@@ -1384,9 +1393,7 @@ oxo_engine *oxo_engine_new_typed(const oxe_model_desc *d, uint64_t seed, int64_t
         for (int k = 0; k < 64; k++) {
             const int32_t t = types[l * 64 + k];
             if (!oxe_kind_is_q8(k)) continue;
-            const bool kq = t >= 11 && t <= 14, ok = t == 8 ||
-                (kq && (k == OXE_T_GATE_EXPS || k == OXE_T_UP_EXPS || k == OXE_T_DOWN_EXPS || k == OXE_T_GATE_SHEXP ||
-                        k == OXE_T_UP_SHEXP || k == OXE_T_DOWN_SHEXP || k == OXE_T_OUTPUT)) ||
+            const bool kq = t >= 11 && t <= 14, ok = t == 8 || (kq && k != OXE_T_EH_PROJ) ||
                 (t == 0 && (k == OXE_T_DN_BETA || k == OXE_T_DN_ALPHA));
             if (!ok) {
                 delete e;

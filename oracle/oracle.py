@@ -128,6 +128,7 @@ def lib():
             "oxo_mtp_entry": (None, [C.c_void_p, u32p, C.c_int, f32p, f32p]),
             "oxo_engine_set_router": (None, [C.c_void_p, C.c_int, C.c_int, C.c_int, f32p]),
             "oxo_synth_q8": (None, [C.c_uint64, C.c_int, C.c_int, C.c_int64, C.c_int64, C.c_int64, i8p, u16p]),
+            "oxo_dequantize_row_kq": (C.c_int, [C.c_int, C.c_void_p, f32p, C.c_int64]),
             "oxo_synth_kq": (C.c_int64, [C.c_uint64, C.c_int, C.c_int, C.c_int, C.c_int64, C.c_int64, C.c_int64,
                                          C.POINTER(C.c_uint8)]),
             "oxo_synth_f32": (None, [C.c_uint64, C.c_int, C.c_int, C.c_int64, f32p]),
@@ -226,6 +227,14 @@ def synth_kq(seed, layer, kind, ty, rows, k, expert=0):
     n = lib().oxo_synth_kq(seed, layer, kind, ty, expert, rows, k, ptr(out, C.c_uint8))
     assert n == out.size
     return out
+
+
+def dequantize_row_kq(ty, raw, k):
+    """dequantize_row_q*_K (ggml type 11..14) of one row of k / 256 blocks -> f32 [k]"""
+    b = np.ascontiguousarray(raw, np.uint8)
+    y = np.empty(k, np.float32)
+    assert lib().oxo_dequantize_row_kq(ty, b.ctypes.data_as(C.c_void_p), ptr(y, C.c_float), k) == 1
+    return y
 
 
 def synth_f32(seed, layer, kind, n):

@@ -45,6 +45,8 @@ void oxo_quantize_row_q8_K(const float *x, void *y, int64_t k);
 int  oxo_vl_gemv(int type, int64_t k, int64_t nr, int nl, const void *w, const void *y, float *s);
 // synthetic K-quant tensor bytes (ggml type 11..14, rows x k/256 blocks of expert `expert`) for the
 // tests' model files; returns the bytes written or 0
+// dequantize_row_q{3,4,5,6}_K as the reference builds it (types 11..14); 1, or 0 for another type
+int oxo_dequantize_row_kq(int type, const void *x, float *y, int64_t k);
 int64_t oxo_synth_kq(uint64_t seed, int layer, int kind, int type, int64_t expert, int64_t rows, int64_t k, uint8_t *out);
 
 // ---- f32 / f16 vector helpers (vendor/ggml-subset/generated/upstream/src/ggml-cpu/vec.{h,cpp})
