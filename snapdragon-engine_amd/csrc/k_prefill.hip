@@ -128,6 +128,7 @@ __global__ __launch_bounds__(256) void delta_kernel(const float *cy, const float
     // two 16-byte reads)
     __shared__ __align__(16) float s_qk[2][DT_T][2][16][8];
     __shared__ float s_v[2][DT_T][16], s_g[2][DT_T], s_b[2][DT_T], s_out[2][DT_T][16];
+    __shared__ float s_junk[256];   // the output stores of the chains other than chain 0
     const int vh = blockIdx.x >> 3, row0 = (blockIdx.x & 7) * 16, kh = vh % NKH;
     const int t = threadIdx.x, rg = t >> 4, cc = t & 15;
     float *srow = ssm + ((int64_t)vh * HV + row0 + rg) * HV;
@@ -195,27 +196,30 @@ __global__ __launch_bounds__(256) void delta_kernel(const float *cy, const float
                 acc = __builtin_fmaf(r[s], qc[s], acc);
             }
             const float sq = dot16_tree_dpp(acc);
-            if (cc == 0) s_out[buf][tt][rg] = sq * scale;
+            // every chain stores (chain 0 the row's output), so no branch splits the token loop and
+            // this token's output dot overlaps the next token's recurrence
+            float *dst = cc == 0 ? &s_out[buf][tt][rg] : &s_junk[t];
+            *dst = sq * scale;
         };
         // tokens in pairs, each token's q / k read from LDS while the previous one runs
         float ka[8], qa[8], kb[8], qb[8], ga, ba, va, gb2, bb, vb;
         ld8(s_qk[buf][0][0][cc], qa);
         ld8(s_qk[buf][0][1][cc], ka);
         gbv(0, ga, ba, va);
-        for (int tt = 0; tt < nt; tt += 2) {
-            const int t1 = tt + 1 < DT_T ? tt + 1 : DT_T - 1;
+        // full pairs without a branch inside, then an odd last token
+        int tt = 0;
+        for (; tt + 1 < nt; tt += 2) {
+            const int t1 = tt + 1, t2 = tt + 2 < DT_T ? tt + 2 : DT_T - 1;
             ld8(s_qk[buf][t1][0][cc], qb);
             ld8(s_qk[buf][t1][1][cc], kb);
             gbv(t1, gb2, bb, vb);
             step(tt, ka, qa, ga, ba, va);
-            if (tt + 1 < nt) {
-                const int t2 = tt + 2 < DT_T ? tt + 2 : DT_T - 1;
-                ld8(s_qk[buf][t2][0][cc], qa);
-                ld8(s_qk[buf][t2][1][cc], ka);
-                gbv(t2, ga, ba, va);
-                step(tt + 1, kb, qb, gb2, bb, vb);
-            }
+            ld8(s_qk[buf][t2][0][cc], qa);
+            ld8(s_qk[buf][t2][1][cc], ka);
+            gbv(t2, ga, ba, va);
+            step(tt + 1, kb, qb, gb2, bb, vb);
         }
+        if (tt < nt) step(tt, ka, qa, ga, ba, va);
         if (more) put(buf ^ 1);
         __syncthreads();
         // the stage's outputs, coalesced (the buffer is rewritten two stages later, after a barrier)
