@@ -206,9 +206,8 @@ __global__ __launch_bounds__(256) void delta_kernel(const float *cy, const float
         ld8(s_qk[buf][0][0][cc], qa);
         ld8(s_qk[buf][0][1][cc], ka);
         gbv(0, ga, ba, va);
-        // full pairs without a branch inside, then an odd last token
-        int tt = 0;
-        for (; tt + 1 < nt; tt += 2) {
+        // tokens tt, tt + 1 without a branch inside
+        auto pair = [&](int tt) {
             const int t1 = tt + 1, t2 = tt + 2 < DT_T ? tt + 2 : DT_T - 1;
             ld8(s_qk[buf][t1][0][cc], qb);
             ld8(s_qk[buf][t1][1][cc], kb);
@@ -218,8 +217,16 @@ __global__ __launch_bounds__(256) void delta_kernel(const float *cy, const float
             ld8(s_qk[buf][t2][1][cc], ka);
             gbv(t2, ga, ba, va);
             step(tt + 1, kb, qb, gb2, bb, vb);
+        };
+        if (nt == DT_T) {
+            // a whole stage unrolled: every LDS address is a constant offset
+#pragma unroll
+            for (int tt = 0; tt < DT_T; tt += 2) pair(tt);
+        } else {
+            int tt = 0;
+            for (; tt + 1 < nt; tt += 2) pair(tt);
+            if (tt < nt) step(tt, ka, qa, ga, ba, va);
         }
-        if (tt < nt) step(tt, ka, qa, ga, ba, va);
         if (more) put(buf ^ 1);
         __syncthreads();
         // the stage's outputs, coalesced (the buffer is rewritten two stages later, after a barrier)
