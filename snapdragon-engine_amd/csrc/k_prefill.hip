@@ -219,9 +219,26 @@ __global__ __launch_bounds__(256) void delta_kernel(const float *cy, const float
             step(tt + 1, kb, qb, gb2, bb, vb);
         };
         if (nt == DT_T) {
-            // a whole stage unrolled: every LDS address is a constant offset
+            // a whole stage unrolled (every LDS address a constant offset), each token's operands
+            // read two tokens ahead (three register sets in rotation)
+            float qs[3][8], ks[3][8], gs[3], bs[3], vs[3];
 #pragma unroll
-            for (int tt = 0; tt < DT_T; tt += 2) pair(tt);
+            for (int i = 0; i < 8; i++) { qs[0][i] = qa[i]; ks[0][i] = ka[i]; }
+            gs[0] = ga; bs[0] = ba; vs[0] = va;
+            ld8(s_qk[buf][1][0][cc], qs[1]);
+            ld8(s_qk[buf][1][1][cc], ks[1]);
+            gbv(1, gs[1], bs[1], vs[1]);
+#pragma unroll
+            for (int tt = 0; tt < DT_T; tt++) {
+                if (tt + 2 < DT_T) {
+                    const int n = (tt + 2) % 3;
+                    ld8(s_qk[buf][tt + 2][0][cc], qs[n]);
+                    ld8(s_qk[buf][tt + 2][1][cc], ks[n]);
+                    gbv(tt + 2, gs[n], bs[n], vs[n]);
+                }
+                const int c3 = tt % 3;
+                step(tt, ks[c3], qs[c3], gs[c3], bs[c3], vs[c3]);
+            }
         } else {
             int tt = 0;
             for (; tt + 1 < nt; tt += 2) pair(tt);
