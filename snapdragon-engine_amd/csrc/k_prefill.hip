@@ -482,32 +482,55 @@ __global__ __launch_bounds__(256, 2) void attn_gqa_kernel(const uint16_t *qh, co
     __syncthreads();
     const int j = tid & 3;
     {
+        // thread (positions pp and pp + 64 of a pass of 128, chain quad j): each query chunk read
+        // from LDS serves both positions
         const int pp = tid >> 2;
         const uint16_t *kb = kc + (int64_t)kvh * n_ctx * HD;
-        for (int p0 = 0; p0 <= pos; p0 += 64) {
-            const int p = p0 + pp;
-            const uint16_t *krow = kb + (int64_t)(p <= pos ? p : pos) * HD;
-            uint4 kvs[HD / 32];
+        // the next pass's K chunks load while this pass runs (rows past pos clamped to pos)
+        uint4 kva[HD / 32], kvb[HD / 32];
+        auto kload = [&](int p0, uint4 (&xa)[HD / 32], uint4 (&xb)[HD / 32]) {
+            const int pa = p0 + pp, pb = p0 + 64 + pp;
+            const uint16_t *ka = kb + (int64_t)(pa <= pos ? pa : pos) * HD;
+            const uint16_t *kr = kb + (int64_t)(pb <= pos ? pb : pos) * HD;
 #pragma unroll
-            for (int sx = 0; sx < HD / 32; sx++) kvs[sx] = *(const uint4 *)(krow + 32 * sx + 8 * j);
-            // one query head at a time (two in flight): its score is finished and stored before the
-            // next head's query chunks are read, so only the K chunks stay in registers
+            for (int sx = 0; sx < HD / 32; sx++) {
+                xa[sx] = *(const uint4 *)(ka + 32 * sx + 8 * j);
+                xb[sx] = *(const uint4 *)(kr + 32 * sx + 8 * j);
+            }
+        };
+        kload(0, kva, kvb);
+        for (int p0 = 0; p0 <= pos; p0 += 128) {
+            const int pa = p0 + pp, pb = p0 + 64 + pp;
+            uint4 nka[HD / 32], nkb[HD / 32];
+            kload(p0 + 128, nka, nkb);
+            // one query head at a time: its two scores are finished and stored before the next
+            // head's query chunks are read, so only the K chunks stay in registers
 #pragma unroll 2
             for (int h = 0; h < GQA; h++) {
-                h2p acc[4];
+                h2p acc[4], acb[4];
 #pragma unroll
-                for (int i = 0; i < 4; i++) acc[i] = h2p{(_Float16)0.0f, (_Float16)0.0f};
+                for (int i = 0; i < 4; i++) acc[i] = acb[i] = h2p{(_Float16)0.0f, (_Float16)0.0f};
 #pragma unroll
                 for (int sx = 0; sx < HD / 32; sx++) {
-                    const uint4 kv = kvs[sx];
                     const uint4 qv = *(const uint4 *)(&s_q[h][32 * sx + 8 * j]);
+                    const uint4 kv = kva[sx], kw = kvb[sx];
                     acc[0] = __builtin_elementwise_fma(u2h(kv.x), u2h(qv.x), acc[0]);
                     acc[1] = __builtin_elementwise_fma(u2h(kv.y), u2h(qv.y), acc[1]);
                     acc[2] = __builtin_elementwise_fma(u2h(kv.z), u2h(qv.z), acc[2]);
                     acc[3] = __builtin_elementwise_fma(u2h(kv.w), u2h(qv.w), acc[3]);
+                    acb[0] = __builtin_elementwise_fma(u2h(kw.x), u2h(qv.x), acb[0]);
+                    acb[1] = __builtin_elementwise_fma(u2h(kw.y), u2h(qv.y), acb[1]);
+                    acb[2] = __builtin_elementwise_fma(u2h(kw.z), u2h(qv.z), acb[2]);
+                    acb[3] = __builtin_elementwise_fma(u2h(kw.w), u2h(qv.w), acb[3]);
                 }
-                const float sc = f16x8_reduce_quad(acc);
-                if (j == 0 && p <= pos) s_s[h * kv_cap + p] = sc;
+                const float sa = f16x8_reduce_quad(acc), sb = f16x8_reduce_quad(acb);
+                if (j == 0 && pa <= pos) s_s[h * kv_cap + pa] = sa;
+                if (j == 0 && pb <= pos) s_s[h * kv_cap + pb] = sb;
+            }
+#pragma unroll
+            for (int sx = 0; sx < HD / 32; sx++) {
+                kva[sx] = nka[sx];
+                kvb[sx] = nkb[sx];
             }
         }
     }
@@ -553,24 +576,35 @@ __global__ __launch_bounds__(256, 2) void attn_gqa_kernel(const uint16_t *qh, co
     __syncthreads();
     const uint16_t *vb = vt + (int64_t)kvh * HD * n_ctx;
     const float *gate = proj + t * DN_ROWS + kvh * GQA * 2 * HD + HD;
-    for (int d0 = 0; d0 < HD; d0 += 64) {
+    // thread (dims d and d + 64 of a pass of 128, chain quad j): each probability chunk read from
+    // LDS serves both dims
+    for (int d0 = 0; d0 < HD; d0 += 128) {
         const int d = d0 + (tid >> 2);
-        const uint16_t *vrow = vb + (int64_t)d * n_ctx;
-        h2p acc[GQA][4];
+        const uint16_t *vrow = vb + (int64_t)d * n_ctx, *vrw = vrow + (int64_t)64 * n_ctx;
+        h2p acc[GQA][4], acb[GQA][4];
 #pragma unroll
         for (int h = 0; h < GQA; h++)
 #pragma unroll
-            for (int i = 0; i < 4; i++) acc[h][i] = h2p{(_Float16)0.0f, (_Float16)0.0f};
-        // n_kv is a multiple of 256: blocks of 32 positions in groups of 4, the group's V^T loads first
-        for (int sx0 = 0; sx0 < n_kv / 32; sx0 += 4) {
-          uint4 vvs[4];
+            for (int i = 0; i < 4; i++) acc[h][i] = acb[h][i] = h2p{(_Float16)0.0f, (_Float16)0.0f};
+        // n_kv is a multiple of 256: blocks of 32 positions in pairs, the pair's V^T loads first
+        // the next pair's V^T chunks load while this pair runs (the last pair loads itself again)
+        uint4 vvs[2], vws[2];
+        auto vload = [&](int sx0, uint4 (&xa)[2], uint4 (&xb)[2]) {
 #pragma unroll
-          for (int u = 0; u < 4; u++) vvs[u] = *(const uint4 *)(vrow + 32 * (sx0 + u) + 8 * j);
+            for (int u = 0; u < 2; u++) {
+                xa[u] = *(const uint4 *)(vrow + 32 * (sx0 + u) + 8 * j);
+                xb[u] = *(const uint4 *)(vrw + 32 * (sx0 + u) + 8 * j);
+            }
+        };
+        vload(0, vvs, vws);
+        for (int sx0 = 0; sx0 < n_kv / 32; sx0 += 2) {
+          uint4 nvv[2], nvw[2];
+          vload(sx0 + 2 < n_kv / 32 ? sx0 + 2 : sx0, nvv, nvw);
 #pragma unroll
-          for (int u = 0; u < 4; u++) {
+          for (int u = 0; u < 2; u++) {
             const int sx = sx0 + u;
             const int p = 32 * sx + 8 * j;   // this lane's 8 positions p .. p + 7 (chain quad j of block sx)
-            uint4 vv = vvs[u];
+            uint4 vv = vvs[u], vw = vws[u];
             if (p + 7 > pos) {   // V^T of positions after pos is +0 in a single-token step
                 uint32_t m[4];
 #pragma unroll
@@ -579,6 +613,7 @@ __global__ __launch_bounds__(256, 2) void attn_gqa_kernel(const uint16_t *qh, co
                     m[i] = q0 > pos ? 0u : (q0 + 1 > pos ? 0xffffu : 0xffffffffu);
                 }
                 vv.x &= m[0]; vv.y &= m[1]; vv.z &= m[2]; vv.w &= m[3];
+                vw.x &= m[0]; vw.y &= m[1]; vw.z &= m[2]; vw.w &= m[3];
             }
 #pragma unroll
             for (int h = 0; h < GQA; h++) {
@@ -587,13 +622,25 @@ __global__ __launch_bounds__(256, 2) void attn_gqa_kernel(const uint16_t *qh, co
                 acc[h][1] = __builtin_elementwise_fma(u2h(vv.y), u2h(pv.y), acc[h][1]);
                 acc[h][2] = __builtin_elementwise_fma(u2h(vv.z), u2h(pv.z), acc[h][2]);
                 acc[h][3] = __builtin_elementwise_fma(u2h(vv.w), u2h(pv.w), acc[h][3]);
+                acb[h][0] = __builtin_elementwise_fma(u2h(vw.x), u2h(pv.x), acb[h][0]);
+                acb[h][1] = __builtin_elementwise_fma(u2h(vw.y), u2h(pv.y), acb[h][1]);
+                acb[h][2] = __builtin_elementwise_fma(u2h(vw.z), u2h(pv.z), acb[h][2]);
+                acb[h][3] = __builtin_elementwise_fma(u2h(vw.w), u2h(pv.w), acb[h][3]);
             }
+          }
+#pragma unroll
+          for (int u = 0; u < 2; u++) {
+            vvs[u] = nvv[u];
+            vws[u] = nvw[u];
           }
         }
 #pragma unroll
         for (int h = 0; h < GQA; h++) {
-            const float out = f16x8_reduce_quad(acc[h]);
-            if (j == 0) o[t * MIX_W + (kvh * GQA + h) * HD + d] = out * sigmoid_c(gate[h * 2 * HD + d]);
+            const float oa = f16x8_reduce_quad(acc[h]), ob = f16x8_reduce_quad(acb[h]);
+            if (j == 0) {
+                o[t * MIX_W + (kvh * GQA + h) * HD + d] = oa * sigmoid_c(gate[h * 2 * HD + d]);
+                o[t * MIX_W + (kvh * GQA + h) * HD + d + 64] = ob * sigmoid_c(gate[h * 2 * HD + d + 64]);
+            }
         }
     }
 }
