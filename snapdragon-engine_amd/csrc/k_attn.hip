@@ -131,6 +131,7 @@ struct PvArgs {
     const uint16_t *vt;     // this layer's V^T [NKV*HD][n_ctx]
     int8_t *oq;             // [NL][MIX_W]
     uint16_t *od;
+    float *o32;             // optional: the gated outputs in f32 [NL][MIX_W] (a K-quant attn_output)
     int n_ctx;
 };
 
@@ -219,6 +220,7 @@ __global__ __launch_bounds__(256) void pv_kernel(const RunCtl *__restrict__ ctl,
         if (j == 0) {
             const float gate = a.proj[(int64_t)l * DN_ROWS + h * 2 * HD + HD + dg];
             s_o[d] = out * sigmoid_c(gate);
+            if (a.o32) a.o32[(int64_t)l * MIX_W + h * HD + dg] = s_o[d];
         }
     }
     __syncthreads();
@@ -228,8 +230,9 @@ __global__ __launch_bounds__(256) void pv_kernel(const RunCtl *__restrict__ ctl,
     }
 }
 
-void launch_pv(const RunCtl *ctl, const ModelRt &m, const LayerW &w, const ActBufs &b, hipStream_t st) {
+void launch_pv(const RunCtl *ctl, const ModelRt &m, const LayerW &w, const ActBufs &b, hipStream_t st, float *o32) {
     PvArgs a{};
+    a.o32 = o32;
     a.proj = b.proj;
     a.scores = b.scores;
     a.vt = m.vcache + (int64_t)w.index * NKV * HD * m.n_ctx;

@@ -836,6 +836,109 @@ __global__ __launch_bounds__(1024) void kq_argmax_kernel(const RunCtl *__restric
     }
 }
 
+// ---- K-quant mixer matrices and token embedding in the per-phase runs ----------------------------
+// dequantize_row_q{3,4,5,6}_K (vendor/ggml-subset/generated/quants_base.c:80-230) of element i of
+// one 256-weight block b (type 11..14), as the reference builds it: GCC's default contraction
+// (crates/kernels-sys/build.rs:5-7) makes the Q4_K / Q5_K element (d * scale) * code - dmin * min
+// one fused multiply-subtract; Q3_K and Q6_K are products in source order.
+OXE_DEV float ld_f16u(const uint8_t *p) { return h2f((uint16_t)(p[0] | (p[1] << 8))); }
+OXE_DEV float kq_elem(int type, const uint8_t *b, int i) {
+    switch (type) {
+        case 12:
+        case 13: {
+            const float d = ld_f16u(b), mn = ld_f16u(b + 2);
+            const int c = i >> 6, hi = (i >> 5) & 1, l = i & 31;
+            const uint8_t *q = b + (type == 12 ? 16 : 48) + 32 * c;
+            int sc, mi;
+            scale_min_k4(2 * c + hi, b + 4, sc, mi);
+            int qq = hi ? (q[l] >> 4) : (q[l] & 0xF);
+            if (type == 13 && (b[16 + l] & ((1 + hi) << (2 * c)))) qq += 16;
+            return __builtin_fmaf(d * (float)sc, (float)qq, -(mn * (float)mi));
+        }
+        case 14: {
+            const float d = ld_f16u(b + 208);
+            const int n = i >> 7, r = i & 127, qd = r >> 5, l = r & 31;
+            const uint8_t *ql = b + 64 * n, *qh = b + 128 + 32 * n;
+            const int8_t sc = (int8_t)b[192 + 8 * n + (l >> 4) + 2 * qd];
+            const int lo = (qd & 1) ? ql[l + 32] : ql[l];
+            const int q = ((qd >> 1) ? (lo >> 4) : (lo & 0xF)) | (((qh[l] >> (2 * qd)) & 3) << 4);
+            return d * (float)sc * (float)(q - 32);
+        }
+        default: {   // 11: Q3_K
+            const float dall = ld_f16u(b + 108);
+            const int n = i >> 7, r = i & 127, j = r >> 5, hf = (r >> 4) & 1, idx = (r & 15) + 16 * hf;
+            const float dl = dall * (float)(q3_raw(b + 96, 8 * n + 2 * j + hf) - 32);
+            const int code = (b[32 + 32 * n + idx] >> (2 * j)) & 3;
+            return dl * (float)(code - ((b[idx] & (1 << (4 * n + j))) ? 0 : 4));
+        }
+    }
+}
+
+// the lanes' token rows of a K-quant embedding (engine.rs:2251-2256): workgroup l = lane
+template <int NL>
+__global__ __launch_bounds__(256) void kq_embed_kernel(const RunCtl *__restrict__ ctl, const uint8_t *w, int type,
+                                                       int64_t row_bytes, float *out) {
+    if (!ctl->active) return;
+    const int l = blockIdx.x;
+    if (l >= ctl->nl) return;
+    const uint8_t *row = w + (int64_t)ctl->tok[l] * row_bytes;
+    const int bb = kq_block_bytes(type);
+    for (int i = threadIdx.x; i < shp::E; i += 256) out[(int64_t)l * shp::E + i] = kq_elem(type, row + (i / QK) * bb, i % QK);
+}
+
+// the lanes' projection input: xn = rms_norm(x) * attn_norm (oxe_ops.cpp:32-42), x the embedding
+// (Q8_0 emb, or the dequantised rows embf; stored to x_store, the residual of layer 0) or x; lanes
+// past the run's are zero
+template <int NL>
+__global__ __launch_bounds__(256) void kq_norm_kernel(const RunCtl *__restrict__ ctl, const float *x, Q8W emb,
+                                                      const float *embf, float *x_store, const float *norm_w, float eps,
+                                                      float *xn) {
+    __shared__ NormScratch ns;
+    __shared__ float s_x[shp::E];
+    if (!ctl->active) return;
+    const int nl = ctl->nl;
+#pragma unroll
+    for (int l = 0; l < NL; l++) {
+        float v[EPT];
+        if (l < nl) {
+            if (embf) load8(embf + (int64_t)l * shp::E, v);
+            else if (emb.q) embed8(emb, ctl->tok[l], v);
+            else load8(x + (int64_t)l * shp::E, v);
+            if (x_store && (embf || emb.q)) store8(x_store + (int64_t)l * shp::E, v);
+            store8(s_x, v);   // the replay source of the exact-sum fallback
+            __syncthreads();
+            rms_norm_mul_e(v, s_x, norm_w, eps, ns);
+            __syncthreads();
+        } else {
+#pragma unroll
+            for (int i = 0; i < EPT; i++) v[i] = 0.0f;
+        }
+        store8(xn + (int64_t)l * shp::E, v);
+    }
+}
+
+// rows [0, rows) of a part's lane GEMV output (src [NL][rows]) into dst [NL][dst_ld] (the projection
+// buffer at the part's offset); V rows also to V^T at pos0 + lane (vt != null)
+__global__ __launch_bounds__(256) void kq_scatter_kernel(const RunCtl *__restrict__ ctl, const float *src, int rows,
+                                                         float *dst, int64_t dst_ld, uint16_t *vt, int64_t vt_ld) {
+    if (!ctl->active) return;
+    const int l = blockIdx.y, r = blockIdx.x * 256 + threadIdx.x;
+    if (l >= ctl->nl || r >= rows) return;
+    const float v = src[(int64_t)l * rows + r];
+    dst[(int64_t)l * dst_ld + r] = v;
+    if (vt) vt[(int64_t)r * vt_ld + ctl->pos0 + l] = f2h(v);
+}
+
+// mixer_out's residual (engine.rs:2573-2609): x1 = out + x, per lane of the run
+__global__ __launch_bounds__(256) void kq_residual_kernel(const RunCtl *__restrict__ ctl, const float *out, const float *x,
+                                                          float *x1) {
+    if (!ctl->active) return;
+    const int l = blockIdx.y, r = blockIdx.x * 256 + threadIdx.x;
+    if (l >= ctl->nl || r >= shp::E) return;
+    const int64_t i = (int64_t)l * shp::E + r;
+    x1[i] = out[i] + x[i];
+}
+
 }  // namespace kq
 
 int launch_ba_f32(const RunCtl *ctl, const ModelRt &m, const LayerW &w, const float *x, const ActBufs &b, hipStream_t st) {
@@ -906,6 +1009,61 @@ int launch_kq_head(const RunCtl *ctl, const ModelRt &m, const float *norm_w, con
     }
     if (rc != 1) return -2;
     hipLaunchKernelGGL(kq::kq_argmax_kernel<OXE_NL>, dim3(OXE_NL), dim3(1024), 0, st, ctl, b.logits, o.rows, b.amax_key, ids);
+    return hipGetLastError() == hipSuccess ? 0 : -2;
+}
+
+// the lane GEMV over a matrix of ggml type 11..14 (nb blocks per row), s[l * rows + r]; 1: done
+static int vl_gemv_any(int type, const uint8_t *w, int nb, int64_t rows, const uint8_t *y, float *s, hipStream_t st) {
+    switch (type) {
+        case 11: return kq::vl_gemv_type<3>(w, nb, rows, y, OXE_NL, s, st);
+        case 12: return kq::vl_gemv_type<4>(w, nb, rows, y, OXE_NL, s, st);
+        case 13: return kq::vl_gemv_type<5>(w, nb, rows, y, OXE_NL, s, st);
+        case 14: return kq::vl_gemv_type<6>(w, nb, rows, y, OXE_NL, s, st);
+        default: return 0;
+    }
+}
+
+int launch_kq_embed(const RunCtl *ctl, const ModelRt &m, float *out, hipStream_t st) {
+    const RawW &e = m.tok_embd_r;
+    if (e.type < 11 || e.type > 14) return -1;
+    hipLaunchKernelGGL(kq::kq_embed_kernel<OXE_NL>, dim3(OXE_NL), dim3(256), 0, st, ctl, e.w, e.type, raw_row_bytes(e), out);
+    return hipGetLastError() == hipSuccess ? 0 : -2;
+}
+
+int launch_kq_proj(const RunCtl *ctl, const ModelRt &m, const LayerW &w, const float *x, bool embed, float *x_store,
+                   const ActBufs &b, hipStream_t st, int64_t row_begin) {
+    using namespace shp;
+    const bool kemb = embed && m.tok_embd_r.type != 8;
+    hipLaunchKernelGGL(kq::kq_norm_kernel<OXE_NL>, dim3(1), dim3(256), 0, st, ctl, x, embed && !kemb ? m.tok_embd : Q8W{},
+                       kemb ? b.emb : nullptr, x_store, w.attn_norm, m.eps, b.xn);
+    quant_k(b.xn, (int64_t)OXE_NL * E / kq::QK, b.xk, st);
+    struct Part {
+        const RawW *r;
+        int64_t off;
+        bool v;
+    };
+    const Part dn[4] = {{&w.qkv_r, 0, false}, {&w.z_r, DN_Z, false}, {&w.beta_r, DN_BETA, false}, {&w.alpha_r, DN_ALPHA, false}};
+    const Part at[3] = {{&w.q_r, 0, false}, {&w.k_r, AT_K, false}, {&w.v_r, AT_V, true}};
+    const Part *ps = w.att ? at : dn;
+    const int np = w.att ? 3 : 4;
+    uint16_t *vt = w.att ? m.vcache + (int64_t)w.index * NKV * HD * m.n_ctx : nullptr;
+    for (int i = 0; i < np; i++) {
+        const RawW &r = *ps[i].r;
+        if (ps[i].off < row_begin || r.type < 11 || r.type > 14) continue;   // F32 beta / alpha: launch_ba_f32
+        if (vl_gemv_any(r.type, r.w, (int)(E / kq::QK), r.rows, b.xk, b.kqo, st) != 1) return -2;
+        hipLaunchKernelGGL(kq::kq_scatter_kernel, dim3((unsigned)((r.rows + 255) / 256), OXE_NL), dim3(256), 0, st, ctl, b.kqo,
+                           (int)r.rows, b.proj + ps[i].off, (int64_t)DN_ROWS, ps[i].v ? vt : nullptr, (int64_t)m.n_ctx);
+    }
+    return hipGetLastError() == hipSuccess ? 0 : -2;
+}
+
+int launch_kq_out(const RunCtl *ctl, const ModelRt &m, const LayerW &w, const float *x, const ActBufs &b, hipStream_t st) {
+    (void)m;
+    using namespace shp;
+    const RawW &r = w.out_r;
+    quant_k(b.o32, (int64_t)OXE_NL * MIX_W / kq::QK, b.ok, st);
+    if (vl_gemv_any(r.type, r.w, (int)(MIX_W / kq::QK), E, b.ok, b.kqo, st) != 1) return -2;
+    hipLaunchKernelGGL(kq::kq_residual_kernel, dim3(E / 256, OXE_NL), dim3(256), 0, st, ctl, b.kqo, x, b.x1);
     return hipGetLastError() == hipSuccess ? 0 : -2;
 }
 

@@ -27,6 +27,7 @@ void launch_set_run(RunCtl *ctl, const RunCtl &v, hipStream_t st) {
 struct ProjArgs {
     const float *x;
     Q8W emb;            // layer 0: x = embd(tok) (emb.q != null)
+    const float *embf;  // layer 0 of a K-quant embedding: the lanes' dequantised rows [NL][E]
     float *x_store;     // workgroup 0 stores the embedded input here (the residual of layer 0)
     const float *norm_w;
     float eps;
@@ -52,14 +53,16 @@ __global__ __launch_bounds__(GEMV_THREADS) void proj_kernel(const RunCtl *__rest
     for (int l = 0; l < NL; l++) {
         if (l < nl) {
             float v[EPT];
-            if (a.emb.q) {
-                embed8(a.emb, ctl->tok[l], v);
+            const bool emb_in = a.emb.q || a.embf;
+            if (emb_in) {
+                if (a.embf) load8(a.embf + (int64_t)l * E, v);
+                else embed8(a.emb, ctl->tok[l], v);
                 if (blockIdx.x == 0 && a.x_store) store8(a.x_store + (int64_t)l * E, v);
             } else {
                 load8(a.x + (int64_t)l * E, v);
             }
             // replay source for the exact-sum fallback: the stored input (embedding) or x
-            const float *xg = a.emb.q ? nullptr : a.x + (int64_t)l * E;
+            const float *xg = emb_in ? nullptr : a.x + (int64_t)l * E;
             if (!xg) {
                 // the embedded row is not in memory for every workgroup: recompute on demand
                 __shared__ float s_emb[E];
@@ -102,7 +105,8 @@ void launch_proj(const RunCtl *ctl, const ModelRt &m, const LayerW &w, const flo
                  const ActBufs &b, hipStream_t st, int64_t row_begin) {
     ProjArgs a{};
     a.x = x;
-    if (embed) a.emb = m.tok_embd;
+    if (embed && m.tok_embd_r.type != 8) a.embf = b.emb;
+    else if (embed) a.emb = m.tok_embd;
     a.x_store = x_store;
     a.norm_w = w.attn_norm;
     a.eps = m.eps;
@@ -138,6 +142,7 @@ struct DnArgs {
     float eps;
     int8_t *oq;             // [NL][DIN]
     uint16_t *od;           // [NL][DIN/32]
+    float *o32;             // optional: the gated outputs in f32 [NL][DIN] (a K-quant ssm_out)
 };
 
 constexpr int DN_THREADS = 1024;
@@ -268,6 +273,10 @@ __global__ __launch_bounds__(DN_THREADS) void dn_kernel(const RunCtl *__restrict
             const float *z = a.proj + (int64_t)l * DN_ROWS + DN_Z + vh * HV;
             const float o0 = ((x0 * sc) * a.ssm_norm[lane]) * v_silu(z[lane]);
             const float o1 = ((x1 * sc) * a.ssm_norm[lane + 64]) * v_silu(z[lane + 64]);
+            if (a.o32) {
+                a.o32[(int64_t)l * DIN + vh * HV + lane] = o0;
+                a.o32[(int64_t)l * DIN + vh * HV + lane + 64] = o1;
+            }
             // Q8_0 blocks of 32: lanes 0..31 hold blocks 0 (o0) and 2 (o1), lanes 32..63 blocks 1 and 3
             float m0 = __builtin_fabsf(o0), m1 = __builtin_fabsf(o1);
             for (int mm = 16; mm >= 1; mm >>= 1) {
@@ -286,7 +295,7 @@ __global__ __launch_bounds__(DN_THREADS) void dn_kernel(const RunCtl *__restrict
     }
 }
 
-void launch_dn(const RunCtl *ctl, const ModelRt &m, const LayerW &w, const ActBufs &b, hipStream_t st) {
+void launch_dn(const RunCtl *ctl, const ModelRt &m, const LayerW &w, const ActBufs &b, hipStream_t st, float *o32) {
     DnArgs a{};
     a.proj = b.proj;
     a.conv_w = w.conv;
@@ -300,6 +309,7 @@ void launch_dn(const RunCtl *ctl, const ModelRt &m, const LayerW &w, const ActBu
     a.eps = m.eps;
     a.oq = b.oq;
     a.od = b.od;
+    a.o32 = o32;
     hipLaunchKernelGGL(dn_kernel<OXE_NL>, dim3(NVH), dim3(DN_THREADS), 0, st, ctl, a);
 }
 
@@ -376,9 +386,9 @@ void launch_kwrite(const RunCtl *ctl, const ModelRt &m, const LayerW &w, const A
 // ------------------------------------------------------------------------------------------------
 // entry (MTP): x2[l] = eh_proj . quantize([rms_norm(embd(tok), enorm); rms_norm(h, hnorm)])
 template <int NL>
-__global__ __launch_bounds__(GEMV_THREADS) void entry_kernel(const RunCtl *__restrict__ ctl, Q8W emb, Q8W w,
-                                                             const float *enorm, const float *hnorm, const float *hid,
-                                                             float *x2, float eps) {
+__global__ __launch_bounds__(GEMV_THREADS) void entry_kernel(const RunCtl *__restrict__ ctl, Q8W emb, const float *embf,
+                                                             Q8W w, const float *enorm, const float *hnorm,
+                                                             const float *hid, float *x2, float eps) {
     constexpr int K = 2 * E, R = GemvR<K>::R;
     __shared__ int8_t s_xq[NL][K];
     __shared__ uint16_t s_xd[NL][K / 32];
@@ -391,7 +401,8 @@ __global__ __launch_bounds__(GEMV_THREADS) void entry_kernel(const RunCtl *__res
     for (int l = 0; l < NL; l++) {
         if (l < nl) {
             float v[EPT];
-            embed8(emb, ctl->tok[l], v);
+            if (embf) load8(embf + (int64_t)l * E, v);   // a K-quant embedding's dequantised row
+            else embed8(emb, ctl->tok[l], v);
             store8(s_emb, v);
             __syncthreads();
             rms_norm_mul_e(v, s_emb, enorm, eps, ns);
@@ -421,8 +432,9 @@ __global__ __launch_bounds__(GEMV_THREADS) void entry_kernel(const RunCtl *__res
     }
 }
 
-void launch_entry(const RunCtl *ctl, const ModelRt &m, const LayerW &w, const ActBufs &b, hipStream_t st) {
-    hipLaunchKernelGGL(entry_kernel<OXE_NL>, dim3(E / GemvR<2 * E>::R), dim3(GEMV_THREADS), 0, st, ctl, m.tok_embd,
+void launch_entry(const RunCtl *ctl, const ModelRt &m, const LayerW &w, const ActBufs &b, hipStream_t st,
+                  const float *emb) {
+    hipLaunchKernelGGL(entry_kernel<OXE_NL>, dim3(E / GemvR<2 * E>::R), dim3(GEMV_THREADS), 0, st, ctl, m.tok_embd, emb,
                        w.eh_proj, w.enorm, w.hnorm, b.hid, b.x2, m.eps);
 }
 

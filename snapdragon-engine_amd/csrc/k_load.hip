@@ -64,9 +64,12 @@ static std::string tensor_check(const GgufTensor *t, const std::string &name, ui
 }
 
 // The types of the matrices that may be other than Q8_0, as the file holds them: gate / up of the
-// experts (or of the shared expert) both Q8_0 or both K-quants, down Q8_0 or a K-quant, ssm_beta /
-// ssm_alpha both Q8_0 or both F32, the LM head Q8_0 or a K-quant. A tensor of any other type keeps
-// Q8_0 here, and the load refuses it by name.
+// experts (or of the shared expert) both Q8_0 or both K-quants, down Q8_0 or a K-quant; a delta-net
+// layer's attn_qkv and attn_gate both K-quants (its ssm_beta / ssm_alpha then both K-quants or both
+// F32) or both Q8_0 (ssm_beta / ssm_alpha both Q8_0 or both F32); an attention layer's attn_q /
+// attn_k / attn_v all K-quants or all Q8_0; ssm_out / attn_output, the token embedding and the LM
+// head Q8_0 or a K-quant. A tensor of any other type or combination keeps Q8_0 here, and the load
+// refuses it by name.
 ModelTypes model_types(const Gguf &g, const oxe_model_desc &d) {
     ModelTypes mt;
     mt.layer.assign(d.n_layer + 1, LayerTypes{});
@@ -81,10 +84,24 @@ ModelTypes model_types(const Gguf &g, const oxe_model_desc &d) {
         const int g1 = ty(p + "ffn_gate_shexp.weight"), u1 = ty(p + "ffn_up_shexp.weight"), d1 = ty(p + "ffn_down_shexp.weight");
         if (kq(g1) && kq(u1)) { lt.sh_gate = g1; lt.sh_up = u1; }
         if (kq(d1)) lt.sh_down = d1;
-        if (ty(p + "ssm_beta.weight") == (int)GGML_F32 && ty(p + "ssm_alpha.weight") == (int)GGML_F32) lt.beta = lt.alpha = 0;
+        const int b0 = ty(p + "ssm_beta.weight"), a0 = ty(p + "ssm_alpha.weight");
+        const bool f32ba = b0 == (int)GGML_F32 && a0 == (int)GGML_F32;
+        if (f32ba) lt.beta = lt.alpha = 0;
+        const int qkv = ty(p + "attn_qkv.weight"), z = ty(p + "attn_gate.weight");
+        if (kq(qkv) && kq(z) && (f32ba || (kq(b0) && kq(a0)))) {
+            lt.qkv = qkv;
+            lt.z = z;
+            if (!f32ba) { lt.beta = b0; lt.alpha = a0; }
+        }
+        const int q = ty(p + "attn_q.weight"), k = ty(p + "attn_k.weight"), v = ty(p + "attn_v.weight");
+        if (kq(q) && kq(k) && kq(v)) { lt.q = q; lt.k = k; lt.v = v; }
+        const int out = ty(p + (g.tensor(p + "ssm_out.weight") ? "ssm_out.weight" : "attn_output.weight"));
+        if (kq(out)) lt.out = out;
     }
     const int o = ty("output.weight");
     if (kq(o)) mt.output = o;
+    const int e = ty("token_embd.weight");
+    if (kq(e)) mt.tok_embd = e;
     return mt;
 }
 
@@ -186,8 +203,13 @@ int Engine::load_gguf(const Gguf &g, uint8_t *given_stage, int64_t given_chunk) 
         f32(p + "attn_norm.weight", {E}, w.attn_norm);
         f32(p + "post_attention_norm.weight", {E}, w.post_norm);
         if (!w.att) {
-            q8(p + "attn_qkv.weight", E, NCH, 1, w.proj.q, w.proj.d, 0, 0, -1);
-            q8(p + "attn_gate.weight", E, DIN, 1, w.proj.q, w.proj.d, DN_Z, 0, -1);
+            if (w.qkv_r.type == 8) {
+                q8(p + "attn_qkv.weight", E, NCH, 1, w.proj.q, w.proj.d, 0, 0, -1);
+                q8(p + "attn_gate.weight", E, DIN, 1, w.proj.q, w.proj.d, DN_Z, 0, -1);
+            } else {
+                raw(p + "attn_qkv.weight", w.qkv_r, {E, NCH});
+                raw(p + "attn_gate.weight", w.z_r, {E, DIN});
+            }
             if (w.beta_r.type == 8) {
                 q8(p + "ssm_beta.weight", E, NVH, 1, w.proj.q, w.proj.d, DN_BETA, 0, -1);
                 q8(p + "ssm_alpha.weight", E, NVH, 1, w.proj.q, w.proj.d, DN_ALPHA, 0, -1);
@@ -195,16 +217,24 @@ int Engine::load_gguf(const Gguf &g, uint8_t *given_stage, int64_t given_chunk) 
                 raw(p + "ssm_beta.weight", w.beta_r, {E, NVH});
                 raw(p + "ssm_alpha.weight", w.alpha_r, {E, NVH});
             }
-            q8(p + "ssm_out.weight", DIN, E, 1, w.out.q, w.out.d, 0, 0, -1);
+            if (w.out_r.type == 8) q8(p + "ssm_out.weight", DIN, E, 1, w.out.q, w.out.d, 0, 0, -1);
+            else raw(p + "ssm_out.weight", w.out_r, {DIN, E});
             f32(p + "ssm_conv1d.weight", {KC, NCH}, w.conv);
             f32(p + "ssm_a", {NVH}, w.ssm_a);
             f32(p + "ssm_dt.bias", {NVH}, w.dt_bias);
             f32(p + "ssm_norm.weight", {HV}, w.ssm_norm);
         } else {
-            q8(p + "attn_q.weight", E, NH * 2 * HD, 1, w.proj.q, w.proj.d, 0, 0, -1);
-            q8(p + "attn_k.weight", E, NKV * HD, 1, w.proj.q, w.proj.d, AT_K, 0, -1);
-            q8(p + "attn_v.weight", E, NKV * HD, 1, w.proj.q, w.proj.d, AT_V, 0, -1);
-            q8(p + "attn_output.weight", NH * HD, E, 1, w.out.q, w.out.d, 0, 0, -1);
+            if (w.q_r.type == 8) {
+                q8(p + "attn_q.weight", E, NH * 2 * HD, 1, w.proj.q, w.proj.d, 0, 0, -1);
+                q8(p + "attn_k.weight", E, NKV * HD, 1, w.proj.q, w.proj.d, AT_K, 0, -1);
+                q8(p + "attn_v.weight", E, NKV * HD, 1, w.proj.q, w.proj.d, AT_V, 0, -1);
+            } else {
+                raw(p + "attn_q.weight", w.q_r, {E, NH * 2 * HD});
+                raw(p + "attn_k.weight", w.k_r, {E, NKV * HD});
+                raw(p + "attn_v.weight", w.v_r, {E, NKV * HD});
+            }
+            if (w.out_r.type == 8) q8(p + "attn_output.weight", NH * HD, E, 1, w.out.q, w.out.d, 0, 0, -1);
+            else raw(p + "attn_output.weight", w.out_r, {NH * HD, E});
             f32(p + "attn_q_norm.weight", {HD}, w.q_norm);
             f32(p + "attn_k_norm.weight", {HD}, w.k_norm);
         }
@@ -235,7 +265,8 @@ int Engine::load_gguf(const Gguf &g, uint8_t *given_stage, int64_t given_chunk) 
             f32(p + "nextn.shared_head_norm.weight", {E}, w.head_norm);
         }
     }
-    q8("token_embd.weight", E, d.n_vocab, 1, m.tok_embd.q, m.tok_embd.d, 0, 0, -1);
+    if (m.tok_embd_r.type == 8) q8("token_embd.weight", E, d.n_vocab, 1, m.tok_embd.q, m.tok_embd.d, 0, 0, -1);
+    else raw("token_embd.weight", m.tok_embd_r, {E, (uint64_t)d.n_vocab});
     if (m.output_r.type == 8) q8("output.weight", E, d.n_vocab, 1, m.output.q, m.output.d, 0, 0, -1);
     else raw("output.weight", m.output_r, {E, (uint64_t)d.n_vocab});
     f32("output_norm.weight", {E}, m.out_norm);

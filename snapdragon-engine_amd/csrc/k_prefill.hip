@@ -1047,9 +1047,19 @@ int Engine::prefill(const uint32_t *toks, int n, uint32_t *next, float *h_all) {
 int Engine::seed_batched(const uint32_t *toks, int n, int pos0, const float *hs) {
     using namespace pf;
     if (n < 1 || pos0 < 0 || pos0 + n > m.n_ctx || !toks_ok(toks, n) || !hs) return -1;
+    const LayerW &w = L[d.n_layer];
+    if (m.tok_embd_r.type != 8 || w.kq_proj()) {
+        // the batched kernels below read the Q8_0 token embedding and the MTP layer's Q8_0
+        // projection; a model with either in other blocks seeds through the seeding runs, OXE_NL
+        // pairs at a time (every pair's K / V rows depend on that pair only)
+        for (int c0 = 0; c0 < n; c0 += OXE_NL) {
+            const int c = std::min(OXE_NL, n - c0);
+            if (int rc = mtp_seed(toks + c0, c, pos0 + c0, hs + (size_t)c0 * E)) return rc;
+        }
+        return 0;
+    }
     int rc = pf_alloc(std::min(n, PF_CHUNK));
     if (rc) return rc;
-    const LayerW &w = L[d.n_layer];
     uint16_t *kcl = m.kcache + (int64_t)w.index * NKV * m.n_ctx * HD;
     uint16_t *vtl = m.vcache + (int64_t)w.index * NKV * HD * m.n_ctx;
     for (int c0 = 0; c0 < n; c0 += PF_CHUNK) {

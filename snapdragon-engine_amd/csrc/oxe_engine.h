@@ -41,19 +41,26 @@ __host__ __device__ inline int64_t raw_row_bytes(const RawW &r) {
 }
 
 // ggml types of the matrices that may be other than Q8_0 (the reference's mv dispatches every type,
-// crates/model/src/engine.rs:2270-2343): K-quant experts, shared expert and LM head; F32 ssm_beta /
-// ssm_alpha. Gate and up of one expert kind are both Q8_0 or both K-quants.
+// crates/model/src/engine.rs:2270-2343): K-quant experts, shared expert, mixer projections, output
+// projections, token embedding and LM head; F32 or K-quant ssm_beta / ssm_alpha. Gate and up of one
+// expert kind are both Q8_0 or both K-quants; a layer's projection parts are all Q8_0 (beta / alpha
+// Q8_0 or F32) or all in the file's blocks.
 struct LayerTypes {
     int gate = 8, up = 8, down = 8, sh_gate = 8, sh_up = 8, sh_down = 8, beta = 8, alpha = 8;
-    bool any() const { return gate != 8 || up != 8 || down != 8 || sh_gate != 8 || sh_up != 8 || sh_down != 8 || beta != 8 || alpha != 8; }
+    // the mixer's projections (delta-net qkv / z, attention q / k / v) and output projection
+    int qkv = 8, z = 8, q = 8, k = 8, v = 8, out = 8;
+    bool any() const {
+        return gate != 8 || up != 8 || down != 8 || sh_gate != 8 || sh_up != 8 || sh_down != 8 || beta != 8 || alpha != 8 ||
+               qkv != 8 || z != 8 || q != 8 || k != 8 || v != 8 || out != 8;
+    }
 };
 struct ModelTypes {
     std::vector<LayerTypes> layer;   // n_layer + 1 (the MTP block last)
-    int output = 8;
+    int output = 8, tok_embd = 8;
     bool any() const {
         for (const LayerTypes &t : layer)
             if (t.any()) return true;
-        return output != 8;
+        return output != 8 || tok_embd != 8;
     }
 };
 
@@ -122,9 +129,14 @@ struct LayerW {
     // matrices of other types (a model file's), used in place of the Q8W ones above when their type
     // is not 8: experts [n_expert][rows][k], the shared expert, ssm_beta / ssm_alpha [n_vheads][n_embd]
     RawW exp_gate_r, exp_up_r, exp_down_r, sh_gate_r, sh_up_r, sh_down_r, beta_r, alpha_r;
+    // K-quant mixer matrices: delta-net qkv / z, attention q (+ gate) / k / v, the output projection
+    RawW qkv_r, z_r, q_r, k_r, v_r, out_r;
     bool kq_moe() const {
         return exp_gate_r.type != 8 || exp_down_r.type != 8 || sh_gate_r.type != 8 || sh_down_r.type != 8;
     }
+    // the projection's parts in the file's blocks, with no Q8_0 projection matrix: a delta-net
+    // layer's qkv and z (its beta / alpha then K-quants or F32), an attention layer's q, k and v
+    bool kq_proj() const { return qkv_r.type != 8 || q_r.type != 8; }
 };
 
 // Per-lane activation buffers, all [OXE_NL][...]
@@ -153,6 +165,10 @@ struct ActBufs {
     uint8_t *xk;          // q8_K blocks of xn [NL][n_embd / 256] (K-quant matrices)
     uint8_t *hk;          // q8_K blocks of hexp [NL][k_used][ff_exp / 256]
     uint8_t *hshk;        // q8_K blocks of hsh [NL][ff_shexp / 256]
+    float *o32;           // the mixer's gated outputs in f32 [NL][4096] (a K-quant output projection)
+    uint8_t *ok;          // their q8_K blocks [NL][4096 / 256]
+    float *emb;           // the lanes' embedded tokens [NL][n_embd] (a K-quant token embedding)
+    float *kqo;           // [NL][DN_ROWS] outputs of a K-quant projection part or output projection
     uint32_t *counters;   // per-kernel completion counters (zeroed at allocation; self-resetting)
 };
 

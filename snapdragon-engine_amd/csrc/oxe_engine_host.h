@@ -245,6 +245,7 @@ struct Engine {
         seed = sd;
         types.layer.assign(d.n_layer + 1, LayerTypes{});
         types.output = 8;
+        types.tok_embd = 8;
         if (mt && (int)mt->layer.size() == d.n_layer + 1) types = *mt;
         kq = types.any();
         if (hipGetDevice(&dev) != hipSuccess) throw std::runtime_error("hipGetDevice failed");
@@ -272,24 +273,34 @@ struct Engine {
         // weights
         for (int il = 0; il < nl_total; il++) {
             LayerW &w = L[il];
+            const LayerTypes &ty = types.layer[il];
+            // a projection in the file's blocks (all its parts) or an output projection of another
+            // type has no Q8_0 matrix; the Q8W keeps the row count the runs read
+            const bool kq_proj = w.att ? ty.q != 8 : ty.qkv != 8;
+            auto q8_or_rows = [&](bool q, int64_t rows, int64_t k) {
+                if (q) return q8(rows, k);
+                Q8W r{};
+                r.rows = rows;
+                r.k = k;
+                return r;
+            };
             w.attn_norm = alloc<float>(E);
             w.post_norm = alloc<float>(E);
             if (!w.att) {
-                w.proj = q8(DN_ROWS, E);
-                w.out = q8(E, DIN);
+                w.proj = q8_or_rows(!kq_proj, DN_ROWS, E);
+                w.out = q8_or_rows(ty.out == 8, E, DIN);
                 w.conv = alloc<float>((size_t)NCH * KC);
                 w.ssm_a = alloc<float>(NVH);
                 w.dt_bias = alloc<float>(NVH);
                 w.ssm_norm = alloc<float>(HV);
             } else {
-                w.proj = q8(AT_ROWS, E);
-                w.out = q8(E, NH * HD);
+                w.proj = q8_or_rows(!kq_proj, AT_ROWS, E);
+                w.out = q8_or_rows(ty.out == 8, E, NH * HD);
                 w.q_norm = alloc<float>(HD);
                 w.k_norm = alloc<float>(HD);
             }
             w.router = alloc<float>((size_t)NEXP * E);
             w.shexp_gate = alloc<float>(E);
-            const LayerTypes &ty = types.layer[il];
             // a matrix of another type lives in its file blocks; its Q8_0 array is not allocated
             auto raw = [&](RawW &r, int type, int64_t n_grp, int64_t rows, int64_t k) {
                 r.type = type;
@@ -306,6 +317,14 @@ struct Engine {
             if (!w.att) {
                 raw(w.beta_r, ty.beta, 1, NVH, E);
                 raw(w.alpha_r, ty.alpha, 1, NVH, E);
+                raw(w.qkv_r, ty.qkv, 1, NCH, E);
+                raw(w.z_r, ty.z, 1, DIN, E);
+                raw(w.out_r, ty.out, 1, E, DIN);
+            } else {
+                raw(w.q_r, ty.q, 1, NH * 2 * HD, E);
+                raw(w.k_r, ty.k, 1, NKV * HD, E);
+                raw(w.v_r, ty.v, 1, NKV * HD, E);
+                raw(w.out_r, ty.out, 1, E, NH * HD);
             }
             if (ty.sh_gate == 8) w.shexp_gu = q8(2 * FFSH, E);
             if (ty.sh_down == 8) w.shexp_down = q8(E, FFSH);
@@ -318,7 +337,18 @@ struct Engine {
                 w.head_norm = alloc<float>(E);
             }
         }
-        m.tok_embd = q8(d.n_vocab, E);
+        m.tok_embd_r = RawW{};
+        if (types.tok_embd != 8) {
+            // a K-quant embedding: its rows are dequantised per run (launch_kq_embed)
+            m.tok_embd_r.type = types.tok_embd;
+            m.tok_embd_r.rows = d.n_vocab;
+            m.tok_embd_r.k = E;
+            m.tok_embd_r.w = alloc<uint8_t>((size_t)(d.n_vocab * raw_row_bytes(m.tok_embd_r)));
+            m.tok_embd.rows = d.n_vocab;
+            m.tok_embd.k = E;
+        } else {
+            m.tok_embd = q8(d.n_vocab, E);
+        }
         m.output_r = RawW{};
         if (types.output != 8) {
             m.output_r.type = types.output;
@@ -362,6 +392,12 @@ struct Engine {
         b.xk = alloc<uint8_t>((size_t)OXE_NL * (E / 256) * 292);
         b.hk = alloc<uint8_t>((size_t)OXE_NL * KUSED * (FF / 256) * 292);
         b.hshk = alloc<uint8_t>((size_t)OXE_NL * (FFSH / 256) * 292);
+        if (kq) {
+            b.o32 = alloc<float>(OXE_NL * MIX_W);
+            b.ok = alloc<uint8_t>((size_t)OXE_NL * (MIX_W / 256) * 292);
+            b.emb = alloc<float>(OXE_NL * E);
+            b.kqo = alloc<float>((size_t)OXE_NL * DN_ROWS);
+        }
         b.counters = alloc<uint32_t>(CNT_N);
         ctl = alloc<RunCtl>(2);
         ctl_draft = ctl + 1;
@@ -611,21 +647,42 @@ struct Engine {
            K_FUSED = 10, K_FUSED_DRAFT = 11,
            // batched prefill: every matrix-core GEMM, the grouped expert GEMMs, attention, delta rule
            K_PF_GEMM = 12, K_PF_EXPERT = 13, K_PF_ATTN = 14, K_PF_DELTA = 15 };
+    // a layer's projection (K-quant parts or the Q8_0 matrix), then F32 ssm_beta / ssm_alpha rows
+    void enqueue_proj(const LayerW &w, const float *x, bool embed, float *x_store, int64_t row_begin = 0) {
+        probe(K_PROJ);
+        if (w.kq_proj()) (void)launch_kq_proj(ctl, m, w, x, embed, x_store, b, st, row_begin);
+        else launch_proj(ctl, m, w, x, embed, x_store, b, st, row_begin);
+        probe(K_PROJ);
+        if (!w.att && w.beta_r.type == 0) (void)launch_ba_f32(ctl, m, w, embed ? x_store : x, b, st);
+    }
+    // the mixer's output projection + residual into x1 (K-quant: from the f32 gated outputs)
+    void enqueue_out(const LayerW &w, const float *x) {
+        probe(K_OUT);
+        if (w.out_r.type != 8) (void)launch_kq_out(ctl, m, w, x, b, st);
+        else launch_out(ctl, w, x, b, st);
+        probe(K_OUT);
+    }
     void enqueue_layer(int l, bool first) {
         const LayerW &w = L[l];
         const float *x = first ? b.x : b.x2;
-        probe(K_PROJ); launch_proj(ctl, m, w, first ? nullptr : b.x2, first, first ? b.x : nullptr, b, st); probe(K_PROJ);
-        // F32 ssm_beta / ssm_alpha: their rows of the projection output (the Q8_0 pass's are unused)
-        if (!w.att && w.beta_r.type != 8) (void)launch_ba_f32(ctl, m, w, first ? b.x : b.x2, b, st);
+        float *o32 = w.out_r.type != 8 ? b.o32 : nullptr;
+        if (first && m.tok_embd_r.type != 8) (void)launch_kq_embed(ctl, m, b.emb, st);
+        enqueue_proj(w, first ? nullptr : b.x2, first, first ? b.x : nullptr);
         if (!w.att) {
-            probe(K_DN); launch_dn(ctl, m, w, b, st); probe(K_DN);
+            probe(K_DN); launch_dn(ctl, m, w, b, st, o32); probe(K_DN);
         } else {
             launch_kwrite(ctl, m, w, b, st);
             probe(K_SCORES); launch_scores(ctl, m, w, b, st); probe(K_SCORES);
-            probe(K_PV); launch_pv(ctl, m, w, b, st); probe(K_PV);
+            probe(K_PV); launch_pv(ctl, m, w, b, st, o32); probe(K_PV);
         }
-        probe(K_OUT); launch_out(ctl, w, x, b, st); probe(K_OUT);
+        enqueue_out(w, x);
         enqueue_moe(w);
+    }
+    // the MTP entry over the lanes' tokens (a K-quant embedding's rows dequantised first)
+    void enqueue_entry(const LayerW &w) {
+        const bool kemb = m.tok_embd_r.type != 8;
+        if (kemb) (void)launch_kq_embed(ctl, m, b.emb, st);
+        probe(K_ENTRY); launch_entry(ctl, m, w, b, st, kemb ? b.emb : nullptr); probe(K_ENTRY);
     }
     void enqueue_moe(const LayerW &w) {
         probe(K_ROUTER); launch_router(ctl, m, w, b, st); probe(K_ROUTER);
@@ -675,13 +732,13 @@ struct Engine {
             return;
         }
         const LayerW &w = L[d.n_layer];
-        probe(K_ENTRY); launch_entry(ctl, m, w, b, st); probe(K_ENTRY);
+        enqueue_entry(w);
         // the MTP layer: input x2 (the entry output), as any layer > 0
-        probe(K_PROJ); launch_proj(ctl, m, w, b.x2, false, nullptr, b, st); probe(K_PROJ);
+        enqueue_proj(w, b.x2, false, nullptr);
         launch_kwrite(ctl, m, w, b, st);
         probe(K_SCORES); launch_scores(ctl, m, w, b, st); probe(K_SCORES);
-        probe(K_PV); launch_pv(ctl, m, w, b, st); probe(K_PV);
-        probe(K_OUT); launch_out(ctl, w, b.x2, b, st); probe(K_OUT);
+        probe(K_PV); launch_pv(ctl, m, w, b, st, w.out_r.type != 8 ? b.o32 : nullptr); probe(K_PV);
+        enqueue_out(w, b.x2);
         enqueue_moe(w);
         probe(K_HEAD); enqueue_head(w.head_norm, false, draft_rows > 0); probe(K_HEAD);
     }
@@ -692,8 +749,8 @@ struct Engine {
             return;
         }
         const LayerW &w = L[d.n_layer];
-        launch_entry(ctl, m, w, b, st);
-        launch_proj(ctl, m, w, b.x2, false, nullptr, b, st, AT_K);  // K and V rows only
+        enqueue_entry(w);
+        enqueue_proj(w, b.x2, false, nullptr, AT_K);  // K and V rows only
         launch_kwrite(ctl, m, w, b, st);
     }
 

@@ -167,7 +167,7 @@ def synth_model_tensors(O, desc, seed, types=None):
 
     out = [("output.weight", ty(G, T["OUTPUT"]), [E, V], q8(G, T["OUTPUT"], V, E)),
            ("output_norm.weight", F32, [E], f32(G, T["OUT_NORM"], E)),
-           ("token_embd.weight", GGML["Q8_0"], [E, V], q8(G, T["TOK_EMBD"], V, E))]
+           ("token_embd.weight", ty(G, T["TOK_EMBD"]), [E, V], q8(G, T["TOK_EMBD"], V, E))]
     for il in range(desc.n_layer + 1):
         p = f"blk.{il}."
         att = il == desc.n_layer or (il + 1) % desc.full_attention_interval == 0

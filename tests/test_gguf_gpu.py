@@ -6,9 +6,8 @@ layouts (tests/gguf_writer.py, from the oracle's generator); an engine created f
 decode bit for bit like the engine that generates the same weights on the device (prefill,
 logits, hidden states, speculative steps), which checks every tensor's name, shape, Q8_0 block
 split, projection concatenation and gate / up interleave at once. The reference's real Qwen3.6 and
-Ornith files (headers rebuilt from its fixtures, sparse files of the real size): the Qwen3.6 file's
-types all load and run; the Ornith file is refused by name at its first tensor type without a
-kernel here."""
+Ornith files (headers rebuilt from its fixtures, sparse files of the real size): both files' types
+all load and run."""
 import json
 import os
 
@@ -109,14 +108,26 @@ def test_real_qwen36_file_loads_and_decodes():
             os.remove(path)
 
 
-def test_real_ornith_file_is_refused_by_tensor_type():
-    """the reference's Ornith file: its Q4_K delta-net projections have no kernel in this build (the
-    engine takes K-quants for the expert, shared-expert and output matrices) -> -1 with the name"""
+def test_real_ornith_file_loads_and_decodes():
+    """the reference's Ornith file (header from its fixture, a sparse 16 GiB file of the real size):
+    Q4_K delta-net projections (attn_qkv, attn_gate, ssm_beta, ssm_alpha, ssm_out) and attention
+    matrices, a Q4_K token embedding, Q3_K / Q4_K experts, Q6_K shared experts and LM head, beside the
+    MTP layer's Q8_0 matrices, all load; with every weight zero each logit is +0, so the first strict
+    maximum is row 0, and an MTP step runs through the Q8_0 MTP layer over the K-quant embedding"""
     import oxe_amd as A
     path = real_header_file("ornith")
     try:
-        with pytest.raises(A.GgufError, match="blk.0.attn_qkv.weight: type Q4_K"):
-            A.Engine.from_gguf(path, n_ctx=256)
+        print("loading the sparse Ornith file", flush=True)
+        g = A.Engine.from_gguf(path, n_ctx=256)
+        assert not g.fused
+        assert g.step(1) == 0
+        lg = np.asarray(g.logits(0), np.float32)
+        assert lg.shape[0] == g.desc.n_vocab and not np.any(bits(lg))
+        g.close()
+        g = A.Engine.from_gguf(path, n_ctx=256)
+        assert g.mtp_prefill_batched([1, 2, 3]) == 0
+        assert all(t == 0 for t in g.mtp_step(0))
+        g.close()
     finally:
         if os.path.exists(path):
             os.remove(path)
