@@ -666,22 +666,35 @@ __global__ __launch_bounds__(256) void router_kernel(const float *xn, const floa
     for (int i = 0; i < 4; i++)
 #pragma unroll
         for (int e = 0; e < 4; e++) acc[i][e] = 0.0f;
-    for (int k0 = 0; k0 < E; k0 += RT_KC) {
-        __syncthreads();
+    // a stage's token and weight elements in registers: the next stage's are loaded while the
+    // current one runs (the last stage loads itself again)
+    constexpr int RT_R = RT_TB * RT_KC / 4 / 256;
+    float4 xr[RT_R], wr4[RT_R];
+    auto stage_load = [&](int k0) {
 #pragma unroll
-        for (int r = 0; r < RT_TB * RT_KC / 4 / 256; r++) {
+        for (int r = 0; r < RT_R; r++) {
             const int i = tid + 256 * r, row = i / (RT_KC / 4), c4 = i % (RT_KC / 4);
             const int64_t tt = t0 + row;
             const int ee = e0 + row;
-            const float4 xv = tt < T ? *(const float4 *)(xn + tt * E + k0 + 4 * c4) : make_float4(0, 0, 0, 0);
+            xr[r] = tt < T ? *(const float4 *)(xn + tt * E + k0 + 4 * c4) : make_float4(0, 0, 0, 0);
             const float *wr = ee < NEXP ? router + (int64_t)ee * E : shg;
-            const float4 wv = ee < RT_NR ? *(const float4 *)(wr + k0 + 4 * c4) : make_float4(0, 0, 0, 0);
+            wr4[r] = ee < RT_NR ? *(const float4 *)(wr + k0 + 4 * c4) : make_float4(0, 0, 0, 0);
+        }
+    };
+    stage_load(0);
+    for (int k0 = 0; k0 < E; k0 += RT_KC) {
+        __syncthreads();
+#pragma unroll
+        for (int r = 0; r < RT_R; r++) {
+            const int i = tid + 256 * r, row = i / (RT_KC / 4), c4 = i % (RT_KC / 4);
+            const float4 xv = xr[r], wv = wr4[r];
             // elements 4 c4 .. 4 c4 + 3 of the stage: step q = c4 / 4, chains 4 (c4 % 4) ..
             const int q = c4 >> 2, cb = 4 * (c4 & 3);
             s_x[row][cb][q] = xv.x; s_x[row][cb + 1][q] = xv.y; s_x[row][cb + 2][q] = xv.z; s_x[row][cb + 3][q] = xv.w;
             s_w[row][cb][q] = wv.x; s_w[row][cb + 1][q] = wv.y; s_w[row][cb + 2][q] = wv.z; s_w[row][cb + 3][q] = wv.w;
         }
         __syncthreads();
+        stage_load(k0 + RT_KC < E ? k0 + RT_KC : k0);
 #pragma unroll
         for (int q4 = 0; q4 < RT_Q / 4; q4++) {
             float4 xv[4], wv[4];
