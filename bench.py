@@ -677,6 +677,89 @@ def bench_forced(args):
     }
 
 
+TYPED_PUBLISHED = {
+    # the reference's published decode figures on the real k-quant files (CPU; not this metric's
+    # config, so never a vs_baseline): README.md:21, 86-89; docs/lab-notes/M3-MTP.md:7-8, 333-338
+    "ornith": "54.4 tok/s, installed oxe decode on Ornith 35B-A3B (README.md:21)",
+    "qwen36": "43.05 tok/s, MTP depth 2 on Qwen3.6 35B-A3B, 8 threads (docs/lab-notes/M3-MTP.md:7-8)",
+}
+
+
+def bench_typed(args):
+    """MTP-1 decode of an engine with a real file's matrix types (the Qwen3.6 or Ornith 35B-A3B
+    GGUF: K-quant experts, projections, embedding, LM head) and its vocabulary, the weights
+    synthesised on the device in those types (oxe_engine_create_typed). Typed engines run one launch
+    per phase; the device-driven MTP steps are graph-captured as in the default line."""
+    import torch
+    import oxe_amd as A
+
+    hdr_path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "tests", "golden",
+                            f"gguf_header_{args.types}.json")
+    with open(hdr_path) as f:
+        hdr = json.load(f)
+    tensors = [(t[0], t[1]) for t in hdr["tensors"]]
+    types = A.types_from_tensors(tensors)
+    vocab = next(t[2][1] for t in hdr["tensors"] if t[0] == "output.weight")
+    d = A.desc_35b_a3b(n_vocab=vocab)
+    n_ctx = args.prompt + 2 * (args.steps + args.warmup) + 256 + 64
+    t_setup = time.time()
+    eng = A.Engine(d, seed=0, n_ctx=n_ctx, types=types)
+    fused = eng.fused
+    prompt = A.bench_prompt(args.prompt)
+    x = eng.mtp_prefill_batched(prompt)
+    eng.sync()
+    setup_s = time.time() - t_setup
+    cap = 2 * (args.steps + args.warmup) + 16
+    eng.mtp_device_begin(x, cap)
+    eng.mtp_device_steps(args.warmup, use_graph=True)
+    _, x = eng.mtp_device_end(cap)
+    pos_start = eng.pos
+    eng.mtp_device_begin(x, cap)
+    stream = torch.cuda.ExternalStream(eng.stream())
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    eng.sync()
+    ev0.record(stream)
+    eng.mtp_device_steps(args.steps, use_graph=True)
+    ev1.record(stream)
+    eng.sync()
+    torch.cuda.synchronize()
+    ms = ev0.elapsed_time(ev1)
+    toks, x = eng.mtp_device_end(cap)
+    n_tok = len(toks)
+    n_types = {}
+    for t in types.values():
+        n_types[t] = n_types.get(t, 0) + 1
+    return {
+        "metric": f"MTP-1 decode tok/s ({args.types} 35B-A3B matrix types, synthetic weights)",
+        "value": round(n_tok / (ms / 1e3), 3),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms / args.steps, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "K-quant / Q8_0 weights (file types), q8_K / Q8_0 activations, fp32 chains; fp16 KV",
+        "data": "synthetic: seeded random weights in the file's types (the oracle's synthetic blocks), "
+                "reference bench prompt ids",
+        "config": {"workload": f"35B-A3B MTP-1 decode with the {args.types} GGUF's matrix types "
+                               f"({os.path.basename(hdr_path)}), vocab {vocab}",
+                   "prompt_tokens": args.prompt, "ctx_positions": [pos_start, eng.pos],
+                   "parallelism": "single GPU",
+                   "non_q8_matrices": {str(k): v for k, v in sorted(n_types.items())}},
+        "tokens": n_tok,
+        "accepted_drafts": n_tok - args.steps,
+        "run_mode": "fused (one persistent launch per run)" if fused else "one launch per phase",
+        "reference_published": TYPED_PUBLISHED[args.types],
+        "setup_s": round(setup_s, 1),
+        "roofline": None,
+        "cpu_baseline": None,
+    }
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -708,6 +791,9 @@ def main():
                          "verify, and so the output, is unchanged")
     ap.add_argument("--depth", type=int, default=0, choices=(0, 1, 2),
                     help="MTP depth 1 or 2 with every draft accepted (forced to the greedy ids): one JSON line")
+    ap.add_argument("--types", choices=("qwen36", "ornith"), default=None,
+                    help="MTP-1 decode of an engine with that real file's matrix types and vocabulary "
+                         "(synthetic weights in those types, one launch per phase): one JSON line")
     ap.add_argument("--gemm-probe", action="store_true",
                     help="only the prefill's Q8_0 GEMM on its 2048-token shapes (for rocprofv3 --pmc)")
     args = ap.parse_args()
@@ -740,6 +826,11 @@ def main():
         if args.steps == ap.get_default("steps"):
             args.steps = 64
         print(json.dumps(bench_forced(args)), flush=True)
+        return
+    if args.types:
+        if args.steps == ap.get_default("steps"):
+            args.steps = 64
+        print(json.dumps(bench_typed(args)), flush=True)
         return
     if args.config:
         fn = {1: bench_config1, 2: bench_config2, 3: bench_config3}[args.config]

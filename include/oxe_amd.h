@@ -114,8 +114,19 @@ OXE_API int oxe_engine_create(const oxe_model_desc *desc, uint64_t seed, int n_c
  * device counterpart. */
 OXE_API int oxe_engine_create_on(const oxe_model_desc *desc, uint64_t seed, int n_ctx, void *stream,
                                  oxe_engine **out);
+/* An engine whose matrices take other types than Q8_0, as a model file's do, without the file:
+ * types[layer * 64 + kind] (layer 63 = the global tensors; kinds of include/oxe_model.h) holds a ggml
+ * type id per matrix, 8 where it is Q8_0: K-quants (11..14) for the experts, shared expert, mixer
+ * and output projections, token embedding and LM head, F32 (0) or K-quants for ssm_beta /
+ * ssm_alpha, in the combinations oxe_engine_create_from_gguf takes (-1 naming any other).
+ * oxe_engine_synth_weights then fills each matrix in its type (the oracle's synthetic K-quant
+ * blocks). The reference builds such an engine only from a file (WeightStore::load, weights.rs:556);
+ * this is that engine with synthetic weights, for tests and benchmarks of the files' types. */
+OXE_API int oxe_engine_create_typed(const oxe_model_desc *desc, uint64_t seed, int n_ctx, const int32_t *types,
+                                    oxe_engine **out);
 OXE_API void oxe_engine_destroy(oxe_engine *e);
-/* Fill every weight with the synthetic model of include/oxe_model.h (the benchmark's model). */
+/* Fill every weight with the synthetic model of include/oxe_model.h (the benchmark's model), each
+ * matrix of a typed engine in its type. */
 OXE_API int oxe_engine_synth_weights(oxe_engine *e);
 
 /* Run n (1..2) tokens at positions pos..pos+n-1 as one batch-invariant run; argmax per lane.

@@ -121,6 +121,73 @@ int oxe_engine_create_on(const oxe_model_desc *desc, uint64_t seed, int n_ctx, v
     return oxe::create_engine(desc, seed, n_ctx, true, stream, nullptr, out);
 }
 
+// An engine whose matrices take the types of a model file without the file: types[layer * 64 +
+// kind] (layer 63: the global tensors, kinds of include/oxe_model.h) is a ggml type id, 8 (Q8_0)
+// where a matrix is Q8_0. The combinations the file loader takes (k_load.hip model_types); any
+// other -> -1 naming it. oxe_engine_synth_weights then fills every matrix in its type.
+int oxe_engine_create_typed(const oxe_model_desc *desc, uint64_t seed, int n_ctx, const int32_t *types, oxe_engine **out) {
+    if (!desc || !types || !out) return -1;
+    auto kq = [](int t) { return t >= 11 && t <= 14; };
+    const int nl = desc->n_layer;
+    if (nl < 1 || nl > 62) {
+        oxe::set_err("typed engine: layer count out of range");
+        return -1;
+    }
+    oxe::ModelTypes mt;
+    mt.layer.assign(nl + 1, oxe::LayerTypes{});
+    std::string bad;
+    auto ty = [&](int l, int k) { return (int)types[l * 64 + k]; };
+    for (int l = 0; l <= nl && bad.empty(); l++) {
+        const bool att = l == nl || ((l + 1) % desc->full_attention_interval == 0);
+        oxe::LayerTypes &t = mt.layer[l];
+        const std::string where = "layer " + std::to_string(l) + ": ";
+        for (int k = 0; k < 64; k++) {
+            const int v = ty(l, k);
+            const bool q8 = v == 8;
+            switch (k) {
+                case OXE_T_GATE_EXPS: case OXE_T_UP_EXPS: case OXE_T_DOWN_EXPS: case OXE_T_GATE_SHEXP:
+                case OXE_T_UP_SHEXP: case OXE_T_DOWN_SHEXP: case OXE_T_DN_QKV: case OXE_T_DN_Z: case OXE_T_DN_OUT:
+                case OXE_T_ATT_Q: case OXE_T_ATT_K: case OXE_T_ATT_V: case OXE_T_ATT_OUT:
+                    if (!q8 && !kq(v)) bad = where + "matrix kind " + std::to_string(k) + " must be Q8_0 or a K-quant";
+                    break;
+                case OXE_T_DN_BETA: case OXE_T_DN_ALPHA:
+                    if (!q8 && !kq(v) && v != 0) bad = where + "ssm_beta / ssm_alpha must be Q8_0, F32 or a K-quant";
+                    break;
+                default:
+                    if (!q8) bad = where + "kind " + std::to_string(k) + " takes no other type";
+            }
+        }
+        if (!bad.empty()) break;
+        t.gate = ty(l, OXE_T_GATE_EXPS); t.up = ty(l, OXE_T_UP_EXPS); t.down = ty(l, OXE_T_DOWN_EXPS);
+        t.sh_gate = ty(l, OXE_T_GATE_SHEXP); t.sh_up = ty(l, OXE_T_UP_SHEXP); t.sh_down = ty(l, OXE_T_DOWN_SHEXP);
+        if ((t.gate == 8) != (t.up == 8) || (t.sh_gate == 8) != (t.sh_up == 8))
+            bad = where + "gate and up are both Q8_0 or both K-quants";
+        if (!att) {
+            t.qkv = ty(l, OXE_T_DN_QKV); t.z = ty(l, OXE_T_DN_Z); t.beta = ty(l, OXE_T_DN_BETA); t.alpha = ty(l, OXE_T_DN_ALPHA);
+            t.out = ty(l, OXE_T_DN_OUT);
+            const bool f32ba = t.beta == 0 && t.alpha == 0, q8ba = t.beta == 8 && t.alpha == 8;
+            const bool kba = kq(t.beta) && kq(t.alpha);
+            if (t.qkv == 8 ? !(t.z == 8 && (q8ba || f32ba)) : !(kq(t.z) && (f32ba || kba)))
+                bad = where + "the delta-net projection parts mix Q8_0 with other types";
+        } else {
+            t.q = ty(l, OXE_T_ATT_Q); t.k = ty(l, OXE_T_ATT_K); t.v = ty(l, OXE_T_ATT_V); t.out = ty(l, OXE_T_ATT_OUT);
+            if (!((t.q == 8 && t.k == 8 && t.v == 8) || (kq(t.q) && kq(t.k) && kq(t.v))))
+                bad = where + "the attention projection parts mix Q8_0 with K-quants";
+        }
+    }
+    for (int k = 0; k < 64 && bad.empty(); k++) {
+        const int v = ty(OXE_GLOBAL_LAYER, k);
+        if (v != 8 && !((k == OXE_T_OUTPUT || k == OXE_T_TOK_EMBD) && kq(v))) bad = "global kind " + std::to_string(k) + " takes no other type";
+    }
+    if (!bad.empty()) {
+        oxe::set_err("typed engine: " + bad);
+        return -1;
+    }
+    mt.output = ty(OXE_GLOBAL_LAYER, OXE_T_OUTPUT);
+    mt.tok_embd = ty(OXE_GLOBAL_LAYER, OXE_T_TOK_EMBD);
+    return oxe::create_engine(desc, seed, n_ctx, false, nullptr, &mt, out);
+}
+
 void oxe_engine_destroy(oxe_engine *e) { delete (Engine *)e; }
 
 int oxe_engine_synth_weights(oxe_engine *e) { return ((Engine *)e)->synth_weights(); }

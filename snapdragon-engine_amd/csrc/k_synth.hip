@@ -89,6 +89,53 @@ int synth_q8(uint64_t seed, int layer, int kind_a, int kind_b, int64_t rows, int
     return hipGetLastError() == hipSuccess ? 0 : -2;
 }
 
+// Synthetic K-quant tensors (the oracle's oxo_synth_kq, oracle/kquants.cpp, so a typed engine built
+// on the device holds the oracle's typed weights): block i of tensor (seed, layer, kind), flat over
+// [expert][row][k / 256], is the first bb bytes of the words oxe_rng(key, 32 i + j), j < 32, with
+// its fp16 fields from the scale key: Q4_K / Q5_K d = fp16(lo + u (hi - lo)) in [0.0005, 0.004),
+// dmin = fp16(d * mean code); Q6_K d in [0.00005, 0.0003); Q3_K d in [0.0005, 0.004). One thread
+// per block.
+__global__ void synth_kq_kernel(uint64_t key, uint64_t skey, int type, int bb, int64_t nb, uint8_t *out) {
+    for (int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; b < nb; b += (int64_t)gridDim.x * blockDim.x) {
+        uint8_t *blk = out + b * bb;
+        for (int j = 0; j < 32; j++) {
+            const uint64_t w = oxe_rng(key, 32 * (uint64_t)b + (uint64_t)j);
+            for (int i = 0; i < 8 && 8 * j + i < bb; i++) blk[8 * j + i] = (uint8_t)(w >> (8 * i));
+        }
+        auto f16_in = [&](uint64_t i, float lo, float hi) {
+            const float u = oxe_synth_unit(skey, i);
+            const float t = u * (hi - lo);
+            return oxe_f32_to_f16_rne(lo + t);
+        };
+        auto put16 = [&](int off, uint16_t h) {
+            blk[off] = (uint8_t)h;
+            blk[off + 1] = (uint8_t)(h >> 8);
+        };
+        if (type == 12 || type == 13) {
+            const uint16_t h0 = f16_in(2 * (uint64_t)b, 0.0005f, 0.004f);
+            put16(0, h0);
+            put16(2, oxe_f32_to_f16_rne(h2f(h0) * (type == 12 ? 7.5f : 15.5f)));
+        } else if (type == 14) {
+            put16(208, f16_in(2 * (uint64_t)b, 0.00005f, 0.0003f));
+        } else {
+            put16(108, f16_in(2 * (uint64_t)b, 0.0005f, 0.004f));
+        }
+    }
+}
+
+// rows x k of a matrix in another type than Q8_0 (rows counts every expert of an expert tensor):
+// K-quant blocks (ggml type 11..14) or F32 values (0)
+int synth_raw(uint64_t seed, int layer, int kind, int type, int64_t rows, int64_t k, void *out, hipStream_t st) {
+    if (type == 0) return synth_f32(seed, layer, kind, rows * k, (float *)out, st);
+    const int bb = type == 11 ? 110 : type == 12 ? 144 : type == 13 ? 176 : type == 14 ? 210 : 0;
+    if (!bb || k % 256) return -1;
+    const int64_t nb = rows * (k / 256);
+    const unsigned grid = (unsigned)std::min<int64_t>((nb + 255) / 256, 65536);
+    hipLaunchKernelGGL(synth_kq_kernel, dim3(grid), dim3(256), 0, st, oxe_tensor_key(seed, layer, kind),
+                       oxe_tensor_key(seed, layer, kind + OXE_T_SCALE_OFFSET), type, bb, nb, (uint8_t *)out);
+    return hipGetLastError() == hipSuccess ? 0 : -2;
+}
+
 int synth_f32(uint64_t seed, int layer, int kind, int64_t n, float *out, hipStream_t st) {
     const unsigned grid = (unsigned)std::min<int64_t>((n + 255) / 256, 4096);
     hipLaunchKernelGGL(synth_f32_kernel, dim3(grid), dim3(256), 0, st, oxe_tensor_key(seed, layer, kind), kind, n, out);

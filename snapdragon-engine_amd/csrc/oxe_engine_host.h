@@ -589,44 +589,78 @@ struct Engine {
     }
 
     int synth_weights() {
-        if (kq) {
-            set_err("synth_weights: the engine holds K-quant / F32 matrices, which come from a model file");
-            return -1;
-        }
         int rc = 0;
         auto chk = [&](int r) { if (r) rc = r; };
+        // a matrix kept in another type (an engine created with types): the oracle's synthetic
+        // K-quant blocks or F32 values of the same tensor; groups: the experts of an expert tensor
+        auto raw = [&](const RawW &r, int il, int kind, int64_t groups) {
+            if (r.type != 8) chk(synth_raw(seed, il, kind, r.type, groups * r.rows, r.k, r.w, st));
+        };
         const int nl_total = d.n_layer + 1;
         for (int il = 0; il < nl_total; il++) {
             LayerW &w = L[il];
             chk(synth_f32(seed, il, OXE_T_ATTN_NORM, E, w.attn_norm, st));
             chk(synth_f32(seed, il, OXE_T_POST_NORM, E, w.post_norm, st));
             if (!w.att) {
-                chk(synth_q8(seed, il, OXE_T_DN_QKV, -1, NCH, E, NCH, 0, w.proj.q, w.proj.d, st));
-                chk(synth_q8(seed, il, OXE_T_DN_Z, -1, DIN, E, DIN, 0, w.proj.q + (int64_t)DN_Z * E, w.proj.d + (int64_t)DN_Z * E / 32, st));
-                chk(synth_q8(seed, il, OXE_T_DN_BETA, -1, NVH, E, NVH, 0, w.proj.q + (int64_t)DN_BETA * E, w.proj.d + (int64_t)DN_BETA * E / 32, st));
-                chk(synth_q8(seed, il, OXE_T_DN_ALPHA, -1, NVH, E, NVH, 0, w.proj.q + (int64_t)DN_ALPHA * E, w.proj.d + (int64_t)DN_ALPHA * E / 32, st));
-                chk(synth_q8(seed, il, OXE_T_DN_OUT, -1, E, DIN, E, 0, w.out.q, w.out.d, st));
+                if (!w.kq_proj()) {
+                    chk(synth_q8(seed, il, OXE_T_DN_QKV, -1, NCH, E, NCH, 0, w.proj.q, w.proj.d, st));
+                    chk(synth_q8(seed, il, OXE_T_DN_Z, -1, DIN, E, DIN, 0, w.proj.q + (int64_t)DN_Z * E, w.proj.d + (int64_t)DN_Z * E / 32, st));
+                } else {
+                    raw(w.qkv_r, il, OXE_T_DN_QKV, 1);
+                    raw(w.z_r, il, OXE_T_DN_Z, 1);
+                }
+                if (w.beta_r.type == 8) {
+                    chk(synth_q8(seed, il, OXE_T_DN_BETA, -1, NVH, E, NVH, 0, w.proj.q + (int64_t)DN_BETA * E, w.proj.d + (int64_t)DN_BETA * E / 32, st));
+                    chk(synth_q8(seed, il, OXE_T_DN_ALPHA, -1, NVH, E, NVH, 0, w.proj.q + (int64_t)DN_ALPHA * E, w.proj.d + (int64_t)DN_ALPHA * E / 32, st));
+                } else {
+                    raw(w.beta_r, il, OXE_T_DN_BETA, 1);
+                    raw(w.alpha_r, il, OXE_T_DN_ALPHA, 1);
+                }
+                if (w.out_r.type == 8) chk(synth_q8(seed, il, OXE_T_DN_OUT, -1, E, DIN, E, 0, w.out.q, w.out.d, st));
+                else raw(w.out_r, il, OXE_T_DN_OUT, 1);
                 chk(synth_f32(seed, il, OXE_T_DN_CONV, (int64_t)NCH * KC, w.conv, st));
                 chk(synth_f32(seed, il, OXE_T_DN_A, NVH, w.ssm_a, st));
                 chk(synth_f32(seed, il, OXE_T_DN_DT, NVH, w.dt_bias, st));
                 chk(synth_f32(seed, il, OXE_T_DN_NORM, HV, w.ssm_norm, st));
             } else {
-                chk(synth_q8(seed, il, OXE_T_ATT_Q, -1, NH * 2 * HD, E, NH * 2 * HD, 0, w.proj.q, w.proj.d, st));
-                chk(synth_q8(seed, il, OXE_T_ATT_K, -1, NKV * HD, E, NKV * HD, 0, w.proj.q + (int64_t)AT_K * E, w.proj.d + (int64_t)AT_K * E / 32, st));
-                chk(synth_q8(seed, il, OXE_T_ATT_V, -1, NKV * HD, E, NKV * HD, 0, w.proj.q + (int64_t)AT_V * E, w.proj.d + (int64_t)AT_V * E / 32, st));
-                chk(synth_q8(seed, il, OXE_T_ATT_OUT, -1, E, NH * HD, E, 0, w.out.q, w.out.d, st));
+                if (!w.kq_proj()) {
+                    chk(synth_q8(seed, il, OXE_T_ATT_Q, -1, NH * 2 * HD, E, NH * 2 * HD, 0, w.proj.q, w.proj.d, st));
+                    chk(synth_q8(seed, il, OXE_T_ATT_K, -1, NKV * HD, E, NKV * HD, 0, w.proj.q + (int64_t)AT_K * E, w.proj.d + (int64_t)AT_K * E / 32, st));
+                    chk(synth_q8(seed, il, OXE_T_ATT_V, -1, NKV * HD, E, NKV * HD, 0, w.proj.q + (int64_t)AT_V * E, w.proj.d + (int64_t)AT_V * E / 32, st));
+                } else {
+                    raw(w.q_r, il, OXE_T_ATT_Q, 1);
+                    raw(w.k_r, il, OXE_T_ATT_K, 1);
+                    raw(w.v_r, il, OXE_T_ATT_V, 1);
+                }
+                if (w.out_r.type == 8) chk(synth_q8(seed, il, OXE_T_ATT_OUT, -1, E, NH * HD, E, 0, w.out.q, w.out.d, st));
+                else raw(w.out_r, il, OXE_T_ATT_OUT, 1);
                 chk(synth_f32(seed, il, OXE_T_ATT_QNORM, HD, w.q_norm, st));
                 chk(synth_f32(seed, il, OXE_T_ATT_KNORM, HD, w.k_norm, st));
             }
             chk(synth_f32(seed, il, OXE_T_ROUTER, (int64_t)NEXP * E, w.router, st));
             chk(synth_f32(seed, il, OXE_T_SHEXP_GATE, E, w.shexp_gate, st));
-            chk(synth_q8(seed, il, OXE_T_GATE_SHEXP, OXE_T_UP_SHEXP, 2 * FFSH, E, FFSH, 0, w.shexp_gu.q, w.shexp_gu.d, st));
-            chk(synth_q8(seed, il, OXE_T_DOWN_SHEXP, -1, E, FFSH, E, 0, w.shexp_down.q, w.shexp_down.d, st));
-            for (int e = 0; e < NEXP; e++) {
-                chk(synth_q8(seed, il, OXE_T_GATE_EXPS, OXE_T_UP_EXPS, 2 * FF, E, FF, e, w.exp_gu.q + (int64_t)e * 2 * FF * E,
-                             w.exp_gu.d + (int64_t)e * 2 * FF * E / 32, st));
-                chk(synth_q8(seed, il, OXE_T_DOWN_EXPS, -1, E, FF, E, e, w.exp_down.q + (int64_t)e * E * FF,
-                             w.exp_down.d + (int64_t)e * E * FF / 32, st));
+            if (w.sh_gate_r.type == 8) {
+                chk(synth_q8(seed, il, OXE_T_GATE_SHEXP, OXE_T_UP_SHEXP, 2 * FFSH, E, FFSH, 0, w.shexp_gu.q, w.shexp_gu.d, st));
+            } else {
+                raw(w.sh_gate_r, il, OXE_T_GATE_SHEXP, 1);
+                raw(w.sh_up_r, il, OXE_T_UP_SHEXP, 1);
+            }
+            if (w.sh_down_r.type == 8) chk(synth_q8(seed, il, OXE_T_DOWN_SHEXP, -1, E, FFSH, E, 0, w.shexp_down.q, w.shexp_down.d, st));
+            else raw(w.sh_down_r, il, OXE_T_DOWN_SHEXP, 1);
+            if (w.exp_gate_r.type == 8) {
+                for (int e = 0; e < NEXP; e++)
+                    chk(synth_q8(seed, il, OXE_T_GATE_EXPS, OXE_T_UP_EXPS, 2 * FF, E, FF, e, w.exp_gu.q + (int64_t)e * 2 * FF * E,
+                                 w.exp_gu.d + (int64_t)e * 2 * FF * E / 32, st));
+            } else {
+                raw(w.exp_gate_r, il, OXE_T_GATE_EXPS, NEXP);
+                raw(w.exp_up_r, il, OXE_T_UP_EXPS, NEXP);
+            }
+            if (w.exp_down_r.type == 8) {
+                for (int e = 0; e < NEXP; e++)
+                    chk(synth_q8(seed, il, OXE_T_DOWN_EXPS, -1, E, FF, E, e, w.exp_down.q + (int64_t)e * E * FF,
+                                 w.exp_down.d + (int64_t)e * E * FF / 32, st));
+            } else {
+                raw(w.exp_down_r, il, OXE_T_DOWN_EXPS, NEXP);
             }
             if (il == d.n_layer) {
                 chk(synth_q8(seed, il, OXE_T_EH_PROJ, -1, E, 2 * E, E, 0, w.eh_proj.q, w.eh_proj.d, st));
@@ -635,8 +669,12 @@ struct Engine {
                 chk(synth_f32(seed, il, OXE_T_HEAD_NORM, E, w.head_norm, st));
             }
         }
-        chk(synth_q8(seed, OXE_GLOBAL_LAYER, OXE_T_TOK_EMBD, -1, d.n_vocab, E, d.n_vocab, 0, m.tok_embd.q, m.tok_embd.d, st));
-        chk(synth_q8(seed, OXE_GLOBAL_LAYER, OXE_T_OUTPUT, -1, d.n_vocab, E, d.n_vocab, 0, m.output.q, m.output.d, st));
+        if (m.tok_embd_r.type == 8)
+            chk(synth_q8(seed, OXE_GLOBAL_LAYER, OXE_T_TOK_EMBD, -1, d.n_vocab, E, d.n_vocab, 0, m.tok_embd.q, m.tok_embd.d, st));
+        else raw(m.tok_embd_r, OXE_GLOBAL_LAYER, OXE_T_TOK_EMBD, 1);
+        if (m.output_r.type == 8)
+            chk(synth_q8(seed, OXE_GLOBAL_LAYER, OXE_T_OUTPUT, -1, d.n_vocab, E, d.n_vocab, 0, m.output.q, m.output.d, st));
+        else raw(m.output_r, OXE_GLOBAL_LAYER, OXE_T_OUTPUT, 1);
         chk(synth_f32(seed, OXE_GLOBAL_LAYER, OXE_T_OUT_NORM, E, m.out_norm, st));
         if (hipStreamSynchronize(st) != hipSuccess) return -2;
         return rc;

@@ -238,6 +238,7 @@ def _engine_sigs(L):
         "oxe_last_error": (C.c_char_p, []),
         "oxe_engine_create": (i32, [vp, C.c_uint64, i32, C.POINTER(C.c_void_p)]),
         "oxe_engine_create_on": (i32, [vp, C.c_uint64, i32, vp, C.POINTER(C.c_void_p)]),
+        "oxe_engine_create_typed": (i32, [vp, C.c_uint64, i32, vp, C.POINTER(C.c_void_p)]),
         "oxe_engine_verify_probe": (i32, [vp, u32p, i32, i32, u32p, C.POINTER(C.c_float), C.POINTER(C.c_int)]),
         "oxe_engine_destroy": (None, [vp]),
         "oxe_engine_synth_weights": (i32, [vp]),
@@ -456,20 +457,60 @@ class Gguf:
         return d
 
 
+# GGUF tensor name (after "blk.N." for layer tensors) -> tensor kind (include/oxe_model.h) of every
+# matrix whose type the engine takes from the file (the names the reference's model reader checks,
+# crates/model/src/desc.rs:140-175)
+_MATRIX_KIND = {"attn_qkv.weight": 2, "attn_gate.weight": 3, "ssm_beta.weight": 4, "ssm_alpha.weight": 5,
+                "ssm_out.weight": 10, "attn_q.weight": 11, "attn_k.weight": 12, "attn_v.weight": 13,
+                "attn_output.weight": 16, "ffn_gate_exps.weight": 19, "ffn_up_exps.weight": 20,
+                "ffn_down_exps.weight": 21, "ffn_gate_shexp.weight": 22, "ffn_up_shexp.weight": 23,
+                "ffn_down_shexp.weight": 24, "nextn.eh_proj.weight": 25}
+_GLOBAL_KIND = {"token_embd.weight": 29, "output.weight": 31}
+_TYPE_ID = {"F32": 0, "Q8_0": 8, "Q3_K": 11, "Q4_K": 12, "Q5_K": 13, "Q6_K": 14}
+
+
+def types_from_tensors(tensors):
+    """{(layer, kind): ggml type id} of the matrices that are not Q8_0 in a GGUF tensor table
+    ((name, type name) pairs, e.g. oxe_gguf's listing), the `types` argument of Engine: an engine
+    with a model file's matrix types and synthetic weights."""
+    out = {}
+    for name, tname in tensors:
+        if name.startswith("blk."):
+            layer, rest = name[4:].split(".", 1)
+            key = (int(layer), _MATRIX_KIND.get(rest))
+        else:
+            key = (63, _GLOBAL_KIND.get(name))
+        if key[1] is None:
+            continue
+        if tname not in _TYPE_ID:
+            raise ValueError(f"{name}: type {tname} is not a matrix type of the engine")
+        if _TYPE_ID[tname] != 8:
+            out[key] = _TYPE_ID[tname]
+    return out
+
+
 class Engine:
     """MI355X engine through the C ABI (Engine::{verify, commit, step, mtp_run, mtp_seed})."""
 
-    def __init__(self, desc, seed=0, n_ctx=1024, synth=True, stream=None):
+    def __init__(self, desc, seed=0, n_ctx=1024, synth=True, stream=None, types=None):
         """stream: a caller's hipStream_t (an int, e.g. torch.cuda.Stream().cuda_stream) that every
-        launch and copy of the engine then goes to (oxe_engine_create_on); None: the engine's own."""
-        import numpy as np  # noqa: F401
+        launch and copy of the engine then goes to (oxe_engine_create_on); None: the engine's own.
+        types: {(layer, kind): ggml type id} of matrices that are not Q8_0 (layer GLOBAL_LAYER = 63:
+        the global tensors), as a model file holds them (oxe_engine_create_typed); the synthetic
+        weights then fill each in its type."""
+        import numpy as np
         L = lib()
         if not hasattr(L, "_engine_sigs"):
             _engine_sigs(L)
             L._engine_sigs = True
         self.desc = desc
         h = C.c_void_p()
-        if stream is None:
+        if types:
+            tt = np.full(64 * 64, 8, np.int32)
+            for (layer, kind), ty in types.items():
+                tt[layer * 64 + kind] = ty
+            rc = L.oxe_engine_create_typed(C.byref(desc), seed, n_ctx, tt.ctypes.data_as(C.c_void_p), C.byref(h))
+        elif stream is None:
             rc = L.oxe_engine_create(C.byref(desc), seed, n_ctx, C.byref(h))
         else:
             rc = L.oxe_engine_create_on(C.byref(desc), seed, n_ctx, C.c_void_p(int(stream)), C.byref(h))

@@ -120,3 +120,25 @@ def test_kquant_projections_mtp_steps_match_oracle_driver(typed_file):
     assert [int(t) for t in gen] == want
     assert nxt == x
     g.close()
+
+
+def test_typed_engine_synthesised_on_device_matches_oracle():
+    """the same types without a file: oxe_engine_create_typed + the device's synthetic weights (the
+    oracle's K-quant blocks and F32 values generated on the device) decode like the typed oracle"""
+    import oxe_amd as A
+    d = O.desc_small()
+    ty = model_types(d)
+    g = A.Engine(d, seed=SEED, n_ctx=512, types=ty)
+    assert not g.fused
+    ref = O.Engine(d, seed=SEED, n_ctx=512, types=ty)
+    toks = [int(v) % d.n_vocab for v in O.bench_prompt(5)]
+    print("prefill 5 tokens", flush=True)
+    nx = g.prefill(toks)
+    assert nx == [ref.step(t) for t in toks][-1]
+    assert np.array_equal(bits(g.logits(0)), bits(ref.logits(0)))
+    assert np.array_equal(bits(g.hidden(0)), bits(ref.hidden(0)))
+    out = g.verify([nx, 17])
+    assert list(out) == list(ref.verify([nx, 17]))
+    for lane in (0, 1):
+        assert np.array_equal(bits(g.logits(lane)), bits(ref.logits(lane))), lane
+    g.close()
