@@ -318,29 +318,76 @@ OXE_DEV void pf_load(u32x4 (&pf)[PF], const uint8_t *w, int64_t g, int64_t nr, i
     for (int j = 0; j < PF; j++) pf[j] = __builtin_nontemporal_load(src + min(t + 64 * j, n16 - 1));
 }
 
+// the consumer of an engine phase's GEMV, applied at its store (ctl null: lane u's value to s[u][r]):
+// row r of lane u < ctl->nl, in an active run only, goes to dst[u][r] (lane stride ld), plus
+// resid[u][r] when resid is given (one fp32 add, as a separate pass would make it), and as fp16 to
+// the V^T cache row r at position pos0 + u when vt is given
+struct KqEpi {
+    const RunCtl *ctl = nullptr;
+    float *dst = nullptr;
+    int64_t ld = 0;
+    const float *resid = nullptr;
+    uint16_t *vt = nullptr;
+    int64_t vt_ld = 0;
+};
+
+// up to four matrices of one type and row length over the same activation in one launch (a
+// projection's parts): groups are numbered through the segments in order; segment i's rows go to
+// dst at row offset off[i] (its lane values to s when there is no epilogue: one segment then), and
+// segment vseg's also to V^T
+constexpr int KQ_SEGS = 4;
+struct KqSegs {
+    int n = 0;
+    int vseg = -1;
+    int64_t ngroups = 0;
+    const uint8_t *w[KQ_SEGS] = {};
+    int64_t nr[KQ_SEGS] = {};
+    int64_t g0[KQ_SEGS] = {};
+    int64_t off[KQ_SEGS] = {};
+};
+
+struct SegRef {
+    const uint8_t *w;
+    int64_t nr, gl, off;   // rows, the group's index within the segment, row offset in dst
+    bool v;
+};
+
+// the segment of group g (fixed indices only, so the table stays in the kernel arguments)
+OXE_DEV SegRef seg_ref(const KqSegs &S, int64_t g) {
+    SegRef r{S.w[0], S.nr[0], g, S.off[0], S.vseg == 0};
+#pragma unroll
+    for (int j = 1; j < KQ_SEGS; j++)
+        if (j < S.n && g >= S.g0[j]) r = SegRef{S.w[j], S.nr[j], g - S.g0[j], S.off[j], S.vseg == j};
+    return r;
+}
+
 // one group of 4 rows (g may be past the end: then nothing is written): its prefetched bytes (pf)
 // and the rest to LDS, pf refilled with group g_next, then the units and the chains
 template <int TY, int NL, int PF>
-OXE_DEV void vl_group(u32x4 (&pf)[PF], int64_t g, int64_t g_next, const uint8_t *__restrict__ w, int nb, int64_t nr,
-                      float *__restrict__ s, uint8_t *wl, const uint32_t *yh, const float *yd, int *res) {
+OXE_DEV void vl_group(u32x4 (&pf)[PF], int64_t g, int64_t g_next, const KqSegs &S, int nb, float *__restrict__ s,
+                      const KqEpi &epi, uint8_t *wl, const uint32_t *yh, const float *yd, int *res) {
     constexpr int BB = BT<TY>::B;
     constexpr int RES = BT<TY>::R;
     constexpr int RS = (NL * RES) | 1;   // odd per-thread stride: no bank conflicts between threads
     const int row_bytes = nb * BB, ls = y_lane_words(nb);
     const int t = threadIdx.x, ri = t >> 4, u = t & 15;
-    const int64_t ngroups = (nr + GR - 1) / GR;
+    const int64_t ngroups = S.ngroups;
     const bool gin = g < ngroups;
-    const int64_t gd = gin ? g : ngroups - 1;   // the group whose bytes pf holds
-    const int sp = (int)(min((int64_t)GR, nr - gd * GR) * row_bytes), n16 = sp / 16;
-    const u32x4 *src = (const u32x4 *)(w + gd * GR * row_bytes);
+    const SegRef sg = seg_ref(S, gin ? g : ngroups - 1);   // the group whose bytes pf holds
+    const int64_t nr = sg.nr;
+    const int sp = (int)(min((int64_t)GR, nr - sg.gl * GR) * row_bytes), n16 = sp / 16;
+    const u32x4 *src = (const u32x4 *)(sg.w + sg.gl * GR * row_bytes);
     __syncthreads();   // the previous group's LDS reads are done
 #pragma unroll
     for (int j = 0; j < PF; j++) ((u32x4 *)wl)[min(t + 64 * j, n16 - 1)] = pf[j];   // clamped: same bytes
     for (int i = t + 64 * PF; i < n16; i += 64) ((u32x4 *)wl)[i] = src[i];
     for (int i = n16 * 4 + t; i < sp / 4; i += 64) ((uint32_t *)wl)[i] = ((const uint32_t *)src)[i];   // tail
     __syncthreads();
-    pf_load(pf, w, g_next < ngroups ? g_next : ngroups - 1, nr, row_bytes, t);   // in flight meanwhile
-    const int64_t r = gd * GR + ri;
+    {
+        const SegRef sn = seg_ref(S, g_next < ngroups ? g_next : ngroups - 1);
+        pf_load(pf, sn.w, sn.gl, sn.nr, row_bytes, t);   // in flight meanwhile
+    }
+    const int64_t r = sg.gl * GR + ri;
     const bool live = gin && r < nr;
     float acc = 0.0f;
     for (int b0 = 0; b0 < nb; b0 += 8) {
@@ -357,12 +404,21 @@ OXE_DEV void vl_group(u32x4 (&pf)[PF], int64_t g, int64_t g_next, const uint8_t 
             }
         __syncthreads();
     }
-    if (u < NL && live) s[(int64_t)u * nr + r] = acc;
+    if (u < NL && live) {
+        if (!epi.ctl) {
+            s[(int64_t)u * nr + r] = acc;
+        } else if (epi.ctl->active && u < epi.ctl->nl) {
+            const int64_t i = (int64_t)u * epi.ld + sg.off + r;
+            const float v = epi.resid ? acc + epi.resid[i] : acc;
+            epi.dst[i] = v;
+            if (sg.v && epi.vt) epi.vt[r * epi.vt_ld + epi.ctl->pos0 + u] = f2h(v);
+        }
+    }
 }
 
 template <int TY, int NL, int PF>
-__global__ __launch_bounds__(64) void vl_gemv_kernel(const uint8_t *__restrict__ w, int nb, int64_t nr,
-                                                     const uint8_t *__restrict__ y, float *__restrict__ s) {
+__global__ __launch_bounds__(64) void vl_gemv_kernel(KqSegs S, int nb, const uint8_t *__restrict__ y,
+                                                     float *__restrict__ s, KqEpi epi) {
     constexpr int BB = BT<TY>::B;
     extern __shared__ __align__(16) uint8_t lds[];
     const int row_bytes = nb * BB;
@@ -371,7 +427,7 @@ __global__ __launch_bounds__(64) void vl_gemv_kernel(const uint8_t *__restrict__
     float *yd = (float *)(yh + NL * y_lane_words(nb));                   // [NL][nb]
     int *res = (int *)((uint8_t *)yh + align16(NL * nb * (2 * YH + 1) * 4));   // [64][(NL * R) | 1]
     const int t = threadIdx.x;
-    const int64_t ngroups = (nr + GR - 1) / GR, G = gridDim.x;
+    const int64_t ngroups = S.ngroups, G = gridDim.x;
     // the lanes' q8_K blocks (lane l block b is block l nb + b) repacked into halves and scales
     for (int i = t; i < NL * nb * 2 * 36; i += 64) {
         const int wd = i % 36, hb = i / 36, h = hb & 1;
@@ -384,12 +440,15 @@ __global__ __launch_bounds__(64) void vl_gemv_kernel(const uint8_t *__restrict__
     // first LDS stores wait for a's only
     u32x4 pa[PF], pb[PF];
     if ((int64_t)blockIdx.x >= ngroups) return;
-    pf_load(pa, w, blockIdx.x, nr, row_bytes, t);
-    __builtin_amdgcn_sched_barrier(0);
-    pf_load(pb, w, min((int64_t)blockIdx.x + G, ngroups - 1), nr, row_bytes, t);
+    {
+        const SegRef sa = seg_ref(S, blockIdx.x), sb = seg_ref(S, min((int64_t)blockIdx.x + G, ngroups - 1));
+        pf_load(pa, sa.w, sa.gl, sa.nr, row_bytes, t);
+        __builtin_amdgcn_sched_barrier(0);
+        pf_load(pb, sb.w, sb.gl, sb.nr, row_bytes, t);
+    }
     for (int64_t g = blockIdx.x; g < ngroups; g += 2 * G) {
-        vl_group<TY, NL, PF>(pa, g, g + 2 * G, w, nb, nr, s, wl, yh, yd, res);
-        vl_group<TY, NL, PF>(pb, g + G, g + 3 * G, w, nb, nr, s, wl, yh, yd, res);
+        vl_group<TY, NL, PF>(pa, g, g + 2 * G, S, nb, s, epi, wl, yh, yd, res);
+        vl_group<TY, NL, PF>(pb, g + G, g + 3 * G, S, nb, s, epi, wl, yh, yd, res);
     }
 }
 
@@ -399,7 +458,7 @@ size_t vl_gemv_lds(int bb, int rr, int nb, int nl) {
 
 constexpr int KQ_MAX_DEV = 64;
 template <int TY, int NL, int PF>
-int vl_gemv_launch_pf(const uint8_t *w, int nb, int64_t nr, const uint8_t *y, float *s, hipStream_t st) {
+int vl_gemv_launch_pf(const KqSegs &S, int nb, const uint8_t *y, float *s, hipStream_t st, const KqEpi &epi) {
     constexpr int BB = BT<TY>::B;
     const size_t lds = vl_gemv_lds(BB, BT<TY>::R, nb, NL);
     int dev = 0;
@@ -448,30 +507,44 @@ int vl_gemv_launch_pf(const uint8_t *w, int nb, int64_t nr, const uint8_t *y, fl
         }
     }
     const int per_cu = std::min(16, occ);
-    const int64_t ngroups = (nr + GR - 1) / GR;
-    const int64_t grid = std::min<int64_t>(ngroups, (int64_t)ncu * per_cu);
-    hipLaunchKernelGGL((vl_gemv_kernel<TY, NL, PF>), dim3((unsigned)grid), dim3(64), lds, st, w, nb, nr, y, s);
+    const int64_t grid = std::min<int64_t>(S.ngroups, (int64_t)ncu * per_cu);
+    hipLaunchKernelGGL((vl_gemv_kernel<TY, NL, PF>), dim3((unsigned)grid), dim3(64), lds, st, S, nb, y, s, epi);
     return hipGetLastError() == hipSuccess ? 1 : -2;
 }
 
 // registers per prefetch buffer: the smallest of 2, 4, 8 KiB-per-wave steps that holds a whole group
 // (the rest of a larger group is copied to LDS directly)
 template <int TY, int NL>
-int vl_gemv_launch(const uint8_t *w, int nb, int64_t nr, const uint8_t *y, float *s, hipStream_t st) {
+int vl_gemv_launch(const KqSegs &S, int nb, const uint8_t *y, float *s, hipStream_t st, const KqEpi &epi) {
     const int n16 = GR * nb * BT<TY>::B / 16;
-    if (n16 <= 128) return vl_gemv_launch_pf<TY, NL, 2>(w, nb, nr, y, s, st);
-    if (n16 <= 256) return vl_gemv_launch_pf<TY, NL, 4>(w, nb, nr, y, s, st);
-    return vl_gemv_launch_pf<TY, NL, 8>(w, nb, nr, y, s, st);
+    if (n16 <= 128) return vl_gemv_launch_pf<TY, NL, 2>(S, nb, y, s, st, epi);
+    if (n16 <= 256) return vl_gemv_launch_pf<TY, NL, 4>(S, nb, y, s, st, epi);
+    return vl_gemv_launch_pf<TY, NL, 8>(S, nb, y, s, st, epi);
+}
+
+// one matrix [nr rows of nb blocks] as a one-segment table
+inline KqSegs one_seg(const uint8_t *w, int64_t nr) {
+    KqSegs S;
+    S.n = 1;
+    S.w[0] = w;
+    S.nr[0] = nr;
+    S.ngroups = (nr + GR - 1) / GR;
+    return S;
+}
+
+template <int TY>
+int vl_gemv_segs(const KqSegs &S, int nb, const uint8_t *y, int nl, float *s, hipStream_t st, const KqEpi &epi) {
+    switch (nl) {
+        case 1: return vl_gemv_launch<TY, 1>(S, nb, y, s, st, epi);
+        case 2: return vl_gemv_launch<TY, 2>(S, nb, y, s, st, epi);
+        case 3: return vl_gemv_launch<TY, 3>(S, nb, y, s, st, epi);
+        default: return vl_gemv_launch<TY, 4>(S, nb, y, s, st, epi);
+    }
 }
 
 template <int TY>
 int vl_gemv_type(const uint8_t *w, int nb, int64_t nr, const uint8_t *y, int nl, float *s, hipStream_t st) {
-    switch (nl) {
-        case 1: return vl_gemv_launch<TY, 1>(w, nb, nr, y, s, st);
-        case 2: return vl_gemv_launch<TY, 2>(w, nb, nr, y, s, st);
-        case 3: return vl_gemv_launch<TY, 3>(w, nb, nr, y, s, st);
-        default: return vl_gemv_launch<TY, 4>(w, nb, nr, y, s, st);
-    }
+    return vl_gemv_segs<TY>(one_seg(w, nr), nb, y, nl, s, st, KqEpi{});
 }
 
 
@@ -917,28 +990,6 @@ __global__ __launch_bounds__(256) void kq_norm_kernel(const RunCtl *__restrict__
     }
 }
 
-// rows [0, rows) of a part's lane GEMV output (src [NL][rows]) into dst [NL][dst_ld] (the projection
-// buffer at the part's offset); V rows also to V^T at pos0 + lane (vt != null)
-__global__ __launch_bounds__(256) void kq_scatter_kernel(const RunCtl *__restrict__ ctl, const float *src, int rows,
-                                                         float *dst, int64_t dst_ld, uint16_t *vt, int64_t vt_ld) {
-    if (!ctl->active) return;
-    const int l = blockIdx.y, r = blockIdx.x * 256 + threadIdx.x;
-    if (l >= ctl->nl || r >= rows) return;
-    const float v = src[(int64_t)l * rows + r];
-    dst[(int64_t)l * dst_ld + r] = v;
-    if (vt) vt[(int64_t)r * vt_ld + ctl->pos0 + l] = f2h(v);
-}
-
-// mixer_out's residual (engine.rs:2573-2609): x1 = out + x, per lane of the run
-__global__ __launch_bounds__(256) void kq_residual_kernel(const RunCtl *__restrict__ ctl, const float *out, const float *x,
-                                                          float *x1) {
-    if (!ctl->active) return;
-    const int l = blockIdx.y, r = blockIdx.x * 256 + threadIdx.x;
-    if (l >= ctl->nl || r >= shp::E) return;
-    const int64_t i = (int64_t)l * shp::E + r;
-    x1[i] = out[i] + x[i];
-}
-
 }  // namespace kq
 
 int launch_ba_f32(const RunCtl *ctl, const ModelRt &m, const LayerW &w, const float *x, const ActBufs &b, hipStream_t st) {
@@ -1013,12 +1064,12 @@ int launch_kq_head(const RunCtl *ctl, const ModelRt &m, const float *norm_w, con
 }
 
 // the lane GEMV over a matrix of ggml type 11..14 (nb blocks per row), s[l * rows + r]; 1: done
-static int vl_gemv_any(int type, const uint8_t *w, int nb, int64_t rows, const uint8_t *y, float *s, hipStream_t st) {
+static int vl_gemv_any(int type, const kq::KqSegs &S, int nb, const uint8_t *y, hipStream_t st, const kq::KqEpi &epi) {
     switch (type) {
-        case 11: return kq::vl_gemv_type<3>(w, nb, rows, y, OXE_NL, s, st);
-        case 12: return kq::vl_gemv_type<4>(w, nb, rows, y, OXE_NL, s, st);
-        case 13: return kq::vl_gemv_type<5>(w, nb, rows, y, OXE_NL, s, st);
-        case 14: return kq::vl_gemv_type<6>(w, nb, rows, y, OXE_NL, s, st);
+        case 11: return kq::vl_gemv_segs<3>(S, nb, y, OXE_NL, nullptr, st, epi);
+        case 12: return kq::vl_gemv_segs<4>(S, nb, y, OXE_NL, nullptr, st, epi);
+        case 13: return kq::vl_gemv_segs<5>(S, nb, y, OXE_NL, nullptr, st, epi);
+        case 14: return kq::vl_gemv_segs<6>(S, nb, y, OXE_NL, nullptr, st, epi);
         default: return 0;
     }
 }
@@ -1046,14 +1097,34 @@ int launch_kq_proj(const RunCtl *ctl, const ModelRt &m, const LayerW &w, const f
     const Part at[3] = {{&w.q_r, 0, false}, {&w.k_r, AT_K, false}, {&w.v_r, AT_V, true}};
     const Part *ps = w.att ? at : dn;
     const int np = w.att ? 3 : 4;
-    uint16_t *vt = w.att ? m.vcache + (int64_t)w.index * NKV * HD * m.n_ctx : nullptr;
+    kq::KqEpi epi;       // the rows straight into the run's projection buffer (V rows also to V^T)
+    epi.ctl = ctl;
+    epi.dst = b.proj;
+    epi.ld = DN_ROWS;
+    epi.vt = w.att ? m.vcache + (int64_t)w.index * NKV * HD * m.n_ctx : nullptr;
+    epi.vt_ld = m.n_ctx;
+    // consecutive parts of one K-quant type share a launch
+    kq::KqSegs S;
+    int ty = 0;
+    auto flush = [&]() {
+        const int rc = S.n ? vl_gemv_any(ty, S, (int)(E / kq::QK), b.xk, st, epi) : 1;
+        S = kq::KqSegs{};
+        return rc == 1;
+    };
     for (int i = 0; i < np; i++) {
         const RawW &r = *ps[i].r;
         if (ps[i].off < row_begin || r.type < 11 || r.type > 14) continue;   // F32 beta / alpha: launch_ba_f32
-        if (vl_gemv_any(r.type, r.w, (int)(E / kq::QK), r.rows, b.xk, b.kqo, st) != 1) return -2;
-        hipLaunchKernelGGL(kq::kq_scatter_kernel, dim3((unsigned)((r.rows + 255) / 256), OXE_NL), dim3(256), 0, st, ctl, b.kqo,
-                           (int)r.rows, b.proj + ps[i].off, (int64_t)DN_ROWS, ps[i].v ? vt : nullptr, (int64_t)m.n_ctx);
+        if (S.n && r.type != ty && !flush()) return -2;
+        ty = r.type;
+        const int j = S.n++;
+        S.w[j] = (const uint8_t *)r.w;
+        S.nr[j] = r.rows;
+        S.g0[j] = S.ngroups;
+        S.off[j] = ps[i].off;
+        if (ps[i].v) S.vseg = j;
+        S.ngroups += (r.rows + kq::GR - 1) / kq::GR;
     }
+    if (!flush()) return -2;
     return hipGetLastError() == hipSuccess ? 0 : -2;
 }
 
@@ -1062,8 +1133,12 @@ int launch_kq_out(const RunCtl *ctl, const ModelRt &m, const LayerW &w, const fl
     using namespace shp;
     const RawW &r = w.out_r;
     quant_k(b.o32, (int64_t)OXE_NL * MIX_W / kq::QK, b.ok, st);
-    if (vl_gemv_any(r.type, r.w, (int)(MIX_W / kq::QK), E, b.ok, b.kqo, st) != 1) return -2;
-    hipLaunchKernelGGL(kq::kq_residual_kernel, dim3(E / 256, OXE_NL), dim3(256), 0, st, ctl, b.kqo, x, b.x1);
+    kq::KqEpi epi;       // mixer_out's residual (engine.rs:2573-2609) at the store: x1 = out + x
+    epi.ctl = ctl;
+    epi.dst = b.x1;
+    epi.ld = E;
+    epi.resid = x;
+    if (vl_gemv_any(r.type, kq::one_seg((const uint8_t *)r.w, E), (int)(MIX_W / kq::QK), b.ok, st, epi) != 1) return -2;
     return hipGetLastError() == hipSuccess ? 0 : -2;
 }
 

@@ -168,7 +168,6 @@ struct ActBufs {
     float *o32;           // the mixer's gated outputs in f32 [NL][4096] (a K-quant output projection)
     uint8_t *ok;          // their q8_K blocks [NL][4096 / 256]
     float *emb;           // the lanes' embedded tokens [NL][n_embd] (a K-quant token embedding)
-    float *kqo;           // [NL][DN_ROWS] outputs of a K-quant projection part or output projection
     uint32_t *counters;   // per-kernel completion counters (zeroed at allocation; self-resetting)
 };
 

@@ -396,7 +396,6 @@ struct Engine {
             b.o32 = alloc<float>(OXE_NL * MIX_W);
             b.ok = alloc<uint8_t>((size_t)OXE_NL * (MIX_W / 256) * 292);
             b.emb = alloc<float>(OXE_NL * E);
-            b.kqo = alloc<float>((size_t)OXE_NL * DN_ROWS);
         }
         b.counters = alloc<uint32_t>(CNT_N);
         ctl = alloc<RunCtl>(2);
