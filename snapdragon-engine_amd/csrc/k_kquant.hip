@@ -638,11 +638,11 @@ __global__ __launch_bounds__(256) void ba_f32_kernel(const RunCtl *__restrict__ 
     }
 }
 
-// ---- MoE gate / up over K-quant matrices: workgroup (unit u, tile of 16 rows), u < OXE_MAX_UNION
-// the union's expert u, u = OXE_MAX_UNION the shared expert. Thread (row t / 16, half block t % 16)
-// forms its half block's integers for every lane; threads t % 16 < NL then run lane t % 16's chain
-// over the row's 8 blocks; gate first, then up, then silu(g) * u (ggml_v_silu, as swiglu) for
-// every lane that routed to the expert (the shared expert: every lane).
+// ---- MoE gate / up over K-quant matrices: workgroup (unit u, tile of 8 rows), u < OXE_MAX_UNION
+// the union's expert u, u = OXE_MAX_UNION the shared expert. Thread (matrix t / 128: gate, up; row
+// t / 16 % 8, half block t % 16) forms its half block's integers for every lane; threads t % 16 < NL
+// then run lane t % 16's chain over the row's 8 blocks, gate and up at once; then silu(g) * u
+// (ggml_v_silu, as swiglu) for every lane that routed to the expert (the shared expert: every lane).
 struct KqGuArgs {
     const uint8_t *xk;          // [NL][E / 256] q8_K blocks of xn
     RawW gate, up, sh_gate, sh_up;
@@ -652,6 +652,7 @@ struct KqGuArgs {
     int do_exp, do_sh;
 };
 constexpr int GU_NB = shp::E / QK;   // 8 blocks per row
+constexpr int GU_R = 8;              // rows per workgroup
 static_assert(GU_NB * 2 == 16 && shp::FF == shp::FFSH, "16 half blocks per row; one tiling for both");
 
 template <int NL>
@@ -660,9 +661,10 @@ __global__ __launch_bounds__(256) void kq_gu_kernel(const RunCtl *__restrict__ c
     __shared__ uint32_t yh[NL * GU_NB * 2 * YH];
     __shared__ float yd[NL * GU_NB];
     __shared__ int res[256 * RS];
+    __shared__ float s_gu[2][GU_R][NL];
     if (!ctl->active) return;
-    const int nl = ctl->nl, t = threadIdx.x, ri = t >> 4, hu = t & 15;
-    const int u = blockIdx.x / (shp::FF / 16), tile = blockIdx.x % (shp::FF / 16);
+    const int nl = ctl->nl, t = threadIdx.x, which = t >> 7, ri = (t >> 4) & (GU_R - 1), hu = t & 15;
+    const int u = blockIdx.x / (shp::FF / GU_R), tile = blockIdx.x % (shp::FF / GU_R);
     const bool sh = u == OXE_MAX_UNION;
     if (sh ? !a.do_sh : !a.do_exp) return;
     int e = 0;
@@ -675,9 +677,8 @@ __global__ __launch_bounds__(256) void kq_gu_kernel(const RunCtl *__restrict__ c
     }
     stage_q8k(a.xk, NL * GU_NB, yh, yd);
     __syncthreads();
-    const int row = tile * 16 + ri;
-    float g = 0.0f, v = 0.0f;
-    for (int which = 0; which < 2; which++) {
+    const int row = tile * GU_R + ri;
+    {
         const RawW &W = sh ? (which ? a.sh_up : a.sh_gate) : (which ? a.up : a.gate);
         const int type = W.type, rs = res_of(type);
         const int64_t rb = raw_row_bytes(W);
@@ -688,16 +689,15 @@ __global__ __launch_bounds__(256) void kq_gu_kernel(const RunCtl *__restrict__ c
         if (hu < NL) {
             float acc = 0.0f;
             for (int b = 0; b < GU_NB; b++) {
-                const int *r0 = res + (ri * 16 + 2 * b) * RS + hu * rs, *r1 = res + (ri * 16 + 2 * b + 1) * RS + hu * rs;
+                const int *r0 = res + ((t & ~15) + 2 * b) * RS + hu * rs, *r1 = res + ((t & ~15) + 2 * b + 1) * RS + hu * rs;
                 acc = chain_rt(type, acc, wr + b * kq_block_bytes(type), yd[hu * GU_NB + b], r0, r1);
             }
-            if (which) v = acc;
-            else g = acc;
+            s_gu[which][ri][hu] = acc;
         }
         __syncthreads();
     }
-    if (hu < NL && hu < nl) {
-        const float h = v_silu(g) * v;
+    if (which == 0 && hu < NL && hu < nl) {
+        const float h = v_silu(s_gu[0][ri][hu]) * s_gu[1][ri][hu];
         if (sh) {
             a.hsh[(int64_t)hu * shp::FFSH + row] = h;
         } else {
@@ -727,7 +727,7 @@ struct KqDownArgs {
     float *x2;
     unsigned long long *amax_key;
 };
-constexpr int DN_R = 16;                     // output rows per workgroup
+constexpr int DN_R = 8;                      // output rows per workgroup (E / 8 = 256 workgroups)
 constexpr int DN_NB = shp::FF / QK;          // 2 blocks per down row
 constexpr int DN_U = OXE_MAX_UNION + 1;
 constexpr int DN_A = shp::KUSED + 1;         // activation rows per lane: the k slots, then the shared h
@@ -787,12 +787,13 @@ __global__ __launch_bounds__(256) void kq_down_kernel(const RunCtl *__restrict__
         }
     }
     __syncthreads();
-    // K-quant units, four per pass: thread (unit u0 + t / 64, row t / 4 % 16, half block t % 4) forms
+    // K-quant units, eight per pass: thread (unit u0 + t / 32, row t / 4 % 8, half block t % 4) forms
     // its half block's integers for every lane with a slot there; threads t % 4 < NL then run lane
     // t % 4's chain over the row's two blocks
+    static_assert(DN_R == 8, "thread mapping of the K-quant units");
     {
-        const int p = t >> 6, rr = (t >> 2) & 15, hu = t & 3;
-        for (int u0 = 0; u0 < DN_U; u0 += 4) {
+        const int p = t >> 5, rr = (t >> 2) & 7, hu = t & 3;
+        for (int u0 = 0; u0 < DN_U; u0 += 8) {
             const int u = u0 + p;
             const bool live = u < DN_U && (u == OXE_MAX_UNION ? sh_kq : (exp_kq && u < nu));
             const RawW &W = u == OXE_MAX_UNION ? a.sh_down_r : a.exp_down_r;
@@ -1021,7 +1022,7 @@ int launch_kq_moe(const RunCtl *ctl, const ModelRt &m, const LayerW &w, const Ac
         a.hsh = b.hsh;
         a.do_exp = exp_gu;
         a.do_sh = sh_gu;
-        hipLaunchKernelGGL(kq::kq_gu_kernel<OXE_NL>, dim3((OXE_MAX_UNION + 1) * (shp::FF / 16)), dim3(256), 0, st, ctl, a);
+        hipLaunchKernelGGL(kq::kq_gu_kernel<OXE_NL>, dim3((OXE_MAX_UNION + 1) * (shp::FF / kq::GU_R)), dim3(256), 0, st, ctl, a);
     }
     if (w.exp_down_r.type != 8) quant_k(b.hexp, (int64_t)OXE_NL * shp::KUSED * shp::FF / kq::QK, b.hk, st);
     if (w.sh_down_r.type != 8) quant_k(b.hsh, (int64_t)OXE_NL * shp::FFSH / kq::QK, b.hshk, st);
