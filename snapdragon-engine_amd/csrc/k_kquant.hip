@@ -63,12 +63,9 @@ struct YView {
 // division), codes = nearest_int(iscale * x) (the float add of 1.5 * 2^23: round half to even),
 // clamped above at 127; bsums = sums of 16 codes; d = 1 / iscale. An all-zero block gets d = 0 and
 // zero codes and sums.
-__global__ __launch_bounds__(256) void quant_q8_K_kernel(const float *__restrict__ x, int64_t nblk,
-                                                         uint8_t *__restrict__ y) {
-    const int lane = threadIdx.x & 63;
-    const int64_t b = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (b >= nblk) return;
-    const float4 v4 = *(const float4 *)(x + b * QK + 4 * lane);
+// (xb: the block's 256 values; every lane of one wave)
+OXE_DEV void q8K_block(const float *xb, int lane, uint8_t *__restrict__ yb) {
+    const float4 v4 = *(const float4 *)(xb + 4 * lane);
     const float v[4] = {v4.x, v4.y, v4.z, v4.w};
     float am = 0.0f, mx = 0.0f;
     int idx = QK;
@@ -89,7 +86,6 @@ __global__ __launch_bounds__(256) void quant_q8_K_kernel(const float *__restrict
             idx = oi;
         }
     }
-    uint8_t *yb = y + b * Q8K_BYTES;
     int q[4] = {0, 0, 0, 0};
     float iscale = 0.0f;
     if (am != 0.0f) {
@@ -108,6 +104,22 @@ __global__ __launch_bounds__(256) void quant_q8_K_kernel(const float *__restrict
     s += shfl_xor_i(s, 2);
     if ((lane & 3) == 0) *(int16_t *)(yb + Q8K_BS + 2 * (lane >> 2)) = (int16_t)s;
     if (lane == 0) *(float *)yb = am != 0.0f ? 1 / iscale : 0.0f;
+}
+
+__global__ __launch_bounds__(256) void quant_q8_K_kernel(const float *__restrict__ x, int64_t nblk,
+                                                         uint8_t *__restrict__ y) {
+    const int64_t b = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (b >= nblk) return;
+    q8K_block(x + b * QK, threadIdx.x & 63, y + b * Q8K_BYTES);
+}
+
+// the q8_K blocks of a workgroup's [NL][E] rows held in LDS (256 threads: wave w takes blocks w,
+// w + 4, ...), after the barrier that completes the rows
+template <int NL>
+OXE_DEV void q8K_rows_lds(const float (&rows)[NL][shp::E], uint8_t *__restrict__ y) {
+    __syncthreads();
+    for (int b = threadIdx.x >> 6; b < NL * shp::E / QK; b += 4)
+        q8K_block(&rows[0][0] + b * QK, threadIdx.x & 63, y + (int64_t)b * Q8K_BYTES);
 }
 
 // ---- integers of one half block (unit h: weights 128 h .. 128 h + 127), every lane ---------------
@@ -621,7 +633,7 @@ __global__ __launch_bounds__(256) void ba_f32_kernel(const RunCtl *__restrict__ 
     float acc[NL];
 #pragma unroll
     for (int l = 0; l < NL; l++) acc[l] = 0.0f;
-#pragma unroll 8
+#pragma unroll 32
     for (int s = 0; s < shp::E / 16; s++) {
         const float wv = w[c + 16 * s];
 #pragma unroll
@@ -862,8 +874,10 @@ __global__ __launch_bounds__(256) void kq_down_kernel(const RunCtl *__restrict__
 // -inf: no key, argmax 0), packed as the per-phase head packs it: (ordered value << 32) | ~row.
 template <int NL>
 __global__ __launch_bounds__(256) void kq_head_norm_kernel(const RunCtl *__restrict__ ctl, const float *x2,
-                                                           const float *norm_w, float eps, float *hid, float *xn) {
+                                                           const float *norm_w, float eps, float *hid, float *xn,
+                                                           uint8_t *xk) {
     __shared__ NormScratch ns;
+    __shared__ float s_n[NL][shp::E];
     if (!ctl->active) return;
     const int nl = ctl->nl, t = threadIdx.x;
 #pragma unroll
@@ -878,7 +892,9 @@ __global__ __launch_bounds__(256) void kq_head_norm_kernel(const RunCtl *__restr
             for (int i = 0; i < EPT; i++) v[i] = 0.0f;
         }
         store8(xn + (int64_t)l * shp::E, v);
+        store8(s_n[l], v);
     }
+    q8K_rows_lds<NL>(s_n, xk);   // the head GEMV's activation
 }
 
 template <int NL>
@@ -966,9 +982,10 @@ __global__ __launch_bounds__(256) void kq_embed_kernel(const RunCtl *__restrict_
 template <int NL>
 __global__ __launch_bounds__(256) void kq_norm_kernel(const RunCtl *__restrict__ ctl, const float *x, Q8W emb,
                                                       const float *embf, float *x_store, const float *norm_w, float eps,
-                                                      float *xn) {
+                                                      float *xn, uint8_t *xk) {
     __shared__ NormScratch ns;
     __shared__ float s_x[shp::E];
+    __shared__ float s_n[NL][shp::E];
     if (!ctl->active) return;
     const int nl = ctl->nl;
 #pragma unroll
@@ -988,7 +1005,9 @@ __global__ __launch_bounds__(256) void kq_norm_kernel(const RunCtl *__restrict__
             for (int i = 0; i < EPT; i++) v[i] = 0.0f;
         }
         store8(xn + (int64_t)l * shp::E, v);
+        store8(s_n[l], v);
     }
+    q8K_rows_lds<NL>(s_n, xk);   // the GEMV's activation: q8_K blocks of xn
 }
 
 }  // namespace kq
@@ -1048,8 +1067,8 @@ int launch_kq_moe(const RunCtl *ctl, const ModelRt &m, const LayerW &w, const Ac
 
 int launch_kq_head(const RunCtl *ctl, const ModelRt &m, const float *norm_w, const ActBufs &b, hipStream_t st,
                    const RawW *w, const uint32_t *ids) {
-    hipLaunchKernelGGL(kq::kq_head_norm_kernel<OXE_NL>, dim3(1), dim3(256), 0, st, ctl, b.x2, norm_w, m.eps, b.hid, b.xn);
-    quant_k(b.xn, (int64_t)OXE_NL * shp::E / kq::QK, b.xk, st);
+    hipLaunchKernelGGL(kq::kq_head_norm_kernel<OXE_NL>, dim3(1), dim3(256), 0, st, ctl, b.x2, norm_w, m.eps, b.hid, b.xn,
+                       b.xk);
     const int nb = shp::E / kq::QK;
     const RawW &o = w ? *w : m.output_r;
     int rc;
@@ -1087,8 +1106,7 @@ int launch_kq_proj(const RunCtl *ctl, const ModelRt &m, const LayerW &w, const f
     using namespace shp;
     const bool kemb = embed && m.tok_embd_r.type != 8;
     hipLaunchKernelGGL(kq::kq_norm_kernel<OXE_NL>, dim3(1), dim3(256), 0, st, ctl, x, embed && !kemb ? m.tok_embd : Q8W{},
-                       kemb ? b.emb : nullptr, x_store, w.attn_norm, m.eps, b.xn);
-    quant_k(b.xn, (int64_t)OXE_NL * E / kq::QK, b.xk, st);
+                       kemb ? b.emb : nullptr, x_store, w.attn_norm, m.eps, b.xn, b.xk);
     struct Part {
         const RawW *r;
         int64_t off;
