@@ -113,6 +113,20 @@ __global__ __launch_bounds__(256) void quant_q8_K_kernel(const float *__restrict
     q8K_block(x + b * QK, threadIdx.x & 63, y + b * Q8K_BYTES);
 }
 
+// two buffers' blocks in one launch: blocks b < n0 of x0 into y0, then n1 of x1 into y1
+__global__ __launch_bounds__(256) void quant_q8_K_two_kernel(const float *__restrict__ x0, int64_t n0,
+                                                             uint8_t *__restrict__ y0, const float *__restrict__ x1,
+                                                             int64_t n1, uint8_t *__restrict__ y1) {
+    int64_t b = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (b >= n0 + n1) return;
+    if (b < n0) {
+        q8K_block(x0 + b * QK, threadIdx.x & 63, y0 + b * Q8K_BYTES);
+    } else {
+        b -= n0;
+        q8K_block(x1 + b * QK, threadIdx.x & 63, y1 + b * Q8K_BYTES);
+    }
+}
+
 // the q8_K blocks of a workgroup's [NL][E] rows held in LDS (256 threads: wave w takes blocks w,
 // w + 4, ...), after the barrier that completes the rows
 template <int NL>
@@ -1043,8 +1057,14 @@ int launch_kq_moe(const RunCtl *ctl, const ModelRt &m, const LayerW &w, const Ac
         a.do_sh = sh_gu;
         hipLaunchKernelGGL(kq::kq_gu_kernel<OXE_NL>, dim3((OXE_MAX_UNION + 1) * (shp::FF / kq::GU_R)), dim3(256), 0, st, ctl, a);
     }
-    if (w.exp_down_r.type != 8) quant_k(b.hexp, (int64_t)OXE_NL * shp::KUSED * shp::FF / kq::QK, b.hk, st);
-    if (w.sh_down_r.type != 8) quant_k(b.hsh, (int64_t)OXE_NL * shp::FFSH / kq::QK, b.hshk, st);
+    {
+        // h of the routed slots and of the shared expert, for whichever down matrices are K-quants
+        const int64_t ne = w.exp_down_r.type != 8 ? (int64_t)OXE_NL * shp::KUSED * shp::FF / kq::QK : 0;
+        const int64_t ns = w.sh_down_r.type != 8 ? (int64_t)OXE_NL * shp::FFSH / kq::QK : 0;
+        if (ne + ns > 0)
+            hipLaunchKernelGGL(kq::quant_q8_K_two_kernel, dim3((unsigned)((ne + ns + 3) / 4)), dim3(256), 0, st, b.hexp, ne,
+                               b.hk, b.hsh, ns, b.hshk);
+    }
     kq::KqDownArgs d{};
     d.uni = b.uni;
     d.route_ids = b.route_ids;
