@@ -685,6 +685,29 @@ TYPED_PUBLISHED = {
 }
 
 
+def typed_step_bytes(hdr, d, pos, u_avg):
+    """Unique HBM bytes of one MTP-1 step with no accepted draft on a typed model, from the file's
+    own tensor sizes: the verify run reads every target layer's tensors once (experts at the
+    measured union size per MoE layer), the LM head, the delta-net state (read, and written per
+    lane) and the attention KV of positions <= pos; the draft run the MTP layer's tensors (its 8
+    routed experts), the LM head and its KV."""
+    dense, exps, head = {}, {}, 0
+    for name, _t, _shape, _off, nbytes in hdr["tensors"]:
+        if name.startswith("blk."):
+            layer = int(name.split(".")[1])
+            tab = exps if "_exps" in name else dense
+            tab[layer] = tab.get(layer, 0) + nbytes
+        elif name == "output.weight":
+            head = nbytes
+    n_exp, nl = d.n_expert, d.n_layer
+    n_att = nl // d.full_attention_interval
+    verify = (sum(dense.get(l, 0) + exps.get(l, 0) * u_avg / n_exp for l in range(nl)) + head
+              + (nl - n_att) * 3 * DN_STATE + n_att * ((pos + 2) * KV_POS + 2 * KV_POS))
+    draft = (dense.get(nl, 0) + exps.get(nl, 0) * d.n_expert_used / n_exp + head
+             + (pos + 1) * KV_POS + KV_POS)
+    return verify + draft
+
+
 def bench_typed(args):
     """MTP-1 decode of an engine with a real file's matrix types (the Qwen3.6 or Ornith 35B-A3B
     GGUF: K-quant experts, projections, embedding, LM head) and its vocabulary, the weights
@@ -714,6 +737,7 @@ def bench_typed(args):
     eng.mtp_device_steps(args.warmup, use_graph=True)
     _, x = eng.mtp_device_end(cap)
     pos_start = eng.pos
+    uni0, calls0 = eng.counter(66), eng.counter(67)
     eng.mtp_device_begin(x, cap)
     stream = torch.cuda.ExternalStream(eng.stream())
     ev0 = torch.cuda.Event(enable_timing=True)
@@ -728,6 +752,13 @@ def bench_typed(args):
     ms = ev0.elapsed_time(ev1)
     toks, x = eng.mtp_device_end(cap)
     n_tok = len(toks)
+    # MoE calls of the timed steps: 40 verify layers (two lanes) and the draft's MTP layer (one lane,
+    # exactly its 8 experts) per step; the verify layers' mean union is what is left
+    calls = eng.counter(67) - calls0 - args.steps
+    units = eng.counter(66) - uni0 - d.n_expert_used * args.steps
+    u_avg = units / calls if calls > 0 else None
+    bytes_step = typed_step_bytes(hdr, d, (pos_start + eng.pos) / 2, u_avg) if u_avg is not None else None
+    step_gbs = bytes_step / (ms / args.steps / 1e3) / 1e9 if bytes_step else None
     n_types = {}
     for t in types.values():
         n_types[t] = n_types.get(t, 0) + 1
@@ -753,6 +784,10 @@ def bench_typed(args):
         "tokens": n_tok,
         "accepted_drafts": n_tok - args.steps,
         "run_mode": "fused (one persistent launch per run)" if fused else "one launch per phase",
+        "union_experts_per_moe_layer": round(u_avg, 3) if u_avg is not None else None,
+        "hbm_bytes_per_step": int(bytes_step) if bytes_step else None,
+        "hbm_GBs_step": round(step_gbs, 1) if step_gbs else None,
+        "hbm_frac_step": round(step_gbs / PEAK_HBM_GBS, 4) if step_gbs else None,
         "reference_published": TYPED_PUBLISHED[args.types],
         "setup_s": round(setup_s, 1),
         "roofline": None,

@@ -676,6 +676,7 @@ struct KqGuArgs {
     float *hexp;                // [NL][KUSED][FF]
     float *hsh;                 // [NL][FFSH]
     int do_exp, do_sh;
+    uint32_t *stats;            // [0] sum of union sizes, [1] launches (as the Q8_0 experts phase counts)
 };
 constexpr int GU_NB = shp::E / QK;   // 8 blocks per row
 constexpr int GU_R = 8;              // rows per workgroup
@@ -692,6 +693,10 @@ __global__ __launch_bounds__(256) void kq_gu_kernel(const RunCtl *__restrict__ c
     const int nl = ctl->nl, t = threadIdx.x, which = t >> 7, ri = (t >> 4) & (GU_R - 1), hu = t & 15;
     const int u = blockIdx.x / (shp::FF / GU_R), tile = blockIdx.x % (shp::FF / GU_R);
     const bool sh = u == OXE_MAX_UNION;
+    if (a.do_exp && blockIdx.x == 0 && t == 0) {
+        atomicAdd(a.stats, (uint32_t)a.uni[0]);
+        atomicAdd(a.stats + 1, 1u);
+    }
     if (sh ? !a.do_sh : !a.do_exp) return;
     int e = 0;
     if (!sh) {
@@ -1055,6 +1060,7 @@ int launch_kq_moe(const RunCtl *ctl, const ModelRt &m, const LayerW &w, const Ac
         a.hsh = b.hsh;
         a.do_exp = exp_gu;
         a.do_sh = sh_gu;
+        a.stats = b.counters + CNT_UNI_SUM;
         hipLaunchKernelGGL(kq::kq_gu_kernel<OXE_NL>, dim3((OXE_MAX_UNION + 1) * (shp::FF / kq::GU_R)), dim3(256), 0, st, ctl, a);
     }
     {
